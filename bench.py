@@ -1,0 +1,237 @@
+#!/usr/bin/env python3
+"""Benchmark of the FLAT-ATTENTION hot path on one MI355X.
+
+One step = one causal GQA prefill with fused RoPE on BASELINE configs[2]
+(B2 Hq32 Hkv8 N4096 D128, bf16 storage, f32 accumulation) followed by one split-K paged decode
+on configs[3] (64 sequences, ctx ~ U[512, 8192], page 16, Hq32 Hkv8 D128, bf16 KV, shuffled
+page pool). Inputs are synthetic and resident in HBM before timing. Each op is bracketed by
+HIP events recorded on the library's own stream.
+
+value = prefill TFLOP/s (algorithmic FLOP over visible (q, k) pairs: 4*B*Hq*D*N(N+1)/2);
+decode GB/s (algorithmic bytes: K+V of every live token once, plus Q, O, LSE, block tables)
+is reported beside it with its own roofline.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "flat-attention_amd"))
+
+import flat_attention_amd as fa  # noqa: E402
+
+PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+
+
+class HipEvents:
+    """hipEvent timing on an arbitrary stream (libamdhip64 via ctypes)."""
+
+    def __init__(self):
+        self.h = ctypes.CDLL("libamdhip64.so")
+        self.h.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+        self.h.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+        self.h.hipEventSynchronize.argtypes = [ctypes.c_void_p]
+        self.h.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p,
+                                               ctypes.c_void_p]
+        self.h.hipEventDestroy.argtypes = [ctypes.c_void_p]
+
+    def create(self):
+        e = ctypes.c_void_p()
+        assert self.h.hipEventCreate(ctypes.byref(e)) == 0
+        return e
+
+    def record(self, e, stream):
+        assert self.h.hipEventRecord(e, ctypes.c_void_p(stream)) == 0
+
+    def elapsed_ms(self, a, b):
+        assert self.h.hipEventSynchronize(b) == 0
+        ms = ctypes.c_float()
+        assert self.h.hipEventElapsedTime(ctypes.byref(ms), a, b) == 0
+        return ms.value
+
+
+def bf16_normal(rng, n):
+    return fa.f32_to_bf16_bits(rng.standard_normal(n, dtype=np.float32))
+
+
+def build_prefill(ctx, rng):
+    B, hq, hkv, S, D = 2, 32, 8, 4096, 128
+    shape = fa.GroupedAttentionShape(B, hq, hkv, S, D)
+    ex = fa.HipRotaryGroupedAttention(ctx, fa.DTYPE_BF16)
+    q = fa.DeviceBuffer.from_array(ctx, bf16_normal(rng, shape.q_tensor_len()))
+    k = fa.DeviceBuffer.from_array(ctx, bf16_normal(rng, shape.kv_tensor_len()))
+    v = fa.DeviceBuffer.from_array(ctx, bf16_normal(rng, shape.kv_tensor_len()))
+    out = fa.DeviceBuffer(ctx, ex.layout(shape).combined_bytes)
+    cfg = fa.FlatAttentionConfig(causal=True)
+    rot = fa.RotaryEmbeddingConfig(10000.0, 0)
+    flop = 4.0 * B * hq * D * S * (S + 1) / 2
+    run = lambda: ex.forward_resident(q, k, v, shape, cfg, rot, out)  # noqa: E731
+    return run, flop, {"workload": "prefill: causal GQA+RoPE B2 Hq32 Hkv8 N4096 D128 bf16",
+                       "flop_per_step": flop}
+
+
+def build_decode(ctx, rng):
+    n, hq, hkv, D, ps = 64, 32, 8, 128, 16
+    ctx_lens = rng.integers(512, 8193, n).astype(np.int32)
+    pages_per = (ctx_lens + ps - 1) // ps
+    total = int(pages_per.sum())
+    ids = rng.permutation(total).astype(np.int32)
+    bt = np.zeros((n, int(pages_per.max())), np.int32)
+    cur = 0
+    for s in range(n):
+        bt[s, :pages_per[s]] = ids[cur:cur + pages_per[s]]
+        cur += pages_per[s]
+    width = hkv * D
+    kp = fa.DeviceBuffer.from_array(ctx, bf16_normal(rng, total * ps * width))
+    vp = fa.DeviceBuffer.from_array(ctx, bf16_normal(rng, total * ps * width))
+    q = fa.DeviceBuffer.from_array(ctx, bf16_normal(rng, n * hq * D))
+    plan = fa.PagedDecodePlan(ctx, bt, ctx_lens, ps, total, hq, hkv, D,
+                              fa.FlatAttentionConfig(True), 10000.0, fa.DTYPE_BF16)
+    out = fa.DeviceBuffer(ctx, plan.layout().combined_bytes)
+    nbytes = (float(ctx_lens.sum()) * hkv * D * 2 * 2 + n * hq * D * 2 * 2 + n * hq * 4
+              + float(pages_per.sum()) * 4)
+    run = lambda: plan.launch(q, kp, vp, out)  # noqa: E731
+    info = plan.info()
+    return run, nbytes, {"workload": "paged decode: 64 seqs ctx U[512,8192] page16 Hq32 Hkv8 "
+                                     "D128 bf16 KV, shuffled pages",
+                         "bytes_per_step": nbytes, "live_tokens": int(ctx_lens.sum()),
+                         "split_tokens": info["split_tokens"], "work_items": info["work_items"]}
+
+
+def cpu_baseline(sample_seconds: float = 20.0):
+    """Scalar C oracle (oracle/) timed on this host on bounded samples of the same workloads."""
+    import oracle  # CPU baseline leg only
+    res = {}
+    # prefill: first (b, h) unit of configs[2] truncated to its first n query rows (causal rows
+    # 0..n-1 do the same work as in the full problem); FLOP counted like the GPU metric.
+    n, D = 2048, 128
+    q = oracle.fill_normal(n * D, 1)
+    k = oracle.fill_normal(n * D, 2)
+    v = oracle.fill_normal(n * D, 3)
+    t0 = time.perf_counter()
+    oracle.forward_grouped_rope(q, k, v, 1, 1, 1, n, D, True, 10000.0, 0)
+    dt = time.perf_counter() - t0
+    flop = 4.0 * D * n * (n + 1) / 2
+    res["prefill"] = {"value": flop / dt / 1e12, "unit": "TFLOP/s", "cores": 1, "kind": "port",
+                      "sample": f"oracle forward_reference_grouped_rope, one (b,h) unit, causal "
+                                f"N={n} rows of configs[2] (D128, RoPE theta 1e4), {dt:.2f} s"}
+    # decode: 16 sequences of 4096 live tokens, Hq32 Hkv8 D128
+    ns, ctxl, hq, hkv, ps = 16, 4096, 32, 8, 16
+    pages = ctxl // ps
+    bt = np.arange(ns * pages, dtype=np.int32).reshape(ns, pages)
+    kp = oracle.fill_normal(ns * ctxl * hkv * D, 4)
+    vp = oracle.fill_normal(ns * ctxl * hkv * D, 5)
+    qd = oracle.fill_normal(ns * hq * D, 6)
+    t0 = time.perf_counter()
+    oracle.paged_decode(qd, kp, vp, ns * pages, ps, bt, [ctxl] * ns, hq, hkv, D, True, 10000.0)
+    dt = time.perf_counter() - t0
+    nbytes = ns * ctxl * hkv * D * 2 * 2  # same bf16 byte accounting as the GPU metric
+    res["decode"] = {"value": nbytes / dt / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
+                     "sample": f"oracle paged decode, 16 seqs x 4096 tokens, Hq32 Hkv8 D128, "
+                               f"{dt:.2f} s"}
+    return res
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--prefill-policy", type=int, default=-1,
+                    help="-1 auto, 0 rotate K on load, 1 pre-rotate K")
+    ap.add_argument("--only", choices=["prefill", "decode"], default=None)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path "
+              "(see DESIGN.md, 'How the path would shard')", file=sys.stderr)
+        sys.exit(2)
+
+    rng = np.random.default_rng(1234)
+    ctx = fa.HipContext(0)
+    ctx.set_prefill_policy(args.prefill_policy)
+    ev = HipEvents()
+    stream = ctx.stream
+    ops = []
+    if args.only in (None, "prefill"):
+        ops.append(("prefill",) + build_prefill(ctx, rng))
+    if args.only in (None, "decode"):
+        ops.append(("decode",) + build_decode(ctx, rng))
+    ctx.synchronize()
+
+    tele = {}
+    for _ in range(args.warmup):
+        for name, run, _, _ in ops:
+            run()
+            tele[name] = ctx.last_telemetry()
+    ctx.synchronize()
+
+    evs = [[ev.create() for _ in range(len(ops) + 1)] for _ in range(args.steps)]
+    t_wall = time.perf_counter()
+    for s in range(args.steps):
+        ev.record(evs[s][0], stream)
+        for i, (name, run, _, _) in enumerate(ops):
+            run()
+            ev.record(evs[s][i + 1], stream)
+    ctx.synchronize()
+    wall = time.perf_counter() - t_wall
+    per_op = {name: [ev.elapsed_ms(evs[s][i], evs[s][i + 1]) for s in range(args.steps)]
+              for i, (name, _, _, _) in enumerate(ops)}
+    step_ms = sum(np.mean(v) for v in per_op.values())
+
+    out = {"metric": "causal GQA prefill TFLOP/s (D128,N4096) + paged-decode HBM GB/s, % of peak",
+           "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+           "ms_per_step": round(step_ms, 4), "higher_is_better": True, "scaling": "weak",
+           "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+           "wall_s": round(wall, 3)}
+    details = {}
+    for name, run, work, meta in ops:
+        ms = float(np.mean(per_op[name]))
+        t = tele[name]
+        d = {"ms": round(ms, 5), "ms_min": round(float(np.min(per_op[name])), 5),
+             "kernel": t.kernel_name, "kernel_id": t.kernel_id, "dispatches": t.dispatch_count,
+             "grid": list(t.workgroups), **meta}
+        if name == "prefill":
+            tf = work / (ms * 1e-3) / 1e12
+            d.update({"TFLOP/s": round(tf, 2),
+                      "roofline": {"bound": "mfma", "achieved": round(tf, 2),
+                                   "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                                   "frac": round(tf / PEAK_BF16_TFLOPS, 4), "traffic": None}})
+        else:
+            gbs = work / (ms * 1e-3) / 1e9
+            d.update({"GB/s": round(gbs, 1),
+                      "roofline": {"bound": "hbm", "achieved": round(gbs, 1),
+                                   "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                                   "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None}})
+        details[name] = d
+    if "prefill" in details:
+        out["value"] = details["prefill"]["TFLOP/s"]
+        out["unit"] = "TFLOP/s"
+        out["roofline"] = details["prefill"]["roofline"]
+    else:
+        out["value"] = details["decode"]["GB/s"]
+        out["unit"] = "GB/s"
+        out["roofline"] = details["decode"]["roofline"]
+    out["config"] = {"workload": " + ".join(d["workload"] for d in details.values()),
+                     "configs": "BASELINE configs[2] (prefill) + configs[3] (decode)",
+                     "parallelism": "single GPU"}
+    out["prefill"] = details.get("prefill")
+    out["decode"] = details.get("decode")
+    if not args.no_cpu_baseline:
+        cb = cpu_baseline()
+        primary = cb["prefill"] if "prefill" in details else cb["decode"]
+        out["cpu_baseline"] = dict(primary, other=cb["decode"] if "prefill" in details else None)
+    ctx.close()
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

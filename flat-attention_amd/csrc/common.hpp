@@ -1,0 +1,109 @@
+// Shared device helpers for the gfx950 (CDNA4) kernels: 16-bit storage types, conversions,
+// MFMA operand types and wave-level utilities. Wavefronts are 64 lanes.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace fa {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+
+// Storage tags. Device code moves 16-bit values as raw uint16 bit patterns.
+struct bf16_t {};
+struct f16_t {};
+
+constexpr int kWave = 64;
+constexpr float kLog2e = 1.4426950408889634f;
+
+// ---------------------------------------------------------------- 16-bit conversions
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+__device__ __forceinline__ float f16_lo(uint32_t w) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(w & 0xffffu));
+}
+__device__ __forceinline__ float f16_hi(uint32_t w) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(w >> 16));
+}
+
+// Round-to-nearest-even f32 -> bf16 pair (hardware v_cvt_pk_bf16_f32 on gfx950).
+__device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
+    __bf16 x = (__bf16)a, y = (__bf16)b;
+    return (uint32_t)__builtin_bit_cast(uint16_t, x) |
+           ((uint32_t)__builtin_bit_cast(uint16_t, y) << 16);
+}
+__device__ __forceinline__ uint32_t pack_f16(float a, float b) {
+    _Float16 x = (_Float16)a, y = (_Float16)b;
+    return (uint32_t)__builtin_bit_cast(uint16_t, x) |
+           ((uint32_t)__builtin_bit_cast(uint16_t, y) << 16);
+}
+
+template <typename T> struct Half;
+template <> struct Half<bf16_t> {
+    __device__ __forceinline__ static float lo(uint32_t w) { return bf16_lo(w); }
+    __device__ __forceinline__ static float hi(uint32_t w) { return bf16_hi(w); }
+    __device__ __forceinline__ static uint32_t pack(float a, float b) { return pack_bf16(a, b); }
+    // D[32x32] += A[32x16] * B[16x32]; A, B hold 8 values per lane.
+    __device__ __forceinline__ static f32x16_t mfma32(u32x4_t a, u32x4_t b, f32x16_t c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                       __builtin_bit_cast(bf16x8_t, b), c, 0, 0,
+                                                       0);
+    }
+    // D[16x16] += A[16x32] * B[32x16].
+    __device__ __forceinline__ static f32x4_t mfma16(u32x4_t a, u32x4_t b, f32x4_t c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                       __builtin_bit_cast(bf16x8_t, b), c, 0, 0,
+                                                       0);
+    }
+};
+template <> struct Half<f16_t> {
+    __device__ __forceinline__ static float lo(uint32_t w) { return f16_lo(w); }
+    __device__ __forceinline__ static float hi(uint32_t w) { return f16_hi(w); }
+    __device__ __forceinline__ static uint32_t pack(float a, float b) { return pack_f16(a, b); }
+    __device__ __forceinline__ static f32x16_t mfma32(u32x4_t a, u32x4_t b, f32x16_t c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a),
+                                                      __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+    }
+    __device__ __forceinline__ static f32x4_t mfma16(u32x4_t a, u32x4_t b, f32x4_t c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a),
+                                                      __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+    }
+};
+
+// ---------------------------------------------------------------- wave utilities
+__device__ __forceinline__ float shfl_xor(float v, int mask) { return __shfl_xor(v, mask, 64); }
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Rotate one interleaved (even, odd) pair: (e c - o s, e s + o c). Written with explicit fmaf
+// so every kernel that rotates (in-register, pre-pass, cache append) rounds identically.
+__device__ __forceinline__ void rope_pair(float& e, float& o, float c, float s) {
+    const float re = fmaf(e, c, -(o * s));
+    const float ro = fmaf(e, s, o * c);
+    e = re;
+    o = ro;
+}
+
+// Rotate four pairs held as 8 f32 values by four (cos, sin) pairs.
+__device__ __forceinline__ void rope4(float* x, const float* cs) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) rope_pair(x[2 * j], x[2 * j + 1], cs[2 * j], cs[2 * j + 1]);
+}
+
+// Workgroup id -> logical id such that consecutive logical ids run on the same XCD.
+// The dispatcher places workgroup i on XCD i % 8; logical ids [x*n/8, (x+1)*n/8) go to XCD x,
+// so workgroups that share K/V (same batch/kv-head) share one XCD's L2.
+__device__ __forceinline__ int xcd_remap(int bid, int nb) {
+    constexpr int kXcd = 8;
+    int q = nb / kXcd, r = nb % kXcd;
+    int xcd = bid % kXcd, slot = bid / kXcd;
+    return xcd < r ? xcd * (q + 1) + slot : r * (q + 1) + (xcd - r) * q + slot;
+}
+
+}  // namespace fa

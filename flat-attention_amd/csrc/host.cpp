@@ -1,0 +1,1589 @@
+// C-ABI host layer of the gfx950 FLAT-ATTENTION backend (include/flat_hip.h).
+//
+// Validation restates the reference's host-side checks before anything is enqueued
+// (AttentionShape::validate src/lib.rs:236, GroupedAttentionShape::validate src/grouped.rs:57,
+// RotaryEmbeddingConfig::validate src/rotary_grouped.rs:22, resolved_scale src/lib.rs:257,
+// WgpuPagedDecodePipeline::encode src/wgpu_paged_decode.rs:300-359, PagedKvTable
+// src/paged_kv.rs:84-188, WgpuPagedKvCache::record_append src/wgpu_paged_kv_cache.rs:206-280).
+// Errors are returned as fa_status codes with the reference's message text; nothing falls back
+// to a CPU path.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <limits>
+#include <string>
+#include <vector>
+
+#include "../../include/flat_hip.h"
+#include "kernels.hpp"
+
+using fa::Dtype;
+
+// ---------------------------------------------------------------------------- errors
+namespace {
+
+thread_local std::string g_error;
+
+int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_error = buf;
+    return code;
+}
+
+int ok() {
+    g_error.clear();
+    return FA_OK;
+}
+
+#define HIP_TRY(expr)                                                                       \
+    do {                                                                                    \
+        hipError_t e_ = (expr);                                                             \
+        if (e_ != hipSuccess)                                                               \
+            return fail(FA_ERR_HIP, "HIP call %s failed: %s", #expr, hipGetErrorString(e_)); \
+    } while (0)
+
+constexpr uint64_t kMaxHeadDim = 128;  // WGSL_MAX_HEAD_DIM src/lib.rs:59-66
+constexpr uint64_t kI32 = (uint64_t)std::numeric_limits<int32_t>::max();
+
+bool mul_ov(uint64_t a, uint64_t b, uint64_t* out) {
+    if (a != 0 && b > std::numeric_limits<uint64_t>::max() / a) return true;
+    *out = a * b;
+    return false;
+}
+
+int elem_bytes(int dtype) { return dtype == FA_DTYPE_F32 ? 4 : 2; }
+
+int check_dtype(int dtype) {
+    if (dtype != FA_DTYPE_F32 && dtype != FA_DTYPE_F16 && dtype != FA_DTYPE_BF16)
+        return fail(FA_ERR_UNSUPPORTED_DTYPE, "unsupported storage dtype %d", dtype);
+    return FA_OK;
+}
+
+const char* dtype_name(int dtype) {
+    return dtype == FA_DTYPE_F32 ? "f32" : dtype == FA_DTYPE_F16 ? "f16" : "bf16";
+}
+
+int resolve_scale(const fa_config* cfg, uint64_t head_dim, float* out) {
+    if (head_dim == 0) return fail(FA_ERR_ZERO_DIMENSION, "attention dimensions must all be non-zero");
+    float s = (cfg && cfg->has_softmax_scale) ? cfg->softmax_scale
+                                              : 1.0f / std::sqrt((float)head_dim);
+    if (!std::isfinite(s) || s <= 0.0f)
+        return fail(FA_ERR_INVALID_SCALE, "softmax scale must be finite and positive, got %g",
+                    (double)s);
+    *out = s;
+    return FA_OK;
+}
+
+// Head-dim support of the MFMA kernels: D <= 128; 16-bit storage needs D % 8 == 0 (16-byte
+// row chunks); f32 storage accepts any D (RoPE additionally needs an even D).
+int check_head_dim(uint64_t d, int dtype) {
+    if (d > kMaxHeadDim)
+        return fail(FA_ERR_UNSUPPORTED_HEAD_DIM, "head_dim %llu exceeds maximum %llu",
+                    (unsigned long long)d, (unsigned long long)kMaxHeadDim);
+    if (dtype != FA_DTYPE_F32 && d % 8 != 0)
+        return fail(FA_ERR_UNSUPPORTED_HEAD_DIM,
+                    "head_dim %llu is not a multiple of 8, required for %s storage",
+                    (unsigned long long)d, dtype_name(dtype));
+    return FA_OK;
+}
+
+int check_rotary(float theta, uint64_t offset, uint64_t head_dim, uint64_t len) {
+    if (head_dim == 0 || head_dim % 2 != 0)
+        return fail(FA_ERR_INVALID_ROTARY_HEAD_DIM,
+                    "rotary attention head_dim must be non-zero and even, got %llu",
+                    (unsigned long long)head_dim);
+    if (!std::isfinite(theta) || theta <= 0.0f)
+        return fail(FA_ERR_INVALID_ROTARY_THETA,
+                    "rotary theta must be finite and positive, got %g", (double)theta);
+    uint64_t last = len == 0 ? 0 : len - 1;
+    if (offset > std::numeric_limits<uint64_t>::max() - last || offset + last > kI32)
+        return fail(FA_ERR_POSITION_OVERFLOW,
+                    "rotary position offset overflows the index space");
+    return FA_OK;
+}
+
+int check_buffer(const char* name, const void* p, size_t have, uint64_t need) {
+    if (!p) return fail(FA_ERR_NULL_ARGUMENT, "buffer %s is null", name);
+    if ((uint64_t)have < need)
+        return fail(FA_ERR_BUFFER_TOO_SMALL, "buffer %s contains %llu bytes, requires at least %llu",
+                    name, (unsigned long long)have, (unsigned long long)need);
+    return FA_OK;
+}
+
+uint64_t fnv1a64(const std::string& s) {
+    uint64_t h = 0xcbf29ce484222325ull;
+    for (unsigned char c : s) {
+        h ^= c;
+        h *= 0x100000001b3ull;
+    }
+    return h;
+}
+
+void copy_str(char* dst, size_t cap, const std::string& s) {
+    size_t n = std::min(cap - 1, s.size());
+    memcpy(dst, s.data(), n);
+    dst[n] = 0;
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------- context
+struct fa_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    std::string name, arch;
+    uint64_t fingerprint = 0;
+    int prerotate_policy = -1;
+    fa_telemetry last{};
+    // (cos, sin) table cache, keyed by (theta, head_dim)
+    float2* rope = nullptr;
+    float rope_theta = 0.0f;
+    uint64_t rope_dim = 0, rope_rows = 0;
+    float* inv_freq = nullptr;
+    // growable scratch for the K pre-rotation pass
+    void* ws = nullptr;
+    size_t ws_bytes = 0;
+    // per-call allocation accounting (telemetry)
+    uint32_t call_allocs = 0;
+    uint64_t call_alloc_bytes = 0;
+};
+
+namespace {
+
+int set_device(fa_ctx* ctx) {
+    HIP_TRY(hipSetDevice(ctx->device));
+    return FA_OK;
+}
+
+void begin_call(fa_ctx* ctx) {
+    ctx->call_allocs = 0;
+    ctx->call_alloc_bytes = 0;
+}
+
+void record(fa_ctx* ctx, int kernel_id, const char* name, uint32_t qrows, uint32_t kvrows,
+            const unsigned grid[3], unsigned block, uint32_t dispatches, uint32_t splits,
+            const char* fallback) {
+    fa_telemetry& t = ctx->last;
+    memset(&t, 0, sizeof t);
+    t.kernel_id = kernel_id;
+    copy_str(t.kernel_name, sizeof t.kernel_name, name);
+    t.query_rows = qrows;
+    t.kv_rows = kvrows;
+    t.workgroups[0] = grid[0];
+    t.workgroups[1] = grid[1];
+    t.workgroups[2] = grid[2];
+    t.workgroup_size = block;
+    t.dispatch_count = dispatches;
+    t.temporary_allocation_count = ctx->call_allocs;
+    t.temporary_allocation_bytes = ctx->call_alloc_bytes;
+    t.splits = splits;
+    if (fallback) {
+        t.has_fallback_reason = 1;
+        copy_str(t.fallback_reason, sizeof t.fallback_reason, fallback);
+    }
+    copy_str(t.device_name, sizeof t.device_name, ctx->name);
+    copy_str(t.device_arch, sizeof t.device_arch, ctx->arch);
+    t.device_fingerprint = ctx->fingerprint;
+}
+
+int dev_alloc(fa_ctx* ctx, void** p, size_t bytes) {
+    HIP_TRY(hipMalloc(p, bytes ? bytes : 16));
+    ctx->call_allocs += 1;
+    ctx->call_alloc_bytes += bytes;
+    return FA_OK;
+}
+
+// (cos, sin) table covering positions [0, rows) for (theta, head_dim).
+int ensure_rope(fa_ctx* ctx, float theta, uint64_t head_dim, uint64_t rows, const float2** out) {
+    if (ctx->rope && ctx->rope_theta == theta && ctx->rope_dim == head_dim &&
+        ctx->rope_rows >= rows) {
+        *out = ctx->rope;
+        return FA_OK;
+    }
+    uint64_t cap = std::max<uint64_t>(rows, 4096);
+    if (ctx->rope_theta == theta && ctx->rope_dim == head_dim)
+        cap = std::max<uint64_t>(cap, ctx->rope_rows * 2);
+    const uint64_t half = head_dim / 2;
+    // inv_freq[p] = theta^(-2p/D) in f32 with the host powf, as rotated_pair computes it
+    std::vector<float> inv(half);
+    for (uint64_t p = 0; p < half; ++p) {
+        float exponent = -2.0f * (float)p / (float)head_dim;
+        inv[p] = powf(theta, exponent);
+    }
+    HIP_TRY(hipStreamSynchronize(ctx->stream));
+    if (ctx->rope) HIP_TRY(hipFree(ctx->rope));
+    if (ctx->inv_freq) HIP_TRY(hipFree(ctx->inv_freq));
+    ctx->rope = nullptr;
+    ctx->inv_freq = nullptr;
+    int rc = dev_alloc(ctx, (void**)&ctx->rope, cap * half * sizeof(float2));
+    if (rc) return rc;
+    rc = dev_alloc(ctx, (void**)&ctx->inv_freq, half * sizeof(float));
+    if (rc) return rc;
+    HIP_TRY(hipMemcpy(ctx->inv_freq, inv.data(), half * sizeof(float), hipMemcpyHostToDevice));
+    fa::launch_rope_table(ctx->rope, ctx->inv_freq, (int)cap, (int)half, ctx->stream);
+    HIP_TRY(hipGetLastError());
+    ctx->rope_theta = theta;
+    ctx->rope_dim = head_dim;
+    ctx->rope_rows = cap;
+    *out = ctx->rope;
+    return FA_OK;
+}
+
+int ensure_ws(fa_ctx* ctx, size_t bytes, void** out) {
+    if (ctx->ws_bytes < bytes) {
+        HIP_TRY(hipStreamSynchronize(ctx->stream));
+        if (ctx->ws) HIP_TRY(hipFree(ctx->ws));
+        ctx->ws = nullptr;
+        ctx->ws_bytes = 0;
+        int rc = dev_alloc(ctx, &ctx->ws, bytes);
+        if (rc) return rc;
+        ctx->ws_bytes = bytes;
+    }
+    *out = ctx->ws;
+    return FA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int fa_abi_version(void) { return FA_ABI_VERSION; }
+
+const char* fa_last_error_message(void) { return g_error.c_str(); }
+
+const char* fa_status_string(int s) {
+    switch (s) {
+        case FA_OK: return "ok";
+        case FA_ERR_ZERO_DIMENSION: return "ZeroDimension";
+        case FA_ERR_SHAPE_OVERFLOW: return "ShapeOverflow";
+        case FA_ERR_INVALID_HEAD_GROUPING: return "InvalidHeadGrouping";
+        case FA_ERR_INVALID_ROTARY_HEAD_DIM: return "InvalidRotaryHeadDim";
+        case FA_ERR_INVALID_ROTARY_THETA: return "InvalidRotaryTheta";
+        case FA_ERR_POSITION_OVERFLOW: return "PositionOverflow";
+        case FA_ERR_LENGTH_MISMATCH: return "LengthMismatch";
+        case FA_ERR_INVALID_SCALE: return "InvalidScale";
+        case FA_ERR_NON_FINITE_INPUT: return "NonFiniteInput";
+        case FA_ERR_UNAVAILABLE: return "Unavailable";
+        case FA_ERR_UNSUPPORTED_HEAD_DIM: return "UnsupportedHeadDim";
+        case FA_ERR_INDEX_SPACE_EXCEEDED: return "IndexSpaceExceeded";
+        case FA_ERR_DISPATCH_LIMIT: return "DispatchLimit";
+        case FA_ERR_BUFFER_TOO_SMALL: return "BufferTooSmall";
+        case FA_ERR_EMPTY_TABLE: return "EmptyTable";
+        case FA_ERR_TOO_MANY_MAPPED_PAGES: return "TooManyMappedPages";
+        case FA_ERR_CAUSAL_VISIBILITY_MISMATCH: return "CausalVisibilityMismatch";
+        case FA_ERR_ZERO_QUERY_CHUNK_SIZE: return "ZeroQueryChunkSize";
+        case FA_ERR_UNSUPPORTED_DTYPE: return "UnsupportedDtype";
+        case FA_ERR_INVALID_PAGE: return "InvalidPage";
+        case FA_ERR_PAGED_ZERO_DIMENSION: return "PagedZeroDimension";
+        case FA_ERR_CAPACITY_OVERFLOW: return "CapacityOverflow";
+        case FA_ERR_CAPACITY_EXCEEDED: return "CapacityExceeded";
+        case FA_ERR_GENERATION_OVERFLOW: return "GenerationOverflow";
+        case FA_ERR_NULL_ARGUMENT: return "NullArgument";
+        case FA_ERR_HIP: return "Hip";
+        default: return "Unknown";
+    }
+}
+
+int fa_resolved_scale(const fa_config* config, uint64_t head_dim, float* out) {
+    if (!out) return fail(FA_ERR_NULL_ARGUMENT, "output pointer is null");
+    int rc = resolve_scale(config, head_dim, out);
+    return rc ? rc : ok();
+}
+
+int fa_packed_layout_for(uint64_t output_elements, uint64_t lse_elements, int dtype,
+                         fa_packed_layout* out) {
+    if (!out) return fail(FA_ERR_NULL_ARGUMENT, "output pointer is null");
+    if (int rc = check_dtype(dtype)) return rc;
+    uint64_t ob, lb;
+    if (mul_ov(output_elements, (uint64_t)elem_bytes(dtype), &ob) || mul_ov(lse_elements, 4, &lb))
+        return fail(FA_ERR_SHAPE_OVERFLOW, "attention shape overflows the address space");
+    out->output_elements = output_elements;
+    out->lse_elements = lse_elements;
+    out->output_bytes = ob;
+    out->lse_byte_offset = (ob + 3) & ~3ull;
+    out->combined_bytes = out->lse_byte_offset + lb;
+    return ok();
+}
+
+int fa_ctx_create(int device, fa_ctx** out) {
+    if (!out) return fail(FA_ERR_NULL_ARGUMENT, "output pointer is null");
+    *out = nullptr;
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || count <= 0)
+        return fail(FA_ERR_UNAVAILABLE, "no HIP device is available");
+    if (device < 0 || device >= count)
+        return fail(FA_ERR_UNAVAILABLE, "HIP device %d does not exist (%d present)", device, count);
+    hipDeviceProp_t prop;
+    HIP_TRY(hipGetDeviceProperties(&prop, device));
+    std::string arch = prop.gcnArchName;
+    if (arch.rfind("gfx950", 0) != 0)
+        return fail(FA_ERR_UNAVAILABLE, "device %d is %s; this backend is built for gfx950 only",
+                    device, arch.c_str());
+    HIP_TRY(hipSetDevice(device));
+    fa_ctx* ctx = new fa_ctx();
+    ctx->device = device;
+    ctx->name = prop.name;
+    ctx->arch = arch;
+    int drv = 0;
+    (void)hipDriverGetVersion(&drv);
+    char rec[512];
+    snprintf(rec, sizeof rec, "name=%s;arch=%s;driver=%d;cus=%d;clock_khz=%d;mem=%zu",
+             prop.name, arch.c_str(), drv, prop.multiProcessorCount, prop.clockRate,
+             (size_t)prop.totalGlobalMem);
+    ctx->fingerprint = fnv1a64(rec);
+    if (hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking) != hipSuccess) {
+        delete ctx;
+        return fail(FA_ERR_HIP, "hipStreamCreate failed");
+    }
+    *out = ctx;
+    return ok();
+}
+
+int fa_ctx_destroy(fa_ctx* ctx) {
+    if (!ctx) return ok();
+    (void)hipSetDevice(ctx->device);
+    (void)hipStreamSynchronize(ctx->stream);
+    if (ctx->rope) (void)hipFree(ctx->rope);
+    if (ctx->inv_freq) (void)hipFree(ctx->inv_freq);
+    if (ctx->ws) (void)hipFree(ctx->ws);
+    (void)hipStreamDestroy(ctx->stream);
+    delete ctx;
+    return ok();
+}
+
+void* fa_ctx_stream(fa_ctx* ctx) { return ctx ? (void*)ctx->stream : nullptr; }
+
+int fa_ctx_synchronize(fa_ctx* ctx) {
+    if (!ctx) return fail(FA_ERR_NULL_ARGUMENT, "context is null");
+    if (int rc = set_device(ctx)) return rc;
+    HIP_TRY(hipStreamSynchronize(ctx->stream));
+    return ok();
+}
+
+int fa_ctx_device_name(fa_ctx* ctx, char* buf, size_t len) {
+    if (!ctx || !buf || !len) return fail(FA_ERR_NULL_ARGUMENT, "null argument");
+    copy_str(buf, len, ctx->name + " (" + ctx->arch + ")");
+    return ok();
+}
+
+int fa_ctx_set_prefill_policy(fa_ctx* ctx, int32_t prerotate_k) {
+    if (!ctx) return fail(FA_ERR_NULL_ARGUMENT, "context is null");
+    ctx->prerotate_policy = prerotate_k < 0 ? -1 : (prerotate_k ? 1 : 0);
+    return ok();
+}
+
+// ---------------------------------------------------------------------------- buffers
+int fa_buf_alloc(fa_ctx* ctx, size_t bytes, void** out) {
+    if (!ctx || !out) return fail(FA_ERR_NULL_ARGUMENT, "null argument");
+    if (int rc = set_device(ctx)) return rc;
+    HIP_TRY(hipMalloc(out, bytes ? bytes : 16));
+    return ok();
+}
+
+int fa_buf_free(fa_ctx* ctx, void* ptr) {
+    if (!ctx) return fail(FA_ERR_NULL_ARGUMENT, "context is null");
+    if (!ptr) return ok();
+    if (int rc = set_device(ctx)) return rc;
+    HIP_TRY(hipStreamSynchronize(ctx->stream));
+    HIP_TRY(hipFree(ptr));
+    return ok();
+}
+
+int fa_buf_upload(fa_ctx* ctx, void* dst, const void* host, size_t bytes) {
+    if (!ctx || !dst || (!host && bytes)) return fail(FA_ERR_NULL_ARGUMENT, "null argument");
+    if (int rc = set_device(ctx)) return rc;
+    HIP_TRY(hipMemcpyAsync(dst, host, bytes, hipMemcpyHostToDevice, ctx->stream));
+    HIP_TRY(hipStreamSynchronize(ctx->stream));
+    return ok();
+}
+
+int fa_buf_download(fa_ctx* ctx, void* host, const void* src, size_t bytes) {
+    if (!ctx || !src || (!host && bytes)) return fail(FA_ERR_NULL_ARGUMENT, "null argument");
+    if (int rc = set_device(ctx)) return rc;
+    HIP_TRY(hipMemcpyAsync(host, src, bytes, hipMemcpyDeviceToHost, ctx->stream));
+    HIP_TRY(hipStreamSynchronize(ctx->stream));
+    return ok();
+}
+
+int fa_buf_fill_u32(fa_ctx* ctx, void* dst, uint32_t value, size_t count) {
+    if (!ctx || !dst) return fail(FA_ERR_NULL_ARGUMENT, "null argument");
+    if (int rc = set_device(ctx)) return rc;
+    HIP_TRY(hipMemsetD32Async((hipDeviceptr_t)dst, (int)value, count, ctx->stream));
+    return ok();
+}
+
+int fa_last_telemetry(fa_ctx* ctx, fa_telemetry* out) {
+    if (!ctx || !out) return fail(FA_ERR_NULL_ARGUMENT, "null argument");
+    *out = ctx->last;
+    return ok();
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------- prefill core
+namespace {
+
+bool want_prerotate(const fa_ctx* ctx, uint64_t head_dim) {
+    if (head_dim % 8 != 0) return false;  // the pre-pass moves 8-element chunks
+    if (ctx->prerotate_policy >= 0) return ctx->prerotate_policy == 1;
+    return true;  // default: rotate K once, then stream pre-rotated K tiles
+}
+
+int prefill_kernel_id(int dtype, bool prerot) {
+    if (dtype == FA_DTYPE_BF16) return prerot ? FA_KERNEL_PREFILL_MFMA_BF16_PREROT : FA_KERNEL_PREFILL_MFMA_BF16;
+    if (dtype == FA_DTYPE_F16) return prerot ? FA_KERNEL_PREFILL_MFMA_F16_PREROT : FA_KERNEL_PREFILL_MFMA_F16;
+    return prerot ? FA_KERNEL_PREFILL_MFMA_F32_PREROT : FA_KERNEL_PREFILL_MFMA_F32;
+}
+
+const char* kernel_name(int id) {
+    switch (id) {
+        case FA_KERNEL_PREFILL_MFMA_BF16: return "prefill_mfma16<bf16> (K rotated on load)";
+        case FA_KERNEL_PREFILL_MFMA_F16: return "prefill_mfma16<f16> (K rotated on load)";
+        case FA_KERNEL_PREFILL_MFMA_F32: return "prefill_mfma_f32";
+        case FA_KERNEL_PREFILL_MFMA_BF16_PREROT: return "rotate_rows + prefill_mfma16<bf16>";
+        case FA_KERNEL_PREFILL_MFMA_F16_PREROT: return "rotate_rows + prefill_mfma16<f16>";
+        case FA_KERNEL_PREFILL_MFMA_F32_PREROT: return "rotate_rows + prefill_mfma_f32";
+        case FA_KERNEL_DECODE_PAGED_SPLITK: return "decode_splitk + decode_combine";
+        default: return "none";
+    }
+}
+
+// Common launch of the prefill kernel. `k_layout_rows`/`k_period`/`k_heads` describe how to
+// pre-rotate contiguous K (rows of k_heads*D elements, row r at position kv_rope_offset +
+// r % k_period) when the pre-rotation variant is selected.
+struct PrefillJob {
+    fa::PrefillArgs a;
+    Dtype dt;
+    int dtype;
+    bool paged = false;
+    bool rope = false;
+    float theta = 0.0f;
+    uint64_t max_pos = 0;  // highest RoPE position used + 1
+    uint64_t kv_bytes = 0;
+    uint64_t k_rows = 0, k_heads = 0, k_period = 0;
+};
+
+int run_prefill(fa_ctx* ctx, PrefillJob& j) {
+    const float2* table = nullptr;
+    bool prerot = false;
+    if (j.rope) {
+        if (int rc = ensure_rope(ctx, j.theta, (uint64_t)j.a.head_dim, j.max_pos, &table)) return rc;
+        j.a.rope_table = table;
+        prerot = j.a.rope_k && !j.paged && want_prerotate(ctx, (uint64_t)j.a.head_dim);
+    }
+    uint32_t dispatches = 0;
+    if (prerot) {
+        void* ws = nullptr;
+        if (int rc = ensure_ws(ctx, j.kv_bytes, &ws)) return rc;
+        fa::launch_rotate_rows(j.dt, j.a.k, ws, (int)j.k_rows, (int)j.k_heads, j.a.head_dim,
+                               (int64_t)j.k_period, table, j.a.kv_rope_offset, ctx->stream);
+        HIP_TRY(hipGetLastError());
+        j.a.k = ws;
+        j.a.rope_k = 0;
+        dispatches++;
+    }
+    unsigned grid[3], block = 0;
+    fa::launch_prefill(j.dt, j.paged, j.a, ctx->stream, grid, &block);
+    HIP_TRY(hipGetLastError());
+    dispatches++;
+    const int kid = prefill_kernel_id(j.dtype, prerot);
+    const char* fb = nullptr;
+    if (j.rope && j.a.rope_k && !prerot && !j.paged && j.a.head_dim % 8 != 0)
+        fb = "K pre-rotation pass needs head_dim % 8 == 0; K rotated on load";
+    record(ctx, kid, kernel_name(kid), 128, 64, grid, block, dispatches, 1, fb);
+    return FA_OK;
+}
+
+int validate_grouped(uint64_t b, uint64_t hq, uint64_t hkv, uint64_t s, uint64_t d) {
+    if (!b || !hq || !hkv || !s || !d)
+        return fail(FA_ERR_ZERO_DIMENSION, "attention dimensions must all be non-zero");
+    if (hq % hkv)
+        return fail(FA_ERR_INVALID_HEAD_GROUPING,
+                    "q_heads (%llu) must be exactly divisible by kv_heads (%llu)",
+                    (unsigned long long)hq, (unsigned long long)hkv);
+    uint64_t t;
+    if (mul_ov(b, hq, &t) || mul_ov(t, s, &t) || mul_ov(t, d, &t))
+        return fail(FA_ERR_SHAPE_OVERFLOW, "attention shape overflows the address space");
+    if (s > kI32 / std::max<uint64_t>(1, hq / hkv) || b * hkv > kI32)
+        return fail(FA_ERR_INDEX_SPACE_EXCEEDED, "attention exceeds the i32 index space at %llu rows",
+                    (unsigned long long)s);
+    return FA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int fa_forward_gqa_rope(fa_ctx* ctx, const void* q, size_t q_bytes, const void* k,
+                        const void* v, size_t kv_bytes, void* out_lse, size_t out_bytes,
+                        const fa_grouped_shape* sh, const fa_config* cfg, const fa_rotary* rot,
+                        int dtype) {
+    if (!sh) return fail(FA_ERR_NULL_ARGUMENT, "shape is null");
+    if (int rc = check_dtype(dtype)) return rc;
+    if (int rc = validate_grouped(sh->batch, sh->q_heads, sh->kv_heads, sh->seq_len, sh->head_dim))
+        return rc;
+    if (rot)
+        if (int rc = check_rotary(rot->theta, rot->position_offset, sh->head_dim, sh->seq_len))
+            return rc;
+    if (int rc = check_head_dim(sh->head_dim, dtype)) return rc;
+    float scale;
+    if (int rc = resolve_scale(cfg, sh->head_dim, &scale)) return rc;
+    const uint64_t eb = elem_bytes(dtype);
+    const uint64_t qn = sh->batch * sh->q_heads * sh->seq_len * sh->head_dim;
+    const uint64_t kvn = sh->batch * sh->kv_heads * sh->seq_len * sh->head_dim;
+    fa_packed_layout lay;
+    if (int rc = fa_packed_layout_for(qn, sh->batch * sh->q_heads * sh->seq_len, dtype, &lay)) return rc;
+    if (int rc = check_buffer("Q", q, q_bytes, qn * eb)) return rc;
+    if (int rc = check_buffer("K", k, kv_bytes, kvn * eb)) return rc;
+    if (int rc = check_buffer("V", v, kv_bytes, kvn * eb)) return rc;
+    if (int rc = check_buffer("O|LSE", out_lse, out_bytes, lay.combined_bytes)) return rc;
+    if (!ctx) return fail(FA_ERR_NULL_ARGUMENT, "context is null");
+    begin_call(ctx);
+    if (int rc = set_device(ctx)) return rc;
+
+    PrefillJob j{};
+    j.dt = (Dtype)dtype;
+    j.dtype = dtype;
+    fa::PrefillArgs& a = j.a;
+    const int64_t S = (int64_t)sh->seq_len, D = (int64_t)sh->head_dim;
+    a.q = q; a.k = k; a.v = v;
+    a.o = out_lse;
+    a.lse = (float*)((uint8_t*)out_lse + lay.lse_byte_offset);
+    a.q_sb = (int64_t)sh->q_heads * S * D; a.q_sh = S * D; a.q_ss = D;
+    a.k_sb = (int64_t)sh->kv_heads * S * D; a.k_sh = S * D; a.k_ss = D;
+    a.o_sb = a.q_sb; a.o_sh = a.q_sh; a.o_ss = a.q_ss;
+    a.lse_sb = (int64_t)sh->q_heads * S; a.lse_sh = S;
+    a.batch = (int)sh->batch; a.q_heads = (int)sh->q_heads; a.kv_heads = (int)sh->kv_heads;
+    a.group = (int)(sh->q_heads / sh->kv_heads);
+    a.q_len = (int)S; a.kv_len = (int)S; a.head_dim = (int)D;
+    a.causal = cfg && cfg->causal; a.causal_offset = 0;
+    a.scale = scale;
+    if (rot) {
+        j.rope = true;
+        j.theta = rot->theta;
+        a.rope_q = 1; a.rope_k = 1;
+        a.q_rope_offset = (int)rot->position_offset;
+        a.kv_rope_offset = (int)rot->position_offset;
+        j.max_pos = rot->position_offset + sh->seq_len;
+        j.kv_bytes = kvn * eb;
+        j.k_rows = sh->batch * sh->kv_heads * sh->seq_len;
+        j.k_heads = 1;
+        j.k_period = sh->seq_len;
+    }
+    if (int rc = run_prefill(ctx, j)) return rc;
+    return ok();
+}
+
+int fa_forward_mha(fa_ctx* ctx, const void* q, const void* k, const void* v, size_t in_bytes,
+                   void* out_lse, size_t out_bytes, const fa_attention_shape* shape,
+                   const fa_config* config, int dtype) {
+    if (!shape) return fail(FA_ERR_NULL_ARGUMENT, "shape is null");
+    fa_grouped_shape g{shape->batch, shape->heads, shape->heads, shape->seq_len, shape->head_dim};
+    return fa_forward_gqa_rope(ctx, q, in_bytes, k, v, in_bytes, out_lse, out_bytes, &g, config,
+                               nullptr, dtype);
+}
+
+int fa_forward_projection_asymmetric(fa_ctx* ctx, const void* q, size_t q_bytes, const void* k,
+                                     const void* v, size_t kv_bytes, void* out_lse,
+                                     size_t out_bytes, const fa_asymmetric_shape* sh,
+                                     const fa_config* cfg, const fa_asymmetric_rotary* rot,
+                                     int32_t rotate_k, int dtype) {
+    if (!sh) return fail(FA_ERR_NULL_ARGUMENT, "shape is null");
+    if (int rc = check_dtype(dtype)) return rc;
+    if (!sh->batch || !sh->q_heads || !sh->kv_heads || !sh->query_len || !sh->kv_len ||
+        !sh->head_dim)
+        return fail(FA_ERR_ZERO_DIMENSION, "attention dimensions must all be non-zero");
+    if (sh->q_heads % sh->kv_heads)
+        return fail(FA_ERR_INVALID_HEAD_GROUPING,
+                    "q_heads (%llu) must be exactly divisible by kv_heads (%llu)",
+                    (unsigned long long)sh->q_heads, (unsigned long long)sh->kv_heads);
+    if (int rc = validate_grouped(sh->batch, sh->q_heads, sh->kv_heads,
+                                  std::max(sh->query_len, sh->kv_len), sh->head_dim))
+        return rc;
+    if (sh->query_position_offset + sh->query_len > kI32)
+        return fail(FA_ERR_POSITION_OVERFLOW, "rotary position offset overflows the index space");
+    if (rot) {
+        if (int rc = check_rotary(rot->theta, rot->query_position_offset, sh->head_dim, sh->query_len))
+            return rc;
+        if (int rc = check_rotary(rot->theta, rot->kv_position_offset, sh->head_dim, sh->kv_len))
+            return rc;
+    }
+    if (int rc = check_head_dim(sh->head_dim, dtype)) return rc;
+    float scale;
+    if (int rc = resolve_scale(cfg, sh->head_dim, &scale)) return rc;
+    const uint64_t eb = elem_bytes(dtype);
+    const uint64_t qn = sh->batch * sh->query_len * sh->q_heads * sh->head_dim;
+    const uint64_t kvn = sh->batch * sh->kv_len * sh->kv_heads * sh->head_dim;
+    fa_packed_layout lay;
+    if (int rc = fa_packed_layout_for(qn, sh->batch * sh->q_heads * sh->query_len, dtype, &lay))
+        return rc;
+    if (int rc = check_buffer("Q", q, q_bytes, qn * eb)) return rc;
+    if (int rc = check_buffer("K", k, kv_bytes, kvn * eb)) return rc;
+    if (int rc = check_buffer("V", v, kv_bytes, kvn * eb)) return rc;
+    if (int rc = check_buffer("O|LSE", out_lse, out_bytes, lay.combined_bytes)) return rc;
+    if (!ctx) return fail(FA_ERR_NULL_ARGUMENT, "context is null");
+    begin_call(ctx);
+    if (int rc = set_device(ctx)) return rc;
+
+    PrefillJob j{};
+    j.dt = (Dtype)dtype;
+    j.dtype = dtype;
+    fa::PrefillArgs& a = j.a;
+    const int64_t D = (int64_t)sh->head_dim, QW = (int64_t)sh->q_heads * D,
+                  KW = (int64_t)sh->kv_heads * D;
+    a.q = q; a.k = k; a.v = v;
+    a.o = out_lse;
+    a.lse = (float*)((uint8_t*)out_lse + lay.lse_byte_offset);
+    a.q_sb = (int64_t)sh->query_len * QW; a.q_sh = D; a.q_ss = QW;
+    a.k_sb = (int64_t)sh->kv_len * KW; a.k_sh = D; a.k_ss = KW;
+    a.o_sb = a.q_sb; a.o_sh = a.q_sh; a.o_ss = a.q_ss;
+    a.lse_sb = (int64_t)sh->q_heads * sh->query_len; a.lse_sh = (int64_t)sh->query_len;
+    a.batch = (int)sh->batch; a.q_heads = (int)sh->q_heads; a.kv_heads = (int)sh->kv_heads;
+    a.group = (int)(sh->q_heads / sh->kv_heads);
+    a.q_len = (int)sh->query_len; a.kv_len = (int)sh->kv_len; a.head_dim = (int)D;
+    a.causal = cfg && cfg->causal;
+    a.causal_offset = (int)sh->query_position_offset;
+    a.scale = scale;
+    if (rot) {
+        j.rope = true;
+        j.theta = rot->theta;
+        a.rope_q = 1;
+        a.rope_k = rotate_k ? 1 : 0;
+        a.q_rope_offset = (int)rot->query_position_offset;
+        a.kv_rope_offset = (int)rot->kv_position_offset;
+        j.max_pos = std::max(rot->query_position_offset + sh->query_len,
+                             rot->kv_position_offset + sh->kv_len);
+        j.kv_bytes = kvn * eb;
+        j.k_rows = sh->batch * sh->kv_len;
+        j.k_heads = sh->kv_heads;
+        j.k_period = sh->kv_len;
+    }
+    if (int rc = run_prefill(ctx, j)) return rc;
+    return ok();
+}
+
+int fa_chunked_prefill(fa_ctx* ctx, const void* q, size_t q_bytes, const void* k, const void* v,
+                       size_t kv_bytes, void* out_lse, size_t out_bytes,
+                       const fa_grouped_shape* sh, const fa_config* cfg, const fa_rotary* rot,
+                       uint64_t query_chunk_size, int dtype) {
+    if (!sh || !rot) return fail(FA_ERR_NULL_ARGUMENT, "null argument");
+    if (query_chunk_size == 0)
+        return fail(FA_ERR_ZERO_QUERY_CHUNK_SIZE,
+                    "chunked projection prefill requires a non-zero query chunk size");
+    if (int rc = validate_grouped(sh->batch, sh->q_heads, sh->kv_heads, sh->seq_len, sh->head_dim))
+        return rc;
+    if (int rc = check_rotary(rot->theta, rot->position_offset, sh->head_dim, sh->seq_len)) return rc;
+    // Every query row's K/V visitation order and online-softmax arithmetic are independent of
+    // the chunk it belongs to (src/chunked_projection_prefill.rs:1-7), so all chunks run in one
+    // launch whose result is identical for every chunk size.
+    fa_asymmetric_shape as{sh->batch, sh->q_heads, sh->kv_heads, sh->seq_len, sh->seq_len,
+                           sh->head_dim, 0};
+    fa_asymmetric_rotary ar{rot->theta, rot->position_offset, rot->position_offset};
+    return fa_forward_projection_asymmetric(ctx, q, q_bytes, k, v, kv_bytes, out_lse, out_bytes,
+                                            &as, cfg, &ar, 1, dtype);
+}
+
+int fa_kernel_variant_for_shape(fa_ctx* ctx, uint64_t head_dim, int32_t has_rope, int dtype,
+                                int32_t* kernel_id) {
+    if (!ctx || !kernel_id) return fail(FA_ERR_NULL_ARGUMENT, "null argument");
+    if (int rc = check_dtype(dtype)) return rc;
+    if (int rc = check_head_dim(head_dim, dtype)) return rc;
+    *kernel_id = prefill_kernel_id(dtype, has_rope && want_prerotate(ctx, head_dim));
+    return ok();
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------- host forwards
+namespace {
+
+bool finite16(uint16_t h, int dtype) {
+    return dtype == FA_DTYPE_BF16 ? (h & 0x7f80u) != 0x7f80u : (h & 0x7c00u) != 0x7c00u;
+}
+
+int validate_host_input(const char* name, const void* data, uint64_t len, uint64_t expected,
+                        int dtype) {
+    if (!data && len) return fail(FA_ERR_NULL_ARGUMENT, "tensor %s is null", name);
+    if (len != expected)
+        return fail(FA_ERR_LENGTH_MISMATCH, "tensor %s contains %llu elements, expected %llu", name,
+                    (unsigned long long)len, (unsigned long long)expected);
+    for (uint64_t i = 0; i < len; ++i) {
+        bool fin = dtype == FA_DTYPE_F32 ? std::isfinite(((const float*)data)[i])
+                                         : finite16(((const uint16_t*)data)[i], dtype);
+        if (!fin)
+            return fail(FA_ERR_NON_FINITE_INPUT, "tensor %s contains a non-finite value at index %llu",
+                        name, (unsigned long long)i);
+    }
+    return FA_OK;
+}
+
+struct DevBuf {
+    void* p = nullptr;
+    ~DevBuf() {
+        if (p) (void)hipFree(p);
+    }
+};
+
+}  // namespace
+
+extern "C" {
+
+int fa_forward_gqa_rope_host(fa_ctx* ctx, const void* q, const void* k, const void* v,
+                             uint64_t q_len, uint64_t k_len, uint64_t v_len,
+                             const fa_grouped_shape* sh, const fa_config* cfg,
+                             const fa_rotary* rot, int dtype, void* out, float* lse) {
+    if (!sh || !out || !lse) return fail(FA_ERR_NULL_ARGUMENT, "null argument");
+    if (int rc = check_dtype(dtype)) return rc;
+    if (int rc = validate_grouped(sh->batch, sh->q_heads, sh->kv_heads, sh->seq_len, sh->head_dim))
+        return rc;
+    if (rot)
+        if (int rc = check_rotary(rot->theta, rot->position_offset, sh->head_dim, sh->seq_len))
+            return rc;
+    const uint64_t qn = sh->batch * sh->q_heads * sh->seq_len * sh->head_dim;
+    const uint64_t kvn = sh->batch * sh->kv_heads * sh->seq_len * sh->head_dim;
+    if (int rc = validate_host_input("Q", q, q_len, qn, dtype)) return rc;
+    if (int rc = validate_host_input("K", k, k_len, kvn, dtype)) return rc;
+    if (int rc = validate_host_input("V", v, v_len, kvn, dtype)) return rc;
+    float scale;
+    if (int rc = resolve_scale(cfg, sh->head_dim, &scale)) return rc;
+    if (int rc = check_head_dim(sh->head_dim, dtype)) return rc;
+    const uint64_t eb = elem_bytes(dtype);
+    fa_packed_layout lay;
+    if (int rc = fa_packed_layout_for(qn, sh->batch * sh->q_heads * sh->seq_len, dtype, &lay)) return rc;
+    if (!ctx) return fail(FA_ERR_NULL_ARGUMENT, "context is null");
+    if (int rc = set_device(ctx)) return rc;
+    DevBuf dq, dk, dv, dout;
+    HIP_TRY(hipMalloc(&dq.p, qn * eb));
+    HIP_TRY(hipMalloc(&dk.p, kvn * eb));
+    HIP_TRY(hipMalloc(&dv.p, kvn * eb));
+    HIP_TRY(hipMalloc(&dout.p, lay.combined_bytes));
+    HIP_TRY(hipMemcpyAsync(dq.p, q, qn * eb, hipMemcpyHostToDevice, ctx->stream));
+    HIP_TRY(hipMemcpyAsync(dk.p, k, kvn * eb, hipMemcpyHostToDevice, ctx->stream));
+    HIP_TRY(hipMemcpyAsync(dv.p, v, kvn * eb, hipMemcpyHostToDevice, ctx->stream));
+    int rc = fa_forward_gqa_rope(ctx, dq.p, qn * eb, dk.p, dv.p, kvn * eb, dout.p,
+                                 lay.combined_bytes, sh, cfg, rot, dtype);
+    if (rc) {
+        (void)hipStreamSynchronize(ctx->stream);
+        return rc;
+    }
+    ctx->last.temporary_allocation_count += 4;
+    ctx->last.temporary_allocation_bytes += 2 * qn * eb + 2 * kvn * eb;
+    HIP_TRY(hipMemcpyAsync(out, dout.p, lay.output_bytes, hipMemcpyDeviceToHost, ctx->stream));
+    HIP_TRY(hipMemcpyAsync(lse, (uint8_t*)dout.p + lay.lse_byte_offset, lay.lse_elements * 4,
+                           hipMemcpyDeviceToHost, ctx->stream));
+    HIP_TRY(hipStreamSynchronize(ctx->stream));
+    return ok();
+}
+
+int fa_forward_mha_host(fa_ctx* ctx, const void* q, const void* k, const void* v,
+                        uint64_t q_len, uint64_t k_len, uint64_t v_len,
+                        const fa_attention_shape* shape, const fa_config* config, int dtype,
+                        void* out, float* lse) {
+    if (!shape) return fail(FA_ERR_NULL_ARGUMENT, "shape is null");
+    if (!shape->batch || !shape->heads || !shape->seq_len || !shape->head_dim)
+        return fail(FA_ERR_ZERO_DIMENSION, "attention dimensions must all be non-zero");
+    fa_grouped_shape g{shape->batch, shape->heads, shape->heads, shape->seq_len, shape->head_dim};
+    return fa_forward_gqa_rope_host(ctx, q, k, v, q_len, k_len, v_len, &g, config, nullptr, dtype,
+                                    out, lse);
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------- paged KV table
+struct fa_kv_table {
+    uint64_t page_size = 0, physical_pages = 0, live = 0, generation = 0;
+    std::vector<std::pair<uint64_t, uint64_t>> logical;  // (physical page, generation)
+    std::vector<uint64_t> free_pages;                     // stack, lowest id on top
+};
+
+namespace {
+
+int table_capacity(const fa_kv_table* t, uint64_t* cap) {
+    if (!t->page_size || !t->physical_pages)
+        return fail(FA_ERR_PAGED_ZERO_DIMENSION, "paged KV dimensions must be non-zero");
+    if (mul_ov(t->page_size, t->physical_pages, cap))
+        return fail(FA_ERR_CAPACITY_OVERFLOW, "paged KV capacity overflows usize");
+    return FA_OK;
+}
+
+void fill_free(fa_kv_table* t) {
+    t->free_pages.clear();
+    t->free_pages.reserve(t->physical_pages);
+    for (uint64_t p = t->physical_pages; p-- > 0;) t->free_pages.push_back(p);
+}
+
+}  // namespace
+
+extern "C" {
+
+int fa_kv_table_create(uint64_t page_size, uint64_t physical_pages, fa_kv_table** out) {
+    if (!out) return fail(FA_ERR_NULL_ARGUMENT, "output pointer is null");
+    fa_kv_table tmp;
+    tmp.page_size = page_size;
+    tmp.physical_pages = physical_pages;
+    uint64_t cap;
+    if (int rc = table_capacity(&tmp, &cap)) return rc;
+    fa_kv_table* t = new fa_kv_table(tmp);
+    fill_free(t);
+    *out = t;
+    return ok();
+}
+
+int fa_kv_table_destroy(fa_kv_table* t) {
+    delete t;
+    return ok();
+}
+
+int fa_kv_table_clone(const fa_kv_table* t, fa_kv_table** out) {
+    if (!t || !out) return fail(FA_ERR_NULL_ARGUMENT, "null argument");
+    *out = new fa_kv_table(*t);
+    return ok();
+}
+
+int fa_kv_table_append(fa_kv_table* t, uint64_t tokens) {
+    if (!t) return fail(FA_ERR_NULL_ARGUMENT, "table is null");
+    if (tokens == 0) return ok();
+    if (t->live > std::numeric_limits<uint64_t>::max() - tokens)
+        return fail(FA_ERR_CAPACITY_OVERFLOW, "paged KV capacity overflows usize");
+    const uint64_t new_len = t->live + tokens;
+    uint64_t cap;
+    if (int rc = table_capacity(t, &cap)) return rc;
+    if (new_len > cap)
+        return fail(FA_ERR_CAPACITY_EXCEEDED, "paged KV append requires %llu tokens, capacity is %llu",
+                    (unsigned long long)new_len, (unsigned long long)cap);
+    const uint64_t required = (new_len + t->page_size - 1) / t->page_size;
+    while (t->logical.size() < required) {
+        const uint64_t p = t->free_pages.back();
+        t->free_pages.pop_back();
+        t->logical.push_back({p, t->generation});
+    }
+    t->live = new_len;
+    return ok();
+}
+
+int fa_kv_table_address(const fa_kv_table* t, uint64_t logical_token, fa_kv_address* out) {
+    if (!t || !out) return fail(FA_ERR_NULL_ARGUMENT, "null argument");
+    if (logical_token >= t->live) return fail(FA_ERR_EMPTY_TABLE, "logical token is not mapped");
+    const uint64_t lp = logical_token / t->page_size;
+    if (lp >= t->logical.size() || t->logical[lp].second != t->generation)
+        return fail(FA_ERR_EMPTY_TABLE, "logical token is not mapped");
+    out->physical_page = t->logical[lp].first;
+    out->offset_in_page = logical_token % t->page_size;
+    out->generation = t->logical[lp].second;
+    return ok();
+}
+
+int fa_kv_table_telemetry(const fa_kv_table* t, fa_kv_telemetry* out) {
+    if (!t || !out) return fail(FA_ERR_NULL_ARGUMENT, "null argument");
+    uint64_t cap;
+    if (int rc = table_capacity(t, &cap)) return rc;
+    uint64_t alloc;
+    if (mul_ov((uint64_t)t->logical.size(), t->page_size, &alloc))
+        return fail(FA_ERR_CAPACITY_OVERFLOW, "paged KV capacity overflows usize");
+    out->live_tokens = t->live;
+    out->capacity_tokens = cap;
+    out->mapped_pages = t->logical.size();
+    out->free_pages = t->free_pages.size();
+    out->internal_fragmentation_tokens = alloc - t->live;
+    out->generation = t->generation;
+    return ok();
+}
+
+int fa_kv_table_reset(fa_kv_table* t) {
+    if (!t) return fail(FA_ERR_NULL_ARGUMENT, "table is null");
+    if (t->generation == std::numeric_limits<uint64_t>::max())
+        return fail(FA_ERR_GENERATION_OVERFLOW, "paged KV generation counter overflowed");
+    t->generation += 1;
+    t->live = 0;
+    t->logical.clear();
+    fill_free(t);
+    return ok();
+}
+
+uint64_t fa_kv_table_len(const fa_kv_table* t) { return t ? t->live : 0; }
+
+int fa_kv_table_block_row(const fa_kv_table* t, int32_t* out, uint64_t capacity, uint64_t* count) {
+    if (!t || !count) return fail(FA_ERR_NULL_ARGUMENT, "null argument");
+    if (t->live == 0 || t->logical.empty())
+        return fail(FA_ERR_EMPTY_TABLE, "paged decode requires at least one live KV token");
+    *count = t->logical.size();
+    if (!out) return ok();
+    if (capacity < t->logical.size())
+        return fail(FA_ERR_BUFFER_TOO_SMALL, "block row holds %llu entries, requires %llu",
+                    (unsigned long long)capacity, (unsigned long long)t->logical.size());
+    for (size_t i = 0; i < t->logical.size(); ++i) {
+        if (t->logical[i].first > kI32)
+            return fail(FA_ERR_INDEX_SPACE_EXCEEDED, "physical page %llu exceeds the i32 index space",
+                        (unsigned long long)t->logical[i].first);
+        out[i] = (int32_t)t->logical[i].first;
+    }
+    return ok();
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------- paged cache
+struct fa_paged_cache {
+    fa_ctx* ctx = nullptr;
+    fa_kv_table table;
+    uint64_t kv_heads = 0, head_dim = 0, row_bytes = 0, tensor_bytes = 0;
+    int dtype = 0;
+    void* k = nullptr;
+    void* v = nullptr;
+};
+
+extern "C" {
+
+int fa_paged_cache_create(fa_ctx* ctx, uint64_t page_size, uint64_t physical_pages,
+                          uint64_t kv_heads, uint64_t head_dim, int dtype, fa_paged_cache** out) {
+    if (!ctx || !out) return fail(FA_ERR_NULL_ARGUMENT, "null argument");
+    if (int rc = check_dtype(dtype)) return rc;
+    if (!kv_heads || !head_dim)
+        return fail(FA_ERR_ZERO_DIMENSION, "paged resident KV dimensions must be non-zero");
+    fa_kv_table* t = nullptr;
+    if (int rc = fa_kv_table_create(page_size, physical_pages, &t)) return rc;
+    uint64_t row_el, row_b, cap, bytes;
+    if (mul_ov(kv_heads, head_dim, &row_el) || mul_ov(row_el, elem_bytes(dtype), &row_b) ||
+        mul_ov(page_size, physical_pages, &cap) || mul_ov(cap, row_b, &bytes)) {
+        delete t;
+        return fail(FA_ERR_SHAPE_OVERFLOW, "paged resident KV shape overflows the address space");
+    }
+    if (int rc = set_device(ctx)) {
+        delete t;
+        return rc;
+    }
+    fa_paged_cache* c = new fa_paged_cache();
+    c->ctx = ctx;
+    c->table = *t;
+    delete t;
+    c->kv_heads = kv_heads;
+    c->head_dim = head_dim;
+    c->row_bytes = row_b;
+    c->tensor_bytes = bytes;
+    c->dtype = dtype;
+    if (hipMalloc(&c->k, bytes) != hipSuccess || hipMalloc(&c->v, bytes) != hipSuccess) {
+        if (c->k) (void)hipFree(c->k);
+        delete c;
+        return fail(FA_ERR_HIP, "paged resident KV requires %llu bytes per tensor",
+                    (unsigned long long)bytes);
+    }
+    *out = c;
+    return ok();
+}
+
+int fa_paged_cache_destroy(fa_paged_cache* c) {
+    if (!c) return ok();
+    (void)hipSetDevice(c->ctx->device);
+    (void)hipStreamSynchronize(c->ctx->stream);
+    (void)hipFree(c->k);
+    (void)hipFree(c->v);
+    delete c;
+    return ok();
+}
+
+int fa_paged_cache_append(fa_paged_cache* c, const void* k_src, const void* v_src,
+                          size_t src_bytes, uint64_t append_len, const fa_rotary* rot,
+                          uint64_t* new_len) {
+    if (!c) return fail(FA_ERR_NULL_ARGUMENT, "cache is null");
+    fa_ctx* ctx = c->ctx;
+    begin_call(ctx);
+    if (append_len == 0)
+        return fail(FA_ERR_ZERO_DIMENSION, "paged resident KV dimensions must be non-zero");
+    uint64_t need;
+    if (mul_ov(append_len, c->row_bytes, &need))
+        return fail(FA_ERR_SHAPE_OVERFLOW, "paged resident KV shape overflows the address space");
+    if (int rc = check_buffer("K", k_src, src_bytes, need)) return rc;
+    if (int rc = check_buffer("V", v_src, src_bytes, need)) return rc;
+    const float2* table = nullptr;
+    if (rot) {
+        if (int rc = check_rotary(rot->theta, rot->position_offset, c->head_dim,
+                                  c->table.live + append_len))
+            return rc;
+        if (c->head_dim % 8 != 0)
+            return fail(FA_ERR_UNSUPPORTED_HEAD_DIM,
+                        "rotate-on-append needs head_dim %% 8 == 0, got %llu",
+                        (unsigned long long)c->head_dim);
+    }
+    fa_kv_table staged = c->table;
+    const uint64_t old_len = staged.live;
+    if (int rc = fa_kv_table_append(&staged, append_len)) return rc;
+    if (int rc = set_device(ctx)) return rc;
+    if (rot) {
+        if (int rc = ensure_rope(ctx, rot->theta, c->head_dim,
+                                 rot->position_offset + staged.live, &table))
+            return rc;
+    }
+    uint32_t dispatches = 0;
+    uint64_t logical = old_len, src_row = 0;
+    while (logical < staged.live) {
+        fa_kv_address addr;
+        if (int rc = fa_kv_table_address(&staged, logical, &addr)) return rc;
+        const uint64_t rows = std::min(staged.page_size - addr.offset_in_page, staged.live - logical);
+        const uint64_t prow = addr.physical_page * staged.page_size + addr.offset_in_page;
+        const uint64_t so = src_row * c->row_bytes, dof = prow * c->row_bytes;
+        if (dof + rows * c->row_bytes > c->tensor_bytes)
+            return fail(FA_ERR_SHAPE_OVERFLOW, "paged resident KV shape overflows the address space");
+        if (rot) {
+            fa::launch_rotate_rows((Dtype)c->dtype, (const uint8_t*)k_src + so, (uint8_t*)c->k + dof,
+                                   (int)rows, (int)c->kv_heads, (int)c->head_dim, (int64_t)kI32,
+                                   table, (int)(rot->position_offset + logical), ctx->stream);
+            HIP_TRY(hipGetLastError());
+        } else {
+            HIP_TRY(hipMemcpyAsync((uint8_t*)c->k + dof, (const uint8_t*)k_src + so,
+                                   rows * c->row_bytes, hipMemcpyDeviceToDevice, ctx->stream));
+        }
+        HIP_TRY(hipMemcpyAsync((uint8_t*)c->v + dof, (const uint8_t*)v_src + so, rows * c->row_bytes,
+                               hipMemcpyDeviceToDevice, ctx->stream));
+        dispatches += 2;
+        logical += rows;
+        src_row += rows;
+    }
+    c->table = staged;
+    if (new_len) *new_len = staged.live;
+    unsigned grid[3] = {(unsigned)append_len, 1, 1};
+    record(ctx, FA_KERNEL_PAGED_APPEND, "paged append (per-page copies)", 0,
+           (uint32_t)c->table.page_size, grid, 0, dispatches, 1, nullptr);
+    return ok();
+}
+
+int fa_paged_cache_reset(fa_paged_cache* c) {
+    if (!c) return fail(FA_ERR_NULL_ARGUMENT, "cache is null");
+    return fa_kv_table_reset(&c->table);
+}
+
+const fa_kv_table* fa_paged_cache_table(const fa_paged_cache* c) { return c ? &c->table : nullptr; }
+void* fa_paged_cache_k(fa_paged_cache* c) { return c ? c->k : nullptr; }
+void* fa_paged_cache_v(fa_paged_cache* c) { return c ? c->v : nullptr; }
+size_t fa_paged_cache_bytes(const fa_paged_cache* c) { return c ? (size_t)c->tensor_bytes : 0; }
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------- paged decode
+struct fa_decode_plan {
+    fa_ctx* ctx = nullptr;
+    uint64_t n_seqs = 0, max_pages = 0, page_size = 0, physical_pages = 0;
+    uint64_t q_heads = 0, kv_heads = 0, head_dim = 0;
+    int dtype = 0;
+    float scale = 0.0f, theta = 0.0f;
+    std::vector<int32_t> ctx_lens;
+    uint64_t split_tokens = 0;
+    uint64_t n_work = 0;
+    uint64_t max_pos = 0;
+    // device
+    int32_t* d_bt = nullptr;
+    int32_t* d_ctx = nullptr;
+    int32_t* d_qpos = nullptr;
+    int32_t* d_work = nullptr;  // [work_seq | work_split | seq_work_off]
+    float* d_part = nullptr;    // partial O then (m, l)
+    uint64_t part_bytes = 0;
+    uint64_t work_cap = 0;
+};
+
+namespace {
+
+uint64_t auto_split(const fa_decode_plan* p) {
+    uint64_t total = 0;
+    for (int32_t c : p->ctx_lens) total += (uint64_t)c;
+    const uint64_t chunks = (p->q_heads / p->kv_heads + 15) / 16;
+    // Aim for ~8192 resident waves (32 per CU) so every CU streams several pages at once.
+    uint64_t st = total * p->kv_heads * chunks / 8192;
+    st = std::max<uint64_t>(64, std::min<uint64_t>(st, 4096));
+    return (st + 15) / 16 * 16;
+}
+
+int build_work(fa_decode_plan* p) {
+    fa_ctx* ctx = p->ctx;
+    std::vector<int32_t> wseq, wsplit, off(p->n_seqs + 1, 0);
+    for (uint64_t s = 0; s < p->n_seqs; ++s) {
+        const uint64_t n = ((uint64_t)p->ctx_lens[s] + p->split_tokens - 1) / p->split_tokens;
+        off[s] = (int32_t)wseq.size();
+        for (uint64_t j = 0; j < n; ++j) {
+            wseq.push_back((int32_t)s);
+            wsplit.push_back((int32_t)j);
+        }
+    }
+    off[p->n_seqs] = (int32_t)wseq.size();
+    p->n_work = wseq.size();
+    if (p->n_work > kI32)
+        return fail(FA_ERR_DISPATCH_LIMIT, "paged decode requires %llu workgroups",
+                    (unsigned long long)p->n_work);
+    const uint64_t need_work = 2 * p->n_work + p->n_seqs + 1;
+    if (p->work_cap < need_work) {
+        if (p->d_work) HIP_TRY(hipFree(p->d_work));
+        p->d_work = nullptr;
+        if (int rc = dev_alloc(ctx, (void**)&p->d_work, need_work * 4)) return rc;
+        p->work_cap = need_work;
+    }
+    std::vector<int32_t> all;
+    all.reserve(need_work);
+    all.insert(all.end(), wseq.begin(), wseq.end());
+    all.insert(all.end(), wsplit.begin(), wsplit.end());
+    all.insert(all.end(), off.begin(), off.end());
+    HIP_TRY(hipMemcpy(p->d_work, all.data(), need_work * 4, hipMemcpyHostToDevice));
+    const uint64_t part = p->n_work * p->q_heads * (p->head_dim + 2) * 4;
+    if (p->part_bytes < part) {
+        if (p->d_part) HIP_TRY(hipFree(p->d_part));
+        p->d_part = nullptr;
+        if (int rc = dev_alloc(ctx, (void**)&p->d_part, part)) return rc;
+        p->part_bytes = part;
+    }
+    return FA_OK;
+}
+
+void free_plan(fa_decode_plan* p) {
+    if (p->d_bt) (void)hipFree(p->d_bt);
+    if (p->d_ctx) (void)hipFree(p->d_ctx);
+    if (p->d_qpos) (void)hipFree(p->d_qpos);
+    if (p->d_work) (void)hipFree(p->d_work);
+    if (p->d_part) (void)hipFree(p->d_part);
+    delete p;
+}
+
+int check_pages(const int32_t* bt, uint64_t max_pages, uint64_t n_seqs, uint64_t live_len,
+                const int32_t* lens, uint64_t page_size, uint64_t physical_pages) {
+    for (uint64_t s = 0; s < n_seqs; ++s) {
+        const uint64_t len = lens ? (uint64_t)lens[s] : live_len;
+        const uint64_t pages = (len + page_size - 1) / page_size;
+        if (pages > max_pages)
+            return fail(FA_ERR_INDEX_SPACE_EXCEEDED,
+                        "sequence %llu needs %llu pages, block table holds %llu",
+                        (unsigned long long)s, (unsigned long long)pages,
+                        (unsigned long long)max_pages);
+        for (uint64_t p = 0; p < pages; ++p) {
+            const int32_t id = bt[s * max_pages + p];
+            if (id < 0 || (uint64_t)id >= physical_pages)
+                return fail(FA_ERR_INVALID_PAGE,
+                            "sequence %llu logical page %llu maps to physical page %d outside [0, %llu)",
+                            (unsigned long long)s, (unsigned long long)p, id,
+                            (unsigned long long)physical_pages);
+        }
+    }
+    return FA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int fa_paged_decode_prepare(fa_ctx* ctx, const int32_t* block_tables, uint64_t max_pages,
+                            const int32_t* ctx_lens, const int32_t* q_positions, uint64_t n_seqs,
+                            uint64_t page_size, uint64_t physical_pages, uint64_t q_heads,
+                            uint64_t kv_heads, uint64_t head_dim, const fa_config* cfg,
+                            float theta, int dtype, fa_decode_plan** out) {
+    if (!out || !block_tables || !ctx_lens) return fail(FA_ERR_NULL_ARGUMENT, "null argument");
+    *out = nullptr;
+    if (int rc = check_dtype(dtype)) return rc;
+    if (!n_seqs || !q_heads || !kv_heads || !head_dim || !max_pages)
+        return fail(FA_ERR_ZERO_DIMENSION, "attention dimensions must all be non-zero");
+    if (!page_size || !physical_pages)
+        return fail(FA_ERR_PAGED_ZERO_DIMENSION, "paged KV dimensions must be non-zero");
+    if (q_heads % kv_heads)
+        return fail(FA_ERR_INVALID_HEAD_GROUPING,
+                    "q_heads (%llu) must be exactly divisible by kv_heads (%llu)",
+                    (unsigned long long)q_heads, (unsigned long long)kv_heads);
+    if (head_dim > kMaxHeadDim)
+        return fail(FA_ERR_UNSUPPORTED_HEAD_DIM, "head_dim %llu exceeds portable maximum %llu",
+                    (unsigned long long)head_dim, (unsigned long long)kMaxHeadDim);
+    if (head_dim % 2)
+        return fail(FA_ERR_INVALID_ROTARY_HEAD_DIM,
+                    "rotary attention head_dim must be non-zero and even, got %llu",
+                    (unsigned long long)head_dim);
+    if (head_dim % (dtype == FA_DTYPE_F32 ? 4 : 8))
+        return fail(FA_ERR_UNSUPPORTED_HEAD_DIM, "head_dim %llu is not a multiple of %d for %s decode",
+                    (unsigned long long)head_dim, dtype == FA_DTYPE_F32 ? 4 : 8, dtype_name(dtype));
+    if (!std::isfinite(theta) || theta <= 0.0f)
+        return fail(FA_ERR_INVALID_ROTARY_THETA,
+                    "paged decode RoPE theta must be finite and positive, got %g", (double)theta);
+    float scale;
+    if (int rc = resolve_scale(cfg, head_dim, &scale)) return rc;
+    uint64_t rows;
+    if (mul_ov(page_size, physical_pages, &rows) || rows > kI32 || max_pages > kI32 ||
+        n_seqs * max_pages > (uint64_t)std::numeric_limits<int64_t>::max() / 4)
+        return fail(FA_ERR_INDEX_SPACE_EXCEEDED, "paged decode exceeds the i32 index space");
+    uint64_t max_pos = 0;
+    std::vector<int32_t> qpos(n_seqs);
+    for (uint64_t s = 0; s < n_seqs; ++s) {
+        if (ctx_lens[s] <= 0)
+            return fail(FA_ERR_EMPTY_TABLE, "paged decode requires at least one live KV token");
+        const int32_t qp = q_positions ? q_positions[s] : ctx_lens[s] - 1;
+        if (qp < 0)
+            return fail(FA_ERR_POSITION_OVERFLOW, "rotary position offset overflows the index space");
+        if (cfg && cfg->causal && (int64_t)qp + 1 < (int64_t)ctx_lens[s])
+            return fail(FA_ERR_CAUSAL_VISIBILITY_MISMATCH,
+                        "paged causal decode query position %d cannot see all %d live KV tokens",
+                        qp, ctx_lens[s]);
+        qpos[s] = qp;
+        max_pos = std::max<uint64_t>(max_pos, (uint64_t)qp + 1);
+    }
+    if (int rc = check_pages(block_tables, max_pages, n_seqs, 0, ctx_lens, page_size, physical_pages))
+        return rc;
+    if (!ctx) return fail(FA_ERR_NULL_ARGUMENT, "context is null");
+    begin_call(ctx);
+    if (int rc = set_device(ctx)) return rc;
+
+    fa_decode_plan* p = new fa_decode_plan();
+    p->ctx = ctx;
+    p->n_seqs = n_seqs;
+    p->max_pages = max_pages;
+    p->page_size = page_size;
+    p->physical_pages = physical_pages;
+    p->q_heads = q_heads;
+    p->kv_heads = kv_heads;
+    p->head_dim = head_dim;
+    p->dtype = dtype;
+    p->scale = scale;
+    p->theta = theta;
+    p->ctx_lens.assign(ctx_lens, ctx_lens + n_seqs);
+    p->max_pos = max_pos;
+    int rc = FA_OK;
+    if (!rc) rc = dev_alloc(ctx, (void**)&p->d_bt, n_seqs * max_pages * 4);
+    if (!rc) rc = dev_alloc(ctx, (void**)&p->d_ctx, n_seqs * 4);
+    if (!rc) rc = dev_alloc(ctx, (void**)&p->d_qpos, n_seqs * 4);
+    if (!rc && hipMemcpy(p->d_bt, block_tables, n_seqs * max_pages * 4, hipMemcpyHostToDevice))
+        rc = fail(FA_ERR_HIP, "block table upload failed");
+    if (!rc && hipMemcpy(p->d_ctx, ctx_lens, n_seqs * 4, hipMemcpyHostToDevice))
+        rc = fail(FA_ERR_HIP, "context length upload failed");
+    if (!rc && hipMemcpy(p->d_qpos, qpos.data(), n_seqs * 4, hipMemcpyHostToDevice))
+        rc = fail(FA_ERR_HIP, "query position upload failed");
+    if (!rc) {
+        p->split_tokens = auto_split(p);
+        rc = build_work(p);
+    }
+    if (rc) {
+        free_plan(p);
+        return rc;
+    }
+    *out = p;
+    return ok();
+}
+
+int fa_paged_decode_plan_set_split(fa_ctx* ctx, fa_decode_plan* p, uint64_t split_tokens) {
+    if (!ctx || !p) return fail(FA_ERR_NULL_ARGUMENT, "null argument");
+    if (split_tokens % 16)
+        return fail(FA_ERR_INDEX_SPACE_EXCEEDED, "split size %llu is not a multiple of 16",
+                    (unsigned long long)split_tokens);
+    if (int rc = set_device(ctx)) return rc;
+    HIP_TRY(hipStreamSynchronize(ctx->stream));
+    p->split_tokens = split_tokens ? split_tokens : auto_split(p);
+    if (int rc = build_work(p)) return rc;
+    return ok();
+}
+
+int fa_paged_decode_plan_info(const fa_decode_plan* p, uint64_t* split_tokens,
+                              uint64_t* work_items, uint64_t* workspace_bytes) {
+    if (!p) return fail(FA_ERR_NULL_ARGUMENT, "plan is null");
+    if (split_tokens) *split_tokens = p->split_tokens;
+    if (work_items) *work_items = p->n_work;
+    if (workspace_bytes) *workspace_bytes = p->part_bytes;
+    return ok();
+}
+
+int fa_paged_decode_plan_destroy(fa_decode_plan* p) {
+    if (!p) return ok();
+    (void)hipSetDevice(p->ctx->device);
+    (void)hipStreamSynchronize(p->ctx->stream);
+    free_plan(p);
+    return ok();
+}
+
+int fa_paged_decode_launch(fa_ctx* ctx, const fa_decode_plan* p, const void* q, size_t q_bytes,
+                           const void* k_pool, const void* v_pool, size_t pool_bytes,
+                           void* out_lse, size_t out_bytes) {
+    if (!ctx || !p) return fail(FA_ERR_NULL_ARGUMENT, "null argument");
+    begin_call(ctx);
+    const uint64_t eb = elem_bytes(p->dtype);
+    const uint64_t qn = p->n_seqs * p->q_heads * p->head_dim;
+    const uint64_t pool = p->physical_pages * p->page_size * p->kv_heads * p->head_dim * eb;
+    fa_packed_layout lay;
+    if (int rc = fa_packed_layout_for(qn, p->n_seqs * p->q_heads, p->dtype, &lay)) return rc;
+    if (int rc = check_buffer("Q", q, q_bytes, qn * eb)) return rc;
+    if (int rc = check_buffer("K", k_pool, pool_bytes, pool)) return rc;
+    if (int rc = check_buffer("V", v_pool, pool_bytes, pool)) return rc;
+    if (int rc = check_buffer("O|LSE", out_lse, out_bytes, lay.combined_bytes)) return rc;
+    if (int rc = set_device(ctx)) return rc;
+    const float2* table = nullptr;
+    if (int rc = ensure_rope(ctx, p->theta, p->head_dim, p->max_pos, &table)) return rc;
+    fa::DecodeArgs a{};
+    a.q = q;
+    a.k_pool = k_pool;
+    a.v_pool = v_pool;
+    a.o = out_lse;
+    a.lse = (float*)((uint8_t*)out_lse + lay.lse_byte_offset);
+    a.block_tables = p->d_bt;
+    a.ctx_lens = p->d_ctx;
+    a.q_positions = p->d_qpos;
+    a.work_seq = p->d_work;
+    a.work_split = p->d_work + p->n_work;
+    a.seq_work_off = p->d_work + 2 * p->n_work;
+    a.part_o = p->d_part;
+    a.part_ml = p->d_part + p->n_work * p->q_heads * p->head_dim;
+    a.rope_table = table;
+    a.n_seqs = (int)p->n_seqs;
+    a.n_work = (int)p->n_work;
+    a.q_heads = (int)p->q_heads;
+    a.kv_heads = (int)p->kv_heads;
+    a.group = (int)(p->q_heads / p->kv_heads);
+    a.head_dim = (int)p->head_dim;
+    a.page_size = (int)p->page_size;
+    a.bt_stride = (int)p->max_pages;
+    a.split_tokens = (int)p->split_tokens;
+    a.scale = p->scale;
+    unsigned grid[3], block;
+    int dispatches = 0;
+    fa::launch_decode((Dtype)p->dtype, a, ctx->stream, grid, &block, &dispatches);
+    HIP_TRY(hipGetLastError());
+    record(ctx, FA_KERNEL_DECODE_PAGED_SPLITK, kernel_name(FA_KERNEL_DECODE_PAGED_SPLITK),
+           (uint32_t)std::min<uint64_t>(16, p->q_heads / p->kv_heads), 16, grid, block,
+           (uint32_t)dispatches, (uint32_t)((p->split_tokens)), nullptr);
+    return ok();
+}
+
+int fa_paged_cache_decode(fa_ctx* ctx, const fa_paged_cache* c, const void* q, size_t q_bytes,
+                          uint64_t q_heads, const fa_config* cfg, float theta,
+                          uint64_t q_rope_position, void* out_lse, size_t out_bytes) {
+    if (!ctx || !c) return fail(FA_ERR_NULL_ARGUMENT, "null argument");
+    uint64_t mapped = 0;
+    if (int rc = fa_kv_table_block_row(&c->table, nullptr, 0, &mapped)) return rc;
+    std::vector<int32_t> row(mapped);
+    if (int rc = fa_kv_table_block_row(&c->table, row.data(), mapped, &mapped)) return rc;
+    if (c->table.live > kI32 || q_rope_position > kI32)
+        return fail(FA_ERR_INDEX_SPACE_EXCEEDED, "paged decode exceeds the i32 index space");
+    const int32_t len = (int32_t)c->table.live, qp = (int32_t)q_rope_position;
+    fa_decode_plan* p = nullptr;
+    if (int rc = fa_paged_decode_prepare(ctx, row.data(), mapped, &len, &qp, 1, c->table.page_size,
+                                         c->table.physical_pages, q_heads, c->kv_heads,
+                                         c->head_dim, cfg, theta, c->dtype, &p))
+        return rc;
+    const uint32_t allocs = ctx->call_allocs;
+    const uint64_t abytes = ctx->call_alloc_bytes;
+    int rc = fa_paged_decode_launch(ctx, p, q, q_bytes, c->k, c->v, c->tensor_bytes, out_lse,
+                                    out_bytes);
+    ctx->last.temporary_allocation_count += allocs;
+    ctx->last.temporary_allocation_bytes += abytes;
+    fa_paged_decode_plan_destroy(p);
+    return rc ? rc : ok();
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------- paged prefill
+struct fa_prefill_plan {
+    fa_ctx* ctx = nullptr;
+    fa_asymmetric_shape shape{};
+    fa_asymmetric_rotary rot{};
+    int causal = 0;
+    float scale = 0.0f;
+    int dtype = 0;
+    uint64_t max_pages = 0, page_size = 0, physical_pages = 0;
+    int32_t* d_bt = nullptr;
+};
+
+extern "C" {
+
+int fa_chunked_prefill_paged_prepare(fa_ctx* ctx, const int32_t* block_tables, uint64_t max_pages,
+                                     uint64_t page_size, uint64_t physical_pages,
+                                     const fa_asymmetric_shape* sh, const fa_config* cfg,
+                                     const fa_asymmetric_rotary* rot, int dtype,
+                                     fa_prefill_plan** out) {
+    if (!block_tables || !sh || !rot || !out) return fail(FA_ERR_NULL_ARGUMENT, "null argument");
+    *out = nullptr;
+    if (int rc = check_dtype(dtype)) return rc;
+    if (!sh->batch || !sh->q_heads || !sh->kv_heads || !sh->query_len || !sh->kv_len ||
+        !sh->head_dim || !max_pages)
+        return fail(FA_ERR_ZERO_DIMENSION, "attention dimensions must all be non-zero");
+    if (!page_size || !physical_pages)
+        return fail(FA_ERR_PAGED_ZERO_DIMENSION, "paged KV dimensions must be non-zero");
+    if (int rc = validate_grouped(sh->batch, sh->q_heads, sh->kv_heads,
+                                  std::max(sh->query_len, sh->kv_len), sh->head_dim))
+        return rc;
+    if (sh->query_position_offset + sh->query_len > kI32)
+        return fail(FA_ERR_POSITION_OVERFLOW, "rotary position offset overflows the index space");
+    if (int rc = check_rotary(rot->theta, rot->query_position_offset, sh->head_dim, sh->query_len))
+        return rc;
+    if (int rc = check_head_dim(sh->head_dim, dtype)) return rc;
+    float scale;
+    if (int rc = resolve_scale(cfg, sh->head_dim, &scale)) return rc;
+    uint64_t rows;
+    if (mul_ov(page_size, physical_pages, &rows) || rows > kI32)
+        return fail(FA_ERR_INDEX_SPACE_EXCEEDED, "paged prefill exceeds the i32 index space");
+    if (int rc = check_pages(block_tables, max_pages, sh->batch, sh->kv_len, nullptr, page_size,
+                             physical_pages))
+        return rc;
+    if (!ctx) return fail(FA_ERR_NULL_ARGUMENT, "context is null");
+    begin_call(ctx);
+    if (int rc = set_device(ctx)) return rc;
+    fa_prefill_plan* p = new fa_prefill_plan();
+    p->ctx = ctx;
+    p->shape = *sh;
+    p->rot = *rot;
+    p->causal = cfg && cfg->causal;
+    p->scale = scale;
+    p->dtype = dtype;
+    p->max_pages = max_pages;
+    p->page_size = page_size;
+    p->physical_pages = physical_pages;
+    int rc = dev_alloc(ctx, (void**)&p->d_bt, sh->batch * max_pages * 4);
+    if (!rc && hipMemcpy(p->d_bt, block_tables, sh->batch * max_pages * 4, hipMemcpyHostToDevice))
+        rc = fail(FA_ERR_HIP, "block table upload failed");
+    if (rc) {
+        if (p->d_bt) (void)hipFree(p->d_bt);
+        delete p;
+        return rc;
+    }
+    *out = p;
+    return ok();
+}
+
+int fa_prefill_plan_destroy(fa_prefill_plan* p) {
+    if (!p) return ok();
+    (void)hipSetDevice(p->ctx->device);
+    (void)hipStreamSynchronize(p->ctx->stream);
+    if (p->d_bt) (void)hipFree(p->d_bt);
+    delete p;
+    return ok();
+}
+
+int fa_chunked_prefill_paged_launch(fa_ctx* ctx, const fa_prefill_plan* p, const void* q,
+                                    size_t q_bytes, const void* k_pool, const void* v_pool,
+                                    size_t pool_bytes, void* out_lse, size_t out_bytes) {
+    if (!ctx || !p) return fail(FA_ERR_NULL_ARGUMENT, "null argument");
+    begin_call(ctx);
+    const fa_asymmetric_shape& sh = p->shape;
+    const uint64_t eb = elem_bytes(p->dtype);
+    const uint64_t qn = sh.batch * sh.query_len * sh.q_heads * sh.head_dim;
+    const uint64_t pool = p->physical_pages * p->page_size * sh.kv_heads * sh.head_dim * eb;
+    fa_packed_layout lay;
+    if (int rc = fa_packed_layout_for(qn, sh.batch * sh.q_heads * sh.query_len, p->dtype, &lay))
+        return rc;
+    if (int rc = check_buffer("Q", q, q_bytes, qn * eb)) return rc;
+    if (int rc = check_buffer("K", k_pool, pool_bytes, pool)) return rc;
+    if (int rc = check_buffer("V", v_pool, pool_bytes, pool)) return rc;
+    if (int rc = check_buffer("O|LSE", out_lse, out_bytes, lay.combined_bytes)) return rc;
+    if (int rc = set_device(ctx)) return rc;
+    PrefillJob j{};
+    j.dt = (Dtype)p->dtype;
+    j.dtype = p->dtype;
+    j.paged = true;
+    j.rope = true;
+    j.theta = p->rot.theta;
+    j.max_pos = p->rot.query_position_offset + sh.query_len;
+    fa::PrefillArgs& a = j.a;
+    const int64_t D = (int64_t)sh.head_dim, QW = (int64_t)sh.q_heads * D,
+                  KW = (int64_t)sh.kv_heads * D;
+    a.q = q; a.k = k_pool; a.v = v_pool;
+    a.o = out_lse;
+    a.lse = (float*)((uint8_t*)out_lse + lay.lse_byte_offset);
+    a.q_sb = (int64_t)sh.query_len * QW; a.q_sh = D; a.q_ss = QW;
+    a.k_sb = 0; a.k_sh = D; a.k_ss = KW;
+    a.o_sb = a.q_sb; a.o_sh = a.q_sh; a.o_ss = a.q_ss;
+    a.lse_sb = (int64_t)sh.q_heads * sh.query_len; a.lse_sh = (int64_t)sh.query_len;
+    a.batch = (int)sh.batch; a.q_heads = (int)sh.q_heads; a.kv_heads = (int)sh.kv_heads;
+    a.group = (int)(sh.q_heads / sh.kv_heads);
+    a.q_len = (int)sh.query_len; a.kv_len = (int)sh.kv_len; a.head_dim = (int)D;
+    a.causal = p->causal;
+    a.causal_offset = (int)sh.query_position_offset;
+    a.rope_q = 1; a.rope_k = 0;  // K in the pool is stored pre-rotated
+    a.q_rope_offset = (int)p->rot.query_position_offset;
+    a.kv_rope_offset = 0;
+    a.scale = p->scale;
+    a.block_tables = p->d_bt;
+    a.bt_stride = (int)p->max_pages;
+    a.page_size = (int)p->page_size;
+    if (int rc = run_prefill(ctx, j)) return rc;
+    return ok();
+}
+
+int fa_paged_append_batched(fa_ctx* ctx, const int32_t* block_tables, uint64_t max_pages,
+                            const int32_t* start_lens, uint64_t n_seqs, uint64_t append_len,
+                            uint64_t page_size, uint64_t physical_pages, uint64_t kv_heads,
+                            uint64_t head_dim, const void* k_src, const void* v_src,
+                            size_t src_bytes, void* k_pool, void* v_pool, size_t pool_bytes,
+                            const fa_rotary* rot, int dtype) {
+    if (!block_tables || !start_lens) return fail(FA_ERR_NULL_ARGUMENT, "null argument");
+    if (int rc = check_dtype(dtype)) return rc;
+    if (!n_seqs || !append_len || !kv_heads || !head_dim || !max_pages)
+        return fail(FA_ERR_ZERO_DIMENSION, "attention dimensions must all be non-zero");
+    if (!page_size || !physical_pages)
+        return fail(FA_ERR_PAGED_ZERO_DIMENSION, "paged KV dimensions must be non-zero");
+    if (head_dim % 8)
+        return fail(FA_ERR_UNSUPPORTED_HEAD_DIM, "append needs head_dim %% 8 == 0, got %llu",
+                    (unsigned long long)head_dim);
+    uint64_t rows;
+    if (mul_ov(page_size, physical_pages, &rows) || rows > kI32 || max_pages * page_size > kI32)
+        return fail(FA_ERR_INDEX_SPACE_EXCEEDED, "paged append exceeds the i32 index space");
+    std::vector<int32_t> ends(n_seqs);
+    for (uint64_t s = 0; s < n_seqs; ++s) {
+        if (start_lens[s] < 0)
+            return fail(FA_ERR_INDEX_SPACE_EXCEEDED, "negative start length for sequence %llu",
+                        (unsigned long long)s);
+        const uint64_t end = (uint64_t)start_lens[s] + append_len;
+        if (end > max_pages * page_size)
+            return fail(FA_ERR_CAPACITY_EXCEEDED,
+                        "paged KV append requires %llu tokens, capacity is %llu",
+                        (unsigned long long)end, (unsigned long long)(max_pages * page_size));
+        ends[s] = (int32_t)end;
+    }
+    if (int rc = check_pages(block_tables, max_pages, n_seqs, 0, ends.data(), page_size,
+                             physical_pages))
+        return rc;
+    const uint64_t eb = elem_bytes(dtype);
+    const uint64_t row = kv_heads * head_dim * eb;
+    if (int rc = check_buffer("K", k_src, src_bytes, n_seqs * append_len * row)) return rc;
+    if (int rc = check_buffer("V", v_src, src_bytes, n_seqs * append_len * row)) return rc;
+    if (int rc = check_buffer("K pool", k_pool, pool_bytes, rows * row)) return rc;
+    if (int rc = check_buffer("V pool", v_pool, pool_bytes, rows * row)) return rc;
+    if (!ctx) return fail(FA_ERR_NULL_ARGUMENT, "context is null");
+    begin_call(ctx);
+    if (int rc = set_device(ctx)) return rc;
+    const float2* table = nullptr;
+    if (rot) {
+        uint64_t maxend = 0;
+        for (int32_t e : ends) maxend = std::max<uint64_t>(maxend, (uint64_t)e);
+        if (int rc = check_rotary(rot->theta, rot->position_offset, head_dim, maxend)) return rc;
+        if (int rc = ensure_rope(ctx, rot->theta, head_dim, rot->position_offset + maxend, &table))
+            return rc;
+    }
+    DevBuf meta;
+    const uint64_t meta_bytes = (n_seqs * max_pages + n_seqs) * 4;
+    HIP_TRY(hipMalloc(&meta.p, meta_bytes));
+    ctx->call_allocs += 1;
+    ctx->call_alloc_bytes += meta_bytes;
+    int32_t* d_bt = (int32_t*)meta.p;
+    int32_t* d_start = d_bt + n_seqs * max_pages;
+    HIP_TRY(hipMemcpyAsync(d_bt, block_tables, n_seqs * max_pages * 4, hipMemcpyHostToDevice,
+                           ctx->stream));
+    HIP_TRY(hipMemcpyAsync(d_start, start_lens, n_seqs * 4, hipMemcpyHostToDevice, ctx->stream));
+    fa::AppendArgs a{};
+    a.k_src = k_src;
+    a.v_src = v_src;
+    a.k_pool = k_pool;
+    a.v_pool = v_pool;
+    a.block_tables = d_bt;
+    a.start_lens = d_start;
+    a.n_seqs = (int)n_seqs;
+    a.append_len = (int)append_len;
+    a.bt_stride = (int)max_pages;
+    a.page_size = (int)page_size;
+    a.kv_heads = (int)kv_heads;
+    a.head_dim = (int)head_dim;
+    a.rope_table = table;
+    a.rope_offset = rot ? (int)rot->position_offset : 0;
+    fa::launch_append((Dtype)dtype, a, ctx->stream);
+    HIP_TRY(hipGetLastError());
+    HIP_TRY(hipStreamSynchronize(ctx->stream));  // metadata buffer is released on return
+    unsigned grid[3] = {(unsigned)append_len, (unsigned)n_seqs, 1};
+    record(ctx, FA_KERNEL_PAGED_APPEND, "append_kernel", 0, (uint32_t)page_size, grid,
+           (unsigned)std::min<uint64_t>(256, std::max<uint64_t>(64, kv_heads * head_dim / 8)), 1, 1,
+           nullptr);
+    return ok();
+}
+
+}  // extern "C"

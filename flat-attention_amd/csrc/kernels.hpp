@@ -1,0 +1,92 @@
+// Kernel argument blocks and host-side launchers shared between the HIP translation units and
+// the C-ABI host layer (host.cpp). Launchers assume the host layer already validated shapes,
+// buffer sizes and page ids; they only enqueue work on `stream`.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace fa {
+
+enum class Dtype : int { F32 = 0, F16 = 1, BF16 = 2 };
+
+// Prefill / rectangular attention over contiguous or paged K/V.
+// Query row (b, h, t) lives at q + b*q_sb + h*q_sh + t*q_ss (head_dim contiguous); the same
+// scheme addresses O with o_* strides and LSE with lse_sb/lse_sh (t contiguous).
+// Contiguous K/V row (b, kvh, key): k + b*k_sb + kvh*k_sh + key*k_ss.
+// Paged K/V row: k + (block_tables[b*bt_stride + key/page_size]*page_size + key%page_size)*k_ss
+//                  + kvh*k_sh.
+struct PrefillArgs {
+    const void* q;
+    const void* k;
+    const void* v;
+    void* o;
+    float* lse;
+    int64_t q_sb, q_sh, q_ss;
+    int64_t k_sb, k_sh, k_ss;
+    int64_t o_sb, o_sh, o_ss;
+    int64_t lse_sb, lse_sh;
+    int batch, q_heads, kv_heads, group;
+    int q_len, kv_len, head_dim;
+    int causal;
+    int causal_offset;   // causal position of query t is causal_offset + t
+    int rope_q, rope_k;  // rotate Q / K while loading
+    int q_rope_offset, kv_rope_offset;
+    const float2* rope_table;  // [rows][head_dim/2] (cos, sin)
+    float scale;               // softmax scale
+    const int* block_tables;   // paged only
+    int bt_stride, page_size;
+};
+
+void launch_prefill(Dtype dt, bool paged, const PrefillArgs& a, hipStream_t s,
+                    unsigned grid[3], unsigned* block);
+
+// Paged q_len=1 decode, split-K over the context of every sequence.
+struct DecodeArgs {
+    const void* q;        // [n_seqs, q_heads*head_dim]
+    const void* k_pool;   // [pages, page_size, kv_heads*head_dim]
+    const void* v_pool;
+    void* o;              // [n_seqs, q_heads*head_dim] (dtype)
+    float* lse;           // [n_seqs, q_heads]
+    const int* block_tables;  // [n_seqs, bt_stride]
+    const int* ctx_lens;      // [n_seqs]
+    const int* q_positions;   // [n_seqs] RoPE position of each query
+    const int* work_seq;      // [n_work] sequence of each work item
+    const int* work_split;    // [n_work] split index within its sequence
+    const int* seq_work_off;  // [n_seqs+1] first work item of each sequence
+    float* part_o;            // [n_work, q_heads, head_dim] un-normalised partial O
+    float* part_ml;           // [n_work, q_heads, 2] partial (max, sum)
+    const float2* rope_table;
+    int n_seqs, n_work, q_heads, kv_heads, group, head_dim;
+    int page_size, bt_stride, split_tokens;
+    float scale;
+};
+
+void launch_decode(Dtype dt, const DecodeArgs& a, hipStream_t s, unsigned grid[3],
+                   unsigned* block, int* dispatches);
+
+// (cos, sin) table: table[pos*half + p] for pos < rows, p < half = head_dim/2, with
+// angle = float(pos) * inv_freq[p].
+void launch_rope_table(float2* table, const float* inv_freq, int rows, int half, hipStream_t s);
+
+// Scatter `append_len` rows per sequence into the page pool, optionally rotating K rows.
+struct AppendArgs {
+    const void* k_src;   // [n_seqs, append_len, kv_heads*head_dim]
+    const void* v_src;
+    void* k_pool;
+    void* v_pool;
+    const int* block_tables;
+    const int* start_lens;   // device [n_seqs], or null with start_len_const
+    int start_len_const;
+    int n_seqs, append_len, bt_stride, page_size, kv_heads, head_dim;
+    const float2* rope_table;  // null: copy K as is
+    int rope_offset;
+};
+void launch_append(Dtype dt, const AppendArgs& a, hipStream_t s);
+
+// Rotate every row of a [rows, heads*head_dim] tensor (in place allowed); row r is at RoPE
+// position offset + r % period. head_dim must be a multiple of 8.
+void launch_rotate_rows(Dtype dt, const void* in, void* out, int rows, int heads, int head_dim,
+                        int64_t period, const float2* table, int offset, hipStream_t s);
+
+}  // namespace fa

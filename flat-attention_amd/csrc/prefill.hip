@@ -1,0 +1,605 @@
+// Fused causal / non-causal GQA prefill with RoPE for gfx950.
+//
+// Replaces the reference's Q4 x KV8 WGSL tiles (shaders/flat_fwd_grouped_rope.wgsl:59-359,
+// shaders/flat_fwd.wgsl, shaders/flat_fwd_projection_rope_asymmetric.wgsl) with an MFMA design.
+// The math is the online softmax of forward_reference (src/lib.rs:454-520): running max m,
+// running sum l, O accumulated with rescale alpha = exp(m_old - m_new), LSE = m + ln l.
+//
+// Workgroup = 4 waves = 128 query rows. Rows of one (batch, kv-head) are flattened as
+// row = t * group + head_in_group, so one workgroup holds every query head of a GQA group for
+// ceil(128/group) consecutive positions: each K/V tile staged in LDS feeds all of them.
+// Per 64-key tile and wave (32 rows):
+//   S^T[64 keys x 32 rows] = K_perm . Q^T      (K from LDS is the A operand, Q in registers)
+//   P^T = exp2((S - m) * scale * log2 e)       (every value a lane holds belongs to ONE row)
+//   O^T[D x 32 rows]  += V^T . P^T             (V^T from LDS is the A operand, P^T registers)
+// Computing the transposed products makes each lane own a single query row, so the softmax row
+// max/sum needs one cross-lane exchange (lane ^ 32) and the alpha rescale is a per-lane scalar.
+// K rows are fed to the MFMA in a permuted order (bits 2 and 3 of the row swapped) so that the
+// eight scores a lane holds per 16-key step are contiguous keys, which is the order the P^T
+// operand of the second MFMA needs.
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace fa {
+
+// Fast unsigned division by a runtime constant (Granlund-Montgomery round-up method).
+struct FastDiv {
+    uint32_t d, m, s;
+    __host__ __device__ FastDiv() : d(1), m(0), s(0) {}
+    __host__ explicit FastDiv(uint32_t div) : d(div) {
+        s = 0;
+        while ((1u << s) < div) ++s;
+        m = (uint32_t)((((uint64_t)1 << 32) * (((uint64_t)1 << s) - div)) / div + 1);
+    }
+    __device__ __forceinline__ uint32_t div(uint32_t n) const {
+        return (uint32_t)(((uint64_t)__umulhi(n, m) + n) >> s);
+    }
+};
+
+struct PrefillKArgs {
+    PrefillArgs a;
+    FastDiv ps;
+};
+
+template <bool PAGED>
+__device__ __forceinline__ int64_t kv_row_offset(const PrefillKArgs& ka, int b, int key) {
+    const PrefillArgs& a = ka.a;
+    if constexpr (PAGED) {
+        uint32_t lp = ka.ps.div((uint32_t)key);
+        uint32_t off = (uint32_t)key - lp * (uint32_t)a.page_size;
+        int page = a.block_tables[(int64_t)b * a.bt_stride + lp];
+        return ((int64_t)page * a.page_size + off) * a.k_ss;
+    } else {
+        return (int64_t)b * a.k_sb + (int64_t)key * a.k_ss;
+    }
+}
+
+__device__ __forceinline__ int k_swizzle(int row) { return (row & 3) | ((row >> 1) & 4); }
+
+// ------------------------------------------------------------------ 16-bit MFMA kernel
+template <typename T, int DPAD, bool PAGED, bool ROPEK>
+__global__ __launch_bounds__(256, 2) void prefill_mfma16(PrefillKArgs ka) {
+    using H = Half<T>;
+    const PrefillArgs& a = ka.a;
+    constexpr int BM = 128, BN = 64;
+    constexpr int KS = DPAD / 16;           // QK^T k-steps (16 dims each)
+    constexpr int MB = DPAD / 32;           // 32-dim blocks of O^T
+    constexpr int CPR = DPAD / 8;           // 16-byte chunks per K row
+    constexpr int KRPP = 256 / CPR;         // K rows staged per pass
+    constexpr int KPASS = BN / KRPP;
+    constexpr int KROWB = DPAD * 2;         // bytes per K row in LDS
+    constexpr int VPAIRS = DPAD / 2;
+    constexpr int VKPT = DPAD / 8;          // keys per thread in V staging
+    constexpr int VROWB = BN * 2;           // bytes per V^T row in LDS
+    __shared__ __attribute__((aligned(16))) uint8_t smem[BN * KROWB + DPAD * VROWB];
+    uint8_t* const k_lds = smem;
+    uint8_t* const v_lds = smem + BN * KROWB;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 5;
+    const int D = a.head_dim, half = D >> 1;
+    const int rows_total = a.q_len * a.group;
+    const int nqb = (rows_total + BM - 1) / BM;
+    const int logical = xcd_remap(blockIdx.x, gridDim.x);
+    const int bh = logical / nqb;
+    const int qb = nqb - 1 - logical % nqb;  // heavy (late, causal) blocks dispatch first
+    const int b = bh / a.kv_heads, kvh = bh % a.kv_heads;
+    const int r0 = qb * BM;
+
+    // This lane's query row.
+    const int row = r0 + wave * 32 + (lane & 31);
+    const bool row_ok = row < rows_total;
+    const int t = row_ok ? row / a.group : a.q_len - 1;
+    const int hq = kvh * a.group + (row_ok ? row % a.group : 0);
+    const int cpos = a.causal_offset + t;
+
+    const int t_max = min(a.q_len - 1, (r0 + BM - 1) / a.group);
+    const int t_min = r0 / a.group;
+    int n_keys = a.kv_len;
+    if (a.causal) n_keys = min(n_keys, a.causal_offset + t_max + 1);
+    const int n_tiles = (n_keys + BN - 1) / BN;
+    const int cpos_min = a.causal_offset + t_min;
+
+    // ---- Q^T operand, rotated in registers: lane holds Q[row][16ks + 8g .. +8].
+    u32x4_t qop[KS];
+    {
+        const uint16_t* qrow = (const uint16_t*)a.q + (int64_t)b * a.q_sb + (int64_t)hq * a.q_sh +
+                               (int64_t)t * a.q_ss;
+        const float2* cs_row =
+            a.rope_q ? a.rope_table + (int64_t)(a.q_rope_offset + t) * half : nullptr;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            const int d0 = 16 * ks + 8 * g;
+            u32x4_t raw = {0u, 0u, 0u, 0u};
+            if (d0 < D) raw = *(const u32x4_t*)(qrow + d0);
+            if (a.rope_q && d0 < D) {
+                float x[8], cs[8];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    x[2 * j] = H::lo(raw[j]);
+                    x[2 * j + 1] = H::hi(raw[j]);
+                }
+                const f32x4_t c0 = *(const f32x4_t*)(cs_row + d0 / 2);
+                const f32x4_t c1 = *(const f32x4_t*)(cs_row + d0 / 2 + 2);
+                cs[0] = c0[0]; cs[1] = c0[1]; cs[2] = c0[2]; cs[3] = c0[3];
+                cs[4] = c1[0]; cs[5] = c1[1]; cs[6] = c1[2]; cs[7] = c1[3];
+                rope4(x, cs);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) raw[j] = H::pack(x[2 * j], x[2 * j + 1]);
+            }
+            qop[ks] = raw;
+        }
+    }
+
+    const uint16_t* kbase = (const uint16_t*)a.k + (int64_t)kvh * a.k_sh;
+    const uint16_t* vbase = (const uint16_t*)a.v + (int64_t)kvh * a.k_sh;
+
+    // ---- register prefetch of one K/V tile
+    u32x4_t kreg[KPASS];
+    uint32_t vreg[VKPT];
+    const int k_dc = tid % CPR, k_r = tid / CPR;
+    const int v_dp = tid % VPAIRS, v_kb = tid / VPAIRS;
+
+    auto load_tile = [&](int tile) {
+#pragma unroll
+        for (int p = 0; p < KPASS; ++p) {
+            const int key = tile * BN + p * KRPP + k_r;
+            const int d0 = k_dc * 8;
+            u32x4_t z = {0u, 0u, 0u, 0u};
+            kreg[p] = z;
+            if (key < a.kv_len && d0 < D)
+                kreg[p] = *(const u32x4_t*)(kbase + kv_row_offset<PAGED>(ka, b, key) + d0);
+        }
+        {
+            const int key0 = tile * BN + v_kb * VKPT;
+            const int d = 2 * v_dp;
+            if constexpr (PAGED) {
+                // consecutive keys: walk pages incrementally; block-table entries are read only
+                // for live keys (key < kv_len), which the host validated.
+                const int key_first = min(key0, a.kv_len - 1);
+                uint32_t lp = ka.ps.div((uint32_t)key_first);
+                int off = key0 - (int)lp * a.page_size;
+                int page = a.block_tables[(int64_t)b * a.bt_stride + lp];
+#pragma unroll
+                for (int j = 0; j < VKPT; ++j) {
+                    const int key = key0 + j;
+                    vreg[j] = 0u;
+                    if (key < a.kv_len && d < D)
+                        vreg[j] = *(const uint32_t*)(vbase +
+                                                     ((int64_t)page * a.page_size + off) * a.k_ss +
+                                                     d);
+                    if (++off == a.page_size && key + 1 < a.kv_len) {
+                        off = 0;
+                        ++lp;
+                        page = a.block_tables[(int64_t)b * a.bt_stride + lp];
+                    }
+                }
+            } else {
+                const uint16_t* vrow = vbase + (int64_t)b * a.k_sb + (int64_t)key0 * a.k_ss + d;
+#pragma unroll
+                for (int j = 0; j < VKPT; ++j) {
+                    vreg[j] = 0u;
+                    if (key0 + j < a.kv_len && d < D)
+                        vreg[j] = *(const uint32_t*)(vrow + (int64_t)j * a.k_ss);
+                }
+            }
+        }
+    };
+
+    auto store_tile = [&](int tile) {
+#pragma unroll
+        for (int p = 0; p < KPASS; ++p) {
+            const int kl = p * KRPP + k_r;
+            u32x4_t val = kreg[p];
+            if (ROPEK && tile * BN + kl < a.kv_len && k_dc * 8 < D) {
+                // K is rotated between the HBM load and the LDS store (cos/sin from the table)
+                const float2* csp = a.rope_table +
+                                    (int64_t)(a.kv_rope_offset + tile * BN + kl) * half + k_dc * 4;
+                const f32x4_t c0 = *(const f32x4_t*)csp;
+                const f32x4_t c1 = *(const f32x4_t*)(csp + 2);
+                float x[8], cs[8] = {c0[0], c0[1], c0[2], c0[3], c1[0], c1[1], c1[2], c1[3]};
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    x[2 * j] = H::lo(val[j]);
+                    x[2 * j + 1] = H::hi(val[j]);
+                }
+                rope4(x, cs);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) val[j] = H::pack(x[2 * j], x[2 * j + 1]);
+            }
+            const int unit = k_dc ^ (k_swizzle(kl) & (CPR - 1));
+            *(u32x4_t*)(k_lds + kl * KROWB + unit * 16) = val;
+        }
+        {
+            const int d = 2 * v_dp;
+            const int kb0 = v_kb * VKPT;  // first key of this thread
+            if constexpr (VKPT >= 8) {
+#pragma unroll
+                for (int u = 0; u < VKPT / 8; ++u) {
+                    u32x4_t lo, hi;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const uint32_t x = vreg[8 * u + 2 * i], y = vreg[8 * u + 2 * i + 1];
+                        lo[i] = (x & 0xffffu) | (y << 16);
+                        hi[i] = (x >> 16) | (y & 0xffff0000u);
+                    }
+                    const int ku = kb0 / 8 + u;
+                    *(u32x4_t*)(v_lds + d * VROWB + ((ku ^ (d & 7)) * 16)) = lo;
+                    *(u32x4_t*)(v_lds + (d + 1) * VROWB + ((ku ^ ((d + 1) & 7)) * 16)) = hi;
+                }
+            } else {
+                u32x2_t lo, hi;
+#pragma unroll
+                for (int i = 0; i < 2; ++i) {
+                    const uint32_t x = vreg[2 * i], y = vreg[2 * i + 1];
+                    lo[i] = (x & 0xffffu) | (y << 16);
+                    hi[i] = (x >> 16) | (y & 0xffff0000u);
+                }
+                const int ku = kb0 / 8, sub = (kb0 % 8) * 2;
+                *(u32x2_t*)(v_lds + d * VROWB + ((ku ^ (d & 7)) * 16) + sub) = lo;
+                *(u32x2_t*)(v_lds + (d + 1) * VROWB + ((ku ^ ((d + 1) & 7)) * 16) + sub) = hi;
+            }
+        }
+    };
+
+    f32x16_t oacc[MB];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) oacc[mb] = (f32x16_t)0.0f;
+    float m_run = -INFINITY, l_run = 0.0f;
+    const float c2 = a.scale * kLog2e;
+
+    // K row fed to MFMA row m of a 32-key block: bits 2 and 3 swapped.
+    const int pm = ((lane & 31) & ~12) | (((lane & 31) & 4) << 1) | (((lane & 31) & 8) >> 1);
+
+    if (n_tiles > 0) load_tile(0);
+    for (int tile = 0; tile < n_tiles; ++tile) {
+        store_tile(tile);
+        __syncthreads();
+        if (tile + 1 < n_tiles) load_tile(tile + 1);
+
+        // ---- S^T = K_perm . Q^T
+        f32x16_t sacc[2];
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+            sacc[kb] = (f32x16_t)0.0f;
+            const int krow = kb * 32 + pm;
+            const int sw = k_swizzle(krow) & (CPR - 1);
+            const uint8_t* kr = k_lds + krow * KROWB;
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+                const u32x4_t av = *(const u32x4_t*)(kr + (((2 * ks + g) ^ sw) * 16));
+                sacc[kb] = H::mfma32(av, qop[ks], sacc[kb]);
+            }
+        }
+
+        // ---- mask (tail keys, causal diagonal)
+        const int tile_end = (tile + 1) * BN;
+        if (tile_end > a.kv_len || (a.causal && tile_end - 1 > cpos_min)) {
+            const int lim = a.causal ? min(a.kv_len - 1, cpos) : a.kv_len - 1;
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const int key = tile * BN + 32 * kb + 16 * (i >> 3) + 8 * g + (i & 7);
+                    if (key > lim) sacc[kb][i] = -INFINITY;
+                }
+        }
+
+        // ---- online softmax (row = this lane's query; partner lane ^ 32 holds the other keys)
+        float mt = sacc[0][0];
+#pragma unroll
+        for (int i = 1; i < 16; ++i) mt = fmaxf(mt, sacc[0][i]);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) mt = fmaxf(mt, sacc[1][i]);
+        mt = fmaxf(mt, shfl_xor(mt, 32));
+        const float m_new = fmaxf(m_run, mt);
+        const float m_base = (m_new == -INFINITY) ? 0.0f : m_new;
+        const float alpha = fast_exp2((m_run - m_base) * c2);
+        const float neg = -m_base * c2;
+        float lsum = 0.0f;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const float p = fast_exp2(fmaf(sacc[kb][i], c2, neg));
+                sacc[kb][i] = p;
+                lsum += p;
+            }
+        l_run = l_run * alpha + lsum;
+        m_run = m_new;
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) oacc[mb] *= alpha;
+
+        // ---- P^T operands (16 keys each)
+        u32x4_t pop[4];
+#pragma unroll
+        for (int s2 = 0; s2 < 4; ++s2) {
+            const int kb = s2 >> 1, h8 = (s2 & 1) * 8;
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                pop[s2][j] = H::pack(sacc[kb][h8 + 2 * j], sacc[kb][h8 + 2 * j + 1]);
+        }
+
+        // ---- O^T += V^T . P^T
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) {
+            const int drow = mb * 32 + (lane & 31);
+            const uint8_t* vr = v_lds + drow * VROWB;
+#pragma unroll
+            for (int s2 = 0; s2 < 4; ++s2) {
+                const u32x4_t av = *(const u32x4_t*)(vr + (((2 * s2 + g) ^ (drow & 7)) * 16));
+                oacc[mb] = H::mfma32(av, pop[s2], oacc[mb]);
+            }
+        }
+        __syncthreads();
+    }
+
+    // ---- epilogue
+    const float l_tot = l_run + shfl_xor(l_run, 32);
+    const float inv = 1.0f / l_tot;
+    if (row_ok) {
+        uint16_t* orow = (uint16_t*)a.o + (int64_t)b * a.o_sb + (int64_t)hq * a.o_sh +
+                         (int64_t)t * a.o_ss;
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+            for (int q4 = 0; q4 < 4; ++q4) {
+                const int d0 = mb * 32 + 8 * q4 + 4 * g;
+                if (d0 < D) {
+                    u32x2_t w;
+                    w[0] = H::pack(oacc[mb][4 * q4] * inv, oacc[mb][4 * q4 + 1] * inv);
+                    w[1] = H::pack(oacc[mb][4 * q4 + 2] * inv, oacc[mb][4 * q4 + 3] * inv);
+                    *(u32x2_t*)(orow + d0) = w;
+                }
+            }
+        if (g == 0)
+            a.lse[(int64_t)b * a.lse_sb + (int64_t)hq * a.lse_sh + t] = m_run * a.scale + logf(l_tot);
+    }
+}
+
+// ------------------------------------------------------------------ f32 MFMA kernel
+// Same decomposition with v_mfma_f32_32x32x2_f32 (f32 I/O contract, 2e-5 tolerance): no value
+// is ever rounded below f32. Lane group g supplies k-index g of every 2-wide k-step; the d
+// mapping is d = g*DPAD/2 + ks so each lane's Q operand is a contiguous half row.
+template <int DPAD, bool PAGED>
+__global__ __launch_bounds__(256, 1) void prefill_mfma_f32(PrefillKArgs ka) {
+    const PrefillArgs& a = ka.a;
+    constexpr int BM = 128, BN = 64;
+    constexpr int HALFD = DPAD / 2;
+    constexpr int MB = DPAD / 32;
+    constexpr int KSTR = DPAD + 1;   // floats per K row in LDS (odd: conflict-free columns)
+    constexpr int VSTR = DPAD;
+    __shared__ float k_lds[BN * KSTR];
+    __shared__ __attribute__((aligned(16))) float v_lds[BN * VSTR];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 5;
+    const int D = a.head_dim, half = D >> 1;
+    const int rows_total = a.q_len * a.group;
+    const int nqb = (rows_total + BM - 1) / BM;
+    const int logical = xcd_remap(blockIdx.x, gridDim.x);
+    const int bh = logical / nqb;
+    const int qb = nqb - 1 - logical % nqb;
+    const int b = bh / a.kv_heads, kvh = bh % a.kv_heads;
+    const int r0 = qb * BM;
+    const int row = r0 + wave * 32 + (lane & 31);
+    const bool row_ok = row < rows_total;
+    const int t = row_ok ? row / a.group : a.q_len - 1;
+    const int hq = kvh * a.group + (row_ok ? row % a.group : 0);
+    const int cpos = a.causal_offset + t;
+    const int t_max = min(a.q_len - 1, (r0 + BM - 1) / a.group);
+    const int t_min = r0 / a.group;
+    int n_keys = a.kv_len;
+    if (a.causal) n_keys = min(n_keys, a.causal_offset + t_max + 1);
+    const int n_tiles = (n_keys + BN - 1) / BN;
+    const int cpos_min = a.causal_offset + t_min;
+
+    // Q operand: qv[ks] = Q[row][g*HALFD + ks] (rotated)
+    float qv[HALFD];
+    {
+        const float* qrow = (const float*)a.q + (int64_t)b * a.q_sb + (int64_t)hq * a.q_sh +
+                            (int64_t)t * a.q_ss;
+#pragma unroll
+        for (int ks = 0; ks < HALFD; ++ks) {
+            const int d = g * HALFD + ks;
+            qv[ks] = d < D ? qrow[d] : 0.0f;
+        }
+        if (a.rope_q) {
+            const float2* cs = a.rope_table + (int64_t)(a.q_rope_offset + t) * half;
+#pragma unroll
+            for (int j = 0; j < HALFD / 2; ++j) {
+                const int p = (g * HALFD) / 2 + j;
+                if (2 * p < D) {
+                    const float2 c = cs[p];
+                    rope_pair(qv[2 * j], qv[2 * j + 1], c.x, c.y);
+                }
+            }
+        }
+    }
+
+    const float* kbase = (const float*)a.k + (int64_t)kvh * a.k_sh;
+    const float* vbase = (const float*)a.v + (int64_t)kvh * a.k_sh;
+
+    f32x16_t oacc[MB];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) oacc[mb] = (f32x16_t)0.0f;
+    float m_run = -INFINITY, l_run = 0.0f;
+    const float c2 = a.scale * kLog2e;
+    constexpr int C4 = DPAD / 4;           // float4 chunks per row
+    constexpr int RPP = 256 / C4;          // rows per staging pass
+    constexpr int PASSES = BN / RPP;
+
+    for (int tile = 0; tile < n_tiles; ++tile) {
+        // ---- stage K (rotated) and V
+#pragma unroll
+        for (int p = 0; p < PASSES; ++p) {
+            const int kl = p * RPP + tid / C4;
+            const int d0 = (tid % C4) * 4;
+            const int key = tile * BN + kl;
+            f32x4_t kv4 = (f32x4_t)0.0f, vv4 = (f32x4_t)0.0f;
+            if (key < a.kv_len) {
+                const int64_t ro = kv_row_offset<PAGED>(ka, b, key);
+                const float* kr = kbase + ro;
+                const float* vr = vbase + ro;
+                if (d0 + 3 < D) {
+                    kv4 = *(const f32x4_t*)(kr + d0);
+                    vv4 = *(const f32x4_t*)(vr + d0);
+                } else {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        if (d0 + j < D) {
+                            kv4[j] = kr[d0 + j];
+                            vv4[j] = vr[d0 + j];
+                        }
+                }
+                if (a.rope_k) {
+                    const float2* cs = a.rope_table + (int64_t)(a.kv_rope_offset + key) * half;
+#pragma unroll
+                    for (int j = 0; j < 2; ++j) {
+                        const int p2 = d0 / 2 + j;
+                        if (2 * p2 < D) {
+                            const float2 c = cs[p2];
+                            float e = kv4[2 * j], o = kv4[2 * j + 1];
+                            rope_pair(e, o, c.x, c.y);
+                            kv4[2 * j] = e;
+                            kv4[2 * j + 1] = o;
+                        }
+                    }
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) k_lds[kl * KSTR + d0 + j] = kv4[j];
+            *(f32x4_t*)(v_lds + kl * VSTR + d0) = vv4;
+        }
+        __syncthreads();
+
+        f32x16_t sacc[2];
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+            sacc[kb] = (f32x16_t)0.0f;
+            const float* kr = k_lds + (kb * 32 + (lane & 31)) * KSTR + g * HALFD;
+#pragma unroll
+            for (int ks = 0; ks < HALFD; ++ks)
+                sacc[kb] = __builtin_amdgcn_mfma_f32_32x32x2f32(kr[ks], qv[ks], sacc[kb], 0, 0, 0);
+        }
+
+        const int tile_end = (tile + 1) * BN;
+        if (tile_end > a.kv_len || (a.causal && tile_end - 1 > cpos_min)) {
+            const int lim = a.causal ? min(a.kv_len - 1, cpos) : a.kv_len - 1;
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const int key = tile * BN + 32 * kb + 8 * (i >> 2) + 4 * g + (i & 3);
+                    if (key > lim) sacc[kb][i] = -INFINITY;
+                }
+        }
+
+        float mt = sacc[0][0];
+#pragma unroll
+        for (int i = 1; i < 16; ++i) mt = fmaxf(mt, sacc[0][i]);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) mt = fmaxf(mt, sacc[1][i]);
+        mt = fmaxf(mt, shfl_xor(mt, 32));
+        const float m_new = fmaxf(m_run, mt);
+        const float m_base = (m_new == -INFINITY) ? 0.0f : m_new;
+        const float alpha = fast_exp2((m_run - m_base) * c2);
+        const float neg = -m_base * c2;
+        float lsum = 0.0f;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const float p = fast_exp2(fmaf(sacc[kb][i], c2, neg));
+                sacc[kb][i] = p;
+                lsum += p;
+            }
+        l_run = l_run * alpha + lsum;
+        m_run = m_new;
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) oacc[mb] *= alpha;
+
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) {
+            const float* vc = v_lds + mb * 32 + (lane & 31);
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const int kl = 32 * kb + 8 * (i >> 2) + 4 * g + (i & 3);
+                    oacc[mb] = __builtin_amdgcn_mfma_f32_32x32x2f32(vc[kl * VSTR], sacc[kb][i],
+                                                                   oacc[mb], 0, 0, 0);
+                }
+        }
+        __syncthreads();
+    }
+
+    const float l_tot = l_run + shfl_xor(l_run, 32);
+    const float inv = 1.0f / l_tot;
+    if (row_ok) {
+        float* orow = (float*)a.o + (int64_t)b * a.o_sb + (int64_t)hq * a.o_sh +
+                      (int64_t)t * a.o_ss;
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+            for (int q4 = 0; q4 < 4; ++q4) {
+                const int d0 = mb * 32 + 8 * q4 + 4 * g;
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    if (d0 + j < D) orow[d0 + j] = oacc[mb][4 * q4 + j] * inv;
+            }
+        if (g == 0)
+            a.lse[(int64_t)b * a.lse_sb + (int64_t)hq * a.lse_sh + t] = m_run * a.scale + logf(l_tot);
+    }
+}
+
+// ------------------------------------------------------------------ launcher
+template <typename T, bool PAGED, bool ROPEK>
+static void launch16r(const PrefillKArgs& ka, int dpad, dim3 grid, hipStream_t s) {
+    switch (dpad) {
+        case 32: prefill_mfma16<T, 32, PAGED, ROPEK><<<grid, 256, 0, s>>>(ka); break;
+        case 64: prefill_mfma16<T, 64, PAGED, ROPEK><<<grid, 256, 0, s>>>(ka); break;
+        default: prefill_mfma16<T, 128, PAGED, ROPEK><<<grid, 256, 0, s>>>(ka); break;
+    }
+}
+
+template <typename T, bool PAGED>
+static void launch16(const PrefillKArgs& ka, int dpad, dim3 grid, hipStream_t s) {
+    if (ka.a.rope_k) launch16r<T, PAGED, true>(ka, dpad, grid, s);
+    else launch16r<T, PAGED, false>(ka, dpad, grid, s);
+}
+
+template <bool PAGED>
+static void launch32(const PrefillKArgs& ka, int dpad, dim3 grid, hipStream_t s) {
+    switch (dpad) {
+        case 32: prefill_mfma_f32<32, PAGED><<<grid, 256, 0, s>>>(ka); break;
+        case 64: prefill_mfma_f32<64, PAGED><<<grid, 256, 0, s>>>(ka); break;
+        default: prefill_mfma_f32<128, PAGED><<<grid, 256, 0, s>>>(ka); break;
+    }
+}
+
+void launch_prefill(Dtype dt, bool paged, const PrefillArgs& a, hipStream_t s, unsigned grid[3],
+                    unsigned* block) {
+    PrefillKArgs ka;
+    ka.a = a;
+    if (paged) ka.ps = FastDiv((uint32_t)a.page_size);
+    const int dpad = a.head_dim <= 32 ? 32 : (a.head_dim <= 64 ? 64 : 128);
+    const int rows_total = a.q_len * a.group;
+    const int nqb = (rows_total + 127) / 128;
+    dim3 g((unsigned)((int64_t)a.batch * a.kv_heads * nqb));
+    grid[0] = g.x;
+    grid[1] = 1;
+    grid[2] = 1;
+    *block = 256;
+    switch (dt) {
+        case Dtype::BF16:
+            paged ? launch16<bf16_t, true>(ka, dpad, g, s) : launch16<bf16_t, false>(ka, dpad, g, s);
+            break;
+        case Dtype::F16:
+            paged ? launch16<f16_t, true>(ka, dpad, g, s) : launch16<f16_t, false>(ka, dpad, g, s);
+            break;
+        default:
+            paged ? launch32<true>(ka, dpad, g, s) : launch32<false>(ka, dpad, g, s);
+            break;
+    }
+}
+
+}  // namespace fa

@@ -1,0 +1,367 @@
+/*
+ * flat_hip.h — C ABI of the MI355X (gfx950 / CDNA4) backend for the FLAT-ATTENTION fused
+ * attention hot path.
+ *
+ * The ABI replaces the roles of the reference crate's wgpu host executors. Every entry point
+ * below names the reference surface it stands in for (file:line under the reference crate).
+ * A Rust `hip_backend` module binds these symbols with `extern "C"` declarations; the Python
+ * ctypes mirror in `flat-attention_amd/flat_attention_amd/` binds the same symbols for tests.
+ *
+ * Conventions
+ *   - Every call returns an `int` status (`fa_status`). 0 is success. Non-zero codes map 1:1
+ *     onto the reference's error enum variants; `fa_last_error_message()` returns the
+ *     human-readable text (thread-local, same wording as the reference's Display impls).
+ *   - Device pointers are plain `void*` obtained from `fa_buf_*` or from any HIP allocation on
+ *     the context's device. Each device pointer is paired with its size in bytes so the library
+ *     can reject undersized buffers before any launch (reference `BufferTooSmall`).
+ *   - All work is enqueued on the context's single HIP stream. No call synchronises except
+ *     `fa_buf_download`, `fa_ctx_synchronize` and the `*_host` convenience forwards.
+ *   - Validation always happens before any launch; nothing ever falls back to the CPU.
+ *
+ * Tensor layouts (element order, row-major):
+ *   MHA / grouped:       Q,O [batch, q_heads, seq, head_dim]   K,V [batch, kv_heads, seq, head_dim]
+ *   projection layout:   Q,O [batch, seq, q_heads*head_dim]    K,V [batch, seq, kv_heads*head_dim]
+ *   paged pool:          K,V [physical_pages, page_size, kv_heads*head_dim]
+ *   packed output:       [O (dtype) | LSE (f32)], LSE at byte offset round_up(O bytes, 4)
+ *                        LSE is [batch, q_heads, query_len] (grouped and projection layouts).
+ */
+#ifndef FLAT_HIP_H
+#define FLAT_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FA_ABI_VERSION 1
+
+/* Status codes. Reference: FlatAttentionError src/lib.rs:362-380, WgpuFlatAttentionError
+ * src/wgpu_backend.rs:39-100, PagedKvError src/paged_kv.rs:37-43, PagedDecodeError
+ * src/wgpu_paged_decode.rs:28-70, WgpuChunkedProjectionPrefillError
+ * src/wgpu_chunked_prefill.rs:40-52, WgpuPagedKvCacheError src/wgpu_paged_kv_cache.rs:15-33. */
+typedef enum fa_status {
+    FA_OK = 0,
+    FA_ERR_ZERO_DIMENSION = 1,
+    FA_ERR_SHAPE_OVERFLOW = 2,
+    FA_ERR_INVALID_HEAD_GROUPING = 3,
+    FA_ERR_INVALID_ROTARY_HEAD_DIM = 4,
+    FA_ERR_INVALID_ROTARY_THETA = 5,
+    FA_ERR_POSITION_OVERFLOW = 6,
+    FA_ERR_LENGTH_MISMATCH = 7,
+    FA_ERR_INVALID_SCALE = 8,
+    FA_ERR_NON_FINITE_INPUT = 9,
+    FA_ERR_UNAVAILABLE = 20,
+    FA_ERR_UNSUPPORTED_HEAD_DIM = 21,
+    FA_ERR_INDEX_SPACE_EXCEEDED = 22,
+    FA_ERR_DISPATCH_LIMIT = 23,
+    FA_ERR_BUFFER_TOO_SMALL = 24,
+    FA_ERR_EMPTY_TABLE = 25,
+    FA_ERR_TOO_MANY_MAPPED_PAGES = 26,
+    FA_ERR_CAUSAL_VISIBILITY_MISMATCH = 27,
+    FA_ERR_ZERO_QUERY_CHUNK_SIZE = 28,
+    FA_ERR_UNSUPPORTED_DTYPE = 29,
+    FA_ERR_INVALID_PAGE = 30,
+    FA_ERR_PAGED_ZERO_DIMENSION = 40,
+    FA_ERR_CAPACITY_OVERFLOW = 41,
+    FA_ERR_CAPACITY_EXCEEDED = 42,
+    FA_ERR_GENERATION_OVERFLOW = 43,
+    FA_ERR_NULL_ARGUMENT = 50,
+    FA_ERR_HIP = 60
+} fa_status;
+
+/* Storage dtype of Q/K/V/O. Math is always f32 (f32 online-softmax state, f32 accumulation);
+ * LSE is always f32. Reference precedent: WgpuIoPrecision src/wgpu_f16_backend.rs:19. */
+typedef enum fa_dtype { FA_DTYPE_F32 = 0, FA_DTYPE_F16 = 1, FA_DTYPE_BF16 = 2 } fa_dtype;
+
+/* AttentionShape src/lib.rs:212. */
+typedef struct fa_attention_shape {
+    uint64_t batch, heads, seq_len, head_dim;
+} fa_attention_shape;
+
+/* GroupedAttentionShape src/grouped.rs:18. */
+typedef struct fa_grouped_shape {
+    uint64_t batch, q_heads, kv_heads, seq_len, head_dim;
+} fa_grouped_shape;
+
+/* AsymmetricGroupedAttentionShape src/asymmetric_grouped.rs:27. */
+typedef struct fa_asymmetric_shape {
+    uint64_t batch, q_heads, kv_heads, query_len, kv_len, head_dim, query_position_offset;
+} fa_asymmetric_shape;
+
+/* FlatAttentionConfig src/lib.rs:249 (softmax_scale: Option<f32> → has_softmax_scale flag). */
+typedef struct fa_config {
+    int32_t causal;
+    int32_t has_softmax_scale;
+    float softmax_scale;
+} fa_config;
+
+/* RotaryEmbeddingConfig src/rotary_grouped.rs:14. */
+typedef struct fa_rotary {
+    float theta;
+    uint64_t position_offset;
+} fa_rotary;
+
+/* AsymmetricRotaryEmbeddingConfig src/projection_asymmetric.rs:19. */
+typedef struct fa_asymmetric_rotary {
+    float theta;
+    uint64_t query_position_offset;
+    uint64_t kv_position_offset;
+} fa_asymmetric_rotary;
+
+/* Packed [O|LSE] geometry. Mirrors PagedDecodeLayout src/wgpu_paged_decode.rs:18 and
+ * WgpuResidentAttentionOutput src/wgpu_backend.rs:133. */
+typedef struct fa_packed_layout {
+    uint64_t output_elements;
+    uint64_t lse_elements;
+    uint64_t output_bytes;
+    uint64_t lse_byte_offset;
+    uint64_t combined_bytes;
+} fa_packed_layout;
+
+/* Kernel identities. Counterpart of RuntimeKernelId src/runtime_telemetry.rs:11 and
+ * WgpuKernelVariant src/wgpu_backend.rs:31. */
+typedef enum fa_kernel_id {
+    FA_KERNEL_NONE = 0,
+    FA_KERNEL_PREFILL_MFMA_BF16 = 1,      /* 32x32x16 bf16 MFMA, K rotated on load */
+    FA_KERNEL_PREFILL_MFMA_F16 = 2,
+    FA_KERNEL_PREFILL_MFMA_F32 = 3,       /* 32x32x2 f32 MFMA (f32 I/O contract) */
+    FA_KERNEL_PREFILL_MFMA_BF16_PREROT = 4, /* K rotated once by a pre-pass */
+    FA_KERNEL_PREFILL_MFMA_F16_PREROT = 5,
+    FA_KERNEL_PREFILL_MFMA_F32_PREROT = 6,
+    FA_KERNEL_DECODE_PAGED_SPLITK = 10,
+    FA_KERNEL_DECODE_COMBINE = 11,
+    FA_KERNEL_PAGED_APPEND = 12,
+    FA_KERNEL_ROPE_TABLE = 13,
+    FA_KERNEL_ROPE_ROTATE = 14
+} fa_kernel_id;
+
+/* RuntimeDispatchTelemetry src/runtime_telemetry.rs:159 + RuntimeTileGeometry :151 +
+ * RuntimeDeviceFingerprint :35. Passive host metadata of the last logical call on a context. */
+typedef struct fa_telemetry {
+    int32_t kernel_id;            /* fa_kernel_id of the dominant (main) kernel */
+    char kernel_name[64];
+    uint32_t query_rows;          /* query rows per workgroup */
+    uint32_t kv_rows;             /* K/V rows per inner tile */
+    uint32_t workgroups[3];       /* grid of the main kernel */
+    uint32_t workgroup_size;
+    uint32_t dispatch_count;      /* kernel launches issued by the logical call */
+    uint32_t temporary_allocation_count;
+    uint64_t temporary_allocation_bytes;
+    uint32_t splits;              /* split-K factor (decode), 1 otherwise */
+    int32_t has_fallback_reason;
+    char fallback_reason[128];
+    char device_name[64];
+    char device_arch[32];
+    uint64_t device_fingerprint;  /* FNV-1a-64 of the canonical device record */
+} fa_telemetry;
+
+typedef struct fa_ctx fa_ctx;
+
+/* ---------------------------------------------------------------- context ---------------
+ * Replaces the owned-context constructors WgpuFlatAttention::new src/wgpu_backend.rs:177 and
+ * WgpuRotaryGroupedAttention::new src/wgpu_rotary_grouped_backend.rs:78. Creates one HIP
+ * stream on `device`; fails with FA_ERR_UNAVAILABLE when no gfx950 device is present. */
+int fa_ctx_create(int device, fa_ctx** out);
+int fa_ctx_destroy(fa_ctx* ctx);
+/* HIP stream (hipStream_t) that every launch of this context is enqueued on. */
+void* fa_ctx_stream(fa_ctx* ctx);
+int fa_ctx_synchronize(fa_ctx* ctx);
+/* adapter_name src/wgpu_backend.rs:337 */
+int fa_ctx_device_name(fa_ctx* ctx, char* buf, size_t len);
+
+const char* fa_status_string(int status);
+const char* fa_last_error_message(void);
+int fa_abi_version(void);
+
+/* Resolved softmax scale: FlatAttentionConfig::resolved_scale src/lib.rs:257. */
+int fa_resolved_scale(const fa_config* config, uint64_t head_dim, float* out);
+
+/* ---------------------------------------------------------------- buffers ---------------
+ * upload src/wgpu_backend.rs:465, download_attention :588. */
+int fa_buf_alloc(fa_ctx* ctx, size_t bytes, void** out);
+int fa_buf_free(fa_ctx* ctx, void* ptr);
+int fa_buf_upload(fa_ctx* ctx, void* dst, const void* host, size_t bytes);
+int fa_buf_download(fa_ctx* ctx, void* host, const void* src, size_t bytes);
+int fa_buf_fill_u32(fa_ctx* ctx, void* dst, uint32_t value, size_t count);
+
+/* ------------------------------------------------------------ packed layouts ------------ */
+/* [O|LSE] geometry for `q_elements` output scalars of `dtype` and `lse_elements` f32. */
+int fa_packed_layout_for(uint64_t output_elements, uint64_t lse_elements, int dtype,
+                         fa_packed_layout* out);
+
+/* ------------------------------------------------------------ prefill ------------------- */
+/* WgpuFlatAttention::forward_resident src/wgpu_backend.rs:484 (MHA, [B,H,S,D]).
+ * q,k,v: `dtype` tensors of shape->tensor_len elements; out_lse: packed [O|LSE]. */
+int fa_forward_mha(fa_ctx* ctx, const void* q, const void* k, const void* v, size_t in_bytes,
+                   void* out_lse, size_t out_bytes, const fa_attention_shape* shape,
+                   const fa_config* config, int dtype);
+
+/* WgpuRotaryGroupedAttention::forward_resident src/wgpu_rotary_grouped_backend.rs:163.
+ * rotary == NULL runs plain GQA/MQA (forward_reference_grouped src/grouped.rs:81).
+ * q_bytes / kv_bytes are the sizes of Q and of each of K, V. */
+int fa_forward_gqa_rope(fa_ctx* ctx, const void* q, size_t q_bytes, const void* k,
+                        const void* v, size_t kv_bytes, void* out_lse, size_t out_bytes,
+                        const fa_grouped_shape* shape, const fa_config* config,
+                        const fa_rotary* rotary, int dtype);
+
+/* Owned-context host forwards: WgpuFlatAttention::forward src/wgpu_backend.rs:445 and
+ * WgpuRotaryGroupedAttention::forward src/wgpu_rotary_grouped_backend.rs:117. Inputs are
+ * validated on the host (length and finiteness, reference validate_input src/lib.rs:428),
+ * uploaded, run and read back. Host data is in `dtype` storage; output O in `dtype`, LSE f32. */
+int fa_forward_mha_host(fa_ctx* ctx, const void* q, const void* k, const void* v,
+                        uint64_t q_len, uint64_t k_len, uint64_t v_len,
+                        const fa_attention_shape* shape, const fa_config* config, int dtype,
+                        void* out, float* lse);
+int fa_forward_gqa_rope_host(fa_ctx* ctx, const void* q, const void* k, const void* v,
+                             uint64_t q_len, uint64_t k_len, uint64_t v_len,
+                             const fa_grouped_shape* shape, const fa_config* config,
+                             const fa_rotary* rotary, int dtype, void* out, float* lse);
+
+/* Rectangular projection-layout GQA + RoPE with a causal query offset:
+ * ExternalAsymmetricProjectionRotaryGroupedPipeline::encode src/wgpu_external_asymmetric.rs:192
+ * (rotate_k = 1) and encode_pre_rotated_k :203 (rotate_k = 0). rotary == NULL: no RoPE. */
+int fa_forward_projection_asymmetric(fa_ctx* ctx, const void* q, size_t q_bytes,
+                                     const void* k, const void* v, size_t kv_bytes,
+                                     void* out_lse, size_t out_bytes,
+                                     const fa_asymmetric_shape* shape, const fa_config* config,
+                                     const fa_asymmetric_rotary* rotary, int32_t rotate_k,
+                                     int dtype);
+
+/* WgpuChunkedProjectionPrefillPipeline::encode src/wgpu_chunked_prefill.rs:156: full-sequence
+ * projection-layout GQA + RoPE prefill whose query rows are processed in chunks of
+ * `query_chunk_size` with absolute causal and RoPE positions. Output is identical for every
+ * chunk size. */
+int fa_chunked_prefill(fa_ctx* ctx, const void* q, size_t q_bytes, const void* k,
+                       const void* v, size_t kv_bytes, void* out_lse, size_t out_bytes,
+                       const fa_grouped_shape* shape, const fa_config* config,
+                       const fa_rotary* rotary, uint64_t query_chunk_size, int dtype);
+
+/* ------------------------------------------------------------ paged KV table ------------
+ * PagedKvTable src/paged_kv.rs:76 (host metadata only). */
+typedef struct fa_kv_table fa_kv_table;
+typedef struct fa_kv_address {
+    uint64_t physical_page, offset_in_page, generation;
+} fa_kv_address;
+typedef struct fa_kv_telemetry {  /* PagedKvTelemetry src/paged_kv.rs:28 */
+    uint64_t live_tokens, capacity_tokens, mapped_pages, free_pages,
+        internal_fragmentation_tokens, generation;
+} fa_kv_telemetry;
+
+int fa_kv_table_create(uint64_t page_size, uint64_t physical_pages, fa_kv_table** out);
+int fa_kv_table_destroy(fa_kv_table* t);
+int fa_kv_table_clone(const fa_kv_table* t, fa_kv_table** out);
+int fa_kv_table_append(fa_kv_table* t, uint64_t tokens);     /* append :113 */
+/* address :143 — returns FA_OK and fills `out`, or FA_ERR_EMPTY_TABLE when unmapped. */
+int fa_kv_table_address(const fa_kv_table* t, uint64_t logical_token, fa_kv_address* out);
+int fa_kv_table_telemetry(const fa_kv_table* t, fa_kv_telemetry* out); /* telemetry :160 */
+int fa_kv_table_reset(fa_kv_table* t);                        /* reset :176 */
+uint64_t fa_kv_table_len(const fa_kv_table* t);
+/* WgpuPagedKvTable::from_table src/wgpu_paged_decode.rs:162: flattens the live logical pages
+ * to physical page ids. `*count` receives the number of mapped pages. */
+int fa_kv_table_block_row(const fa_kv_table* t, int32_t* out, uint64_t capacity,
+                          uint64_t* count);
+
+/* ------------------------------------------------------------ paged KV cache ------------
+ * WgpuPagedKvCache src/wgpu_paged_kv_cache.rs:76. Device storage
+ * [physical_pages, page_size, kv_heads*head_dim] in `dtype` for K and V, plus a table. */
+typedef struct fa_paged_cache fa_paged_cache;
+int fa_paged_cache_create(fa_ctx* ctx, uint64_t page_size, uint64_t physical_pages,
+                          uint64_t kv_heads, uint64_t head_dim, int dtype,
+                          fa_paged_cache** out);                   /* new :99 */
+int fa_paged_cache_destroy(fa_paged_cache* cache);
+/* record_append :206. Sources are device [append_len, kv_heads*head_dim] rows. K must already
+ * be RoPE-rotated (reference contract :73) unless `rotate_k` is non-NULL, in which case rows are
+ * rotated at positions rotate_k->position_offset + live_len + i while they are scattered. */
+int fa_paged_cache_append(fa_paged_cache* cache, const void* k_src, const void* v_src,
+                          size_t src_bytes, uint64_t append_len, const fa_rotary* rotate_k,
+                          uint64_t* new_len);
+int fa_paged_cache_reset(fa_paged_cache* cache);                  /* reset */
+const fa_kv_table* fa_paged_cache_table(const fa_paged_cache* cache); /* table */
+void* fa_paged_cache_k(fa_paged_cache* cache);                    /* k_buffer */
+void* fa_paged_cache_v(fa_paged_cache* cache);                    /* v_buffer */
+size_t fa_paged_cache_bytes(const fa_paged_cache* cache);          /* bytes of K (= of V) */
+
+/* ------------------------------------------------------------ paged decode --------------
+ * WgpuPagedDecodePipeline::encode src/wgpu_paged_decode.rs:300 generalised to a batch of
+ * sequences over one shared page pool. Prepare validates the host block tables (every entry a
+ * valid physical page, coverage of each context, causal visibility q_position + 1 >= ctx_len)
+ * and makes them resident; launch enqueues the split-K kernel plus the LSE combine.
+ *   block_tables: [n_seqs, max_pages] int32 physical page ids (host)
+ *   ctx_lens:     [n_seqs] live tokens per sequence (host)
+ *   q_positions:  [n_seqs] RoPE position of each query, NULL → ctx_len - 1
+ *   q:            [n_seqs, q_heads*head_dim], out_lse: [O n_seqs*q_heads*head_dim | LSE n_seqs*q_heads]
+ */
+typedef struct fa_decode_plan fa_decode_plan;
+int fa_paged_decode_prepare(fa_ctx* ctx, const int32_t* block_tables, uint64_t max_pages,
+                            const int32_t* ctx_lens, const int32_t* q_positions,
+                            uint64_t n_seqs, uint64_t page_size, uint64_t physical_pages,
+                            uint64_t q_heads, uint64_t kv_heads, uint64_t head_dim,
+                            const fa_config* config, float theta, int dtype,
+                            fa_decode_plan** out);
+int fa_paged_decode_launch(fa_ctx* ctx, const fa_decode_plan* plan, const void* q,
+                           size_t q_bytes, const void* k_pool, const void* v_pool,
+                           size_t pool_bytes, void* out_lse, size_t out_bytes);
+int fa_paged_decode_plan_destroy(fa_decode_plan* plan);
+/* Number of split-K partitions per sequence the plan uses (tokens per split). */
+int fa_paged_decode_plan_info(const fa_decode_plan* plan, uint64_t* split_tokens,
+                              uint64_t* work_items, uint64_t* workspace_bytes);
+/* Override tokens per split (multiple of 16; 0 = automatic) before launch. Tests use this to
+ * check split invariance. */
+int fa_paged_decode_plan_set_split(fa_ctx* ctx, fa_decode_plan* plan, uint64_t split_tokens);
+
+/* Single-sequence convenience mirror of WgpuPagedDecodePipeline::encode: decode one query
+ * vector over `cache` at `q_rope_position`. */
+int fa_paged_cache_decode(fa_ctx* ctx, const fa_paged_cache* cache, const void* q,
+                          size_t q_bytes, uint64_t q_heads, const fa_config* config,
+                          float theta, uint64_t q_rope_position, void* out_lse,
+                          size_t out_bytes);
+
+/* ------------------------------------------------------------ chunked prefill (paged) ---
+ * Chunked prefill whose K/V live in the shared page pool: the chunk's queries
+ * [batch, query_len, q_heads*head_dim] attend causally (query i at absolute position
+ * query_position_offset + i) over kv_len live tokens of each sequence's block table.
+ * K in the pool is pre-rotated; Q is rotated at rotary->query_position_offset + i.
+ * Follows forward_reference_projection_grouped_rope_chunked_prefill
+ * src/chunked_projection_prefill.rs:63 with the K/V source of WgpuPagedKvCache. */
+typedef struct fa_prefill_plan fa_prefill_plan;
+int fa_chunked_prefill_paged_prepare(fa_ctx* ctx, const int32_t* block_tables,
+                                     uint64_t max_pages, uint64_t page_size,
+                                     uint64_t physical_pages, const fa_asymmetric_shape* shape,
+                                     const fa_config* config, const fa_asymmetric_rotary* rotary,
+                                     int dtype, fa_prefill_plan** out);
+int fa_chunked_prefill_paged_launch(fa_ctx* ctx, const fa_prefill_plan* plan, const void* q,
+                                    size_t q_bytes, const void* k_pool, const void* v_pool,
+                                    size_t pool_bytes, void* out_lse, size_t out_bytes);
+int fa_prefill_plan_destroy(fa_prefill_plan* plan);
+
+/* Batched paged append with RoPE-on-append (record_append src/wgpu_paged_kv_cache.rs:206 for a
+ * batch of sequences): rows i of sequence s, from [n_seqs, append_len, kv_heads*head_dim]
+ * sources, land at logical token start_lens[s] + i of that sequence's block table. K rows are
+ * rotated at position rotary->position_offset + start_lens[s] + i when rotary != NULL.
+ * block_tables [n_seqs, max_pages] and start_lens [n_seqs] are host arrays, validated (page ids,
+ * capacity) before anything is enqueued; the call returns once the scatter has completed. */
+int fa_paged_append_batched(fa_ctx* ctx, const int32_t* block_tables, uint64_t max_pages,
+                            const int32_t* start_lens, uint64_t n_seqs, uint64_t append_len,
+                            uint64_t page_size, uint64_t physical_pages, uint64_t kv_heads,
+                            uint64_t head_dim, const void* k_src, const void* v_src,
+                            size_t src_bytes, void* k_pool, void* v_pool, size_t pool_bytes,
+                            const fa_rotary* rotary, int dtype);
+
+/* ------------------------------------------------------------ telemetry ------------------
+ * runtime_telemetry src/wgpu_backend.rs:374: metadata of the last logical call on `ctx`. */
+int fa_last_telemetry(fa_ctx* ctx, fa_telemetry* out);
+
+/* Variant selection policy. kernel_variant_for_head_dim src/wgpu_backend.rs:430.
+ * prerotate_k: 0 = rotate K tiles on load inside the prefill kernel, 1 = rotate K once in a
+ * pre-pass, -1 = automatic (default). */
+int fa_ctx_set_prefill_policy(fa_ctx* ctx, int32_t prerotate_k);
+int fa_kernel_variant_for_shape(fa_ctx* ctx, uint64_t head_dim, int32_t has_rope, int dtype,
+                                int32_t* kernel_id);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FLAT_HIP_H */

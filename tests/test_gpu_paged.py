@@ -1,0 +1,333 @@
+"""GPU parity of the paged KV cache, split-K paged decode and paged chunked prefill.
+
+Paged gather indexing is checked bit-exactly: the same data under a shuffled block table must
+give bitwise identical output to the identity table. Numerics: f32 2e-5 + 1e-4|e|; bf16 2e-2.
+"""
+import numpy as np
+import pytest
+
+import oracle
+from _inputs import bf16_round, normal
+from conftest import assert_close
+
+import flat_attention_amd as fa
+
+pytestmark = pytest.mark.gpu
+
+F32_ATOL, F32_RTOL = 2e-5, 1e-4
+H16_ATOL = 2e-2
+
+
+def _fixture(n, phase):
+    """Closed-form generator of tests/m16_paged_decode.rs:49-56."""
+    x = np.arange(n, dtype=np.float32) * np.float32(0.021) + np.float32(phase)
+    return (np.sin(x) * np.float32(1.1875) + np.cos(x * np.float32(0.43)) * np.float32(0.34375)).astype(np.float32)
+
+
+def test_m16_paged_decode_matches_contiguous_oracle_across_page_boundaries(hip):
+    """tests/m16_paged_decode.rs:171: Hq4 Hkv2 kv_len 7, page 3, 4 physical pages, D64, f32,
+    unused rows filled with sentinels 17.0 / -19.0."""
+    hq, hkv, kv_len, ps, pages, D, theta = 4, 2, 7, 3, 4, 64, 10000.0
+    qpos = kv_len - 1
+    q = _fixture(hq * D, 0.2)
+    raw_k = _fixture(kv_len * hkv * D, 0.8)
+    v = _fixture(kv_len * hkv * D, 1.4)
+    eo, el = oracle.forward_projection_asymmetric(q, raw_k, v, 1, hq, hkv, 1, kv_len, D, qpos,
+                                                  True, theta, qpos, 0, True)
+    rot_k = oracle.rope_rotate_rows(raw_k, kv_len, hkv, D, theta)
+    rows, width = ps * pages, hkv * D
+    pk = np.full(rows * width, 17.0, np.float32)
+    pv = np.full(rows * width, -19.0, np.float32)
+    pk[:rot_k.size] = rot_k
+    pv[:v.size] = v
+    table = fa.PagedKvTable(fa.PagedKvConfig(ps, pages))
+    table.append(kv_len)
+    assert table.telemetry().mapped_pages == 3
+    row = table.block_row()
+    plan = fa.PagedDecodePlan(hip, row[None, :], np.array([kv_len]), ps, pages, hq, hkv, D,
+                              fa.FlatAttentionConfig(True), theta, fa.DTYPE_F32,
+                              q_positions=np.array([qpos]))
+    qb, kb, vb = (fa.DeviceBuffer.from_array(hip, x) for x in (q, pk, pv))
+    out = fa.DeviceBuffer(hip, plan.layout().combined_bytes)
+    plan.launch(qb, kb, vb, out)
+    res = fa.download_attention(out, plan.layout(), fa.DTYPE_F32)
+    assert_close("paged O", res.output, eo, F32_ATOL, F32_RTOL)
+    assert_close("paged LSE", res.lse, el, F32_ATOL, F32_RTOL)
+    t = hip.last_telemetry()
+    assert t.kernel_id == "DecodePagedSplitK" and t.dispatch_count == 2
+
+
+def _make_pool(rng, ctx_lens, ps, hkv, D, rnd, shuffle=True, seed=7):
+    pages_per = [(c + ps - 1) // ps for c in ctx_lens]
+    total = sum(pages_per)
+    ids = rng.permutation(total) if shuffle else np.arange(total)
+    max_pages = max(pages_per)
+    bt = np.zeros((len(ctx_lens), max_pages), np.int32)
+    cur = 0
+    for s, n in enumerate(pages_per):
+        bt[s, :n] = ids[cur:cur + n]
+        cur += n
+    width = hkv * D
+    kp = rnd(normal(total * ps * width, seed))
+    vp = rnd(normal(total * ps * width, seed + 1))
+    return bt, kp, vp, total
+
+
+def _decode(hip, bt, ctx_lens, kp, vp, total, ps, hq, hkv, D, q, dtype, theta=1e4, split=None,
+            causal=True):
+    plan = fa.PagedDecodePlan(hip, bt, np.asarray(ctx_lens), ps, total, hq, hkv, D,
+                              fa.FlatAttentionConfig(causal), theta, dtype)
+    if split is not None:
+        plan.set_split(split)
+    qb, kb, vb = (fa.DeviceBuffer.from_array(hip, fa.host_storage(x, dtype)) for x in (q, kp, vp))
+    out = fa.DeviceBuffer(hip, plan.layout().combined_bytes)
+    plan.launch(qb, kb, vb, out)
+    res = fa.download_attention(out, plan.layout(), dtype)
+    return fa.storage_to_f32(res.output, dtype), res.lse, plan
+
+
+@pytest.mark.parametrize("hq,hkv", [(32, 8), (8, 8), (32, 1), (12, 4)])
+def test_batched_bf16_decode_matches_oracle(hip, hq, hkv):
+    rng = np.random.default_rng(hq * 10 + hkv)
+    ps, D = 16, 128
+    ctx_lens = [1, 15, 16, 17, 100, 513, 1000, 2049]
+    bt, kp, vp, total = _make_pool(rng, ctx_lens, ps, hkv, D, bf16_round)
+    q = bf16_round(normal(len(ctx_lens) * hq * D, 3))
+    o, l, _ = _decode(hip, bt, ctx_lens, kp, vp, total, ps, hq, hkv, D, q, fa.DTYPE_BF16)
+    eo, el = oracle.paged_decode(q, kp, vp, total, ps, bt, ctx_lens, hq, hkv, D, True, 1e4)
+    assert_close("O", o, eo, H16_ATOL, 0.0)
+    assert_close("LSE", l, el, H16_ATOL, 0.0)
+
+
+@pytest.mark.parametrize("ps", [3, 16, 32])
+@pytest.mark.parametrize("D", [64, 128])
+def test_f32_decode_matches_oracle(hip, ps, D):
+    rng = np.random.default_rng(ps + D)
+    hq, hkv = 8, 2
+    ctx_lens = [5, 48, 333, 900]
+    bt, kp, vp, total = _make_pool(rng, ctx_lens, ps, hkv, D, lambda x: x)
+    q = normal(len(ctx_lens) * hq * D, 4)
+    o, l, _ = _decode(hip, bt, ctx_lens, kp, vp, total, ps, hq, hkv, D, q, fa.DTYPE_F32)
+    eo, el = oracle.paged_decode(q, kp, vp, total, ps, bt, ctx_lens, hq, hkv, D, True, 1e4)
+    assert_close("O", o, eo, F32_ATOL, F32_RTOL)
+    assert_close("LSE", l, el, F32_ATOL, F32_RTOL)
+
+
+def test_shuffled_block_table_is_bitwise_identical_to_identity(hip):
+    """Same logical K/V rows placed under a shuffled vs identity page map."""
+    rng = np.random.default_rng(3)
+    ps, hq, hkv, D = 16, 32, 8, 128
+    ctx_lens = [700, 1500, 33]
+    bt_id, kp, vp, total = _make_pool(rng, ctx_lens, ps, hkv, D, bf16_round, shuffle=False)
+    perm = rng.permutation(total)
+    width = ps * hkv * D
+    kp2 = np.empty_like(kp)
+    vp2 = np.empty_like(vp)
+    for logical_page in range(total):  # identity page p moves to physical perm[p]
+        kp2[perm[logical_page] * width:(perm[logical_page] + 1) * width] = kp[logical_page * width:(logical_page + 1) * width]
+        vp2[perm[logical_page] * width:(perm[logical_page] + 1) * width] = vp[logical_page * width:(logical_page + 1) * width]
+    bt_sh = np.where(bt_id >= 0, perm[bt_id], 0).astype(np.int32)
+    q = bf16_round(normal(len(ctx_lens) * hq * D, 9))
+    o1, l1, _ = _decode(hip, bt_id, ctx_lens, kp, vp, total, ps, hq, hkv, D, q, fa.DTYPE_BF16)
+    o2, l2, _ = _decode(hip, bt_sh, ctx_lens, kp2, vp2, total, ps, hq, hkv, D, q, fa.DTYPE_BF16)
+    assert np.array_equal(o1.view(np.uint32), o2.view(np.uint32))
+    assert np.array_equal(l1.view(np.uint32), l2.view(np.uint32))
+
+
+def test_split_count_invariance(hip):
+    rng = np.random.default_rng(5)
+    ps, hq, hkv, D = 16, 32, 8, 128
+    ctx_lens = [4000, 17, 1234]
+    bt, kp, vp, total = _make_pool(rng, ctx_lens, ps, hkv, D, bf16_round)
+    q = bf16_round(normal(len(ctx_lens) * hq * D, 2))
+    ref = None
+    for split in (16, 64, 256, 4096):
+        o, l, plan = _decode(hip, bt, ctx_lens, kp, vp, total, ps, hq, hkv, D, q, fa.DTYPE_BF16,
+                             split=split)
+        assert plan.info()["split_tokens"] == split
+        if ref is None:
+            ref = (o, l)
+        else:
+            assert_close(f"O split {split}", o, ref[0], 1e-2, 0.0)
+            assert_close(f"LSE split {split}", l, ref[1], 1e-4, 1e-5)
+
+
+def test_cfg4_full_size_bf16_decode(hip):
+    """64 sequences, ctx ~ U[512, 8192], page 16, Hq32 Hkv8 D128, bf16 KV,
+    randomly permuted physical pages. Full oracle comparison."""
+    rng = np.random.default_rng(2024)
+    ps, hq, hkv, D = 16, 32, 8, 128
+    ctx_lens = rng.integers(512, 8193, 64).tolist()
+    bt, kp, vp, total = _make_pool(rng, ctx_lens, ps, hkv, D, bf16_round, seed=40)
+    q = bf16_round(normal(64 * hq * D, 41))
+    o, l, _ = _decode(hip, bt, ctx_lens, kp, vp, total, ps, hq, hkv, D, q, fa.DTYPE_BF16)
+    eo, el = oracle.paged_decode(q, kp, vp, total, ps, bt, ctx_lens, hq, hkv, D, True, 1e4,
+                                 threads=8)
+    assert_close("O", o, eo, H16_ATOL, 0.0)
+    assert_close("LSE", l, el, H16_ATOL, 0.0)
+
+
+def test_decode_validation_errors(hip):
+    bt = np.array([[0, 1]], np.int32)
+    cfg = fa.FlatAttentionConfig(True)
+    with pytest.raises(fa.FlatHipError) as e:
+        fa.PagedDecodePlan(hip, bt, np.array([20]), 16, 2, 4, 2, 64, cfg, 1e4, fa.DTYPE_F32,
+                           q_positions=np.array([10]))
+    assert e.value.variant == "CausalVisibilityMismatch"
+    with pytest.raises(fa.FlatHipError) as e:
+        fa.PagedDecodePlan(hip, np.array([[0, 5]], np.int32), np.array([20]), 16, 2, 4, 2, 64,
+                           cfg, 1e4, fa.DTYPE_F32)
+    assert e.value.variant == "InvalidPage"
+    with pytest.raises(fa.FlatHipError) as e:
+        fa.PagedDecodePlan(hip, bt, np.array([0]), 16, 2, 4, 2, 64, cfg, 1e4, fa.DTYPE_F32)
+    assert e.value.variant == "EmptyTable"
+    with pytest.raises(fa.FlatHipError) as e:
+        fa.PagedDecodePlan(hip, bt, np.array([20]), 16, 2, 4, 2, 64, cfg, float("nan"),
+                           fa.DTYPE_F32)
+    assert e.value.variant == "InvalidRotaryTheta"
+
+
+# ------------------------------------------------------------------------------- cache
+
+
+def test_paged_cache_append_crosses_pages_and_never_rewrites_prefix(hip):
+    """tests/m16_paged_kv_cache.rs:159: appends split at page boundaries, prefix untouched."""
+    ps, pages, hkv, D = 4, 5, 2, 16
+    cache = fa.HipPagedKvCache(hip, fa.PagedKvConfig(ps, pages), hkv, D, fa.DTYPE_F32)
+    width = hkv * D
+    src_k1, src_v1 = normal(6 * width, 1), normal(6 * width, 2)
+    src_k2, src_v2 = normal(5 * width, 3), normal(5 * width, 4)
+    kb1, vb1 = fa.DeviceBuffer.from_array(hip, src_k1), fa.DeviceBuffer.from_array(hip, src_v1)
+    assert cache.record_append(kb1, vb1, 6) == 6
+    before = cache.k_buffer().download(np.float32, ps * pages * width).copy()
+    kb2, vb2 = fa.DeviceBuffer.from_array(hip, src_k2), fa.DeviceBuffer.from_array(hip, src_v2)
+    assert cache.record_append(kb2, vb2, 5) == 11
+    kpool = cache.k_buffer().download(np.float32, ps * pages * width)
+    vpool = cache.v_buffer().download(np.float32, ps * pages * width)
+    table = cache.table()
+    allk = np.concatenate([src_k1, src_k2]).reshape(11, width)
+    allv = np.concatenate([src_v1, src_v2]).reshape(11, width)
+    for tok in range(11):
+        a = table.address(tok)
+        r = a.physical_page * ps + a.offset_in_page
+        assert np.array_equal(kpool[r * width:(r + 1) * width], allk[tok])
+        assert np.array_equal(vpool[r * width:(r + 1) * width], allv[tok])
+    for tok in range(6):  # prefix rows unchanged by the second append
+        a = table.address(tok)
+        r = a.physical_page * ps + a.offset_in_page
+        assert np.array_equal(before[r * width:(r + 1) * width], kpool[r * width:(r + 1) * width])
+    big_k = fa.DeviceBuffer.from_array(hip, normal(10 * width, 5))
+    big_v = fa.DeviceBuffer.from_array(hip, normal(10 * width, 6))
+    with pytest.raises(fa.FlatHipError) as e:
+        cache.record_append(kb2, vb2, 10)  # source holds 5 rows: rejected before the table
+    assert e.value.variant == "BufferTooSmall"
+    with pytest.raises(fa.FlatHipError) as e:
+        cache.record_append(big_k, big_v, 10)  # 21 > 20 tokens of capacity
+    assert e.value.variant == "CapacityExceeded"
+    assert len(cache.table()) == 11  # failed appends leave the table unchanged
+
+
+def test_paged_cache_feeds_decode_with_rotate_on_append(hip):
+    """Cache filled through rotate-on-append decodes like the raw-K asymmetric oracle."""
+    ps, pages, hq, hkv, D, theta = 16, 8, 8, 2, 64, 1e4
+    n = 75
+    cache = fa.HipPagedKvCache(hip, fa.PagedKvConfig(ps, pages), hkv, D, fa.DTYPE_F32)
+    raw_k, v = normal(n * hkv * D, 5), normal(n * hkv * D, 6)
+    cache.record_append(fa.DeviceBuffer.from_array(hip, raw_k[:40 * hkv * D]),
+                        fa.DeviceBuffer.from_array(hip, v[:40 * hkv * D]), 40,
+                        rotate_k=fa.RotaryEmbeddingConfig(theta, 0))
+    cache.record_append(fa.DeviceBuffer.from_array(hip, raw_k[40 * hkv * D:]),
+                        fa.DeviceBuffer.from_array(hip, v[40 * hkv * D:]), n - 40,
+                        rotate_k=fa.RotaryEmbeddingConfig(theta, 0))
+    q = normal(hq * D, 7)
+    pipe = fa.HipPagedDecodePipeline(hip, fa.DTYPE_F32)
+    out = pipe.create_output_buffer(hq, D)
+    lay = pipe.encode(fa.DeviceBuffer.from_array(hip, q), cache, out, hq,
+                      fa.FlatAttentionConfig(True), theta, n - 1)
+    res = fa.download_attention(out, lay, fa.DTYPE_F32)
+    eo, el = oracle.forward_projection_asymmetric(q, raw_k, v, 1, hq, hkv, 1, n, D, n - 1, True,
+                                                  theta, n - 1, 0, True)
+    assert_close("O", res.output, eo, F32_ATOL, F32_RTOL)
+    assert_close("LSE", res.lse, el, F32_ATOL, F32_RTOL)
+
+
+def test_batched_append_scatter_is_bit_exact(hip):
+    rng = np.random.default_rng(11)
+    ps, hkv, D, n_seqs, app = 16, 8, 128, 4, 40
+    starts = np.array([0, 5, 16, 31], np.int32)
+    pages_per = [(s + app + ps - 1) // ps for s in starts]
+    total = sum(pages_per) + 3
+    ids = rng.permutation(total)
+    bt = np.zeros((n_seqs, max(pages_per)), np.int32)
+    cur = 0
+    for s, n in enumerate(pages_per):
+        bt[s, :n] = ids[cur:cur + n]
+        cur += n
+    width = hkv * D
+    ks = bf16_round(normal(n_seqs * app * width, 1))
+    vs = bf16_round(normal(n_seqs * app * width, 2))
+    pool_el = total * ps * width
+    kp = fa.DeviceBuffer(hip, pool_el * 2)
+    vp = fa.DeviceBuffer(hip, pool_el * 2)
+    kp.fill_u32(0)
+    vp.fill_u32(0)
+    fa.paged_append_batched(hip, bt, starts, app, ps, total, hkv, D,
+                            fa.DeviceBuffer.from_array(hip, fa.host_storage(ks, fa.DTYPE_BF16)),
+                            fa.DeviceBuffer.from_array(hip, fa.host_storage(vs, fa.DTYPE_BF16)),
+                            kp, vp, None, fa.DTYPE_BF16)
+    kpool = fa.bf16_bits_to_f32(kp.download(np.uint16, pool_el))
+    vpool = fa.bf16_bits_to_f32(vp.download(np.uint16, pool_el))
+    for s in range(n_seqs):
+        for i in range(app):
+            tok = int(starts[s]) + i
+            r = bt[s, tok // ps] * ps + tok % ps
+            src = (s * app + i) * width
+            assert np.array_equal(kpool[r * width:(r + 1) * width], ks[src:src + width])
+            assert np.array_equal(vpool[r * width:(r + 1) * width], vs[src:src + width])
+
+
+def test_cfg5_chunked_prefill_over_paged_cache(hip):
+    """BASELINE configs[4] shape, reduced batch for the oracle: each sequence holds 2048 cached
+    tokens + a new 512-token chunk in a shuffled page pool; the chunk attends causally at
+    offset 2048 with Q RoPE at 2048 + i and pre-rotated K (rotate-on-append)."""
+    rng = np.random.default_rng(8)
+    n_seqs, hq, hkv, D, ps, cached, ql, theta = 2, 32, 8, 128, 16, 2048, 512, 1e4
+    kv_len = cached + ql
+    pages_per = kv_len // ps
+    total = n_seqs * pages_per
+    bt = rng.permutation(total).astype(np.int32).reshape(n_seqs, pages_per)
+    width = hkv * D
+    raw_k = bf16_round(normal(n_seqs * kv_len * width, 1))
+    v = bf16_round(normal(n_seqs * kv_len * width, 2))
+    q = bf16_round(normal(n_seqs * ql * hq * D, 3))
+    kp = fa.DeviceBuffer(hip, total * ps * width * 2)
+    vp = fa.DeviceBuffer(hip, total * ps * width * 2)
+    fa.paged_append_batched(hip, bt, np.zeros(n_seqs, np.int32), kv_len, ps, total, hkv, D,
+                            fa.DeviceBuffer.from_array(hip, fa.host_storage(raw_k, fa.DTYPE_BF16)),
+                            fa.DeviceBuffer.from_array(hip, fa.host_storage(v, fa.DTYPE_BF16)),
+                            kp, vp, fa.RotaryEmbeddingConfig(theta, 0), fa.DTYPE_BF16)
+    shape = fa.AsymmetricGroupedAttentionShape(n_seqs, hq, hkv, ql, kv_len, D, cached)
+    plan = fa.PagedChunkedPrefillPlan(hip, bt, ps, total, shape, fa.FlatAttentionConfig(True),
+                                      fa.AsymmetricRotaryEmbeddingConfig(theta, cached, 0),
+                                      fa.DTYPE_BF16)
+    out = fa.DeviceBuffer(hip, plan.layout().combined_bytes)
+    plan.launch(fa.DeviceBuffer.from_array(hip, fa.host_storage(q, fa.DTYPE_BF16)), kp, vp, out)
+    res = fa.download_attention(out, plan.layout(), fa.DTYPE_BF16)
+    o = fa.storage_to_f32(res.output, fa.DTYPE_BF16)
+    # oracle: RoPE materialised on Q (positions cached + i) and K (positions 0..kv_len-1) —
+    # bit-exact to rotation inside the dot product (pinned in test_oracle.py) — then the
+    # asymmetric oracle without RoPE on two head units per sequence.
+    for s in range(n_seqs):
+        sl_kv = slice(s * kv_len * width, (s + 1) * kv_len * width)
+        qs = oracle.rope_rotate_rows(q[s * ql * hq * D:(s + 1) * ql * hq * D], ql, hq, D, theta,
+                                     cached)
+        ks = oracle.rope_rotate_rows(raw_k[sl_kv], kv_len, hkv, D, theta, 0)
+        for unit in (0, hq - 1):
+            eo, el = oracle.forward_projection_asymmetric(
+                qs, ks, v[sl_kv], 1, hq, hkv, ql, kv_len, D, cached, True, None,
+                units=(unit, unit + 1))
+            got = o[s * ql * hq * D:(s + 1) * ql * hq * D].reshape(ql, hq, D)[:, unit]
+            exp = eo.reshape(ql, hq, D)[:, unit]
+            assert_close(f"O seq {s} head {unit}", got, exp, H16_ATOL, 0.0)
+            gl = res.lse[(s * hq + unit) * ql:(s * hq + unit + 1) * ql]
+            assert_close(f"LSE seq {s} head {unit}", gl, el[unit * ql:(unit + 1) * ql], H16_ATOL, 0.0)

@@ -1,0 +1,244 @@
+"""GPU parity of the MFMA prefill kernels against the CPU oracle (through the C ABI).
+
+Tolerances: f32 I/O |a-e| <= 2e-5 + 1e-4|e| for O and LSE;
+16-bit I/O (f16/bf16 storage, f32 accumulation) max-abs 2e-2 after quantising the oracle's
+inputs to the storage type (tests/wgpu_f16.rs:68-100 convention).
+"""
+import numpy as np
+import pytest
+
+import oracle
+from _inputs import bf16_round, f16_round, normal
+from conftest import assert_close
+
+import flat_attention_amd as fa
+
+pytestmark = pytest.mark.gpu
+
+F32_ATOL, F32_RTOL = 2e-5, 1e-4
+H16_ATOL = 2e-2
+
+
+def _run_grouped(hip, q, k, v, shape, cfg, rot, dtype):
+    ex = fa.HipRotaryGroupedAttention(hip, dtype)
+    qb, kb, vb = (fa.DeviceBuffer.from_array(hip, fa.host_storage(x, dtype)) for x in (q, k, v))
+    out = ex.forward_resident(qb, kb, vb, shape, cfg, rot)
+    res = ex.download_attention(out, shape)
+    return fa.storage_to_f32(res.output, dtype), res.lse
+
+
+def _oracle_grouped(q, k, v, shape, causal, rot, units=oracle.UNIT_ALL):
+    args = (q, k, v, shape.batch, shape.q_heads, shape.kv_heads, shape.seq_len, shape.head_dim,
+            causal)
+    if rot is None:
+        return oracle.forward_grouped(*args, units=units)
+    return oracle.forward_grouped_rope(*args, rot.theta, rot.position_offset, units=units)
+
+
+def test_cfg1_mha_f32_causal_matches_oracle(hip):
+    """MHA B1 H2 N128 D64 causal f32."""
+    B, H, S, D = 1, 2, 128, 64
+    q, k, v = (normal(B * H * S * D, s) for s in (11, 12, 13))
+    shape = fa.AttentionShape(B, H, S, D)
+    cfg = fa.FlatAttentionConfig(causal=True)
+    ex = fa.HipFlatAttention(hip, fa.DTYPE_F32)
+    res = ex.forward(q, k, v, shape, cfg)
+    eo, el = oracle.forward(q, k, v, B, H, S, D, True)
+    assert_close("O", res.output, eo, F32_ATOL, F32_RTOL)
+    assert_close("LSE", res.lse, el, F32_ATOL, F32_RTOL)
+    t = ex.runtime_telemetry()
+    assert t.kernel_id == "PrefillMfmaF32" and t.dispatch_count == 1
+    assert t.device_arch.startswith("gfx950")
+
+
+@pytest.mark.parametrize("D", [32, 64, 80, 128])
+@pytest.mark.parametrize("S", [1, 7, 64, 65, 130])
+@pytest.mark.parametrize("causal", [False, True])
+def test_mha_f32_shapes(hip, D, S, causal):
+    B, H = 2, 3
+    q, k, v = (normal(B * H * S * D, 100 + s + D + S) for s in range(3))
+    shape = fa.GroupedAttentionShape(B, H, H, S, D)
+    o, l = _run_grouped(hip, q, k, v, shape, fa.FlatAttentionConfig(causal), None, fa.DTYPE_F32)
+    eo, el = _oracle_grouped(q, k, v, shape, causal, None)
+    assert_close("O", o, eo, F32_ATOL, F32_RTOL)
+    assert_close("LSE", l, el, F32_ATOL, F32_RTOL)
+
+
+@pytest.mark.parametrize("hq,hkv", [(4, 4), (8, 2), (6, 1), (32, 8)])
+@pytest.mark.parametrize("theta,offset", [(1e4, 0), (5e5, 37)])
+def test_gqa_rope_f32(hip, hq, hkv, theta, offset):
+    B, S, D = 1, 97, 64
+    q = normal(B * hq * S * D, 1)
+    k, v = normal(B * hkv * S * D, 2), normal(B * hkv * S * D, 3)
+    shape = fa.GroupedAttentionShape(B, hq, hkv, S, D)
+    rot = fa.RotaryEmbeddingConfig(theta, offset)
+    for causal in (True, False):
+        o, l = _run_grouped(hip, q, k, v, shape, fa.FlatAttentionConfig(causal), rot, fa.DTYPE_F32)
+        eo, el = _oracle_grouped(q, k, v, shape, causal, rot)
+        assert_close("O", o, eo, F32_ATOL, F32_RTOL)
+        assert_close("LSE", l, el, F32_ATOL, F32_RTOL)
+
+
+@pytest.mark.parametrize("dtype,rnd", [(fa.DTYPE_BF16, bf16_round), (fa.DTYPE_F16, f16_round)])
+@pytest.mark.parametrize("D", [64, 128])
+def test_gqa_rope_16bit(hip, dtype, rnd, D):
+    B, hq, hkv, S = 2, 8, 2, 200
+    q = rnd(normal(B * hq * S * D, 21))
+    k, v = rnd(normal(B * hkv * S * D, 22)), rnd(normal(B * hkv * S * D, 23))
+    shape = fa.GroupedAttentionShape(B, hq, hkv, S, D)
+    rot = fa.RotaryEmbeddingConfig(1e4, 5)
+    for causal in (True, False):
+        o, l = _run_grouped(hip, q, k, v, shape, fa.FlatAttentionConfig(causal), rot, dtype)
+        eo, el = _oracle_grouped(q, k, v, shape, causal, rot)
+        assert_close("O", o, eo, H16_ATOL, 0.0)
+        assert_close("LSE", l, el, H16_ATOL, 0.0)
+
+
+def test_prerotated_and_fused_k_rotation_are_bit_identical(hip):
+    B, hq, hkv, S, D = 1, 8, 2, 150, 128
+    q, k, v = (bf16_round(normal(n, s)) for n, s in
+               ((B * hq * S * D, 1), (B * hkv * S * D, 2), (B * hkv * S * D, 3)))
+    shape = fa.GroupedAttentionShape(B, hq, hkv, S, D)
+    rot = fa.RotaryEmbeddingConfig(1e4, 0)
+    cfg = fa.FlatAttentionConfig(True)
+    hip.set_prefill_policy(0)
+    o0, l0 = _run_grouped(hip, q, k, v, shape, cfg, rot, fa.DTYPE_BF16)
+    assert hip.last_telemetry().kernel_id == "PrefillMfmaBf16"
+    hip.set_prefill_policy(1)
+    o1, l1 = _run_grouped(hip, q, k, v, shape, cfg, rot, fa.DTYPE_BF16)
+    t = hip.last_telemetry()
+    assert t.kernel_id == "PrefillMfmaBf16PreRotatedK" and t.dispatch_count == 2
+    hip.set_prefill_policy(-1)
+    assert np.array_equal(o0.view(np.uint32), o1.view(np.uint32))
+    assert np.array_equal(l0.view(np.uint32), l1.view(np.uint32))
+
+
+def test_cfg3_full_size_bf16_gqa_rope_causal(hip):
+    """BASELINE configs[2] at full size: B2 Hq32 Hkv8 N4096 D128 bf16, theta 1e4, causal.
+    The oracle checks two full (batch, head) units via materialised RoPE (bit-exact to the fused
+    oracle, pinned in test_oracle.py); every row is checked for finiteness and LSE bounds."""
+    B, hq, hkv, S, D = 2, 32, 8, 4096, 128
+    q = bf16_round(normal(B * hq * S * D, 31))
+    k = bf16_round(normal(B * hkv * S * D, 32))
+    v = bf16_round(normal(B * hkv * S * D, 33))
+    shape = fa.GroupedAttentionShape(B, hq, hkv, S, D)
+    rot = fa.RotaryEmbeddingConfig(1e4, 0)
+    o, l = _run_grouped(hip, q, k, v, shape, fa.FlatAttentionConfig(True), rot, fa.DTYPE_BF16)
+    assert np.all(np.isfinite(o)) and np.all(np.isfinite(l))
+    # LSE of causal row t lies in [max score, max score + ln(t+1)] -> at least >= -inf; check
+    # structure on the oracle units below.
+    qr = oracle.rope_rotate_rows(q, B * hq * S, 1, D, 1e4, 0, positions=np.tile(np.arange(S), B * hq))
+    kr = oracle.rope_rotate_rows(k, B * hkv * S, 1, D, 1e4, 0,
+                                 positions=np.tile(np.arange(S), B * hkv))
+    for unit in (0, B * hq - 1):
+        eo, el = oracle.forward_grouped(qr, kr, v, B, hq, hkv, S, D, True, units=(unit, unit + 1))
+        sl = slice(unit * S * D, (unit + 1) * S * D)
+        assert_close(f"O unit {unit}", o[sl], eo[sl], H16_ATOL, 0.0)
+        ls = slice(unit * S, (unit + 1) * S)
+        assert_close(f"LSE unit {unit}", l[ls], el[ls], H16_ATOL, 0.0)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_cfg2_full_size_f32_mha(hip, causal):
+    """MHA B4 H16 N2048 D128 f32; oracle on two full units."""
+    B, H, S, D = 4, 16, 2048, 128
+    q, k, v = (normal(B * H * S * D, 41 + s) for s in range(3))
+    shape = fa.GroupedAttentionShape(B, H, H, S, D)
+    o, l = _run_grouped(hip, q, k, v, shape, fa.FlatAttentionConfig(causal), None, fa.DTYPE_F32)
+    for unit in (0, B * H - 1):
+        eo, el = oracle.forward(q, k, v, B, H, S, D, causal, units=(unit, unit + 1))
+        sl = slice(unit * S * D, (unit + 1) * S * D)
+        assert_close(f"O unit {unit}", o[sl], eo[sl], F32_ATOL, F32_RTOL)
+        ls = slice(unit * S, (unit + 1) * S)
+        assert_close(f"LSE unit {unit}", l[ls], el[ls], F32_ATOL, F32_RTOL)
+    # size-independent property on every row: V = 1 gives O = 1 exactly up to rounding
+    ones = np.ones_like(v)
+    o1, _ = _run_grouped(hip, q, k, ones, shape, fa.FlatAttentionConfig(causal), None, fa.DTYPE_F32)
+    assert np.max(np.abs(o1 - 1.0)) <= 3e-5
+
+
+@pytest.mark.parametrize("dtype,rnd,atol,rtol", [(fa.DTYPE_F32, lambda x: x, F32_ATOL, F32_RTOL),
+                                                  (fa.DTYPE_BF16, bf16_round, H16_ATOL, 0.0)])
+def test_projection_asymmetric_rect_and_decode(hip, dtype, rnd, atol, rtol):
+    """Rectangular projection-layout GQA + RoPE (M11) incl. q_len = 1 decode and causal offset."""
+    B, hq, hkv, D, theta = 2, 8, 2, 64, 1e4
+    for ql, kl, off in ((1, 77, 76), (19, 90, 71), (33, 33, 0), (16, 40, 100)):
+        q = rnd(normal(B * ql * hq * D, ql))
+        k, v = rnd(normal(B * kl * hkv * D, kl)), rnd(normal(B * kl * hkv * D, kl + 1))
+        shape = fa.AsymmetricGroupedAttentionShape(B, hq, hkv, ql, kl, D, off)
+        rot = fa.AsymmetricRotaryEmbeddingConfig(theta, off + 3, 3)
+        for causal in (True, False):
+            pipe = fa.HipAsymmetricProjectionPipeline(hip, dtype)
+            lay = pipe.layout(shape)
+            out = fa.DeviceBuffer(hip, lay.combined_bytes)
+            qb, kb, vb = (fa.DeviceBuffer.from_array(hip, fa.host_storage(x, dtype)) for x in (q, k, v))
+            pipe.encode(qb, kb, vb, out, shape, fa.FlatAttentionConfig(causal), rot)
+            res = fa.download_attention(out, lay, dtype)
+            eo, el = oracle.forward_projection_asymmetric(q, k, v, B, hq, hkv, ql, kl, D, off,
+                                                          causal, theta, off + 3, 3, True)
+            assert_close("O", fa.storage_to_f32(res.output, dtype), eo, atol, rtol)
+            assert_close("LSE", res.lse, el, atol, rtol)
+
+
+def test_chunked_prefill_is_chunk_invariant_and_matches_oracle(hip):
+    B, hq, hkv, S, D, theta, off = 2, 4, 2, 70, 64, 1e4, 5
+    q = normal(B * S * hq * D, 1)
+    k, v = normal(B * S * hkv * D, 2), normal(B * S * hkv * D, 3)
+    shape = fa.GroupedAttentionShape(B, hq, hkv, S, D)
+    rot = fa.RotaryEmbeddingConfig(theta, off)
+    pipe = fa.HipChunkedProjectionPrefillPipeline(hip, fa.DTYPE_F32)
+    qb, kb, vb = (fa.DeviceBuffer.from_array(hip, x) for x in (q, k, v))
+    outs = []
+    for chunk in (1, 2, 3, 16, 70, 1000):
+        out = pipe.create_output_buffer(shape)
+        pipe.encode(qb, kb, vb, out, shape, fa.FlatAttentionConfig(True), rot, chunk)
+        outs.append(fa.download_attention(out, pipe.layout(shape), fa.DTYPE_F32))
+    for r in outs[1:]:
+        assert np.array_equal(r.output.view(np.uint32), outs[0].output.view(np.uint32))
+        assert np.array_equal(r.lse.view(np.uint32), outs[0].lse.view(np.uint32))
+    eo, el = oracle.chunked_prefill(q, k, v, B, hq, hkv, S, D, True, theta, off, 3)
+    assert_close("O", outs[0].output, eo, F32_ATOL, F32_RTOL)
+    assert_close("LSE", outs[0].lse, el, F32_ATOL, F32_RTOL)
+    with pytest.raises(fa.FlatHipError) as e:
+        pipe.encode(qb, kb, vb, out, shape, fa.FlatAttentionConfig(True), rot, 0)
+    assert e.value.variant == "ZeroQueryChunkSize"
+
+
+def test_host_forward_rejects_non_finite_and_bad_lengths(hip):
+    ex = fa.HipFlatAttention(hip, fa.DTYPE_F32)
+    shape = fa.AttentionShape(1, 1, 4, 8)
+    q = np.zeros(32, np.float32)
+    k = q.copy()
+    k[5] = np.inf
+    with pytest.raises(fa.FlatHipError) as e:
+        ex.forward(q, k, q, shape, fa.FlatAttentionConfig())
+    assert e.value.variant == "NonFiniteInput" and "index 5" in str(e.value)
+    with pytest.raises(fa.FlatHipError) as e:
+        ex.forward(q, q[:31], q, shape, fa.FlatAttentionConfig())
+    assert e.value.variant == "LengthMismatch"
+
+
+def test_adversarial_scores_stay_finite(hip):
+    """tests/numerical_policy.rs corpus: ties, near ties, +-7.75 cancellation, +-24 scores."""
+    S, D = 16, 8
+    base = np.zeros((S, D), np.float32)
+    q = base.copy()
+    q[:, 0] = 1.0
+    cases = []
+    k_tie = np.tile(np.eye(1, D, 0, np.float32), (S, 1))
+    cases.append(k_tie)
+    k_cancel = base.copy()
+    k_cancel[:, 0] = np.where(np.arange(S) % 2 == 0, 7.75, -7.75) * np.sqrt(D)
+    cases.append(k_cancel)
+    k_large = base.copy()
+    k_large[:, 0] = np.where(np.arange(S) % 3 == 0, 24.0, -24.0) * np.sqrt(D)
+    cases.append(k_large)
+    v = normal(S * D, 5)
+    for kk in cases:
+        for causal in (False, True):
+            shape = fa.GroupedAttentionShape(1, 1, 1, S, D)
+            o, l = _run_grouped(hip, q.ravel(), kk.ravel(), v, shape,
+                                fa.FlatAttentionConfig(causal), None, fa.DTYPE_F32)
+            eo, el = oracle.forward(q.ravel(), kk.ravel(), v, 1, 1, S, D, causal)
+            assert_close("O", o, eo, F32_ATOL, F32_RTOL)
+            assert_close("LSE", l, el, F32_ATOL, F32_RTOL)
