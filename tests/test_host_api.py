@@ -1,0 +1,217 @@
+"""Host-side checks of the C ABI that need no GPU: every symbol declared in include/flat_hip.h
+is exported by the built library, the PagedKvTable restatement reproduces the reference's
+known-answer tests (src/paged_kv.rs:196-271), and argument validation fails closed with the
+reference's error variants before any device work (a null context is only reported once the
+arguments are valid)."""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+import flat_attention_amd as fa
+from flat_attention_amd import _lib as L
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "flat_hip.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(fa_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = fa.lib()
+    names = declared_functions()
+    assert len(names) >= 40
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+    assert set(names) == set(L.PROTOTYPES), set(names) ^ set(L.PROTOTYPES)
+    assert lib.fa_abi_version() == 1
+
+
+def test_no_device_is_reported_as_unavailable_or_context_is_created():
+    try:
+        ctx = fa.HipContext(0)
+    except fa.FlatHipError as e:
+        assert e.variant == "Unavailable"
+    else:
+        ctx.close()
+
+
+def test_resolved_scale_default_and_errors():
+    assert fa.FlatAttentionConfig().resolved_scale(64) == 0.125  # src/lib.rs:527
+    assert fa.FlatAttentionConfig(softmax_scale=0.5).resolved_scale(64) == 0.5
+    for bad in (0.0, -1.0, float("inf"), float("nan")):
+        with pytest.raises(fa.FlatHipError) as e:
+            fa.FlatAttentionConfig(softmax_scale=bad).resolved_scale(64)
+        assert e.value.variant == "InvalidScale"
+    with pytest.raises(fa.FlatHipError) as e:
+        fa.FlatAttentionConfig().resolved_scale(0)
+    assert e.value.variant == "ZeroDimension"
+
+
+def test_packed_layout():
+    lay = fa.packed_layout(10, 3, fa.DTYPE_F32)
+    assert (lay.output_bytes, lay.lse_byte_offset, lay.combined_bytes) == (40, 40, 52)
+    lay = fa.packed_layout(5, 2, fa.DTYPE_BF16)  # odd 16-bit count: LSE aligned to 4 bytes
+    assert (lay.output_bytes, lay.lse_byte_offset, lay.combined_bytes) == (10, 12, 20)
+
+
+# --------------------------------------------------------------------------- PagedKvTable
+
+def test_mapping_is_stable_across_page_boundaries():
+    t = fa.PagedKvTable(fa.PagedKvConfig(4, 3))
+    t.append(9)
+    assert t.address(0).physical_page == 0
+    assert t.address(3).offset_in_page == 3
+    assert t.address(4).physical_page == 1
+    assert t.address(8).physical_page == 2
+    assert t.address(9) is None
+
+
+def test_telemetry_reports_exact_internal_fragmentation():
+    t = fa.PagedKvTable(fa.PagedKvConfig(8, 4))
+    t.append(9)
+    assert t.telemetry() == fa.PagedKvTelemetry(9, 32, 2, 2, 7, 0)
+
+
+def test_reset_invalidates_old_generation_before_page_reuse():
+    t = fa.PagedKvTable(fa.PagedKvConfig(2, 2))
+    t.append(1)
+    old = t.address(0)
+    t.reset()
+    assert t.address(0) is None
+    t.append(1)
+    new = t.address(0)
+    assert old.physical_page == new.physical_page and old.generation != new.generation
+
+
+def test_capacity_overflow_is_explicit_and_non_mutating():
+    t = fa.PagedKvTable(fa.PagedKvConfig(4, 2))
+    t.append(7)
+    before = (len(t), t.telemetry(), t.block_row().tolist())
+    with pytest.raises(fa.FlatHipError) as e:
+        t.append(2)
+    assert e.value.variant == "CapacityExceeded" and "requires 9 tokens, capacity is 8" in str(e.value)
+    assert (len(t), t.telemetry(), t.block_row().tolist()) == before
+
+
+def test_table_zero_dimension_and_block_row():
+    with pytest.raises(fa.FlatHipError) as e:
+        fa.PagedKvTable(fa.PagedKvConfig(0, 4))
+    assert e.value.variant == "PagedZeroDimension"
+    t = fa.PagedKvTable(fa.PagedKvConfig(3, 4))
+    with pytest.raises(fa.FlatHipError) as e:
+        t.block_row()
+    assert e.value.variant == "EmptyTable"
+    t.append(7)
+    assert t.block_row().tolist() == [0, 1, 2]
+    t.append(0)  # zero-token append is a no-op
+    assert len(t) == 7
+    c = t.clone()
+    c.append(3)
+    assert len(t) == 7 and len(c) == 10
+
+
+# --------------------------------------------------------------------------- validation
+
+FAKE = 0x1000  # non-null stand-in pointer: validation must fail before it is ever used
+
+
+def _gqa(shape, cfg=None, rot=None, dtype=fa.DTYPE_F32, q_bytes=1 << 40, kv_bytes=1 << 40,
+         out_bytes=1 << 40):
+    cfg = cfg or fa.FlatAttentionConfig()
+    r = ctypes.byref(rot.c()) if rot else None
+    return fa.lib().fa_forward_gqa_rope(None, FAKE, q_bytes, FAKE, FAKE, kv_bytes, FAKE, out_bytes,
+                                        ctypes.byref(shape.c()), ctypes.byref(cfg.c()), r, dtype)
+
+
+def _variant(rc):
+    return L.STATUS[rc]
+
+
+def test_forward_validation_variants():
+    g = fa.GroupedAttentionShape
+    assert _variant(_gqa(g(0, 4, 2, 8, 64))) == "ZeroDimension"
+    assert _variant(_gqa(g(1, 6, 4, 8, 64))) == "InvalidHeadGrouping"
+    assert _variant(_gqa(g(1, 4, 2, 8, 256))) == "UnsupportedHeadDim"
+    assert _variant(_gqa(g(1, 4, 2, 8, 60), dtype=fa.DTYPE_BF16)) == "UnsupportedHeadDim"
+    assert _variant(_gqa(g(1, 4, 2, 8, 63), rot=fa.RotaryEmbeddingConfig(1e4))) == "InvalidRotaryHeadDim"
+    assert _variant(_gqa(g(1, 4, 2, 8, 64), rot=fa.RotaryEmbeddingConfig(-1.0))) == "InvalidRotaryTheta"
+    assert _variant(_gqa(g(1, 4, 2, 8, 64), rot=fa.RotaryEmbeddingConfig(1e4, 2**64 - 2))) == "PositionOverflow"
+    assert _variant(_gqa(g(1, 4, 2, 8, 64), cfg=fa.FlatAttentionConfig(softmax_scale=0.0))) == "InvalidScale"
+    assert _variant(_gqa(g(2**40, 2**20, 2**20, 2**10, 64))) == "ShapeOverflow"
+    assert _variant(_gqa(g(1, 4, 2, 8, 64), q_bytes=100)) == "BufferTooSmall"
+    assert _variant(_gqa(g(1, 4, 2, 8, 64), kv_bytes=100)) == "BufferTooSmall"
+    assert _variant(_gqa(g(1, 4, 2, 8, 64), out_bytes=4 * 4 * 8 * 64)) == "BufferTooSmall"
+    assert _variant(_gqa(g(1, 4, 2, 8, 64), dtype=7)) == "UnsupportedDtype"
+    # valid arguments, no context: reported last
+    assert _variant(_gqa(g(1, 4, 2, 8, 64))) == "NullArgument"
+    msg = fa.lib().fa_last_error_message().decode()
+    assert "context" in msg
+
+
+def test_buffer_too_small_message_names_tensor_and_sizes():
+    rc = _gqa(fa.GroupedAttentionShape(1, 4, 2, 8, 64), q_bytes=100)
+    assert _variant(rc) == "BufferTooSmall"
+    assert fa.lib().fa_last_error_message().decode() == \
+        "buffer Q contains 100 bytes, requires at least 8192"
+
+
+def test_chunked_prefill_zero_chunk_rejected():
+    sh = fa.GroupedAttentionShape(1, 4, 2, 8, 64)
+    rc = fa.lib().fa_chunked_prefill(None, FAKE, 1 << 30, FAKE, FAKE, 1 << 30, FAKE, 1 << 30,
+                                     ctypes.byref(sh.c()),
+                                     ctypes.byref(fa.FlatAttentionConfig(True).c()),
+                                     ctypes.byref(fa.RotaryEmbeddingConfig(1e4).c()), 0,
+                                     fa.DTYPE_F32)
+    assert _variant(rc) == "ZeroQueryChunkSize"
+
+
+def _decode_prepare(bt, lens, qpos=None, ps=16, pages=8, hq=4, hkv=2, D=64, theta=1e4,
+                    causal=True, dtype=fa.DTYPE_F32):
+    bt = np.ascontiguousarray(bt, np.int32)
+    lens = np.ascontiguousarray(lens, np.int32)
+    qp = None if qpos is None else np.ascontiguousarray(qpos, np.int32)
+    h = L.VP()
+    rc = fa.lib().fa_paged_decode_prepare(None, bt.ctypes.data, bt.shape[1], lens.ctypes.data,
+                                          None if qp is None else qp.ctypes.data, lens.shape[0],
+                                          ps, pages, hq, hkv, D,
+                                          ctypes.byref(fa.FlatAttentionConfig(causal).c()), theta,
+                                          dtype, ctypes.byref(h))
+    return _variant(rc)
+
+
+def test_decode_prepare_validation_variants():
+    bt = [[0, 1, 2]]
+    assert _decode_prepare(bt, [40], qpos=[20]) == "CausalVisibilityMismatch"
+    assert _decode_prepare(bt, [40], qpos=[20], causal=False) == "NullArgument"
+    assert _decode_prepare(bt, [0]) == "EmptyTable"
+    assert _decode_prepare(bt, [49]) == "IndexSpaceExceeded"
+    assert _decode_prepare([[0, 9, 1]], [40]) == "InvalidPage"
+    assert _decode_prepare([[0, -1, 1]], [40]) == "InvalidPage"
+    assert _decode_prepare(bt, [40], hq=6, hkv=4) == "InvalidHeadGrouping"
+    assert _decode_prepare(bt, [40], D=256) == "UnsupportedHeadDim"
+    assert _decode_prepare(bt, [40], D=66) == "UnsupportedHeadDim"
+    assert _decode_prepare(bt, [40], D=63) == "InvalidRotaryHeadDim"
+    assert _decode_prepare(bt, [40], theta=0.0) == "InvalidRotaryTheta"
+    assert _decode_prepare(bt, [40], ps=0) == "PagedZeroDimension"
+    assert _decode_prepare(bt, [40]) == "NullArgument"  # all valid, no context
+
+
+def test_append_batched_validation():
+    bt = np.array([[0, 1]], np.int32)
+    st = np.array([20], np.int32)
+
+    def call(bt=bt, st=st, app=8, pages=4, ps=16, D=64):
+        return _variant(fa.lib().fa_paged_append_batched(
+            None, bt.ctypes.data, bt.shape[1], st.ctypes.data, st.shape[0], app, ps, pages, 2, D,
+            FAKE, FAKE, 1 << 30, FAKE, FAKE, 1 << 30, None, fa.DTYPE_BF16))
+    assert call(app=20) == "CapacityExceeded"
+    assert call(bt=np.array([[0, 7]], np.int32)) == "InvalidPage"
+    assert call(D=60) == "UnsupportedHeadDim"
+    assert call() == "NullArgument"
