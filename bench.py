@@ -181,6 +181,8 @@ def main():
         for i, (name, run, _, _) in enumerate(ops):
             run()
             ev.record(evs[s][i + 1], stream)
+            if s == 0:
+                tele[name] = ctx.last_telemetry()
     ctx.synchronize()
     wall = time.perf_counter() - t_wall
     per_op = {name: [ev.elapsed_ms(evs[s][i], evs[s][i + 1]) for s in range(args.steps)]

@@ -78,18 +78,16 @@ __device__ __forceinline__ void store8(void* dst, const float* x) {
     }
 }
 
+// One work item: (work index w = (sequence, split), kv head, head chunk of <= 16 heads).
 // GT: compile-time head-chunk width (>= group size of the chunk, <= 16).
 template <typename T, int DPAD, int GT>
-__global__ __launch_bounds__(64) void decode_splitk(DecodeKArgs ka) {
+__device__ __forceinline__ void decode_item(const DecodeKArgs& ka, int w, int kvh, int hc,
+                                            float* p_lds, float* misc_lds) {
     constexpr bool F32 = std::is_same<T, float>::value;
     constexpr int EB = DecodeIO<T>::kBytes;
     const DecodeArgs& a = ka.a;
-    __shared__ __attribute__((aligned(16))) float p_lds[16 * 16];
-    __shared__ __attribute__((aligned(16))) float misc_lds[3 * 16];
-
     const int lane = threadIdx.x;
     const int n = lane & 15, g4 = lane >> 4;
-    const int w = blockIdx.x, kvh = blockIdx.y, hc = blockIdx.z;
     const int s = a.work_seq[w], split = a.work_split[w];
     const int ctx = a.ctx_lens[s];
     const int k0 = split * a.split_tokens;
@@ -169,31 +167,26 @@ __global__ __launch_bounds__(64) void decode_splitk(DecodeKArgs ka) {
 
     u32x4_t kop[NQ];
     u32x4_t vreg[4][VCH];
+    // Loads never branch: keys past the split end are clamped to its last live key (finite
+    // data whose scores are masked to -inf and whose V rows get probability exactly 0).
     auto load_step = [&](int key0) {
-        const int kk = key0 + n;  // K row for the A operand
-        const bool kvalid = kk < k1;
-        const int64_t krow = kvalid ? row_of(kk) : 0;
+        const int64_t krow = row_of(min(key0 + n, k1 - 1));
 #pragma unroll
         for (int c = 0; c < NQ; ++c) {
             int d0;
             if constexpr (F32) d0 = 16 * c + 4 * g4;
             else d0 = 32 * c + 8 * g4;
-            u32x4_t z = {0u, 0u, 0u, 0u};
-            kop[c] = (kvalid && d0 < D)
-                         ? *(const u32x4_t*)(kpool + (krow * width + d0) * EB)
-                         : z;
+            const int dl = d0 < D ? d0 : 0;
+            kop[c] = *(const u32x4_t*)(kpool + (krow * width + dl) * EB);
+            if (d0 >= D) kop[c] = u32x4_t{0u, 0u, 0u, 0u};
         }
-        const int dv = 8 * n;
+        const int dv = 8 * n < D ? 8 * n : 0;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int key = key0 + 4 * g4 + i;
-            const bool ok = key < k1 && dv < D;
-            const int64_t vr = ok ? row_of(key) : 0;
+            const int64_t vr = row_of(min(key0 + 4 * g4 + i, k1 - 1));
 #pragma unroll
-            for (int c = 0; c < VCH; ++c) {
-                u32x4_t z = {0u, 0u, 0u, 0u};
-                vreg[i][c] = ok ? *(const u32x4_t*)(vpool + (vr * width + dv + 4 * c) * EB) : z;
-            }
+            for (int c = 0; c < VCH; ++c)
+                vreg[i][c] = *(const u32x4_t*)(vpool + (vr * width + dv + 4 * c) * EB);
         }
     };
 
@@ -330,61 +323,105 @@ __global__ __launch_bounds__(64) void decode_splitk(DecodeKArgs ka) {
     }
 }
 
+// Persistent split kernel: each one-wave workgroup walks work items with a static stride so
+// the grid is sized to what is resident at once (no partially filled last round). Every wave
+// exits once its stride passes n_items.
+template <typename T, int DPAD, int GT>
+__global__ __launch_bounds__(64) void decode_splitk(DecodeKArgs ka, int n_items, int chunks) {
+    __shared__ __attribute__((aligned(16))) float p_lds[16 * 16];
+    __shared__ __attribute__((aligned(16))) float misc_lds[3 * 16];
+    const int per_w = ka.a.kv_heads * chunks;
+    for (int it = blockIdx.x; it < n_items; it += gridDim.x) {
+        const int w = it / per_w, r = it % per_w;
+        decode_item<T, DPAD, GT>(ka, w, r / chunks, r % chunks, p_lds, misc_lds);
+        __syncthreads();
+    }
+}
+
 // One workgroup per (query head, sequence); lanes stride over head_dim.
 template <typename T>
-__global__ __launch_bounds__(128) void decode_combine(DecodeArgs a) {
+__global__ __launch_bounds__(64) void decode_combine(DecodeArgs a) {
     constexpr int EB = DecodeIO<T>::kBytes;
-    const int hq = blockIdx.x, s = blockIdx.y;
+    const int hq = blockIdx.x, s = blockIdx.y, lane = threadIdx.x;
     const int w0 = a.seq_work_off[s], w1 = a.seq_work_off[s + 1];
-    if (w1 - w0 <= 1) return;
+    const int ns = w1 - w0;
+    if (ns <= 1) return;  // finalised by the split kernel
     const float c2 = a.scale * kLog2e;
+    // split statistics, 64 splits per pass held across the lanes
     float M = -INFINITY;
-    for (int w = w0; w < w1; ++w) M = fmaxf(M, a.part_ml[((int64_t)w * a.q_heads + hq) * 2]);
+    for (int j = lane; j < ns; j += 64)
+        M = fmaxf(M, a.part_ml[((int64_t)(w0 + j) * a.q_heads + hq) * 2]);
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) M = fmaxf(M, shfl_xor(M, o));
     float L = 0.0f;
-    for (int w = w0; w < w1; ++w) {
-        const float* ml = a.part_ml + ((int64_t)w * a.q_heads + hq) * 2;
+    for (int j = lane; j < ns; j += 64) {
+        const float* ml = a.part_ml + ((int64_t)(w0 + j) * a.q_heads + hq) * 2;
         L += ml[1] * fast_exp2((ml[0] - M) * c2);
     }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) L += shfl_xor(L, o);
     const float inv = 1.0f / L;
-    for (int d = threadIdx.x; d < a.head_dim; d += blockDim.x) {
-        float acc = 0.0f;
-        for (int w = w0; w < w1; ++w) {
-            const float* ml = a.part_ml + ((int64_t)w * a.q_heads + hq) * 2;
-            acc += a.part_o[((int64_t)w * a.q_heads + hq) * a.head_dim + d] *
-                   fast_exp2((ml[0] - M) * c2);
+    const int d = 2 * lane;
+    if (d < a.head_dim) {
+        float acc0 = 0.0f, acc1 = 0.0f;
+        for (int j = 0; j < ns; ++j) {
+            const int64_t base = (int64_t)(w0 + j) * a.q_heads + hq;
+            const float wgt = fast_exp2((a.part_ml[base * 2] - M) * c2);
+            const float2 v = *(const float2*)(a.part_o + base * a.head_dim + d);
+            acc0 = fmaf(v.x, wgt, acc0);
+            acc1 = fmaf(v.y, wgt, acc1);
         }
-        const float val = acc * inv;
         uint8_t* dst = (uint8_t*)a.o + (((int64_t)s * a.q_heads + hq) * a.head_dim + d) * EB;
         if constexpr (std::is_same<T, float>::value) {
-            *(float*)dst = val;
+            *(float2*)dst = make_float2(acc0 * inv, acc1 * inv);
         } else {
-            const uint32_t pk = Half<T>::pack(val, 0.0f);
-            *(uint16_t*)dst = (uint16_t)(pk & 0xffffu);
+            *(uint32_t*)dst = Half<T>::pack(acc0 * inv, acc1 * inv);
         }
     }
-    if (threadIdx.x == 0) a.lse[(int64_t)s * a.q_heads + hq] = M * a.scale + logf(L);
+    if (lane == 0) a.lse[(int64_t)s * a.q_heads + hq] = M * a.scale + logf(L);
+}
+
+template <typename T, int DPAD, int GT>
+static void launch_one(const DecodeKArgs& ka, int n_items, int chunks, hipStream_t s,
+                       unsigned* grid_x) {
+    static int resident = 0;  // resident one-wave workgroups per CU for this instantiation
+    if (!resident) {
+        int per_cu = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_splitk<T, DPAD, GT>, 64,
+                                                         0) != hipSuccess || per_cu <= 0)
+            per_cu = 8;
+        resident = per_cu;
+    }
+    int dev = 0, cus = 256;
+    if (hipGetDevice(&dev) == hipSuccess)
+        (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    const int cap = resident * cus;
+    const int g = n_items < cap ? n_items : cap;
+    *grid_x = (unsigned)g;
+    decode_splitk<T, DPAD, GT><<<g, 64, 0, s>>>(ka, n_items, chunks);
 }
 
 template <typename T, int DPAD>
-static void launch_gt(const DecodeKArgs& ka, int gt, dim3 grid, hipStream_t s) {
+static void launch_gt(const DecodeKArgs& ka, int gt, int n_items, int chunks, hipStream_t s,
+                      unsigned* gx) {
     switch (gt) {
-        case 1: decode_splitk<T, DPAD, 1><<<grid, 64, 0, s>>>(ka); break;
-        case 2: decode_splitk<T, DPAD, 2><<<grid, 64, 0, s>>>(ka); break;
-        case 4: decode_splitk<T, DPAD, 4><<<grid, 64, 0, s>>>(ka); break;
-        case 8: decode_splitk<T, DPAD, 8><<<grid, 64, 0, s>>>(ka); break;
-        default: decode_splitk<T, DPAD, 16><<<grid, 64, 0, s>>>(ka); break;
+        case 1: launch_one<T, DPAD, 1>(ka, n_items, chunks, s, gx); break;
+        case 2: launch_one<T, DPAD, 2>(ka, n_items, chunks, s, gx); break;
+        case 4: launch_one<T, DPAD, 4>(ka, n_items, chunks, s, gx); break;
+        case 8: launch_one<T, DPAD, 8>(ka, n_items, chunks, s, gx); break;
+        default: launch_one<T, DPAD, 16>(ka, n_items, chunks, s, gx); break;
     }
 }
 
 template <typename T>
-static void launch_t(const DecodeKArgs& ka, int dpad, int gt, dim3 grid, dim3 cgrid,
-                     hipStream_t s) {
+static void launch_t(const DecodeKArgs& ka, int dpad, int gt, int n_items, int chunks,
+                     dim3 cgrid, hipStream_t s, unsigned* gx) {
     switch (dpad) {
-        case 32: launch_gt<T, 32>(ka, gt, grid, s); break;
-        case 64: launch_gt<T, 64>(ka, gt, grid, s); break;
-        default: launch_gt<T, 128>(ka, gt, grid, s); break;
+        case 32: launch_gt<T, 32>(ka, gt, n_items, chunks, s, gx); break;
+        case 64: launch_gt<T, 64>(ka, gt, n_items, chunks, s, gx); break;
+        default: launch_gt<T, 128>(ka, gt, n_items, chunks, s, gx); break;
     }
-    decode_combine<T><<<cgrid, 128, 0, s>>>(ka.a);
+    decode_combine<T><<<cgrid, 64, 0, s>>>(ka.a);
 }
 
 void launch_decode(Dtype dt, const DecodeArgs& a, hipStream_t s, unsigned grid[3],
@@ -401,18 +438,19 @@ void launch_decode(Dtype dt, const DecodeArgs& a, hipStream_t s, unsigned grid[3
     const int chunks = (a.group + 15) / 16;
     const int gmax = a.group >= 16 ? 16 : a.group;
     const int gt = gmax <= 1 ? 1 : gmax <= 2 ? 2 : gmax <= 4 ? 4 : gmax <= 8 ? 8 : 16;
-    dim3 g((unsigned)a.n_work, (unsigned)a.kv_heads, (unsigned)chunks);
+    const int n_items = a.n_work * a.kv_heads * chunks;
     dim3 cg((unsigned)a.q_heads, (unsigned)a.n_seqs);
-    grid[0] = g.x;
-    grid[1] = g.y;
-    grid[2] = g.z;
+    unsigned gx = 0;
+    switch (dt) {
+        case Dtype::BF16: launch_t<bf16_t>(ka, dpad, gt, n_items, chunks, cg, s, &gx); break;
+        case Dtype::F16: launch_t<f16_t>(ka, dpad, gt, n_items, chunks, cg, s, &gx); break;
+        default: launch_t<float>(ka, dpad, gt, n_items, chunks, cg, s, &gx); break;
+    }
+    grid[0] = gx;
+    grid[1] = 1;
+    grid[2] = 1;
     *block = 64;
     *dispatches = 2;
-    switch (dt) {
-        case Dtype::BF16: launch_t<bf16_t>(ka, dpad, gt, g, cg, s); break;
-        case Dtype::F16: launch_t<f16_t>(ka, dpad, gt, g, cg, s); break;
-        default: launch_t<float>(ka, dpad, gt, g, cg, s); break;
-    }
 }
 
 }  // namespace fa

@@ -472,6 +472,13 @@ struct PrefillJob {
 };
 
 int run_prefill(fa_ctx* ctx, PrefillJob& j) {
+    // 16-bit contiguous K/V are read through 32-bit buffer offsets within one (batch, kv-head)
+    // slice: kv_len rows of k_ss elements must stay below 2 GiB.
+    if (!j.paged && j.dtype != FA_DTYPE_F32 &&
+        (uint64_t)j.a.kv_len * (uint64_t)j.a.k_ss * 2u > (uint64_t)INT32_MAX)
+        return fail(FA_ERR_INDEX_SPACE_EXCEEDED,
+                    "one K/V slice spans %llu bytes; the 16-bit kernels address at most 2 GiB",
+                    (unsigned long long)((uint64_t)j.a.kv_len * (uint64_t)j.a.k_ss * 2u));
     const float2* table = nullptr;
     bool prerot = false;
     if (j.rope) {

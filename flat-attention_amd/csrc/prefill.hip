@@ -54,24 +54,50 @@ __device__ __forceinline__ int64_t kv_row_offset(const PrefillKArgs& ka, int b, 
     }
 }
 
-__device__ __forceinline__ int k_swizzle(int row) { return (row & 3) | ((row >> 1) & 4); }
+// Running-max slack (log2 units) tolerated before O is rescaled: probabilities stay <= 2^8.
+constexpr float kRescaleLog2 = 8.0f;
 
 // ------------------------------------------------------------------ 16-bit MFMA kernel
-template <typename T, int DPAD, bool PAGED, bool ROPEK>
+// K/V source addressing modes.
+enum : int { kContig = 0, kPaged16 = 1, kPagedAny = 2 };
+
+// Physical row of `key` for batch b. kPaged16 requires page_size % 16 == 0 and a key group of
+// 16 consecutive keys per wave, so the block-table entry is wave-uniform (one scalar load).
+template <int PMODE>
+__device__ __forceinline__ int64_t paged_row(const PrefillKArgs& ka, int b, int key) {
+    const PrefillArgs& a = ka.a;
+    if constexpr (PMODE == kPaged16) {
+        const int g16 = __builtin_amdgcn_readfirstlane(key & ~15);
+        const uint32_t lp = ka.ps.div((uint32_t)g16);
+        const int page = a.block_tables[(int64_t)b * a.bt_stride + lp];
+        return (int64_t)page * a.page_size + (key - (int)lp * a.page_size);
+    } else {
+        const uint32_t lp = ka.ps.div((uint32_t)key);
+        const int page = a.block_tables[(int64_t)b * a.bt_stride + lp];
+        return (int64_t)page * a.page_size + (key - (int)lp * a.page_size);
+    }
+}
+
+// LDS tiles, both row-major [64 keys][DPAD] 16-bit:
+//   K rows padded to 2*DPAD + 16 bytes: the one-lane-per-row ds_read_b128 of the S^T A operand
+//     is bank-conflict free;
+//   V rows padded to 2*DPAD + 64 bytes: the V^T A operand of O^T is read with
+//     ds_read_b64_tr_b16, which hands each lane 4 keys of one dim (the 16-lane group transposes
+//     the 4x4 blocks it addresses), so V needs no transposition when it is staged.
+// Every per-step LDS address is a per-lane base plus a compile-time immediate.
+template <typename T, int DPAD, int PMODE, bool ROPEK, bool FULLD>
 __global__ __launch_bounds__(256, 2) void prefill_mfma16(PrefillKArgs ka) {
     using H = Half<T>;
     const PrefillArgs& a = ka.a;
     constexpr int BM = 128, BN = 64;
     constexpr int KS = DPAD / 16;           // QK^T k-steps (16 dims each)
     constexpr int MB = DPAD / 32;           // 32-dim blocks of O^T
-    constexpr int CPR = DPAD / 8;           // 16-byte chunks per K row
-    constexpr int KRPP = 256 / CPR;         // K rows staged per pass
+    constexpr int CPR = DPAD / 8;           // 16-byte chunks per row
+    constexpr int KRPP = 256 / CPR;         // rows staged per pass
     constexpr int KPASS = BN / KRPP;
-    constexpr int KROWB = DPAD * 2;         // bytes per K row in LDS
-    constexpr int VPAIRS = DPAD / 2;
-    constexpr int VKPT = DPAD / 8;          // keys per thread in V staging
-    constexpr int VROWB = BN * 2;           // bytes per V^T row in LDS
-    __shared__ __attribute__((aligned(16))) uint8_t smem[BN * KROWB + DPAD * VROWB];
+    constexpr int KROWB = DPAD * 2 + 16;    // padded K row (bytes)
+    constexpr int VROWB = DPAD * 2 + 64;    // padded V row (bytes)
+    __shared__ __attribute__((aligned(16))) uint8_t smem[BN * KROWB + BN * VROWB];
     uint8_t* const k_lds = smem;
     uint8_t* const v_lds = smem + BN * KROWB;
 
@@ -110,9 +136,9 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma16(PrefillKArgs ka) {
         for (int ks = 0; ks < KS; ++ks) {
             const int d0 = 16 * ks + 8 * g;
             u32x4_t raw = {0u, 0u, 0u, 0u};
-            if (d0 < D) raw = *(const u32x4_t*)(qrow + d0);
-            if (a.rope_q && d0 < D) {
-                float x[8], cs[8];
+            if (FULLD || d0 < D) raw = *(const u32x4_t*)(qrow + d0);
+            if (a.rope_q && (FULLD || d0 < D)) {
+                float x[8];
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     x[2 * j] = H::lo(raw[j]);
@@ -120,8 +146,7 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma16(PrefillKArgs ka) {
                 }
                 const f32x4_t c0 = *(const f32x4_t*)(cs_row + d0 / 2);
                 const f32x4_t c1 = *(const f32x4_t*)(cs_row + d0 / 2 + 2);
-                cs[0] = c0[0]; cs[1] = c0[1]; cs[2] = c0[2]; cs[3] = c0[3];
-                cs[4] = c1[0]; cs[5] = c1[1]; cs[6] = c1[2]; cs[7] = c1[3];
+                float cs[8] = {c0[0], c0[1], c0[2], c0[3], c1[0], c1[1], c1[2], c1[3]};
                 rope4(x, cs);
 #pragma unroll
                 for (int j = 0; j < 4; ++j) raw[j] = H::pack(x[2 * j], x[2 * j + 1]);
@@ -130,58 +155,72 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma16(PrefillKArgs ka) {
         }
     }
 
-    const uint16_t* kbase = (const uint16_t*)a.k + (int64_t)kvh * a.k_sh;
-    const uint16_t* vbase = (const uint16_t*)a.v + (int64_t)kvh * a.k_sh;
-
-    // ---- register prefetch of one K/V tile
-    u32x4_t kreg[KPASS];
-    uint32_t vreg[VKPT];
+    // ---- global -> register staging of one K/V tile.
+    // Buffer loads: a scalar resource (base + byte range) plus a 32-bit per-lane offset. Reads
+    // past the resource range return 0, so rows past kv_len (and never-written pool rows) read
+    // as zeros: their scores are masked and their V rows weigh 0. Dims past head_dim (only when
+    // head_dim < DPAD) are zeroed explicitly.
+    const uint32_t row_bytes = (uint32_t)a.k_ss * 2u;
+    const int64_t head_off =
+        (int64_t)kvh * a.k_sh * 2 + (PMODE == kContig ? (int64_t)b * a.k_sb * 2 : 0);
+    const uint8_t* const kb8 = (const uint8_t*)a.k + head_off;
+    const uint8_t* const vb8 = (const uint8_t*)a.v + head_off;
     const int k_dc = tid % CPR, k_r = tid / CPR;
-    const int v_dp = tid % VPAIRS, v_kb = tid / VPAIRS;
+    const uint32_t kd2 = (uint32_t)(FULLD ? k_dc * 8 : min(k_dc * 8, D - 8)) * 2u;
+    const uint32_t lane_off = (uint32_t)k_r * row_bytes + kd2;  // this thread's row/chunk
+    constexpr int kRsrcFlags = 0x00020000;
+    u32x4_t kreg[KPASS], vreg[KPASS];
 
     auto load_tile = [&](int tile) {
+        const int key_base = tile * BN;
+        if constexpr (PMODE == kContig) {
+            const int nrec = (a.kv_len - 1) * (int)row_bytes + D * 2;
+            const __amdgpu_buffer_rsrc_t rk =
+                __builtin_amdgcn_make_buffer_rsrc((void*)kb8, (short)0, nrec, kRsrcFlags);
+            const __amdgpu_buffer_rsrc_t rv =
+                __builtin_amdgcn_make_buffer_rsrc((void*)vb8, (short)0, nrec, kRsrcFlags);
 #pragma unroll
-        for (int p = 0; p < KPASS; ++p) {
-            const int key = tile * BN + p * KRPP + k_r;
-            const int d0 = k_dc * 8;
-            u32x4_t z = {0u, 0u, 0u, 0u};
-            kreg[p] = z;
-            if (key < a.kv_len && d0 < D)
-                kreg[p] = *(const u32x4_t*)(kbase + kv_row_offset<PAGED>(ka, b, key) + d0);
-        }
-        {
-            const int key0 = tile * BN + v_kb * VKPT;
-            const int d = 2 * v_dp;
-            if constexpr (PAGED) {
-                // consecutive keys: walk pages incrementally; block-table entries are read only
-                // for live keys (key < kv_len), which the host validated.
-                const int key_first = min(key0, a.kv_len - 1);
-                uint32_t lp = ka.ps.div((uint32_t)key_first);
-                int off = key0 - (int)lp * a.page_size;
-                int page = a.block_tables[(int64_t)b * a.bt_stride + lp];
-#pragma unroll
-                for (int j = 0; j < VKPT; ++j) {
-                    const int key = key0 + j;
-                    vreg[j] = 0u;
-                    if (key < a.kv_len && d < D)
-                        vreg[j] = *(const uint32_t*)(vbase +
-                                                     ((int64_t)page * a.page_size + off) * a.k_ss +
-                                                     d);
-                    if (++off == a.page_size && key + 1 < a.kv_len) {
-                        off = 0;
-                        ++lp;
-                        page = a.block_tables[(int64_t)b * a.bt_stride + lp];
-                    }
-                }
-            } else {
-                const uint16_t* vrow = vbase + (int64_t)b * a.k_sb + (int64_t)key0 * a.k_ss + d;
-#pragma unroll
-                for (int j = 0; j < VKPT; ++j) {
-                    vreg[j] = 0u;
-                    if (key0 + j < a.kv_len && d < D)
-                        vreg[j] = *(const uint32_t*)(vrow + (int64_t)j * a.k_ss);
-                }
+            for (int p = 0; p < KPASS; ++p) {
+                const uint32_t off = lane_off + (uint32_t)(key_base + p * KRPP) * row_bytes;
+                kreg[p] = __builtin_amdgcn_raw_buffer_load_b128(rk, (int)off, 0, 0);
+                vreg[p] = __builtin_amdgcn_raw_buffer_load_b128(rv, (int)off, 0, 0);
             }
+        } else if constexpr (PMODE == kPaged16) {
+            // One 16-key group (one page, since page_size % 16 == 0) per wave and pass; the
+            // resources span the group's live rows only.
+#pragma unroll
+            for (int p = 0; p < KPASS; ++p) {
+                const int key = key_base + p * KRPP + k_r;
+                const int g16 = __builtin_amdgcn_readfirstlane(key & ~15);
+                const int live = min(16, a.kv_len - g16);
+                const int gq = live > 0 ? g16 : 0;
+                const uint32_t lp = ka.ps.div((uint32_t)gq);
+                const int page = a.block_tables[(int64_t)b * a.bt_stride + lp];
+                const int64_t gofs = ((int64_t)page * a.page_size + (gq - (int)lp * a.page_size)) *
+                                     (int64_t)row_bytes;
+                const int nrec = live > 0 ? (live - 1) * (int)row_bytes + D * 2 : 0;
+                const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+                    (void*)(kb8 + gofs), (short)0, nrec, kRsrcFlags);
+                const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+                    (void*)(vb8 + gofs), (short)0, nrec, kRsrcFlags);
+                const int off = (int)((uint32_t)(key & 15) * row_bytes + kd2);
+                kreg[p] = __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 0);
+                vreg[p] = __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, 0);
+            }
+        } else {
+#pragma unroll
+            for (int p = 0; p < KPASS; ++p) {
+                const int key_raw = key_base + p * KRPP + k_r;
+                const int key = min(key_raw, a.kv_len - 1);
+                const int64_t r = paged_row<PMODE>(ka, b, key);
+                kreg[p] = *(const u32x4_t*)(kb8 + r * row_bytes + kd2);
+                vreg[p] = *(const u32x4_t*)(vb8 + r * row_bytes + kd2);
+                if (key_raw >= a.kv_len) kreg[p] = vreg[p] = u32x4_t{0u, 0u, 0u, 0u};
+            }
+        }
+        if (!FULLD && k_dc * 8 >= D) {
+#pragma unroll
+            for (int p = 0; p < KPASS; ++p) kreg[p] = vreg[p] = u32x4_t{0u, 0u, 0u, 0u};
         }
     };
 
@@ -190,8 +229,8 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma16(PrefillKArgs ka) {
         for (int p = 0; p < KPASS; ++p) {
             const int kl = p * KRPP + k_r;
             u32x4_t val = kreg[p];
-            if (ROPEK && tile * BN + kl < a.kv_len && k_dc * 8 < D) {
-                // K is rotated between the HBM load and the LDS store (cos/sin from the table)
+            if (ROPEK && tile * BN + kl < a.kv_len && (FULLD || k_dc * 8 < D)) {
+                // K rotated between the HBM load and the LDS store (cos/sin from the table)
                 const float2* csp = a.rope_table +
                                     (int64_t)(a.kv_rope_offset + tile * BN + kl) * half + k_dc * 4;
                 const f32x4_t c0 = *(const f32x4_t*)csp;
@@ -206,39 +245,11 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma16(PrefillKArgs ka) {
 #pragma unroll
                 for (int j = 0; j < 4; ++j) val[j] = H::pack(x[2 * j], x[2 * j + 1]);
             }
-            const int unit = k_dc ^ (k_swizzle(kl) & (CPR - 1));
-            *(u32x4_t*)(k_lds + kl * KROWB + unit * 16) = val;
+            *(u32x4_t*)(k_lds + kl * KROWB + k_dc * 16) = val;
         }
-        {
-            const int d = 2 * v_dp;
-            const int kb0 = v_kb * VKPT;  // first key of this thread
-            if constexpr (VKPT >= 8) {
 #pragma unroll
-                for (int u = 0; u < VKPT / 8; ++u) {
-                    u32x4_t lo, hi;
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const uint32_t x = vreg[8 * u + 2 * i], y = vreg[8 * u + 2 * i + 1];
-                        lo[i] = (x & 0xffffu) | (y << 16);
-                        hi[i] = (x >> 16) | (y & 0xffff0000u);
-                    }
-                    const int ku = kb0 / 8 + u;
-                    *(u32x4_t*)(v_lds + d * VROWB + ((ku ^ (d & 7)) * 16)) = lo;
-                    *(u32x4_t*)(v_lds + (d + 1) * VROWB + ((ku ^ ((d + 1) & 7)) * 16)) = hi;
-                }
-            } else {
-                u32x2_t lo, hi;
-#pragma unroll
-                for (int i = 0; i < 2; ++i) {
-                    const uint32_t x = vreg[2 * i], y = vreg[2 * i + 1];
-                    lo[i] = (x & 0xffffu) | (y << 16);
-                    hi[i] = (x >> 16) | (y & 0xffff0000u);
-                }
-                const int ku = kb0 / 8, sub = (kb0 % 8) * 2;
-                *(u32x2_t*)(v_lds + d * VROWB + ((ku ^ (d & 7)) * 16) + sub) = lo;
-                *(u32x2_t*)(v_lds + (d + 1) * VROWB + ((ku ^ ((d + 1) & 7)) * 16) + sub) = hi;
-            }
-        }
+        for (int p = 0; p < KPASS; ++p)
+            *(u32x4_t*)(v_lds + (p * KRPP + k_r) * VROWB + k_dc * 16) = vreg[p];
     };
 
     f32x16_t oacc[MB];
@@ -249,6 +260,27 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma16(PrefillKArgs ka) {
 
     // K row fed to MFMA row m of a 32-key block: bits 2 and 3 swapped.
     const int pm = ((lane & 31) & ~12) | (((lane & 31) & 4) << 1) | (((lane & 31) & 8) >> 1);
+    const uint8_t* const k_rd0 = k_lds + pm * KROWB + g * 16;
+    // ds_read_b64_tr_b16 source: lane (16-group G, index s) addresses key 8g + s/4 and dims
+    // 16*(G&1) + 4*(s&3) .. +3; it receives dim (lane & 31) of keys 8g + 0..3.
+    const uint8_t* const v_rd = v_lds + (8 * g + ((lane & 15) >> 2)) * VROWB +
+                                (16 * ((lane >> 4) & 1) + 4 * (lane & 3)) * 2;
+
+    // Threshold rescale: the running max m_run only moves when a tile max exceeds it by more
+    // than kRescaleLog2 (in log2 units). Until then probabilities are taken against the stale
+    // max, so p <= 2^kRescaleLog2 and O, l stay consistent; the final O / l and
+    // LSE = m_run*scale + ln l are exact either way. This skips the O^T rescale on most tiles.
+    auto rescale = [&](float mt) {
+        const bool need = mt * c2 > m_run * c2 + kRescaleLog2;
+        if (__any(need)) {
+            const float m_use = need ? mt : m_run;
+            const float alpha = fast_exp2((m_run - m_use) * c2);  // m_run = -inf -> 0
+            l_run *= alpha;
+#pragma unroll
+            for (int mb = 0; mb < MB; ++mb) oacc[mb] *= alpha;
+            m_run = m_use;
+        }
+    };
 
     if (n_tiles > 0) load_tile(0);
     for (int tile = 0; tile < n_tiles; ++tile) {
@@ -261,12 +293,9 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma16(PrefillKArgs ka) {
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) {
             sacc[kb] = (f32x16_t)0.0f;
-            const int krow = kb * 32 + pm;
-            const int sw = k_swizzle(krow) & (CPR - 1);
-            const uint8_t* kr = k_lds + krow * KROWB;
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) {
-                const u32x4_t av = *(const u32x4_t*)(kr + (((2 * ks + g) ^ sw) * 16));
+                const u32x4_t av = *(const u32x4_t*)(k_rd0 + kb * 32 * KROWB + ks * 32);
                 sacc[kb] = H::mfma32(av, qop[ks], sacc[kb]);
             }
         }
@@ -274,14 +303,12 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma16(PrefillKArgs ka) {
         // ---- mask (tail keys, causal diagonal)
         const int tile_end = (tile + 1) * BN;
         if (tile_end > a.kv_len || (a.causal && tile_end - 1 > cpos_min)) {
-            const int lim = a.causal ? min(a.kv_len - 1, cpos) : a.kv_len - 1;
+            const int lim = (a.causal ? min(a.kv_len - 1, cpos) : a.kv_len - 1) - tile * BN - 8 * g;
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    const int key = tile * BN + 32 * kb + 16 * (i >> 3) + 8 * g + (i & 7);
-                    if (key > lim) sacc[kb][i] = -INFINITY;
-                }
+                for (int i = 0; i < 16; ++i)
+                    if (32 * kb + 16 * (i >> 3) + (i & 7) > lim) sacc[kb][i] = -INFINITY;
         }
 
         // ---- online softmax (row = this lane's query; partner lane ^ 32 holds the other keys)
@@ -291,10 +318,8 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma16(PrefillKArgs ka) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) mt = fmaxf(mt, sacc[1][i]);
         mt = fmaxf(mt, shfl_xor(mt, 32));
-        const float m_new = fmaxf(m_run, mt);
-        const float m_base = (m_new == -INFINITY) ? 0.0f : m_new;
-        const float alpha = fast_exp2((m_run - m_base) * c2);
-        const float neg = -m_base * c2;
+        rescale(mt);
+        const float neg = -m_run * c2;
         float lsum = 0.0f;
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
@@ -304,10 +329,7 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma16(PrefillKArgs ka) {
                 sacc[kb][i] = p;
                 lsum += p;
             }
-        l_run = l_run * alpha + lsum;
-        m_run = m_new;
-#pragma unroll
-        for (int mb = 0; mb < MB; ++mb) oacc[mb] *= alpha;
+        l_run += lsum;
 
         // ---- P^T operands (16 keys each)
         u32x4_t pop[4];
@@ -321,15 +343,20 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma16(PrefillKArgs ka) {
 
         // ---- O^T += V^T . P^T
 #pragma unroll
-        for (int mb = 0; mb < MB; ++mb) {
-            const int drow = mb * 32 + (lane & 31);
-            const uint8_t* vr = v_lds + drow * VROWB;
+        for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
             for (int s2 = 0; s2 < 4; ++s2) {
-                const u32x4_t av = *(const u32x4_t*)(vr + (((2 * s2 + g) ^ (drow & 7)) * 16));
+                typedef short v4i16_t __attribute__((ext_vector_type(4)));
+                typedef __attribute__((address_space(3))) v4i16_t lds_v4i16_t;
+                const uint8_t* src = v_rd + s2 * 16 * VROWB + mb * 64;
+                const v4i16_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)src);
+                const v4i16_t hi =
+                    __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)(src + 4 * VROWB));
+                const u32x2_t l2 = __builtin_bit_cast(u32x2_t, lo);
+                const u32x2_t h2 = __builtin_bit_cast(u32x2_t, hi);
+                const u32x4_t av = {l2[0], l2[1], h2[0], h2[1]};
                 oacc[mb] = H::mfma32(av, pop[s2], oacc[mb]);
             }
-        }
         __syncthreads();
     }
 
@@ -344,7 +371,7 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma16(PrefillKArgs ka) {
 #pragma unroll
             for (int q4 = 0; q4 < 4; ++q4) {
                 const int d0 = mb * 32 + 8 * q4 + 4 * g;
-                if (d0 < D) {
+                if (FULLD || d0 < D) {
                     u32x2_t w;
                     w[0] = H::pack(oacc[mb][4 * q4] * inv, oacc[mb][4 * q4 + 1] * inv);
                     w[1] = H::pack(oacc[mb][4 * q4 + 2] * inv, oacc[mb][4 * q4 + 3] * inv);
@@ -499,10 +526,18 @@ __global__ __launch_bounds__(256, 1) void prefill_mfma_f32(PrefillKArgs ka) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) mt = fmaxf(mt, sacc[1][i]);
         mt = fmaxf(mt, shfl_xor(mt, 32));
-        const float m_new = fmaxf(m_run, mt);
-        const float m_base = (m_new == -INFINITY) ? 0.0f : m_new;
-        const float alpha = fast_exp2((m_run - m_base) * c2);
-        const float neg = -m_base * c2;
+        {
+            const bool need = mt * c2 > m_run * c2 + kRescaleLog2;
+            if (__any(need)) {
+                const float m_use = need ? mt : m_run;
+                const float alpha = fast_exp2((m_run - m_use) * c2);
+                l_run *= alpha;
+#pragma unroll
+                for (int mb = 0; mb < MB; ++mb) oacc[mb] *= alpha;
+                m_run = m_use;
+            }
+        }
+        const float neg = -m_run * c2;
         float lsum = 0.0f;
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
@@ -512,10 +547,7 @@ __global__ __launch_bounds__(256, 1) void prefill_mfma_f32(PrefillKArgs ka) {
                 sacc[kb][i] = p;
                 lsum += p;
             }
-        l_run = l_run * alpha + lsum;
-        m_run = m_new;
-#pragma unroll
-        for (int mb = 0; mb < MB; ++mb) oacc[mb] *= alpha;
+        l_run += lsum;
 
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb) {
@@ -552,19 +584,36 @@ __global__ __launch_bounds__(256, 1) void prefill_mfma_f32(PrefillKArgs ka) {
 }
 
 // ------------------------------------------------------------------ launcher
-template <typename T, bool PAGED, bool ROPEK>
+template <typename T, int PMODE, bool ROPEK>
 static void launch16r(const PrefillKArgs& ka, int dpad, dim3 grid, hipStream_t s) {
+    const bool full = ka.a.head_dim == dpad;
     switch (dpad) {
-        case 32: prefill_mfma16<T, 32, PAGED, ROPEK><<<grid, 256, 0, s>>>(ka); break;
-        case 64: prefill_mfma16<T, 64, PAGED, ROPEK><<<grid, 256, 0, s>>>(ka); break;
-        default: prefill_mfma16<T, 128, PAGED, ROPEK><<<grid, 256, 0, s>>>(ka); break;
+        case 32:
+            full ? prefill_mfma16<T, 32, PMODE, ROPEK, true><<<grid, 256, 0, s>>>(ka)
+                 : prefill_mfma16<T, 32, PMODE, ROPEK, false><<<grid, 256, 0, s>>>(ka);
+            break;
+        case 64:
+            full ? prefill_mfma16<T, 64, PMODE, ROPEK, true><<<grid, 256, 0, s>>>(ka)
+                 : prefill_mfma16<T, 64, PMODE, ROPEK, false><<<grid, 256, 0, s>>>(ka);
+            break;
+        default:
+            full ? prefill_mfma16<T, 128, PMODE, ROPEK, true><<<grid, 256, 0, s>>>(ka)
+                 : prefill_mfma16<T, 128, PMODE, ROPEK, false><<<grid, 256, 0, s>>>(ka);
+            break;
     }
 }
 
-template <typename T, bool PAGED>
-static void launch16(const PrefillKArgs& ka, int dpad, dim3 grid, hipStream_t s) {
-    if (ka.a.rope_k) launch16r<T, PAGED, true>(ka, dpad, grid, s);
-    else launch16r<T, PAGED, false>(ka, dpad, grid, s);
+template <typename T>
+static void launch16(const PrefillKArgs& ka, bool paged, int dpad, dim3 grid, hipStream_t s) {
+    if (!paged) {
+        if (ka.a.rope_k) launch16r<T, kContig, true>(ka, dpad, grid, s);
+        else launch16r<T, kContig, false>(ka, dpad, grid, s);
+    } else if (ka.a.page_size % 16 == 0) {
+        // paged K is stored pre-rotated: no K rotation variants
+        launch16r<T, kPaged16, false>(ka, dpad, grid, s);
+    } else {
+        launch16r<T, kPagedAny, false>(ka, dpad, grid, s);
+    }
 }
 
 template <bool PAGED>
@@ -590,12 +639,8 @@ void launch_prefill(Dtype dt, bool paged, const PrefillArgs& a, hipStream_t s, u
     grid[2] = 1;
     *block = 256;
     switch (dt) {
-        case Dtype::BF16:
-            paged ? launch16<bf16_t, true>(ka, dpad, g, s) : launch16<bf16_t, false>(ka, dpad, g, s);
-            break;
-        case Dtype::F16:
-            paged ? launch16<f16_t, true>(ka, dpad, g, s) : launch16<f16_t, false>(ka, dpad, g, s);
-            break;
+        case Dtype::BF16: launch16<bf16_t>(ka, paged, dpad, g, s); break;
+        case Dtype::F16: launch16<f16_t>(ka, paged, dpad, g, s); break;
         default:
             paged ? launch32<true>(ka, dpad, g, s) : launch32<false>(ka, dpad, g, s);
             break;
