@@ -149,11 +149,19 @@ __device__ __forceinline__ void decode_item(const DecodeKArgs& ka, int w, int kv
 
     const uint8_t* kpool = (const uint8_t*)a.k_pool + (int64_t)kvh * D * EB;
     const uint8_t* vpool = (const uint8_t*)a.v_pool + (int64_t)kvh * D * EB;
+    // The split's block-table entries (at most 64: the host bounds split_tokens accordingly) are
+    // loaded once into one register per lane; page ids are then fetched with a lane shuffle.
+    // A per-key global load of the table would make every K/V address wait on a memory round
+    // trip and, as vmcnt drains in order, on every older prefetch as well.
     const int* bt = a.block_tables + (int64_t)s * a.bt_stride;
+    const int lp0 = (int)fdiv((uint32_t)k0, ka.ps_m, ka.ps_s);
+    const int lp_last = (int)fdiv((uint32_t)(k1 - 1), ka.ps_m, ka.ps_s);
+    const int bt_reg = lp0 + lane <= lp_last ? bt[lp0 + lane] : 0;
     auto row_of = [&](int key) -> int64_t {
         const uint32_t lp = fdiv((uint32_t)key, ka.ps_m, ka.ps_s);
         const int off = key - (int)lp * a.page_size;
-        return (int64_t)bt[lp] * a.page_size + off;
+        const int page = __shfl(bt_reg, (int)lp - lp0, 64);
+        return (int64_t)page * a.page_size + off;
     };
 
     constexpr int VCH = F32 ? 2 : 1;  // 16-byte loads per 8-dim V slice
@@ -165,11 +173,16 @@ __device__ __forceinline__ void decode_item(const DecodeKArgs& ka, int w, int kv
     float m_run = -INFINITY, l_run = 0.0f;
     const float c2 = a.scale * kLog2e;
 
-    u32x4_t kop[NQ];
-    u32x4_t vreg[4][VCH];
-    // Loads never branch: keys past the split end are clamped to its last live key (finite
-    // data whose scores are masked to -inf and whose V rows get probability exactly 0).
-    auto load_step = [&](int key0) {
+    // Register ring of NS steps of K/V: the K slot is refilled right after its MFMA and the V
+    // slot right after its P.V, so each wave keeps about NS-1 steps (8 KiB each at D = 128,
+    // 16-bit) of loads in flight. Loads never branch: keys past the split end are clamped to its
+    // last live key (finite data whose scores are masked to -inf and whose V rows get
+    // probability exactly 0).
+    constexpr int NS = 3;
+    u32x4_t kbuf[NS][NQ];
+    u32x4_t vbuf[NS][4][VCH];
+    const int dv_ld = 8 * n < D ? 8 * n : 0;
+    auto load_k = [&](u32x4_t* kd, int key0) {
         const int64_t krow = row_of(min(key0 + n, k1 - 1));
 #pragma unroll
         for (int c = 0; c < NQ; ++c) {
@@ -177,94 +190,112 @@ __device__ __forceinline__ void decode_item(const DecodeKArgs& ka, int w, int kv
             if constexpr (F32) d0 = 16 * c + 4 * g4;
             else d0 = 32 * c + 8 * g4;
             const int dl = d0 < D ? d0 : 0;
-            kop[c] = *(const u32x4_t*)(kpool + (krow * width + dl) * EB);
-            if (d0 >= D) kop[c] = u32x4_t{0u, 0u, 0u, 0u};
+            kd[c] = *(const u32x4_t*)(kpool + (krow * width + dl) * EB);
+            if (d0 >= D) kd[c] = u32x4_t{0u, 0u, 0u, 0u};
         }
-        const int dv = 8 * n < D ? 8 * n : 0;
+    };
+    auto load_v = [&](u32x4_t (*vd)[VCH], int key0) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int64_t vr = row_of(min(key0 + 4 * g4 + i, k1 - 1));
 #pragma unroll
             for (int c = 0; c < VCH; ++c)
-                vreg[i][c] = *(const u32x4_t*)(vpool + (vr * width + dv + 4 * c) * EB);
+                vd[i][c] = *(const u32x4_t*)(vpool + (vr * width + dv_ld + 4 * c) * EB);
         }
     };
 
-    if (k0 < k1) load_step(k0);
-    for (int key0 = k0; key0 < k1; key0 += 16) {
-        // ---- S^T[key = 4 g4 + i][head n]
-        f32x4_t sc = {0.f, 0.f, 0.f, 0.f};
+    // Loads are issued unconditionally (keys clamped to the split end: redundant refills re-read
+    // the last rows, which the caches already hold). A load under a branch would force a
+    // register copy at the merge point and, with it, a wait for the data right after the issue.
 #pragma unroll
-        for (int c = 0; c < NQ; ++c) {
-            if constexpr (F32) {
+    for (int s = 0; s < NS; ++s) {
+        load_k(kbuf[s], k0 + 16 * s);
+        load_v(vbuf[s], k0 + 16 * s);
+    }
+    for (int base = k0; base < k1; base += 16 * NS) {
 #pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    sc = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(kop[c][j]),
-                                                             __uint_as_float(qop[c][j]), sc, 0, 0,
-                                                             0);
-            } else {
-                sc = Half<T>::mfma16(kop[c], qop[c], sc);
+        for (int s = 0; s < NS; ++s) {
+            const int key0 = base + 16 * s;
+            const bool live = key0 < k1;  // uniform
+            // ---- S^T[key = 4 g4 + i][head n]
+            f32x4_t sc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int c = 0; c < NQ; ++c) {
+                if constexpr (F32) {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        sc = __builtin_amdgcn_mfma_f32_16x16x4f32(
+                            __uint_as_float(kbuf[s][c][j]), __uint_as_float(qop[c][j]), sc, 0, 0, 0);
+                } else {
+                    sc = Half<T>::mfma16(kbuf[s][c], qop[c], sc);
+                }
             }
-        }
-        u32x4_t vcur[4][VCH];
+            load_k(kbuf[s], key0 + 16 * NS);
+            if (live) {
+                if (key0 + 16 > k1) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+                    for (int i = 0; i < 4; ++i)
+                        if (key0 + 4 * g4 + i >= k1) sc[i] = -INFINITY;
+                }
+                float mt = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+                mt = fmaxf(mt, shfl_xor(mt, 16));
+                mt = fmaxf(mt, shfl_xor(mt, 32));
+                // Threshold rescale (as in the prefill kernel): the running max only moves when a
+                // step max exceeds it by more than 2^8 in probability, so the O rescale is rare.
+                const bool need = mt * c2 > m_run * c2 + 8.0f;
+                const bool any = __any(need);
+                if (any) {
+                    const float m_use = need ? mt : m_run;
+                    const float alpha = fast_exp2((m_run - m_use) * c2);  // m_run = -inf -> 0
+                    l_run *= alpha;
+                    m_run = m_use;
+                    if (g4 == 0) misc_lds[n] = alpha;
+                }
+                const float neg = -m_run * c2;
+                float lsum = 0.0f;
 #pragma unroll
-            for (int c = 0; c < VCH; ++c) vcur[i][c] = vreg[i][c];
-        if (key0 + 16 < k1) load_step(key0 + 16);
+                for (int i = 0; i < 4; ++i) {
+                    const float p = fast_exp2(fmaf(sc[i], c2, neg));
+                    p_lds[(4 * g4 + i) * 16 + n] = p;
+                    lsum += p;
+                }
+                l_run += lsum;
+                __syncthreads();
 
-        if (key0 + 16 > k1) {
+                // ---- O[h][8n .. 8n+7] += sum_i P[4 g4 + i][h] V[4 g4 + i][...]  (lane n = dims)
+                if (any) {
+                    float al[GT];
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-                if (key0 + 4 * g4 + i >= k1) sc[i] = -INFINITY;
-        }
-        float mt = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
-        mt = fmaxf(mt, shfl_xor(mt, 16));
-        mt = fmaxf(mt, shfl_xor(mt, 32));
-        const float m_new = fmaxf(m_run, mt);  // finite: key0 < k1 is live for every head
-        const float alpha = fast_exp2((m_run - m_new) * c2);
-        const float neg = -m_new * c2;
-        float lsum = 0.0f;
+                    for (int h = 0; h < GT; h += 4) {
+                        const f32x4_t v4 = *(const f32x4_t*)(misc_lds + h);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float p = fast_exp2(fmaf(sc[i], c2, neg));
-            p_lds[(4 * g4 + i) * 16 + n] = p;
-            lsum += p;
-        }
-        l_run = l_run * alpha + lsum;
-        m_run = m_new;
-        if (g4 == 0) misc_lds[n] = alpha;
-        __syncthreads();
-
-        // ---- O[h][8n .. 8n+7] += sum_i P[4 g4 + i][h] V[4 g4 + i][...]   (lane n = dim slice)
-        float al[GT];
+                        for (int j = 0; j < 4 && h + j < GT; ++j) al[h + j] = v4[j];
+                    }
 #pragma unroll
-        for (int h = 0; h < GT; h += 4) {
-            const f32x4_t v4 = *(const f32x4_t*)(misc_lds + h);
+                    for (int h = 0; h < GT; ++h)
 #pragma unroll
-            for (int j = 0; j < 4 && h + j < GT; ++j) al[h + j] = v4[j];
-        }
+                        for (int j = 0; j < 8; ++j) o[h][j] *= al[h];
+                }
 #pragma unroll
-        for (int h = 0; h < GT; ++h)
+                for (int i = 0; i < 4; ++i) {
+                    float vx[8];
+                    unpack8<T>(vbuf[s][i], vx);
+                    float pr[GT];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) o[h][j] *= al[h];
+                    for (int h = 0; h < GT; h += 4) {
+                        const f32x4_t p4 = *(const f32x4_t*)(p_lds + (4 * g4 + i) * 16 + h);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            float vx[8];
-            unpack8<T>(vcur[i], vx);
-            float pr[GT];
+                        for (int j = 0; j < 4 && h + j < GT; ++j) pr[h + j] = p4[j];
+                    }
 #pragma unroll
-            for (int h = 0; h < GT; h += 4) {
-                const f32x4_t p4 = *(const f32x4_t*)(p_lds + (4 * g4 + i) * 16 + h);
+                    for (int h = 0; h < GT; ++h)
 #pragma unroll
-                for (int j = 0; j < 4 && h + j < GT; ++j) pr[h + j] = p4[j];
+                        for (int j = 0; j < 8; ++j) o[h][j] = fmaf(pr[h], vx[j], o[h][j]);
+                }
+                __syncthreads();
             }
-#pragma unroll
-            for (int h = 0; h < GT; ++h)
-#pragma unroll
-                for (int j = 0; j < 8; ++j) o[h][j] = fmaf(pr[h], vx[j], o[h][j]);
+            load_v(vbuf[s], key0 + 16 * NS);
         }
-        __syncthreads();
     }
 
     // ---- reduce partial O over the 4 key groups, l over key groups
@@ -323,6 +354,239 @@ __device__ __forceinline__ void decode_item(const DecodeKArgs& ka, int w, int kv
     }
 }
 
+// ---------------------------------------------------------------------------------------
+// MFMA decode for 16-bit K/V with page_size % 16 == 0 (the serving configuration).
+//
+// Per 16-key step (one page-aligned group, so one wave-uniform block-table lookup):
+//   S^T[16 keys x 16 heads]  = K . Q^T        v_mfma_f32_16x16x32, K straight from HBM
+//   O^T[16 dims x 16 heads] += V^T . P^T      v_mfma_f32_16x16x16 per 16 dims
+// The S^T accumulator layout (lane = head n, keys 4g4 + i) is exactly the P^T B operand, so the
+// probabilities never leave registers; V is written row-major to a small LDS tile and read back
+// as V^T operands with ds_read_b64_tr_b16. Every value a lane holds belongs to one head, so the
+// online-softmax rescale is a per-lane scalar. Splits are merged by decode_combine.
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+
+template <typename T>
+__device__ __forceinline__ f32x4_t mfma16x16x16(s16x4_t a, s16x4_t b, f32x4_t c) {
+    if constexpr (std::is_same<T, bf16_t>::value) {
+        return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
+    } else {
+        typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
+        return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(h4_t, a),
+                                                     __builtin_bit_cast(h4_t, b), c, 0, 0, 0);
+    }
+}
+
+template <typename T, int DPAD, int GT>
+__device__ __forceinline__ void decode_mfma_item(const DecodeKArgs& ka, int w, int kvh, int hc,
+                                                 uint8_t* v_lds) {
+    using Hf = Half<T>;
+    constexpr int NQ = DPAD / 32;        // 16x16x32 k-steps for S
+    constexpr int NMB = DPAD / 16;       // 16-dim blocks of O^T
+    constexpr int VROWB = DPAD * 2 + 32; // padded V row in LDS (bytes)
+    constexpr int NS = 3;                // register ring depth (steps of 16 keys)
+    const DecodeArgs& a = ka.a;
+    const int lane = threadIdx.x;
+    const int n = lane & 15, g4 = lane >> 4;
+    const int s = a.work_seq[w], split = a.work_split[w];
+    const int ctx = a.ctx_lens[s];
+    const int k0 = split * a.split_tokens;
+    const int k1 = min(ctx, k0 + a.split_tokens);
+    const int D = a.head_dim, half = D >> 1;
+    const int hl0 = hc * 16;
+    const int nh = min(GT, a.group - hl0);
+    const int width = a.kv_heads * D;
+    const int qpos = a.q_positions[s];
+    const int hq0 = kvh * a.group + hl0;
+
+    // ---- Q^T operand (16x16x32 B operand): lane (head n, g4) holds dims 32c + 8g4 .. +8, rotated.
+    u32x4_t qop[NQ];
+    {
+        const bool hv = n < nh;
+        const uint16_t* qrow = (const uint16_t*)a.q + ((int64_t)s * a.q_heads + hq0 + (hv ? n : 0)) * D;
+        const float2* cs = a.rope_table + (int64_t)qpos * half;
+#pragma unroll
+        for (int c = 0; c < NQ; ++c) {
+            const int d0 = 32 * c + 8 * g4;
+            u32x4_t raw = {0u, 0u, 0u, 0u};
+            if (hv && d0 < D) {
+                raw = *(const u32x4_t*)(qrow + d0);
+                float x[8], c8[8];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    x[2 * j] = Hf::lo(raw[j]);
+                    x[2 * j + 1] = Hf::hi(raw[j]);
+                    const float2 cc = cs[d0 / 2 + j];
+                    c8[2 * j] = cc.x;
+                    c8[2 * j + 1] = cc.y;
+                }
+                rope4(x, c8);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) raw[j] = Hf::pack(x[2 * j], x[2 * j + 1]);
+            }
+            qop[c] = raw;
+        }
+    }
+
+    // ---- block table of this split (<= 64 pages) in one register; one uniform page per step
+    const int* bt = a.block_tables + (int64_t)s * a.bt_stride;
+    const int lp0 = (int)fdiv((uint32_t)k0, ka.ps_m, ka.ps_s);
+    const int lp_last = (int)fdiv((uint32_t)(k1 - 1), ka.ps_m, ka.ps_s);
+    const int bt_reg = lp0 + lane <= lp_last ? bt[lp0 + lane] : 0;
+    const uint8_t* const kpool = (const uint8_t*)a.k_pool + (int64_t)kvh * D * 2;
+    const uint8_t* const vpool = (const uint8_t*)a.v_pool + (int64_t)kvh * D * 2;
+    // first pool row of the page group holding keys [key0, key0 + 16)
+    auto group_row = [&](int key0) -> int64_t {
+        const int kc = min(key0, k1 - 1) & ~15;
+        const uint32_t lp = fdiv((uint32_t)kc, ka.ps_m, ka.ps_s);
+        const int page = __builtin_amdgcn_readlane(bt_reg, (int)lp - lp0);
+        return (int64_t)page * a.page_size + (kc - (int)lp * a.page_size);
+    };
+
+    // ---- register ring: K A operands (lane key row n, dims 32c + 8g4) and V rows (4g4 + i,
+    // dims 8n .. 8n+7). Keys past k1 are clamped to the last live key: finite data whose scores
+    // are masked and whose probabilities are exactly 0. Loads are unconditional (see above).
+    u32x4_t kbuf[NS][NQ];
+    u32x4_t vbuf[NS][4];
+    const int dk = min(8 * g4, D - 8), dv = min(8 * n, D - 8);
+    auto load_k = [&](u32x4_t* kd, int key0) {
+        const int64_t r0 = group_row(key0);
+        const int kr = min(key0 + n, k1 - 1) - (min(key0, k1 - 1) & ~15);
+        const uint8_t* rowp = kpool + (r0 + kr) * (int64_t)width * 2;
+#pragma unroll
+        for (int c = 0; c < NQ; ++c) {
+            kd[c] = *(const u32x4_t*)(rowp + (min(32 * c + 8 * g4, D - 8)) * 2);
+            if (32 * c + 8 * g4 >= D) kd[c] = u32x4_t{0u, 0u, 0u, 0u};
+        }
+        (void)dk;
+    };
+    auto load_v = [&](u32x4_t* vd, int key0) {
+        const int64_t r0 = group_row(key0);
+        const int base = min(key0, k1 - 1) & ~15;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int vr = min(key0 + 4 * g4 + i, k1 - 1) - base;
+            vd[i] = *(const u32x4_t*)(vpool + (r0 + vr) * (int64_t)width * 2 + dv * 2);
+        }
+    };
+
+    f32x4_t oacc[NMB];
+#pragma unroll
+    for (int mb = 0; mb < NMB; ++mb) oacc[mb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    float m_run = -INFINITY, l_run = 0.0f;
+    const float c2 = a.scale * kLog2e;
+    // ds_read_b64_tr_b16 source address of this lane: row 4g4 + (n >> 2), dims 4*(n & 3) .. +3
+    const uint8_t* const v_rd = v_lds + (4 * g4 + (n >> 2)) * VROWB + 8 * (n & 3);
+
+#pragma unroll
+    for (int t = 0; t < NS; ++t) {
+        load_k(kbuf[t], k0 + 16 * t);
+        load_v(vbuf[t], k0 + 16 * t);
+    }
+    for (int base = k0; base < k1; base += 16 * NS) {
+#pragma unroll
+        for (int t = 0; t < NS; ++t) {
+            const int key0 = base + 16 * t;
+            const bool live = key0 < k1;  // uniform
+            f32x4_t sc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int c = 0; c < NQ; ++c) sc = Hf::mfma16(kbuf[t][c], qop[c], sc);
+            load_k(kbuf[t], key0 + 16 * NS);
+            if (live) {
+                // V rows of this step -> LDS (row-major, padded)
+                if (n < DPAD / 8) {  // lanes past the padded head width hold no V chunk
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        *(u32x4_t*)(v_lds + (4 * g4 + i) * VROWB + n * 16) = vbuf[t][i];
+                }
+                if (key0 + 16 > k1) {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        if (key0 + 4 * g4 + i >= k1) sc[i] = -INFINITY;
+                }
+                float mt = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+                mt = fmaxf(mt, shfl_xor(mt, 16));
+                mt = fmaxf(mt, shfl_xor(mt, 32));
+                const bool need = mt * c2 > m_run * c2 + 8.0f;
+                if (__any(need)) {
+                    const float m_use = need ? mt : m_run;
+                    const float alpha = fast_exp2((m_run - m_use) * c2);  // m_run = -inf -> 0
+                    l_run *= alpha;
+#pragma unroll
+                    for (int mb = 0; mb < NMB; ++mb) oacc[mb] *= alpha;
+                    m_run = m_use;
+                }
+                const float neg = -m_run * c2;
+                float p[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    p[i] = fast_exp2(fmaf(sc[i], c2, neg));
+                    l_run += p[i];
+                }
+                const u32x2_t pw = {Hf::pack(p[0], p[1]), Hf::pack(p[2], p[3])};
+                const s16x4_t pb = __builtin_bit_cast(s16x4_t, pw);
+                __syncthreads();
+#pragma unroll
+                for (int mb = 0; mb < NMB; ++mb) {
+                    typedef __attribute__((address_space(3))) s16x4_t lds_s16x4_t;
+                    const s16x4_t av =
+                        __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(v_rd + mb * 32));
+                    oacc[mb] = mfma16x16x16<T>(av, pb, oacc[mb]);
+                }
+                __syncthreads();
+            }
+            load_v(vbuf[t], key0 + 16 * NS);
+        }
+    }
+
+    // ---- per-head totals (lane = head n; dims 16mb + 4g4 + i)
+    l_run += shfl_xor(l_run, 16);
+    l_run += shfl_xor(l_run, 32);
+    const int nsplit = a.seq_work_off[s + 1] - a.seq_work_off[s];
+    const bool hv = n < nh;
+    if (nsplit == 1) {
+        if (hv) {
+            const float inv = 1.0f / l_run;
+            uint16_t* orow = (uint16_t*)a.o + ((int64_t)s * a.q_heads + hq0 + n) * D;
+#pragma unroll
+            for (int mb = 0; mb < NMB; ++mb) {
+                const int d0 = 16 * mb + 4 * g4;
+                if (d0 < D) {
+                    const u32x2_t wv = {Hf::pack(oacc[mb][0] * inv, oacc[mb][1] * inv),
+                                        Hf::pack(oacc[mb][2] * inv, oacc[mb][3] * inv)};
+                    *(u32x2_t*)(orow + d0) = wv;
+                }
+            }
+            if (g4 == 0) a.lse[(int64_t)s * a.q_heads + hq0 + n] = m_run * a.scale + logf(l_run);
+        }
+        return;
+    }
+    if (hv) {
+        float* po = a.part_o + ((int64_t)w * a.q_heads + hq0 + n) * D;
+#pragma unroll
+        for (int mb = 0; mb < NMB; ++mb) {
+            const int d0 = 16 * mb + 4 * g4;
+            if (d0 < D) *(f32x4_t*)(po + d0) = oacc[mb];
+        }
+        if (g4 == 0) {
+            float* ml = a.part_ml + ((int64_t)w * a.q_heads + hq0 + n) * 2;
+            ml[0] = m_run;
+            ml[1] = l_run;
+        }
+    }
+}
+
+template <typename T, int DPAD, int GT>
+__global__ __launch_bounds__(64) void decode_mfma(DecodeKArgs ka, int n_items, int chunks) {
+    __shared__ __attribute__((aligned(16))) uint8_t v_lds[16 * (DPAD * 2 + 32)];
+    const int per_w = ka.a.kv_heads * chunks;
+    for (int it = blockIdx.x; it < n_items; it += gridDim.x) {
+        const int w = it / per_w, r = it % per_w;
+        decode_mfma_item<T, DPAD, GT>(ka, w, r / chunks, r % chunks, v_lds);
+        __syncthreads();
+    }
+}
+
 // Persistent split kernel: each one-wave workgroup walks work items with a static stride so
 // the grid is sized to what is resident at once (no partially filled last round). Every wave
 // exits once its stride passes n_items.
@@ -347,30 +611,51 @@ __global__ __launch_bounds__(64) void decode_combine(DecodeArgs a) {
     const int ns = w1 - w0;
     if (ns <= 1) return;  // finalised by the split kernel
     const float c2 = a.scale * kLog2e;
-    // split statistics, 64 splits per pass held across the lanes
+    const float* ml0 = a.part_ml + ((int64_t)w0 * a.q_heads + hq) * 2;
+    const int64_t step_ml = (int64_t)a.q_heads * 2;
+    // split statistics: split j in lane j % 64 (one pass for up to 64 splits)
     float M = -INFINITY;
-    for (int j = lane; j < ns; j += 64)
-        M = fmaxf(M, a.part_ml[((int64_t)(w0 + j) * a.q_heads + hq) * 2]);
+    for (int j = lane; j < ns; j += 64) M = fmaxf(M, ml0[j * step_ml]);
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) M = fmaxf(M, shfl_xor(M, o));
     float L = 0.0f;
-    for (int j = lane; j < ns; j += 64) {
-        const float* ml = a.part_ml + ((int64_t)(w0 + j) * a.q_heads + hq) * 2;
-        L += ml[1] * fast_exp2((ml[0] - M) * c2);
-    }
+    for (int j = lane; j < ns; j += 64) L += ml0[j * step_ml + 1] * fast_exp2((ml0[j * step_ml] - M) * c2);
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) L += shfl_xor(L, o);
     const float inv = 1.0f / L;
     const int d = 2 * lane;
-    if (d < a.head_dim) {
-        float acc0 = 0.0f, acc1 = 0.0f;
-        for (int j = 0; j < ns; ++j) {
-            const int64_t base = (int64_t)(w0 + j) * a.q_heads + hq;
-            const float wgt = fast_exp2((a.part_ml[base * 2] - M) * c2);
-            const float2 v = *(const float2*)(a.part_o + base * a.head_dim + d);
-            acc0 = fmaf(v.x, wgt, acc0);
-            acc1 = fmaf(v.y, wgt, acc1);
+    const float* po = a.part_o + ((int64_t)w0 * a.q_heads + hq) * a.head_dim + d;
+    const int64_t step_o = (int64_t)a.q_heads * a.head_dim;
+    float acc0 = 0.0f, acc1 = 0.0f;
+    for (int jb = 0; jb < ns; jb += 64) {
+        // weight of split jb + lane, broadcast by shuffle; O loads unrolled for memory parallelism
+        const int jl = jb + lane;
+        const float wl = jl < ns ? fast_exp2((ml0[jl * step_ml] - M) * c2) : 0.0f;
+        const int cnt = min(64, ns - jb);
+        int j = 0;
+        for (; j + 4 <= cnt; j += 4) {
+            float2 v[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+                v[u] = d < a.head_dim ? *(const float2*)(po + (jb + j + u) * step_o)
+                                      : make_float2(0.f, 0.f);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const float wgt = __shfl(wl, j + u, 64);
+                acc0 = fmaf(v[u].x, wgt, acc0);
+                acc1 = fmaf(v[u].y, wgt, acc1);
+            }
         }
+        for (; j < cnt; ++j) {
+            const float wgt = __shfl(wl, j, 64);
+            if (d < a.head_dim) {
+                const float2 v = *(const float2*)(po + (jb + j) * step_o);
+                acc0 = fmaf(v.x, wgt, acc0);
+                acc1 = fmaf(v.y, wgt, acc1);
+            }
+        }
+    }
+    if (d < a.head_dim) {
         uint8_t* dst = (uint8_t*)a.o + (((int64_t)s * a.q_heads + hq) * a.head_dim + d) * EB;
         if constexpr (std::is_same<T, float>::value) {
             *(float2*)dst = make_float2(acc0 * inv, acc1 * inv);
@@ -381,47 +666,65 @@ __global__ __launch_bounds__(64) void decode_combine(DecodeArgs a) {
     if (lane == 0) a.lse[(int64_t)s * a.q_heads + hq] = M * a.scale + logf(L);
 }
 
-template <typename T, int DPAD, int GT>
-static void launch_one(const DecodeKArgs& ka, int n_items, int chunks, hipStream_t s,
-                       unsigned* grid_x) {
-    static int resident = 0;  // resident one-wave workgroups per CU for this instantiation
-    if (!resident) {
-        int per_cu = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_splitk<T, DPAD, GT>, 64,
-                                                         0) != hipSuccess || per_cu <= 0)
-            per_cu = 8;
-        resident = per_cu;
-    }
+template <typename K>
+static int persistent_grid(K kernel, int n_items) {
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, 64, 0) != hipSuccess ||
+        per_cu <= 0)
+        per_cu = 8;
     int dev = 0, cus = 256;
     if (hipGetDevice(&dev) == hipSuccess)
         (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-    const int cap = resident * cus;
-    const int g = n_items < cap ? n_items : cap;
-    *grid_x = (unsigned)g;
-    decode_splitk<T, DPAD, GT><<<g, 64, 0, s>>>(ka, n_items, chunks);
+    const int cap = per_cu * cus;
+    return n_items < cap ? n_items : cap;
+}
+
+template <typename T, int DPAD, int GT>
+static void launch_one(const DecodeKArgs& ka, int n_items, int chunks, hipStream_t s,
+                       unsigned* grid_x, bool* fused) {
+    if constexpr (!std::is_same<T, float>::value) {
+        if (ka.a.page_size % 16 == 0) {
+            static int g = -1;
+            if (g < 0) g = persistent_grid(decode_mfma<T, DPAD, GT>, 1 << 30);
+            const int gg = n_items < g ? n_items : g;
+            *grid_x = (unsigned)gg;
+            *fused = false;
+            decode_mfma<T, DPAD, GT><<<gg, 64, 0, s>>>(ka, n_items, chunks);
+            return;
+        }
+    }
+    static int g = -1;
+    if (g < 0) g = persistent_grid(decode_splitk<T, DPAD, GT>, 1 << 30);
+    const int gg = n_items < g ? n_items : g;
+    *grid_x = (unsigned)gg;
+    *fused = false;
+    decode_splitk<T, DPAD, GT><<<gg, 64, 0, s>>>(ka, n_items, chunks);
 }
 
 template <typename T, int DPAD>
 static void launch_gt(const DecodeKArgs& ka, int gt, int n_items, int chunks, hipStream_t s,
-                      unsigned* gx) {
+                      unsigned* gx, bool* fused) {
     switch (gt) {
-        case 1: launch_one<T, DPAD, 1>(ka, n_items, chunks, s, gx); break;
-        case 2: launch_one<T, DPAD, 2>(ka, n_items, chunks, s, gx); break;
-        case 4: launch_one<T, DPAD, 4>(ka, n_items, chunks, s, gx); break;
-        case 8: launch_one<T, DPAD, 8>(ka, n_items, chunks, s, gx); break;
-        default: launch_one<T, DPAD, 16>(ka, n_items, chunks, s, gx); break;
+        case 1: launch_one<T, DPAD, 1>(ka, n_items, chunks, s, gx, fused); break;
+        case 2: launch_one<T, DPAD, 2>(ka, n_items, chunks, s, gx, fused); break;
+        case 4: launch_one<T, DPAD, 4>(ka, n_items, chunks, s, gx, fused); break;
+        case 8: launch_one<T, DPAD, 8>(ka, n_items, chunks, s, gx, fused); break;
+        default: launch_one<T, DPAD, 16>(ka, n_items, chunks, s, gx, fused); break;
     }
 }
 
 template <typename T>
-static void launch_t(const DecodeKArgs& ka, int dpad, int gt, int n_items, int chunks,
-                     dim3 cgrid, hipStream_t s, unsigned* gx) {
+static int launch_t(const DecodeKArgs& ka, int dpad, int gt, int n_items, int chunks,
+                    dim3 cgrid, hipStream_t s, unsigned* gx) {
+    bool fused = false;
     switch (dpad) {
-        case 32: launch_gt<T, 32>(ka, gt, n_items, chunks, s, gx); break;
-        case 64: launch_gt<T, 64>(ka, gt, n_items, chunks, s, gx); break;
-        default: launch_gt<T, 128>(ka, gt, n_items, chunks, s, gx); break;
+        case 32: launch_gt<T, 32>(ka, gt, n_items, chunks, s, gx, &fused); break;
+        case 64: launch_gt<T, 64>(ka, gt, n_items, chunks, s, gx, &fused); break;
+        default: launch_gt<T, 128>(ka, gt, n_items, chunks, s, gx, &fused); break;
     }
+    if (fused) return 1;
     decode_combine<T><<<cgrid, 64, 0, s>>>(ka.a);
+    return 2;
 }
 
 void launch_decode(Dtype dt, const DecodeArgs& a, hipStream_t s, unsigned grid[3],
@@ -441,16 +744,17 @@ void launch_decode(Dtype dt, const DecodeArgs& a, hipStream_t s, unsigned grid[3
     const int n_items = a.n_work * a.kv_heads * chunks;
     dim3 cg((unsigned)a.q_heads, (unsigned)a.n_seqs);
     unsigned gx = 0;
+    int nd = 0;
     switch (dt) {
-        case Dtype::BF16: launch_t<bf16_t>(ka, dpad, gt, n_items, chunks, cg, s, &gx); break;
-        case Dtype::F16: launch_t<f16_t>(ka, dpad, gt, n_items, chunks, cg, s, &gx); break;
-        default: launch_t<float>(ka, dpad, gt, n_items, chunks, cg, s, &gx); break;
+        case Dtype::BF16: nd = launch_t<bf16_t>(ka, dpad, gt, n_items, chunks, cg, s, &gx); break;
+        case Dtype::F16: nd = launch_t<f16_t>(ka, dpad, gt, n_items, chunks, cg, s, &gx); break;
+        default: nd = launch_t<float>(ka, dpad, gt, n_items, chunks, cg, s, &gx); break;
     }
     grid[0] = gx;
     grid[1] = 1;
     grid[2] = 1;
     *block = 64;
-    *dispatches = 2;
+    *dispatches = nd;
 }
 
 }  // namespace fa

@@ -1096,6 +1096,12 @@ struct fa_decode_plan {
 
 namespace {
 
+// A split may touch at most 64 pages (one block-table entry per lane of the decode wave).
+uint64_t max_split_tokens(uint64_t page_size) {
+    const uint64_t t = (63 * page_size + 1) / 16 * 16;
+    return std::max<uint64_t>(16, t);
+}
+
 uint64_t auto_split(const fa_decode_plan* p) {
     uint64_t total = 0;
     for (int32_t c : p->ctx_lens) total += (uint64_t)c;
@@ -1103,7 +1109,8 @@ uint64_t auto_split(const fa_decode_plan* p) {
     // Aim for ~8192 resident waves (32 per CU) so every CU streams several pages at once.
     uint64_t st = total * p->kv_heads * chunks / 8192;
     st = std::max<uint64_t>(64, std::min<uint64_t>(st, 4096));
-    return (st + 15) / 16 * 16;
+    st = (st + 15) / 16 * 16;
+    return std::min(st, max_split_tokens(p->page_size));
 }
 
 int build_work(fa_decode_plan* p) {
@@ -1277,6 +1284,10 @@ int fa_paged_decode_plan_set_split(fa_ctx* ctx, fa_decode_plan* p, uint64_t spli
     if (split_tokens % 16)
         return fail(FA_ERR_INDEX_SPACE_EXCEEDED, "split size %llu is not a multiple of 16",
                     (unsigned long long)split_tokens);
+    if (split_tokens > max_split_tokens(p->page_size))
+        return fail(FA_ERR_INDEX_SPACE_EXCEEDED,
+                    "split size %llu spans more than 64 pages of %llu tokens",
+                    (unsigned long long)split_tokens, (unsigned long long)p->page_size);
     if (int rc = set_device(ctx)) return rc;
     HIP_TRY(hipStreamSynchronize(ctx->stream));
     p->split_tokens = split_tokens ? split_tokens : auto_split(p);
@@ -1332,6 +1343,8 @@ int fa_paged_decode_launch(fa_ctx* ctx, const fa_decode_plan* p, const void* q, 
     a.seq_work_off = p->d_work + 2 * p->n_work;
     a.part_o = p->d_part;
     a.part_ml = p->d_part + p->n_work * p->q_heads * p->head_dim;
+    if (!a.part_o || !a.block_tables || !a.work_seq)
+        return fail(FA_ERR_NULL_ARGUMENT, "decode plan is missing device state");
     a.rope_table = table;
     a.n_seqs = (int)p->n_seqs;
     a.n_work = (int)p->n_work;
