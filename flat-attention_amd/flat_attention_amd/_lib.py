@@ -9,7 +9,9 @@ import ctypes
 import os
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "libflat_hip.so")
+# FLAT_HIP_LIBRARY selects another build of the same library (kernel experiments); the default
+# is the in-tree build.
+LIB_PATH = os.environ.get("FLAT_HIP_LIBRARY") or os.path.join(_HERE, "libflat_hip.so")
 
 U64 = ctypes.c_uint64
 I32 = ctypes.c_int32
