@@ -9,7 +9,12 @@ HIP events recorded on the library's own stream.
 
 value = prefill TFLOP/s (algorithmic FLOP over visible (q, k) pairs: 4*B*Hq*D*N(N+1)/2);
 decode GB/s (algorithmic bytes: K+V of every live token once, plus Q, O, LSE, block tables)
-is reported beside it with its own roofline.
+is reported beside it with its own roofline. `value` and each op's rate use the op's whole
+duration (the prefill op includes the K pre-rotation pass); each `roofline.achieved` divides the
+same algorithmic work by the average duration of the op's dominant kernel alone, timed by the
+library's per-dispatch events (fa_ctx_set_kernel_timing). `roofline.traffic` is the HBM bytes
+per launch of that kernel from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary
+(profiles/hbm_traffic_prefill_decode.json), scaled by a 1 GiB device-copy calibration.
 """
 from __future__ import annotations
 
@@ -42,6 +47,11 @@ class HipEvents:
         self.h.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p,
                                                ctypes.c_void_p]
         self.h.hipEventDestroy.argtypes = [ctypes.c_void_p]
+        self.h.hipMemcpyAsync.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t,
+                                          ctypes.c_int, ctypes.c_void_p]
+
+    def copy_d2d(self, dst, src, nbytes, stream):
+        assert self.h.hipMemcpyAsync(dst, src, nbytes, 3, ctypes.c_void_p(stream)) == 0
 
     def create(self):
         e = ctypes.c_void_p()
@@ -106,13 +116,64 @@ def build_decode(ctx, rng):
                          "split_tokens": info["split_tokens"], "work_items": info["work_items"]}
 
 
+TRAFFIC_JSON = os.path.join(ROOT, "profiles", "hbm_traffic_prefill_decode.json")
+COPY_BYTES = 1 << 30  # calibration copy: reads and writes exactly this many bytes
+
+
+def summarize_pmc(fetch_csv: str, write_csv: str) -> dict:
+    """HBM bytes per launch from two `rocprofv3 --pmc` runs of `bench.py --calibrate-copy`.
+
+    FETCH_SIZE / WRITE_SIZE (KiB per dispatch) are scaled by what the same counter reads for
+    the calibration copy of COPY_BYTES, so that the copy counts exactly COPY_BYTES each way."""
+    import collections
+    import csv
+
+    def load(path, counter):
+        per = collections.defaultdict(list)
+        for r in csv.DictReader(open(path)):
+            if r["Counter_Name"] == counter:
+                per[r["Kernel_Name"]].append(float(r["Counter_Value"]))
+        # median per kernel; for the copy kernel the largest dispatch is the calibration copy
+        return {k: float(np.max(v) if "copyBuffer" in k else np.median(v)) for k, v in per.items()}
+
+    fetch, write = load(fetch_csv, "FETCH_SIZE"), load(write_csv, "WRITE_SIZE")
+
+    def pick(d, *keys):
+        for k, v in d.items():
+            if all(x in k for x in keys):
+                return v
+        raise KeyError(keys)
+
+    copy_f = pick(fetch, "copyBuffer") * 1024.0
+    copy_w = pick(write, "copyBuffer") * 1024.0
+    f_scale, w_scale = COPY_BYTES / copy_f, COPY_BYTES / copy_w
+    res = {"copy_bytes": COPY_BYTES, "fetch_scale": f_scale, "write_scale": w_scale}
+    for name, key in (("prefill", "prefill_mfma16"), ("decode", "decode_mfma"),
+                      ("combine", "decode_combine"), ("rotate", "rotate_rows")):
+        try:
+            fb = pick(fetch, key) * 1024.0 * f_scale
+            wb = pick(write, key) * 1024.0 * w_scale
+        except KeyError:
+            continue
+        res[name] = {"fetch_bytes": fb, "write_bytes": wb, "traffic_bytes": fb + wb,
+                     "raw_fetch_kib": fb / 1024.0 / f_scale, "raw_write_kib": wb / 1024.0 / w_scale}
+    return res
+
+
+def load_traffic():
+    try:
+        return json.load(open(TRAFFIC_JSON))
+    except (OSError, ValueError):
+        return None
+
+
 def cpu_baseline(sample_seconds: float = 20.0):
     """Scalar C oracle (oracle/) timed on this host on bounded samples of the same workloads."""
     import oracle  # CPU baseline leg only
     res = {}
     # prefill: first (b, h) unit of configs[2] truncated to its first n query rows (causal rows
     # 0..n-1 do the same work as in the full problem); FLOP counted like the GPU metric.
-    n, D = 2048, 128
+    n, D = 4096, 128
     q = oracle.fill_normal(n * D, 1)
     k = oracle.fill_normal(n * D, 2)
     v = oracle.fill_normal(n * D, 3)
@@ -123,8 +184,8 @@ def cpu_baseline(sample_seconds: float = 20.0):
     res["prefill"] = {"value": flop / dt / 1e12, "unit": "TFLOP/s", "cores": 1, "kind": "port",
                       "sample": f"oracle forward_reference_grouped_rope, one (b,h) unit, causal "
                                 f"N={n} rows of configs[2] (D128, RoPE theta 1e4), {dt:.2f} s"}
-    # decode: 16 sequences of 4096 live tokens, Hq32 Hkv8 D128
-    ns, ctxl, hq, hkv, ps = 16, 4096, 32, 8, 16
+    # decode: 48 sequences of 4096 live tokens, Hq32 Hkv8 D128
+    ns, ctxl, hq, hkv, ps = 48, 4096, 32, 8, 16
     pages = ctxl // ps
     bt = np.arange(ns * pages, dtype=np.int32).reshape(ns, pages)
     kp = oracle.fill_normal(ns * ctxl * hkv * D, 4)
@@ -135,9 +196,16 @@ def cpu_baseline(sample_seconds: float = 20.0):
     dt = time.perf_counter() - t0
     nbytes = ns * ctxl * hkv * D * 2 * 2  # same bf16 byte accounting as the GPU metric
     res["decode"] = {"value": nbytes / dt / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
-                     "sample": f"oracle paged decode, 16 seqs x 4096 tokens, Hq32 Hkv8 D128, "
+                     "sample": f"oracle paged decode, {ns} seqs x {ctxl} tokens, Hq32 Hkv8 D128, "
                                f"{dt:.2f} s"}
     return res
+
+
+def _traffic(traffic, name):
+    """HBM bytes per launch of the op's dominant kernel, from the committed PMC summary."""
+    if not traffic or name not in traffic:
+        return None
+    return round(traffic[name]["traffic_bytes"])
 
 
 def main():
@@ -149,7 +217,18 @@ def main():
     ap.add_argument("--prefill-policy", type=int, default=-1,
                     help="-1 auto, 0 rotate K on load, 1 pre-rotate K")
     ap.add_argument("--only", choices=["prefill", "decode"], default=None)
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="also run one device copy of 1 GiB (counter calibration for --pmc runs)")
+    ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                    help="turn two rocprofv3 --pmc counter CSVs into the traffic summary")
     args = ap.parse_args()
+    if args.summarize_pmc:
+        res = summarize_pmc(*args.summarize_pmc)
+        os.makedirs(os.path.dirname(TRAFFIC_JSON), exist_ok=True)
+        with open(TRAFFIC_JSON, "w") as f:
+            json.dump(res, f, indent=1)
+        print(json.dumps(res))
+        return
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
               "(see DESIGN.md, 'How the path would shard')", file=sys.stderr)
@@ -175,6 +254,7 @@ def main():
     ctx.synchronize()
 
     evs = [[ev.create() for _ in range(len(ops) + 1)] for _ in range(args.steps)]
+    ctx.set_kernel_timing(True)
     t_wall = time.perf_counter()
     for s in range(args.steps):
         ev.record(evs[s][0], stream)
@@ -185,6 +265,18 @@ def main():
                 tele[name] = ctx.last_telemetry()
     ctx.synchronize()
     wall = time.perf_counter() - t_wall
+    if args.calibrate_copy:
+        a, b = fa.DeviceBuffer(ctx, COPY_BYTES), fa.DeviceBuffer(ctx, COPY_BYTES)
+        ev.copy_d2d(b.ptr, a.ptr, COPY_BYTES, stream)
+        ctx.synchronize()
+        a.free()
+        b.free()
+    # dominant kernel of each op, timed by the library's own events around each dispatch
+    kern = {}
+    for name, _, _, _ in ops:
+        total, n = ctx.kernel_timing(tele[name].kernel_id)
+        kern[name] = total / max(n, 1)
+    ctx.set_kernel_timing(False)
     per_op = {name: [ev.elapsed_ms(evs[s][i], evs[s][i + 1]) for s in range(args.steps)]
               for i, (name, _, _, _) in enumerate(ops)}
     step_ms = sum(np.mean(v) for v in per_op.values())
@@ -195,24 +287,30 @@ def main():
            "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
            "wall_s": round(wall, 3)}
     details = {}
+    traffic = load_traffic()
     for name, run, work, meta in ops:
         ms = float(np.mean(per_op[name]))
         t = tele[name]
         d = {"ms": round(ms, 5), "ms_min": round(float(np.min(per_op[name])), 5),
              "kernel": t.kernel_name, "kernel_id": t.kernel_id, "dispatches": t.dispatch_count,
              "grid": list(t.workgroups), **meta}
+        d["kernel_ms"] = round(kern[name], 5)
         if name == "prefill":
             tf = work / (ms * 1e-3) / 1e12
+            ktf = work / (kern[name] * 1e-3) / 1e12
             d.update({"TFLOP/s": round(tf, 2),
-                      "roofline": {"bound": "mfma", "achieved": round(tf, 2),
+                      "roofline": {"bound": "mfma", "achieved": round(ktf, 2),
                                    "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                                   "frac": round(tf / PEAK_BF16_TFLOPS, 4), "traffic": None}})
+                                   "frac": round(ktf / PEAK_BF16_TFLOPS, 4),
+                                   "traffic": _traffic(traffic, "prefill")}})
         else:
             gbs = work / (ms * 1e-3) / 1e9
+            kgbs = work / (kern[name] * 1e-3) / 1e9
             d.update({"GB/s": round(gbs, 1),
-                      "roofline": {"bound": "hbm", "achieved": round(gbs, 1),
+                      "roofline": {"bound": "hbm", "achieved": round(kgbs, 1),
                                    "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                                   "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None}})
+                                   "frac": round(kgbs / PEAK_HBM_GBS, 4),
+                                   "traffic": _traffic(traffic, "decode")}})
         details[name] = d
     if "prefill" in details:
         out["value"] = details["prefill"]["TFLOP/s"]

@@ -681,14 +681,14 @@ static int persistent_grid(K kernel, int n_items) {
 
 template <typename T, int DPAD, int GT>
 static void launch_one(const DecodeKArgs& ka, int n_items, int chunks, hipStream_t s,
-                       unsigned* grid_x, bool* fused) {
+                       unsigned* grid_x, bool* mfma) {
     if constexpr (!std::is_same<T, float>::value) {
         if (ka.a.page_size % 16 == 0) {
             static int g = -1;
             if (g < 0) g = persistent_grid(decode_mfma<T, DPAD, GT>, 1 << 30);
             const int gg = n_items < g ? n_items : g;
             *grid_x = (unsigned)gg;
-            *fused = false;
+            *mfma = true;
             decode_mfma<T, DPAD, GT><<<gg, 64, 0, s>>>(ka, n_items, chunks);
             return;
         }
@@ -697,38 +697,39 @@ static void launch_one(const DecodeKArgs& ka, int n_items, int chunks, hipStream
     if (g < 0) g = persistent_grid(decode_splitk<T, DPAD, GT>, 1 << 30);
     const int gg = n_items < g ? n_items : g;
     *grid_x = (unsigned)gg;
-    *fused = false;
+    *mfma = false;
     decode_splitk<T, DPAD, GT><<<gg, 64, 0, s>>>(ka, n_items, chunks);
 }
 
 template <typename T, int DPAD>
 static void launch_gt(const DecodeKArgs& ka, int gt, int n_items, int chunks, hipStream_t s,
-                      unsigned* gx, bool* fused) {
+                      unsigned* gx, bool* mfma) {
     switch (gt) {
-        case 1: launch_one<T, DPAD, 1>(ka, n_items, chunks, s, gx, fused); break;
-        case 2: launch_one<T, DPAD, 2>(ka, n_items, chunks, s, gx, fused); break;
-        case 4: launch_one<T, DPAD, 4>(ka, n_items, chunks, s, gx, fused); break;
-        case 8: launch_one<T, DPAD, 8>(ka, n_items, chunks, s, gx, fused); break;
-        default: launch_one<T, DPAD, 16>(ka, n_items, chunks, s, gx, fused); break;
+        case 1: launch_one<T, DPAD, 1>(ka, n_items, chunks, s, gx, mfma); break;
+        case 2: launch_one<T, DPAD, 2>(ka, n_items, chunks, s, gx, mfma); break;
+        case 4: launch_one<T, DPAD, 4>(ka, n_items, chunks, s, gx, mfma); break;
+        case 8: launch_one<T, DPAD, 8>(ka, n_items, chunks, s, gx, mfma); break;
+        default: launch_one<T, DPAD, 16>(ka, n_items, chunks, s, gx, mfma); break;
     }
 }
 
 template <typename T>
 static int launch_t(const DecodeKArgs& ka, int dpad, int gt, int n_items, int chunks,
-                    dim3 cgrid, hipStream_t s, unsigned* gx) {
-    bool fused = false;
+                    dim3 cgrid, hipStream_t s, unsigned* gx, bool* mfma, void (*between)(void*),
+                    void* user) {
     switch (dpad) {
-        case 32: launch_gt<T, 32>(ka, gt, n_items, chunks, s, gx, &fused); break;
-        case 64: launch_gt<T, 64>(ka, gt, n_items, chunks, s, gx, &fused); break;
-        default: launch_gt<T, 128>(ka, gt, n_items, chunks, s, gx, &fused); break;
+        case 32: launch_gt<T, 32>(ka, gt, n_items, chunks, s, gx, mfma); break;
+        case 64: launch_gt<T, 64>(ka, gt, n_items, chunks, s, gx, mfma); break;
+        default: launch_gt<T, 128>(ka, gt, n_items, chunks, s, gx, mfma); break;
     }
-    if (fused) return 1;
+    if (between) between(user);
     decode_combine<T><<<cgrid, 64, 0, s>>>(ka.a);
     return 2;
 }
 
 void launch_decode(Dtype dt, const DecodeArgs& a, hipStream_t s, unsigned grid[3],
-                   unsigned* block, int* dispatches) {
+                   unsigned* block, int* dispatches, bool* mfma, void (*between)(void*),
+                   void* user) {
     DecodeKArgs ka;
     ka.a = a;
     uint32_t sh = 0;
@@ -746,9 +747,9 @@ void launch_decode(Dtype dt, const DecodeArgs& a, hipStream_t s, unsigned grid[3
     unsigned gx = 0;
     int nd = 0;
     switch (dt) {
-        case Dtype::BF16: nd = launch_t<bf16_t>(ka, dpad, gt, n_items, chunks, cg, s, &gx); break;
-        case Dtype::F16: nd = launch_t<f16_t>(ka, dpad, gt, n_items, chunks, cg, s, &gx); break;
-        default: nd = launch_t<float>(ka, dpad, gt, n_items, chunks, cg, s, &gx); break;
+        case Dtype::BF16: nd = launch_t<bf16_t>(ka, dpad, gt, n_items, chunks, cg, s, &gx, mfma, between, user); break;
+        case Dtype::F16: nd = launch_t<f16_t>(ka, dpad, gt, n_items, chunks, cg, s, &gx, mfma, between, user); break;
+        default: nd = launch_t<float>(ka, dpad, gt, n_items, chunks, cg, s, &gx, mfma, between, user); break;
     }
     grid[0] = gx;
     grid[1] = 1;

@@ -154,6 +154,16 @@ struct fa_ctx {
     // per-call allocation accounting (telemetry)
     uint32_t call_allocs = 0;
     uint64_t call_alloc_bytes = 0;
+    // per-kernel device timing (fa_ctx_set_kernel_timing)
+    struct Span {
+        int kernel_id;
+        hipEvent_t begin, end;
+    };
+    bool timing = false;
+    hipEvent_t open_begin = nullptr;
+    std::vector<hipEvent_t> free_events;
+    std::vector<Span> pending;
+    std::vector<std::pair<double, uint64_t>> timed;  // indexed by kernel id
 };
 
 namespace {
@@ -194,6 +204,58 @@ void record(fa_ctx* ctx, int kernel_id, const char* name, uint32_t qrows, uint32
     t.device_fingerprint = ctx->fingerprint;
 }
 
+// Timing marks: begin_span records an event before a dispatch, end_span one after it and
+// files the pair under `kernel_id`. Both are no-ops while timing is off; an event failure
+// drops that one measurement rather than failing the call.
+hipEvent_t take_event(fa_ctx* ctx) {
+    if (!ctx->free_events.empty()) {
+        hipEvent_t e = ctx->free_events.back();
+        ctx->free_events.pop_back();
+        return e;
+    }
+    hipEvent_t e = nullptr;
+    return hipEventCreate(&e) == hipSuccess ? e : nullptr;
+}
+
+void begin_span(fa_ctx* ctx) {
+    if (!ctx->timing) return;
+    hipEvent_t e = take_event(ctx);
+    if (e && hipEventRecord(e, ctx->stream) != hipSuccess) {
+        ctx->free_events.push_back(e);
+        e = nullptr;
+    }
+    ctx->open_begin = e;
+}
+
+void end_span(fa_ctx* ctx, int kernel_id) {
+    if (!ctx->timing || !ctx->open_begin) return;
+    hipEvent_t e = take_event(ctx);
+    if (!e || hipEventRecord(e, ctx->stream) != hipSuccess) {
+        ctx->free_events.push_back(ctx->open_begin);
+        if (e) ctx->free_events.push_back(e);
+    } else {
+        ctx->pending.push_back({kernel_id, ctx->open_begin, e});
+    }
+    ctx->open_begin = nullptr;
+}
+
+// Folds completed spans into the per-kernel totals (waits for the stream first).
+int resolve_spans(fa_ctx* ctx) {
+    HIP_TRY(hipStreamSynchronize(ctx->stream));
+    for (const auto& s : ctx->pending) {
+        float ms = 0.0f;
+        if (hipEventElapsedTime(&ms, s.begin, s.end) == hipSuccess && s.kernel_id >= 0) {
+            if ((size_t)s.kernel_id >= ctx->timed.size()) ctx->timed.resize(s.kernel_id + 1, {0.0, 0});
+            ctx->timed[s.kernel_id].first += ms;
+            ctx->timed[s.kernel_id].second += 1;
+        }
+        ctx->free_events.push_back(s.begin);
+        ctx->free_events.push_back(s.end);
+    }
+    ctx->pending.clear();
+    return FA_OK;
+}
+
 int dev_alloc(fa_ctx* ctx, void** p, size_t bytes) {
     HIP_TRY(hipMalloc(p, bytes ? bytes : 16));
     ctx->call_allocs += 1;
@@ -228,7 +290,9 @@ int ensure_rope(fa_ctx* ctx, float theta, uint64_t head_dim, uint64_t rows, cons
     rc = dev_alloc(ctx, (void**)&ctx->inv_freq, half * sizeof(float));
     if (rc) return rc;
     HIP_TRY(hipMemcpy(ctx->inv_freq, inv.data(), half * sizeof(float), hipMemcpyHostToDevice));
+    begin_span(ctx);
     fa::launch_rope_table(ctx->rope, ctx->inv_freq, (int)cap, (int)half, ctx->stream);
+    end_span(ctx, FA_KERNEL_ROPE_TABLE);
     HIP_TRY(hipGetLastError());
     ctx->rope_theta = theta;
     ctx->rope_dim = head_dim;
@@ -354,6 +418,12 @@ int fa_ctx_destroy(fa_ctx* ctx) {
     if (ctx->rope) (void)hipFree(ctx->rope);
     if (ctx->inv_freq) (void)hipFree(ctx->inv_freq);
     if (ctx->ws) (void)hipFree(ctx->ws);
+    for (const auto& s : ctx->pending) {
+        (void)hipEventDestroy(s.begin);
+        (void)hipEventDestroy(s.end);
+    }
+    if (ctx->open_begin) (void)hipEventDestroy(ctx->open_begin);
+    for (hipEvent_t e : ctx->free_events) (void)hipEventDestroy(e);
     (void)hipStreamDestroy(ctx->stream);
     delete ctx;
     return ok();
@@ -371,6 +441,28 @@ int fa_ctx_synchronize(fa_ctx* ctx) {
 int fa_ctx_device_name(fa_ctx* ctx, char* buf, size_t len) {
     if (!ctx || !buf || !len) return fail(FA_ERR_NULL_ARGUMENT, "null argument");
     copy_str(buf, len, ctx->name + " (" + ctx->arch + ")");
+    return ok();
+}
+
+int fa_ctx_set_kernel_timing(fa_ctx* ctx, int32_t enable) {
+    if (!ctx) return fail(FA_ERR_NULL_ARGUMENT, "context is null");
+    if (int rc = set_device(ctx)) return rc;
+    if (int rc = resolve_spans(ctx)) return rc;
+    ctx->timed.clear();
+    ctx->timing = enable != 0;
+    return ok();
+}
+
+int fa_ctx_kernel_timing(fa_ctx* ctx, int32_t kernel_id, double* total_ms, uint64_t* launches) {
+    if (!ctx || !total_ms || !launches) return fail(FA_ERR_NULL_ARGUMENT, "null argument");
+    if (int rc = set_device(ctx)) return rc;
+    if (int rc = resolve_spans(ctx)) return rc;
+    *total_ms = 0.0;
+    *launches = 0;
+    if (kernel_id >= 0 && (size_t)kernel_id < ctx->timed.size()) {
+        *total_ms = ctx->timed[kernel_id].first;
+        *launches = ctx->timed[kernel_id].second;
+    }
     return ok();
 }
 
@@ -452,9 +544,21 @@ const char* kernel_name(int id) {
         case FA_KERNEL_PREFILL_MFMA_F16_PREROT: return "rotate_rows + prefill_mfma16<f16>";
         case FA_KERNEL_PREFILL_MFMA_F32_PREROT: return "rotate_rows + prefill_mfma_f32";
         case FA_KERNEL_DECODE_PAGED_SPLITK: return "decode_splitk + decode_combine";
+        case FA_KERNEL_DECODE_PAGED_MFMA: return "decode_mfma + decode_combine";
         default: return "none";
     }
 }
+
+// Closes the split kernel's timing span and opens the combine's, between the two launches.
+struct DecodeMarks {
+    fa_ctx* ctx;
+    const bool* mfma;
+    static void between(void* user) {
+        auto* m = static_cast<DecodeMarks*>(user);
+        end_span(m->ctx, *m->mfma ? FA_KERNEL_DECODE_PAGED_MFMA : FA_KERNEL_DECODE_PAGED_SPLITK);
+        begin_span(m->ctx);
+    }
+};
 
 // Common launch of the prefill kernel. `k_layout_rows`/`k_period`/`k_heads` describe how to
 // pre-rotate contiguous K (rows of k_heads*D elements, row r at position kv_rope_offset +
@@ -490,18 +594,22 @@ int run_prefill(fa_ctx* ctx, PrefillJob& j) {
     if (prerot) {
         void* ws = nullptr;
         if (int rc = ensure_ws(ctx, j.kv_bytes, &ws)) return rc;
+        begin_span(ctx);
         fa::launch_rotate_rows(j.dt, j.a.k, ws, (int)j.k_rows, (int)j.k_heads, j.a.head_dim,
                                (int64_t)j.k_period, table, j.a.kv_rope_offset, ctx->stream);
+        end_span(ctx, FA_KERNEL_ROPE_ROTATE);
         HIP_TRY(hipGetLastError());
         j.a.k = ws;
         j.a.rope_k = 0;
         dispatches++;
     }
     unsigned grid[3], block = 0;
+    const int kid = prefill_kernel_id(j.dtype, prerot);
+    begin_span(ctx);
     fa::launch_prefill(j.dt, j.paged, j.a, ctx->stream, grid, &block);
+    end_span(ctx, kid);
     HIP_TRY(hipGetLastError());
     dispatches++;
-    const int kid = prefill_kernel_id(j.dtype, prerot);
     const char* fb = nullptr;
     if (j.rope && j.a.rope_k && !prerot && !j.paged && j.a.head_dim % 8 != 0)
         fb = "K pre-rotation pass needs head_dim % 8 == 0; K rotated on load";
@@ -1039,9 +1147,11 @@ int fa_paged_cache_append(fa_paged_cache* c, const void* k_src, const void* v_sr
         if (dof + rows * c->row_bytes > c->tensor_bytes)
             return fail(FA_ERR_SHAPE_OVERFLOW, "paged resident KV shape overflows the address space");
         if (rot) {
+            begin_span(ctx);
             fa::launch_rotate_rows((Dtype)c->dtype, (const uint8_t*)k_src + so, (uint8_t*)c->k + dof,
                                    (int)rows, (int)c->kv_heads, (int)c->head_dim, (int64_t)kI32,
                                    table, (int)(rot->position_offset + logical), ctx->stream);
+            end_span(ctx, FA_KERNEL_ROPE_ROTATE);
             HIP_TRY(hipGetLastError());
         } else {
             HIP_TRY(hipMemcpyAsync((uint8_t*)c->k + dof, (const uint8_t*)k_src + so,
@@ -1358,9 +1468,15 @@ int fa_paged_decode_launch(fa_ctx* ctx, const fa_decode_plan* p, const void* q, 
     a.scale = p->scale;
     unsigned grid[3], block;
     int dispatches = 0;
-    fa::launch_decode((Dtype)p->dtype, a, ctx->stream, grid, &block, &dispatches);
+    bool mfma = false;
+    DecodeMarks marks{ctx, &mfma};
+    begin_span(ctx);
+    fa::launch_decode((Dtype)p->dtype, a, ctx->stream, grid, &block, &dispatches, &mfma,
+                      &DecodeMarks::between, &marks);
+    end_span(ctx, FA_KERNEL_DECODE_COMBINE);
     HIP_TRY(hipGetLastError());
-    record(ctx, FA_KERNEL_DECODE_PAGED_SPLITK, kernel_name(FA_KERNEL_DECODE_PAGED_SPLITK),
+    const int kid = mfma ? FA_KERNEL_DECODE_PAGED_MFMA : FA_KERNEL_DECODE_PAGED_SPLITK;
+    record(ctx, kid, kernel_name(kid),
            (uint32_t)std::min<uint64_t>(16, p->q_heads / p->kv_heads), 16, grid, block,
            (uint32_t)dispatches, (uint32_t)((p->split_tokens)), nullptr);
     return ok();
@@ -1596,7 +1712,9 @@ int fa_paged_append_batched(fa_ctx* ctx, const int32_t* block_tables, uint64_t m
     a.head_dim = (int)head_dim;
     a.rope_table = table;
     a.rope_offset = rot ? (int)rot->position_offset : 0;
+    begin_span(ctx);
     fa::launch_append((Dtype)dtype, a, ctx->stream);
+    end_span(ctx, FA_KERNEL_PAGED_APPEND);
     HIP_TRY(hipGetLastError());
     HIP_TRY(hipStreamSynchronize(ctx->stream));  // metadata buffer is released on return
     unsigned grid[3] = {(unsigned)append_len, (unsigned)n_seqs, 1};

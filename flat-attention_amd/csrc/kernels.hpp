@@ -62,8 +62,11 @@ struct DecodeArgs {
     float scale;
 };
 
+// Launches the split kernel then the combine; `between(user)` (if set) runs on the host between
+// the two launches. *mfma tells whether the MFMA split kernel was chosen.
 void launch_decode(Dtype dt, const DecodeArgs& a, hipStream_t s, unsigned grid[3],
-                   unsigned* block, int* dispatches);
+                   unsigned* block, int* dispatches, bool* mfma, void (*between)(void*),
+                   void* user);
 
 // (cos, sin) table: table[pos*half + p] for pos < rows, p < half = head_dim/2, with
 // angle = float(pos) * inv_freq[p].

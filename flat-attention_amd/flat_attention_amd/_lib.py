@@ -40,7 +40,7 @@ KERNEL_IDS = {
     0: "None", 1: "PrefillMfmaBf16", 2: "PrefillMfmaF16", 3: "PrefillMfmaF32",
     4: "PrefillMfmaBf16PreRotatedK", 5: "PrefillMfmaF16PreRotatedK",
     6: "PrefillMfmaF32PreRotatedK", 10: "DecodePagedSplitK", 11: "DecodeCombine",
-    12: "PagedAppend", 13: "RopeTable", 14: "RopeRotate",
+    12: "PagedAppend", 13: "RopeTable", 14: "RopeRotate", 15: "DecodePagedMfma",
 }
 
 
@@ -157,6 +157,8 @@ PROTOTYPES = {
     "fa_paged_append_batched": (INT, [VP, VP, U64, VP, U64, U64, U64, U64, U64, U64, VP, VP, SZ,
                                       VP, VP, SZ, P(RotaryC), INT]),
     "fa_last_telemetry": (INT, [VP, P(TelemetryC)]),
+    "fa_ctx_set_kernel_timing": (INT, [VP, I32]),
+    "fa_ctx_kernel_timing": (INT, [VP, I32, P(ctypes.c_double), P(U64)]),
 }
 
 

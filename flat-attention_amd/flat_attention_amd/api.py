@@ -249,6 +249,19 @@ class HipContext:
     def set_prefill_policy(self, prerotate_k: int):
         check(lib().fa_ctx_set_prefill_policy(self.handle, prerotate_k))
 
+    def set_kernel_timing(self, enable: bool):
+        """Bracket every dispatch with HIP events on the context's stream (clears totals)."""
+        check(lib().fa_ctx_set_kernel_timing(self.handle, 1 if enable else 0))
+
+    def kernel_timing(self, kernel_id) -> tuple[float, int]:
+        """(total ms, dispatch count) of one kernel since timing was enabled. `kernel_id` is an
+        fa_kernel_id number or its name (e.g. "DecodePagedMfma")."""
+        if isinstance(kernel_id, str):
+            kernel_id = {v: k for k, v in L.KERNEL_IDS.items()}[kernel_id]
+        ms, n = ctypes.c_double(), ctypes.c_uint64()
+        check(lib().fa_ctx_kernel_timing(self.handle, kernel_id, ctypes.byref(ms), ctypes.byref(n)))
+        return ms.value, n.value
+
     def last_telemetry(self) -> RuntimeDispatchTelemetry:
         t = L.TelemetryC()
         check(lib().fa_last_telemetry(self.handle, ctypes.byref(t)))

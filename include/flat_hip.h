@@ -134,7 +134,8 @@ typedef enum fa_kernel_id {
     FA_KERNEL_DECODE_COMBINE = 11,
     FA_KERNEL_PAGED_APPEND = 12,
     FA_KERNEL_ROPE_TABLE = 13,
-    FA_KERNEL_ROPE_ROTATE = 14
+    FA_KERNEL_ROPE_ROTATE = 14,
+    FA_KERNEL_DECODE_PAGED_MFMA = 15      /* 16-bit KV, page_size % 16 == 0: P.V on MFMA */
 } fa_kernel_id;
 
 /* RuntimeDispatchTelemetry src/runtime_telemetry.rs:159 + RuntimeTileGeometry :151 +
@@ -359,6 +360,17 @@ int fa_last_telemetry(fa_ctx* ctx, fa_telemetry* out);
 int fa_ctx_set_prefill_policy(fa_ctx* ctx, int32_t prerotate_k);
 int fa_kernel_variant_for_shape(fa_ctx* ctx, uint64_t head_dim, int32_t has_rope, int dtype,
                                 int32_t* kernel_id);
+
+/* Per-kernel device timing (extends runtime_telemetry src/wgpu_backend.rs:374, which carries no
+ * durations). While enabled, every dispatch the context issues is bracketed by HIP events on
+ * the context's stream. Enabling (or disabling) clears the accumulated totals. */
+int fa_ctx_set_kernel_timing(fa_ctx* ctx, int32_t enable);
+/* Waits for the context's stream, then returns the summed duration (ms) and the number of
+ * timed dispatches of `kernel_id` (an fa_kernel_id naming one kernel: a prefill variant id
+ * names the prefill kernel alone, FA_KERNEL_ROPE_ROTATE the K pre-rotation pass,
+ * FA_KERNEL_DECODE_PAGED_SPLITK / _MFMA the split kernel and FA_KERNEL_DECODE_COMBINE the
+ * combine) since timing was enabled. */
+int fa_ctx_kernel_timing(fa_ctx* ctx, int32_t kernel_id, double* total_ms, uint64_t* launches);
 
 #ifdef __cplusplus
 }

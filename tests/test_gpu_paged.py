@@ -331,3 +331,28 @@ def test_cfg5_chunked_prefill_over_paged_cache(hip):
             assert_close(f"O seq {s} head {unit}", got, exp, H16_ATOL, 0.0)
             gl = res.lse[(s * hq + unit) * ql:(s * hq + unit + 1) * ql]
             assert_close(f"LSE seq {s} head {unit}", gl, el[unit * ql:(unit + 1) * ql], H16_ATOL, 0.0)
+
+
+@pytest.mark.gpu
+def test_kernel_timing_and_mfma_variant_telemetry(hip):
+    """bf16 KV with page_size % 16 == 0 selects the MFMA split kernel; per-kernel timing counts
+    one split and one combine dispatch per launch and clears when re-enabled."""
+    rng = np.random.default_rng(5)
+    ctx_lens = [700, 1500, 33]
+    ps, hq, hkv, D = 16, 8, 2, 128
+    bt, kp, vp, total = _make_pool(rng, ctx_lens, ps, hkv, D, bf16_round)
+    q = bf16_round(normal(len(ctx_lens) * hq * D, 3))
+    hip.set_kernel_timing(True)
+    try:
+        _, _, plan = _decode(hip, bt, ctx_lens, kp, vp, total, ps, hq, hkv, D, q, fa.DTYPE_BF16)
+        t = hip.last_telemetry()
+        assert t.kernel_id == "DecodePagedMfma" and t.dispatch_count == 2
+        ms, n = hip.kernel_timing("DecodePagedMfma")
+        assert n == 1 and ms > 0.0
+        ms, n = hip.kernel_timing("DecodeCombine")
+        assert n == 1 and ms > 0.0
+        assert hip.kernel_timing("DecodePagedSplitK") == (0.0, 0)
+        hip.set_kernel_timing(True)
+        assert hip.kernel_timing("DecodePagedMfma") == (0.0, 0)
+    finally:
+        hip.set_kernel_timing(False)
