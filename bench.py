@@ -116,6 +116,99 @@ def build_decode(ctx, rng):
                          "split_tokens": info["split_tokens"], "work_items": info["work_items"]}
 
 
+PEAK_F32_TFLOPS = 157.3    # MI355X dense fp32 matrix
+
+
+def build_mha_f32(ctx, rng, causal):
+    """MHA B4 H16 N2048 D128, f32 I/O."""
+    B, H, S, D = 4, 16, 2048, 128
+    shape = fa.AttentionShape(B, H, S, D)
+    ex = fa.HipFlatAttention(ctx)
+    mk = lambda: fa.DeviceBuffer.from_array(ctx, rng.standard_normal(B * H * S * D, dtype=np.float32))  # noqa: E731
+    q, k, v = mk(), mk(), mk()
+    out = fa.DeviceBuffer(ctx, ex.layout(shape).combined_bytes)
+    cfg = fa.FlatAttentionConfig(causal=causal)
+    flop = 4.0 * B * H * D * (S * (S + 1) / 2 if causal else S * S)
+    return (lambda: ex.forward_resident(q, k, v, shape, cfg, out)), flop
+
+
+def build_chunked_paged(ctx, rng):
+    """8 sequences x (2048 cached + 512 new) in a shuffled page-16 pool, Hq32 Hkv8
+    D128 bf16, causal at offset 2048, RoPE theta 1e4 (K rotated on append). One step = the
+    batched append of the 512 new tokens followed by the chunk's prefill over the paged cache."""
+    n, hq, hkv, D, ps, cached, ql, theta = 8, 32, 8, 128, 16, 2048, 512, 1e4
+    kv_len = cached + ql
+    pages_per = kv_len // ps
+    total = n * pages_per
+    bt = rng.permutation(total).astype(np.int32).reshape(n, pages_per)
+    width = hkv * D
+    kp = fa.DeviceBuffer(ctx, total * ps * width * 2)
+    vp = fa.DeviceBuffer(ctx, total * ps * width * 2)
+    rot = fa.RotaryEmbeddingConfig(theta, 0)
+    fa.paged_append_batched(ctx, bt, np.zeros(n, np.int32), cached, ps, total, hkv, D,
+                            fa.DeviceBuffer.from_array(ctx, bf16_normal(rng, n * cached * width)),
+                            fa.DeviceBuffer.from_array(ctx, bf16_normal(rng, n * cached * width)),
+                            kp, vp, rot, fa.DTYPE_BF16)
+    new_k = fa.DeviceBuffer.from_array(ctx, bf16_normal(rng, n * ql * width))
+    new_v = fa.DeviceBuffer.from_array(ctx, bf16_normal(rng, n * ql * width))
+    starts = np.full(n, cached, np.int32)
+    shape = fa.AsymmetricGroupedAttentionShape(n, hq, hkv, ql, kv_len, D, cached)
+    plan = fa.PagedChunkedPrefillPlan(ctx, bt, ps, total, shape, fa.FlatAttentionConfig(True),
+                                      fa.AsymmetricRotaryEmbeddingConfig(theta, cached, 0),
+                                      fa.DTYPE_BF16)
+    q = fa.DeviceBuffer.from_array(ctx, bf16_normal(rng, n * ql * hq * D))
+    out = fa.DeviceBuffer(ctx, plan.layout().combined_bytes)
+
+    def append():
+        fa.paged_append_batched(ctx, bt, starts, ql, ps, total, hkv, D, new_k, new_v, kp, vp,
+                                rot, fa.DTYPE_BF16)
+
+    flop = 4.0 * n * hq * D * (ql * cached + ql * (ql + 1) / 2)
+    append_bytes = 2.0 * 2 * n * ql * width * 2  # K and V: read source, write pool
+    return (lambda: plan.launch(q, kp, vp, out)), flop, append, append_bytes
+
+
+def measure_all_configs(ctx, ev, rng, steps):
+    """The other BASELINE configs, each timed alone (op events + its kernel's own events)."""
+    stream = ctx.stream
+    res = {}
+
+    def timed(run):
+        for _ in range(2):
+            run()
+        tel = ctx.last_telemetry()
+        ctx.synchronize()
+        ctx.set_kernel_timing(True)
+        a, b = ev.create(), ev.create()
+        ev.record(a, stream)
+        for _ in range(steps):
+            run()
+        ev.record(b, stream)
+        op_ms = ev.elapsed_ms(a, b) / steps
+        total, cnt = ctx.kernel_timing(tel.kernel_id)
+        ctx.set_kernel_timing(False)
+        return op_ms, total / max(cnt, 1), tel
+
+    for causal in (False, True):
+        run, flop = build_mha_f32(ctx, rng, causal)
+        op_ms, k_ms, tel = timed(run)
+        tf = flop / (k_ms * 1e-3) / 1e12
+        res[f"cfg2_mha_f32_{'causal' if causal else 'noncausal'}"] = {
+            "kernel": tel.kernel_name, "ms": round(op_ms, 4), "kernel_ms": round(k_ms, 4),
+            "TFLOP/s": round(tf, 2), "frac_of_fp32_matrix_peak": round(tf / PEAK_F32_TFLOPS, 4)}
+    run, flop, append, append_bytes = build_chunked_paged(ctx, rng)
+    op_ms, k_ms, tel = timed(run)
+    tf = flop / (k_ms * 1e-3) / 1e12
+    res["cfg5_chunked_paged_prefill"] = {
+        "kernel": tel.kernel_name, "ms": round(op_ms, 4), "kernel_ms": round(k_ms, 4),
+        "TFLOP/s": round(tf, 2), "frac": round(tf / PEAK_BF16_TFLOPS, 4)}
+    op_ms, k_ms, tel = timed(append)
+    res["cfg5_batched_append_512"] = {
+        "kernel": tel.kernel_name, "ms": round(op_ms, 4), "kernel_ms": round(k_ms, 4),
+        "GB/s": round(append_bytes / (k_ms * 1e-3) / 1e9, 1)}
+    return res
+
+
 TRAFFIC_JSON = os.path.join(ROOT, "profiles", "hbm_traffic_prefill_decode.json")
 COPY_BYTES = 1 << 30  # calibration copy: reads and writes exactly this many bytes
 
@@ -217,6 +310,8 @@ def main():
     ap.add_argument("--prefill-policy", type=int, default=-1,
                     help="-1 auto, 0 rotate K on load, 1 pre-rotate K")
     ap.add_argument("--only", choices=["prefill", "decode"], default=None)
+    ap.add_argument("--all-configs", action="store_true",
+                    help="also time configs[1] (f32 MHA) and configs[4] (chunked paged prefill)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run one device copy of 1 GiB (counter calibration for --pmc runs)")
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
@@ -329,6 +424,8 @@ def main():
         cb = cpu_baseline()
         primary = cb["prefill"] if "prefill" in details else cb["decode"]
         out["cpu_baseline"] = dict(primary, other=cb["decode"] if "prefill" in details else None)
+    if args.all_configs:
+        out["other_configs"] = measure_all_configs(ctx, ev, rng, max(args.steps // 2, 5))
     ctx.close()
     print(json.dumps(out))
 

@@ -32,16 +32,19 @@ __device__ __forceinline__ float f16_hi(uint32_t w) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)(w >> 16));
 }
 
-// Round-to-nearest-even f32 -> bf16 pair (hardware v_cvt_pk_bf16_f32 on gfx950).
+// Round-to-nearest-even f32 pair -> packed 16-bit pair (a in the low half). The two-element
+// vector conversion selects the single gfx950 instruction v_cvt_pk_bf16_f32 / v_cvt_pk_f16_f32;
+// converting the halves one at a time costs two converts, a shift and an OR.
+typedef float pk_f32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 pk_bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 pk_f16x2_t __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
-    __bf16 x = (__bf16)a, y = (__bf16)b;
-    return (uint32_t)__builtin_bit_cast(uint16_t, x) |
-           ((uint32_t)__builtin_bit_cast(uint16_t, y) << 16);
+    const pk_f32x2_t v = {a, b};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, pk_bf16x2_t));
 }
 __device__ __forceinline__ uint32_t pack_f16(float a, float b) {
-    _Float16 x = (_Float16)a, y = (_Float16)b;
-    return (uint32_t)__builtin_bit_cast(uint16_t, x) |
-           ((uint32_t)__builtin_bit_cast(uint16_t, y) << 16);
+    const pk_f32x2_t v = {a, b};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, pk_f16x2_t));
 }
 
 template <typename T> struct Half;

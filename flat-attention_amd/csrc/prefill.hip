@@ -17,6 +17,8 @@
 // K rows are fed to the MFMA in a permuted order (bits 2 and 3 of the row swapped) so that the
 // eight scores a lane holds per 16-key step are contiguous keys, which is the order the P^T
 // operand of the second MFMA needs.
+#include <type_traits>
+
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -85,8 +87,22 @@ __device__ __forceinline__ int64_t paged_row(const PrefillKArgs& ka, int b, int 
 //     ds_read_b64_tr_b16, which hands each lane 4 keys of one dim (the 16-lane group transposes
 //     the 4x4 blocks it addresses), so V needs no transposition when it is staged.
 // Every per-step LDS address is a per-lane base plus a compile-time immediate.
+#ifndef FA_PREFILL_PIPE
+#define FA_PREFILL_PIPE 0
+#endif
+// Scheduling groups (LLVM AMDGPU sched_group_barrier masks: 0x2 VALU, 0x8 MFMA, 0x100 DS read, 0x400 transcendental).
+#define FA_SG(mask, n) __builtin_amdgcn_sched_group_barrier(mask, n, 0)
+#define FA_SG_MRV(nv) \
+    FA_SG(0x008, 1);  \
+    FA_SG(0x100, 1);  \
+    FA_SG(0x402, nv)
+#define FA_SG_MV(nv) \
+    FA_SG(0x008, 1);  \
+    FA_SG(0x402, nv)
+
 template <typename T, int DPAD, int PMODE, bool ROPEK, bool FULLD>
 __global__ __launch_bounds__(256, 2) void prefill_mfma16(PrefillKArgs ka) {
+    constexpr bool PIPE = FA_PREFILL_PIPE != 0;
     using H = Half<T>;
     const PrefillArgs& a = ka.a;
     constexpr int BM = 128, BN = 64;
@@ -171,23 +187,19 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma16(PrefillKArgs ka) {
     constexpr int kRsrcFlags = 0x00020000;
     u32x4_t kreg[KPASS], vreg[KPASS];
 
-    auto load_tile = [&](int tile) {
+    // One tile of K or V (base = kb8 or vb8) into `reg`.
+    auto load_one = [&](int tile, const uint8_t* base, u32x4_t (&reg)[KPASS]) {
         const int key_base = tile * BN;
         if constexpr (PMODE == kContig) {
             const int nrec = (a.kv_len - 1) * (int)row_bytes + D * 2;
-            const __amdgpu_buffer_rsrc_t rk =
-                __builtin_amdgcn_make_buffer_rsrc((void*)kb8, (short)0, nrec, kRsrcFlags);
-            const __amdgpu_buffer_rsrc_t rv =
-                __builtin_amdgcn_make_buffer_rsrc((void*)vb8, (short)0, nrec, kRsrcFlags);
+            const __amdgpu_buffer_rsrc_t rs =
+                __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, nrec, kRsrcFlags);
 #pragma unroll
             for (int p = 0; p < KPASS; ++p) {
                 const uint32_t off = lane_off + (uint32_t)(key_base + p * KRPP) * row_bytes;
-                kreg[p] = __builtin_amdgcn_raw_buffer_load_b128(rk, (int)off, 0, 0);
-                vreg[p] = __builtin_amdgcn_raw_buffer_load_b128(rv, (int)off, 0, 0);
+                reg[p] = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)off, 0, 0);
             }
         } else if constexpr (PMODE == kPaged16) {
-            // One 16-key group (one page, since page_size % 16 == 0) per wave and pass; the
-            // resources span the group's live rows only.
 #pragma unroll
             for (int p = 0; p < KPASS; ++p) {
                 const int key = key_base + p * KRPP + k_r;
@@ -199,13 +211,10 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma16(PrefillKArgs ka) {
                 const int64_t gofs = ((int64_t)page * a.page_size + (gq - (int)lp * a.page_size)) *
                                      (int64_t)row_bytes;
                 const int nrec = live > 0 ? (live - 1) * (int)row_bytes + D * 2 : 0;
-                const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
-                    (void*)(kb8 + gofs), (short)0, nrec, kRsrcFlags);
-                const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
-                    (void*)(vb8 + gofs), (short)0, nrec, kRsrcFlags);
+                const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+                    (void*)(base + gofs), (short)0, nrec, kRsrcFlags);
                 const int off = (int)((uint32_t)(key & 15) * row_bytes + kd2);
-                kreg[p] = __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 0);
-                vreg[p] = __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, 0);
+                reg[p] = __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0);
             }
         } else {
 #pragma unroll
@@ -213,18 +222,17 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma16(PrefillKArgs ka) {
                 const int key_raw = key_base + p * KRPP + k_r;
                 const int key = min(key_raw, a.kv_len - 1);
                 const int64_t r = paged_row<PMODE>(ka, b, key);
-                kreg[p] = *(const u32x4_t*)(kb8 + r * row_bytes + kd2);
-                vreg[p] = *(const u32x4_t*)(vb8 + r * row_bytes + kd2);
-                if (key_raw >= a.kv_len) kreg[p] = vreg[p] = u32x4_t{0u, 0u, 0u, 0u};
+                reg[p] = *(const u32x4_t*)(base + r * row_bytes + kd2);
+                if (key_raw >= a.kv_len) reg[p] = u32x4_t{0u, 0u, 0u, 0u};
             }
         }
         if (!FULLD && k_dc * 8 >= D) {
 #pragma unroll
-            for (int p = 0; p < KPASS; ++p) kreg[p] = vreg[p] = u32x4_t{0u, 0u, 0u, 0u};
+            for (int p = 0; p < KPASS; ++p) reg[p] = u32x4_t{0u, 0u, 0u, 0u};
         }
     };
 
-    auto store_tile = [&](int tile) {
+    auto store_k = [&](int tile) {
 #pragma unroll
         for (int p = 0; p < KPASS; ++p) {
             const int kl = p * KRPP + k_r;
@@ -247,6 +255,8 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma16(PrefillKArgs ka) {
             }
             *(u32x4_t*)(k_lds + kl * KROWB + k_dc * 16) = val;
         }
+    };
+    auto store_v = [&]() {
 #pragma unroll
         for (int p = 0; p < KPASS; ++p)
             *(u32x4_t*)(v_lds + (p * KRPP + k_r) * VROWB + k_dc * 16) = vreg[p];
@@ -270,26 +280,13 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma16(PrefillKArgs ka) {
     // than kRescaleLog2 (in log2 units). Until then probabilities are taken against the stale
     // max, so p <= 2^kRescaleLog2 and O, l stay consistent; the final O / l and
     // LSE = m_run*scale + ln l are exact either way. This skips the O^T rescale on most tiles.
-    auto rescale = [&](float mt) {
-        const bool need = mt * c2 > m_run * c2 + kRescaleLog2;
-        if (__any(need)) {
-            const float m_use = need ? mt : m_run;
-            const float alpha = fast_exp2((m_run - m_use) * c2);  // m_run = -inf -> 0
-            l_run *= alpha;
-#pragma unroll
-            for (int mb = 0; mb < MB; ++mb) oacc[mb] *= alpha;
-            m_run = m_use;
-        }
-    };
+    // The decision and the new max are branch-free (so the scores' exponentials can be
+    // scheduled between independent MFMAs); only the O^T multiply is conditional.
+    float alpha = 1.0f;
+    bool moved = false;
 
-    if (n_tiles > 0) load_tile(0);
-    for (int tile = 0; tile < n_tiles; ++tile) {
-        store_tile(tile);
-        __syncthreads();
-        if (tile + 1 < n_tiles) load_tile(tile + 1);
-
-        // ---- S^T = K_perm . Q^T
-        f32x16_t sacc[2];
+    // ---- S^T = K_perm . Q^T over the K tile in LDS
+    auto compute_s = [&](f32x16_t (&sacc)[2]) {
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) {
             sacc[kb] = (f32x16_t)0.0f;
@@ -299,10 +296,11 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma16(PrefillKArgs ka) {
                 sacc[kb] = H::mfma32(av, qop[ks], sacc[kb]);
             }
         }
+    };
 
-        // ---- mask (tail keys, causal diagonal)
-        const int tile_end = (tile + 1) * BN;
-        if (tile_end > a.kv_len || (a.causal && tile_end - 1 > cpos_min)) {
+    // ---- mask (tail keys, causal diagonal) and the running-max update of the online softmax
+    auto softmax_max = [&](f32x16_t (&sacc)[2], int tile, auto masked) {
+        if constexpr (decltype(masked)::value) {
             const int lim = (a.causal ? min(a.kv_len - 1, cpos) : a.kv_len - 1) - tile * BN - 8 * g;
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb)
@@ -310,29 +308,39 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma16(PrefillKArgs ka) {
                 for (int i = 0; i < 16; ++i)
                     if (32 * kb + 16 * (i >> 3) + (i & 7) > lim) sacc[kb][i] = -INFINITY;
         }
-
-        // ---- online softmax (row = this lane's query; partner lane ^ 32 holds the other keys)
-        float mt = sacc[0][0];
+        // row = this lane's query; partner lane ^ 32 holds the other keys. Four partial
+        // chains keep the max and sum dependency chains short.
+        float mx[4];
 #pragma unroll
-        for (int i = 1; i < 16; ++i) mt = fmaxf(mt, sacc[0][i]);
-#pragma unroll
-        for (int i = 0; i < 16; ++i) mt = fmaxf(mt, sacc[1][i]);
+        for (int c = 0; c < 4; ++c) {
+            const f32x16_t& v = sacc[c >> 1];
+            const int o = (c & 1) * 8;
+            mx[c] = fmaxf(fmaxf(fmaxf(v[o], v[o + 1]), fmaxf(v[o + 2], v[o + 3])),
+                          fmaxf(fmaxf(v[o + 4], v[o + 5]), fmaxf(v[o + 6], v[o + 7])));
+        }
+        float mt = fmaxf(fmaxf(mx[0], mx[1]), fmaxf(mx[2], mx[3]));
         mt = fmaxf(mt, shfl_xor(mt, 32));
-        rescale(mt);
+        const bool need = mt * c2 > m_run * c2 + kRescaleLog2;
+        moved = __any(need);
+        const float m_use = need ? mt : m_run;
+        alpha = need ? fast_exp2((m_run - m_use) * c2) : 1.0f;  // m_run = -inf -> 0
+        m_run = m_use;
+        l_run *= alpha;
+    };
+
+    // ---- probabilities, row sum and the P^T operands (16 keys each)
+    auto softmax_exp = [&](f32x16_t (&sacc)[2], u32x4_t (&pop)[4]) {
         const float neg = -m_run * c2;
-        float lsum = 0.0f;
+        float ls[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
                 const float p = fast_exp2(fmaf(sacc[kb][i], c2, neg));
                 sacc[kb][i] = p;
-                lsum += p;
+                ls[(i & 1) + 2 * kb] += p;
             }
-        l_run += lsum;
-
-        // ---- P^T operands (16 keys each)
-        u32x4_t pop[4];
+        l_run += (ls[0] + ls[1]) + (ls[2] + ls[3]);
 #pragma unroll
         for (int s2 = 0; s2 < 4; ++s2) {
             const int kb = s2 >> 1, h8 = (s2 & 1) * 8;
@@ -340,8 +348,17 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma16(PrefillKArgs ka) {
             for (int j = 0; j < 4; ++j)
                 pop[s2][j] = H::pack(sacc[kb][h8 + 2 * j], sacc[kb][h8 + 2 * j + 1]);
         }
+    };
 
-        // ---- O^T += V^T . P^T
+    auto rescale_o = [&]() {
+        if (moved) {
+#pragma unroll
+            for (int mb = 0; mb < MB; ++mb) oacc[mb] *= alpha;
+        }
+    };
+
+    // ---- O^T += V^T . P^T over the V tile in LDS
+    auto compute_pv = [&](const u32x4_t (&pop)[4]) {
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
@@ -357,7 +374,87 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma16(PrefillKArgs ka) {
                 const u32x4_t av = {l2[0], l2[1], h2[0], h2[1]};
                 oacc[mb] = H::mfma32(av, pop[s2], oacc[mb]);
             }
-        __syncthreads();
+    };
+
+    // Leading tiles that need no mask: every key is < kv_len and visible to every row.
+    int n_full = a.kv_len / BN;
+    if (a.causal) n_full = min(n_full, (cpos_min + 1) / BN);
+    using NoMask = std::integral_constant<bool, false>;
+    using Mask = std::integral_constant<bool, true>;
+
+    if constexpr (!PIPE) {
+        if (n_tiles > 0) {
+            load_one(0, kb8, kreg);
+            load_one(0, vb8, vreg);
+        }
+        for (int tile = 0; tile < n_tiles; ++tile) {
+            store_k(tile);
+            store_v();
+            __syncthreads();
+            if (tile + 1 < n_tiles) {
+                load_one(tile + 1, kb8, kreg);
+                load_one(tile + 1, vb8, vreg);
+            }
+            f32x16_t sacc[2];
+            u32x4_t pop[4];
+            compute_s(sacc);
+            if (tile < n_full) softmax_max(sacc, tile, NoMask{});
+            else softmax_max(sacc, tile, Mask{});
+            rescale_o();
+            softmax_exp(sacc, pop);
+            compute_pv(pop);
+            __syncthreads();
+        }
+    } else {
+        // Software pipeline: the K tile in LDS runs one tile ahead of the V tile, so the MFMAs
+        // of S(j+1) are independent of the softmax of tile j and are interleaved with it.
+        // Loop invariant at the top of step j: LDS holds K(j+1) and V(j); kreg holds (or is
+        // loading) K(j+2) and vreg V(j+1). On the last step S(j+1) is computed from a stale K
+        // tile and discarded.
+        f32x16_t s_a[2], s_b[2];
+        if (n_tiles > 0) {
+            load_one(0, kb8, kreg);
+            load_one(0, vb8, vreg);
+            store_k(0);
+            store_v();
+            if (n_tiles > 1) load_one(1, kb8, kreg);
+            __syncthreads();
+            compute_s(s_a);
+            if (n_tiles > 1) load_one(1, vb8, vreg);
+            __syncthreads();
+            if (n_tiles > 1) {
+                store_k(1);
+                if (n_tiles > 2) load_one(2, kb8, kreg);
+            }
+        }
+        auto step = [&](int j, f32x16_t (&cur)[2], f32x16_t (&nxt)[2], auto masked) {
+            softmax_max(cur, j, masked);
+            rescale_o();
+            __syncthreads();
+            u32x4_t pop[4];
+            compute_s(nxt);
+            softmax_exp(cur, pop);
+            // 16 K reads + 16 MFMAs of S(j+1) spread through the exponentials of tile j
+            FA_SG_MV(7); FA_SG_MV(7); FA_SG_MV(7); FA_SG_MV(7);
+            FA_SG_MV(7); FA_SG_MV(7); FA_SG_MV(7); FA_SG_MV(7);
+            FA_SG_MV(7); FA_SG_MV(7); FA_SG_MV(7); FA_SG_MV(7);
+            FA_SG_MV(7); FA_SG_MV(7); FA_SG_MV(7); FA_SG_MV(7);
+            __builtin_amdgcn_sched_barrier(0);
+            compute_pv(pop);
+            __syncthreads();
+            if (j + 1 < n_tiles) store_v();
+            if (j + 2 < n_tiles) store_k(j + 2);
+            if (j + 2 < n_tiles) load_one(j + 2, vb8, vreg);
+            if (j + 3 < n_tiles) load_one(j + 3, kb8, kreg);
+        };
+        auto step_any = [&](int j, f32x16_t (&cur)[2], f32x16_t (&nxt)[2]) {
+            if (j < n_full) step(j, cur, nxt, NoMask{});
+            else step(j, cur, nxt, Mask{});
+        };
+        for (int j = 0; j < n_tiles; j += 2) {
+            step_any(j, s_a, s_b);
+            if (j + 1 < n_tiles) step_any(j + 1, s_b, s_a);
+        }
     }
 
     // ---- epilogue
