@@ -604,7 +604,8 @@ int run_prefill(fa_ctx* ctx, PrefillJob& j) {
         dispatches++;
     }
     unsigned grid[3], block = 0;
-    const int kid = prefill_kernel_id(j.dtype, prerot);
+    // K read already rotated (pre-pass, or a paged cache that stores K rotated on append)
+    const int kid = prefill_kernel_id(j.dtype, prerot || (j.paged && j.rope));
     begin_span(ctx);
     fa::launch_prefill(j.dt, j.paged, j.a, ctx->stream, grid, &block);
     end_span(ctx, kid);
@@ -613,7 +614,18 @@ int run_prefill(fa_ctx* ctx, PrefillJob& j) {
     const char* fb = nullptr;
     if (j.rope && j.a.rope_k && !prerot && !j.paged && j.a.head_dim % 8 != 0)
         fb = "K pre-rotation pass needs head_dim % 8 == 0; K rotated on load";
-    record(ctx, kid, kernel_name(kid), 128, 64, grid, block, dispatches, 1, fb);
+    const char* dt = j.dtype == FA_DTYPE_BF16 ? "bf16" : j.dtype == FA_DTYPE_F16 ? "f16" : "f32";
+    const char* base = j.dtype == FA_DTYPE_F32 ? "prefill_mfma_f32" : "prefill_mfma16";
+    char name[64];
+    if (prerot)
+        snprintf(name, sizeof name, "rotate_rows + %s<%s>", base, dt);
+    else if (j.paged)
+        snprintf(name, sizeof name, "%s<%s> (paged%s)", base, dt, j.rope ? ", K stored rotated" : "");
+    else if (j.a.rope_k)
+        snprintf(name, sizeof name, "%s<%s> (K rotated on load)", base, dt);
+    else
+        snprintf(name, sizeof name, "%s<%s>", base, dt);
+    record(ctx, kid, name, 128, 64, grid, block, dispatches, 1, fb);
     return FA_OK;
 }
 
