@@ -82,6 +82,14 @@ template <> struct Half<f16_t> {
 // ---------------------------------------------------------------- wave utilities
 __device__ __forceinline__ float shfl_xor(float v, int mask) { return __shfl_xor(v, mask, 64); }
 
+// Value of lane (l ^ 32): one v_permlane32_swap (gfx950) swaps the wave halves in registers,
+// where a generic shuffle goes through the LDS crossbar (ds_bpermute).
+__device__ __forceinline__ float xor32(float v) {
+    const auto r =
+        __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float((threadIdx.x & 32) ? r[0] : r[1]);
+}
+
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // Rotate one interleaved (even, odd) pair: (e c - o s, e s + o c). Written with explicit fmaf

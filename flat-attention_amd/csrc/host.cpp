@@ -151,6 +151,10 @@ struct fa_ctx {
     // growable scratch for the K pre-rotation pass
     void* ws = nullptr;
     size_t ws_bytes = 0;
+    // growable scratch for the transposed V copy of the prefill
+    void* ws_vt = nullptr;
+    size_t ws_vt_bytes = 0;
+    int transpose_v_policy = -1;
     // per-call allocation accounting (telemetry)
     uint32_t call_allocs = 0;
     uint64_t call_alloc_bytes = 0;
@@ -301,18 +305,22 @@ int ensure_rope(fa_ctx* ctx, float theta, uint64_t head_dim, uint64_t rows, cons
     return FA_OK;
 }
 
-int ensure_ws(fa_ctx* ctx, size_t bytes, void** out) {
-    if (ctx->ws_bytes < bytes) {
+int grow(fa_ctx* ctx, void** buf, size_t* cap, size_t bytes, void** out) {
+    if (*cap < bytes) {
         HIP_TRY(hipStreamSynchronize(ctx->stream));
-        if (ctx->ws) HIP_TRY(hipFree(ctx->ws));
-        ctx->ws = nullptr;
-        ctx->ws_bytes = 0;
-        int rc = dev_alloc(ctx, &ctx->ws, bytes);
+        if (*buf) HIP_TRY(hipFree(*buf));
+        *buf = nullptr;
+        *cap = 0;
+        int rc = dev_alloc(ctx, buf, bytes);
         if (rc) return rc;
-        ctx->ws_bytes = bytes;
+        *cap = bytes;
     }
-    *out = ctx->ws;
+    *out = *buf;
     return FA_OK;
+}
+
+int ensure_ws(fa_ctx* ctx, size_t bytes, void** out) {
+    return grow(ctx, &ctx->ws, &ctx->ws_bytes, bytes, out);
 }
 
 }  // namespace
@@ -418,6 +426,7 @@ int fa_ctx_destroy(fa_ctx* ctx) {
     if (ctx->rope) (void)hipFree(ctx->rope);
     if (ctx->inv_freq) (void)hipFree(ctx->inv_freq);
     if (ctx->ws) (void)hipFree(ctx->ws);
+    if (ctx->ws_vt) (void)hipFree(ctx->ws_vt);
     for (const auto& s : ctx->pending) {
         (void)hipEventDestroy(s.begin);
         (void)hipEventDestroy(s.end);
@@ -463,6 +472,12 @@ int fa_ctx_kernel_timing(fa_ctx* ctx, int32_t kernel_id, double* total_ms, uint6
         *total_ms = ctx->timed[kernel_id].first;
         *launches = ctx->timed[kernel_id].second;
     }
+    return ok();
+}
+
+int fa_ctx_set_prefill_v_layout(fa_ctx* ctx, int32_t transpose_v) {
+    if (!ctx) return fail(FA_ERR_NULL_ARGUMENT, "context is null");
+    ctx->transpose_v_policy = transpose_v < 0 ? -1 : (transpose_v ? 1 : 0);
     return ok();
 }
 
@@ -603,6 +618,32 @@ int run_prefill(fa_ctx* ctx, PrefillJob& j) {
         j.a.rope_k = 0;
         dispatches++;
     }
+    // Optional transposed V copy for the 16-bit contiguous kernel (off unless selected): the V^T
+    // operand then comes from plain 16-byte LDS reads instead of transposing ones. It measured
+    // no faster at D = 128, so the extra pass is not run by default.
+    const bool vt = !j.paged && j.dtype != FA_DTYPE_F32 && j.a.head_dim % 8 == 0 &&
+                    ctx->transpose_v_policy == 1;
+    j.a.vt = nullptr;
+    j.a.vt_row = 0;
+    if (vt) {
+        const uint64_t s_pad = ((uint64_t)j.a.kv_len + 63) / 64 * 64;
+        const uint64_t bytes = (uint64_t)j.a.batch * j.a.kv_heads * j.a.head_dim * s_pad * 2u;
+        if ((uint64_t)j.a.head_dim * s_pad * 2u > (uint64_t)INT32_MAX)
+            return fail(FA_ERR_INDEX_SPACE_EXCEEDED,
+                        "one transposed V slice spans %llu bytes; the kernel addresses at most 2 GiB",
+                        (unsigned long long)((uint64_t)j.a.head_dim * s_pad * 2u));
+        void* wsv = nullptr;
+        if (int rc = grow(ctx, &ctx->ws_vt, &ctx->ws_vt_bytes, bytes, &wsv)) return rc;
+        begin_span(ctx);
+        fa::launch_transpose_v(j.dt, j.a.v, j.a.k_sb, j.a.k_sh, j.a.k_ss, j.a.batch,
+                               j.a.kv_heads, j.a.kv_len, j.a.head_dim, (int)s_pad, wsv,
+                               ctx->stream);
+        end_span(ctx, FA_KERNEL_TRANSPOSE_V);
+        HIP_TRY(hipGetLastError());
+        j.a.vt = wsv;
+        j.a.vt_row = (int)s_pad;
+        dispatches++;
+    }
     unsigned grid[3], block = 0;
     // K read already rotated (pre-pass, or a paged cache that stores K rotated on append)
     const int kid = prefill_kernel_id(j.dtype, prerot || (j.paged && j.rope));
@@ -617,8 +658,9 @@ int run_prefill(fa_ctx* ctx, PrefillJob& j) {
     const char* dt = j.dtype == FA_DTYPE_BF16 ? "bf16" : j.dtype == FA_DTYPE_F16 ? "f16" : "f32";
     const char* base = j.dtype == FA_DTYPE_F32 ? "prefill_mfma_f32" : "prefill_mfma16";
     char name[64];
-    if (prerot)
-        snprintf(name, sizeof name, "rotate_rows + %s<%s>", base, dt);
+    if (prerot || vt)
+        snprintf(name, sizeof name, "%s%s%s<%s>", prerot ? "rotate_rows + " : "",
+                 vt ? "transpose_v + " : "", base, dt);
     else if (j.paged)
         snprintf(name, sizeof name, "%s<%s> (paged%s)", base, dt, j.rope ? ", K stored rotated" : "");
     else if (j.a.rope_k)

@@ -61,7 +61,9 @@ constexpr float kRescaleLog2 = 8.0f;
 
 // ------------------------------------------------------------------ 16-bit MFMA kernel
 // K/V source addressing modes.
-enum : int { kContig = 0, kPaged16 = 1, kPagedAny = 2 };
+// kContigVT: contiguous K, V read from its transposed copy (PrefillArgs::vt), so the V^T operand
+// of O^T += V^T.P^T is a plain 16-byte LDS read rather than a transposing one.
+enum : int { kContig = 0, kPaged16 = 1, kPagedAny = 2, kContigVT = 3 };
 
 // Physical row of `key` for batch b. kPaged16 requires page_size % 16 == 0 and a key group of
 // 16 consecutive keys per wave, so the block-table entry is wave-uniform (one scalar load).
@@ -113,7 +115,11 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma16(PrefillKArgs ka) {
     constexpr int KPASS = BN / KRPP;
     constexpr int KROWB = DPAD * 2 + 16;    // padded K row (bytes)
     constexpr int VROWB = DPAD * 2 + 64;    // padded V row (bytes)
-    __shared__ __attribute__((aligned(16))) uint8_t smem[BN * KROWB + BN * VROWB];
+    constexpr bool VT = PMODE == kContigVT;
+    constexpr bool CONTIG = PMODE == kContig || VT;
+    constexpr int VTROWB = BN * 2 + 16;     // padded V^T row: 64 keys of one dim (bytes)
+    constexpr int VBYTES = VT ? DPAD * VTROWB : BN * VROWB;
+    __shared__ __attribute__((aligned(16))) uint8_t smem[BN * KROWB + VBYTES];
     uint8_t* const k_lds = smem;
     uint8_t* const v_lds = smem + BN * KROWB;
 
@@ -178,7 +184,7 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma16(PrefillKArgs ka) {
     // head_dim < DPAD) are zeroed explicitly.
     const uint32_t row_bytes = (uint32_t)a.k_ss * 2u;
     const int64_t head_off =
-        (int64_t)kvh * a.k_sh * 2 + (PMODE == kContig ? (int64_t)b * a.k_sb * 2 : 0);
+        (int64_t)kvh * a.k_sh * 2 + (CONTIG ? (int64_t)b * a.k_sb * 2 : 0);
     const uint8_t* const kb8 = (const uint8_t*)a.k + head_off;
     const uint8_t* const vb8 = (const uint8_t*)a.v + head_off;
     const int k_dc = tid % CPR, k_r = tid / CPR;
@@ -186,11 +192,28 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma16(PrefillKArgs ka) {
     const uint32_t lane_off = (uint32_t)k_r * row_bytes + kd2;  // this thread's row/chunk
     constexpr int kRsrcFlags = 0x00020000;
     u32x4_t kreg[KPASS], vreg[KPASS];
+    // V^T staging: thread chunk p covers dim (tid + 256p) / 8, keys 8 * (tid % 8) .. +7 of the
+    // tile; dims >= head_dim lie past the resource range and read as 0. (DPAD * 8 / 256 ==
+    // KPASS chunks per thread.)
+    const uint8_t* const vtb8 =
+        VT ? (const uint8_t*)a.vt + (((int64_t)b * a.kv_heads + kvh) * D) * a.vt_row * 2 : nullptr;
+
+    auto load_vt = [&](int tile) {
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)vtb8, (short)0, D * a.vt_row * 2, kRsrcFlags);
+#pragma unroll
+        for (int p = 0; p < KPASS; ++p) {
+            const int c = tid + 256 * p;
+            const uint32_t off = ((uint32_t)(c >> 3) * (uint32_t)a.vt_row +
+                                  (uint32_t)(tile * BN + (c & 7) * 8)) * 2u;
+            vreg[p] = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)off, 0, 0);
+        }
+    };
 
     // One tile of K or V (base = kb8 or vb8) into `reg`.
     auto load_one = [&](int tile, const uint8_t* base, u32x4_t (&reg)[KPASS]) {
         const int key_base = tile * BN;
-        if constexpr (PMODE == kContig) {
+        if constexpr (CONTIG) {
             const int nrec = (a.kv_len - 1) * (int)row_bytes + D * 2;
             const __amdgpu_buffer_rsrc_t rs =
                 __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, nrec, kRsrcFlags);
@@ -257,9 +280,21 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma16(PrefillKArgs ka) {
         }
     };
     auto store_v = [&]() {
+        if constexpr (VT) {
 #pragma unroll
-        for (int p = 0; p < KPASS; ++p)
-            *(u32x4_t*)(v_lds + (p * KRPP + k_r) * VROWB + k_dc * 16) = vreg[p];
+            for (int p = 0; p < KPASS; ++p) {
+                const int c = tid + 256 * p;
+                *(u32x4_t*)(v_lds + (c >> 3) * VTROWB + (c & 7) * 16) = vreg[p];
+            }
+        } else {
+#pragma unroll
+            for (int p = 0; p < KPASS; ++p)
+                *(u32x4_t*)(v_lds + (p * KRPP + k_r) * VROWB + k_dc * 16) = vreg[p];
+        }
+    };
+    auto load_v = [&](int tile) {
+        if constexpr (VT) load_vt(tile);
+        else load_one(tile, vb8, vreg);
     };
 
     f32x16_t oacc[MB];
@@ -358,7 +393,19 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma16(PrefillKArgs ka) {
     };
 
     // ---- O^T += V^T . P^T over the V tile in LDS
+    // V^T layout: lane reads dim mb*32 + (lane & 31), keys 16 s2 + 8 g .. +7 (16 bytes).
+    const uint8_t* const vt_rd = v_lds + (lane & 31) * VTROWB + g * 16;
     auto compute_pv = [&](const u32x4_t (&pop)[4]) {
+        if constexpr (VT) {
+#pragma unroll
+            for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+                for (int s2 = 0; s2 < 4; ++s2) {
+                    const u32x4_t av = *(const u32x4_t*)(vt_rd + mb * 32 * VTROWB + s2 * 32);
+                    oacc[mb] = H::mfma32(av, pop[s2], oacc[mb]);
+                }
+            return;
+        }
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
@@ -385,7 +432,7 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma16(PrefillKArgs ka) {
     if constexpr (!PIPE) {
         if (n_tiles > 0) {
             load_one(0, kb8, kreg);
-            load_one(0, vb8, vreg);
+            load_v(0);
         }
         for (int tile = 0; tile < n_tiles; ++tile) {
             store_k(tile);
@@ -393,7 +440,7 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma16(PrefillKArgs ka) {
             __syncthreads();
             if (tile + 1 < n_tiles) {
                 load_one(tile + 1, kb8, kreg);
-                load_one(tile + 1, vb8, vreg);
+                load_v(tile + 1);
             }
             f32x16_t sacc[2];
             u32x4_t pop[4];
@@ -414,13 +461,13 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma16(PrefillKArgs ka) {
         f32x16_t s_a[2], s_b[2];
         if (n_tiles > 0) {
             load_one(0, kb8, kreg);
-            load_one(0, vb8, vreg);
+            load_v(0);
             store_k(0);
             store_v();
             if (n_tiles > 1) load_one(1, kb8, kreg);
             __syncthreads();
             compute_s(s_a);
-            if (n_tiles > 1) load_one(1, vb8, vreg);
+            if (n_tiles > 1) load_v(1);
             __syncthreads();
             if (n_tiles > 1) {
                 store_k(1);
@@ -444,7 +491,7 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma16(PrefillKArgs ka) {
             __syncthreads();
             if (j + 1 < n_tiles) store_v();
             if (j + 2 < n_tiles) store_k(j + 2);
-            if (j + 2 < n_tiles) load_one(j + 2, vb8, vreg);
+            if (j + 2 < n_tiles) load_v(j + 2);
             if (j + 3 < n_tiles) load_one(j + 3, kb8, kreg);
         };
         auto step_any = [&](int j, f32x16_t (&cur)[2], f32x16_t (&nxt)[2]) {
@@ -703,8 +750,14 @@ static void launch16r(const PrefillKArgs& ka, int dpad, dim3 grid, hipStream_t s
 template <typename T>
 static void launch16(const PrefillKArgs& ka, bool paged, int dpad, dim3 grid, hipStream_t s) {
     if (!paged) {
-        if (ka.a.rope_k) launch16r<T, kContig, true>(ka, dpad, grid, s);
-        else launch16r<T, kContig, false>(ka, dpad, grid, s);
+        if (ka.a.vt) {
+            if (ka.a.rope_k) launch16r<T, kContigVT, true>(ka, dpad, grid, s);
+            else launch16r<T, kContigVT, false>(ka, dpad, grid, s);
+        } else if (ka.a.rope_k) {
+            launch16r<T, kContig, true>(ka, dpad, grid, s);
+        } else {
+            launch16r<T, kContig, false>(ka, dpad, grid, s);
+        }
     } else if (ka.a.page_size % 16 == 0) {
         // paged K is stored pre-rotated: no K rotation variants
         launch16r<T, kPaged16, false>(ka, dpad, grid, s);

@@ -40,7 +40,7 @@ KERNEL_IDS = {
     0: "None", 1: "PrefillMfmaBf16", 2: "PrefillMfmaF16", 3: "PrefillMfmaF32",
     4: "PrefillMfmaBf16PreRotatedK", 5: "PrefillMfmaF16PreRotatedK",
     6: "PrefillMfmaF32PreRotatedK", 10: "DecodePagedSplitK", 11: "DecodeCombine",
-    12: "PagedAppend", 13: "RopeTable", 14: "RopeRotate", 15: "DecodePagedMfma",
+    12: "PagedAppend", 13: "RopeTable", 14: "RopeRotate", 15: "DecodePagedMfma", 16: "TransposeV",
 }
 
 
@@ -108,6 +108,7 @@ PROTOTYPES = {
     "fa_ctx_synchronize": (INT, [VP]),
     "fa_ctx_device_name": (INT, [VP, ctypes.c_char_p, SZ]),
     "fa_ctx_set_prefill_policy": (INT, [VP, I32]),
+    "fa_ctx_set_prefill_v_layout": (INT, [VP, I32]),
     "fa_kernel_variant_for_shape": (INT, [VP, U64, I32, INT, P(I32)]),
     "fa_buf_alloc": (INT, [VP, SZ, P(VP)]),
     "fa_buf_free": (INT, [VP, VP]),

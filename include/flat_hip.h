@@ -135,7 +135,8 @@ typedef enum fa_kernel_id {
     FA_KERNEL_PAGED_APPEND = 12,
     FA_KERNEL_ROPE_TABLE = 13,
     FA_KERNEL_ROPE_ROTATE = 14,
-    FA_KERNEL_DECODE_PAGED_MFMA = 15      /* 16-bit KV, page_size % 16 == 0: P.V on MFMA */
+    FA_KERNEL_DECODE_PAGED_MFMA = 15,     /* 16-bit KV, page_size % 16 == 0: P.V on MFMA */
+    FA_KERNEL_TRANSPOSE_V = 16            /* V -> V^T pre-pass of the 16-bit contiguous prefill */
 } fa_kernel_id;
 
 /* RuntimeDispatchTelemetry src/runtime_telemetry.rs:159 + RuntimeTileGeometry :151 +
@@ -358,6 +359,11 @@ int fa_last_telemetry(fa_ctx* ctx, fa_telemetry* out);
  * prerotate_k: 0 = rotate K tiles on load inside the prefill kernel, 1 = rotate K once in a
  * pre-pass, -1 = automatic (default). */
 int fa_ctx_set_prefill_policy(fa_ctx* ctx, int32_t prerotate_k);
+/* V layout policy of the 16-bit contiguous prefill (same role as the K policy above): 1 = copy
+ * V once into a transposed workspace [batch, kv_heads, head_dim, kv_len rounded up to 64] and
+ * stream V^T tiles, 0 = stream V rows and transpose in the kernel, -1 = automatic (currently
+ * 0). Both layouts give bit-identical results. */
+int fa_ctx_set_prefill_v_layout(fa_ctx* ctx, int32_t transpose_v);
 int fa_kernel_variant_for_shape(fa_ctx* ctx, uint64_t head_dim, int32_t has_rope, int dtype,
                                 int32_t* kernel_id);
 
