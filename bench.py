@@ -12,7 +12,7 @@ decode GB/s (algorithmic bytes: K+V of every live token once, plus Q, O, LSE, bl
 is reported beside it with its own roofline. `value` and each op's rate use the op's whole
 duration (the prefill op includes the K pre-rotation pass); each `roofline.achieved` divides the
 same algorithmic work by the average duration of the op's dominant kernel alone, timed by the
-library's per-dispatch events (fa_ctx_set_kernel_timing). `roofline.traffic` is the HBM bytes
+library's per-dispatch events (fa_ctx_set_kernel_timing) in a second pass of the same steps. `roofline.traffic` is the HBM bytes
 per launch of that kernel from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary
 (profiles/hbm_traffic_prefill_decode.json), scaled by a 1 GiB device-copy calibration.
 """
@@ -88,7 +88,7 @@ def build_prefill(ctx, rng):
                        "flop_per_step": flop}
 
 
-def build_decode(ctx, rng):
+def build_decode(ctx, rng, split=None):
     n, hq, hkv, D, ps = 64, 32, 8, 128, 16
     ctx_lens = rng.integers(512, 8193, n).astype(np.int32)
     pages_per = (ctx_lens + ps - 1) // ps
@@ -105,6 +105,8 @@ def build_decode(ctx, rng):
     q = fa.DeviceBuffer.from_array(ctx, bf16_normal(rng, n * hq * D))
     plan = fa.PagedDecodePlan(ctx, bt, ctx_lens, ps, total, hq, hkv, D,
                               fa.FlatAttentionConfig(True), 10000.0, fa.DTYPE_BF16)
+    if split:
+        plan.set_split(split)
     out = fa.DeviceBuffer(ctx, plan.layout().combined_bytes)
     nbytes = (float(ctx_lens.sum()) * hkv * D * 2 * 2 + n * hq * D * 2 * 2 + n * hq * 4
               + float(pages_per.sum()) * 4)
@@ -310,6 +312,8 @@ def main():
     ap.add_argument("--prefill-policy", type=int, default=-1,
                     help="-1 auto, 0 rotate K on load, 1 pre-rotate K")
     ap.add_argument("--only", choices=["prefill", "decode"], default=None)
+    ap.add_argument("--decode-split", type=int, default=None,
+                    help="tokens per split-K partition of the decode plan (default: automatic)")
     ap.add_argument("--all-configs", action="store_true",
                     help="also time configs[1] (f32 MHA) and configs[4] (chunked paged prefill)")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -338,7 +342,7 @@ def main():
     if args.only in (None, "prefill"):
         ops.append(("prefill",) + build_prefill(ctx, rng))
     if args.only in (None, "decode"):
-        ops.append(("decode",) + build_decode(ctx, rng))
+        ops.append(("decode",) + build_decode(ctx, rng, args.decode_split))
     ctx.synchronize()
 
     tele = {}
@@ -349,7 +353,6 @@ def main():
     ctx.synchronize()
 
     evs = [[ev.create() for _ in range(len(ops) + 1)] for _ in range(args.steps)]
-    ctx.set_kernel_timing(True)
     t_wall = time.perf_counter()
     for s in range(args.steps):
         ev.record(evs[s][0], stream)
@@ -366,7 +369,12 @@ def main():
         ctx.synchronize()
         a.free()
         b.free()
-    # dominant kernel of each op, timed by the library's own events around each dispatch
+    # Dominant kernel of each op: a second timed pass of the same steps with the library's own
+    # events around every dispatch (kept out of the first pass, whose op times they would pad).
+    ctx.set_kernel_timing(True)
+    for _ in range(args.steps):
+        for _, run, _, _ in ops:
+            run()
     kern = {}
     for name, _, _, _ in ops:
         total, n = ctx.kernel_timing(tele[name].kernel_id)

@@ -4,7 +4,7 @@
 // 8-row tiles with a 64-lane tree reduction per key). Math is unchanged: Q rotated at its RoPE
 // position, K pre-rotated in the cache, online softmax over every live token, O and LSE.
 //
-// One wave per (work item = (sequence, split of `split_tokens` keys), kv head, head chunk).
+// One wave runs a list of segments, each a key range of one (sequence, kv head, head chunk).
 // Each wave keeps the (up to 16) query heads of its GQA group in registers so every K/V byte is
 // read from HBM exactly once. Per 16-key step:
 //   - K rows go straight from HBM into MFMA A operands (16-byte loads, no LDS round trip);
@@ -12,9 +12,11 @@
 //   - the per-head online softmax runs on the 16x16 tile (max over keys: 2 lane exchanges);
 //   - P and alpha go through a 1 KiB LDS tile; every lane then FMAs its 8-dim slice of V for
 //     4 keys and all heads (VALU), V loaded with 16-byte row-contiguous loads.
-// Each split writes an un-normalised partial (O, m, l); a second kernel merges the splits:
+// The host cuts the whole (sequence, unit) x key space into equal contiguous ranges, one per
+// resident wave, so every wave streams the same number of bytes. Each segment writes an
+// un-normalised partial (O, m, l); a second kernel merges the partials of a unit:
 //   M = max m_i, L = sum l_i 2^((m_i - M) c), O = sum O_i 2^((m_i - M) c) / L, LSE = M s + ln L.
-// A sequence that fits one split is finalised directly by the split kernel.
+// A unit covered by one segment is finalised directly by the split kernel.
 #include <type_traits>
 
 #include "common.hpp"
@@ -78,20 +80,17 @@ __device__ __forceinline__ void store8(void* dst, const float* x) {
     }
 }
 
-// One work item: (work index w = (sequence, split), kv head, head chunk of <= 16 heads).
-// GT: compile-time head-chunk width (>= group size of the chunk, <= 16).
+// One segment: keys [k0, k1) of sequence s for (kv head, head chunk of <= 16 heads); partial
+// slot `slot` (< 0: write O and LSE). GT: compile-time head-chunk width (>= group size of the
+// chunk, <= 16).
 template <typename T, int DPAD, int GT>
-__device__ __forceinline__ void decode_item(const DecodeKArgs& ka, int w, int kvh, int hc,
-                                            float* p_lds, float* misc_lds) {
+__device__ __forceinline__ void decode_item(const DecodeKArgs& ka, int s, int kvh, int hc, int k0,
+                                            int k1, int slot, float* p_lds, float* misc_lds) {
     constexpr bool F32 = std::is_same<T, float>::value;
     constexpr int EB = DecodeIO<T>::kBytes;
     const DecodeArgs& a = ka.a;
     const int lane = threadIdx.x;
     const int n = lane & 15, g4 = lane >> 4;
-    const int s = a.work_seq[w], split = a.work_split[w];
-    const int ctx = a.ctx_lens[s];
-    const int k0 = split * a.split_tokens;
-    const int k1 = min(ctx, k0 + a.split_tokens);
     const int D = a.head_dim, half = D >> 1;
     const int hl0 = hc * 16;                 // first head of this chunk within the group
     const int nh = min(GT, a.group - hl0);   // heads in this chunk
@@ -314,10 +313,9 @@ __device__ __forceinline__ void decode_item(const DecodeKArgs& ka, int w, int kv
     }
     __syncthreads();
 
-    const int nsplit = a.seq_work_off[s + 1] - a.seq_work_off[s];
     const int hq0 = kvh * a.group + hl0;
     const int dv = 8 * n;
-    if (nsplit == 1) {
+    if (slot < 0) {
         if (g4 == 0 && dv < D) {
 #pragma unroll
             for (int h = 0; h < GT; ++h) {
@@ -338,7 +336,7 @@ __device__ __forceinline__ void decode_item(const DecodeKArgs& ka, int w, int kv
 #pragma unroll
             for (int h = 0; h < GT; ++h) {
                 if (h < nh) {
-                    float* dst = a.part_o + ((int64_t)w * a.q_heads + hq0 + h) * D + dv;
+                    float* dst = a.part_o + ((int64_t)slot * 16 + h) * D + dv;
                     f32x4_t x0 = {o[h][0], o[h][1], o[h][2], o[h][3]};
                     f32x4_t x1 = {o[h][4], o[h][5], o[h][6], o[h][7]};
                     ((f32x4_t*)dst)[0] = x0;
@@ -347,7 +345,7 @@ __device__ __forceinline__ void decode_item(const DecodeKArgs& ka, int w, int kv
             }
         }
         if (g4 == 0 && n < nh) {
-            float* ml = a.part_ml + ((int64_t)w * a.q_heads + hq0 + n) * 2;
+            float* ml = a.part_ml + ((int64_t)slot * 16 + n) * 2;
             ml[0] = m_run;
             ml[1] = l_run;
         }
@@ -378,8 +376,8 @@ __device__ __forceinline__ f32x4_t mfma16x16x16(s16x4_t a, s16x4_t b, f32x4_t c)
 }
 
 template <typename T, int DPAD, int GT>
-__device__ __forceinline__ void decode_mfma_item(const DecodeKArgs& ka, int w, int kvh, int hc,
-                                                 uint8_t* v_lds) {
+__device__ __forceinline__ void decode_mfma_item(const DecodeKArgs& ka, int s, int kvh, int hc,
+                                                 int k0, int k1, int slot, uint8_t* v_lds) {
     using Hf = Half<T>;
     constexpr int NQ = DPAD / 32;        // 16x16x32 k-steps for S
     constexpr int NMB = DPAD / 16;       // 16-dim blocks of O^T
@@ -388,10 +386,6 @@ __device__ __forceinline__ void decode_mfma_item(const DecodeKArgs& ka, int w, i
     const DecodeArgs& a = ka.a;
     const int lane = threadIdx.x;
     const int n = lane & 15, g4 = lane >> 4;
-    const int s = a.work_seq[w], split = a.work_split[w];
-    const int ctx = a.ctx_lens[s];
-    const int k0 = split * a.split_tokens;
-    const int k1 = min(ctx, k0 + a.split_tokens);
     const int D = a.head_dim, half = D >> 1;
     const int hl0 = hc * 16;
     const int nh = min(GT, a.group - hl0);
@@ -542,9 +536,8 @@ __device__ __forceinline__ void decode_mfma_item(const DecodeKArgs& ka, int w, i
     // ---- per-head totals (lane = head n; dims 16mb + 4g4 + i)
     l_run += shfl_xor(l_run, 16);
     l_run += shfl_xor(l_run, 32);
-    const int nsplit = a.seq_work_off[s + 1] - a.seq_work_off[s];
     const bool hv = n < nh;
-    if (nsplit == 1) {
+    if (slot < 0) {
         if (hv) {
             const float inv = 1.0f / l_run;
             uint16_t* orow = (uint16_t*)a.o + ((int64_t)s * a.q_heads + hq0 + n) * D;
@@ -562,42 +555,56 @@ __device__ __forceinline__ void decode_mfma_item(const DecodeKArgs& ka, int w, i
         return;
     }
     if (hv) {
-        float* po = a.part_o + ((int64_t)w * a.q_heads + hq0 + n) * D;
+        float* po = a.part_o + ((int64_t)slot * 16 + n) * D;
 #pragma unroll
         for (int mb = 0; mb < NMB; ++mb) {
             const int d0 = 16 * mb + 4 * g4;
             if (d0 < D) *(f32x4_t*)(po + d0) = oacc[mb];
         }
         if (g4 == 0) {
-            float* ml = a.part_ml + ((int64_t)w * a.q_heads + hq0 + n) * 2;
+            float* ml = a.part_ml + ((int64_t)slot * 16 + n) * 2;
             ml[0] = m_run;
             ml[1] = l_run;
         }
     }
 }
 
+// Minimum resident waves per SIMD the MFMA split kernel is compiled for (caps its registers);
+// 0 leaves the choice to the compiler.
+#ifndef FA_DECODE_WPE
+#define FA_DECODE_WPE 0
+#endif
+#if FA_DECODE_WPE > 0
+#define FA_DECODE_ATTR __attribute__((amdgpu_waves_per_eu(FA_DECODE_WPE, 8)))
+#else
+#define FA_DECODE_ATTR
+#endif
+
 template <typename T, int DPAD, int GT>
-__global__ __launch_bounds__(64) void decode_mfma(DecodeKArgs ka, int n_items, int chunks) {
+__global__ __launch_bounds__(64) FA_DECODE_ATTR void decode_mfma(DecodeKArgs ka, int n_items,
+                                                                int chunks) {
     __shared__ __attribute__((aligned(16))) uint8_t v_lds[16 * (DPAD * 2 + 32)];
-    const int per_w = ka.a.kv_heads * chunks;
-    for (int it = blockIdx.x; it < n_items; it += gridDim.x) {
-        const int w = it / per_w, r = it % per_w;
-        decode_mfma_item<T, DPAD, GT>(ka, w, r / chunks, r % chunks, v_lds);
+    (void)n_items;
+    for (int j = ka.a.wave_off[blockIdx.x]; j < ka.a.wave_off[blockIdx.x + 1]; ++j) {
+        const int* sg = ka.a.seg + 5 * j;
+        const int u = sg[1];
+        decode_mfma_item<T, DPAD, GT>(ka, sg[0], u / chunks, u % chunks, sg[2], sg[3], sg[4], v_lds);
         __syncthreads();
     }
 }
 
-// Persistent split kernel: each one-wave workgroup walks work items with a static stride so
-// the grid is sized to what is resident at once (no partially filled last round). Every wave
-// exits once its stride passes n_items.
+// Persistent split kernel: one one-wave workgroup per resident wave, each running the segment
+// list the host built for it (equal key counts per wave), so no wave idles in a partial round.
 template <typename T, int DPAD, int GT>
 __global__ __launch_bounds__(64) void decode_splitk(DecodeKArgs ka, int n_items, int chunks) {
     __shared__ __attribute__((aligned(16))) float p_lds[16 * 16];
     __shared__ __attribute__((aligned(16))) float misc_lds[3 * 16];
-    const int per_w = ka.a.kv_heads * chunks;
-    for (int it = blockIdx.x; it < n_items; it += gridDim.x) {
-        const int w = it / per_w, r = it % per_w;
-        decode_item<T, DPAD, GT>(ka, w, r / chunks, r % chunks, p_lds, misc_lds);
+    (void)n_items;
+    for (int j = ka.a.wave_off[blockIdx.x]; j < ka.a.wave_off[blockIdx.x + 1]; ++j) {
+        const int* sg = ka.a.seg + 5 * j;
+        const int u = sg[1];
+        decode_item<T, DPAD, GT>(ka, sg[0], u / chunks, u % chunks, sg[2], sg[3], sg[4], p_lds,
+                                 misc_lds);
         __syncthreads();
     }
 }
@@ -607,12 +614,15 @@ template <typename T>
 __global__ __launch_bounds__(64) void decode_combine(DecodeArgs a) {
     constexpr int EB = DecodeIO<T>::kBytes;
     const int hq = blockIdx.x, s = blockIdx.y, lane = threadIdx.x;
-    const int w0 = a.seq_work_off[s], w1 = a.seq_work_off[s + 1];
-    const int ns = w1 - w0;
-    if (ns <= 1) return;  // finalised by the split kernel
+    const int hl = hq % a.group;
+    const int u = (hq / a.group) * a.chunks + hl / 16;
+    const int units = a.kv_heads * a.chunks;
+    const int p0 = a.unit_part[s * units + u], p1 = a.unit_part[s * units + u + 1];
+    const int ns = p1 - p0;
+    if (ns <= 0) return;  // one segment: finalised by the split kernel
     const float c2 = a.scale * kLog2e;
-    const float* ml0 = a.part_ml + ((int64_t)w0 * a.q_heads + hq) * 2;
-    const int64_t step_ml = (int64_t)a.q_heads * 2;
+    const float* ml0 = a.part_ml + ((int64_t)p0 * 16 + hl % 16) * 2;
+    const int64_t step_ml = 16 * 2;
     // split statistics: split j in lane j % 64 (one pass for up to 64 splits)
     float M = -INFINITY;
     for (int j = lane; j < ns; j += 64) M = fmaxf(M, ml0[j * step_ml]);
@@ -624,8 +634,8 @@ __global__ __launch_bounds__(64) void decode_combine(DecodeArgs a) {
     for (int o = 32; o >= 1; o >>= 1) L += shfl_xor(L, o);
     const float inv = 1.0f / L;
     const int d = 2 * lane;
-    const float* po = a.part_o + ((int64_t)w0 * a.q_heads + hq) * a.head_dim + d;
-    const int64_t step_o = (int64_t)a.q_heads * a.head_dim;
+    const float* po = a.part_o + ((int64_t)p0 * 16 + hl % 16) * a.head_dim + d;
+    const int64_t step_o = (int64_t)16 * a.head_dim;
     float acc0 = 0.0f, acc1 = 0.0f;
     for (int jb = 0; jb < ns; jb += 64) {
         // weight of split jb + lane, broadcast by shuffle; O loads unrolled for memory parallelism
@@ -679,52 +689,81 @@ static int persistent_grid(K kernel, int n_items) {
     return n_items < cap ? n_items : cap;
 }
 
+// With `query` set, only reports (in *grid_x) how many one-wave workgroups of the kernel this
+// configuration selects can be resident at once; otherwise launches a.n_waves of them.
 template <typename T, int DPAD, int GT>
-static void launch_one(const DecodeKArgs& ka, int n_items, int chunks, hipStream_t s,
-                       unsigned* grid_x, bool* mfma) {
+static void launch_one(const DecodeKArgs& ka, int chunks, hipStream_t s, unsigned* grid_x,
+                       bool* mfma, bool query) {
     if constexpr (!std::is_same<T, float>::value) {
         if (ka.a.page_size % 16 == 0) {
             static int g = -1;
             if (g < 0) g = persistent_grid(decode_mfma<T, DPAD, GT>, 1 << 30);
-            const int gg = n_items < g ? n_items : g;
-            *grid_x = (unsigned)gg;
             *mfma = true;
-            decode_mfma<T, DPAD, GT><<<gg, 64, 0, s>>>(ka, n_items, chunks);
+            if (query) {
+                *grid_x = (unsigned)g;
+                return;
+            }
+            *grid_x = (unsigned)ka.a.n_waves;
+            decode_mfma<T, DPAD, GT><<<ka.a.n_waves, 64, 0, s>>>(ka, 0, chunks);
             return;
         }
     }
     static int g = -1;
     if (g < 0) g = persistent_grid(decode_splitk<T, DPAD, GT>, 1 << 30);
-    const int gg = n_items < g ? n_items : g;
-    *grid_x = (unsigned)gg;
     *mfma = false;
-    decode_splitk<T, DPAD, GT><<<gg, 64, 0, s>>>(ka, n_items, chunks);
+    if (query) {
+        *grid_x = (unsigned)g;
+        return;
+    }
+    *grid_x = (unsigned)ka.a.n_waves;
+    decode_splitk<T, DPAD, GT><<<ka.a.n_waves, 64, 0, s>>>(ka, 0, chunks);
 }
 
 template <typename T, int DPAD>
-static void launch_gt(const DecodeKArgs& ka, int gt, int n_items, int chunks, hipStream_t s,
-                      unsigned* gx, bool* mfma) {
+static void launch_gt(const DecodeKArgs& ka, int gt, int chunks, hipStream_t s, unsigned* gx,
+                      bool* mfma, bool query) {
     switch (gt) {
-        case 1: launch_one<T, DPAD, 1>(ka, n_items, chunks, s, gx, mfma); break;
-        case 2: launch_one<T, DPAD, 2>(ka, n_items, chunks, s, gx, mfma); break;
-        case 4: launch_one<T, DPAD, 4>(ka, n_items, chunks, s, gx, mfma); break;
-        case 8: launch_one<T, DPAD, 8>(ka, n_items, chunks, s, gx, mfma); break;
-        default: launch_one<T, DPAD, 16>(ka, n_items, chunks, s, gx, mfma); break;
+        case 1: launch_one<T, DPAD, 1>(ka, chunks, s, gx, mfma, query); break;
+        case 2: launch_one<T, DPAD, 2>(ka, chunks, s, gx, mfma, query); break;
+        case 4: launch_one<T, DPAD, 4>(ka, chunks, s, gx, mfma, query); break;
+        case 8: launch_one<T, DPAD, 8>(ka, chunks, s, gx, mfma, query); break;
+        default: launch_one<T, DPAD, 16>(ka, chunks, s, gx, mfma, query); break;
     }
 }
 
 template <typename T>
-static int launch_t(const DecodeKArgs& ka, int dpad, int gt, int n_items, int chunks,
-                    dim3 cgrid, hipStream_t s, unsigned* gx, bool* mfma, void (*between)(void*),
-                    void* user) {
+static void split_t(const DecodeKArgs& ka, int dpad, int gt, int chunks, hipStream_t s,
+                    unsigned* gx, bool* mfma, bool query) {
     switch (dpad) {
-        case 32: launch_gt<T, 32>(ka, gt, n_items, chunks, s, gx, mfma); break;
-        case 64: launch_gt<T, 64>(ka, gt, n_items, chunks, s, gx, mfma); break;
-        default: launch_gt<T, 128>(ka, gt, n_items, chunks, s, gx, mfma); break;
+        case 32: launch_gt<T, 32>(ka, gt, chunks, s, gx, mfma, query); break;
+        case 64: launch_gt<T, 64>(ka, gt, chunks, s, gx, mfma, query); break;
+        default: launch_gt<T, 128>(ka, gt, chunks, s, gx, mfma, query); break;
     }
-    if (between) between(user);
-    decode_combine<T><<<cgrid, 64, 0, s>>>(ka.a);
-    return 2;
+}
+
+static void split_kernel(Dtype dt, const DecodeKArgs& ka, hipStream_t s, unsigned* gx, bool* mfma,
+                         bool query) {
+    const DecodeArgs& a = ka.a;
+    const int dpad = a.head_dim <= 32 ? 32 : (a.head_dim <= 64 ? 64 : 128);
+    const int chunks = (a.group + 15) / 16;
+    const int gmax = a.group >= 16 ? 16 : a.group;
+    const int gt = gmax <= 1 ? 1 : gmax <= 2 ? 2 : gmax <= 4 ? 4 : gmax <= 8 ? 8 : 16;
+    switch (dt) {
+        case Dtype::BF16: split_t<bf16_t>(ka, dpad, gt, chunks, s, gx, mfma, query); break;
+        case Dtype::F16: split_t<f16_t>(ka, dpad, gt, chunks, s, gx, mfma, query); break;
+        default: split_t<float>(ka, dpad, gt, chunks, s, gx, mfma, query); break;
+    }
+}
+
+int decode_resident_waves(Dtype dt, int head_dim, int group, int page_size) {
+    DecodeKArgs ka{};
+    ka.a.head_dim = head_dim;
+    ka.a.group = group;
+    ka.a.page_size = page_size;
+    unsigned g = 0;
+    bool mfma = false;
+    split_kernel(dt, ka, nullptr, &g, &mfma, true);
+    return (int)g;
 }
 
 void launch_decode(Dtype dt, const DecodeArgs& a, hipStream_t s, unsigned grid[3],
@@ -738,24 +777,20 @@ void launch_decode(Dtype dt, const DecodeArgs& a, hipStream_t s, unsigned grid[3
     ka.ps_m = (uint32_t)((((uint64_t)1 << 32) * (((uint64_t)1 << sh) - (uint64_t)a.page_size)) /
                              (uint64_t)a.page_size +
                          1);
-    const int dpad = a.head_dim <= 32 ? 32 : (a.head_dim <= 64 ? 64 : 128);
-    const int chunks = (a.group + 15) / 16;
-    const int gmax = a.group >= 16 ? 16 : a.group;
-    const int gt = gmax <= 1 ? 1 : gmax <= 2 ? 2 : gmax <= 4 ? 4 : gmax <= 8 ? 8 : 16;
-    const int n_items = a.n_work * a.kv_heads * chunks;
-    dim3 cg((unsigned)a.q_heads, (unsigned)a.n_seqs);
     unsigned gx = 0;
-    int nd = 0;
+    split_kernel(dt, ka, s, &gx, mfma, false);
+    if (between) between(user);
+    const dim3 cg((unsigned)a.q_heads, (unsigned)a.n_seqs);
     switch (dt) {
-        case Dtype::BF16: nd = launch_t<bf16_t>(ka, dpad, gt, n_items, chunks, cg, s, &gx, mfma, between, user); break;
-        case Dtype::F16: nd = launch_t<f16_t>(ka, dpad, gt, n_items, chunks, cg, s, &gx, mfma, between, user); break;
-        default: nd = launch_t<float>(ka, dpad, gt, n_items, chunks, cg, s, &gx, mfma, between, user); break;
+        case Dtype::BF16: decode_combine<bf16_t><<<cg, 64, 0, s>>>(a); break;
+        case Dtype::F16: decode_combine<f16_t><<<cg, 64, 0, s>>>(a); break;
+        default: decode_combine<float><<<cg, 64, 0, s>>>(a); break;
     }
     grid[0] = gx;
     grid[1] = 1;
     grid[2] = 1;
     *block = 64;
-    *dispatches = nd;
+    *dispatches = 2;
 }
 
 }  // namespace fa

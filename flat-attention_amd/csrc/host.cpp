@@ -1245,14 +1245,16 @@ struct fa_decode_plan {
     int dtype = 0;
     float scale = 0.0f, theta = 0.0f;
     std::vector<int32_t> ctx_lens;
-    uint64_t split_tokens = 0;
-    uint64_t n_work = 0;
+    uint64_t split_req = 0;     // requested segment length (0 = equal ranges per wave)
+    uint64_t split_tokens = 0;  // longest segment of the current work list
+    uint64_t n_work = 0;        // segments
+    uint64_t n_waves = 0, n_slots = 0, units = 0;
     uint64_t max_pos = 0;
     // device
     int32_t* d_bt = nullptr;
     int32_t* d_ctx = nullptr;
     int32_t* d_qpos = nullptr;
-    int32_t* d_work = nullptr;  // [work_seq | work_split | seq_work_off]
+    int32_t* d_work = nullptr;  // [seg (5 per segment) | wave_off | unit_part]
     float* d_part = nullptr;    // partial O then (m, l)
     uint64_t part_bytes = 0;
     uint64_t work_cap = 0;
@@ -1266,34 +1268,101 @@ uint64_t max_split_tokens(uint64_t page_size) {
     return std::max<uint64_t>(16, t);
 }
 
-uint64_t auto_split(const fa_decode_plan* p) {
-    uint64_t total = 0;
-    for (int32_t c : p->ctx_lens) total += (uint64_t)c;
-    const uint64_t chunks = (p->q_heads / p->kv_heads + 15) / 16;
-    // Aim for ~8192 resident waves (32 per CU) so every CU streams several pages at once.
-    uint64_t st = total * p->kv_heads * chunks / 8192;
-    st = std::max<uint64_t>(64, std::min<uint64_t>(st, 4096));
-    st = (st + 15) / 16 * 16;
-    return std::min(st, max_split_tokens(p->page_size));
-}
-
+// Work list of a decode plan. A unit is (kv head, chunk of <= 16 query heads); the key space
+// of every (sequence, unit) is laid end to end, each unit padded to a multiple of 16 keys, and
+// cut into segments:
+//  * automatic (split_req == 0): one equal range of whole 16-key steps per resident wave, so
+//    every wave streams the same number of K/V bytes (segments also end at unit boundaries and
+//    after max_split_tokens keys);
+//  * split_req = x: every unit cut every x keys, segments dealt to the resident waves in turn.
+// Units covered by one segment are finalised by the split kernel; the others get one partial
+// slot per segment, merged by the combine kernel.
 int build_work(fa_decode_plan* p) {
     fa_ctx* ctx = p->ctx;
-    std::vector<int32_t> wseq, wsplit, off(p->n_seqs + 1, 0);
-    for (uint64_t s = 0; s < p->n_seqs; ++s) {
-        const uint64_t n = ((uint64_t)p->ctx_lens[s] + p->split_tokens - 1) / p->split_tokens;
-        off[s] = (int32_t)wseq.size();
-        for (uint64_t j = 0; j < n; ++j) {
-            wseq.push_back((int32_t)s);
-            wsplit.push_back((int32_t)j);
+    const uint64_t chunks = (p->q_heads / p->kv_heads + 15) / 16;
+    const uint64_t units = p->kv_heads * chunks;
+    const uint64_t maxseg = max_split_tokens(p->page_size);
+    const int resident = fa::decode_resident_waves(
+        (Dtype)p->dtype, (int)p->head_dim, (int)(p->q_heads / p->kv_heads), (int)p->page_size);
+    const uint64_t G = (uint64_t)std::max(1, resident);
+    struct Seg { int32_t s, u, k0, k1, slot; uint64_t wave; };
+    std::vector<Seg> segs;
+    uint64_t total = 0;
+    for (int32_t c : p->ctx_lens) total += ((uint64_t)c + 15) / 16 * 16 * units;
+    uint64_t longest = 0;
+    if (p->split_req == 0) {
+        const uint64_t L = std::max<uint64_t>(16, ((total + G - 1) / G + 15) / 16 * 16);
+        uint64_t pos = 0;
+        for (uint64_t s = 0; s < p->n_seqs; ++s) {
+            const uint64_t c = (uint64_t)p->ctx_lens[s];
+            const uint64_t cpad = (c + 15) / 16 * 16;
+            for (uint64_t u = 0; u < units; ++u) {
+                for (uint64_t t = 0; t < cpad;) {
+                    const uint64_t wave = (pos + t) / L;
+                    const uint64_t wave_end = (wave + 1) * L - pos;  // unit-relative
+                    const uint64_t e = std::min(std::min(cpad, wave_end), t + maxseg);
+                    segs.push_back({(int32_t)s, (int32_t)u, (int32_t)t,
+                                    (int32_t)std::min(c, e), -1, wave});
+                    longest = std::max(longest, e - t);
+                    t = e;
+                }
+                pos += cpad;
+            }
+        }
+    } else {
+        uint64_t i = 0;
+        for (uint64_t s = 0; s < p->n_seqs; ++s) {
+            const uint64_t c = (uint64_t)p->ctx_lens[s];
+            for (uint64_t u = 0; u < units; ++u)
+                for (uint64_t t = 0; t < c; t += p->split_req, ++i) {
+                    const uint64_t e = std::min(c, t + p->split_req);
+                    segs.push_back({(int32_t)s, (int32_t)u, (int32_t)t, (int32_t)e, -1, i % G});
+                    longest = std::max(longest, e - t);
+                }
         }
     }
-    off[p->n_seqs] = (int32_t)wseq.size();
-    p->n_work = wseq.size();
-    if (p->n_work > kI32)
-        return fail(FA_ERR_DISPATCH_LIMIT, "paged decode requires %llu workgroups",
-                    (unsigned long long)p->n_work);
-    const uint64_t need_work = 2 * p->n_work + p->n_seqs + 1;
+    if (segs.size() > kI32)
+        return fail(FA_ERR_DISPATCH_LIMIT, "paged decode requires %llu segments",
+                    (unsigned long long)segs.size());
+    // partial slots: units with more than one segment
+    std::vector<int32_t> unit_part(p->n_seqs * units + 1, 0);
+    {
+        size_t i = 0;
+        int32_t slot = 0;
+        for (uint64_t su = 0; su < p->n_seqs * units; ++su) {
+            unit_part[su] = slot;
+            size_t j = i;
+            while (j < segs.size() && (uint64_t)segs[j].s * units + segs[j].u == su) ++j;
+            if (j - i > 1)
+                for (size_t k = i; k < j; ++k) segs[k].slot = slot++;
+            i = j;
+        }
+        unit_part[p->n_seqs * units] = slot;
+        p->n_slots = (uint64_t)slot;
+    }
+    // per-wave lists (segments are generated in increasing wave order in the automatic mode)
+    uint64_t n_waves = 0;
+    for (const Seg& g : segs) n_waves = std::max(n_waves, g.wave + 1);
+    std::vector<int32_t> wave_off(n_waves + 1, 0);
+    for (const Seg& g : segs) wave_off[g.wave + 1]++;
+    for (uint64_t w = 0; w < n_waves; ++w) wave_off[w + 1] += wave_off[w];
+    std::vector<int32_t> seg_arr(5 * segs.size());
+    {
+        std::vector<int32_t> fill(wave_off.begin(), wave_off.end() - 1);
+        for (const Seg& g : segs) {
+            const int32_t at = fill[g.wave]++;
+            seg_arr[5 * at + 0] = g.s;
+            seg_arr[5 * at + 1] = g.u;
+            seg_arr[5 * at + 2] = g.k0;
+            seg_arr[5 * at + 3] = g.k1;
+            seg_arr[5 * at + 4] = g.slot;
+        }
+    }
+    p->n_work = segs.size();
+    p->n_waves = n_waves;
+    p->units = units;
+    p->split_tokens = longest;
+    const uint64_t need_work = seg_arr.size() + wave_off.size() + unit_part.size();
     if (p->work_cap < need_work) {
         if (p->d_work) HIP_TRY(hipFree(p->d_work));
         p->d_work = nullptr;
@@ -1302,11 +1371,11 @@ int build_work(fa_decode_plan* p) {
     }
     std::vector<int32_t> all;
     all.reserve(need_work);
-    all.insert(all.end(), wseq.begin(), wseq.end());
-    all.insert(all.end(), wsplit.begin(), wsplit.end());
-    all.insert(all.end(), off.begin(), off.end());
+    all.insert(all.end(), seg_arr.begin(), seg_arr.end());
+    all.insert(all.end(), wave_off.begin(), wave_off.end());
+    all.insert(all.end(), unit_part.begin(), unit_part.end());
     HIP_TRY(hipMemcpy(p->d_work, all.data(), need_work * 4, hipMemcpyHostToDevice));
-    const uint64_t part = p->n_work * p->q_heads * (p->head_dim + 2) * 4;
+    const uint64_t part = std::max<uint64_t>(1, p->n_slots) * 16 * (p->head_dim + 2) * 4;
     if (p->part_bytes < part) {
         if (p->d_part) HIP_TRY(hipFree(p->d_part));
         p->d_part = nullptr;
@@ -1432,7 +1501,7 @@ int fa_paged_decode_prepare(fa_ctx* ctx, const int32_t* block_tables, uint64_t m
     if (!rc && hipMemcpy(p->d_qpos, qpos.data(), n_seqs * 4, hipMemcpyHostToDevice))
         rc = fail(FA_ERR_HIP, "query position upload failed");
     if (!rc) {
-        p->split_tokens = auto_split(p);
+        p->split_req = 0;
         rc = build_work(p);
     }
     if (rc) {
@@ -1454,7 +1523,7 @@ int fa_paged_decode_plan_set_split(fa_ctx* ctx, fa_decode_plan* p, uint64_t spli
                     (unsigned long long)split_tokens, (unsigned long long)p->page_size);
     if (int rc = set_device(ctx)) return rc;
     HIP_TRY(hipStreamSynchronize(ctx->stream));
-    p->split_tokens = split_tokens ? split_tokens : auto_split(p);
+    p->split_req = split_tokens;
     if (int rc = build_work(p)) return rc;
     return ok();
 }
@@ -1502,23 +1571,23 @@ int fa_paged_decode_launch(fa_ctx* ctx, const fa_decode_plan* p, const void* q, 
     a.block_tables = p->d_bt;
     a.ctx_lens = p->d_ctx;
     a.q_positions = p->d_qpos;
-    a.work_seq = p->d_work;
-    a.work_split = p->d_work + p->n_work;
-    a.seq_work_off = p->d_work + 2 * p->n_work;
+    a.seg = p->d_work;
+    a.wave_off = p->d_work + 5 * p->n_work;
+    a.unit_part = a.wave_off + p->n_waves + 1;
     a.part_o = p->d_part;
-    a.part_ml = p->d_part + p->n_work * p->q_heads * p->head_dim;
-    if (!a.part_o || !a.block_tables || !a.work_seq)
+    a.part_ml = p->d_part + std::max<uint64_t>(1, p->n_slots) * 16 * p->head_dim;
+    if (!a.part_o || !a.block_tables || !a.seg)
         return fail(FA_ERR_NULL_ARGUMENT, "decode plan is missing device state");
     a.rope_table = table;
     a.n_seqs = (int)p->n_seqs;
-    a.n_work = (int)p->n_work;
+    a.n_waves = (int)p->n_waves;
+    a.chunks = (int)p->units / (int)p->kv_heads;
     a.q_heads = (int)p->q_heads;
     a.kv_heads = (int)p->kv_heads;
     a.group = (int)(p->q_heads / p->kv_heads);
     a.head_dim = (int)p->head_dim;
     a.page_size = (int)p->page_size;
     a.bt_stride = (int)p->max_pages;
-    a.split_tokens = (int)p->split_tokens;
     a.scale = p->scale;
     unsigned grid[3], block;
     int dispatches = 0;

@@ -55,18 +55,25 @@ struct DecodeArgs {
     const int* block_tables;  // [n_seqs, bt_stride]
     const int* ctx_lens;      // [n_seqs]
     const int* q_positions;   // [n_seqs] RoPE position of each query
-    const int* work_seq;      // [n_work] sequence of each work item
-    const int* work_split;    // [n_work] split index within its sequence
-    const int* seq_work_off;  // [n_seqs+1] first work item of each sequence
-    float* part_o;            // [n_work, q_heads, head_dim] un-normalised partial O
-    float* part_ml;           // [n_work, q_heads, 2] partial (max, sum)
+    // Work: a "unit" is (kv head, chunk of <= 16 query heads of its group), u = kvh*chunks + hc.
+    // A segment is a key range [k0, k1) of one (sequence, unit); it writes partial slot `slot`,
+    // or O and LSE directly when slot < 0 (the segment covers its whole unit).
+    const int* seg;        // [n_seg, 5]: seq, unit, k0, k1, slot
+    const int* wave_off;   // [n_waves+1]: wave b runs segments wave_off[b] .. wave_off[b+1]-1
+    const int* unit_part;  // [n_seqs*units+1]: slots of (s, u) are unit_part[s*units+u] .. next-1
+    float* part_o;         // [slots, 16, head_dim] un-normalised partial O
+    float* part_ml;        // [slots, 16, 2] partial (max, sum)
     const float2* rope_table;
-    int n_seqs, n_work, q_heads, kv_heads, group, head_dim;
-    int page_size, bt_stride, split_tokens;
+    int n_seqs, n_waves, q_heads, kv_heads, group, head_dim, chunks;
+    int page_size, bt_stride;
     float scale;
 };
 
-// Launches the split kernel then the combine; `between(user)` (if set) runs on the host between
+// Number of one-wave workgroups of the split kernel that launch_decode keeps resident at once
+// for this configuration (the work lists are built for exactly this many waves or fewer).
+int decode_resident_waves(Dtype dt, int head_dim, int group, int page_size);
+
+// Launches the split kernel (a.n_waves workgroups) then the combine; `between(user)` (if set) runs on the host between
 // the two launches. *mfma tells whether the MFMA split kernel was chosen.
 void launch_decode(Dtype dt, const DecodeArgs& a, hipStream_t s, unsigned grid[3],
                    unsigned* block, int* dispatches, bool* mfma, void (*between)(void*),
