@@ -12,7 +12,8 @@ decode GB/s (algorithmic bytes: K+V of every live token once, plus Q, O, LSE, bl
 is reported beside it with its own roofline. `value` and each op's rate use the op's whole
 duration (the prefill op includes the K pre-rotation pass); each `roofline.achieved` divides the
 same algorithmic work by the average duration of the op's dominant kernel alone, timed by the
-library's per-dispatch events (fa_ctx_set_kernel_timing) in a second pass of the same steps. `roofline.traffic` is the HBM bytes
+library's per-dispatch events (fa_ctx_set_kernel_timing) in a second pass of the same steps.
+`roofline.traffic` is the HBM bytes
 per launch of that kernel from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary
 (profiles/hbm_traffic_prefill_decode.json), scaled by a 1 GiB device-copy calibration.
 """

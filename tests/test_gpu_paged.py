@@ -334,6 +334,25 @@ def test_cfg5_chunked_prefill_over_paged_cache(hip):
 
 
 @pytest.mark.gpu
+def test_mixed_lengths_equal_work_partition_matches_oracle(hip):
+    """Equal-work segment lists: 40 sequences from 1 to 3000 tokens, so some (sequence, head)
+    units are finalised by one segment, others merge several partials, and one wave's range
+    crosses sequence and head boundaries. Every row is checked against the oracle."""
+    rng = np.random.default_rng(21)
+    ctx_lens = list(rng.integers(1, 3001, 40))
+    ctx_lens[:4] = [1, 15, 16, 17]
+    ps, hq, hkv, D = 16, 32, 8, 128
+    bt, kp, vp, total = _make_pool(rng, ctx_lens, ps, hkv, D, bf16_round, seed=31)
+    q = bf16_round(normal(len(ctx_lens) * hq * D, 33))
+    o, lse, plan = _decode(hip, bt, ctx_lens, kp, vp, total, ps, hq, hkv, D, q, fa.DTYPE_BF16)
+    info = plan.info()
+    assert info["work_items"] > len(ctx_lens) * hkv  # some units are split
+    eo, el = oracle.paged_decode(q, kp, vp, total, ps, bt, ctx_lens, hq, hkv, D, True, 1e4)
+    assert_close("O", o, eo, H16_ATOL, 0.0)
+    assert_close("LSE", lse, el, H16_ATOL, 0.0)
+
+
+@pytest.mark.gpu
 def test_kernel_timing_and_mfma_variant_telemetry(hip):
     """bf16 KV with page_size % 16 == 0 selects the MFMA split kernel; per-kernel timing counts
     one split and one combine dispatch per launch and clears when re-enabled."""
