@@ -375,16 +375,31 @@ __device__ __forceinline__ f32x4_t mfma16x16x16(s16x4_t a, s16x4_t b, f32x4_t c)
     }
 }
 
-template <typename T, int DPAD, int GT>
+// Register ring depth of the MFMA split kernel (16-key steps in flight per wave).
+#ifndef FA_DECODE_NS
+#define FA_DECODE_NS 2
+#endif
+
+// Orders this wave's LDS accesses around a reuse of its private tile. LDS operations of one
+// wave execute in issue order, so only the compiler has to be kept from moving them.
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// WSYNC: v_lds is private to this wave (multi-wave workgroups): its reuse needs no workgroup
+// barrier; the workgroup still meets once per 16-key step.
+template <typename T, int DPAD, int GT, bool WSYNC>
 __device__ __forceinline__ void decode_mfma_item(const DecodeKArgs& ka, int s, int kvh, int hc,
                                                  int k0, int k1, int slot, uint8_t* v_lds) {
     using Hf = Half<T>;
     constexpr int NQ = DPAD / 32;        // 16x16x32 k-steps for S
     constexpr int NMB = DPAD / 16;       // 16-dim blocks of O^T
     constexpr int VROWB = DPAD * 2 + 32; // padded V row in LDS (bytes)
-    constexpr int NS = 3;                // register ring depth (steps of 16 keys)
+    constexpr int NS = FA_DECODE_NS;     // register ring depth (steps of 16 keys)
     const DecodeArgs& a = ka.a;
-    const int lane = threadIdx.x;
+    const int lane = threadIdx.x & 63;
     const int n = lane & 15, g4 = lane >> 4;
     const int D = a.head_dim, half = D >> 1;
     const int hl0 = hc * 16;
@@ -482,6 +497,9 @@ __device__ __forceinline__ void decode_mfma_item(const DecodeKArgs& ka, int s, i
         for (int t = 0; t < NS; ++t) {
             const int key0 = base + 16 * t;
             const bool live = key0 < k1;  // uniform
+            // Head-grouped workgroups: one barrier per step keeps the waves (kv heads) of a
+            // token row within a step of each other, so a page is streamed by one CU at once.
+            if constexpr (WSYNC) __syncthreads();
             f32x4_t sc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int c = 0; c < NQ; ++c) sc = Hf::mfma16(kbuf[t][c], qop[c], sc);
@@ -519,7 +537,7 @@ __device__ __forceinline__ void decode_mfma_item(const DecodeKArgs& ka, int s, i
                 }
                 const u32x2_t pw = {Hf::pack(p[0], p[1]), Hf::pack(p[2], p[3])};
                 const s16x4_t pb = __builtin_bit_cast(s16x4_t, pw);
-                __syncthreads();
+                if constexpr (WSYNC) wave_lds_sync(); else __syncthreads();
 #pragma unroll
                 for (int mb = 0; mb < NMB; ++mb) {
                     typedef __attribute__((address_space(3))) s16x4_t lds_s16x4_t;
@@ -527,7 +545,7 @@ __device__ __forceinline__ void decode_mfma_item(const DecodeKArgs& ka, int s, i
                         __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(v_rd + mb * 32));
                     oacc[mb] = mfma16x16x16<T>(av, pb, oacc[mb]);
                 }
-                __syncthreads();
+                if constexpr (WSYNC) wave_lds_sync(); else __syncthreads();
             }
             load_v(vbuf[t], key0 + 16 * NS);
         }
@@ -588,8 +606,27 @@ __global__ __launch_bounds__(64) FA_DECODE_ATTR void decode_mfma(DecodeKArgs ka,
     for (int j = ka.a.wave_off[blockIdx.x]; j < ka.a.wave_off[blockIdx.x + 1]; ++j) {
         const int* sg = ka.a.seg + 5 * j;
         const int u = sg[1];
-        decode_mfma_item<T, DPAD, GT>(ka, sg[0], u / chunks, u % chunks, sg[2], sg[3], sg[4], v_lds);
+        decode_mfma_item<T, DPAD, GT, false>(ka, sg[0], u / chunks, u % chunks, sg[2], sg[3], sg[4], v_lds);
         __syncthreads();
+    }
+}
+
+// Head-grouped variant: one workgroup of a.grouped (= kv_heads * chunks <= 8) waves per
+// resident slot, wave w serving unit w. All waves of a workgroup run the same segment list
+// (sequence, key range) in step, so the K/V rows of a page (every kv head of a token side by
+// side, 2 KiB at Hkv 8 x D 128 bf16) are streamed by one CU at about the same time: +9 % HBM
+// throughput over one-wave workgroups that each read 256-byte slices of the rows. Segment fields: seq, slot stride, k0, k1, first
+// slot (< 0: finalise directly); unit w writes partial slot first + w * stride.
+template <typename T, int DPAD, int GT>
+__global__ __launch_bounds__(512) void decode_mfma_grouped(DecodeKArgs ka, int chunks) {
+    __shared__ __attribute__((aligned(16))) uint8_t v_lds[8][16 * (DPAD * 2 + 32)];
+    const int wave = threadIdx.x >> 6;
+    for (int j = ka.a.wave_off[blockIdx.x]; j < ka.a.wave_off[blockIdx.x + 1]; ++j) {
+        const int* sg = ka.a.seg + 5 * j;
+        const int slot = sg[4] < 0 ? -1 : sg[4] + wave * sg[1];
+        decode_mfma_item<T, DPAD, GT, true>(ka, sg[0], wave / chunks, wave % chunks, sg[2], sg[3],
+                                            slot, v_lds[wave]);
+        wave_lds_sync();
     }
 }
 
@@ -695,6 +732,25 @@ template <typename T, int DPAD, int GT>
 static void launch_one(const DecodeKArgs& ka, int chunks, hipStream_t s, unsigned* grid_x,
                        bool* mfma, bool query) {
     if constexpr (!std::is_same<T, float>::value) {
+        if (ka.a.page_size % 16 == 0 && ka.a.grouped > 0) {
+            const int threads = 64 * ka.a.grouped;
+            *mfma = true;
+            if (query) {
+                int per_cu = 0;
+                if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                        &per_cu, decode_mfma_grouped<T, DPAD, GT>, threads, 0) != hipSuccess ||
+                    per_cu <= 0)
+                    per_cu = 1;
+                int dev = 0, cus = 256;
+                if (hipGetDevice(&dev) == hipSuccess)
+                    (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+                *grid_x = (unsigned)(per_cu * cus);
+                return;
+            }
+            *grid_x = (unsigned)ka.a.n_waves;
+            decode_mfma_grouped<T, DPAD, GT><<<ka.a.n_waves, threads, 0, s>>>(ka, chunks);
+            return;
+        }
         if (ka.a.page_size % 16 == 0) {
             static int g = -1;
             if (g < 0) g = persistent_grid(decode_mfma<T, DPAD, GT>, 1 << 30);
@@ -755,8 +811,9 @@ static void split_kernel(Dtype dt, const DecodeKArgs& ka, hipStream_t s, unsigne
     }
 }
 
-int decode_resident_waves(Dtype dt, int head_dim, int group, int page_size) {
+int decode_resident_waves(Dtype dt, int head_dim, int group, int page_size, int grouped) {
     DecodeKArgs ka{};
+    ka.a.grouped = grouped;
     ka.a.head_dim = head_dim;
     ka.a.group = group;
     ka.a.page_size = page_size;
@@ -789,7 +846,7 @@ void launch_decode(Dtype dt, const DecodeArgs& a, hipStream_t s, unsigned grid[3
     grid[0] = gx;
     grid[1] = 1;
     grid[2] = 1;
-    *block = 64;
+    *block = a.grouped > 0 && dt != Dtype::F32 && a.page_size % 16 == 0 ? 64 * a.grouped : 64;
     *dispatches = 2;
 }
 

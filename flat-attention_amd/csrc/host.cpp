@@ -1249,6 +1249,7 @@ struct fa_decode_plan {
     uint64_t split_tokens = 0;  // longest segment of the current work list
     uint64_t n_work = 0;        // segments
     uint64_t n_waves = 0, n_slots = 0, units = 0;
+    int grouped = 0;  // > 0: head-grouped workgroups of this many waves (one per unit)
     uint64_t max_pos = 0;
     // device
     int32_t* d_bt = nullptr;
@@ -1282,14 +1283,59 @@ int build_work(fa_decode_plan* p) {
     const uint64_t chunks = (p->q_heads / p->kv_heads + 15) / 16;
     const uint64_t units = p->kv_heads * chunks;
     const uint64_t maxseg = max_split_tokens(p->page_size);
+    // Head-grouped mode (16-bit KV, page_size % 16 == 0, automatic split, <= 8 units): one
+    // workgroup of `units` waves per segment list, every wave on the same key ranges.
+    const char* env_grouped = std::getenv("FA_DECODE_GROUPED");
+    const bool want_grouped = !(env_grouped && env_grouped[0] == '0');
+    p->grouped = (want_grouped && p->split_req == 0 && p->dtype != (int)Dtype::F32 &&
+                  p->page_size % 16 == 0 && units <= 8)
+                     ? (int)units
+                     : 0;
     const int resident = fa::decode_resident_waves(
-        (Dtype)p->dtype, (int)p->head_dim, (int)(p->q_heads / p->kv_heads), (int)p->page_size);
+        (Dtype)p->dtype, (int)p->head_dim, (int)(p->q_heads / p->kv_heads), (int)p->page_size,
+        p->grouped);
     const uint64_t G = (uint64_t)std::max(1, resident);
     struct Seg { int32_t s, u, k0, k1, slot; uint64_t wave; };
     std::vector<Seg> segs;
+    std::vector<int32_t> unit_part(p->n_seqs * units + 1, 0);
+    uint64_t longest = 0;
+    if (p->grouped > 0) {
+        uint64_t total = 0;
+        for (int32_t c : p->ctx_lens) total += ((uint64_t)c + 15) / 16 * 16;
+        const uint64_t L = std::max<uint64_t>(16, ((total + G - 1) / G + 15) / 16 * 16);
+        uint64_t pos = 0;
+        int32_t slot = 0;
+        for (uint64_t s = 0; s < p->n_seqs; ++s) {
+            const uint64_t c = (uint64_t)p->ctx_lens[s];
+            const uint64_t cpad = (c + 15) / 16 * 16;
+            const size_t first = segs.size();
+            for (uint64_t t = 0; t < cpad;) {
+                const uint64_t wave = (pos + t) / L;
+                const uint64_t e = std::min(std::min(cpad, (wave + 1) * L - pos), t + maxseg);
+                segs.push_back({(int32_t)s, 0, (int32_t)t, (int32_t)std::min(c, e), -1, wave});
+                longest = std::max(longest, e - t);
+                t = e;
+            }
+            pos += cpad;
+            const int32_t nseg = (int32_t)(segs.size() - first);
+            for (uint64_t u = 0; u < units; ++u)
+                unit_part[s * units + u] = nseg > 1 ? slot + (int32_t)u * nseg : slot;
+            if (nseg > 1) {
+                for (int32_t j = 0; j < nseg; ++j) {
+                    segs[first + j].u = nseg;
+                    segs[first + j].slot = slot + j;
+                }
+                slot += (int32_t)units * nseg;
+            }
+        }
+        unit_part[p->n_seqs * units] = slot;
+        p->n_slots = (uint64_t)slot;
+        if (segs.size() > kI32)
+            return fail(FA_ERR_DISPATCH_LIMIT, "paged decode requires %llu segments",
+                        (unsigned long long)segs.size());
+    } else {
     uint64_t total = 0;
     for (int32_t c : p->ctx_lens) total += ((uint64_t)c + 15) / 16 * 16 * units;
-    uint64_t longest = 0;
     if (p->split_req == 0) {
         const uint64_t L = std::max<uint64_t>(16, ((total + G - 1) / G + 15) / 16 * 16);
         uint64_t pos = 0;
@@ -1325,7 +1371,6 @@ int build_work(fa_decode_plan* p) {
         return fail(FA_ERR_DISPATCH_LIMIT, "paged decode requires %llu segments",
                     (unsigned long long)segs.size());
     // partial slots: units with more than one segment
-    std::vector<int32_t> unit_part(p->n_seqs * units + 1, 0);
     {
         size_t i = 0;
         int32_t slot = 0;
@@ -1340,6 +1385,7 @@ int build_work(fa_decode_plan* p) {
         unit_part[p->n_seqs * units] = slot;
         p->n_slots = (uint64_t)slot;
     }
+    }  // one-wave mode
     // per-wave lists (segments are generated in increasing wave order in the automatic mode)
     uint64_t n_waves = 0;
     for (const Seg& g : segs) n_waves = std::max(n_waves, g.wave + 1);
@@ -1532,7 +1578,8 @@ int fa_paged_decode_plan_info(const fa_decode_plan* p, uint64_t* split_tokens,
                               uint64_t* work_items, uint64_t* workspace_bytes) {
     if (!p) return fail(FA_ERR_NULL_ARGUMENT, "plan is null");
     if (split_tokens) *split_tokens = p->split_tokens;
-    if (work_items) *work_items = p->n_work;
+    // one work item = one (segment, unit) pair; a head-grouped segment serves every unit
+    if (work_items) *work_items = p->grouped > 0 ? p->n_work * p->units : p->n_work;
     if (workspace_bytes) *workspace_bytes = p->part_bytes;
     return ok();
 }
@@ -1589,6 +1636,7 @@ int fa_paged_decode_launch(fa_ctx* ctx, const fa_decode_plan* p, const void* q, 
     a.page_size = (int)p->page_size;
     a.bt_stride = (int)p->max_pages;
     a.scale = p->scale;
+    a.grouped = p->grouped;
     unsigned grid[3], block;
     int dispatches = 0;
     bool mfma = false;

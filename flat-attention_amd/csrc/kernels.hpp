@@ -67,11 +67,15 @@ struct DecodeArgs {
     int n_seqs, n_waves, q_heads, kv_heads, group, head_dim, chunks;
     int page_size, bt_stride;
     float scale;
+    // > 0: head-grouped MFMA split kernel, workgroups of `grouped` waves (one per unit) sharing
+    // one segment list; seg[1] is then the partial-slot stride between units.
+    int grouped;
 };
 
-// Number of one-wave workgroups of the split kernel that launch_decode keeps resident at once
-// for this configuration (the work lists are built for exactly this many waves or fewer).
-int decode_resident_waves(Dtype dt, int head_dim, int group, int page_size);
+// Number of workgroups of the split kernel that launch_decode keeps resident at once for this
+// configuration (one-wave workgroups, or `grouped`-wave ones when grouped > 0); the work lists
+// are built for exactly this many workgroups or fewer.
+int decode_resident_waves(Dtype dt, int head_dim, int group, int page_size, int grouped);
 
 // Launches the split kernel (a.n_waves workgroups) then the combine; `between(user)` (if set) runs on the host between
 // the two launches. *mfma tells whether the MFMA split kernel was chosen.

@@ -306,7 +306,8 @@ int fa_paged_decode_launch(fa_ctx* ctx, const fa_decode_plan* plan, const void* 
                            size_t q_bytes, const void* k_pool, const void* v_pool,
                            size_t pool_bytes, void* out_lse, size_t out_bytes);
 int fa_paged_decode_plan_destroy(fa_decode_plan* plan);
-/* Number of split-K partitions per sequence the plan uses (tokens per split). */
+/* Longest split-K segment (tokens), number of (segment, unit) work items, where a unit is
+ * (kv head, chunk of <= 16 query heads), and the partials workspace in bytes. */
 int fa_paged_decode_plan_info(const fa_decode_plan* plan, uint64_t* split_tokens,
                               uint64_t* work_items, uint64_t* workspace_bytes);
 /* Override tokens per split (multiple of 16; 0 = automatic) before launch. Tests use this to

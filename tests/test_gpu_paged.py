@@ -334,10 +334,14 @@ def test_cfg5_chunked_prefill_over_paged_cache(hip):
 
 
 @pytest.mark.gpu
-def test_mixed_lengths_equal_work_partition_matches_oracle(hip):
+@pytest.mark.parametrize("grouped", ["1", "0"])
+def test_mixed_lengths_equal_work_partition_matches_oracle(hip, monkeypatch, grouped):
     """Equal-work segment lists: 40 sequences from 1 to 3000 tokens, so some (sequence, head)
-    units are finalised by one segment, others merge several partials, and one wave's range
-    crosses sequence and head boundaries. Every row is checked against the oracle."""
+    units are finalised by one segment, others merge several partials, and one workgroup's range
+    crosses sequence (and, with one-wave workgroups, head) boundaries. Both work layouts (the
+    default head-grouped workgroups, and one-wave workgroups via FA_DECODE_GROUPED=0) are
+    checked row by row against the oracle."""
+    monkeypatch.setenv("FA_DECODE_GROUPED", grouped)
     rng = np.random.default_rng(21)
     ctx_lens = list(rng.integers(1, 3001, 40))
     ctx_lens[:4] = [1, 15, 16, 17]
