@@ -307,8 +307,10 @@ def _traffic(traffic, name):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    # The GPU's clocks take a few tens of milliseconds of sustained work to settle: 200 untimed
+    # steps (~0.1 s) precede 100 timed ones, so the figures are steady-state throughput.
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--prefill-policy", type=int, default=-1,
                     help="-1 auto, 0 rotate K on load, 1 pre-rotate K")

@@ -52,6 +52,13 @@ template <> struct Half<bf16_t> {
     __device__ __forceinline__ static float lo(uint32_t w) { return bf16_lo(w); }
     __device__ __forceinline__ static float hi(uint32_t w) { return bf16_hi(w); }
     __device__ __forceinline__ static uint32_t pack(float a, float b) { return pack_bf16(a, b); }
+    // acc + lo(w) + hi(w) in f32 (one v_dot2 against (1, 1)).
+    __device__ __forceinline__ static float sum2(uint32_t w, float acc) {
+        typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+        return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w),
+                                               __builtin_bit_cast(bf16x2_t, 0x3f803f80u), acc,
+                                               false);
+    }
     // D[32x32] += A[32x16] * B[16x32]; A, B hold 8 values per lane.
     __device__ __forceinline__ static f32x16_t mfma32(u32x4_t a, u32x4_t b, f32x16_t c) {
         return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
@@ -69,6 +76,11 @@ template <> struct Half<f16_t> {
     __device__ __forceinline__ static float lo(uint32_t w) { return f16_lo(w); }
     __device__ __forceinline__ static float hi(uint32_t w) { return f16_hi(w); }
     __device__ __forceinline__ static uint32_t pack(float a, float b) { return pack_f16(a, b); }
+    __device__ __forceinline__ static float sum2(uint32_t w, float acc) {
+        typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+        return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, w),
+                                      __builtin_bit_cast(f16x2_t, 0x3c003c00u), acc, false);
+    }
     __device__ __forceinline__ static f32x16_t mfma32(u32x4_t a, u32x4_t b, f32x16_t c) {
         return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a),
                                                       __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);

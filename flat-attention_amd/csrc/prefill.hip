@@ -56,6 +56,32 @@ __device__ __forceinline__ int64_t kv_row_offset(const PrefillKArgs& ka, int b, 
     }
 }
 
+// 16 bytes per lane from a buffer straight into LDS: lane i writes LDS byte address
+// lds + 16 i (buffer_load_dwordx4 ... lds, M0 = lds). Out-of-range offsets write zeros and
+// fetch nothing. Issued from inline assembly so the compiler's wait-count tracking does not
+// treat the transfer as aliasing every later LDS read (it would otherwise wait for the next
+// tile's transfer before reading the current one); the caller waits with wait_dma().
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void_t;
+__device__ __forceinline__ void buffer_to_lds16(i32x4_t rsrc, uint32_t lds, uint32_t voff) {
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+                 :
+                 : "s"(lds), "v"(voff), "s"(rsrc)
+                 : "memory", "m0");
+}
+__device__ __forceinline__ void wait_dma() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+// Buffer resource words: base, stride 0, num_records bytes, the same flags as
+// __builtin_amdgcn_make_buffer_rsrc is given elsewhere (0x00020000).
+__device__ __forceinline__ i32x4_t make_rsrc_words(const void* base, int nrec) {
+    const uint64_t b = (uint64_t)base;
+    i32x4_t r;
+    r[0] = __builtin_amdgcn_readfirstlane((int)(uint32_t)b);
+    r[1] = __builtin_amdgcn_readfirstlane((int)((uint32_t)(b >> 32) & 0xffffu));
+    r[2] = __builtin_amdgcn_readfirstlane(nrec);
+    r[3] = 0x00020000;
+    return r;
+}
+
 // Running-max slack (log2 units) tolerated before O is rescaled: probabilities stay <= 2^8.
 constexpr float kRescaleLog2 = 8.0f;
 
@@ -92,6 +118,19 @@ __device__ __forceinline__ int64_t paged_row(const PrefillKArgs& ka, int b, int 
 #ifndef FA_PREFILL_PIPE
 #define FA_PREFILL_PIPE 0
 #endif
+#ifndef FA_PREFILL_DB
+#define FA_PREFILL_DB 1
+#endif
+#ifndef FA_PREFILL_DMA
+#define FA_PREFILL_DMA 1
+#endif
+#ifndef FA_PREFILL_KRING
+#define FA_PREFILL_KRING 4
+#endif
+#ifndef FA_PREFILL_SGS
+#define FA_PREFILL_SGS 1
+#endif
+
 // Scheduling groups (LLVM AMDGPU sched_group_barrier masks: 0x2 VALU, 0x8 MFMA, 0x100 DS read, 0x400 transcendental).
 #define FA_SG(mask, n) __builtin_amdgcn_sched_group_barrier(mask, n, 0)
 #define FA_SG_MRV(nv) \
@@ -119,11 +158,23 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma16(PrefillKArgs ka) {
     constexpr bool CONTIG = PMODE == kContig || VT;
     constexpr int VTROWB = BN * 2 + 16;     // padded V^T row: 64 keys of one dim (bytes)
     constexpr int VBYTES = VT ? DPAD * VTROWB : BN * VROWB;
-    __shared__ __attribute__((aligned(16))) uint8_t smem[BN * KROWB + VBYTES];
-    uint8_t* const k_lds = smem;
-    uint8_t* const v_lds = smem + BN * KROWB;
+    // One K/V stage, or two (double buffering: tile j+1 is staged while tile j is computed).
+    constexpr bool DB = FA_PREFILL_DB != 0 && !PIPE;
+    constexpr int STAGE = BN * KROWB + VBYTES;
+    // Contiguous K/V go straight from memory into LDS (buffer_load ... lds): no staging
+    // registers and no LDS store instructions. One instruction fills 64 consecutive 16-byte
+    // slots; padded rows are kept by giving pad slots an out-of-range (zero-filling, no
+    // memory traffic) offset. Instructions beyond a tile's slot count target a dummy KiB.
+    constexpr bool DMA = FA_PREFILL_DMA != 0 && DB && PMODE == kContig && !ROPEK;
+    constexpr int KSL = KROWB / 16, VSL = VROWB / 16;  // 16-byte slots per padded row
+    constexpr int KI = (KSL + 3) / 4, VI = (VSL + 3) / 4;  // DMA instructions per wave
+    constexpr int DUMMY = 2 * STAGE;
+    __shared__ __attribute__((aligned(16))) uint8_t smem[(DB ? 2 : 1) * STAGE + (DMA ? 1024 : 0)];
+    int st_r = 0, st_w = 0;  // byte offsets of the stage being read / written
+    int st_k = 0, st_v = 0;  // stage offsets the K (S^T) and V (P.V) operand reads use
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 5;
+    const int tid = threadIdx.x, lane = tid & 63, g = lane >> 5;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar registers
     const int D = a.head_dim, half = D >> 1;
     const int rows_total = a.q_len * a.group;
     const int nqb = (rows_total + BM - 1) / BM;
@@ -144,7 +195,7 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma16(PrefillKArgs ka) {
     const int t_min = r0 / a.group;
     int n_keys = a.kv_len;
     if (a.causal) n_keys = min(n_keys, a.causal_offset + t_max + 1);
-    const int n_tiles = (n_keys + BN - 1) / BN;
+    const int n_tiles = __builtin_amdgcn_readfirstlane((n_keys + BN - 1) / BN);
     const int cpos_min = a.causal_offset + t_min;
 
     // ---- Q^T operand, rotated in registers: lane holds Q[row][16ks + 8g .. +8].
@@ -276,7 +327,7 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma16(PrefillKArgs ka) {
 #pragma unroll
                 for (int j = 0; j < 4; ++j) val[j] = H::pack(x[2 * j], x[2 * j + 1]);
             }
-            *(u32x4_t*)(k_lds + kl * KROWB + k_dc * 16) = val;
+            *(u32x4_t*)(smem + st_w + kl * KROWB + k_dc * 16) = val;
         }
     };
     auto store_v = [&]() {
@@ -284,12 +335,14 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma16(PrefillKArgs ka) {
 #pragma unroll
             for (int p = 0; p < KPASS; ++p) {
                 const int c = tid + 256 * p;
-                *(u32x4_t*)(v_lds + (c >> 3) * VTROWB + (c & 7) * 16) = vreg[p];
+                *(u32x4_t*)(smem + st_w + BN * KROWB + (c >> 3) * VTROWB + (c & 7) * 16) =
+                    vreg[p];
             }
         } else {
 #pragma unroll
             for (int p = 0; p < KPASS; ++p)
-                *(u32x4_t*)(v_lds + (p * KRPP + k_r) * VROWB + k_dc * 16) = vreg[p];
+                *(u32x4_t*)(smem + st_w + BN * KROWB + (p * KRPP + k_r) * VROWB + k_dc * 16) =
+                    vreg[p];
         }
     };
     auto load_v = [&](int tile) {
@@ -305,10 +358,10 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma16(PrefillKArgs ka) {
 
     // K row fed to MFMA row m of a 32-key block: bits 2 and 3 swapped.
     const int pm = ((lane & 31) & ~12) | (((lane & 31) & 4) << 1) | (((lane & 31) & 8) >> 1);
-    const uint8_t* const k_rd0 = k_lds + pm * KROWB + g * 16;
+    const int k_rd0 = pm * KROWB + g * 16;
     // ds_read_b64_tr_b16 source: lane (16-group G, index s) addresses key 8g + s/4 and dims
     // 16*(G&1) + 4*(s&3) .. +3; it receives dim (lane & 31) of keys 8g + 0..3.
-    const uint8_t* const v_rd = v_lds + (8 * g + ((lane & 15) >> 2)) * VROWB +
+    const int v_rd = BN * KROWB + (8 * g + ((lane & 15) >> 2)) * VROWB +
                                 (16 * ((lane >> 4) & 1) + 4 * (lane & 3)) * 2;
 
     // Threshold rescale: the running max m_run only moves when a tile max exceeds it by more
@@ -321,15 +374,34 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma16(PrefillKArgs ka) {
     bool moved = false;
 
     // ---- S^T = K_perm . Q^T over the K tile in LDS
-    auto compute_s = [&](f32x16_t (&sacc)[2]) {
+    // Step i uses accumulator kb = i & 1 and k-step ks = i >> 1 (the two chains alternate);
+    // the K operands of the next KR steps are already being read (a KR-deep register ring).
+    auto compute_s = [&](f32x16_t (&sacc)[2], auto own_order) {
+        constexpr int NSTEP = 2 * KS, KR = FA_PREFILL_KRING;
+        auto kread = [&](int i) {
+            return *(const u32x4_t*)(smem + st_k + k_rd0 + (i & 1) * 32 * KROWB + (i >> 1) * 32);
+        };
+        u32x4_t ring[KR];
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-            sacc[kb] = (f32x16_t)0.0f;
+        for (int i = 0; i < KR; ++i) ring[i] = kread(i);
+        sacc[0] = (f32x16_t)0.0f;
+        sacc[1] = (f32x16_t)0.0f;
 #pragma unroll
-            for (int ks = 0; ks < KS; ++ks) {
-                const u32x4_t av = *(const u32x4_t*)(k_rd0 + kb * 32 * KROWB + ks * 32);
-                sacc[kb] = H::mfma32(av, qop[ks], sacc[kb]);
+        for (int i = 0; i < NSTEP; ++i) {
+            const u32x4_t av = ring[i % KR];
+            if (i + KR < NSTEP) ring[i % KR] = kread(i + KR);
+            sacc[i & 1] = H::mfma32(av, qop[i >> 1], sacc[i & 1]);
+        }
+        if constexpr (FA_PREFILL_SGS != 0 && decltype(own_order)::value) {
+            // Keep the issue order: KR reads, then (MFMA, read) pairs, then the last MFMAs, so
+            // each MFMA's operand was requested KR steps earlier.
+            FA_SG(0x100, KR);
+#pragma unroll
+            for (int i = 0; i < NSTEP - KR; ++i) {
+                FA_SG(0x008, 1);
+                FA_SG(0x100, 1);
             }
+            FA_SG(0x008, KR);
         }
     };
 
@@ -345,16 +417,18 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma16(PrefillKArgs ka) {
         }
         // row = this lane's query; partner lane ^ 32 holds the other keys. Four partial
         // chains keep the max and sum dependency chains short.
+        // (three-input maxima: 16 v_max3 for the 32 scores)
         float mx[4];
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
             const f32x16_t& v = sacc[c >> 1];
             const int o = (c & 1) * 8;
-            mx[c] = fmaxf(fmaxf(fmaxf(v[o], v[o + 1]), fmaxf(v[o + 2], v[o + 3])),
-                          fmaxf(fmaxf(v[o + 4], v[o + 5]), fmaxf(v[o + 6], v[o + 7])));
+            const float a0 = fmaxf(fmaxf(v[o], v[o + 1]), v[o + 2]);
+            const float a1 = fmaxf(fmaxf(v[o + 3], v[o + 4]), v[o + 5]);
+            mx[c] = fmaxf(fmaxf(a0, a1), fmaxf(v[o + 6], v[o + 7]));
         }
         float mt = fmaxf(fmaxf(mx[0], mx[1]), fmaxf(mx[2], mx[3]));
-        mt = fmaxf(mt, shfl_xor(mt, 32));
+        mt = fmaxf(mt, xor32(mt));
         const bool need = mt * c2 > m_run * c2 + kRescaleLog2;
         moved = __any(need);
         const float m_use = need ? mt : m_run;
@@ -366,16 +440,10 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma16(PrefillKArgs ka) {
     // ---- probabilities, row sum and the P^T operands (16 keys each)
     auto softmax_exp = [&](f32x16_t (&sacc)[2], u32x4_t (&pop)[4]) {
         const float neg = -m_run * c2;
-        float ls[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const float p = fast_exp2(fmaf(sacc[kb][i], c2, neg));
-                sacc[kb][i] = p;
-                ls[(i & 1) + 2 * kb] += p;
-            }
-        l_run += (ls[0] + ls[1]) + (ls[2] + ls[3]);
+            for (int i = 0; i < 16; ++i) sacc[kb][i] = fast_exp2(fmaf(sacc[kb][i], c2, neg));
 #pragma unroll
         for (int s2 = 0; s2 < 4; ++s2) {
             const int kb = s2 >> 1, h8 = (s2 & 1) * 8;
@@ -383,6 +451,14 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma16(PrefillKArgs ka) {
             for (int j = 0; j < 4; ++j)
                 pop[s2][j] = H::pack(sacc[kb][h8 + 2 * j], sacc[kb][h8 + 2 * j + 1]);
         }
+        // Row sum of the rounded probabilities the P.V product uses: one v_dot2 per pair,
+        // four independent chains.
+        float ls[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int s2 = 0; s2 < 4; ++s2)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) ls[j] = H::sum2(pop[s2][j], ls[j]);
+        l_run += (ls[0] + ls[1]) + (ls[2] + ls[3]);
     };
 
     auto rescale_o = [&]() {
@@ -394,14 +470,15 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma16(PrefillKArgs ka) {
 
     // ---- O^T += V^T . P^T over the V tile in LDS
     // V^T layout: lane reads dim mb*32 + (lane & 31), keys 16 s2 + 8 g .. +7 (16 bytes).
-    const uint8_t* const vt_rd = v_lds + (lane & 31) * VTROWB + g * 16;
+    const int vt_rd = BN * KROWB + (lane & 31) * VTROWB + g * 16;
     auto compute_pv = [&](const u32x4_t (&pop)[4]) {
         if constexpr (VT) {
 #pragma unroll
             for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
                 for (int s2 = 0; s2 < 4; ++s2) {
-                    const u32x4_t av = *(const u32x4_t*)(vt_rd + mb * 32 * VTROWB + s2 * 32);
+                    const u32x4_t av =
+                        *(const u32x4_t*)(smem + st_v + vt_rd + mb * 32 * VTROWB + s2 * 32);
                     oacc[mb] = H::mfma32(av, pop[s2], oacc[mb]);
                 }
             return;
@@ -412,7 +489,7 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma16(PrefillKArgs ka) {
             for (int s2 = 0; s2 < 4; ++s2) {
                 typedef short v4i16_t __attribute__((ext_vector_type(4)));
                 typedef __attribute__((address_space(3))) v4i16_t lds_v4i16_t;
-                const uint8_t* src = v_rd + s2 * 16 * VROWB + mb * 64;
+                const uint8_t* src = smem + st_v + v_rd + s2 * 16 * VROWB + mb * 64;
                 const v4i16_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)src);
                 const v4i16_t hi =
                     __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)(src + 4 * VROWB));
@@ -426,15 +503,124 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma16(PrefillKArgs ka) {
     // Leading tiles that need no mask: every key is < kv_len and visible to every row.
     int n_full = a.kv_len / BN;
     if (a.causal) n_full = min(n_full, (cpos_min + 1) / BN);
+    n_full = __builtin_amdgcn_readfirstlane(n_full);
     using NoMask = std::integral_constant<bool, false>;
     using Mask = std::integral_constant<bool, true>;
 
-    if constexpr (!PIPE) {
+    if constexpr (DMA) {
+        // Per-lane byte offsets of this wave's DMA instructions (k = wave + 4 i fills slots
+        // 64 k .. 64 k + 63 of the tile: row q / SL, slot q % SL), constant across tiles.
+        constexpr uint32_t kOob = 0x7fff0000u;
+        uint32_t koff[KI], voff[VI];
+#pragma unroll
+        for (int i = 0; i < KI; ++i) {
+            const int q = 64 * (wave + 4 * i) + lane, r = q / KSL, c = q % KSL;
+            koff[i] = (wave + 4 * i < KSL && c < CPR && (FULLD || c * 8 < D))
+                          ? (uint32_t)r * row_bytes + (uint32_t)c * 16u
+                          : kOob;
+        }
+#pragma unroll
+        for (int i = 0; i < VI; ++i) {
+            const int q = 64 * (wave + 4 * i) + lane, r = q / VSL, c = q % VSL;
+            voff[i] = (wave + 4 * i < VSL && c < CPR && (FULLD || c * 8 < D))
+                          ? (uint32_t)r * row_bytes + (uint32_t)c * 16u
+                          : kOob;
+        }
+        const int nrec_all = (a.kv_len - 1) * (int)row_bytes + D * 2;
+        // Tile `tile` of K and V into the stage at byte offset `st`.
+        const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_void_t*)smem;
+        auto dma_k = [&](int tile, int st) {
+            const int base = tile * BN * (int)row_bytes;
+            const i32x4_t rk = make_rsrc_words(kb8 + base, nrec_all - base);
+#pragma unroll
+            for (int i = 0; i < KI; ++i) {
+                const int k = wave + 4 * i;
+                const int dst = k < KSL ? st + k * 1024 : DUMMY;
+                buffer_to_lds16(rk, __builtin_amdgcn_readfirstlane(lds0 + dst), koff[i]);
+            }
+        };
+        auto dma_v = [&](int tile, int st) {
+            const int base = tile * BN * (int)row_bytes;
+            const i32x4_t rv = make_rsrc_words(vb8 + base, nrec_all - base);
+#pragma unroll
+            for (int i = 0; i < VI; ++i) {
+                const int k = wave + 4 * i;
+                const int dst = k < VSL ? st + BN * KROWB + k * 1024 : DUMMY;
+                buffer_to_lds16(rv, __builtin_amdgcn_readfirstlane(lds0 + dst), voff[i]);
+            }
+        };
+        auto dma_tile = [&](int tile, int st) {
+            dma_k(tile, st);
+            dma_v(tile, st);
+        };
+        // Stage j & 1 holds tile j. Iteration j first starts tile j+1's transfer into the other
+        // stage (free: every wave passed the barrier that ended iteration j-1), computes tile j,
+        // then waits for its own transfers and meets the other waves: one barrier per tile.
+        if (n_tiles > 0) dma_tile(0, 0);
+        wait_dma();
+        __syncthreads();
+        auto tile_step = [&](int tile, auto masked) {
+            st_r = (tile & 1) * STAGE;
+            st_k = st_v = st_r;
+            if (tile + 1 < n_tiles) dma_tile(tile + 1, STAGE - st_r);
+            f32x16_t sacc[2];
+            u32x4_t pop[4];
+            compute_s(sacc, std::true_type{});
+            softmax_max(sacc, tile, masked);
+            rescale_o();
+            softmax_exp(sacc, pop);
+            compute_pv(pop);
+            wait_dma();
+            __syncthreads();
+        };
+        int tile = 0;
+        for (; tile < n_full; ++tile) tile_step(tile, NoMask{});
+        for (; tile < n_tiles; ++tile) tile_step(tile, Mask{});
+    } else if constexpr (DB) {
+        // Double-buffered: stage j & 1 holds tile j. Tile j+1 (loaded into registers one tile
+        // earlier) is stored to the other stage between the softmax and P.V of tile j, then the
+        // loads of tile j+2 are issued; one barrier per tile.
+        if (n_tiles > 0) {
+            load_one(0, kb8, kreg);
+            load_v(0);
+            store_k(0);
+            store_v();
+            if (n_tiles > 1) {
+                load_one(1, kb8, kreg);
+                load_v(1);
+            }
+        }
+        __syncthreads();
+        auto tile_step = [&](int tile, auto masked) {
+            st_r = (tile & 1) * STAGE;
+            st_k = st_v = st_r;
+            f32x16_t sacc[2];
+            u32x4_t pop[4];
+            compute_s(sacc, std::true_type{});
+            softmax_max(sacc, tile, masked);
+            rescale_o();
+            softmax_exp(sacc, pop);
+            if (tile + 1 < n_tiles) {
+                st_w = STAGE - st_r;
+                store_k(tile + 1);
+                store_v();
+                if (tile + 2 < n_tiles) {
+                    load_one(tile + 2, kb8, kreg);
+                    load_v(tile + 2);
+                }
+            }
+            compute_pv(pop);
+            __syncthreads();
+        };
+        int tile = 0;
+        for (; tile < n_full; ++tile) tile_step(tile, NoMask{});
+        for (; tile < n_tiles; ++tile) tile_step(tile, Mask{});
+    } else if constexpr (!PIPE) {
         if (n_tiles > 0) {
             load_one(0, kb8, kreg);
             load_v(0);
         }
-        for (int tile = 0; tile < n_tiles; ++tile) {
+        auto tile_step = [&](int tile, auto masked) {
             store_k(tile);
             store_v();
             __syncthreads();
@@ -444,14 +630,17 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma16(PrefillKArgs ka) {
             }
             f32x16_t sacc[2];
             u32x4_t pop[4];
-            compute_s(sacc);
-            if (tile < n_full) softmax_max(sacc, tile, NoMask{});
-            else softmax_max(sacc, tile, Mask{});
+            compute_s(sacc, std::true_type{});
+            softmax_max(sacc, tile, masked);
             rescale_o();
             softmax_exp(sacc, pop);
             compute_pv(pop);
             __syncthreads();
-        }
+        };
+        // Two loops, so the mask-free tiles carry no predicated mask code.
+        int tile = 0;
+        for (; tile < n_full; ++tile) tile_step(tile, NoMask{});
+        for (; tile < n_tiles; ++tile) tile_step(tile, Mask{});
     } else {
         // Software pipeline: the K tile in LDS runs one tile ahead of the V tile, so the MFMAs
         // of S(j+1) are independent of the softmax of tile j and are interleaved with it.
@@ -466,7 +655,7 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma16(PrefillKArgs ka) {
             store_v();
             if (n_tiles > 1) load_one(1, kb8, kreg);
             __syncthreads();
-            compute_s(s_a);
+            compute_s(s_a, std::true_type{});
             if (n_tiles > 1) load_v(1);
             __syncthreads();
             if (n_tiles > 1) {
@@ -479,7 +668,7 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma16(PrefillKArgs ka) {
             rescale_o();
             __syncthreads();
             u32x4_t pop[4];
-            compute_s(nxt);
+            compute_s(nxt, std::true_type{});
             softmax_exp(cur, pop);
             // 16 K reads + 16 MFMAs of S(j+1) spread through the exponentials of tile j
             FA_SG_MV(7); FA_SG_MV(7); FA_SG_MV(7); FA_SG_MV(7);
