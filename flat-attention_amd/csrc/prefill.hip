@@ -57,17 +57,16 @@ __device__ __forceinline__ int64_t kv_row_offset(const PrefillKArgs& ka, int b, 
 }
 
 // 16 bytes per lane from a buffer straight into LDS: lane i writes LDS byte address
-// lds + 16 i (buffer_load_dwordx4 ... lds, M0 = lds). Out-of-range offsets write zeros and
+// lds + 16 i (buffer_load_dwordx4 ... lds; the compiler loads M0 = lds). Out-of-range offsets write zeros and
 // fetch nothing. Issued from inline assembly so the compiler's wait-count tracking does not
 // treat the transfer as aliasing every later LDS read (it would otherwise wait for the next
 // tile's transfer before reading the current one); the caller waits with wait_dma().
 typedef int i32x4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) void lds_void_t;
 __device__ __forceinline__ void buffer_to_lds16(i32x4_t rsrc, uint32_t lds, uint32_t voff) {
-    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
-                 :
-                 : "s"(lds), "v"(voff), "s"(rsrc)
-                 : "memory", "m0");
+    // No memory clobber: the transfer writes a stage no LDS access near it touches, and the
+    // barriers / wait_dma() that order it against its readers are themselves ordered.
+    asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds" : : "v"(voff), "s"(rsrc), "{m0}"(lds));
 }
 __device__ __forceinline__ void wait_dma() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 // Buffer resource words: base, stride 0, num_records bytes, the same flags as
@@ -124,8 +123,19 @@ __device__ __forceinline__ int64_t paged_row(const PrefillKArgs& ka, int b, int 
 #ifndef FA_PREFILL_DMA
 #define FA_PREFILL_DMA 1
 #endif
+// 8-wave ping-pong workgroups for the contiguous DMA path (off: measured level with the 4-wave
+// kernel; its MFMA phases are bound by the LDS instruction rate of the operand reads).
+#ifndef FA_PREFILL_PP
+#define FA_PREFILL_PP 0
+#endif
+__host__ __device__ constexpr bool prefill_pingpong_enabled() {
+    return FA_PREFILL_PP != 0 && FA_PREFILL_DMA != 0 && FA_PREFILL_DB != 0 && FA_PREFILL_PIPE == 0;
+}
 #ifndef FA_PREFILL_KRING
 #define FA_PREFILL_KRING 4
+#endif
+#ifndef FA_PREFILL_VRING
+#define FA_PREFILL_VRING 3
 #endif
 #ifndef FA_PREFILL_SGS
 #define FA_PREFILL_SGS 1
@@ -141,12 +151,16 @@ __device__ __forceinline__ int64_t paged_row(const PrefillKArgs& ka, int b, int 
     FA_SG(0x008, 1);  \
     FA_SG(0x402, nv)
 
-template <typename T, int DPAD, int PMODE, bool ROPEK, bool FULLD>
-__global__ __launch_bounds__(256, 2) void prefill_mfma16(PrefillKArgs ka) {
+// NW = 4: four waves, 128 query rows per workgroup, two workgroups per CU.
+// NW = 8: eight waves (two groups of four, 256 rows), one workgroup per CU, ping-pong schedule
+// (contiguous DMA path only): while one group runs its MFMAs the other runs its softmax.
+template <typename T, int DPAD, int PMODE, bool ROPEK, bool FULLD, int NW>
+__global__ __launch_bounds__(64 * NW, 2) void prefill_mfma16(PrefillKArgs ka) {
     constexpr bool PIPE = FA_PREFILL_PIPE != 0;
     using H = Half<T>;
     const PrefillArgs& a = ka.a;
-    constexpr int BM = 128, BN = 64;
+    constexpr int BM = 32 * NW, BN = 64;
+    constexpr bool PP = NW == 8;
     constexpr int KS = DPAD / 16;           // QK^T k-steps (16 dims each)
     constexpr int MB = DPAD / 32;           // 32-dim blocks of O^T
     constexpr int CPR = DPAD / 8;           // 16-byte chunks per row
@@ -167,7 +181,9 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma16(PrefillKArgs ka) {
     // memory traffic) offset. Instructions beyond a tile's slot count target a dummy KiB.
     constexpr bool DMA = FA_PREFILL_DMA != 0 && DB && PMODE == kContig && !ROPEK;
     constexpr int KSL = KROWB / 16, VSL = VROWB / 16;  // 16-byte slots per padded row
-    constexpr int KI = (KSL + 3) / 4, VI = (VSL + 3) / 4;  // DMA instructions per wave
+    // Waves sharing the transfers: all of them, or group 1 alone under the ping-pong schedule.
+    constexpr int NWD = PP ? 4 : NW;
+    constexpr int KI = (KSL + NWD - 1) / NWD, VI = (VSL + NWD - 1) / NWD;  // DMA instrs per wave
     constexpr int DUMMY = 2 * STAGE;
     __shared__ __attribute__((aligned(16))) uint8_t smem[(DB ? 2 : 1) * STAGE + (DMA ? 1024 : 0)];
     int st_r = 0, st_w = 0;  // byte offsets of the stage being read / written
@@ -191,12 +207,20 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma16(PrefillKArgs ka) {
     const int hq = kvh * a.group + (row_ok ? row % a.group : 0);
     const int cpos = a.causal_offset + t;
 
-    const int t_max = min(a.q_len - 1, (r0 + BM - 1) / a.group);
-    const int t_min = r0 / a.group;
+    // Key tiles this wave's rows need (its group's 128 rows under the ping-pong schedule) and,
+    // for the ping-pong barrier count, the whole block's.
+    const int r0w = PP ? r0 + 128 * (wave >> 2) : r0;
+    const int t_max = min(a.q_len - 1, (r0w + 127) / a.group);
+    const int t_min = r0w / a.group;
     int n_keys = a.kv_len;
     if (a.causal) n_keys = min(n_keys, a.causal_offset + t_max + 1);
     const int n_tiles = __builtin_amdgcn_readfirstlane((n_keys + BN - 1) / BN);
     const int cpos_min = a.causal_offset + t_min;
+    int n_keys_blk = a.kv_len;
+    if (a.causal)
+        n_keys_blk = min(n_keys_blk, a.causal_offset + min(a.q_len - 1, (r0 + BM - 1) / a.group) + 1);
+    const int n_blk = __builtin_amdgcn_readfirstlane((n_keys_blk + BN - 1) / BN);
+    (void)n_blk;
 
     // ---- Q^T operand, rotated in registers: lane holds Q[row][16ks + 8g .. +8].
     u32x4_t qop[KS];
@@ -376,7 +400,9 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma16(PrefillKArgs ka) {
     // ---- S^T = K_perm . Q^T over the K tile in LDS
     // Step i uses accumulator kb = i & 1 and k-step ks = i >> 1 (the two chains alternate);
     // the K operands of the next KR steps are already being read (a KR-deep register ring).
-    auto compute_s = [&](f32x16_t (&sacc)[2], auto own_order) {
+    // hook(i) runs after MFMA i (the ping-pong kernel issues its K/V transfers there).
+    auto no_hook = [](int) {};
+    auto compute_s = [&](f32x16_t (&sacc)[2], auto own_order, auto&& hook) {
         constexpr int NSTEP = 2 * KS, KR = FA_PREFILL_KRING;
         auto kread = [&](int i) {
             return *(const u32x4_t*)(smem + st_k + k_rd0 + (i & 1) * 32 * KROWB + (i >> 1) * 32);
@@ -391,6 +417,7 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma16(PrefillKArgs ka) {
             const u32x4_t av = ring[i % KR];
             if (i + KR < NSTEP) ring[i % KR] = kread(i + KR);
             sacc[i & 1] = H::mfma32(av, qop[i >> 1], sacc[i & 1]);
+            hook(i);
         }
         if constexpr (FA_PREFILL_SGS != 0 && decltype(own_order)::value) {
             // Keep the issue order: KR reads, then (MFMA, read) pairs, then the last MFMAs, so
@@ -471,7 +498,7 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma16(PrefillKArgs ka) {
     // ---- O^T += V^T . P^T over the V tile in LDS
     // V^T layout: lane reads dim mb*32 + (lane & 31), keys 16 s2 + 8 g .. +7 (16 bytes).
     const int vt_rd = BN * KROWB + (lane & 31) * VTROWB + g * 16;
-    auto compute_pv = [&](const u32x4_t (&pop)[4]) {
+    auto compute_pv = [&](const u32x4_t (&pop)[4], auto&& hook) {
         if constexpr (VT) {
 #pragma unroll
             for (int mb = 0; mb < MB; ++mb)
@@ -483,21 +510,40 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma16(PrefillKArgs ka) {
                 }
             return;
         }
+        // Step i: O^T block mb = i % MB (the MB accumulators rotate), keys 16 s2 .. (s2 = i / MB);
+        // the V^T operands of the next RV steps are already being read (two ds_read_b64_tr_b16
+        // per step, a register ring).
+        typedef short v4i16_t __attribute__((ext_vector_type(4)));
+        typedef __attribute__((address_space(3))) v4i16_t lds_v4i16_t;
+        constexpr int NSTEP = 4 * MB, RV = FA_PREFILL_VRING;
+        auto vread = [&](int i) {
+            const uint8_t* src = smem + st_v + v_rd + (i / MB) * 16 * VROWB + (i % MB) * 64;
+            const v4i16_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)src);
+            const v4i16_t hi =
+                __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)(src + 4 * VROWB));
+            const u32x2_t l2 = __builtin_bit_cast(u32x2_t, lo);
+            const u32x2_t h2 = __builtin_bit_cast(u32x2_t, hi);
+            return u32x4_t{l2[0], l2[1], h2[0], h2[1]};
+        };
+        u32x4_t ring[RV];
 #pragma unroll
-        for (int mb = 0; mb < MB; ++mb)
+        for (int i = 0; i < RV; ++i) ring[i] = vread(i);
 #pragma unroll
-            for (int s2 = 0; s2 < 4; ++s2) {
-                typedef short v4i16_t __attribute__((ext_vector_type(4)));
-                typedef __attribute__((address_space(3))) v4i16_t lds_v4i16_t;
-                const uint8_t* src = smem + st_v + v_rd + s2 * 16 * VROWB + mb * 64;
-                const v4i16_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)src);
-                const v4i16_t hi =
-                    __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)(src + 4 * VROWB));
-                const u32x2_t l2 = __builtin_bit_cast(u32x2_t, lo);
-                const u32x2_t h2 = __builtin_bit_cast(u32x2_t, hi);
-                const u32x4_t av = {l2[0], l2[1], h2[0], h2[1]};
-                oacc[mb] = H::mfma32(av, pop[s2], oacc[mb]);
+        for (int i = 0; i < NSTEP; ++i) {
+            const u32x4_t av = ring[i % RV];
+            if (i + RV < NSTEP) ring[i % RV] = vread(i + RV);
+            oacc[i % MB] = H::mfma32(av, pop[i / MB], oacc[i % MB]);
+            hook(i);
+        }
+        if constexpr (FA_PREFILL_SGS != 0) {
+            FA_SG(0x100, 2 * RV);
+#pragma unroll
+            for (int i = 0; i < NSTEP - RV; ++i) {
+                FA_SG(0x008, 1);
+                FA_SG(0x100, 2);
             }
+            FA_SG(0x008, RV);
+        }
     };
 
     // Leading tiles that need no mask: every key is < kv_len and visible to every row.
@@ -511,48 +557,154 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma16(PrefillKArgs ka) {
         // Per-lane byte offsets of this wave's DMA instructions (k = wave + 4 i fills slots
         // 64 k .. 64 k + 63 of the tile: row q / SL, slot q % SL), constant across tiles.
         constexpr uint32_t kOob = 0x7fff0000u;
+        const int dw = PP ? wave & 3 : wave;  // this wave's index among the transferring waves
         uint32_t koff[KI], voff[VI];
 #pragma unroll
         for (int i = 0; i < KI; ++i) {
-            const int q = 64 * (wave + 4 * i) + lane, r = q / KSL, c = q % KSL;
-            koff[i] = (wave + 4 * i < KSL && c < CPR && (FULLD || c * 8 < D))
+            const int q = 64 * (dw + NWD * i) + lane, r = q / KSL, c = q % KSL;
+            koff[i] = (dw + NWD * i < KSL && c < CPR && (FULLD || c * 8 < D))
                           ? (uint32_t)r * row_bytes + (uint32_t)c * 16u
                           : kOob;
         }
 #pragma unroll
         for (int i = 0; i < VI; ++i) {
-            const int q = 64 * (wave + 4 * i) + lane, r = q / VSL, c = q % VSL;
-            voff[i] = (wave + 4 * i < VSL && c < CPR && (FULLD || c * 8 < D))
+            const int q = 64 * (dw + NWD * i) + lane, r = q / VSL, c = q % VSL;
+            voff[i] = (dw + NWD * i < VSL && c < CPR && (FULLD || c * 8 < D))
                           ? (uint32_t)r * row_bytes + (uint32_t)c * 16u
                           : kOob;
         }
         const int nrec_all = (a.kv_len - 1) * (int)row_bytes + D * 2;
         // Tile `tile` of K and V into the stage at byte offset `st`.
         const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_void_t*)smem;
-        auto dma_k = [&](int tile, int st) {
+        // One transfer instruction (i-th of this wave) of tile `tile` of K / V into stage `st`.
+        auto dma_k1 = [&](int tile, int st, int i) {
             const int base = tile * BN * (int)row_bytes;
             const i32x4_t rk = make_rsrc_words(kb8 + base, nrec_all - base);
-#pragma unroll
-            for (int i = 0; i < KI; ++i) {
-                const int k = wave + 4 * i;
-                const int dst = k < KSL ? st + k * 1024 : DUMMY;
-                buffer_to_lds16(rk, __builtin_amdgcn_readfirstlane(lds0 + dst), koff[i]);
-            }
+            const int k = dw + NWD * i;
+            const int dst = k < KSL ? st + k * 1024 : DUMMY;
+            buffer_to_lds16(rk, __builtin_amdgcn_readfirstlane(lds0 + dst), koff[i]);
         };
-        auto dma_v = [&](int tile, int st) {
+        auto dma_v1 = [&](int tile, int st, int i) {
             const int base = tile * BN * (int)row_bytes;
             const i32x4_t rv = make_rsrc_words(vb8 + base, nrec_all - base);
+            const int k = dw + NWD * i;
+            const int dst = k < VSL ? st + BN * KROWB + k * 1024 : DUMMY;
+            buffer_to_lds16(rv, __builtin_amdgcn_readfirstlane(lds0 + dst), voff[i]);
+        };
+        auto dma_k = [&](int tile, int st) {
 #pragma unroll
-            for (int i = 0; i < VI; ++i) {
-                const int k = wave + 4 * i;
-                const int dst = k < VSL ? st + BN * KROWB + k * 1024 : DUMMY;
-                buffer_to_lds16(rv, __builtin_amdgcn_readfirstlane(lds0 + dst), voff[i]);
-            }
+            for (int i = 0; i < KI; ++i) dma_k1(tile, st, i);
+        };
+        auto dma_v = [&](int tile, int st) {
+#pragma unroll
+            for (int i = 0; i < VI; ++i) dma_v1(tile, st, i);
         };
         auto dma_tile = [&](int tile, int st) {
             dma_k(tile, st);
             dma_v(tile, st);
         };
+        if constexpr (PP) {
+            // Ping-pong: global phase p, local phase q = p - group (group 1 runs one phase
+            // behind). Even q = 2j: MFMAs of P.V(j-1) and S(j); odd q = 2j+1: softmax of tile j
+            // (max, rescale, exponentials into P(j)). The two waves sharing a SIMD belong to
+            // different groups, so one issues MFMAs while the other issues VALU work; a barrier
+            // ends every phase. K(t) and V(t) use slot t & 1: K(m+1) and V(m) are started at
+            // phase 2m (their slots' previous tiles were last read by phase 2m-1) and waited
+            // for at the end of phase 2m+1, before their first reader (phase 2m+2).
+            const int grp = wave >> 2;
+            f32x16_t sacc[2];
+            u32x4_t pop[4];
+            using T_ = std::true_type;
+            using F_ = std::false_type;
+            // MFMA phase of tile m: P.V(m-1) then S(m); softmax phase of tile m.
+            auto mfma_phase = [&](int m, auto pv, auto sc) {
+                if constexpr (decltype(pv)::value) {
+                    st_v = ((m - 1) & 1) * STAGE;
+                    compute_pv(pop, no_hook);
+                }
+                // P dies before the next scores are produced: keep S's operand reads out of
+                // the P.V region (register pressure)
+                __builtin_amdgcn_sched_barrier(0);
+                if constexpr (decltype(sc)::value) {
+                    st_k = (m & 1) * STAGE;
+                    compute_s(sacc, T_{}, no_hook);
+                }
+            };
+            auto softmax_phase = [&](int m) {
+                if (m < n_full) softmax_max(sacc, m, NoMask{});
+                else softmax_max(sacc, m, Mask{});
+                rescale_o();
+                softmax_exp(sacc, pop);
+            };
+            // Global iteration m = 0 .. n_blk: phases 2m and 2m+1. K(m+1) and V(m) are started
+            // at phase 2m (into slots whose previous tiles were last read by phase 2m-1) and
+            // waited for at the end of phase 2m+1, before their first reader (phase 2m+2).
+            // Group 1 issues every transfer, at the start of its softmax phases: the VALU phase
+            // has slack, the MFMA stream of group 0 is left alone.
+            auto start_dma = [&](int m) {
+                if (m + 1 < n_blk) dma_k(m + 1, ((m + 1) & 1) * STAGE);
+                if (m < n_blk) dma_v(m, (m & 1) * STAGE);
+            };
+            auto end_even = [&]() { __syncthreads(); };
+            auto end_odd = [&]() {
+                wait_dma();
+                __syncthreads();
+            };
+            if (n_blk > 0 && wave >= 4) dma_k(0, 0);
+            wait_dma();
+            __syncthreads();
+            int m = 0;
+            const int n = n_tiles;  // this group's tiles (<= n_blk)
+            if (grp == 0) {
+                // group 0: MFMAs in even phases, softmax in odd phases
+                if (n > 0) {
+                    mfma_phase(0, F_{}, T_{});
+                    end_even();
+                    softmax_phase(0);
+                    end_odd();
+                    for (m = 1; m < n; ++m) {
+                        mfma_phase(m, T_{}, T_{});
+                        end_even();
+                        softmax_phase(m);
+                        end_odd();
+                    }
+                    mfma_phase(m, T_{}, F_{});
+                    end_even();
+                    end_odd();
+                    ++m;
+                }
+                for (; m <= n_blk; ++m) {  // fewer tiles than group 1: keep meeting the barriers
+                    end_even();
+                    end_odd();
+                }
+            } else {
+                // group 1: one phase behind (softmax in even phases, MFMAs in odd phases)
+                if (n > 0) {
+                    start_dma(0);
+                    end_even();
+                    mfma_phase(0, F_{}, T_{});
+                    end_odd();
+                    for (m = 1; m < n; ++m) {
+                        start_dma(m);
+                        softmax_phase(m - 1);
+                        end_even();
+                        mfma_phase(m, T_{}, T_{});
+                        end_odd();
+                    }
+                    start_dma(m);
+                    softmax_phase(m - 1);
+                    end_even();
+                    mfma_phase(m, T_{}, F_{});
+                    end_odd();
+                    ++m;
+                }
+                for (; m <= n_blk; ++m) {  // no tiles left: keep transferring, meet the barriers
+                    start_dma(m);
+                    end_even();
+                    end_odd();
+                }
+            }
+        } else {
         // Stage j & 1 holds tile j. Iteration j first starts tile j+1's transfer into the other
         // stage (free: every wave passed the barrier that ended iteration j-1), computes tile j,
         // then waits for its own transfers and meets the other waves: one barrier per tile.
@@ -565,17 +717,18 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma16(PrefillKArgs ka) {
             if (tile + 1 < n_tiles) dma_tile(tile + 1, STAGE - st_r);
             f32x16_t sacc[2];
             u32x4_t pop[4];
-            compute_s(sacc, std::true_type{});
+            compute_s(sacc, std::true_type{}, no_hook);
             softmax_max(sacc, tile, masked);
             rescale_o();
             softmax_exp(sacc, pop);
-            compute_pv(pop);
+            compute_pv(pop, no_hook);
             wait_dma();
             __syncthreads();
         };
         int tile = 0;
         for (; tile < n_full; ++tile) tile_step(tile, NoMask{});
         for (; tile < n_tiles; ++tile) tile_step(tile, Mask{});
+        }
     } else if constexpr (DB) {
         // Double-buffered: stage j & 1 holds tile j. Tile j+1 (loaded into registers one tile
         // earlier) is stored to the other stage between the softmax and P.V of tile j, then the
@@ -596,7 +749,7 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma16(PrefillKArgs ka) {
             st_k = st_v = st_r;
             f32x16_t sacc[2];
             u32x4_t pop[4];
-            compute_s(sacc, std::true_type{});
+            compute_s(sacc, std::true_type{}, no_hook);
             softmax_max(sacc, tile, masked);
             rescale_o();
             softmax_exp(sacc, pop);
@@ -609,7 +762,7 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma16(PrefillKArgs ka) {
                     load_v(tile + 2);
                 }
             }
-            compute_pv(pop);
+            compute_pv(pop, no_hook);
             __syncthreads();
         };
         int tile = 0;
@@ -630,11 +783,11 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma16(PrefillKArgs ka) {
             }
             f32x16_t sacc[2];
             u32x4_t pop[4];
-            compute_s(sacc, std::true_type{});
+            compute_s(sacc, std::true_type{}, no_hook);
             softmax_max(sacc, tile, masked);
             rescale_o();
             softmax_exp(sacc, pop);
-            compute_pv(pop);
+            compute_pv(pop, no_hook);
             __syncthreads();
         };
         // Two loops, so the mask-free tiles carry no predicated mask code.
@@ -655,7 +808,7 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma16(PrefillKArgs ka) {
             store_v();
             if (n_tiles > 1) load_one(1, kb8, kreg);
             __syncthreads();
-            compute_s(s_a, std::true_type{});
+            compute_s(s_a, std::true_type{}, no_hook);
             if (n_tiles > 1) load_v(1);
             __syncthreads();
             if (n_tiles > 1) {
@@ -668,7 +821,7 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma16(PrefillKArgs ka) {
             rescale_o();
             __syncthreads();
             u32x4_t pop[4];
-            compute_s(nxt, std::true_type{});
+            compute_s(nxt, std::true_type{}, no_hook);
             softmax_exp(cur, pop);
             // 16 K reads + 16 MFMAs of S(j+1) spread through the exponentials of tile j
             FA_SG_MV(7); FA_SG_MV(7); FA_SG_MV(7); FA_SG_MV(7);
@@ -676,7 +829,7 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma16(PrefillKArgs ka) {
             FA_SG_MV(7); FA_SG_MV(7); FA_SG_MV(7); FA_SG_MV(7);
             FA_SG_MV(7); FA_SG_MV(7); FA_SG_MV(7); FA_SG_MV(7);
             __builtin_amdgcn_sched_barrier(0);
-            compute_pv(pop);
+            compute_pv(pop, no_hook);
             __syncthreads();
             if (j + 1 < n_tiles) store_v();
             if (j + 2 < n_tiles) store_k(j + 2);
@@ -919,19 +1072,21 @@ __global__ __launch_bounds__(256, 1) void prefill_mfma_f32(PrefillKArgs ka) {
 // ------------------------------------------------------------------ launcher
 template <typename T, int PMODE, bool ROPEK>
 static void launch16r(const PrefillKArgs& ka, int dpad, dim3 grid, hipStream_t s) {
+    // contiguous K/V, K not rotated in the kernel: the 8-wave ping-pong kernel (when enabled)
+    constexpr int NW = (PMODE == kContig && !ROPEK && prefill_pingpong_enabled()) ? 8 : 4;
     const bool full = ka.a.head_dim == dpad;
     switch (dpad) {
         case 32:
-            full ? prefill_mfma16<T, 32, PMODE, ROPEK, true><<<grid, 256, 0, s>>>(ka)
-                 : prefill_mfma16<T, 32, PMODE, ROPEK, false><<<grid, 256, 0, s>>>(ka);
+            full ? prefill_mfma16<T, 32, PMODE, ROPEK, true, NW><<<grid, 64 * NW, 0, s>>>(ka)
+                 : prefill_mfma16<T, 32, PMODE, ROPEK, false, NW><<<grid, 64 * NW, 0, s>>>(ka);
             break;
         case 64:
-            full ? prefill_mfma16<T, 64, PMODE, ROPEK, true><<<grid, 256, 0, s>>>(ka)
-                 : prefill_mfma16<T, 64, PMODE, ROPEK, false><<<grid, 256, 0, s>>>(ka);
+            full ? prefill_mfma16<T, 64, PMODE, ROPEK, true, NW><<<grid, 64 * NW, 0, s>>>(ka)
+                 : prefill_mfma16<T, 64, PMODE, ROPEK, false, NW><<<grid, 64 * NW, 0, s>>>(ka);
             break;
         default:
-            full ? prefill_mfma16<T, 128, PMODE, ROPEK, true><<<grid, 256, 0, s>>>(ka)
-                 : prefill_mfma16<T, 128, PMODE, ROPEK, false><<<grid, 256, 0, s>>>(ka);
+            full ? prefill_mfma16<T, 128, PMODE, ROPEK, true, NW><<<grid, 64 * NW, 0, s>>>(ka)
+                 : prefill_mfma16<T, 128, PMODE, ROPEK, false, NW><<<grid, 64 * NW, 0, s>>>(ka);
             break;
     }
 }
@@ -971,12 +1126,15 @@ void launch_prefill(Dtype dt, bool paged, const PrefillArgs& a, hipStream_t s, u
     if (paged) ka.ps = FastDiv((uint32_t)a.page_size);
     const int dpad = a.head_dim <= 32 ? 32 : (a.head_dim <= 64 ? 64 : 128);
     const int rows_total = a.q_len * a.group;
-    const int nqb = (rows_total + 127) / 128;
+    // 16-bit contiguous K/V without in-kernel K rotation runs 256-row ping-pong workgroups
+    const bool pp = prefill_pingpong_enabled() && dt != Dtype::F32 && !paged && !a.vt && !a.rope_k;
+    const int bm = pp ? 256 : 128;
+    const int nqb = (rows_total + bm - 1) / bm;
     dim3 g((unsigned)((int64_t)a.batch * a.kv_heads * nqb));
     grid[0] = g.x;
     grid[1] = 1;
     grid[2] = 1;
-    *block = 256;
+    *block = pp ? 512 : 256;
     switch (dt) {
         case Dtype::BF16: launch16<bf16_t>(ka, paged, dpad, g, s); break;
         case Dtype::F16: launch16<f16_t>(ka, paged, dpad, g, s); break;
