@@ -312,6 +312,8 @@ def main():
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--prefill-v-layout", type=int, default=0,
+                    help="1: transposed-V pre-pass for the 16-bit prefill (fa_ctx_set_prefill_v_layout)")
     ap.add_argument("--prefill-policy", type=int, default=-1,
                     help="-1 auto, 0 rotate K on load, 1 pre-rotate K")
     ap.add_argument("--only", choices=["prefill", "decode"], default=None)
@@ -339,6 +341,7 @@ def main():
     rng = np.random.default_rng(1234)
     ctx = fa.HipContext(0)
     ctx.set_prefill_policy(args.prefill_policy)
+    ctx.set_prefill_v_layout(args.prefill_v_layout)
     ev = HipEvents()
     stream = ctx.stream
     ops = []

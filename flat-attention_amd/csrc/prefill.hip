@@ -81,6 +81,27 @@ __device__ __forceinline__ i32x4_t make_rsrc_words(const void* base, int nrec) {
     return r;
 }
 
+#ifndef FA_PREFILL_LPT
+#define FA_PREFILL_LPT 1
+#endif
+// Query block of this workgroup: (batch * kv_heads + kv head, query block index). The blocks
+// an XCD runs form a contiguous chunk of xcd_remap's order; when that chunk is a whole number of
+// (batch, kv head) units it is dispatched heaviest first across its units (query blocks in
+// decreasing causal length, units interleaved), otherwise unit by unit, heaviest first.
+__device__ __forceinline__ void block_coords(int bid, int nb, int nqb, int& bh, int& qb) {
+    const int logical = xcd_remap(bid, nb);
+    const int per_xcd = nb / 8;
+    if (FA_PREFILL_LPT != 0 && nb % 8 == 0 && per_xcd % nqb == 0) {
+        const int units = per_xcd / nqb;
+        const int x = logical / per_xcd, l = logical % per_xcd;
+        bh = x * units + l % units;
+        qb = nqb - 1 - l / units;
+    } else {
+        bh = logical / nqb;
+        qb = nqb - 1 - logical % nqb;
+    }
+}
+
 // Running-max slack (log2 units) tolerated before O is rescaled: probabilities stay <= 2^8.
 constexpr float kRescaleLog2 = 8.0f;
 
@@ -131,6 +152,9 @@ __device__ __forceinline__ int64_t paged_row(const PrefillKArgs& ka, int b, int 
 __host__ __device__ constexpr bool prefill_pingpong_enabled() {
     return FA_PREFILL_PP != 0 && FA_PREFILL_DMA != 0 && FA_PREFILL_DB != 0 && FA_PREFILL_PIPE == 0;
 }
+#ifndef FA_PP_DMA
+#define FA_PP_DMA 0
+#endif
 #ifndef FA_PREFILL_KRING
 #define FA_PREFILL_KRING 4
 #endif
@@ -171,7 +195,8 @@ __global__ __launch_bounds__(64 * NW, 2) void prefill_mfma16(PrefillKArgs ka) {
     constexpr bool VT = PMODE == kContigVT;
     constexpr bool CONTIG = PMODE == kContig || VT;
     constexpr int VTROWB = BN * 2 + 16;     // padded V^T row: 64 keys of one dim (bytes)
-    constexpr int VBYTES = VT ? DPAD * VTROWB : BN * VROWB;
+    // (V^T region rounded to whole KiB: each transfer instruction fills 1 KiB)
+    constexpr int VBYTES = VT ? (DPAD * VTROWB + 1023) / 1024 * 1024 : BN * VROWB;
     // One K/V stage, or two (double buffering: tile j+1 is staged while tile j is computed).
     constexpr bool DB = FA_PREFILL_DB != 0 && !PIPE;
     constexpr int STAGE = BN * KROWB + VBYTES;
@@ -179,11 +204,14 @@ __global__ __launch_bounds__(64 * NW, 2) void prefill_mfma16(PrefillKArgs ka) {
     // registers and no LDS store instructions. One instruction fills 64 consecutive 16-byte
     // slots; padded rows are kept by giving pad slots an out-of-range (zero-filling, no
     // memory traffic) offset. Instructions beyond a tile's slot count target a dummy KiB.
-    constexpr bool DMA = FA_PREFILL_DMA != 0 && DB && PMODE == kContig && !ROPEK;
-    constexpr int KSL = KROWB / 16, VSL = VROWB / 16;  // 16-byte slots per padded row
+    constexpr bool DMA = FA_PREFILL_DMA != 0 && DB && CONTIG && !ROPEK;
+    // 16-byte slots per padded row: K, V, V^T (64 keys of one dim)
+    constexpr int KSL = KROWB / 16, VSL = VROWB / 16, VTSL = VTROWB / 16;
+    // transfer instructions per tile (64 slots each)
+    constexpr int KINS = KSL, VINS = VT ? (DPAD * VTSL + 63) / 64 : VSL;
     // Waves sharing the transfers: all of them, or group 1 alone under the ping-pong schedule.
-    constexpr int NWD = PP ? 4 : NW;
-    constexpr int KI = (KSL + NWD - 1) / NWD, VI = (VSL + NWD - 1) / NWD;  // DMA instrs per wave
+    constexpr int NWD = PP ? (FA_PP_DMA == 2 ? 8 : 4) : NW;
+    constexpr int KI = (KINS + NWD - 1) / NWD, VI = (VINS + NWD - 1) / NWD;  // per wave
     constexpr int DUMMY = 2 * STAGE;
     __shared__ __attribute__((aligned(16))) uint8_t smem[(DB ? 2 : 1) * STAGE + (DMA ? 1024 : 0)];
     int st_r = 0, st_w = 0;  // byte offsets of the stage being read / written
@@ -194,9 +222,8 @@ __global__ __launch_bounds__(64 * NW, 2) void prefill_mfma16(PrefillKArgs ka) {
     const int D = a.head_dim, half = D >> 1;
     const int rows_total = a.q_len * a.group;
     const int nqb = (rows_total + BM - 1) / BM;
-    const int logical = xcd_remap(blockIdx.x, gridDim.x);
-    const int bh = logical / nqb;
-    const int qb = nqb - 1 - logical % nqb;  // heavy (late, causal) blocks dispatch first
+    int bh, qb;  // heavy (late, causal) blocks dispatch first
+    block_coords(blockIdx.x, gridDim.x, nqb, bh, qb);
     const int b = bh / a.kv_heads, kvh = bh % a.kv_heads;
     const int r0 = qb * BM;
 
@@ -557,23 +584,33 @@ __global__ __launch_bounds__(64 * NW, 2) void prefill_mfma16(PrefillKArgs ka) {
         // Per-lane byte offsets of this wave's DMA instructions (k = wave + 4 i fills slots
         // 64 k .. 64 k + 63 of the tile: row q / SL, slot q % SL), constant across tiles.
         constexpr uint32_t kOob = 0x7fff0000u;
-        const int dw = PP ? wave & 3 : wave;  // this wave's index among the transferring waves
+        // this wave's index among the transferring waves
+        const int dw = PP ? (FA_PP_DMA == 2 ? wave : wave & 3) : wave;
         uint32_t koff[KI], voff[VI];
 #pragma unroll
         for (int i = 0; i < KI; ++i) {
             const int q = 64 * (dw + NWD * i) + lane, r = q / KSL, c = q % KSL;
-            koff[i] = (dw + NWD * i < KSL && c < CPR && (FULLD || c * 8 < D))
+            koff[i] = (dw + NWD * i < KINS && c < CPR && (FULLD || c * 8 < D))
                           ? (uint32_t)r * row_bytes + (uint32_t)c * 16u
                           : kOob;
         }
 #pragma unroll
         for (int i = 0; i < VI; ++i) {
-            const int q = 64 * (dw + NWD * i) + lane, r = q / VSL, c = q % VSL;
-            voff[i] = (dw + NWD * i < VSL && c < CPR && (FULLD || c * 8 < D))
-                          ? (uint32_t)r * row_bytes + (uint32_t)c * 16u
-                          : kOob;
+            if constexpr (VT) {
+                // V^T row r = dim r, 64 keys (8 slots) of the tile, then one pad slot
+                const int q = 64 * (dw + NWD * i) + lane, r = q / VTSL, c = q % VTSL;
+                voff[i] = (dw + NWD * i < VINS && c < 8 && r < D)
+                              ? ((uint32_t)r * (uint32_t)a.vt_row + (uint32_t)c * 8u) * 2u
+                              : kOob;
+            } else {
+                const int q = 64 * (dw + NWD * i) + lane, r = q / VSL, c = q % VSL;
+                voff[i] = (dw + NWD * i < VINS && c < CPR && (FULLD || c * 8 < D))
+                              ? (uint32_t)r * row_bytes + (uint32_t)c * 16u
+                              : kOob;
+            }
         }
         const int nrec_all = (a.kv_len - 1) * (int)row_bytes + D * 2;
+        const int nrec_vt = VT ? D * a.vt_row * 2 : 0;
         // Tile `tile` of K and V into the stage at byte offset `st`.
         const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_void_t*)smem;
         // One transfer instruction (i-th of this wave) of tile `tile` of K / V into stage `st`.
@@ -581,14 +618,20 @@ __global__ __launch_bounds__(64 * NW, 2) void prefill_mfma16(PrefillKArgs ka) {
             const int base = tile * BN * (int)row_bytes;
             const i32x4_t rk = make_rsrc_words(kb8 + base, nrec_all - base);
             const int k = dw + NWD * i;
-            const int dst = k < KSL ? st + k * 1024 : DUMMY;
+            const int dst = k < KINS ? st + k * 1024 : DUMMY;
             buffer_to_lds16(rk, __builtin_amdgcn_readfirstlane(lds0 + dst), koff[i]);
         };
         auto dma_v1 = [&](int tile, int st, int i) {
-            const int base = tile * BN * (int)row_bytes;
-            const i32x4_t rv = make_rsrc_words(vb8 + base, nrec_all - base);
+            i32x4_t rv;
+            if constexpr (VT) {
+                const int base = tile * BN * 2;  // key offset within every V^T row
+                rv = make_rsrc_words(vtb8 + base, nrec_vt - base);
+            } else {
+                const int base = tile * BN * (int)row_bytes;
+                rv = make_rsrc_words(vb8 + base, nrec_all - base);
+            }
             const int k = dw + NWD * i;
-            const int dst = k < VSL ? st + BN * KROWB + k * 1024 : DUMMY;
+            const int dst = k < VINS ? st + BN * KROWB + k * 1024 : DUMMY;
             buffer_to_lds16(rv, __builtin_amdgcn_readfirstlane(lds0 + dst), voff[i]);
         };
         auto dma_k = [&](int tile, int st) {
@@ -641,7 +684,10 @@ __global__ __launch_bounds__(64 * NW, 2) void prefill_mfma16(PrefillKArgs ka) {
             // waited for at the end of phase 2m+1, before their first reader (phase 2m+2).
             // Group 1 issues every transfer, at the start of its softmax phases: the VALU phase
             // has slack, the MFMA stream of group 0 is left alone.
+            // waves that issue the transfers (FA_PP_DMA: 0 group 1, 1 group 0, 2 all)
+            const bool xfer = FA_PP_DMA == 2 || (FA_PP_DMA == 0 ? grp == 1 : grp == 0);
             auto start_dma = [&](int m) {
+                if (!xfer) return;
                 if (m + 1 < n_blk) dma_k(m + 1, ((m + 1) & 1) * STAGE);
                 if (m < n_blk) dma_v(m, (m & 1) * STAGE);
             };
@@ -650,7 +696,7 @@ __global__ __launch_bounds__(64 * NW, 2) void prefill_mfma16(PrefillKArgs ka) {
                 wait_dma();
                 __syncthreads();
             };
-            if (n_blk > 0 && wave >= 4) dma_k(0, 0);
+            if (n_blk > 0 && xfer) dma_k(0, 0);
             wait_dma();
             __syncthreads();
             int m = 0;
@@ -658,22 +704,26 @@ __global__ __launch_bounds__(64 * NW, 2) void prefill_mfma16(PrefillKArgs ka) {
             if (grp == 0) {
                 // group 0: MFMAs in even phases, softmax in odd phases
                 if (n > 0) {
+                    start_dma(0);
                     mfma_phase(0, F_{}, T_{});
                     end_even();
                     softmax_phase(0);
                     end_odd();
                     for (m = 1; m < n; ++m) {
+                        start_dma(m);
                         mfma_phase(m, T_{}, T_{});
                         end_even();
                         softmax_phase(m);
                         end_odd();
                     }
+                    start_dma(m);
                     mfma_phase(m, T_{}, F_{});
                     end_even();
                     end_odd();
                     ++m;
                 }
                 for (; m <= n_blk; ++m) {  // fewer tiles than group 1: keep meeting the barriers
+                    start_dma(m);
                     end_even();
                     end_odd();
                 }
@@ -888,9 +938,8 @@ __global__ __launch_bounds__(256, 1) void prefill_mfma_f32(PrefillKArgs ka) {
     const int D = a.head_dim, half = D >> 1;
     const int rows_total = a.q_len * a.group;
     const int nqb = (rows_total + BM - 1) / BM;
-    const int logical = xcd_remap(blockIdx.x, gridDim.x);
-    const int bh = logical / nqb;
-    const int qb = nqb - 1 - logical % nqb;
+    int bh, qb;
+    block_coords(blockIdx.x, gridDim.x, nqb, bh, qb);
     const int b = bh / a.kv_heads, kvh = bh % a.kv_heads;
     const int r0 = qb * BM;
     const int row = r0 + wave * 32 + (lane & 31);
@@ -1073,7 +1122,8 @@ __global__ __launch_bounds__(256, 1) void prefill_mfma_f32(PrefillKArgs ka) {
 template <typename T, int PMODE, bool ROPEK>
 static void launch16r(const PrefillKArgs& ka, int dpad, dim3 grid, hipStream_t s) {
     // contiguous K/V, K not rotated in the kernel: the 8-wave ping-pong kernel (when enabled)
-    constexpr int NW = (PMODE == kContig && !ROPEK && prefill_pingpong_enabled()) ? 8 : 4;
+    constexpr int NW =
+        ((PMODE == kContig || PMODE == kContigVT) && !ROPEK && prefill_pingpong_enabled()) ? 8 : 4;
     const bool full = ka.a.head_dim == dpad;
     switch (dpad) {
         case 32:
@@ -1127,7 +1177,7 @@ void launch_prefill(Dtype dt, bool paged, const PrefillArgs& a, hipStream_t s, u
     const int dpad = a.head_dim <= 32 ? 32 : (a.head_dim <= 64 ? 64 : 128);
     const int rows_total = a.q_len * a.group;
     // 16-bit contiguous K/V without in-kernel K rotation runs 256-row ping-pong workgroups
-    const bool pp = prefill_pingpong_enabled() && dt != Dtype::F32 && !paged && !a.vt && !a.rope_k;
+    const bool pp = prefill_pingpong_enabled() && dt != Dtype::F32 && !paged && !a.rope_k;
     const int bm = pp ? 256 : 128;
     const int nqb = (rows_total + bm - 1) / bm;
     dim3 g((unsigned)((int64_t)a.batch * a.kv_heads * nqb));
