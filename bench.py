@@ -171,6 +171,26 @@ def build_chunked_paged(ctx, rng):
     return (lambda: plan.launch(q, kp, vp, out)), flop, append, append_bytes
 
 
+def build_resident_decode(ctx, rng, dtype):
+    """The reference's only published decode shape (M15/M48, docs/M48_THOR_REQUALIFICATION.md:69):
+    B1 Hq16 Hkv4 D64 over 8192 resident rows (pre-rotated K), query at position 8191."""
+    B, hq, hkv, D, cap = 1, 16, 4, 64, 8192
+    width = hkv * D
+    if dtype == fa.DTYPE_F32:
+        mk = lambda n: rng.standard_normal(n, dtype=np.float32)  # noqa: E731
+    else:
+        mk = lambda n: bf16_normal(rng, n)  # noqa: E731
+    k = fa.DeviceBuffer.from_array(ctx, mk(B * cap * width))
+    v = fa.DeviceBuffer.from_array(ctx, mk(B * cap * width))
+    q = fa.DeviceBuffer.from_array(ctx, mk(B * hq * D))
+    plan = fa.ResidentDecodePlan(ctx, B, cap, cap, hq, hkv, D, fa.FlatAttentionConfig(True), 1e4,
+                                 cap - 1, dtype)
+    out = fa.DeviceBuffer(ctx, plan.layout().combined_bytes)
+    eb = 4 if dtype == fa.DTYPE_F32 else 2
+    nbytes = 2.0 * B * cap * width * eb + B * hq * D * eb * 2 + B * hq * 4
+    return (lambda: plan.launch(q, k, v, out)), nbytes
+
+
 def measure_all_configs(ctx, ev, rng, steps):
     """The other BASELINE configs, each timed alone (op events + its kernel's own events)."""
     stream = ctx.stream
@@ -209,6 +229,15 @@ def measure_all_configs(ctx, ev, rng, steps):
     res["cfg5_batched_append_512"] = {
         "kernel": tel.kernel_name, "ms": round(op_ms, 4), "kernel_ms": round(k_ms, 4),
         "GB/s": round(append_bytes / (k_ms * 1e-3) / 1e9, 1)}
+    for dt, name in ((fa.DTYPE_F32, "f32"), (fa.DTYPE_BF16, "bf16")):
+        run, nbytes = build_resident_decode(ctx, rng, dt)
+        op_ms, k_ms, tel = timed(run)
+        res[f"resident_decode_B1_Hq16_Hkv4_D64_kv8192_{name}"] = {
+            "kernel": tel.kernel_name, "ms": round(op_ms, 4), "kernel_ms": round(k_ms, 4),
+            "GB/s": round(nbytes / (k_ms * 1e-3) / 1e9, 1),
+            "note": "one sequence: the op time is launch-bound, GB/s uses the kernel time",
+            "reference_published_ms": {"M15": 23.843433, "M48": 19.562844,
+                                       "hardware": "Jetson Thor, Vulkan, f32 (not comparable)"}}
     return res
 
 

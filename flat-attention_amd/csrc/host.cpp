@@ -354,6 +354,8 @@ const char* fa_status_string(int s) {
         case FA_ERR_ZERO_QUERY_CHUNK_SIZE: return "ZeroQueryChunkSize";
         case FA_ERR_UNSUPPORTED_DTYPE: return "UnsupportedDtype";
         case FA_ERR_INVALID_PAGE: return "InvalidPage";
+        case FA_ERR_EMPTY_CACHE: return "EmptyCache";
+        case FA_ERR_INVALID_CACHE_LENGTH: return "InvalidCacheLength";
         case FA_ERR_PAGED_ZERO_DIMENSION: return "PagedZeroDimension";
         case FA_ERR_CAPACITY_OVERFLOW: return "CapacityOverflow";
         case FA_ERR_CAPACITY_EXCEEDED: return "CapacityExceeded";
@@ -1668,6 +1670,165 @@ int fa_paged_cache_decode(fa_ctx* ctx, const fa_paged_cache* c, const void* q, s
     if (int rc = fa_paged_decode_prepare(ctx, row.data(), mapped, &len, &qp, 1, c->table.page_size,
                                          c->table.physical_pages, q_heads, c->kv_heads,
                                          c->head_dim, cfg, theta, c->dtype, &p))
+        return rc;
+    const uint32_t allocs = ctx->call_allocs;
+    const uint64_t abytes = ctx->call_alloc_bytes;
+    int rc = fa_paged_decode_launch(ctx, p, q, q_bytes, c->k, c->v, c->tensor_bytes, out_lse,
+                                    out_bytes);
+    ctx->last.temporary_allocation_count += allocs;
+    ctx->last.temporary_allocation_bytes += abytes;
+    fa_paged_decode_plan_destroy(p);
+    return rc ? rc : ok();
+}
+
+// ---------------------------------------------------------------------------- resident KV
+// WgpuResidentKvCache src/wgpu_kv_cache.rs:79: fixed-capacity K and V
+// [batch, capacity, kv_heads*head_dim] with one logical length shared by the batch.
+struct fa_resident_cache {
+    fa_ctx* ctx = nullptr;
+    uint64_t batch = 0, kv_heads = 0, capacity = 0, head_dim = 0, row_bytes = 0;
+    uint64_t tensor_bytes = 0, len = 0;
+    int dtype = 0;
+    void* k = nullptr;
+    void* v = nullptr;
+};
+
+int fa_resident_cache_create(fa_ctx* ctx, uint64_t batch, uint64_t kv_heads, uint64_t capacity,
+                             uint64_t head_dim, int dtype, fa_resident_cache** out) {
+    if (!ctx || !out) return fail(FA_ERR_NULL_ARGUMENT, "null argument");
+    *out = nullptr;
+    if (int rc = check_dtype(dtype)) return rc;
+    if (!batch || !kv_heads || !capacity || !head_dim)
+        return fail(FA_ERR_ZERO_DIMENSION, "resident KV cache dimensions must be non-zero");
+    uint64_t row_el, row_b, rows, bytes;
+    if (mul_ov(kv_heads, head_dim, &row_el) || mul_ov(row_el, elem_bytes(dtype), &row_b) ||
+        mul_ov(batch, capacity, &rows) || mul_ov(rows, row_b, &bytes))
+        return fail(FA_ERR_SHAPE_OVERFLOW, "resident KV cache shape overflows the address space");
+    if (int rc = set_device(ctx)) return rc;
+    fa_resident_cache* c = new fa_resident_cache();
+    c->ctx = ctx;
+    c->batch = batch;
+    c->kv_heads = kv_heads;
+    c->capacity = capacity;
+    c->head_dim = head_dim;
+    c->row_bytes = row_b;
+    c->tensor_bytes = bytes;
+    c->dtype = dtype;
+    if (hipMalloc(&c->k, bytes) != hipSuccess || hipMalloc(&c->v, bytes) != hipSuccess) {
+        if (c->k) (void)hipFree(c->k);
+        delete c;
+        return fail(FA_ERR_HIP, "resident KV cache requires %llu bytes per tensor",
+                    (unsigned long long)bytes);
+    }
+    *out = c;
+    return ok();
+}
+
+int fa_resident_cache_destroy(fa_resident_cache* c) {
+    if (!c) return ok();
+    (void)hipSetDevice(c->ctx->device);
+    (void)hipStreamSynchronize(c->ctx->stream);
+    (void)hipFree(c->k);
+    (void)hipFree(c->v);
+    delete c;
+    return ok();
+}
+
+// record_append src/wgpu_kv_cache.rs:212: batch b's source rows [b, append_len) land at cache
+// rows b*capacity + len ..; the prefix is never moved; the length advances once every copy of
+// the append is enqueued.
+int fa_resident_cache_append(fa_resident_cache* c, const void* k_src, const void* v_src,
+                             size_t src_bytes, uint64_t append_len, uint64_t* new_len) {
+    if (!c) return fail(FA_ERR_NULL_ARGUMENT, "cache is null");
+    fa_ctx* ctx = c->ctx;
+    begin_call(ctx);
+    if (append_len == 0)
+        return fail(FA_ERR_ZERO_DIMENSION, "resident KV cache dimensions must be non-zero");
+    const uint64_t grown = c->len + append_len;
+    if (grown < c->len)
+        return fail(FA_ERR_SHAPE_OVERFLOW, "resident KV cache shape overflows the address space");
+    if (grown > c->capacity)
+        return fail(FA_ERR_CAPACITY_EXCEEDED,
+                    "resident KV cache append %llu at length %llu exceeds capacity %llu",
+                    (unsigned long long)append_len, (unsigned long long)c->len,
+                    (unsigned long long)c->capacity);
+    uint64_t per_batch, need;
+    if (mul_ov(append_len, c->row_bytes, &per_batch) || mul_ov(c->batch, per_batch, &need))
+        return fail(FA_ERR_SHAPE_OVERFLOW, "resident KV cache shape overflows the address space");
+    if (int rc = check_buffer("K", k_src, src_bytes, need)) return rc;
+    if (int rc = check_buffer("V", v_src, src_bytes, need)) return rc;
+    if (int rc = set_device(ctx)) return rc;
+    // one strided copy per tensor: batch rows of per_batch bytes, pitches src per_batch,
+    // dst capacity*row_bytes
+    const size_t dpitch = (size_t)(c->capacity * c->row_bytes);
+    uint8_t* kd = (uint8_t*)c->k + c->len * c->row_bytes;
+    uint8_t* vd = (uint8_t*)c->v + c->len * c->row_bytes;
+    HIP_TRY(hipMemcpy2DAsync(kd, dpitch, k_src, (size_t)per_batch, (size_t)per_batch,
+                             (size_t)c->batch, hipMemcpyDeviceToDevice, ctx->stream));
+    HIP_TRY(hipMemcpy2DAsync(vd, dpitch, v_src, (size_t)per_batch, (size_t)per_batch,
+                             (size_t)c->batch, hipMemcpyDeviceToDevice, ctx->stream));
+    c->len = grown;
+    if (new_len) *new_len = grown;
+    unsigned grid[3] = {(unsigned)append_len, (unsigned)c->batch, 1};
+    record(ctx, FA_KERNEL_PAGED_APPEND, "resident append (strided copies)", 0,
+           (uint32_t)c->capacity, grid, 0, 2, 1, nullptr);
+    return ok();
+}
+
+int fa_resident_cache_reset(fa_resident_cache* c) {  // reset :200 (metadata only)
+    if (!c) return fail(FA_ERR_NULL_ARGUMENT, "cache is null");
+    c->len = 0;
+    return ok();
+}
+
+uint64_t fa_resident_cache_len(const fa_resident_cache* c) { return c ? c->len : 0; }
+void* fa_resident_cache_k(fa_resident_cache* c) { return c ? c->k : nullptr; }
+void* fa_resident_cache_v(fa_resident_cache* c) { return c ? c->v : nullptr; }
+size_t fa_resident_cache_bytes(const fa_resident_cache* c) { return c ? (size_t)c->tensor_bytes : 0; }
+
+// WgpuResidentDecodePipeline::encode_external_pre_rotated_k src/wgpu_decode.rs:301 (checks in
+// the order of validate_external_semantics :419 and validate_kv_view :467). The fixed-capacity
+// layout is a page pool with one page of `capacity` rows per batch element, so the plan is a
+// paged decode plan whose block table row b is [b].
+int fa_resident_decode_prepare(fa_ctx* ctx, uint64_t batch, uint64_t capacity, uint64_t kv_len,
+                               uint64_t q_heads, uint64_t kv_heads, uint64_t head_dim,
+                               const fa_config* cfg, float theta, uint64_t q_rope_position,
+                               int dtype, fa_decode_plan** out) {
+    if (!out) return fail(FA_ERR_NULL_ARGUMENT, "null argument");
+    *out = nullptr;
+    if (cfg && cfg->causal && q_rope_position + 1 < kv_len)
+        return fail(FA_ERR_CAUSAL_VISIBILITY_MISMATCH,
+                    "resident causal decode query position %llu cannot see all %llu live KV rows",
+                    (unsigned long long)q_rope_position, (unsigned long long)kv_len);
+    if (!batch || !kv_heads || !capacity || !head_dim)
+        return fail(FA_ERR_ZERO_DIMENSION, "attention dimensions must all be non-zero");
+    if (kv_len == 0) return fail(FA_ERR_EMPTY_CACHE, "resident decode requires at least one live KV row");
+    if (kv_len > capacity)
+        return fail(FA_ERR_INVALID_CACHE_LENGTH,
+                    "resident decode live KV length %llu exceeds physical capacity %llu",
+                    (unsigned long long)kv_len, (unsigned long long)capacity);
+    if (batch > kI32 || capacity > kI32 || kv_len > kI32 || q_rope_position > kI32)
+        return fail(FA_ERR_INDEX_SPACE_EXCEEDED, "resident decode exceeds the i32 index space");
+    std::vector<int32_t> table(batch), lens(batch, (int32_t)kv_len), qpos(batch, (int32_t)q_rope_position);
+    for (uint64_t b = 0; b < batch; ++b) table[b] = (int32_t)b;
+    return fa_paged_decode_prepare(ctx, table.data(), 1, lens.data(), qpos.data(), batch, capacity,
+                                   batch, q_heads, kv_heads, head_dim, cfg, theta, dtype, out);
+}
+
+// WgpuResidentDecodePipeline::encode src/wgpu_decode.rs:265: decode over the cache's live rows.
+int fa_resident_cache_decode(fa_ctx* ctx, const fa_resident_cache* c, const void* q,
+                             size_t q_bytes, uint64_t q_heads, const fa_config* cfg, float theta,
+                             uint64_t q_rope_position, void* out_lse, size_t out_bytes) {
+    if (!ctx || !c) return fail(FA_ERR_NULL_ARGUMENT, "null argument");
+    // encode_view :332 checks no causal visibility (the pass carries no causal position);
+    // decode attends every live row either way
+    fa_config nc{};
+    if (cfg) nc = *cfg;
+    nc.causal = 0;
+    fa_decode_plan* p = nullptr;
+    if (int rc = fa_resident_decode_prepare(ctx, c->batch, c->capacity, c->len, q_heads,
+                                            c->kv_heads, c->head_dim, &nc, theta,
+                                            q_rope_position, c->dtype, &p))
         return rc;
     const uint32_t allocs = ctx->call_allocs;
     const uint64_t abytes = ctx->call_alloc_bytes;

@@ -11,7 +11,8 @@ from .api import (AsymmetricGroupedAttentionShape, AsymmetricRotaryEmbeddingConf
                   AttentionShape, DeviceBuffer, FlatAttentionConfig, FlatAttentionOutput,
                   GroupedAttentionShape, HipAsymmetricProjectionPipeline,
                   HipChunkedProjectionPrefillPipeline, HipContext, HipFlatAttention,
-                  HipPagedDecodePipeline, HipPagedKvCache, HipRotaryGroupedAttention,
+                  HipPagedDecodePipeline, HipPagedKvCache, HipResidentDecodePipeline,
+                  HipResidentKvCache, HipRotaryGroupedAttention, ResidentDecodePlan,
                   PackedLayout, PagedChunkedPrefillPlan, PagedDecodePlan, PagedKvAddress,
                   PagedKvConfig, PagedKvTable, PagedKvTelemetry, RotaryEmbeddingConfig,
                   RuntimeDispatchTelemetry, bf16_bits_to_f32, download_attention,

@@ -32,7 +32,7 @@ STATUS = {
     21: "UnsupportedHeadDim", 22: "IndexSpaceExceeded", 23: "DispatchLimit",
     24: "BufferTooSmall", 25: "EmptyTable", 26: "TooManyMappedPages",
     27: "CausalVisibilityMismatch", 28: "ZeroQueryChunkSize", 29: "UnsupportedDtype",
-    30: "InvalidPage", 40: "PagedZeroDimension", 41: "CapacityOverflow",
+    30: "InvalidPage", 31: "EmptyCache", 32: "InvalidCacheLength", 40: "PagedZeroDimension", 41: "CapacityOverflow",
     42: "CapacityExceeded", 43: "GenerationOverflow", 50: "NullArgument", 60: "Hip",
 }
 
@@ -151,6 +151,17 @@ PROTOTYPES = {
     "fa_paged_decode_plan_info": (INT, [VP, P(U64), P(U64), P(U64)]),
     "fa_paged_decode_plan_set_split": (INT, [VP, VP, U64]),
     "fa_paged_cache_decode": (INT, [VP, VP, VP, SZ, U64, P(ConfigC), F32, U64, VP, SZ]),
+    "fa_resident_cache_create": (INT, [VP, U64, U64, U64, U64, INT, P(VP)]),
+    "fa_resident_cache_destroy": (INT, [VP]),
+    "fa_resident_cache_append": (INT, [VP, VP, VP, SZ, U64, P(U64)]),
+    "fa_resident_cache_reset": (INT, [VP]),
+    "fa_resident_cache_len": (U64, [VP]),
+    "fa_resident_cache_k": (VP, [VP]),
+    "fa_resident_cache_v": (VP, [VP]),
+    "fa_resident_cache_bytes": (SZ, [VP]),
+    "fa_resident_decode_prepare": (INT, [VP, U64, U64, U64, U64, U64, U64, P(ConfigC), F32, U64,
+                                         INT, P(VP)]),
+    "fa_resident_cache_decode": (INT, [VP, VP, VP, SZ, U64, P(ConfigC), F32, U64, VP, SZ]),
     "fa_chunked_prefill_paged_prepare": (INT, [VP, VP, U64, U64, U64, P(AsymmetricShapeC),
                                                P(ConfigC), P(AsymmetricRotaryC), INT, P(VP)]),
     "fa_chunked_prefill_paged_launch": (INT, [VP, VP, VP, SZ, VP, VP, SZ, VP, SZ]),

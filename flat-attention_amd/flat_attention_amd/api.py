@@ -685,6 +685,119 @@ class HipPagedDecodePipeline:
         return self.layout(q_heads, cache.head_dim)
 
 
+class HipResidentKvCache:
+    """WgpuResidentKvCache src/wgpu_kv_cache.rs:79: fixed-capacity K/V
+    [batch, capacity, kv_heads*head_dim], one live length shared by the batch."""
+
+    def __init__(self, ctx: HipContext, batch: int, kv_heads: int, capacity: int, head_dim: int,
+                 dtype: int = L.DTYPE_F32):
+        h = L.VP()
+        check(lib().fa_resident_cache_create(ctx.handle, batch, kv_heads, capacity, head_dim,
+                                             dtype, ctypes.byref(h)))
+        self.ctx, self.handle, self.dtype = ctx, h.value, dtype
+        self.batch, self.kv_heads, self.capacity, self.head_dim = batch, kv_heads, capacity, head_dim
+        ctx._adopt(self)
+
+    def release(self):
+        if getattr(self, "handle", None) and self.ctx.handle:
+            lib().fa_resident_cache_destroy(self.handle)
+        self.handle = None
+
+    def __del__(self):
+        self.release()
+
+    def __len__(self) -> int:
+        return lib().fa_resident_cache_len(self.handle)
+
+    def remaining_capacity(self) -> int:  # :184
+        return self.capacity - len(self)
+
+    def k_buffer(self) -> DeviceBuffer:
+        return DeviceBuffer(self.ctx, lib().fa_resident_cache_bytes(self.handle),
+                            lib().fa_resident_cache_k(self.handle), owned=False)
+
+    def v_buffer(self) -> DeviceBuffer:
+        return DeviceBuffer(self.ctx, lib().fa_resident_cache_bytes(self.handle),
+                            lib().fa_resident_cache_v(self.handle), owned=False)
+
+    def record_append(self, k_source: DeviceBuffer, v_source: DeviceBuffer, append_len: int) -> int:
+        """record_append :212 (sources [batch, append_len, kv_heads*head_dim], K pre-rotated)."""
+        n = L.U64()
+        check(lib().fa_resident_cache_append(self.handle, k_source.ptr, v_source.ptr,
+                                             min(k_source.nbytes, v_source.nbytes), append_len,
+                                             ctypes.byref(n)))
+        return n.value
+
+    def reset(self):
+        check(lib().fa_resident_cache_reset(self.handle))
+
+
+class ResidentDecodePlan(PagedDecodePlan):
+    """WgpuResidentDecodePipeline::encode_external_pre_rotated_k src/wgpu_decode.rs:301 over
+    framework-owned [batch, capacity, kv_heads*head_dim] K (pre-rotated) / V; launch() takes the
+    two K/V buffers in place of a page pool."""
+
+    def __init__(self, ctx: HipContext, batch: int, capacity: int, kv_len: int, q_heads: int,
+                 kv_heads: int, head_dim: int, config: FlatAttentionConfig, theta: float,
+                 q_rope_position: int, dtype: int):
+        h = L.VP()
+        check(lib().fa_resident_decode_prepare(ctx.handle, batch, capacity, kv_len, q_heads,
+                                               kv_heads, head_dim, ctypes.byref(config.c()),
+                                               theta, q_rope_position, dtype, ctypes.byref(h)))
+        self.ctx, self.handle, self.dtype = ctx, h.value, dtype
+        self.n_seqs, self.q_heads, self.head_dim = batch, q_heads, head_dim
+        ctx._adopt(self)
+
+
+class HipResidentDecodePipeline:
+    """WgpuResidentDecodePipeline src/wgpu_decode.rs:214 (q_len = 1 decode over resident K/V)."""
+
+    def __init__(self, ctx: HipContext, dtype: int = L.DTYPE_F32):
+        self.ctx = ctx
+        self.dtype = dtype
+
+    def layout(self, batch: int, q_heads: int, head_dim: int) -> PackedLayout:
+        return packed_layout(batch * q_heads * head_dim, batch * q_heads, self.dtype)
+
+    def create_output_buffer(self, cache: HipResidentKvCache, q_heads: int) -> DeviceBuffer:
+        return DeviceBuffer(self.ctx, self.layout(cache.batch, q_heads, cache.head_dim).combined_bytes)
+
+    def encode(self, q: DeviceBuffer, cache: HipResidentKvCache, out_and_lse: DeviceBuffer,
+               q_heads: int, config: FlatAttentionConfig, theta: float,
+               q_rope_position: int) -> PackedLayout:
+        """encode :265 (ResidentDecodePass over FLAT's cache)."""
+        check(lib().fa_resident_cache_decode(self.ctx.handle, cache.handle, q.ptr, q.nbytes,
+                                             q_heads, ctypes.byref(config.c()), theta,
+                                             q_rope_position, out_and_lse.ptr, out_and_lse.nbytes))
+        return self.layout(cache.batch, q_heads, cache.head_dim)
+
+    def encode_external_pre_rotated_k(self, q: DeviceBuffer, k: DeviceBuffer, v: DeviceBuffer,
+                                      out_and_lse: DeviceBuffer,
+                                      shape: "AsymmetricGroupedAttentionShape",
+                                      config: FlatAttentionConfig,
+                                      rotary: "AsymmetricRotaryEmbeddingConfig",
+                                      kv_capacity: int) -> PackedLayout:
+        """encode_external_pre_rotated_k :301. shape.query_len must be 1 (else InvalidQueryLen
+        in the reference; here LengthMismatch)."""
+        if shape.query_len != 1:
+            raise L.FlatHipError(7, f"specialized resident decode requires query_len=1, got "
+                                  f"{shape.query_len}")
+        # validate_external_semantics :419: causal visibility uses the shape's query position
+        # (RoPE uses the rotary one); a q_len = 1 decode then attends every live row either way
+        if config.causal and shape.query_position_offset + 1 < shape.kv_len:
+            raise L.FlatHipError(27, f"resident causal decode query position "
+                                   f"{shape.query_position_offset} cannot see all {shape.kv_len} "
+                                   f"live KV rows")
+        plan = ResidentDecodePlan(self.ctx, shape.batch, kv_capacity, shape.kv_len, shape.q_heads,
+                                  shape.kv_heads, shape.head_dim,
+                                  FlatAttentionConfig(False, config.softmax_scale), rotary.theta,
+                                  rotary.query_position_offset, self.dtype)
+        plan.launch(q, k, v, out_and_lse)
+        layout = plan.layout()
+        plan.release()
+        return layout
+
+
 class PagedChunkedPrefillPlan:
     """Chunked prefill of a query chunk over a shared paged cache (pre-rotated K)."""
 

@@ -63,6 +63,8 @@ typedef enum fa_status {
     FA_ERR_ZERO_QUERY_CHUNK_SIZE = 28,
     FA_ERR_UNSUPPORTED_DTYPE = 29,
     FA_ERR_INVALID_PAGE = 30,
+    FA_ERR_EMPTY_CACHE = 31,          /* ResidentDecodeError::EmptyCache src/wgpu_decode.rs:105 */
+    FA_ERR_INVALID_CACHE_LENGTH = 32, /* ResidentDecodeError::InvalidCacheLength :106 */
     FA_ERR_PAGED_ZERO_DIMENSION = 40,
     FA_ERR_CAPACITY_OVERFLOW = 41,
     FA_ERR_CAPACITY_EXCEEDED = 42,
@@ -320,6 +322,44 @@ int fa_paged_cache_decode(fa_ctx* ctx, const fa_paged_cache* cache, const void* 
                           size_t q_bytes, uint64_t q_heads, const fa_config* config,
                           float theta, uint64_t q_rope_position, void* out_lse,
                           size_t out_bytes);
+
+/* ------------------------------------------------------------ resident KV cache ---------
+ * WgpuResidentKvCache src/wgpu_kv_cache.rs:79: fixed-capacity K and V storage
+ * [batch, capacity, kv_heads*head_dim] in `dtype`, one live length shared by the batch. */
+typedef struct fa_resident_cache fa_resident_cache;
+int fa_resident_cache_create(fa_ctx* ctx, uint64_t batch, uint64_t kv_heads, uint64_t capacity,
+                             uint64_t head_dim, int dtype, fa_resident_cache** out); /* new :104 */
+int fa_resident_cache_destroy(fa_resident_cache* cache);
+/* record_append :212. Sources are device [batch, append_len, kv_heads*head_dim]; K is already
+ * RoPE-rotated (the decode contract). Rows land after the live prefix of every batch element;
+ * FA_ERR_CAPACITY_EXCEEDED when len + append_len > capacity. */
+int fa_resident_cache_append(fa_resident_cache* cache, const void* k_src, const void* v_src,
+                             size_t src_bytes, uint64_t append_len, uint64_t* new_len);
+int fa_resident_cache_reset(fa_resident_cache* cache);               /* reset :200 */
+uint64_t fa_resident_cache_len(const fa_resident_cache* cache);       /* len :174 */
+void* fa_resident_cache_k(fa_resident_cache* cache);                  /* k_buffer :189 */
+void* fa_resident_cache_v(fa_resident_cache* cache);                  /* v_buffer :194 */
+size_t fa_resident_cache_bytes(const fa_resident_cache* cache);        /* bytes of K (= of V) */
+
+/* ------------------------------------------------------------ resident decode -----------
+ * WgpuResidentDecodePipeline::encode_external_pre_rotated_k src/wgpu_decode.rs:301: q_len = 1
+ * decode of `batch` queries over framework-owned fixed-capacity K (pre-rotated) and V
+ * [batch, capacity, kv_heads*head_dim], kv_len live rows each, Q rotated at q_rope_position.
+ * Validation follows the reference (causal visibility, zero dimensions, EmptyCache,
+ * InvalidCacheLength, head_dim, head grouping, theta, scale). The returned plan launches with
+ * fa_paged_decode_launch(ctx, plan, q, q_bytes, k, v, kv_bytes, out_lse, out_bytes): the layout
+ * is a page pool with one `capacity`-row page per batch element. Output [O | LSE] as for paged
+ * decode (batch*q_heads rows). */
+int fa_resident_decode_prepare(fa_ctx* ctx, uint64_t batch, uint64_t capacity, uint64_t kv_len,
+                               uint64_t q_heads, uint64_t kv_heads, uint64_t head_dim,
+                               const fa_config* config, float theta, uint64_t q_rope_position,
+                               int dtype, fa_decode_plan** out);
+/* WgpuResidentDecodePipeline::encode src/wgpu_decode.rs:265: decode over a resident cache's live
+ * rows (prepares, launches and releases a plan; waits for the stream when releasing). */
+int fa_resident_cache_decode(fa_ctx* ctx, const fa_resident_cache* cache, const void* q,
+                             size_t q_bytes, uint64_t q_heads, const fa_config* config,
+                             float theta, uint64_t q_rope_position, void* out_lse,
+                             size_t out_bytes);
 
 /* ------------------------------------------------------------ chunked prefill (paged) ---
  * Chunked prefill whose K/V live in the shared page pool: the chunk's queries

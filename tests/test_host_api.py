@@ -203,6 +203,34 @@ def test_decode_prepare_validation_variants():
     assert _decode_prepare(bt, [40]) == "NullArgument"  # all valid, no context
 
 
+def _resident_prepare(batch=2, cap=64, kv_len=40, hq=4, hkv=2, D=64, theta=1e4, qpos=39,
+                      causal=True, dtype=fa.DTYPE_F32):
+    h = L.VP()
+    rc = fa.lib().fa_resident_decode_prepare(None, batch, cap, kv_len, hq, hkv, D,
+                                             ctypes.byref(fa.FlatAttentionConfig(causal).c()),
+                                             theta, qpos, dtype, ctypes.byref(h))
+    return _variant(rc)
+
+
+def test_resident_decode_prepare_validation_variants():
+    """ResidentDecodeError variants in the reference's check order (src/wgpu_decode.rs:419-510):
+    causal visibility first, then zero dimensions, EmptyCache, InvalidCacheLength, head_dim,
+    head grouping, theta; a null context is reported only once everything else is valid."""
+    assert _resident_prepare(qpos=20) == "CausalVisibilityMismatch"
+    assert _resident_prepare(qpos=20, causal=False) == "NullArgument"
+    assert _resident_prepare(qpos=20, batch=0) == "CausalVisibilityMismatch"
+    assert _resident_prepare(batch=0) == "ZeroDimension"
+    assert _resident_prepare(cap=0, kv_len=0, qpos=0) == "ZeroDimension"
+    assert _resident_prepare(kv_len=0, qpos=0) == "EmptyCache"
+    assert _resident_prepare(kv_len=65, qpos=64) == "InvalidCacheLength"
+    assert _resident_prepare(D=63) == "InvalidRotaryHeadDim"
+    assert _resident_prepare(D=256) == "UnsupportedHeadDim"
+    assert _resident_prepare(hq=6, hkv=4) == "InvalidHeadGrouping"
+    assert _resident_prepare(theta=float("nan")) == "InvalidRotaryTheta"
+    assert _resident_prepare() == "NullArgument"
+    assert _resident_prepare(dtype=fa.DTYPE_BF16) == "NullArgument"
+
+
 def test_append_batched_validation():
     bt = np.array([[0, 1]], np.int32)
     st = np.array([20], np.int32)
