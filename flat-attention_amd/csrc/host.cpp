@@ -155,6 +155,14 @@ struct fa_ctx {
     void* ws_vt = nullptr;
     size_t ws_vt_bytes = 0;
     int transpose_v_policy = -1;
+    // per-sequence metadata of variable-length prefill: device copy + pinned staging, reused
+    // once the event recorded after the previous copy has completed
+    int32_t* meta_dev = nullptr;
+    size_t meta_dev_bytes = 0;
+    int32_t* meta_host = nullptr;
+    size_t meta_host_bytes = 0;
+    hipEvent_t meta_event = nullptr;
+    bool meta_pending = false;
     // per-call allocation accounting (telemetry)
     uint32_t call_allocs = 0;
     uint64_t call_alloc_bytes = 0;
@@ -323,6 +331,32 @@ int ensure_ws(fa_ctx* ctx, size_t bytes, void** out) {
     return grow(ctx, &ctx->ws, &ctx->ws_bytes, bytes, out);
 }
 
+// Stream-ordered upload of `n` int32 values to the context's metadata buffer: a later launch on
+// the stream reads them, an earlier one has finished with the previous contents (same stream).
+int upload_meta(fa_ctx* ctx, const int32_t* vals, size_t n, const int32_t** dev) {
+    const size_t bytes = n * sizeof(int32_t);
+    if (ctx->meta_pending) {
+        HIP_TRY(hipEventSynchronize(ctx->meta_event));
+        ctx->meta_pending = false;
+    }
+    if (ctx->meta_host_bytes < bytes) {
+        if (ctx->meta_host) HIP_TRY(hipHostFree(ctx->meta_host));
+        ctx->meta_host = nullptr;
+        ctx->meta_host_bytes = 0;
+        HIP_TRY(hipHostMalloc((void**)&ctx->meta_host, bytes, hipHostMallocDefault));
+        ctx->meta_host_bytes = bytes;
+    }
+    void* d = nullptr;
+    if (int rc = grow(ctx, (void**)&ctx->meta_dev, &ctx->meta_dev_bytes, bytes, &d)) return rc;
+    if (!ctx->meta_event) HIP_TRY(hipEventCreateWithFlags(&ctx->meta_event, hipEventDisableTiming));
+    memcpy(ctx->meta_host, vals, bytes);
+    HIP_TRY(hipMemcpyAsync(d, ctx->meta_host, bytes, hipMemcpyHostToDevice, ctx->stream));
+    HIP_TRY(hipEventRecord(ctx->meta_event, ctx->stream));
+    ctx->meta_pending = true;
+    *dev = (const int32_t*)d;
+    return FA_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -429,6 +463,9 @@ int fa_ctx_destroy(fa_ctx* ctx) {
     if (ctx->inv_freq) (void)hipFree(ctx->inv_freq);
     if (ctx->ws) (void)hipFree(ctx->ws);
     if (ctx->ws_vt) (void)hipFree(ctx->ws_vt);
+    if (ctx->meta_dev) (void)hipFree(ctx->meta_dev);
+    if (ctx->meta_host) (void)hipHostFree(ctx->meta_host);
+    if (ctx->meta_event) (void)hipEventDestroy(ctx->meta_event);
     for (const auto& s : ctx->pending) {
         (void)hipEventDestroy(s.begin);
         (void)hipEventDestroy(s.end);
@@ -590,6 +627,7 @@ struct PrefillJob {
     uint64_t max_pos = 0;  // highest RoPE position used + 1
     uint64_t kv_bytes = 0;
     uint64_t k_rows = 0, k_heads = 0, k_period = 0;
+    bool no_vt = false;  // never use the transposed-V copy
 };
 
 int run_prefill(fa_ctx* ctx, PrefillJob& j) {
@@ -623,7 +661,7 @@ int run_prefill(fa_ctx* ctx, PrefillJob& j) {
     // Optional transposed V copy for the 16-bit contiguous kernel (off unless selected): the V^T
     // operand then comes from plain 16-byte LDS reads instead of transposing ones. It measured
     // no faster at D = 128, so the extra pass is not run by default.
-    const bool vt = !j.paged && j.dtype != FA_DTYPE_F32 && j.a.head_dim % 8 == 0 &&
+    const bool vt = !j.paged && !j.no_vt && j.dtype != FA_DTYPE_F32 && j.a.head_dim % 8 == 0 &&
                     ctx->transpose_v_policy == 1;
     j.a.vt = nullptr;
     j.a.vt_row = 0;
@@ -837,6 +875,115 @@ int fa_forward_projection_asymmetric(fa_ctx* ctx, const void* q, size_t q_bytes,
         j.k_heads = sh->kv_heads;
         j.k_period = sh->kv_len;
     }
+    if (int rc = run_prefill(ctx, j)) return rc;
+    return ok();
+}
+
+// ExternalVariableProjectionRotaryGroupedPipeline::encode src/wgpu_external_variable.rs:138 with
+// the checks of validate_dispatch :229 in their order. Q/K/V/O keep the padded projection layout;
+// sequence b attends over its active rows only (padded K/V rows are never read) and its padded
+// query rows get O = 0, LSE = -inf. Q is rotated at meta[b].query_rope_position_offset + t, K at
+// kv_position_offset + key; causal masking uses meta[b].query_position_offset + t.
+int fa_forward_projection_variable(fa_ctx* ctx, const void* q, size_t q_bytes, const void* k,
+                                   const void* v, size_t kv_bytes, void* out_lse,
+                                   size_t out_bytes, const fa_asymmetric_shape* sh,
+                                   const fa_variable_sequence* meta, uint64_t n_meta,
+                                   const fa_config* cfg, float theta, uint64_t kv_position_offset,
+                                   int dtype) {
+    if (!sh) return fail(FA_ERR_NULL_ARGUMENT, "shape is null");
+    if (int rc = check_dtype(dtype)) return rc;
+    if (!sh->batch || !sh->q_heads || !sh->kv_heads || !sh->query_len || !sh->kv_len ||
+        !sh->head_dim)
+        return fail(FA_ERR_ZERO_DIMENSION, "attention dimensions must all be non-zero");
+    if (sh->q_heads % sh->kv_heads)
+        return fail(FA_ERR_INVALID_HEAD_GROUPING,
+                    "q_heads (%llu) must be exactly divisible by kv_heads (%llu)",
+                    (unsigned long long)sh->q_heads, (unsigned long long)sh->kv_heads);
+    if (int rc = validate_grouped(sh->batch, sh->q_heads, sh->kv_heads,
+                                  std::max(sh->query_len, sh->kv_len), sh->head_dim))
+        return rc;
+    if (n_meta != sh->batch)
+        return fail(FA_ERR_LENGTH_MISMATCH,
+                    "active sequence metadata contains %llu elements, expected %llu",
+                    (unsigned long long)n_meta, (unsigned long long)sh->batch);
+    if (n_meta && !meta) return fail(FA_ERR_NULL_ARGUMENT, "metadata is null");
+    uint64_t max_pos = 0;
+    std::vector<int32_t> m(4 * sh->batch);
+    for (uint64_t b = 0; b < sh->batch; ++b) {
+        const fa_variable_sequence& e = meta[b];
+        if (!e.active_query_len || !e.active_kv_len)
+            return fail(FA_ERR_ZERO_DIMENSION, "attention dimensions must all be non-zero");
+        if (e.active_query_len > sh->query_len)
+            return fail(FA_ERR_LENGTH_MISMATCH, "active query length contains %llu elements, expected %llu",
+                        (unsigned long long)e.active_query_len, (unsigned long long)sh->query_len);
+        if (e.active_kv_len > sh->kv_len)
+            return fail(FA_ERR_LENGTH_MISMATCH, "active KV length contains %llu elements, expected %llu",
+                        (unsigned long long)e.active_kv_len, (unsigned long long)sh->kv_len);
+        // positions must fit the kernels' i32 index space (the reference bounds them by u32)
+        const uint64_t causal_end = e.query_position_offset + e.active_query_len;
+        const uint64_t q_rope_end = e.query_rope_position_offset + e.active_query_len;
+        const uint64_t kv_rope_end = kv_position_offset + e.active_kv_len;
+        if (causal_end < e.query_position_offset || causal_end > kI32 ||
+            q_rope_end < e.query_rope_position_offset || q_rope_end > kI32 ||
+            kv_rope_end < kv_position_offset || kv_rope_end > kI32)
+            return fail(FA_ERR_POSITION_OVERFLOW, "rotary position offset overflows the index space");
+        if (int rc = check_rotary(theta, e.query_rope_position_offset, sh->head_dim, e.active_query_len))
+            return rc;
+        if (int rc = check_rotary(theta, kv_position_offset, sh->head_dim, e.active_kv_len))
+            return rc;
+        m[4 * b + 0] = (int32_t)e.active_query_len;
+        m[4 * b + 1] = (int32_t)e.active_kv_len;
+        m[4 * b + 2] = (int32_t)e.query_position_offset;
+        m[4 * b + 3] = (int32_t)e.query_rope_position_offset;
+        max_pos = std::max(max_pos, std::max(q_rope_end, kv_rope_end));
+    }
+    if (int rc = check_head_dim(sh->head_dim, dtype)) return rc;
+    const uint64_t eb = elem_bytes(dtype);
+    const uint64_t qn = sh->batch * sh->query_len * sh->q_heads * sh->head_dim;
+    const uint64_t kvn = sh->batch * sh->kv_len * sh->kv_heads * sh->head_dim;
+    fa_packed_layout lay;
+    if (int rc = fa_packed_layout_for(qn, sh->batch * sh->q_heads * sh->query_len, dtype, &lay))
+        return rc;
+    if (int rc = check_buffer("Q", q, q_bytes, qn * eb)) return rc;
+    if (int rc = check_buffer("K", k, kv_bytes, kvn * eb)) return rc;
+    if (int rc = check_buffer("V", v, kv_bytes, kvn * eb)) return rc;
+    if (int rc = check_buffer("O|LSE", out_lse, out_bytes, lay.combined_bytes)) return rc;
+    float scale;
+    if (int rc = resolve_scale(cfg, sh->head_dim, &scale)) return rc;
+    if (!ctx) return fail(FA_ERR_NULL_ARGUMENT, "context is null");
+    begin_call(ctx);
+    if (int rc = set_device(ctx)) return rc;
+
+    PrefillJob j{};
+    j.dt = (Dtype)dtype;
+    j.dtype = dtype;
+    j.no_vt = true;  // the transposed-V copy would include padded rows
+    fa::PrefillArgs& a = j.a;
+    const int64_t D = (int64_t)sh->head_dim, QW = (int64_t)sh->q_heads * D,
+                  KW = (int64_t)sh->kv_heads * D;
+    a.q = q; a.k = k; a.v = v;
+    a.o = out_lse;
+    a.lse = (float*)((uint8_t*)out_lse + lay.lse_byte_offset);
+    a.q_sb = (int64_t)sh->query_len * QW; a.q_sh = D; a.q_ss = QW;
+    a.k_sb = (int64_t)sh->kv_len * KW; a.k_sh = D; a.k_ss = KW;
+    a.o_sb = a.q_sb; a.o_sh = a.q_sh; a.o_ss = a.q_ss;
+    a.lse_sb = (int64_t)sh->q_heads * sh->query_len; a.lse_sh = (int64_t)sh->query_len;
+    a.batch = (int)sh->batch; a.q_heads = (int)sh->q_heads; a.kv_heads = (int)sh->kv_heads;
+    a.group = (int)(sh->q_heads / sh->kv_heads);
+    a.q_len = (int)sh->query_len; a.kv_len = (int)sh->kv_len; a.head_dim = (int)D;
+    a.causal = cfg && cfg->causal;
+    a.scale = scale;
+    j.rope = true;
+    j.theta = theta;
+    a.rope_q = 1;
+    a.rope_k = 1;
+    a.kv_rope_offset = (int)kv_position_offset;
+    j.max_pos = max_pos;
+    j.kv_bytes = kvn * eb;
+    j.k_rows = sh->batch * sh->kv_len;
+    j.k_heads = sh->kv_heads;
+    j.k_period = sh->kv_len;
+    if (int rc = upload_meta(ctx, m.data(), m.size(), &a.var_meta)) return rc;
     if (int rc = run_prefill(ctx, j)) return rc;
     return ok();
 }

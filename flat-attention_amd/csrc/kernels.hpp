@@ -40,6 +40,11 @@ struct PrefillArgs {
     // rows of vt_row keys (kv_len rounded up to 64, zero padded). nullptr = read V directly.
     const void* vt;
     int vt_row;
+    // Variable-length batch (contiguous K/V only): 4 ints per batch element — active query
+    // rows, active K/V rows, causal position and RoPE position of query row 0 — overriding
+    // q_len, kv_len, causal_offset and q_rope_offset; padded query rows get O = 0, LSE = -inf.
+    // nullptr: every batch element uses the padded extents.
+    const int* var_meta;
 };
 
 void launch_prefill(Dtype dt, bool paged, const PrefillArgs& a, hipStream_t s,

@@ -81,6 +81,20 @@ __device__ __forceinline__ i32x4_t make_rsrc_words(const void* base, int nrec) {
     return r;
 }
 
+// Padded query row `row` (t = row / group) of a variable-length batch: O = 0 in every dim,
+// LSE = -inf. Lane group g writes the dims of 4-element groups of its parity, as the epilogue.
+template <typename E>
+__device__ __forceinline__ void write_padded_row(const PrefillArgs& a, int b, int kvh, int row,
+                                                 int g, int D) {
+    const int t = row / a.group, hq = kvh * a.group + row % a.group;
+    E* orow = (E*)a.o + (int64_t)b * a.o_sb + (int64_t)hq * a.o_sh + (int64_t)t * a.o_ss;
+    for (int d0 = 4 * g; d0 < D; d0 += 8)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            if (d0 + j < D) orow[d0 + j] = E(0);
+    if (g == 0) a.lse[(int64_t)b * a.lse_sb + (int64_t)hq * a.lse_sh + t] = -INFINITY;
+}
+
 #ifndef FA_PREFILL_LPT
 #define FA_PREFILL_LPT 1
 #endif
@@ -220,32 +234,49 @@ __global__ __launch_bounds__(64 * NW, 2) void prefill_mfma16(PrefillKArgs ka) {
     const int tid = threadIdx.x, lane = tid & 63, g = lane >> 5;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar registers
     const int D = a.head_dim, half = D >> 1;
-    const int rows_total = a.q_len * a.group;
-    const int nqb = (rows_total + BM - 1) / BM;
+    const int rows_pad = a.q_len * a.group;  // padded extent of the grid
+    const int nqb = (rows_pad + BM - 1) / BM;
     int bh, qb;  // heavy (late, causal) blocks dispatch first
     block_coords(blockIdx.x, gridDim.x, nqb, bh, qb);
     const int b = bh / a.kv_heads, kvh = bh % a.kv_heads;
     const int r0 = qb * BM;
+    // Per-sequence extents of a variable-length batch (PrefillArgs::var_meta); the grid covers
+    // the padded extents. A block of padded query rows only writes O = 0, LSE = -inf.
+    int q_len_ = a.q_len, kv_len_ = a.kv_len, causal_off_ = a.causal_offset;
+    int q_rope_off_ = a.q_rope_offset;
+    if (a.var_meta) {
+        const int* m = a.var_meta + 4 * b;
+        q_len_ = m[0];
+        kv_len_ = m[1];
+        causal_off_ = m[2];
+        q_rope_off_ = m[3];
+    }
+    const int rows_total = q_len_ * a.group;
+    if (a.var_meta && r0 >= rows_total) {
+        const int prow = r0 + wave * 32 + (lane & 31);
+        if (prow < rows_pad) write_padded_row<uint16_t>(a, b, kvh, prow, g, D);
+        return;
+    }
 
     // This lane's query row.
     const int row = r0 + wave * 32 + (lane & 31);
     const bool row_ok = row < rows_total;
-    const int t = row_ok ? row / a.group : a.q_len - 1;
+    const int t = row_ok ? row / a.group : q_len_ - 1;
     const int hq = kvh * a.group + (row_ok ? row % a.group : 0);
-    const int cpos = a.causal_offset + t;
+    const int cpos = causal_off_ + t;
 
     // Key tiles this wave's rows need (its group's 128 rows under the ping-pong schedule) and,
     // for the ping-pong barrier count, the whole block's.
     const int r0w = PP ? r0 + 128 * (wave >> 2) : r0;
-    const int t_max = min(a.q_len - 1, (r0w + 127) / a.group);
+    const int t_max = min(q_len_ - 1, (r0w + 127) / a.group);
     const int t_min = r0w / a.group;
-    int n_keys = a.kv_len;
-    if (a.causal) n_keys = min(n_keys, a.causal_offset + t_max + 1);
+    int n_keys = kv_len_;
+    if (a.causal) n_keys = min(n_keys, causal_off_ + t_max + 1);
     const int n_tiles = __builtin_amdgcn_readfirstlane((n_keys + BN - 1) / BN);
-    const int cpos_min = a.causal_offset + t_min;
-    int n_keys_blk = a.kv_len;
+    const int cpos_min = causal_off_ + t_min;
+    int n_keys_blk = kv_len_;
     if (a.causal)
-        n_keys_blk = min(n_keys_blk, a.causal_offset + min(a.q_len - 1, (r0 + BM - 1) / a.group) + 1);
+        n_keys_blk = min(n_keys_blk, causal_off_ + min(q_len_ - 1, (r0 + BM - 1) / a.group) + 1);
     const int n_blk = __builtin_amdgcn_readfirstlane((n_keys_blk + BN - 1) / BN);
     (void)n_blk;
 
@@ -255,7 +286,7 @@ __global__ __launch_bounds__(64 * NW, 2) void prefill_mfma16(PrefillKArgs ka) {
         const uint16_t* qrow = (const uint16_t*)a.q + (int64_t)b * a.q_sb + (int64_t)hq * a.q_sh +
                                (int64_t)t * a.q_ss;
         const float2* cs_row =
-            a.rope_q ? a.rope_table + (int64_t)(a.q_rope_offset + t) * half : nullptr;
+            a.rope_q ? a.rope_table + (int64_t)(q_rope_off_ + t) * half : nullptr;
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
             const int d0 = 16 * ks + 8 * g;
@@ -316,7 +347,7 @@ __global__ __launch_bounds__(64 * NW, 2) void prefill_mfma16(PrefillKArgs ka) {
     auto load_one = [&](int tile, const uint8_t* base, u32x4_t (&reg)[KPASS]) {
         const int key_base = tile * BN;
         if constexpr (CONTIG) {
-            const int nrec = (a.kv_len - 1) * (int)row_bytes + D * 2;
+            const int nrec = (kv_len_ - 1) * (int)row_bytes + D * 2;
             const __amdgpu_buffer_rsrc_t rs =
                 __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, nrec, kRsrcFlags);
 #pragma unroll
@@ -329,7 +360,7 @@ __global__ __launch_bounds__(64 * NW, 2) void prefill_mfma16(PrefillKArgs ka) {
             for (int p = 0; p < KPASS; ++p) {
                 const int key = key_base + p * KRPP + k_r;
                 const int g16 = __builtin_amdgcn_readfirstlane(key & ~15);
-                const int live = min(16, a.kv_len - g16);
+                const int live = min(16, kv_len_ - g16);
                 const int gq = live > 0 ? g16 : 0;
                 const uint32_t lp = ka.ps.div((uint32_t)gq);
                 const int page = a.block_tables[(int64_t)b * a.bt_stride + lp];
@@ -345,10 +376,10 @@ __global__ __launch_bounds__(64 * NW, 2) void prefill_mfma16(PrefillKArgs ka) {
 #pragma unroll
             for (int p = 0; p < KPASS; ++p) {
                 const int key_raw = key_base + p * KRPP + k_r;
-                const int key = min(key_raw, a.kv_len - 1);
+                const int key = min(key_raw, kv_len_ - 1);
                 const int64_t r = paged_row<PMODE>(ka, b, key);
                 reg[p] = *(const u32x4_t*)(base + r * row_bytes + kd2);
-                if (key_raw >= a.kv_len) reg[p] = u32x4_t{0u, 0u, 0u, 0u};
+                if (key_raw >= kv_len_) reg[p] = u32x4_t{0u, 0u, 0u, 0u};
             }
         }
         if (!FULLD && k_dc * 8 >= D) {
@@ -362,7 +393,7 @@ __global__ __launch_bounds__(64 * NW, 2) void prefill_mfma16(PrefillKArgs ka) {
         for (int p = 0; p < KPASS; ++p) {
             const int kl = p * KRPP + k_r;
             u32x4_t val = kreg[p];
-            if (ROPEK && tile * BN + kl < a.kv_len && (FULLD || k_dc * 8 < D)) {
+            if (ROPEK && tile * BN + kl < kv_len_ && (FULLD || k_dc * 8 < D)) {
                 // K rotated between the HBM load and the LDS store (cos/sin from the table)
                 const float2* csp = a.rope_table +
                                     (int64_t)(a.kv_rope_offset + tile * BN + kl) * half + k_dc * 4;
@@ -462,7 +493,7 @@ __global__ __launch_bounds__(64 * NW, 2) void prefill_mfma16(PrefillKArgs ka) {
     // ---- mask (tail keys, causal diagonal) and the running-max update of the online softmax
     auto softmax_max = [&](f32x16_t (&sacc)[2], int tile, auto masked) {
         if constexpr (decltype(masked)::value) {
-            const int lim = (a.causal ? min(a.kv_len - 1, cpos) : a.kv_len - 1) - tile * BN - 8 * g;
+            const int lim = (a.causal ? min(kv_len_ - 1, cpos) : kv_len_ - 1) - tile * BN - 8 * g;
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
@@ -574,7 +605,7 @@ __global__ __launch_bounds__(64 * NW, 2) void prefill_mfma16(PrefillKArgs ka) {
     };
 
     // Leading tiles that need no mask: every key is < kv_len and visible to every row.
-    int n_full = a.kv_len / BN;
+    int n_full = kv_len_ / BN;
     if (a.causal) n_full = min(n_full, (cpos_min + 1) / BN);
     n_full = __builtin_amdgcn_readfirstlane(n_full);
     using NoMask = std::integral_constant<bool, false>;
@@ -609,7 +640,7 @@ __global__ __launch_bounds__(64 * NW, 2) void prefill_mfma16(PrefillKArgs ka) {
                               : kOob;
             }
         }
-        const int nrec_all = (a.kv_len - 1) * (int)row_bytes + D * 2;
+        const int nrec_all = (kv_len_ - 1) * (int)row_bytes + D * 2;
         const int nrec_vt = VT ? D * a.vt_row * 2 : 0;
         // Tile `tile` of K and V into the stage at byte offset `st`.
         const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_void_t*)smem;
@@ -916,6 +947,8 @@ __global__ __launch_bounds__(64 * NW, 2) void prefill_mfma16(PrefillKArgs ka) {
             }
         if (g == 0)
             a.lse[(int64_t)b * a.lse_sb + (int64_t)hq * a.lse_sh + t] = m_run * a.scale + logf(l_tot);
+    } else if (a.var_meta && row < rows_pad) {
+        write_padded_row<uint16_t>(a, b, kvh, row, g, D);
     }
 }
 
@@ -936,23 +969,40 @@ __global__ __launch_bounds__(256, 1) void prefill_mfma_f32(PrefillKArgs ka) {
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 5;
     const int D = a.head_dim, half = D >> 1;
-    const int rows_total = a.q_len * a.group;
-    const int nqb = (rows_total + BM - 1) / BM;
+    const int rows_pad = a.q_len * a.group;  // padded extent of the grid
+    const int nqb = (rows_pad + BM - 1) / BM;
     int bh, qb;
     block_coords(blockIdx.x, gridDim.x, nqb, bh, qb);
     const int b = bh / a.kv_heads, kvh = bh % a.kv_heads;
     const int r0 = qb * BM;
+    // Per-sequence extents of a variable-length batch (PrefillArgs::var_meta); the grid covers
+    // the padded extents. A block of padded query rows only writes O = 0, LSE = -inf.
+    int q_len_ = a.q_len, kv_len_ = a.kv_len, causal_off_ = a.causal_offset;
+    int q_rope_off_ = a.q_rope_offset;
+    if (a.var_meta) {
+        const int* m = a.var_meta + 4 * b;
+        q_len_ = m[0];
+        kv_len_ = m[1];
+        causal_off_ = m[2];
+        q_rope_off_ = m[3];
+    }
+    const int rows_total = q_len_ * a.group;
+    if (a.var_meta && r0 >= rows_total) {
+        const int prow = r0 + wave * 32 + (lane & 31);
+        if (prow < rows_pad) write_padded_row<float>(a, b, kvh, prow, g, D);
+        return;
+    }
     const int row = r0 + wave * 32 + (lane & 31);
     const bool row_ok = row < rows_total;
-    const int t = row_ok ? row / a.group : a.q_len - 1;
+    const int t = row_ok ? row / a.group : q_len_ - 1;
     const int hq = kvh * a.group + (row_ok ? row % a.group : 0);
-    const int cpos = a.causal_offset + t;
-    const int t_max = min(a.q_len - 1, (r0 + BM - 1) / a.group);
+    const int cpos = causal_off_ + t;
+    const int t_max = min(q_len_ - 1, (r0 + BM - 1) / a.group);
     const int t_min = r0 / a.group;
-    int n_keys = a.kv_len;
-    if (a.causal) n_keys = min(n_keys, a.causal_offset + t_max + 1);
+    int n_keys = kv_len_;
+    if (a.causal) n_keys = min(n_keys, causal_off_ + t_max + 1);
     const int n_tiles = (n_keys + BN - 1) / BN;
-    const int cpos_min = a.causal_offset + t_min;
+    const int cpos_min = causal_off_ + t_min;
 
     // Q operand: qv[ks] = Q[row][g*HALFD + ks] (rotated)
     float qv[HALFD];
@@ -965,7 +1015,7 @@ __global__ __launch_bounds__(256, 1) void prefill_mfma_f32(PrefillKArgs ka) {
             qv[ks] = d < D ? qrow[d] : 0.0f;
         }
         if (a.rope_q) {
-            const float2* cs = a.rope_table + (int64_t)(a.q_rope_offset + t) * half;
+            const float2* cs = a.rope_table + (int64_t)(q_rope_off_ + t) * half;
 #pragma unroll
             for (int j = 0; j < HALFD / 2; ++j) {
                 const int p = (g * HALFD) / 2 + j;
@@ -997,7 +1047,7 @@ __global__ __launch_bounds__(256, 1) void prefill_mfma_f32(PrefillKArgs ka) {
             const int d0 = (tid % C4) * 4;
             const int key = tile * BN + kl;
             f32x4_t kv4 = (f32x4_t)0.0f, vv4 = (f32x4_t)0.0f;
-            if (key < a.kv_len) {
+            if (key < kv_len_) {
                 const int64_t ro = kv_row_offset<PAGED>(ka, b, key);
                 const float* kr = kbase + ro;
                 const float* vr = vbase + ro;
@@ -1044,8 +1094,8 @@ __global__ __launch_bounds__(256, 1) void prefill_mfma_f32(PrefillKArgs ka) {
         }
 
         const int tile_end = (tile + 1) * BN;
-        if (tile_end > a.kv_len || (a.causal && tile_end - 1 > cpos_min)) {
-            const int lim = a.causal ? min(a.kv_len - 1, cpos) : a.kv_len - 1;
+        if (tile_end > kv_len_ || (a.causal && tile_end - 1 > cpos_min)) {
+            const int lim = a.causal ? min(kv_len_ - 1, cpos) : kv_len_ - 1;
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
@@ -1115,6 +1165,8 @@ __global__ __launch_bounds__(256, 1) void prefill_mfma_f32(PrefillKArgs ka) {
             }
         if (g == 0)
             a.lse[(int64_t)b * a.lse_sb + (int64_t)hq * a.lse_sh + t] = m_run * a.scale + logf(l_tot);
+    } else if (a.var_meta && row < rows_pad) {
+        write_padded_row<float>(a, b, kvh, row, g, D);
     }
 }
 

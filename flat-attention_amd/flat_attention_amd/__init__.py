@@ -15,7 +15,9 @@ from .api import (AsymmetricGroupedAttentionShape, AsymmetricRotaryEmbeddingConf
                   HipResidentKvCache, HipRotaryGroupedAttention, ResidentDecodePlan,
                   PackedLayout, PagedChunkedPrefillPlan, PagedDecodePlan, PagedKvAddress,
                   PagedKvConfig, PagedKvTable, PagedKvTelemetry, RotaryEmbeddingConfig,
-                  RuntimeDispatchTelemetry, bf16_bits_to_f32, download_attention,
+                  RuntimeDispatchTelemetry, HipVariableProjectionPipeline,
+                  VariableLengthRotaryEmbeddingConfig, VariableLengthSequenceMetadata,
+                  bf16_bits_to_f32, download_attention,
                   f32_to_bf16_bits, host_storage, packed_layout, paged_append_batched,
                   storage_np_dtype, storage_to_f32)
 

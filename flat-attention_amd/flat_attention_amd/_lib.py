@@ -66,6 +66,11 @@ class RotaryC(ctypes.Structure):
     _fields_ = [("theta", F32), ("position_offset", U64)]
 
 
+class VariableSequenceC(ctypes.Structure):
+    _fields_ = [("active_query_len", U64), ("active_kv_len", U64),
+                ("query_position_offset", U64), ("query_rope_position_offset", U64)]
+
+
 class AsymmetricRotaryC(ctypes.Structure):
     _fields_ = [("theta", F32), ("query_position_offset", U64), ("kv_position_offset", U64)]
 
@@ -151,6 +156,9 @@ PROTOTYPES = {
     "fa_paged_decode_plan_info": (INT, [VP, P(U64), P(U64), P(U64)]),
     "fa_paged_decode_plan_set_split": (INT, [VP, VP, U64]),
     "fa_paged_cache_decode": (INT, [VP, VP, VP, SZ, U64, P(ConfigC), F32, U64, VP, SZ]),
+    "fa_forward_projection_variable": (INT, [VP, VP, SZ, VP, VP, SZ, VP, SZ, P(AsymmetricShapeC),
+                                             P(VariableSequenceC), U64, P(ConfigC), F32, U64,
+                                             INT]),
     "fa_resident_cache_create": (INT, [VP, U64, U64, U64, U64, INT, P(VP)]),
     "fa_resident_cache_destroy": (INT, [VP]),
     "fa_resident_cache_append": (INT, [VP, VP, VP, SZ, U64, P(U64)]),

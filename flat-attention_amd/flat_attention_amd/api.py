@@ -462,6 +462,49 @@ class HipAsymmetricProjectionPipeline:
         self.encode(q, k, v, out, shape, config, rotary, rotate_k=False)
 
 
+@dataclass(frozen=True)
+class VariableLengthSequenceMetadata:
+    """VariableLengthSequenceMetadata src/wgpu_external_variable.rs:25."""
+    active_query_len: int
+    active_kv_len: int
+    query_position_offset: int
+    query_rope_position_offset: int
+
+
+@dataclass(frozen=True)
+class VariableLengthRotaryEmbeddingConfig:
+    """VariableLengthRotaryEmbeddingConfig src/wgpu_external_variable.rs:40."""
+    theta: float
+    kv_position_offset: int = 0
+
+
+class HipVariableProjectionPipeline:
+    """ExternalVariableProjectionRotaryGroupedPipeline src/wgpu_external_variable.rs:66 (M12:
+    padded variable-length projection-layout GQA + RoPE; padded query rows O = 0, LSE = -inf)."""
+
+    def __init__(self, ctx: HipContext, dtype: int = L.DTYPE_F32):
+        self.ctx = ctx
+        self.dtype = dtype
+
+    def layout(self, shape: AsymmetricGroupedAttentionShape) -> PackedLayout:
+        return packed_layout(shape.q_tensor_len(), shape.lse_len(), self.dtype)
+
+    def create_output_buffer(self, shape: AsymmetricGroupedAttentionShape) -> DeviceBuffer:
+        return DeviceBuffer(self.ctx, self.layout(shape).combined_bytes)
+
+    def encode(self, q, k, v, out_and_lse, shape: AsymmetricGroupedAttentionShape,
+               metadata, config: FlatAttentionConfig,
+               rotary: VariableLengthRotaryEmbeddingConfig) -> PackedLayout:
+        arr = (L.VariableSequenceC * max(len(metadata), 1))(
+            *[L.VariableSequenceC(m.active_query_len, m.active_kv_len, m.query_position_offset,
+                                  m.query_rope_position_offset) for m in metadata])
+        check(lib().fa_forward_projection_variable(
+            self.ctx.handle, q.ptr, q.nbytes, k.ptr, v.ptr, min(k.nbytes, v.nbytes),
+            out_and_lse.ptr, out_and_lse.nbytes, ctypes.byref(shape.c()), arr, len(metadata),
+            ctypes.byref(config.c()), rotary.theta, rotary.kv_position_offset, self.dtype))
+        return self.layout(shape)
+
+
 class HipChunkedProjectionPrefillPipeline:
     """WgpuChunkedProjectionPrefillPipeline src/wgpu_chunked_prefill.rs:99."""
 

@@ -323,6 +323,27 @@ int fa_paged_cache_decode(fa_ctx* ctx, const fa_paged_cache* cache, const void* 
                           float theta, uint64_t q_rope_position, void* out_lse,
                           size_t out_bytes);
 
+/* ------------------------------------------------------------ variable-length prefill ----
+ * ExternalVariableProjectionRotaryGroupedPipeline::encode src/wgpu_external_variable.rs:138 (M12).
+ * Q [batch, shape->query_len, q_heads*head_dim], K/V [batch, shape->kv_len, kv_heads*head_dim] are
+ * padded projection-layout tensors (shape->query_position_offset is ignored); meta[b] gives the
+ * active extents and query origins of sequence b (VariableLengthSequenceMetadata :25). Sequence b
+ * attends over its first active_kv_len K/V rows only (padded rows are never read), causally at
+ * query_position_offset + t; Q is rotated at query_rope_position_offset + t, K at
+ * kv_position_offset + key (VariableLengthRotaryEmbeddingConfig :40). Output [O | LSE] as for
+ * fa_forward_projection_asymmetric; padded query rows get O = 0 and LSE = -inf. Errors follow
+ * validate_dispatch :229 (LengthMismatch for the metadata count and for active lengths above the
+ * padded ones, PositionOverflow past the i32 position space); there is no batch limit. */
+typedef struct fa_variable_sequence {
+    uint64_t active_query_len, active_kv_len, query_position_offset, query_rope_position_offset;
+} fa_variable_sequence;
+int fa_forward_projection_variable(fa_ctx* ctx, const void* q, size_t q_bytes, const void* k,
+                                   const void* v, size_t kv_bytes, void* out_lse,
+                                   size_t out_bytes, const fa_asymmetric_shape* shape,
+                                   const fa_variable_sequence* meta, uint64_t n_meta,
+                                   const fa_config* config, float theta,
+                                   uint64_t kv_position_offset, int dtype);
+
 /* ------------------------------------------------------------ resident KV cache ---------
  * WgpuResidentKvCache src/wgpu_kv_cache.rs:79: fixed-capacity K and V storage
  * [batch, capacity, kv_heads*head_dim] in `dtype`, one live length shared by the batch. */

@@ -231,6 +231,32 @@ def test_resident_decode_prepare_validation_variants():
     assert _resident_prepare(dtype=fa.DTYPE_BF16) == "NullArgument"
 
 
+def _variable(meta, shape=(2, 4, 2, 8, 16, 64, 0), theta=1e4, kv_off=0, q_bytes=1 << 30):
+    sh = fa.AsymmetricGroupedAttentionShape(*shape)
+    arr = (L.VariableSequenceC * max(len(meta), 1))(*[L.VariableSequenceC(*m) for m in meta])
+    return _variant(fa.lib().fa_forward_projection_variable(
+        None, FAKE, q_bytes, FAKE, FAKE, 1 << 30, FAKE, 1 << 30, ctypes.byref(sh.c()), arr,
+        len(meta), ctypes.byref(fa.FlatAttentionConfig(True).c()), theta, kv_off, fa.DTYPE_BF16))
+
+
+def test_variable_prefill_validation_variants():
+    """validate_dispatch src/wgpu_external_variable.rs:229, in its order; a null context is
+    reported last."""
+    ok = [(8, 16, 0, 0), (3, 5, 2, 7)]
+    assert _variable(ok[:1]) == "LengthMismatch"
+    assert _variable([(0, 16, 0, 0), ok[1]]) == "ZeroDimension"
+    assert _variable([(9, 16, 0, 0), ok[1]]) == "LengthMismatch"
+    assert _variable([(8, 17, 0, 0), ok[1]]) == "LengthMismatch"
+    assert _variable([(8, 16, 2**31 - 4, 0), ok[1]]) == "PositionOverflow"
+    assert _variable([(8, 16, 0, 2**31 - 4), ok[1]]) == "PositionOverflow"
+    assert _variable(ok, kv_off=2**31 - 8) == "PositionOverflow"
+    assert _variable(ok, theta=0.0) == "InvalidRotaryTheta"
+    assert _variable(ok, shape=(2, 4, 2, 8, 16, 63, 0)) == "InvalidRotaryHeadDim"
+    assert _variable(ok, shape=(2, 6, 4, 8, 16, 64, 0)) == "InvalidHeadGrouping"
+    assert _variable(ok, q_bytes=16) == "BufferTooSmall"
+    assert _variable(ok) == "NullArgument"
+
+
 def test_append_batched_validation():
     bt = np.array([[0, 1]], np.int32)
     st = np.array([20], np.int32)
