@@ -7,7 +7,8 @@ library (``flat-attention_amd``) never imports, links or calls it.
 This module is a thin numpy/ctypes wrapper over ``liboracle.so`` (built from ``oracle.c``
 by ``oracle/Makefile``), which restates the reference crate's scalar Rust oracles
 (``src/lib.rs:454``, ``src/grouped.rs:81``, ``src/rotary_grouped.rs:57``,
-``src/projection_asymmetric.rs:97``, ``src/chunked_projection_prefill.rs:63``) loop for
+``src/projection_asymmetric.rs:97``, ``src/chunked_projection_prefill.rs:63``,
+``src/backward_grouped.rs:17``) loop for
 loop. Each wrapper returns ``(out, lse)`` float32 arrays or raises ``OracleError``.
 """
 
@@ -98,6 +99,23 @@ def forward_grouped(q, k, v, batch, q_heads, kv_heads, seq, dim, causal, scale=N
                                    _I(threads))
     _check(rc, "forward_grouped")
     return out, lse
+
+
+def backward_grouped(q, k, v, d_out, out, lse, batch, q_heads, kv_heads, seq, dim, causal,
+                     scale=None, threads=1):
+    """backward_reference_grouped src/backward_grouped.rs:17 -> (dq, dk, dv) float32."""
+    q, k, v, d_out, out, lse = (_f32(x) for x in (q, k, v, d_out, out, lse))
+    s = resolved_scale(dim, scale)
+    qn, kvn = batch * q_heads * seq * dim, batch * kv_heads * seq * dim
+    dq = np.zeros(qn, np.float32)
+    dk = np.zeros(kvn, np.float32)
+    dv = np.zeros(kvn, np.float32)
+    rc = lib().ora_backward_grouped(_ptr(q), _ptr(k), _ptr(v), _ptr(d_out), _ptr(out), _ptr(lse),
+                                    _U64(batch), _U64(q_heads), _U64(kv_heads), _U64(seq),
+                                    _U64(dim), _I(int(causal)), _F(s), _ptr(dq), _ptr(dk),
+                                    _ptr(dv), _I(threads))
+    _check(rc, "backward_grouped")
+    return dq, dk, dv
 
 
 def forward_grouped_rope(q, k, v, batch, q_heads, kv_heads, seq, dim, causal, theta,

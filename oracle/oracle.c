@@ -474,6 +474,77 @@ int ora_paged_prefill(const float* q, const float* k_pool, const float* v_pool,
 /* ------------------------------------------------------------------ 16-bit formats ---- */
 
 /* F16::from_f32 src/f16.rs:26-80 */
+/* ------------------------------------------------------------------ recompute backward */
+/* backward_reference_grouped src/backward_grouped.rs:17-95 (backward_reference
+ * src/backward.rs:27 is its q_heads == kv_heads case). One unit is one (batch, kv head): its
+ * query heads run in ascending order inside the unit, so the dK/dV accumulation order of every
+ * element is the reference's (batch, q_head, query, key) order. */
+typedef struct {
+    const float *q, *k, *v, *d_out, *out, *lse;
+    uint64_t q_heads, kv_heads, seq, dim;
+    int causal;
+    float scale;
+    float *dq, *dk, *dv;
+} bwd_args;
+
+static void bwd_unit(void* p, uint64_t unit) {
+    const bwd_args* a = (const bwd_args*)p;
+    uint64_t batch = unit / a->kv_heads, kv_head = unit % a->kv_heads;
+    uint64_t group_size = a->q_heads / a->kv_heads;
+    uint64_t head_stride = a->seq * a->dim;
+    uint64_t kv_bh = batch * a->kv_heads + kv_head;
+    uint64_t kv_head_base = kv_bh * head_stride;
+    for (uint64_t q_head = kv_head * group_size; q_head < (kv_head + 1) * group_size; ++q_head) {
+        uint64_t q_bh = batch * a->q_heads + q_head;
+        uint64_t q_head_base = q_bh * head_stride, lse_base = q_bh * a->seq;
+        for (uint64_t qp = 0; qp < a->seq; ++qp) {
+            uint64_t q_base = q_head_base + qp * a->dim;
+            float lse = a->lse[lse_base + qp];
+            float delta = 0.0f;
+            for (uint64_t d = 0; d < a->dim; ++d) delta += a->d_out[q_base + d] * a->out[q_base + d];
+            uint64_t key_limit = a->causal ? qp + 1 : a->seq;
+            for (uint64_t kp = 0; kp < key_limit; ++kp) {
+                uint64_t kv_base = kv_head_base + kp * a->dim;
+                float dot_qk = 0.0f, d_probability = 0.0f;
+                for (uint64_t d = 0; d < a->dim; ++d) {
+                    dot_qk += a->q[q_base + d] * a->k[kv_base + d];
+                    d_probability += a->d_out[q_base + d] * a->v[kv_base + d];
+                }
+                float score = dot_qk * a->scale;
+                float probability = expf(score - lse);
+                float d_score = probability * (d_probability - delta);
+                float d_dot = d_score * a->scale;
+                for (uint64_t d = 0; d < a->dim; ++d) {
+                    a->dq[q_base + d] += d_dot * a->k[kv_base + d];
+                    a->dk[kv_base + d] += d_dot * a->q[q_base + d];
+                    a->dv[kv_base + d] += probability * a->d_out[q_base + d];
+                }
+            }
+        }
+    }
+}
+
+int ora_backward_grouped(const float* q, const float* k, const float* v, const float* d_out,
+                         const float* out, const float* lse, uint64_t batch, uint64_t q_heads,
+                         uint64_t kv_heads, uint64_t seq, uint64_t dim, int causal, float scale,
+                         float* dq, float* dk, float* dv, int threads) {
+    /* GroupedAttentionShape::validate src/grouped.rs:24 */
+    if (!batch || !q_heads || !kv_heads || !seq || !dim) return FA_ERR_ZERO_DIMENSION;
+    if (q_heads % kv_heads) return FA_ERR_INVALID_HEAD_GROUPING;
+    if (!isfinite(scale) || scale <= 0.0f) return FA_ERR_INVALID_SCALE;
+    uint64_t qn, kvn, units;
+    if (!mul_ok(batch, q_heads, &qn) || !mul_ok(qn, seq, &qn) || !mul_ok(qn, dim, &qn) ||
+        !mul_ok(batch, kv_heads, &units) || !mul_ok(units, seq, &kvn) || !mul_ok(kvn, dim, &kvn))
+        return FA_ERR_SHAPE_OVERFLOW;
+    memset(dq, 0, (size_t)qn * sizeof(float));
+    memset(dk, 0, (size_t)kvn * sizeof(float));
+    memset(dv, 0, (size_t)kvn * sizeof(float));
+    bwd_args a = {q, k, v, d_out, out, lse, q_heads, kv_heads, seq, dim, causal, scale,
+                  dq, dk, dv};
+    run_units(bwd_unit, &a, units, 0, units, threads);
+    return FA_OK;
+}
+
 uint16_t ora_f32_to_f16(float value) {
     uint32_t bits;
     memcpy(&bits, &value, 4);

@@ -109,6 +109,14 @@ void ora_f16_to_f32_array(const uint16_t* in, float* out, uint64_t n);
  * 1442695040888963407, tests/m38_property_stress.rs:7-30) driving Box-Muller N(0,1) in f32. */
 void ora_fill_normal(float* out, uint64_t n, uint64_t seed);
 
+/* backward_reference_grouped src/backward_grouped.rs:17-95: dQ, dK, dV recomputed from
+ * Q, K, V, dO and the forward's O and LSE ([B,H,S,D] / [B,Hkv,S,D] / [B,H,S]). Threads split
+ * the (batch, kv head) units; each unit keeps the reference's accumulation order. */
+int ora_backward_grouped(const float* q, const float* k, const float* v, const float* d_out,
+                         const float* out, const float* lse, uint64_t batch, uint64_t q_heads,
+                         uint64_t kv_heads, uint64_t seq, uint64_t dim, int causal, float scale,
+                         float* dq, float* dk, float* dv, int threads);
+
 #ifdef __cplusplus
 }
 #endif
