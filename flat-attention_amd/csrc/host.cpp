@@ -154,6 +154,9 @@ struct fa_ctx {
     // growable scratch for the transposed V copy of the prefill
     void* ws_vt = nullptr;
     size_t ws_vt_bytes = 0;
+    // growable scratch for the backward's per-row delta = rowsum(dO * O)
+    void* ws_delta = nullptr;
+    size_t ws_delta_bytes = 0;
     int transpose_v_policy = -1;
     // per-sequence metadata of variable-length prefill: device copy + pinned staging, reused
     // once the event recorded after the previous copy has completed
@@ -463,6 +466,7 @@ int fa_ctx_destroy(fa_ctx* ctx) {
     if (ctx->inv_freq) (void)hipFree(ctx->inv_freq);
     if (ctx->ws) (void)hipFree(ctx->ws);
     if (ctx->ws_vt) (void)hipFree(ctx->ws_vt);
+    if (ctx->ws_delta) (void)hipFree(ctx->ws_delta);
     if (ctx->meta_dev) (void)hipFree(ctx->meta_dev);
     if (ctx->meta_host) (void)hipHostFree(ctx->meta_host);
     if (ctx->meta_event) (void)hipEventDestroy(ctx->meta_event);
@@ -2201,6 +2205,117 @@ int fa_paged_append_batched(fa_ctx* ctx, const int32_t* block_tables, uint64_t m
            (unsigned)std::min<uint64_t>(256, std::max<uint64_t>(64, kv_heads * head_dim / 8)), 1, 1,
            nullptr);
     return ok();
+}
+
+// ------------------------------------------------------------------ recompute backward
+// WgpuGroupedBackwardRecomputePipeline src/wgpu_backward_grouped.rs:181-329.
+
+int fa_backward_grouped_layout(const fa_grouped_shape* sh, int dtype, fa_backward_layout* out) {
+    if (!sh || !out) return fail(FA_ERR_NULL_ARGUMENT, "null argument");
+    if (int rc = check_dtype(dtype)) return rc;
+    // shape.validate() then the checked tensor lengths (src/wgpu_backward_grouped.rs:184-187)
+    if (!sh->batch || !sh->q_heads || !sh->kv_heads || !sh->seq_len || !sh->head_dim)
+        return fail(FA_ERR_ZERO_DIMENSION, "attention dimensions must all be non-zero");
+    if (sh->q_heads % sh->kv_heads)
+        return fail(FA_ERR_INVALID_HEAD_GROUPING,
+                    "q_heads (%llu) must be exactly divisible by kv_heads (%llu)",
+                    (unsigned long long)sh->q_heads, (unsigned long long)sh->kv_heads);
+    uint64_t qn, kvn, ln, eb = (uint64_t)elem_bytes(dtype), fwd, grads, t;
+    if (mul_ov(sh->batch, sh->q_heads, &ln) || mul_ov(ln, sh->seq_len, &ln) ||
+        mul_ov(ln, sh->head_dim, &qn) || mul_ov(sh->batch, sh->kv_heads, &kvn) ||
+        mul_ov(kvn, sh->seq_len, &kvn) || mul_ov(kvn, sh->head_dim, &kvn) ||
+        mul_ov(qn, 3 * eb, &fwd) || mul_ov(kvn, 2 * eb, &t) || fwd + t < fwd)
+        return fail(FA_ERR_SHAPE_OVERFLOW, "backward shape overflows the address space");
+    fwd += t;
+    if (mul_ov(ln, 4, &t) || fwd + t < fwd || mul_ov(qn, eb, &grads) ||
+        mul_ov(kvn, 2 * eb, &t) || grads + t < grads)
+        return fail(FA_ERR_SHAPE_OVERFLOW, "backward shape overflows the address space");
+    grads += t;
+    fwd += ln * 4;
+    fa_backward_layout& l = *out;
+    l.q_elements = qn;
+    l.kv_elements = kvn;
+    l.lse_elements = ln;
+    l.q_offset = 0;
+    l.k_offset = qn * eb;
+    l.v_offset = l.k_offset + kvn * eb;
+    l.d_out_offset = l.v_offset + kvn * eb;
+    l.output_offset = l.d_out_offset + qn * eb;
+    l.lse_offset = l.output_offset + qn * eb;
+    l.packed_forward_bytes = fwd;
+    l.dq_offset = 0;
+    l.dk_offset = qn * eb;
+    l.dv_offset = l.dk_offset + kvn * eb;
+    l.gradient_bytes = grads;
+    return ok();
+}
+
+int fa_backward_grouped(fa_ctx* ctx, const void* q, const void* k, const void* v,
+                        const void* d_out, const void* out, const float* lse, void* dq, void* dk,
+                        void* dv, const fa_grouped_shape* sh, const fa_config* cfg, int dtype) {
+    fa_backward_layout lay;
+    if (int rc = fa_backward_grouped_layout(sh, dtype, &lay)) return rc;
+    if (int rc = validate_grouped(sh->batch, sh->q_heads, sh->kv_heads, sh->seq_len, sh->head_dim))
+        return rc;
+    if (int rc = check_head_dim(sh->head_dim, dtype)) return rc;
+    const void* ptrs[] = {q, k, v, d_out, out, lse, dq, dk, dv};
+    for (const void* p : ptrs)
+        if (!p) return fail(FA_ERR_NULL_ARGUMENT, "backward tensor pointer is null");
+    float scale;
+    if (int rc = resolve_scale(cfg, sh->head_dim, &scale)) return rc;
+    if (!ctx) return fail(FA_ERR_NULL_ARGUMENT, "context is null");
+    begin_call(ctx);
+    if (int rc = set_device(ctx)) return rc;
+    void* delta = nullptr;
+    if (int rc = grow(ctx, &ctx->ws_delta, &ctx->ws_delta_bytes, lay.lse_elements * 4, &delta))
+        return rc;
+
+    fa::BackwardArgs a{};
+    a.q = q; a.k = k; a.v = v; a.dout = d_out; a.o = out; a.lse = lse;
+    a.dq = dq; a.dk = dk; a.dv = dv;
+    a.delta = (float*)delta;
+    a.batch = (int)sh->batch;
+    a.q_heads = (int)sh->q_heads;
+    a.kv_heads = (int)sh->kv_heads;
+    a.group = (int)(sh->q_heads / sh->kv_heads);
+    a.seq = (int)sh->seq_len;
+    a.head_dim = (int)sh->head_dim;
+    a.causal = cfg && cfg->causal;
+    a.scale = scale;
+    const uint64_t chunk = 16 / (uint64_t)elem_bytes(dtype);
+    bool vec = sh->head_dim % chunk == 0;
+    for (const void* p : ptrs) vec = vec && ((uintptr_t)p % 16 == 0);
+    a.vec = vec;
+    begin_span(ctx);
+    fa::launch_backward((Dtype)dtype, a, ctx->stream);
+    end_span(ctx, FA_KERNEL_BACKWARD_RECOMPUTE);
+    HIP_TRY(hipGetLastError());
+    const unsigned grid[3] = {(unsigned)(((sh->seq_len + 127) / 128) * sh->batch * sh->kv_heads),
+                              1, 1};
+    char name[64];
+    snprintf(name, sizeof name, "bwd_delta + bwd_dkdv + bwd_dq<%s>", dtype_name(dtype));
+    record(ctx, FA_KERNEL_BACKWARD_RECOMPUTE, name, 128, 64, grid, 256, 3, 1,
+           vec ? nullptr : "unaligned tensors or head_dim off the 16-byte chunk: scalar loads");
+    return ok();
+}
+
+int fa_backward_grouped_recompute(fa_ctx* ctx, const void* packed_forward, size_t forward_bytes,
+                                  void* packed_grads, size_t grads_bytes,
+                                  const fa_grouped_shape* sh, const fa_config* cfg, int dtype) {
+    fa_backward_layout lay;
+    if (int rc = fa_backward_grouped_layout(sh, dtype, &lay)) return rc;
+    // validate_buffer order of prepare (src/wgpu_backward_grouped.rs:236-241)
+    if (int rc = check_buffer("Q|K|V|dO|O|LSE", packed_forward, forward_bytes,
+                              lay.packed_forward_bytes))
+        return rc;
+    if (int rc = check_buffer("dQ|dK|dV", packed_grads, grads_bytes, lay.gradient_bytes))
+        return rc;
+    const uint8_t* f = (const uint8_t*)packed_forward;
+    uint8_t* gr = (uint8_t*)packed_grads;
+    return fa_backward_grouped(ctx, f + lay.q_offset, f + lay.k_offset, f + lay.v_offset,
+                               f + lay.d_out_offset, f + lay.output_offset,
+                               (const float*)(f + lay.lse_offset), gr + lay.dq_offset,
+                               gr + lay.dk_offset, gr + lay.dv_offset, sh, cfg, dtype);
 }
 
 }  // extern "C"

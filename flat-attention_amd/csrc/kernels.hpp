@@ -88,6 +88,27 @@ void launch_decode(Dtype dt, const DecodeArgs& a, hipStream_t s, unsigned grid[3
                    unsigned* block, int* dispatches, bool* mfma, void (*between)(void*),
                    void* user);
 
+// Recompute backward of grouped attention. Q, dO, O, dQ: [batch, q_heads, seq, head_dim];
+// K, V, dK, dV: [batch, kv_heads, seq, head_dim]; LSE and delta: [batch, q_heads, seq] f32.
+// `delta` is scratch of batch*q_heads*seq floats (rowsum of dO * O, written by the first
+// launch). vec: head_dim is a multiple of the 16-byte chunk and every tensor 16-byte aligned.
+struct BackwardArgs {
+    const void* q;
+    const void* k;
+    const void* v;
+    const void* dout;
+    const void* o;
+    const float* lse;
+    void* dq;
+    void* dk;
+    void* dv;
+    float* delta;
+    int batch, q_heads, kv_heads, group, seq, head_dim, causal, vec;
+    float scale;
+};
+// Three launches: delta, dK/dV, dQ.
+void launch_backward(Dtype dt, const BackwardArgs& a, hipStream_t s);
+
 // (cos, sin) table: table[pos*half + p] for pos < rows, p < half = head_dim/2, with
 // angle = float(pos) * inv_freq[p].
 void launch_rope_table(float2* table, const float* inv_freq, int rows, int half, hipStream_t s);

@@ -41,6 +41,7 @@ KERNEL_IDS = {
     4: "PrefillMfmaBf16PreRotatedK", 5: "PrefillMfmaF16PreRotatedK",
     6: "PrefillMfmaF32PreRotatedK", 10: "DecodePagedSplitK", 11: "DecodeCombine",
     12: "PagedAppend", 13: "RopeTable", 14: "RopeRotate", 15: "DecodePagedMfma", 16: "TransposeV",
+    17: "BackwardRecompute",
 }
 
 
@@ -78,6 +79,13 @@ class AsymmetricRotaryC(ctypes.Structure):
 class PackedLayoutC(ctypes.Structure):
     _fields_ = [("output_elements", U64), ("lse_elements", U64), ("output_bytes", U64),
                 ("lse_byte_offset", U64), ("combined_bytes", U64)]
+
+
+class BackwardLayoutC(ctypes.Structure):
+    _fields_ = [(n, U64) for n in (
+        "q_elements", "kv_elements", "lse_elements", "packed_forward_bytes", "gradient_bytes",
+        "q_offset", "k_offset", "v_offset", "d_out_offset", "output_offset", "lse_offset",
+        "dq_offset", "dk_offset", "dv_offset")]
 
 
 class TelemetryC(ctypes.Structure):
@@ -176,6 +184,11 @@ PROTOTYPES = {
     "fa_prefill_plan_destroy": (INT, [VP]),
     "fa_paged_append_batched": (INT, [VP, VP, U64, VP, U64, U64, U64, U64, U64, U64, VP, VP, SZ,
                                       VP, VP, SZ, P(RotaryC), INT]),
+    "fa_backward_grouped_layout": (INT, [P(GroupedShapeC), INT, P(BackwardLayoutC)]),
+    "fa_backward_grouped_recompute": (INT, [VP, VP, SZ, VP, SZ, P(GroupedShapeC), P(ConfigC),
+                                            INT]),
+    "fa_backward_grouped": (INT, [VP, VP, VP, VP, VP, VP, VP, VP, VP, VP, P(GroupedShapeC),
+                                  P(ConfigC), INT]),
     "fa_last_telemetry": (INT, [VP, P(TelemetryC)]),
     "fa_ctx_set_kernel_timing": (INT, [VP, I32]),
     "fa_ctx_kernel_timing": (INT, [VP, I32, P(ctypes.c_double), P(U64)]),

@@ -889,3 +889,155 @@ def paged_append_batched(ctx: HipContext, block_tables: np.ndarray, start_lens: 
                                         kv_heads, head_dim, k_src.ptr, v_src.ptr,
                                         min(k_src.nbytes, v_src.nbytes), k_pool.ptr, v_pool.ptr,
                                         min(k_pool.nbytes, v_pool.nbytes), rot, dtype))
+
+
+# ----------------------------------------------------------------------------- backward
+
+@dataclass
+class FlatAttentionBackwardOutput:
+    """FlatAttentionBackwardOutput src/backward.rs:12 (dq, dk, dv as float32 arrays)."""
+    dq: np.ndarray
+    dk: np.ndarray
+    dv: np.ndarray
+
+
+@dataclass(frozen=True)
+class GroupedBackwardRecomputeLayout:
+    """GroupedBackwardRecomputeLayout src/wgpu_backward_grouped.rs:18. Offsets and sizes are in
+    bytes: tensors are stored in the pipeline dtype and LSE in f32 (for f32 every offset is the
+    reference's element offset times 4)."""
+    q_elements: int
+    kv_elements: int
+    lse_elements: int
+    packed_forward_bytes: int
+    gradient_bytes: int
+    q_offset: int
+    k_offset: int
+    v_offset: int
+    d_out_offset: int
+    output_offset: int
+    lse_offset: int
+    dq_offset: int
+    dk_offset: int
+    dv_offset: int
+
+
+@dataclass(frozen=True)
+class PreparedGroupedBackwardRecompute:
+    """PreparedGroupedBackwardRecompute src/wgpu_backward_grouped.rs:124: a validated
+    (buffers, shape, config) tuple that encode_prepared launches without re-deriving it."""
+    packed_forward: DeviceBuffer
+    packed_grads: DeviceBuffer
+    shape: GroupedAttentionShape
+    config: FlatAttentionConfig
+    layout: GroupedBackwardRecomputeLayout
+    scale: float
+
+
+def grouped_backward_layout(shape: GroupedAttentionShape,
+                            dtype: int) -> GroupedBackwardRecomputeLayout:
+    """WgpuGroupedBackwardRecomputePipeline::layout src/wgpu_backward_grouped.rs:181."""
+    c = L.BackwardLayoutC()
+    check(lib().fa_backward_grouped_layout(ctypes.byref(shape.c()), dtype, ctypes.byref(c)))
+    return GroupedBackwardRecomputeLayout(*(getattr(c, n) for n, _ in c._fields_))
+
+
+class HipGroupedBackwardRecomputePipeline:
+    """WgpuGroupedBackwardRecomputePipeline src/wgpu_backward_grouped.rs:146: recompute
+    backward of native GQA/MQA attention over the packed Q|K|V|dO|O|LSE -> dQ|dK|dV contract."""
+
+    def __init__(self, ctx: HipContext, dtype: int = L.DTYPE_F32):
+        self.ctx = ctx
+        self.dtype = dtype
+
+    def layout(self, shape: GroupedAttentionShape) -> GroupedBackwardRecomputeLayout:
+        return grouped_backward_layout(shape, self.dtype)
+
+    def create_gradient_buffer(self, shape: GroupedAttentionShape) -> DeviceBuffer:
+        return DeviceBuffer(self.ctx, self.layout(shape).gradient_bytes)
+
+    def prepare(self, packed_forward: DeviceBuffer, packed_grads: DeviceBuffer,
+                shape: GroupedAttentionShape,
+                config: FlatAttentionConfig) -> PreparedGroupedBackwardRecompute:
+        lay = self.layout(shape)
+        for name, buf, need in (("Q|K|V|dO|O|LSE", packed_forward, lay.packed_forward_bytes),
+                                ("dQ|dK|dV", packed_grads, lay.gradient_bytes)):
+            if buf.nbytes < need:
+                raise L.FlatHipError(24, f"buffer {name} contains {buf.nbytes} bytes, requires "
+                                         f"at least {need}")
+        scale = ctypes.c_float()
+        check(lib().fa_resolved_scale(ctypes.byref(config.c()), shape.head_dim,
+                                      ctypes.byref(scale)))
+        return PreparedGroupedBackwardRecompute(packed_forward, packed_grads, shape, config, lay,
+                                                scale.value)
+
+    def encode_prepared(self, prepared: PreparedGroupedBackwardRecompute
+                        ) -> GroupedBackwardRecomputeLayout:
+        p = prepared
+        check(lib().fa_backward_grouped_recompute(
+            self.ctx.handle, p.packed_forward.ptr, p.packed_forward.nbytes, p.packed_grads.ptr,
+            p.packed_grads.nbytes, ctypes.byref(p.shape.c()), ctypes.byref(p.config.c()),
+            self.dtype))
+        return p.layout
+
+    def encode(self, packed_forward: DeviceBuffer, packed_grads: DeviceBuffer,
+               shape: GroupedAttentionShape,
+               config: FlatAttentionConfig) -> GroupedBackwardRecomputeLayout:
+        return self.encode_prepared(self.prepare(packed_forward, packed_grads, shape, config))
+
+    def encode_tensors(self, q, k, v, d_out, out, lse_ptr: int, dq, dk, dv,
+                       shape: GroupedAttentionShape, config: FlatAttentionConfig):
+        """fa_backward_grouped over separate device tensors (DeviceBuffer-like objects with
+        ``ptr``); ``lse_ptr`` is a raw device address of the f32 LSE rows."""
+        check(lib().fa_backward_grouped(self.ctx.handle, q.ptr, k.ptr, v.ptr, d_out.ptr, out.ptr,
+                                        lse_ptr, dq.ptr, dk.ptr, dv.ptr,
+                                        ctypes.byref(shape.c()), ctypes.byref(config.c()),
+                                        self.dtype))
+
+    def download_gradients(self, grads: DeviceBuffer,
+                           shape: GroupedAttentionShape) -> FlatAttentionBackwardOutput:
+        lay = self.layout(shape)
+        sd = storage_np_dtype(self.dtype)
+        parts = [grads.download(sd, n, off) for n, off in ((lay.q_elements, lay.dq_offset),
+                                                          (lay.kv_elements, lay.dk_offset),
+                                                          (lay.kv_elements, lay.dv_offset))]
+        return FlatAttentionBackwardOutput(*(storage_to_f32(x, self.dtype) for x in parts))
+
+    def backward(self, q, k, v, d_out, forward: FlatAttentionOutput,
+                 shape: GroupedAttentionShape,
+                 config: FlatAttentionConfig) -> FlatAttentionBackwardOutput:
+        """Host convenience: pack, upload, encode, download (float32 gradients)."""
+        packed = pack_grouped_backward_recompute_inputs(q, k, v, d_out, forward, shape,
+                                                        self.dtype, self.layout(shape))
+        fwd = DeviceBuffer.from_array(self.ctx, packed)
+        grads = self.create_gradient_buffer(shape)
+        self.encode(fwd, grads, shape, config)
+        res = self.download_gradients(grads, shape)
+        fwd.free()
+        grads.free()
+        return res
+
+
+def pack_grouped_backward_recompute_inputs(q, k, v, d_out, forward: FlatAttentionOutput,
+                                           shape: GroupedAttentionShape,
+                                           dtype: int = L.DTYPE_F32,
+                                           layout: Optional[GroupedBackwardRecomputeLayout] = None
+                                           ) -> np.ndarray:
+    """pack_grouped_backward_recompute_inputs src/wgpu_backward_grouped.rs:331 as bytes: Q, K,
+    V, dO, O in the storage dtype (float32 inputs are converted; storage arrays pass through),
+    then LSE f32. Lengths are validated like validate_input (LengthMismatch)."""
+    lay = layout or grouped_backward_layout(shape, dtype)
+    sd = storage_np_dtype(dtype)
+    parts = []
+    for name, x, n in (("Q", q, lay.q_elements), ("K", k, lay.kv_elements),
+                       ("V", v, lay.kv_elements), ("dO", d_out, lay.q_elements),
+                       ("O", forward.output, lay.q_elements)):
+        x = np.asarray(x).ravel()
+        if x.size != n:
+            raise L.FlatHipError(7, f"{name} has {x.size} values, expected {n}")
+        parts.append(np.ascontiguousarray(x if x.dtype == sd else host_storage(x, dtype)))
+    lse = np.ascontiguousarray(np.asarray(forward.lse, np.float32).ravel())
+    if lse.size != lay.lse_elements:
+        raise L.FlatHipError(7, f"LSE has {lse.size} values, expected {lay.lse_elements}")
+    parts.append(lse)
+    return np.concatenate([p.view(np.uint8) for p in parts])

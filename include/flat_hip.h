@@ -138,7 +138,8 @@ typedef enum fa_kernel_id {
     FA_KERNEL_ROPE_TABLE = 13,
     FA_KERNEL_ROPE_ROTATE = 14,
     FA_KERNEL_DECODE_PAGED_MFMA = 15,     /* 16-bit KV, page_size % 16 == 0: P.V on MFMA */
-    FA_KERNEL_TRANSPOSE_V = 16            /* V -> V^T pre-pass of the 16-bit contiguous prefill */
+    FA_KERNEL_TRANSPOSE_V = 16,           /* V -> V^T pre-pass of the 16-bit contiguous prefill */
+    FA_KERNEL_BACKWARD_RECOMPUTE = 17     /* delta + dK/dV + dQ recompute backward (MFMA) */
 } fa_kernel_id;
 
 /* RuntimeDispatchTelemetry src/runtime_telemetry.rs:159 + RuntimeTileGeometry :151 +
@@ -381,6 +382,36 @@ int fa_resident_cache_decode(fa_ctx* ctx, const fa_resident_cache* cache, const 
                              size_t q_bytes, uint64_t q_heads, const fa_config* config,
                              float theta, uint64_t q_rope_position, void* out_lse,
                              size_t out_bytes);
+
+/* ------------------------------------------------------------ recompute backward -------- */
+/* WgpuGroupedBackwardRecomputeLayout src/wgpu_backward_grouped.rs:17-56: the packed contract
+ * Q|K|V|dO|O|LSE (forward side) and dQ|dK|dV (gradients). Q, dO, O, dQ hold
+ * [batch, q_heads, seq, head_dim], K, V, dK, dV [batch, kv_heads, seq, head_dim] (native KV-head
+ * cardinality), LSE [batch, q_heads, seq]. Tensors are `dtype` elements, LSE is f32; offsets and
+ * sizes here are in BYTES (for f32 they are the reference's element offsets times 4). */
+typedef struct fa_backward_layout {
+    uint64_t q_elements, kv_elements, lse_elements;
+    uint64_t packed_forward_bytes, gradient_bytes;
+    uint64_t q_offset, k_offset, v_offset, d_out_offset, output_offset, lse_offset;
+    uint64_t dq_offset, dk_offset, dv_offset;
+} fa_backward_layout;
+/* WgpuGroupedBackwardRecomputePipeline::layout src/wgpu_backward_grouped.rs:181 */
+int fa_backward_grouped_layout(const fa_grouped_shape* shape, int dtype, fa_backward_layout* out);
+/* WgpuGroupedBackwardRecomputePipeline::encode src/wgpu_backward_grouped.rs:318 (prepare :231 +
+ * encode_prepared :302): dQ, dK, dV recomputed from the packed forward buffer into the packed
+ * gradient buffer (shaders/flat_backward_grouped_recompute.wgsl; CPU oracle
+ * backward_reference_grouped src/backward_grouped.rs:17). Buffer sizes are checked against the
+ * layout (FA_ERR_BUFFER_TOO_SMALL). Deterministic: every gradient element has one writer. */
+int fa_backward_grouped_recompute(fa_ctx* ctx, const void* packed_forward, size_t forward_bytes,
+                                  void* packed_grads, size_t grads_bytes,
+                                  const fa_grouped_shape* shape, const fa_config* config,
+                                  int dtype);
+/* The same backward over separate tensors (e.g. O|LSE straight from fa_forward_gqa_rope's packed
+ * output): q, d_out, out, dq hold q_elements, k, v, dk, dv kv_elements, lse lse_elements. */
+int fa_backward_grouped(fa_ctx* ctx, const void* q, const void* k, const void* v,
+                        const void* d_out, const void* out, const float* lse, void* dq, void* dk,
+                        void* dv, const fa_grouped_shape* shape, const fa_config* config,
+                        int dtype);
 
 /* ------------------------------------------------------------ chunked prefill (paged) ---
  * Chunked prefill whose K/V live in the shared page pool: the chunk's queries

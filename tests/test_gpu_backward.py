@@ -1,0 +1,197 @@
+"""GPU parity of the recompute backward (M19-M21, WgpuGroupedBackwardRecomputePipeline,
+src/wgpu_backward_grouped.rs) against the CPU oracle (backward_reference_grouped,
+src/backward_grouped.rs:17).
+
+Cases follow the reference's GPU tests: the M19 GQA/MQA pair (tests/m19_grouped_backward_wgpu.rs,
+tolerance 4e-4 + 2e-3|e|), the M20 stress matrix with three repeated encodes
+(tests/m20_grouped_backward_stress.rs, 5e-4 + 2.5e-3|e|) and the M21 prepared-reuse cases with
+four encode_prepared calls (tests/m21_prepared_grouped_backward_reuse.rs, 4e-4 + 2e-3|e|), then
+tile-crossing sequence lengths and head dims up to 128, 16-bit storage, bitwise determinism and
+the separate-tensor entry fed by this library's own forward.
+
+16-bit storage: the oracle runs on the bf16/f16-rounded inputs (and the forward it was given);
+the kernel rounds P and dS to the storage type for the MFMA products and stores gradients in it,
+so the bound is 2e-2 of the tensor's largest magnitude plus 2e-2|e|.
+"""
+import numpy as np
+import pytest
+
+import oracle
+from _inputs import bf16_round, f16_round, normal
+from conftest import assert_close
+
+import flat_attention_amd as fa
+
+pytestmark = pytest.mark.gpu
+
+
+def _fx(n, phase, step, a, b, w):
+    x = np.arange(n, dtype=np.float32) * np.float32(step) + np.float32(phase)
+    return (np.sin(x) * np.float32(a) + np.cos(x * np.float32(w)) * np.float32(b)).astype(np.float32)
+
+
+def fx_m19(n, phase):  # tests/m19_grouped_backward_wgpu.rs:49
+    return _fx(n, phase, 0.071, 0.75, 0.25, 0.37)
+
+
+def fx_m20(n, phase):  # tests/m20_grouped_backward_stress.rs:49
+    return _fx(n, phase, 0.031, 0.63, 0.37, 0.47)
+
+
+def fx_m21(n, phase):  # tests/m21_prepared_grouped_backward_reuse.rs:48
+    return _fx(n, phase, 0.053, 0.7, 0.3, 0.37)
+
+
+def _expected(q, k, v, do, shape, causal, scale):
+    s = shape
+    o, lse = oracle.forward_grouped(q, k, v, s.batch, s.q_heads, s.kv_heads, s.seq_len,
+                                    s.head_dim, causal, scale)
+    grads = oracle.backward_grouped(q, k, v, do, o, lse, s.batch, s.q_heads, s.kv_heads,
+                                    s.seq_len, s.head_dim, causal, scale, threads=8)
+    return fa.FlatAttentionOutput(o, lse), grads
+
+
+def _check(tag, got, want, atol, rtol):
+    for name, a, e in zip(("dQ", "dK", "dV"), (got.dq, got.dk, got.dv), want):
+        assert_close(f"{tag}-{name}", a, e, atol, rtol)
+
+
+def _packed_case(hip, shape, config, fixture, phases, repeats, atol, rtol, prepared=False):
+    q = fixture(shape.q_tensor_len(), phases[0])
+    k = fixture(shape.kv_tensor_len(), phases[1])
+    v = fixture(shape.kv_tensor_len(), phases[2])
+    do = fixture(shape.q_tensor_len(), phases[3])
+    fwd, want = _expected(q, k, v, do, shape, config.causal, config.softmax_scale)
+    pipe = fa.HipGroupedBackwardRecomputePipeline(hip, fa.DTYPE_F32)
+    packed = fa.pack_grouped_backward_recompute_inputs(q, k, v, do, fwd, shape)
+    fbuf = fa.DeviceBuffer.from_array(hip, packed)
+    gbuf = pipe.create_gradient_buffer(shape)
+    prep = pipe.prepare(fbuf, gbuf, shape, config) if prepared else None
+    for rep in range(repeats):
+        gbuf.fill_u32(0x7FC00000)  # NaN: every gradient element must be written
+        lay = pipe.encode_prepared(prep) if prepared else pipe.encode(fbuf, gbuf, shape, config)
+        assert lay == pipe.layout(shape)
+        got = pipe.download_gradients(gbuf, shape)
+        _check(f"{shape}-causal{config.causal}-rep{rep}", got, want, atol, rtol)
+    tele = hip.last_telemetry()
+    assert tele.kernel_id == "BackwardRecompute" and tele.dispatch_count == 3
+    fbuf.free()
+    gbuf.free()
+
+
+@pytest.mark.parametrize("kv_heads,causal", [(2, True), (1, False)])
+def test_m19_gqa_mqa_matches_oracle(hip, kv_heads, causal):
+    shape = fa.GroupedAttentionShape(2, 4, kv_heads, 5, 8)
+    _packed_case(hip, shape, fa.FlatAttentionConfig(causal, 0.41), fx_m19,
+                 (0.1, 0.7, 1.3, 1.9), 1, 4e-4, 2e-3)
+
+
+M20_CASES = [((1, 1, 1, 1, 2), False, None), ((1, 4, 4, 3, 8), True, None),
+             ((2, 8, 2, 5, 16), False, 0.23), ((1, 8, 1, 9, 32), True, 0.17),
+             ((2, 12, 3, 7, 6), True, None)]
+
+
+@pytest.mark.parametrize("idx", range(len(M20_CASES)))
+def test_m20_stress_matrix_repeated(hip, idx):
+    dims, causal, scale = M20_CASES[idx]
+    ph = idx * 0.37
+    _packed_case(hip, fa.GroupedAttentionShape(*dims), fa.FlatAttentionConfig(causal, scale),
+                 fx_m20, (ph + 0.1, ph + 0.7, ph + 1.3, ph + 1.9), 3, 5e-4, 2.5e-3)
+
+
+@pytest.mark.parametrize("dims,causal,scale", [((1, 4, 4, 7, 8), True, None),
+                                               ((1, 8, 2, 9, 16), False, 0.27),
+                                               ((2, 4, 1, 5, 12), True, 0.31)])
+def test_m21_prepared_reuse(hip, dims, causal, scale):
+    _packed_case(hip, fa.GroupedAttentionShape(*dims), fa.FlatAttentionConfig(causal, scale),
+                 fx_m21, (0.1, 0.7, 1.3, 1.9), 4, 4e-4, 2e-3, prepared=True)
+
+
+# Tile edges: 64-row staged tiles, 128-row workgroups, 32-row waves; head dims padded to 32/64/128.
+@pytest.mark.parametrize("dims,causal", [
+    ((1, 4, 2, 130, 64), True), ((1, 4, 2, 130, 64), False), ((2, 2, 1, 257, 128), True),
+    ((1, 8, 8, 64, 128), False), ((1, 6, 2, 200, 96), True), ((1, 2, 1, 33, 40), True),
+    ((1, 4, 1, 129, 20), False), ((1, 4, 2, 96, 7), True)])
+def test_f32_tile_edges(hip, dims, causal):
+    shape = fa.GroupedAttentionShape(*dims)
+    B, Hq, Hkv, S, D = dims
+    q, k, v, do = (normal(n, 11 + i) for i, n in enumerate(
+        (B * Hq * S * D, B * Hkv * S * D, B * Hkv * S * D, B * Hq * S * D)))
+    _packed_case(hip, shape, fa.FlatAttentionConfig(causal), lambda n, p: (q, k, v, do)[int(p)],
+                 (0, 1, 2, 3), 1, 5e-4, 2.5e-3)
+
+
+@pytest.mark.parametrize("dtype", [fa.DTYPE_BF16, fa.DTYPE_F16])
+@pytest.mark.parametrize("dims,causal", [((1, 8, 2, 256, 128), True),
+                                         ((2, 4, 4, 130, 64), False),
+                                         ((1, 4, 1, 77, 32), True)])
+def test_16bit_storage(hip, dtype, dims, causal):
+    rnd = bf16_round if dtype == fa.DTYPE_BF16 else f16_round
+    shape = fa.GroupedAttentionShape(*dims)
+    B, Hq, Hkv, S, D = dims
+    q, k, v, do = (rnd(normal(n, 21 + i)) for i, n in enumerate(
+        (B * Hq * S * D, B * Hkv * S * D, B * Hkv * S * D, B * Hq * S * D)))
+    fwd, want = _expected(q, k, v, do, shape, causal, None)
+    fwd = fa.FlatAttentionOutput(rnd(fwd.output), fwd.lse)
+    # the oracle's gradients for the rounded O the kernel is given
+    want = oracle.backward_grouped(q, k, v, do, fwd.output, fwd.lse, B, Hq, Hkv, S, D, causal,
+                                   threads=8)
+    pipe = fa.HipGroupedBackwardRecomputePipeline(hip, dtype)
+    got = pipe.backward(q, k, v, do, fwd, shape, fa.FlatAttentionConfig(causal))
+    for name, a, e in zip(("dQ", "dK", "dV"), (got.dq, got.dk, got.dv), want):
+        assert_close(name, a, e, 2e-2 * float(np.abs(e).max()), 2e-2)
+
+
+def test_deterministic_bitwise(hip):
+    shape = fa.GroupedAttentionShape(1, 8, 2, 300, 128)
+    B, Hq, Hkv, S, D = 1, 8, 2, 300, 128
+    q, k, v, do = (bf16_round(normal(n, 31 + i)) for i, n in enumerate(
+        (B * Hq * S * D, B * Hkv * S * D, B * Hkv * S * D, B * Hq * S * D)))
+    fwd, _ = _expected(q, k, v, do, shape, True, None)
+    pipe = fa.HipGroupedBackwardRecomputePipeline(hip, fa.DTYPE_BF16)
+    packed = fa.pack_grouped_backward_recompute_inputs(q, k, v, do, fwd, shape, fa.DTYPE_BF16)
+    fbuf = fa.DeviceBuffer.from_array(hip, packed)
+    lay = pipe.layout(shape)
+    outs = []
+    for _ in range(3):
+        g = pipe.create_gradient_buffer(shape)
+        pipe.encode(fbuf, g, shape, fa.FlatAttentionConfig(True))
+        outs.append(g.download(np.uint8, lay.gradient_bytes))
+        g.free()
+    assert all(np.array_equal(outs[0], o) for o in outs[1:])
+
+
+@pytest.mark.parametrize("dtype", [fa.DTYPE_F32, fa.DTYPE_BF16])
+def test_training_chain_own_forward(hip, dtype):
+    """Forward (fa_forward_gqa_rope, no RoPE) -> backward (fa_backward_grouped) over the forward's
+    own packed O|LSE, like tests/m23_wgpu_training_chain.rs; checked against the oracle given the
+    same O and LSE."""
+    B, Hq, Hkv, S, D = 2, 8, 2, 192, 64
+    rnd = (lambda x: x) if dtype == fa.DTYPE_F32 else bf16_round
+    q, k, v, do = (rnd(normal(n, 41 + i)) for i, n in enumerate(
+        (B * Hq * S * D, B * Hkv * S * D, B * Hkv * S * D, B * Hq * S * D)))
+    shape = fa.GroupedAttentionShape(B, Hq, Hkv, S, D)
+    cfg = fa.FlatAttentionConfig(True)
+    fwd_pipe = fa.HipRotaryGroupedAttention(hip, dtype)
+    bq, bk, bv, bdo = (fwd_pipe.upload(x) for x in (q, k, v, do))
+    out = fwd_pipe.forward_resident(bq, bk, bv, shape, cfg, None)
+    res = fwd_pipe.download_attention(out, shape)
+    o = fa.storage_to_f32(res.output, dtype)
+    want = oracle.backward_grouped(q, k, v, do, o, res.lse, B, Hq, Hkv, S, D, True, threads=8)
+    pipe = fa.HipGroupedBackwardRecomputePipeline(hip, dtype)
+    lay = pipe.layout(shape)
+    eb = 4 if dtype == fa.DTYPE_F32 else 2
+    dq = fa.DeviceBuffer(hip, lay.q_elements * eb)
+    dk = fa.DeviceBuffer(hip, lay.kv_elements * eb)
+    dv = fa.DeviceBuffer(hip, lay.kv_elements * eb)
+    flay = fwd_pipe.layout(shape)
+    pipe.encode_tensors(bq, bk, bv, bdo, out, out.ptr + flay.lse_byte_offset, dq, dk, dv, shape,
+                        cfg)
+    sd = fa.storage_np_dtype(dtype)
+    got = [fa.storage_to_f32(b.download(sd, n), dtype)
+           for b, n in ((dq, lay.q_elements), (dk, lay.kv_elements), (dv, lay.kv_elements))]
+    for name, a, e in zip(("dQ", "dK", "dV"), got, want):
+        if dtype == fa.DTYPE_F32:
+            assert_close(name, a, e, 5e-4, 2.5e-3)
+        else:
+            assert_close(name, a, e, 2e-2 * float(np.abs(e).max()), 2e-2)

@@ -269,3 +269,47 @@ def test_append_batched_validation():
     assert call(bt=np.array([[0, 7]], np.int32)) == "InvalidPage"
     assert call(D=60) == "UnsupportedHeadDim"
     assert call() == "NullArgument"
+
+
+def _backward(shape=(2, 8, 2, 5, 16), dtype=fa.DTYPE_F32, fwd=None, grads=None, cfg=None):
+    sh = L.GroupedShapeC(*shape)
+    lay = L.BackwardLayoutC()
+    rc = fa.lib().fa_backward_grouped_layout(ctypes.byref(sh), dtype, ctypes.byref(lay))
+    if rc:
+        return _variant(rc)
+    fwd = lay.packed_forward_bytes if fwd is None else fwd
+    grads = lay.gradient_bytes if grads is None else grads
+    return _variant(fa.lib().fa_backward_grouped_recompute(
+        None, FAKE, fwd, FAKE, grads, ctypes.byref(sh),
+        ctypes.byref(cfg or L.ConfigC(0, 0, 0.0)), dtype))
+
+
+def test_backward_layout_matches_reference_offsets():
+    """GroupedBackwardRecomputeLayout src/wgpu_backward_grouped.rs:28-55 (element offsets,
+    times 4 bytes for f32): Q | K | V | dO | O | LSE and dQ | dK | dV."""
+    lay = fa.grouped_backward_layout(fa.GroupedAttentionShape(2, 8, 2, 5, 16), fa.DTYPE_F32)
+    qe, ke, le = 2 * 8 * 5 * 16, 2 * 2 * 5 * 16, 2 * 8 * 5
+    assert (lay.q_elements, lay.kv_elements, lay.lse_elements) == (qe, ke, le)
+    assert [lay.q_offset, lay.k_offset, lay.v_offset, lay.d_out_offset, lay.output_offset,
+            lay.lse_offset] == [4 * x for x in (0, qe, qe + ke, qe + 2 * ke, 2 * qe + 2 * ke,
+                                                3 * qe + 2 * ke)]
+    assert lay.packed_forward_bytes == 4 * (3 * qe + 2 * ke + le)
+    assert [lay.dq_offset, lay.dk_offset, lay.dv_offset, lay.gradient_bytes] == \
+        [0, 4 * qe, 4 * (qe + ke), 4 * (qe + 2 * ke)]
+    l16 = fa.grouped_backward_layout(fa.GroupedAttentionShape(2, 8, 2, 5, 16), fa.DTYPE_BF16)
+    assert l16.lse_offset == 2 * (3 * qe + 2 * ke) and l16.gradient_bytes == 2 * (qe + 2 * ke)
+
+
+def test_backward_validation_variants():
+    """prepare src/wgpu_backward_grouped.rs:231-246 order: shape, buffers (forward then
+    gradients), scale; then head-dim support; a null context is reported last."""
+    assert _backward(shape=(0, 8, 2, 5, 16)) == "ZeroDimension"
+    assert _backward(shape=(2, 6, 4, 5, 16)) == "InvalidHeadGrouping"
+    assert _backward(shape=(2**40, 2**20, 1, 2**20, 16)) == "ShapeOverflow"
+    assert _backward(fwd=100) == "BufferTooSmall"
+    assert _backward(grads=100) == "BufferTooSmall"
+    assert _backward(cfg=L.ConfigC(0, 1, -1.0)) == "InvalidScale"
+    assert _backward(shape=(1, 2, 1, 8, 256)) == "UnsupportedHeadDim"
+    assert _backward(shape=(1, 2, 1, 8, 12), dtype=fa.DTYPE_BF16) == "UnsupportedHeadDim"
+    assert _backward(shape=(1, 2, 1, 8, 6)) == "NullArgument"
+    assert _backward() == "NullArgument"
