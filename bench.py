@@ -191,6 +191,41 @@ def build_resident_decode(ctx, rng, dtype):
     return (lambda: plan.launch(q, k, v, out)), nbytes
 
 
+def build_backward(ctx, rng, S=4096):
+    """Recompute backward (dQ, dK, dV) at the prefill's shape without RoPE (the reference's
+    backward has none): causal GQA B2 Hq32 Hkv8 D128 bf16. Algorithmic work: the five
+    S x S x D products of attention backward (Q K^T, dO V^T, P^T dO, dS^T Q, dS K), i.e. 2.5x
+    the forward's FLOPs; the kernels recompute Q K^T and dO V^T once more for dQ."""
+    B, hq, hkv, D = 2, 32, 8, 128
+    shape = fa.GroupedAttentionShape(B, hq, hkv, S, D)
+    pipe = fa.HipGroupedBackwardRecomputePipeline(ctx, fa.DTYPE_BF16)
+    lay = pipe.layout(shape)
+    fwd = fa.DeviceBuffer(ctx, lay.packed_forward_bytes)
+    nq, nkv = lay.q_elements, lay.kv_elements
+    for off, n in ((lay.q_offset, nq), (lay.k_offset, nkv), (lay.v_offset, nkv),
+                   (lay.d_out_offset, nq)):
+        fwd.upload(bf16_normal(rng, n), off)
+    cfg = fa.FlatAttentionConfig(causal=True)
+    # O and LSE from this library's forward over the same Q, K, V
+    ex = fa.HipRotaryGroupedAttention(ctx, fa.DTYPE_BF16)
+    flay = ex.layout(shape)
+    out = fa.DeviceBuffer(ctx, flay.combined_bytes)
+    view = lambda off, n: fa.DeviceBuffer(ctx, n, fwd.ptr + off)  # noqa: E731
+    ex.forward_resident(view(lay.q_offset, nq * 2), view(lay.k_offset, nkv * 2),
+                        view(lay.v_offset, nkv * 2), shape, cfg, None, out)
+    ctx.synchronize()
+    ev = HipEvents()
+    ev.copy_d2d(fwd.ptr + lay.output_offset, out.ptr, nq * 2, ctx.stream)
+    ev.copy_d2d(fwd.ptr + lay.lse_offset, out.ptr + flay.lse_byte_offset, lay.lse_elements * 4,
+                ctx.stream)
+    ctx.synchronize()
+    out.free()
+    grads = pipe.create_gradient_buffer(shape)
+    prep = pipe.prepare(fwd, grads, shape, cfg)
+    flop = 10.0 * B * hq * D * S * (S + 1) / 2
+    return (lambda: pipe.encode_prepared(prep)), flop
+
+
 def measure_all_configs(ctx, ev, rng, steps):
     """The other BASELINE configs, each timed alone (op events + its kernel's own events)."""
     stream = ctx.stream
@@ -229,6 +264,13 @@ def measure_all_configs(ctx, ev, rng, steps):
     res["cfg5_batched_append_512"] = {
         "kernel": tel.kernel_name, "ms": round(op_ms, 4), "kernel_ms": round(k_ms, 4),
         "GB/s": round(append_bytes / (k_ms * 1e-3) / 1e9, 1)}
+    run, flop = build_backward(ctx, rng)
+    op_ms, k_ms, tel = timed(run)
+    tf = flop / (k_ms * 1e-3) / 1e12
+    res["backward_causal_gqa_B2_Hq32_Hkv8_N4096_D128_bf16"] = {
+        "kernel": tel.kernel_name, "ms": round(op_ms, 4), "kernel_ms": round(k_ms, 4),
+        "TFLOP/s": round(tf, 2), "frac": round(tf / PEAK_BF16_TFLOPS, 4),
+        "note": "algorithmic FLOPs = 2.5x forward (five S x S x D products); three launches"}
     for dt, name in ((fa.DTYPE_F32, "f32"), (fa.DTYPE_BF16, "bf16")):
         run, nbytes = build_resident_decode(ctx, rng, dt)
         op_ms, k_ms, tel = timed(run)

@@ -2,7 +2,7 @@
 // and the forward's O and LSE, without materialising the N x N probability matrix.
 //
 // Three launches, no atomics, one writer per gradient element (deterministic):
-//   bwd_delta  delta[b, h, q] = sum_d dO * O                                  (HBM bound)
+//   bwd_delta  (LSE log2 e, delta = sum_d dO * O) per query row                   (HBM bound)
 //   bwd_dkdv   one workgroup per (batch, kv head, 128 keys); every query head of the group and
 //              every visible query tile is swept, so dK/dV of a KV head are summed over its
 //              query heads in registers (native KV-head cardinality, no expansion);
@@ -14,6 +14,8 @@
 // 32x32x2 f32 for f32 storage.
 #include "common.hpp"
 #include "kernels.hpp"
+
+#include <utility>
 
 namespace fa {
 namespace {
@@ -200,23 +202,47 @@ __device__ __forceinline__ void stage_rows(uint8_t* dst, const void* src, int nv
     }
 }
 
-// 16 per-row values of this lane (rows kidx(g, t), t = 0..15) from an LDS float vector: the
-// rows come in runs of four.
+// (LSE * log2 e, delta) of this lane's 16 rows (rows kidx(g, t), t = 0..15) from an LDS array
+// of float2 per row: the rows come in runs of four.
 template <typename T>
-__device__ __forceinline__ void rows16(const float* v, int g, float (&out)[16]) {
+__device__ __forceinline__ void rows16(const uint8_t* ld, int g, float (&l2)[16], float (&dl)[16]) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        const f32x4_t x = *(const f32x4_t*)(v + Blk<T>::kidx(g, 4 * j));
-#pragma unroll
-        for (int i = 0; i < 4; ++i) out[4 * j + i] = x[i];
+        const uint8_t* p = ld + Blk<T>::kidx(g, 4 * j) * 8;
+        const f32x4_t x = *(const f32x4_t*)p, y = *(const f32x4_t*)(p + 16);
+        l2[4 * j] = x[0]; dl[4 * j] = x[1]; l2[4 * j + 1] = x[2]; dl[4 * j + 1] = x[3];
+        l2[4 * j + 2] = y[0]; dl[4 * j + 2] = y[1]; l2[4 * j + 3] = y[2]; dl[4 * j + 3] = y[3];
     }
 }
 
-constexpr int kBwdKeys = 128;   // keys per bwd_dkdv workgroup (32 per wave)
+constexpr int kBwdKeys = 128;     // keys per bwd_dkdv workgroup (32 per wave)
 constexpr int kBwdQueries = 128;  // queries per bwd_dq workgroup (32 per wave)
-constexpr int kBwdTile = 64;    // rows per staged tile (Q/dO in bwd_dkdv, K/V in bwd_dq)
+constexpr int kBwdTile = 64;      // rows per staged tile (Q/dO in bwd_dkdv, K/V in bwd_dq)
+constexpr uint32_t kOob = 0x7fff0000u;  // transfer offset past every buffer: writes zeros
 
-// ------------------------------------------------------------------ delta = rowsum(dO * O)
+// LDS geometry of a 64-row tile of DPAD columns: rows of SL 16-byte slots (the data, then one
+// pad slot that keeps the row reads of different rows on different banks), so one tile is SL
+// KiB and a transfer instruction (64 slots) fills exactly one KiB of it.
+template <typename T, int DPAD> struct TileGeom {
+    static constexpr int ES = Blk<T>::ES;
+    static constexpr int CPR = DPAD * ES / 16;  // data slots per row
+    static constexpr int SL = CPR + 1;
+    static constexpr int RB = SL * 16;           // bytes per LDS row
+    static constexpr int BYTES = kBwdTile * RB;  // = SL KiB
+};
+
+// Per-lane offset of transfer instruction `k` (slots 64 k .. 64 k + 63) of a tile whose rows
+// are `row_bytes` apart in memory: row q / SL, slot q % SL; pad slots and columns >= D get the
+// out-of-range offset.
+template <typename T, int DPAD>
+__device__ __forceinline__ uint32_t tile_slot_offset(int k, int lane, int D) {
+    using TG = TileGeom<T, DPAD>;
+    const int q = 64 * k + lane, r = q / TG::SL, c = q % TG::SL;
+    return (c < TG::CPR && c * 16 < D * TG::ES) ? (uint32_t)(r * D * TG::ES + c * 16) : kOob;
+}
+
+// ------------------------------------------------------------------ (LSE log2 e, delta)
+// ld[row] = (LSE * log2 e, sum_d dO * O) for every query row.
 template <typename T>
 __global__ __launch_bounds__(256) void bwd_delta(BackwardArgs a, int64_t rows) {
     using B = Blk<T>;
@@ -249,18 +275,27 @@ __global__ __launch_bounds__(256) void bwd_delta(BackwardArgs a, int64_t rows) {
     }
 #pragma unroll
     for (int m = 8; m >= 1; m >>= 1) acc += __shfl_xor(acc, m, 16);
-    if (row < rows && sub == 0) a.delta[row] = acc;
+    if (row < rows && sub == 0) a.ld[row] = make_float2(a.lse[row] * kLog2e, acc);
 }
 
 // ------------------------------------------------------------------ dK, dV
-template <typename T, int DPAD>
-__global__ __launch_bounds__(256) void bwd_dkdv(BackwardArgs a) {
+// One workgroup: 128 keys of one (batch, kv head), 32 per wave, K and V of them in registers.
+// Tiles of 64 query rows (Q, dO and their (LSE, delta)) of every query head of the group are
+// swept; with DMA they go from memory straight into a double-buffered LDS stage (the next
+// tile's transfer runs under the current tile's products). Padded query rows read as zeros:
+// their dO is zero, so they add nothing to dV or dK.
+template <typename T, int DPAD, bool DMA>
+__global__ __launch_bounds__(256, 1) void bwd_dkdv(BackwardArgs a) {
     using B = Blk<T>;
     using F = typename B::Frag;
-    constexpr int ES = B::ES, MB = DPAD / 32, QT = kBwdTile;
-    constexpr int RB = DPAD * ES + 16;  // padded LDS row (bytes)
-    constexpr int T_Q = 0, T_DO = QT * RB, T_L = 2 * QT * RB, T_DL = T_L + QT * 4;
-    __shared__ __attribute__((aligned(16))) uint8_t smem[2 * QT * RB + 2 * QT * 4];
+    using TG = TileGeom<T, DPAD>;
+    constexpr int ES = B::ES, MB = DPAD / 32, QT = kBwdTile, RB = TG::RB;
+    constexpr int T_DO = TG::BYTES, T_LD = 2 * TG::BYTES;  // within a stage
+    constexpr int NINS = 2 * TG::SL + 1;                    // transfers per stage: Q, dO, ld
+    constexpr int STAGE = NINS * 1024;
+    constexpr int KI = (NINS + 3) / 4;                      // per wave
+    constexpr int DUMMY = 2 * STAGE;
+    __shared__ __attribute__((aligned(16))) uint8_t smem[(DMA ? 2 : 1) * STAGE + (DMA ? 1024 : 0)];
 
     const int tid = threadIdx.x, lane = tid & 63, g = lane >> 5, c = lane & 31;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -272,6 +307,51 @@ __global__ __launch_bounds__(256) void bwd_dkdv(BackwardArgs a) {
     const int b = bkv / a.kv_heads, kvh = bkv - b * a.kv_heads;
     const int k0 = kb * kBwdKeys + wave * 32;
     const int64_t krow0 = (int64_t)bkv * S;
+    const int qstart = a.causal ? kb * kBwdKeys : 0;  // a multiple of QT
+    const int nqt = (S - qstart + QT - 1) / QT, ntiles = G * nqt;
+    const int64_t qhead0 = ((int64_t)b * a.q_heads + (int64_t)kvh * G) * S;  // first row of the group
+    auto tile_row = [&](int j) {  // first query row (global) of tile j and its offset qt
+        const int hh = j / nqt, qt = qstart + (j - hh * nqt) * QT;
+        return std::pair<int64_t, int>(qhead0 + (int64_t)hh * S + qt, qt);
+    };
+
+    uint32_t doff[DMA ? KI : 1];
+    const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_void_t*)smem;
+    if constexpr (DMA) {
+#pragma unroll
+        for (int i = 0; i < KI; ++i) {
+            const int k = wave + 4 * i;
+            doff[i] = k < TG::SL ? tile_slot_offset<T, DPAD>(k, lane, D)
+                    : k < 2 * TG::SL ? tile_slot_offset<T, DPAD>(k - TG::SL, lane, D)
+                    : (k == 2 * TG::SL && lane < 32) ? (uint32_t)lane * 16u : kOob;
+        }
+    }
+    auto dma_tile = [&](int j, int st) {
+        const auto [row, qt] = tile_row(j);
+        const int left = S - qt;
+#pragma unroll
+        for (int i = 0; i < KI; ++i) {
+            const int k = wave + 4 * i;
+            i32x4_t rs;
+            if (k < TG::SL)
+                rs = make_rsrc_words((const uint8_t*)a.q + row * D * ES, left * D * ES);
+            else if (k < 2 * TG::SL)
+                rs = make_rsrc_words((const uint8_t*)a.dout + row * D * ES, left * D * ES);
+            else
+                rs = make_rsrc_words(a.ld + row, left * 8);
+            const int dst = k < NINS ? st + k * 1024 : DUMMY;
+            buffer_to_lds16(rs, __builtin_amdgcn_readfirstlane(lds0 + dst), doff[i]);
+        }
+    };
+    auto stage_tile = [&](int j) {  // synchronous staging (no DMA)
+        const auto [row, qt] = tile_row(j);
+        const int nv = min(QT, S - qt);
+        stage_rows<T, DPAD, QT, RB>(smem, (const uint8_t*)a.q + row * D * ES, nv, D, a.vec);
+        stage_rows<T, DPAD, QT, RB>(smem + T_DO, (const uint8_t*)a.dout + row * D * ES, nv, D,
+                                    a.vec);
+        if (tid < QT)
+            ((float2*)(smem + T_LD))[tid] = tid < nv ? a.ld[row + tid] : make_float2(0.0f, 0.0f);
+    };
 
     F kf[MB], vf[MB];
 #pragma unroll
@@ -286,56 +366,57 @@ __global__ __launch_bounds__(256) void bwd_dkdv(BackwardArgs a) {
         dv[m] = (f32x16_t)0.0f;
     }
     const float c2 = a.scale * kLog2e;
-    const int qstart = a.causal ? kb * kBwdKeys : 0;  // a multiple of QT
 
-    for (int hh = 0; hh < G; ++hh) {
-        const int h = kvh * G + hh;
-        const int64_t qrow0 = ((int64_t)b * a.q_heads + h) * S;
-        for (int qt = qstart; qt < S; qt += QT) {
-            const int nv = min(QT, S - qt);
+    if constexpr (DMA) {
+        dma_tile(0, 0);
+        wait_dma();
+        __syncthreads();
+    }
+    for (int j = 0; j < ntiles; ++j) {
+        int st = 0;
+        if constexpr (DMA) {
+            st = (j & 1) * STAGE;
+            if (j + 1 < ntiles) dma_tile(j + 1, STAGE - st);
+        } else {
             __syncthreads();
-            stage_rows<T, DPAD, QT, RB>(smem + T_Q, (const uint8_t*)a.q + (qrow0 + qt) * D * ES,
-                                        nv, D, a.vec);
-            stage_rows<T, DPAD, QT, RB>(smem + T_DO,
-                                        (const uint8_t*)a.dout + (qrow0 + qt) * D * ES, nv, D,
-                                        a.vec);
-            if (tid < QT) {
-                const bool ok = tid < nv;
-                ((float*)(smem + T_L))[tid] = ok ? a.lse[qrow0 + qt + tid] * kLog2e : INFINITY;
-                ((float*)(smem + T_DL))[tid] = ok ? a.delta[qrow0 + qt + tid] : 0.0f;
-            }
+            stage_tile(j);
             __syncthreads();
+        }
+        const int qt = tile_row(j).second;
 #pragma unroll
-            for (int sub = 0; sub < QT / 32; ++sub) {
-                const int q0 = qt + sub * 32;
-                if (q0 >= S) break;
-                if (a.causal && q0 + 31 < k0) continue;  // no query of the block sees a key
-                f32x16_t s = (f32x16_t)0.0f, dp = (f32x16_t)0.0f;
-                const uint8_t* qa = smem + T_Q + (sub * 32 + B::arow(c)) * RB;
-                const uint8_t* oa = smem + T_DO + (sub * 32 + B::arow(c)) * RB;
+        for (int sub = 0; sub < QT / 32; ++sub) {
+            const int q0 = qt + sub * 32;
+            if (q0 >= S) break;
+            if (a.causal && q0 + 31 < k0) continue;  // no query of the block sees a key
+            f32x16_t s = (f32x16_t)0.0f, dp = (f32x16_t)0.0f;
+            const uint8_t* qa = smem + st + (sub * 32 + B::arow(c)) * RB;
+            const uint8_t* oa = qa + T_DO;
 #pragma unroll
-                for (int m = 0; m < MB; ++m) {
-                    s = B::mma(B::row_lds(qa + m * 32 * ES, g), kf[m], s);
-                    dp = B::mma(B::row_lds(oa + m * 32 * ES, g), vf[m], dp);
-                }
-                float l2[16], dl[16], pv[16], dsv[16];
-                rows16<T>((const float*)(smem + T_L) + sub * 32, g, l2);
-                rows16<T>((const float*)(smem + T_DL) + sub * 32, g, dl);
-                const bool mask = a.causal && k0 + 31 > q0;
-#pragma unroll
-                for (int t = 0; t < 16; ++t) {
-                    float p = fast_exp2(fmaf(s[t], c2, -l2[t]));
-                    if (mask && k0 + c > q0 + B::kidx(g, t)) p = 0.0f;
-                    pv[t] = p;
-                    dsv[t] = p * (dp[t] - dl[t]);
-                }
-                const F pf = B::pack(pv), df = B::pack(dsv);
-#pragma unroll
-                for (int m = 0; m < MB; ++m) {
-                    dv[m] = B::mma(pf, B::template col_lds<RB>(smem + T_DO + sub * 32 * RB, 32 * m, lane), dv[m]);
-                    dk[m] = B::mma(df, B::template col_lds<RB>(smem + T_Q + sub * 32 * RB, 32 * m, lane), dk[m]);
-                }
+            for (int m = 0; m < MB; ++m) {
+                s = B::mma(B::row_lds(qa + m * 32 * ES, g), kf[m], s);
+                dp = B::mma(B::row_lds(oa + m * 32 * ES, g), vf[m], dp);
             }
+            float l2[16], dl[16], pv[16], dsv[16];
+            rows16<T>(smem + st + T_LD + sub * 32 * 8, g, l2, dl);
+            const bool mask = a.causal && k0 + 31 > q0;
+#pragma unroll
+            for (int t = 0; t < 16; ++t) {
+                float p = fast_exp2(fmaf(s[t], c2, -l2[t]));
+                if (mask && k0 + c > q0 + B::kidx(g, t)) p = 0.0f;
+                pv[t] = p;
+                dsv[t] = p * (dp[t] - dl[t]);
+            }
+            const F pf = B::pack(pv), df = B::pack(dsv);
+            const uint8_t* qt_tile = smem + st + sub * 32 * RB;
+#pragma unroll
+            for (int m = 0; m < MB; ++m) {
+                dv[m] = B::mma(pf, B::template col_lds<RB>(qt_tile + T_DO, 32 * m, lane), dv[m]);
+                dk[m] = B::mma(df, B::template col_lds<RB>(qt_tile, 32 * m, lane), dk[m]);
+            }
+        }
+        if constexpr (DMA) {
+            wait_dma();
+            __syncthreads();
         }
     }
     // register r: key k0 + 8 (r / 4) + 4 g + r % 4, dim 32 m + c
@@ -354,14 +435,20 @@ __global__ __launch_bounds__(256) void bwd_dkdv(BackwardArgs a) {
 }
 
 // ------------------------------------------------------------------ dQ
-template <typename T, int DPAD>
-__global__ __launch_bounds__(256) void bwd_dq(BackwardArgs a) {
+// One workgroup: 128 queries of one (batch, query head), 32 per wave, Q and dO of them in
+// registers; tiles of 64 keys (K, V) of the KV head are swept, DMA double-buffered as above.
+template <typename T, int DPAD, bool DMA>
+__global__ __launch_bounds__(256, Blk<T>::ES == 2 ? 2 : 1) void bwd_dq(BackwardArgs a) {
     using B = Blk<T>;
     using F = typename B::Frag;
-    constexpr int ES = B::ES, MB = DPAD / 32, KT = kBwdTile;
-    constexpr int RB = DPAD * ES + 16;
-    constexpr int T_K = 0, T_V = KT * RB;
-    __shared__ __attribute__((aligned(16))) uint8_t smem[2 * KT * RB];
+    using TG = TileGeom<T, DPAD>;
+    constexpr int ES = B::ES, MB = DPAD / 32, KT = kBwdTile, RB = TG::RB;
+    constexpr int T_V = TG::BYTES;
+    constexpr int NINS = 2 * TG::SL;  // transfers per stage: K, V
+    constexpr int STAGE = NINS * 1024;
+    constexpr int KI = (NINS + 3) / 4;
+    constexpr int DUMMY = 2 * STAGE;
+    __shared__ __attribute__((aligned(16))) uint8_t smem[(DMA ? 2 : 1) * STAGE + (DMA ? 1024 : 0)];
 
     const int tid = threadIdx.x, lane = tid & 63, g = lane >> 5, c = lane & 31;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -374,6 +461,29 @@ __global__ __launch_bounds__(256) void bwd_dq(BackwardArgs a) {
     const int q0 = qb * kBwdQueries + wave * 32;
     const int64_t qrow0 = (int64_t)bh * S, krow0 = ((int64_t)b * a.kv_heads + kvh) * S;
     const bool qok = q0 + c < S;
+    const int kend = a.causal ? min(S, (qb + 1) * kBwdQueries) : S;
+    const int ntiles = (kend + KT - 1) / KT;
+
+    uint32_t doff[DMA ? KI : 1];
+    const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_void_t*)smem;
+    if constexpr (DMA) {
+#pragma unroll
+        for (int i = 0; i < KI; ++i) {
+            const int k = wave + 4 * i;
+            doff[i] = tile_slot_offset<T, DPAD>(k < TG::SL ? k : k - TG::SL, lane, D);
+        }
+    }
+    auto dma_tile = [&](int j, int st) {
+        const int kt = j * KT, left = S - kt;
+#pragma unroll
+        for (int i = 0; i < KI; ++i) {
+            const int k = wave + 4 * i;
+            const i32x4_t rs = make_rsrc_words(
+                (const uint8_t*)(k < TG::SL ? a.k : a.v) + (krow0 + kt) * D * ES, left * D * ES);
+            const int dst = k < NINS ? st + k * 1024 : DUMMY;
+            buffer_to_lds16(rs, __builtin_amdgcn_readfirstlane(lds0 + dst), doff[i]);
+        }
+    };
 
     F qf[MB], of[MB];
 #pragma unroll
@@ -381,30 +491,41 @@ __global__ __launch_bounds__(256) void bwd_dq(BackwardArgs a) {
         qf[m] = B::row_global(a.q, qrow0 + q0 + c, qok, 32 * m, D, g, a.vec);
         of[m] = B::row_global(a.dout, qrow0 + q0 + c, qok, 32 * m, D, g, a.vec);
     }
-    const float l2 = qok ? a.lse[qrow0 + q0 + c] * kLog2e : 0.0f;
-    const float dl = qok ? a.delta[qrow0 + q0 + c] : 0.0f;
+    const float2 ldq = qok ? a.ld[qrow0 + q0 + c] : make_float2(0.0f, 0.0f);
+    const float l2 = ldq.x, dl = ldq.y;
     f32x16_t dq[MB];
 #pragma unroll
     for (int m = 0; m < MB; ++m) dq[m] = (f32x16_t)0.0f;
     const float c2 = a.scale * kLog2e;
-    const int kend = a.causal ? min(S, (qb + 1) * kBwdQueries) : S;
 
-    for (int kt = 0; kt < kend; kt += KT) {
-        const int nv = min(KT, S - kt);
+    if constexpr (DMA) {
+        dma_tile(0, 0);
+        wait_dma();
         __syncthreads();
-        stage_rows<T, DPAD, KT, RB>(smem + T_K, (const uint8_t*)a.k + (krow0 + kt) * D * ES, nv,
-                                    D, a.vec);
-        stage_rows<T, DPAD, KT, RB>(smem + T_V, (const uint8_t*)a.v + (krow0 + kt) * D * ES, nv,
-                                    D, a.vec);
-        __syncthreads();
+    }
+    for (int j = 0; j < ntiles; ++j) {
+        const int kt = j * KT;
+        int st = 0;
+        if constexpr (DMA) {
+            st = (j & 1) * STAGE;
+            if (j + 1 < ntiles) dma_tile(j + 1, STAGE - st);
+        } else {
+            const int nv = min(KT, S - kt);
+            __syncthreads();
+            stage_rows<T, DPAD, KT, RB>(smem, (const uint8_t*)a.k + (krow0 + kt) * D * ES, nv, D,
+                                        a.vec);
+            stage_rows<T, DPAD, KT, RB>(smem + T_V, (const uint8_t*)a.v + (krow0 + kt) * D * ES,
+                                        nv, D, a.vec);
+            __syncthreads();
+        }
 #pragma unroll
         for (int sub = 0; sub < KT / 32; ++sub) {
             const int kk0 = kt + sub * 32;
             if (kk0 >= S) break;
             if (a.causal && kk0 > q0 + 31) continue;  // every key of the block is masked
             f32x16_t s = (f32x16_t)0.0f, dp = (f32x16_t)0.0f;
-            const uint8_t* ka = smem + T_K + (sub * 32 + B::arow(c)) * RB;
-            const uint8_t* va = smem + T_V + (sub * 32 + B::arow(c)) * RB;
+            const uint8_t* ka = smem + st + (sub * 32 + B::arow(c)) * RB;
+            const uint8_t* va = ka + T_V;
 #pragma unroll
             for (int m = 0; m < MB; ++m) {
                 s = B::mma(B::row_lds(ka + m * 32 * ES, g), qf[m], s);
@@ -423,7 +544,11 @@ __global__ __launch_bounds__(256) void bwd_dq(BackwardArgs a) {
             const F df = B::pack(dsv);
 #pragma unroll
             for (int m = 0; m < MB; ++m)
-                dq[m] = B::mma(df, B::template col_lds<RB>(smem + T_K + sub * 32 * RB, 32 * m, lane), dq[m]);
+                dq[m] = B::mma(df, B::template col_lds<RB>(smem + st + sub * 32 * RB, 32 * m, lane), dq[m]);
+        }
+        if constexpr (DMA) {
+            wait_dma();
+            __syncthreads();
         }
     }
 #pragma unroll
@@ -437,12 +562,20 @@ __global__ __launch_bounds__(256) void bwd_dq(BackwardArgs a) {
     }
 }
 
-template <typename T, int DPAD>
+template <typename T, int DPAD, bool DMA>
 void launch_typed(const BackwardArgs& a, hipStream_t s) {
     const int S = a.seq;
     const int nkb = (S + kBwdKeys - 1) / kBwdKeys, nqb = (S + kBwdQueries - 1) / kBwdQueries;
-    hipLaunchKernelGGL((bwd_dkdv<T, DPAD>), dim3(nkb * a.batch * a.kv_heads), dim3(256), 0, s, a);
-    hipLaunchKernelGGL((bwd_dq<T, DPAD>), dim3(nqb * a.batch * a.q_heads), dim3(256), 0, s, a);
+    hipLaunchKernelGGL((bwd_dkdv<T, DPAD, DMA>), dim3(nkb * a.batch * a.kv_heads), dim3(256), 0,
+                       s, a);
+    hipLaunchKernelGGL((bwd_dq<T, DPAD, DMA>), dim3(nqb * a.batch * a.q_heads), dim3(256), 0, s,
+                       a);
+}
+
+template <typename T, int DPAD>
+void launch_dma(const BackwardArgs& a, hipStream_t s) {
+    if (a.dma) launch_typed<T, DPAD, true>(a, s);
+    else launch_typed<T, DPAD, false>(a, s);
 }
 
 template <typename T>
@@ -450,9 +583,9 @@ void launch_dims(const BackwardArgs& a, hipStream_t s) {
     const int64_t rows = (int64_t)a.batch * a.q_heads * a.seq;
     hipLaunchKernelGGL((bwd_delta<T>), dim3((unsigned)((rows + 15) / 16)), dim3(256), 0, s, a,
                        rows);
-    if (a.head_dim <= 32) launch_typed<T, 32>(a, s);
-    else if (a.head_dim <= 64) launch_typed<T, 64>(a, s);
-    else launch_typed<T, 128>(a, s);
+    if (a.head_dim <= 32) launch_dma<T, 32>(a, s);
+    else if (a.head_dim <= 64) launch_dma<T, 64>(a, s);
+    else launch_dma<T, 128>(a, s);
 }
 
 }  // namespace

@@ -129,4 +129,30 @@ __device__ __forceinline__ int xcd_remap(int bid, int nb) {
     return xcd < r ? xcd * (q + 1) + slot : r * (q + 1) + (xcd - r) * q + slot;
 }
 
+// ---------------------------------------------------------------- buffer -> LDS transfers
+// 16 bytes per lane from a buffer straight into LDS: lane i writes LDS byte address
+// lds + 16 i (buffer_load_dwordx4 ... lds; the compiler loads M0 = lds). Out-of-range offsets write zeros and
+// fetch nothing. Issued from inline assembly so the compiler's wait-count tracking does not
+// treat the transfer as aliasing every later LDS read (it would otherwise wait for the next
+// tile's transfer before reading the current one); the caller waits with wait_dma().
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void_t;
+__device__ __forceinline__ void buffer_to_lds16(i32x4_t rsrc, uint32_t lds, uint32_t voff) {
+    // No memory clobber: the transfer writes a stage no LDS access near it touches, and the
+    // barriers / wait_dma() that order it against its readers are themselves ordered.
+    asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds" : : "v"(voff), "s"(rsrc), "{m0}"(lds));
+}
+__device__ __forceinline__ void wait_dma() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+// Buffer resource words: base, stride 0, num_records bytes, the same flags as
+// __builtin_amdgcn_make_buffer_rsrc is given elsewhere (0x00020000).
+__device__ __forceinline__ i32x4_t make_rsrc_words(const void* base, int nrec) {
+    const uint64_t b = (uint64_t)base;
+    i32x4_t r;
+    r[0] = __builtin_amdgcn_readfirstlane((int)(uint32_t)b);
+    r[1] = __builtin_amdgcn_readfirstlane((int)((uint32_t)(b >> 32) & 0xffffu));
+    r[2] = __builtin_amdgcn_readfirstlane(nrec);
+    r[3] = 0x00020000;
+    return r;
+}
+
 }  // namespace fa

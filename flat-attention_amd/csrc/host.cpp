@@ -154,7 +154,7 @@ struct fa_ctx {
     // growable scratch for the transposed V copy of the prefill
     void* ws_vt = nullptr;
     size_t ws_vt_bytes = 0;
-    // growable scratch for the backward's per-row delta = rowsum(dO * O)
+    // growable scratch for the backward's per-row (LSE log2 e, rowsum(dO * O))
     void* ws_delta = nullptr;
     size_t ws_delta_bytes = 0;
     int transpose_v_policy = -1;
@@ -2267,13 +2267,13 @@ int fa_backward_grouped(fa_ctx* ctx, const void* q, const void* k, const void* v
     begin_call(ctx);
     if (int rc = set_device(ctx)) return rc;
     void* delta = nullptr;
-    if (int rc = grow(ctx, &ctx->ws_delta, &ctx->ws_delta_bytes, lay.lse_elements * 4, &delta))
+    if (int rc = grow(ctx, &ctx->ws_delta, &ctx->ws_delta_bytes, lay.lse_elements * 8, &delta))
         return rc;
 
     fa::BackwardArgs a{};
     a.q = q; a.k = k; a.v = v; a.dout = d_out; a.o = out; a.lse = lse;
     a.dq = dq; a.dk = dk; a.dv = dv;
-    a.delta = (float*)delta;
+    a.ld = (float2*)delta;
     a.batch = (int)sh->batch;
     a.q_heads = (int)sh->q_heads;
     a.kv_heads = (int)sh->kv_heads;
@@ -2286,6 +2286,7 @@ int fa_backward_grouped(fa_ctx* ctx, const void* q, const void* k, const void* v
     bool vec = sh->head_dim % chunk == 0;
     for (const void* p : ptrs) vec = vec && ((uintptr_t)p % 16 == 0);
     a.vec = vec;
+    a.dma = vec && sh->seq_len * sh->head_dim * (uint64_t)elem_bytes(dtype) < (1ull << 31);
     begin_span(ctx);
     fa::launch_backward((Dtype)dtype, a, ctx->stream);
     end_span(ctx, FA_KERNEL_BACKWARD_RECOMPUTE);

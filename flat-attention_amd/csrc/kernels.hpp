@@ -90,8 +90,9 @@ void launch_decode(Dtype dt, const DecodeArgs& a, hipStream_t s, unsigned grid[3
 
 // Recompute backward of grouped attention. Q, dO, O, dQ: [batch, q_heads, seq, head_dim];
 // K, V, dK, dV: [batch, kv_heads, seq, head_dim]; LSE and delta: [batch, q_heads, seq] f32.
-// `delta` is scratch of batch*q_heads*seq floats (rowsum of dO * O, written by the first
-// launch). vec: head_dim is a multiple of the 16-byte chunk and every tensor 16-byte aligned.
+// `ld` is scratch of batch*q_heads*seq float2 (LSE * log2 e, rowsum of dO * O), written by the
+// first launch. vec: head_dim is a multiple of the 16-byte chunk and every tensor 16-byte
+// aligned; dma: vec, and one (batch, head) slice spans less than 2 GiB (32-bit buffer offsets).
 struct BackwardArgs {
     const void* q;
     const void* k;
@@ -102,8 +103,8 @@ struct BackwardArgs {
     void* dq;
     void* dk;
     void* dv;
-    float* delta;
-    int batch, q_heads, kv_heads, group, seq, head_dim, causal, vec;
+    float2* ld;
+    int batch, q_heads, kv_heads, group, seq, head_dim, causal, vec, dma;
     float scale;
 };
 // Three launches: delta, dK/dV, dQ.
