@@ -169,39 +169,6 @@ template <typename S> struct Blk16 {
 template <> struct Blk<bf16_t> : Blk16<bf16_t> {};
 template <> struct Blk<f16_t> : Blk16<f16_t> {};
 
-// Rows [0, R) of a row-major [*, D] tensor starting at `src` (nvalid of them real, the rest
-// zero) into an LDS tile of DPAD columns (zero beyond D) and RB bytes per row. `vec`: D is a
-// multiple of the 16-byte chunk and the tensor is 16-byte aligned.
-template <typename T, int DPAD, int R, int RB>
-__device__ __forceinline__ void stage_rows(uint8_t* dst, const void* src, int nvalid, int D,
-                                           bool vec) {
-    constexpr int ES = Blk<T>::ES, W = 16 / ES, CPR = DPAD / W;
-    const int tid = threadIdx.x;
-    if (vec) {
-        for (int i = tid; i < R * CPR; i += blockDim.x) {
-            const int r = i / CPR, col = (i % CPR) * W;
-            u32x4_t v = {0, 0, 0, 0};
-            if (r < nvalid && col < D)
-                v = *(const u32x4_t*)((const uint8_t*)src + ((int64_t)r * D + col) * ES);
-            *(u32x4_t*)(dst + r * RB + col * ES) = v;
-        }
-    } else {
-        for (int i = tid; i < R * DPAD; i += blockDim.x) {
-            const int r = i / DPAD, col = i % DPAD;
-            if constexpr (ES == 4) {
-                const float v = (r < nvalid && col < D) ? ((const float*)src)[(int64_t)r * D + col]
-                                                        : 0.0f;
-                *(float*)(dst + r * RB + col * 4) = v;
-            } else {
-                const uint16_t v = (r < nvalid && col < D)
-                                       ? ((const uint16_t*)src)[(int64_t)r * D + col]
-                                       : (uint16_t)0;
-                *(uint16_t*)(dst + r * RB + col * 2) = v;
-            }
-        }
-    }
-}
-
 // (LSE * log2 e, delta) of this lane's 16 rows (rows kidx(g, t), t = 0..15) from an LDS array
 // of float2 per row: the rows come in runs of four.
 template <typename T>
@@ -220,25 +187,119 @@ constexpr int kBwdQueries = 128;  // queries per bwd_dq workgroup (32 per wave)
 constexpr int kBwdTile = 64;      // rows per staged tile (Q/dO in bwd_dkdv, K/V in bwd_dq)
 constexpr uint32_t kOob = 0x7fff0000u;  // transfer offset past every buffer: writes zeros
 
-// LDS geometry of a 64-row tile of DPAD columns: rows of SL 16-byte slots (the data, then one
-// pad slot that keeps the row reads of different rows on different banks), so one tile is SL
-// KiB and a transfer instruction (64 slots) fills exactly one KiB of it.
-template <typename T, int DPAD> struct TileGeom {
+#ifndef FA_BWD_SGS
+#define FA_BWD_SGS 1
+#endif
+#if FA_BWD_SGS
+#define FA_BWD_SG(mask, n) __builtin_amdgcn_sched_group_barrier(mask, n, 0)
+#else
+#define FA_BWD_SG(mask, n) ((void)0)
+#endif
+
+// LDS geometry of a tile of ROWS rows and DPAD columns, in rows of SL 16-byte slots; a tile is
+// a whole number of KiB, so a transfer instruction (64 slots) fills one KiB of it.
+// Every 16-bit tile is read two ways: rows (ds_read_b128: 16 lanes read one 16-byte chunk of
+// 16 different rows) and columns (ds_read_b64_tr_b16: 32 lanes read 4 chunks of 4 consecutive
+// rows). With 64 four-byte banks (16 chunk positions) both are conflict-free when
+//   padded (XOR4 false): rows of CPR + 4 slots (CPR + 4 = 4 mod 8 chunks of stride, or 12 for
+//     CPR = 4) and the low two chunk bits XORed with (row >> 2) & 3;
+//   unpadded (XOR4 true, CPR = 16): the chunk index XORed with 4 (row & 3) + ((row >> 2) & 3).
+// f32 tiles keep one pad slot per row and no swizzle.
+template <typename T, int DPAD, int ROWS, bool XOR4 = false> struct TileGeom {
     static constexpr int ES = Blk<T>::ES;
     static constexpr int CPR = DPAD * ES / 16;  // data slots per row
-    static constexpr int SL = CPR + 1;
+    static constexpr bool SWZ = ES == 2;
+    static_assert(!XOR4 || (SWZ && CPR == 16), "the 4-bit swizzle needs 16 chunks per row");
+    static constexpr int SL = !SWZ ? CPR + 1 : XOR4 ? CPR : (CPR % 8 == 0 ? CPR + 4 : 12);
     static constexpr int RB = SL * 16;           // bytes per LDS row
-    static constexpr int BYTES = kBwdTile * RB;  // = SL KiB
+    static constexpr int BYTES = ROWS * RB;
+    static constexpr int INS = BYTES / 1024;     // transfer instructions per tile
+    static_assert(BYTES % 1024 == 0, "tile must be whole KiB");
+    // physical slot of logical chunk q in row r and back (the swizzles are involutions)
+    __device__ __forceinline__ static int swz(int r, int q) {
+        if constexpr (!SWZ) return q;
+        else if constexpr (XOR4) return q ^ (((r & 3) << 2) | ((r >> 2) & 3));
+        else return (q & ~3) | ((q & 3) ^ ((r >> 2) & 3));
+    }
 };
 
 // Per-lane offset of transfer instruction `k` (slots 64 k .. 64 k + 63) of a tile whose rows
-// are `row_bytes` apart in memory: row q / SL, slot q % SL; pad slots and columns >= D get the
-// out-of-range offset.
-template <typename T, int DPAD>
+// are D elements apart in memory: LDS row q / SL, slot q % SL holds logical chunk swz(row,
+// slot); pad slots and columns >= D get the out-of-range offset.
+template <typename TG>
 __device__ __forceinline__ uint32_t tile_slot_offset(int k, int lane, int D) {
-    using TG = TileGeom<T, DPAD>;
-    const int q = 64 * k + lane, r = q / TG::SL, c = q % TG::SL;
-    return (c < TG::CPR && c * 16 < D * TG::ES) ? (uint32_t)(r * D * TG::ES + c * 16) : kOob;
+    const int q = 64 * k + lane, r = q / TG::SL, pc = q % TG::SL;
+    if (pc >= TG::CPR) return kOob;
+    const int c = TG::swz(r, pc);
+    return c * 16 < D * TG::ES ? (uint32_t)(r * D * TG::ES + c * 16) : kOob;
+}
+
+// Per-lane LDS offsets of the two operand reads of 16-bit tiles (relative to row 0 of a
+// 32-row sub-block; the swizzle only depends on row & 15, so sub-blocks and the 16-row halves
+// are immediate offsets).
+//   rread(m, s): row arow(c), dims 32 m + 16 s + 8 g .. +7 (A operand, contraction over dims);
+//   tread(m, s): dim 32 m + c of rows 16 s + 8 g .. +7 (B operand, contraction over rows).
+template <typename TG, typename B, int MB> struct Ops16 {
+    static constexpr int NM = TG::SL == TG::CPR ? MB : 1;  // distinct offsets over m
+    uint32_t ro[NM][2], to[NM][2];
+    __device__ __forceinline__ void init(int lane) {
+        const int g = lane >> 5, c = lane & 31, rr = B::arow(c);
+        const int tr = 8 * g + ((lane & 15) >> 2), tq = 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);
+#pragma unroll
+        for (int m = 0; m < NM; ++m)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                ro[m][h] = rr * TG::RB + TG::swz(rr, 4 * m + 2 * h + g) * 16;  // h: dims +16
+                to[m][h] = (tr + 4 * h) * TG::RB + TG::swz(tr + 4 * h, 4 * m + tq) * 16 +
+                           8 * (lane & 1);                                     // h: rows +4
+            }
+    }
+    __device__ __forceinline__ u32x4_t rread(const uint8_t* tile, int m, int s) const {
+        return *(const u32x4_t*)(tile + ro[NM == 1 ? 0 : m][s] + (NM == 1 ? 64 * m : 0));
+    }
+    __device__ __forceinline__ u32x4_t tread(const uint8_t* tile, int m, int s) const {
+        typedef short v4i16_t __attribute__((ext_vector_type(4)));
+        typedef __attribute__((address_space(3))) v4i16_t lds_v4i16_t;
+        const uint8_t* p = tile + 16 * s * TG::RB + (NM == 1 ? 64 * m : 0);
+        const int mi = NM == 1 ? 0 : m;
+        const v4i16_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)(p + to[mi][0]));
+        const v4i16_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)(p + to[mi][1]));
+        const u32x2_t l2 = __builtin_bit_cast(u32x2_t, lo);
+        const u32x2_t h2 = __builtin_bit_cast(u32x2_t, hi);
+        return u32x4_t{l2[0], l2[1], h2[0], h2[1]};
+    }
+};
+
+// Rows [0, ROWS) of a row-major [*, D] tensor starting at `src` (nvalid of them real, the rest
+// zero) into an LDS tile of geometry TG (zero beyond D). `vec`: D is a multiple of the 16-byte
+// chunk and the tensor is 16-byte aligned.
+template <typename TG, int ROWS>
+__device__ __forceinline__ void stage_rows(uint8_t* dst, const void* src, int nvalid, int D,
+                                           bool vec) {
+    constexpr int ES = TG::ES, W = 16 / ES, CPR = TG::CPR, RB = TG::RB;
+    const int tid = threadIdx.x;
+    if (vec) {
+        for (int i = tid; i < ROWS * CPR; i += blockDim.x) {
+            const int r = i / CPR, q = i % CPR, col = q * W;
+            u32x4_t v = {0, 0, 0, 0};
+            if (r < nvalid && col < D)
+                v = *(const u32x4_t*)((const uint8_t*)src + ((int64_t)r * D + col) * ES);
+            *(u32x4_t*)(dst + r * RB + TG::swz(r, q) * 16) = v;
+        }
+    } else {
+        for (int i = tid; i < ROWS * CPR * W; i += blockDim.x) {
+            const int r = i / (CPR * W), col = i % (CPR * W);
+            uint8_t* d = dst + r * RB + TG::swz(r, col / W) * 16 + (col % W) * ES;
+            if constexpr (ES == 4) {
+                *(float*)d = (r < nvalid && col < D) ? ((const float*)src)[(int64_t)r * D + col]
+                                                     : 0.0f;
+            } else {
+                *(uint16_t*)d = (r < nvalid && col < D)
+                                    ? ((const uint16_t*)src)[(int64_t)r * D + col]
+                                    : (uint16_t)0;
+            }
+        }
+    }
 }
 
 // ------------------------------------------------------------------ (LSE log2 e, delta)
@@ -280,22 +341,36 @@ __global__ __launch_bounds__(256) void bwd_delta(BackwardArgs a, int64_t rows) {
 
 // ------------------------------------------------------------------ dK, dV
 // One workgroup: 128 keys of one (batch, kv head), 32 per wave, K and V of them in registers.
-// Tiles of 64 query rows (Q, dO and their (LSE, delta)) of every query head of the group are
-// swept; with DMA they go from memory straight into a double-buffered LDS stage (the next
+// Tiles of query rows (Q, dO and their (LSE log2 e, delta)) of every query head of the group
+// are swept; with DMA they go from memory straight into a double-buffered LDS stage (the next
 // tile's transfer runs under the current tile's products). Padded query rows read as zeros:
 // their dO is zero, so they add nothing to dV or dK.
+//
+// 16-bit storage runs the 32-row sub-blocks of a 128-row tile as a software pipeline: the
+// probabilities of sub-block i (VALU: exp2, dS, packing) are computed while the MFMAs of
+// S and dP of sub-block i+1 run, then the dV/dK MFMAs of sub-block i run while the transposed
+// operand reads of the next products and the (LSE, delta) rows of sub-block i+1 are issued.
+// One wave per SIMD (the K/V fragments and both accumulators take ~330 registers), so the
+// overlap has to come from this single instruction stream; scheduling group barriers keep the
+// compiler from separating the phases again.
 template <typename T, int DPAD, bool DMA>
 __global__ __launch_bounds__(256, 1) void bwd_dkdv(BackwardArgs a) {
     using B = Blk<T>;
     using F = typename B::Frag;
-    using TG = TileGeom<T, DPAD>;
-    constexpr int ES = B::ES, MB = DPAD / 32, QT = kBwdTile, RB = TG::RB;
+    constexpr int ES = B::ES, MB = DPAD / 32;
+    constexpr bool PIPE = ES == 2;
+    // query rows per tile: two stages of Q and dO must fit the 160 KiB of LDS
+    constexpr int QT = PIPE ? (DPAD == 128 ? 96 : 128) : 64, NSUB = QT / 32;
+    using TG = TileGeom<T, DPAD, QT>;
+    constexpr int RB = TG::RB;
     constexpr int T_DO = TG::BYTES, T_LD = 2 * TG::BYTES;  // within a stage
-    constexpr int NINS = 2 * TG::SL + 1;                    // transfers per stage: Q, dO, ld
+    constexpr int NINS = 2 * TG::INS + 1;                   // transfers per stage: Q, dO, ld
     constexpr int STAGE = NINS * 1024;
-    constexpr int KI = (NINS + 3) / 4;                      // per wave
+    constexpr int KI = (TG::INS + 3) / 4;  // per wave and tensor (Q and dO share the offsets)
     constexpr int DUMMY = 2 * STAGE;
-    __shared__ __attribute__((aligned(16))) uint8_t smem[(DMA ? 2 : 1) * STAGE + (DMA ? 1024 : 0)];
+    constexpr bool NEED_DUMMY = DMA && TG::INS % 4 != 0;
+    __shared__ __attribute__((aligned(16)))
+    uint8_t smem[(DMA ? 2 : 1) * STAGE + (NEED_DUMMY ? 1024 : 0)];
 
     const int tid = threadIdx.x, lane = tid & 63, g = lane >> 5, c = lane & 31;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -314,41 +389,38 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv(BackwardArgs a) {
         const int hh = j / nqt, qt = qstart + (j - hh * nqt) * QT;
         return std::pair<int64_t, int>(qhead0 + (int64_t)hh * S + qt, qt);
     };
+    const bool vec = DMA || a.vec;
 
+    // Wave w issues the Q and dO transfers w, w + 4, ... (same per-lane offsets for both) and
+    // wave 0 the (LSE, delta) one.
     uint32_t doff[DMA ? KI : 1];
     const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_void_t*)smem;
     if constexpr (DMA) {
 #pragma unroll
-        for (int i = 0; i < KI; ++i) {
-            const int k = wave + 4 * i;
-            doff[i] = k < TG::SL ? tile_slot_offset<T, DPAD>(k, lane, D)
-                    : k < 2 * TG::SL ? tile_slot_offset<T, DPAD>(k - TG::SL, lane, D)
-                    : (k == 2 * TG::SL && lane < 32) ? (uint32_t)lane * 16u : kOob;
-        }
+        for (int i = 0; i < KI; ++i) doff[i] = tile_slot_offset<TG>(wave + 4 * i, lane, D);
     }
     auto dma_tile = [&](int j, int st) {
         const auto [row, qt] = tile_row(j);
         const int left = S - qt;
+        const i32x4_t rq = make_rsrc_words((const uint8_t*)a.q + row * D * ES, left * D * ES);
+        const i32x4_t ro = make_rsrc_words((const uint8_t*)a.dout + row * D * ES, left * D * ES);
 #pragma unroll
         for (int i = 0; i < KI; ++i) {
             const int k = wave + 4 * i;
-            i32x4_t rs;
-            if (k < TG::SL)
-                rs = make_rsrc_words((const uint8_t*)a.q + row * D * ES, left * D * ES);
-            else if (k < 2 * TG::SL)
-                rs = make_rsrc_words((const uint8_t*)a.dout + row * D * ES, left * D * ES);
-            else
-                rs = make_rsrc_words(a.ld + row, left * 8);
-            const int dst = k < NINS ? st + k * 1024 : DUMMY;
-            buffer_to_lds16(rs, __builtin_amdgcn_readfirstlane(lds0 + dst), doff[i]);
+            const int dq_ = k < TG::INS ? st + k * 1024 : DUMMY;
+            const int do_ = k < TG::INS ? st + T_DO + k * 1024 : DUMMY;
+            buffer_to_lds16(rq, __builtin_amdgcn_readfirstlane(lds0 + dq_), doff[i]);
+            buffer_to_lds16(ro, __builtin_amdgcn_readfirstlane(lds0 + do_), doff[i]);
         }
+        if (wave == 0)
+            buffer_to_lds16(make_rsrc_words(a.ld + row, left * 8), lds0 + st + T_LD,
+                            lane * 16 < QT * 8 ? (uint32_t)lane * 16u : kOob);
     };
     auto stage_tile = [&](int j) {  // synchronous staging (no DMA)
         const auto [row, qt] = tile_row(j);
         const int nv = min(QT, S - qt);
-        stage_rows<T, DPAD, QT, RB>(smem, (const uint8_t*)a.q + row * D * ES, nv, D, a.vec);
-        stage_rows<T, DPAD, QT, RB>(smem + T_DO, (const uint8_t*)a.dout + row * D * ES, nv, D,
-                                    a.vec);
+        stage_rows<TG, QT>(smem, (const uint8_t*)a.q + row * D * ES, nv, D, a.vec);
+        stage_rows<TG, QT>(smem + T_DO, (const uint8_t*)a.dout + row * D * ES, nv, D, a.vec);
         if (tid < QT)
             ((float2*)(smem + T_LD))[tid] = tid < nv ? a.ld[row + tid] : make_float2(0.0f, 0.0f);
     };
@@ -356,8 +428,8 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv(BackwardArgs a) {
     F kf[MB], vf[MB];
 #pragma unroll
     for (int m = 0; m < MB; ++m) {
-        kf[m] = B::row_global(a.k, krow0 + k0 + c, k0 + c < S, 32 * m, D, g, a.vec);
-        vf[m] = B::row_global(a.v, krow0 + k0 + c, k0 + c < S, 32 * m, D, g, a.vec);
+        kf[m] = B::row_global(a.k, krow0 + k0 + c, k0 + c < S, 32 * m, D, g, vec);
+        vf[m] = B::row_global(a.v, krow0 + k0 + c, k0 + c < S, 32 * m, D, g, vec);
     }
     f32x16_t dk[MB], dv[MB];
 #pragma unroll
@@ -366,6 +438,25 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv(BackwardArgs a) {
         dv[m] = (f32x16_t)0.0f;
     }
     const float c2 = a.scale * kLog2e;
+    Ops16<TG, B, MB> ops;
+    if constexpr (PIPE) ops.init(lane);
+
+    // Probabilities and dS of one sub-block from its S and dP accumulators; `diag`: the
+    // sub-block on the causal diagonal (query q0 + kidx(g, t) against key q0 + c).
+    auto softmax = [&](auto diag, const f32x16_t& s, const f32x16_t& dp, const float (&l2)[16],
+                       const float (&dl)[16], F& pf, F& df) {
+        float pv[16], dsv[16];
+#pragma unroll
+        for (int t = 0; t < 16; ++t) {
+            float p = fast_exp2(fmaf(s[t], c2, -l2[t]));
+            if constexpr (decltype(diag)::value)
+                if (c > B::kidx(g, t)) p = 0.0f;
+            pv[t] = p;
+            dsv[t] = p * (dp[t] - dl[t]);
+        }
+        pf = B::pack(pv);
+        df = B::pack(dsv);
+    };
 
     if constexpr (DMA) {
         dma_tile(0, 0);
@@ -383,35 +474,122 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv(BackwardArgs a) {
             __syncthreads();
         }
         const int qt = tile_row(j).second;
+        // active sub-blocks [s0, s1): causal skips the ones wholly before the wave's keys
+        const int s0 = a.causal ? min(NSUB, max(0, (k0 - qt) >> 5)) : 0;
+        const int s1 = min(NSUB, (S - qt + 31) >> 5);
+        if constexpr (PIPE) {
+            using H = typename B::H;
+            constexpr int NS = 4 * MB;  // MFMAs of S+dP, and of dV+dK, per sub-block
+            constexpr int R = 2, RV = 2;
+            const uint8_t* tile0 = smem + st;
+            // A operand of MFMA i of S / dP: chain i & 1 (Q for S, dO for dP), dims
+            // 32 (i >> 2) + 16 ((i >> 1) & 1) + 8 g ..
+            auto aread = [&](int sb, int i) {
+                return ops.rread(tile0 + (i & 1 ? T_DO : 0) + sb * 32 * RB, i >> 2, (i >> 1) & 1);
+            };
+            auto sdp = [&](int sb, f32x16_t& sa, f32x16_t& da) {
+                u32x4_t ring[R];
 #pragma unroll
-        for (int sub = 0; sub < QT / 32; ++sub) {
-            const int q0 = qt + sub * 32;
-            if (q0 >= S) break;
-            if (a.causal && q0 + 31 < k0) continue;  // no query of the block sees a key
-            f32x16_t s = (f32x16_t)0.0f, dp = (f32x16_t)0.0f;
-            const uint8_t* qa = smem + st + (sub * 32 + B::arow(c)) * RB;
-            const uint8_t* oa = qa + T_DO;
+                for (int i = 0; i < R; ++i) ring[i] = aread(sb, i);
+                sa = (f32x16_t)0.0f;
+                da = (f32x16_t)0.0f;
 #pragma unroll
-            for (int m = 0; m < MB; ++m) {
-                s = B::mma(B::row_lds(qa + m * 32 * ES, g), kf[m], s);
-                dp = B::mma(B::row_lds(oa + m * 32 * ES, g), vf[m], dp);
+                for (int i = 0; i < NS; ++i) {
+                    const u32x4_t av = ring[i % R];
+                    if (i + R < NS) ring[i % R] = aread(sb, i + R);
+                    if (i & 1) da = H::mfma32(av, vf[i >> 2].v[(i >> 1) & 1], da);
+                    else sa = H::mfma32(av, kf[i >> 2].v[(i >> 1) & 1], sa);
+                }
+            };
+            // B operand of MFMA i of dV / dK: chain i & 1 (dO^T for dV, Q^T for dK), column
+            // block i >> 2, rows 16 ((i >> 1) & 1) + 8 g .. (two transposing reads)
+            auto bread = [&](int sb, int i) {
+                return ops.tread(tile0 + (i & 1 ? 0 : T_DO) + sb * 32 * RB, i >> 2, (i >> 1) & 1);
+            };
+            auto dvdk = [&](int sb, const F& pf, const F& df) {
+                u32x4_t ring[RV];
+#pragma unroll
+                for (int i = 0; i < RV; ++i) ring[i] = bread(sb, i);
+#pragma unroll
+                for (int i = 0; i < NS; ++i) {
+                    const u32x4_t bv = ring[i % RV];
+                    if (i + RV < NS) ring[i % RV] = bread(sb, i + RV);
+                    if (i & 1) dk[i >> 2] = H::mfma32(df.v[(i >> 1) & 1], bv, dk[i >> 2]);
+                    else dv[i >> 2] = H::mfma32(pf.v[(i >> 1) & 1], bv, dv[i >> 2]);
+                }
+            };
+            auto load_ld = [&](int sb, float (&l2)[16], float (&dl)[16]) {
+                rows16<T>(smem + st + T_LD + sb * 32 * 8, g, l2, dl);
+            };
+            // VALU instructions of one softmax call, spread over the NS MFMAs it overlaps
+            constexpr int VX = (80 + NS - 1) / NS;
+
+            f32x16_t sacc[2], dacc[2];
+            float l2[2][16], dl[2][16];
+            F pf, df;
+#pragma unroll
+            for (int sb = 0; sb < NSUB; ++sb) {
+                if (sb < s0 || sb >= s1) continue;
+                const int u = sb & 1;
+                if (sb == s0) {
+                    load_ld(sb, l2[u], dl[u]);
+                    sdp(sb, sacc[u], dacc[u]);
+                }
+                const bool diag = a.causal && qt + 32 * sb == k0;
+                const bool next = sb + 1 < s1;
+                if (next) {
+                    // phase X: S, dP of sb+1 under the softmax of sb
+                    auto phase_x = [&](auto dg) {
+                        sdp(sb + 1, sacc[u ^ 1], dacc[u ^ 1]);
+                        softmax(dg, sacc[u], dacc[u], l2[u], dl[u], pf, df);
+                        FA_BWD_SG(0x100, R);
+#pragma unroll
+                        for (int i = 0; i < NS; ++i) {
+                            FA_BWD_SG(0x008, 1);
+                            if (i + R < NS) FA_BWD_SG(0x100, 1);
+                            FA_BWD_SG(0x402, VX);
+                        }
+                    };
+                    if (diag) phase_x(std::true_type{});
+                    else phase_x(std::false_type{});
+                } else {
+                    if (diag) softmax(std::true_type{}, sacc[u], dacc[u], l2[u], dl[u], pf, df);
+                    else softmax(std::false_type{}, sacc[u], dacc[u], l2[u], dl[u], pf, df);
+                }
+                // phase Y: dV, dK of sb; (LSE, delta) rows of sb+1
+                dvdk(sb, pf, df);
+                if (next) load_ld(sb + 1, l2[u ^ 1], dl[u ^ 1]);
+                FA_BWD_SG(0x100, 2 * RV);
+#pragma unroll
+                for (int i = 0; i < NS; ++i) {
+                    FA_BWD_SG(0x008, 1);
+                    if (i + RV < NS) FA_BWD_SG(0x100, 2);
+                }
             }
-            float l2[16], dl[16], pv[16], dsv[16];
-            rows16<T>(smem + st + T_LD + sub * 32 * 8, g, l2, dl);
-            const bool mask = a.causal && k0 + 31 > q0;
+        } else {
 #pragma unroll
-            for (int t = 0; t < 16; ++t) {
-                float p = fast_exp2(fmaf(s[t], c2, -l2[t]));
-                if (mask && k0 + c > q0 + B::kidx(g, t)) p = 0.0f;
-                pv[t] = p;
-                dsv[t] = p * (dp[t] - dl[t]);
-            }
-            const F pf = B::pack(pv), df = B::pack(dsv);
-            const uint8_t* qt_tile = smem + st + sub * 32 * RB;
+            for (int sb = 0; sb < NSUB; ++sb) {
+                if (sb < s0 || sb >= s1) continue;
+                const int q0 = qt + sb * 32;
+                f32x16_t s = (f32x16_t)0.0f, dp = (f32x16_t)0.0f;
+                const uint8_t* qa = smem + st + (sb * 32 + B::arow(c)) * RB;
+                const uint8_t* oa = qa + T_DO;
 #pragma unroll
-            for (int m = 0; m < MB; ++m) {
-                dv[m] = B::mma(pf, B::template col_lds<RB>(qt_tile + T_DO, 32 * m, lane), dv[m]);
-                dk[m] = B::mma(df, B::template col_lds<RB>(qt_tile, 32 * m, lane), dk[m]);
+                for (int m = 0; m < MB; ++m) {
+                    s = B::mma(B::row_lds(qa + m * 32 * ES, g), kf[m], s);
+                    dp = B::mma(B::row_lds(oa + m * 32 * ES, g), vf[m], dp);
+                }
+                float l2[16], dl[16];
+                rows16<T>(smem + st + T_LD + sb * 32 * 8, g, l2, dl);
+                F pf, df;
+                if (a.causal && q0 == k0) softmax(std::true_type{}, s, dp, l2, dl, pf, df);
+                else softmax(std::false_type{}, s, dp, l2, dl, pf, df);
+                const uint8_t* tile = smem + st + sb * 32 * RB;
+#pragma unroll
+                for (int m = 0; m < MB; ++m) {
+                    dv[m] = B::mma(pf, B::template col_lds<RB>(tile + T_DO, 32 * m, lane), dv[m]);
+                    dk[m] = B::mma(df, B::template col_lds<RB>(tile, 32 * m, lane), dk[m]);
+                }
             }
         }
         if constexpr (DMA) {
@@ -437,18 +615,21 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv(BackwardArgs a) {
 // ------------------------------------------------------------------ dQ
 // One workgroup: 128 queries of one (batch, query head), 32 per wave, Q and dO of them in
 // registers; tiles of 64 keys (K, V) of the KV head are swept, DMA double-buffered as above.
+// Two waves per SIMD (16-bit), so the phases of the two waves overlap.
 template <typename T, int DPAD, bool DMA>
 __global__ __launch_bounds__(256, Blk<T>::ES == 2 ? 2 : 1) void bwd_dq(BackwardArgs a) {
     using B = Blk<T>;
     using F = typename B::Frag;
-    using TG = TileGeom<T, DPAD>;
-    constexpr int ES = B::ES, MB = DPAD / 32, KT = kBwdTile, RB = TG::RB;
-    constexpr int T_V = TG::BYTES;
-    constexpr int NINS = 2 * TG::SL;  // transfers per stage: K, V
+    constexpr int ES = B::ES, MB = DPAD / 32, KT = kBwdTile;
+    using TG = TileGeom<T, DPAD, KT, ES == 2 && DPAD == 128>;
+    constexpr int RB = TG::RB, T_V = TG::BYTES;
+    constexpr int NINS = 2 * TG::INS;  // transfers per stage: K, V
     constexpr int STAGE = NINS * 1024;
-    constexpr int KI = (NINS + 3) / 4;
+    constexpr int KI = (TG::INS + 3) / 4;  // per wave and tensor (K and V share the offsets)
     constexpr int DUMMY = 2 * STAGE;
-    __shared__ __attribute__((aligned(16))) uint8_t smem[(DMA ? 2 : 1) * STAGE + (DMA ? 1024 : 0)];
+    constexpr bool NEED_DUMMY = DMA && TG::INS % 4 != 0;
+    __shared__ __attribute__((aligned(16)))
+    uint8_t smem[(DMA ? 2 : 1) * STAGE + (NEED_DUMMY ? 1024 : 0)];
 
     const int tid = threadIdx.x, lane = tid & 63, g = lane >> 5, c = lane & 31;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -463,33 +644,33 @@ __global__ __launch_bounds__(256, Blk<T>::ES == 2 ? 2 : 1) void bwd_dq(BackwardA
     const bool qok = q0 + c < S;
     const int kend = a.causal ? min(S, (qb + 1) * kBwdQueries) : S;
     const int ntiles = (kend + KT - 1) / KT;
+    const bool vec = DMA || a.vec;
 
     uint32_t doff[DMA ? KI : 1];
     const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_void_t*)smem;
     if constexpr (DMA) {
 #pragma unroll
-        for (int i = 0; i < KI; ++i) {
-            const int k = wave + 4 * i;
-            doff[i] = tile_slot_offset<T, DPAD>(k < TG::SL ? k : k - TG::SL, lane, D);
-        }
+        for (int i = 0; i < KI; ++i) doff[i] = tile_slot_offset<TG>(wave + 4 * i, lane, D);
     }
     auto dma_tile = [&](int j, int st) {
         const int kt = j * KT, left = S - kt;
+        const i32x4_t rk = make_rsrc_words((const uint8_t*)a.k + (krow0 + kt) * D * ES, left * D * ES);
+        const i32x4_t rv = make_rsrc_words((const uint8_t*)a.v + (krow0 + kt) * D * ES, left * D * ES);
 #pragma unroll
         for (int i = 0; i < KI; ++i) {
             const int k = wave + 4 * i;
-            const i32x4_t rs = make_rsrc_words(
-                (const uint8_t*)(k < TG::SL ? a.k : a.v) + (krow0 + kt) * D * ES, left * D * ES);
-            const int dst = k < NINS ? st + k * 1024 : DUMMY;
-            buffer_to_lds16(rs, __builtin_amdgcn_readfirstlane(lds0 + dst), doff[i]);
+            const int dk_ = k < TG::INS ? st + k * 1024 : DUMMY;
+            const int dv_ = k < TG::INS ? st + T_V + k * 1024 : DUMMY;
+            buffer_to_lds16(rk, __builtin_amdgcn_readfirstlane(lds0 + dk_), doff[i]);
+            buffer_to_lds16(rv, __builtin_amdgcn_readfirstlane(lds0 + dv_), doff[i]);
         }
     };
 
     F qf[MB], of[MB];
 #pragma unroll
     for (int m = 0; m < MB; ++m) {
-        qf[m] = B::row_global(a.q, qrow0 + q0 + c, qok, 32 * m, D, g, a.vec);
-        of[m] = B::row_global(a.dout, qrow0 + q0 + c, qok, 32 * m, D, g, a.vec);
+        qf[m] = B::row_global(a.q, qrow0 + q0 + c, qok, 32 * m, D, g, vec);
+        of[m] = B::row_global(a.dout, qrow0 + q0 + c, qok, 32 * m, D, g, vec);
     }
     const float2 ldq = qok ? a.ld[qrow0 + q0 + c] : make_float2(0.0f, 0.0f);
     const float l2 = ldq.x, dl = ldq.y;
@@ -497,6 +678,8 @@ __global__ __launch_bounds__(256, Blk<T>::ES == 2 ? 2 : 1) void bwd_dq(BackwardA
 #pragma unroll
     for (int m = 0; m < MB; ++m) dq[m] = (f32x16_t)0.0f;
     const float c2 = a.scale * kLog2e;
+    Ops16<TG, B, MB> ops;
+    if constexpr (ES == 2) ops.init(lane);
 
     if constexpr (DMA) {
         dma_tile(0, 0);
@@ -512,10 +695,9 @@ __global__ __launch_bounds__(256, Blk<T>::ES == 2 ? 2 : 1) void bwd_dq(BackwardA
         } else {
             const int nv = min(KT, S - kt);
             __syncthreads();
-            stage_rows<T, DPAD, KT, RB>(smem, (const uint8_t*)a.k + (krow0 + kt) * D * ES, nv, D,
-                                        a.vec);
-            stage_rows<T, DPAD, KT, RB>(smem + T_V, (const uint8_t*)a.v + (krow0 + kt) * D * ES,
-                                        nv, D, a.vec);
+            stage_rows<TG, KT>(smem, (const uint8_t*)a.k + (krow0 + kt) * D * ES, nv, D, a.vec);
+            stage_rows<TG, KT>(smem + T_V, (const uint8_t*)a.v + (krow0 + kt) * D * ES, nv, D,
+                               a.vec);
             __syncthreads();
         }
 #pragma unroll
@@ -524,12 +706,23 @@ __global__ __launch_bounds__(256, Blk<T>::ES == 2 ? 2 : 1) void bwd_dq(BackwardA
             if (kk0 >= S) break;
             if (a.causal && kk0 > q0 + 31) continue;  // every key of the block is masked
             f32x16_t s = (f32x16_t)0.0f, dp = (f32x16_t)0.0f;
-            const uint8_t* ka = smem + st + (sub * 32 + B::arow(c)) * RB;
-            const uint8_t* va = ka + T_V;
+            const uint8_t* tk = smem + st + sub * 32 * RB;
+            if constexpr (ES == 2) {
+                using H = typename B::H;
 #pragma unroll
-            for (int m = 0; m < MB; ++m) {
-                s = B::mma(B::row_lds(ka + m * 32 * ES, g), qf[m], s);
-                dp = B::mma(B::row_lds(va + m * 32 * ES, g), of[m], dp);
+                for (int m = 0; m < MB; ++m)
+#pragma unroll
+                    for (int h2 = 0; h2 < 2; ++h2) {
+                        s = H::mfma32(ops.rread(tk, m, h2), qf[m].v[h2], s);
+                        dp = H::mfma32(ops.rread(tk + T_V, m, h2), of[m].v[h2], dp);
+                    }
+            } else {
+                const uint8_t* ka = tk + B::arow(c) * RB;
+#pragma unroll
+                for (int m = 0; m < MB; ++m) {
+                    s = B::mma(B::row_lds(ka + m * 32 * ES, g), qf[m], s);
+                    dp = B::mma(B::row_lds(ka + T_V + m * 32 * ES, g), of[m], dp);
+                }
             }
             // register t: key kk0 + kidx(g, t), query q0 + c
             const bool mask = (a.causal && kk0 + 31 > q0) || kk0 + 31 >= S;
@@ -542,9 +735,18 @@ __global__ __launch_bounds__(256, Blk<T>::ES == 2 ? 2 : 1) void bwd_dq(BackwardA
                 dsv[t] = p * (dp[t] - dl);
             }
             const F df = B::pack(dsv);
+            if constexpr (ES == 2) {
+                using H = typename B::H;
 #pragma unroll
-            for (int m = 0; m < MB; ++m)
-                dq[m] = B::mma(df, B::template col_lds<RB>(smem + st + sub * 32 * RB, 32 * m, lane), dq[m]);
+                for (int m = 0; m < MB; ++m)
+#pragma unroll
+                    for (int h2 = 0; h2 < 2; ++h2)
+                        dq[m] = H::mfma32(df.v[h2], ops.tread(tk, m, h2), dq[m]);
+            } else {
+#pragma unroll
+                for (int m = 0; m < MB; ++m)
+                    dq[m] = B::mma(df, B::template col_lds<RB>(tk, 32 * m, lane), dq[m]);
+            }
         }
         if constexpr (DMA) {
             wait_dma();
