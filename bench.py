@@ -226,6 +226,40 @@ def build_backward(ctx, rng, S=4096):
     return (lambda: pipe.encode_prepared(prep)), flop
 
 
+def measure_backward(ctx, rng, steps, warmup):
+    """`--only backward`: the recompute backward alone, op time from HIP events on the library's
+    stream, the three kernels' time from the library's per-dispatch events."""
+    run, flop = build_backward(ctx, rng)
+    ev = HipEvents()
+    for _ in range(warmup):
+        run()
+    tel = ctx.last_telemetry()
+    ctx.synchronize()
+    a, b = ev.create(), ev.create()
+    ev.record(a, ctx.stream)
+    for _ in range(steps):
+        run()
+    ev.record(b, ctx.stream)
+    op_ms = ev.elapsed_ms(a, b) / steps
+    ctx.set_kernel_timing(True)
+    for _ in range(steps):
+        run()
+    total, cnt = ctx.kernel_timing(tel.kernel_id)
+    ctx.set_kernel_timing(False)
+    k_ms = total / max(cnt, 1)
+    tf, ktf = flop / (op_ms * 1e-3) / 1e12, flop / (k_ms * 1e-3) / 1e12
+    return {"metric": "recompute backward (dQ, dK, dV) TFLOP/s, causal GQA D128 N4096",
+            "value": round(tf, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": steps,
+            "warmup": warmup, "ms_per_step": round(op_ms, 4), "higher_is_better": True,
+            "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+            "config": {"workload": "recompute backward: causal GQA B2 Hq32 Hkv8 N4096 D128 bf16",
+                       "flop_per_step": flop, "parallelism": "single GPU"},
+            "kernel": tel.kernel_name, "kernel_ms": round(k_ms, 4),
+            "roofline": {"bound": "mfma", "achieved": round(ktf, 2), "peak": PEAK_BF16_TFLOPS,
+                         "unit": "TFLOP/s", "frac": round(ktf / PEAK_BF16_TFLOPS, 4),
+                         "traffic": None}}
+
+
 def measure_all_configs(ctx, ev, rng, steps):
     """The other BASELINE configs, each timed alone (op events + its kernel's own events)."""
     stream = ctx.stream
@@ -387,7 +421,9 @@ def main():
                     help="1: transposed-V pre-pass for the 16-bit prefill (fa_ctx_set_prefill_v_layout)")
     ap.add_argument("--prefill-policy", type=int, default=-1,
                     help="-1 auto, 0 rotate K on load, 1 pre-rotate K")
-    ap.add_argument("--only", choices=["prefill", "decode"], default=None)
+    ap.add_argument("--only", choices=["prefill", "decode", "backward"], default=None,
+                    help="time one op alone (backward: the recompute backward at the prefill "
+                         "shape, a line of its own)")
     ap.add_argument("--decode-split", type=int, default=None,
                     help="tokens per split-K partition of the decode plan (default: automatic)")
     ap.add_argument("--all-configs", action="store_true",
@@ -411,6 +447,10 @@ def main():
 
     rng = np.random.default_rng(1234)
     ctx = fa.HipContext(0)
+    if args.only == "backward":
+        print(json.dumps(measure_backward(ctx, rng, args.steps, args.warmup)))
+        ctx.close()
+        return
     ctx.set_prefill_policy(args.prefill_policy)
     ctx.set_prefill_v_layout(args.prefill_v_layout)
     ev = HipEvents()

@@ -2319,4 +2319,19 @@ int fa_backward_grouped_recompute(fa_ctx* ctx, const void* packed_forward, size_
                                gr + lay.dk_offset, gr + lay.dv_offset, sh, cfg, dtype);
 }
 
+int fa_backward_layout_mha(const fa_attention_shape* sh, int dtype, fa_backward_layout* out) {
+    if (!sh) return fail(FA_ERR_NULL_ARGUMENT, "shape is null");
+    const fa_grouped_shape g{sh->batch, sh->heads, sh->heads, sh->seq_len, sh->head_dim};
+    return fa_backward_grouped_layout(&g, dtype, out);
+}
+
+int fa_backward_recompute_mha(fa_ctx* ctx, const void* packed_forward, size_t forward_bytes,
+                              void* packed_grads, size_t grads_bytes,
+                              const fa_attention_shape* sh, const fa_config* cfg, int dtype) {
+    if (!sh) return fail(FA_ERR_NULL_ARGUMENT, "shape is null");
+    const fa_grouped_shape g{sh->batch, sh->heads, sh->heads, sh->seq_len, sh->head_dim};
+    return fa_backward_grouped_recompute(ctx, packed_forward, forward_bytes, packed_grads,
+                                         grads_bytes, &g, cfg, dtype);
+}
+
 }  // extern "C"

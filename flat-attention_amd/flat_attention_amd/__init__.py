@@ -20,6 +20,7 @@ from .api import (AsymmetricGroupedAttentionShape, AsymmetricRotaryEmbeddingConf
                   FlatAttentionBackwardOutput, GroupedBackwardRecomputeLayout,
                   HipGroupedBackwardRecomputePipeline, PreparedGroupedBackwardRecompute,
                   grouped_backward_layout, pack_grouped_backward_recompute_inputs,
+                  HipBackwardRecomputePipeline, pack_backward_recompute_inputs,
                   bf16_bits_to_f32, download_attention,
                   f32_to_bf16_bits, host_storage, packed_layout, paged_append_batched,
                   storage_np_dtype, storage_to_f32)

@@ -187,6 +187,9 @@ PROTOTYPES = {
     "fa_backward_grouped_layout": (INT, [P(GroupedShapeC), INT, P(BackwardLayoutC)]),
     "fa_backward_grouped_recompute": (INT, [VP, VP, SZ, VP, SZ, P(GroupedShapeC), P(ConfigC),
                                             INT]),
+    "fa_backward_layout_mha": (INT, [P(AttentionShapeC), INT, P(BackwardLayoutC)]),
+    "fa_backward_recompute_mha": (INT, [VP, VP, SZ, VP, SZ, P(AttentionShapeC), P(ConfigC),
+                                        INT]),
     "fa_backward_grouped": (INT, [VP, VP, VP, VP, VP, VP, VP, VP, VP, VP, P(GroupedShapeC),
                                   P(ConfigC), INT]),
     "fa_last_telemetry": (INT, [VP, P(TelemetryC)]),

@@ -1041,3 +1041,36 @@ def pack_grouped_backward_recompute_inputs(q, k, v, d_out, forward: FlatAttentio
         raise L.FlatHipError(7, f"LSE has {lse.size} values, expected {lay.lse_elements}")
     parts.append(lse)
     return np.concatenate([p.view(np.uint8) for p in parts])
+
+
+class HipBackwardRecomputePipeline:
+    """WgpuBackwardRecomputePipeline src/wgpu_backward.rs:127 (M18 canonical MHA recompute
+    backward): the grouped backward with kv_heads == heads over the same packed contract."""
+
+    def __init__(self, ctx: HipContext, dtype: int = L.DTYPE_F32):
+        self.ctx = ctx
+        self.dtype = dtype
+
+    def layout(self, shape: AttentionShape) -> GroupedBackwardRecomputeLayout:
+        c = L.BackwardLayoutC()
+        check(lib().fa_backward_layout_mha(ctypes.byref(shape.c()), self.dtype, ctypes.byref(c)))
+        return GroupedBackwardRecomputeLayout(*(getattr(c, n) for n, _ in c._fields_))
+
+    def create_gradient_buffer(self, shape: AttentionShape) -> DeviceBuffer:
+        return DeviceBuffer(self.ctx, self.layout(shape).gradient_bytes)
+
+    def encode(self, packed_forward: DeviceBuffer, packed_grads: DeviceBuffer,
+               shape: AttentionShape, config: FlatAttentionConfig
+               ) -> GroupedBackwardRecomputeLayout:
+        check(lib().fa_backward_recompute_mha(
+            self.ctx.handle, packed_forward.ptr, packed_forward.nbytes, packed_grads.ptr,
+            packed_grads.nbytes, ctypes.byref(shape.c()), ctypes.byref(config.c()), self.dtype))
+        return self.layout(shape)
+
+
+def pack_backward_recompute_inputs(q, k, v, d_out, forward: FlatAttentionOutput,
+                                   shape: AttentionShape, dtype: int = L.DTYPE_F32) -> np.ndarray:
+    """pack_backward_recompute_inputs src/wgpu_backward.rs:282 (bytes, as the grouped packer)."""
+    g = GroupedAttentionShape(shape.batch, shape.heads, shape.heads, shape.seq_len,
+                              shape.head_dim)
+    return pack_grouped_backward_recompute_inputs(q, k, v, d_out, forward, g, dtype)

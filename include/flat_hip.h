@@ -406,6 +406,14 @@ int fa_backward_grouped_recompute(fa_ctx* ctx, const void* packed_forward, size_
                                   void* packed_grads, size_t grads_bytes,
                                   const fa_grouped_shape* shape, const fa_config* config,
                                   int dtype);
+/* M18 canonical MHA form: WgpuBackwardRecomputePipeline::layout src/wgpu_backward.rs:162 and
+ * encode :201 (packing pack_backward_recompute_inputs :282) — the grouped backward with
+ * kv_heads == heads; the fa_backward_layout fields are filled the same way (q_elements ==
+ * kv_elements = tensor_elements). */
+int fa_backward_layout_mha(const fa_attention_shape* shape, int dtype, fa_backward_layout* out);
+int fa_backward_recompute_mha(fa_ctx* ctx, const void* packed_forward, size_t forward_bytes,
+                              void* packed_grads, size_t grads_bytes,
+                              const fa_attention_shape* shape, const fa_config* config, int dtype);
 /* The same backward over separate tensors (e.g. O|LSE straight from fa_forward_gqa_rope's packed
  * output): q, d_out, out, dq hold q_elements, k, v, dk, dv kv_elements, lse lse_elements. */
 int fa_backward_grouped(fa_ctx* ctx, const void* q, const void* k, const void* v,

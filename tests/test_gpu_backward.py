@@ -195,3 +195,32 @@ def test_training_chain_own_forward(hip, dtype):
             assert_close(name, a, e, 5e-4, 2.5e-3)
         else:
             assert_close(name, a, e, 2e-2 * float(np.abs(e).max()), 2e-2)
+
+
+@pytest.mark.parametrize("causal,scale,dims", [(False, 0.61, (2, 2, 3, 4)), (True, 0.61, (2, 2, 3, 4)),
+                                               (True, 0.57, (1, 2, 3, 4))])
+def test_m18_canonical_mha_pipeline(hip, causal, scale, dims):
+    """tests/m18_wgpu_backward.rs:168 (B2 H2 S3 D4, scale 0.61, both masks) and
+    tests/m18_wgpu_backward_pipeline.rs:95 (B1 H2 S3 D4, causal, 0.57), 4e-4 + 2e-3|e|."""
+    B, H, S, D = dims
+    n = B * H * S * D
+    if dims[0] == 2:
+        fx = lambda p: _fx(n, p, 0.071, 0.75, 0.1875, 0.43)  # noqa: E731
+        q, k, v, do = fx(0.1), fx(0.7), fx(1.3), fx(1.9)
+    else:
+        fx = lambda p: _fx(n, p, 0.083, 0.625, 0.25, 0.31)  # noqa: E731
+        q, k, v, do = fx(0.1), fx(0.7), fx(1.2), fx(1.9)
+    o, lse = oracle.forward(q, k, v, B, H, S, D, causal, scale)
+    want = oracle.backward_grouped(q, k, v, do, o, lse, B, H, H, S, D, causal, scale)
+    shape = fa.AttentionShape(B, H, S, D)
+    pipe = fa.HipBackwardRecomputePipeline(hip, fa.DTYPE_F32)
+    lay = pipe.layout(shape)
+    assert lay.packed_forward_bytes == 4 * (5 * n + B * H * S) and lay.gradient_bytes == 12 * n
+    fbuf = fa.DeviceBuffer.from_array(
+        hip, fa.pack_backward_recompute_inputs(q, k, v, do, fa.FlatAttentionOutput(o, lse), shape))
+    gbuf = pipe.create_gradient_buffer(shape)
+    gbuf.fill_u32(0x7FC00000)
+    pipe.encode(fbuf, gbuf, shape, fa.FlatAttentionConfig(causal, scale))
+    got = [gbuf.download(np.float32, n, off) for off in (0, 4 * n, 8 * n)]
+    for name, a, e in zip(("dQ", "dK", "dV"), got, want):
+        assert_close(name, a, e, 4e-4, 2e-3)

@@ -313,3 +313,25 @@ def test_backward_validation_variants():
     assert _backward(shape=(1, 2, 1, 8, 12), dtype=fa.DTYPE_BF16) == "UnsupportedHeadDim"
     assert _backward(shape=(1, 2, 1, 8, 6)) == "NullArgument"
     assert _backward() == "NullArgument"
+
+
+def test_mha_backward_layout_and_validation():
+    """WgpuBackwardRecomputePipeline::layout src/wgpu_backward.rs:162-185 (Q|K|V|dO|O|LSE with
+    five equal tensors) and encode's validation order :207-214."""
+    sh = L.AttentionShapeC(2, 3, 5, 8)
+    lay = L.BackwardLayoutC()
+    assert fa.lib().fa_backward_layout_mha(ctypes.byref(sh), fa.DTYPE_F32, ctypes.byref(lay)) == 0
+    t = 2 * 3 * 5 * 8
+    assert lay.packed_forward_bytes == 4 * (5 * t + 30) and lay.gradient_bytes == 12 * t
+    assert (lay.k_offset, lay.lse_offset, lay.dv_offset) == (4 * t, 20 * t, 8 * t)
+
+    def call(shape=(2, 3, 5, 8), fwd=None, grads=None):
+        s_ = L.AttentionShapeC(*shape)
+        return _variant(fa.lib().fa_backward_recompute_mha(
+            None, FAKE, lay.packed_forward_bytes if fwd is None else fwd, FAKE,
+            lay.gradient_bytes if grads is None else grads, ctypes.byref(s_),
+            ctypes.byref(L.ConfigC(1, 0, 0.0)), fa.DTYPE_F32))
+    assert call(shape=(2, 0, 5, 8)) == "ZeroDimension"
+    assert call(fwd=64) == "BufferTooSmall"
+    assert call(grads=64) == "BufferTooSmall"
+    assert call() == "NullArgument"
