@@ -312,8 +312,10 @@ __global__ __launch_bounds__(256) void bwd_delta(BackwardArgs a, int64_t rows) {
     float acc = 0.0f;
     if (row < rows) {
         const int64_t base = row * D;
+        // Lane `sub` of a row sums chunks sub, sub + 16, ... of W elements in element order,
+        // with 16-byte loads or element loads: both give the same bits.
+        constexpr int W = 16 / B::ES;
         if (a.vec) {
-            constexpr int W = 16 / B::ES;
             for (int col = sub * W; col < D; col += 16 * W) {
                 const u32x4_t x = *(const u32x4_t*)((const uint8_t*)a.dout + (base + col) * B::ES);
                 const u32x4_t y = *(const u32x4_t*)((const uint8_t*)a.o + (base + col) * B::ES);
@@ -330,8 +332,9 @@ __global__ __launch_bounds__(256) void bwd_delta(BackwardArgs a, int64_t rows) {
                 }
             }
         } else {
-            for (int col = sub; col < D; col += 16)
-                acc = fmaf(B::load(a.dout, base + col), B::load(a.o, base + col), acc);
+            for (int col = sub * W; col < D; col += 16 * W)
+                for (int i = 0; i < W && col + i < D; ++i)
+                    acc = fmaf(B::load(a.dout, base + col + i), B::load(a.o, base + col + i), acc);
         }
     }
 #pragma unroll

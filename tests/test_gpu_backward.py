@@ -224,3 +224,75 @@ def test_m18_canonical_mha_pipeline(hip, causal, scale, dims):
     got = [gbuf.download(np.float32, n, off) for off in (0, 4 * n, 8 * n)]
     for name, a, e in zip(("dQ", "dK", "dV"), got, want):
         assert_close(name, a, e, 4e-4, 2e-3)
+
+
+@pytest.mark.parametrize("dtype", [fa.DTYPE_BF16, fa.DTYPE_F16])
+@pytest.mark.parametrize("dims,causal", [((1, 4, 2, 100, 8), True), ((2, 4, 1, 70, 40), False),
+                                         ((1, 6, 3, 150, 96), True)])
+def test_16bit_partial_head_dims(hip, dtype, dims, causal):
+    """Head dims below the padded tile width (32 / 64 / 128 columns): columns >= D are zero in
+    every staged tile and never stored."""
+    rnd = bf16_round if dtype == fa.DTYPE_BF16 else f16_round
+    shape = fa.GroupedAttentionShape(*dims)
+    B, Hq, Hkv, S, D = dims
+    q, k, v, do = (rnd(normal(n, 51 + i)) for i, n in enumerate(
+        (B * Hq * S * D, B * Hkv * S * D, B * Hkv * S * D, B * Hq * S * D)))
+    fwd, _ = _expected(q, k, v, do, shape, causal, None)
+    fwd = fa.FlatAttentionOutput(rnd(fwd.output), fwd.lse)
+    want = oracle.backward_grouped(q, k, v, do, fwd.output, fwd.lse, B, Hq, Hkv, S, D, causal,
+                                   threads=8)
+    got = fa.HipGroupedBackwardRecomputePipeline(hip, dtype).backward(
+        q, k, v, do, fwd, shape, fa.FlatAttentionConfig(causal))
+    for name, a, e in zip(("dQ", "dK", "dV"), (got.dq, got.dk, got.dv), want):
+        assert_close(name, a, e, 2e-2 * float(np.abs(e).max()), 2e-2)
+
+
+@pytest.mark.parametrize("dtype", [fa.DTYPE_BF16, fa.DTYPE_F32])
+def test_unaligned_tensors_take_the_staged_path(hip, dtype):
+    """Tensors at 2-byte (16-bit) / 4-byte (f32) offsets: no 16-byte loads or buffer->LDS
+    transfers are possible, the kernels stage through registers (telemetry names the reason);
+    results equal the aligned call's bit for bit."""
+    B, Hq, Hkv, S, D = 1, 4, 2, 130, 64
+    rnd = bf16_round if dtype == fa.DTYPE_BF16 else (lambda x: x)
+    q, k, v, do = (rnd(normal(n, 61 + i)) for i, n in enumerate(
+        (B * Hq * S * D, B * Hkv * S * D, B * Hkv * S * D, B * Hq * S * D)))
+    shape = fa.GroupedAttentionShape(B, Hq, Hkv, S, D)
+    fwd, _ = _expected(q, k, v, do, shape, True, None)
+    o = rnd(fwd.output)
+    eb = 2 if dtype == fa.DTYPE_BF16 else 4
+    pipe = fa.HipGroupedBackwardRecomputePipeline(hip, dtype)
+    lay = pipe.layout(shape)
+    cfg = fa.FlatAttentionConfig(True)
+
+    def run(shift):
+        ins = [fa.host_storage(x, dtype) for x in (q, k, v, do, o)] + [fwd.lse.astype(np.float32)]
+        bufs = []
+        for x in ins:
+            b = fa.DeviceBuffer(hip, x.nbytes + 64)
+            b.upload(x, shift)
+            bufs.append(b)
+        outs = [fa.DeviceBuffer(hip, n * eb + 64) for n in (lay.q_elements, lay.kv_elements,
+                                                          lay.kv_elements)]
+        view = lambda b: fa.DeviceBuffer(hip, b.nbytes - shift, b.ptr + shift)  # noqa: E731
+        pipe.encode_tensors(*(view(b) for b in bufs[:5]), bufs[5].ptr + shift,
+                            *(view(b) for b in outs), shape, cfg)
+        tele = hip.last_telemetry()
+        res = [b.download(np.uint8, n * eb, shift) for b, n in zip(
+            outs, (lay.q_elements, lay.kv_elements, lay.kv_elements))]
+        for b in bufs + outs:
+            b.free()
+        return res, tele
+
+    aligned, t0 = run(0)
+    shifted, t1 = run(eb)
+    assert t0.fallback_reason is None and t1.fallback_reason is not None
+    for a, b_ in zip(aligned, shifted):
+        np.testing.assert_array_equal(a, b_)
+    want = oracle.backward_grouped(q, k, v, do, o, fwd.lse, B, Hq, Hkv, S, D, True)
+    got = [fa.storage_to_f32(x.view(fa.storage_np_dtype(dtype)), dtype) for x in aligned]
+    tol = (5e-4, 2.5e-3) if dtype == fa.DTYPE_F32 else None
+    for name, a, e in zip(("dQ", "dK", "dV"), got, want):
+        if tol:
+            assert_close(name, a, e, *tol)
+        else:
+            assert_close(name, a, e, 2e-2 * float(np.abs(e).max()), 2e-2)
