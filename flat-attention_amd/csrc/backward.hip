@@ -362,9 +362,10 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv(BackwardArgs a) {
     using F = typename B::Frag;
     constexpr int ES = B::ES, MB = DPAD / 32;
     constexpr bool PIPE = ES == 2;
-    // query rows per tile: two stages of Q and dO must fit the 160 KiB of LDS
-    constexpr int QT = PIPE ? (DPAD == 128 ? 96 : 128) : 64, NSUB = QT / 32;
-    using TG = TileGeom<T, DPAD, QT>;
+    // 128 query rows per tile (16-bit; two stages of Q and dO in 130 KiB with the unpadded
+    // swizzled rows at D 128), 64 for f32
+    constexpr int QT = PIPE ? 128 : 64, NSUB = QT / 32;
+    using TG = TileGeom<T, DPAD, QT, PIPE && DPAD == 128>;
     constexpr int RB = TG::RB;
     constexpr int T_DO = TG::BYTES, T_LD = 2 * TG::BYTES;  // within a stage
     constexpr int NINS = 2 * TG::INS + 1;                   // transfers per stage: Q, dO, ld
