@@ -402,6 +402,26 @@ def cpu_baseline(sample_seconds: float = 20.0):
     return res
 
 
+def cpu_baseline_backward():
+    """Scalar C oracle of the recompute backward (oracle/, backward_reference_grouped) on one
+    (batch, kv head) unit of the backward workload: its 4 query heads, causal, N = 4096 rows
+    (about 10 s on one core)."""
+    import oracle  # CPU baseline leg only
+    n, D, G = 4096, 128, 4
+    q = oracle.fill_normal(G * n * D, 11)
+    k = oracle.fill_normal(n * D, 12)
+    v = oracle.fill_normal(n * D, 13)
+    do = oracle.fill_normal(G * n * D, 14)
+    o, lse = oracle.forward_grouped(q, k, v, 1, G, 1, n, D, True)
+    t0 = time.perf_counter()
+    oracle.backward_grouped(q, k, v, do, o, lse, 1, G, 1, n, D, True)
+    dt = time.perf_counter() - t0
+    flop = 10.0 * G * D * n * (n + 1) / 2
+    return {"value": flop / dt / 1e12, "unit": "TFLOP/s", "cores": 1, "kind": "port",
+            "sample": f"oracle backward_reference_grouped, one (b, kv head) unit with its {G} "
+                      f"query heads, causal N={n}, D{D}, {dt:.2f} s"}
+
+
 def _traffic(traffic, name):
     """HBM bytes per launch of the op's dominant kernel, from the committed PMC summary."""
     if not traffic or name not in traffic:
@@ -448,7 +468,10 @@ def main():
     rng = np.random.default_rng(1234)
     ctx = fa.HipContext(0)
     if args.only == "backward":
-        print(json.dumps(measure_backward(ctx, rng, args.steps, args.warmup)))
+        out = measure_backward(ctx, rng, args.steps, args.warmup)
+        if not args.no_cpu_baseline:
+            out["cpu_baseline"] = cpu_baseline_backward()
+        print(json.dumps(out))
         ctx.close()
         return
     ctx.set_prefill_policy(args.prefill_policy)
