@@ -266,7 +266,8 @@ def measure_all_configs(ctx, ev, rng, steps):
     res = {}
 
     def timed(run):
-        for _ in range(2):
+        # warm up for 100 calls (clocks settle after tens of milliseconds of sustained work)
+        for _ in range(100):
             run()
         tel = ctx.last_telemetry()
         ctx.synchronize()
