@@ -903,24 +903,39 @@ __global__ __launch_bounds__(64 * NW, 2) void prefill_mfma16(PrefillKArgs ka) {
         }
     }
 
-    // ---- epilogue
+    // ---- epilogue: the wave's 32 normalised O rows are staged in its own LDS region (free once
+    // every wave has passed its last K/V read) and written back as whole rows with streaming
+    // 16-byte stores, so they leave the caches while this compute-bound kernel still runs
+    // instead of being written back under the next (memory-bound) kernel.
     const float l_tot = l_run + shfl_xor(l_run, 32);
     const float inv = 1.0f / l_tot;
+    constexpr int ORB = DPAD * 2 + 16;  // staged row pitch (bytes)
+    constexpr int OCH = DPAD / 8;       // 16-byte chunks per row
+    constexpr int ORI = 64 / OCH;       // rows per store instruction
+    __syncthreads();
+    uint8_t* ost = smem + wave * 32 * ORB;
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) {
+            const int d0 = mb * 32 + 8 * q4 + 4 * g;
+            u32x2_t w;
+            w[0] = H::pack(oacc[mb][4 * q4] * inv, oacc[mb][4 * q4 + 1] * inv);
+            w[1] = H::pack(oacc[mb][4 * q4 + 2] * inv, oacc[mb][4 * q4 + 3] * inv);
+            *(u32x2_t*)(ost + (lane & 31) * ORB + d0 * 2) = w;
+        }
+#pragma unroll
+    for (int i = 0; i < 32 / ORI; ++i) {
+        const int r = i * ORI + lane / OCH, ch = lane % OCH;
+        const u32x4_t v = *(const u32x4_t*)(ost + r * ORB + ch * 16);
+        const int t_r = __shfl(t, r), hq_r = __shfl(hq, r), ok_r = __shfl((int)row_ok, r);
+        if (ok_r && (FULLD || ch * 8 < D)) {
+            uint16_t* dst = (uint16_t*)a.o + (int64_t)b * a.o_sb + (int64_t)hq_r * a.o_sh +
+                            (int64_t)t_r * a.o_ss + ch * 8;
+            __builtin_nontemporal_store(v, (u32x4_t*)dst);
+        }
+    }
     if (row_ok) {
-        uint16_t* orow = (uint16_t*)a.o + (int64_t)b * a.o_sb + (int64_t)hq * a.o_sh +
-                         (int64_t)t * a.o_ss;
-#pragma unroll
-        for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-            for (int q4 = 0; q4 < 4; ++q4) {
-                const int d0 = mb * 32 + 8 * q4 + 4 * g;
-                if (FULLD || d0 < D) {
-                    u32x2_t w;
-                    w[0] = H::pack(oacc[mb][4 * q4] * inv, oacc[mb][4 * q4 + 1] * inv);
-                    w[1] = H::pack(oacc[mb][4 * q4 + 2] * inv, oacc[mb][4 * q4 + 3] * inv);
-                    *(u32x2_t*)(orow + d0) = w;
-                }
-            }
         if (g == 0)
             a.lse[(int64_t)b * a.lse_sb + (int64_t)hq * a.lse_sh + t] = m_run * a.scale + logf(l_tot);
     } else if (a.var_meta && row < rows_pad) {
