@@ -104,6 +104,12 @@ __device__ __forceinline__ float xor32(float v) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// 16-byte load of data read exactly once (the K/V stream of a decode step): non-temporal, so
+// the stream neither evicts data that is reused nor leaves lines behind for the next kernel.
+__device__ __forceinline__ u32x4_t stream_load16(const void* p) {
+    return __builtin_nontemporal_load((const u32x4_t*)p);
+}
+
 // Rotate one interleaved (even, odd) pair: (e c - o s, e s + o c). Written with explicit fmaf
 // so every kernel that rotates (in-register, pre-pass, cache append) rounds identically.
 __device__ __forceinline__ void rope_pair(float& e, float& o, float c, float s) {

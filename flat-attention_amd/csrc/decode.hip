@@ -189,7 +189,7 @@ __device__ __forceinline__ void decode_item(const DecodeKArgs& ka, int s, int kv
             if constexpr (F32) d0 = 16 * c + 4 * g4;
             else d0 = 32 * c + 8 * g4;
             const int dl = d0 < D ? d0 : 0;
-            kd[c] = *(const u32x4_t*)(kpool + (krow * width + dl) * EB);
+            kd[c] = stream_load16(kpool + (krow * width + dl) * EB);
             if (d0 >= D) kd[c] = u32x4_t{0u, 0u, 0u, 0u};
         }
     };
@@ -199,7 +199,7 @@ __device__ __forceinline__ void decode_item(const DecodeKArgs& ka, int s, int kv
             const int64_t vr = row_of(min(key0 + 4 * g4 + i, k1 - 1));
 #pragma unroll
             for (int c = 0; c < VCH; ++c)
-                vd[i][c] = *(const u32x4_t*)(vpool + (vr * width + dv_ld + 4 * c) * EB);
+                vd[i][c] = stream_load16(vpool + (vr * width + dv_ld + 4 * c) * EB);
         }
     };
 
@@ -464,7 +464,7 @@ __device__ __forceinline__ void decode_mfma_item(const DecodeKArgs& ka, int s, i
         const uint8_t* rowp = kpool + (r0 + kr) * (int64_t)width * 2;
 #pragma unroll
         for (int c = 0; c < NQ; ++c) {
-            kd[c] = *(const u32x4_t*)(rowp + (min(32 * c + 8 * g4, D - 8)) * 2);
+            kd[c] = stream_load16(rowp + (min(32 * c + 8 * g4, D - 8)) * 2);
             if (32 * c + 8 * g4 >= D) kd[c] = u32x4_t{0u, 0u, 0u, 0u};
         }
         (void)dk;
@@ -475,7 +475,7 @@ __device__ __forceinline__ void decode_mfma_item(const DecodeKArgs& ka, int s, i
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int vr = min(key0 + 4 * g4 + i, k1 - 1) - base;
-            vd[i] = *(const u32x4_t*)(vpool + (r0 + vr) * (int64_t)width * 2 + dv * 2);
+            vd[i] = stream_load16(vpool + (r0 + vr) * (int64_t)width * 2 + dv * 2);
         }
     };
 
