@@ -88,6 +88,7 @@ template <> struct Blk<float> {
     }
 };
 
+// 16-bit storage: LDS operands are read through the swizzled tile readers (Ops16 below).
 template <typename S> struct Blk16 {
     using H = Half<S>;
     struct Frag { u32x4_t v[2]; };
@@ -109,34 +110,6 @@ template <typename S> struct Blk16 {
         for (int s = 0; s < 2; ++s)
 #pragma unroll
             for (int j = 0; j < 4; ++j) f.v[s][j] = H::pack(x[8 * s + 2 * j], x[8 * s + 2 * j + 1]);
-        return f;
-    }
-    __device__ __forceinline__ static Frag row_lds(const uint8_t* p, int g) {
-        Frag f;
-#pragma unroll
-        for (int s = 0; s < 2; ++s) f.v[s] = *(const u32x4_t*)(p + (16 * s + 8 * g) * 2);
-        return f;
-    }
-    // ds_read_b64_tr_b16: lane (16-lane group G, index i) addresses row 8 g + i / 4 and columns
-    // 16 (G & 1) + 4 (i & 3) .. +3 of the block; it receives column c of rows 8 g + 0..3. A
-    // second read 4 rows further gives rows 8 g + 4..7.
-    template <int RB>
-    __device__ __forceinline__ static Frag col_lds(const uint8_t* tile, int col0, int lane) {
-        typedef short v4i16_t __attribute__((ext_vector_type(4)));
-        typedef __attribute__((address_space(3))) v4i16_t lds_v4i16_t;
-        const int g = lane >> 5;
-        const uint8_t* src = tile + (8 * g + ((lane & 15) >> 2)) * RB +
-                             (col0 + 16 * ((lane >> 4) & 1) + 4 * (lane & 3)) * 2;
-        Frag f;
-#pragma unroll
-        for (int s = 0; s < 2; ++s) {
-            const uint8_t* p = src + s * 16 * RB;
-            const v4i16_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)p);
-            const v4i16_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)(p + 4 * RB));
-            const u32x2_t l2 = __builtin_bit_cast(u32x2_t, lo);
-            const u32x2_t h2 = __builtin_bit_cast(u32x2_t, hi);
-            f.v[s] = u32x4_t{l2[0], l2[1], h2[0], h2[1]};
-        }
         return f;
     }
     __device__ __forceinline__ static Frag row_global(const void* base, int64_t row, bool valid,
