@@ -204,7 +204,11 @@ __global__ __launch_bounds__(64 * NW, 2) void prefill_mfma16(PrefillKArgs ka) {
     constexpr int NWD = PP ? (FA_PP_DMA == 2 ? 8 : 4) : NW;
     constexpr int KI = (KINS + NWD - 1) / NWD, VI = (VINS + NWD - 1) / NWD;  // per wave
     constexpr int DUMMY = 2 * STAGE;
-    __shared__ __attribute__((aligned(16))) uint8_t smem[(DB ? 2 : 1) * STAGE + (DMA ? 1024 : 0)];
+    // LDS: the K/V stages (+ the dummy KiB of the transfers), reused at the end to stage the
+    // output rows (NW waves x 32 rows of DPAD * 2 + 16 bytes)
+    constexpr int SMEM_KV = (DB ? 2 : 1) * STAGE + (DMA ? 1024 : 0);
+    constexpr int SMEM_O = NW * 32 * (DPAD * 2 + 16);
+    __shared__ __attribute__((aligned(16))) uint8_t smem[SMEM_KV > SMEM_O ? SMEM_KV : SMEM_O];
     int st_r = 0, st_w = 0;  // byte offsets of the stage being read / written
     int st_k = 0, st_v = 0;  // stage offsets the K (S^T) and V (P.V) operand reads use
 
