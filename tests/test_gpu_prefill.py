@@ -64,6 +64,37 @@ def test_mha_f32_shapes(hip, D, S, causal):
     assert_close("LSE", l, el, F32_ATOL, F32_RTOL)
 
 
+@pytest.mark.parametrize("D", [32, 64, 80, 128])
+@pytest.mark.parametrize("S", [1, 7, 64, 65, 130, 300])
+@pytest.mark.parametrize("causal", [False, True])
+def test_mha_16bit_shapes(hip, D, S, causal):
+    """The 16-bit kernel (256-row ping-pong workgroups) at edge shapes: a single key, partial
+    key tiles, head dims below the padded width, and query blocks whose rows run out part-way
+    through either wave group."""
+    B, H = 2, 3
+    q, k, v = (bf16_round(normal(B * H * S * D, 300 + s + D + S)) for s in range(3))
+    shape = fa.GroupedAttentionShape(B, H, H, S, D)
+    o, l = _run_grouped(hip, q, k, v, shape, fa.FlatAttentionConfig(causal), None, fa.DTYPE_BF16)
+    eo, el = _oracle_grouped(q, k, v, shape, causal, None)
+    assert_close("O", o, eo, H16_ATOL, 0.0)
+    assert_close("LSE", l, el, H16_ATOL, 0.0)
+
+
+@pytest.mark.parametrize("hq,hkv,S", [(8, 2, 65), (12, 4, 97), (32, 8, 33), (6, 1, 129)])
+@pytest.mark.parametrize("causal", [False, True])
+def test_gqa_rope_f16_group_shapes(hip, hq, hkv, S, causal):
+    """GQA groups whose query rows (S x group) end inside a 256-row block, with RoPE, f16."""
+    B, D = 2, 128
+    q = f16_round(normal(B * hq * S * D, 400 + S))
+    k, v = f16_round(normal(B * hkv * S * D, 401 + S)), f16_round(normal(B * hkv * S * D, 402 + S))
+    shape = fa.GroupedAttentionShape(B, hq, hkv, S, D)
+    rot = fa.RotaryEmbeddingConfig(1e4, 3)
+    o, l = _run_grouped(hip, q, k, v, shape, fa.FlatAttentionConfig(causal), rot, fa.DTYPE_F16)
+    eo, el = _oracle_grouped(q, k, v, shape, causal, rot)
+    assert_close("O", o, eo, H16_ATOL, 0.0)
+    assert_close("LSE", l, el, H16_ATOL, 0.0)
+
+
 @pytest.mark.parametrize("hq,hkv", [(4, 4), (8, 2), (6, 1), (32, 8)])
 @pytest.mark.parametrize("theta,offset", [(1e4, 0), (5e5, 37)])
 def test_gqa_rope_f32(hip, hq, hkv, theta, offset):
