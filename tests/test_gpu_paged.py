@@ -7,7 +7,7 @@ import numpy as np
 import pytest
 
 import oracle
-from _inputs import bf16_round, normal
+from _inputs import bf16_round, f16_round, normal
 from conftest import assert_close
 
 import flat_attention_amd as fa
@@ -379,3 +379,59 @@ def test_kernel_timing_and_mfma_variant_telemetry(hip):
         assert hip.kernel_timing("DecodePagedMfma") == (0.0, 0)
     finally:
         hip.set_kernel_timing(False)
+
+
+def _paged_prefill(hip, bt, ps, total, n_seqs, hq, hkv, D, cached, ql, theta, raw_k, v, q, dtype,
+                   causal):
+    kv_len = cached + ql
+    kp = fa.DeviceBuffer(hip, total * ps * hkv * D * 4)
+    vp = fa.DeviceBuffer(hip, total * ps * hkv * D * 4)
+    fa.paged_append_batched(hip, bt, np.zeros(n_seqs, np.int32), kv_len, ps, total, hkv, D,
+                            fa.DeviceBuffer.from_array(hip, fa.host_storage(raw_k, dtype)),
+                            fa.DeviceBuffer.from_array(hip, fa.host_storage(v, dtype)),
+                            kp, vp, fa.RotaryEmbeddingConfig(theta, 0), dtype)
+    shape = fa.AsymmetricGroupedAttentionShape(n_seqs, hq, hkv, ql, kv_len, D, cached)
+    plan = fa.PagedChunkedPrefillPlan(hip, bt, ps, total, shape, fa.FlatAttentionConfig(causal),
+                                      fa.AsymmetricRotaryEmbeddingConfig(theta, cached, 0), dtype)
+    out = fa.DeviceBuffer(hip, plan.layout().combined_bytes)
+    plan.launch(fa.DeviceBuffer.from_array(hip, fa.host_storage(q, dtype)), kp, vp, out)
+    res = fa.download_attention(out, plan.layout(), dtype)
+    return fa.storage_to_f32(res.output, dtype), res.lse
+
+
+@pytest.mark.parametrize("dtype", [fa.DTYPE_BF16, fa.DTYPE_F16, fa.DTYPE_F32])
+@pytest.mark.parametrize("ps", [16, 5, 32])
+@pytest.mark.parametrize("D,causal", [(128, True), (64, True), (128, False)])
+def test_paged_prefill_modes_match_oracle_and_gather_bit_exactly(hip, dtype, ps, D, causal):
+    """Chunked prefill over the paged cache in every addressing mode: 16-bit with page size a
+    multiple of 16 (one page per 16-key group), 16-bit with any page size, and f32. A query
+    chunk of 50 rows after 37 cached tokens, so key tiles and pages end mid-way. The same
+    data under the identity block table and a shuffled one must give bitwise identical O/LSE."""
+    rnd = {fa.DTYPE_BF16: bf16_round, fa.DTYPE_F16: f16_round, fa.DTYPE_F32: lambda x: x}[dtype]
+    atol, rtol = (F32_ATOL, F32_RTOL) if dtype == fa.DTYPE_F32 else (H16_ATOL, 0.0)
+    n_seqs, hq, hkv, cached, ql, theta = 2, 8, 2, 37, 50, 1e4
+    kv_len = cached + ql
+    pages_per = -(-kv_len // ps)
+    total = n_seqs * pages_per + 3  # a few pool pages no table names
+    rng = np.random.default_rng(ps * 7 + D)
+    width = hkv * D
+    raw_k = rnd(normal(n_seqs * kv_len * width, 31 + ps))
+    v = rnd(normal(n_seqs * kv_len * width, 32 + ps))
+    q = rnd(normal(n_seqs * ql * hq * D, 33 + ps))
+    ident = np.arange(n_seqs * pages_per, dtype=np.int32).reshape(n_seqs, pages_per)
+    shuf = rng.permutation(total)[:n_seqs * pages_per].astype(np.int32).reshape(n_seqs, pages_per)
+    o1, l1 = _paged_prefill(hip, ident, ps, total, n_seqs, hq, hkv, D, cached, ql, theta, raw_k,
+                            v, q, dtype, causal)
+    o2, l2 = _paged_prefill(hip, shuf, ps, total, n_seqs, hq, hkv, D, cached, ql, theta, raw_k,
+                            v, q, dtype, causal)
+    assert np.array_equal(o1.view(np.uint32), o2.view(np.uint32))
+    assert np.array_equal(l1.view(np.uint32), l2.view(np.uint32))
+    for s in range(n_seqs):
+        sl_kv = slice(s * kv_len * width, (s + 1) * kv_len * width)
+        qs = oracle.rope_rotate_rows(q[s * ql * hq * D:(s + 1) * ql * hq * D], ql, hq, D, theta,
+                                     cached)
+        ks = oracle.rope_rotate_rows(raw_k[sl_kv], kv_len, hkv, D, theta, 0)
+        eo, el = oracle.forward_projection_asymmetric(qs, ks, v[sl_kv], 1, hq, hkv, ql, kv_len,
+                                                      D, cached, causal, None)
+        assert_close(f"O seq {s}", o1[s * ql * hq * D:(s + 1) * ql * hq * D], eo, atol, rtol)
+        assert_close(f"LSE seq {s}", l1[s * hq * ql:(s + 1) * hq * ql], el, atol, rtol)
