@@ -99,6 +99,26 @@ def test_batched_bf16_decode_matches_oracle(hip, hq, hkv):
     assert_close("LSE", l, el, H16_ATOL, 0.0)
 
 
+@pytest.mark.parametrize("dtype", [fa.DTYPE_BF16, fa.DTYPE_F16])
+@pytest.mark.parametrize("ps,D,hq,hkv", [(16, 64, 8, 2), (32, 128, 16, 4), (48, 128, 8, 8),
+                                         (5, 128, 8, 2), (24, 64, 4, 1), (16, 128, 32, 16)])
+def test_16bit_decode_modes_match_oracle(hip, dtype, ps, D, hq, hkv):
+    """16-bit KV in every decode layout: grouped MFMA (page size a multiple of 16, up to 8 KV
+    heads), one-wave MFMA (more KV heads), VALU split-K (other page sizes); contexts ending
+    inside pages and key steps."""
+    rnd = bf16_round if dtype == fa.DTYPE_BF16 else f16_round
+    rng = np.random.default_rng(ps * 3 + D + hkv)
+    ctx_lens = [1, 17, 64, 95, 700]
+    bt, kp, vp, total = _make_pool(rng, ctx_lens, ps, hkv, D, rnd, seed=ps + D)
+    q = rnd(normal(len(ctx_lens) * hq * D, 5 + ps))
+    o, l, _ = _decode(hip, bt, ctx_lens, kp, vp, total, ps, hq, hkv, D, q, dtype)
+    t = hip.last_telemetry()
+    assert t.kernel_id == ("DecodePagedMfma" if ps % 16 == 0 else "DecodePagedSplitK")
+    eo, el = oracle.paged_decode(q, kp, vp, total, ps, bt, ctx_lens, hq, hkv, D, True, 1e4)
+    assert_close("O", o, eo, H16_ATOL, 0.0)
+    assert_close("LSE", l, el, H16_ATOL, 0.0)
+
+
 @pytest.mark.parametrize("ps", [3, 16, 32])
 @pytest.mark.parametrize("D", [64, 128])
 def test_f32_decode_matches_oracle(hip, ps, D):
