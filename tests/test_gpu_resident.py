@@ -10,7 +10,7 @@ import numpy as np
 import pytest
 
 import oracle
-from _inputs import bf16_round, normal
+from _inputs import bf16_round, f16_round, normal
 from conftest import assert_close
 
 import flat_attention_amd as fa
@@ -75,7 +75,7 @@ def test_resident_cache_appends_in_place_and_decode_matches_oracle(hip):
     assert len(cache) == 0
 
 
-@pytest.mark.parametrize("dtype", [fa.DTYPE_BF16, fa.DTYPE_F32])
+@pytest.mark.parametrize("dtype", [fa.DTYPE_BF16, fa.DTYPE_F16, fa.DTYPE_F32])
 @pytest.mark.parametrize("batch,hq,hkv,cap,kv_len,D",
                          [(1, 16, 4, 8192, 8192, 64), (4, 32, 8, 1024, 777, 128),
                           (2, 8, 8, 48, 17, 64)])
@@ -84,7 +84,7 @@ def test_external_pre_rotated_k_decode_matches_oracle(hip, dtype, batch, hq, hkv
     row 1 is the published M15/M48 decode shape (B1 Hq16 Hkv4 D64, kv 8192)."""
     rng = np.random.default_rng(batch * 1000 + kv_len)
     width = hkv * D
-    rnd = bf16_round if dtype == fa.DTYPE_BF16 else (lambda x: x)
+    rnd = {fa.DTYPE_BF16: bf16_round, fa.DTYPE_F16: f16_round}.get(dtype, lambda x: x)
     k = rnd(normal(batch * cap * width, int(rng.integers(1 << 30))))
     v = rnd(normal(batch * cap * width, int(rng.integers(1 << 30))))
     q = rnd(normal(batch * hq * D, int(rng.integers(1 << 30))))

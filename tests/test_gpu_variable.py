@@ -10,7 +10,7 @@ import numpy as np
 import pytest
 
 import oracle
-from _inputs import bf16_round, normal
+from _inputs import bf16_round, f16_round, normal
 from conftest import assert_close
 
 import flat_attention_amd as fa
@@ -41,7 +41,7 @@ def _run_case(hip, shape, meta, config, rotary, dtype, q, k, v, check_seqs=None)
     res = fa.download_attention(out, lay, dtype)
     o = fa.storage_to_f32(res.output, dtype).reshape(shape.batch, shape.query_len, qw)
     lse = res.lse.reshape(shape.batch, shape.q_heads, shape.query_len)
-    rnd = bf16_round if dtype == fa.DTYPE_BF16 else (lambda x: x)
+    rnd = {fa.DTYPE_BF16: bf16_round, fa.DTYPE_F16: f16_round}.get(dtype, lambda x: x)
     for b, m in enumerate(meta):
         aq, ak = m.active_query_len, m.active_kv_len
         if check_seqs is None or b in check_seqs:
@@ -63,7 +63,9 @@ def _run_case(hip, shape, meta, config, rotary, dtype, q, k, v, check_seqs=None)
         assert np.all(np.isneginf(lse[b, :, aq:])), f"padded LSE rows of sequence {b}"
 
 
-@pytest.mark.parametrize("dtype", [fa.DTYPE_F32, fa.DTYPE_BF16])
+# (f16: the poisoned padding overflows to inf on conversion, which is still never read)
+@pytest.mark.filterwarnings("ignore:overflow encountered in cast")
+@pytest.mark.parametrize("dtype", [fa.DTYPE_F32, fa.DTYPE_BF16, fa.DTYPE_F16])
 def test_mixed_length_causal_gqa_matches_independent_oracles(hip, dtype):
     """tests/wgpu_external_variable.rs:295."""
     shape = fa.AsymmetricGroupedAttentionShape(2, 8, 2, 5, 9, 64, 0)
@@ -76,7 +78,9 @@ def test_mixed_length_causal_gqa_matches_independent_oracles(hip, dtype):
               fa.VariableLengthRotaryEmbeddingConfig(10000.0, 11), dtype, q, k, v)
 
 
-@pytest.mark.parametrize("dtype", [fa.DTYPE_F32, fa.DTYPE_BF16])
+# (f16: the poisoned padding overflows to inf on conversion, which is still never read)
+@pytest.mark.filterwarnings("ignore:overflow encountered in cast")
+@pytest.mark.parametrize("dtype", [fa.DTYPE_F32, fa.DTYPE_BF16, fa.DTYPE_F16])
 def test_mixed_length_noncausal_mqa_matches_independent_oracles(hip, dtype):
     """tests/wgpu_external_variable.rs:340 (head_dim 80, explicit scale 0.125, theta 5e5)."""
     shape = fa.AsymmetricGroupedAttentionShape(3, 8, 1, 6, 10, 80, 0)
