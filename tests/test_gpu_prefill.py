@@ -301,3 +301,33 @@ def test_adversarial_scores_stay_finite(hip):
             eo, el = oracle.forward(q.ravel(), kk.ravel(), v, 1, 1, S, D, causal)
             assert_close("O", o, eo, F32_ATOL, F32_RTOL)
             assert_close("LSE", l, el, F32_ATOL, F32_RTOL)
+
+
+@pytest.mark.parametrize("dtype,rnd", [(fa.DTYPE_BF16, bf16_round), (fa.DTYPE_F16, f16_round)])
+def test_adversarial_scores_16bit(hip, dtype, rnd):
+    """The 16-bit kernel's running max only moves when a tile's max exceeds it by 2^8 (log2
+    units): scores rising across every key force a move on every tile, falling scores never
+    move it and leave most probabilities below the 16-bit range, +-24 alternation and ties
+    across several 64-key tiles and both wave groups of a 256-row workgroup."""
+    S, D, H = 300, 64, 2
+    idx = np.arange(S, dtype=np.float32)
+    cases = {
+        "rising": 0.5 * idx,
+        "falling": -0.5 * idx,
+        "alternating": np.where(np.arange(S) % 3 == 0, 24.0, -24.0).astype(np.float32),
+        "ties": np.zeros(S, np.float32),
+    }
+    v = rnd(normal(H * S * D, 6))
+    for name, scores in cases.items():
+        q = np.zeros((H, S, D), np.float32)
+        q[:, :, 0] = 1.0
+        k = np.zeros((H, S, D), np.float32)
+        k[:, :, 0] = scores * np.sqrt(D)
+        q, k = rnd(q.ravel()), rnd(k.ravel())
+        for causal in (False, True):
+            shape = fa.GroupedAttentionShape(1, H, H, S, D)
+            o, l = _run_grouped(hip, q, k, v, shape, fa.FlatAttentionConfig(causal), None, dtype)
+            eo, el = oracle.forward(q, k, v, 1, H, S, D, causal)
+            assert np.isfinite(o).all() and np.isfinite(l).all(), name
+            assert_close(f"O {name}", o, eo, H16_ATOL, 0.0)
+            assert_close(f"LSE {name}", l, el, H16_ATOL, 0.0)
