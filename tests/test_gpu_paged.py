@@ -455,3 +455,35 @@ def test_paged_prefill_modes_match_oracle_and_gather_bit_exactly(hip, dtype, ps,
                                                       D, cached, causal, None)
         assert_close(f"O seq {s}", o1[s * ql * hq * D:(s + 1) * ql * hq * D], eo, atol, rtol)
         assert_close(f"LSE seq {s}", l1[s * hq * ql:(s + 1) * hq * ql], el, atol, rtol)
+
+
+@pytest.mark.parametrize("pattern", ["rising", "falling", "alternating"])
+def test_adversarial_scores_bf16_decode(hip, pattern):
+    """Split-K decode with scores that rise over the whole context (every segment's maximum
+    exceeds the previous ones, so the combine rescales every partial), fall (later segments'
+    probabilities underflow), or alternate between +-24."""
+    ps, hq, hkv, D = 16, 4, 1, 128
+    ctx_lens = [2000, 700]
+    rng = np.random.default_rng(11)
+    bt, kp, vp, total = _make_pool(rng, ctx_lens, ps, hkv, D, bf16_round, seed=12)
+    kp = kp.reshape(total * ps, hkv, D)
+    kp[:] = 0.0
+    for s, n in enumerate(ctx_lens):
+        idx = np.arange(n, dtype=np.float32)
+        sc = {"rising": 0.05 * idx, "falling": -0.05 * idx,
+              "alternating": np.where(np.arange(n) % 3 == 0, 24.0, -24.0)}[pattern]
+        rows = bt[s, np.arange(n) // ps] * ps + np.arange(n) % ps
+        kp[rows, :, 0] = (sc * np.sqrt(D))[:, None]
+    kp = bf16_round(kp.ravel())
+    q = np.zeros((len(ctx_lens), hq, D), np.float32)
+    q[:, :, 0] = 1.0
+    q = q.ravel()
+    o, l, _ = _decode(hip, bt, ctx_lens, kp, vp, total, ps, hq, hkv, D, q, fa.DTYPE_BF16,
+                      split=256)
+    eo, el = oracle.paged_decode(q, kp, vp, total, ps, bt, ctx_lens, hq, hkv, D, True, 1e4)
+    assert np.isfinite(o).all() and np.isfinite(l).all()
+    assert_close("O", o, eo, H16_ATOL, 0.0)
+    # The query is rotated in f32 and then rounded to bf16 for the MFMA, so every score carries a
+    # relative error up to 2^-9: with scores near 60 that moves LSE by ~0.2 (the reference's f16
+    # convention rounds only the inputs). LSE is held to 2e-2 + 2^-8 |LSE|.
+    assert_close("LSE", l, el, H16_ATOL, 2.0 ** -8)
