@@ -99,7 +99,9 @@ __device__ __forceinline__ void decode_item(const DecodeKArgs& ka, int s, int kv
 
     // ---- Q^T operand (rotated). Lane (n = head, g4) holds dims per k-step.
     constexpr int NQ = F32 ? DPAD / 16 : DPAD / 32;
-    u32x4_t qop[NQ];
+    // 16-bit: the rotated query as a high part and the rounding of its residual (one MFMA each,
+    // so scores keep f32-level accuracy)
+    u32x4_t qop[NQ], qlo[NQ];
     {
         const bool hv = n < nh;
         const uint8_t* qrow = (const uint8_t*)a.q +
@@ -113,7 +115,7 @@ __device__ __forceinline__ void decode_item(const DecodeKArgs& ka, int s, int kv
             int d0;
             if constexpr (F32) d0 = 16 * c + 4 * g4;
             else d0 = 32 * c + 8 * g4;
-            u32x4_t raw = {0u, 0u, 0u, 0u};
+            u32x4_t raw = {0u, 0u, 0u, 0u}, lo = {0u, 0u, 0u, 0u};
             if (hv && d0 < D) {
                 if constexpr (F32) {
                     raw = *(const u32x4_t*)(qrow + d0 * 4);
@@ -139,10 +141,15 @@ __device__ __forceinline__ void decode_item(const DecodeKArgs& ka, int s, int kv
                     }
                     rope4(x, c8);
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) raw[j] = Half<T>::pack(x[2 * j], x[2 * j + 1]);
+                    for (int j = 0; j < 4; ++j) {
+                        raw[j] = Half<T>::pack(x[2 * j], x[2 * j + 1]);
+                        lo[j] = Half<T>::pack(x[2 * j] - Half<T>::lo(raw[j]),
+                                              x[2 * j + 1] - Half<T>::hi(raw[j]));
+                    }
                 }
             }
             qop[c] = raw;
+            qlo[c] = lo;
         }
     }
 
@@ -227,6 +234,7 @@ __device__ __forceinline__ void decode_item(const DecodeKArgs& ka, int s, int kv
                             __uint_as_float(kbuf[s][c][j]), __uint_as_float(qop[c][j]), sc, 0, 0, 0);
                 } else {
                     sc = Half<T>::mfma16(kbuf[s][c], qop[c], sc);
+                    sc = Half<T>::mfma16(kbuf[s][c], qlo[c], sc);
                 }
             }
             load_k(kbuf[s], key0 + 16 * NS);
@@ -409,7 +417,11 @@ __device__ __forceinline__ void decode_mfma_item(const DecodeKArgs& ka, int s, i
     const int hq0 = kvh * a.group + hl0;
 
     // ---- Q^T operand (16x16x32 B operand): lane (head n, g4) holds dims 32c + 8g4 .. +8, rotated.
-    u32x4_t qop[NQ];
+    // The rotated query is kept as a 16-bit high part plus the 16-bit rounding of its residual,
+    // and S takes one MFMA for each: scores keep f32-level accuracy (the query is rotated after
+    // loading, so rounding it once would add a 2^-9 relative error to every score). The decode
+    // is HBM-bound, so the second MFMA costs no time.
+    u32x4_t qop[NQ], qlo[NQ];
     {
         const bool hv = n < nh;
         const uint16_t* qrow = (const uint16_t*)a.q + ((int64_t)s * a.q_heads + hq0 + (hv ? n : 0)) * D;
@@ -417,7 +429,7 @@ __device__ __forceinline__ void decode_mfma_item(const DecodeKArgs& ka, int s, i
 #pragma unroll
         for (int c = 0; c < NQ; ++c) {
             const int d0 = 32 * c + 8 * g4;
-            u32x4_t raw = {0u, 0u, 0u, 0u};
+            u32x4_t raw = {0u, 0u, 0u, 0u}, lo = {0u, 0u, 0u, 0u};
             if (hv && d0 < D) {
                 raw = *(const u32x4_t*)(qrow + d0);
                 float x[8], c8[8];
@@ -431,9 +443,13 @@ __device__ __forceinline__ void decode_mfma_item(const DecodeKArgs& ka, int s, i
                 }
                 rope4(x, c8);
 #pragma unroll
-                for (int j = 0; j < 4; ++j) raw[j] = Hf::pack(x[2 * j], x[2 * j + 1]);
+                for (int j = 0; j < 4; ++j) {
+                    raw[j] = Hf::pack(x[2 * j], x[2 * j + 1]);
+                    lo[j] = Hf::pack(x[2 * j] - Hf::lo(raw[j]), x[2 * j + 1] - Hf::hi(raw[j]));
+                }
             }
             qop[c] = raw;
+            qlo[c] = lo;
         }
     }
 
@@ -502,7 +518,10 @@ __device__ __forceinline__ void decode_mfma_item(const DecodeKArgs& ka, int s, i
             if constexpr (WSYNC) __syncthreads();
             f32x4_t sc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int c = 0; c < NQ; ++c) sc = Hf::mfma16(kbuf[t][c], qop[c], sc);
+            for (int c = 0; c < NQ; ++c) {
+                sc = Hf::mfma16(kbuf[t][c], qop[c], sc);
+                sc = Hf::mfma16(kbuf[t][c], qlo[c], sc);
+            }
             load_k(kbuf[t], key0 + 16 * NS);
             if (live) {
                 // V rows of this step -> LDS (row-major, padded)

@@ -483,7 +483,6 @@ def test_adversarial_scores_bf16_decode(hip, pattern):
     eo, el = oracle.paged_decode(q, kp, vp, total, ps, bt, ctx_lens, hq, hkv, D, True, 1e4)
     assert np.isfinite(o).all() and np.isfinite(l).all()
     assert_close("O", o, eo, H16_ATOL, 0.0)
-    # The query is rotated in f32 and then rounded to bf16 for the MFMA, so every score carries a
-    # relative error up to 2^-9: with scores near 60 that moves LSE by ~0.2 (the reference's f16
-    # convention rounds only the inputs). LSE is held to 2e-2 + 2^-8 |LSE|.
-    assert_close("LSE", l, el, H16_ATOL, 2.0 ** -8)
+    # scores near 60: a once-rounded rotated query would move LSE by ~0.2; the decode keeps the
+    # query's residual as a second MFMA operand, so LSE stays within the 16-bit bar
+    assert_close("LSE", l, el, H16_ATOL, 0.0)
