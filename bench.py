@@ -462,8 +462,9 @@ def main():
         print(json.dumps(res))
         return
     if args.gpus != 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path "
-              "(see DESIGN.md, 'How the path would shard')", file=sys.stderr)
+        print("bench.py measures one GPU: this build has no multi-GPU path (each GPU would "
+              "run its own shard of sequences / heads; nothing crosses GPUs on this path)",
+              file=sys.stderr)
         sys.exit(2)
 
     rng = np.random.default_rng(1234)
