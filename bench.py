@@ -369,37 +369,100 @@ def load_traffic():
         return None
 
 
-def cpu_baseline(sample_seconds: float = 20.0):
-    """Scalar C oracle (oracle/) timed on this host on bounded samples of the same workloads."""
+def _cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _cpu_threads() -> int:
+    """Worker threads for the all-core leg: the host cores this process may use, at most 16
+    (one GPU's share of the box)."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return max(1, min(16, n))
+
+
+def _timed_samples(fn, samples: int) -> dict:
+    """One untimed warm-up call, then `samples` timed calls (wall clock, output allocation
+    included as in examples/m28_scalar_flat_baseline.rs:100-179): median and p95 seconds."""
+    fn()
+    ts = []
+    for _ in range(samples):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return {"median_s": float(np.median(ts)), "p95_s": float(np.percentile(ts, 95)),
+            "samples": samples}
+
+
+def cpu_baseline(samples: int = 5):
+    """Scalar C oracle (oracle/) timed on this host on bounded samples of the same workloads,
+    single-threaded and over all cores (independent (batch, head) units / sequences per
+    thread). Rates use the median sample; p95 is reported beside it."""
     import oracle  # CPU baseline leg only
+    threads = _cpu_threads()
+    model = _cpu_model()
     res = {}
-    # prefill: first (b, h) unit of configs[2] truncated to its first n query rows (causal rows
+    # prefill: (b, h) units of configs[2] truncated to their first n query rows (causal rows
     # 0..n-1 do the same work as in the full problem); FLOP counted like the GPU metric.
-    n, D = 4096, 128
-    q = oracle.fill_normal(n * D, 1)
-    k = oracle.fill_normal(n * D, 2)
-    v = oracle.fill_normal(n * D, 3)
-    t0 = time.perf_counter()
-    oracle.forward_grouped_rope(q, k, v, 1, 1, 1, n, D, True, 10000.0, 0)
-    dt = time.perf_counter() - t0
-    flop = 4.0 * D * n * (n + 1) / 2
-    res["prefill"] = {"value": flop / dt / 1e12, "unit": "TFLOP/s", "cores": 1, "kind": "port",
-                      "sample": f"oracle forward_reference_grouped_rope, one (b,h) unit, causal "
-                                f"N={n} rows of configs[2] (D128, RoPE theta 1e4), {dt:.2f} s"}
-    # decode: 48 sequences of 4096 live tokens, Hq32 Hkv8 D128
-    ns, ctxl, hq, hkv, ps = 48, 4096, 32, 8, 16
+    n, D, theta = 1024, 128, 10000.0
+    flop_unit = 4.0 * D * n * (n + 1) / 2
+    q = oracle.fill_normal(threads * n * D, 1)
+    k = oracle.fill_normal(threads * n * D, 2)
+    v = oracle.fill_normal(threads * n * D, 3)
+    one = _timed_samples(lambda: oracle.forward_grouped_rope(
+        q[:n * D], k[:n * D], v[:n * D], 1, 1, 1, n, D, True, theta, 0), samples)
+    allc = _timed_samples(lambda: oracle.forward_grouped_rope(
+        q, k, v, 1, threads, threads, n, D, True, theta, 0, threads=threads), samples)
+    res["prefill"] = {
+        "value": flop_unit / one["median_s"] / 1e12, "unit": "TFLOP/s", "cores": 1,
+        "kind": "port", "p95_value": flop_unit / one["p95_s"] / 1e12,
+        "sample": f"oracle forward_reference_grouped_rope (RoPE theta 1e4, D128, causal), one "
+                  f"(b,h) unit of configs[2], its first {n} query rows; median of {samples} "
+                  f"after a warm-up ({one['median_s']:.2f} s, p95 {one['p95_s']:.2f} s)",
+        "all_cores": {"value": threads * flop_unit / allc["median_s"] / 1e12,
+                      "p95_value": threads * flop_unit / allc["p95_s"] / 1e12,
+                      "cores": threads, "sample": f"{threads} such units, one per thread "
+                      f"({allc['median_s']:.2f} s median)"},
+        "cpu_model": model}
+    # decode: sequences of 4096 live tokens, Hq32 Hkv8 D128. The oracle reads f32 pools, so the
+    # bytes are counted at 4 per element (every live K/V element once, plus Q, O, LSE, tables).
+    ctxl, hq, hkv, ps = 4096, 32, 8, 16
+    ns = 2 * threads
     pages = ctxl // ps
     bt = np.arange(ns * pages, dtype=np.int32).reshape(ns, pages)
     kp = oracle.fill_normal(ns * ctxl * hkv * D, 4)
     vp = oracle.fill_normal(ns * ctxl * hkv * D, 5)
     qd = oracle.fill_normal(ns * hq * D, 6)
-    t0 = time.perf_counter()
-    oracle.paged_decode(qd, kp, vp, ns * pages, ps, bt, [ctxl] * ns, hq, hkv, D, True, 10000.0)
-    dt = time.perf_counter() - t0
-    nbytes = ns * ctxl * hkv * D * 2 * 2  # same bf16 byte accounting as the GPU metric
-    res["decode"] = {"value": nbytes / dt / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
-                     "sample": f"oracle paged decode, {ns} seqs x {ctxl} tokens, Hq32 Hkv8 D128, "
-                               f"{dt:.2f} s"}
+
+    def nbytes(m):
+        return m * (ctxl * hkv * D * 2 * 4 + hq * D * 4 * 2 + hq * 4 + pages * 4)
+
+    n1 = 4
+    one = _timed_samples(lambda: oracle.paged_decode(
+        qd[:n1 * hq * D], kp, vp, ns * pages, ps, bt[:n1], [ctxl] * n1, hq, hkv, D, True, theta),
+        samples)
+    allc = _timed_samples(lambda: oracle.paged_decode(
+        qd, kp, vp, ns * pages, ps, bt, [ctxl] * ns, hq, hkv, D, True, theta, threads=threads),
+        samples)
+    res["decode"] = {
+        "value": nbytes(n1) / one["median_s"] / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
+        "p95_value": nbytes(n1) / one["p95_s"] / 1e9,
+        "sample": f"oracle paged decode, {n1} seqs x {ctxl} tokens, Hq32 Hkv8 D128, f32 pools "
+                  f"(4 B per element); median of {samples} after a warm-up "
+                  f"({one['median_s']:.2f} s, p95 {one['p95_s']:.2f} s)",
+        "all_cores": {"value": nbytes(ns) / allc["median_s"] / 1e9,
+                      "p95_value": nbytes(ns) / allc["p95_s"] / 1e9, "cores": threads,
+                      "sample": f"{ns} seqs over {threads} threads "
+                                f"({allc['median_s']:.2f} s median)"},
+        "cpu_model": model}
     return res
 
 
@@ -494,7 +557,11 @@ def main():
             tele[name] = ctx.last_telemetry()
     ctx.synchronize()
 
+    # One timed pass: HIP events around each op on the library's stream, and the library's own
+    # per-dispatch events (fa_ctx_set_kernel_timing) around every kernel inside it, so the op
+    # times and the dominant kernels' times describe the same steps at the same clocks.
     evs = [[ev.create() for _ in range(len(ops) + 1)] for _ in range(args.steps)]
+    ctx.set_kernel_timing(True)
     t_wall = time.perf_counter()
     for s in range(args.steps):
         ev.record(evs[s][0], stream)
@@ -505,23 +572,18 @@ def main():
                 tele[name] = ctx.last_telemetry()
     ctx.synchronize()
     wall = time.perf_counter() - t_wall
+    kern, kern_min = {}, {}
+    for name, _, _, _ in ops:
+        total, n = ctx.kernel_timing(tele[name].kernel_id)
+        kern[name] = total / max(n, 1)
+        kern_min[name] = ctx.kernel_timing_range(tele[name].kernel_id)[0]
+    ctx.set_kernel_timing(False)
     if args.calibrate_copy:
         a, b = fa.DeviceBuffer(ctx, COPY_BYTES), fa.DeviceBuffer(ctx, COPY_BYTES)
         ev.copy_d2d(b.ptr, a.ptr, COPY_BYTES, stream)
         ctx.synchronize()
         a.free()
         b.free()
-    # Dominant kernel of each op: a second timed pass of the same steps with the library's own
-    # events around every dispatch (kept out of the first pass, whose op times they would pad).
-    ctx.set_kernel_timing(True)
-    for _ in range(args.steps):
-        for _, run, _, _ in ops:
-            run()
-    kern = {}
-    for name, _, _, _ in ops:
-        total, n = ctx.kernel_timing(tele[name].kernel_id)
-        kern[name] = total / max(n, 1)
-    ctx.set_kernel_timing(False)
     per_op = {name: [ev.elapsed_ms(evs[s][i], evs[s][i + 1]) for s in range(args.steps)]
               for i, (name, _, _, _) in enumerate(ops)}
     step_ms = sum(np.mean(v) for v in per_op.values())
@@ -540,6 +602,7 @@ def main():
              "kernel": t.kernel_name, "kernel_id": t.kernel_id, "dispatches": t.dispatch_count,
              "grid": list(t.workgroups), **meta}
         d["kernel_ms"] = round(kern[name], 5)
+        d["kernel_ms_min"] = round(kern_min[name], 5)
         if name == "prefill":
             tf = work / (ms * 1e-3) / 1e12
             ktf = work / (kern[name] * 1e-3) / 1e12

@@ -178,7 +178,11 @@ struct fa_ctx {
     hipEvent_t open_begin = nullptr;
     std::vector<hipEvent_t> free_events;
     std::vector<Span> pending;
-    std::vector<std::pair<double, uint64_t>> timed;  // indexed by kernel id
+    struct Timed {
+        double total_ms = 0.0, min_ms = 0.0, max_ms = 0.0;
+        uint64_t launches = 0;
+    };
+    std::vector<Timed> timed;  // indexed by kernel id
 };
 
 namespace {
@@ -260,9 +264,12 @@ int resolve_spans(fa_ctx* ctx) {
     for (const auto& s : ctx->pending) {
         float ms = 0.0f;
         if (hipEventElapsedTime(&ms, s.begin, s.end) == hipSuccess && s.kernel_id >= 0) {
-            if ((size_t)s.kernel_id >= ctx->timed.size()) ctx->timed.resize(s.kernel_id + 1, {0.0, 0});
-            ctx->timed[s.kernel_id].first += ms;
-            ctx->timed[s.kernel_id].second += 1;
+            if ((size_t)s.kernel_id >= ctx->timed.size()) ctx->timed.resize(s.kernel_id + 1);
+            fa_ctx::Timed& t = ctx->timed[s.kernel_id];
+            t.min_ms = t.launches ? std::min(t.min_ms, (double)ms) : ms;
+            t.max_ms = t.launches ? std::max(t.max_ms, (double)ms) : ms;
+            t.total_ms += ms;
+            t.launches += 1;
         }
         ctx->free_events.push_back(s.begin);
         ctx->free_events.push_back(s.end);
@@ -512,8 +519,21 @@ int fa_ctx_kernel_timing(fa_ctx* ctx, int32_t kernel_id, double* total_ms, uint6
     *total_ms = 0.0;
     *launches = 0;
     if (kernel_id >= 0 && (size_t)kernel_id < ctx->timed.size()) {
-        *total_ms = ctx->timed[kernel_id].first;
-        *launches = ctx->timed[kernel_id].second;
+        *total_ms = ctx->timed[kernel_id].total_ms;
+        *launches = ctx->timed[kernel_id].launches;
+    }
+    return ok();
+}
+
+int fa_ctx_kernel_timing_range(fa_ctx* ctx, int32_t kernel_id, double* min_ms, double* max_ms) {
+    if (!ctx || !min_ms || !max_ms) return fail(FA_ERR_NULL_ARGUMENT, "null argument");
+    if (int rc = set_device(ctx)) return rc;
+    if (int rc = resolve_spans(ctx)) return rc;
+    *min_ms = 0.0;
+    *max_ms = 0.0;
+    if (kernel_id >= 0 && (size_t)kernel_id < ctx->timed.size()) {
+        *min_ms = ctx->timed[kernel_id].min_ms;
+        *max_ms = ctx->timed[kernel_id].max_ms;
     }
     return ok();
 }
@@ -1800,7 +1820,8 @@ int fa_paged_decode_launch(fa_ctx* ctx, const fa_decode_plan* p, const void* q, 
     end_span(ctx, FA_KERNEL_DECODE_COMBINE);
     HIP_TRY(hipGetLastError());
     const int kid = mfma ? FA_KERNEL_DECODE_PAGED_MFMA : FA_KERNEL_DECODE_PAGED_SPLITK;
-    record(ctx, kid, kernel_name(kid),
+    record(ctx, kid,
+           mfma && p->grouped ? "decode_mfma_grouped + decode_combine" : kernel_name(kid),
            (uint32_t)std::min<uint64_t>(16, p->q_heads / p->kv_heads), 16, grid, block,
            (uint32_t)dispatches, (uint32_t)((p->split_tokens)), nullptr);
     return ok();

@@ -266,6 +266,15 @@ class HipContext:
         check(lib().fa_ctx_kernel_timing(self.handle, kernel_id, ctypes.byref(ms), ctypes.byref(n)))
         return ms.value, n.value
 
+    def kernel_timing_range(self, kernel_id) -> tuple[float, float]:
+        """(shortest, longest) single dispatch in ms of one kernel since timing was enabled."""
+        if isinstance(kernel_id, str):
+            kernel_id = {v: k for k, v in L.KERNEL_IDS.items()}[kernel_id]
+        lo, hi = ctypes.c_double(), ctypes.c_double()
+        check(lib().fa_ctx_kernel_timing_range(self.handle, kernel_id, ctypes.byref(lo),
+                                               ctypes.byref(hi)))
+        return lo.value, hi.value
+
     def last_telemetry(self) -> RuntimeDispatchTelemetry:
         t = L.TelemetryC()
         check(lib().fa_last_telemetry(self.handle, ctypes.byref(t)))

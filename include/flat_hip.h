@@ -478,6 +478,9 @@ int fa_ctx_set_kernel_timing(fa_ctx* ctx, int32_t enable);
  * FA_KERNEL_DECODE_PAGED_SPLITK / _MFMA the split kernel and FA_KERNEL_DECODE_COMBINE the
  * combine) since timing was enabled. */
 int fa_ctx_kernel_timing(fa_ctx* ctx, int32_t kernel_id, double* total_ms, uint64_t* launches);
+/* Shortest and longest single timed dispatch (ms) of `kernel_id` since timing was enabled
+ * (0 when none ran); waits for the context's stream like fa_ctx_kernel_timing. */
+int fa_ctx_kernel_timing_range(fa_ctx* ctx, int32_t kernel_id, double* min_ms, double* max_ms);
 
 #ifdef __cplusplus
 }

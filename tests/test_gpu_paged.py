@@ -307,11 +307,13 @@ def test_batched_append_scatter_is_bit_exact(hip):
 
 
 def test_cfg5_chunked_prefill_over_paged_cache(hip):
-    """BASELINE configs[4] shape, reduced batch for the oracle: each sequence holds 2048 cached
-    tokens + a new 512-token chunk in a shuffled page pool; the chunk attends causally at
-    offset 2048 with Q RoPE at 2048 + i and pre-rotated K (rotate-on-append)."""
+    """BASELINE configs[4] at its stated size: 8 sequences, each holding 2048 cached tokens + a
+    new 512-token chunk in one shuffled page pool (page 16); the chunk attends causally at
+    offset 2048 with Q RoPE at 2048 + i and pre-rotated K (rotate-on-append). The oracle checks
+    the first and last head of the first and last sequence; V = 1 checks O = 1 on every row of
+    every sequence and head (same Q/K, so LSE must repeat bit for bit)."""
     rng = np.random.default_rng(8)
-    n_seqs, hq, hkv, D, ps, cached, ql, theta = 2, 32, 8, 128, 16, 2048, 512, 1e4
+    n_seqs, hq, hkv, D, ps, cached, ql, theta = 8, 32, 8, 128, 16, 2048, 512, 1e4
     kv_len = cached + ql
     pages_per = kv_len // ps
     total = n_seqs * pages_per
@@ -320,24 +322,31 @@ def test_cfg5_chunked_prefill_over_paged_cache(hip):
     raw_k = bf16_round(normal(n_seqs * kv_len * width, 1))
     v = bf16_round(normal(n_seqs * kv_len * width, 2))
     q = bf16_round(normal(n_seqs * ql * hq * D, 3))
-    kp = fa.DeviceBuffer(hip, total * ps * width * 2)
-    vp = fa.DeviceBuffer(hip, total * ps * width * 2)
-    fa.paged_append_batched(hip, bt, np.zeros(n_seqs, np.int32), kv_len, ps, total, hkv, D,
-                            fa.DeviceBuffer.from_array(hip, fa.host_storage(raw_k, fa.DTYPE_BF16)),
-                            fa.DeviceBuffer.from_array(hip, fa.host_storage(v, fa.DTYPE_BF16)),
-                            kp, vp, fa.RotaryEmbeddingConfig(theta, 0), fa.DTYPE_BF16)
     shape = fa.AsymmetricGroupedAttentionShape(n_seqs, hq, hkv, ql, kv_len, D, cached)
     plan = fa.PagedChunkedPrefillPlan(hip, bt, ps, total, shape, fa.FlatAttentionConfig(True),
                                       fa.AsymmetricRotaryEmbeddingConfig(theta, cached, 0),
                                       fa.DTYPE_BF16)
-    out = fa.DeviceBuffer(hip, plan.layout().combined_bytes)
-    plan.launch(fa.DeviceBuffer.from_array(hip, fa.host_storage(q, fa.DTYPE_BF16)), kp, vp, out)
-    res = fa.download_attention(out, plan.layout(), fa.DTYPE_BF16)
-    o = fa.storage_to_f32(res.output, fa.DTYPE_BF16)
+    qb = fa.DeviceBuffer.from_array(hip, fa.host_storage(q, fa.DTYPE_BF16))
+    kb = fa.DeviceBuffer.from_array(hip, fa.host_storage(raw_k, fa.DTYPE_BF16))
+
+    def run(v_host):
+        kp = fa.DeviceBuffer(hip, total * ps * width * 2)
+        vp = fa.DeviceBuffer(hip, total * ps * width * 2)
+        fa.paged_append_batched(hip, bt, np.zeros(n_seqs, np.int32), kv_len, ps, total, hkv, D,
+                                kb, fa.DeviceBuffer.from_array(hip, fa.host_storage(
+                                    v_host, fa.DTYPE_BF16)),
+                                kp, vp, fa.RotaryEmbeddingConfig(theta, 0), fa.DTYPE_BF16)
+        out = fa.DeviceBuffer(hip, plan.layout().combined_bytes)
+        plan.launch(qb, kp, vp, out)
+        res = fa.download_attention(out, plan.layout(), fa.DTYPE_BF16)
+        return fa.storage_to_f32(res.output, fa.DTYPE_BF16), res.lse
+
+    o, lse = run(v)
+    assert np.isfinite(o).all() and np.isfinite(lse).all()
     # oracle: RoPE materialised on Q (positions cached + i) and K (positions 0..kv_len-1) —
     # bit-exact to rotation inside the dot product (pinned in test_oracle.py) — then the
-    # asymmetric oracle without RoPE on two head units per sequence.
-    for s in range(n_seqs):
+    # asymmetric oracle without RoPE on two head units per checked sequence.
+    for s in (0, n_seqs - 1):
         sl_kv = slice(s * kv_len * width, (s + 1) * kv_len * width)
         qs = oracle.rope_rotate_rows(q[s * ql * hq * D:(s + 1) * ql * hq * D], ql, hq, D, theta,
                                      cached)
@@ -345,12 +354,15 @@ def test_cfg5_chunked_prefill_over_paged_cache(hip):
         for unit in (0, hq - 1):
             eo, el = oracle.forward_projection_asymmetric(
                 qs, ks, v[sl_kv], 1, hq, hkv, ql, kv_len, D, cached, True, None,
-                units=(unit, unit + 1))
+                units=(unit, unit + 1), threads=4)
             got = o[s * ql * hq * D:(s + 1) * ql * hq * D].reshape(ql, hq, D)[:, unit]
             exp = eo.reshape(ql, hq, D)[:, unit]
             assert_close(f"O seq {s} head {unit}", got, exp, H16_ATOL, 0.0)
-            gl = res.lse[(s * hq + unit) * ql:(s * hq + unit + 1) * ql]
+            gl = lse[(s * hq + unit) * ql:(s * hq + unit + 1) * ql]
             assert_close(f"LSE seq {s} head {unit}", gl, el[unit * ql:(unit + 1) * ql], H16_ATOL, 0.0)
+    o1, l1 = run(np.ones_like(v))
+    assert np.max(np.abs(o1 - 1.0)) <= 2e-2
+    assert np.array_equal(l1.view(np.uint32), lse.view(np.uint32))
 
 
 @pytest.mark.gpu
@@ -392,20 +404,23 @@ def test_kernel_timing_and_mfma_variant_telemetry(hip):
         assert t.kernel_id == "DecodePagedMfma" and t.dispatch_count == 2
         ms, n = hip.kernel_timing("DecodePagedMfma")
         assert n == 1 and ms > 0.0
+        assert hip.kernel_timing_range("DecodePagedMfma") == (ms, ms)  # one dispatch
         ms, n = hip.kernel_timing("DecodeCombine")
         assert n == 1 and ms > 0.0
         assert hip.kernel_timing("DecodePagedSplitK") == (0.0, 0)
         hip.set_kernel_timing(True)
         assert hip.kernel_timing("DecodePagedMfma") == (0.0, 0)
+        assert hip.kernel_timing_range("DecodePagedMfma") == (0.0, 0.0)
     finally:
         hip.set_kernel_timing(False)
 
 
 def _paged_prefill(hip, bt, ps, total, n_seqs, hq, hkv, D, cached, ql, theta, raw_k, v, q, dtype,
-                   causal):
+                   causal, pools=None):
     kv_len = cached + ql
     kp = fa.DeviceBuffer(hip, total * ps * hkv * D * 4)
     vp = fa.DeviceBuffer(hip, total * ps * hkv * D * 4)
+    kp.fill_u32(0x7FC00000)  # pool rows no table names hold NaN: a wrong gather shows
     fa.paged_append_batched(hip, bt, np.zeros(n_seqs, np.int32), kv_len, ps, total, hkv, D,
                             fa.DeviceBuffer.from_array(hip, fa.host_storage(raw_k, dtype)),
                             fa.DeviceBuffer.from_array(hip, fa.host_storage(v, dtype)),
@@ -416,6 +431,10 @@ def _paged_prefill(hip, bt, ps, total, n_seqs, hq, hkv, D, cached, ql, theta, ra
     out = fa.DeviceBuffer(hip, plan.layout().combined_bytes)
     plan.launch(fa.DeviceBuffer.from_array(hip, fa.host_storage(q, dtype)), kp, vp, out)
     res = fa.download_attention(out, plan.layout(), dtype)
+    if pools is not None:  # the pools as the device holds them (pre-rotated K), in f32
+        n = total * ps * hkv * D
+        sd = {fa.DTYPE_F32: np.float32, fa.DTYPE_BF16: np.uint16, fa.DTYPE_F16: np.uint16}[dtype]
+        pools.extend(fa.storage_to_f32(b.download(sd, n), dtype) for b in (kp, vp))
     return fa.storage_to_f32(res.output, dtype), res.lse
 
 
@@ -442,10 +461,17 @@ def test_paged_prefill_modes_match_oracle_and_gather_bit_exactly(hip, dtype, ps,
     shuf = rng.permutation(total)[:n_seqs * pages_per].astype(np.int32).reshape(n_seqs, pages_per)
     o1, l1 = _paged_prefill(hip, ident, ps, total, n_seqs, hq, hkv, D, cached, ql, theta, raw_k,
                             v, q, dtype, causal)
+    pools = []
     o2, l2 = _paged_prefill(hip, shuf, ps, total, n_seqs, hq, hkv, D, cached, ql, theta, raw_k,
-                            v, q, dtype, causal)
+                            v, q, dtype, causal, pools)
     assert np.array_equal(o1.view(np.uint32), o2.view(np.uint32))
     assert np.array_equal(l1.view(np.uint32), l2.view(np.uint32))
+    # the paged oracle over the device's own shuffled pool (pre-rotated K as appended): checks
+    # the gather and the Q rotation independently of the append's rounding of rotated K
+    po, pl = oracle.paged_prefill(q, pools[0], pools[1], total, ps, shuf, hq, hkv, ql, kv_len, D,
+                                  cached, causal, theta, cached, threads=2)
+    assert_close("O vs paged oracle", o2, po, atol, rtol)
+    assert_close("LSE vs paged oracle", l2, pl, atol, rtol)
     for s in range(n_seqs):
         sl_kv = slice(s * kv_len * width, (s + 1) * kv_len * width)
         qs = oracle.rope_rotate_rows(q[s * ql * hq * D:(s + 1) * ql * hq * D], ql, hq, D, theta,
@@ -458,14 +484,22 @@ def test_paged_prefill_modes_match_oracle_and_gather_bit_exactly(hip, dtype, ps,
 
 
 @pytest.mark.parametrize("pattern", ["rising", "falling", "alternating"])
-def test_adversarial_scores_bf16_decode(hip, pattern):
+@pytest.mark.parametrize("dtype", [fa.DTYPE_BF16, fa.DTYPE_F16])
+@pytest.mark.parametrize("layout", ["1", "0"])
+@pytest.mark.parametrize("split", [None, 256])
+def test_adversarial_scores_16bit_decode(hip, monkeypatch, pattern, dtype, layout, split):
     """Split-K decode with scores that rise over the whole context (every segment's maximum
     exceeds the previous ones, so the combine rescales every partial), fall (later segments'
-    probabilities underflow), or alternate between +-24."""
+    probabilities underflow), or alternate between +-24; in both 16-bit formats, both MFMA work
+    layouts (head-grouped workgroups and one-wave workgroups, FA_DECODE_GROUPED=0) and with the
+    automatic and an explicit split, so every kernel variant that carries the rotated query's
+    residual operand is covered."""
+    monkeypatch.setenv("FA_DECODE_GROUPED", layout)
+    rnd = bf16_round if dtype == fa.DTYPE_BF16 else f16_round
     ps, hq, hkv, D = 16, 4, 1, 128
     ctx_lens = [2000, 700]
     rng = np.random.default_rng(11)
-    bt, kp, vp, total = _make_pool(rng, ctx_lens, ps, hkv, D, bf16_round, seed=12)
+    bt, kp, vp, total = _make_pool(rng, ctx_lens, ps, hkv, D, rnd, seed=12)
     kp = kp.reshape(total * ps, hkv, D)
     kp[:] = 0.0
     for s, n in enumerate(ctx_lens):
@@ -474,12 +508,15 @@ def test_adversarial_scores_bf16_decode(hip, pattern):
               "alternating": np.where(np.arange(n) % 3 == 0, 24.0, -24.0)}[pattern]
         rows = bt[s, np.arange(n) // ps] * ps + np.arange(n) % ps
         kp[rows, :, 0] = (sc * np.sqrt(D))[:, None]
-    kp = bf16_round(kp.ravel())
+    kp = rnd(kp.ravel())
     q = np.zeros((len(ctx_lens), hq, D), np.float32)
     q[:, :, 0] = 1.0
     q = q.ravel()
-    o, l, _ = _decode(hip, bt, ctx_lens, kp, vp, total, ps, hq, hkv, D, q, fa.DTYPE_BF16,
-                      split=256)
+    o, l, plan = _decode(hip, bt, ctx_lens, kp, vp, total, ps, hq, hkv, D, q, dtype, split=split)
+    t = hip.last_telemetry()
+    assert t.kernel_id == "DecodePagedMfma"
+    # head-grouped workgroups run with the automatic split only
+    assert ("grouped" in t.kernel_name) == (layout == "1" and split is None), t.kernel_name
     eo, el = oracle.paged_decode(q, kp, vp, total, ps, bt, ctx_lens, hq, hkv, D, True, 1e4)
     assert np.isfinite(o).all() and np.isfinite(l).all()
     assert_close("O", o, eo, H16_ATOL, 0.0)

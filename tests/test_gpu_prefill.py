@@ -95,6 +95,27 @@ def test_gqa_rope_f16_group_shapes(hip, hq, hkv, S, causal):
     assert_close("LSE", l, el, H16_ATOL, 0.0)
 
 
+@pytest.mark.parametrize("dtype", [fa.DTYPE_F32, fa.DTYPE_BF16, fa.DTYPE_F16])
+@pytest.mark.parametrize("hq,hkv,S", [(8, 2, 97), (32, 8, 65), (6, 1, 130)])
+@pytest.mark.parametrize("causal", [False, True])
+def test_gqa_without_rope_matches_grouped_oracle(hip, dtype, hq, hkv, S, causal):
+    """forward_reference_grouped (src/grouped.rs:81-153): GQA with group > 1 and no RoPE
+    (rotary == NULL at the C ABI), ragged S, against oracle.forward_grouped."""
+    rnd = {fa.DTYPE_BF16: bf16_round, fa.DTYPE_F16: f16_round, fa.DTYPE_F32: lambda x: x}[dtype]
+    atol, rtol = (F32_ATOL, F32_RTOL) if dtype == fa.DTYPE_F32 else (H16_ATOL, 0.0)
+    B, D = 2, 128 if dtype != fa.DTYPE_F32 else 64
+    q = rnd(normal(B * hq * S * D, 500 + S))
+    k, v = rnd(normal(B * hkv * S * D, 501 + S)), rnd(normal(B * hkv * S * D, 502 + S))
+    shape = fa.GroupedAttentionShape(B, hq, hkv, S, D)
+    o, l = _run_grouped(hip, q, k, v, shape, fa.FlatAttentionConfig(causal), None, dtype)
+    eo, el = _oracle_grouped(q, k, v, shape, causal, None)
+    assert_close("O", o, eo, atol, rtol)
+    assert_close("LSE", l, el, atol, rtol)
+    t = hip.last_telemetry()
+    assert t.kernel_id.startswith("PrefillMfma") and "PreRotatedK" not in t.kernel_id
+    assert t.dispatch_count == 1  # no K rotation pass without RoPE
+
+
 @pytest.mark.parametrize("hq,hkv", [(4, 4), (8, 2), (6, 1), (32, 8)])
 @pytest.mark.parametrize("theta,offset", [(1e4, 0), (5e5, 37)])
 def test_gqa_rope_f32(hip, hq, hkv, theta, offset):
@@ -195,6 +216,13 @@ def test_cfg3_full_size_bf16_gqa_rope_causal(hip):
         assert_close(f"O unit {unit}", o[sl], eo[sl], H16_ATOL, 0.0)
         ls = slice(unit * S, (unit + 1) * S)
         assert_close(f"LSE unit {unit}", l[ls], el[ls], H16_ATOL, 0.0)
+    # size-independent property on every row of every unit: V = 1 gives O = 1 (the row's
+    # probabilities sum to the normaliser the kernel divides by)
+    ones = bf16_round(np.ones_like(v))
+    o1, l1 = _run_grouped(hip, q, k, ones, shape, fa.FlatAttentionConfig(True), rot,
+                          fa.DTYPE_BF16)
+    assert np.max(np.abs(o1 - 1.0)) <= 2e-2
+    assert np.array_equal(l1.view(np.uint32), l.view(np.uint32))
 
 
 @pytest.mark.parametrize("causal", [False, True])
@@ -331,3 +359,64 @@ def test_adversarial_scores_16bit(hip, dtype, rnd):
             assert np.isfinite(o).all() and np.isfinite(l).all(), name
             assert_close(f"O {name}", o, eo, H16_ATOL, 0.0)
             assert_close(f"LSE {name}", l, el, H16_ATOL, 0.0)
+
+
+def _rope64(x, pos, D, theta, sign):
+    """Rotate [rows, D] float64 rows by sign * pos * theta^(-2j/D) (interleaved pairs)."""
+    j = np.arange(D // 2)
+    freq = np.float32(theta) ** (-2.0 * j / D).astype(np.float32)
+    ang = sign * np.asarray(pos, np.float64)[:, None] * freq.astype(np.float64)[None, :]
+    c, s = np.cos(ang), np.sin(ang)
+    e, o = x[:, 0::2], x[:, 1::2]
+    y = np.empty_like(x)
+    y[:, 0::2] = e * c - o * s
+    y[:, 1::2] = e * s + o * c
+    return y
+
+
+def _rope_adversarial_inputs(pattern, S, D, theta, spread):
+    """Q/K whose *rotated* rows are aligned with one direction u, so the score of key t is
+    sc[t] for every query: pre-rotation rows are u (or sc[t]*sqrt(D)*u) rotated back by their
+    position. `spread` puts u on pair 0 only (lowest frequency: the rotation of the largest
+    component is rounded in full) or across every dim."""
+    u = np.zeros(D)
+    if spread:
+        u[:] = 1.0 / np.sqrt(D)
+    else:
+        u[0] = 1.0
+    idx = np.arange(S, dtype=np.float64)
+    sc = {"rising": 60.0 * idx / S, "falling": -60.0 * idx / S,
+          "alternating": np.where(np.arange(S) % 3 == 0, 24.0, -24.0)}[pattern]
+    pos = np.arange(S)
+    q = _rope64(np.tile(u, (S, 1)), pos, D, theta, -1.0)
+    k = _rope64(sc[:, None] * np.sqrt(D) * u[None, :], pos, D, theta, -1.0)
+    return q.astype(np.float32).ravel(), k.astype(np.float32).ravel()
+
+
+@pytest.mark.parametrize("pattern", ["rising", "falling", "alternating"])
+@pytest.mark.parametrize("spread", [False, True])
+def test_adversarial_scores_16bit_rope_prefill(hip, pattern, spread):
+    """RoPE (theta 1e4, positions 0..4095) with scores rising to 60, falling to -60, or
+    alternating +-24 over the whole context, through the 16-bit prefill in both K-rotation
+    modes, against the f32 oracle on the same bf16 inputs (tests/numerical_policy.rs:12-55
+    corpus, extended to RoPE). Bound: 2e-2 on O and LSE."""
+    S, D, theta = 4096, 128, 1e4
+    q, k = _rope_adversarial_inputs(pattern, S, D, theta, spread)
+    q, k = bf16_round(q), bf16_round(k)
+    v = bf16_round(normal(S * D, 77))
+    shape = fa.GroupedAttentionShape(1, 1, 1, S, D)
+    rot = fa.RotaryEmbeddingConfig(theta, 0)
+    # materialised RoPE + plain attention: bit-exact to the fused oracle (test_oracle.py)
+    qr = oracle.rope_rotate_rows(q, S, 1, D, theta, 0)
+    kr = oracle.rope_rotate_rows(k, S, 1, D, theta, 0)
+    eo, el = oracle.forward(qr, kr, v, 1, 1, S, D, True)
+    try:
+        for policy in (0, 1):
+            hip.set_prefill_policy(policy)
+            o, l = _run_grouped(hip, q, k, v, shape, fa.FlatAttentionConfig(True), rot,
+                                fa.DTYPE_BF16)
+            assert np.isfinite(o).all() and np.isfinite(l).all()
+            assert_close(f"O policy {policy}", o, eo, H16_ATOL, 0.0)
+            assert_close(f"LSE policy {policy}", l, el, H16_ATOL, 0.0)
+    finally:
+        hip.set_prefill_policy(-1)

@@ -422,3 +422,70 @@ def test_input_generator_is_standard_normal_and_seeded():
     x = normal(200000, 77)
     assert abs(float(x.mean())) < 0.01 and abs(float(x.std()) - 1) < 0.01
     assert np.array_equal(x, normal(200000, 77)) and not np.array_equal(x, normal(200000, 78))
+
+
+def _paged_prefill_case(seed, n, ps, kv_len, hq, hkv, D, shuffled):
+    """Pool of pages for n sequences of kv_len rows; identity or shuffled physical ids, plus two
+    spare pages that no table names (filled with sentinels that would show in any wrong gather)."""
+    rng = np.random.default_rng(seed)
+    width = hkv * D
+    pages = (kv_len + ps - 1) // ps
+    total = n * pages + 2
+    ids = rng.permutation(total) if shuffled else np.arange(total)
+    bt = ids[:n * pages].reshape(n, pages).astype(np.int32)
+    kc = normal(n * kv_len * width, 100 + seed)  # logical rows, contiguous per sequence
+    vc = normal(n * kv_len * width, 200 + seed)
+    kp = np.full(total * ps * width, 17.0, np.float32)
+    vp = np.full(total * ps * width, -19.0, np.float32)
+    for s in range(n):
+        for t in range(kv_len):
+            r = (bt[s, t // ps] * ps + t % ps) * width
+            kp[r:r + width] = kc[(s * kv_len + t) * width:(s * kv_len + t + 1) * width]
+            vp[r:r + width] = vc[(s * kv_len + t) * width:(s * kv_len + t + 1) * width]
+    return total, bt, kp, vp, kc, vc
+
+
+@pytest.mark.parametrize("ps,kv_len,qlen,qoff,causal", [
+    (4, 13, 5, 8, True), (16, 40, 8, 32, True), (5, 23, 23, 0, True), (3, 10, 4, 2, False)])
+def test_paged_prefill_is_gather_then_asymmetric_bit_exact(ps, kv_len, qlen, qoff, causal):
+    """ora_paged_prefill == (gather rows by block table -> forward_projection_asymmetric with
+    pre-rotated K) per sequence, bit for bit, and a shuffled table gives the same bits as the
+    identity table (src/chunked_projection_prefill.rs:194-259, src/paged_kv.rs:200-270)."""
+    n, hq, hkv, D, theta, qro = 3, 4, 2, 8, 1e4, qoff + 3
+    q = normal(n * qlen * hq * D, 7)
+    results = []
+    for shuffled in (False, True):
+        total, bt, kp, vp, kc, vc = _paged_prefill_case(1, n, ps, kv_len, hq, hkv, D, shuffled)
+        o, l = oracle.paged_prefill(q, kp, vp, total, ps, bt, hq, hkv, qlen, kv_len, D, qoff,
+                                    causal, theta, qro)
+        qw, kw = qlen * hq * D, kv_len * hkv * D
+        for s in range(n):
+            eo, el = oracle.forward_projection_asymmetric(
+                q[s * qw:(s + 1) * qw], kc[s * kw:(s + 1) * kw], vc[s * kw:(s + 1) * kw], 1, hq,
+                hkv, qlen, kv_len, D, qoff, causal, theta, qro, 0, False)
+            assert np.array_equal(o[s * qw:(s + 1) * qw], eo)
+            assert np.array_equal(l[s * hq * qlen:(s + 1) * hq * qlen], el)
+        results.append((o, l))
+    assert np.array_equal(results[0][0], results[1][0])
+    assert np.array_equal(results[0][1], results[1][1])
+    # Independent float64 check: rotate Q at q_rope_offset, attend over the logical rows.
+    o, l = results[1]
+    for s in range(n):
+        qs = q[s * qlen * hq * D:(s + 1) * qlen * hq * D]
+        qr = oracle.rope_rotate_rows(qs, qlen, hq, D, theta, qro)
+        eo, el = naive64(qr, kc[s * kv_len * hkv * D:(s + 1) * kv_len * hkv * D],
+                         vc[s * kv_len * hkv * D:(s + 1) * kv_len * hkv * D], 1, hq, hkv, None, D,
+                         causal, qpos_off=qoff, kv_len=kv_len, layout="proj", q_len=qlen)
+        assert_close("paged O", o[s * qlen * hq * D:(s + 1) * qlen * hq * D], eo, 2e-5, 1e-4)
+        assert_close("paged LSE", l[s * hq * qlen:(s + 1) * hq * qlen], el, 2e-5, 1e-4)
+
+
+def test_paged_prefill_rejects_bad_pages_and_short_tables():
+    x = np.zeros(4096, np.float32)
+    with pytest.raises(oracle.OracleError) as e:  # physical id 9 outside a 2-page pool
+        oracle.paged_prefill(x[:16], x, x, 2, 4, np.array([[0, 9]], np.int32), 1, 1, 2, 6, 8, 4,
+                             True, 1e4, 4)
+    assert e.value.code == 30
+    with pytest.raises(oracle.OracleError):  # 6 rows need 2 pages, the table holds 1
+        oracle.paged_prefill(x[:16], x, x, 2, 4, np.array([[0]], np.int32), 1, 1, 2, 6, 8, 4,
+                             True, 1e4, 4)
