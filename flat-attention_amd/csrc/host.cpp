@@ -158,6 +158,9 @@ struct fa_ctx {
     void* ws_delta = nullptr;
     size_t ws_delta_bytes = 0;
     int transpose_v_policy = -1;
+    // 16-bit RoPE prefill scores: 0 = rotated Q/K rounded to the storage type, 1 = split
+    // high/residual operands (fa_ctx_set_prefill_precision)
+    int prefill_precision = 0;
     // per-sequence metadata of variable-length prefill: device copy + pinned staging, reused
     // once the event recorded after the previous copy has completed
     int32_t* meta_dev = nullptr;
@@ -544,6 +547,14 @@ int fa_ctx_set_prefill_v_layout(fa_ctx* ctx, int32_t transpose_v) {
     return ok();
 }
 
+int fa_ctx_set_prefill_precision(fa_ctx* ctx, int32_t mode) {
+    if (!ctx) return fail(FA_ERR_NULL_ARGUMENT, "context is null");
+    if (mode != 0 && mode != 1)
+        return fail(FA_ERR_UNAVAILABLE, "prefill precision mode %d is not one of 0, 1", (int)mode);
+    ctx->prefill_precision = mode;
+    return ok();
+}
+
 int fa_ctx_set_prefill_policy(fa_ctx* ctx, int32_t prerotate_k) {
     if (!ctx) return fail(FA_ERR_NULL_ARGUMENT, "context is null");
     ctx->prerotate_policy = prerotate_k < 0 ? -1 : (prerotate_k ? 1 : 0);
@@ -668,6 +679,11 @@ int run_prefill(fa_ctx* ctx, PrefillJob& j) {
         if (int rc = ensure_rope(ctx, j.theta, (uint64_t)j.a.head_dim, j.max_pos, &table)) return rc;
         j.a.rope_table = table;
         prerot = j.a.rope_k && !j.paged && want_prerotate(ctx, (uint64_t)j.a.head_dim);
+        // precise scores: K rotated in the kernel, which keeps its 16-bit residual
+        if (ctx->prefill_precision == 1 && j.a.rope_k && !j.paged && j.dtype != FA_DTYPE_F32) {
+            prerot = false;
+            j.a.split_qk = 1;
+        }
     }
     uint32_t dispatches = 0;
     if (prerot) {
@@ -727,6 +743,8 @@ int run_prefill(fa_ctx* ctx, PrefillJob& j) {
                  vt ? "transpose_v + " : "", base, dt);
     else if (j.paged)
         snprintf(name, sizeof name, "%s<%s> (paged%s)", base, dt, j.rope ? ", K stored rotated" : "");
+    else if (j.a.split_qk)
+        snprintf(name, sizeof name, "%s<%s> (K rotated on load, split Q/K scores)", base, dt);
     else if (j.a.rope_k)
         snprintf(name, sizeof name, "%s<%s> (K rotated on load)", base, dt);
     else

@@ -45,6 +45,9 @@ struct PrefillArgs {
     // q_len, kv_len, causal_offset and q_rope_offset; padded query rows get O = 0, LSE = -inf.
     // nullptr: every batch element uses the padded extents.
     const int* var_meta;
+    // 16-bit contiguous K rotated on load only: carry the rotated Q and K as 16-bit high part +
+    // 16-bit residual and take three MFMAs per score block (f32-level scores).
+    int split_qk;
 };
 
 void launch_prefill(Dtype dt, bool paged, const PrefillArgs& a, hipStream_t s,

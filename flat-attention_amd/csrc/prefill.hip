@@ -174,8 +174,13 @@ __host__ __device__ constexpr bool prefill_pingpong_enabled() {
 // NW = 4: four waves, 128 query rows per workgroup, two workgroups per CU.
 // NW = 8: eight waves (two groups of four, 256 rows), one workgroup per CU, ping-pong schedule
 // (contiguous DMA path only): while one group runs its MFMAs the other runs its softmax.
-template <typename T, int DPAD, int PMODE, bool ROPEK, bool FULLD, int NW>
+// SPLIT (precise scores, with ROPEK only): the rotated Q and K are carried as a 16-bit high part
+// plus the 16-bit rounding of their residual, and S = Khi.Qhi + Khi.Qlo + Klo.Qhi (the lo.lo
+// term is below f32 rounding of the sum), so scores keep f32-level accuracy where a once-rounded
+// rotation would move a score of magnitude s by up to s * 2^-8.
+template <typename T, int DPAD, int PMODE, bool ROPEK, bool FULLD, int NW, bool SPLIT = false>
 __global__ __launch_bounds__(64 * NW, 2) void prefill_mfma16(PrefillKArgs ka) {
+    static_assert(!SPLIT || (ROPEK && NW == 4), "split scores need the in-kernel K rotation");
     constexpr bool PIPE = FA_PREFILL_PIPE != 0;
     using H = Half<T>;
     const PrefillArgs& a = ka.a;
@@ -195,7 +200,9 @@ __global__ __launch_bounds__(64 * NW, 2) void prefill_mfma16(PrefillKArgs ka) {
     constexpr int VBYTES = VT ? (DPAD * VTROWB + 1023) / 1024 * 1024 : BN * VROWB;
     // One K/V stage, or two (double buffering: tile j+1 is staged while tile j is computed).
     constexpr bool DB = FA_PREFILL_DB != 0 && !PIPE;
-    constexpr int STAGE = BN * KROWB + VBYTES;
+    // (SPLIT: the K residual tile follows V in every stage)
+    constexpr int KLO = BN * KROWB + VBYTES;
+    constexpr int STAGE = KLO + (SPLIT ? BN * KROWB : 0);
     // Contiguous K/V go straight from memory into LDS (buffer_load ... lds): no staging
     // registers and no LDS store instructions. One instruction fills 64 consecutive 16-byte
     // slots; padded rows are kept by giving pad slots an out-of-range (zero-filling, no
@@ -268,6 +275,7 @@ __global__ __launch_bounds__(64 * NW, 2) void prefill_mfma16(PrefillKArgs ka) {
 
     // ---- Q^T operand, rotated in registers: lane holds Q[row][16ks + 8g .. +8].
     u32x4_t qop[KS];
+    u32x4_t qlo[SPLIT ? KS : 1];
     {
         const uint16_t* qrow = (const uint16_t*)a.q + (int64_t)b * a.q_sb + (int64_t)hq * a.q_sh +
                                (int64_t)t * a.q_ss;
@@ -291,6 +299,13 @@ __global__ __launch_bounds__(64 * NW, 2) void prefill_mfma16(PrefillKArgs ka) {
                 rope4(x, cs);
 #pragma unroll
                 for (int j = 0; j < 4; ++j) raw[j] = H::pack(x[2 * j], x[2 * j + 1]);
+                if constexpr (SPLIT) {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        qlo[ks][j] = H::pack(x[2 * j] - H::lo(raw[j]), x[2 * j + 1] - H::hi(raw[j]));
+                }
+            } else if constexpr (SPLIT) {
+                qlo[ks] = u32x4_t{0u, 0u, 0u, 0u};
             }
             qop[ks] = raw;
         }
@@ -394,6 +409,15 @@ __global__ __launch_bounds__(64 * NW, 2) void prefill_mfma16(PrefillKArgs ka) {
                 rope4(x, cs);
 #pragma unroll
                 for (int j = 0; j < 4; ++j) val[j] = H::pack(x[2 * j], x[2 * j + 1]);
+                if constexpr (SPLIT) {
+                    u32x4_t lo;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        lo[j] = H::pack(x[2 * j] - H::lo(val[j]), x[2 * j + 1] - H::hi(val[j]));
+                    *(u32x4_t*)(smem + st_w + KLO + kl * KROWB + k_dc * 16) = lo;
+                }
+            } else if constexpr (SPLIT) {
+                *(u32x4_t*)(smem + st_w + KLO + kl * KROWB + k_dc * 16) = u32x4_t{0u, 0u, 0u, 0u};
             }
             *(u32x4_t*)(smem + st_w + kl * KROWB + k_dc * 16) = val;
         }
@@ -481,6 +505,20 @@ __global__ __launch_bounds__(64 * NW, 2) void prefill_mfma16(PrefillKArgs ka) {
         }
     };
     auto compute_s = [&](f32x16_t (&sacc)[2], auto own_order, auto&& hook) {
+        if constexpr (SPLIT) {
+            sacc[0] = (f32x16_t)0.0f;
+            sacc[1] = (f32x16_t)0.0f;
+#pragma unroll
+            for (int i = 0; i < 2 * KS; ++i) {
+                const u32x4_t khi = kread(i);
+                const u32x4_t klo = *(const u32x4_t*)(smem + st_k + KLO + k_rd0 +
+                                                      (i & 1) * 32 * KROWB + (i >> 1) * 32);
+                sacc[i & 1] = H::mfma32(klo, qop[i >> 1], sacc[i & 1]);
+                sacc[i & 1] = H::mfma32(khi, qlo[i >> 1], sacc[i & 1]);
+                sacc[i & 1] = H::mfma32(khi, qop[i >> 1], sacc[i & 1]);
+            }
+            return;
+        }
         u32x4_t ring[KR];
         s_ring_start(ring);
         compute_s_pre(sacc, ring, own_order, hook, false);
@@ -1192,7 +1230,7 @@ __global__ __launch_bounds__(256, 1) void prefill_mfma_f32(PrefillKArgs ka) {
 }
 
 // ------------------------------------------------------------------ launcher
-template <typename T, int PMODE, bool ROPEK>
+template <typename T, int PMODE, bool ROPEK, bool SPLIT = false>
 static void launch16r(const PrefillKArgs& ka, int dpad, dim3 grid, hipStream_t s) {
     // contiguous K/V, K not rotated in the kernel: the 8-wave ping-pong kernel (when enabled)
     constexpr int NW =
@@ -1200,16 +1238,16 @@ static void launch16r(const PrefillKArgs& ka, int dpad, dim3 grid, hipStream_t s
     const bool full = ka.a.head_dim == dpad;
     switch (dpad) {
         case 32:
-            full ? prefill_mfma16<T, 32, PMODE, ROPEK, true, NW><<<grid, 64 * NW, 0, s>>>(ka)
-                 : prefill_mfma16<T, 32, PMODE, ROPEK, false, NW><<<grid, 64 * NW, 0, s>>>(ka);
+            full ? prefill_mfma16<T, 32, PMODE, ROPEK, true, NW, SPLIT><<<grid, 64 * NW, 0, s>>>(ka)
+                 : prefill_mfma16<T, 32, PMODE, ROPEK, false, NW, SPLIT><<<grid, 64 * NW, 0, s>>>(ka);
             break;
         case 64:
-            full ? prefill_mfma16<T, 64, PMODE, ROPEK, true, NW><<<grid, 64 * NW, 0, s>>>(ka)
-                 : prefill_mfma16<T, 64, PMODE, ROPEK, false, NW><<<grid, 64 * NW, 0, s>>>(ka);
+            full ? prefill_mfma16<T, 64, PMODE, ROPEK, true, NW, SPLIT><<<grid, 64 * NW, 0, s>>>(ka)
+                 : prefill_mfma16<T, 64, PMODE, ROPEK, false, NW, SPLIT><<<grid, 64 * NW, 0, s>>>(ka);
             break;
         default:
-            full ? prefill_mfma16<T, 128, PMODE, ROPEK, true, NW><<<grid, 64 * NW, 0, s>>>(ka)
-                 : prefill_mfma16<T, 128, PMODE, ROPEK, false, NW><<<grid, 64 * NW, 0, s>>>(ka);
+            full ? prefill_mfma16<T, 128, PMODE, ROPEK, true, NW, SPLIT><<<grid, 64 * NW, 0, s>>>(ka)
+                 : prefill_mfma16<T, 128, PMODE, ROPEK, false, NW, SPLIT><<<grid, 64 * NW, 0, s>>>(ka);
             break;
     }
 }
@@ -1220,6 +1258,8 @@ static void launch16(const PrefillKArgs& ka, bool paged, int dpad, dim3 grid, hi
         if (ka.a.vt) {
             if (ka.a.rope_k) launch16r<T, kContigVT, true>(ka, dpad, grid, s);
             else launch16r<T, kContigVT, false>(ka, dpad, grid, s);
+        } else if (ka.a.rope_k && ka.a.split_qk) {
+            launch16r<T, kContig, true, true>(ka, dpad, grid, s);
         } else if (ka.a.rope_k) {
             launch16r<T, kContig, true>(ka, dpad, grid, s);
         } else {

@@ -249,6 +249,11 @@ class HipContext:
     def set_prefill_policy(self, prerotate_k: int):
         check(lib().fa_ctx_set_prefill_policy(self.handle, prerotate_k))
 
+    def set_prefill_precision(self, mode: int):
+        """0: rotated Q/K rounded to the 16-bit storage type before Q.K^T (default, fastest);
+        1: split high/residual operands, f32-level scores for the 16-bit RoPE prefill."""
+        check(lib().fa_ctx_set_prefill_precision(self.handle, mode))
+
     def set_prefill_v_layout(self, transpose_v: int):
         """-1 automatic, 0 stream V rows, 1 stream a transposed V copy (16-bit prefill)."""
         check(lib().fa_ctx_set_prefill_v_layout(self.handle, transpose_v))

@@ -460,6 +460,15 @@ int fa_last_telemetry(fa_ctx* ctx, fa_telemetry* out);
  * prerotate_k: 0 = rotate K tiles on load inside the prefill kernel, 1 = rotate K once in a
  * pre-pass, -1 = automatic (default). */
 int fa_ctx_set_prefill_policy(fa_ctx* ctx, int32_t prerotate_k);
+/* Score precision of the 16-bit RoPE prefill (the NumericalMode choice of src/numerical.rs:18,
+ * applied to this backend). 0 (default): the rotated Q and K are rounded to the storage type
+ * before Q.K^T, so a score s carries a relative error up to about 2^-8 (bf16) -- within the
+ * 2e-2 bar for unit-scale inputs, not for scores of tens. 1: the rotated Q and K keep their
+ * 16-bit residuals and each score block takes three MFMAs (f32-level scores; K is then rotated
+ * in the kernel, about half the throughput). Applies to contiguous K that the call rotates;
+ * K that is stored rotated (paged cache, pre-rotated asymmetric input) is used as stored.
+ * Other values: FA_ERR_UNAVAILABLE. */
+int fa_ctx_set_prefill_precision(fa_ctx* ctx, int32_t mode);
 /* V layout policy of the 16-bit contiguous prefill (same role as the K policy above): 1 = copy
  * V once into a transposed workspace [batch, kv_heads, head_dim, kv_len rounded up to 64] and
  * stream V^T tiles, 0 = stream V rows and transpose in the kernel, -1 = automatic (currently

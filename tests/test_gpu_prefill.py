@@ -397,9 +397,12 @@ def _rope_adversarial_inputs(pattern, S, D, theta, spread):
 @pytest.mark.parametrize("spread", [False, True])
 def test_adversarial_scores_16bit_rope_prefill(hip, pattern, spread):
     """RoPE (theta 1e4, positions 0..4095) with scores rising to 60, falling to -60, or
-    alternating +-24 over the whole context, through the 16-bit prefill in both K-rotation
-    modes, against the f32 oracle on the same bf16 inputs (tests/numerical_policy.rs:12-55
-    corpus, extended to RoPE). Bound: 2e-2 on O and LSE."""
+    alternating +-24 over the whole context, through the 16-bit prefill, against the f32 oracle
+    on the same bf16 inputs (tests/numerical_policy.rs:12-55 corpus, extended to RoPE).
+    Precise scores (fa_ctx_set_prefill_precision(1): rotated Q and K carried as high part +
+    residual) hold the 2e-2 bar on O and LSE. The default mode rounds the rotated Q and K to
+    bf16 once: its score error is bounded by |s| * 2^-7 (two roundings of 2^-9 relative each,
+    plus the products' rounding), which bounds the LSE error by max|s| * 2^-7."""
     S, D, theta = 4096, 128, 1e4
     q, k = _rope_adversarial_inputs(pattern, S, D, theta, spread)
     q, k = bf16_round(q), bf16_round(k)
@@ -410,13 +413,46 @@ def test_adversarial_scores_16bit_rope_prefill(hip, pattern, spread):
     qr = oracle.rope_rotate_rows(q, S, 1, D, theta, 0)
     kr = oracle.rope_rotate_rows(k, S, 1, D, theta, 0)
     eo, el = oracle.forward(qr, kr, v, 1, 1, S, D, True)
+    smax = float(np.max(np.abs(np.asarray(qr).reshape(S, D) @ np.asarray(kr).reshape(S, D).T
+                               / np.sqrt(D))))
     try:
+        hip.set_prefill_precision(1)
+        o, l = _run_grouped(hip, q, k, v, shape, fa.FlatAttentionConfig(True), rot,
+                            fa.DTYPE_BF16)
+        assert "split" in hip.last_telemetry().kernel_name
+        assert_close("O precise", o, eo, H16_ATOL, 0.0)
+        assert_close("LSE precise", l, el, H16_ATOL, 0.0)
+        hip.set_prefill_precision(0)
         for policy in (0, 1):
             hip.set_prefill_policy(policy)
             o, l = _run_grouped(hip, q, k, v, shape, fa.FlatAttentionConfig(True), rot,
                                 fa.DTYPE_BF16)
             assert np.isfinite(o).all() and np.isfinite(l).all()
-            assert_close(f"O policy {policy}", o, eo, H16_ATOL, 0.0)
-            assert_close(f"LSE policy {policy}", l, el, H16_ATOL, 0.0)
+            assert_close(f"LSE default policy {policy}", l, el, smax * 2.0 ** -7, 0.0)
     finally:
+        hip.set_prefill_precision(0)
         hip.set_prefill_policy(-1)
+
+
+@pytest.mark.parametrize("dtype,rnd", [(fa.DTYPE_BF16, bf16_round), (fa.DTYPE_F16, f16_round)])
+@pytest.mark.parametrize("hq,hkv,S,D", [(8, 2, 200, 128), (6, 1, 77, 64), (4, 4, 130, 32),
+                                        (8, 2, 150, 120)])
+@pytest.mark.parametrize("causal", [False, True])
+def test_precise_rope_prefill_matches_oracle(hip, dtype, rnd, hq, hkv, S, D, causal):
+    """The split-score kernel (precision mode 1) at edge shapes: ragged key tiles, GQA groups,
+    head dims below the padded width, both 16-bit formats, a RoPE offset."""
+    B = 2
+    q = rnd(normal(B * hq * S * D, 600 + S + D))
+    k, v = rnd(normal(B * hkv * S * D, 601 + S)), rnd(normal(B * hkv * S * D, 602 + S))
+    shape = fa.GroupedAttentionShape(B, hq, hkv, S, D)
+    rot = fa.RotaryEmbeddingConfig(1e4, 9)
+    try:
+        hip.set_prefill_precision(1)
+        o, l = _run_grouped(hip, q, k, v, shape, fa.FlatAttentionConfig(causal), rot, dtype)
+        t = hip.last_telemetry()
+        assert "split" in t.kernel_name and t.dispatch_count == 1
+    finally:
+        hip.set_prefill_precision(0)
+    eo, el = _oracle_grouped(q, k, v, shape, causal, rot)
+    assert_close("O", o, eo, H16_ATOL, 0.0)
+    assert_close("LSE", l, el, H16_ATOL, 0.0)
