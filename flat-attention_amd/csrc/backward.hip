@@ -160,14 +160,7 @@ constexpr int kBwdQueries = 128;  // queries per bwd_dq workgroup (32 per wave)
 constexpr int kBwdTile = 64;      // rows per staged tile (Q/dO in bwd_dkdv, K/V in bwd_dq)
 constexpr uint32_t kOob = 0x7fff0000u;  // transfer offset past every buffer: writes zeros
 
-#ifndef FA_BWD_SGS
-#define FA_BWD_SGS 1
-#endif
-#if FA_BWD_SGS
 #define FA_BWD_SG(mask, n) __builtin_amdgcn_sched_group_barrier(mask, n, 0)
-#else
-#define FA_BWD_SG(mask, n) ((void)0)
-#endif
 
 // LDS geometry of a tile of ROWS rows and DPAD columns, in rows of SL 16-byte slots; a tile is
 // a whole number of KiB, so a transfer instruction (64 slots) fills one KiB of it.

@@ -384,9 +384,6 @@ __device__ __forceinline__ f32x4_t mfma16x16x16(s16x4_t a, s16x4_t b, f32x4_t c)
 }
 
 // Register ring depth of the MFMA split kernel (16-key steps in flight per wave).
-#ifndef FA_DECODE_NS
-#define FA_DECODE_NS 2
-#endif
 
 // Orders this wave's LDS accesses around a reuse of its private tile. LDS operations of one
 // wave execute in issue order, so only the compiler has to be kept from moving them.
@@ -405,7 +402,7 @@ __device__ __forceinline__ void decode_mfma_item(const DecodeKArgs& ka, int s, i
     constexpr int NQ = DPAD / 32;        // 16x16x32 k-steps for S
     constexpr int NMB = DPAD / 16;       // 16-dim blocks of O^T
     constexpr int VROWB = DPAD * 2 + 32; // padded V row in LDS (bytes)
-    constexpr int NS = FA_DECODE_NS;     // register ring depth (steps of 16 keys)
+    constexpr int NS = 2;                // register ring depth (steps of 16 keys)
     const DecodeArgs& a = ka.a;
     const int lane = threadIdx.x & 63;
     const int n = lane & 15, g4 = lane >> 4;
@@ -606,20 +603,8 @@ __device__ __forceinline__ void decode_mfma_item(const DecodeKArgs& ka, int s, i
     }
 }
 
-// Minimum resident waves per SIMD the MFMA split kernel is compiled for (caps its registers);
-// 0 leaves the choice to the compiler.
-#ifndef FA_DECODE_WPE
-#define FA_DECODE_WPE 0
-#endif
-#if FA_DECODE_WPE > 0
-#define FA_DECODE_ATTR __attribute__((amdgpu_waves_per_eu(FA_DECODE_WPE, 8)))
-#else
-#define FA_DECODE_ATTR
-#endif
-
 template <typename T, int DPAD, int GT>
-__global__ __launch_bounds__(64) FA_DECODE_ATTR void decode_mfma(DecodeKArgs ka, int n_items,
-                                                                int chunks) {
+__global__ __launch_bounds__(64) void decode_mfma(DecodeKArgs ka, int n_items, int chunks) {
     __shared__ __attribute__((aligned(16))) uint8_t v_lds[16 * (DPAD * 2 + 32)];
     (void)n_items;
     for (int j = ka.a.wave_off[blockIdx.x]; j < ka.a.wave_off[blockIdx.x + 1]; ++j) {

@@ -161,6 +161,9 @@ struct fa_ctx {
     // 16-bit RoPE prefill scores: 0 = rotated Q/K rounded to the storage type, 1 = split
     // high/residual operands (fa_ctx_set_prefill_precision)
     int prefill_precision = 0;
+    // decode work layout: -1 automatic (head-grouped workgroups where they apply), 0 one-wave
+    // workgroups (fa_ctx_set_decode_policy; read when a decode plan is prepared)
+    int decode_grouped_policy = -1;
     // per-sequence metadata of variable-length prefill: device copy + pinned staging, reused
     // once the event recorded after the previous copy has completed
     int32_t* meta_dev = nullptr;
@@ -544,6 +547,12 @@ int fa_ctx_kernel_timing_range(fa_ctx* ctx, int32_t kernel_id, double* min_ms, d
 int fa_ctx_set_prefill_v_layout(fa_ctx* ctx, int32_t transpose_v) {
     if (!ctx) return fail(FA_ERR_NULL_ARGUMENT, "context is null");
     ctx->transpose_v_policy = transpose_v < 0 ? -1 : (transpose_v ? 1 : 0);
+    return ok();
+}
+
+int fa_ctx_set_decode_policy(fa_ctx* ctx, int32_t grouped) {
+    if (!ctx) return fail(FA_ERR_NULL_ARGUMENT, "context is null");
+    ctx->decode_grouped_policy = grouped < 0 ? -1 : (grouped ? 1 : 0);
     return ok();
 }
 
@@ -1476,8 +1485,7 @@ int build_work(fa_decode_plan* p) {
     const uint64_t maxseg = max_split_tokens(p->page_size);
     // Head-grouped mode (16-bit KV, page_size % 16 == 0, automatic split, <= 8 units): one
     // workgroup of `units` waves per segment list, every wave on the same key ranges.
-    const char* env_grouped = std::getenv("FA_DECODE_GROUPED");
-    const bool want_grouped = !(env_grouped && env_grouped[0] == '0');
+    const bool want_grouped = ctx->decode_grouped_policy != 0;
     p->grouped = (want_grouped && p->split_req == 0 && p->dtype != (int)Dtype::F32 &&
                   p->page_size % 16 == 0 && units <= 8)
                      ? (int)units

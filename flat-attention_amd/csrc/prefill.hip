@@ -71,9 +71,6 @@ __device__ __forceinline__ void write_padded_row(const PrefillArgs& a, int b, in
     if (g == 0) a.lse[(int64_t)b * a.lse_sb + (int64_t)hq * a.lse_sh + t] = -INFINITY;
 }
 
-#ifndef FA_PREFILL_LPT
-#define FA_PREFILL_LPT 1
-#endif
 // Query block of this workgroup: (batch * kv_heads + kv head, query block index). The blocks
 // an XCD runs form a contiguous chunk of xcd_remap's order; when that chunk is a whole number of
 // (batch, kv head) units it is dispatched heaviest first across its units (query blocks in
@@ -81,7 +78,7 @@ __device__ __forceinline__ void write_padded_row(const PrefillArgs& a, int b, in
 __device__ __forceinline__ void block_coords(int bid, int nb, int nqb, int& bh, int& qb) {
     const int logical = xcd_remap(bid, nb);
     const int per_xcd = nb / 8;
-    if (FA_PREFILL_LPT != 0 && nb % 8 == 0 && per_xcd % nqb == 0) {
+    if (nb % 8 == 0 && per_xcd % nqb == 0) {
         const int units = per_xcd / nqb;
         const int x = logical / per_xcd, l = logical % per_xcd;
         bh = x * units + l % units;
@@ -125,41 +122,12 @@ __device__ __forceinline__ int64_t paged_row(const PrefillKArgs& ka, int b, int 
 //     ds_read_b64_tr_b16, which hands each lane 4 keys of one dim (the 16-lane group transposes
 //     the 4x4 blocks it addresses), so V needs no transposition when it is staged.
 // Every per-step LDS address is a per-lane base plus a compile-time immediate.
-#ifndef FA_PREFILL_PIPE
-#define FA_PREFILL_PIPE 0
-#endif
-#ifndef FA_PREFILL_DB
-#define FA_PREFILL_DB 1
-#endif
-#ifndef FA_PREFILL_DMA
-#define FA_PREFILL_DMA 1
-#endif
-// 8-wave ping-pong workgroups for the contiguous DMA path: two groups of four waves kept in
-// opposite phases (one group's MFMAs against the other's softmax). 3 % ahead of the 4-wave
-// kernel once the output left with streaming stores and the decode stopped flushing the caches.
-#ifndef FA_PREFILL_PP
-#define FA_PREFILL_PP 1
-#endif
-__host__ __device__ constexpr bool prefill_pingpong_enabled() {
-    return FA_PREFILL_PP != 0 && FA_PREFILL_DMA != 0 && FA_PREFILL_DB != 0 && FA_PREFILL_PIPE == 0;
+// The 8-wave ping-pong kernel (contiguous K/V moved by buffer->LDS transfers, K not rotated in
+// the kernel): two groups of four waves kept in opposite phases, one group's MFMAs against the
+// other group's softmax.
+__host__ __device__ constexpr bool prefill_pingpong(int pmode, bool ropek) {
+    return (pmode == kContig || pmode == kContigVT) && !ropek;
 }
-#ifndef FA_PP_DMA
-#define FA_PP_DMA 0
-#endif
-#ifndef FA_PREFILL_KRING
-#define FA_PREFILL_KRING 4
-#endif
-// Ping-pong MFMA phase: read the first K operands of S(j) before the P.V(j-1) MFMAs, so the
-// S chain starts without an LDS round trip (3 % faster at cfg3; 0 = read them after P.V)
-#ifndef FA_PP_SPRE
-#define FA_PP_SPRE 1
-#endif
-#ifndef FA_PREFILL_VRING
-#define FA_PREFILL_VRING 3
-#endif
-#ifndef FA_PREFILL_SGS
-#define FA_PREFILL_SGS 1
-#endif
 
 // Scheduling groups (LLVM AMDGPU sched_group_barrier masks: 0x2 VALU, 0x8 MFMA, 0x100 DS read, 0x400 transcendental).
 #define FA_SG(mask, n) __builtin_amdgcn_sched_group_barrier(mask, n, 0)
@@ -179,9 +147,8 @@ __host__ __device__ constexpr bool prefill_pingpong_enabled() {
 // term is below f32 rounding of the sum), so scores keep f32-level accuracy where a once-rounded
 // rotation would move a score of magnitude s by up to s * 2^-8.
 template <typename T, int DPAD, int PMODE, bool ROPEK, bool FULLD, int NW, bool SPLIT = false>
-__global__ __launch_bounds__(64 * NW, 2) void prefill_mfma16(PrefillKArgs ka) {
+__global__ __launch_bounds__(64 * NW, SPLIT ? 1 : 2) void prefill_mfma16(PrefillKArgs ka) {
     static_assert(!SPLIT || (ROPEK && NW == 4), "split scores need the in-kernel K rotation");
-    constexpr bool PIPE = FA_PREFILL_PIPE != 0;
     using H = Half<T>;
     const PrefillArgs& a = ka.a;
     constexpr int BM = 32 * NW, BN = 64;
@@ -199,7 +166,6 @@ __global__ __launch_bounds__(64 * NW, 2) void prefill_mfma16(PrefillKArgs ka) {
     // (V^T region rounded to whole KiB: each transfer instruction fills 1 KiB)
     constexpr int VBYTES = VT ? (DPAD * VTROWB + 1023) / 1024 * 1024 : BN * VROWB;
     // One K/V stage, or two (double buffering: tile j+1 is staged while tile j is computed).
-    constexpr bool DB = FA_PREFILL_DB != 0 && !PIPE;
     // (SPLIT: the K residual tile follows V in every stage)
     constexpr int KLO = BN * KROWB + VBYTES;
     constexpr int STAGE = KLO + (SPLIT ? BN * KROWB : 0);
@@ -207,18 +173,18 @@ __global__ __launch_bounds__(64 * NW, 2) void prefill_mfma16(PrefillKArgs ka) {
     // registers and no LDS store instructions. One instruction fills 64 consecutive 16-byte
     // slots; padded rows are kept by giving pad slots an out-of-range (zero-filling, no
     // memory traffic) offset. Instructions beyond a tile's slot count target a dummy KiB.
-    constexpr bool DMA = FA_PREFILL_DMA != 0 && DB && CONTIG && !ROPEK;
+    constexpr bool DMA = CONTIG && !ROPEK;
     // 16-byte slots per padded row: K, V, V^T (64 keys of one dim)
     constexpr int KSL = KROWB / 16, VSL = VROWB / 16, VTSL = VTROWB / 16;
     // transfer instructions per tile (64 slots each)
     constexpr int KINS = KSL, VINS = VT ? (DPAD * VTSL + 63) / 64 : VSL;
     // Waves sharing the transfers: all of them, or group 1 alone under the ping-pong schedule.
-    constexpr int NWD = PP ? (FA_PP_DMA == 2 ? 8 : 4) : NW;
+    constexpr int NWD = PP ? 4 : NW;
     constexpr int KI = (KINS + NWD - 1) / NWD, VI = (VINS + NWD - 1) / NWD;  // per wave
     constexpr int DUMMY = 2 * STAGE;
     // LDS: the K/V stages (+ the dummy KiB of the transfers), reused at the end to stage the
     // output rows (NW waves x 32 rows of DPAD * 2 + 16 bytes)
-    constexpr int SMEM_KV = (DB ? 2 : 1) * STAGE + (DMA ? 1024 : 0);
+    constexpr int SMEM_KV = 2 * STAGE + (DMA ? 1024 : 0);
     constexpr int SMEM_O = NW * 32 * (DPAD * 2 + 16);
     __shared__ __attribute__((aligned(16))) uint8_t smem[SMEM_KV > SMEM_O ? SMEM_KV : SMEM_O];
     int st_r = 0, st_w = 0;  // byte offsets of the stage being read / written
@@ -470,7 +436,7 @@ __global__ __launch_bounds__(64 * NW, 2) void prefill_mfma16(PrefillKArgs ka) {
     // the K operands of the next KR steps are already being read (a KR-deep register ring).
     // hook(i) runs after MFMA i (the ping-pong kernel issues its K/V transfers there).
     auto no_hook = [](int) {};
-    constexpr int KR = FA_PREFILL_KRING;
+    constexpr int KR = 4;
     auto kread = [&](int i) {
         return *(const u32x4_t*)(smem + st_k + k_rd0 + (i & 1) * 32 * KROWB + (i >> 1) * 32);
     };
@@ -492,7 +458,7 @@ __global__ __launch_bounds__(64 * NW, 2) void prefill_mfma16(PrefillKArgs ka) {
             sacc[i & 1] = H::mfma32(av, qop[i >> 1], sacc[i & 1]);
             hook(i);
         }
-        if constexpr (FA_PREFILL_SGS != 0 && decltype(own_order)::value) {
+        if constexpr (decltype(own_order)::value) {
             // Keep the issue order: KR reads, then (MFMA, read) pairs, then the last MFMAs, so
             // each MFMA's operand was requested KR steps earlier.
             if (!pre) FA_SG(0x100, KR);
@@ -607,7 +573,7 @@ __global__ __launch_bounds__(64 * NW, 2) void prefill_mfma16(PrefillKArgs ka) {
         // per step, a register ring).
         typedef short v4i16_t __attribute__((ext_vector_type(4)));
         typedef __attribute__((address_space(3))) v4i16_t lds_v4i16_t;
-        constexpr int NSTEP = 4 * MB, RV = FA_PREFILL_VRING;
+        constexpr int NSTEP = 4 * MB, RV = 3;
         auto vread = [&](int i) {
             const uint8_t* src = smem + st_v + v_rd + (i / MB) * 16 * VROWB + (i % MB) * 64;
             const v4i16_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)src);
@@ -627,7 +593,7 @@ __global__ __launch_bounds__(64 * NW, 2) void prefill_mfma16(PrefillKArgs ka) {
             oacc[i % MB] = H::mfma32(av, pop[i / MB], oacc[i % MB]);
             hook(i);
         }
-        if constexpr (FA_PREFILL_SGS != 0) {
+        {
             FA_SG(0x100, 2 * RV);
 #pragma unroll
             for (int i = 0; i < NSTEP - RV; ++i) {
@@ -650,7 +616,7 @@ __global__ __launch_bounds__(64 * NW, 2) void prefill_mfma16(PrefillKArgs ka) {
         // 64 k .. 64 k + 63 of the tile: row q / SL, slot q % SL), constant across tiles.
         constexpr uint32_t kOob = 0x7fff0000u;
         // this wave's index among the transferring waves
-        const int dw = PP ? (FA_PP_DMA == 2 ? wave : wave & 3) : wave;
+        const int dw = PP ? wave & 3 : wave;
         uint32_t koff[KI], voff[VI];
 #pragma unroll
         for (int i = 0; i < KI; ++i) {
@@ -727,7 +693,7 @@ __global__ __launch_bounds__(64 * NW, 2) void prefill_mfma16(PrefillKArgs ka) {
             // MFMA phase of tile m: P.V(m-1) then S(m); softmax phase of tile m.
             auto mfma_phase = [&](int m, auto pv, auto sc) {
                 u32x4_t kring[KR];
-                if constexpr (FA_PP_SPRE != 0 && decltype(pv)::value && decltype(sc)::value) {
+                if constexpr (decltype(pv)::value && decltype(sc)::value) {
                     // S's first operands are read before P.V: no LDS latency between the two
                     st_k = (m & 1) * STAGE;
                     s_ring_start(kring);
@@ -742,7 +708,7 @@ __global__ __launch_bounds__(64 * NW, 2) void prefill_mfma16(PrefillKArgs ka) {
                 __builtin_amdgcn_sched_barrier(0);
                 if constexpr (decltype(sc)::value) {
                     st_k = (m & 1) * STAGE;
-                    if constexpr (FA_PP_SPRE != 0 && decltype(pv)::value)
+                    if constexpr (decltype(pv)::value)
                         compute_s_pre(sacc, kring, T_{}, no_hook, true);
                     else
                         compute_s(sacc, T_{}, no_hook);
@@ -759,8 +725,8 @@ __global__ __launch_bounds__(64 * NW, 2) void prefill_mfma16(PrefillKArgs ka) {
             // waited for at the end of phase 2m+1, before their first reader (phase 2m+2).
             // Group 1 issues every transfer, at the start of its softmax phases: the VALU phase
             // has slack, the MFMA stream of group 0 is left alone.
-            // waves that issue the transfers (FA_PP_DMA: 0 group 1, 1 group 0, 2 all)
-            const bool xfer = FA_PP_DMA == 2 || (FA_PP_DMA == 0 ? grp == 1 : grp == 0);
+            // group 1 issues the transfers
+            const bool xfer = grp == 1;
             auto start_dma = [&](int m) {
                 if (!xfer) return;
                 if (m + 1 < n_blk) dma_k(m + 1, ((m + 1) & 1) * STAGE);
@@ -854,7 +820,7 @@ __global__ __launch_bounds__(64 * NW, 2) void prefill_mfma16(PrefillKArgs ka) {
         for (; tile < n_full; ++tile) tile_step(tile, NoMask{});
         for (; tile < n_tiles; ++tile) tile_step(tile, Mask{});
         }
-    } else if constexpr (DB) {
+    } else {
         // Double-buffered: stage j & 1 holds tile j. Tile j+1 (loaded into registers one tile
         // earlier) is stored to the other stage between the softmax and P.V of tile j, then the
         // loads of tile j+2 are issued; one barrier per tile.
@@ -893,82 +859,6 @@ __global__ __launch_bounds__(64 * NW, 2) void prefill_mfma16(PrefillKArgs ka) {
         int tile = 0;
         for (; tile < n_full; ++tile) tile_step(tile, NoMask{});
         for (; tile < n_tiles; ++tile) tile_step(tile, Mask{});
-    } else if constexpr (!PIPE) {
-        if (n_tiles > 0) {
-            load_one(0, kb8, kreg);
-            load_v(0);
-        }
-        auto tile_step = [&](int tile, auto masked) {
-            store_k(tile);
-            store_v();
-            __syncthreads();
-            if (tile + 1 < n_tiles) {
-                load_one(tile + 1, kb8, kreg);
-                load_v(tile + 1);
-            }
-            f32x16_t sacc[2];
-            u32x4_t pop[4];
-            compute_s(sacc, std::true_type{}, no_hook);
-            softmax_max(sacc, tile, masked);
-            rescale_o();
-            softmax_exp(sacc, pop);
-            compute_pv(pop, no_hook);
-            __syncthreads();
-        };
-        // Two loops, so the mask-free tiles carry no predicated mask code.
-        int tile = 0;
-        for (; tile < n_full; ++tile) tile_step(tile, NoMask{});
-        for (; tile < n_tiles; ++tile) tile_step(tile, Mask{});
-    } else {
-        // Software pipeline: the K tile in LDS runs one tile ahead of the V tile, so the MFMAs
-        // of S(j+1) are independent of the softmax of tile j and are interleaved with it.
-        // Loop invariant at the top of step j: LDS holds K(j+1) and V(j); kreg holds (or is
-        // loading) K(j+2) and vreg V(j+1). On the last step S(j+1) is computed from a stale K
-        // tile and discarded.
-        f32x16_t s_a[2], s_b[2];
-        if (n_tiles > 0) {
-            load_one(0, kb8, kreg);
-            load_v(0);
-            store_k(0);
-            store_v();
-            if (n_tiles > 1) load_one(1, kb8, kreg);
-            __syncthreads();
-            compute_s(s_a, std::true_type{}, no_hook);
-            if (n_tiles > 1) load_v(1);
-            __syncthreads();
-            if (n_tiles > 1) {
-                store_k(1);
-                if (n_tiles > 2) load_one(2, kb8, kreg);
-            }
-        }
-        auto step = [&](int j, f32x16_t (&cur)[2], f32x16_t (&nxt)[2], auto masked) {
-            softmax_max(cur, j, masked);
-            rescale_o();
-            __syncthreads();
-            u32x4_t pop[4];
-            compute_s(nxt, std::true_type{}, no_hook);
-            softmax_exp(cur, pop);
-            // 16 K reads + 16 MFMAs of S(j+1) spread through the exponentials of tile j
-            FA_SG_MV(7); FA_SG_MV(7); FA_SG_MV(7); FA_SG_MV(7);
-            FA_SG_MV(7); FA_SG_MV(7); FA_SG_MV(7); FA_SG_MV(7);
-            FA_SG_MV(7); FA_SG_MV(7); FA_SG_MV(7); FA_SG_MV(7);
-            FA_SG_MV(7); FA_SG_MV(7); FA_SG_MV(7); FA_SG_MV(7);
-            __builtin_amdgcn_sched_barrier(0);
-            compute_pv(pop, no_hook);
-            __syncthreads();
-            if (j + 1 < n_tiles) store_v();
-            if (j + 2 < n_tiles) store_k(j + 2);
-            if (j + 2 < n_tiles) load_v(j + 2);
-            if (j + 3 < n_tiles) load_one(j + 3, kb8, kreg);
-        };
-        auto step_any = [&](int j, f32x16_t (&cur)[2], f32x16_t (&nxt)[2]) {
-            if (j < n_full) step(j, cur, nxt, NoMask{});
-            else step(j, cur, nxt, Mask{});
-        };
-        for (int j = 0; j < n_tiles; j += 2) {
-            step_any(j, s_a, s_b);
-            if (j + 1 < n_tiles) step_any(j + 1, s_b, s_a);
-        }
     }
 
     // ---- epilogue: the wave's 32 normalised O rows are staged in its own LDS region (free once
@@ -1234,7 +1124,7 @@ template <typename T, int PMODE, bool ROPEK, bool SPLIT = false>
 static void launch16r(const PrefillKArgs& ka, int dpad, dim3 grid, hipStream_t s) {
     // contiguous K/V, K not rotated in the kernel: the 8-wave ping-pong kernel (when enabled)
     constexpr int NW =
-        ((PMODE == kContig || PMODE == kContigVT) && !ROPEK && prefill_pingpong_enabled()) ? 8 : 4;
+        prefill_pingpong(PMODE, ROPEK) ? 8 : 4;
     const bool full = ka.a.head_dim == dpad;
     switch (dpad) {
         case 32:
@@ -1290,7 +1180,7 @@ void launch_prefill(Dtype dt, bool paged, const PrefillArgs& a, hipStream_t s, u
     const int dpad = a.head_dim <= 32 ? 32 : (a.head_dim <= 64 ? 64 : 128);
     const int rows_total = a.q_len * a.group;
     // 16-bit contiguous K/V without in-kernel K rotation runs 256-row ping-pong workgroups
-    const bool pp = prefill_pingpong_enabled() && dt != Dtype::F32 && !paged && !a.rope_k;
+    const bool pp = dt != Dtype::F32 && !paged && !a.rope_k;
     const int bm = pp ? 256 : 128;
     const int nqb = (rows_total + bm - 1) / bm;
     dim3 g((unsigned)((int64_t)a.batch * a.kv_heads * nqb));

@@ -195,6 +195,7 @@ PROTOTYPES = {
     "fa_last_telemetry": (INT, [VP, P(TelemetryC)]),
     "fa_ctx_set_kernel_timing": (INT, [VP, I32]),
     "fa_ctx_set_prefill_precision": (INT, [VP, I32]),
+    "fa_ctx_set_decode_policy": (INT, [VP, I32]),
     "fa_ctx_kernel_timing": (INT, [VP, I32, P(ctypes.c_double), P(U64)]),
     "fa_ctx_kernel_timing_range": (INT, [VP, I32, P(ctypes.c_double), P(ctypes.c_double)]),
 }

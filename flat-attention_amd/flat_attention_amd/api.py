@@ -249,6 +249,11 @@ class HipContext:
     def set_prefill_policy(self, prerotate_k: int):
         check(lib().fa_ctx_set_prefill_policy(self.handle, prerotate_k))
 
+    def set_decode_policy(self, grouped: int):
+        """-1 automatic decode work layout (head-grouped workgroups where they apply), 0 one-wave
+        workgroups; read when a PagedDecodePlan is prepared."""
+        check(lib().fa_ctx_set_decode_policy(self.handle, grouped))
+
     def set_prefill_precision(self, mode: int):
         """0: rotated Q/K rounded to the 16-bit storage type before Q.K^T (default, fastest);
         1: split high/residual operands, f32-level scores for the 16-bit RoPE prefill."""

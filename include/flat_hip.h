@@ -469,6 +469,11 @@ int fa_ctx_set_prefill_policy(fa_ctx* ctx, int32_t prerotate_k);
  * K that is stored rotated (paged cache, pre-rotated asymmetric input) is used as stored.
  * Other values: FA_ERR_UNAVAILABLE. */
 int fa_ctx_set_prefill_precision(fa_ctx* ctx, int32_t mode);
+/* Decode work layout, read when a decode plan is prepared (kernel_variant_for_head_dim
+ * src/wgpu_backend.rs:430 generalised). grouped: -1 = automatic (default: 16-bit KV with
+ * page_size % 16 == 0, automatic split and <= 8 KV-head units run head-grouped workgroups),
+ * 0 = one-wave workgroups for every plan; 1 = the same as -1. */
+int fa_ctx_set_decode_policy(fa_ctx* ctx, int32_t grouped);
 /* V layout policy of the 16-bit contiguous prefill (same role as the K policy above): 1 = copy
  * V once into a transposed workspace [batch, kv_heads, head_dim, kv_len rounded up to 64] and
  * stream V^T tiles, 0 = stream V rows and transpose in the kernel, -1 = automatic (currently

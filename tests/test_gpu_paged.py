@@ -367,13 +367,14 @@ def test_cfg5_chunked_prefill_over_paged_cache(hip):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("grouped", ["1", "0"])
-def test_mixed_lengths_equal_work_partition_matches_oracle(hip, monkeypatch, grouped):
+def test_mixed_lengths_equal_work_partition_matches_oracle(hip, request, grouped):
     """Equal-work segment lists: 40 sequences from 1 to 3000 tokens, so some (sequence, head)
     units are finalised by one segment, others merge several partials, and one workgroup's range
     crosses sequence (and, with one-wave workgroups, head) boundaries. Both work layouts (the
-    default head-grouped workgroups, and one-wave workgroups via FA_DECODE_GROUPED=0) are
+    default head-grouped workgroups, and one-wave workgroups via fa_ctx_set_decode_policy(0)) are
     checked row by row against the oracle."""
-    monkeypatch.setenv("FA_DECODE_GROUPED", grouped)
+    hip.set_decode_policy(-1 if grouped == "1" else 0)
+    request.addfinalizer(lambda: hip.set_decode_policy(-1))
     rng = np.random.default_rng(21)
     ctx_lens = list(rng.integers(1, 3001, 40))
     ctx_lens[:4] = [1, 15, 16, 17]
@@ -487,14 +488,15 @@ def test_paged_prefill_modes_match_oracle_and_gather_bit_exactly(hip, dtype, ps,
 @pytest.mark.parametrize("dtype", [fa.DTYPE_BF16, fa.DTYPE_F16])
 @pytest.mark.parametrize("layout", ["1", "0"])
 @pytest.mark.parametrize("split", [None, 256])
-def test_adversarial_scores_16bit_decode(hip, monkeypatch, pattern, dtype, layout, split):
+def test_adversarial_scores_16bit_decode(hip, request, pattern, dtype, layout, split):
     """Split-K decode with scores that rise over the whole context (every segment's maximum
     exceeds the previous ones, so the combine rescales every partial), fall (later segments'
     probabilities underflow), or alternate between +-24; in both 16-bit formats, both MFMA work
-    layouts (head-grouped workgroups and one-wave workgroups, FA_DECODE_GROUPED=0) and with the
+    layouts (head-grouped workgroups and one-wave workgroups, fa_ctx_set_decode_policy(0)) and with the
     automatic and an explicit split, so every kernel variant that carries the rotated query's
     residual operand is covered."""
-    monkeypatch.setenv("FA_DECODE_GROUPED", layout)
+    hip.set_decode_policy(-1 if layout == "1" else 0)
+    request.addfinalizer(lambda: hip.set_decode_policy(-1))
     rnd = bf16_round if dtype == fa.DTYPE_BF16 else f16_round
     ps, hq, hkv, D = 16, 4, 1, 128
     ctx_lens = [2000, 700]
