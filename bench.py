@@ -12,7 +12,8 @@ decode GB/s (algorithmic bytes: K+V of every live token once, plus Q, O, LSE, bl
 is reported beside it with its own roofline. `value` and each op's rate use the op's whole
 duration (the prefill op includes the K pre-rotation pass); each `roofline.achieved` divides the
 same algorithmic work by the average duration of the op's dominant kernel alone, timed by the
-library's per-dispatch events (fa_ctx_set_kernel_timing) in a second pass of the same steps.
+library's per-dispatch events (fa_ctx_set_kernel_timing) in the same timed steps, so both
+figures describe the same clocks.
 `roofline.traffic` is the HBM bytes
 per launch of that kernel from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary
 (profiles/hbm_traffic_prefill_decode.json), scaled by a 1 GiB device-copy calibration.
@@ -84,9 +85,13 @@ def build_prefill(ctx, rng):
     cfg = fa.FlatAttentionConfig(causal=True)
     rot = fa.RotaryEmbeddingConfig(10000.0, 0)
     flop = 4.0 * B * hq * D * S * (S + 1) / 2
-    run = lambda: ex.forward_resident(q, k, v, shape, cfg, rot, out)  # noqa: E731
+    # the prepared forward (PreparedGroupedForward::prepare / encode_prepared): a step only
+    # enqueues the K rotation pass and the prefill kernel
+    prep = ex.prepare(q, k, v, out, shape, cfg, rot)
+    run = lambda: ex.encode_prepared(prep)  # noqa: E731
+    run._keep = prep
     return run, flop, {"workload": "prefill: causal GQA+RoPE B2 Hq32 Hkv8 N4096 D128 bf16",
-                       "flop_per_step": flop}
+                       "flop_per_step": flop, "entry": "fa_prepare_gqa_rope + fa_launch_prepared"}
 
 
 def build_decode(ctx, rng, split=None):
@@ -109,6 +114,16 @@ def build_decode(ctx, rng, split=None):
     if split:
         plan.set_split(split)
     out = fa.DeviceBuffer(ctx, plan.layout().combined_bytes)
+    # prepare cost: host work (work lists, validation, allocation) plus the stream-ordered
+    # upload of the tables, until the stream has completed it; median of 5 after one warm-up
+    prep_ms = []
+    for _ in range(6):
+        t0 = time.perf_counter()
+        p2 = fa.PagedDecodePlan(ctx, bt, ctx_lens, ps, total, hq, hkv, D,
+                                fa.FlatAttentionConfig(True), 10000.0, fa.DTYPE_BF16)
+        ctx.synchronize()
+        prep_ms.append((time.perf_counter() - t0) * 1e3)
+        p2.release()
     nbytes = (float(ctx_lens.sum()) * hkv * D * 2 * 2 + n * hq * D * 2 * 2 + n * hq * 4
               + float(pages_per.sum()) * 4)
     run = lambda: plan.launch(q, kp, vp, out)  # noqa: E731
@@ -116,6 +131,7 @@ def build_decode(ctx, rng, split=None):
     return run, nbytes, {"workload": "paged decode: 64 seqs ctx U[512,8192] page16 Hq32 Hkv8 "
                                      "D128 bf16 KV, shuffled pages",
                          "bytes_per_step": nbytes, "live_tokens": int(ctx_lens.sum()),
+                         "prepare_ms": round(float(np.median(prep_ms[1:])), 4),
                          "split_tokens": info["split_tokens"], "work_items": info["work_items"]}
 
 

@@ -147,7 +147,6 @@ struct fa_ctx {
     float2* rope = nullptr;
     float rope_theta = 0.0f;
     uint64_t rope_dim = 0, rope_rows = 0;
-    float* inv_freq = nullptr;
     // growable scratch for the K pre-rotation pass
     void* ws = nullptr;
     size_t ws_bytes = 0;
@@ -164,14 +163,21 @@ struct fa_ctx {
     // decode work layout: -1 automatic (head-grouped workgroups where they apply), 0 one-wave
     // workgroups (fa_ctx_set_decode_policy; read when a decode plan is prepared)
     int decode_grouped_policy = -1;
-    // per-sequence metadata of variable-length prefill: device copy + pinned staging, reused
-    // once the event recorded after the previous copy has completed
+    // per-call metadata (variable-length prefill, batched append): one device buffer that each
+    // call overwrites by a stream-ordered copy just before its launch
     int32_t* meta_dev = nullptr;
     size_t meta_dev_bytes = 0;
-    int32_t* meta_host = nullptr;
-    size_t meta_host_bytes = 0;
-    hipEvent_t meta_event = nullptr;
-    bool meta_pending = false;
+    // pinned host staging for stream-ordered uploads: a slot is reused once the event recorded
+    // after its copy has completed, so no upload waits for the stream
+    struct Staging {
+        void* host = nullptr;
+        size_t bytes = 0;
+        hipEvent_t done = nullptr;
+        bool busy = false;
+    };
+    std::vector<Staging> staging;
+    // device buffers replaced by larger ones while work may still read them: freed at destroy
+    std::vector<void*> retired;
     // per-call allocation accounting (telemetry)
     uint32_t call_allocs = 0;
     uint64_t call_alloc_bytes = 0;
@@ -291,7 +297,29 @@ int dev_alloc(fa_ctx* ctx, void** p, size_t bytes) {
     return FA_OK;
 }
 
-// (cos, sin) table covering positions [0, rows) for (theta, head_dim).
+// inv_freq[p] = theta^(-2p/D) in f32 with the host powf, as rotated_pair computes it
+fa::RopeFreqs rope_freqs(float theta, uint64_t head_dim) {
+    fa::RopeFreqs f{};
+    for (uint64_t p = 0; p < head_dim / 2; ++p) {
+        float exponent = -2.0f * (float)p / (float)head_dim;
+        f.inv_freq[p] = powf(theta, exponent);
+    }
+    return f;
+}
+
+// Builds a (cos, sin) table of `rows` positions into `table` on the context's stream.
+int build_rope_table(fa_ctx* ctx, float2* table, float theta, uint64_t head_dim, uint64_t rows) {
+    begin_span(ctx);
+    fa::launch_rope_table(table, rope_freqs(theta, head_dim), (int)rows, (int)(head_dim / 2),
+                          ctx->stream);
+    end_span(ctx, FA_KERNEL_ROPE_TABLE);
+    HIP_TRY(hipGetLastError());
+    return FA_OK;
+}
+
+// (cos, sin) table covering positions [0, rows) for (theta, head_dim), cached by the context.
+// A larger table replaces the cached one without waiting for the stream (the old one is
+// retired).
 int ensure_rope(fa_ctx* ctx, float theta, uint64_t head_dim, uint64_t rows, const float2** out) {
     if (ctx->rope && ctx->rope_theta == theta && ctx->rope_dim == head_dim &&
         ctx->rope_rows >= rows) {
@@ -301,45 +329,57 @@ int ensure_rope(fa_ctx* ctx, float theta, uint64_t head_dim, uint64_t rows, cons
     uint64_t cap = std::max<uint64_t>(rows, 4096);
     if (ctx->rope_theta == theta && ctx->rope_dim == head_dim)
         cap = std::max<uint64_t>(cap, ctx->rope_rows * 2);
-    const uint64_t half = head_dim / 2;
-    // inv_freq[p] = theta^(-2p/D) in f32 with the host powf, as rotated_pair computes it
-    std::vector<float> inv(half);
-    for (uint64_t p = 0; p < half; ++p) {
-        float exponent = -2.0f * (float)p / (float)head_dim;
-        inv[p] = powf(theta, exponent);
-    }
-    HIP_TRY(hipStreamSynchronize(ctx->stream));
-    if (ctx->rope) HIP_TRY(hipFree(ctx->rope));
-    if (ctx->inv_freq) HIP_TRY(hipFree(ctx->inv_freq));
-    ctx->rope = nullptr;
-    ctx->inv_freq = nullptr;
-    int rc = dev_alloc(ctx, (void**)&ctx->rope, cap * half * sizeof(float2));
-    if (rc) return rc;
-    rc = dev_alloc(ctx, (void**)&ctx->inv_freq, half * sizeof(float));
-    if (rc) return rc;
-    HIP_TRY(hipMemcpy(ctx->inv_freq, inv.data(), half * sizeof(float), hipMemcpyHostToDevice));
-    begin_span(ctx);
-    fa::launch_rope_table(ctx->rope, ctx->inv_freq, (int)cap, (int)half, ctx->stream);
-    end_span(ctx, FA_KERNEL_ROPE_TABLE);
-    HIP_TRY(hipGetLastError());
+    float2* fresh = nullptr;
+    if (int rc = dev_alloc(ctx, (void**)&fresh, cap * (head_dim / 2) * sizeof(float2))) return rc;
+    if (ctx->rope) ctx->retired.push_back(ctx->rope);
+    ctx->rope = fresh;
     ctx->rope_theta = theta;
     ctx->rope_dim = head_dim;
     ctx->rope_rows = cap;
+    if (int rc = build_rope_table(ctx, fresh, theta, head_dim, cap)) return rc;
     *out = ctx->rope;
     return FA_OK;
 }
 
+// Grows a context-owned buffer without waiting for the stream: work already enqueued keeps
+// reading the old buffer, which is retired (freed when the context is destroyed).
 int grow(fa_ctx* ctx, void** buf, size_t* cap, size_t bytes, void** out) {
     if (*cap < bytes) {
-        HIP_TRY(hipStreamSynchronize(ctx->stream));
-        if (*buf) HIP_TRY(hipFree(*buf));
-        *buf = nullptr;
-        *cap = 0;
-        int rc = dev_alloc(ctx, buf, bytes);
-        if (rc) return rc;
+        void* fresh = nullptr;
+        if (int rc = dev_alloc(ctx, &fresh, bytes)) return rc;
+        if (*buf) ctx->retired.push_back(*buf);
+        *buf = fresh;
         *cap = bytes;
     }
     *out = *buf;
+    return FA_OK;
+}
+
+// Stream-ordered host -> device copy of `bytes` from `src` through a pinned staging slot. The
+// host never waits: a slot whose previous copy has not completed is skipped and, when none is
+// free, a new slot is allocated.
+int stage_upload(fa_ctx* ctx, void* dst, const void* src, size_t bytes) {
+    if (!bytes) return FA_OK;
+    fa_ctx::Staging* slot = nullptr;
+    for (auto& st : ctx->staging) {
+        if (st.busy && hipEventQuery(st.done) == hipSuccess) st.busy = false;
+        if (!st.busy && st.bytes >= bytes && (!slot || st.bytes < slot->bytes)) slot = &st;
+    }
+    if (!slot) {
+        fa_ctx::Staging st;
+        st.bytes = std::max<size_t>(bytes, 4096);
+        HIP_TRY(hipHostMalloc(&st.host, st.bytes, hipHostMallocDefault));
+        if (hipEventCreateWithFlags(&st.done, hipEventDisableTiming) != hipSuccess) {
+            (void)hipHostFree(st.host);
+            return fail(FA_ERR_HIP, "hipEventCreateWithFlags failed");
+        }
+        ctx->staging.push_back(st);
+        slot = &ctx->staging.back();
+    }
+    memcpy(slot->host, src, bytes);
+    HIP_TRY(hipMemcpyAsync(dst, slot->host, bytes, hipMemcpyHostToDevice, ctx->stream));
+    HIP_TRY(hipEventRecord(slot->done, ctx->stream));
+    slot->busy = true;
     return FA_OK;
 }
 
@@ -351,24 +391,9 @@ int ensure_ws(fa_ctx* ctx, size_t bytes, void** out) {
 // the stream reads them, an earlier one has finished with the previous contents (same stream).
 int upload_meta(fa_ctx* ctx, const int32_t* vals, size_t n, const int32_t** dev) {
     const size_t bytes = n * sizeof(int32_t);
-    if (ctx->meta_pending) {
-        HIP_TRY(hipEventSynchronize(ctx->meta_event));
-        ctx->meta_pending = false;
-    }
-    if (ctx->meta_host_bytes < bytes) {
-        if (ctx->meta_host) HIP_TRY(hipHostFree(ctx->meta_host));
-        ctx->meta_host = nullptr;
-        ctx->meta_host_bytes = 0;
-        HIP_TRY(hipHostMalloc((void**)&ctx->meta_host, bytes, hipHostMallocDefault));
-        ctx->meta_host_bytes = bytes;
-    }
     void* d = nullptr;
     if (int rc = grow(ctx, (void**)&ctx->meta_dev, &ctx->meta_dev_bytes, bytes, &d)) return rc;
-    if (!ctx->meta_event) HIP_TRY(hipEventCreateWithFlags(&ctx->meta_event, hipEventDisableTiming));
-    memcpy(ctx->meta_host, vals, bytes);
-    HIP_TRY(hipMemcpyAsync(d, ctx->meta_host, bytes, hipMemcpyHostToDevice, ctx->stream));
-    HIP_TRY(hipEventRecord(ctx->meta_event, ctx->stream));
-    ctx->meta_pending = true;
+    if (int rc = stage_upload(ctx, d, vals, bytes)) return rc;
     *dev = (const int32_t*)d;
     return FA_OK;
 }
@@ -395,6 +420,7 @@ const char* fa_status_string(int s) {
         case FA_ERR_NON_FINITE_INPUT: return "NonFiniteInput";
         case FA_ERR_UNAVAILABLE: return "Unavailable";
         case FA_ERR_UNSUPPORTED_HEAD_DIM: return "UnsupportedHeadDim";
+        case FA_ERR_FOREIGN_BUFFER: return "ForeignBuffer";
         case FA_ERR_INDEX_SPACE_EXCEEDED: return "IndexSpaceExceeded";
         case FA_ERR_DISPATCH_LIMIT: return "DispatchLimit";
         case FA_ERR_BUFFER_TOO_SMALL: return "BufferTooSmall";
@@ -476,13 +502,15 @@ int fa_ctx_destroy(fa_ctx* ctx) {
     (void)hipSetDevice(ctx->device);
     (void)hipStreamSynchronize(ctx->stream);
     if (ctx->rope) (void)hipFree(ctx->rope);
-    if (ctx->inv_freq) (void)hipFree(ctx->inv_freq);
+    for (void* r : ctx->retired) (void)hipFree(r);
+    for (auto& st : ctx->staging) {
+        (void)hipHostFree(st.host);
+        (void)hipEventDestroy(st.done);
+    }
     if (ctx->ws) (void)hipFree(ctx->ws);
     if (ctx->ws_vt) (void)hipFree(ctx->ws_vt);
     if (ctx->ws_delta) (void)hipFree(ctx->ws_delta);
     if (ctx->meta_dev) (void)hipFree(ctx->meta_dev);
-    if (ctx->meta_host) (void)hipHostFree(ctx->meta_host);
-    if (ctx->meta_event) (void)hipEventDestroy(ctx->meta_event);
     for (const auto& s : ctx->pending) {
         (void)hipEventDestroy(s.begin);
         (void)hipEventDestroy(s.end);
@@ -674,7 +702,19 @@ struct PrefillJob {
     bool no_vt = false;  // never use the transposed-V copy
 };
 
-int run_prefill(fa_ctx* ctx, PrefillJob& j) {
+// The resolved form of a prefill job: variant decisions and the device memory the launch uses
+// (the context's caches for a one-shot call, memory owned by a prepared forward otherwise).
+struct PrefillRun {
+    PrefillJob j;
+    bool prerot = false, vt = false;
+    float2* table = nullptr;  // RoPE (cos, sin) rows [0, max_pos)
+    void* ws = nullptr;       // rotated K (prerot)
+    void* wsv = nullptr;      // V^T (vt)
+};
+
+// Decides the variant and gathers the memory. own == false: the context's growable caches;
+// own == true: fresh allocations that the caller (a prepared forward) keeps and frees.
+int resolve_prefill(fa_ctx* ctx, PrefillJob& j, bool own, PrefillRun* r) {
     // 16-bit contiguous K/V are read through 32-bit buffer offsets within one (batch, kv-head)
     // slice: kv_len rows of k_ss elements must stay below 2 GiB.
     if (!j.paged && j.dtype != FA_DTYPE_F32 &&
@@ -682,84 +722,120 @@ int run_prefill(fa_ctx* ctx, PrefillJob& j) {
         return fail(FA_ERR_INDEX_SPACE_EXCEEDED,
                     "one K/V slice spans %llu bytes; the 16-bit kernels address at most 2 GiB",
                     (unsigned long long)((uint64_t)j.a.kv_len * (uint64_t)j.a.k_ss * 2u));
-    const float2* table = nullptr;
+    r->j = j;
     bool prerot = false;
     if (j.rope) {
-        if (int rc = ensure_rope(ctx, j.theta, (uint64_t)j.a.head_dim, j.max_pos, &table)) return rc;
-        j.a.rope_table = table;
+        if (own) {
+            if (int rc = dev_alloc(ctx, (void**)&r->table,
+                                   j.max_pos * ((uint64_t)j.a.head_dim / 2) * sizeof(float2)))
+                return rc;
+            if (int rc = build_rope_table(ctx, r->table, j.theta, (uint64_t)j.a.head_dim,
+                                          j.max_pos))
+                return rc;
+        } else {
+            const float2* t = nullptr;
+            if (int rc = ensure_rope(ctx, j.theta, (uint64_t)j.a.head_dim, j.max_pos, &t))
+                return rc;
+            r->table = const_cast<float2*>(t);
+        }
+        r->j.a.rope_table = r->table;
         prerot = j.a.rope_k && !j.paged && want_prerotate(ctx, (uint64_t)j.a.head_dim);
         // precise scores: K rotated in the kernel, which keeps its 16-bit residual
         if (ctx->prefill_precision == 1 && j.a.rope_k && !j.paged && j.dtype != FA_DTYPE_F32) {
             prerot = false;
-            j.a.split_qk = 1;
+            r->j.a.split_qk = 1;
         }
     }
-    uint32_t dispatches = 0;
+    r->prerot = prerot;
     if (prerot) {
-        void* ws = nullptr;
-        if (int rc = ensure_ws(ctx, j.kv_bytes, &ws)) return rc;
-        begin_span(ctx);
-        fa::launch_rotate_rows(j.dt, j.a.k, ws, (int)j.k_rows, (int)j.k_heads, j.a.head_dim,
-                               (int64_t)j.k_period, table, j.a.kv_rope_offset, ctx->stream);
-        end_span(ctx, FA_KERNEL_ROPE_ROTATE);
-        HIP_TRY(hipGetLastError());
-        j.a.k = ws;
-        j.a.rope_k = 0;
-        dispatches++;
+        if (own) {
+            if (int rc = dev_alloc(ctx, &r->ws, j.kv_bytes)) return rc;
+        } else if (int rc = ensure_ws(ctx, j.kv_bytes, &r->ws)) {
+            return rc;
+        }
     }
     // Optional transposed V copy for the 16-bit contiguous kernel (off unless selected): the V^T
     // operand then comes from plain 16-byte LDS reads instead of transposing ones. It measured
     // no faster at D = 128, so the extra pass is not run by default.
-    const bool vt = !j.paged && !j.no_vt && j.dtype != FA_DTYPE_F32 && j.a.head_dim % 8 == 0 &&
-                    ctx->transpose_v_policy == 1;
-    j.a.vt = nullptr;
-    j.a.vt_row = 0;
-    if (vt) {
+    r->vt = !j.paged && !j.no_vt && j.dtype != FA_DTYPE_F32 && j.a.head_dim % 8 == 0 &&
+            ctx->transpose_v_policy == 1;
+    r->j.a.vt = nullptr;
+    r->j.a.vt_row = 0;
+    if (r->vt) {
         const uint64_t s_pad = ((uint64_t)j.a.kv_len + 63) / 64 * 64;
         const uint64_t bytes = (uint64_t)j.a.batch * j.a.kv_heads * j.a.head_dim * s_pad * 2u;
         if ((uint64_t)j.a.head_dim * s_pad * 2u > (uint64_t)INT32_MAX)
             return fail(FA_ERR_INDEX_SPACE_EXCEEDED,
                         "one transposed V slice spans %llu bytes; the kernel addresses at most 2 GiB",
                         (unsigned long long)((uint64_t)j.a.head_dim * s_pad * 2u));
-        void* wsv = nullptr;
-        if (int rc = grow(ctx, &ctx->ws_vt, &ctx->ws_vt_bytes, bytes, &wsv)) return rc;
+        if (own) {
+            if (int rc = dev_alloc(ctx, &r->wsv, bytes)) return rc;
+        } else if (int rc = grow(ctx, &ctx->ws_vt, &ctx->ws_vt_bytes, bytes, &r->wsv)) {
+            return rc;
+        }
+        r->j.a.vt_row = (int)s_pad;
+    }
+    return FA_OK;
+}
+
+// Enqueues the resolved prefill on the context's stream: optional K pre-rotation and V
+// transpose passes, then the prefill kernel. No allocation, copy or wait.
+int enqueue_prefill(fa_ctx* ctx, const PrefillRun& r) {
+    fa::PrefillArgs a = r.j.a;
+    const PrefillJob& j = r.j;
+    uint32_t dispatches = 0;
+    if (r.prerot) {
         begin_span(ctx);
-        fa::launch_transpose_v(j.dt, j.a.v, j.a.k_sb, j.a.k_sh, j.a.k_ss, j.a.batch,
-                               j.a.kv_heads, j.a.kv_len, j.a.head_dim, (int)s_pad, wsv,
-                               ctx->stream);
+        fa::launch_rotate_rows(j.dt, a.k, r.ws, (int)j.k_rows, (int)j.k_heads, a.head_dim,
+                               (int64_t)j.k_period, r.table, a.kv_rope_offset, ctx->stream);
+        end_span(ctx, FA_KERNEL_ROPE_ROTATE);
+        HIP_TRY(hipGetLastError());
+        a.k = r.ws;
+        a.rope_k = 0;
+        dispatches++;
+    }
+    if (r.vt) {
+        begin_span(ctx);
+        fa::launch_transpose_v(j.dt, a.v, a.k_sb, a.k_sh, a.k_ss, a.batch, a.kv_heads, a.kv_len,
+                               a.head_dim, a.vt_row, r.wsv, ctx->stream);
         end_span(ctx, FA_KERNEL_TRANSPOSE_V);
         HIP_TRY(hipGetLastError());
-        j.a.vt = wsv;
-        j.a.vt_row = (int)s_pad;
+        a.vt = r.wsv;
         dispatches++;
     }
     unsigned grid[3], block = 0;
     // K read already rotated (pre-pass, or a paged cache that stores K rotated on append)
-    const int kid = prefill_kernel_id(j.dtype, prerot || (j.paged && j.rope));
+    const int kid = prefill_kernel_id(j.dtype, r.prerot || (j.paged && j.rope));
     begin_span(ctx);
-    fa::launch_prefill(j.dt, j.paged, j.a, ctx->stream, grid, &block);
+    fa::launch_prefill(j.dt, j.paged, a, ctx->stream, grid, &block);
     end_span(ctx, kid);
     HIP_TRY(hipGetLastError());
     dispatches++;
     const char* fb = nullptr;
-    if (j.rope && j.a.rope_k && !prerot && !j.paged && j.a.head_dim % 8 != 0)
+    if (j.rope && a.rope_k && !r.prerot && !j.paged && a.head_dim % 8 != 0)
         fb = "K pre-rotation pass needs head_dim % 8 == 0; K rotated on load";
     const char* dt = j.dtype == FA_DTYPE_BF16 ? "bf16" : j.dtype == FA_DTYPE_F16 ? "f16" : "f32";
     const char* base = j.dtype == FA_DTYPE_F32 ? "prefill_mfma_f32" : "prefill_mfma16";
     char name[64];
-    if (prerot || vt)
-        snprintf(name, sizeof name, "%s%s%s<%s>", prerot ? "rotate_rows + " : "",
-                 vt ? "transpose_v + " : "", base, dt);
+    if (r.prerot || r.vt)
+        snprintf(name, sizeof name, "%s%s%s<%s>", r.prerot ? "rotate_rows + " : "",
+                 r.vt ? "transpose_v + " : "", base, dt);
     else if (j.paged)
         snprintf(name, sizeof name, "%s<%s> (paged%s)", base, dt, j.rope ? ", K stored rotated" : "");
-    else if (j.a.split_qk)
+    else if (a.split_qk)
         snprintf(name, sizeof name, "%s<%s> (K rotated on load, split Q/K scores)", base, dt);
-    else if (j.a.rope_k)
+    else if (a.rope_k)
         snprintf(name, sizeof name, "%s<%s> (K rotated on load)", base, dt);
     else
         snprintf(name, sizeof name, "%s<%s>", base, dt);
     record(ctx, kid, name, 128, 64, grid, block, dispatches, 1, fb);
     return FA_OK;
+}
+
+int run_prefill(fa_ctx* ctx, PrefillJob& j) {
+    PrefillRun r;
+    if (int rc = resolve_prefill(ctx, j, false, &r)) return rc;
+    return enqueue_prefill(ctx, r);
 }
 
 int validate_grouped(uint64_t b, uint64_t hq, uint64_t hkv, uint64_t s, uint64_t d) {
@@ -782,10 +858,16 @@ int validate_grouped(uint64_t b, uint64_t hq, uint64_t hkv, uint64_t s, uint64_t
 
 extern "C" {
 
-int fa_forward_gqa_rope(fa_ctx* ctx, const void* q, size_t q_bytes, const void* k,
-                        const void* v, size_t kv_bytes, void* out_lse, size_t out_bytes,
-                        const fa_grouped_shape* sh, const fa_config* cfg, const fa_rotary* rot,
-                        int dtype) {
+}  // extern "C"
+
+namespace {
+
+// Validation and kernel arguments of the contiguous grouped (optionally RoPE) forward, shared by
+// the one-shot call and the prepared forward.
+int build_gqa_job(fa_ctx* ctx, const void* q, size_t q_bytes, const void* k, const void* v,
+                  size_t kv_bytes, void* out_lse, size_t out_bytes, const fa_grouped_shape* sh,
+                  const fa_config* cfg, const fa_rotary* rot, int dtype, PrefillJob& j,
+                  fa_packed_layout* layout) {
     if (!sh) return fail(FA_ERR_NULL_ARGUMENT, "shape is null");
     if (int rc = check_dtype(dtype)) return rc;
     if (int rc = validate_grouped(sh->batch, sh->q_heads, sh->kv_heads, sh->seq_len, sh->head_dim))
@@ -806,10 +888,9 @@ int fa_forward_gqa_rope(fa_ctx* ctx, const void* q, size_t q_bytes, const void* 
     if (int rc = check_buffer("V", v, kv_bytes, kvn * eb)) return rc;
     if (int rc = check_buffer("O|LSE", out_lse, out_bytes, lay.combined_bytes)) return rc;
     if (!ctx) return fail(FA_ERR_NULL_ARGUMENT, "context is null");
-    begin_call(ctx);
-    if (int rc = set_device(ctx)) return rc;
+    if (layout) *layout = lay;
 
-    PrefillJob j{};
+    j = PrefillJob{};
     j.dt = (Dtype)dtype;
     j.dtype = dtype;
     fa::PrefillArgs& a = j.a;
@@ -838,7 +919,92 @@ int fa_forward_gqa_rope(fa_ctx* ctx, const void* q, size_t q_bytes, const void* 
         j.k_heads = 1;
         j.k_period = sh->seq_len;
     }
+    return FA_OK;
+}
+
+}  // namespace
+
+// A contiguous grouped forward with its buffers, shape, configuration and variant resolved and
+// its device memory (RoPE table, K rotation workspace) owned, so a launch only enqueues.
+struct fa_prepared_forward {
+    fa_ctx* ctx = nullptr;
+    PrefillRun run;
+    fa_packed_layout layout{};
+};
+
+extern "C" {
+
+int fa_forward_gqa_rope(fa_ctx* ctx, const void* q, size_t q_bytes, const void* k,
+                        const void* v, size_t kv_bytes, void* out_lse, size_t out_bytes,
+                        const fa_grouped_shape* sh, const fa_config* cfg, const fa_rotary* rot,
+                        int dtype) {
+    PrefillJob j;
+    if (int rc = build_gqa_job(ctx, q, q_bytes, k, v, kv_bytes, out_lse, out_bytes, sh, cfg, rot,
+                               dtype, j, nullptr))
+        return rc;
+    begin_call(ctx);
+    if (int rc = set_device(ctx)) return rc;
     if (int rc = run_prefill(ctx, j)) return rc;
+    return ok();
+}
+
+int fa_prepare_gqa_rope(fa_ctx* ctx, const void* q, size_t q_bytes, const void* k,
+                        const void* v, size_t kv_bytes, void* out_lse, size_t out_bytes,
+                        const fa_grouped_shape* sh, const fa_config* cfg, const fa_rotary* rot,
+                        int dtype, fa_prepared_forward** out) {
+    if (!out) return fail(FA_ERR_NULL_ARGUMENT, "output handle is null");
+    *out = nullptr;
+    PrefillJob j;
+    fa_packed_layout lay;
+    if (int rc = build_gqa_job(ctx, q, q_bytes, k, v, kv_bytes, out_lse, out_bytes, sh, cfg, rot,
+                               dtype, j, &lay))
+        return rc;
+    if (int rc = set_device(ctx)) return rc;
+    auto* p = new fa_prepared_forward();
+    p->ctx = ctx;
+    p->layout = lay;
+    if (int rc = resolve_prefill(ctx, j, true, &p->run)) {
+        (void)hipStreamSynchronize(ctx->stream);  // error path: the table build may be in flight
+        fa_prepared_forward_destroy(p);
+        return rc;
+    }
+    *out = p;
+    return ok();
+}
+
+int fa_prepare_mha(fa_ctx* ctx, const void* q, const void* k, const void* v, size_t in_bytes,
+                   void* out_lse, size_t out_bytes, const fa_attention_shape* shape,
+                   const fa_config* config, int dtype, fa_prepared_forward** out) {
+    if (!shape) return fail(FA_ERR_NULL_ARGUMENT, "shape is null");
+    fa_grouped_shape g{shape->batch, shape->heads, shape->heads, shape->seq_len, shape->head_dim};
+    return fa_prepare_gqa_rope(ctx, q, in_bytes, k, v, in_bytes, out_lse, out_bytes, &g, config,
+                               nullptr, dtype, out);
+}
+
+int fa_launch_prepared(fa_ctx* ctx, const fa_prepared_forward* p) {
+    if (!ctx || !p) return fail(FA_ERR_NULL_ARGUMENT, "null argument");
+    if (p->ctx != ctx)
+        return fail(FA_ERR_FOREIGN_BUFFER, "prepared forward belongs to another context");
+    begin_call(ctx);
+    if (int rc = set_device(ctx)) return rc;
+    if (int rc = enqueue_prefill(ctx, p->run)) return rc;
+    return ok();
+}
+
+int fa_prepared_forward_layout(const fa_prepared_forward* p, fa_packed_layout* out) {
+    if (!p || !out) return fail(FA_ERR_NULL_ARGUMENT, "null argument");
+    *out = p->layout;
+    return ok();
+}
+
+int fa_prepared_forward_destroy(fa_prepared_forward* p) {
+    if (!p) return ok();
+    (void)hipSetDevice(p->ctx->device);
+    (void)hipStreamSynchronize(p->ctx->stream);
+    if (p->run.table) (void)hipFree(p->run.table);
+    if (p->run.ws) (void)hipFree(p->run.ws);
+    if (p->run.wsv) (void)hipFree(p->run.wsv);
+    delete p;
     return ok();
 }
 
@@ -1608,10 +1774,13 @@ int build_work(fa_decode_plan* p) {
     p->units = units;
     p->split_tokens = longest;
     const uint64_t need_work = seg_arr.size() + wave_off.size() + unit_part.size();
+    // (a plan rebuilt by set_split may still be read by launches in flight: a buffer that grows
+    // is retired to the context, and the new lists arrive by a stream-ordered copy)
     if (p->work_cap < need_work) {
-        if (p->d_work) HIP_TRY(hipFree(p->d_work));
-        p->d_work = nullptr;
-        if (int rc = dev_alloc(ctx, (void**)&p->d_work, need_work * 4)) return rc;
+        void* fresh = nullptr;
+        if (int rc = dev_alloc(ctx, &fresh, need_work * 4)) return rc;
+        if (p->d_work) ctx->retired.push_back(p->d_work);
+        p->d_work = (int32_t*)fresh;
         p->work_cap = need_work;
     }
     std::vector<int32_t> all;
@@ -1619,12 +1788,13 @@ int build_work(fa_decode_plan* p) {
     all.insert(all.end(), seg_arr.begin(), seg_arr.end());
     all.insert(all.end(), wave_off.begin(), wave_off.end());
     all.insert(all.end(), unit_part.begin(), unit_part.end());
-    HIP_TRY(hipMemcpy(p->d_work, all.data(), need_work * 4, hipMemcpyHostToDevice));
+    if (int rc = stage_upload(ctx, p->d_work, all.data(), need_work * 4)) return rc;
     const uint64_t part = std::max<uint64_t>(1, p->n_slots) * 16 * (p->head_dim + 2) * 4;
     if (p->part_bytes < part) {
-        if (p->d_part) HIP_TRY(hipFree(p->d_part));
-        p->d_part = nullptr;
-        if (int rc = dev_alloc(ctx, (void**)&p->d_part, part)) return rc;
+        void* fresh = nullptr;
+        if (int rc = dev_alloc(ctx, &fresh, part)) return rc;
+        if (p->d_part) ctx->retired.push_back(p->d_part);
+        p->d_part = (float*)fresh;
         p->part_bytes = part;
     }
     return FA_OK;
@@ -1739,17 +1909,15 @@ int fa_paged_decode_prepare(fa_ctx* ctx, const int32_t* block_tables, uint64_t m
     if (!rc) rc = dev_alloc(ctx, (void**)&p->d_bt, n_seqs * max_pages * 4);
     if (!rc) rc = dev_alloc(ctx, (void**)&p->d_ctx, n_seqs * 4);
     if (!rc) rc = dev_alloc(ctx, (void**)&p->d_qpos, n_seqs * 4);
-    if (!rc && hipMemcpy(p->d_bt, block_tables, n_seqs * max_pages * 4, hipMemcpyHostToDevice))
-        rc = fail(FA_ERR_HIP, "block table upload failed");
-    if (!rc && hipMemcpy(p->d_ctx, ctx_lens, n_seqs * 4, hipMemcpyHostToDevice))
-        rc = fail(FA_ERR_HIP, "context length upload failed");
-    if (!rc && hipMemcpy(p->d_qpos, qpos.data(), n_seqs * 4, hipMemcpyHostToDevice))
-        rc = fail(FA_ERR_HIP, "query position upload failed");
+    if (!rc) rc = stage_upload(ctx, p->d_bt, block_tables, n_seqs * max_pages * 4);
+    if (!rc) rc = stage_upload(ctx, p->d_ctx, ctx_lens, n_seqs * 4);
+    if (!rc) rc = stage_upload(ctx, p->d_qpos, qpos.data(), n_seqs * 4);
     if (!rc) {
         p->split_req = 0;
         rc = build_work(p);
     }
     if (rc) {
+        (void)hipStreamSynchronize(ctx->stream);  // error path: no copy may still target it
         free_plan(p);
         return rc;
     }
@@ -1767,7 +1935,6 @@ int fa_paged_decode_plan_set_split(fa_ctx* ctx, fa_decode_plan* p, uint64_t spli
                     "split size %llu spans more than 64 pages of %llu tokens",
                     (unsigned long long)split_tokens, (unsigned long long)p->page_size);
     if (int rc = set_device(ctx)) return rc;
-    HIP_TRY(hipStreamSynchronize(ctx->stream));
     p->split_req = split_tokens;
     if (int rc = build_work(p)) return rc;
     return ok();
@@ -2097,9 +2264,9 @@ int fa_chunked_prefill_paged_prepare(fa_ctx* ctx, const int32_t* block_tables, u
     p->page_size = page_size;
     p->physical_pages = physical_pages;
     int rc = dev_alloc(ctx, (void**)&p->d_bt, sh->batch * max_pages * 4);
-    if (!rc && hipMemcpy(p->d_bt, block_tables, sh->batch * max_pages * 4, hipMemcpyHostToDevice))
-        rc = fail(FA_ERR_HIP, "block table upload failed");
+    if (!rc) rc = stage_upload(ctx, p->d_bt, block_tables, sh->batch * max_pages * 4);
     if (rc) {
+        (void)hipStreamSynchronize(ctx->stream);  // error path: no copy may still target it
         if (p->d_bt) (void)hipFree(p->d_bt);
         delete p;
         return rc;
@@ -2217,16 +2384,13 @@ int fa_paged_append_batched(fa_ctx* ctx, const int32_t* block_tables, uint64_t m
         if (int rc = ensure_rope(ctx, rot->theta, head_dim, rot->position_offset + maxend, &table))
             return rc;
     }
-    DevBuf meta;
-    const uint64_t meta_bytes = (n_seqs * max_pages + n_seqs) * 4;
-    HIP_TRY(hipMalloc(&meta.p, meta_bytes));
-    ctx->call_allocs += 1;
-    ctx->call_alloc_bytes += meta_bytes;
-    int32_t* d_bt = (int32_t*)meta.p;
-    int32_t* d_start = d_bt + n_seqs * max_pages;
-    HIP_TRY(hipMemcpyAsync(d_bt, block_tables, n_seqs * max_pages * 4, hipMemcpyHostToDevice,
-                           ctx->stream));
-    HIP_TRY(hipMemcpyAsync(d_start, start_lens, n_seqs * 4, hipMemcpyHostToDevice, ctx->stream));
+    // block tables and start lengths reach the device by one stream-ordered copy
+    std::vector<int32_t> meta(block_tables, block_tables + n_seqs * max_pages);
+    meta.insert(meta.end(), start_lens, start_lens + n_seqs);
+    const int32_t* d_meta = nullptr;
+    if (int rc = upload_meta(ctx, meta.data(), meta.size(), &d_meta)) return rc;
+    const int32_t* d_bt = d_meta;
+    const int32_t* d_start = d_meta + n_seqs * max_pages;
     fa::AppendArgs a{};
     a.k_src = k_src;
     a.v_src = v_src;
@@ -2246,7 +2410,6 @@ int fa_paged_append_batched(fa_ctx* ctx, const int32_t* block_tables, uint64_t m
     fa::launch_append((Dtype)dtype, a, ctx->stream);
     end_span(ctx, FA_KERNEL_PAGED_APPEND);
     HIP_TRY(hipGetLastError());
-    HIP_TRY(hipStreamSynchronize(ctx->stream));  // metadata buffer is released on return
     unsigned grid[3] = {(unsigned)append_len, (unsigned)n_seqs, 1};
     record(ctx, FA_KERNEL_PAGED_APPEND, "append_kernel", 0, (uint32_t)page_size, grid,
            (unsigned)std::min<uint64_t>(256, std::max<uint64_t>(64, kv_heads * head_dim / 8)), 1, 1,

@@ -114,8 +114,11 @@ struct BackwardArgs {
 void launch_backward(Dtype dt, const BackwardArgs& a, hipStream_t s);
 
 // (cos, sin) table: table[pos*half + p] for pos < rows, p < half = head_dim/2, with
-// angle = float(pos) * inv_freq[p].
-void launch_rope_table(float2* table, const float* inv_freq, int rows, int half, hipStream_t s);
+// angle = float(pos) * inv_freq[p]. The frequencies travel in the kernel arguments (no copy).
+struct RopeFreqs {
+    float inv_freq[64];
+};
+void launch_rope_table(float2* table, const RopeFreqs& f, int rows, int half, hipStream_t s);
 
 // Scatter `append_len` rows per sequence into the page pool, optionally rotating K rows.
 struct AppendArgs {

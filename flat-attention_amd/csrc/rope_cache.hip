@@ -12,19 +12,19 @@
 
 namespace fa {
 
-__global__ void rope_table_kernel(float2* table, const float* inv_freq, int rows, int half) {
+__global__ void rope_table_kernel(float2* table, RopeFreqs f, int rows, int half) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= (int64_t)rows * half) return;
     const int pos = (int)(i / half), p = (int)(i % half);
-    const float angle = (float)pos * inv_freq[p];
+    const float angle = (float)pos * f.inv_freq[p];
     float s, c;
     sincosf(angle, &s, &c);
     table[i] = make_float2(c, s);
 }
 
-void launch_rope_table(float2* table, const float* inv_freq, int rows, int half, hipStream_t s) {
+void launch_rope_table(float2* table, const RopeFreqs& f, int rows, int half, hipStream_t s) {
     const int64_t n = (int64_t)rows * half;
-    rope_table_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(table, inv_freq, rows, half);
+    rope_table_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(table, f, rows, half);
 }
 
 // Load / rotate / store 8 consecutive elements (4 pairs) of one head.

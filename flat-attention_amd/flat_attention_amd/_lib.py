@@ -32,7 +32,7 @@ STATUS = {
     21: "UnsupportedHeadDim", 22: "IndexSpaceExceeded", 23: "DispatchLimit",
     24: "BufferTooSmall", 25: "EmptyTable", 26: "TooManyMappedPages",
     27: "CausalVisibilityMismatch", 28: "ZeroQueryChunkSize", 29: "UnsupportedDtype",
-    30: "InvalidPage", 31: "EmptyCache", 32: "InvalidCacheLength", 40: "PagedZeroDimension", 41: "CapacityOverflow",
+    30: "InvalidPage", 31: "EmptyCache", 32: "InvalidCacheLength", 33: "ForeignBuffer", 40: "PagedZeroDimension", 41: "CapacityOverflow",
     42: "CapacityExceeded", 43: "GenerationOverflow", 50: "NullArgument", 60: "Hip",
 }
 
@@ -131,6 +131,13 @@ PROTOTYPES = {
     "fa_forward_mha": (INT, [VP, VP, VP, VP, SZ, VP, SZ, P(AttentionShapeC), P(ConfigC), INT]),
     "fa_forward_gqa_rope": (INT, [VP, VP, SZ, VP, VP, SZ, VP, SZ, P(GroupedShapeC), P(ConfigC),
                                   P(RotaryC), INT]),
+    "fa_prepare_gqa_rope": (INT, [VP, VP, SZ, VP, VP, SZ, VP, SZ, P(GroupedShapeC), P(ConfigC),
+                                  P(RotaryC), INT, P(VP)]),
+    "fa_prepare_mha": (INT, [VP, VP, VP, VP, SZ, VP, SZ, P(AttentionShapeC), P(ConfigC), INT,
+                             P(VP)]),
+    "fa_launch_prepared": (INT, [VP, VP]),
+    "fa_prepared_forward_layout": (INT, [VP, P(PackedLayoutC)]),
+    "fa_prepared_forward_destroy": (INT, [VP]),
     "fa_forward_mha_host": (INT, [VP, VP, VP, VP, U64, U64, U64, P(AttentionShapeC), P(ConfigC),
                                   INT, VP, VP]),
     "fa_forward_gqa_rope_host": (INT, [VP, VP, VP, VP, U64, U64, U64, P(GroupedShapeC),

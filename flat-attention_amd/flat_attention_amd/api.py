@@ -440,6 +440,23 @@ class HipRotaryGroupedAttention:
                                         self.dtype))
         return out
 
+    def prepare(self, q, k, v, out, shape: GroupedAttentionShape, config: FlatAttentionConfig,
+                rotary: Optional[RotaryEmbeddingConfig]) -> "PreparedGroupedForward":
+        """PreparedGroupedForward::prepare src/wgpu_forward_grouped.rs:352: bind the buffers,
+        resolve the variant, own the RoPE table and workspaces; launches only enqueue."""
+        h = ctypes.c_void_p()
+        rot = ctypes.byref(rotary.c()) if rotary is not None else None
+        check(lib().fa_prepare_gqa_rope(self.ctx.handle, q.ptr, q.nbytes, k.ptr, v.ptr,
+                                        min(k.nbytes, v.nbytes), out.ptr, out.nbytes,
+                                        ctypes.byref(shape.c()), ctypes.byref(config.c()), rot,
+                                        self.dtype, ctypes.byref(h)))
+        return PreparedGroupedForward(self.ctx, h.value, (q, k, v, out))
+
+    def encode_prepared(self, prepared: "PreparedGroupedForward"):
+        """encode_prepared src/wgpu_forward_grouped.rs:496."""
+        check(lib().fa_launch_prepared(self.ctx.handle, prepared.handle))
+        return prepared.layout()
+
     def download_attention(self, out: DeviceBuffer, shape) -> FlatAttentionOutput:
         return download_attention(out, self.layout(shape), self.dtype)
 
@@ -457,6 +474,32 @@ class HipRotaryGroupedAttention:
 
     def runtime_telemetry(self) -> RuntimeDispatchTelemetry:
         return self.ctx.last_telemetry()
+
+
+class PreparedGroupedForward:
+    """PreparedGroupedForward src/wgpu_forward_grouped.rs:352-513 (owns its device state)."""
+
+    def __init__(self, ctx: HipContext, handle: int, buffers):
+        self.ctx, self.handle = ctx, handle
+        self._buffers = buffers  # the bound buffers stay alive with the prepared forward
+        ctx._adopt(self)  # released before its context is destroyed
+
+    def layout(self) -> PackedLayout:
+        lay = L.PackedLayoutC()
+        check(lib().fa_prepared_forward_layout(self.handle, ctypes.byref(lay)))
+        return PackedLayout(lay.output_elements, lay.lse_elements, lay.output_bytes,
+                            lay.lse_byte_offset, lay.combined_bytes)
+
+    def release(self):
+        if self.handle:
+            lib().fa_prepared_forward_destroy(self.handle)
+        self.handle = None
+
+    def __del__(self):
+        try:
+            self.release()
+        except Exception:
+            pass
 
 
 class HipAsymmetricProjectionPipeline:

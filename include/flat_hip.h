@@ -14,8 +14,13 @@
  *   - Device pointers are plain `void*` obtained from `fa_buf_*` or from any HIP allocation on
  *     the context's device. Each device pointer is paired with its size in bytes so the library
  *     can reject undersized buffers before any launch (reference `BufferTooSmall`).
- *   - All work is enqueued on the context's single HIP stream. No call synchronises except
- *     `fa_buf_download`, `fa_ctx_synchronize` and the `*_host` convenience forwards.
+ *   - All work is enqueued on the context's single HIP stream. Only `fa_buf_download`,
+ *     `fa_ctx_synchronize`, `fa_ctx_kernel_timing*`, the `*_host` convenience forwards and the
+ *     destroy/free calls wait for it. Host metadata (block tables, work lists, per-sequence
+ *     lengths) reaches the device by stream-ordered copies from pinned staging; a context cache
+ *     that must grow is replaced without waiting (the old buffer is freed at context destroy).
+ *     Prepared objects (`fa_prepare_*`, decode and paged-prefill plans) allocate at prepare
+ *     time; their launches allocate nothing and copy nothing.
  *   - Validation always happens before any launch; nothing ever falls back to the CPU.
  *
  * Tensor layouts (element order, row-major):
@@ -65,6 +70,8 @@ typedef enum fa_status {
     FA_ERR_INVALID_PAGE = 30,
     FA_ERR_EMPTY_CACHE = 31,          /* ResidentDecodeError::EmptyCache src/wgpu_decode.rs:105 */
     FA_ERR_INVALID_CACHE_LENGTH = 32, /* ResidentDecodeError::InvalidCacheLength :106 */
+    FA_ERR_FOREIGN_BUFFER = 33,       /* WgpuFlatAttentionError::ForeignBuffer src/wgpu_backend.rs:56:
+                                         a prepared object used with another context */
     FA_ERR_PAGED_ZERO_DIMENSION = 40,
     FA_ERR_CAPACITY_OVERFLOW = 41,
     FA_ERR_CAPACITY_EXCEEDED = 42,
@@ -210,6 +217,27 @@ int fa_forward_gqa_rope(fa_ctx* ctx, const void* q, size_t q_bytes, const void* 
                         const void* v, size_t kv_bytes, void* out_lse, size_t out_bytes,
                         const fa_grouped_shape* shape, const fa_config* config,
                         const fa_rotary* rotary, int dtype);
+
+/* Prepared forward: PreparedGroupedForward::prepare src/wgpu_forward_grouped.rs:352 /
+ * encode_prepared :496. prepare validates the buffers (Q, K, V, [O|LSE]), shape, config and
+ * rotary exactly as fa_forward_gqa_rope does, resolves the kernel variant under the context's
+ * current policies, and allocates what every launch needs: the RoPE (cos, sin) table for the
+ * shape's positions (built on the context's stream) and the K rotation workspace. It may
+ * allocate; it does not wait for the stream. fa_launch_prepared only enqueues kernels on the
+ * context's stream (no allocation, copy or wait); a prepared forward used with another context
+ * fails with FA_ERR_FOREIGN_BUFFER. Buffers stay bound: the caller keeps them alive and may
+ * change their contents between launches. destroy waits for the stream, then frees. */
+typedef struct fa_prepared_forward fa_prepared_forward;
+int fa_prepare_gqa_rope(fa_ctx* ctx, const void* q, size_t q_bytes, const void* k,
+                        const void* v, size_t kv_bytes, void* out_lse, size_t out_bytes,
+                        const fa_grouped_shape* shape, const fa_config* config,
+                        const fa_rotary* rotary, int dtype, fa_prepared_forward** out);
+int fa_prepare_mha(fa_ctx* ctx, const void* q, const void* k, const void* v, size_t in_bytes,
+                   void* out_lse, size_t out_bytes, const fa_attention_shape* shape,
+                   const fa_config* config, int dtype, fa_prepared_forward** out);
+int fa_launch_prepared(fa_ctx* ctx, const fa_prepared_forward* prepared);
+int fa_prepared_forward_layout(const fa_prepared_forward* prepared, fa_packed_layout* out);
+int fa_prepared_forward_destroy(fa_prepared_forward* prepared);
 
 /* Owned-context host forwards: WgpuFlatAttention::forward src/wgpu_backend.rs:445 and
  * WgpuRotaryGroupedAttention::forward src/wgpu_rotary_grouped_backend.rs:117. Inputs are

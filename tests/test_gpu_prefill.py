@@ -456,3 +456,44 @@ def test_precise_rope_prefill_matches_oracle(hip, dtype, rnd, hq, hkv, S, D, cau
     eo, el = _oracle_grouped(q, k, v, shape, causal, rot)
     assert_close("O", o, eo, H16_ATOL, 0.0)
     assert_close("LSE", l, el, H16_ATOL, 0.0)
+
+
+@pytest.mark.parametrize("dtype,rnd,atol,rtol", [(fa.DTYPE_BF16, bf16_round, H16_ATOL, 0.0),
+                                                  (fa.DTYPE_F32, lambda x: x, F32_ATOL, F32_RTOL)])
+def test_prepared_forward_matches_one_shot_and_oracle(hip, dtype, rnd, atol, rtol):
+    """PreparedGroupedForward::prepare / encode_prepared (src/wgpu_forward_grouped.rs:352,496):
+    prepare binds the buffers and owns the RoPE table and K rotation workspace; repeated
+    launches, with the inputs' contents changed in between, give bitwise the one-shot call's
+    results; a prepared forward is rejected by another context (ForeignBuffer)."""
+    B, hq, hkv, S, D = 2, 8, 2, 150, 128
+    shape = fa.GroupedAttentionShape(B, hq, hkv, S, D)
+    rot = fa.RotaryEmbeddingConfig(1e4, 7)
+    cfg = fa.FlatAttentionConfig(True)
+    ex = fa.HipRotaryGroupedAttention(hip, dtype)
+    ins = [[rnd(normal(n, s0 + i)) for i, n in enumerate(
+        (B * hq * S * D, B * hkv * S * D, B * hkv * S * D))] for s0 in (61, 71)]
+    qb, kb, vb = (fa.DeviceBuffer.from_array(hip, fa.host_storage(x, dtype)) for x in ins[0])
+    out = fa.DeviceBuffer(hip, ex.layout(shape).combined_bytes)
+    prep = ex.prepare(qb, kb, vb, out, shape, cfg, rot)
+    assert prep.layout() == ex.layout(shape)
+    for q, k, v in ins + ins[:1]:
+        for buf, x in zip((qb, kb, vb), (q, k, v)):
+            buf.upload(fa.host_storage(x, dtype))
+        ex.encode_prepared(prep)
+        got = ex.download_attention(out, shape)
+        one = _run_grouped(hip, q, k, v, shape, cfg, rot, dtype)
+        assert np.array_equal(fa.storage_to_f32(got.output, dtype).view(np.uint32),
+                              one[0].view(np.uint32))
+        assert np.array_equal(got.lse.view(np.uint32), one[1].view(np.uint32))
+        eo, el = _oracle_grouped(q, k, v, shape, True, rot, units=(0, 1))
+        assert_close("O unit 0", fa.storage_to_f32(got.output, dtype)[:S * D], eo[:S * D], atol,
+                     rtol)
+        assert_close("LSE unit 0", got.lse[:S], el[:S], atol, rtol)
+    other = fa.HipContext(0)
+    try:
+        with pytest.raises(fa.FlatHipError) as e:
+            fa.HipRotaryGroupedAttention(other, dtype).encode_prepared(prep)
+        assert e.value.variant == "ForeignBuffer"
+    finally:
+        other.close()
+    prep.release()
