@@ -52,6 +52,9 @@ int ok() {
 
 constexpr uint64_t kMaxHeadDim = 128;  // WGSL_MAX_HEAD_DIM src/lib.rs:59-66
 constexpr uint64_t kI32 = (uint64_t)std::numeric_limits<int32_t>::max();
+// metadata part (block tables, lengths, positions, work list) of the allocation-free decode's
+// scratch; the rest holds the queries' (cos, sin) rows and the split partials
+constexpr size_t kNoAllocMetaBytes = (size_t)4 << 20;
 
 bool mul_ov(uint64_t a, uint64_t b, uint64_t* out) {
     if (a != 0 && b > std::numeric_limits<uint64_t>::max() / a) return true;
@@ -190,6 +193,13 @@ struct fa_ctx {
     hipEvent_t open_begin = nullptr;
     std::vector<hipEvent_t> free_events;
     std::vector<Span> pending;
+    // allocation-free decode: the device's static scratch (fa::noalloc_scratch, resolved when the
+    // context is created), a host staging area for its metadata and the event that marks the
+    // last copy out of that area
+    void* na_scratch = nullptr;
+    std::vector<int32_t> na_host;
+    hipEvent_t na_copied = nullptr;
+    bool na_pending = false;
     struct Timed {
         double total_ms = 0.0, min_ms = 0.0, max_ms = 0.0;
         uint64_t launches = 0;
@@ -438,6 +448,7 @@ const char* fa_status_string(int s) {
         case FA_ERR_GENERATION_OVERFLOW: return "GenerationOverflow";
         case FA_ERR_NULL_ARGUMENT: return "NullArgument";
         case FA_ERR_HIP: return "Hip";
+        case FA_ERR_SCRATCH_EXCEEDED: return "ScratchExceeded";
         default: return "Unknown";
     }
 }
@@ -493,6 +504,12 @@ int fa_ctx_create(int device, fa_ctx** out) {
         delete ctx;
         return fail(FA_ERR_HIP, "hipStreamCreate failed");
     }
+    // set-up of the allocation-free decode (device current): the scratch address of this
+    // device and the host staging area; a failure here surfaces at that entry point
+    if (fa::noalloc_scratch(device, &ctx->na_scratch) != hipSuccess) ctx->na_scratch = nullptr;
+    if (hipEventCreateWithFlags(&ctx->na_copied, hipEventDisableTiming) != hipSuccess)
+        ctx->na_copied = nullptr;
+    ctx->na_host.resize(kNoAllocMetaBytes / sizeof(int32_t));
     *out = ctx;
     return ok();
 }
@@ -516,6 +533,7 @@ int fa_ctx_destroy(fa_ctx* ctx) {
         (void)hipEventDestroy(s.end);
     }
     if (ctx->open_begin) (void)hipEventDestroy(ctx->open_begin);
+    if (ctx->na_copied) (void)hipEventDestroy(ctx->na_copied);
     for (hipEvent_t e : ctx->free_events) (void)hipEventDestroy(e);
     (void)hipStreamDestroy(ctx->stream);
     delete ctx;
@@ -1644,7 +1662,7 @@ uint64_t max_split_tokens(uint64_t page_size) {
 //  * split_req = x: every unit cut every x keys, segments dealt to the resident waves in turn.
 // Units covered by one segment are finalised by the split kernel; the others get one partial
 // slot per segment, merged by the combine kernel.
-int build_work(fa_decode_plan* p) {
+int compute_work(fa_decode_plan* p, std::vector<int32_t>* all_out) {
     fa_ctx* ctx = p->ctx;
     const uint64_t chunks = (p->q_heads / p->kv_heads + 15) / 16;
     const uint64_t units = p->kv_heads * chunks;
@@ -1774,6 +1792,25 @@ int build_work(fa_decode_plan* p) {
     p->units = units;
     p->split_tokens = longest;
     const uint64_t need_work = seg_arr.size() + wave_off.size() + unit_part.size();
+    std::vector<int32_t>& all = *all_out;
+    all.clear();
+    all.reserve(need_work);
+    all.insert(all.end(), seg_arr.begin(), seg_arr.end());
+    all.insert(all.end(), wave_off.begin(), wave_off.end());
+    all.insert(all.end(), unit_part.begin(), unit_part.end());
+    return FA_OK;
+}
+
+// Partial slots hold un-normalised O (16 heads x head_dim) then (m, l) per head.
+uint64_t partial_bytes(const fa_decode_plan* p) {
+    return std::max<uint64_t>(1, p->n_slots) * 16 * (p->head_dim + 2) * 4;
+}
+
+int build_work(fa_decode_plan* p) {
+    fa_ctx* ctx = p->ctx;
+    std::vector<int32_t> all;
+    if (int rc = compute_work(p, &all)) return rc;
+    const uint64_t need_work = all.size();
     // (a plan rebuilt by set_split may still be read by launches in flight: a buffer that grows
     // is retired to the context, and the new lists arrive by a stream-ordered copy)
     if (p->work_cap < need_work) {
@@ -1783,13 +1820,8 @@ int build_work(fa_decode_plan* p) {
         p->d_work = (int32_t*)fresh;
         p->work_cap = need_work;
     }
-    std::vector<int32_t> all;
-    all.reserve(need_work);
-    all.insert(all.end(), seg_arr.begin(), seg_arr.end());
-    all.insert(all.end(), wave_off.begin(), wave_off.end());
-    all.insert(all.end(), unit_part.begin(), unit_part.end());
     if (int rc = stage_upload(ctx, p->d_work, all.data(), need_work * 4)) return rc;
-    const uint64_t part = std::max<uint64_t>(1, p->n_slots) * 16 * (p->head_dim + 2) * 4;
+    const uint64_t part = partial_bytes(p);
     if (p->part_bytes < part) {
         void* fresh = nullptr;
         if (int rc = dev_alloc(ctx, &fresh, part)) return rc;
@@ -1831,17 +1863,14 @@ int check_pages(const int32_t* bt, uint64_t max_pages, uint64_t n_seqs, uint64_t
     return FA_OK;
 }
 
-}  // namespace
-
-extern "C" {
-
-int fa_paged_decode_prepare(fa_ctx* ctx, const int32_t* block_tables, uint64_t max_pages,
-                            const int32_t* ctx_lens, const int32_t* q_positions, uint64_t n_seqs,
-                            uint64_t page_size, uint64_t physical_pages, uint64_t q_heads,
-                            uint64_t kv_heads, uint64_t head_dim, const fa_config* cfg,
-                            float theta, int dtype, fa_decode_plan** out) {
-    if (!out || !block_tables || !ctx_lens) return fail(FA_ERR_NULL_ARGUMENT, "null argument");
-    *out = nullptr;
+// Arguments of a paged decode (fa_paged_decode_prepare): every check that precedes device work.
+// Fills the softmax scale, each query's RoPE position and the table rows they need.
+int validate_decode(const int32_t* block_tables, uint64_t max_pages, const int32_t* ctx_lens,
+                    const int32_t* q_positions, uint64_t n_seqs, uint64_t page_size,
+                    uint64_t physical_pages, uint64_t q_heads, uint64_t kv_heads,
+                    uint64_t head_dim, const fa_config* cfg, float theta, int dtype, float* scale,
+                    std::vector<int32_t>* qpos_out, uint64_t* max_pos_out) {
+    if (!block_tables || !ctx_lens) return fail(FA_ERR_NULL_ARGUMENT, "null argument");
     if (int rc = check_dtype(dtype)) return rc;
     if (!n_seqs || !q_heads || !kv_heads || !head_dim || !max_pages)
         return fail(FA_ERR_ZERO_DIMENSION, "attention dimensions must all be non-zero");
@@ -1864,14 +1893,14 @@ int fa_paged_decode_prepare(fa_ctx* ctx, const int32_t* block_tables, uint64_t m
     if (!std::isfinite(theta) || theta <= 0.0f)
         return fail(FA_ERR_INVALID_ROTARY_THETA,
                     "paged decode RoPE theta must be finite and positive, got %g", (double)theta);
-    float scale;
-    if (int rc = resolve_scale(cfg, head_dim, &scale)) return rc;
+    if (int rc = resolve_scale(cfg, head_dim, scale)) return rc;
     uint64_t rows;
     if (mul_ov(page_size, physical_pages, &rows) || rows > kI32 || max_pages > kI32 ||
         n_seqs * max_pages > (uint64_t)std::numeric_limits<int64_t>::max() / 4)
         return fail(FA_ERR_INDEX_SPACE_EXCEEDED, "paged decode exceeds the i32 index space");
     uint64_t max_pos = 0;
-    std::vector<int32_t> qpos(n_seqs);
+    std::vector<int32_t>& qpos = *qpos_out;
+    qpos.resize(n_seqs);
     for (uint64_t s = 0; s < n_seqs; ++s) {
         if (ctx_lens[s] <= 0)
             return fail(FA_ERR_EMPTY_TABLE, "paged decode requires at least one live KV token");
@@ -1886,6 +1915,28 @@ int fa_paged_decode_prepare(fa_ctx* ctx, const int32_t* block_tables, uint64_t m
         max_pos = std::max<uint64_t>(max_pos, (uint64_t)qp + 1);
     }
     if (int rc = check_pages(block_tables, max_pages, n_seqs, 0, ctx_lens, page_size, physical_pages))
+        return rc;
+    *max_pos_out = max_pos;
+    return FA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int fa_paged_decode_prepare(fa_ctx* ctx, const int32_t* block_tables, uint64_t max_pages,
+                            const int32_t* ctx_lens, const int32_t* q_positions, uint64_t n_seqs,
+                            uint64_t page_size, uint64_t physical_pages, uint64_t q_heads,
+                            uint64_t kv_heads, uint64_t head_dim, const fa_config* cfg,
+                            float theta, int dtype, fa_decode_plan** out) {
+    if (!out) return fail(FA_ERR_NULL_ARGUMENT, "null argument");
+    *out = nullptr;
+    float scale;
+    uint64_t max_pos = 0;
+    std::vector<int32_t> qpos;
+    if (int rc = validate_decode(block_tables, max_pages, ctx_lens, q_positions, n_seqs, page_size,
+                                 physical_pages, q_heads, kv_heads, head_dim, cfg, theta, dtype,
+                                 &scale, &qpos, &max_pos))
         return rc;
     if (!ctx) return fail(FA_ERR_NULL_ARGUMENT, "context is null");
     begin_call(ctx);
@@ -1958,23 +2009,15 @@ int fa_paged_decode_plan_destroy(fa_decode_plan* p) {
     return ok();
 }
 
-int fa_paged_decode_launch(fa_ctx* ctx, const fa_decode_plan* p, const void* q, size_t q_bytes,
-                           const void* k_pool, const void* v_pool, size_t pool_bytes,
-                           void* out_lse, size_t out_bytes) {
-    if (!ctx || !p) return fail(FA_ERR_NULL_ARGUMENT, "null argument");
-    begin_call(ctx);
-    const uint64_t eb = elem_bytes(p->dtype);
-    const uint64_t qn = p->n_seqs * p->q_heads * p->head_dim;
-    const uint64_t pool = p->physical_pages * p->page_size * p->kv_heads * p->head_dim * eb;
-    fa_packed_layout lay;
-    if (int rc = fa_packed_layout_for(qn, p->n_seqs * p->q_heads, p->dtype, &lay)) return rc;
-    if (int rc = check_buffer("Q", q, q_bytes, qn * eb)) return rc;
-    if (int rc = check_buffer("K", k_pool, pool_bytes, pool)) return rc;
-    if (int rc = check_buffer("V", v_pool, pool_bytes, pool)) return rc;
-    if (int rc = check_buffer("O|LSE", out_lse, out_bytes, lay.combined_bytes)) return rc;
-    if (int rc = set_device(ctx)) return rc;
-    const float2* table = nullptr;
-    if (int rc = ensure_rope(ctx, p->theta, p->head_dim, p->max_pos, &table)) return rc;
+}  // extern "C"
+
+namespace {
+
+// Enqueues the split kernel and the combine of plan `p` (device state in place) with the RoPE
+// (cos, sin) rows `table` addressed by the plan's query positions.
+int enqueue_decode(fa_ctx* ctx, const fa_decode_plan* p, const float2* table, const void* q,
+                   const void* k_pool, const void* v_pool, void* out_lse,
+                   const fa_packed_layout& lay) {
     fa::DecodeArgs a{};
     a.q = q;
     a.k_pool = k_pool;
@@ -2017,6 +2060,134 @@ int fa_paged_decode_launch(fa_ctx* ctx, const fa_decode_plan* p, const void* q, 
            mfma && p->grouped ? "decode_mfma_grouped + decode_combine" : kernel_name(kid),
            (uint32_t)std::min<uint64_t>(16, p->q_heads / p->kv_heads), 16, grid, block,
            (uint32_t)dispatches, (uint32_t)((p->split_tokens)), nullptr);
+    return FA_OK;
+}
+
+
+}  // namespace
+
+extern "C" {
+
+int fa_paged_decode_launch(fa_ctx* ctx, const fa_decode_plan* p, const void* q, size_t q_bytes,
+                           const void* k_pool, const void* v_pool, size_t pool_bytes,
+                           void* out_lse, size_t out_bytes) {
+    if (!ctx || !p) return fail(FA_ERR_NULL_ARGUMENT, "null argument");
+    begin_call(ctx);
+    const uint64_t eb = elem_bytes(p->dtype);
+    const uint64_t qn = p->n_seqs * p->q_heads * p->head_dim;
+    const uint64_t pool = p->physical_pages * p->page_size * p->kv_heads * p->head_dim * eb;
+    fa_packed_layout lay;
+    if (int rc = fa_packed_layout_for(qn, p->n_seqs * p->q_heads, p->dtype, &lay)) return rc;
+    if (int rc = check_buffer("Q", q, q_bytes, qn * eb)) return rc;
+    if (int rc = check_buffer("K", k_pool, pool_bytes, pool)) return rc;
+    if (int rc = check_buffer("V", v_pool, pool_bytes, pool)) return rc;
+    if (int rc = check_buffer("O|LSE", out_lse, out_bytes, lay.combined_bytes)) return rc;
+    if (int rc = set_device(ctx)) return rc;
+    const float2* table = nullptr;
+    if (int rc = ensure_rope(ctx, p->theta, p->head_dim, p->max_pos, &table)) return rc;
+    if (int rc = enqueue_decode(ctx, p, table, q, k_pool, v_pool, out_lse, lay)) return rc;
+    return ok();
+}
+
+int fa_paged_decode_noalloc(fa_ctx* ctx, const int32_t* block_tables, uint64_t max_pages,
+                            const int32_t* ctx_lens, const int32_t* q_positions, uint64_t n_seqs,
+                            uint64_t page_size, uint64_t physical_pages, uint64_t q_heads,
+                            uint64_t kv_heads, uint64_t head_dim, const fa_config* cfg,
+                            float theta, int dtype, const void* q, size_t q_bytes,
+                            const void* k_pool, const void* v_pool, size_t pool_bytes,
+                            void* out_lse, size_t out_bytes) {
+    float scale;
+    uint64_t max_pos = 0;
+    std::vector<int32_t> qpos;
+    if (int rc = validate_decode(block_tables, max_pages, ctx_lens, q_positions, n_seqs, page_size,
+                                 physical_pages, q_heads, kv_heads, head_dim, cfg, theta, dtype,
+                                 &scale, &qpos, &max_pos))
+        return rc;
+    const uint64_t eb = elem_bytes(dtype);
+    const uint64_t qn = n_seqs * q_heads * head_dim;
+    const uint64_t pool = physical_pages * page_size * kv_heads * head_dim * eb;
+    fa_packed_layout lay;
+    if (int rc = fa_packed_layout_for(qn, n_seqs * q_heads, dtype, &lay)) return rc;
+    if (int rc = check_buffer("Q", q, q_bytes, qn * eb)) return rc;
+    if (int rc = check_buffer("K", k_pool, pool_bytes, pool)) return rc;
+    if (int rc = check_buffer("V", v_pool, pool_bytes, pool)) return rc;
+    if (int rc = check_buffer("O|LSE", out_lse, out_bytes, lay.combined_bytes)) return rc;
+    if (!ctx) return fail(FA_ERR_NULL_ARGUMENT, "context is null");
+    begin_call(ctx);
+    if (int rc = set_device(ctx)) return rc;
+    if (!ctx->na_scratch || !ctx->na_copied)
+        return fail(FA_ERR_HIP, "the static decode scratch of device %d is not addressable",
+                    ctx->device);
+
+    // The plan lives on the stack; its device state points into the scratch.
+    fa_decode_plan p;
+    p.ctx = ctx;
+    p.n_seqs = n_seqs;
+    p.max_pages = max_pages;
+    p.page_size = page_size;
+    p.physical_pages = physical_pages;
+    p.q_heads = q_heads;
+    p.kv_heads = kv_heads;
+    p.head_dim = head_dim;
+    p.dtype = dtype;
+    p.scale = scale;
+    p.theta = theta;
+    p.ctx_lens.assign(ctx_lens, ctx_lens + n_seqs);
+    p.max_pos = max_pos;
+    p.split_req = 0;
+    std::vector<int32_t> work;
+    if (int rc = compute_work(&p, &work)) return rc;
+
+    // Scratch layout: [metadata (kNoAllocMetaBytes) | (cos, sin) rows of the queries | partials].
+    // Metadata ints: block tables | context lengths | query positions | 0..n_seqs-1 (each query's
+    // row of the compact table) | work list.
+    const uint64_t n_bt = n_seqs * max_pages;
+    const uint64_t meta_ints = n_bt + 4 * n_seqs + work.size();
+    const uint64_t rope_bytes = (n_seqs * (head_dim / 2) * sizeof(float2) + 255) / 256 * 256;
+    const uint64_t part_bytes = partial_bytes(&p);
+    if (meta_ints * 4 > kNoAllocMetaBytes)
+        return fail(FA_ERR_SCRATCH_EXCEEDED,
+                    "allocation-free decode needs %llu bytes of block tables and work lists; "
+                    "its scratch holds %llu",
+                    (unsigned long long)(meta_ints * 4), (unsigned long long)kNoAllocMetaBytes);
+    if (kNoAllocMetaBytes + rope_bytes + part_bytes > fa::kNoAllocScratchBytes)
+        return fail(FA_ERR_SCRATCH_EXCEEDED,
+                    "allocation-free decode needs %llu bytes of scratch; the static scratch "
+                    "holds %llu",
+                    (unsigned long long)(kNoAllocMetaBytes + rope_bytes + part_bytes),
+                    (unsigned long long)fa::kNoAllocScratchBytes);
+    // the previous call's copy must have left the host staging area before it is rewritten
+    if (ctx->na_pending) {
+        HIP_TRY(hipEventSynchronize(ctx->na_copied));
+        ctx->na_pending = false;
+    }
+    int32_t* h = ctx->na_host.data();
+    memcpy(h, block_tables, n_bt * 4);
+    memcpy(h + n_bt, ctx_lens, n_seqs * 4);
+    memcpy(h + n_bt + n_seqs, qpos.data(), n_seqs * 4);
+    for (uint64_t s = 0; s < n_seqs; ++s) h[n_bt + 2 * n_seqs + s] = (int32_t)s;
+    memcpy(h + n_bt + 3 * n_seqs, work.data(), work.size() * 4);
+    uint8_t* base = (uint8_t*)ctx->na_scratch;
+    HIP_TRY(hipMemcpyAsync(base, h, meta_ints * 4, hipMemcpyHostToDevice, ctx->stream));
+    HIP_TRY(hipEventRecord(ctx->na_copied, ctx->stream));
+    ctx->na_pending = true;
+    int32_t* d = (int32_t*)base;
+    p.d_bt = d;
+    p.d_ctx = d + n_bt;
+    const int32_t* d_positions = p.d_ctx + n_seqs;
+    p.d_qpos = p.d_ctx + 2 * n_seqs;
+    p.d_work = p.d_ctx + 3 * n_seqs;
+    float2* table = (float2*)(base + kNoAllocMetaBytes);
+    p.d_part = (float*)(base + kNoAllocMetaBytes + rope_bytes);
+    p.part_bytes = part_bytes;
+    // Nothing in the scratch has to start at zero: every partial slot is written by its segment
+    // before the combine reads it.
+    begin_span(ctx);
+    fa::launch_rope_rows(table, rope_freqs(theta, head_dim), d_positions, (int)n_seqs,
+                         (int)(head_dim / 2), ctx->stream);
+    end_span(ctx, FA_KERNEL_ROPE_TABLE);
+    HIP_TRY(hipGetLastError());
+    if (int rc = enqueue_decode(ctx, &p, table, q, k_pool, v_pool, out_lse, lay)) return rc;
     return ok();
 }
 

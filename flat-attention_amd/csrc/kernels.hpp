@@ -119,6 +119,15 @@ struct RopeFreqs {
     float inv_freq[64];
 };
 void launch_rope_table(float2* table, const RopeFreqs& f, int rows, int half, hipStream_t s);
+// (cos, sin) rows of n listed positions: table[i*half + p] for position positions[i], with the
+// same angle expression as launch_rope_table (bitwise equal rows).
+void launch_rope_rows(float2* table, const RopeFreqs& f, const int* positions, int n, int half,
+                      hipStream_t s);
+
+// Allocation-free paged decode: size of the per-device static scratch array and its device
+// address (resolved once per device with hipGetSymbolAddress; never the array's host-side name).
+constexpr size_t kNoAllocScratchBytes = (size_t)64 << 20;
+hipError_t noalloc_scratch(int device, void** out);
 
 // Scatter `append_len` rows per sequence into the page pool, optionally rotating K rows.
 struct AppendArgs {

@@ -27,6 +27,23 @@ void launch_rope_table(float2* table, const RopeFreqs& f, int rows, int half, hi
     rope_table_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(table, f, rows, half);
 }
 
+__global__ void rope_rows_kernel(float2* table, RopeFreqs f, const int* positions, int n,
+                                 int half) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (int64_t)n * half) return;
+    const int r = (int)(i / half), p = (int)(i % half);
+    const float angle = (float)positions[r] * f.inv_freq[p];
+    float s, c;
+    sincosf(angle, &s, &c);
+    table[i] = make_float2(c, s);
+}
+
+void launch_rope_rows(float2* table, const RopeFreqs& f, const int* positions, int n, int half,
+                      hipStream_t s) {
+    const int64_t m = (int64_t)n * half;
+    rope_rows_kernel<<<(unsigned)((m + 255) / 256), 256, 0, s>>>(table, f, positions, n, half);
+}
+
 // Load / rotate / store 8 consecutive elements (4 pairs) of one head.
 template <typename T>
 __device__ __forceinline__ void copy8(const uint8_t* src, uint8_t* dst, const float2* cs) {

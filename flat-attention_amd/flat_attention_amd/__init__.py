@@ -23,6 +23,7 @@ from .api import (AsymmetricGroupedAttentionShape, AsymmetricRotaryEmbeddingConf
                   HipBackwardRecomputePipeline, pack_backward_recompute_inputs,
                   bf16_bits_to_f32, download_attention,
                   f32_to_bf16_bits, host_storage, packed_layout, paged_append_batched,
+                  paged_decode_noalloc,
                   storage_np_dtype, storage_to_f32)
 
 __all__ = [n for n in dir() if not n.startswith("_")]

@@ -34,6 +34,7 @@ STATUS = {
     27: "CausalVisibilityMismatch", 28: "ZeroQueryChunkSize", 29: "UnsupportedDtype",
     30: "InvalidPage", 31: "EmptyCache", 32: "InvalidCacheLength", 33: "ForeignBuffer", 40: "PagedZeroDimension", 41: "CapacityOverflow",
     42: "CapacityExceeded", 43: "GenerationOverflow", 50: "NullArgument", 60: "Hip",
+    61: "ScratchExceeded",
 }
 
 KERNEL_IDS = {
@@ -170,6 +171,9 @@ PROTOTYPES = {
     "fa_paged_decode_plan_destroy": (INT, [VP]),
     "fa_paged_decode_plan_info": (INT, [VP, P(U64), P(U64), P(U64)]),
     "fa_paged_decode_plan_set_split": (INT, [VP, VP, U64]),
+    "fa_paged_decode_noalloc": (INT, [VP, VP, U64, VP, VP, U64, U64, U64, U64, U64, U64,
+                                      P(ConfigC),
+                                      F32, INT, VP, SZ, VP, VP, SZ, VP, SZ]),
     "fa_paged_cache_decode": (INT, [VP, VP, VP, SZ, U64, P(ConfigC), F32, U64, VP, SZ]),
     "fa_forward_projection_variable": (INT, [VP, VP, SZ, VP, VP, SZ, VP, SZ, P(AsymmetricShapeC),
                                              P(VariableSequenceC), U64, P(ConfigC), F32, U64,

@@ -768,6 +768,27 @@ class PagedDecodePlan:
                                            out_and_lse.nbytes))
 
 
+def paged_decode_noalloc(ctx: HipContext, block_tables: np.ndarray, ctx_lens: np.ndarray,
+                         page_size: int, physical_pages: int, q_heads: int, kv_heads: int,
+                         head_dim: int, config: FlatAttentionConfig, theta: float, dtype: int,
+                         q: DeviceBuffer, k_pool: DeviceBuffer, v_pool: DeviceBuffer,
+                         out_and_lse: DeviceBuffer,
+                         q_positions: Optional[np.ndarray] = None) -> PackedLayout:
+    """Allocation-free batched paged decode (no reference counterpart): PagedDecodePlan's
+    prepare + launch in one call whose device state lives in the library's static per-device
+    scratch. Calls that overlap on one GPU race."""
+    bt = np.ascontiguousarray(block_tables, np.int32)
+    cl = np.ascontiguousarray(ctx_lens, np.int32)
+    qp = None if q_positions is None else np.ascontiguousarray(q_positions, np.int32)
+    check(lib().fa_paged_decode_noalloc(
+        ctx.handle, bt.ctypes.data, bt.shape[1], cl.ctypes.data,
+        None if qp is None else qp.ctypes.data, cl.shape[0], page_size, physical_pages, q_heads,
+        kv_heads, head_dim, ctypes.byref(config.c()), theta, dtype, q.ptr, q.nbytes, k_pool.ptr,
+        v_pool.ptr, min(k_pool.nbytes, v_pool.nbytes), out_and_lse.ptr, out_and_lse.nbytes))
+    n = cl.shape[0] * q_heads
+    return packed_layout(n * head_dim, n, dtype)
+
+
 class HipPagedDecodePipeline:
     """WgpuPagedDecodePipeline src/wgpu_paged_decode.rs:244 (single sequence over a cache)."""
 

@@ -77,7 +77,8 @@ typedef enum fa_status {
     FA_ERR_CAPACITY_EXCEEDED = 42,
     FA_ERR_GENERATION_OVERFLOW = 43,
     FA_ERR_NULL_ARGUMENT = 50,
-    FA_ERR_HIP = 60
+    FA_ERR_HIP = 60,
+    FA_ERR_SCRATCH_EXCEEDED = 61  /* no reference variant: fa_paged_decode_noalloc's scratch */
 } fa_status;
 
 /* Storage dtype of Q/K/V/O. Math is always f32 (f32 online-softmax state, f32 accumulation);
@@ -344,6 +345,26 @@ int fa_paged_decode_plan_info(const fa_decode_plan* plan, uint64_t* split_tokens
 /* Override tokens per split (multiple of 16; 0 = automatic) before launch. Tests use this to
  * check split invariance. */
 int fa_paged_decode_plan_set_split(fa_ctx* ctx, fa_decode_plan* plan, uint64_t split_tokens);
+
+/* Allocation-free paged decode. No counterpart in the reference: it is for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc). Same arguments, validation and results (bitwise) as
+ * fa_paged_decode_prepare followed by fa_paged_decode_launch with the automatic split, in one
+ * call that allocates no device or pinned host memory: the block tables, lengths, query
+ * positions, work list, the queries' RoPE (cos, sin) rows and the split-K partials live in a
+ * static per-device scratch array of 64 MiB (4 MiB of it for tables and work lists), which each
+ * GPU holds until the process ends. A call needing more fails with FA_ERR_SCRATCH_EXCEEDED
+ * before any device work. The metadata reaches the scratch by a stream-ordered copy from a
+ * host area owned by the context; a call waits only until the previous call's copy has left
+ * that area. Every call on one GPU shares that GPU's scratch: calls that overlap on one GPU
+ * (other contexts, other streams) race. */
+int fa_paged_decode_noalloc(fa_ctx* ctx, const int32_t* block_tables, uint64_t max_pages,
+                            const int32_t* ctx_lens, const int32_t* q_positions, uint64_t n_seqs,
+                            uint64_t page_size, uint64_t physical_pages, uint64_t q_heads,
+                            uint64_t kv_heads, uint64_t head_dim, const fa_config* config,
+                            float theta, int dtype, const void* q, size_t q_bytes,
+                            const void* k_pool, const void* v_pool, size_t pool_bytes,
+                            void* out_lse, size_t out_bytes);
 
 /* Single-sequence convenience mirror of WgpuPagedDecodePipeline::encode: decode one query
  * vector over `cache` at `q_rope_position`. */
