@@ -74,13 +74,19 @@ def bf16_normal(rng, n):
     return fa.f32_to_bf16_bits(rng.standard_normal(n, dtype=np.float32))
 
 
-def build_prefill(ctx, rng):
+def build_prefill(ctx, rng, data="normal"):
     B, hq, hkv, S, D = 2, 32, 8, 4096, 128
     shape = fa.GroupedAttentionShape(B, hq, hkv, S, D)
     ex = fa.HipRotaryGroupedAttention(ctx, fa.DTYPE_BF16)
-    q = fa.DeviceBuffer.from_array(ctx, bf16_normal(rng, shape.q_tensor_len()))
-    k = fa.DeviceBuffer.from_array(ctx, bf16_normal(rng, shape.kv_tensor_len()))
-    v = fa.DeviceBuffer.from_array(ctx, bf16_normal(rng, shape.kv_tensor_len()))
+    if data == "constant":
+        # power-limit diagnostic: the same instruction stream and memory traffic on data whose
+        # MFMA operands never toggle
+        fill = lambda n: fa.f32_to_bf16_bits(np.full(n, 0.5, np.float32))  # noqa: E731
+    else:
+        fill = lambda n: bf16_normal(rng, n)  # noqa: E731
+    q = fa.DeviceBuffer.from_array(ctx, fill(shape.q_tensor_len()))
+    k = fa.DeviceBuffer.from_array(ctx, fill(shape.kv_tensor_len()))
+    v = fa.DeviceBuffer.from_array(ctx, fill(shape.kv_tensor_len()))
     out = fa.DeviceBuffer(ctx, ex.layout(shape).combined_bytes)
     cfg = fa.FlatAttentionConfig(causal=True)
     rot = fa.RotaryEmbeddingConfig(10000.0, 0)
@@ -530,6 +536,9 @@ def main():
                     help="also time configs[1] (f32 MHA) and configs[4] (chunked paged prefill)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run one device copy of 1 GiB (counter calibration for --pmc runs)")
+    ap.add_argument("--data", choices=["normal", "constant"], default="normal",
+                    help="prefill inputs: N(0,1) (the benchmark), or a constant 0.5 everywhere "
+                         "(power-limit diagnostic; not a benchmark figure)")
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="turn two rocprofv3 --pmc counter CSVs into the traffic summary")
     args = ap.parse_args()
@@ -561,7 +570,7 @@ def main():
     stream = ctx.stream
     ops = []
     if args.only in (None, "prefill"):
-        ops.append(("prefill",) + build_prefill(ctx, rng))
+        ops.append(("prefill",) + build_prefill(ctx, rng, args.data))
     if args.only in (None, "decode"):
         ops.append(("decode",) + build_decode(ctx, rng, args.decode_split))
     ctx.synchronize()
@@ -607,7 +616,9 @@ def main():
     out = {"metric": "causal GQA prefill TFLOP/s (D128,N4096) + paged-decode HBM GB/s, % of peak",
            "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
            "ms_per_step": round(step_ms, 4), "higher_is_better": True, "scaling": "weak",
-           "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+           "vs_baseline": None, "dtype": "bf16",
+           "data": "synthetic" if args.data == "normal" else
+                   "synthetic constant 0.5 (power-limit diagnostic, not the benchmark)",
            "wall_s": round(wall, 3)}
     details = {}
     traffic = load_traffic()

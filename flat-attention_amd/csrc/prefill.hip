@@ -239,19 +239,32 @@ __global__ __launch_bounds__(64 * NW, SPLIT ? 1 : 2) void prefill_mfma16(Prefill
     const int n_blk = __builtin_amdgcn_readfirstlane((n_keys_blk + BN - 1) / BN);
     (void)n_blk;
 
-    // ---- Q^T operand, rotated in registers: lane holds Q[row][16ks + 8g .. +8].
+    // ---- Q^T operand, rotated in registers: lane holds Q[row][16ks + 8g .. +8]. The ping-pong
+    // kernel issues these loads after the first K tile's transfer, so the two latencies overlap.
     u32x4_t qop[KS];
     u32x4_t qlo[SPLIT ? KS : 1];
-    {
+    auto load_q = [&]() {
         const uint16_t* qrow = (const uint16_t*)a.q + (int64_t)b * a.q_sb + (int64_t)hq * a.q_sh +
                                (int64_t)t * a.q_ss;
         const float2* cs_row =
             a.rope_q ? a.rope_table + (int64_t)(q_rope_off_ + t) * half : nullptr;
+        // every Q and (cos, sin) load is issued before the first rotation: one round trip
+        u32x4_t rawv[KS];
+        f32x4_t c0v[KS], c1v[KS];
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
             const int d0 = 16 * ks + 8 * g;
-            u32x4_t raw = {0u, 0u, 0u, 0u};
-            if (FULLD || d0 < D) raw = *(const u32x4_t*)(qrow + d0);
+            rawv[ks] = u32x4_t{0u, 0u, 0u, 0u};
+            if (FULLD || d0 < D) rawv[ks] = *(const u32x4_t*)(qrow + d0);
+            if (a.rope_q && (FULLD || d0 < D)) {
+                c0v[ks] = *(const f32x4_t*)(cs_row + d0 / 2);
+                c1v[ks] = *(const f32x4_t*)(cs_row + d0 / 2 + 2);
+            }
+        }
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            const int d0 = 16 * ks + 8 * g;
+            u32x4_t raw = rawv[ks];
             if (a.rope_q && (FULLD || d0 < D)) {
                 float x[8];
 #pragma unroll
@@ -259,8 +272,7 @@ __global__ __launch_bounds__(64 * NW, SPLIT ? 1 : 2) void prefill_mfma16(Prefill
                     x[2 * j] = H::lo(raw[j]);
                     x[2 * j + 1] = H::hi(raw[j]);
                 }
-                const f32x4_t c0 = *(const f32x4_t*)(cs_row + d0 / 2);
-                const f32x4_t c1 = *(const f32x4_t*)(cs_row + d0 / 2 + 2);
+                const f32x4_t c0 = c0v[ks], c1 = c1v[ks];
                 float cs[8] = {c0[0], c0[1], c0[2], c0[3], c1[0], c1[1], c1[2], c1[3]};
                 rope4(x, cs);
 #pragma unroll
@@ -275,7 +287,8 @@ __global__ __launch_bounds__(64 * NW, SPLIT ? 1 : 2) void prefill_mfma16(Prefill
             }
             qop[ks] = raw;
         }
-    }
+    };
+    if constexpr (!(DMA && PP)) load_q();
 
     // ---- global -> register staging of one K/V tile.
     // Buffer loads: a scalar resource (base + byte range) plus a 32-bit per-lane offset. Reads
@@ -738,6 +751,7 @@ __global__ __launch_bounds__(64 * NW, SPLIT ? 1 : 2) void prefill_mfma16(Prefill
                 __syncthreads();
             };
             if (n_blk > 0 && xfer) dma_k(0, 0);
+            load_q();
             wait_dma();
             __syncthreads();
             int m = 0;
