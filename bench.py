@@ -213,7 +213,7 @@ def build_resident_decode(ctx, rng, dtype):
     return (lambda: plan.launch(q, k, v, out)), nbytes
 
 
-def build_backward(ctx, rng, S=4096):
+def build_backward(ctx, rng, S=4096, data="normal"):
     """Recompute backward (dQ, dK, dV) at the prefill's shape without RoPE (the reference's
     backward has none): causal GQA B2 Hq32 Hkv8 D128 bf16. Algorithmic work: the five
     S x S x D products of attention backward (Q K^T, dO V^T, P^T dO, dS^T Q, dS K), i.e. 2.5x
@@ -226,7 +226,8 @@ def build_backward(ctx, rng, S=4096):
     nq, nkv = lay.q_elements, lay.kv_elements
     for off, n in ((lay.q_offset, nq), (lay.k_offset, nkv), (lay.v_offset, nkv),
                    (lay.d_out_offset, nq)):
-        fwd.upload(bf16_normal(rng, n), off)
+        fwd.upload(bf16_normal(rng, n) if data == "normal"
+                   else fa.f32_to_bf16_bits(np.full(n, 0.5, np.float32)), off)
     cfg = fa.FlatAttentionConfig(causal=True)
     # O and LSE from this library's forward over the same Q, K, V
     ex = fa.HipRotaryGroupedAttention(ctx, fa.DTYPE_BF16)
@@ -248,24 +249,22 @@ def build_backward(ctx, rng, S=4096):
     return (lambda: pipe.encode_prepared(prep)), flop
 
 
-def measure_backward(ctx, rng, steps, warmup):
+def measure_backward(ctx, rng, steps, warmup, data="normal"):
     """`--only backward`: the recompute backward alone, op time from HIP events on the library's
-    stream, the three kernels' time from the library's per-dispatch events."""
-    run, flop = build_backward(ctx, rng)
+    stream and the three kernels' time from the library's per-dispatch events, in one pass."""
+    run, flop = build_backward(ctx, rng, data=data)
     ev = HipEvents()
     for _ in range(warmup):
         run()
     tel = ctx.last_telemetry()
     ctx.synchronize()
     a, b = ev.create(), ev.create()
+    ctx.set_kernel_timing(True)
     ev.record(a, ctx.stream)
     for _ in range(steps):
         run()
     ev.record(b, ctx.stream)
     op_ms = ev.elapsed_ms(a, b) / steps
-    ctx.set_kernel_timing(True)
-    for _ in range(steps):
-        run()
     total, cnt = ctx.kernel_timing(tel.kernel_id)
     ctx.set_kernel_timing(False)
     k_ms = total / max(cnt, 1)
@@ -273,7 +272,9 @@ def measure_backward(ctx, rng, steps, warmup):
     return {"metric": "recompute backward (dQ, dK, dV) TFLOP/s, causal GQA D128 N4096",
             "value": round(tf, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": steps,
             "warmup": warmup, "ms_per_step": round(op_ms, 4), "higher_is_better": True,
-            "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+            "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+            "data": "synthetic" if data == "normal" else
+                    "synthetic constant 0.5 (power-limit diagnostic, not the benchmark)",
             "config": {"workload": "recompute backward: causal GQA B2 Hq32 Hkv8 N4096 D128 bf16",
                        "flop_per_step": flop, "parallelism": "single GPU"},
             "kernel": tel.kernel_name, "kernel_ms": round(k_ms, 4),
@@ -537,7 +538,7 @@ def main():
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run one device copy of 1 GiB (counter calibration for --pmc runs)")
     ap.add_argument("--data", choices=["normal", "constant"], default="normal",
-                    help="prefill inputs: N(0,1) (the benchmark), or a constant 0.5 everywhere "
+                    help="prefill and backward inputs: N(0,1) (the benchmark), or a constant 0.5 everywhere "
                          "(power-limit diagnostic; not a benchmark figure)")
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="turn two rocprofv3 --pmc counter CSVs into the traffic summary")
@@ -558,7 +559,7 @@ def main():
     rng = np.random.default_rng(1234)
     ctx = fa.HipContext(0)
     if args.only == "backward":
-        out = measure_backward(ctx, rng, args.steps, args.warmup)
+        out = measure_backward(ctx, rng, args.steps, args.warmup, args.data)
         if not args.no_cpu_baseline:
             out["cpu_baseline"] = cpu_baseline_backward()
         print(json.dumps(out))
