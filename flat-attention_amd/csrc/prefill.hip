@@ -125,8 +125,9 @@ __device__ __forceinline__ int64_t paged_row(const PrefillKArgs& ka, int b, int 
 // The 8-wave ping-pong kernel (contiguous K/V moved by buffer->LDS transfers, K not rotated in
 // the kernel): two groups of four waves kept in opposite phases, one group's MFMAs against the
 // other group's softmax.
+// (kPaged16: the transferring group stages the paged K/V tiles through registers)
 __host__ __device__ constexpr bool prefill_pingpong(int pmode, bool ropek) {
-    return (pmode == kContig || pmode == kContigVT) && !ropek;
+    return (pmode == kContig || pmode == kContigVT || pmode == kPaged16) && !ropek;
 }
 
 // Scheduling groups (LLVM AMDGPU sched_group_barrier masks: 0x2 VALU, 0x8 MFMA, 0x100 DS read, 0x400 transcendental).
@@ -300,7 +301,9 @@ __global__ __launch_bounds__(64 * NW, SPLIT ? 1 : 2) void prefill_mfma16(Prefill
         (int64_t)kvh * a.k_sh * 2 + (CONTIG ? (int64_t)b * a.k_sb * 2 : 0);
     const uint8_t* const kb8 = (const uint8_t*)a.k + head_off;
     const uint8_t* const vb8 = (const uint8_t*)a.v + head_off;
-    const int k_dc = tid % CPR, k_r = tid / CPR;
+    // (ping-pong: the 256 threads of the transferring group 1 stage the tiles)
+    const int tst = PP ? (tid & 255) : tid;
+    const int k_dc = tst % CPR, k_r = tst / CPR;
     const uint32_t kd2 = (uint32_t)(FULLD ? k_dc * 8 : min(k_dc * 8, D - 8)) * 2u;
     const uint32_t lane_off = (uint32_t)k_r * row_bytes + kd2;  // this thread's row/chunk
     constexpr int kRsrcFlags = 0x00020000;
@@ -624,7 +627,7 @@ __global__ __launch_bounds__(64 * NW, SPLIT ? 1 : 2) void prefill_mfma16(Prefill
     using NoMask = std::integral_constant<bool, false>;
     using Mask = std::integral_constant<bool, true>;
 
-    if constexpr (DMA) {
+    if constexpr (DMA || PP) {
         // Per-lane byte offsets of this wave's DMA instructions (k = wave + 4 i fills slots
         // 64 k .. 64 k + 63 of the tile: row q / SL, slot q % SL), constant across tiles.
         constexpr uint32_t kOob = 0x7fff0000u;
@@ -740,19 +743,47 @@ __global__ __launch_bounds__(64 * NW, SPLIT ? 1 : 2) void prefill_mfma16(Prefill
             // has slack, the MFMA stream of group 0 is left alone.
             // group 1 issues the transfers
             const bool xfer = grp == 1;
+            // Paged K/V (kPaged16) take the same schedule through registers: group 1 loads
+            // K(m+1) and V(m) at phase 2m and stores them to their slots at the end of phase
+            // 2m+1, before the barrier.
             auto start_dma = [&](int m) {
                 if (!xfer) return;
-                if (m + 1 < n_blk) dma_k(m + 1, ((m + 1) & 1) * STAGE);
-                if (m < n_blk) dma_v(m, (m & 1) * STAGE);
+                if constexpr (DMA) {
+                    if (m + 1 < n_blk) dma_k(m + 1, ((m + 1) & 1) * STAGE);
+                    if (m < n_blk) dma_v(m, (m & 1) * STAGE);
+                } else {
+                    if (m + 1 < n_blk) load_one(m + 1, kb8, kreg);
+                    if (m < n_blk) load_one(m, vb8, vreg);
+                }
             };
             auto end_even = [&]() { __syncthreads(); };
-            auto end_odd = [&]() {
-                wait_dma();
+            auto end_odd = [&](int m) {
+                if constexpr (DMA) {
+                    wait_dma();
+                } else if (xfer) {
+                    if (m + 1 < n_blk) {
+                        st_w = ((m + 1) & 1) * STAGE;
+                        store_k(m + 1);
+                    }
+                    if (m < n_blk) {
+                        st_w = (m & 1) * STAGE;
+                        store_v();
+                    }
+                }
                 __syncthreads();
             };
-            if (n_blk > 0 && xfer) dma_k(0, 0);
-            load_q();
-            wait_dma();
+            if constexpr (DMA) {
+                if (n_blk > 0 && xfer) dma_k(0, 0);
+                load_q();
+                wait_dma();
+            } else {
+                if (n_blk > 0 && xfer) load_one(0, kb8, kreg);
+                load_q();
+                if (n_blk > 0 && xfer) {
+                    st_w = 0;
+                    store_k(0);
+                }
+            }
             __syncthreads();
             int m = 0;
             const int n = n_tiles;  // this group's tiles (<= n_blk)
@@ -763,24 +794,24 @@ __global__ __launch_bounds__(64 * NW, SPLIT ? 1 : 2) void prefill_mfma16(Prefill
                     mfma_phase(0, F_{}, T_{});
                     end_even();
                     softmax_phase(0);
-                    end_odd();
+                    end_odd(m);
                     for (m = 1; m < n; ++m) {
                         start_dma(m);
                         mfma_phase(m, T_{}, T_{});
                         end_even();
                         softmax_phase(m);
-                        end_odd();
+                        end_odd(m);
                     }
                     start_dma(m);
                     mfma_phase(m, T_{}, F_{});
                     end_even();
-                    end_odd();
+                    end_odd(m);
                     ++m;
                 }
                 for (; m <= n_blk; ++m) {  // fewer tiles than group 1: keep meeting the barriers
                     start_dma(m);
                     end_even();
-                    end_odd();
+                    end_odd(m);
                 }
             } else {
                 // group 1: one phase behind (softmax in even phases, MFMAs in odd phases)
@@ -788,25 +819,25 @@ __global__ __launch_bounds__(64 * NW, SPLIT ? 1 : 2) void prefill_mfma16(Prefill
                     start_dma(0);
                     end_even();
                     mfma_phase(0, F_{}, T_{});
-                    end_odd();
+                    end_odd(m);
                     for (m = 1; m < n; ++m) {
                         start_dma(m);
                         softmax_phase(m - 1);
                         end_even();
                         mfma_phase(m, T_{}, T_{});
-                        end_odd();
+                        end_odd(m);
                     }
                     start_dma(m);
                     softmax_phase(m - 1);
                     end_even();
                     mfma_phase(m, T_{}, F_{});
-                    end_odd();
+                    end_odd(m);
                     ++m;
                 }
                 for (; m <= n_blk; ++m) {  // no tiles left: keep transferring, meet the barriers
                     start_dma(m);
                     end_even();
-                    end_odd();
+                    end_odd(m);
                 }
             }
         } else {
@@ -1194,7 +1225,7 @@ void launch_prefill(Dtype dt, bool paged, const PrefillArgs& a, hipStream_t s, u
     const int dpad = a.head_dim <= 32 ? 32 : (a.head_dim <= 64 ? 64 : 128);
     const int rows_total = a.q_len * a.group;
     // 16-bit contiguous K/V without in-kernel K rotation runs 256-row ping-pong workgroups
-    const bool pp = dt != Dtype::F32 && !paged && !a.rope_k;
+    const bool pp = dt != Dtype::F32 && !a.rope_k && (!paged || a.page_size % 16 == 0);
     const int bm = pp ? 256 : 128;
     const int nqb = (rows_total + bm - 1) / bm;
     dim3 g((unsigned)((int64_t)a.batch * a.kv_heads * nqb));
