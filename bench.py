@@ -258,13 +258,7 @@ def measure_backward(ctx, rng, steps, warmup, data="normal"):
         run()
     tel = ctx.last_telemetry()
     ctx.synchronize()
-    a, b = ev.create(), ev.create()
-    ctx.set_kernel_timing(True)
-    ev.record(a, ctx.stream)
-    for _ in range(steps):
-        run()
-    ev.record(b, ctx.stream)
-    op_ms = ev.elapsed_ms(a, b) / steps
+    op_ms = alternate_timing(ctx, ev, run, steps)
     total, cnt = ctx.kernel_timing(tel.kernel_id)
     ctx.set_kernel_timing(False)
     k_ms = total / max(cnt, 1)
@@ -283,6 +277,23 @@ def measure_backward(ctx, rng, steps, warmup, data="normal"):
                          "traffic": None}}
 
 
+def alternate_timing(ctx, ev, run, steps):
+    """`steps` calls of `run` in one pass: odd calls bracketed by HIP events only (op time),
+    even calls with the library's per-dispatch events too (kernel times). Returns the mean op
+    time in ms; the kernel totals stay in the context."""
+    evs = [(ev.create(), ev.create()) for _ in range(steps)]
+    ctx.set_kernel_timing(True)
+    for s in range(steps):
+        ctx.pause_kernel_timing(s % 2 == 1)
+        ev.record(evs[s][0], ctx.stream)
+        run()
+        ev.record(evs[s][1], ctx.stream)
+    ctx.pause_kernel_timing(False)
+    ctx.synchronize()
+    op_steps = [s for s in range(steps) if s % 2 == 1] or list(range(steps))
+    return float(np.mean([ev.elapsed_ms(*evs[s]) for s in op_steps]))
+
+
 def measure_all_configs(ctx, ev, rng, steps):
     """The other BASELINE configs, each timed alone (op events + its kernel's own events)."""
     stream = ctx.stream
@@ -294,13 +305,7 @@ def measure_all_configs(ctx, ev, rng, steps):
             run()
         tel = ctx.last_telemetry()
         ctx.synchronize()
-        ctx.set_kernel_timing(True)
-        a, b = ev.create(), ev.create()
-        ev.record(a, stream)
-        for _ in range(steps):
-            run()
-        ev.record(b, stream)
-        op_ms = ev.elapsed_ms(a, b) / steps
+        op_ms = alternate_timing(ctx, ev, run, steps)
         total, cnt = ctx.kernel_timing(tel.kernel_id)
         ctx.set_kernel_timing(False)
         return op_ms, total / max(cnt, 1), tel
@@ -583,13 +588,15 @@ def main():
             tele[name] = ctx.last_telemetry()
     ctx.synchronize()
 
-    # One timed pass: HIP events around each op on the library's stream, and the library's own
-    # per-dispatch events (fa_ctx_set_kernel_timing) around every kernel inside it, so the op
-    # times and the dominant kernels' times describe the same steps at the same clocks.
+    # One timed pass of alternating steps: odd steps carry only HIP events around each op on
+    # the library's stream (the op times), even steps also the library's own per-dispatch
+    # events around every kernel (fa_ctx_set_kernel_timing; they add a few µs between kernels,
+    # so they stay out of the op times). Both describe the same run at the same clocks.
     evs = [[ev.create() for _ in range(len(ops) + 1)] for _ in range(args.steps)]
     ctx.set_kernel_timing(True)
     t_wall = time.perf_counter()
     for s in range(args.steps):
+        ctx.pause_kernel_timing(s % 2 == 1)
         ev.record(evs[s][0], stream)
         for i, (name, run, _, _) in enumerate(ops):
             run()
@@ -610,7 +617,8 @@ def main():
         ctx.synchronize()
         a.free()
         b.free()
-    per_op = {name: [ev.elapsed_ms(evs[s][i], evs[s][i + 1]) for s in range(args.steps)]
+    op_steps = [s for s in range(args.steps) if s % 2 == 1] or list(range(args.steps))
+    per_op = {name: [ev.elapsed_ms(evs[s][i], evs[s][i + 1]) for s in op_steps]
               for i, (name, _, _, _) in enumerate(ops)}
     step_ms = sum(np.mean(v) for v in per_op.values())
 

@@ -190,6 +190,7 @@ struct fa_ctx {
         hipEvent_t begin, end;
     };
     bool timing = false;
+    bool timing_paused = false;  // fa_ctx_pause_kernel_timing
     hipEvent_t open_begin = nullptr;
     std::vector<hipEvent_t> free_events;
     std::vector<Span> pending;
@@ -259,7 +260,7 @@ hipEvent_t take_event(fa_ctx* ctx) {
 }
 
 void begin_span(fa_ctx* ctx) {
-    if (!ctx->timing) return;
+    if (!ctx->timing || ctx->timing_paused) return;
     hipEvent_t e = take_event(ctx);
     if (e && hipEventRecord(e, ctx->stream) != hipSuccess) {
         ctx->free_events.push_back(e);
@@ -269,7 +270,7 @@ void begin_span(fa_ctx* ctx) {
 }
 
 void end_span(fa_ctx* ctx, int kernel_id) {
-    if (!ctx->timing || !ctx->open_begin) return;
+    if (!ctx->timing || ctx->timing_paused || !ctx->open_begin) return;
     hipEvent_t e = take_event(ctx);
     if (!e || hipEventRecord(e, ctx->stream) != hipSuccess) {
         ctx->free_events.push_back(ctx->open_begin);
@@ -561,6 +562,13 @@ int fa_ctx_set_kernel_timing(fa_ctx* ctx, int32_t enable) {
     if (int rc = resolve_spans(ctx)) return rc;
     ctx->timed.clear();
     ctx->timing = enable != 0;
+    ctx->timing_paused = false;
+    return ok();
+}
+
+int fa_ctx_pause_kernel_timing(fa_ctx* ctx, int32_t paused) {
+    if (!ctx) return fail(FA_ERR_NULL_ARGUMENT, "context is null");
+    ctx->timing_paused = paused != 0;
     return ok();
 }
 

@@ -205,6 +205,7 @@ PROTOTYPES = {
                                   P(ConfigC), INT]),
     "fa_last_telemetry": (INT, [VP, P(TelemetryC)]),
     "fa_ctx_set_kernel_timing": (INT, [VP, I32]),
+    "fa_ctx_pause_kernel_timing": (INT, [VP, I32]),
     "fa_ctx_set_prefill_precision": (INT, [VP, I32]),
     "fa_ctx_set_decode_policy": (INT, [VP, I32]),
     "fa_ctx_kernel_timing": (INT, [VP, I32, P(ctypes.c_double), P(U64)]),

@@ -267,6 +267,10 @@ class HipContext:
         """Bracket every dispatch with HIP events on the context's stream (clears totals)."""
         check(lib().fa_ctx_set_kernel_timing(self.handle, 1 if enable else 0))
 
+    def pause_kernel_timing(self, paused: bool):
+        """Stop (or resume) bracketing dispatches with events, keeping the totals; never waits."""
+        check(lib().fa_ctx_pause_kernel_timing(self.handle, 1 if paused else 0))
+
     def kernel_timing(self, kernel_id) -> tuple[float, int]:
         """(total ms, dispatch count) of one kernel since timing was enabled. `kernel_id` is an
         fa_kernel_id number or its name (e.g. "DecodePagedMfma")."""

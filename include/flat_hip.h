@@ -535,6 +535,11 @@ int fa_kernel_variant_for_shape(fa_ctx* ctx, uint64_t head_dim, int32_t has_rope
  * durations). While enabled, every dispatch the context issues is bracketed by HIP events on
  * the context's stream. Enabling (or disabling) clears the accumulated totals. */
 int fa_ctx_set_kernel_timing(fa_ctx* ctx, int32_t enable);
+/* Pauses (paused != 0) or resumes per-dispatch timing without waiting for the stream and
+ * without clearing the totals: dispatches issued while paused carry no events. Lets a caller
+ * time whole operations (its own events, no per-kernel events inside) and their kernels in
+ * alternate steps of one run. No effect while timing is disabled. */
+int fa_ctx_pause_kernel_timing(fa_ctx* ctx, int32_t paused);
 /* Waits for the context's stream, then returns the summed duration (ms) and the number of
  * timed dispatches of `kernel_id` (an fa_kernel_id naming one kernel: a prefill variant id
  * names the prefill kernel alone, FA_KERNEL_ROPE_ROTATE the K pre-rotation pass,

@@ -444,7 +444,8 @@ def _paged_prefill(hip, bt, ps, total, n_seqs, hq, hkv, D, cached, ql, theta, ra
 @pytest.mark.parametrize("D,causal", [(128, True), (64, True), (128, False)])
 def test_paged_prefill_modes_match_oracle_and_gather_bit_exactly(hip, dtype, ps, D, causal):
     """Chunked prefill over the paged cache in every addressing mode: 16-bit with page size a
-    multiple of 16 (one page per 16-key group), 16-bit with any page size, and f32. A query
+    multiple of 16 (one page per 16-key group, 8-wave ping-pong kernel), 16-bit with any page
+    size (4-wave kernel), and f32. A query
     chunk of 50 rows after 37 cached tokens, so key tiles and pages end mid-way. The same
     data under the identity block table and a shuffled one must give bitwise identical O/LSE."""
     rnd = {fa.DTYPE_BF16: bf16_round, fa.DTYPE_F16: f16_round, fa.DTYPE_F32: lambda x: x}[dtype]
@@ -462,6 +463,8 @@ def test_paged_prefill_modes_match_oracle_and_gather_bit_exactly(hip, dtype, ps,
     shuf = rng.permutation(total)[:n_seqs * pages_per].astype(np.int32).reshape(n_seqs, pages_per)
     o1, l1 = _paged_prefill(hip, ident, ps, total, n_seqs, hq, hkv, D, cached, ql, theta, raw_k,
                             v, q, dtype, causal)
+    if dtype != fa.DTYPE_F32:  # page % 16 == 0: 8-wave ping-pong kernel; else the 4-wave one
+        assert hip.last_telemetry().workgroup_size == (512 if ps % 16 == 0 else 256)
     pools = []
     o2, l2 = _paged_prefill(hip, shuf, ps, total, n_seqs, hq, hkv, D, cached, ql, theta, raw_k,
                             v, q, dtype, causal, pools)
