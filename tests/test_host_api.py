@@ -203,6 +203,53 @@ def test_decode_prepare_validation_variants():
     assert _decode_prepare(bt, [40]) == "NullArgument"  # all valid, no context
 
 
+def _decode_noalloc(bt, lens, qpos=None, ps=16, pages=8, hq=4, hkv=2, D=64, theta=1e4,
+                    causal=True, dtype=fa.DTYPE_F32, q_bytes=None, pool_bytes=None,
+                    out_bytes=None):
+    """fa_paged_decode_noalloc with no context: every check before device work. The buffer
+    arguments are stand-in addresses that are never dereferenced (the call stops at the null
+    context, or earlier)."""
+    bt = np.ascontiguousarray(bt, np.int32)
+    lens = np.ascontiguousarray(lens, np.int32)
+    qp = None if qpos is None else np.ascontiguousarray(qpos, np.int32)
+    eb = 4 if dtype == fa.DTYPE_F32 else 2
+    n = lens.shape[0]
+    q_need = n * hq * D * eb
+    pool_need = pages * ps * hkv * D * eb
+    out_need = fa.packed_layout(n * hq * D, n * hq, dtype).combined_bytes
+    fake = ctypes.c_void_p(0x1000)
+    rc = fa.lib().fa_paged_decode_noalloc(
+        None, bt.ctypes.data, bt.shape[1], lens.ctypes.data,
+        None if qp is None else qp.ctypes.data, n, ps, pages, hq, hkv, D,
+        ctypes.byref(fa.FlatAttentionConfig(causal).c()), theta, dtype,
+        fake, q_need if q_bytes is None else q_bytes, fake, fake,
+        pool_need if pool_bytes is None else pool_bytes, fake,
+        out_need if out_bytes is None else out_bytes)
+    return _variant(rc)
+
+
+def test_noalloc_decode_validation_matches_prepare():
+    """The allocation-free decode validates exactly as fa_paged_decode_prepare (shared checks),
+    then its buffers, before it needs the context."""
+    bt = [[0, 1, 2]]
+    for kw in (dict(lens=[40], qpos=[20]), dict(lens=[0]), dict(lens=[49]),
+               dict(lens=[40], hq=6, hkv=4), dict(lens=[40], D=256), dict(lens=[40], D=63),
+               dict(lens=[40], theta=0.0), dict(lens=[40], ps=0)):
+        lens = kw.pop("lens")
+        assert _decode_noalloc(bt, lens, **kw) == _decode_prepare(bt, lens, **kw)
+    assert _decode_noalloc([[0, 9, 1]], [40]) == "InvalidPage"
+    assert _decode_noalloc(bt, [40], q_bytes=8) == "BufferTooSmall"
+    assert _decode_noalloc(bt, [40], pool_bytes=8) == "BufferTooSmall"
+    assert _decode_noalloc(bt, [40], out_bytes=8) == "BufferTooSmall"
+    assert _decode_noalloc(bt, [40]) == "NullArgument"  # all valid, no context
+    assert "context is null" in fa.lib().fa_last_error_message().decode()
+
+
+def test_kernel_timing_calls_need_a_context():
+    assert _variant(fa.lib().fa_ctx_pause_kernel_timing(None, 1)) == "NullArgument"
+    assert _variant(fa.lib().fa_ctx_set_kernel_timing(None, 1)) == "NullArgument"
+
+
 def _resident_prepare(batch=2, cap=64, kv_len=40, hq=4, hkv=2, D=64, theta=1e4, qpos=39,
                       causal=True, dtype=fa.DTYPE_F32):
     h = L.VP()
