@@ -5,9 +5,12 @@
 // The math is the online softmax of forward_reference (src/lib.rs:454-520): running max m,
 // running sum l, O accumulated with rescale alpha = exp(m_old - m_new), LSE = m + ln l.
 //
-// Workgroup = 4 waves = 128 query rows. Rows of one (batch, kv-head) are flattened as
-// row = t * group + head_in_group, so one workgroup holds every query head of a GQA group for
-// ceil(128/group) consecutive positions: each K/V tile staged in LDS feeds all of them.
+// Workgroup = 8 waves = 256 query rows in two groups of four on a ping-pong schedule (one
+// group's MFMAs against the other group's softmax) for contiguous K/V and for paged K/V with a
+// page size that is a multiple of 16; 4 waves = 128 rows otherwise (other page sizes, K rotated
+// in the kernel). Rows of one (batch, kv-head) are flattened as row = t * group +
+// head_in_group, so one workgroup holds every query head of a GQA group for consecutive
+// positions: each K/V tile staged in LDS feeds all of them.
 // Per 64-key tile and wave (32 rows):
 //   S^T[64 keys x 32 rows] = K_perm . Q^T      (K from LDS is the A operand, Q in registers)
 //   P^T = exp2((S - m) * scale * log2 e)       (every value a lane holds belongs to ONE row)
