@@ -536,6 +536,9 @@ def main():
     ap.add_argument("--only", choices=["prefill", "decode", "backward"], default=None,
                     help="time one op alone (backward: the recompute backward at the prefill "
                          "shape, a line of its own)")
+    ap.add_argument("--backward-policy", type=int, default=-1,
+                    help="--only backward: -1 stored dS (default), 0 dQ recomputes S and dP "
+                         "(fa_ctx_set_backward_policy)")
     ap.add_argument("--decode-split", type=int, default=None,
                     help="tokens per split-K partition of the decode plan (default: automatic)")
     ap.add_argument("--all-configs", action="store_true",
@@ -564,6 +567,7 @@ def main():
     rng = np.random.default_rng(1234)
     ctx = fa.HipContext(0)
     if args.only == "backward":
+        ctx.set_backward_policy(args.backward_policy)
         out = measure_backward(ctx, rng, args.steps, args.warmup, args.data)
         if not args.no_cpu_baseline:
             out["cpu_baseline"] = cpu_baseline_backward()

@@ -5,8 +5,11 @@
 //   bwd_delta  (LSE log2 e, delta = sum_d dO * O) per query row                   (HBM bound)
 //   bwd_dkdv   one workgroup per (batch, kv head, 128 keys); every query head of the group and
 //              every visible query tile is swept, so dK/dV of a KV head are summed over its
-//              query heads in registers (native KV-head cardinality, no expansion);
-//   bwd_dq     one workgroup per (batch, query head, 128 queries), sweeping the visible keys.
+//              query heads in registers (native KV-head cardinality, no expansion); with a dS
+//              workspace (16-bit storage) it also stores the dS of every block it computes;
+//   bwd_dq_ds  dQ = dS K from that workspace (HBM bound: 2 bytes of dS per (query, key) pair),
+//   or bwd_dq  one workgroup per (batch, query head, 128 queries), sweeping the visible keys
+//              and recomputing S and dP.
 // Per 32x32 (query, key) block: S = Q K^T and dP = dO V^T (K, V or Q, dO held in registers),
 // P = exp2(S * scale * log2 e - LSE * log2 e), dS = P (dP - delta), then dV += P^T dO,
 // dK += dS^T Q (bwd_dkdv) or dQ += dS K (bwd_dq); dK and dQ take the softmax scale at the end.
@@ -322,12 +325,13 @@ __global__ __launch_bounds__(256) void bwd_delta(BackwardArgs a, int64_t rows) {
 // One wave per SIMD (the K/V fragments and both accumulators take ~330 registers), so the
 // overlap has to come from this single instruction stream; scheduling group barriers keep the
 // compiler from separating the phases again.
-template <typename T, int DPAD, bool DMA>
+template <typename T, int DPAD, bool DMA, bool DSO = false>
 __global__ __launch_bounds__(256, 1) void bwd_dkdv(BackwardArgs a) {
     using B = Blk<T>;
     using F = typename B::Frag;
     constexpr int ES = B::ES, MB = DPAD / 32;
     constexpr bool PIPE = ES == 2;
+    static_assert(!DSO || (PIPE && DMA), "dS is stored by the 16-bit DMA kernel only");
     // 128 query rows per tile (16-bit; two stages of Q and dO in 130 KiB with the unpadded
     // swizzled rows at D 128), 64 for f32
     constexpr int QT = PIPE ? 128 : 64, NSUB = QT / 32;
@@ -411,6 +415,44 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv(BackwardArgs a) {
     Ops16<TG, B, MB> ops;
     if constexpr (PIPE) ops.init(lane);
 
+    // DSO: the dS of every sub-block goes to its block of a.ds (layout in BackwardArgs): the
+    // group of (head, tile qt / 128, key block k0 / 32), block sb. Lane l = 32 g + c holds key
+    // k0 + c for query rows kidx(g, t): half h of the fragment is rows 16 h + 8 g .. + 7, i.e.
+    // bytes 2048 sb + 1024 h + 16 l of the group, one 16-byte store each. Keys past the
+    // sequence are stored as computed (bwd_dq_ds zeroes them). The store keeps almost no state
+    // live across the products (this kernel holds ~450 registers): the group offset, one
+    // scalar per tile, goes into the buffer resource, whose range ends at the allocation (and
+    // is empty for a wave without keys, whose non-causal groups would alias the next tile's,
+    // so its stores are dropped); the lane offset is recomputed at every store. Group indices
+    // fit 32 bits (the allocation is under 2 GiB).
+    const uint32_t ds_nt = (uint32_t)(S + 127) >> 7;
+    const uint32_t ds_gph = DSO ? (a.causal ? 2u * ds_nt * (ds_nt + 1u) : ds_nt * (uint32_t)a.ds_nb)
+                                : 0u;
+    // byte offset of the group of tile (hh, qt)
+    auto ds_group_off = [&](int hh, int qt) {
+        const uint32_t t = (uint32_t)qt >> 7;
+        return ((uint32_t)(b * a.q_heads + kvh * G + hh) * ds_gph +
+                (a.causal ? 2u * t * (t + 1u) : t * (uint32_t)a.ds_nb) + ((uint32_t)k0 >> 5)) *
+               8192u;
+    };
+    auto store_ds = [&](uint32_t goff, int sb, const F& df) {
+        if constexpr (DSO) {
+            const int nrec = k0 < S ? a.ds_bytes - (int)goff : 0;
+            const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+                (uint8_t*)a.ds + goff, (short)0, nrec, 0x00020000);
+            uint32_t vo;
+            asm volatile(
+                "v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0\n\t"
+                "v_lshlrev_b32 %0, 4, %0"
+                : "=v"(vo));
+            // non-temporal (written once, read once by bwd_dq_ds): the 2 bytes per pair must
+            // not evict the Q / dO tiles the other key blocks reuse
+            __builtin_amdgcn_raw_buffer_store_b128(df.v[0], rs, (int)(vo + 2048u * sb), 0, 2);
+            __builtin_amdgcn_raw_buffer_store_b128(df.v[1], rs, (int)(vo + 2048u * sb + 1024u), 0,
+                                                   2);
+        }
+    };
+
     // Probabilities and dS of one sub-block from its S and dP accumulators; `diag`: the
     // sub-block on the causal diagonal (query q0 + kidx(g, t) against key q0 + c).
     auto softmax = [&](auto diag, const f32x16_t& s, const f32x16_t& dp, const float (&l2)[16],
@@ -444,6 +486,7 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv(BackwardArgs a) {
             __syncthreads();
         }
         const int qt = tile_row(j).second;
+        const uint32_t ds_goff = DSO ? ds_group_off(j / nqt, qt) : 0u;
         // active sub-blocks [s0, s1): causal skips the ones wholly before the wave's keys
         const int s0 = a.causal ? min(NSUB, max(0, (k0 - qt) >> 5)) : 0;
         const int s1 = min(NSUB, (S - qt + 31) >> 5);
@@ -528,13 +571,16 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv(BackwardArgs a) {
                 }
                 // phase Y: dV, dK of sb; (LSE, delta) rows of sb+1
                 dvdk(sb, pf, df);
-                if (next) load_ld(sb + 1, l2[u ^ 1], dl[u ^ 1]);
+                // unconditional (a branch would split these products from their schedule
+                // below); past the last active sub-block the rows read go unused
+                load_ld(sb + 1 < NSUB ? sb + 1 : sb, l2[u ^ 1], dl[u ^ 1]);
                 FA_BWD_SG(0x100, 2 * RV);
 #pragma unroll
                 for (int i = 0; i < NS; ++i) {
                     FA_BWD_SG(0x008, 1);
                     if (i + RV < NS) FA_BWD_SG(0x100, 2);
                 }
+                if constexpr (DSO) store_ds(ds_goff, sb, df);
             }
         } else {
 #pragma unroll
@@ -562,7 +608,19 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv(BackwardArgs a) {
                 }
             }
         }
-        if constexpr (DMA) {
+        if constexpr (DSO) {
+            // The dS stores of this tile were issued after the next tile's transfers: wait for
+            // the transfers only and leave the stores in flight (a wait for them here stalls
+            // every tile for a write round trip).
+            switch (k0 < S ? 2 * max(0, s1 - s0) : 0) {
+                case 2: wait_vmcnt<2>(); break;
+                case 4: wait_vmcnt<4>(); break;
+                case 6: wait_vmcnt<6>(); break;
+                case 8: wait_vmcnt<8>(); break;
+                default: wait_vmcnt<0>(); break;
+            }
+            __syncthreads();
+        } else if constexpr (DMA) {
             wait_dma();
             __syncthreads();
         }
@@ -734,10 +792,185 @@ __global__ __launch_bounds__(256, Blk<T>::ES == 2 ? 2 : 1) void bwd_dq(BackwardA
     }
 }
 
+// ------------------------------------------------------------------ dQ from the stored dS
+// dQ = scale * dS K with dS written by bwd_dkdv: one workgroup per (batch, query head, 256
+// queries), 32 per wave, eight waves sharing each 64-key K tile. Per tile the transfer unit
+// moves the K tile and every wave's two 2 KiB dS blocks (contiguous in a.ds) into one of three
+// LDS stages, two tiles ahead of the products (the kernel streams dS from HBM: 2 bytes per
+// (query, key) pair for 4 FLOP). The A operand of each MFMA (query c, eight consecutive keys)
+// is two transposing LDS reads of the stored rows of keys, the B operand the transposing read
+// of K. No exponentials and no S or dP products. Blocks past the causal diagonal or the
+// sequence are skipped like bwd_dq's, and every dS transfer is bounded to the allocation
+// (blocks of a query row past its last written one read other rows' data or zeros and are
+// never used).
+constexpr int kDqDsQueries = 256;
+template <typename T, int DPAD>
+__global__ __launch_bounds__(512, 2) void bwd_dq_ds(BackwardArgs a) {
+    using B = Blk<T>;
+    using H = typename B::H;
+    static_assert(B::ES == 2, "16-bit storage only");
+    constexpr int ES = 2, MB = DPAD / 32, KT = kBwdTile, NW = kDqDsQueries / 32;
+    using TG = TileGeom<T, DPAD, KT, DPAD == 128>;
+    constexpr int RB = TG::RB;
+    constexpr int T_DS = TG::BYTES;          // then 4 KiB of dS per wave
+    constexpr int STAGE = T_DS + NW * 4096;
+    constexpr int NST = 3;
+    constexpr int KI = (TG::INS + NW - 1) / NW;  // K transfers per wave
+    constexpr int NI = KI + 4;                    // transfers per wave and tile
+    constexpr int DUMMY = NST * STAGE;
+    constexpr bool NEED_DUMMY = TG::INS % NW != 0;
+    __shared__ __attribute__((aligned(16))) uint8_t smem[NST * STAGE + (NEED_DUMMY ? 1024 : 0)];
+
+    const int tid = threadIdx.x, lane = tid & 63, c = lane & 31;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int S = a.seq, D = a.head_dim;
+    const int nbh = a.batch * a.q_heads, nqb = (S + kDqDsQueries - 1) / kDqDsQueries;
+    // causal: the last query blocks see the most keys and dispatch first
+    const int qb = a.causal ? nqb - 1 - (int)(blockIdx.x / nbh) : (int)(blockIdx.x / nbh);
+    const int bh = blockIdx.x % nbh;
+    const int b = bh / a.q_heads, h = bh - b * a.q_heads, kvh = h / a.group;
+    const int q0 = qb * kDqDsQueries + wave * 32;
+    const int64_t qrow0 = (int64_t)bh * S, krow0 = ((int64_t)b * a.kv_heads + kvh) * S;
+    const int kend = a.causal ? min(S, (qb + 1) * kDqDsQueries) : S;
+    const int ntiles = (kend + KT - 1) / KT;
+
+    // this wave's 32 query rows: block (q0 / 32) % 4 of the groups of tile q0 / 128 of head bh;
+    // key block kb at ds_row + 8192 kb
+    const uint32_t nt = (uint32_t)(S + 127) >> 7, t = (uint32_t)q0 >> 7;
+    const uint32_t gph = a.causal ? 2u * nt * (nt + 1u) : nt * (uint32_t)a.ds_nb;
+    const uint32_t ds_row =
+        ((uint32_t)bh * gph + (a.causal ? 2u * t * (t + 1u) : t * (uint32_t)a.ds_nb)) * 8192u +
+        2048u * (((uint32_t)q0 >> 5) & 3u);
+    const i32x4_t rds = make_rsrc_words(a.ds, a.ds_bytes);
+    // Chunk x (16 bytes: eight queries of one key; x = 64 (q >> 4) + 32 ((q >> 3) & 1) + k) sits
+    // in LDS at chunk x ^ 4 ((x >> 5) & 1), so the two runs of four keys a transposing read
+    // gathers (chunks x and x + 32) fall in different banks.
+    const uint32_t ds_src = 16u * (uint32_t)(lane ^ (((lane >> 5) & 1) << 2));
+
+    uint32_t koff[KI];
+#pragma unroll
+    for (int i = 0; i < KI; ++i) koff[i] = tile_slot_offset<TG>(wave + NW * i, lane, D);
+    const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_void_t*)smem;
+    // NI transfer instructions per wave, every tile (the ones past the K tile write DUMMY)
+    auto dma_tile = [&](int j) {
+        const int st = (j % NST) * STAGE;
+        const int kt = j * KT, left = S - kt;
+        const i32x4_t rk =
+            make_rsrc_words((const uint8_t*)a.k + (krow0 + kt) * D * ES, left * D * ES);
+#pragma unroll
+        for (int i = 0; i < KI; ++i) {
+            const int k = wave + NW * i;
+            buffer_to_lds16(
+                rk, __builtin_amdgcn_readfirstlane(lds0 + (k < TG::INS ? st + k * 1024 : DUMMY)),
+                koff[i]);
+        }
+        // key blocks 2 j and 2 j + 1 of the wave's rows (2 KiB each, at ds_row + 8192 kb),
+        // 16-byte chunk x of a block to LDS chunk swz(x) (an involution)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            buffer_to_lds16_nt(
+                rds, __builtin_amdgcn_readfirstlane(lds0 + st + T_DS + wave * 4096 + i * 1024),
+                ds_row + 8192u * (uint32_t)(2 * j + (i >> 1)) + 1024u * (i & 1) + ds_src);
+    };
+
+    f32x16_t dq[MB];
+#pragma unroll
+    for (int m = 0; m < MB; ++m) dq[m] = (f32x16_t)0.0f;
+    Ops16<TG, B, MB> ops;
+    ops.init(lane);
+    // Transposing read of the A operand: lane (16-group G, index s) addresses key
+    // 16 ks + 8 (lane >> 5) + s / 4 (+ 4 for the second read) and queries 16 (G & 1) +
+    // 4 (s & 3) .. + 3 (chunk 64 (G & 1) + 32 ((s >> 1) & 1) + key, half s & 1 of it, swizzled as
+    // above); it receives query lane & 31 of those four keys.
+    uint32_t a_off[2];
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+        const int s16 = lane & 15, hb = (s16 >> 1) & 1;
+        const int x = 64 * ((lane >> 4) & 1) + 32 * hb + 8 * (lane >> 5) + 4 * hf + (s16 >> 2);
+        a_off[hf] = 16u * (uint32_t)(x ^ (hb << 2)) + 8u * (uint32_t)(s16 & 1);
+    }
+    typedef short v4i16_t __attribute__((ext_vector_type(4)));
+    typedef __attribute__((address_space(3))) v4i16_t lds_v4i16_t;
+    auto aread = [&](const uint8_t* blk, int ks) {
+        const uint8_t* p = blk + 256 * ks;
+        const v4i16_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)(p + a_off[0]));
+        const v4i16_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)(p + a_off[1]));
+        const u32x2_t l2 = __builtin_bit_cast(u32x2_t, lo);
+        const u32x2_t h2 = __builtin_bit_cast(u32x2_t, hi);
+        return u32x4_t{l2[0], l2[1], h2[0], h2[1]};
+    };
+
+    dma_tile(0);
+    if (ntiles > 1) {
+        dma_tile(1);
+        wait_vmcnt<NI>();
+    } else {
+        wait_vmcnt<0>();
+    }
+    __syncthreads();
+    for (int j = 0; j < ntiles; ++j) {
+        // tile j + 2 goes to the stage tile j - 1 used: every wave passed the barrier after it
+        if (j + 2 < ntiles) dma_tile(j + 2);
+        const int st = (j % NST) * STAGE, kt = j * KT;
+#pragma unroll
+        for (int sub = 0; sub < KT / 32; ++sub) {
+            const int kk0 = kt + sub * 32;
+            if (kk0 >= S) break;
+            if (a.causal && kk0 > q0 + 31) continue;  // the block lies past the diagonal
+            const uint8_t* tk = smem + st + sub * 32 * RB;
+            const uint8_t* tds = smem + st + T_DS + wave * 4096 + sub * 2048;
+            u32x4_t a0 = aread(tds, 0), a1 = aread(tds, 1);
+            if (kk0 + 32 > S) {
+                // keys past the sequence: bwd_dkdv stored their dS unmasked (finite unless the
+                // row's LSE is extreme); zero them so the zero K rows contribute exactly zero
+                const int kb = kk0 + 8 * (lane >> 5);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const uint32_t m0 = kb + 2 * i < S ? 0x0000ffffu : 0u;
+                    const uint32_t m1 = kb + 2 * i + 1 < S ? 0xffff0000u : 0u;
+                    const uint32_t n0 = kb + 16 + 2 * i < S ? 0x0000ffffu : 0u;
+                    const uint32_t n1 = kb + 16 + 2 * i + 1 < S ? 0xffff0000u : 0u;
+                    a0[i] &= m0 | m1;
+                    a1[i] &= n0 | n1;
+                }
+            }
+#pragma unroll
+            for (int m = 0; m < MB; ++m) {
+                dq[m] = H::mfma32(a0, ops.tread(tk, m, 0), dq[m]);
+                dq[m] = H::mfma32(a1, ops.tread(tk, m, 1), dq[m]);
+            }
+        }
+        // tile j + 1 landed (the NI transfers of tile j + 2 may still be in flight)
+        if (j + 2 < ntiles) wait_vmcnt<NI>();
+        else wait_vmcnt<0>();
+        __syncthreads();
+    }
+    const int g = lane >> 5;
+#pragma unroll
+    for (int m = 0; m < MB; ++m) {
+        const int d = 32 * m + c;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int q = q0 + 8 * (r >> 2) + 4 * g + (r & 3);
+            if (q < S && d < D) B::store(a.dq, (qrow0 + q) * D + d, dq[m][r] * a.scale);
+        }
+    }
+}
+
 template <typename T, int DPAD, bool DMA>
 void launch_typed(const BackwardArgs& a, hipStream_t s) {
     const int S = a.seq;
     const int nkb = (S + kBwdKeys - 1) / kBwdKeys, nqb = (S + kBwdQueries - 1) / kBwdQueries;
+    if constexpr (DMA && Blk<T>::ES == 2) {
+        if (a.ds) {
+            hipLaunchKernelGGL((bwd_dkdv<T, DPAD, true, true>), dim3(nkb * a.batch * a.kv_heads),
+                               dim3(256), 0, s, a);
+            const int nqd = (S + kDqDsQueries - 1) / kDqDsQueries;
+            hipLaunchKernelGGL((bwd_dq_ds<T, DPAD>), dim3(nqd * a.batch * a.q_heads), dim3(512),
+                               0, s, a);
+            return;
+        }
+    }
     hipLaunchKernelGGL((bwd_dkdv<T, DPAD, DMA>), dim3(nkb * a.batch * a.kv_heads), dim3(256), 0,
                        s, a);
     hipLaunchKernelGGL((bwd_dq<T, DPAD, DMA>), dim3(nqb * a.batch * a.q_heads), dim3(256), 0, s,

@@ -148,7 +148,19 @@ __device__ __forceinline__ void buffer_to_lds16(i32x4_t rsrc, uint32_t lds, uint
     // barriers / wait_dma() that order it against its readers are themselves ordered.
     asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds" : : "v"(voff), "s"(rsrc), "{m0}"(lds));
 }
+// The same for data read exactly once (non-temporal: the stream does not evict reused lines).
+__device__ __forceinline__ void buffer_to_lds16_nt(i32x4_t rsrc, uint32_t lds, uint32_t voff) {
+    asm volatile("buffer_load_dwordx4 %0, %1, 0 offen nt lds"
+                 :
+                 : "v"(voff), "s"(rsrc), "{m0}"(lds));
+}
 __device__ __forceinline__ void wait_dma() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+// Wait until at most N vector memory operations of this wave are outstanding. Loads, transfers
+// and stores complete in issue order, so this waits for everything but the N most recent.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
 // Buffer resource words: base, stride 0, num_records bytes, the same flags as
 // __builtin_amdgcn_make_buffer_rsrc is given elsewhere (0x00020000).
 __device__ __forceinline__ i32x4_t make_rsrc_words(const void* base, int nrec) {

@@ -159,6 +159,10 @@ struct fa_ctx {
     // growable scratch for the backward's per-row (LSE log2 e, rowsum(dO * O))
     void* ws_delta = nullptr;
     size_t ws_delta_bytes = 0;
+    // growable scratch for the backward's stored dS (16-bit storage; fa_ctx_set_backward_policy)
+    void* ws_ds = nullptr;
+    size_t ws_ds_bytes = 0;
+    int backward_ds_policy = -1;
     int transpose_v_policy = -1;
     // 16-bit RoPE prefill scores: 0 = rotated Q/K rounded to the storage type, 1 = split
     // high/residual operands (fa_ctx_set_prefill_precision)
@@ -528,6 +532,7 @@ int fa_ctx_destroy(fa_ctx* ctx) {
     if (ctx->ws) (void)hipFree(ctx->ws);
     if (ctx->ws_vt) (void)hipFree(ctx->ws_vt);
     if (ctx->ws_delta) (void)hipFree(ctx->ws_delta);
+    if (ctx->ws_ds) (void)hipFree(ctx->ws_ds);
     if (ctx->meta_dev) (void)hipFree(ctx->meta_dev);
     for (const auto& s : ctx->pending) {
         (void)hipEventDestroy(s.begin);
@@ -607,6 +612,12 @@ int fa_ctx_set_prefill_v_layout(fa_ctx* ctx, int32_t transpose_v) {
 int fa_ctx_set_decode_policy(fa_ctx* ctx, int32_t grouped) {
     if (!ctx) return fail(FA_ERR_NULL_ARGUMENT, "context is null");
     ctx->decode_grouped_policy = grouped < 0 ? -1 : (grouped ? 1 : 0);
+    return ok();
+}
+
+int fa_ctx_set_backward_policy(fa_ctx* ctx, int32_t store_ds) {
+    if (!ctx) return fail(FA_ERR_NULL_ARGUMENT, "context is null");
+    ctx->backward_ds_policy = store_ds < 0 ? -1 : (store_ds ? 1 : 0);
     return ok();
 }
 
@@ -2676,6 +2687,22 @@ int fa_backward_grouped(fa_ctx* ctx, const void* q, const void* k, const void* v
     for (const void* p : ptrs) vec = vec && ((uintptr_t)p % 16 == 0);
     a.vec = vec;
     a.dma = vec && sh->seq_len * sh->head_dim * (uint64_t)elem_bytes(dtype) < (1ull << 31);
+    // Stored dS: 16-bit storage on the transfer path, 8 KiB per (128-query tile, 32-key block)
+    // group of the causal or full square, at most 2 GiB (32-bit buffer offsets); otherwise
+    // bwd_dq recomputes S and dP.
+    if (ctx->backward_ds_policy != 0 && elem_bytes(dtype) == 2 && a.dma) {
+        const unsigned __int128 nb = (sh->seq_len + 31) / 32, nt = (sh->seq_len + 127) / 128;
+        const unsigned __int128 gph = a.causal ? 2 * nt * (nt + 1) : nt * nb;
+        const unsigned __int128 bytes =
+            (unsigned __int128)sh->batch * sh->q_heads * gph * 8192u;
+        if (bytes <= (unsigned __int128)INT32_MAX) {
+            void* ds = nullptr;
+            if (int rc = grow(ctx, &ctx->ws_ds, &ctx->ws_ds_bytes, (size_t)bytes, &ds)) return rc;
+            a.ds = ds;
+            a.ds_nb = (int)nb;
+            a.ds_bytes = (int)bytes;
+        }
+    }
     begin_span(ctx);
     fa::launch_backward((Dtype)dtype, a, ctx->stream);
     end_span(ctx, FA_KERNEL_BACKWARD_RECOMPUTE);
@@ -2683,7 +2710,8 @@ int fa_backward_grouped(fa_ctx* ctx, const void* q, const void* k, const void* v
     const unsigned grid[3] = {(unsigned)(((sh->seq_len + 127) / 128) * sh->batch * sh->kv_heads),
                               1, 1};
     char name[64];
-    snprintf(name, sizeof name, "bwd_delta + bwd_dkdv + bwd_dq<%s>", dtype_name(dtype));
+    snprintf(name, sizeof name, "bwd_delta + bwd_dkdv + %s<%s>", a.ds ? "bwd_dq_ds" : "bwd_dq",
+             dtype_name(dtype));
     record(ctx, FA_KERNEL_BACKWARD_RECOMPUTE, name, 128, 64, grid, 256, 3, 1,
            vec ? nullptr : "unaligned tensors or head_dim off the 16-byte chunk: scalar loads");
     return ok();

@@ -107,10 +107,20 @@ struct BackwardArgs {
     void* dk;
     void* dv;
     float2* ld;
+    // Stored dS (16-bit storage with DMA only; null: bwd_dq recomputes S and dP). Per (batch,
+    // query head) and 128-query tile t, one 8 KiB group per 32-key block kb (kb < 4 t + 4 under a
+    // causal mask, else kb < ds_nb = ceil(seq / 32)): group t * ds_nb + kb, or 2 t (t + 1) + kb
+    // causal, of the head's 2 nt (nt + 1) (causal) or nt * ds_nb groups, nt = ceil(seq / 128).
+    // A group holds the four 32 x 32 blocks of its 32-query rows, 2 KiB each; inside a block,
+    // element (q, k) sits at byte 1024 (q >> 4) + 512 ((q >> 3) & 1) + 16 k + 2 (q & 7): the dK
+    // product's dS^T fragment (one key, eight consecutive queries per lane) is one 16-byte
+    // piece per lane at 1024 h + 16 lane, 1 KiB per store instruction.
+    void* ds;
+    int ds_nb, ds_bytes;
     int batch, q_heads, kv_heads, group, seq, head_dim, causal, vec, dma;
     float scale;
 };
-// Three launches: delta, dK/dV, dQ.
+// Three launches: delta, dK/dV (which also writes dS when `ds` is set), dQ.
 void launch_backward(Dtype dt, const BackwardArgs& a, hipStream_t s);
 
 // (cos, sin) table: table[pos*half + p] for pos < rows, p < half = head_dim/2, with

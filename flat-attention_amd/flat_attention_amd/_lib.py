@@ -208,6 +208,7 @@ PROTOTYPES = {
     "fa_ctx_pause_kernel_timing": (INT, [VP, I32]),
     "fa_ctx_set_prefill_precision": (INT, [VP, I32]),
     "fa_ctx_set_decode_policy": (INT, [VP, I32]),
+    "fa_ctx_set_backward_policy": (INT, [VP, I32]),
     "fa_ctx_kernel_timing": (INT, [VP, I32, P(ctypes.c_double), P(U64)]),
     "fa_ctx_kernel_timing_range": (INT, [VP, I32, P(ctypes.c_double), P(ctypes.c_double)]),
 }

@@ -254,6 +254,11 @@ class HipContext:
         workgroups; read when a PagedDecodePlan is prepared."""
         check(lib().fa_ctx_set_decode_policy(self.handle, grouped))
 
+    def set_backward_policy(self, store_ds: int):
+        """-1 automatic (16-bit storage: bwd_dkdv stores dS and dQ = dS K reads it back when the
+        workspace fits in 2 GiB), 0 dQ recomputes S and dP."""
+        check(lib().fa_ctx_set_backward_policy(self.handle, store_ds))
+
     def set_prefill_precision(self, mode: int):
         """0: rotated Q/K rounded to the 16-bit storage type before Q.K^T (default, fastest);
         1: split high/residual operands, f32-level scores for the 16-bit RoPE prefill."""

@@ -528,6 +528,13 @@ int fa_ctx_set_decode_policy(fa_ctx* ctx, int32_t grouped);
  * stream V^T tiles, 0 = stream V rows and transpose in the kernel, -1 = automatic (currently
  * 0). Both layouts give bit-identical results. */
 int fa_ctx_set_prefill_v_layout(fa_ctx* ctx, int32_t transpose_v);
+/* dQ policy of the recompute backward (no counterpart in the reference, whose backward
+ * recomputes every product per scalar gradient, src/wgpu_backward_grouped.rs:318). store_ds:
+ * -1 = automatic (default) and 1: with 16-bit storage and 16-byte aligned tensors, bwd_dkdv also
+ * writes dS (2 bytes per (query, key) pair of every visible 32 x 32 block, kept in a context
+ * workspace, used when it fits in 2 GiB) and dQ = dS K reads it back; 0 = dQ recomputes S and dP
+ * (no workspace). Both are deterministic and use the same dS values up to MFMA summation order. */
+int fa_ctx_set_backward_policy(fa_ctx* ctx, int32_t store_ds);
 int fa_kernel_variant_for_shape(fa_ctx* ctx, uint64_t head_dim, int32_t has_rope, int dtype,
                                 int32_t* kernel_id);
 

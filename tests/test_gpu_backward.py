@@ -296,3 +296,36 @@ def test_unaligned_tensors_take_the_staged_path(hip, dtype):
             assert_close(name, a, e, *tol)
         else:
             assert_close(name, a, e, 2e-2 * float(np.abs(e).max()), 2e-2)
+
+
+@pytest.mark.parametrize("dtype", [fa.DTYPE_BF16, fa.DTYPE_F16])
+@pytest.mark.parametrize("dims,causal", [((1, 8, 2, 256, 128), True), ((2, 4, 4, 130, 64), False),
+                                         ((1, 4, 1, 77, 32), True), ((1, 6, 3, 200, 96), False),
+                                         ((1, 2, 1, 33, 128), True)])
+def test_stored_ds_path_matches_recompute_path(hip, request, dtype, dims, causal):
+    """16-bit storage, aligned tensors: by default bwd_dkdv also writes dS (32 x 32 blocks of the
+    storage type) and dQ = dS K reads it back (telemetry names bwd_dq_ds); policy 0 recomputes S
+    and dP in bwd_dq. Both use the same dS values in the same MFMA order, so the gradients agree
+    bit for bit, and both match the oracle. Ragged lengths leave partial key blocks, whose keys
+    past the sequence must read as zero dS."""
+    rnd = bf16_round if dtype == fa.DTYPE_BF16 else f16_round
+    shape = fa.GroupedAttentionShape(*dims)
+    B, Hq, Hkv, S, D = dims
+    q, k, v, do = (rnd(normal(n, 71 + i)) for i, n in enumerate(
+        (B * Hq * S * D, B * Hkv * S * D, B * Hkv * S * D, B * Hq * S * D)))
+    fwd, _ = _expected(q, k, v, do, shape, causal, None)
+    fwd = fa.FlatAttentionOutput(rnd(fwd.output), fwd.lse)
+    want = oracle.backward_grouped(q, k, v, do, fwd.output, fwd.lse, B, Hq, Hkv, S, D, causal,
+                                   threads=8)
+    pipe = fa.HipGroupedBackwardRecomputePipeline(hip, dtype)
+    request.addfinalizer(lambda: hip.set_backward_policy(-1))
+    runs = {}
+    for policy in (-1, 0):
+        hip.set_backward_policy(policy)
+        got = pipe.backward(q, k, v, do, fwd, shape, fa.FlatAttentionConfig(causal))
+        runs[policy] = (got, hip.last_telemetry().kernel_name)
+    assert "bwd_dq_ds" in runs[-1][1] and "bwd_dq_ds" not in runs[0][1]
+    for name, a, b_, e in zip(("dQ", "dK", "dV"), (runs[-1][0].dq, runs[-1][0].dk, runs[-1][0].dv),
+                              (runs[0][0].dq, runs[0][0].dk, runs[0][0].dv), want):
+        np.testing.assert_array_equal(a, b_, err_msg=name)
+        assert_close(name, a, e, 2e-2 * float(np.abs(e).max()), 2e-2)
