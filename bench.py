@@ -379,7 +379,9 @@ def summarize_pmc(fetch_csv: str, write_csv: str) -> dict:
     f_scale, w_scale = COPY_BYTES / copy_f, COPY_BYTES / copy_w
     res = {"copy_bytes": COPY_BYTES, "fetch_scale": f_scale, "write_scale": w_scale}
     for name, key in (("prefill", "prefill_mfma16"), ("decode", "decode_mfma"),
-                      ("combine", "decode_combine"), ("rotate", "rotate_rows")):
+                      ("combine", "decode_combine"), ("rotate", "rotate_rows"),
+                      ("bwd_delta", "bwd_delta<"), ("bwd_dkdv", "bwd_dkdv<"),
+                      ("bwd_dq_ds", "bwd_dq_ds<"), ("bwd_dq", "bwd_dq<")):
         try:
             fb = pick(fetch, key) * 1024.0 * f_scale
             wb = pick(write, key) * 1024.0 * w_scale
@@ -550,11 +552,14 @@ def main():
                          "(power-limit diagnostic; not a benchmark figure)")
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="turn two rocprofv3 --pmc counter CSVs into the traffic summary")
+    ap.add_argument("--traffic-out", default=TRAFFIC_JSON,
+                    help="where --summarize-pmc writes (default: the prefill/decode summary that "
+                         "the bench line's roofline.traffic reads)")
     args = ap.parse_args()
     if args.summarize_pmc:
         res = summarize_pmc(*args.summarize_pmc)
-        os.makedirs(os.path.dirname(TRAFFIC_JSON), exist_ok=True)
-        with open(TRAFFIC_JSON, "w") as f:
+        os.makedirs(os.path.dirname(os.path.abspath(args.traffic_out)), exist_ok=True)
+        with open(args.traffic_out, "w") as f:
             json.dump(res, f, indent=1)
         print(json.dumps(res))
         return
@@ -569,6 +574,12 @@ def main():
     if args.only == "backward":
         ctx.set_backward_policy(args.backward_policy)
         out = measure_backward(ctx, rng, args.steps, args.warmup, args.data)
+        if args.calibrate_copy:
+            a, b = fa.DeviceBuffer(ctx, COPY_BYTES), fa.DeviceBuffer(ctx, COPY_BYTES)
+            HipEvents().copy_d2d(b.ptr, a.ptr, COPY_BYTES, ctx.stream)
+            ctx.synchronize()
+            a.free()
+            b.free()
         if not args.no_cpu_baseline:
             out["cpu_baseline"] = cpu_baseline_backward()
         print(json.dumps(out))

@@ -359,8 +359,12 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv(BackwardArgs a) {
     const int qstart = a.causal ? kb * kBwdKeys : 0;  // a multiple of QT
     const int nqt = (S - qstart + QT - 1) / QT, ntiles = G * nqt;
     const int64_t qhead0 = ((int64_t)b * a.q_heads + (int64_t)kvh * G) * S;  // first row of the group
+    auto tile_hq = [&](int j) {  // head of the group and query offset qt of tile j
+        const int hh = j / nqt;
+        return std::pair<int, int>(hh, qstart + (j - hh * nqt) * QT);
+    };
     auto tile_row = [&](int j) {  // first query row (global) of tile j and its offset qt
-        const int hh = j / nqt, qt = qstart + (j - hh * nqt) * QT;
+        const auto [hh, qt] = tile_hq(j);
         return std::pair<int64_t, int>(qhead0 + (int64_t)hh * S + qt, qt);
     };
     const bool vec = DMA || a.vec;
@@ -485,8 +489,8 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv(BackwardArgs a) {
             stage_tile(j);
             __syncthreads();
         }
-        const int qt = tile_row(j).second;
-        const uint32_t ds_goff = DSO ? ds_group_off(j / nqt, qt) : 0u;
+        const auto [hh, qt] = tile_hq(j);
+        const uint32_t ds_goff = DSO ? ds_group_off(hh, qt) : 0u;
         // active sub-blocks [s0, s1): causal skips the ones wholly before the wave's keys
         const int s0 = a.causal ? min(NSUB, max(0, (k0 - qt) >> 5)) : 0;
         const int s1 = min(NSUB, (S - qt + 31) >> 5);
