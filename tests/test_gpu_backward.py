@@ -329,3 +329,32 @@ def test_stored_ds_path_matches_recompute_path(hip, request, dtype, dims, causal
                               (runs[0][0].dq, runs[0][0].dk, runs[0][0].dv), want):
         np.testing.assert_array_equal(a, b_, err_msg=name)
         assert_close(name, a, e, 2e-2 * float(np.abs(e).max()), 2e-2)
+
+
+def test_stored_ds_falls_back_to_recompute_past_2gib(hip):
+    """The dS workspace is used only under 2 GiB: one causal head of 49,152 tokens needs
+    2 nt (nt + 1) groups of 8 KiB with nt = 384 (2.42 GB), so the default policy takes the
+    recompute path (telemetry names bwd_dq). The long-sequence offsets stay in range: every
+    gradient is finite, and dV of the last 64 keys, which only the last 64 queries see, matches
+    a float64 evaluation with the forward's own LSE."""
+    B, Hq, Hkv, S, D = 1, 1, 1, 49152, 64
+    q, k, v, do = (bf16_round(normal(n, 81 + i)) for i, n in enumerate((S * D,) * 4))
+    shape = fa.GroupedAttentionShape(B, Hq, Hkv, S, D)
+    fwd_pipe = fa.HipRotaryGroupedAttention(hip, fa.DTYPE_BF16)
+    res = fwd_pipe.forward(q, k, v, shape, fa.FlatAttentionConfig(True), None)
+    o = fa.storage_to_f32(res.output, fa.DTYPE_BF16)
+    got = fa.HipGroupedBackwardRecomputePipeline(hip, fa.DTYPE_BF16).backward(
+        q, k, v, do, fa.FlatAttentionOutput(o, res.lse), shape, fa.FlatAttentionConfig(True))
+    assert "bwd_dq<" in hip.last_telemetry().kernel_name
+    for name, x in (("dQ", got.dq), ("dK", got.dk), ("dV", got.dv)):
+        assert np.isfinite(x).all(), name
+    # dV of key j = sum over queries q >= j of P[q, j] dO[q]: for the last W keys only the last W
+    # queries contribute, and P[q, j] = exp(s_qj - LSE_q) uses the full-row LSE the forward gave.
+    W = 64
+    qs, ks = q.reshape(S, D)[-W:], k.reshape(S, D)[-W:]
+    sc = (qs @ ks.T) / np.sqrt(D)
+    mask = np.tril(np.ones((W, W), bool))
+    p = np.where(mask, np.exp(sc - res.lse[-W:, None]), 0.0)
+    dv_want = p.T @ do.reshape(S, D)[-W:]
+    assert_close("dV-tail", got.dv.reshape(S, D)[-W:], dv_want,
+                 2e-2 * float(np.abs(dv_want).max()), 2e-2)
