@@ -550,6 +550,9 @@ def main():
     ap.add_argument("--data", choices=["normal", "constant"], default="normal",
                     help="prefill and backward inputs: N(0,1) (the benchmark), or a constant 0.5 everywhere "
                          "(power-limit diagnostic; not a benchmark figure)")
+    ap.add_argument("--ceilings", action="store_true",
+                    help="print the practical ceilings instead: a pure bf16 MFMA stream on random "
+                         "and constant operands, streaming HBM reads at 4 / 8 / 16 loads in flight")
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="turn two rocprofv3 --pmc counter CSVs into the traffic summary")
     ap.add_argument("--traffic-out", default=TRAFFIC_JSON,
@@ -571,6 +574,15 @@ def main():
 
     rng = np.random.default_rng(1234)
     ctx = fa.HipContext(0)
+    if args.ceilings:
+        res = {"mfma_bf16_tflops": {"random": round(ctx.mfma_ceiling(False), 1),
+                                    "constant": round(ctx.mfma_ceiling(True), 1),
+                                    "spec": PEAK_BF16_TFLOPS},
+               "stream_read_tbps": {str(d): round(ctx.stream_read(d), 3) for d in (4, 8, 16)},
+               "hbm_spec_tbps": PEAK_HBM_GBS / 1000.0}
+        print(json.dumps(res))
+        ctx.close()
+        return
     if args.only == "backward":
         ctx.set_backward_policy(args.backward_policy)
         out = measure_backward(ctx, rng, args.steps, args.warmup, args.data)

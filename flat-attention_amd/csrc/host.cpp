@@ -571,6 +571,80 @@ int fa_ctx_set_kernel_timing(fa_ctx* ctx, int32_t enable) {
     return ok();
 }
 
+// ------------------------------------------------------------------ measurement aids
+extern "C++" {
+namespace {
+// ms per call of `run` on the context's stream: `warm` untimed calls, then `reps` timed ones.
+template <typename F>
+int time_calls(fa_ctx* ctx, int warm, int reps, F run, double* ms) {
+    for (int i = 0; i < warm; ++i) run();
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    HIP_TRY(hipEventCreate(&e0));
+    HIP_TRY(hipEventCreate(&e1));
+    HIP_TRY(hipEventRecord(e0, ctx->stream));
+    for (int i = 0; i < reps; ++i) run();
+    HIP_TRY(hipEventRecord(e1, ctx->stream));
+    HIP_TRY(hipEventSynchronize(e1));
+    float t = 0.0f;
+    HIP_TRY(hipEventElapsedTime(&t, e0, e1));
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    HIP_TRY(hipGetLastError());
+    *ms = (double)t / reps;
+    return FA_OK;
+}
+}  // namespace
+}  // extern "C++"
+
+int fa_diag_mfma_ceiling(fa_ctx* ctx, int32_t constant_operands, double* tflops) {
+    if (!ctx || !tflops) return fail(FA_ERR_NULL_ARGUMENT, "null argument");
+    if (int rc = set_device(ctx)) return rc;
+    constexpr int kBlocks = 2048, kIters = 4000;  // ~2.5 ms per launch on 256 CUs
+    float* out = nullptr;
+    HIP_TRY(hipMalloc(&out, (size_t)kBlocks * 256 * sizeof(float)));
+    double ms = 0.0;
+    // 400 untimed launches (~1 s: the clock settles under sustained load), 200 timed (~0.5 s)
+    const int rc = time_calls(ctx, 400, 200, [&] {
+        fa::launch_mfma_ceiling(out, kBlocks, kIters, constant_operands != 0, ctx->stream);
+    }, &ms);
+    (void)hipStreamSynchronize(ctx->stream);
+    (void)hipFree(out);
+    if (rc) return rc;
+    const double flop = (double)kBlocks * 4 /* waves */ * kIters * 4 /* chains */ * 32768.0;
+    *tflops = flop / (ms * 1e-3) / 1e12;
+    return ok();
+}
+
+int fa_diag_stream_read(fa_ctx* ctx, int32_t loads_in_flight, double* tbps) {
+    if (!ctx || !tbps) return fail(FA_ERR_NULL_ARGUMENT, "null argument");
+    if (loads_in_flight != 4 && loads_in_flight != 8 && loads_in_flight != 16)
+        return fail(FA_ERR_UNAVAILABLE, "loads_in_flight must be 4, 8 or 16");
+    if (int rc = set_device(ctx)) return rc;
+    int cus = 0;
+    HIP_TRY(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, ctx->device));
+    constexpr size_t kBytes = (size_t)4 << 30;  // 4 GiB, far beyond every cache level
+    void* buf = nullptr;
+    uint32_t* out = nullptr;
+    HIP_TRY(hipMalloc(&buf, kBytes));
+    if (hipMalloc(&out, (size_t)cus * 512 * sizeof(uint32_t)) != hipSuccess) {
+        (void)hipFree(buf);
+        return fail(FA_ERR_HIP, "hipMalloc failed");
+    }
+    double ms = 0.0;
+    // one workgroup of 8 waves per CU (the decode's occupancy), 100 untimed and 200 timed
+    // passes (~0.2 s at 7 TB/s)
+    const int rc = time_calls(ctx, 100, 200, [&] {
+        fa::launch_stream_read(buf, (int64_t)(kBytes >> 15), loads_in_flight, cus, out,
+                               ctx->stream);
+    }, &ms);
+    (void)hipStreamSynchronize(ctx->stream);
+    (void)hipFree(out);
+    (void)hipFree(buf);
+    if (rc) return rc;
+    *tbps = (double)kBytes / (ms * 1e-3) / 1e12;
+    return ok();
+}
+
 int fa_ctx_pause_kernel_timing(fa_ctx* ctx, int32_t paused) {
     if (!ctx) return fail(FA_ERR_NULL_ARGUMENT, "context is null");
     ctx->timing_paused = paused != 0;

@@ -134,6 +134,12 @@ void launch_rope_table(float2* table, const RopeFreqs& f, int rows, int half, hi
 void launch_rope_rows(float2* table, const RopeFreqs& f, const int* positions, int n, int half,
                       hipStream_t s);
 
+// Measurement aids: a pure MFMA stream (random or constant bf16 operands) and a streaming read
+// of `n_chunks` 32 KiB chunks with `depth` (4, 8 or 16) loads in flight per lane.
+void launch_mfma_ceiling(float* out, int blocks, int iters, int constant, hipStream_t s);
+void launch_stream_read(const void* buf, int64_t n_chunks, int depth, int blocks, uint32_t* out,
+                        hipStream_t s);
+
 // Allocation-free paged decode: size of the per-device static scratch array and its device
 // address (resolved once per device with hipGetSymbolAddress; never the array's host-side name).
 constexpr size_t kNoAllocScratchBytes = (size_t)64 << 20;

@@ -254,6 +254,19 @@ class HipContext:
         workgroups; read when a PagedDecodePlan is prepared."""
         check(lib().fa_ctx_set_decode_policy(self.handle, grouped))
 
+    def mfma_ceiling(self, constant_operands: bool = False) -> float:
+        """TFLOP/s of a pure v_mfma_f32_32x32x16_bf16 stream (random or constant operands),
+        measured after the clock settles (~1.5 s)."""
+        out = ctypes.c_double()
+        check(lib().fa_diag_mfma_ceiling(self.handle, int(constant_operands), ctypes.byref(out)))
+        return out.value
+
+    def stream_read(self, loads_in_flight: int = 8) -> float:
+        """TB/s of non-temporal 16-byte streaming reads of a 4 GiB buffer."""
+        out = ctypes.c_double()
+        check(lib().fa_diag_stream_read(self.handle, loads_in_flight, ctypes.byref(out)))
+        return out.value
+
     def set_backward_policy(self, store_ds: int):
         """-1 automatic (16-bit storage: bwd_dkdv stores dS and dQ = dS K reads it back when the
         workspace fits in 2 GiB), 0 dQ recomputes S and dP."""

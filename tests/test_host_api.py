@@ -382,3 +382,12 @@ def test_mha_backward_layout_and_validation():
     assert call(fwd=64) == "BufferTooSmall"
     assert call(grads=64) == "BufferTooSmall"
     assert call() == "NullArgument"
+
+
+def test_diagnostic_probes_validate_arguments():
+    """fa_diag_mfma_ceiling / fa_diag_stream_read reject a null context or output and an
+    unsupported number of loads in flight before touching a device."""
+    lib = fa.lib()
+    out = ctypes.c_double()
+    assert lib.fa_diag_mfma_ceiling(None, 0, ctypes.byref(out)) == 50  # NullArgument
+    assert lib.fa_diag_stream_read(None, 8, ctypes.byref(out)) == 50
