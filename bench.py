@@ -578,6 +578,9 @@ def main():
         res = {"mfma_bf16_tflops": {"random": round(ctx.mfma_ceiling(False), 1),
                                     "constant": round(ctx.mfma_ceiling(True), 1),
                                     "spec": PEAK_BF16_TFLOPS},
+               "mfma_f32_tflops": {"random": round(ctx.mfma_ceiling(False, fa.DTYPE_F32), 1),
+                                   "constant": round(ctx.mfma_ceiling(True, fa.DTYPE_F32), 1),
+                                   "spec": PEAK_F32_TFLOPS},
                "stream_read_tbps": {str(d): round(ctx.stream_read(d), 3) for d in (4, 8, 16)},
                "hbm_spec_tbps": PEAK_HBM_GBS / 1000.0}
         print(json.dumps(res))

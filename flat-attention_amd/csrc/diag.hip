@@ -1,8 +1,8 @@
 // Measurement aids: the practical ceilings this part reaches on the two resources the
 // library's kernels are bound by, read against the same spec peaks the rooflines use.
-//   mfma_ceiling_kernel  back-to-back v_mfma_f32_32x32x16_bf16 on register operands, with
-//                        random (attention-like) or constant data: the MFMA rate the power
-//                        limit leaves for a pure matrix stream;
+//   mfma_ceiling_kernel  back-to-back v_mfma_f32_32x32x16_bf16 (or v_mfma_f32_32x32x2_f32) on
+//                        register operands, with random (attention-like) or constant data: the
+//                        MFMA rate the power limit leaves for a pure matrix stream;
 //   stream_read_kernel   non-temporal 16-byte loads of a large buffer in 32 KiB chunks per
 //                        wave with a fixed number of loads in flight per lane: the streaming
 //                        read rate of HBM.
@@ -32,6 +32,9 @@ __device__ __forceinline__ uint32_t random_bf16x2(uint32_t h) {
 
 // Four independent accumulator chains, each with its own operands, so consecutive MFMAs of a
 // wave see different data (as the prefill's K and V^T operands do). 256 threads, any grid.
+// F32: four v_mfma_f32_32x32x2_f32 per chain and trip (one f32 per lane and operand, 4096 FLOP
+// each); else one v_mfma_f32_32x32x16_bf16 per chain and trip (32768 FLOP).
+template <bool F32>
 __global__ __launch_bounds__(256) void mfma_ceiling_kernel(float* out, int iters, int constant) {
     using H = Half<bf16_t>;
     const uint32_t t = blockIdx.x * 256u + threadIdx.x;
@@ -40,15 +43,34 @@ __global__ __launch_bounds__(256) void mfma_ceiling_kernel(float* out, int iters
     for (int c = 0; c < 4; ++c)
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            a[c][j] = constant ? 0x3f003f00u : random_bf16x2(mix32(t * 32u + c * 8u + j));
-            b[c][j] = constant ? 0x3f003f00u : random_bf16x2(mix32(t * 32u + c * 8u + 4u + j));
+            if constexpr (F32) {
+                // random sign and mantissa, magnitude 1/8 .. 2 (f32 bit patterns)
+                const uint32_t ha = mix32(t * 32u + c * 8u + j), hb = mix32(t * 32u + c * 8u + 4u + j);
+                a[c][j] = constant ? 0x3f000000u
+                                   : ((ha & 1u) << 31) | ((124u + ((ha >> 1) & 3u)) << 23) | (ha >> 9);
+                b[c][j] = constant ? 0x3f000000u
+                                   : ((hb & 1u) << 31) | ((124u + ((hb >> 1) & 3u)) << 23) | (hb >> 9);
+            } else {
+                a[c][j] = constant ? 0x3f003f00u : random_bf16x2(mix32(t * 32u + c * 8u + j));
+                b[c][j] = constant ? 0x3f003f00u : random_bf16x2(mix32(t * 32u + c * 8u + 4u + j));
+            }
         }
     f32x16_t acc[4];
 #pragma unroll
     for (int c = 0; c < 4; ++c) acc[c] = (f32x16_t)0.0f;
     for (int i = 0; i < iters; ++i) {
 #pragma unroll
-        for (int c = 0; c < 4; ++c) acc[c] = H::mfma32(a[c], b[c], acc[c]);
+        for (int c = 0; c < 4; ++c) {
+            if constexpr (F32) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    acc[c] = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(a[c][j]),
+                                                                  __uint_as_float(b[c][j]),
+                                                                  acc[c], 0, 0, 0);
+            } else {
+                acc[c] = H::mfma32(a[c], b[c], acc[c]);
+            }
+        }
     }
     float s = 0.0f;
 #pragma unroll
@@ -85,8 +107,10 @@ __global__ __launch_bounds__(512) void stream_read_kernel(const uint8_t* buf, in
 
 }  // namespace
 
-void launch_mfma_ceiling(float* out, int blocks, int iters, int constant, hipStream_t s) {
-    mfma_ceiling_kernel<<<blocks, 256, 0, s>>>(out, iters, constant);
+void launch_mfma_ceiling(bool f32, float* out, int blocks, int iters, int constant,
+                         hipStream_t s) {
+    if (f32) mfma_ceiling_kernel<true><<<blocks, 256, 0, s>>>(out, iters, constant);
+    else mfma_ceiling_kernel<false><<<blocks, 256, 0, s>>>(out, iters, constant);
 }
 
 void launch_stream_read(const void* buf, int64_t n_chunks, int depth, int blocks, uint32_t* out,

@@ -596,21 +596,28 @@ int time_calls(fa_ctx* ctx, int warm, int reps, F run, double* ms) {
 }  // namespace
 }  // extern "C++"
 
-int fa_diag_mfma_ceiling(fa_ctx* ctx, int32_t constant_operands, double* tflops) {
+int fa_diag_mfma_ceiling(fa_ctx* ctx, int32_t dtype, int32_t constant_operands, double* tflops) {
     if (!ctx || !tflops) return fail(FA_ERR_NULL_ARGUMENT, "null argument");
+    if (dtype != FA_DTYPE_BF16 && dtype != FA_DTYPE_F32)
+        return fail(FA_ERR_UNSUPPORTED_DTYPE, "the MFMA ceiling probe runs bf16 or f32");
     if (int rc = set_device(ctx)) return rc;
-    constexpr int kBlocks = 2048, kIters = 4000;  // ~2.5 ms per launch on 256 CUs
+    const bool f32 = dtype == FA_DTYPE_F32;
+    // ~2.5 ms per launch on 256 CUs either way (an f32 32x32x2 MFMA takes twice the bf16 one's
+    // cycles for 1/8 of its work)
+    constexpr int kBlocks = 2048;
+    const int iters = f32 ? 500 : 4000;
     float* out = nullptr;
     HIP_TRY(hipMalloc(&out, (size_t)kBlocks * 256 * sizeof(float)));
     double ms = 0.0;
     // 400 untimed launches (~1 s: the clock settles under sustained load), 200 timed (~0.5 s)
     const int rc = time_calls(ctx, 400, 200, [&] {
-        fa::launch_mfma_ceiling(out, kBlocks, kIters, constant_operands != 0, ctx->stream);
+        fa::launch_mfma_ceiling(f32, out, kBlocks, iters, constant_operands != 0, ctx->stream);
     }, &ms);
     (void)hipStreamSynchronize(ctx->stream);
     (void)hipFree(out);
     if (rc) return rc;
-    const double flop = (double)kBlocks * 4 /* waves */ * kIters * 4 /* chains */ * 32768.0;
+    const double per_chain = f32 ? 4.0 * 4096.0 : 32768.0;
+    const double flop = (double)kBlocks * 4 /* waves */ * iters * 4 /* chains */ * per_chain;
     *tflops = flop / (ms * 1e-3) / 1e12;
     return ok();
 }

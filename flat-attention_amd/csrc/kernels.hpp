@@ -134,9 +134,10 @@ void launch_rope_table(float2* table, const RopeFreqs& f, int rows, int half, hi
 void launch_rope_rows(float2* table, const RopeFreqs& f, const int* positions, int n, int half,
                       hipStream_t s);
 
-// Measurement aids: a pure MFMA stream (random or constant bf16 operands) and a streaming read
+// Measurement aids: a pure MFMA stream (bf16 or f32, random or constant operands) and a streaming read
 // of `n_chunks` 32 KiB chunks with `depth` (4, 8 or 16) loads in flight per lane.
-void launch_mfma_ceiling(float* out, int blocks, int iters, int constant, hipStream_t s);
+void launch_mfma_ceiling(bool f32, float* out, int blocks, int iters, int constant,
+                         hipStream_t s);
 void launch_stream_read(const void* buf, int64_t n_chunks, int depth, int blocks, uint32_t* out,
                         hipStream_t s);
 

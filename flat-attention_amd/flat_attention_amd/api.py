@@ -254,11 +254,12 @@ class HipContext:
         workgroups; read when a PagedDecodePlan is prepared."""
         check(lib().fa_ctx_set_decode_policy(self.handle, grouped))
 
-    def mfma_ceiling(self, constant_operands: bool = False) -> float:
-        """TFLOP/s of a pure v_mfma_f32_32x32x16_bf16 stream (random or constant operands),
-        measured after the clock settles (~1.5 s)."""
+    def mfma_ceiling(self, constant_operands: bool = False, dtype: int = L.DTYPE_BF16) -> float:
+        """TFLOP/s of a pure MFMA stream (bf16 32x32x16 or f32 32x32x2; random or constant
+        operands), measured after the clock settles (~1.5 s)."""
         out = ctypes.c_double()
-        check(lib().fa_diag_mfma_ceiling(self.handle, int(constant_operands), ctypes.byref(out)))
+        check(lib().fa_diag_mfma_ceiling(self.handle, dtype, int(constant_operands),
+                                         ctypes.byref(out)))
         return out.value
 
     def stream_read(self, loads_in_flight: int = 8) -> float:

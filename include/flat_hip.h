@@ -539,12 +539,13 @@ int fa_kernel_variant_for_shape(fa_ctx* ctx, uint64_t head_dim, int32_t has_rope
                                 int32_t* kernel_id);
 
 /* Measurement aids (no counterpart in the reference): the practical ceilings the rooflines are
- * read against. fa_diag_mfma_ceiling runs back-to-back v_mfma_f32_32x32x16_bf16 on register
- * operands (random attention-like bf16 values, or a constant 0.5 when constant_operands != 0)
- * for ~1.5 s (1 s untimed, so the clock settles) and returns the rate in TFLOP/s. fa_diag_stream_read streams a 4 GiB buffer with
+ * read against. fa_diag_mfma_ceiling runs back-to-back v_mfma_f32_32x32x16_bf16 (dtype
+ * FA_DTYPE_BF16) or v_mfma_f32_32x32x2_f32 (FA_DTYPE_F32) on register operands (random
+ * attention-like values, or a constant 0.5 when constant_operands != 0) for ~1.5 s (1 s
+ * untimed, so the clock settles) and returns the rate in TFLOP/s. fa_diag_stream_read streams a 4 GiB buffer with
  * non-temporal 16-byte loads, loads_in_flight (4, 8 or 16) per lane, one 8-wave workgroup per
  * CU, and returns TB/s. Both allocate (and free) their own buffers and synchronize. */
-int fa_diag_mfma_ceiling(fa_ctx* ctx, int32_t constant_operands, double* tflops);
+int fa_diag_mfma_ceiling(fa_ctx* ctx, int32_t dtype, int32_t constant_operands, double* tflops);
 int fa_diag_stream_read(fa_ctx* ctx, int32_t loads_in_flight, double* tbps);
 
 /* Per-kernel device timing (extends runtime_telemetry src/wgpu_backend.rs:374, which carries no

@@ -389,5 +389,5 @@ def test_diagnostic_probes_validate_arguments():
     unsupported number of loads in flight before touching a device."""
     lib = fa.lib()
     out = ctypes.c_double()
-    assert lib.fa_diag_mfma_ceiling(None, 0, ctypes.byref(out)) == 50  # NullArgument
+    assert lib.fa_diag_mfma_ceiling(None, 3, 0, ctypes.byref(out)) == 50  # NullArgument
     assert lib.fa_diag_stream_read(None, 8, ctypes.byref(out)) == 50
