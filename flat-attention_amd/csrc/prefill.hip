@@ -953,16 +953,31 @@ __global__ __launch_bounds__(64 * NW, SPLIT ? 1 : 2) void prefill_mfma16(Prefill
 // Same decomposition with v_mfma_f32_32x32x2_f32 (f32 I/O contract, 2e-5 tolerance): no value
 // is ever rounded below f32. Lane group g supplies k-index g of every 2-wide k-step; the d
 // mapping is d = g*DPAD/2 + ks so each lane's Q operand is a contiguous half row.
-template <int DPAD, bool PAGED>
+// DMA (contiguous K/V, K not rotated in the kernel, head_dim % 4 == 0): K/V tiles go straight
+// from memory into two LDS stages (buffer -> LDS transfers, the next tile's under the current
+// tile's products); K rows are padded by one 16-byte slot so each lane reads four K operands
+// per 16-byte LDS read without bank conflicts. Otherwise tiles are staged through registers
+// (paged pools, K rotated on load, other head dims), K rows at an odd stride.
+template <int DPAD, bool PAGED, bool DMA = false>
 __global__ __launch_bounds__(256, 1) void prefill_mfma_f32(PrefillKArgs ka) {
+    static_assert(!(DMA && PAGED), "transfers need contiguous K/V");
     const PrefillArgs& a = ka.a;
     constexpr int BM = 128, BN = 64;
     constexpr int HALFD = DPAD / 2;
     constexpr int MB = DPAD / 32;
-    constexpr int KSTR = DPAD + 1;   // floats per K row in LDS (odd: conflict-free columns)
+    constexpr int KSTR = DMA ? DPAD + 4 : DPAD + 1;  // floats per K row in LDS
     constexpr int VSTR = DPAD;
-    __shared__ float k_lds[BN * KSTR];
-    __shared__ __attribute__((aligned(16))) float v_lds[BN * VSTR];
+    constexpr int STAGE = BN * KSTR * 4 + BN * VSTR * 4;  // bytes; a whole number of KiB
+    constexpr int KSL = KSTR / 4, VSL = VSTR / 4, CPR = DPAD / 4;  // 16-byte slots per row
+    constexpr int KINS = BN * KSL / 64, VINS = BN * VSL / 64;     // transfers per tile
+    constexpr int KI = (KINS + 3) / 4, VI = (VINS + 3) / 4;        // per wave
+    constexpr int DUMMY = 2 * STAGE;
+    constexpr bool NEED_DUMMY = DMA && (KINS % 4 != 0 || VINS % 4 != 0);
+    static_assert(!DMA || STAGE % 1024 == 0, "transfer stages are whole KiB");
+    __shared__ __attribute__((aligned(16)))
+    uint8_t smem[DMA ? 2 * STAGE + (NEED_DUMMY ? 1024 : 0) : STAGE];
+    float* const k_lds = (float*)smem;
+    float* const v_lds = (float*)(smem + BN * KSTR * 4);
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 5;
     const int D = a.head_dim, half = D >> 1;
@@ -1027,6 +1042,48 @@ __global__ __launch_bounds__(256, 1) void prefill_mfma_f32(PrefillKArgs ka) {
     const float* kbase = (const float*)a.k + (int64_t)kvh * a.k_sh;
     const float* vbase = (const float*)a.v + (int64_t)kvh * a.k_sh;
 
+    // ---- DMA: per-lane offsets of this wave's transfer instructions (slot q = 64 k + lane of
+    // a tile: row q / SL, chunk q % SL; pad chunks and chunks past head_dim read nothing)
+    constexpr uint32_t kOob = 0x7fff0000u;
+    const uint32_t row_bytes = (uint32_t)a.k_ss * 4u;
+    uint32_t koff[DMA ? KI : 1], voff[DMA ? VI : 1];
+    if constexpr (DMA) {
+#pragma unroll
+        for (int i = 0; i < KI; ++i) {
+            const int k = wave + 4 * i, q = 64 * k + lane, r = q / KSL, c = q % KSL;
+            koff[i] = (k < KINS && c < CPR && c * 4 < D) ? (uint32_t)r * row_bytes + (uint32_t)c * 16u
+                                                          : kOob;
+        }
+#pragma unroll
+        for (int i = 0; i < VI; ++i) {
+            const int k = wave + 4 * i, q = 64 * k + lane, r = q / VSL, c = q % VSL;
+            voff[i] = (k < VINS && c * 4 < D) ? (uint32_t)r * row_bytes + (uint32_t)c * 16u : kOob;
+        }
+    }
+    const uint8_t* const kb8 = (const uint8_t*)(kbase + (int64_t)b * a.k_sb);
+    const uint8_t* const vb8 = (const uint8_t*)(vbase + (int64_t)b * a.k_sb);
+    const int nrec_all = (kv_len_ - 1) * (int)row_bytes + D * 4;
+    const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_void_t*)smem;
+    auto dma_tile = [&](int tile, int st) {
+        const int base = tile * BN * (int)row_bytes;
+        const i32x4_t rk = make_rsrc_words(kb8 + base, nrec_all - base);
+        const i32x4_t rv = make_rsrc_words(vb8 + base, nrec_all - base);
+#pragma unroll
+        for (int i = 0; i < KI; ++i) {
+            const int k = wave + 4 * i;
+            buffer_to_lds16(rk, __builtin_amdgcn_readfirstlane(lds0 + (k < KINS ? st + k * 1024 : DUMMY)),
+                            koff[i]);
+        }
+#pragma unroll
+        for (int i = 0; i < VI; ++i) {
+            const int k = wave + 4 * i;
+            buffer_to_lds16(rv,
+                            __builtin_amdgcn_readfirstlane(
+                                lds0 + (k < VINS ? st + BN * KSTR * 4 + k * 1024 : DUMMY)),
+                            voff[i]);
+        }
+    };
+
     f32x16_t oacc[MB];
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) oacc[mb] = (f32x16_t)0.0f;
@@ -1036,7 +1093,20 @@ __global__ __launch_bounds__(256, 1) void prefill_mfma_f32(PrefillKArgs ka) {
     constexpr int RPP = 256 / C4;          // rows per staging pass
     constexpr int PASSES = BN / RPP;
 
+    if constexpr (DMA) {
+        if (n_tiles > 0) dma_tile(0, 0);
+        wait_dma();
+        __syncthreads();
+    }
     for (int tile = 0; tile < n_tiles; ++tile) {
+        const float* kst = k_lds;  // this tile's K and V rows in LDS
+        const float* vst = v_lds;
+        if constexpr (DMA) {
+            const int st = (tile & 1) * STAGE;
+            if (tile + 1 < n_tiles) dma_tile(tile + 1, STAGE - st);
+            kst = (const float*)(smem + st);
+            vst = (const float*)(smem + st + BN * KSTR * 4);
+        } else {
         // ---- stage K (rotated) and V
 #pragma unroll
         for (int p = 0; p < PASSES; ++p) {
@@ -1079,15 +1149,33 @@ __global__ __launch_bounds__(256, 1) void prefill_mfma_f32(PrefillKArgs ka) {
             *(f32x4_t*)(v_lds + kl * VSTR + d0) = vv4;
         }
         __syncthreads();
+        }
 
         f32x16_t sacc[2];
+        if constexpr (DMA) {
+            // four K operands per 16-byte read; the two key blocks' chains alternate
+            sacc[0] = (f32x16_t)0.0f;
+            sacc[1] = (f32x16_t)0.0f;
+            const float* kr0 = kst + (lane & 31) * KSTR + g * HALFD;
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-            sacc[kb] = (f32x16_t)0.0f;
-            const float* kr = k_lds + (kb * 32 + (lane & 31)) * KSTR + g * HALFD;
+            for (int j = 0; j < HALFD / 4; ++j)
 #pragma unroll
-            for (int ks = 0; ks < HALFD; ++ks)
-                sacc[kb] = __builtin_amdgcn_mfma_f32_32x32x2f32(kr[ks], qv[ks], sacc[kb], 0, 0, 0);
+                for (int kb = 0; kb < 2; ++kb) {
+                    const f32x4_t k4 = *(const f32x4_t*)(kr0 + kb * 32 * KSTR + 4 * j);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        sacc[kb] = __builtin_amdgcn_mfma_f32_32x32x2f32(k4[e], qv[4 * j + e],
+                                                                        sacc[kb], 0, 0, 0);
+                }
+        } else {
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+                sacc[kb] = (f32x16_t)0.0f;
+                const float* kr = kst + (kb * 32 + (lane & 31)) * KSTR + g * HALFD;
+#pragma unroll
+                for (int ks = 0; ks < HALFD; ++ks)
+                    sacc[kb] = __builtin_amdgcn_mfma_f32_32x32x2f32(kr[ks], qv[ks], sacc[kb], 0, 0, 0);
+            }
         }
 
         const int tile_end = (tile + 1) * BN;
@@ -1133,7 +1221,7 @@ __global__ __launch_bounds__(256, 1) void prefill_mfma_f32(PrefillKArgs ka) {
 
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb) {
-            const float* vc = v_lds + mb * 32 + (lane & 31);
+            const float* vc = vst + mb * 32 + (lane & 31);
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
@@ -1143,6 +1231,7 @@ __global__ __launch_bounds__(256, 1) void prefill_mfma_f32(PrefillKArgs ka) {
                                                                    oacc[mb], 0, 0, 0);
                 }
         }
+        if constexpr (DMA) wait_dma();
         __syncthreads();
     }
 
@@ -1211,12 +1300,12 @@ static void launch16(const PrefillKArgs& ka, bool paged, int dpad, dim3 grid, hi
     }
 }
 
-template <bool PAGED>
+template <bool PAGED, bool DMA = false>
 static void launch32(const PrefillKArgs& ka, int dpad, dim3 grid, hipStream_t s) {
     switch (dpad) {
-        case 32: prefill_mfma_f32<32, PAGED><<<grid, 256, 0, s>>>(ka); break;
-        case 64: prefill_mfma_f32<64, PAGED><<<grid, 256, 0, s>>>(ka); break;
-        default: prefill_mfma_f32<128, PAGED><<<grid, 256, 0, s>>>(ka); break;
+        case 32: prefill_mfma_f32<32, PAGED, DMA><<<grid, 256, 0, s>>>(ka); break;
+        case 64: prefill_mfma_f32<64, PAGED, DMA><<<grid, 256, 0, s>>>(ka); break;
+        default: prefill_mfma_f32<128, PAGED, DMA><<<grid, 256, 0, s>>>(ka); break;
     }
 }
 
@@ -1240,7 +1329,12 @@ void launch_prefill(Dtype dt, bool paged, const PrefillArgs& a, hipStream_t s, u
         case Dtype::BF16: launch16<bf16_t>(ka, paged, dpad, g, s); break;
         case Dtype::F16: launch16<f16_t>(ka, paged, dpad, g, s); break;
         default:
-            paged ? launch32<true>(ka, dpad, g, s) : launch32<false>(ka, dpad, g, s);
+            if (paged) launch32<true>(ka, dpad, g, s);
+            else if (!a.rope_k && a.head_dim % 4 == 0 && (uintptr_t)a.k % 16 == 0 &&
+                     (uintptr_t)a.v % 16 == 0 && a.k_ss % 4 == 0 && a.k_sh % 4 == 0 &&
+                     a.k_sb % 4 == 0)
+                launch32<false, true>(ka, dpad, g, s);  // 16-byte aligned rows: transfers
+            else launch32<false>(ka, dpad, g, s);
             break;
     }
 }
