@@ -799,14 +799,14 @@ __global__ __launch_bounds__(256, Blk<T>::ES == 2 ? 2 : 1) void bwd_dq(BackwardA
 // ------------------------------------------------------------------ dQ from the stored dS
 // dQ = scale * dS K with dS written by bwd_dkdv: one workgroup per (batch, query head, 256
 // queries), 32 per wave, eight waves sharing each 64-key K tile. Per tile the transfer unit
-// moves the K tile and every wave's two 2 KiB dS blocks (contiguous in a.ds) into one of three
-// LDS stages, two tiles ahead of the products (the kernel streams dS from HBM: 2 bytes per
-// (query, key) pair for 4 FLOP). The A operand of each MFMA (query c, eight consecutive keys)
-// is two transposing LDS reads of the stored rows of keys, the B operand the transposing read
-// of K. No exponentials and no S or dP products. Blocks past the causal diagonal or the
-// sequence are skipped like bwd_dq's, and every dS transfer is bounded to the allocation
-// (blocks of a query row past its last written one read other rows' data or zeros and are
-// never used).
+// moves the K tile and every wave's two 2 KiB dS blocks (key blocks 2 j and 2 j + 1 of its
+// rows, 8 KiB apart in a.ds) into one of three LDS stages, two tiles ahead of the products (the
+// kernel streams dS from HBM: 2 bytes per (query, key) pair for 4 FLOP). The A operand of each
+// MFMA (query c, eight consecutive keys) is two transposing LDS reads of the stored rows of
+// keys, the B operand the transposing read of K. No exponentials and no S or dP products.
+// Blocks past the causal diagonal or the sequence are skipped like bwd_dq's; their transfers
+// read unwritten or other tiles' groups (or zeros past the allocation, every dS transfer being
+// bounded to it), never used.
 constexpr int kDqDsQueries = 256;
 template <typename T, int DPAD>
 __global__ __launch_bounds__(512, 2) void bwd_dq_ds(BackwardArgs a) {
