@@ -1330,10 +1330,12 @@ void launch_prefill(Dtype dt, bool paged, const PrefillArgs& a, hipStream_t s, u
         case Dtype::F16: launch16<f16_t>(ka, paged, dpad, g, s); break;
         default:
             if (paged) launch32<true>(ka, dpad, g, s);
+            // transfers: 16-byte aligned rows, and one (batch, kv head) slice addressable by
+            // 32-bit buffer offsets (register staging uses 64-bit addresses)
             else if (!a.rope_k && a.head_dim % 4 == 0 && (uintptr_t)a.k % 16 == 0 &&
                      (uintptr_t)a.v % 16 == 0 && a.k_ss % 4 == 0 && a.k_sh % 4 == 0 &&
-                     a.k_sb % 4 == 0)
-                launch32<false, true>(ka, dpad, g, s);  // 16-byte aligned rows: transfers
+                     a.k_sb % 4 == 0 && (uint64_t)a.kv_len * (uint64_t)a.k_ss * 4u <= INT32_MAX)
+                launch32<false, true>(ka, dpad, g, s);
             else launch32<false>(ka, dpad, g, s);
             break;
     }
