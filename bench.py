@@ -130,6 +130,17 @@ def build_decode(ctx, rng, split=None):
         ctx.synchronize()
         prep_ms.append((time.perf_counter() - t0) * 1e3)
         p2.release()
+    # one serving step through the allocation-free entry point (work lists rebuilt on the host,
+    # the stream-ordered metadata copy and the kernels) until the stream has completed it, the
+    # Python call included; median of 10 after two warm-ups
+    na_ms = []
+    for _ in range(12):
+        t0 = time.perf_counter()
+        fa.paged_decode_noalloc(ctx, bt, ctx_lens, ps, total, hq, hkv, D,
+                                fa.FlatAttentionConfig(True), 10000.0, fa.DTYPE_BF16, q, kp, vp,
+                                out)
+        ctx.synchronize()
+        na_ms.append((time.perf_counter() - t0) * 1e3)
     nbytes = (float(ctx_lens.sum()) * hkv * D * 2 * 2 + n * hq * D * 2 * 2 + n * hq * 4
               + float(pages_per.sum()) * 4)
     run = lambda: plan.launch(q, kp, vp, out)  # noqa: E731
@@ -138,6 +149,7 @@ def build_decode(ctx, rng, split=None):
                                      "D128 bf16 KV, shuffled pages",
                          "bytes_per_step": nbytes, "live_tokens": int(ctx_lens.sum()),
                          "prepare_ms": round(float(np.median(prep_ms[1:])), 4),
+                         "noalloc_step_ms": round(float(np.median(na_ms[2:])), 4),
                          "split_tokens": info["split_tokens"], "work_items": info["work_items"]}
 
 
