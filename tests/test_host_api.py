@@ -391,3 +391,64 @@ def test_diagnostic_probes_validate_arguments():
     out = ctypes.c_double()
     assert lib.fa_diag_mfma_ceiling(None, 3, 0, ctypes.byref(out)) == 50  # NullArgument
     assert lib.fa_diag_stream_read(None, 8, ctypes.byref(out)) == 50
+
+
+# --------------------------------------------------------------------------- contract fuzz
+# tests/m39_host_api_fuzz.rs drives 4096 arbitrary shapes and configs (dimensions 0, 1, the
+# integer maximum, half of it plus one, 128, 129 or 1..65; scales absent, 0, -1, NaN, +inf or
+# in (0, 1]) through the host contract and requires that nothing panics. The same sweep goes
+# through the C ABI here: with a null context every call must return a known error status (the
+# context is only reported after the arguments are valid, so no call reaches the device), and
+# the pure host layout / scale functions must return a known status too.
+
+
+class _Fuzz:
+    """xorshift64 stream with the reference's seed and value classes (restated)."""
+
+    def __init__(self, seed):
+        self.x = seed
+
+    def next(self):
+        x = self.x
+        x ^= (x << 13) & 0xFFFFFFFFFFFFFFFF
+        x ^= x >> 7
+        x ^= (x << 17) & 0xFFFFFFFFFFFFFFFF
+        self.x = x
+        return x
+
+    def dimension(self):
+        m = self.next() & 15
+        if m < 6:
+            return (0, 1, 2**64 - 1, 2**63 + 1, 128, 129)[m]
+        return self.next() % 65 + 1
+
+    def scale(self):
+        m = self.next() & 7
+        if m < 5:
+            return (None, 0.0, -1.0, float("nan"), float("inf"))[m]
+        return ((self.next() % 10_000) + 1.0) / 10_000.0
+
+
+def test_host_contract_fuzz_fails_closed():
+    known = set(L.STATUS)
+    st = _Fuzz(0x6D39F0221BADC0DE)
+    lib = fa.lib()
+    lay = L.BackwardLayoutC()
+    scale_out = ctypes.c_float()
+    for case in range(4096):
+        b, hq, hkv, s, d, off = (st.dimension() for _ in range(6))
+        cfg = fa.FlatAttentionConfig(st.next() & 1 == 0, st.scale())
+        dtype = (fa.DTYPE_F32, fa.DTYPE_F16, fa.DTYPE_BF16, 7)[st.next() & 3]
+        q_bytes, kv_bytes, out_bytes = (st.next() % (1 << 41) for _ in range(3))
+        rc = _gqa(fa.GroupedAttentionShape(b, hq, hkv, s, d), cfg, None, dtype, q_bytes,
+                  kv_bytes, out_bytes)
+        assert rc in known and rc != 0, (case, rc)
+        ash = fa.AsymmetricGroupedAttentionShape(b, hq, hkv, s, st.dimension(), d, off)
+        rc = lib.fa_forward_projection_asymmetric(None, FAKE, q_bytes, FAKE, FAKE, kv_bytes, FAKE,
+                                                  out_bytes, ctypes.byref(ash.c()),
+                                                  ctypes.byref(cfg.c()), None, 0, dtype)
+        assert rc in known and rc != 0, (case, rc)
+        assert lib.fa_resolved_scale(ctypes.byref(cfg.c()), d, ctypes.byref(scale_out)) in known
+        rc = lib.fa_backward_grouped_layout(ctypes.byref(fa.GroupedAttentionShape(
+            b, hq, hkv, s, d).c()), dtype, ctypes.byref(lay))
+        assert rc in known, (case, rc)
