@@ -130,6 +130,26 @@ uint64_t fnv1a64(const std::string& s) {
     return h;
 }
 
+// escape_component src/runtime_telemetry.rs:70-81: the record's delimiters inside a value
+std::string escape_component(const char* v) {
+    std::string out;
+    for (const char* c = v; *c; ++c) {
+        if (*c == '%') out += "%25";
+        else if (*c == ';') out += "%3b";
+        else if (*c == '=') out += "%3d";
+        else out += *c;
+    }
+    return out;
+}
+
+std::string device_record(const char* name, const char* arch, int driver, int cus,
+                          int clock_khz, uint64_t mem_bytes) {
+    char tail[160];
+    snprintf(tail, sizeof tail, ";driver=%d;cus=%d;clock_khz=%d;mem=%llu", driver, cus,
+             clock_khz, (unsigned long long)mem_bytes);
+    return "name=" + escape_component(name) + ";arch=" + escape_component(arch) + tail;
+}
+
 void copy_str(char* dst, size_t cap, const std::string& s) {
     size_t n = std::min(cap - 1, s.size());
     memcpy(dst, s.data(), n);
@@ -500,11 +520,9 @@ int fa_ctx_create(int device, fa_ctx** out) {
     ctx->arch = arch;
     int drv = 0;
     (void)hipDriverGetVersion(&drv);
-    char rec[512];
-    snprintf(rec, sizeof rec, "name=%s;arch=%s;driver=%d;cus=%d;clock_khz=%d;mem=%zu",
-             prop.name, arch.c_str(), drv, prop.multiProcessorCount, prop.clockRate,
-             (size_t)prop.totalGlobalMem);
-    ctx->fingerprint = fnv1a64(rec);
+    ctx->fingerprint = fnv1a64(device_record(prop.name, arch.c_str(), drv,
+                                             prop.multiProcessorCount, prop.clockRate,
+                                             (uint64_t)prop.totalGlobalMem));
     if (hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking) != hipSuccess) {
         delete ctx;
         return fail(FA_ERR_HIP, "hipStreamCreate failed");
@@ -558,6 +576,16 @@ int fa_ctx_synchronize(fa_ctx* ctx) {
 int fa_ctx_device_name(fa_ctx* ctx, char* buf, size_t len) {
     if (!ctx || !buf || !len) return fail(FA_ERR_NULL_ARGUMENT, "null argument");
     copy_str(buf, len, ctx->name + " (" + ctx->arch + ")");
+    return ok();
+}
+
+int fa_device_record(const char* name, const char* arch, int32_t driver, int32_t cus,
+                     int32_t clock_khz, uint64_t mem_bytes, char* out, size_t cap,
+                     uint64_t* fingerprint) {
+    if (!name || !arch || !fingerprint) return fail(FA_ERR_NULL_ARGUMENT, "null argument");
+    const std::string rec = device_record(name, arch, driver, cus, clock_khz, mem_bytes);
+    if (out && cap) copy_str(out, cap, rec);
+    *fingerprint = fnv1a64(rec);
     return ok();
 }
 

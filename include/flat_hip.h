@@ -167,7 +167,7 @@ typedef struct fa_telemetry {
     char fallback_reason[128];
     char device_name[64];
     char device_arch[32];
-    uint64_t device_fingerprint;  /* FNV-1a-64 of the canonical device record */
+    uint64_t device_fingerprint;  /* FNV-1a-64 of the canonical device record (fa_device_record) */
 } fa_telemetry;
 
 typedef struct fa_ctx fa_ctx;
@@ -537,6 +537,16 @@ int fa_ctx_set_prefill_v_layout(fa_ctx* ctx, int32_t transpose_v);
 int fa_ctx_set_backward_policy(fa_ctx* ctx, int32_t store_ds);
 int fa_kernel_variant_for_shape(fa_ctx* ctx, uint64_t head_dim, int32_t has_rope, int dtype,
                                 int32_t* kernel_id);
+
+/* RuntimeDeviceFingerprint::{canonical_record, stable_fingerprint} src/runtime_telemetry.rs:49-67
+ * (escape_component :70, fnv1a64 :83): the device record behind fa_telemetry::device_fingerprint,
+ * "name=..;arch=..;driver=..;cus=..;clock_khz=..;mem=.." with '%', ';' and '=' inside values
+ * escaped as %25, %3b and %3d, and its FNV-1a-64 hash. The fields are this build's (the HIP
+ * device properties), not the WGPU adapter's. Writes the record (truncated to cap - 1 bytes,
+ * NUL-terminated) when out is not null. Pure host code. */
+int fa_device_record(const char* name, const char* arch, int32_t driver, int32_t cus,
+                     int32_t clock_khz, uint64_t mem_bytes, char* out, size_t cap,
+                     uint64_t* fingerprint);
 
 /* Measurement aids (no counterpart in the reference): the practical ceilings the rooflines are
  * read against. fa_diag_mfma_ceiling runs back-to-back v_mfma_f32_32x32x16_bf16 (dtype

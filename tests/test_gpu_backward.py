@@ -358,3 +358,48 @@ def test_stored_ds_falls_back_to_recompute_past_2gib(hip):
     dv_want = p.T @ do.reshape(S, D)[-W:]
     assert_close("dV-tail", got.dv.reshape(S, D)[-W:], dv_want,
                  2e-2 * float(np.abs(dv_want).max()), 2e-2)
+
+
+def fx_m20_adversarial(n, phase):
+    """tests/m20_adversarial_numerics.rs:48 fixture: bucketed values up to +-2.09 with
+    alternating signs and a small ripple (adversarial but finite)."""
+    i = np.arange(n, dtype=np.int64)
+    bucket = ((i * 17 + phase * 11) % 23 - 11).astype(np.float32)
+    sign = np.where((i + phase) % 2 == 0, 1.0, -1.0).astype(np.float32)
+    ripple = np.sin((i + phase).astype(np.float32) * np.float32(0.013)) * np.float32(0.07)
+    return (sign * bucket * np.float32(0.19) + ripple).astype(np.float32)
+
+
+M20_ADVERSARIAL = [((1, 8, 2, 17, 64), True, None), ((1, 8, 1, 33, 32), False, 0.31)]
+
+
+@pytest.mark.parametrize("idx", range(len(M20_ADVERSARIAL)))
+def test_m20_adversarial_numerics(hip, idx):
+    """tests/m20_adversarial_numerics.rs:200: the grouped backward on adversarial but finite
+    inputs (phases index * 13 + 1, 3, 5, 7 for Q, K, V, dO), 1e-3 + 5e-3 |e|, every gradient
+    finite."""
+    dims, causal, scale = M20_ADVERSARIAL[idx]
+    ph = idx * 13
+    _packed_case(hip, fa.GroupedAttentionShape(*dims), fa.FlatAttentionConfig(causal, scale),
+                 fx_m20_adversarial, (ph + 1, ph + 3, ph + 5, ph + 7), 1, 1e-3, 5e-3)
+
+
+@pytest.mark.parametrize("idx", range(len(M20_ADVERSARIAL)))
+def test_m20_adversarial_numerics_bf16_stored_ds(hip, idx):
+    """The same adversarial inputs rounded to bf16 through the default 16-bit path (dS stored by
+    the dK/dV kernel): against the oracle given the same rounded inputs and forward."""
+    dims, causal, scale = M20_ADVERSARIAL[idx]
+    B, Hq, Hkv, S, D = dims
+    ph = idx * 13
+    q, k, v, do = (bf16_round(fx_m20_adversarial(n, ph + p)) for n, p in (
+        (B * Hq * S * D, 1), (B * Hkv * S * D, 3), (B * Hkv * S * D, 5), (B * Hq * S * D, 7)))
+    shape = fa.GroupedAttentionShape(*dims)
+    fwd, _ = _expected(q, k, v, do, shape, causal, scale)
+    fwd = fa.FlatAttentionOutput(bf16_round(fwd.output), fwd.lse)
+    want = oracle.backward_grouped(q, k, v, do, fwd.output, fwd.lse, B, Hq, Hkv, S, D, causal,
+                                   scale, threads=8)
+    got = fa.HipGroupedBackwardRecomputePipeline(hip, fa.DTYPE_BF16).backward(
+        q, k, v, do, fwd, shape, fa.FlatAttentionConfig(causal, scale))
+    assert "bwd_dq_ds" in hip.last_telemetry().kernel_name
+    for name, a, e in zip(("dQ", "dK", "dV"), (got.dq, got.dk, got.dv), want):
+        assert_close(name, a, e, 2e-2 * float(np.abs(e).max()), 2e-2)

@@ -452,3 +452,35 @@ def test_host_contract_fuzz_fails_closed():
         rc = lib.fa_backward_grouped_layout(ctypes.byref(fa.GroupedAttentionShape(
             b, hq, hkv, s, d).c()), dtype, ctypes.byref(lay))
         assert rc in known, (case, rc)
+
+
+# --------------------------------------------------------------------------- device fingerprint
+def _record(name, arch="gfx950", driver=70000, cus=256, clock=2400000, mem=288 << 30):
+    buf = ctypes.create_string_buffer(512)
+    fp = ctypes.c_uint64()
+    assert fa.lib().fa_device_record(name.encode(), arch.encode(), driver, cus, clock, mem, buf,
+                                     512, ctypes.byref(fp)) == 0
+    return buf.value.decode(), fp.value
+
+
+def _fnv1a64(data: bytes) -> int:
+    h = 0xCBF29CE484222325
+    for byte in data:
+        h = ((h ^ byte) * 0x100000001B3) & 0xFFFFFFFFFFFFFFFF
+    return h
+
+
+def test_device_fingerprint_is_deterministic_driver_sensitive_and_escaped():
+    """src/runtime_telemetry.rs:197-215 (the reference's unit tests of the record): the hash is
+    deterministic and changes with the driver; delimiters inside a value are escaped while UTF-8
+    is kept; the hash is FNV-1a-64 of the record's bytes (offset basis 0xcbf29ce484222325,
+    prime 0x100000001b3; the empty input hashes to the basis)."""
+    rec, fp = _record("AMD Instinct MI355X")
+    assert _record("AMD Instinct MI355X") == (rec, fp)
+    assert _record("AMD Instinct MI355X", driver=70001)[1] != fp
+    assert rec == "name=AMD Instinct MI355X;arch=gfx950;driver=70000;cus=256;clock_khz=2400000;mem=309237645312"
+    assert fp == _fnv1a64(rec.encode())
+    assert _fnv1a64(b"") == 0xCBF29CE484222325
+    assert _fnv1a64(b"a") == 0xAF63DC4C8601EC8C  # published FNV-1a-64 test vector
+    rec2, _ = _record("GPU été;a=b%")
+    assert "name=GPU été%3ba%3db%25;" in rec2
