@@ -360,6 +360,8 @@ def test_backward_validation_variants():
     assert _backward(shape=(1, 2, 1, 8, 12), dtype=fa.DTYPE_BF16) == "UnsupportedHeadDim"
     assert _backward(shape=(1, 2, 1, 8, 6)) == "NullArgument"
     assert _backward() == "NullArgument"
+    # tests/m22_prepared_validation.rs:143: overprovisioned buffers pass validation
+    assert _backward(fwd=1 << 30, grads=1 << 30, cfg=L.ConfigC(1, 1, 0.25)) == "NullArgument"
 
 
 def test_mha_backward_layout_and_validation():
