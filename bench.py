@@ -225,6 +225,25 @@ def build_resident_decode(ctx, rng, dtype):
     return (lambda: plan.launch(q, k, v, out)), nbytes
 
 
+def build_m48_decode(ctx, rng, kv_len):
+    """The M48 candidate (encode_pre_rotated_k_decode_kv_reuse src/wgpu_external_asymmetric.rs:216)
+    at the published shape B1 Hq16 Hkv4 D64 f32 (docs/M48_THOR_REQUALIFICATION.md:65-69): one
+    call validates, builds the one-page-per-sequence plan, launches and releases it."""
+    B, hq, hkv, D = 1, 16, 4, 64
+    width = hkv * D
+    mk = lambda n: rng.standard_normal(n, dtype=np.float32)  # noqa: E731
+    k = fa.DeviceBuffer.from_array(ctx, mk(B * kv_len * width))
+    v = fa.DeviceBuffer.from_array(ctx, mk(B * kv_len * width))
+    q = fa.DeviceBuffer.from_array(ctx, mk(B * hq * D))
+    shape = fa.AsymmetricGroupedAttentionShape(B, hq, hkv, 1, kv_len, D, kv_len - 1)
+    rot = fa.AsymmetricRotaryEmbeddingConfig(1e4, kv_len - 1, 0)
+    pipe = fa.HipAsymmetricProjectionPipeline.with_decode_kv_reuse(ctx, True)
+    out = pipe.create_output_buffer(shape)
+    cfg = fa.FlatAttentionConfig(True)
+    nbytes = 2.0 * B * kv_len * width * 4 + B * hq * D * 4 * 2 + B * hq * 4
+    return (lambda: pipe.encode_pre_rotated_k_decode_kv_reuse(q, k, v, out, shape, cfg, rot)), nbytes
+
+
 def build_backward(ctx, rng, S=4096, data="normal"):
     """Recompute backward (dQ, dK, dV) at the prefill's shape without RoPE (the reference's
     backward has none): causal GQA B2 Hq32 Hkv8 D128 bf16. Algorithmic work: the five
@@ -354,6 +373,15 @@ def measure_all_configs(ctx, ev, rng, steps):
             "GB/s": round(nbytes / (k_ms * 1e-3) / 1e9, 1),
             "note": "one sequence: the op time is launch-bound, GB/s uses the kernel time",
             "reference_published_ms": {"M15": 23.843433, "M48": 19.562844,
+                                       "hardware": "Jetson Thor, Vulkan, f32 (not comparable)"}}
+    for kv_len, ref_ms in ((8192, 19.562844), (512, 1.317097)):
+        run, nbytes = build_m48_decode(ctx, rng, kv_len)
+        op_ms, k_ms, tel = timed(run)
+        res[f"m48_decode_kv_reuse_B1_Hq16_Hkv4_D64_kv{kv_len}_f32"] = {
+            "kernel": tel.kernel_name, "ms": round(op_ms, 4), "kernel_ms": round(k_ms, 4),
+            "GB/s": round(nbytes / (k_ms * 1e-3) / 1e9, 1),
+            "note": "ms includes the per-call plan (table upload, release waits for the stream)",
+            "reference_published_ms": {"M48": ref_ms,
                                        "hardware": "Jetson Thor, Vulkan, f32 (not comparable)"}}
     return res
 

@@ -1163,13 +1163,12 @@ int fa_forward_mha(fa_ctx* ctx, const void* q, const void* k, const void* v, siz
                                nullptr, dtype);
 }
 
-int fa_forward_projection_asymmetric(fa_ctx* ctx, const void* q, size_t q_bytes, const void* k,
-                                     const void* v, size_t kv_bytes, void* out_lse,
-                                     size_t out_bytes, const fa_asymmetric_shape* sh,
-                                     const fa_config* cfg, const fa_asymmetric_rotary* rot,
-                                     int32_t rotate_k, int dtype) {
-    if (!sh) return fail(FA_ERR_NULL_ARGUMENT, "shape is null");
-    if (int rc = check_dtype(dtype)) return rc;
+}  // extern "C"
+
+namespace {
+
+// AsymmetricGroupedAttentionShape::validate (zero dimensions, head grouping, overflow).
+int check_asymmetric_shape(const fa_asymmetric_shape* sh) {
     if (!sh->batch || !sh->q_heads || !sh->kv_heads || !sh->query_len || !sh->kv_len ||
         !sh->head_dim)
         return fail(FA_ERR_ZERO_DIMENSION, "attention dimensions must all be non-zero");
@@ -1177,9 +1176,17 @@ int fa_forward_projection_asymmetric(fa_ctx* ctx, const void* q, size_t q_bytes,
         return fail(FA_ERR_INVALID_HEAD_GROUPING,
                     "q_heads (%llu) must be exactly divisible by kv_heads (%llu)",
                     (unsigned long long)sh->q_heads, (unsigned long long)sh->kv_heads);
-    if (int rc = validate_grouped(sh->batch, sh->q_heads, sh->kv_heads,
-                                  std::max(sh->query_len, sh->kv_len), sh->head_dim))
-        return rc;
+    return validate_grouped(sh->batch, sh->q_heads, sh->kv_heads,
+                            std::max(sh->query_len, sh->kv_len), sh->head_dim);
+}
+
+// The remaining checks of encode_with_options src/wgpu_external_asymmetric.rs:291 that precede
+// device work: positions, RoPE, head_dim, scale and buffer sizes. Fills the scale and layout.
+int check_asymmetric_pass(const fa_asymmetric_shape* sh, const fa_config* cfg,
+                          const fa_asymmetric_rotary* rot, int dtype, const void* q,
+                          size_t q_bytes, const void* k, const void* v, size_t kv_bytes,
+                          const void* out_lse, size_t out_bytes, float* scale,
+                          fa_packed_layout* lay) {
     if (sh->query_position_offset + sh->query_len > kI32)
         return fail(FA_ERR_POSITION_OVERFLOW, "rotary position offset overflows the index space");
     if (rot) {
@@ -1189,22 +1196,41 @@ int fa_forward_projection_asymmetric(fa_ctx* ctx, const void* q, size_t q_bytes,
             return rc;
     }
     if (int rc = check_head_dim(sh->head_dim, dtype)) return rc;
-    float scale;
-    if (int rc = resolve_scale(cfg, sh->head_dim, &scale)) return rc;
+    if (int rc = resolve_scale(cfg, sh->head_dim, scale)) return rc;
     const uint64_t eb = elem_bytes(dtype);
     const uint64_t qn = sh->batch * sh->query_len * sh->q_heads * sh->head_dim;
     const uint64_t kvn = sh->batch * sh->kv_len * sh->kv_heads * sh->head_dim;
-    fa_packed_layout lay;
-    if (int rc = fa_packed_layout_for(qn, sh->batch * sh->q_heads * sh->query_len, dtype, &lay))
+    if (int rc = fa_packed_layout_for(qn, sh->batch * sh->q_heads * sh->query_len, dtype, lay))
         return rc;
     if (int rc = check_buffer("Q", q, q_bytes, qn * eb)) return rc;
     if (int rc = check_buffer("K", k, kv_bytes, kvn * eb)) return rc;
     if (int rc = check_buffer("V", v, kv_bytes, kvn * eb)) return rc;
-    if (int rc = check_buffer("O|LSE", out_lse, out_bytes, lay.combined_bytes)) return rc;
+    return check_buffer("O|LSE", out_lse, out_bytes, lay->combined_bytes);
+}
+
+}  // namespace
+
+extern "C" {
+
+int fa_forward_projection_asymmetric(fa_ctx* ctx, const void* q, size_t q_bytes, const void* k,
+                                     const void* v, size_t kv_bytes, void* out_lse,
+                                     size_t out_bytes, const fa_asymmetric_shape* sh,
+                                     const fa_config* cfg, const fa_asymmetric_rotary* rot,
+                                     int32_t rotate_k, int dtype) {
+    if (!sh) return fail(FA_ERR_NULL_ARGUMENT, "shape is null");
+    if (int rc = check_dtype(dtype)) return rc;
+    if (int rc = check_asymmetric_shape(sh)) return rc;
+    float scale;
+    fa_packed_layout lay;
+    if (int rc = check_asymmetric_pass(sh, cfg, rot, dtype, q, q_bytes, k, v, kv_bytes, out_lse,
+                                       out_bytes, &scale, &lay))
+        return rc;
     if (!ctx) return fail(FA_ERR_NULL_ARGUMENT, "context is null");
     begin_call(ctx);
     if (int rc = set_device(ctx)) return rc;
 
+    const uint64_t eb = elem_bytes(dtype);
+    const uint64_t kvn = sh->batch * sh->kv_len * sh->kv_heads * sh->head_dim;
     PrefillJob j{};
     j.dt = (Dtype)dtype;
     j.dtype = dtype;
@@ -2498,6 +2524,64 @@ int fa_resident_cache_decode(fa_ctx* ctx, const fa_resident_cache* c, const void
     const uint64_t abytes = ctx->call_alloc_bytes;
     int rc = fa_paged_decode_launch(ctx, p, q, q_bytes, c->k, c->v, c->tensor_bytes, out_lse,
                                     out_bytes);
+    ctx->last.temporary_allocation_count += allocs;
+    ctx->last.temporary_allocation_bytes += abytes;
+    fa_paged_decode_plan_destroy(p);
+    return rc ? rc : ok();
+}
+
+// ExternalAsymmetricProjectionRotaryGroupedPipeline::encode_pre_rotated_k_decode_kv_reuse
+// src/wgpu_external_asymmetric.rs:216: the candidate's own shape checks, then those of
+// encode_with_options :291. The [batch, kv_len, Hkv*D] K/V tensors are a page pool with one
+// kv_len-row page per batch element, so the grouped paged decode runs it: one wave group per
+// (sequence, KV head) holds each K/V tile once for all q_heads / kv_heads query heads. Causal
+// masking at query_position_offset p keeps keys 0..p, i.e. a live length of min(kv_len, p + 1).
+// Head dims the decode kernels do not tile (not a multiple of 4 for f32, 8 for 16-bit) take the
+// pre-rotated-K prefill kernel, whose result is the same attention.
+int fa_forward_projection_asymmetric_decode_kv_reuse(fa_ctx* ctx, const void* q, size_t q_bytes,
+                                                     const void* k, const void* v,
+                                                     size_t kv_bytes, void* out_lse,
+                                                     size_t out_bytes,
+                                                     const fa_asymmetric_shape* sh,
+                                                     const fa_config* cfg,
+                                                     const fa_asymmetric_rotary* rot, int dtype) {
+    if (!sh || !rot) return fail(FA_ERR_NULL_ARGUMENT, "null argument");
+    if (int rc = check_dtype(dtype)) return rc;
+    if (int rc = check_asymmetric_shape(sh)) return rc;
+    if (sh->query_len != 1)
+        return fail(FA_ERR_UNSUPPORTED_CANDIDATE_SHAPE,
+                    "external FLAT candidate M48 does not support this shape: query_len must "
+                    "equal 1");
+    if (sh->q_heads / sh->kv_heads < 2)
+        return fail(FA_ERR_UNSUPPORTED_CANDIDATE_SHAPE,
+                    "external FLAT candidate M48 does not support this shape: GQA group size "
+                    "must be at least 2");
+    float scale;
+    fa_packed_layout lay;
+    if (int rc = check_asymmetric_pass(sh, cfg, rot, dtype, q, q_bytes, k, v, kv_bytes, out_lse,
+                                       out_bytes, &scale, &lay))
+        return rc;
+    if (!ctx) return fail(FA_ERR_NULL_ARGUMENT, "context is null");
+    if (sh->head_dim % (dtype == FA_DTYPE_F32 ? 4 : 8))
+        return fa_forward_projection_asymmetric(ctx, q, q_bytes, k, v, kv_bytes, out_lse,
+                                                out_bytes, sh, cfg, rot, 0, dtype);
+    const uint64_t live = cfg && cfg->causal
+                              ? std::min<uint64_t>(sh->kv_len, sh->query_position_offset + 1)
+                              : sh->kv_len;
+    std::vector<int32_t> table(sh->batch), lens(sh->batch, (int32_t)live),
+        qpos(sh->batch, (int32_t)rot->query_position_offset);
+    for (uint64_t b = 0; b < sh->batch; ++b) table[b] = (int32_t)b;
+    fa_config nc{};
+    if (cfg) nc = *cfg;
+    nc.causal = 0;  // applied above as the live length
+    fa_decode_plan* p = nullptr;
+    if (int rc = fa_paged_decode_prepare(ctx, table.data(), 1, lens.data(), qpos.data(), sh->batch,
+                                         sh->kv_len, sh->batch, sh->q_heads, sh->kv_heads,
+                                         sh->head_dim, &nc, rot->theta, dtype, &p))
+        return rc;
+    const uint32_t allocs = ctx->call_allocs;
+    const uint64_t abytes = ctx->call_alloc_bytes;
+    int rc = fa_paged_decode_launch(ctx, p, q, q_bytes, k, v, kv_bytes, out_lse, out_bytes);
     ctx->last.temporary_allocation_count += allocs;
     ctx->last.temporary_allocation_bytes += abytes;
     fa_paged_decode_plan_destroy(p);

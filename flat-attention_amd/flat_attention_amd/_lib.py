@@ -32,7 +32,8 @@ STATUS = {
     21: "UnsupportedHeadDim", 22: "IndexSpaceExceeded", 23: "DispatchLimit",
     24: "BufferTooSmall", 25: "EmptyTable", 26: "TooManyMappedPages",
     27: "CausalVisibilityMismatch", 28: "ZeroQueryChunkSize", 29: "UnsupportedDtype",
-    30: "InvalidPage", 31: "EmptyCache", 32: "InvalidCacheLength", 33: "ForeignBuffer", 40: "PagedZeroDimension", 41: "CapacityOverflow",
+    30: "InvalidPage", 31: "EmptyCache", 32: "InvalidCacheLength", 33: "ForeignBuffer", 34: "CandidateNotEnabled",
+    35: "UnsupportedCandidateShape", 40: "PagedZeroDimension", 41: "CapacityOverflow",
     42: "CapacityExceeded", 43: "GenerationOverflow", 50: "NullArgument", 60: "Hip",
     61: "ScratchExceeded",
 }
@@ -146,6 +147,9 @@ PROTOTYPES = {
     "fa_forward_projection_asymmetric": (INT, [VP, VP, SZ, VP, VP, SZ, VP, SZ,
                                                P(AsymmetricShapeC), P(ConfigC),
                                                P(AsymmetricRotaryC), I32, INT]),
+    "fa_forward_projection_asymmetric_decode_kv_reuse": (INT, [
+        VP, VP, SZ, VP, VP, SZ, VP, SZ, P(AsymmetricShapeC), P(ConfigC), P(AsymmetricRotaryC),
+        INT]),
     "fa_chunked_prefill": (INT, [VP, VP, SZ, VP, VP, SZ, VP, SZ, P(GroupedShapeC), P(ConfigC),
                                  P(RotaryC), U64, INT]),
     "fa_kv_table_create": (INT, [U64, U64, P(VP)]),

@@ -527,11 +527,24 @@ class PreparedGroupedForward:
 
 class HipAsymmetricProjectionPipeline:
     """ExternalAsymmetricProjectionRotaryGroupedPipeline src/wgpu_external_asymmetric.rs
-    (rectangular projection-layout GQA + RoPE; encode :192 / encode_pre_rotated_k :203)."""
+    (rectangular projection-layout GQA + RoPE; encode :192 / encode_pre_rotated_k :203).
 
-    def __init__(self, ctx: HipContext, dtype: int = L.DTYPE_F32):
+    ``decode_kv_reuse=True`` (with_decode_kv_reuse :81) enables the opt-in M48 q_len = 1
+    candidate, encode_pre_rotated_k_decode_kv_reuse; encode and encode_pre_rotated_k keep their
+    route either way."""
+
+    def __init__(self, ctx: HipContext, dtype: int = L.DTYPE_F32, decode_kv_reuse: bool = False):
         self.ctx = ctx
         self.dtype = dtype
+        self.decode_kv_reuse = bool(decode_kv_reuse)
+
+    @classmethod
+    def with_decode_kv_reuse(cls, ctx: HipContext, enable_candidate: bool,
+                             dtype: int = L.DTYPE_F32) -> "HipAsymmetricProjectionPipeline":
+        return cls(ctx, dtype, decode_kv_reuse=enable_candidate)
+
+    def create_output_buffer(self, shape: AsymmetricGroupedAttentionShape) -> DeviceBuffer:
+        return DeviceBuffer(self.ctx, self.layout(shape).combined_bytes)
 
     def layout(self, shape: AsymmetricGroupedAttentionShape) -> PackedLayout:
         return packed_layout(shape.q_tensor_len(), shape.lse_len(), self.dtype)
@@ -545,6 +558,19 @@ class HipAsymmetricProjectionPipeline:
 
     def encode_pre_rotated_k(self, q, k, v, out, shape, config, rotary):
         self.encode(q, k, v, out, shape, config, rotary, rotate_k=False)
+
+    def encode_pre_rotated_k_decode_kv_reuse(self, q, k, v, out, shape, config,
+                                             rotary) -> PackedLayout:
+        """encode_pre_rotated_k_decode_kv_reuse :216 (M48): q_len = 1 decode over pre-rotated K
+        whose K/V tiles are read once per GQA group; CandidateNotEnabled unless the pipeline was
+        built with the candidate."""
+        if not self.decode_kv_reuse:
+            raise L.FlatHipError(34, "external FLAT candidate M48 was not enabled")
+        check(lib().fa_forward_projection_asymmetric_decode_kv_reuse(
+            self.ctx.handle, q.ptr, q.nbytes, k.ptr, v.ptr, min(k.nbytes, v.nbytes), out.ptr,
+            out.nbytes, ctypes.byref(shape.c()), ctypes.byref(config.c()),
+            ctypes.byref(rotary.c()), self.dtype))
+        return self.layout(shape)
 
 
 @dataclass(frozen=True)

@@ -72,6 +72,9 @@ typedef enum fa_status {
     FA_ERR_INVALID_CACHE_LENGTH = 32, /* ResidentDecodeError::InvalidCacheLength :106 */
     FA_ERR_FOREIGN_BUFFER = 33,       /* WgpuFlatAttentionError::ForeignBuffer src/wgpu_backend.rs:56:
                                          a prepared object used with another context */
+    FA_ERR_CANDIDATE_NOT_ENABLED = 34,        /* ExternalWgpuError::CandidateNotEnabled
+                                               * src/wgpu_external.rs:62 */
+    FA_ERR_UNSUPPORTED_CANDIDATE_SHAPE = 35,  /* ExternalWgpuError::UnsupportedCandidateShape :65 */
     FA_ERR_PAGED_ZERO_DIMENSION = 40,
     FA_ERR_CAPACITY_OVERFLOW = 41,
     FA_ERR_CAPACITY_EXCEEDED = 42,
@@ -262,6 +265,23 @@ int fa_forward_projection_asymmetric(fa_ctx* ctx, const void* q, size_t q_bytes,
                                      const fa_asymmetric_shape* shape, const fa_config* config,
                                      const fa_asymmetric_rotary* rotary, int32_t rotate_k,
                                      int dtype);
+
+/* ExternalAsymmetricProjectionRotaryGroupedPipeline::encode_pre_rotated_k_decode_kv_reuse
+ * src/wgpu_external_asymmetric.rs:216 (the opt-in M48 candidate): q_len = 1 decode over
+ * pre-rotated K in projection layout, each K/V tile read once for every query head of its GQA
+ * group. Fails with FA_ERR_UNSUPPORTED_CANDIDATE_SHAPE unless query_len == 1 and
+ * q_heads / kv_heads >= 2, then checks as fa_forward_projection_asymmetric. Q is rotated at
+ * rotary->query_position_offset; causal masking keeps keys <= shape->query_position_offset.
+ * Output [O | LSE] as for fa_forward_projection_asymmetric. Prepares, launches and releases a
+ * decode plan (waits for the stream when releasing). */
+int fa_forward_projection_asymmetric_decode_kv_reuse(fa_ctx* ctx, const void* q, size_t q_bytes,
+                                                     const void* k, const void* v,
+                                                     size_t kv_bytes, void* out_lse,
+                                                     size_t out_bytes,
+                                                     const fa_asymmetric_shape* shape,
+                                                     const fa_config* config,
+                                                     const fa_asymmetric_rotary* rotary,
+                                                     int dtype);
 
 /* WgpuChunkedProjectionPrefillPipeline::encode src/wgpu_chunked_prefill.rs:156: full-sequence
  * projection-layout GQA + RoPE prefill whose query rows are processed in chunks of

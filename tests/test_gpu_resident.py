@@ -123,3 +123,121 @@ def test_external_decode_rejects_invisible_rows_and_query_len(hip):
             buf, buf, buf, buf, fa.AsymmetricGroupedAttentionShape(1, 2, 1, 2, 40, 64, 39),
             fa.FlatAttentionConfig(True), fa.AsymmetricRotaryEmbeddingConfig(1e4, 39, 0), 64)
     assert e.value.variant == "LengthMismatch"
+
+
+def _m15_fixture(n, phase):
+    x = np.arange(n, dtype=np.float32) * np.float32(0.023) + np.float32(phase)
+    return (np.sin(x) * 1.125 + np.cos(x * np.float32(0.29)) * 0.4375).astype(np.float32)
+
+
+def test_one_pipeline_tracks_token_by_token_cache_growth(hip):
+    """tests/m15_growing_cache.rs:146: one pipeline and one output buffer serve a capacity-6
+    cache grown one pre-rotated K row at a time; after every append the decode at the newest
+    position matches the raw-K asymmetric RoPE oracle (projection_asymmetric.rs:97)."""
+    hq, hkv, cap, D, theta = 4, 1, 6, 32, 1e4
+    cache = fa.HipResidentKvCache(hip, 1, hkv, cap, D, fa.DTYPE_F32)
+    pipe = fa.HipResidentDecodePipeline(hip, fa.DTYPE_F32)
+    out = None
+    raw_k, vs = [], []
+    for pos in range(cap):
+        k_row = _m15_fixture(D, 0.4 + pos * 0.13)
+        v_row = _m15_fixture(D, 1.1 + pos * 0.17)
+        raw_k.append(k_row)
+        vs.append(v_row)
+        rot = oracle.rope_rotate_rows(k_row, 1, hkv, D, theta, position_offset=pos)
+        assert cache.record_append(fa.DeviceBuffer.from_array(hip, rot),
+                                   fa.DeviceBuffer.from_array(hip, v_row), 1) == pos + 1
+        assert len(cache) == pos + 1
+        if out is None:
+            out = pipe.create_output_buffer(cache, hq)
+        q = _m15_fixture(hq * D, 2.0 + pos * 0.19)
+        lay = pipe.encode(fa.DeviceBuffer.from_array(hip, q), cache, out, hq,
+                          fa.FlatAttentionConfig(True), theta, pos)
+        res = fa.download_attention(out, lay, fa.DTYPE_F32)
+        eo, el = oracle.forward_projection_asymmetric(
+            q, np.concatenate(raw_k), np.concatenate(vs), 1, hq, hkv, 1, pos + 1, D, pos, True,
+            theta=theta, q_rope_offset=pos, kv_rope_offset=0)
+        assert_close(f"O@{pos}", res.output, eo, 2e-4, 1e-3)
+        assert_close(f"LSE@{pos}", res.lse, el, 2e-4, 1e-3)
+    assert cache.remaining_capacity() == 0
+
+
+def _m48_fixture(n, phase):
+    x = np.arange(n, dtype=np.float32) * np.float32(0.021) + np.float32(phase)
+    return (np.sin(x) * 1.75 + np.cos(x * np.float32(0.43)) * 0.34375).astype(np.float32)
+
+
+@pytest.mark.parametrize("dtype", [fa.DTYPE_F32, fa.DTYPE_BF16, fa.DTYPE_F16])
+@pytest.mark.parametrize("batch,hq,hkv,kv_len,D,causal_pos,q_rope,causal", [
+    (1, 16, 4, 192, 64, 191, 191, True),   # m48_sciagent_decode_matches_oracle :105
+    (1, 16, 4, 16, 64, 7, 7, True),        # m48_causal_offset_masks_future_kv :179
+    (3, 32, 4, 777, 128, 900, 1234, True),  # past the end: every key visible
+    (2, 8, 2, 300, 64, 120, 40, True),     # causal and RoPE positions differ
+    (2, 12, 2, 33, 32, 0, 5, False),
+    (1, 4, 2, 9, 6, 8, 8, True),           # f32 head_dim 6: the prefill-kernel route
+])
+def test_m48_decode_kv_reuse_matches_oracle(hip, dtype, batch, hq, hkv, kv_len, D, causal_pos,
+                                            q_rope, causal):
+    """encode_pre_rotated_k_decode_kv_reuse src/wgpu_external_asymmetric.rs:216 against the
+    raw-K asymmetric oracle (projection_asymmetric.rs:97) with K rotated on the host as the
+    reference's test does (tests/m48_decode_kv_reuse.rs:21); causal masking keeps keys up to the
+    shape's query position. Tolerance: f32 1.5e-4 + 1e-3|e| (the reference's), 16-bit 2e-2 on
+    inputs rounded to the storage type."""
+    if D % 8 and dtype != fa.DTYPE_F32:
+        pytest.skip("16-bit storage needs head_dim % 8 == 0")
+    rnd = {fa.DTYPE_BF16: bf16_round, fa.DTYPE_F16: f16_round}.get(dtype, lambda x: x)
+    width = hkv * D
+    q = rnd(_m48_fixture(batch * hq * D, 0.2))
+    raw_k = _m48_fixture(batch * kv_len * width, 0.8)
+    v = rnd(_m48_fixture(batch * kv_len * width, 1.4))
+    k = np.concatenate([oracle.rope_rotate_rows(raw_k.reshape(batch, -1)[b], kv_len, hkv, D, 1e4)
+                        for b in range(batch)])
+    k = rnd(k)
+    shape = fa.AsymmetricGroupedAttentionShape(batch, hq, hkv, 1, kv_len, D, causal_pos)
+    rot = fa.AsymmetricRotaryEmbeddingConfig(1e4, q_rope, 0)
+    pipe = fa.HipAsymmetricProjectionPipeline.with_decode_kv_reuse(hip, True, dtype)
+    out = pipe.create_output_buffer(shape)
+    bufs = [fa.DeviceBuffer.from_array(hip, fa.host_storage(x, dtype)) for x in (q, k, v)]
+    lay = pipe.encode_pre_rotated_k_decode_kv_reuse(bufs[0], bufs[1], bufs[2], out, shape,
+                                                    fa.FlatAttentionConfig(causal), rot)
+    res = fa.download_attention(out, lay, dtype)
+    eo, el = oracle.forward_projection_asymmetric(
+        q, k, v, batch, hq, hkv, 1, kv_len, D, causal_pos, causal, theta=1e4, q_rope_offset=q_rope,
+        rotate_k=False)
+    o = fa.storage_to_f32(res.output, dtype)
+    if dtype == fa.DTYPE_F32:
+        assert_close("O", o, eo, 1.5e-4, 1e-3)
+        assert_close("LSE", res.lse, el, 1.5e-4, 1e-3)
+    else:
+        assert_close("O", o, eo, H16_ATOL, 0.0)
+        assert_close("LSE", res.lse, el, H16_ATOL, 0.0)
+    kid = hip.last_telemetry().kernel_id
+    if D % 4:
+        assert kid.startswith("Prefill")
+    else:
+        assert kid == ("DecodePagedMfma" if dtype != fa.DTYPE_F32 and kv_len % 16 == 0
+                       else "DecodePagedSplitK")
+    if causal and causal_pos == 7 and kv_len == 16 and dtype == fa.DTYPE_F32:
+        # the reference's own oracle anchor for the masking: the first 8 keys alone
+        eo8, el8 = oracle.forward_projection_asymmetric(
+            q, k.reshape(kv_len, width)[:8].reshape(-1), v.reshape(kv_len, width)[:8].reshape(-1),
+            1, hq, hkv, 1, 8, D, 7, False, theta=1e4, q_rope_offset=7, rotate_k=False)
+        assert_close("O(8 keys)", o, eo8, 1.5e-4, 1e-3)
+
+
+def test_m48_is_opt_in_and_baseline_routes_unchanged(hip):
+    """m48_is_opt_in tests/m48_decode_kv_reuse.rs:318; encode_pre_rotated_k on a pipeline with the
+    candidate keeps its prefill route (with_decode_kv_reuse :78)."""
+    shape = fa.AsymmetricGroupedAttentionShape(1, 16, 4, 1, 1, 64, 0)
+    rot = fa.AsymmetricRotaryEmbeddingConfig(1e4, 0, 0)
+    zq = fa.DeviceBuffer.from_array(hip, np.zeros(16 * 64, np.float32))
+    zkv = fa.DeviceBuffer.from_array(hip, np.zeros(4 * 64, np.float32))
+    base = fa.HipAsymmetricProjectionPipeline(hip)
+    out = base.create_output_buffer(shape)
+    with pytest.raises(fa.FlatHipError) as e:
+        base.encode_pre_rotated_k_decode_kv_reuse(zq, zkv, zkv, out, shape,
+                                                  fa.FlatAttentionConfig(True), rot)
+    assert e.value.variant == "CandidateNotEnabled"
+    cand = fa.HipAsymmetricProjectionPipeline.with_decode_kv_reuse(hip, True)
+    cand.encode_pre_rotated_k(zq, zkv, zkv, out, shape, fa.FlatAttentionConfig(True), rot)
+    assert hip.last_telemetry().kernel_id.startswith("Prefill")

@@ -304,6 +304,44 @@ def test_variable_prefill_validation_variants():
     assert _variable(ok) == "NullArgument"
 
 
+def _kv_reuse(shape=(1, 16, 4, 1, 192, 64, 191), theta=1e4, q_rope=191, kv_rope=0,
+              q_bytes=1 << 30, dtype=fa.DTYPE_F32, rotary=True):
+    sh = fa.AsymmetricGroupedAttentionShape(*shape)
+    rot = fa.AsymmetricRotaryEmbeddingConfig(theta, q_rope, kv_rope)
+    return _variant(fa.lib().fa_forward_projection_asymmetric_decode_kv_reuse(
+        None, FAKE, q_bytes, FAKE, FAKE, 1 << 30, FAKE, 1 << 30, ctypes.byref(sh.c()),
+        ctypes.byref(fa.FlatAttentionConfig(True).c()),
+        ctypes.byref(rot.c()) if rotary else None, dtype))
+
+
+def test_decode_kv_reuse_validation_variants():
+    """encode_pre_rotated_k_decode_kv_reuse src/wgpu_external_asymmetric.rs:216 in its order:
+    shape validation (tests/m48_decode_kv_reuse.rs:267: zero KV heads is ZeroDimension), the
+    candidate's query_len and group-size limits, then encode_with_options :291; a null context is
+    reported last. Without the candidate the pipeline refuses (m48_is_opt_in :318)."""
+    assert _kv_reuse(rotary=False) == "NullArgument"
+    assert _kv_reuse(shape=(1, 16, 0, 1, 1, 64, 0), q_rope=0) == "ZeroDimension"
+    assert _kv_reuse(shape=(1, 16, 5, 1, 8, 64, 7)) == "InvalidHeadGrouping"
+    assert _kv_reuse(shape=(1, 16, 4, 2, 8, 64, 7)) == "UnsupportedCandidateShape"
+    assert _kv_reuse(shape=(1, 4, 4, 1, 8, 64, 7)) == "UnsupportedCandidateShape"
+    assert _kv_reuse(shape=(1, 16, 4, 1, 8, 64, 2**31 - 1)) == "PositionOverflow"
+    assert _kv_reuse(q_rope=2**31) == "PositionOverflow"
+    assert _kv_reuse(theta=-1.0) == "InvalidRotaryTheta"
+    assert _kv_reuse(shape=(1, 16, 4, 1, 8, 63, 7)) == "InvalidRotaryHeadDim"
+    assert _kv_reuse(shape=(1, 16, 4, 1, 8, 132, 7)) == "UnsupportedHeadDim"
+    assert _kv_reuse(dtype=fa.DTYPE_BF16, shape=(1, 16, 4, 1, 8, 60, 7)) == "UnsupportedHeadDim"
+    assert _kv_reuse(q_bytes=16) == "BufferTooSmall"
+    assert _kv_reuse(dtype=9) == "UnsupportedDtype"
+    assert _kv_reuse() == "NullArgument"
+    assert _kv_reuse(shape=(1, 16, 4, 1, 8, 6, 7)) == "NullArgument"  # prefill-kernel route
+    pipe = fa.HipAsymmetricProjectionPipeline(None)
+    with pytest.raises(fa.FlatHipError) as e:
+        pipe.encode_pre_rotated_k_decode_kv_reuse(None, None, None, None, None, None, None)
+    assert e.value.variant == "CandidateNotEnabled"
+    assert "external FLAT candidate M48 was not enabled" in str(e.value)
+    assert fa.HipAsymmetricProjectionPipeline.with_decode_kv_reuse(None, True).decode_kv_reuse
+
+
 def test_append_batched_validation():
     bt = np.array([[0, 1]], np.int32)
     st = np.array([20], np.int32)
@@ -449,6 +487,11 @@ def test_host_contract_fuzz_fails_closed():
         rc = lib.fa_forward_projection_asymmetric(None, FAKE, q_bytes, FAKE, FAKE, kv_bytes, FAKE,
                                                   out_bytes, ctypes.byref(ash.c()),
                                                   ctypes.byref(cfg.c()), None, 0, dtype)
+        assert rc in known and rc != 0, (case, rc)
+        rot = fa.AsymmetricRotaryEmbeddingConfig(st.scale() or 1e4, st.dimension(), off)
+        rc = lib.fa_forward_projection_asymmetric_decode_kv_reuse(
+            None, FAKE, q_bytes, FAKE, FAKE, kv_bytes, FAKE, out_bytes, ctypes.byref(ash.c()),
+            ctypes.byref(cfg.c()), ctypes.byref(rot.c()), dtype)
         assert rc in known and rc != 0, (case, rc)
         assert lib.fa_resolved_scale(ctypes.byref(cfg.c()), d, ctypes.byref(scale_out)) in known
         rc = lib.fa_backward_grouped_layout(ctypes.byref(fa.GroupedAttentionShape(
