@@ -11,7 +11,7 @@ from .api import (AsymmetricGroupedAttentionShape, AsymmetricRotaryEmbeddingConf
                   AttentionShape, DeviceBuffer, FlatAttentionConfig, FlatAttentionOutput,
                   GroupedAttentionShape, HipAsymmetricProjectionPipeline,
                   HipChunkedProjectionPrefillPipeline, HipContext, HipFlatAttention,
-                  HipPagedDecodePipeline, HipPagedKvCache, HipResidentDecodePipeline,
+                  HipPagedDecodePipeline, HipPagedKvCache, HipProjectionRotaryGroupedPipeline, HipResidentDecodePipeline,
                   HipResidentKvCache, HipRotaryGroupedAttention, ResidentDecodePlan,
                   PackedLayout, PagedChunkedPrefillPlan, PagedDecodePlan, PagedKvAddress,
                   PagedKvConfig, PagedKvTable, PagedKvTelemetry, RotaryEmbeddingConfig,

@@ -573,6 +573,35 @@ class HipAsymmetricProjectionPipeline:
         return self.layout(shape)
 
 
+class HipProjectionRotaryGroupedPipeline:
+    """ExternalProjectionRotaryGroupedPipeline src/wgpu_external.rs:124 (equal-length GQA + RoPE
+    in projection layout [batch, seq, heads*head_dim]; Q and K rotated from
+    rotary.position_offset, causal within the sequence). encode :206 is the asymmetric pass with
+    query_len = kv_len, causal offset 0 and both RoPE offsets at rotary.position_offset."""
+
+    def __init__(self, ctx: HipContext, dtype: int = L.DTYPE_F32):
+        self.ctx = ctx
+        self.dtype = dtype
+
+    def layout(self, shape: GroupedAttentionShape) -> PackedLayout:  # :159
+        return packed_layout(shape.q_tensor_len(), shape.lse_len(), self.dtype)
+
+    def create_output_buffer(self, shape: GroupedAttentionShape) -> DeviceBuffer:  # :184
+        return DeviceBuffer(self.ctx, self.layout(shape).combined_bytes)
+
+    def encode(self, q, k, v, out, shape: GroupedAttentionShape, config: FlatAttentionConfig,
+               rotary: RotaryEmbeddingConfig) -> PackedLayout:
+        ash = AsymmetricGroupedAttentionShape(shape.batch, shape.q_heads, shape.kv_heads,
+                                              shape.seq_len, shape.seq_len, shape.head_dim, 0)
+        rot = AsymmetricRotaryEmbeddingConfig(rotary.theta, rotary.position_offset,
+                                              rotary.position_offset)
+        check(lib().fa_forward_projection_asymmetric(
+            self.ctx.handle, q.ptr, q.nbytes, k.ptr, v.ptr, min(k.nbytes, v.nbytes), out.ptr,
+            out.nbytes, ctypes.byref(ash.c()), ctypes.byref(config.c()), ctypes.byref(rot.c()),
+            1, self.dtype))
+        return self.layout(shape)
+
+
 @dataclass(frozen=True)
 class VariableLengthSequenceMetadata:
     """VariableLengthSequenceMetadata src/wgpu_external_variable.rs:25."""
@@ -883,6 +912,9 @@ class HipResidentKvCache:
 
     def __len__(self) -> int:
         return lib().fa_resident_cache_len(self.handle)
+
+    def is_empty(self) -> bool:
+        return len(self) == 0
 
     def remaining_capacity(self) -> int:  # :184
         return self.capacity - len(self)
