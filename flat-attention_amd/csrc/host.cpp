@@ -244,10 +244,10 @@ void begin_call(fa_ctx* ctx) {
     ctx->call_alloc_bytes = 0;
 }
 
-void record(fa_ctx* ctx, int kernel_id, const char* name, uint32_t qrows, uint32_t kvrows,
-            const unsigned grid[3], unsigned block, uint32_t dispatches, uint32_t splits,
-            const char* fallback) {
-    fa_telemetry& t = ctx->last;
+void fill_telemetry(fa_telemetry& t, const fa_ctx* ctx, int kernel_id, const char* name,
+                    uint32_t qrows, uint32_t kvrows, const unsigned grid[3], unsigned block,
+                    uint32_t dispatches, uint32_t splits, const char* fallback, uint32_t allocs,
+                    uint64_t alloc_bytes) {
     memset(&t, 0, sizeof t);
     t.kernel_id = kernel_id;
     copy_str(t.kernel_name, sizeof t.kernel_name, name);
@@ -258,8 +258,8 @@ void record(fa_ctx* ctx, int kernel_id, const char* name, uint32_t qrows, uint32
     t.workgroups[2] = grid[2];
     t.workgroup_size = block;
     t.dispatch_count = dispatches;
-    t.temporary_allocation_count = ctx->call_allocs;
-    t.temporary_allocation_bytes = ctx->call_alloc_bytes;
+    t.temporary_allocation_count = allocs;
+    t.temporary_allocation_bytes = alloc_bytes;
     t.splits = splits;
     if (fallback) {
         t.has_fallback_reason = 1;
@@ -268,6 +268,13 @@ void record(fa_ctx* ctx, int kernel_id, const char* name, uint32_t qrows, uint32
     copy_str(t.device_name, sizeof t.device_name, ctx->name);
     copy_str(t.device_arch, sizeof t.device_arch, ctx->arch);
     t.device_fingerprint = ctx->fingerprint;
+}
+
+void record(fa_ctx* ctx, int kernel_id, const char* name, uint32_t qrows, uint32_t kvrows,
+            const unsigned grid[3], unsigned block, uint32_t dispatches, uint32_t splits,
+            const char* fallback) {
+    fill_telemetry(ctx->last, ctx, kernel_id, name, qrows, kvrows, grid, block, dispatches,
+                   splits, fallback, ctx->call_allocs, ctx->call_alloc_bytes);
 }
 
 // Timing marks: begin_span records an event before a dispatch, end_span one after it and
@@ -516,11 +523,12 @@ int fa_ctx_create(int device, fa_ctx** out) {
     HIP_TRY(hipSetDevice(device));
     fa_ctx* ctx = new fa_ctx();
     ctx->device = device;
-    ctx->name = prop.name;
+    // some drivers report no marketing name: name the part by its architecture instead
+    ctx->name = prop.name[0] ? std::string(prop.name) : "AMD " + arch.substr(0, arch.find(':'));
     ctx->arch = arch;
     int drv = 0;
     (void)hipDriverGetVersion(&drv);
-    ctx->fingerprint = fnv1a64(device_record(prop.name, arch.c_str(), drv,
+    ctx->fingerprint = fnv1a64(device_record(ctx->name.c_str(), arch.c_str(), drv,
                                              prop.multiProcessorCount, prop.clockRate,
                                              (uint64_t)prop.totalGlobalMem));
     if (hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking) != hipSuccess) {
@@ -860,6 +868,57 @@ struct PrefillRun {
 
 // Decides the variant and gathers the memory. own == false: the context's growable caches;
 // own == true: fresh allocations that the caller (a prepared forward) keeps and frees.
+// Variant decisions of a prefill job under the context's policies (no device work).
+struct PrefillChoice {
+    bool prerot = false;  // K rotated once by the pre-pass
+    bool split_qk = false;  // precise 16-bit scores: K rotated on load, split Q/K
+    bool vt = false;      // transposed-V copy
+};
+
+PrefillChoice choose_prefill(const fa_ctx* ctx, const PrefillJob& j) {
+    PrefillChoice c;
+    if (j.rope) {
+        c.prerot = j.a.rope_k && !j.paged && want_prerotate(ctx, (uint64_t)j.a.head_dim);
+        if (ctx->prefill_precision == 1 && j.a.rope_k && !j.paged && j.dtype != FA_DTYPE_F32) {
+            c.prerot = false;
+            c.split_qk = true;
+        }
+    }
+    c.vt = !j.paged && !j.no_vt && j.dtype != FA_DTYPE_F32 && j.a.head_dim % 8 == 0 &&
+           ctx->transpose_v_policy == 1;
+    return c;
+}
+
+uint64_t vt_bytes(const PrefillJob& j) {
+    const uint64_t s_pad = ((uint64_t)j.a.kv_len + 63) / 64 * 64;
+    return (uint64_t)j.a.batch * j.a.kv_heads * j.a.head_dim * s_pad * 2u;
+}
+
+// Device allocations a one-shot call of `j` would make through the context's growable caches
+// (RoPE table, rotated-K and V^T workspaces), given what they hold now.
+void predict_prefill_allocs(const fa_ctx* ctx, const PrefillJob& j, const PrefillChoice& c,
+                            uint32_t* count, uint64_t* bytes) {
+    *count = 0;
+    *bytes = 0;
+    const uint64_t hd = (uint64_t)j.a.head_dim;
+    if (j.rope && !(ctx->rope && ctx->rope_theta == j.theta && ctx->rope_dim == hd &&
+                    ctx->rope_rows >= j.max_pos)) {
+        uint64_t cap = std::max<uint64_t>(j.max_pos, 4096);
+        if (ctx->rope_theta == j.theta && ctx->rope_dim == hd)
+            cap = std::max<uint64_t>(cap, ctx->rope_rows * 2);
+        ++*count;
+        *bytes += cap * (hd / 2) * sizeof(float2);
+    }
+    if (c.prerot && ctx->ws_bytes < j.kv_bytes) {
+        ++*count;
+        *bytes += j.kv_bytes;
+    }
+    if (c.vt && ctx->ws_vt_bytes < vt_bytes(j)) {
+        ++*count;
+        *bytes += vt_bytes(j);
+    }
+}
+
 int resolve_prefill(fa_ctx* ctx, PrefillJob& j, bool own, PrefillRun* r) {
     // 16-bit contiguous K/V are read through 32-bit buffer offsets within one (batch, kv-head)
     // slice: kv_len rows of k_ss elements must stay below 2 GiB.
@@ -885,12 +944,10 @@ int resolve_prefill(fa_ctx* ctx, PrefillJob& j, bool own, PrefillRun* r) {
             r->table = const_cast<float2*>(t);
         }
         r->j.a.rope_table = r->table;
-        prerot = j.a.rope_k && !j.paged && want_prerotate(ctx, (uint64_t)j.a.head_dim);
+        const PrefillChoice c = choose_prefill(ctx, j);
+        prerot = c.prerot;
         // precise scores: K rotated in the kernel, which keeps its 16-bit residual
-        if (ctx->prefill_precision == 1 && j.a.rope_k && !j.paged && j.dtype != FA_DTYPE_F32) {
-            prerot = false;
-            r->j.a.split_qk = 1;
-        }
+        if (c.split_qk) r->j.a.split_qk = 1;
     }
     r->prerot = prerot;
     if (prerot) {
@@ -903,13 +960,12 @@ int resolve_prefill(fa_ctx* ctx, PrefillJob& j, bool own, PrefillRun* r) {
     // Optional transposed V copy for the 16-bit contiguous kernel (off unless selected): the V^T
     // operand then comes from plain 16-byte LDS reads instead of transposing ones. It measured
     // no faster at D = 128, so the extra pass is not run by default.
-    r->vt = !j.paged && !j.no_vt && j.dtype != FA_DTYPE_F32 && j.a.head_dim % 8 == 0 &&
-            ctx->transpose_v_policy == 1;
+    r->vt = choose_prefill(ctx, j).vt;
     r->j.a.vt = nullptr;
     r->j.a.vt_row = 0;
     if (r->vt) {
         const uint64_t s_pad = ((uint64_t)j.a.kv_len + 63) / 64 * 64;
-        const uint64_t bytes = (uint64_t)j.a.batch * j.a.kv_heads * j.a.head_dim * s_pad * 2u;
+        const uint64_t bytes = vt_bytes(j);
         if ((uint64_t)j.a.head_dim * s_pad * 2u > (uint64_t)INT32_MAX)
             return fail(FA_ERR_INDEX_SPACE_EXCEEDED,
                         "one transposed V slice spans %llu bytes; the kernel addresses at most 2 GiB",
@@ -922,6 +978,37 @@ int resolve_prefill(fa_ctx* ctx, PrefillJob& j, bool own, PrefillRun* r) {
         r->j.a.vt_row = (int)s_pad;
     }
     return FA_OK;
+}
+
+// Telemetry of a prefill whose kernel arguments are `a` (after the pre-passes' substitutions):
+// kernel id and name, geometry, dispatch count, allocations and the fallback reason.
+void describe_prefill(const fa_ctx* ctx, const PrefillJob& j, const fa::PrefillArgs& a,
+                      bool prerot, bool vt, uint32_t dispatches, uint32_t allocs,
+                      uint64_t alloc_bytes, fa_telemetry* out) {
+    // K read already rotated (pre-pass, or a paged cache that stores K rotated on append)
+    const int kid = prefill_kernel_id(j.dtype, prerot || (j.paged && j.rope));
+    unsigned grid[3], block = 0, rows = 0;
+    fa::prefill_geometry(j.dt, j.paged, a, grid, &block, &rows);
+    const char* fb = nullptr;
+
+    if (j.rope && a.rope_k && !prerot && !j.paged && a.head_dim % 8 != 0)
+        fb = "K pre-rotation pass needs head_dim % 8 == 0; K rotated on load";
+    const char* dt = j.dtype == FA_DTYPE_BF16 ? "bf16" : j.dtype == FA_DTYPE_F16 ? "f16" : "f32";
+    const char* base = j.dtype == FA_DTYPE_F32 ? "prefill_mfma_f32" : "prefill_mfma16";
+    char name[64];
+    if (prerot || vt)
+        snprintf(name, sizeof name, "%s%s%s<%s>", prerot ? "rotate_rows + " : "",
+                 vt ? "transpose_v + " : "", base, dt);
+    else if (j.paged)
+        snprintf(name, sizeof name, "%s<%s> (paged%s)", base, dt, j.rope ? ", K stored rotated" : "");
+    else if (a.split_qk)
+        snprintf(name, sizeof name, "%s<%s> (K rotated on load, split Q/K scores)", base, dt);
+    else if (a.rope_k)
+        snprintf(name, sizeof name, "%s<%s> (K rotated on load)", base, dt);
+    else
+        snprintf(name, sizeof name, "%s<%s>", base, dt);
+    fill_telemetry(*out, ctx, kid, name, rows, 64, grid, block, dispatches, 1, fb, allocs,
+                   alloc_bytes);
 }
 
 // Enqueues the resolved prefill on the context's stream: optional K pre-rotation and V
@@ -957,24 +1044,8 @@ int enqueue_prefill(fa_ctx* ctx, const PrefillRun& r) {
     end_span(ctx, kid);
     HIP_TRY(hipGetLastError());
     dispatches++;
-    const char* fb = nullptr;
-    if (j.rope && a.rope_k && !r.prerot && !j.paged && a.head_dim % 8 != 0)
-        fb = "K pre-rotation pass needs head_dim % 8 == 0; K rotated on load";
-    const char* dt = j.dtype == FA_DTYPE_BF16 ? "bf16" : j.dtype == FA_DTYPE_F16 ? "f16" : "f32";
-    const char* base = j.dtype == FA_DTYPE_F32 ? "prefill_mfma_f32" : "prefill_mfma16";
-    char name[64];
-    if (r.prerot || r.vt)
-        snprintf(name, sizeof name, "%s%s%s<%s>", r.prerot ? "rotate_rows + " : "",
-                 r.vt ? "transpose_v + " : "", base, dt);
-    else if (j.paged)
-        snprintf(name, sizeof name, "%s<%s> (paged%s)", base, dt, j.rope ? ", K stored rotated" : "");
-    else if (a.split_qk)
-        snprintf(name, sizeof name, "%s<%s> (K rotated on load, split Q/K scores)", base, dt);
-    else if (a.rope_k)
-        snprintf(name, sizeof name, "%s<%s> (K rotated on load)", base, dt);
-    else
-        snprintf(name, sizeof name, "%s<%s>", base, dt);
-    record(ctx, kid, name, 128, 64, grid, block, dispatches, 1, fb);
+    describe_prefill(ctx, j, a, r.prerot, r.vt, dispatches, ctx->call_allocs,
+                     ctx->call_alloc_bytes, &ctx->last);
     return FA_OK;
 }
 
@@ -1013,7 +1084,7 @@ namespace {
 int build_gqa_job(fa_ctx* ctx, const void* q, size_t q_bytes, const void* k, const void* v,
                   size_t kv_bytes, void* out_lse, size_t out_bytes, const fa_grouped_shape* sh,
                   const fa_config* cfg, const fa_rotary* rot, int dtype, PrefillJob& j,
-                  fa_packed_layout* layout) {
+                  fa_packed_layout* layout, bool check_buffers = true) {
     if (!sh) return fail(FA_ERR_NULL_ARGUMENT, "shape is null");
     if (int rc = check_dtype(dtype)) return rc;
     if (int rc = validate_grouped(sh->batch, sh->q_heads, sh->kv_heads, sh->seq_len, sh->head_dim))
@@ -1029,10 +1100,12 @@ int build_gqa_job(fa_ctx* ctx, const void* q, size_t q_bytes, const void* k, con
     const uint64_t kvn = sh->batch * sh->kv_heads * sh->seq_len * sh->head_dim;
     fa_packed_layout lay;
     if (int rc = fa_packed_layout_for(qn, sh->batch * sh->q_heads * sh->seq_len, dtype, &lay)) return rc;
-    if (int rc = check_buffer("Q", q, q_bytes, qn * eb)) return rc;
-    if (int rc = check_buffer("K", k, kv_bytes, kvn * eb)) return rc;
-    if (int rc = check_buffer("V", v, kv_bytes, kvn * eb)) return rc;
-    if (int rc = check_buffer("O|LSE", out_lse, out_bytes, lay.combined_bytes)) return rc;
+    if (check_buffers) {
+        if (int rc = check_buffer("Q", q, q_bytes, qn * eb)) return rc;
+        if (int rc = check_buffer("K", k, kv_bytes, kvn * eb)) return rc;
+        if (int rc = check_buffer("V", v, kv_bytes, kvn * eb)) return rc;
+        if (int rc = check_buffer("O|LSE", out_lse, out_bytes, lay.combined_bytes)) return rc;
+    }
     if (!ctx) return fail(FA_ERR_NULL_ARGUMENT, "context is null");
     if (layout) *layout = lay;
 
@@ -1092,6 +1165,34 @@ int fa_forward_gqa_rope(fa_ctx* ctx, const void* q, size_t q_bytes, const void* 
     if (int rc = set_device(ctx)) return rc;
     if (int rc = run_prefill(ctx, j)) return rc;
     return ok();
+}
+
+// Passive telemetry (WgpuFlatAttention::runtime_telemetry src/wgpu_backend.rs): the record a
+// one-shot forward of this shape would leave, built on the host with no device work.
+int fa_forward_gqa_rope_telemetry(fa_ctx* ctx, const fa_grouped_shape* sh, const fa_config* cfg,
+                                  const fa_rotary* rot, int dtype, fa_telemetry* out) {
+    if (!out) return fail(FA_ERR_NULL_ARGUMENT, "output is null");
+    PrefillJob j;
+    if (int rc = build_gqa_job(ctx, nullptr, 0, nullptr, nullptr, 0, nullptr, 0, sh, cfg, rot,
+                               dtype, j, nullptr, false))
+        return rc;
+    const PrefillChoice c = choose_prefill(ctx, j);
+    uint32_t allocs;
+    uint64_t bytes;
+    predict_prefill_allocs(ctx, j, c, &allocs, &bytes);
+    fa::PrefillArgs a = j.a;  // the arguments the prefill kernel would receive
+    if (c.prerot) a.rope_k = 0;
+    if (c.split_qk) a.split_qk = 1;
+    a.vt = c.vt ? (const void*)1 : nullptr;
+    describe_prefill(ctx, j, a, c.prerot, c.vt, 1u + c.prerot + c.vt, allocs, bytes, out);
+    return ok();
+}
+
+int fa_forward_mha_telemetry(fa_ctx* ctx, const fa_attention_shape* shape, const fa_config* cfg,
+                             int dtype, fa_telemetry* out) {
+    if (!shape) return fail(FA_ERR_NULL_ARGUMENT, "shape is null");
+    fa_grouped_shape g{shape->batch, shape->heads, shape->heads, shape->seq_len, shape->head_dim};
+    return fa_forward_gqa_rope_telemetry(ctx, &g, cfg, nullptr, dtype, out);
 }
 
 int fa_prepare_gqa_rope(fa_ctx* ctx, const void* q, size_t q_bytes, const void* k,

@@ -52,6 +52,9 @@ struct PrefillArgs {
 
 void launch_prefill(Dtype dt, bool paged, const PrefillArgs& a, hipStream_t s,
                     unsigned grid[3], unsigned* block);
+// The grid, workgroup size and query rows per workgroup launch_prefill uses for `a` (host only).
+void prefill_geometry(Dtype dt, bool paged, const PrefillArgs& a, unsigned grid[3],
+                      unsigned* block, unsigned* rows);
 
 // Paged q_len=1 decode, split-K over the context of every sequence.
 struct DecodeArgs {

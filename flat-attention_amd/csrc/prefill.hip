@@ -1309,22 +1309,28 @@ static void launch32(const PrefillKArgs& ka, int dpad, dim3 grid, hipStream_t s)
     }
 }
 
+void prefill_geometry(Dtype dt, bool paged, const PrefillArgs& a, unsigned grid[3],
+                      unsigned* block, unsigned* rows) {
+    // 16-bit contiguous K/V without in-kernel K rotation runs 256-row ping-pong workgroups
+    const bool pp = dt != Dtype::F32 && !a.rope_k && (!paged || a.page_size % 16 == 0);
+    const int bm = pp ? 256 : 128;
+    const int nqb = (a.q_len * a.group + bm - 1) / bm;
+    grid[0] = (unsigned)((int64_t)a.batch * a.kv_heads * nqb);
+    grid[1] = 1;
+    grid[2] = 1;
+    *block = pp ? 512 : 256;
+    *rows = (unsigned)bm;
+}
+
 void launch_prefill(Dtype dt, bool paged, const PrefillArgs& a, hipStream_t s, unsigned grid[3],
                     unsigned* block) {
     PrefillKArgs ka;
     ka.a = a;
     if (paged) ka.ps = FastDiv((uint32_t)a.page_size);
     const int dpad = a.head_dim <= 32 ? 32 : (a.head_dim <= 64 ? 64 : 128);
-    const int rows_total = a.q_len * a.group;
-    // 16-bit contiguous K/V without in-kernel K rotation runs 256-row ping-pong workgroups
-    const bool pp = dt != Dtype::F32 && !a.rope_k && (!paged || a.page_size % 16 == 0);
-    const int bm = pp ? 256 : 128;
-    const int nqb = (rows_total + bm - 1) / bm;
-    dim3 g((unsigned)((int64_t)a.batch * a.kv_heads * nqb));
-    grid[0] = g.x;
-    grid[1] = 1;
-    grid[2] = 1;
-    *block = pp ? 512 : 256;
+    unsigned rows;
+    prefill_geometry(dt, paged, a, grid, block, &rows);
+    dim3 g(grid[0]);
     switch (dt) {
         case Dtype::BF16: launch16<bf16_t>(ka, paged, dpad, g, s); break;
         case Dtype::F16: launch16<f16_t>(ka, paged, dpad, g, s); break;

@@ -208,6 +208,9 @@ PROTOTYPES = {
     "fa_backward_grouped": (INT, [VP, VP, VP, VP, VP, VP, VP, VP, VP, VP, P(GroupedShapeC),
                                   P(ConfigC), INT]),
     "fa_last_telemetry": (INT, [VP, P(TelemetryC)]),
+    "fa_forward_gqa_rope_telemetry": (INT, [VP, P(GroupedShapeC), P(ConfigC), P(RotaryC), INT,
+                                            P(TelemetryC)]),
+    "fa_forward_mha_telemetry": (INT, [VP, P(AttentionShapeC), P(ConfigC), INT, P(TelemetryC)]),
     "fa_ctx_set_kernel_timing": (INT, [VP, I32]),
     "fa_ctx_pause_kernel_timing": (INT, [VP, I32]),
     "fa_ctx_set_prefill_precision": (INT, [VP, I32]),

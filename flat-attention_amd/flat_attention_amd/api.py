@@ -311,18 +311,38 @@ class HipContext:
     def last_telemetry(self) -> RuntimeDispatchTelemetry:
         t = L.TelemetryC()
         check(lib().fa_last_telemetry(self.handle, ctypes.byref(t)))
-        return RuntimeDispatchTelemetry(
-            L.KERNEL_IDS.get(t.kernel_id, str(t.kernel_id)), t.kernel_name.decode(), t.query_rows,
-            t.kv_rows, tuple(t.workgroups), t.workgroup_size, t.dispatch_count,
-            t.temporary_allocation_count, t.temporary_allocation_bytes, t.splits,
-            t.fallback_reason.decode() if t.has_fallback_reason else None,
-            t.device_name.decode(), t.device_arch.decode(), t.device_fingerprint)
+        return _telemetry(t)
+
+    def forward_telemetry(self, shape, config: "FlatAttentionConfig" = None,
+                          rotary: "RotaryEmbeddingConfig" = None,
+                          dtype: int = L.DTYPE_F32) -> RuntimeDispatchTelemetry:
+        """Passive snapshot of what a one-shot forward of `shape` (AttentionShape: MHA;
+        GroupedAttentionShape: GQA, optional RoPE) would dispatch; no device work."""
+        t = L.TelemetryC()
+        cfg = ctypes.byref((config or FlatAttentionConfig()).c())
+        if isinstance(shape, AttentionShape):
+            check(lib().fa_forward_mha_telemetry(self.handle, ctypes.byref(shape.c()), cfg, dtype,
+                                                 ctypes.byref(t)))
+        else:
+            rot = ctypes.byref(rotary.c()) if rotary is not None else None
+            check(lib().fa_forward_gqa_rope_telemetry(self.handle, ctypes.byref(shape.c()), cfg,
+                                                      rot, dtype, ctypes.byref(t)))
+        return _telemetry(t)
 
     def kernel_variant_for_shape(self, head_dim: int, rope: bool, dtype: int) -> str:
         out = L.I32()
         check(lib().fa_kernel_variant_for_shape(self.handle, head_dim, int(rope), dtype,
                                                 ctypes.byref(out)))
         return L.KERNEL_IDS[out.value]
+
+
+def _telemetry(t) -> RuntimeDispatchTelemetry:
+    return RuntimeDispatchTelemetry(
+            L.KERNEL_IDS.get(t.kernel_id, str(t.kernel_id)), t.kernel_name.decode(), t.query_rows,
+            t.kv_rows, tuple(t.workgroups), t.workgroup_size, t.dispatch_count,
+            t.temporary_allocation_count, t.temporary_allocation_bytes, t.splits,
+            t.fallback_reason.decode() if t.has_fallback_reason else None,
+            t.device_name.decode(), t.device_arch.decode(), t.device_fingerprint)
 
 
 class DeviceBuffer:
@@ -432,8 +452,13 @@ class HipFlatAttention:
                                         self.dtype, out.ctypes.data, lse.ctypes.data))
         return FlatAttentionOutput(out, lse)
 
-    def runtime_telemetry(self) -> RuntimeDispatchTelemetry:
-        return self.ctx.last_telemetry()
+    def runtime_telemetry(self, shape: Optional[AttentionShape] = None,
+                          config: Optional[FlatAttentionConfig] = None) -> RuntimeDispatchTelemetry:
+        """runtime_telemetry src/wgpu_backend.rs: with a shape, the passive snapshot of the
+        dispatch a forward of it would make (no device work); without, the last dispatch's."""
+        if shape is None:
+            return self.ctx.last_telemetry()
+        return self.ctx.forward_telemetry(shape, config, None, self.dtype)
 
 
 class HipRotaryGroupedAttention:
@@ -495,8 +520,13 @@ class HipRotaryGroupedAttention:
                                              rot, self.dtype, out.ctypes.data, lse.ctypes.data))
         return FlatAttentionOutput(out, lse)
 
-    def runtime_telemetry(self) -> RuntimeDispatchTelemetry:
-        return self.ctx.last_telemetry()
+    def runtime_telemetry(self, shape: Optional[GroupedAttentionShape] = None,
+                          config: Optional[FlatAttentionConfig] = None,
+                          rotary: Optional[RotaryEmbeddingConfig] = None) -> RuntimeDispatchTelemetry:
+        """Passive snapshot for `shape` (no device work), else the last dispatch's record."""
+        if shape is None:
+            return self.ctx.last_telemetry()
+        return self.ctx.forward_telemetry(shape, config, rotary, self.dtype)
 
 
 class PreparedGroupedForward:

@@ -524,6 +524,17 @@ int fa_paged_append_batched(fa_ctx* ctx, const int32_t* block_tables, uint64_t m
 /* ------------------------------------------------------------ telemetry ------------------
  * runtime_telemetry src/wgpu_backend.rs:374: metadata of the last logical call on `ctx`. */
 int fa_last_telemetry(fa_ctx* ctx, fa_telemetry* out);
+/* Passive telemetry snapshot: WgpuFlatAttention::runtime_telemetry src/wgpu_backend.rs (M29,
+ * tests/m29_runtime_telemetry.rs:7): the record a one-shot fa_forward_gqa_rope / fa_forward_mha
+ * of this shape would leave in fa_last_telemetry (kernel, geometry, dispatch count, the
+ * allocations the context's caches would still need, fallback reason), built on the host from
+ * the same decisions without device work, allocation or synchronisation. Shape, rotary and
+ * dtype errors as for the forward; buffers are not involved. */
+int fa_forward_gqa_rope_telemetry(fa_ctx* ctx, const fa_grouped_shape* shape,
+                                  const fa_config* config, const fa_rotary* rotary, int dtype,
+                                  fa_telemetry* out);
+int fa_forward_mha_telemetry(fa_ctx* ctx, const fa_attention_shape* shape,
+                             const fa_config* config, int dtype, fa_telemetry* out);
 
 /* Variant selection policy. kernel_variant_for_head_dim src/wgpu_backend.rs:430.
  * prerotate_k: 0 = rotate K tiles on load inside the prefill kernel, 1 = rotate K once in a

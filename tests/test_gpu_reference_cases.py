@@ -583,3 +583,70 @@ def test_excessive_head_dimension_is_rejected_before_dispatch(hip):
         fa.HipFlatAttention(hip).forward(z, z, z, shape, fa.FlatAttentionConfig())
     assert e.value.variant == "UnsupportedHeadDim"
     assert "129" in str(e.value) and "128" in str(e.value)
+
+
+# ------------------------------------------------------------------ passive telemetry (M29)
+def _same_dispatch(snap, real):
+    for f in ("kernel_id", "kernel_name", "query_rows", "kv_rows", "workgroups", "workgroup_size",
+              "dispatch_count", "temporary_allocation_count", "temporary_allocation_bytes",
+              "splits", "fallback_reason", "device_name", "device_arch", "device_fingerprint"):
+        assert getattr(snap, f) == getattr(real, f), (f, getattr(snap, f), getattr(real, f))
+
+
+@pytest.mark.parametrize("case", [
+    ("mha", (1, 4, 9, 32), fa.DTYPE_F32, None, {}),
+    ("mha", (2, 2, 300, 128), fa.DTYPE_BF16, None, {}),
+    ("gqa", (2, 8, 2, 130, 128), fa.DTYPE_BF16, (1e4, 3), {}),
+    ("gqa", (1, 6, 1, 77, 64), fa.DTYPE_F16, (5e5, 0), {"precision": 1}),
+    ("gqa", (1, 8, 2, 65, 128), fa.DTYPE_BF16, (1e4, 0), {"v_layout": 1}),
+    ("gqa", (1, 4, 2, 33, 6), fa.DTYPE_F32, (1e4, 0), {}),
+    ("gqa", (1, 4, 2, 33, 64), fa.DTYPE_F32, (1e4, 0), {"prerotate": 0}),
+])
+def test_passive_telemetry_snapshot_matches_the_dispatch(case):
+    """passive_snapshot_matches_selected_portable_dispatch tests/m29_runtime_telemetry.rs:7: the
+    snapshot names the kernel, geometry, dispatch count and fallback reason the forward then
+    reports for a resident forward, and submits nothing (the last dispatch's record is
+    unchanged by it). A fresh
+    context is used so the predicted allocations (RoPE table, workspaces) are the first call's;
+    a second snapshot after the call predicts none."""
+    kind, dims, dtype, rope, pol = case
+    ctx = fa.HipContext(0)
+    try:
+        if "precision" in pol:
+            ctx.set_prefill_precision(pol["precision"])
+        if "v_layout" in pol:
+            ctx.set_prefill_v_layout(pol["v_layout"])
+        if "prerotate" in pol:
+            ctx.set_prefill_policy(pol["prerotate"])
+        cfg = fa.FlatAttentionConfig(True)
+        rng = np.random.default_rng(7)
+        if kind == "mha":
+            shape = fa.AttentionShape(*dims)
+            ex = fa.HipFlatAttention(ctx, dtype)
+            snap = ex.runtime_telemetry(shape, cfg)
+            assert ctx.last_telemetry().kernel_id == "None"
+            x = [ex.upload(rng.standard_normal(shape.tensor_len()).astype(np.float32))
+                 for _ in range(3)]
+            ex.forward_resident(*x, shape, cfg)
+        else:
+            shape = fa.GroupedAttentionShape(*dims)
+            rot = fa.RotaryEmbeddingConfig(*rope) if rope else None
+            ex = fa.HipRotaryGroupedAttention(ctx, dtype)
+            snap = ex.runtime_telemetry(shape, cfg, rot)
+            assert ctx.last_telemetry().kernel_id == "None"
+            q = rng.standard_normal(shape.q_tensor_len()).astype(np.float32)
+            k, v = (rng.standard_normal(shape.kv_tensor_len()).astype(np.float32) for _ in range(2))
+            bq, bk, bv = (ex.upload(t) for t in (q, k, v))
+            ex.forward_resident(bq, bk, bv, shape, cfg, rot)
+        real = ctx.last_telemetry()
+        _same_dispatch(snap, real)
+        assert real.device_name and real.device_arch.startswith("gfx950")  # m29 :33-34
+        if kind == "gqa" and rope and dims[-1] % 8 and dtype == fa.DTYPE_F32:
+            assert real.fallback_reason == ("K pre-rotation pass needs head_dim % 8 == 0; "
+                                            "K rotated on load")
+        again = (ex.runtime_telemetry(shape, cfg) if kind == "mha"
+                 else ex.runtime_telemetry(shape, cfg, rot))
+        assert again.temporary_allocation_count == 0 and again.temporary_allocation_bytes == 0
+        assert ctx.last_telemetry() == real
+    finally:
+        ctx.close()

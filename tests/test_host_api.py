@@ -529,3 +529,28 @@ def test_device_fingerprint_is_deterministic_driver_sensitive_and_escaped():
     assert _fnv1a64(b"a") == 0xAF63DC4C8601EC8C  # published FNV-1a-64 test vector
     rec2, _ = _record("GPU été;a=b%")
     assert "name=GPU été%3ba%3db%25;" in rec2
+
+
+def test_passive_telemetry_validates_like_the_forward():
+    """The snapshot (runtime_telemetry, tests/m29_runtime_telemetry.rs) checks the shape, RoPE,
+    head_dim and dtype as the forward does; a null context is reported last."""
+    lib = fa.lib()
+    t = L.TelemetryC()
+    cfg = ctypes.byref(fa.FlatAttentionConfig(True).c())
+
+    def gqa(shape, rot=None, dtype=fa.DTYPE_BF16, out=True):
+        return _variant(lib.fa_forward_gqa_rope_telemetry(
+            None, ctypes.byref(fa.GroupedAttentionShape(*shape).c()), cfg,
+            ctypes.byref(rot.c()) if rot else None, dtype, ctypes.byref(t) if out else None))
+
+    assert gqa((1, 4, 2, 8, 64), out=False) == "NullArgument"
+    assert gqa((1, 4, 0, 8, 64)) == "ZeroDimension"
+    assert gqa((1, 6, 4, 8, 64)) == "InvalidHeadGrouping"
+    assert gqa((1, 4, 2, 8, 63), fa.RotaryEmbeddingConfig(1e4, 0)) == "InvalidRotaryHeadDim"
+    assert gqa((1, 4, 2, 8, 64), fa.RotaryEmbeddingConfig(0.0, 0)) == "InvalidRotaryTheta"
+    assert gqa((1, 4, 2, 8, 60)) == "UnsupportedHeadDim"
+    assert gqa((1, 4, 2, 8, 64), dtype=5) == "UnsupportedDtype"
+    assert gqa((1, 4, 2, 8, 64)) == "NullArgument"
+    assert _variant(lib.fa_forward_mha_telemetry(
+        None, ctypes.byref(fa.AttentionShape(1, 2, 3, 129).c()), cfg, fa.DTYPE_F32,
+        ctypes.byref(t))) == "UnsupportedHeadDim"
