@@ -650,3 +650,171 @@ def test_passive_telemetry_snapshot_matches_the_dispatch(case):
         assert ctx.last_telemetry() == real
     finally:
         ctx.close()
+
+
+# ------------------------------------------------------- repeatability (numerical policy)
+def _policy_fixture(shape):  # tests/wgpu_numerical_policy.rs:20
+    i = np.arange(shape.tensor_len())
+    fi = i.astype(np.float32)
+    q = (np.where(i % 3 == 0, -1.0, 1.0).astype(np.float32)
+         * (np.sin(fi * np.float32(0.027)) * np.float32(3.5) + np.float32(0.125))).astype(np.float32)
+    k = (np.where((i // 5) % 2 == 0, 1.0, -1.0).astype(np.float32)
+         * (np.cos(fi * np.float32(0.019)) * np.float32(2.75) - np.float32(0.0625))).astype(np.float32)
+    v = (np.sin(fi * np.float32(0.013)) * np.float32(4.0)).astype(np.float32)
+    return q, k, v
+
+
+@pytest.mark.parametrize("seq_len,head_dim", [(17, 64), (33, 80), (9, 128)])
+@pytest.mark.parametrize("causal", [False, True])
+def test_forward_is_bit_repeatable_on_same_context(hip, seq_len, head_dim, causal):
+    """deterministic_mode_is_bit_repeatable_on_same_context tests/wgpu_numerical_policy.rs:84:
+    every kernel here has one writer per output element and a fixed reduction order, so repeated
+    forwards give the same bits; the first matches the oracle to 5e-5 + 5e-4|e|."""
+    shape = fa.AttentionShape(1, 2, seq_len, head_dim)
+    q, k, v = _policy_fixture(shape)
+    cfg = fa.FlatAttentionConfig(causal, 0.125)
+    ex = fa.HipFlatAttention(hip)
+    first = ex.forward(q, k, v, shape, cfg)
+    for it in range(4):
+        again = ex.forward(q, k, v, shape, cfg)
+        assert np.array_equal(again.output.view(np.uint32), first.output.view(np.uint32)), it
+        assert np.array_equal(again.lse.view(np.uint32), first.lse.view(np.uint32)), it
+    eo, el = oracle.forward(q, k, v, 1, 2, seq_len, head_dim, causal, scale=0.125)
+    assert_close("O", first.output, eo, 5e-5, 5e-4)
+    assert_close("LSE", first.lse, el, 5e-5, 5e-4)
+
+
+def test_host_input_validation_names_the_non_finite_element(hip):
+    """deterministic_mode_preserves_host_input_validation tests/wgpu_numerical_policy.rs:162:
+    a NaN at Q[7] is NonFiniteInput naming Q and index 7."""
+    shape = fa.AttentionShape(1, 1, 1, 64)
+    q = np.zeros(64, np.float32)
+    q[7] = np.nan
+    z = np.zeros(64, np.float32)
+    with pytest.raises(fa.FlatHipError) as e:
+        fa.HipFlatAttention(hip).forward(q, z, z, shape, fa.FlatAttentionConfig())
+    assert e.value.variant == "NonFiniteInput"
+    assert "Q" in str(e.value) and "7" in str(e.value)
+
+
+# --------------------------------------------------------------- M3 device matrix (MHA)
+def _m3_fixture(shape):  # tests/wgpu_device.rs:12
+    i = np.arange(shape.tensor_len(), dtype=np.float32)
+    q = (np.sin(i * np.float32(0.071) - np.float32(0.8)) * np.float32(0.75)).astype(np.float32)
+    k = (np.cos(i * np.float32(0.113) + np.float32(0.2)) * np.float32(0.65)).astype(np.float32)
+    v = (np.sin(i * np.float32(0.047) - np.float32(0.4)) * np.float32(1.25)).astype(np.float32)
+    return q, k, v
+
+
+def _m3_parity(hip, shape, causal, qkv=None, scale=None, tol=((2e-5, 2e-4), (3e-5, 3e-4))):
+    """assert_forward_parity tests/wgpu_device.rs:64: O 2e-5 + 2e-4|e|, LSE 3e-5 + 3e-4|e|."""
+    q, k, v = qkv if qkv is not None else _m3_fixture(shape)
+    got = fa.HipFlatAttention(hip).forward(q, k, v, shape, fa.FlatAttentionConfig(causal, scale))
+    eo, el = oracle.forward(q, k, v, shape.batch, shape.heads, shape.seq_len, shape.head_dim,
+                            causal, scale=scale)
+    assert_close("O", got.output, eo, *tol[0])
+    assert_close("LSE", got.lse, el, *tol[1])
+
+
+def test_m3_head_dimension_matrix_matches_reference(hip):
+    """m3_head_dimension_matrix_matches_reference tests/wgpu_device.rs:96."""
+    for d in [1, 8, 16, 32, 64, 80, 96, 128]:
+        for causal in (False, True):
+            _m3_parity(hip, fa.AttentionShape(1, 1, 17, d), causal)
+
+
+def test_m3_sequence_tile_boundaries_match_reference(hip):
+    """m3_sequence_tile_boundaries_match_reference tests/wgpu_device.rs:117."""
+    for s in [1, 15, 16, 17, 31, 32, 63, 64, 65, 127, 128, 129]:
+        for causal in (False, True):
+            _m3_parity(hip, fa.AttentionShape(1, 1, s, 32), causal)
+
+
+def test_m3_multiple_batches_and_heads_match_reference(hip):
+    """m3_multiple_batches_and_heads_match_reference tests/wgpu_device.rs:137."""
+    for causal in (False, True):
+        _m3_parity(hip, fa.AttentionShape(2, 3, 31, 16), causal)
+
+
+def test_m3_large_score_range_remains_finite_and_matches_reference(hip):
+    """m3_large_score_range_remains_finite_and_matches_reference tests/wgpu_device.rs:154:
+    |q|, |k| ~ 7 at scale 0.125; O 8e-5 + 8e-4|e|, LSE 2e-4 + 8e-4|e|."""
+    shape = fa.AttentionShape(1, 2, 31, 64)
+    i = np.arange(shape.tensor_len())
+    q = (np.where(i % 2 == 0, 1.0, -1.0) * (7.0 + (i % 11) * 0.125)).astype(np.float32)
+    k = (np.where((i // 3) % 2 == 0, -1.0, 1.0) * (6.5 + (i % 13) * 0.1875)).astype(np.float32)
+    v = (np.sin(i.astype(np.float32) * np.float32(0.03125)) * np.float32(3.0)).astype(np.float32)
+    for causal in (False, True):
+        _m3_parity(hip, shape, causal, (q, k, v), 0.125, ((8e-5, 8e-4), (2e-4, 8e-4)))
+
+
+def test_m3_causal_future_tokens_have_zero_contribution(hip):
+    """m3_causal_future_tokens_have_zero_contribution tests/wgpu_device.rs:191: K/V rows past
+    the first changed to +-1000 / 500+ leave causal row 0 unchanged (O = V[0]); 1e-6."""
+    shape = fa.AttentionShape(1, 1, 9, 8)
+    q, k, v = _m3_fixture(shape)
+    km, vm = k.copy().reshape(9, 8), v.copy().reshape(9, 8)
+    km[1:] = np.where(np.arange(8) % 2 == 0, 1000.0, -1000.0)
+    vm[1:] = 500.0 + np.arange(1, 9)[:, None] * 10.0 + np.arange(8)[None, :]
+    ex = fa.HipFlatAttention(hip)
+    cfg = fa.FlatAttentionConfig(True)
+    base = ex.forward(q, k, v, shape, cfg)
+    mut = ex.forward(q, km.ravel(), vm.ravel(), shape, cfg)
+    assert_close("row 0 invariance", mut.output[:8], base.output[:8], 1e-6, 1e-6)
+    assert_close("row 0 = V0", mut.output[:8], v[:8], 1e-6, 1e-6)
+    assert_close("LSE row 0", mut.lse[:1], base.lse[:1], 1e-6, 1e-6)
+
+
+# ------------------------------------------------------------------------- binary16 I/O
+def _f16_fixture(shape):  # tests/wgpu_f16.rs:13
+    i = np.arange(shape.tensor_len(), dtype=np.float32)
+    q = (np.sin(i * np.float32(0.031) - np.float32(0.7)) * np.float32(0.85)).astype(np.float32)
+    k = (np.cos(i * np.float32(0.047) + np.float32(0.2)) * np.float32(0.75)).astype(np.float32)
+    v = (np.sin(i * np.float32(0.019) - np.float32(0.4)) * np.float32(1.2)).astype(np.float32)
+    return q, k, v
+
+
+@pytest.mark.parametrize("dims", [(1, 2, 17, 64), (1, 1, 9, 128)])
+def test_f16_path_matches_reference(hip, dims):
+    """packed_f16_path_is_baseline_wgsl_and_matches_reference tests/wgpu_f16.rs:104 (check_raw_
+    f16_parity :67): binary16 inputs, O against the f32 oracle on the widened inputs rounded to
+    binary16 (2e-3 + 5e-3|e|), LSE f32 (8e-4 + 2e-3|e|)."""
+    shape = fa.AttentionShape(*dims)
+    q, k, v = (x.astype(np.float16) for x in _f16_fixture(shape))
+    ex = fa.HipFlatAttention(hip, fa.DTYPE_F16)
+    for causal in (False, True):
+        got = ex.forward(q, k, v, shape, fa.FlatAttentionConfig(causal))
+        eo, el = oracle.forward(*(x.astype(np.float32) for x in (q, k, v)), *dims, causal)
+        assert got.output.dtype == np.float16
+        assert_close("O", got.output.astype(np.float32), eo.astype(np.float16).astype(np.float32),
+                     2e-3, 5e-3)
+        assert_close("LSE", got.lse, el, 8e-4, 2e-3)
+
+
+def test_resident_f16_output_keeps_binary16_o_and_fp32_lse_lengths(hip):
+    """resident_f16_output_keeps_binary16_o_and_fp32_lse_lengths tests/wgpu_f16.rs:212: the
+    packed output holds tensor_len binary16 O values (tensor_len / 2 words) then lse_len f32."""
+    shape = fa.AttentionShape(1, 1, 9, 64)
+    ex = fa.HipFlatAttention(hip, fa.DTYPE_F16)
+    bufs = [ex.upload(x.astype(np.float16)) for x in _f16_fixture(shape)]
+    out = ex.forward_resident(*bufs, shape, fa.FlatAttentionConfig())
+    lay = ex.layout(shape)
+    n, m = shape.tensor_len(), shape.lse_len()
+    assert lay.output_elements == n and lay.lse_elements == m
+    assert lay.lse_byte_offset == n * 2 and lay.combined_bytes == (n // 2 + m) * 4
+    assert out.nbytes == lay.combined_bytes
+    res = ex.download_attention(out, shape)
+    assert res.output.size == n and res.lse.size == m
+
+
+def test_raw_f16_rejects_non_finite_input_before_dispatch(hip):
+    """raw_f16_rejects_non_finite_input_before_dispatch tests/wgpu_f16.rs:249: +inf (0x7c00) at
+    Q[3] is NonFiniteInput naming Q and index 3."""
+    shape = fa.AttentionShape(1, 1, 1, 64)
+    q = np.zeros(64, np.float16)
+    q.view(np.uint16)[3] = 0x7C00
+    z = np.zeros(64, np.float16)
+    with pytest.raises(fa.FlatHipError) as e:
+        fa.HipFlatAttention(hip, fa.DTYPE_F16).forward(q, z, z, shape, fa.FlatAttentionConfig())
+    assert e.value.variant == "NonFiniteInput"
+    assert "Q" in str(e.value) and "3" in str(e.value)

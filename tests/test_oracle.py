@@ -489,3 +489,49 @@ def test_paged_prefill_rejects_bad_pages_and_short_tables():
     with pytest.raises(oracle.OracleError):  # 6 rows need 2 pages, the table holds 1
         oracle.paged_prefill(x[:16], x, x, 2, 4, np.array([[0]], np.int32), 1, 1, 2, 6, 8, 4,
                              True, 1e4, 4)
+
+
+def _fx37(n, phase):  # tests/grouped.rs:5
+    x = np.arange(n, dtype=np.float32) * np.float32(0.037) + np.float32(phase)
+    return (np.sin(x) * np.float32(1.75) + np.cos(x * np.float32(0.41)) * np.float32(0.25)).astype(
+        np.float32)
+
+
+@pytest.mark.parametrize("hq,hkv", [(8, 8), (8, 2), (8, 1)])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("scale", [None, 0.19])
+def test_grouped_oracle_matches_expanded_mha_oracle_bit_exactly(hq, hkv, causal, scale):
+    """grouped_oracle_matches_expanded_mha_oracle_bit_exactly tests/grouped.rs:30: B2 S7 D16;
+    K/V copied out to every query head of their group give the same bits through the MHA oracle
+    (and MQA storage is never expanded by the grouped one)."""
+    B, S, D = 2, 7, 16
+    q = _fx37(B * hq * S * D, 0.1)
+    k = _fx37(B * hkv * S * D, 0.7)
+    v = _fx37(B * hkv * S * D, 1.3)
+    g = oracle.forward_grouped(q, k, v, B, hq, hkv, S, D, causal, scale=scale)
+    expand = lambda x: np.repeat(x.reshape(B, hkv, S * D), hq // hkv, axis=1).ravel()  # noqa: E731
+    m = oracle.forward(q, expand(k), expand(v), B, hq, S, D, causal, scale=scale)
+    assert np.array_equal(g[0].view(np.uint32), m[0].view(np.uint32))
+    assert np.array_equal(g[1].view(np.uint32), m[1].view(np.uint32))
+
+
+@pytest.mark.parametrize("dims", [(1, 4, 4, 7, 16), (2, 8, 2, 9, 64), (1, 8, 1, 5, 32)])
+@pytest.mark.parametrize("theta,off", [(1e4, 0), (5e5, 19)])
+@pytest.mark.parametrize("causal", [False, True])
+def test_projection_oracle_is_bit_exact_with_canonical_after_layout_transform(dims, theta, off,
+                                                                              causal):
+    """projection_oracle_is_bit_exact_with_canonical_r1_after_layout_transform
+    tests/projection_grouped.rs:73: the projection-layout RoPE oracle equals the head-major one
+    after moving [B, S, H*D] to [B, H, S, D], bit for bit."""
+    B, hq, hkv, S, D = dims
+    qp = _fx37(B * S * hq * D, 0.3)
+    kp = _fx37(B * S * hkv * D, 0.9)
+    vp = _fx37(B * S * hkv * D, 1.5)
+    a = oracle.forward_projection_asymmetric(qp, kp, vp, B, hq, hkv, S, S, D, 0, causal, theta,
+                                             off, off, True)
+    to_bhsd = lambda x, H: x.reshape(B, S, H, D).transpose(0, 2, 1, 3).ravel()  # noqa: E731
+    g = oracle.forward_grouped_rope(to_bhsd(qp, hq), to_bhsd(kp, hkv), to_bhsd(vp, hkv), B, hq,
+                                    hkv, S, D, causal, theta, off)
+    assert np.array_equal(a[0].view(np.uint32),
+                          g[0].reshape(B, hq, S, D).transpose(0, 2, 1, 3).ravel().view(np.uint32))
+    assert np.array_equal(a[1].view(np.uint32), g[1].view(np.uint32))
