@@ -325,6 +325,25 @@ def alternate_timing(ctx, ev, run, steps):
     return float(np.mean([ev.elapsed_ms(*evs[s]) for s in op_steps]))
 
 
+def graph_replay_ms(ctx, ev, run, steps=20):
+    """Median op time of `run` captured once into a HIP graph (fa_graph_*) and replayed:
+    HIP events around each replay on the library's stream, after five untimed replays."""
+    run()  # the context's caches are sized before the capture
+    with ctx.capture() as cap:
+        run()
+    for _ in range(5):
+        cap.graph.launch()
+    evs = [(ev.create(), ev.create()) for _ in range(steps)]
+    for e0, e1 in evs:
+        ev.record(e0, ctx.stream)
+        cap.graph.launch()
+        ev.record(e1, ctx.stream)
+    ctx.synchronize()
+    ms = float(np.median([ev.elapsed_ms(e0, e1) for e0, e1 in evs]))
+    cap.graph.release()
+    return ms
+
+
 def measure_all_configs(ctx, ev, rng, steps):
     """The other BASELINE configs, each timed alone (op events + its kernel's own events)."""
     stream = ctx.stream
@@ -370,6 +389,7 @@ def measure_all_configs(ctx, ev, rng, steps):
         op_ms, k_ms, tel = timed(run)
         res[f"resident_decode_B1_Hq16_Hkv4_D64_kv8192_{name}"] = {
             "kernel": tel.kernel_name, "ms": round(op_ms, 4), "kernel_ms": round(k_ms, 4),
+            "graph_ms": round(graph_replay_ms(ctx, ev, run), 4),
             "GB/s": round(nbytes / (k_ms * 1e-3) / 1e9, 1),
             "note": "one sequence: the op time is launch-bound, GB/s uses the kernel time",
             "reference_published_ms": {"M15": 23.843433, "M48": 19.562844,
@@ -690,6 +710,9 @@ def main():
     op_steps = [s for s in range(args.steps) if s % 2 == 1] or list(range(args.steps))
     per_op = {name: [ev.elapsed_ms(evs[s][i], evs[s][i + 1]) for s in op_steps]
               for i, (name, _, _, _) in enumerate(ops)}
+    # the same ops replayed from a captured HIP graph (launch overhead removed), after the
+    # timed pass; reported beside the op times, not used for `value`
+    graph_ms = {name: graph_replay_ms(ctx, ev, run) for name, run, _, _ in ops}
     step_ms = sum(np.mean(v) for v in per_op.values())
 
     out = {"metric": "causal GQA prefill TFLOP/s (D128,N4096) + paged-decode HBM GB/s, % of peak",
@@ -709,6 +732,7 @@ def main():
              "grid": list(t.workgroups), **meta}
         d["kernel_ms"] = round(kern[name], 5)
         d["kernel_ms_min"] = round(kern_min[name], 5)
+        d["graph_ms"] = round(graph_ms[name], 5)
         if name == "prefill":
             tf = work / (ms * 1e-3) / 1e12
             ktf = work / (kern[name] * 1e-3) / 1e12

@@ -187,6 +187,8 @@ struct fa_ctx {
     // 16-bit RoPE prefill scores: 0 = rotated Q/K rounded to the storage type, 1 = split
     // high/residual operands (fa_ctx_set_prefill_precision)
     int prefill_precision = 0;
+    // the stream is being captured into a graph (fa_graph_capture_begin)
+    bool capturing = false;
     // decode work layout: -1 automatic (head-grouped workgroups where they apply), 0 one-wave
     // workgroups (fa_ctx_set_decode_policy; read when a decode plan is prepared)
     int decode_grouped_policy = -1;
@@ -235,8 +237,16 @@ struct fa_ctx {
 namespace {
 
 int set_device(fa_ctx* ctx) {
+    if (ctx->capturing) return FA_OK;  // made current when the capture began
     HIP_TRY(hipSetDevice(ctx->device));
     return FA_OK;
+}
+
+int refuse_in_capture(const fa_ctx* ctx, const char* what) {
+    if (!ctx->capturing) return FA_OK;
+    return fail(FA_ERR_GRAPH_CAPTURE,
+                "%s while the stream is being captured; prepare plans and warm the context's "
+                "caches before fa_graph_capture_begin", what);
 }
 
 void begin_call(fa_ctx* ctx) {
@@ -291,7 +301,7 @@ hipEvent_t take_event(fa_ctx* ctx) {
 }
 
 void begin_span(fa_ctx* ctx) {
-    if (!ctx->timing || ctx->timing_paused) return;
+    if (!ctx->timing || ctx->timing_paused || ctx->capturing) return;
     hipEvent_t e = take_event(ctx);
     if (e && hipEventRecord(e, ctx->stream) != hipSuccess) {
         ctx->free_events.push_back(e);
@@ -301,7 +311,7 @@ void begin_span(fa_ctx* ctx) {
 }
 
 void end_span(fa_ctx* ctx, int kernel_id) {
-    if (!ctx->timing || ctx->timing_paused || !ctx->open_begin) return;
+    if (!ctx->timing || ctx->timing_paused || ctx->capturing || !ctx->open_begin) return;
     hipEvent_t e = take_event(ctx);
     if (!e || hipEventRecord(e, ctx->stream) != hipSuccess) {
         ctx->free_events.push_back(ctx->open_begin);
@@ -333,6 +343,7 @@ int resolve_spans(fa_ctx* ctx) {
 }
 
 int dev_alloc(fa_ctx* ctx, void** p, size_t bytes) {
+    if (int rc = refuse_in_capture(ctx, "device allocation")) return rc;
     HIP_TRY(hipMalloc(p, bytes ? bytes : 16));
     ctx->call_allocs += 1;
     ctx->call_alloc_bytes += bytes;
@@ -402,6 +413,7 @@ int grow(fa_ctx* ctx, void** buf, size_t* cap, size_t bytes, void** out) {
 // free, a new slot is allocated.
 int stage_upload(fa_ctx* ctx, void* dst, const void* src, size_t bytes) {
     if (!bytes) return FA_OK;
+    if (int rc = refuse_in_capture(ctx, "host upload")) return rc;
     fa_ctx::Staging* slot = nullptr;
     for (auto& st : ctx->staging) {
         if (st.busy && hipEventQuery(st.done) == hipSuccess) st.busy = false;
@@ -576,6 +588,7 @@ void* fa_ctx_stream(fa_ctx* ctx) { return ctx ? (void*)ctx->stream : nullptr; }
 
 int fa_ctx_synchronize(fa_ctx* ctx) {
     if (!ctx) return fail(FA_ERR_NULL_ARGUMENT, "context is null");
+    if (int rc = refuse_in_capture(ctx, "stream synchronisation")) return rc;
     if (int rc = set_device(ctx)) return rc;
     HIP_TRY(hipStreamSynchronize(ctx->stream));
     return ok();
@@ -755,6 +768,7 @@ int fa_ctx_set_prefill_policy(fa_ctx* ctx, int32_t prerotate_k) {
 // ---------------------------------------------------------------------------- buffers
 int fa_buf_alloc(fa_ctx* ctx, size_t bytes, void** out) {
     if (!ctx || !out) return fail(FA_ERR_NULL_ARGUMENT, "null argument");
+    if (int rc = refuse_in_capture(ctx, "buffer allocation or copy")) return rc;
     if (int rc = set_device(ctx)) return rc;
     HIP_TRY(hipMalloc(out, bytes ? bytes : 16));
     return ok();
@@ -762,6 +776,7 @@ int fa_buf_alloc(fa_ctx* ctx, size_t bytes, void** out) {
 
 int fa_buf_free(fa_ctx* ctx, void* ptr) {
     if (!ctx) return fail(FA_ERR_NULL_ARGUMENT, "context is null");
+    if (int rc = refuse_in_capture(ctx, "buffer allocation or copy")) return rc;
     if (!ptr) return ok();
     if (int rc = set_device(ctx)) return rc;
     HIP_TRY(hipStreamSynchronize(ctx->stream));
@@ -771,6 +786,7 @@ int fa_buf_free(fa_ctx* ctx, void* ptr) {
 
 int fa_buf_upload(fa_ctx* ctx, void* dst, const void* host, size_t bytes) {
     if (!ctx || !dst || (!host && bytes)) return fail(FA_ERR_NULL_ARGUMENT, "null argument");
+    if (int rc = refuse_in_capture(ctx, "buffer allocation or copy")) return rc;
     if (int rc = set_device(ctx)) return rc;
     HIP_TRY(hipMemcpyAsync(dst, host, bytes, hipMemcpyHostToDevice, ctx->stream));
     HIP_TRY(hipStreamSynchronize(ctx->stream));
@@ -779,6 +795,7 @@ int fa_buf_upload(fa_ctx* ctx, void* dst, const void* host, size_t bytes) {
 
 int fa_buf_download(fa_ctx* ctx, void* host, const void* src, size_t bytes) {
     if (!ctx || !src || (!host && bytes)) return fail(FA_ERR_NULL_ARGUMENT, "null argument");
+    if (int rc = refuse_in_capture(ctx, "buffer allocation or copy")) return rc;
     if (int rc = set_device(ctx)) return rc;
     HIP_TRY(hipMemcpyAsync(host, src, bytes, hipMemcpyDeviceToHost, ctx->stream));
     HIP_TRY(hipStreamSynchronize(ctx->stream));
@@ -787,8 +804,66 @@ int fa_buf_download(fa_ctx* ctx, void* host, const void* src, size_t bytes) {
 
 int fa_buf_fill_u32(fa_ctx* ctx, void* dst, uint32_t value, size_t count) {
     if (!ctx || !dst) return fail(FA_ERR_NULL_ARGUMENT, "null argument");
+    // a memset node must not enter a graph: its replays have given wrong results on this part
+    if (int rc = refuse_in_capture(ctx, "buffer fill")) return rc;
     if (int rc = set_device(ctx)) return rc;
     HIP_TRY(hipMemsetD32Async((hipDeviceptr_t)dst, (int)value, count, ctx->stream));
+    return ok();
+}
+
+// ------------------------------------------------------------------------------ graphs
+struct fa_graph {
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    int device = 0;
+};
+
+int fa_graph_capture_begin(fa_ctx* ctx) {
+    if (!ctx) return fail(FA_ERR_NULL_ARGUMENT, "context is null");
+    if (ctx->capturing) return fail(FA_ERR_GRAPH_CAPTURE, "the stream is already being captured");
+    if (int rc = set_device(ctx)) return rc;
+    HIP_TRY(hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
+    ctx->capturing = true;
+    return ok();
+}
+
+int fa_graph_capture_end(fa_ctx* ctx, fa_graph** out) {
+    if (!ctx || !out) return fail(FA_ERR_NULL_ARGUMENT, "null argument");
+    *out = nullptr;
+    if (!ctx->capturing) return fail(FA_ERR_GRAPH_CAPTURE, "the stream is not being captured");
+    ctx->capturing = false;
+    hipGraph_t g = nullptr;
+    HIP_TRY(hipStreamEndCapture(ctx->stream, &g));
+    hipGraphExec_t e = nullptr;
+    const hipError_t err = hipGraphInstantiate(&e, g, nullptr, nullptr, 0);
+    if (err != hipSuccess) {
+        (void)hipGraphDestroy(g);
+        return fail(FA_ERR_HIP, "hipGraphInstantiate: %s", hipGetErrorString(err));
+    }
+    fa_graph* r = new fa_graph();
+    r->graph = g;
+    r->exec = e;
+    r->device = ctx->device;
+    *out = r;
+    return ok();
+}
+
+int fa_graph_launch(fa_ctx* ctx, const fa_graph* graph) {
+    if (!ctx || !graph) return fail(FA_ERR_NULL_ARGUMENT, "null argument");
+    if (graph->device != ctx->device)
+        return fail(FA_ERR_FOREIGN_BUFFER, "graph was captured on device %d, context is on %d",
+                    graph->device, ctx->device);
+    if (int rc = refuse_in_capture(ctx, "graph launch")) return rc;
+    if (int rc = set_device(ctx)) return rc;
+    HIP_TRY(hipGraphLaunch(graph->exec, ctx->stream));
+    return ok();
+}
+
+int fa_graph_destroy(fa_graph* graph) {
+    if (!graph) return ok();
+    if (graph->exec) (void)hipGraphExecDestroy(graph->exec);
+    if (graph->graph) (void)hipGraphDestroy(graph->graph);
+    delete graph;
     return ok();
 }
 
@@ -1246,6 +1321,8 @@ int fa_prepared_forward_layout(const fa_prepared_forward* p, fa_packed_layout* o
 
 int fa_prepared_forward_destroy(fa_prepared_forward* p) {
     if (!p) return ok();
+    if (p->ctx && p->ctx->capturing)
+        return refuse_in_capture(p->ctx, "release (it waits for the stream)");
     (void)hipSetDevice(p->ctx->device);
     (void)hipStreamSynchronize(p->ctx->stream);
     if (p->run.table) (void)hipFree(p->run.table);
@@ -1789,6 +1866,8 @@ int fa_paged_cache_create(fa_ctx* ctx, uint64_t page_size, uint64_t physical_pag
 
 int fa_paged_cache_destroy(fa_paged_cache* c) {
     if (!c) return ok();
+    if (c->ctx && c->ctx->capturing)
+        return refuse_in_capture(c->ctx, "release (it waits for the stream)");
     (void)hipSetDevice(c->ctx->device);
     (void)hipStreamSynchronize(c->ctx->stream);
     (void)hipFree(c->k);
@@ -2258,6 +2337,8 @@ int fa_paged_decode_plan_info(const fa_decode_plan* p, uint64_t* split_tokens,
 
 int fa_paged_decode_plan_destroy(fa_decode_plan* p) {
     if (!p) return ok();
+    if (p->ctx && p->ctx->capturing)
+        return refuse_in_capture(p->ctx, "release (it waits for the stream)");
     (void)hipSetDevice(p->ctx->device);
     (void)hipStreamSynchronize(p->ctx->stream);
     free_plan(p);
@@ -2517,6 +2598,8 @@ int fa_resident_cache_create(fa_ctx* ctx, uint64_t batch, uint64_t kv_heads, uin
 
 int fa_resident_cache_destroy(fa_resident_cache* c) {
     if (!c) return ok();
+    if (c->ctx && c->ctx->capturing)
+        return refuse_in_capture(c->ctx, "release (it waits for the stream)");
     (void)hipSetDevice(c->ctx->device);
     (void)hipStreamSynchronize(c->ctx->stream);
     (void)hipFree(c->k);
@@ -2761,6 +2844,8 @@ int fa_chunked_prefill_paged_prepare(fa_ctx* ctx, const int32_t* block_tables, u
 
 int fa_prefill_plan_destroy(fa_prefill_plan* p) {
     if (!p) return ok();
+    if (p->ctx && p->ctx->capturing)
+        return refuse_in_capture(p->ctx, "release (it waits for the stream)");
     (void)hipSetDevice(p->ctx->device);
     (void)hipStreamSynchronize(p->ctx->stream);
     if (p->d_bt) (void)hipFree(p->d_bt);

@@ -10,7 +10,7 @@ from ._lib import (DTYPE_BF16, DTYPE_F16, DTYPE_F32, LIB_PATH, FlatHipError, lib
 from .api import (AsymmetricGroupedAttentionShape, AsymmetricRotaryEmbeddingConfig,
                   AttentionShape, DeviceBuffer, FlatAttentionConfig, FlatAttentionOutput,
                   GroupedAttentionShape, HipAsymmetricProjectionPipeline,
-                  HipChunkedProjectionPrefillPipeline, HipContext, HipFlatAttention,
+                  HipChunkedProjectionPrefillPipeline, HipContext, HipFlatAttention, HipGraph,
                   HipPagedDecodePipeline, HipPagedKvCache, HipProjectionRotaryGroupedPipeline, HipResidentDecodePipeline,
                   HipResidentKvCache, HipRotaryGroupedAttention, ResidentDecodePlan,
                   PackedLayout, PagedChunkedPrefillPlan, PagedDecodePlan, PagedKvAddress,

@@ -35,7 +35,7 @@ STATUS = {
     30: "InvalidPage", 31: "EmptyCache", 32: "InvalidCacheLength", 33: "ForeignBuffer", 34: "CandidateNotEnabled",
     35: "UnsupportedCandidateShape", 40: "PagedZeroDimension", 41: "CapacityOverflow",
     42: "CapacityExceeded", 43: "GenerationOverflow", 50: "NullArgument", 60: "Hip",
-    61: "ScratchExceeded",
+    61: "ScratchExceeded", 62: "GraphCapture",
 }
 
 KERNEL_IDS = {
@@ -121,6 +121,10 @@ PROTOTYPES = {
     "fa_ctx_destroy": (INT, [VP]),
     "fa_ctx_stream": (VP, [VP]),
     "fa_ctx_synchronize": (INT, [VP]),
+    "fa_graph_capture_begin": (INT, [VP]),
+    "fa_graph_capture_end": (INT, [VP, P(VP)]),
+    "fa_graph_launch": (INT, [VP, VP]),
+    "fa_graph_destroy": (INT, [VP]),
     "fa_ctx_device_name": (INT, [VP, ctypes.c_char_p, SZ]),
     "fa_ctx_set_prefill_policy": (INT, [VP, I32]),
     "fa_ctx_set_prefill_v_layout": (INT, [VP, I32]),

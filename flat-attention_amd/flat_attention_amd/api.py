@@ -8,7 +8,9 @@ the host.
 
 from __future__ import annotations
 
+import contextlib
 import ctypes
+import types
 import weakref
 from dataclasses import dataclass
 from typing import Optional
@@ -241,6 +243,26 @@ class HipContext:
     def synchronize(self):
         check(lib().fa_ctx_synchronize(self.handle))
 
+    def capture_begin(self):
+        """Start recording this context's launches into a HIP graph (fa_graph_capture_begin)."""
+        check(lib().fa_graph_capture_begin(self.handle))
+
+    def capture_end(self) -> "HipGraph":
+        h = L.VP()
+        check(lib().fa_graph_capture_end(self.handle, ctypes.byref(h)))
+        return HipGraph(self, h.value)
+
+    @contextlib.contextmanager
+    def capture(self):
+        """``with ctx.capture() as cap: <launches>`` then ``cap.graph.launch()``. The capture is
+        ended (and its graph built) even when the body raises."""
+        cap = types.SimpleNamespace(graph=None)
+        self.capture_begin()
+        try:
+            yield cap
+        finally:
+            cap.graph = self.capture_end()
+
     def adapter_name(self) -> str:
         buf = ctypes.create_string_buffer(256)
         check(lib().fa_ctx_device_name(self.handle, buf, 256))
@@ -343,6 +365,26 @@ def _telemetry(t) -> RuntimeDispatchTelemetry:
             t.temporary_allocation_count, t.temporary_allocation_bytes, t.splits,
             t.fallback_reason.decode() if t.has_fallback_reason else None,
             t.device_name.decode(), t.device_arch.decode(), t.device_fingerprint)
+
+
+class HipGraph:
+    """An executable graph of captured launches (fa_graph_*): replays them on the context's
+    stream with the buffers and arguments they were captured with."""
+
+    def __init__(self, ctx: "HipContext", handle: int):
+        self.ctx, self.handle = ctx, handle
+        ctx._adopt(self)
+
+    def launch(self):
+        check(lib().fa_graph_launch(self.ctx.handle, self.handle))
+
+    def release(self):
+        if getattr(self, "handle", None):
+            lib().fa_graph_destroy(self.handle)
+        self.handle = None
+
+    def __del__(self):
+        self.release()
 
 
 class DeviceBuffer:

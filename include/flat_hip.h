@@ -81,7 +81,9 @@ typedef enum fa_status {
     FA_ERR_GENERATION_OVERFLOW = 43,
     FA_ERR_NULL_ARGUMENT = 50,
     FA_ERR_HIP = 60,
-    FA_ERR_SCRATCH_EXCEEDED = 61  /* no reference variant: fa_paged_decode_noalloc's scratch */
+    FA_ERR_SCRATCH_EXCEEDED = 61, /* no reference variant: fa_paged_decode_noalloc's scratch */
+    FA_ERR_GRAPH_CAPTURE = 62     /* no reference variant: a call that allocates, uploads from the
+                                     host, fills or waits while the stream is being captured */
 } fa_status;
 
 /* Storage dtype of Q/K/V/O. Math is always f32 (f32 online-softmax state, f32 accumulation);
@@ -367,8 +369,9 @@ int fa_paged_decode_plan_info(const fa_decode_plan* plan, uint64_t* split_tokens
 int fa_paged_decode_plan_set_split(fa_ctx* ctx, fa_decode_plan* plan, uint64_t split_tokens);
 
 /* Allocation-free paged decode. No counterpart in the reference: it is for callers that cannot
- * allocate device memory (code under HIP graph capture, tight serving loops, harnesses that
- * forbid hipMalloc). Same arguments, validation and results (bitwise) as
+ * allocate device memory (tight serving loops, harnesses that forbid hipMalloc). It uploads
+ * its host-built work list on every call, so it is not for graph capture (capture a prepared
+ * plan's fa_paged_decode_launch with fa_graph_* instead). Same arguments, validation and results (bitwise) as
  * fa_paged_decode_prepare followed by fa_paged_decode_launch with the automatic split, in one
  * call that allocates no device or pinned host memory: the block tables, lengths, query
  * positions, work list, the queries' RoPE (cos, sin) rows and the split-K partials live in a
@@ -524,6 +527,24 @@ int fa_paged_append_batched(fa_ctx* ctx, const int32_t* block_tables, uint64_t m
 /* ------------------------------------------------------------ telemetry ------------------
  * runtime_telemetry src/wgpu_backend.rs:374: metadata of the last logical call on `ctx`. */
 int fa_last_telemetry(fa_ctx* ctx, fa_telemetry* out);
+/* ------------------------------------------------------------ HIP graphs -----------------
+ * No counterpart in the reference (its callers record passes into a wgpu command encoder and
+ * submit it; these are the HIP form of that for launch-bound loops). capture_begin starts a
+ * thread-local capture of the context's stream; the launches that follow are recorded, not
+ * run, until capture_end turns them into an executable graph that fa_graph_launch replays on
+ * the stream (same buffers, same arguments; the caller changes buffer contents between
+ * replays). Only launches that enqueue kernels alone may be captured: prepared plans
+ * (fa_paged_decode_launch, fa_launch_prepared, fa_chunked_prefill_paged_launch,
+ * fa_backward_launch_prepared) and one-shot calls whose context caches are already sized. While
+ * capturing, a call that would allocate device memory, upload host data, fill a buffer or wait
+ * for the stream fails with FA_ERR_GRAPH_CAPTURE and enqueues nothing; per-kernel timing
+ * events are not recorded. */
+typedef struct fa_graph fa_graph;
+int fa_graph_capture_begin(fa_ctx* ctx);
+int fa_graph_capture_end(fa_ctx* ctx, fa_graph** out);
+int fa_graph_launch(fa_ctx* ctx, const fa_graph* graph);
+int fa_graph_destroy(fa_graph* graph);
+
 /* Passive telemetry snapshot: WgpuFlatAttention::runtime_telemetry src/wgpu_backend.rs (M29,
  * tests/m29_runtime_telemetry.rs:7): the record a one-shot fa_forward_gqa_rope / fa_forward_mha
  * of this shape would leave in fa_last_telemetry (kernel, geometry, dispatch count, the

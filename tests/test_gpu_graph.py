@@ -1,0 +1,112 @@
+"""HIP graphs over the library's launches (fa_graph_*; no counterpart in the reference, whose
+callers record passes into a command encoder and submit it).
+
+A prepared paged decode and a prepared contiguous forward (K pre-rotation pass + prefill) are
+captured once and replayed several times with new buffer contents between replays and eager
+work and synchronisations in between; every replay must give the same bits as an eager launch
+on the same inputs. Calls that would allocate, upload, fill or wait are refused while
+capturing and leave the capture usable.
+"""
+import numpy as np
+import pytest
+
+from _inputs import bf16_round, normal
+
+import flat_attention_amd as fa
+
+pytestmark = pytest.mark.gpu
+
+
+def _bits(buf, n):
+    return buf.download(np.uint8, n)
+
+
+def test_captured_paged_decode_replays_match_eager(hip):
+    rng = np.random.default_rng(11)
+    ctx_lens = np.array([700, 1500, 33, 1024], np.int32)
+    ps, hq, hkv, D = 16, 8, 2, 128
+    pages = (ctx_lens + ps - 1) // ps
+    total = int(pages.sum())
+    ids = rng.permutation(total)
+    bt = np.zeros((len(ctx_lens), int(pages.max())), np.int32)
+    cur = 0
+    for s, n in enumerate(pages):
+        bt[s, :n] = ids[cur:cur + n]
+        cur += n
+    width = hkv * D
+    dt = fa.DTYPE_BF16
+    kb = fa.DeviceBuffer.from_array(hip, fa.host_storage(normal(total * ps * width, 1), dt))
+    vb = fa.DeviceBuffer.from_array(hip, fa.host_storage(normal(total * ps * width, 2), dt))
+    plan = fa.PagedDecodePlan(hip, bt, ctx_lens, ps, total, hq, hkv, D,
+                              fa.FlatAttentionConfig(True), 1e4, dt)
+    nq = len(ctx_lens) * hq * D
+    qb = fa.DeviceBuffer(hip, nq * 2)
+    out_g = fa.DeviceBuffer(hip, plan.layout().combined_bytes)
+    out_e = fa.DeviceBuffer(hip, plan.layout().combined_bytes)
+    qb.upload(fa.host_storage(bf16_round(normal(nq, 3)), dt))
+    plan.launch(qb, kb, vb, out_e)  # warms the RoPE table cache before capturing
+    with hip.capture() as cap:
+        plan.launch(qb, kb, vb, out_g)
+    n = plan.layout().combined_bytes
+    for rep in range(3):
+        qb.upload(fa.host_storage(bf16_round(normal(nq, 10 + rep)), dt))
+        cap.graph.launch()
+        plan.launch(qb, kb, vb, out_e)
+        hip.synchronize()
+        assert np.array_equal(_bits(out_g, n), _bits(out_e, n)), rep
+        res = fa.download_attention(out_g, plan.layout(), dt)
+        assert np.all(np.isfinite(res.lse))
+
+
+def test_captured_prepared_forward_replays_match_eager(hip):
+    B, hq, hkv, S, D = 1, 8, 2, 300, 128
+    shape = fa.GroupedAttentionShape(B, hq, hkv, S, D)
+    cfg = fa.FlatAttentionConfig(True)
+    rot = fa.RotaryEmbeddingConfig(1e4, 5)
+    ex = fa.HipRotaryGroupedAttention(hip, fa.DTYPE_BF16)
+    bq = ex.upload(normal(shape.q_tensor_len(), 1))
+    bk = ex.upload(normal(shape.kv_tensor_len(), 2))
+    bv = ex.upload(normal(shape.kv_tensor_len(), 3))
+    n = ex.layout(shape).combined_bytes
+    out_g, out_e = fa.DeviceBuffer(hip, n), fa.DeviceBuffer(hip, n)
+    prep = ex.prepare(bq, bk, bv, out_g, shape, cfg, rot)
+    with hip.capture() as cap:
+        ex.encode_prepared(prep)
+    assert hip.last_telemetry().dispatch_count == 2  # rotate_rows + prefill, recorded
+    for rep in range(3):
+        bk.upload(fa.host_storage(normal(shape.kv_tensor_len(), 20 + rep), fa.DTYPE_BF16))
+        cap.graph.launch()
+        ex.forward_resident(bq, bk, bv, shape, cfg, rot, out_e)
+        hip.synchronize()
+        assert np.array_equal(_bits(out_g, n), _bits(out_e, n)), rep
+
+
+def test_capture_refuses_allocation_upload_fill_and_wait(hip):
+    fresh = fa.HipContext(0)
+    try:
+        buf = fa.DeviceBuffer(fresh, 1024)
+        ex = fa.HipRotaryGroupedAttention(fresh, fa.DTYPE_BF16)
+        shape = fa.GroupedAttentionShape(1, 4, 2, 64, 64)
+        q = ex.upload(normal(shape.q_tensor_len(), 1))
+        kv = ex.upload(normal(shape.kv_tensor_len(), 2))
+        out = fa.DeviceBuffer(fresh, ex.layout(shape).combined_bytes)
+        with fresh.capture() as cap:
+            for call in (lambda: buf.fill_u32(0),
+                         lambda: hip_sync(fresh),
+                         # cold context: the RoPE table and K workspace would be allocated
+                         lambda: ex.forward_resident(q, kv, kv, shape, fa.FlatAttentionConfig(True),
+                                                     fa.RotaryEmbeddingConfig(1e4, 0), out)):
+                with pytest.raises(fa.FlatHipError) as e:
+                    call()
+                assert e.value.variant == "GraphCapture", e.value
+            with pytest.raises(fa.FlatHipError) as e:
+                fresh.capture_begin()
+            assert e.value.variant == "GraphCapture"
+        cap.graph.launch()  # an empty graph
+        fresh.synchronize()
+    finally:
+        fresh.close()
+
+
+def hip_sync(ctx):
+    ctx.synchronize()

@@ -554,3 +554,12 @@ def test_passive_telemetry_validates_like_the_forward():
     assert _variant(lib.fa_forward_mha_telemetry(
         None, ctypes.byref(fa.AttentionShape(1, 2, 3, 129).c()), cfg, fa.DTYPE_F32,
         ctypes.byref(t))) == "UnsupportedHeadDim"
+
+
+def test_graph_calls_need_a_context_and_a_capture():
+    lib = fa.lib()
+    h = ctypes.c_void_p()
+    assert _variant(lib.fa_graph_capture_begin(None)) == "NullArgument"
+    assert _variant(lib.fa_graph_capture_end(None, ctypes.byref(h))) == "NullArgument"
+    assert _variant(lib.fa_graph_launch(None, None)) == "NullArgument"
+    assert lib.fa_graph_destroy(None) == 0
