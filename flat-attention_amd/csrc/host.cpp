@@ -1365,7 +1365,8 @@ int check_asymmetric_pass(const fa_asymmetric_shape* sh, const fa_config* cfg,
                           size_t q_bytes, const void* k, const void* v, size_t kv_bytes,
                           const void* out_lse, size_t out_bytes, float* scale,
                           fa_packed_layout* lay) {
-    if (sh->query_position_offset + sh->query_len > kI32)
+    // (written so that a position near the top of the u64 range cannot wrap past the test)
+    if (sh->query_len > kI32 || sh->query_position_offset > kI32 - sh->query_len)
         return fail(FA_ERR_POSITION_OVERFLOW, "rotary position offset overflows the index space");
     if (rot) {
         if (int rc = check_rotary(rot->theta, rot->query_position_offset, sh->head_dim, sh->query_len))
@@ -2804,7 +2805,8 @@ int fa_chunked_prefill_paged_prepare(fa_ctx* ctx, const int32_t* block_tables, u
     if (int rc = validate_grouped(sh->batch, sh->q_heads, sh->kv_heads,
                                   std::max(sh->query_len, sh->kv_len), sh->head_dim))
         return rc;
-    if (sh->query_position_offset + sh->query_len > kI32)
+    // (written so that a position near the top of the u64 range cannot wrap past the test)
+    if (sh->query_len > kI32 || sh->query_position_offset > kI32 - sh->query_len)
         return fail(FA_ERR_POSITION_OVERFLOW, "rotary position offset overflows the index space");
     if (int rc = check_rotary(rot->theta, rot->query_position_offset, sh->head_dim, sh->query_len))
         return rc;

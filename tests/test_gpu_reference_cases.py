@@ -818,3 +818,73 @@ def test_raw_f16_rejects_non_finite_input_before_dispatch(hip):
         fa.HipFlatAttention(hip, fa.DTYPE_F16).forward(q, z, z, shape, fa.FlatAttentionConfig())
     assert e.value.variant == "NonFiniteInput"
     assert "Q" in str(e.value) and "3" in str(e.value)
+
+
+# --------------------------------------------------------------------- M38 property stress
+def test_m38_repeated_resident_dispatch_reuses_inputs_without_numerical_drift(hip):
+    """repeated_resident_dispatch_reuses_inputs_without_numerical_drift
+    tests/m38_property_stress.rs:161: B1 Hq8 Hkv2 S17 D32 causal, the m38 LCG inputs, 32 resident
+    forwards over the same buffers, each within 2e-4 + 1e-3|e| of the oracle (and, here, bitwise
+    equal to the first)."""
+    from _inputs import Lcg
+    shape = fa.GroupedAttentionShape(1, 8, 2, 17, 32)
+    rng = Lcg(0x4D38D15CA7C40001)
+    q, k, v = rng.vec(shape.q_tensor_len()), rng.vec(shape.kv_tensor_len()), rng.vec(shape.kv_tensor_len())
+    cfg = fa.FlatAttentionConfig(True)
+    eo, el = oracle.forward_grouped(q, k, v, 1, 8, 2, 17, 32, True)
+    ex = fa.HipRotaryGroupedAttention(hip)
+    bq, bk, bv = (ex.upload(x) for x in (q, k, v))
+    first = None
+    for it in range(32):
+        got = ex.download_attention(ex.forward_resident(bq, bk, bv, shape, cfg, None), shape)
+        assert_close(f"O {it}", got.output, eo, 2e-4, 1e-3)
+        assert_close(f"LSE {it}", got.lse, el, 2e-4, 1e-3)
+        if first is None:
+            first = got
+        assert np.array_equal(got.output.view(np.uint32), first.output.view(np.uint32))
+
+
+@pytest.mark.parametrize("dtype", [fa.DTYPE_F32, fa.DTYPE_BF16])
+def test_m38_extreme_but_finite_scores_remain_finite_and_normalized(hip, dtype):
+    """extreme_but_finite_scores_remain_finite_and_normalized tests/m38_property_stress.rs:109
+    on the device: B1 Hq8 Hkv1 S33 D128, Q = +-1000, K = +-1000 (scores ~1e7), V = 1: O = 1 to
+    3e-5 (f32; bf16 storage rounds O to 2^-8) and LSE finite, both masks."""
+    shape = fa.GroupedAttentionShape(1, 8, 1, 33, 128)
+    i = np.arange(shape.q_tensor_len())
+    q = np.where(i % 2 == 0, 1000.0, -1000.0).astype(np.float32)
+    j = np.arange(shape.kv_tensor_len())
+    k = np.where(j % 3 == 0, -1000.0, 1000.0).astype(np.float32)
+    v = np.ones(shape.kv_tensor_len(), np.float32)
+    ex = fa.HipRotaryGroupedAttention(hip, dtype)
+    for causal in (False, True):
+        got = ex.forward(q, k, v, shape, fa.FlatAttentionConfig(causal), None)
+        o = fa.storage_to_f32(got.output, dtype)
+        assert np.all(np.isfinite(o)) and np.all(np.isfinite(got.lse))
+        assert np.max(np.abs(o - 1.0)) <= (3e-5 if dtype == fa.DTYPE_F32 else 2 ** -8)
+
+
+def test_m38_resident_kv_cache_reset_and_reuse_preserve_logical_length_contract(hip):
+    """resident_kv_cache_reset_and_reuse_preserve_logical_length_contract
+    tests/m38_property_stress.rs:205: capacity 8 (B1 Hkv2 D16): append 3, reset, append 2."""
+    cache = fa.HipResidentKvCache(hip, 1, 2, 8, 16)
+    src = lambda rows: fa.DeviceBuffer(hip, rows * 2 * 16 * 4)  # noqa: E731
+    assert cache.record_append(src(3), src(3), 3) == 3
+    assert len(cache) == 3 and cache.remaining_capacity() == 5
+    cache.reset()
+    assert cache.is_empty() and cache.remaining_capacity() == 8
+    assert cache.record_append(src(2), src(2), 2) == 2
+    assert len(cache) == 2 and cache.remaining_capacity() == 6
+
+
+def test_m39_every_nonfinite_input_class_is_rejected(hip):
+    """every_nonfinite_input_class_is_rejected tests/m39_host_api_fuzz.rs:158: NaN, +inf and -inf
+    in each of Q, K, V (B1 H1 S1 D1) are NonFiniteInput naming the tensor."""
+    shape = fa.AttentionShape(1, 1, 1, 1)
+    ex = fa.HipFlatAttention(hip)
+    for bad in (np.nan, np.inf, -np.inf):
+        for t, name in enumerate("QKV"):
+            x = [np.zeros(1, np.float32) for _ in range(3)]
+            x[t][0] = bad
+            with pytest.raises(fa.FlatHipError) as e:
+                ex.forward(*x, shape, fa.FlatAttentionConfig())
+            assert e.value.variant == "NonFiniteInput" and name in str(e.value), (bad, name)

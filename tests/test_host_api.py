@@ -563,3 +563,28 @@ def test_graph_calls_need_a_context_and_a_capture():
     assert _variant(lib.fa_graph_capture_end(None, ctypes.byref(h))) == "NullArgument"
     assert _variant(lib.fa_graph_launch(None, None)) == "NullArgument"
     assert lib.fa_graph_destroy(None) == 0
+
+
+def test_m39_overflow_position_and_length_fail_closed():
+    """overflow_position_and_length_fail_closed tests/m39_host_api_fuzz.rs:108: batch or
+    q_heads at usize::MAX and a query position at usize::MAX fail validation (asymmetric shape
+    B1 Hq4 Hkv2 q2 kv3 D8); buffers one element short are BufferTooSmall."""
+    lib = fa.lib()
+    cfg = ctypes.byref(fa.FlatAttentionConfig(True).c())
+    M = 2**64 - 1
+
+    def asym(shape, q_bytes=1 << 30, kv_bytes=1 << 30):
+        sh = fa.AsymmetricGroupedAttentionShape(*shape)
+        return _variant(lib.fa_forward_projection_asymmetric(
+            None, FAKE, q_bytes, FAKE, FAKE, kv_bytes, FAKE, 1 << 30, ctypes.byref(sh.c()), cfg,
+            None, 0, fa.DTYPE_F32))
+
+    valid = (1, 4, 2, 2, 3, 8, 0)
+    for bad in ((M, 4, 2, 2, 3, 8, 0), (1, M, 1, 2, 3, 8, 0)):
+        assert asym(bad) not in ("Ok", "NullArgument"), bad
+    # offset + query_len wraps past 2^64: must still be PositionOverflow
+    assert asym((1, 4, 2, 2, 3, 8, M)) == "PositionOverflow"
+    assert asym((1, 4, 2, 2, 3, 8, M - 1)) == "PositionOverflow"
+    assert asym(valid, q_bytes=4 * 2 * 8 * 4 - 4) == "BufferTooSmall"
+    assert asym(valid, kv_bytes=2 * 3 * 8 * 4 - 4) == "BufferTooSmall"
+    assert asym(valid) == "NullArgument"
