@@ -1138,7 +1138,8 @@ int validate_grouped(uint64_t b, uint64_t hq, uint64_t hkv, uint64_t s, uint64_t
                     "q_heads (%llu) must be exactly divisible by kv_heads (%llu)",
                     (unsigned long long)hq, (unsigned long long)hkv);
     uint64_t t;
-    if (mul_ov(b, hq, &t) || mul_ov(t, s, &t) || mul_ov(t, d, &t))
+    // the byte sizes too (up to 4 bytes per element) must fit, or a buffer check would wrap
+    if (mul_ov(b, hq, &t) || mul_ov(t, s, &t) || mul_ov(t, d, &t) || mul_ov(t, 4, &t))
         return fail(FA_ERR_SHAPE_OVERFLOW, "attention shape overflows the address space");
     if (s > kI32 / std::max<uint64_t>(1, hq / hkv) || b * hkv > kI32)
         return fail(FA_ERR_INDEX_SPACE_EXCEEDED, "attention exceeds the i32 index space at %llu rows",
@@ -2229,10 +2230,14 @@ int validate_decode(const int32_t* block_tables, uint64_t max_pages, const int32
         return fail(FA_ERR_INVALID_ROTARY_THETA,
                     "paged decode RoPE theta must be finite and positive, got %g", (double)theta);
     if (int rc = resolve_scale(cfg, head_dim, scale)) return rc;
-    uint64_t rows;
+    uint64_t rows, x;
     if (mul_ov(page_size, physical_pages, &rows) || rows > kI32 || max_pages > kI32 ||
-        n_seqs * max_pages > (uint64_t)std::numeric_limits<int64_t>::max() / 4)
+        mul_ov(n_seqs, max_pages, &x) || x > (uint64_t)std::numeric_limits<int64_t>::max() / 4)
         return fail(FA_ERR_INDEX_SPACE_EXCEEDED, "paged decode exceeds the i32 index space");
+    // Q, O and pool byte sizes (head_dim <= 128 here, so head_dim * 4 cannot overflow)
+    if (mul_ov(n_seqs, q_heads, &x) || mul_ov(x, head_dim * 4, &x) ||
+        mul_ov(rows, kv_heads, &x) || mul_ov(x, head_dim * 4, &x))
+        return fail(FA_ERR_SHAPE_OVERFLOW, "attention shape overflows the address space");
     uint64_t max_pos = 0;
     std::vector<int32_t>& qpos = *qpos_out;
     qpos.resize(n_seqs);
@@ -2813,9 +2818,11 @@ int fa_chunked_prefill_paged_prepare(fa_ctx* ctx, const int32_t* block_tables, u
     if (int rc = check_head_dim(sh->head_dim, dtype)) return rc;
     float scale;
     if (int rc = resolve_scale(cfg, sh->head_dim, &scale)) return rc;
-    uint64_t rows;
+    uint64_t rows, x;
     if (mul_ov(page_size, physical_pages, &rows) || rows > kI32)
         return fail(FA_ERR_INDEX_SPACE_EXCEEDED, "paged prefill exceeds the i32 index space");
+    if (mul_ov(rows, sh->kv_heads, &x) || mul_ov(x, sh->head_dim * 4, &x))
+        return fail(FA_ERR_SHAPE_OVERFLOW, "attention shape overflows the address space");
     if (int rc = check_pages(block_tables, max_pages, sh->batch, sh->kv_len, nullptr, page_size,
                              physical_pages))
         return rc;
@@ -2920,30 +2927,36 @@ int fa_paged_append_batched(fa_ctx* ctx, const int32_t* block_tables, uint64_t m
     if (head_dim % 8)
         return fail(FA_ERR_UNSUPPORTED_HEAD_DIM, "append needs head_dim %% 8 == 0, got %llu",
                     (unsigned long long)head_dim);
-    uint64_t rows;
-    if (mul_ov(page_size, physical_pages, &rows) || rows > kI32 || max_pages * page_size > kI32)
+    uint64_t rows, cap_tokens, row, src_need, pool_need, x;
+    if (mul_ov(page_size, physical_pages, &rows) || rows > kI32 ||
+        mul_ov(max_pages, page_size, &cap_tokens) || cap_tokens > kI32)
         return fail(FA_ERR_INDEX_SPACE_EXCEEDED, "paged append exceeds the i32 index space");
     std::vector<int32_t> ends(n_seqs);
     for (uint64_t s = 0; s < n_seqs; ++s) {
         if (start_lens[s] < 0)
             return fail(FA_ERR_INDEX_SPACE_EXCEEDED, "negative start length for sequence %llu",
                         (unsigned long long)s);
-        const uint64_t end = (uint64_t)start_lens[s] + append_len;
-        if (end > max_pages * page_size)
+        // start_lens[s] < 2^31 and cap_tokens <= 2^31 - 1: compare without forming a sum that
+        // could wrap
+        if (append_len > cap_tokens || (uint64_t)start_lens[s] > cap_tokens - append_len)
             return fail(FA_ERR_CAPACITY_EXCEEDED,
                         "paged KV append requires %llu tokens, capacity is %llu",
-                        (unsigned long long)end, (unsigned long long)(max_pages * page_size));
-        ends[s] = (int32_t)end;
+                        (unsigned long long)((uint64_t)start_lens[s] + std::min(append_len, cap_tokens + 1)),
+                        (unsigned long long)cap_tokens);
+        ends[s] = (int32_t)((uint64_t)start_lens[s] + append_len);
     }
     if (int rc = check_pages(block_tables, max_pages, n_seqs, 0, ends.data(), page_size,
                              physical_pages))
         return rc;
-    const uint64_t eb = elem_bytes(dtype);
-    const uint64_t row = kv_heads * head_dim * eb;
-    if (int rc = check_buffer("K", k_src, src_bytes, n_seqs * append_len * row)) return rc;
-    if (int rc = check_buffer("V", v_src, src_bytes, n_seqs * append_len * row)) return rc;
-    if (int rc = check_buffer("K pool", k_pool, pool_bytes, rows * row)) return rc;
-    if (int rc = check_buffer("V pool", v_pool, pool_bytes, rows * row)) return rc;
+    // every size product is checked: a wrapped size would pass the buffer checks
+    if (mul_ov(kv_heads, head_dim, &x) || mul_ov(x, elem_bytes(dtype), &row) ||
+        mul_ov(n_seqs, append_len, &x) || mul_ov(x, row, &src_need) ||
+        mul_ov(rows, row, &pool_need))
+        return fail(FA_ERR_SHAPE_OVERFLOW, "paged append shape overflows the address space");
+    if (int rc = check_buffer("K", k_src, src_bytes, src_need)) return rc;
+    if (int rc = check_buffer("V", v_src, src_bytes, src_need)) return rc;
+    if (int rc = check_buffer("K pool", k_pool, pool_bytes, pool_need)) return rc;
+    if (int rc = check_buffer("V pool", v_pool, pool_bytes, pool_need)) return rc;
     if (!ctx) return fail(FA_ERR_NULL_ARGUMENT, "context is null");
     begin_call(ctx);
     if (int rc = set_device(ctx)) return rc;

@@ -588,3 +588,31 @@ def test_m39_overflow_position_and_length_fail_closed():
     assert asym(valid, q_bytes=4 * 2 * 8 * 4 - 4) == "BufferTooSmall"
     assert asym(valid, kv_bytes=2 * 3 * 8 * 4 - 4) == "BufferTooSmall"
     assert asym(valid) == "NullArgument"
+
+
+def test_sizes_near_the_top_of_u64_fail_closed():
+    """Element counts whose byte sizes would wrap past 2^64 (and sums of positions or lengths
+    that would) are rejected before any buffer check could pass on a wrapped size: the
+    fail-closed rule of tests/m39_host_api_fuzz.rs:108 applied to every size product."""
+    lib = fa.lib()
+    # 2^27 * 1 * 2^28 * 128 = 2^62 elements: 2^64 bytes in f32
+    assert _variant(_gqa(fa.GroupedAttentionShape(2**27, 1, 1, 2**28, 128))) == "ShapeOverflow"
+    sh = fa.AsymmetricGroupedAttentionShape(2**27, 1, 1, 1, 2**28, 128, 0)
+    assert _variant(lib.fa_forward_projection_asymmetric(
+        None, FAKE, 1 << 30, FAKE, FAKE, 1 << 30, FAKE, 1 << 30, ctypes.byref(sh.c()),
+        ctypes.byref(fa.FlatAttentionConfig(False).c()), None, 0, fa.DTYPE_F32)) == "ShapeOverflow"
+    # decode: heads whose Q / pool byte sizes wrap
+    assert _decode_prepare([[0, 1, 2]], [40], hq=2**60, hkv=2**60) == "ShapeOverflow"
+    assert _decode_prepare([[0, 1, 2]], [40], hq=2**59, hkv=2**58) == "ShapeOverflow"
+    # append: a length that would wrap the end position, heads that wrap the row size
+    bt = np.array([[0, 1]], np.int32)
+    st = np.array([20], np.int32)
+
+    def app(n=8, hkv=2, D=64):
+        return _variant(lib.fa_paged_append_batched(
+            None, bt.ctypes.data, bt.shape[1], st.ctypes.data, 1, n, 16, 4, hkv, D,
+            FAKE, FAKE, 1 << 30, FAKE, FAKE, 1 << 30, None, fa.DTYPE_BF16))
+    assert app(n=2**64 - 10) == "CapacityExceeded"
+    assert app(n=2**64 - 1) == "CapacityExceeded"
+    assert app(hkv=2**61) == "ShapeOverflow"
+    assert app() == "NullArgument"
