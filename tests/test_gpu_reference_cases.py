@@ -888,3 +888,29 @@ def test_m39_every_nonfinite_input_class_is_rejected(hip):
             with pytest.raises(fa.FlatHipError) as e:
                 ex.forward(*x, shape, fa.FlatAttentionConfig())
             assert e.value.variant == "NonFiniteInput" and name in str(e.value), (bad, name)
+
+
+def test_m19_grouped_backward_public_api_matches_oracle(hip):
+    """grouped_backward_public_api_matches_oracle tests/m19_grouped_backward_api.rs:153:
+    B1 Hq4 Hkv1 S5 D8, causal, scale 0.41; the forward oracle's O and LSE packed with Q, K, V,
+    dO into the Q|K|V|dO|O|LSE contract, one backward encode; 4e-4 + 2e-3|e|."""
+    b, hq, hkv, s, d = 1, 4, 1, 5, 8
+    shape = fa.GroupedAttentionShape(b, hq, hkv, s, d)
+    cfg = fa.FlatAttentionConfig(True, 0.41)
+    fx = _fx(0.067, 0.75, 0.31, 0.25)
+    q, k, v = fx(shape.q_tensor_len(), 0.1), fx(shape.kv_tensor_len(), 0.7), fx(shape.kv_tensor_len(), 1.3)
+    do = fx(shape.q_tensor_len(), 1.9)
+    eo, el = oracle.forward_grouped(q, k, v, b, hq, hkv, s, d, True, scale=0.41)
+    edq, edk, edv = oracle.backward_grouped(q, k, v, do, eo, el, b, hq, hkv, s, d, True, scale=0.41)
+    pipe = fa.HipGroupedBackwardRecomputePipeline(hip)
+    packed = fa.DeviceBuffer.from_array(
+        hip, fa.pack_grouped_backward_recompute_inputs(q, k, v, do, fa.FlatAttentionOutput(eo, el),
+                                                       shape))
+    grads = pipe.create_gradient_buffer(shape)
+    lay = pipe.encode(packed, grads, shape, cfg)
+    assert lay.kv_elements == b * hkv * s * d  # native KV-head cardinality
+    g = grads.download(np.float32, lay.gradient_bytes // 4)
+    for name, off, n, e in (("dQ", lay.dq_offset, lay.q_elements, edq),
+                            ("dK", lay.dk_offset, lay.kv_elements, edk),
+                            ("dV", lay.dv_offset, lay.kv_elements, edv)):
+        assert_close(name, g[off // 4:][:n], e, 4e-4, 2e-3)
