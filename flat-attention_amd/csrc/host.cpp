@@ -2819,7 +2819,8 @@ int fa_chunked_prefill_paged_prepare(fa_ctx* ctx, const int32_t* block_tables, u
     float scale;
     if (int rc = resolve_scale(cfg, sh->head_dim, &scale)) return rc;
     uint64_t rows, x;
-    if (mul_ov(page_size, physical_pages, &rows) || rows > kI32)
+    if (mul_ov(page_size, physical_pages, &rows) || rows > kI32 || max_pages > kI32 ||
+        mul_ov(sh->batch, max_pages, &x) || x > kI32)
         return fail(FA_ERR_INDEX_SPACE_EXCEEDED, "paged prefill exceeds the i32 index space");
     if (mul_ov(rows, sh->kv_heads, &x) || mul_ov(x, sh->head_dim * 4, &x))
         return fail(FA_ERR_SHAPE_OVERFLOW, "attention shape overflows the address space");
