@@ -19,6 +19,7 @@ from .api import (AsymmetricGroupedAttentionShape, AsymmetricRotaryEmbeddingConf
                   VariableLengthRotaryEmbeddingConfig, VariableLengthSequenceMetadata,
                   FlatAttentionBackwardOutput, GroupedBackwardRecomputeLayout,
                   HipGroupedBackwardRecomputePipeline, PreparedGroupedBackwardRecompute,
+                  PreparedGroupedForward,
                   grouped_backward_layout, pack_grouped_backward_recompute_inputs,
                   HipBackwardRecomputePipeline, pack_backward_recompute_inputs,
                   bf16_bits_to_f32, download_attention,

@@ -616,3 +616,14 @@ def test_sizes_near_the_top_of_u64_fail_closed():
     assert app(n=2**64 - 1) == "CapacityExceeded"
     assert app(hkv=2**61) == "ShapeOverflow"
     assert app() == "NullArgument"
+
+
+def test_prepared_and_pipeline_types_are_publicly_nameable():
+    """prepared_grouped_forward_type_is_publicly_nameable
+    tests/m44_prepared_grouped_public_api.rs:6: the prepared forward (and the other pipeline
+    types a caller names in signatures) are exported at the package top level."""
+    for name in ("PreparedGroupedForward", "PreparedGroupedBackwardRecompute", "HipGraph",
+                 "HipRotaryGroupedAttention", "HipAsymmetricProjectionPipeline",
+                 "HipProjectionRotaryGroupedPipeline", "HipResidentDecodePipeline",
+                 "HipPagedDecodePipeline", "PagedDecodePlan", "PagedChunkedPrefillPlan"):
+        assert isinstance(getattr(fa, name), type), name
