@@ -175,6 +175,7 @@ def _m48_fixture(n, phase):
     (2, 8, 2, 300, 64, 120, 40, True),     # causal and RoPE positions differ
     (2, 12, 2, 33, 32, 0, 5, False),
     (1, 4, 2, 9, 6, 8, 8, True),           # f32 head_dim 6: the prefill-kernel route
+    (1, 16, 4, 8192, 64, 8191, 8191, True),  # the published M48 shape (bench line)
 ])
 def test_m48_decode_kv_reuse_matches_oracle(hip, dtype, batch, hq, hkv, kv_len, D, causal_pos,
                                             q_rope, causal):
