@@ -632,20 +632,20 @@ def main():
               file=sys.stderr)
         sys.exit(2)
 
-    rng = np.random.default_rng(1234)
-    ctx = fa.HipContext(0)
     if args.ceilings:
-        res = {"mfma_bf16_tflops": {"random": round(ctx.mfma_ceiling(False), 1),
-                                    "constant": round(ctx.mfma_ceiling(True), 1),
+        from flat_attention_amd import diag
+        res = {"mfma_bf16_tflops": {"random": round(diag.mfma_ceiling(0, False), 1),
+                                    "constant": round(diag.mfma_ceiling(0, True), 1),
                                     "spec": PEAK_BF16_TFLOPS},
-               "mfma_f32_tflops": {"random": round(ctx.mfma_ceiling(False, fa.DTYPE_F32), 1),
-                                   "constant": round(ctx.mfma_ceiling(True, fa.DTYPE_F32), 1),
+               "mfma_f32_tflops": {"random": round(diag.mfma_ceiling(0, False, diag.DTYPE_F32), 1),
+                                   "constant": round(diag.mfma_ceiling(0, True, diag.DTYPE_F32), 1),
                                    "spec": PEAK_F32_TFLOPS},
-               "stream_read_tbps": {str(d): round(ctx.stream_read(d), 3) for d in (4, 8, 16)},
+               "stream_read_tbps": {str(d): round(diag.stream_read(0, d), 3) for d in (4, 8, 16)},
                "hbm_spec_tbps": PEAK_HBM_GBS / 1000.0}
         print(json.dumps(res))
-        ctx.close()
         return
+    rng = np.random.default_rng(1234)
+    ctx = fa.HipContext(0)
     if args.only == "backward":
         ctx.set_backward_policy(args.backward_policy)
         out = measure_backward(ctx, rng, args.steps, args.warmup, args.data)

@@ -224,7 +224,7 @@ struct fa_ctx {
     // context is created), a host staging area for its metadata and the event that marks the
     // last copy out of that area
     void* na_scratch = nullptr;
-    std::vector<int32_t> na_host;
+    int32_t* na_host = nullptr;  // pinned, kNoAllocMetaBytes
     hipEvent_t na_copied = nullptr;
     bool na_pending = false;
     struct Timed {
@@ -552,7 +552,9 @@ int fa_ctx_create(int device, fa_ctx** out) {
     if (fa::noalloc_scratch(device, &ctx->na_scratch) != hipSuccess) ctx->na_scratch = nullptr;
     if (hipEventCreateWithFlags(&ctx->na_copied, hipEventDisableTiming) != hipSuccess)
         ctx->na_copied = nullptr;
-    ctx->na_host.resize(kNoAllocMetaBytes / sizeof(int32_t));
+    if (hipHostMalloc((void**)&ctx->na_host, kNoAllocMetaBytes, hipHostMallocDefault) !=
+        hipSuccess)
+        ctx->na_host = nullptr;
     *out = ctx;
     return ok();
 }
@@ -578,6 +580,7 @@ int fa_ctx_destroy(fa_ctx* ctx) {
     }
     if (ctx->open_begin) (void)hipEventDestroy(ctx->open_begin);
     if (ctx->na_copied) (void)hipEventDestroy(ctx->na_copied);
+    if (ctx->na_host) (void)hipHostFree(ctx->na_host);
     for (hipEvent_t e : ctx->free_events) (void)hipEventDestroy(e);
     (void)hipStreamDestroy(ctx->stream);
     delete ctx;
@@ -617,87 +620,6 @@ int fa_ctx_set_kernel_timing(fa_ctx* ctx, int32_t enable) {
     ctx->timed.clear();
     ctx->timing = enable != 0;
     ctx->timing_paused = false;
-    return ok();
-}
-
-// ------------------------------------------------------------------ measurement aids
-extern "C++" {
-namespace {
-// ms per call of `run` on the context's stream: `warm` untimed calls, then `reps` timed ones.
-template <typename F>
-int time_calls(fa_ctx* ctx, int warm, int reps, F run, double* ms) {
-    for (int i = 0; i < warm; ++i) run();
-    hipEvent_t e0 = nullptr, e1 = nullptr;
-    HIP_TRY(hipEventCreate(&e0));
-    HIP_TRY(hipEventCreate(&e1));
-    HIP_TRY(hipEventRecord(e0, ctx->stream));
-    for (int i = 0; i < reps; ++i) run();
-    HIP_TRY(hipEventRecord(e1, ctx->stream));
-    HIP_TRY(hipEventSynchronize(e1));
-    float t = 0.0f;
-    HIP_TRY(hipEventElapsedTime(&t, e0, e1));
-    (void)hipEventDestroy(e0);
-    (void)hipEventDestroy(e1);
-    HIP_TRY(hipGetLastError());
-    *ms = (double)t / reps;
-    return FA_OK;
-}
-}  // namespace
-}  // extern "C++"
-
-int fa_diag_mfma_ceiling(fa_ctx* ctx, int32_t dtype, int32_t constant_operands, double* tflops) {
-    if (!ctx || !tflops) return fail(FA_ERR_NULL_ARGUMENT, "null argument");
-    if (dtype != FA_DTYPE_BF16 && dtype != FA_DTYPE_F32)
-        return fail(FA_ERR_UNSUPPORTED_DTYPE, "the MFMA ceiling probe runs bf16 or f32");
-    if (int rc = set_device(ctx)) return rc;
-    const bool f32 = dtype == FA_DTYPE_F32;
-    // ~2.5 ms per launch on 256 CUs either way (an f32 32x32x2 MFMA takes twice the bf16 one's
-    // cycles for 1/8 of its work)
-    constexpr int kBlocks = 2048;
-    const int iters = f32 ? 500 : 4000;
-    float* out = nullptr;
-    HIP_TRY(hipMalloc(&out, (size_t)kBlocks * 256 * sizeof(float)));
-    double ms = 0.0;
-    // 400 untimed launches (~1 s: the clock settles under sustained load), 200 timed (~0.5 s)
-    const int rc = time_calls(ctx, 400, 200, [&] {
-        fa::launch_mfma_ceiling(f32, out, kBlocks, iters, constant_operands != 0, ctx->stream);
-    }, &ms);
-    (void)hipStreamSynchronize(ctx->stream);
-    (void)hipFree(out);
-    if (rc) return rc;
-    const double per_chain = f32 ? 4.0 * 4096.0 : 32768.0;
-    const double flop = (double)kBlocks * 4 /* waves */ * iters * 4 /* chains */ * per_chain;
-    *tflops = flop / (ms * 1e-3) / 1e12;
-    return ok();
-}
-
-int fa_diag_stream_read(fa_ctx* ctx, int32_t loads_in_flight, double* tbps) {
-    if (!ctx || !tbps) return fail(FA_ERR_NULL_ARGUMENT, "null argument");
-    if (loads_in_flight != 4 && loads_in_flight != 8 && loads_in_flight != 16)
-        return fail(FA_ERR_UNAVAILABLE, "loads_in_flight must be 4, 8 or 16");
-    if (int rc = set_device(ctx)) return rc;
-    int cus = 0;
-    HIP_TRY(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, ctx->device));
-    constexpr size_t kBytes = (size_t)4 << 30;  // 4 GiB, far beyond every cache level
-    void* buf = nullptr;
-    uint32_t* out = nullptr;
-    HIP_TRY(hipMalloc(&buf, kBytes));
-    if (hipMalloc(&out, (size_t)cus * 512 * sizeof(uint32_t)) != hipSuccess) {
-        (void)hipFree(buf);
-        return fail(FA_ERR_HIP, "hipMalloc failed");
-    }
-    double ms = 0.0;
-    // one workgroup of 8 waves per CU (the decode's occupancy), 100 untimed and 200 timed
-    // passes (~0.2 s at 7 TB/s)
-    const int rc = time_calls(ctx, 100, 200, [&] {
-        fa::launch_stream_read(buf, (int64_t)(kBytes >> 15), loads_in_flight, cus, out,
-                               ctx->stream);
-    }, &ms);
-    (void)hipStreamSynchronize(ctx->stream);
-    (void)hipFree(out);
-    (void)hipFree(buf);
-    if (rc) return rc;
-    *tbps = (double)kBytes / (ms * 1e-3) / 1e12;
     return ok();
 }
 
@@ -2405,6 +2327,12 @@ int enqueue_decode(fa_ctx* ctx, const fa_decode_plan* p, const float2* table, co
     return FA_OK;
 }
 
+// The enqueue half of fa_paged_decode_noalloc, run while the device's scratch is held.
+int noalloc_enqueue(fa_ctx* ctx, uint8_t* base, const int32_t* h, uint64_t meta_ints,
+                    uint64_t n_bt, uint64_t n_seqs, uint64_t rope_bytes, uint64_t part_bytes,
+                    float theta, uint64_t head_dim, fa_decode_plan* pp, const void* q,
+                    const void* k_pool, const void* v_pool, void* out_lse,
+                    const fa_packed_layout& lay);
 
 }  // namespace
 
@@ -2456,8 +2384,11 @@ int fa_paged_decode_noalloc(fa_ctx* ctx, const int32_t* block_tables, uint64_t m
     if (int rc = check_buffer("O|LSE", out_lse, out_bytes, lay.combined_bytes)) return rc;
     if (!ctx) return fail(FA_ERR_NULL_ARGUMENT, "context is null");
     begin_call(ctx);
+    // the metadata is copied from a host staging area that the next call rewrites: a graph
+    // replay would read whatever that area holds by then
+    if (int rc = refuse_in_capture(ctx, "host upload")) return rc;
     if (int rc = set_device(ctx)) return rc;
-    if (!ctx->na_scratch || !ctx->na_copied)
+    if (!ctx->na_scratch || !ctx->na_copied || !ctx->na_host)
         return fail(FA_ERR_HIP, "the static decode scratch of device %d is not addressable",
                     ctx->device);
 
@@ -2503,13 +2434,35 @@ int fa_paged_decode_noalloc(fa_ctx* ctx, const int32_t* block_tables, uint64_t m
         HIP_TRY(hipEventSynchronize(ctx->na_copied));
         ctx->na_pending = false;
     }
-    int32_t* h = ctx->na_host.data();
+    int32_t* h = ctx->na_host;
     memcpy(h, block_tables, n_bt * 4);
     memcpy(h + n_bt, ctx_lens, n_seqs * 4);
     memcpy(h + n_bt + n_seqs, qpos.data(), n_seqs * 4);
     for (uint64_t s = 0; s < n_seqs; ++s) h[n_bt + 2 * n_seqs + s] = (int32_t)s;
     memcpy(h + n_bt + 3 * n_seqs, work.data(), work.size() * 4);
     uint8_t* base = (uint8_t*)ctx->na_scratch;
+    // Every context on this device shares the scratch: wait (on the GPU) for the previous
+    // user's kernels before overwriting it, and publish this call's completion afterwards.
+    if (hipError_t e = fa::noalloc_order_begin(ctx->device, ctx->stream))
+        return fail(FA_ERR_HIP, "ordering the shared decode scratch: %s", hipGetErrorString(e));
+    const int rc = noalloc_enqueue(ctx, base, h, meta_ints, n_bt, n_seqs, rope_bytes, part_bytes,
+                                   theta, head_dim, &p, q, k_pool, v_pool, out_lse, lay);
+    const hipError_t e = fa::noalloc_order_end(ctx->device, ctx->stream, true);
+    if (rc) return rc;
+    if (e != hipSuccess)
+        return fail(FA_ERR_HIP, "ordering the shared decode scratch: %s", hipGetErrorString(e));
+    return ok();
+}
+
+}  // extern "C"
+
+namespace {
+int noalloc_enqueue(fa_ctx* ctx, uint8_t* base, const int32_t* h, uint64_t meta_ints,
+                    uint64_t n_bt, uint64_t n_seqs, uint64_t rope_bytes, uint64_t part_bytes,
+                    float theta, uint64_t head_dim, fa_decode_plan* pp, const void* q,
+                    const void* k_pool, const void* v_pool, void* out_lse,
+                    const fa_packed_layout& lay) {
+    fa_decode_plan& p = *pp;
     HIP_TRY(hipMemcpyAsync(base, h, meta_ints * 4, hipMemcpyHostToDevice, ctx->stream));
     HIP_TRY(hipEventRecord(ctx->na_copied, ctx->stream));
     ctx->na_pending = true;
@@ -2530,8 +2483,11 @@ int fa_paged_decode_noalloc(fa_ctx* ctx, const int32_t* block_tables, uint64_t m
     end_span(ctx, FA_KERNEL_ROPE_TABLE);
     HIP_TRY(hipGetLastError());
     if (int rc = enqueue_decode(ctx, &p, table, q, k_pool, v_pool, out_lse, lay)) return rc;
-    return ok();
+    return FA_OK;
 }
+}  // namespace
+
+extern "C" {
 
 int fa_paged_cache_decode(fa_ctx* ctx, const fa_paged_cache* c, const void* q, size_t q_bytes,
                           uint64_t q_heads, const fa_config* cfg, float theta,
@@ -2764,6 +2720,17 @@ int fa_forward_projection_asymmetric_decode_kv_reuse(fa_ctx* ctx, const void* q,
     fa_config nc{};
     if (cfg) nc = *cfg;
     nc.causal = 0;  // applied above as the live length
+    // Each batch element is one page of kv_len rows. The per-token path goes through the
+    // allocation-free decode (no plan to allocate, upload into and tear down per token); a shape
+    // whose work lists or partials exceed its static scratch takes a one-call plan instead,
+    // which allocates and waits for the stream when it is destroyed.
+    {
+        const int rc = fa_paged_decode_noalloc(
+            ctx, table.data(), 1, lens.data(), qpos.data(), sh->batch, sh->kv_len, sh->batch,
+            sh->q_heads, sh->kv_heads, sh->head_dim, &nc, rot->theta, dtype, q, q_bytes, k, v,
+            kv_bytes, out_lse, out_bytes);
+        if (rc != FA_ERR_SCRATCH_EXCEEDED) return rc;
+    }
     fa_decode_plan* p = nullptr;
     if (int rc = fa_paged_decode_prepare(ctx, table.data(), 1, lens.data(), qpos.data(), sh->batch,
                                          sh->kv_len, sh->batch, sh->q_heads, sh->kv_heads,

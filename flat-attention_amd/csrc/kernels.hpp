@@ -137,17 +137,16 @@ void launch_rope_table(float2* table, const RopeFreqs& f, int rows, int half, hi
 void launch_rope_rows(float2* table, const RopeFreqs& f, const int* positions, int n, int half,
                       hipStream_t s);
 
-// Measurement aids: a pure MFMA stream (bf16 or f32, random or constant operands) and a streaming read
-// of `n_chunks` 32 KiB chunks with `depth` (4, 8 or 16) loads in flight per lane.
-void launch_mfma_ceiling(bool f32, float* out, int blocks, int iters, int constant,
-                         hipStream_t s);
-void launch_stream_read(const void* buf, int64_t n_chunks, int depth, int blocks, uint32_t* out,
-                        hipStream_t s);
-
 // Allocation-free paged decode: size of the per-device static scratch array and its device
 // address (resolved once per device with hipGetSymbolAddress; never the array's host-side name).
 constexpr size_t kNoAllocScratchBytes = (size_t)64 << 20;
 hipError_t noalloc_scratch(int device, void** out);
+// Orders every use of a device's scratch across streams and contexts: begin locks the device's
+// mutex and makes `s` wait (on the GPU) for the previous user's completion event; end records
+// this call's completion into that event (when it enqueued work) and unlocks. Every begin that
+// returns hipSuccess is paired with one end.
+hipError_t noalloc_order_begin(int device, hipStream_t s);
+hipError_t noalloc_order_end(int device, hipStream_t s, bool enqueued);
 
 // Scatter `append_len` rows per sequence into the page pool, optionally rotating K rows.
 struct AppendArgs {

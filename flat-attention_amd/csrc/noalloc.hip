@@ -16,7 +16,31 @@ namespace {
 constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mu;
 void* g_scratch_ptr[kMaxDevices] = {};
+// Calls on one device are ordered through the scratch: each call holds the device's mutex
+// while it enqueues, makes its stream wait for the event the previous user recorded, and
+// records its own completion into that event. Stream-ordered, no host wait, no allocation.
+std::mutex g_order_mu[kMaxDevices];
+hipEvent_t g_last_user[kMaxDevices] = {};
 }  // namespace
+
+hipError_t noalloc_order_begin(int device, hipStream_t s) {
+    if (device < 0 || device >= kMaxDevices) return hipErrorInvalidDevice;
+    g_order_mu[device].lock();
+    hipError_t e = hipSuccess;
+    if (!g_last_user[device])
+        e = hipEventCreateWithFlags(&g_last_user[device], hipEventDisableTiming);
+    else
+        e = hipStreamWaitEvent(s, g_last_user[device], 0);
+    if (e != hipSuccess) g_order_mu[device].unlock();
+    return e;
+}
+
+hipError_t noalloc_order_end(int device, hipStream_t s, bool enqueued) {
+    hipError_t e = hipSuccess;
+    if (enqueued) e = hipEventRecord(g_last_user[device], s);
+    g_order_mu[device].unlock();
+    return e;
+}
 
 hipError_t noalloc_scratch(int device, void** out) {
     *out = nullptr;

@@ -9,9 +9,7 @@ import ctypes
 import os
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-# FLAT_HIP_LIBRARY selects another build of the same library (kernel experiments); the default
-# is the in-tree build.
-LIB_PATH = os.environ.get("FLAT_HIP_LIBRARY") or os.path.join(_HERE, "libflat_hip.so")
+LIB_PATH = os.path.join(_HERE, "libflat_hip.so")
 
 U64 = ctypes.c_uint64
 I32 = ctypes.c_int32
@@ -223,8 +221,6 @@ PROTOTYPES = {
     "fa_device_record": (INT, [ctypes.c_char_p, ctypes.c_char_p, I32, I32, I32, ctypes.c_uint64,
                                ctypes.c_char_p, ctypes.c_size_t,
                                ctypes.POINTER(ctypes.c_uint64)]),
-    "fa_diag_mfma_ceiling": (INT, [VP, I32, I32, ctypes.POINTER(ctypes.c_double)]),
-    "fa_diag_stream_read": (INT, [VP, I32, ctypes.POINTER(ctypes.c_double)]),
     "fa_ctx_kernel_timing": (INT, [VP, I32, P(ctypes.c_double), P(U64)]),
     "fa_ctx_kernel_timing_range": (INT, [VP, I32, P(ctypes.c_double), P(ctypes.c_double)]),
 }

@@ -276,20 +276,6 @@ class HipContext:
         workgroups; read when a PagedDecodePlan is prepared."""
         check(lib().fa_ctx_set_decode_policy(self.handle, grouped))
 
-    def mfma_ceiling(self, constant_operands: bool = False, dtype: int = L.DTYPE_BF16) -> float:
-        """TFLOP/s of a pure MFMA stream (bf16 32x32x16 or f32 32x32x2; random or constant
-        operands), measured after the clock settles (~1.5 s)."""
-        out = ctypes.c_double()
-        check(lib().fa_diag_mfma_ceiling(self.handle, dtype, int(constant_operands),
-                                         ctypes.byref(out)))
-        return out.value
-
-    def stream_read(self, loads_in_flight: int = 8) -> float:
-        """TB/s of non-temporal 16-byte streaming reads of a 4 GiB buffer."""
-        out = ctypes.c_double()
-        check(lib().fa_diag_stream_read(self.handle, loads_in_flight, ctypes.byref(out)))
-        return out.value
-
     def set_backward_policy(self, store_ds: int):
         """-1 automatic (16-bit storage: bwd_dkdv stores dS and dQ = dS K reads it back when the
         workspace fits in 2 GiB), 0 dQ recomputes S and dP."""
@@ -926,7 +912,8 @@ def paged_decode_noalloc(ctx: HipContext, block_tables: np.ndarray, ctx_lens: np
                          q_positions: Optional[np.ndarray] = None) -> PackedLayout:
     """Allocation-free batched paged decode (no reference counterpart): PagedDecodePlan's
     prepare + launch in one call whose device state lives in the library's static per-device
-    scratch. Calls that overlap on one GPU race."""
+    scratch. Calls from different contexts on one GPU are ordered on the GPU (each waits for the
+    previous user's kernels); refused while the context's stream is being captured."""
     bt = np.ascontiguousarray(block_tables, np.int32)
     cl = np.ascontiguousarray(ctx_lens, np.int32)
     qp = None if q_positions is None else np.ascontiguousarray(q_positions, np.int32)

@@ -274,8 +274,11 @@ int fa_forward_projection_asymmetric(fa_ctx* ctx, const void* q, size_t q_bytes,
  * group. Fails with FA_ERR_UNSUPPORTED_CANDIDATE_SHAPE unless query_len == 1 and
  * q_heads / kv_heads >= 2, then checks as fa_forward_projection_asymmetric. Q is rotated at
  * rotary->query_position_offset; causal masking keeps keys <= shape->query_position_offset.
- * Output [O | LSE] as for fa_forward_projection_asymmetric. Prepares, launches and releases a
- * decode plan (waits for the stream when releasing). */
+ * Output [O | LSE] as for fa_forward_projection_asymmetric. Runs through the allocation-free
+ * decode (fa_paged_decode_noalloc, each batch element one page of kv_len rows): no allocation
+ * and no wait for the stream per token. A shape whose work lists or partials exceed that
+ * scratch prepares, launches and releases a one-call decode plan instead (allocates, and waits
+ * for the stream when releasing it). Refused with FA_ERR_GRAPH_CAPTURE while capturing. */
 int fa_forward_projection_asymmetric_decode_kv_reuse(fa_ctx* ctx, const void* q, size_t q_bytes,
                                                      const void* k, const void* v,
                                                      size_t kv_bytes, void* out_lse,
@@ -379,8 +382,11 @@ int fa_paged_decode_plan_set_split(fa_ctx* ctx, fa_decode_plan* plan, uint64_t s
  * GPU holds until the process ends. A call needing more fails with FA_ERR_SCRATCH_EXCEEDED
  * before any device work. The metadata reaches the scratch by a stream-ordered copy from a
  * host area owned by the context; a call waits only until the previous call's copy has left
- * that area. Every call on one GPU shares that GPU's scratch: calls that overlap on one GPU
- * (other contexts, other streams) race. */
+ * that area. Every call on one GPU shares that GPU's scratch; calls from different contexts
+ * (streams) are ordered on the GPU: each call makes its stream wait for the event the previous
+ * call on that GPU recorded after its kernels, and records its own (no host wait, no
+ * allocation). Refused with FA_ERR_GRAPH_CAPTURE while the context's stream is captured (the
+ * metadata copy would read a host area that later calls rewrite). */
 int fa_paged_decode_noalloc(fa_ctx* ctx, const int32_t* block_tables, uint64_t max_pages,
                             const int32_t* ctx_lens, const int32_t* q_positions, uint64_t n_seqs,
                             uint64_t page_size, uint64_t physical_pages, uint64_t q_heads,
@@ -599,16 +605,6 @@ int fa_kernel_variant_for_shape(fa_ctx* ctx, uint64_t head_dim, int32_t has_rope
 int fa_device_record(const char* name, const char* arch, int32_t driver, int32_t cus,
                      int32_t clock_khz, uint64_t mem_bytes, char* out, size_t cap,
                      uint64_t* fingerprint);
-
-/* Measurement aids (no counterpart in the reference): the practical ceilings the rooflines are
- * read against. fa_diag_mfma_ceiling runs back-to-back v_mfma_f32_32x32x16_bf16 (dtype
- * FA_DTYPE_BF16) or v_mfma_f32_32x32x2_f32 (FA_DTYPE_F32) on register operands (random
- * attention-like values, or a constant 0.5 when constant_operands != 0) for ~1.5 s (1 s
- * untimed, so the clock settles) and returns the rate in TFLOP/s. fa_diag_stream_read streams a 4 GiB buffer with
- * non-temporal 16-byte loads, loads_in_flight (4, 8 or 16) per lane, one 8-wave workgroup per
- * CU, and returns TB/s. Both allocate (and free) their own buffers and synchronize. */
-int fa_diag_mfma_ceiling(fa_ctx* ctx, int32_t dtype, int32_t constant_operands, double* tflops);
-int fa_diag_stream_read(fa_ctx* ctx, int32_t loads_in_flight, double* tbps);
 
 /* Per-kernel device timing (extends runtime_telemetry src/wgpu_backend.rs:374, which carries no
  * durations). While enabled, every dispatch the context issues is bracketed by HIP events on

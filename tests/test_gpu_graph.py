@@ -90,9 +90,18 @@ def test_capture_refuses_allocation_upload_fill_and_wait(hip):
         q = ex.upload(normal(shape.q_tensor_len(), 1))
         kv = ex.upload(normal(shape.kv_tensor_len(), 2))
         out = fa.DeviceBuffer(fresh, ex.layout(shape).combined_bytes)
+        bt = np.zeros((1, 1), np.int32)
+        lens = np.array([16], np.int32)
+        dq = fa.DeviceBuffer(fresh, 4 * 64 * 2)
+        dkv = fa.DeviceBuffer(fresh, 16 * 2 * 64 * 2)
+        dout = fa.DeviceBuffer(fresh, fa.packed_layout(4 * 64, 4, fa.DTYPE_BF16).combined_bytes)
         with fresh.capture() as cap:
             for call in (lambda: buf.fill_u32(0),
                          lambda: hip_sync(fresh),
+                         # the allocation-free decode copies its metadata from a host area
+                         lambda: fa.paged_decode_noalloc(fresh, bt, lens, 16, 1, 4, 2, 64,
+                                                         fa.FlatAttentionConfig(True), 1e4,
+                                                         fa.DTYPE_BF16, dq, dkv, dkv, dout),
                          # cold context: the RoPE table and K workspace would be allocated
                          lambda: ex.forward_resident(q, kv, kv, shape, fa.FlatAttentionConfig(True),
                                                      fa.RotaryEmbeddingConfig(1e4, 0), out)):

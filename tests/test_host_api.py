@@ -425,12 +425,17 @@ def test_mha_backward_layout_and_validation():
 
 
 def test_diagnostic_probes_validate_arguments():
-    """fa_diag_mfma_ceiling / fa_diag_stream_read reject a null context or output and an
-    unsupported number of loads in flight before touching a device."""
-    lib = fa.lib()
+    """The measurement aids live in their own library (libflat_diag.so): they reject a null
+    output, an unknown dtype and an unsupported number of loads in flight before touching a
+    device, and the attention library exports none of them."""
+    from flat_attention_amd import diag
+    lib = diag.lib()
     out = ctypes.c_double()
-    assert lib.fa_diag_mfma_ceiling(None, 3, 0, ctypes.byref(out)) == 50  # NullArgument
-    assert lib.fa_diag_stream_read(None, 8, ctypes.byref(out)) == 50
+    assert lib.fad_mfma_ceiling(0, 2, 0, None) == 50  # NullArgument
+    assert lib.fad_mfma_ceiling(0, 3, 0, ctypes.byref(out)) == 29  # UnsupportedDtype
+    assert lib.fad_stream_read(0, 5, ctypes.byref(out)) == 20  # Unavailable
+    assert lib.fad_stream_read(0, 8, None) == 50
+    assert not hasattr(fa.lib(), "fa_diag_mfma_ceiling")
 
 
 # --------------------------------------------------------------------------- contract fuzz

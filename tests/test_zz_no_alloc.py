@@ -103,3 +103,46 @@ def test_noalloc_decode_rejects_oversized_metadata_before_device_work(hip):
     assert e.value.variant == "ScratchExceeded"
     a, b, _, _ = _both(hip, [100, 250], ps, hq, hkv, D, fa.DTYPE_BF16, 13)
     _assert_identical(a, b)
+
+
+def test_noalloc_decode_two_contexts_interleaved(hip):
+    """Two contexts (two streams) on one GPU share the device's scratch. Calls issued back to
+    back from both, with no host synchronisation between them, are ordered on the GPU by the
+    scratch's last-user event: each output is bitwise equal to the prepared decode's."""
+    other = fa.HipContext(0)
+    try:
+        cases = []
+        for i, (lens, hq, hkv, D) in enumerate(
+                [([3000, 17, 4100, 700, 5000, 2049], 32, 8, 128), ([33, 900, 16], 8, 2, 64),
+                 ([8000, 512, 1], 32, 8, 128), ([65, 4000], 16, 4, 128)]):
+            rng = np.random.default_rng(70 + i)
+            bt, kp, vp, total = _pool(rng, lens, 16, hkv, D, bf16_round, 70 + i)
+            cl = np.asarray(lens, np.int32)
+            q = bf16_round(normal(len(lens) * hq * D, 80 + i))
+            cfg = fa.FlatAttentionConfig(True)
+            ctx = hip if i % 2 == 0 else other
+            qb, kb, vb = (fa.DeviceBuffer.from_array(ctx, fa.host_storage(x, fa.DTYPE_BF16))
+                          for x in (q, kp, vp))
+            plan = fa.PagedDecodePlan(hip, bt, cl, 16, total, hq, hkv, D, cfg, 1e4, fa.DTYPE_BF16)
+            lay = plan.layout()
+            ref = fa.DeviceBuffer(hip, lay.combined_bytes)
+            q_ref, k_ref, v_ref = (fa.DeviceBuffer.from_array(hip, fa.host_storage(x, fa.DTYPE_BF16))
+                                   for x in (q, kp, vp))
+            plan.launch(q_ref, k_ref, v_ref, ref)
+            got = fa.DeviceBuffer(ctx, lay.combined_bytes)
+            got.fill_u32(0x7FC00003)
+            cases.append((ctx, bt, cl, total, hq, hkv, D, cfg, qb, kb, vb, got, ref, lay))
+        hip.synchronize()
+        other.synchronize()
+        for _ in range(3):  # interleaved, no host wait between the calls
+            for (ctx, bt, cl, total, hq, hkv, D, cfg, qb, kb, vb, got, ref, lay) in cases:
+                fa.paged_decode_noalloc(ctx, bt, cl, 16, total, hq, hkv, D, cfg, 1e4,
+                                        fa.DTYPE_BF16, qb, kb, vb, got)
+        for n, (ctx, *_, got, ref, lay) in enumerate(cases):
+            a = ref.download(np.uint8, lay.combined_bytes)
+            b = got.download(np.uint8, lay.combined_bytes)
+            print(f"two-context case {n}", flush=True)
+            _assert_identical(a, b)
+    finally:
+        other.synchronize()
+        other.close()
