@@ -593,6 +593,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--prefill-v-layout", type=int, default=0,
                     help="1: transposed-V pre-pass for the 16-bit prefill (fa_ctx_set_prefill_v_layout)")
+    ap.add_argument("--prefill-kernel", type=int, default=-1,
+                    help="-1 auto (assembly main loop where it applies), 0 HIP kernels only "
+                         "(fa_ctx_set_prefill_kernel)")
     ap.add_argument("--prefill-policy", type=int, default=-1,
                     help="-1 auto, 0 rotate K on load, 1 pre-rotate K")
     ap.add_argument("--only", choices=["prefill", "decode", "backward"], default=None,
@@ -661,6 +664,7 @@ def main():
         ctx.close()
         return
     ctx.set_prefill_policy(args.prefill_policy)
+    ctx.set_prefill_kernel(args.prefill_kernel)
     ctx.set_prefill_v_layout(args.prefill_v_layout)
     ev = HipEvents()
     stream = ctx.stream

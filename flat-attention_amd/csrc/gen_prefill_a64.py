@@ -1,0 +1,1455 @@
+#!/usr/bin/env python3
+"""Generates the gfx950 assembly of the 16-bit prefill kernel `fa_prefill_a64` (64 query rows per
+wave, one wave per SIMD) and the header that fixes its kernel-argument layout.
+
+Usage: gen_prefill_a64.py OUT.s OUT_ARGS.h
+
+Why assembly: a wave that holds 64 query rows keeps O^T (128 accumulators) and the rotated Q^T
+operands (64 registers) resident in AGPRs, the scores of two 32-key half-tiles in VGPRs, and reads
+every K and V^T operand once for two MFMAs (half the LDS bytes per MFMA of a 32-row wave). The
+compiler cannot hold that register layout (it moves accumulators through VGPRs), so the kernel is
+written here, with every register fixed and the instruction order chosen by the schedule below.
+
+Math (forward_reference, src/lib.rs:454-520; RoPE rotated_pair, src/rotary_grouped.rs:37-50):
+online softmax with running max m, running sum l, O accumulated with rescale alpha =
+exp2((m_old - m_new) * scale * log2 e), LSE = m * scale + ln l. The running max only moves when a
+half-tile's max exceeds it by more than 2^8 (in exp2 units): probabilities stay <= 2^8 and O, l
+stay consistent, so the final O / l and LSE are exact either way.
+
+Layout of the work (per workgroup of 4 waves = 256 query rows of one (batch, kv head)):
+  row = t * group + head   (every query head of a GQA group shares each K/V tile)
+  wave w holds rows r0 + 64 w .. +63 as two 32-row blocks rb = 0, 1; lane l holds row l % 32
+  of each block; g = l / 32 selects which 8 of every 16 keys (dims) the lane supplies.
+Per 32-key half-tile h (the pipeline unit):
+  S^T[32 keys x 32 rows] (rb) = K_perm . Q^T(rb)   v_mfma_f32_32x32x16_bf16, A = K from LDS,
+                                                   B = Q^T from AGPRs, 8 k-steps of 16 dims
+  P^T = exp2(S * c2 - m * c2) packed to bf16        (every value a lane holds is its own row)
+  O^T[128 dims x 32 rows] (rb) += V^T . P^T         A = V^T from LDS (ds_read_b64_tr_b16),
+                                                   B = P^T from VGPRs, O in AGPRs
+K rows are fed in a permuted order (bits 2 and 3 of the row swapped) so that accumulator i of a
+lane holds key 16 (i / 8) + 8 g + i % 8: the 8 scores of one 16-key step are the P^T operand.
+
+Software pipeline (one wave per SIMD, so a wave hides its own softmax): phase p issues the MFMAs
+of P.V(p-1) and S(p+1) and, between them, the softmax VALU work of half-tile p. Tiles of 64 keys
+(two half-tiles) go straight from memory into LDS (buffer_load ... lds) in three stages; the
+transfer of tile j+2 is issued at the start of iteration j and waited for at its end, where one
+barrier per tile publishes it and frees the stage of tile j-1.
+
+LDS rows are 256 bytes unpadded; the 16-byte chunk c of row r is stored at chunk
+c ^ (4 (r & 3) + ((r >> 2) & 3)), which keeps both the row reads (ds_read_b128) and the
+transposing reads (ds_read_b64_tr_b16) free of bank conflicts. A transfer instruction fills 1 KiB
+(four rows); each lane fetches the global chunk that lands in its swizzled slot.
+
+Memory safety: every global access is a buffer instruction. K/V transfers use a resource bounded
+to the live rows of the tile (rows past kv_len read as zeros, masked by the softmax); Q, O and
+LSE offsets are formed from clamped row indices, and the stores of rows past the sequence use an
+offset beyond the resource range (dropped). All waves of a workgroup run the same tile count, so
+every barrier is met by all four waves, and every loop has a trip count fixed at entry.
+
+Hazards: instructions are issued in the order written; the required independent-instruction
+distances (MFMA result -> other use 12, VALU write -> MFMA read 2, transcendental -> use 1,
+VALU write -> v_permlane32_swap 2, M0 write -> LDS transfer 1) are enforced by a checker that
+inserts s_nop over every control-flow path into each block.
+"""
+
+from __future__ import annotations
+
+import re
+import sys
+
+# --------------------------------------------------------------------------- kernel arguments
+# (name, byte offset, size); mirrored by the generated header for the host launcher.
+ARGS = [
+    ("q", 0, 8), ("k", 8, 8), ("v", 16, 8), ("o", 24, 8), ("lse", 32, 8), ("rope", 40, 8),
+    ("q_sb", 48, 8), ("k_sb", 56, 8), ("o_sb", 64, 8), ("lse_sb", 72, 8), ("k_sh", 80, 8),
+    ("q_sh", 88, 4), ("o_sh", 92, 4), ("lse_sh", 96, 4), ("q_ss", 100, 4), ("o_ss", 104, 4),
+    ("k_ss", 108, 4), ("q_len", 112, 4), ("kv_len", 116, 4), ("gshift", 120, 4),
+    ("kv_heads", 124, 4), ("causal", 128, 4), ("causal_off", 132, 4), ("rope_q", 136, 4),
+    ("q_rope_off", 140, 4), ("c2", 144, 4), ("nqb", 148, 4), ("nb", 152, 4), ("grid", 156, 4),
+    ("units", 160, 4), ("fd_units_m", 164, 4), ("fd_units_s", 168, 4), ("batch", 172, 4),
+    ("q_nrec", 176, 4), ("o_nrec", 180, 4), ("lse_nrec", 192, 4), ("fd_kvh_m", 196, 4),
+    ("fd_kvh_s", 200, 4), ("rope_bytes", 204, 4),
+]
+ARG_BYTES = 208
+S_QNREC, S_ONREC, S_LNREC = 52, 53, 56  # (argument registers of q_nrec, o_nrec, lse_nrec)
+S_SPARE = 54          # [54:55]: argument bytes 184..191 are unused (a free aligned pair)
+S_ROUND = 3           # persistent loop: blocks this workgroup has finished
+ARG_SGPR0 = 8  # argument dword i lives in s[8 + i]
+
+
+def arg(name: str, hi: bool = False) -> str:
+    for n, off, sz in ARGS:
+        if n == name:
+            return f"s{ARG_SGPR0 + off // 4 + (1 if hi else 0)}"
+    raise KeyError(name)
+
+
+def arg64(name: str) -> str:
+    for n, off, sz in ARGS:
+        if n == name:
+            assert sz == 8
+            return f"s[{ARG_SGPR0 + off // 4}:{ARG_SGPR0 + off // 4 + 1}]"
+    raise KeyError(name)
+
+
+KERNEL = "fa_prefill_a64_bf16"
+NSTAGE = 4            # LDS stages of (K 16 KiB, V 16 KiB): tiles j .. j + NSTAGE - 1 resident
+LDS_BYTES = NSTAGE * 32768
+INVALID_OFF = 0x80000000  # beyond every resource range used for stores
+
+# --------------------------------------------------------------------------- registers
+# VGPRs
+V_TID = 0
+V_LANE = 1
+SB = [2, 34]          # score buffers: SB[x] + 16 rb .. +15
+PB = [66, 82]         # probability buffers: PB[x] + 8 rb + 4 s .. +3
+RK = 4                # K operand ring: operands read ahead (4 registers each)
+RV = 3                # V^T operand ring
+KRING = 98            # RK slots x 4 (up to 4 here; more go to the spare area)
+VRING = 114           # RV slots x 4
+VKA = 126             # 8 K read addresses (one per k-step)
+VVA = 134             # 8 V^T read addresses (mb * 2 + hi)
+VTOFF = 142           # 4 transfer offsets
+V_M = 146             # running max per row, in exp2 units (m * scale * log2 e)
+V_L = 148             # running sum
+V_LT = 150            # this half-tile's partial row sums
+V_NBV = 152           # 2 temps: new bias value (-m) per row
+V_ALPHA = 154
+V_LIMB = 156          # causal/tail limit base per rb
+V_LIM = 158
+V_MX = 160            # 4 temps for the cross-lane max
+V_U = 164             # 2 temps
+V_NINF = 166
+V_ONES = 167          # packed bf16 (1, 1)
+V_TMP = 168           # 8 temps (rescale)
+V_QOFF = 176          # Q byte offsets per rb (2)
+V_CSOFF = 178         # (cos, sin) row byte offsets per rb (2)
+V_OOFF = 180          # O byte offsets per rb (2)
+V_LOFF = 182          # LSE byte offsets per rb (2)
+V_ROW = 184           # 4 setup temps
+NB = 188              # score bias blocks: NB + 16 rb .. +15 all hold -m of the lane's row
+V_BIG = 220           # 2^64: a half-tile row sum above it sends the phase to the exact path
+NUM_VGPR = 222
+# AGPRs
+A_O = 0               # O[rb][mb]: a[(rb*4+mb)*16 ..]
+A_Q = 128             # Q[rb][ks]: a[128 + (rb*8+ks)*4 ..]
+NUM_AGPR = 192
+
+# SGPRs (beyond s[0:1] kernarg pointer, s2 workgroup id, s[8:59] arguments)
+S_WAVE = 60
+S_BH = 61
+S_QB = 62
+S_B = 63
+S_KVH = 64
+S_N = 65              # tiles of the block
+S_NFULL = 66
+S_J = 67
+S_JU = 68             # end of the unmasked loop
+S_NM1 = 69            # n - 1
+S_MV = 70             # [70:71] overflow flags of the phase
+S_NEED0 = 72          # [72:73]
+S_NEED1 = 74          # [74:75]
+S_HIMASK = 76         # [76:77] lanes 32..63
+S_KEY0 = 78           # first key of the masked half-tile
+S_RK = 80             # [80:83] K transfer resource
+S_RV = 84             # [84:87] V transfer resource
+S_KBASE = 88          # [88:89]
+S_VBASE = 90          # [90:91]
+S_NREC = 92
+S_TSLOT = 93          # stage of the next transfer
+S_TT = 94             # tile of the next transfer
+S_KDELTA = 95
+S_T0 = 96             # [96:99] temps (4-aligned: also a resource)
+S_T1 = 97
+S_T2 = 98
+S_T3 = 99
+S_KSLOT = 100
+S_VSLOT = 101
+S_RQ = 4              # [4:7] Q / O / LSE resource (reused)
+NUM_SGPR = 102
+
+RB_ROWS = 32
+
+
+def vr(base: int, n: int = 1) -> str:
+    return f"v{base}" if n == 1 else f"v[{base}:{base + n - 1}]"
+
+
+def ar(base: int, n: int = 1) -> str:
+    return f"a{base}" if n == 1 else f"a[{base}:{base + n - 1}]"
+
+
+def sr(base: int, n: int = 1) -> str:
+    return f"s{base}" if n == 1 else f"s[{base}:{base + n - 1}]"
+
+
+def s_of(x: int) -> int:  # score register: buffer x, block rb, value i
+    return x
+
+
+# --------------------------------------------------------------------------- instructions
+_REG_RE = re.compile(r"\b([vas])\[(\d+):(\d+)\]|\b([vas])(\d+)\b")
+
+
+def regs_in(text: str) -> list[str]:
+    out = []
+    for m in _REG_RE.finditer(text):
+        if m.group(1):
+            k, a, b = m.group(1), int(m.group(2)), int(m.group(3))
+            out += [f"{k}{i}" for i in range(a, b + 1)]
+        else:
+            out.append(f"{m.group(4)}{m.group(5)}")
+    return out
+
+
+TRANS = ("v_exp_f32", "v_log_f32", "v_rcp_f32")
+
+
+class Ins:
+    __slots__ = ("text", "kind", "reads", "writes", "nops", "dsid", "needs", "srcc_chain")
+
+    def __init__(self, text, kind=None, reads=None, writes=None):
+        self.text = text
+        op = text.split()[0] if text.strip() else ""
+        if kind is None:
+            if op.startswith("v_mfma"):
+                kind = "mfma"
+            elif op.startswith(TRANS):
+                kind = "trans"
+            elif op.startswith("v_permlane"):
+                kind = "permlane"
+            elif op.startswith("v_"):
+                kind = "valu"
+            elif op.startswith("ds_"):
+                kind = "ds"
+            elif op.startswith("buffer_"):
+                kind = "vmem"
+            elif op == "s_nop":
+                kind = "nop"
+            elif op.endswith(":") or op == "":
+                kind = "label"
+            elif op.startswith("s_"):
+                kind = "salu"
+            else:
+                kind = "other"
+        self.kind = kind
+        self.nops = 0
+        self.dsid = None
+        self.needs = []
+        self.srcc_chain = False
+        if reads is None or writes is None:
+            r, w = self._operands()
+            reads = r if reads is None else reads
+            writes = w if writes is None else writes
+        self.reads = set(reads)
+        self.writes = set(writes)
+
+    def _operands(self):
+        t = self.text.split(None, 1)
+        if len(t) < 2:
+            return [], []
+        op, rest = t
+        parts = [p.strip() for p in rest.split(",")]
+        if self.kind in ("vmem",):
+            if op.startswith("buffer_store"):
+                return regs_in(rest), []
+            if " lds" in rest:
+                return regs_in(rest), []
+            return regs_in(",".join(parts[1:])), regs_in(parts[0])
+        if self.kind == "ds":
+            return regs_in(",".join(parts[1:])), regs_in(parts[0])
+        if self.kind == "permlane":
+            rr = regs_in(rest)
+            return rr, rr
+        if self.kind == "salu":
+            if op.startswith(("s_cmp", "s_bitcmp", "s_waitcnt", "s_barrier", "s_cbranch",
+                              "s_branch", "s_endpgm")):
+                return regs_in(rest), []
+            return regs_in(",".join(parts[1:])), regs_in(parts[0])
+        if op.startswith("v_cmp"):
+            return regs_in(",".join(parts[1:])), regs_in(parts[0])
+        if op.startswith("v_dot2c"):
+            rr = regs_in(rest)
+            return rr, regs_in(parts[0])
+        return regs_in(",".join(parts[1:])), regs_in(parts[0])
+
+    def ws(self) -> int:
+        if self.kind == "label":
+            return 0
+        if self.kind == "nop":
+            return int(self.text.split()[1]) + 1
+        return 1
+
+
+def I(text, **kw) -> Ins:
+    return Ins(text, **kw)
+
+
+# --------------------------------------------------------------------------- hazard checker
+def _is_vreg(r: str) -> bool:
+    return r[0] in "va"
+
+
+def required(prev: Ins, cur: Ins) -> int:
+    """Independent wait states `cur` needs after `prev` (the rules LLVM's hazard recognizer
+    applies on gfx950, verified against the compiler's own output)."""
+    if cur.kind in ("label", "nop"):
+        return 0
+    need = 0
+    pw = {r for r in prev.writes if _is_vreg(r)}
+    if prev.kind == "mfma" and pw:
+        touched = (cur.reads | cur.writes) & pw
+        if touched:
+            if cur.kind == "mfma" and cur.srcc_chain and touched <= cur.writes:
+                pass  # same accumulator, back-to-back chain: handled by the hardware
+            else:
+                need = max(need, 12)
+    if prev.kind in ("valu", "trans", "permlane") and pw:
+        if cur.kind == "mfma" and ((cur.reads | cur.writes) & pw):
+            need = max(need, 2)
+        if cur.kind == "permlane" and (cur.reads & pw):
+            need = max(need, 2)
+    if prev.kind == "trans" and pw and cur.kind in ("valu", "trans", "permlane"):
+        if cur.reads & pw:
+            need = max(need, 1)
+    if prev.kind == "permlane" and pw and (cur.reads & pw):
+        need = max(need, 2)
+    # v_dot* execute outside the VALU pipeline: their result reaches another instruction 3
+    # wait states later, except the next v_dot* accumulating onto the same register
+    if prev.text.startswith("v_dot") and pw and ((cur.reads | cur.writes) & pw):
+        chain = cur.text.startswith("v_dot2c") and cur.writes == pw
+        if not chain:
+            need = max(need, 3)
+    if prev.kind == "salu" and "m0" in prev.text.split(",")[0] and cur.kind == "vmem" and " lds" in cur.text:
+        need = max(need, 1)
+    return need
+
+
+def check_path(path: list[Ins], start: int):
+    """Raise nops of instructions path[start:] so every hazard against any earlier instruction
+    of `path` is covered. Instructions before `start` are context (already fixed)."""
+    window = 40
+    for i in range(start, len(path)):
+        cur = path[i]
+        if cur.kind in ("label",):
+            continue
+        dist = cur.nops if cur.kind != "nop" else 0
+        req_extra = 0
+        j = i - 1
+        d = dist
+        while j >= 0 and i - j <= window and d < 13:
+            p = path[j]
+            r = required(p, cur)
+            if r > d:
+                req_extra = max(req_extra, r - d)
+            d += p.ws() + (p.nops if p.kind != "nop" else 0)
+            j -= 1
+        if req_extra:
+            cur.nops += req_extra
+
+
+class Block:
+    def __init__(self, name: str):
+        self.name = name
+        self.ins: list[Ins] = []
+        self.preds: list["Block"] = []
+
+    def add(self, x):
+        if isinstance(x, Ins):
+            self.ins.append(x)
+        elif isinstance(x, str):
+            self.ins.append(I(x))
+        else:
+            for y in x:
+                self.add(y)
+
+
+def tails(block: Block, need_ws: int = 16, depth: int = 4) -> list[list[Ins]]:
+    """All instruction tails (>= need_ws wait states) of the paths entering `block`."""
+    if depth == 0 or not block.preds:
+        return [[]]
+    out = []
+    for p in block.preds:
+        seq = p.ins
+        ws = sum(x.ws() + (x.nops if x.kind != "nop" else 0) for x in seq)
+        if ws >= need_ws:
+            out.append(seq[-40:])
+        else:
+            for t in tails(p, need_ws - ws, depth - 1):
+                out.append(t + seq)
+    return out
+
+
+def fix_hazards(blocks: list[Block]):
+    for _ in range(3):  # nops only ever grow; repeat so predecessors' nops are counted
+        for b in blocks:
+            for t in tails(b):
+                check_path(t + b.ins, len(t))
+
+
+# --------------------------------------------------------------------------- helpers
+def valu(text):
+    return I(text)
+
+
+def fdiv(dst, n, m, s, tmp):
+    """dst = n / d for the FastDiv magic (m, s) of d: (mulhi(n, m) + n) >> s (n < 2^24)."""
+    return [I(f"s_mul_hi_u32 {tmp}, {n}, {m}"), I(f"s_add_u32 {tmp}, {tmp}, {n}"),
+            I(f"s_lshr_b32 {dst}, {tmp}, {s}")]
+
+
+def swz_py(r: int) -> int:
+    return 4 * (r & 3) + ((r >> 2) & 3)
+
+
+# --------------------------------------------------------------------------- the program
+class Gen:
+    def __init__(self):
+        self.blocks: list[Block] = []
+        self.cur: Block | None = None
+        self.ds_outstanding: list[int] = []  # ids of LDS reads in flight (oldest first)
+        self.ds_next = 0
+
+    def new_block(self, name, preds=()):
+        b = Block(name)
+        b.preds = list(preds)
+        self.blocks.append(b)
+        self.cur = b
+        return b
+
+    def emit(self, x):
+        self.cur.add(x)
+
+    # ---- LDS read bookkeeping (in-order completion: lgkmcnt counts younger reads)
+    def ds_issue(self, text) -> int:
+        ins = I(text)
+        ins.dsid = self.ds_next
+        self.ds_next += 1
+        self.ds_outstanding.append(ins.dsid)
+        self.emit(ins)
+        return ins.dsid
+
+    def ds_wait_for(self, ids):
+        if not ids:
+            return
+        pend = [i for i in ids if i in self.ds_outstanding]
+        if not pend:
+            return
+        last = max(self.ds_outstanding.index(i) for i in pend)
+        younger = len(self.ds_outstanding) - 1 - last
+        n = min(younger, 15)
+        self.emit(I(f"s_waitcnt lgkmcnt({n})"))
+        self.ds_outstanding = self.ds_outstanding[len(self.ds_outstanding) - n:] if n else []
+
+    def ds_wait_all(self):
+        if self.ds_outstanding:
+            self.emit(I("s_waitcnt lgkmcnt(0)"))
+            self.ds_outstanding = []
+
+
+# ---- operand reads ----------------------------------------------------------------------------
+def k_read_text(slot: int, ks: int, hh: int) -> str:
+    return f"ds_read_b128 {vr(KRING + 4 * slot, 4)}, {vr(VKA + ks)} offset:{hh * 8192}"
+
+
+def v_read_texts(slot: int, mb: int, s: int, hh: int) -> list[str]:
+    off = hh * 8192 + s * 4096
+    base = VRING + 4 * slot
+    return [f"ds_read_b64_tr_b16 {vr(base, 2)}, {vr(VVA + mb * 2 + 0)} offset:{off}",
+            f"ds_read_b64_tr_b16 {vr(base + 2, 2)}, {vr(VVA + mb * 2 + 1)} offset:{off}"]
+
+
+def q_op(rb: int, ks: int) -> str:
+    return ar(A_Q + (rb * 8 + ks) * 4, 4)
+
+
+def o_acc(rb: int, mb: int) -> str:
+    return ar(A_O + (rb * 4 + mb) * 16, 16)
+
+
+def s_acc(x: int, rb: int) -> str:
+    return vr(SB[x] + 16 * rb, 16)
+
+
+def p_op(x: int, rb: int, s: int) -> str:
+    return vr(PB[x] + 8 * rb + 4 * s, 4)
+
+
+# ---- softmax VALU program of one half-tile --------------------------------------------------
+# Scores arrive as S' = S * c2 - m (the first MFMA of a score block accumulates onto the bias
+# block NB = -m, and Q carries the factor c2 = scale * log2 e), so P = exp2(S') needs one
+# instruction per score. The running max m is not recomputed per tile: a half-tile whose row sum
+# exceeds 2^64 (an exponent that would overflow, or the first tile, taken exactly by the
+# prologue) sends the phase to the exact path, which recomputes that half-tile's scores, takes
+# the row maxima, moves m, rescales O and l and redoes P. With m at least the first half-tile's
+# row max, every row keeps l >= 1 and P stays below 2^64, so O and l cannot overflow in f32.
+def mask_program(x: int) -> list[Ins]:
+    out = []
+    S = SB[x]
+    for rb in range(2):
+        out.append(I(f"v_subrev_u32 {vr(V_LIM + rb)}, {sr(S_KEY0)}, {vr(V_LIMB + rb)}"))
+    for rb in range(2):
+        for i in range(16):
+            key = 16 * (i >> 3) + (i & 7)
+            out.append(I(f"v_cmp_gt_i32 vcc, {key}, {vr(V_LIM + rb)}",
+                         reads=[f"v{V_LIM + rb}"], writes=["vcc"]))
+            reg = S + 16 * rb + i
+            out.append(I(f"v_cndmask_b32 {vr(reg)}, {vr(reg)}, {vr(V_NINF)}, vcc",
+                         reads=[f"v{reg}", f"v{V_NINF}", "vcc"], writes=[f"v{reg}"]))
+    return out
+
+
+def exp_pack_sum(x: int) -> list[Ins]:
+    """P^T = bf16(exp2(S')) into PB[x] and the half-tile row sums of P into V_LT (f32 sums of the
+    exponentials: v_dot* instructions issue to the matrix pipeline and would stall behind the
+    MFMAs, ordinary adds overlap them)."""
+    out = []
+    S = SB[x]
+    pend = []
+    for rb in range(2):
+        for s in range(2):
+            for j in range(4):
+                i0 = 8 * s + 2 * j
+                r = S + 16 * rb + i0
+                out += [I(f"v_exp_f32 {vr(r)}, {vr(r)}"), I(f"v_exp_f32 {vr(r + 1)}, {vr(r + 1)}")]
+                out += pend
+                pend = []
+                dst = PB[x] + 8 * rb + 4 * s + j
+                pend.append(I(f"v_cvt_pk_bf16_f32 {vr(dst)}, {vr(r)}, {vr(r + 1)}"))
+                lt = vr(V_LT + rb)
+                if i0 == 0:
+                    pend.append(I(f"v_add_f32 {lt}, {vr(r)}, {vr(r + 1)}"))
+                else:
+                    pend += [I(f"v_add_f32 {lt}, {lt}, {vr(r)}"),
+                             I(f"v_add_f32 {lt}, {lt}, {vr(r + 1)}")]
+    out += pend
+    return out
+
+
+def softmax_program(x: int, masked: bool) -> list[Ins]:
+    """Fast path of the half-tile in SB[x]: (mask,) exponentials, P^T, row sums, overflow flags."""
+    out = mask_program(x) if masked else []
+    out += exp_pack_sum(x)
+    out += [I(f"v_cmp_gt_f32 {sr(S_NEED0, 2)}, {vr(V_LT)}, {vr(V_BIG)}",
+              reads=[f"v{V_LT}", f"v{V_BIG}"], writes=[f"s{S_NEED0}", f"s{S_NEED0 + 1}"]),
+            I(f"v_cmp_gt_f32 {sr(S_NEED1, 2)}, {vr(V_LT + 1)}, {vr(V_BIG)}",
+              reads=[f"v{V_LT + 1}", f"v{V_BIG}"], writes=[f"s{S_NEED1}", f"s{S_NEED1 + 1}"]),
+            I(f"s_or_b64 {sr(S_MV, 2)}, {sr(S_NEED0, 2)}, {sr(S_NEED1, 2)}")]
+    return out
+
+
+def rescale_block() -> list[Ins]:
+    """O^T *= alpha (per row)."""
+    out = []
+    for rb in range(2):
+        for mb in range(4):
+            base = A_O + (rb * 4 + mb) * 16
+            for h in range(2):
+                regs = [base + 8 * h + i for i in range(8)]
+                out += [I(f"v_accvgpr_read_b32 {vr(V_TMP + i)}, {ar(a)}") for i, a in enumerate(regs)]
+                out += [I(f"v_mul_f32 {vr(V_TMP + i)}, {vr(V_TMP + i)}, {vr(V_ALPHA + rb)}")
+                        for i in range(8)]
+                out += [I(f"v_accvgpr_write_b32 {ar(a)}, {vr(V_TMP + i)}") for i, a in enumerate(regs)]
+    return out
+
+
+def exact_path(gen: "Gen", x: int, hh: int, s_x) -> None:
+    """Exact softmax of the half-tile whose scores belong in SB[x] (K half hh of the stage before
+    the current K read stage): recompute the raw scores S * c2, mask, take the row maxima, move m
+    (alpha = exp2(m_old - m_new)), rescale O and l, re-bias the scores SB[s_x] that this phase's
+    MFMAs accumulated onto the old bias, set the bias blocks, and redo P^T and the row sums."""
+    e = gen.emit
+    gen.ds_wait_all()
+    e(I("s_waitcnt lgkmcnt(0)"))
+    # K addresses of the previous stage
+    d = sr(S_T0)
+    e([I(f"s_cmp_eq_u32 {sr(S_KSLOT)}, 0"),
+       I(f"s_mov_b32 {d}, 0xffff8000"),
+       I(f"s_cselect_b32 {d}, 0x{(NSTAGE - 1) * 32768:x}, {d}")])
+    e([I(f"v_add_u32 {vr(V_TMP + i)}, {d}, {vr(VKA + i)}") for i in range(8)])
+    for half in range(2):
+        for k4 in range(4):
+            ks = 4 * half + k4
+            e(I(f"ds_read_b128 {vr(KRING + 4 * k4, 4)}, {vr(V_TMP + ks)} offset:{hh * 8192}"))
+        e(I("s_waitcnt lgkmcnt(0)"))
+        for k4 in range(4):
+            ks = 4 * half + k4
+            for rb in range(2):
+                src_c = "0" if ks == 0 else s_acc(x, rb)
+                ins = I(f"v_mfma_f32_32x32x16_bf16 {s_acc(x, rb)}, {vr(KRING + 4 * k4, 4)}, "
+                        f"{q_op(rb, ks)}, {src_c}")
+                ins.srcc_chain = ks != 0
+                e(ins)
+    e(mask_program(x))
+    S = SB[x]
+    for rb in range(2):
+        r = S + 16 * rb
+        t = V_MX + 2 * rb
+        e([I(f"v_max3_f32 {vr(t)}, {vr(r)}, {vr(r + 1)}, {vr(r + 2)}"),
+           I(f"v_max3_f32 {vr(t + 1)}, {vr(r + 3)}, {vr(r + 4)}, {vr(r + 5)}"),
+           I(f"v_max3_f32 {vr(t)}, {vr(t)}, {vr(r + 6)}, {vr(r + 7)}"),
+           I(f"v_max3_f32 {vr(t + 1)}, {vr(t + 1)}, {vr(r + 8)}, {vr(r + 9)}"),
+           I(f"v_max3_f32 {vr(t)}, {vr(t)}, {vr(r + 10)}, {vr(r + 11)}"),
+           I(f"v_max3_f32 {vr(t + 1)}, {vr(t + 1)}, {vr(r + 12)}, {vr(r + 13)}"),
+           I(f"v_max3_f32 {vr(t)}, {vr(t)}, {vr(r + 14)}, {vr(r + 15)}")])
+    mx0, mx1 = V_U, V_U + 1
+    F, G = V_MX, V_MX + 1
+    # swap(mx0.hi, mx1.lo): max(mx0, mx1) is row 0's max on lanes < 32 and row 1's on lanes >= 32;
+    # a second swap of that value against its copy gives both rows' maxima on every lane
+    e([I(f"v_max_f32 {vr(mx0)}, {vr(V_MX)}, {vr(V_MX + 1)}"),
+       I(f"v_max_f32 {vr(mx1)}, {vr(V_MX + 2)}, {vr(V_MX + 3)}"),
+       I(f"v_permlane32_swap_b32 {vr(mx0)}, {vr(mx1)}"),
+       I(f"v_max_f32 {vr(F)}, {vr(mx0)}, {vr(mx1)}"),
+       I(f"v_mov_b32 {vr(G)}, {vr(F)}"),
+       I(f"v_permlane32_swap_b32 {vr(F)}, {vr(G)}")])
+    for rb, mt in ((0, F), (1, G)):
+        m, al, nbv = V_M + rb, V_ALPHA + rb, V_NBV + rb
+        e([I(f"v_max_f32 {vr(mt)}, {vr(mt)}, {vr(m)}"),            # m_new (finite)
+           I(f"v_sub_f32 {vr(al)}, {vr(m)}, {vr(mt)}"),
+           I(f"v_exp_f32 {vr(al)}, {vr(al)}"),                      # m_old = -inf: 0
+           I(f"v_mov_b32 {vr(m)}, {vr(mt)}"),
+           I(f"v_mul_f32 {vr(V_L + rb)}, {vr(V_L + rb)}, {vr(al)}"),
+           I(f"v_xor_b32 {vr(nbv)}, 0x80000000, {vr(mt)}"),        # new bias -m_new
+           I(f"v_sub_f32 {vr(V_U + rb)}, {vr(nbv)}, {vr(NB + 16 * rb)}")])  # bias change
+    if s_x is not None:
+        for rb in range(2):
+            r = SB[s_x] + 16 * rb
+            e([I(f"v_add_f32 {vr(r + i)}, {vr(r + i)}, {vr(V_U + rb)}") for i in range(16)])
+    for rb in range(2):
+        e([I(f"v_mov_b32 {vr(NB + 16 * rb + i)}, {vr(V_NBV + rb)}") for i in range(16)])
+    e(rescale_block())
+    for rb in range(2):
+        r = S + 16 * rb
+        e([I(f"v_add_f32 {vr(r + i)}, {vr(r + i)}, {vr(V_NBV + rb)}") for i in range(16)])
+    e(exp_pack_sum(x))
+
+
+# ---- one pipeline phase ------------------------------------------------------------------------
+def phase(gen: Gen, *, pv_x, pv_hh, s_x, s_hh, sm_x, sm_masked, pre=(),
+          prefetch_v_hh=None, after_last_v=(), after_last_k=(), vring_state=None):
+    """Emits one phase: MFMAs of P.V (P in PB[pv_x], V half pv_hh of the current V stage) then
+    S (into SB[s_x], K half s_hh), with the softmax of SB[sm_x] spread between them.
+    vring_state: dict carrying the V operands already read into the ring by the previous phase:
+    {'ready': {op_index: (slot, [ds ids])}}, and after the phase the prefetched operands of the
+    next phase. Returns the new ring state."""
+    mf: list[tuple[str, list, dict]] = []  # (text, operand key, info)
+    # P.V: operand o = (s, mb) in order s-major; each operand feeds rb = 0, 1
+    pv_ops = [(s, mb) for s in range(2) for mb in range(4)] if pv_x is not None else []
+    k_ops = list(range(8)) if s_x is not None else []
+    DV, DK = RV, RK
+    ready = dict(vring_state["ready"]) if vring_state else {}
+    # slots: V ring slots 0..2; op o uses slot o % 3 (ready ops from the previous phase agree)
+    valu_stream = softmax_program(sm_x, sm_masked) if sm_x is not None else []
+    # the phase's scalar set-up (transfers, key base) is spread over the first MFMA slots
+    valu_stream = list(pre) + valu_stream
+    # plan MFMA list
+    mlist = []
+    for oi, (s, mb) in enumerate(pv_ops):
+        for rb in range(2):
+            mlist.append(("pv", oi, rb))
+    for ks in k_ops:
+        order_rb = (0, 1)
+        for rb in order_rb:
+            mlist.append(("s", ks, rb))
+    nm = len(mlist)
+    vi = 0  # next VALU item
+
+    # issue helpers
+    v_issued = {}   # op index -> ds ids
+    k_issued = {}
+    v_slot_free_after = {}  # slot -> index in mlist of last MFMA using it (must be issued)
+    for oi, ids in ready.items():
+        v_issued[oi] = ids
+    next_v = max(ready.keys()) + 1 if ready else 0
+    next_k = 0
+    issued_m = -1  # index of last MFMA emitted
+
+    def v_slot(oi):
+        return oi % DV
+
+    def last_use_v(oi):  # mlist index of the last MFMA reading operand oi
+        return 2 * oi + 1
+
+    def last_use_k(ks):
+        return len(pv_ops) * 2 + 2 * ks + 1
+
+    def can_issue_v(oi):
+        prev = oi - DV
+        return prev < 0 or last_use_v(prev) <= issued_m
+
+    def can_issue_k(ks):
+        prev = ks - DK
+        return prev < 0 or last_use_k(prev) <= issued_m
+
+    def issue_reads(budget):
+        nonlocal next_v, next_k
+        n = 0
+        while n < budget:
+            if next_v < len(pv_ops) and can_issue_v(next_v):
+                s, mb = pv_ops[next_v]
+                ids = [gen.ds_issue(t) for t in v_read_texts(v_slot(next_v), mb, s, pv_hh)]
+                v_issued[next_v] = ids
+                if next_v == len(pv_ops) - 1:
+                    for x in after_last_v:
+                        gen.emit(x)
+                next_v += 1
+                n += 1
+                continue
+            if next_k < len(k_ops) and can_issue_k(next_k):
+                k_issued[next_k] = [gen.ds_issue(k_read_text(next_k % DK, next_k, s_hh))]
+                if next_k == len(k_ops) - 1:
+                    for x in after_last_k:
+                        gen.emit(x)
+                next_k += 1
+                n += 1
+                continue
+            break
+        return n
+
+    # initial reads: fill the rings
+    issue_reads(DV + DK)
+    total_valu = len(valu_stream)
+    for mi, (kind, idx, rb) in enumerate(mlist):
+        if kind == "pv":
+            gen.ds_wait_for(v_issued[idx])
+            s, mb = pv_ops[idx]
+            slot = v_slot(idx)
+            ins = I(f"v_mfma_f32_32x32x16_bf16 {o_acc(rb, mb)}, {vr(VRING + 4 * slot, 4)}, "
+                    f"{p_op(pv_x, rb, s)}, {o_acc(rb, mb)}")
+            ins.srcc_chain = True
+        else:
+            gen.ds_wait_for(k_issued[idx])
+            slot = idx % DK
+            # k-step 0 accumulates onto the bias block (-m of the lane's row)
+            src_c = vr(NB + 16 * rb, 16) if idx == 0 else s_acc(s_x, rb)
+            ins = I(f"v_mfma_f32_32x32x16_bf16 {s_acc(s_x, rb)}, {vr(KRING + 4 * slot, 4)}, "
+                    f"{q_op(rb, idx)}, {src_c}")
+            ins.srcc_chain = idx != 0
+        gen.emit(ins)
+        issued_m = mi
+        issue_reads(2)
+        # spread the VALU work evenly over the remaining MFMAs
+        remaining_m = nm - mi
+        take = (total_valu - vi + remaining_m - 1) // remaining_m if remaining_m else 0
+        for _ in range(take):
+            if vi < total_valu:
+                gen.emit(valu_stream[vi])
+                vi += 1
+    while vi < total_valu:
+        gen.emit(valu_stream[vi])
+        vi += 1
+    issue_reads(99)
+    # prefetch the next phase's first V operands
+    new_ready = {}
+    if prefetch_v_hh is not None:
+        s_h = prefetch_v_hh
+        for oi in range(DV):
+            s, mb = (oi // 4, oi % 4)
+            ids = [gen.ds_issue(t) for t in v_read_texts(oi % DV, mb, s, s_h)]
+            new_ready[oi] = (oi % DV, ids)
+    return {"ready": {k: v[1] for k, v in new_ready.items()}} if new_ready else None
+
+
+def transfer_block(which: str) -> list[Ins]:
+    """The 4 K or V transfer instructions of this wave for the tile whose resource is set up;
+    M0 = stage base (S_T2) + region + (wave + 4 i) KiB."""
+    out = []
+    rs = S_RK if which == "k" else S_RV
+    region = 0 if which == "k" else 16384
+    for i in range(4):
+        out.append(I(f"s_add_u32 m0, {sr(S_T2)}, {region + 1024 * 4 * i}", writes=["m0"],
+                     reads=[f"s{S_T2}"]))
+        out.append(I(f"buffer_load_dwordx4 {vr(VTOFF + i)}, {sr(rs, 4)}, 0 offen lds"))
+    return out
+
+
+def transfer_setup(tile_sgpr: str) -> list[Ins]:
+    """Resources of the K and V rows of tile `tile_sgpr` (bounded to its live rows) and the
+    stage base S_T2 = stage * 32 KiB + wave KiB."""
+    t0, t1 = sr(S_T0), sr(S_T1)
+    rb = arg("k_ss")
+    out = [
+        # byte offset of the tile: tile * 64 * row_bytes
+        I(f"s_mul_i32 {t0}, {tile_sgpr}, {rb}"),
+        I(f"s_lshl_b32 {t0}, {t0}, 6"),
+        I(f"s_sub_u32 {t1}, {sr(S_NREC)}, {t0}"),
+        I(f"s_cmp_lt_i32 {t1}, 0"),
+        I(f"s_cselect_b32 {t1}, 0, {t1}"),
+        I(f"s_cmp_lt_i32 {tile_sgpr}, {sr(S_N)}"),
+        I(f"s_cselect_b32 {t1}, {t1}, 0"),
+        I(f"s_add_u32 {sr(S_RK)}, {sr(S_KBASE)}, {t0}"),
+        I(f"s_addc_u32 {sr(S_RK + 1)}, {sr(S_KBASE + 1)}, 0"),
+        I(f"s_and_b32 {sr(S_RK + 1)}, {sr(S_RK + 1)}, 0xffff"),
+        I(f"s_mov_b32 {sr(S_RK + 2)}, {t1}"),
+        I(f"s_mov_b32 {sr(S_RK + 3)}, 0x20000"),
+        I(f"s_add_u32 {sr(S_RV)}, {sr(S_VBASE)}, {t0}"),
+        I(f"s_addc_u32 {sr(S_RV + 1)}, {sr(S_VBASE + 1)}, 0"),
+        I(f"s_and_b32 {sr(S_RV + 1)}, {sr(S_RV + 1)}, 0xffff"),
+        I(f"s_mov_b32 {sr(S_RV + 2)}, {t1}"),
+        I(f"s_mov_b32 {sr(S_RV + 3)}, 0x20000"),
+        # stage base: tslot * 32 KiB + wave KiB
+        I(f"s_lshl_b32 {sr(S_T2)}, {sr(S_TSLOT)}, 15"),
+        I(f"s_lshl_b32 {sr(S_T3)}, {sr(S_WAVE)}, 10"),
+        I(f"s_add_u32 {sr(S_T2)}, {sr(S_T2)}, {sr(S_T3)}"),
+    ]
+    return out
+
+
+def advance_slot(slot_sgpr: int, addr_base: int, n_addr: int) -> list[Ins]:
+    """slot = (slot + 1) % NSTAGE and every read address += the matching stage delta."""
+    d = sr(S_KDELTA)
+    s = sr(slot_sgpr)
+    out = [I(f"s_add_u32 {s}, {s}, 1"),
+           I(f"s_cmp_eq_u32 {s}, {NSTAGE}"),
+           I(f"s_cselect_b32 {s}, 0, {s}"),
+           I(f"s_mov_b32 {d}, 0x8000"),
+           I(f"s_cselect_b32 {d}, 0x{(-(NSTAGE - 1) * 32768) & 0xffffffff:x}, {d}")]
+    out += [I(f"v_add_u32 {vr(addr_base + i)}, {d}, {vr(addr_base + i)}") for i in range(n_addr)]
+    return out
+
+
+# --------------------------------------------------------------------------- setup code
+def setup(gen: Gen):
+    e = gen.emit
+    e(I("s_load_dwordx16 s[8:23], s[0:1], 0x0"))
+    e(I("s_load_dwordx16 s[24:39], s[0:1], 0x40"))
+    e(I("s_load_dwordx16 s[40:55], s[0:1], 0x80"))
+    e(I("s_load_dwordx4 s[56:59], s[0:1], 0xc0"))
+    e(I(f"v_and_b32 {vr(V_LANE)}, 63, {vr(V_TID)}"))
+    e(I(f"v_readfirstlane_b32 {sr(S_WAVE)}, {vr(V_TID)}"))
+    e(I("s_waitcnt lgkmcnt(0)"))
+    e(I("s_nop 4"))
+    e(I(f"s_lshr_b32 {sr(S_WAVE)}, {sr(S_WAVE)}, 6"))
+    T0, T1, T2, T3 = (sr(S_T0), sr(S_T1), sr(S_T2), sr(S_T3))
+    e([I(f"v_mov_b32 {vr(V_NINF)}, 0xff800000"),
+       I(f"v_mov_b32 {vr(V_ONES)}, 0x3f803f80"),
+       I(f"v_mov_b32 {vr(V_BIG)}, 0x5f800000"),
+       I(f"s_mov_b32 {sr(S_HIMASK)}, 0"),
+       I(f"s_mov_b32 {sr(S_HIMASK + 1)}, -1"),
+       I(f"s_mov_b32 {sr(S_ROUND)}, 0")])
+
+
+def setup_block(gen: Gen):
+    """Per-block set-up of the persistent loop. Blocks are ranked heaviest first (query block
+    qb = nqb - 1 - o / units, unit bh = o % units, so every causal rank holds equal work) and dealt
+    to the grid's workgroups in snake order: round r gives workgroup w the block
+    o = r * grid + (r even ? w : grid - 1 - w), which balances the causal work across rounds."""
+    e = gen.emit
+    T0, T1, T2, T3 = (sr(S_T0), sr(S_T1), sr(S_T2), sr(S_T3))
+    e(I(".Lblock:"))
+    # every wave has finished the previous block's LDS reads before its stages are refilled
+    e(I("s_barrier"))
+    grid = arg("grid")
+    e([I(f"s_mul_i32 {T0}, {sr(S_ROUND)}, {grid}"),
+       I(f"s_sub_u32 {T1}, {grid}, 1"),
+       I(f"s_sub_u32 {T1}, {T1}, s2"),
+       I(f"s_bitcmp1_b32 {sr(S_ROUND)}, 0"),              # (after the subtractions: SCC)
+       I(f"s_cselect_b32 {T1}, {T1}, s2"),
+       I(f"s_add_u32 {T0}, {T0}, {T1}"),                      # o
+       I(f"s_cmp_ge_u32 {T0}, {arg('nb')}"),
+       I("s_cbranch_scc0 .Lhave_block"),
+       I("s_endpgm"),
+       I(".Lhave_block:")])
+    e(fdiv(T1, T0, arg("fd_units_m"), arg("fd_units_s"), T3))   # rank = o / units
+    e([I(f"s_mul_i32 {T2}, {T1}, {arg('units')}"),
+       I(f"s_sub_u32 {sr(S_BH)}, {T0}, {T2}"),                 # bh = o % units
+       I(f"s_sub_u32 {sr(S_QB)}, {arg('nqb')}, 1"),
+       I(f"s_sub_u32 {sr(S_QB)}, {sr(S_QB)}, {T1}")])
+    e(fdiv(sr(S_B), sr(S_BH), arg("fd_kvh_m"), arg("fd_kvh_s"), T3))
+    e([I(f"s_mul_i32 {T1}, {sr(S_B)}, {arg('kv_heads')}"),
+       I(f"s_sub_u32 {sr(S_KVH)}, {sr(S_BH)}, {T1}"),
+       # a block beyond the batch (never produced by the host's arguments) exits before any access
+       I(f"s_cmp_ge_u32 {sr(S_B)}, {arg('batch')}"),
+       I("s_cbranch_scc0 .Lbatch_ok"),
+       I("s_endpgm"),
+       I(".Lbatch_ok:")])
+
+    # ---- tile counts of the block: rows qb*256 .. +255
+    gs = arg("gshift")
+    e([I(f"s_lshl_b32 {T0}, {sr(S_QB)}, 8"),               # first row
+       I(f"s_lshr_b32 {T1}, {T0}, {gs}"),                   # t_min
+       I(f"s_add_u32 {T2}, {T0}, 255"),
+       I(f"s_lshr_b32 {T2}, {T2}, {gs}"),
+       I(f"s_sub_u32 {T3}, {arg('q_len')}, 1"),
+       I(f"s_min_u32 {T2}, {T2}, {T3}"),                    # t_max
+       I(f"s_add_u32 {T2}, {T2}, {arg('causal_off')}"),
+       I(f"s_add_u32 {T2}, {T2}, 1"),                       # keys a causal block needs
+       I(f"s_min_u32 {T2}, {T2}, {arg('kv_len')}"),
+       I(f"s_cmp_eq_u32 {arg('causal')}, 0"),
+       I(f"s_cselect_b32 {T2}, {arg('kv_len')}, {T2}"),
+       I(f"s_add_u32 {T2}, {T2}, 63"),
+       I(f"s_lshr_b32 {sr(S_N)}, {T2}, 6"),                 # n tiles
+       I(f"s_lshr_b32 {T3}, {arg('kv_len')}, 6"),           # tiles without a tail
+       I(f"s_add_u32 {T1}, {T1}, {arg('causal_off')}"),
+       I(f"s_add_u32 {T1}, {T1}, 1"),
+       I(f"s_lshr_b32 {T1}, {T1}, 6"),
+       I(f"s_cmp_eq_u32 {arg('causal')}, 0"),
+       I(f"s_cselect_b32 {T1}, {T3}, {T1}"),
+       I(f"s_min_u32 {sr(S_NFULL)}, {T1}, {T3}"),
+       I(f"s_sub_u32 {sr(S_NM1)}, {sr(S_N)}, 1"),
+       # unmasked loop iterations: j < min(n - 1, nfull - 1)
+       I(f"s_sub_u32 {T1}, {sr(S_NFULL)}, 1"),
+       I(f"s_cmp_lt_i32 {T1}, 0"),
+       I(f"s_cselect_b32 {T1}, 0, {T1}"),
+       I(f"s_min_u32 {sr(S_JU)}, {T1}, {sr(S_NM1)}")])
+
+    # ---- per-lane rows: row = r0 + 32 rb + (lane & 31); t = row >> gshift; head = row & (G-1)
+    e([I(f"s_lshl_b32 {T0}, {sr(S_QB)}, 8"),
+       I(f"s_lshl_b32 {T1}, {sr(S_WAVE)}, 6"),
+       I(f"s_add_u32 {T0}, {T0}, {T1}"),                    # wave's first row
+       I(f"s_lshl_b32 {T2}, {arg('q_len')}, {gs}"),         # rows_total
+       I(f"s_lshl_b32 {T3}, 1, {gs}"),
+       I(f"s_sub_u32 {T3}, {T3}, 1"),                       # group - 1
+       I(f"v_and_b32 {vr(V_ROW + 3)}, 31, {vr(V_LANE)}")])
+    for rb in range(2):
+        row, t, hd, ok = V_ROW, V_ROW + 1, V_ROW + 2, None
+        e([I(f"v_add_u32 {vr(row)}, {T0}, {vr(V_ROW + 3)}"),
+           I(f"v_add_u32 {vr(row)}, {32 * rb}, {vr(row)}"),
+           I(f"v_cmp_gt_u32 vcc, {T2}, {vr(row)}", reads=[T2, f"v{row}"], writes=["vcc"]),
+           I(f"v_lshrrev_b32 {vr(t)}, {gs}, {vr(row)}"),
+           I(f"v_and_b32 {vr(hd)}, {T3}, {vr(row)}"),
+           I(f"s_sub_u32 {T1}, {arg('q_len')}, 1"),
+           I(f"v_mov_b32 {vr(V_TMP)}, {T1}"),
+           I(f"v_cndmask_b32 {vr(t)}, {vr(V_TMP)}, {vr(t)}, vcc",
+             reads=[f"v{V_TMP}", f"v{t}", "vcc"], writes=[f"v{t}"]),
+           I(f"v_cndmask_b32 {vr(hd)}, 0, {vr(hd)}, vcc", reads=[f"v{hd}", "vcc"],
+             writes=[f"v{hd}"]),
+           # O and LSE offsets (INVALID for rows past the sequence); LSE only from lanes < 32
+           I(f"v_mul_lo_u32 {vr(V_OOFF + rb)}, {vr(hd)}, {arg('o_sh')}"),
+           I(f"v_mul_lo_u32 {vr(V_TMP + 1)}, {vr(t)}, {arg('o_ss')}"),
+           I(f"v_add_u32 {vr(V_OOFF + rb)}, {vr(V_OOFF + rb)}, {vr(V_TMP + 1)}"),
+           I(f"v_mul_lo_u32 {vr(V_LOFF + rb)}, {vr(hd)}, {arg('lse_sh')}"),
+           I(f"v_lshl_add_u32 {vr(V_LOFF + rb)}, {vr(t)}, 2, {vr(V_LOFF + rb)}"),
+           I(f"v_mov_b32 {vr(V_TMP + 2)}, 0x{INVALID_OFF:x}"),
+           I(f"v_cndmask_b32 {vr(V_OOFF + rb)}, {vr(V_TMP + 2)}, {vr(V_OOFF + rb)}, vcc",
+             reads=[f"v{V_TMP + 2}", f"v{V_OOFF + rb}", "vcc"], writes=[f"v{V_OOFF + rb}"]),
+           I(f"v_cndmask_b32 {vr(V_LOFF + rb)}, {vr(V_TMP + 2)}, {vr(V_LOFF + rb)}, vcc",
+             reads=[f"v{V_TMP + 2}", f"v{V_LOFF + rb}", "vcc"], writes=[f"v{V_LOFF + rb}"]),
+           # Q offset: head * q_sh + t * q_ss + 16 g
+           I(f"v_mul_lo_u32 {vr(V_QOFF + rb)}, {vr(hd)}, {arg('q_sh')}"),
+           I(f"v_mul_lo_u32 {vr(V_TMP + 1)}, {vr(t)}, {arg('q_ss')}"),
+           I(f"v_add_u32 {vr(V_QOFF + rb)}, {vr(V_QOFF + rb)}, {vr(V_TMP + 1)}"),
+           # (cos, sin) row of position q_rope_off + t: 512 bytes per position (64 pairs)
+           I(f"v_add_u32 {vr(V_CSOFF + rb)}, {arg('q_rope_off')}, {vr(t)}"),
+           I(f"v_lshlrev_b32 {vr(V_CSOFF + rb)}, 9, {vr(V_CSOFF + rb)}"),
+           # limit base: (causal ? min(kv_len - 1, causal_off + t) : kv_len - 1) - 8 g
+           I(f"s_sub_u32 {T1}, {arg('kv_len')}, 1"),
+           I(f"v_add_u32 {vr(V_LIMB + rb)}, {arg('causal_off')}, {vr(t)}"),
+           I(f"v_min_i32 {vr(V_LIMB + rb)}, {T1}, {vr(V_LIMB + rb)}"),
+           I(f"v_mov_b32 {vr(V_TMP + 1)}, {T1}"),
+           I(f"s_cmp_eq_u32 {arg('causal')}, 0"),
+           I(f"s_cselect_b64 vcc, -1, 0", writes=["vcc"]),
+           I("s_nop 1"),
+           I(f"v_cndmask_b32 {vr(V_LIMB + rb)}, {vr(V_LIMB + rb)}, {vr(V_TMP + 1)}, vcc",
+             reads=[f"v{V_LIMB + rb}", f"v{V_TMP + 1}", "vcc"], writes=[f"v{V_LIMB + rb}"])])
+    # g-dependent parts: +16 g bytes (Q, O), 8 g keys off the limit, LSE stores only from g == 0
+    e([I(f"v_lshrrev_b32 {vr(V_ROW)}, 5, {vr(V_LANE)}"),          # g
+       I(f"v_lshlrev_b32 {vr(V_ROW + 1)}, 4, {vr(V_ROW)}"),       # 16 g
+       I(f"v_lshlrev_b32 {vr(V_ROW + 2)}, 3, {vr(V_ROW)}"),       # 8 g
+       I(f"v_cmp_eq_u32 vcc, 0, {vr(V_ROW)}", reads=[f"v{V_ROW}"], writes=["vcc"]),
+       I(f"v_mov_b32 {vr(V_TMP + 2)}, 0x{INVALID_OFF:x}")])
+    for rb in range(2):
+        e([I(f"v_add_u32 {vr(V_QOFF + rb)}, {vr(V_QOFF + rb)}, {vr(V_ROW + 1)}"),
+           I(f"v_add_u32 {vr(V_CSOFF + rb)}, {vr(V_CSOFF + rb)}, {vr(V_ROW + 1)}"),
+           I(f"v_add_u32 {vr(V_CSOFF + rb)}, {vr(V_CSOFF + rb)}, {vr(V_ROW + 1)}"),
+           I(f"v_sub_u32 {vr(V_LIMB + rb)}, {vr(V_LIMB + rb)}, {vr(V_ROW + 2)}"),
+           I(f"v_cndmask_b32 {vr(V_LOFF + rb)}, {vr(V_TMP + 2)}, {vr(V_LOFF + rb)}, vcc",
+             reads=[f"v{V_TMP + 2}", f"v{V_LOFF + rb}", "vcc"], writes=[f"v{V_LOFF + rb}"]),
+           # O: the lane writes dims mb*32 + 8 q4 + 4 g: + 8 g bytes, skip if row invalid
+           I(f"v_cmp_ne_u32 {sr(S_NEED0, 2)}, {vr(V_TMP + 2)}, {vr(V_OOFF + rb)}",
+             reads=[f"v{V_OOFF + rb}", f"v{V_TMP + 2}"], writes=[f"s{S_NEED0}", f"s{S_NEED0 + 1}"]),
+           I(f"v_add_u32 {vr(V_TMP + 3)}, {vr(V_OOFF + rb)}, {vr(V_ROW + 2)}"),
+           I(f"v_cndmask_b32_e64 {vr(V_OOFF + rb)}, {vr(V_OOFF + rb)}, {vr(V_TMP + 3)}, "
+             f"{sr(S_NEED0, 2)}", reads=[f"v{V_OOFF + rb}", f"v{V_TMP + 3}", f"s{S_NEED0}",
+                                         f"s{S_NEED0 + 1}"], writes=[f"v{V_OOFF + rb}"])])
+    # ---- base addresses: K/V of (b, kvh); Q/O/LSE of (b, first head of the group)
+    def base64(dst, ptr, sb, sh_lo, sh_hi, headmul):
+        # dst = ptr + b * sb + headmul * sh   (64-bit)
+        return [I(f"s_mul_i32 {T0}, {sr(S_B)}, {arg(sb)}"),
+                I(f"s_mul_hi_u32 {T1}, {sr(S_B)}, {arg(sb)}"),
+                I(f"s_mul_i32 {T2}, {sr(S_B)}, {arg(sb, True)}"),
+                I(f"s_add_u32 {T1}, {T1}, {T2}"),
+                I(f"s_add_u32 {sr(dst)}, {arg(ptr)}, {T0}"),
+                I(f"s_addc_u32 {sr(dst + 1)}, {arg(ptr, True)}, {T1}"),
+                I(f"s_mul_i32 {T0}, {headmul}, {sh_lo}"),
+                I(f"s_mul_hi_u32 {T1}, {headmul}, {sh_lo}")] + \
+               ([I(f"s_mul_i32 {T2}, {headmul}, {sh_hi}"), I(f"s_add_u32 {T1}, {T1}, {T2}")]
+                if sh_hi else []) + \
+               [I(f"s_add_u32 {sr(dst)}, {sr(dst)}, {T0}"),
+                I(f"s_addc_u32 {sr(dst + 1)}, {sr(dst + 1)}, {T1}")]
+    e(base64(S_KBASE, "k", "k_sb", arg("k_sh"), arg("k_sh", True), sr(S_KVH)))
+    e(base64(S_VBASE, "v", "k_sb", arg("k_sh"), arg("k_sh", True), sr(S_KVH)))
+    # nrec_all = (kv_len - 1) * row_bytes + 256
+    e([I(f"s_sub_u32 {T0}, {arg('kv_len')}, 1"),
+       I(f"s_mul_i32 {sr(S_NREC)}, {T0}, {arg('k_ss')}"),
+       I(f"s_add_u32 {sr(S_NREC)}, {sr(S_NREC)}, 256")])
+    # transfer offsets: instruction i covers rows 4 (wave + 4 i) + (lane >> 4); slot chunk
+    # lane & 15 holds global chunk (lane & 15) ^ (4 (lane >> 4) + wave)
+    e([I(f"v_lshrrev_b32 {vr(V_ROW)}, 4, {vr(V_LANE)}"),           # lane >> 4
+       I(f"v_and_b32 {vr(V_ROW + 1)}, 15, {vr(V_LANE)}"),
+       I(f"v_lshl_add_u32 {vr(V_ROW + 2)}, {vr(V_ROW)}, 2, {sr(S_WAVE)}"),
+       I(f"v_xor_b32 {vr(V_ROW + 2)}, {vr(V_ROW + 2)}, {vr(V_ROW + 1)}"),   # global chunk
+       I(f"v_lshlrev_b32 {vr(V_ROW + 2)}, 4, {vr(V_ROW + 2)}"),
+       I(f"s_lshl_b32 {T0}, {sr(S_WAVE)}, 2"),
+       I(f"v_add_u32 {vr(V_ROW + 3)}, {T0}, {vr(V_ROW)}")])          # row of instruction 0
+    for i in range(4):
+        e([I(f"v_add_u32 {vr(V_TMP)}, {16 * i}, {vr(V_ROW + 3)}"),
+           I(f"v_mul_lo_u32 {vr(VTOFF + i)}, {vr(V_TMP)}, {arg('k_ss')}"),
+           I(f"v_add_u32 {vr(VTOFF + i)}, {vr(VTOFF + i)}, {vr(V_ROW + 2)}")])
+    # K read addresses (stage 0): row p = perm(lane & 31) (bits 2, 3 swapped),
+    # chunk (2 ks + g) ^ swz(p); V^T read addresses (stage 0, V region at +16 KiB)
+    e([I(f"v_and_b32 {vr(V_ROW)}, 31, {vr(V_LANE)}"),
+       I(f"v_and_b32 {vr(V_ROW + 1)}, 0x13, {vr(V_ROW)}"),
+       I(f"v_bfe_u32 {vr(V_ROW + 2)}, {vr(V_ROW)}, 2, 1"),
+       I(f"v_lshl_or_b32 {vr(V_ROW + 1)}, {vr(V_ROW + 2)}, 3, {vr(V_ROW + 1)}"),
+       I(f"v_bfe_u32 {vr(V_ROW + 2)}, {vr(V_ROW)}, 3, 1"),
+       I(f"v_lshl_or_b32 {vr(V_ROW + 1)}, {vr(V_ROW + 2)}, 2, {vr(V_ROW + 1)}"),  # p
+       # swz(p) = 4 (p & 3) + ((p >> 2) & 3)
+       I(f"v_and_b32 {vr(V_ROW + 2)}, 3, {vr(V_ROW + 1)}"),
+       I(f"v_bfe_u32 {vr(V_ROW + 3)}, {vr(V_ROW + 1)}, 2, 2"),
+       I(f"v_lshl_or_b32 {vr(V_ROW + 2)}, {vr(V_ROW + 2)}, 2, {vr(V_ROW + 3)}"),
+       I(f"v_lshrrev_b32 {vr(V_ROW + 3)}, 5, {vr(V_LANE)}"),      # g
+       I(f"v_xor_b32 {vr(V_ROW + 2)}, {vr(V_ROW + 2)}, {vr(V_ROW + 3)}"),  # g ^ swz(p)
+       I(f"v_lshlrev_b32 {vr(V_ROW + 1)}, 8, {vr(V_ROW + 1)}")])  # p * 256
+    for ks in range(8):
+        e([I(f"v_xor_b32 {vr(V_TMP)}, {2 * ks}, {vr(V_ROW + 2)}"),
+           I(f"v_lshl_add_u32 {vr(VKA + ks)}, {vr(V_TMP)}, 4, {vr(V_ROW + 1)}")])
+    # V^T: row = 8 g + ((lane & 15) >> 2) (+4 for hi); chunk 4 mb + 2 ((lane >> 4) & 1) +
+    # ((lane & 3) >> 1); byte 8 (lane & 1)
+    e([I(f"v_lshrrev_b32 {vr(V_ROW)}, 5, {vr(V_LANE)}"),
+       I(f"v_bfe_u32 {vr(V_ROW + 1)}, {vr(V_LANE)}, 2, 2"),
+       I(f"v_lshl_add_u32 {vr(V_ROW)}, {vr(V_ROW)}, 3, {vr(V_ROW + 1)}"),   # row lo
+       I(f"v_bfe_u32 {vr(V_ROW + 1)}, {vr(V_LANE)}, 4, 1"),
+       I(f"v_bfe_u32 {vr(V_ROW + 2)}, {vr(V_LANE)}, 1, 1"),
+       I(f"v_lshl_or_b32 {vr(V_ROW + 1)}, {vr(V_ROW + 1)}, 1, {vr(V_ROW + 2)}"),  # chunk low
+       I(f"v_and_b32 {vr(V_ROW + 2)}, 1, {vr(V_LANE)}"),
+       I(f"v_lshlrev_b32 {vr(V_ROW + 2)}, 3, {vr(V_ROW + 2)}")])              # byte in chunk
+    for mb in range(4):
+        for hi in range(2):
+            # row r = rowlo + 4 hi; swz(r); addr = 16 KiB + r * 256 + 16 ((4 mb + cl) ^ swz) + byte
+            e([I(f"v_add_u32 {vr(V_TMP)}, {4 * hi}, {vr(V_ROW)}"),
+               I(f"v_and_b32 {vr(V_TMP + 1)}, 3, {vr(V_TMP)}"),
+               I(f"v_bfe_u32 {vr(V_TMP + 2)}, {vr(V_TMP)}, 2, 2"),
+               I(f"v_lshl_or_b32 {vr(V_TMP + 1)}, {vr(V_TMP + 1)}, 2, {vr(V_TMP + 2)}"),
+               I(f"v_add_u32 {vr(V_TMP + 2)}, {4 * mb}, {vr(V_ROW + 1)}"),
+               I(f"v_xor_b32 {vr(V_TMP + 1)}, {vr(V_TMP + 1)}, {vr(V_TMP + 2)}"),
+               I(f"v_lshlrev_b32 {vr(V_TMP + 1)}, 4, {vr(V_TMP + 1)}"),
+               I(f"v_lshl_add_u32 {vr(V_TMP)}, {vr(V_TMP)}, 8, {vr(V_TMP + 1)}"),
+               I(f"v_add_u32 {vr(V_TMP)}, {vr(V_TMP)}, {vr(V_ROW + 2)}"),
+               I(f"v_add_u32 {vr(VVA + mb * 2 + hi)}, 0x4000, {vr(V_TMP)}")])
+    # ---- transfers of tiles 0 and 1 into stages 0 and 1
+    e(I(f"s_mov_b32 {sr(S_TSLOT)}, 0"))
+    e(I(f"s_mov_b32 {sr(S_TT)}, 0"))
+    for _ in range(2):
+        e(transfer_setup(sr(S_TT)))
+        e(transfer_block("k"))
+        e(transfer_block("v"))
+        e([I(f"s_add_u32 {sr(S_TT)}, {sr(S_TT)}, 1"),
+           I(f"s_add_u32 {sr(S_TSLOT)}, {sr(S_TSLOT)}, 1")])
+    # ---- Q rows into AGPRs, rotated when rope_q
+    # Q resource base = q + b * q_sb + (kvh << gshift) * q_sh
+    e([I(f"s_lshl_b32 {sr(S_T3)}, {sr(S_KVH)}, {gs}")])
+    e([I(f"s_mul_i32 {T0}, {sr(S_B)}, {arg('q_sb')}"),
+       I(f"s_mul_hi_u32 {T1}, {sr(S_B)}, {arg('q_sb')}"),
+       I(f"s_mul_i32 {T2}, {sr(S_B)}, {arg('q_sb', True)}"),
+       I(f"s_add_u32 {T1}, {T1}, {T2}"),
+       I(f"s_add_u32 {sr(S_RQ)}, {arg('q')}, {T0}"),
+       I(f"s_addc_u32 {sr(S_RQ + 1)}, {arg('q', True)}, {T1}"),
+       I(f"s_mul_i32 {T0}, {T3}, {arg('q_sh')}"),
+       I(f"s_mul_hi_u32 {T1}, {T3}, {arg('q_sh')}"),
+       I(f"s_add_u32 {sr(S_RQ)}, {sr(S_RQ)}, {T0}"),
+       I(f"s_addc_u32 {sr(S_RQ + 1)}, {sr(S_RQ + 1)}, {T1}"),
+       I(f"s_and_b32 {sr(S_RQ + 1)}, {sr(S_RQ + 1)}, 0xffff"),
+       I(f"s_mov_b32 {sr(S_RQ + 2)}, {sr(S_QNREC)}"),
+       I(f"s_mov_b32 {sr(S_RQ + 3)}, 0x20000")])
+    # Q^T operands: Q rotated (rope_q) and scaled by c2, rounded once to bf16, into AGPRs.
+    # Loads: both blocks' Q rows first, then the (cos, sin) rows in four batches of four 16-dim
+    # chunks alternating between two register areas, each batch's rotation overlapping the next
+    # batch's loads.
+    RT = S_T0
+    qt = [SB[0], SB[1]]          # 32 registers of Q per block (8 chunks x 4)
+    cs_area = [PB[0], NB]        # 32 registers each: 4 chunks x 8 (cos, sin)
+    for rb in range(2):
+        for ks in range(8):
+            e(I(f"buffer_load_dwordx4 {vr(qt[rb] + 4 * ks, 4)}, {vr(V_QOFF + rb)}, {sr(S_RQ, 4)}, 0 "
+                f"offen offset:{32 * ks}"))
+    c2 = arg("c2")
+
+    def rotate_chunk(w0, cs0):
+        out = []
+        for j in range(4):
+            w = w0 + j
+            c, sn = cs0 + 2 * j, cs0 + 2 * j + 1
+            ev, od, t1 = V_TMP, V_TMP + 1, V_TMP + 2
+            out += [I(f"v_lshlrev_b32 {vr(ev)}, 16, {vr(w)}"),
+                    I(f"v_and_b32 {vr(od)}, 0xffff0000, {vr(w)}"),
+                    I(f"v_mul_f32 {vr(t1)}, {vr(od)}, {vr(sn)}"),
+                    I(f"v_fma_f32 {vr(t1)}, {vr(ev)}, {vr(c)}, -{vr(t1)}"),
+                    I(f"v_mul_f32 {vr(od)}, {vr(od)}, {vr(c)}"),
+                    I(f"v_fma_f32 {vr(od)}, {vr(ev)}, {vr(sn)}, {vr(od)}"),
+                    I(f"v_mul_f32 {vr(t1)}, {c2}, {vr(t1)}"),
+                    I(f"v_mul_f32 {vr(od)}, {c2}, {vr(od)}"),
+                    I(f"v_cvt_pk_bf16_f32 {vr(w)}, {vr(t1)}, {vr(od)}")]
+        return out
+
+    e(I(f"s_cmp_eq_u32 {arg('rope_q')}, 0"))
+    e(I("s_cbranch_scc1 .Lq_norope"))
+    e([I(f"s_mov_b32 {sr(RT)}, {arg('rope')}"),
+       I(f"s_and_b32 {sr(RT + 1)}, {arg('rope', True)}, 0xffff"),
+       I(f"s_mov_b32 {sr(RT + 2)}, {arg('rope_bytes')}"),
+       I(f"s_mov_b32 {sr(RT + 3)}, 0x20000")])
+
+    def cs_batch(bi):
+        rb, k0 = bi // 2, 4 * (bi % 2)
+        area = cs_area[bi % 2]
+        return [I(f"buffer_load_dwordx4 {vr(area + 8 * k + 4 * h, 4)}, {vr(V_CSOFF + rb)}, "
+                  f"{sr(RT, 4)}, 0 offen offset:{64 * (k0 + k) + 16 * h}")
+                for k in range(4) for h in range(2)]
+
+    e(cs_batch(0))
+    e(cs_batch(1))
+    for bi in range(4):
+        rb, k0 = bi // 2, 4 * (bi % 2)
+        e(I(f"s_waitcnt vmcnt({8 if bi < 3 else 0})"))
+        for k in range(4):
+            e(rotate_chunk(qt[rb] + 4 * (k0 + k), cs_area[bi % 2] + 8 * k))
+        if bi + 2 < 4:
+            e(cs_batch(bi + 2))
+    e(I("s_branch .Lq_done"))
+    e(I(".Lq_norope:"))
+    e(I("s_waitcnt vmcnt(0)"))
+    for rb in range(2):
+        for w in range(32):
+            r = qt[rb] + w
+            ev, od = V_TMP, V_TMP + 1
+            e([I(f"v_lshlrev_b32 {vr(ev)}, 16, {vr(r)}"),
+               I(f"v_and_b32 {vr(od)}, 0xffff0000, {vr(r)}"),
+               I(f"v_mul_f32 {vr(ev)}, {c2}, {vr(ev)}"),
+               I(f"v_mul_f32 {vr(od)}, {c2}, {vr(od)}"),
+               I(f"v_cvt_pk_bf16_f32 {vr(r)}, {vr(ev)}, {vr(od)}")])
+    e(I(".Lq_done:"))
+    e(I("s_waitcnt vmcnt(0)"))
+    for rb in range(2):
+        for w in range(32):
+            e(I(f"v_accvgpr_write_b32 {ar(A_Q + rb * 32 + w)}, {vr(qt[rb] + w)}"))
+    # ---- O = 0, running statistics
+    for i in range(128):
+        e(I(f"v_accvgpr_write_b32 {ar(A_O + i)}, 0"))
+    for rb in range(2):
+        e([I(f"v_mov_b32 {vr(V_M + rb)}, 0xff800000"),
+           I(f"v_mov_b32 {vr(V_L + rb)}, 0")])
+    e([I(f"v_mov_b32 {vr(NB + i)}, 0") for i in range(32)])
+    e(I(f"s_mov_b32 {sr(S_KSLOT)}, 0"))
+    e(I(f"s_mov_b32 {sr(S_VSLOT)}, 0"))
+    e(I("s_waitcnt vmcnt(0)"))
+    # tiles 2 .. NSTAGE - 2 (their waits come at the ends of the first iterations)
+    for _ in range(NSTAGE - 3):
+        e(transfer_setup(sr(S_TT)))
+        e(transfer_block("k"))
+        e(transfer_block("v"))
+        e([I(f"s_add_u32 {sr(S_TT)}, {sr(S_TT)}, 1"),
+           I(f"s_add_u32 {sr(S_TSLOT)}, {sr(S_TSLOT)}, 1")])
+    e(I("s_barrier"))
+
+
+def epilogue_store(gen: Gen):
+    e = gen.emit
+    # l_tot = l + l(partner); LSE = m * scale + ln l_tot; inv = 1 / l_tot
+    for rb in range(2):
+        a, b = V_MX, V_MX + 1
+        e([I(f"v_mov_b32 {vr(a)}, {vr(V_L + rb)}"),
+           I(f"v_mov_b32 {vr(b)}, {vr(V_L + rb)}"),
+           I(f"v_permlane32_swap_b32 {vr(a)}, {vr(b)}"),
+           I(f"v_cndmask_b32_e64 {vr(b)}, {vr(b)}, {vr(a)}, {sr(S_HIMASK, 2)}",
+             reads=[f"v{a}", f"v{b}", f"s{S_HIMASK}", f"s{S_HIMASK + 1}"], writes=[f"v{b}"]),
+           I(f"v_add_f32 {vr(V_L + rb)}, {vr(V_L + rb)}, {vr(b)}"),
+           I(f"v_rcp_f32 {vr(V_ALPHA + rb)}, {vr(V_L + rb)}"),
+           I(f"v_log_f32 {vr(V_U + rb)}, {vr(V_L + rb)}"),
+           I(f"v_add_f32 {vr(V_U + rb)}, {vr(V_U + rb)}, {vr(V_M + rb)}"),
+           I(f"v_mul_f32 {vr(V_U + rb)}, 0x3f317218, {vr(V_U + rb)}")])
+    # O/LSE resources
+    T0, T1, T2, T3 = (sr(S_T0), sr(S_T1), sr(S_T2), sr(S_T3))
+    gs = arg("gshift")
+
+    def res(dst, ptr, sb, sh, nrec):
+        return [I(f"s_lshl_b32 {T3}, {sr(S_KVH)}, {gs}"),
+                I(f"s_mul_i32 {T0}, {sr(S_B)}, {arg(sb)}"),
+                I(f"s_mul_hi_u32 {T1}, {sr(S_B)}, {arg(sb)}"),
+                I(f"s_mul_i32 {T2}, {sr(S_B)}, {arg(sb, True)}"),
+                I(f"s_add_u32 {T1}, {T1}, {T2}"),
+                I(f"s_add_u32 {sr(dst)}, {arg(ptr)}, {T0}"),
+                I(f"s_addc_u32 {sr(dst + 1)}, {arg(ptr, True)}, {T1}"),
+                I(f"s_mul_i32 {T0}, {T3}, {arg(sh)}"),
+                I(f"s_mul_hi_u32 {T1}, {T3}, {arg(sh)}"),
+                I(f"s_add_u32 {sr(dst)}, {sr(dst)}, {T0}"),
+                I(f"s_addc_u32 {sr(dst + 1)}, {sr(dst + 1)}, {T1}"),
+                I(f"s_and_b32 {sr(dst + 1)}, {sr(dst + 1)}, 0xffff"),
+                I(f"s_mov_b32 {sr(dst + 2)}, {sr(nrec)}"),
+                I(f"s_mov_b32 {sr(dst + 3)}, 0x20000")]
+    e(res(S_RQ, "o", "o_sb", "o_sh", S_ONREC))
+    e(res(S_RK, "lse", "lse_sb", "lse_sh", S_LNREC))
+    for rb in range(2):
+        e(I(f"buffer_store_dword {vr(V_U + rb)}, {vr(V_LOFF + rb)}, {sr(S_RK, 4)}, 0 offen"))
+    for rb in range(2):
+        for mb in range(4):
+            for q4 in range(4):
+                regs = [A_O + (rb * 4 + mb) * 16 + 4 * q4 + i for i in range(4)]
+                t = V_TMP
+                e([I(f"v_accvgpr_read_b32 {vr(t + i)}, {ar(a)}") for i, a in enumerate(regs)])
+                e([I(f"v_mul_f32 {vr(t + i)}, {vr(t + i)}, {vr(V_ALPHA + rb)}") for i in range(4)])
+                e([I(f"v_cvt_pk_bf16_f32 {vr(t + 4)}, {vr(t)}, {vr(t + 1)}"),
+                   I(f"v_cvt_pk_bf16_f32 {vr(t + 5)}, {vr(t + 2)}, {vr(t + 3)}")])
+                e(I(f"buffer_store_dwordx2 {vr(t + 4, 2)}, {vr(V_OOFF + rb)}, {sr(S_RQ, 4)}, 0 "
+                    f"offen offset:{mb * 64 + 16 * q4} nt"))
+    # next block of the persistent loop
+    e([I(f"s_add_u32 {sr(S_ROUND)}, {sr(S_ROUND)}, 1"), I("s_branch .Lblock")])
+
+
+# --------------------------------------------------------------------------- assembly of phases
+def build() -> Gen:
+    gen = Gen()
+    gen.exact = []  # out-of-line exact paths: (tag, x, hh, s_x, branch block, continuation block)
+    b_setup = gen.new_block("setup")
+    setup(gen)
+    b_block = gen.new_block("setup_block", [b_setup])
+    setup_block(gen)
+    # ---- prologue: S(0) alone, then S(1) with the exact softmax of half-tile 0 (sets m)
+    gen.new_block("prologue", [b_block])
+    gen.ds_outstanding = []
+    phase(gen, pv_x=None, pv_hh=0, s_x=0, s_hh=0, sm_x=None, sm_masked=False)
+    gen.ds_wait_all()
+    gen.emit(I(f"s_mov_b32 {sr(S_KEY0)}, 0"))
+    phase(gen, pv_x=None, pv_hh=0, s_x=1, s_hh=1, sm_x=None, sm_masked=False, prefetch_v_hh=0,
+          after_last_k=advance_slot(S_KSLOT, VKA, 8))
+    exact_path(gen, 0, 0, 1)
+    gen.emit([I(f"v_add_f32 {vr(V_L + rb)}, {vr(V_L + rb)}, {vr(V_LT + rb)}") for rb in range(2)])
+    # loop control
+    gen.emit([I(f"s_mov_b32 {sr(S_J)}, 0"),
+              I(f"s_cmp_ge_u32 {sr(S_J)}, {sr(S_JU)}"),
+              I("s_cbranch_scc1 .Lmasked_check")])
+    pro_end = gen.cur
+    firsts, lasts = {}, {}
+    for masked in (False, True):
+        name = "loop_m" if masked else "loop_u"
+        b = gen.new_block(name)
+        firsts[masked] = b
+        gen.emit(I(f".L{name}:"))
+        pre_ids = list(range(gen.ds_next, gen.ds_next + 2 * RV))
+        gen.ds_next += 2 * RV
+        gen.ds_outstanding = list(pre_ids)
+        ring_in = {"ready": {o: pre_ids[2 * o:2 * o + 2] for o in range(RV)}}
+        # iteration j: transfer of tile j + NSTAGE - 1 into the stage of tile j - 1
+        xfer = [I(f"s_add_u32 {sr(S_TT)}, {sr(S_J)}, {NSTAGE - 1}")] + \
+            transfer_setup(sr(S_TT)) + transfer_block("k") + transfer_block("v") + \
+            [I(f"s_add_u32 {sr(S_TSLOT)}, {sr(S_TSLOT)}, 1"),
+             I(f"s_cmp_eq_u32 {sr(S_TSLOT)}, {NSTAGE}"),
+             I(f"s_cselect_b32 {sr(S_TSLOT)}, 0, {sr(S_TSLOT)}")]
+        key_a = [I(f"s_lshl_b32 {sr(S_KEY0)}, {sr(S_J)}, 6"),
+                 I(f"s_add_u32 {sr(S_KEY0)}, {sr(S_KEY0)}, 32")]
+        # phase 2j+1: P.V(2j) (PB0, V half 0), S(2j+2) (SB0, K half 0), softmax(2j+1) (SB1)
+        ring = phase(gen, pv_x=0, pv_hh=0, s_x=0, s_hh=0, sm_x=1, sm_masked=masked,
+                     pre=key_a + xfer, vring_state=ring_in, prefetch_v_hh=1)
+        finish_phase(gen, f"{name}_a", 1, 1, 0)
+        key_b = [I(f"s_lshl_b32 {sr(S_KEY0)}, {sr(S_J)}, 6"),
+                 I(f"s_add_u32 {sr(S_KEY0)}, {sr(S_KEY0)}, 64")]
+        # phase 2j+2: P.V(2j+1) (PB1, V half 1), S(2j+3) (SB1, K half 1), softmax(2j+2) (SB0)
+        ring = phase(gen, pv_x=1, pv_hh=1, s_x=1, s_hh=1, sm_x=0, sm_masked=masked,
+                     pre=key_b, vring_state=ring,
+                     after_last_v=advance_slot(S_VSLOT, VVA, 8),
+                     after_last_k=advance_slot(S_KSLOT, VKA, 8), prefetch_v_hh=0)
+        finish_phase(gen, f"{name}_b", 0, 0, 1)
+        # tile j + 2 (first read by the next iteration) has landed: the NSTAGE - 3 younger
+        # tiles' transfers (8 instructions each) may still be in flight
+        gen.emit([I(f"s_waitcnt vmcnt({(NSTAGE - 3) * 8})"), I("s_barrier")])
+        lim = sr(S_JU) if not masked else sr(S_NM1)
+        gen.emit([I(f"s_add_u32 {sr(S_J)}, {sr(S_J)}, 1"),
+                  I(f"s_cmp_lt_u32 {sr(S_J)}, {lim}"),
+                  I(f"s_cbranch_scc1 .L{name}")])
+        lasts[masked] = gen.cur
+        if not masked:
+            gen.new_block("masked_check")
+            gen.emit([I(".Lmasked_check:"),
+                      I(f"s_cmp_ge_u32 {sr(S_J)}, {sr(S_NM1)}"),
+                      I("s_cbranch_scc1 .Lepi")])
+    b_mc = [b for b in gen.blocks if b.name == "masked_check"][0]
+    firsts[False].preds = [pro_end, lasts[False]]
+    b_mc.preds = [pro_end, lasts[False]]
+    firsts[True].preds = [b_mc, lasts[True]]
+    # ---- epilogue phases: P.V(2n-2) + softmax(2n-1) (masked), then P.V(2n-1)
+    gen.new_block("epi", [pro_end, b_mc, lasts[True]])
+    gen.emit(I(".Lepi:"))
+    pre_ids = list(range(gen.ds_next, gen.ds_next + 2 * RV))
+    gen.ds_next += 2 * RV
+    gen.ds_outstanding = list(pre_ids)
+    ring_in = {"ready": {o: pre_ids[2 * o:2 * o + 2] for o in range(RV)}}
+    key_e = [I(f"s_lshl_b32 {sr(S_KEY0)}, {sr(S_NM1)}, 6"),
+             I(f"s_add_u32 {sr(S_KEY0)}, {sr(S_KEY0)}, 32")]
+    ring = phase(gen, pv_x=0, pv_hh=0, s_x=None, s_hh=0, sm_x=1, sm_masked=True,
+                 pre=key_e, vring_state=ring_in, prefetch_v_hh=1)
+    finish_phase(gen, "epi_a", 1, 1, None)
+    ring = phase(gen, pv_x=1, pv_hh=1, s_x=None, s_hh=0, sm_x=None, sm_masked=False,
+                 vring_state=ring)
+    gen.ds_wait_all()
+    epilogue_store(gen)
+    b_block.preds.append(gen.cur)
+    # ---- the out-of-line exact paths
+    for tag, x, hh, s_x, br, cont in gen.exact:
+        b = gen.new_block(f"exact_{tag}", [br])
+        gen.emit(I(f".Lexact_{tag}:"))
+        gen.ds_outstanding = [-1] * (2 * RV)
+        exact_path(gen, x, hh, s_x)
+        gen.emit(I(f"s_branch .Lcont_{tag}"))
+        cont.preds.append(b)
+    return gen
+
+
+def finish_phase(gen: Gen, tag: str, x: int, hh: int, s_x) -> None:
+    """End of a phase with a fast softmax: to the exact path when a row sum overflowed, then
+    l += the half-tile's row sums."""
+    gen.emit([I(f"s_cmp_lg_u64 {sr(S_MV, 2)}, 0"), I(f"s_cbranch_scc1 .Lexact_{tag}")])
+    br = gen.cur
+    cont = gen.new_block(f"cont_{tag}", [br])
+    gen.emit(I(f".Lcont_{tag}:"))
+    gen.emit([I(f"v_add_f32 {vr(V_L + rb)}, {vr(V_L + rb)}, {vr(V_LT + rb)}") for rb in range(2)])
+    gen.exact.append((tag, x, hh, s_x, br, cont))
+
+
+# --------------------------------------------------------------------------- output
+def render(gen: Gen) -> str:
+    # split the straight-line blocks at conditional branches for the hazard check: the
+    # rescale block is optional; check both with and without it by treating labels as joins.
+    fix_hazards(gen.blocks)
+    lines = []
+    lines.append('\t.amdgcn_target "amdgcn-amd-amdhsa--gfx950"')
+    lines.append("\t.amdhsa_code_object_version 5")
+    lines.append("\t.text")
+    lines.append(f"\t.globl {KERNEL}")
+    lines.append("\t.p2align 8")
+    lines.append(f"\t.type {KERNEL},@function")
+    lines.append(f"{KERNEL}:")
+    for b in gen.blocks:
+        for x in b.ins:
+            if x.kind == "nop":
+                lines.append("\t" + x.text)
+                continue
+            n = x.nops
+            while n > 0:
+                k = min(n, 16)
+                lines.append(f"\ts_nop {k - 1}")
+                n -= k
+            if x.kind == "label":
+                lines.append(x.text)
+            else:
+                lines.append("\t" + x.text)
+    lines.append(f".Lfunc_end:")
+    lines.append(f"\t.size {KERNEL}, .Lfunc_end-{KERNEL}")
+    lines.append("")
+    lines.append("\t.rodata")
+    lines.append("\t.p2align 6")
+    lines.append(f"\t.amdhsa_kernel {KERNEL}")
+    lines.append(f"\t\t.amdhsa_group_segment_fixed_size {LDS_BYTES}")
+    lines.append("\t\t.amdhsa_private_segment_fixed_size 0")
+    lines.append(f"\t\t.amdhsa_kernarg_size {ARG_BYTES}")
+    lines.append("\t\t.amdhsa_user_sgpr_count 2")
+    lines.append("\t\t.amdhsa_user_sgpr_kernarg_segment_ptr 1")
+    lines.append("\t\t.amdhsa_system_sgpr_workgroup_id_x 1")
+    lines.append("\t\t.amdhsa_system_vgpr_workitem_id 0")
+    acc_off = (NUM_VGPR + 3) // 4 * 4
+    lines.append(f"\t\t.amdhsa_next_free_vgpr {acc_off + NUM_AGPR}")
+    lines.append(f"\t\t.amdhsa_next_free_sgpr {NUM_SGPR}")
+    lines.append(f"\t\t.amdhsa_accum_offset {acc_off}")
+    lines.append("\t\t.amdhsa_reserve_vcc 1")
+    lines.append("\t\t.amdhsa_float_denorm_mode_32 3")
+    lines.append("\t\t.amdhsa_float_denorm_mode_16_64 3")
+    lines.append("\t\t.amdhsa_ieee_mode 1")
+    lines.append("\t\t.amdhsa_dx10_clamp 1")
+    lines.append("\t.end_amdhsa_kernel")
+    lines.append("")
+    lines.append("\t.amdgpu_metadata")
+    lines.append("---")
+    lines.append("amdhsa.kernels:")
+    lines.append(f"  - .agpr_count:     {NUM_AGPR}")
+    lines.append("    .args:")
+    lines.append("      - .offset:         0")
+    lines.append(f"        .size:           {ARG_BYTES}")
+    lines.append("        .value_kind:     by_value")
+    lines.append(f"    .group_segment_fixed_size: {LDS_BYTES}")
+    lines.append("    .kernarg_segment_align: 8")
+    lines.append(f"    .kernarg_segment_size: {ARG_BYTES}")
+    lines.append("    .max_flat_workgroup_size: 256")
+    lines.append(f"    .name:           {KERNEL}")
+    lines.append("    .private_segment_fixed_size: 0")
+    lines.append(f"    .sgpr_count:     {NUM_SGPR + 2}")
+    lines.append(f"    .symbol:         {KERNEL}.kd")
+    lines.append(f"    .vgpr_count:     {acc_off + NUM_AGPR}")
+    lines.append("    .wavefront_size: 64")
+    lines.append("amdhsa.target:   amdgcn-amd-amdhsa--gfx950")
+    lines.append("amdhsa.version:")
+    lines.append("  - 1")
+    lines.append("  - 2")
+    lines.append("...")
+    lines.append("\t.end_amdgpu_metadata")
+    return "\n".join(lines) + "\n"
+
+
+def fix_hazards_with_optional(blocks: list[Block]):
+    """Hazard check over every path: block predecessors, plus inside a block the optional
+    rescale sequences (between 's_cbranch_scc1 .Lnors_X' and '.Lnors_X:') taken or skipped."""
+    def variants(seq: list[Ins]) -> list[list[Ins]]:
+        out = [[]]
+        i = 0
+        while i < len(seq):
+            x = seq[i]
+            if x.text.startswith("s_cbranch_scc1 .Lnors_"):
+                tag = x.text.split()[1]
+                j = i + 1
+                while not seq[j].text.startswith(tag + ":"):
+                    j += 1
+                opt = seq[i + 1:j]
+                out = [v + [x] + opt for v in out] + [v + [x] for v in out]
+                i = j
+                continue
+            out = [v + [x] for v in out]
+            i += 1
+        # cap the combinations: keep all-taken, all-skipped and single toggles
+        return out[:8]
+
+    for _ in range(3):
+        for b in blocks:
+            for t in tails(b):
+                for v in variants(b.ins):
+                    check_path(t + v, len(t))
+
+
+def header(path: str):
+    lines = ["// Generated by gen_prefill_a64.py: kernel-argument layout of fa_prefill_a64_bf16.",
+             "#pragma once", f"#define FA_A64_ARG_BYTES {ARG_BYTES}",
+             f"#define FA_A64_LDS_BYTES {LDS_BYTES}",
+             f'#define FA_A64_KERNEL "{KERNEL}"']
+    for n, off, sz in ARGS:
+        lines.append(f"#define FA_A64_OFF_{n.upper()} {off}")
+    open(path, "w").write("\n".join(lines) + "\n")
+
+
+def blob(co_path: str, out_cpp: str):
+    data = open(co_path, "rb").read()
+    rows = [", ".join(f"0x{b:02x}" for b in data[i:i + 16]) for i in range(0, len(data), 16)]
+    text = ("// Generated by gen_prefill_a64.py --blob: the assembled gfx950 code object of "
+            "fa_prefill_a64_bf16.\n#include <stddef.h>\nnamespace fa {\n"
+            f"extern const unsigned char kPrefillA64Co[] = {{\n" + ",\n".join(rows) +
+            f"\n}};\nextern const size_t kPrefillA64CoSize = {len(data)};\n}}  // namespace fa\n")
+    open(out_cpp, "w").write(text)
+
+
+def main():
+    if sys.argv[1] == "--blob":
+        blob(sys.argv[2], sys.argv[3])
+        return
+    out_s, out_h = sys.argv[1], sys.argv[2]
+    gen = build()
+    open(out_s, "w").write(render(gen))
+    header(out_h)
+
+
+if __name__ == "__main__":
+    main()

@@ -187,6 +187,9 @@ struct fa_ctx {
     // 16-bit RoPE prefill scores: 0 = rotated Q/K rounded to the storage type, 1 = split
     // high/residual operands (fa_ctx_set_prefill_precision)
     int prefill_precision = 0;
+    // 16-bit contiguous prefill main loop: -1 automatic (the assembly kernel where it applies),
+    // 0 the HIP kernels only (fa_ctx_set_prefill_kernel)
+    int prefill_kernel_policy = -1;
     // the stream is being captured into a graph (fa_graph_capture_begin)
     bool capturing = false;
     // decode work layout: -1 automatic (head-grouped workgroups where they apply), 0 one-wave
@@ -550,6 +553,9 @@ int fa_ctx_create(int device, fa_ctx** out) {
     // set-up of the allocation-free decode (device current): the scratch address of this
     // device and the host staging area; a failure here surfaces at that entry point
     if (fa::noalloc_scratch(device, &ctx->na_scratch) != hipSuccess) ctx->na_scratch = nullptr;
+    // the assembly prefill's code object (a load failure leaves the HIP kernels in use, which
+    // the telemetry's kernel name shows)
+    (void)fa::prefill_a64_load(device);
     if (hipEventCreateWithFlags(&ctx->na_copied, hipEventDisableTiming) != hipSuccess)
         ctx->na_copied = nullptr;
     if (hipHostMalloc((void**)&ctx->na_host, kNoAllocMetaBytes, hipHostMallocDefault) !=
@@ -678,6 +684,12 @@ int fa_ctx_set_prefill_precision(fa_ctx* ctx, int32_t mode) {
     if (mode != 0 && mode != 1)
         return fail(FA_ERR_UNAVAILABLE, "prefill precision mode %d is not one of 0, 1", (int)mode);
     ctx->prefill_precision = mode;
+    return ok();
+}
+
+int fa_ctx_set_prefill_kernel(fa_ctx* ctx, int32_t assembly) {
+    if (!ctx) return fail(FA_ERR_NULL_ARGUMENT, "context is null");
+    ctx->prefill_kernel_policy = assembly < 0 ? -1 : (assembly ? 1 : 0);
     return ok();
 }
 
@@ -945,7 +957,9 @@ int resolve_prefill(fa_ctx* ctx, PrefillJob& j, bool own, PrefillRun* r) {
         prerot = c.prerot;
         // precise scores: K rotated in the kernel, which keeps its 16-bit residual
         if (c.split_qk) r->j.a.split_qk = 1;
+        r->j.a.rope_rows = (int)j.max_pos;
     }
+    r->j.a.a64 = ctx->prefill_kernel_policy == 1;
     r->prerot = prerot;
     if (prerot) {
         if (own) {
@@ -991,7 +1005,9 @@ void describe_prefill(const fa_ctx* ctx, const PrefillJob& j, const fa::PrefillA
     if (j.rope && a.rope_k && !prerot && !j.paged && a.head_dim % 8 != 0)
         fb = "K pre-rotation pass needs head_dim % 8 == 0; K rotated on load";
     const char* dt = j.dtype == FA_DTYPE_BF16 ? "bf16" : j.dtype == FA_DTYPE_F16 ? "f16" : "f32";
-    const char* base = j.dtype == FA_DTYPE_F32 ? "prefill_mfma_f32" : "prefill_mfma16";
+    const bool a64 = fa::prefill_a64_eligible(j.dt, j.paged, a);
+    const char* base =
+        j.dtype == FA_DTYPE_F32 ? "prefill_mfma_f32" : (a64 ? "prefill_a64" : "prefill_mfma16");
     char name[64];
     if (prerot || vt)
         snprintf(name, sizeof name, "%s%s%s<%s>", prerot ? "rotate_rows + " : "",
@@ -1182,6 +1198,9 @@ int fa_forward_gqa_rope_telemetry(fa_ctx* ctx, const fa_grouped_shape* sh, const
     if (c.prerot) a.rope_k = 0;
     if (c.split_qk) a.split_qk = 1;
     a.vt = c.vt ? (const void*)1 : nullptr;
+    a.a64 = ctx->prefill_kernel_policy == 1;
+    a.rope_rows = (int)j.max_pos;
+    if (j.rope) a.rope_table = (const float2*)(uintptr_t)16;  // stands for the table the call builds
     describe_prefill(ctx, j, a, c.prerot, c.vt, 1u + c.prerot + c.vt, allocs, bytes, out);
     return ok();
 }

@@ -48,7 +48,23 @@ struct PrefillArgs {
     // 16-bit contiguous K rotated on load only: carry the rotated Q and K as 16-bit high part +
     // 16-bit residual and take three MFMAs per score block (f32-level scores).
     int split_qk;
+    // Allow the assembly main loop (fa_prefill_a64_bf16) where it applies (prefill_a64_eligible).
+    int a64;
+    // Rows of rope_table (positions it covers); bounds the assembly kernel's table reads.
+    int rope_rows;
 };
+
+// The assembly prefill (64 query rows per wave, code object loaded per device): bf16, Q rotated
+// in the kernel (RoPE), contiguous K/V of 128 dims not rotated in the kernel, power-of-two GQA
+// group, no variable-length metadata,
+// 16-byte aligned rows and slices addressable with 32-bit offsets, module loaded on the current
+// device.
+bool prefill_a64_eligible(Dtype dt, bool paged, const PrefillArgs& a);
+// Loads the code object on `device` (current); idempotent. Failure leaves the HIP kernels in use.
+hipError_t prefill_a64_load(int device);
+void launch_prefill_a64(const PrefillArgs& a, hipStream_t s, unsigned grid[3], unsigned* block);
+// Workgroups of its persistent grid: min(query blocks, CUs of the current device).
+unsigned prefill_a64_workgroups(const PrefillArgs& a);
 
 void launch_prefill(Dtype dt, bool paged, const PrefillArgs& a, hipStream_t s,
                     unsigned grid[3], unsigned* block);

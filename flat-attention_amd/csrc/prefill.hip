@@ -1311,6 +1311,13 @@ static void launch32(const PrefillKArgs& ka, int dpad, dim3 grid, hipStream_t s)
 
 void prefill_geometry(Dtype dt, bool paged, const PrefillArgs& a, unsigned grid[3],
                       unsigned* block, unsigned* rows) {
+    if (prefill_a64_eligible(dt, paged, a)) {  // assembly kernel: 4 waves x 64 rows, persistent
+        grid[0] = prefill_a64_workgroups(a);
+        grid[1] = grid[2] = 1;
+        *block = 256;
+        *rows = 256;
+        return;
+    }
     // 16-bit contiguous K/V without in-kernel K rotation runs 256-row ping-pong workgroups
     const bool pp = dt != Dtype::F32 && !a.rope_k && (!paged || a.page_size % 16 == 0);
     const int bm = pp ? 256 : 128;
@@ -1328,6 +1335,10 @@ void launch_prefill(Dtype dt, bool paged, const PrefillArgs& a, hipStream_t s, u
     ka.a = a;
     if (paged) ka.ps = FastDiv((uint32_t)a.page_size);
     const int dpad = a.head_dim <= 32 ? 32 : (a.head_dim <= 64 ? 64 : 128);
+    if (prefill_a64_eligible(dt, paged, a)) {
+        launch_prefill_a64(a, s, grid, block);
+        return;
+    }
     unsigned rows;
     prefill_geometry(dt, paged, a, grid, block, &rows);
     dim3 g(grid[0]);

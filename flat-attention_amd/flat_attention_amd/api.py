@@ -271,6 +271,11 @@ class HipContext:
     def set_prefill_policy(self, prerotate_k: int):
         check(lib().fa_ctx_set_prefill_policy(self.handle, prerotate_k))
 
+    def set_prefill_kernel(self, assembly: int):
+        """-1 automatic (the assembly main loop fa_prefill_a64_bf16 where it applies), 0 the
+        HIP prefill kernels only."""
+        check(lib().fa_ctx_set_prefill_kernel(self.handle, assembly))
+
     def set_decode_policy(self, grouped: int):
         """-1 automatic decode work layout (head-grouped workgroups where they apply), 0 one-wave
         workgroups; read when a PagedDecodePlan is prepared."""
