@@ -93,7 +93,8 @@ def arg64(name: str) -> str:
 
 
 KERNEL = "fa_prefill_a64_bf16"
-NSTAGE = 4            # LDS stages of (K 16 KiB, V 16 KiB): tiles j .. j + NSTAGE - 1 resident
+NSTAGE = 5            # LDS stages of (K 16 KiB, V 16 KiB): tiles j .. j + NSTAGE - 1 resident
+PAIR = True           # one barrier per two iterations (needs NSTAGE = 5)
 LDS_BYTES = NSTAGE * 32768
 INVALID_OFF = 0x80000000  # beyond every resource range used for stores
 
@@ -1040,7 +1041,7 @@ def setup_block(gen: Gen):
     # ---- transfers of tiles 0 and 1 into stages 0 and 1
     e(I(f"s_mov_b32 {sr(S_TSLOT)}, 0"))
     e(I(f"s_mov_b32 {sr(S_TT)}, 0"))
-    for _ in range(2):
+    for _ in range(3 if PAIR else 2):
         e(transfer_setup(sr(S_TT)))
         e(transfer_block("k"))
         e(transfer_block("v"))
@@ -1143,7 +1144,7 @@ def setup_block(gen: Gen):
     e(I(f"s_mov_b32 {sr(S_VSLOT)}, 0"))
     e(I("s_waitcnt vmcnt(0)"))
     # tiles 2 .. NSTAGE - 2 (their waits come at the ends of the first iterations)
-    for _ in range(NSTAGE - 3):
+    for _ in range(0 if PAIR else NSTAGE - 3):
         e(transfer_setup(sr(S_TT)))
         e(transfer_block("k"))
         e(transfer_block("v"))
@@ -1223,11 +1224,44 @@ def build() -> Gen:
           after_last_k=advance_slot(S_KSLOT, VKA, 8))
     exact_path(gen, 0, 0, 1)
     gen.emit([I(f"v_add_f32 {vr(V_L + rb)}, {vr(V_L + rb)}, {vr(V_LT + rb)}") for rb in range(2)])
-    # loop control
+    pro_end = gen.cur
+    if PAIR:
+        epi_preds = pair_loops(gen, pro_end)
+    else:
+        epi_preds = single_loops(gen, pro_end)
+    # ---- epilogue phases: P.V(2n-2) + softmax(2n-1) (masked), then P.V(2n-1)
+    gen.new_block("epi", epi_preds)
+    gen.emit(I(".Lepi:"))
+    pre_ids = list(range(gen.ds_next, gen.ds_next + 2 * RV))
+    gen.ds_next += 2 * RV
+    gen.ds_outstanding = list(pre_ids)
+    ring_in = {"ready": {o: pre_ids[2 * o:2 * o + 2] for o in range(RV)}}
+    key_e = [I(f"s_lshl_b32 {sr(S_KEY0)}, {sr(S_NM1)}, 6"),
+             I(f"s_add_u32 {sr(S_KEY0)}, {sr(S_KEY0)}, 32")]
+    ring = phase(gen, pv_x=0, pv_hh=0, s_x=None, s_hh=0, sm_x=1, sm_masked=True,
+                 pre=key_e, vring_state=ring_in, prefetch_v_hh=1)
+    finish_phase(gen, "epi_a", 1, 1, None)
+    ring = phase(gen, pv_x=1, pv_hh=1, s_x=None, s_hh=0, sm_x=None, sm_masked=False,
+                 vring_state=ring)
+    gen.ds_wait_all()
+    epilogue_store(gen)
+    b_block.preds.append(gen.cur)
+    # ---- the out-of-line exact paths
+    for tag, x, hh, s_x, br, cont in gen.exact:
+        b = gen.new_block(f"exact_{tag}", [br])
+        gen.emit(I(f".Lexact_{tag}:"))
+        gen.ds_outstanding = [-1] * (2 * RV)
+        exact_path(gen, x, hh, s_x)
+        gen.emit(I(f"s_branch .Lcont_{tag}"))
+        cont.preds.append(b)
+    return gen
+
+
+def single_loops(gen: Gen, pro_end: Block) -> list:
+    """One barrier per iteration (NSTAGE >= 3 stages)."""
     gen.emit([I(f"s_mov_b32 {sr(S_J)}, 0"),
               I(f"s_cmp_ge_u32 {sr(S_J)}, {sr(S_JU)}"),
               I("s_cbranch_scc1 .Lmasked_check")])
-    pro_end = gen.cur
     firsts, lasts = {}, {}
     for masked in (False, True):
         name = "loop_m" if masked else "loop_u"
@@ -1275,32 +1309,85 @@ def build() -> Gen:
     firsts[False].preds = [pro_end, lasts[False]]
     b_mc.preds = [pro_end, lasts[False]]
     firsts[True].preds = [b_mc, lasts[True]]
-    # ---- epilogue phases: P.V(2n-2) + softmax(2n-1) (masked), then P.V(2n-1)
-    gen.new_block("epi", [pro_end, b_mc, lasts[True]])
-    gen.emit(I(".Lepi:"))
+    return [pro_end, b_mc, lasts[True]]
+
+
+def iteration(gen: Gen, masked: bool, tag: str, jofs: int, ring_in, xfer_tile_ofs):
+    """One loop iteration j = S_J + jofs (phases 2j+1, 2j+2), optionally issuing the transfer of
+    tile S_J + xfer_tile_ofs at its start. Returns the V ring state after it."""
+    xfer = []
+    if xfer_tile_ofs is not None:
+        xfer = [I(f"s_add_u32 {sr(S_TT)}, {sr(S_J)}, {xfer_tile_ofs}")] + \
+            transfer_setup(sr(S_TT)) + transfer_block("k") + transfer_block("v") + \
+            [I(f"s_add_u32 {sr(S_TSLOT)}, {sr(S_TSLOT)}, 1"),
+             I(f"s_cmp_eq_u32 {sr(S_TSLOT)}, {NSTAGE}"),
+             I(f"s_cselect_b32 {sr(S_TSLOT)}, 0, {sr(S_TSLOT)}")]
+    key_a = [I(f"s_lshl_b32 {sr(S_KEY0)}, {sr(S_J)}, 6"),
+             I(f"s_add_u32 {sr(S_KEY0)}, {sr(S_KEY0)}, {64 * jofs + 32}")]
+    ring = phase(gen, pv_x=0, pv_hh=0, s_x=0, s_hh=0, sm_x=1, sm_masked=masked,
+                 pre=key_a + xfer, vring_state=ring_in, prefetch_v_hh=1)
+    finish_phase(gen, f"{tag}_a", 1, 1, 0)
+    key_b = [I(f"s_lshl_b32 {sr(S_KEY0)}, {sr(S_J)}, 6"),
+             I(f"s_add_u32 {sr(S_KEY0)}, {sr(S_KEY0)}, {64 * jofs + 64}")]
+    ring = phase(gen, pv_x=1, pv_hh=1, s_x=1, s_hh=1, sm_x=0, sm_masked=masked,
+                 pre=key_b, vring_state=ring,
+                 after_last_v=advance_slot(S_VSLOT, VVA, 8),
+                 after_last_k=advance_slot(S_KSLOT, VKA, 8), prefetch_v_hh=0)
+    finish_phase(gen, f"{tag}_b", 0, 0, 1)
+    return ring
+
+
+def ring_entry(gen: Gen):
     pre_ids = list(range(gen.ds_next, gen.ds_next + 2 * RV))
     gen.ds_next += 2 * RV
     gen.ds_outstanding = list(pre_ids)
-    ring_in = {"ready": {o: pre_ids[2 * o:2 * o + 2] for o in range(RV)}}
-    key_e = [I(f"s_lshl_b32 {sr(S_KEY0)}, {sr(S_NM1)}, 6"),
-             I(f"s_add_u32 {sr(S_KEY0)}, {sr(S_KEY0)}, 32")]
-    ring = phase(gen, pv_x=0, pv_hh=0, s_x=None, s_hh=0, sm_x=1, sm_masked=True,
-                 pre=key_e, vring_state=ring_in, prefetch_v_hh=1)
-    finish_phase(gen, "epi_a", 1, 1, None)
-    ring = phase(gen, pv_x=1, pv_hh=1, s_x=None, s_hh=0, sm_x=None, sm_masked=False,
-                 vring_state=ring)
-    gen.ds_wait_all()
-    epilogue_store(gen)
-    b_block.preds.append(gen.cur)
-    # ---- the out-of-line exact paths
-    for tag, x, hh, s_x, br, cont in gen.exact:
-        b = gen.new_block(f"exact_{tag}", [br])
-        gen.emit(I(f".Lexact_{tag}:"))
-        gen.ds_outstanding = [-1] * (2 * RV)
-        exact_path(gen, x, hh, s_x)
-        gen.emit(I(f"s_branch .Lcont_{tag}"))
-        cont.preds.append(b)
-    return gen
+    return {"ready": {o: pre_ids[2 * o:2 * o + 2] for o in range(RV)}}
+
+
+def pair_loops(gen: Gen, pro_end: Block) -> list:
+    """Iterations in pairs (j, j+1) with one barrier per pair: the pair issues the transfers of
+    tiles j+3 and j+4 (into the stages of tiles j-2 and j-1, dead since the previous barrier) and
+    waits for both before its closing barrier; tiles j+2 .. j+4 are then resident for the next
+    pair. Unmasked pairs while j + 2 <= JU, masked pairs while j + 2 <= n - 1, then at most one
+    single (masked) iteration with no transfer (the tiles it reads landed by the last barrier)."""
+    J, JU, NM1, T0 = sr(S_J), sr(S_JU), sr(S_NM1), sr(S_T0)
+    gen.emit([I(f"s_mov_b32 {J}, 0")])
+    blocks = {}
+    for masked in (False, True):
+        name = "pair_m" if masked else "pair_u"
+        lim = NM1 if masked else JU
+        chk = gen.new_block(f"{name}_check")
+        blocks[f"{name}_check"] = chk
+        gen.emit([I(f".L{name}_check:"),
+                  I(f"s_add_u32 {T0}, {J}, 2"),
+                  I(f"s_cmp_gt_u32 {T0}, {lim}"),
+                  I(f"s_cbranch_scc1 .L{name}_done")])
+        body = gen.new_block(name, [chk])
+        blocks[name] = body
+        ring = ring_entry(gen)
+        ring = iteration(gen, masked, f"{name}0", 0, ring, 3)
+        ring = iteration(gen, masked, f"{name}1", 1, ring, 4)
+        gen.emit([I("s_waitcnt vmcnt(0)"), I("s_barrier"),
+                  I(f"s_add_u32 {J}, {J}, 2"),
+                  I(f"s_branch .L{name}_check")])
+        blocks[f"{name}_end"] = gen.cur
+        gen.new_block(f"{name}_done_blk")
+        blocks[f"{name}_done_blk"] = gen.cur
+        gen.emit(I(f".L{name}_done:"))
+    # one single iteration when an odd number remains
+    gen.emit([I(f"s_cmp_ge_u32 {J}, {NM1}"), I("s_cbranch_scc1 .Lepi")])
+    single_chk = gen.cur
+    sb = gen.new_block("single", [single_chk])
+    ring = ring_entry(gen)
+    iteration(gen, True, "single", 0, ring, None)
+    single_end = gen.cur
+    blocks["pair_u_check"].preds = [pro_end, blocks["pair_u_end"]]
+    blocks["pair_u"].preds = [blocks["pair_u_check"]]
+    blocks["pair_m_check"].preds = [blocks["pair_u_done_blk"], blocks["pair_m_end"]]
+    blocks["pair_u_done_blk"].preds = [blocks["pair_u_check"]]
+    blocks["pair_m"].preds = [blocks["pair_m_check"]]
+    blocks["pair_m_done_blk"].preds = [blocks["pair_m_check"]]
+    return [single_chk, single_end]
 
 
 def finish_phase(gen: Gen, tag: str, x: int, hh: int, s_x) -> None:
