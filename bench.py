@@ -156,9 +156,9 @@ def build_decode(ctx, rng, split=None):
 PEAK_F32_TFLOPS = 157.3    # MI355X dense fp32 matrix
 
 
-def build_mha_f32(ctx, rng, causal):
-    """MHA B4 H16 N2048 D128, f32 I/O."""
-    B, H, S, D = 4, 16, 2048, 128
+def build_mha_f32(ctx, rng, causal, shape=(4, 16, 2048, 128)):
+    """MHA B4 H16 N2048 D128, f32 I/O (configs[0] with shape=(1, 2, 128, 64))."""
+    B, H, S, D = shape
     shape = fa.AttentionShape(B, H, S, D)
     ex = fa.HipFlatAttention(ctx)
     mk = lambda: fa.DeviceBuffer.from_array(ctx, rng.standard_normal(B * H * S * D, dtype=np.float32))  # noqa: E731
@@ -344,8 +344,89 @@ def graph_replay_ms(ctx, ev, run, steps=20):
     return ms
 
 
+def _rec(kernel, op_ms, k_ms, work, bound, peak, unit, traffic=None, **extra):
+    """A sub-record: op and kernel times, the rate over the whole op and the kernel's roofline."""
+    rate_op = work / (op_ms * 1e-3) / (1e12 if unit == "TFLOP/s" else 1e9)
+    rate_k = work / (k_ms * 1e-3) / (1e12 if unit == "TFLOP/s" else 1e9)
+    return {"kernel": kernel, "ms": round(op_ms, 5), "kernel_ms": round(k_ms, 5),
+            unit: round(rate_op, 2),
+            "roofline": {"bound": bound, "achieved": round(rate_k, 2), "peak": peak,
+                         "unit": unit, "frac": round(rate_k / peak, 4), "traffic": traffic},
+            **extra}
+
+
+def measure_baseline_configs(ctx, ev, rng, steps, with_cpu, warm=100):
+    """Every other BASELINE config (and the two alternative cfg3 prefill kernels), each timed
+    alone after `warm` untimed calls: op time from HIP events, the dominant kernel's time from
+    the library's per-dispatch events, a roofline, and the CPU oracle timed on a bounded sample
+    of the same workload (single core)."""
+    res = {}
+
+    def timed(run):
+        for _ in range(warm):
+            run()
+        tel = ctx.last_telemetry()
+        ctx.synchronize()
+        op_ms = alternate_timing(ctx, ev, run, steps)
+        total, cnt = ctx.kernel_timing(tel.kernel_id)
+        ctx.set_kernel_timing(False)
+        return op_ms, total / max(cnt, 1), tel
+
+    cpu = cpu_baseline_configs() if with_cpu else {}
+    # configs[0]: the reference's CPU-runnable case (MHA B1 H2 N128 D64 causal f32)
+    run, flop = build_mha_f32(ctx, rng, True, shape=(1, 2, 128, 64))
+    op_ms, k_ms, tel = timed(run)
+    res["cfg1_mha_f32_causal_B1_H2_N128_D64"] = _rec(
+        tel.kernel_name, op_ms, k_ms, flop, "mfma", PEAK_F32_TFLOPS, "TFLOP/s",
+        note="launch-bound: 4.2 MFLOP", cpu_baseline=cpu.get("cfg1"))
+    # configs[1]: MHA B4 H16 N2048 D128 f32, causal and non-causal
+    for causal in (False, True):
+        run, flop = build_mha_f32(ctx, rng, causal)
+        op_ms, k_ms, tel = timed(run)
+        key = "causal" if causal else "noncausal"
+        res[f"cfg2_mha_f32_{key}_B4_H16_N2048_D128"] = _rec(
+            tel.kernel_name, op_ms, k_ms, flop, "mfma", PEAK_F32_TFLOPS, "TFLOP/s",
+            cpu_baseline=cpu.get(f"cfg2_{key}"))
+    # configs[2] with the alternatives to the default prefill kernel
+    ctx.set_prefill_precision(1)
+    run, flop, _ = build_prefill(ctx, rng)
+    op_ms, k_ms, tel = timed(run)
+    res["cfg3_prefill_precise_scores"] = _rec(
+        tel.kernel_name, op_ms, k_ms, flop, "mfma", PEAK_BF16_TFLOPS, "TFLOP/s",
+        note="fa_ctx_set_prefill_precision(1): rotated Q and K carried as a 16-bit high part "
+             "plus the residual, three Q.K^T MFMAs per k-step (f32-level scores; holds 2e-2 on "
+             "the adversarial RoPE corpus)")
+    ctx.set_prefill_precision(0)
+    ctx.set_prefill_kernel(1)
+    run, flop, _ = build_prefill(ctx, rng)
+    op_ms, k_ms, tel = timed(run)
+    res["cfg3_prefill_assembly_main_loop"] = _rec(
+        tel.kernel_name, op_ms, k_ms, flop, "mfma", PEAK_BF16_TFLOPS, "TFLOP/s",
+        note="fa_ctx_set_prefill_kernel(1): the generated gfx950 assembly kernel (64 query rows "
+             "per wave, persistent grid); opt-in")
+    ctx.set_prefill_kernel(-1)
+    # configs[4]: chunked prefill into the paged cache (+ the batched append of the chunk)
+    run, flop, append, append_bytes = build_chunked_paged(ctx, rng)
+    op_ms, k_ms, tel = timed(run)
+    res["cfg5_chunked_paged_prefill"] = _rec(
+        tel.kernel_name, op_ms, k_ms, flop, "mfma", PEAK_BF16_TFLOPS, "TFLOP/s",
+        cpu_baseline=cpu.get("cfg5"))
+    op_ms, k_ms, tel = timed(append)
+    res["cfg5_batched_append_512"] = _rec(tel.kernel_name, op_ms, k_ms, append_bytes, "hbm",
+                                          PEAK_HBM_GBS, "GB/s")
+    # the recompute backward at the prefill's shape (the reference's M18-M21 path)
+    run, flop = build_backward(ctx, rng)
+    op_ms, k_ms, tel = timed(run)
+    res["backward_causal_gqa_B2_Hq32_Hkv8_N4096_D128_bf16"] = _rec(
+        tel.kernel_name, op_ms, k_ms, flop, "mfma", PEAK_BF16_TFLOPS, "TFLOP/s",
+        note="algorithmic FLOPs = 2.5x forward (five S x S x D products); kernel_ms is the "
+             "dK/dV kernel, the op has three launches", cpu_baseline=cpu.get("backward"))
+    return res
+
+
 def measure_all_configs(ctx, ev, rng, steps):
-    """The other BASELINE configs, each timed alone (op events + its kernel's own events)."""
+    """`--all-configs`: the reference's published decode shapes (M15 resident cache, M48), each
+    timed alone (op events + its kernel's own events)."""
     stream = ctx.stream
     res = {}
 
@@ -360,30 +441,6 @@ def measure_all_configs(ctx, ev, rng, steps):
         ctx.set_kernel_timing(False)
         return op_ms, total / max(cnt, 1), tel
 
-    for causal in (False, True):
-        run, flop = build_mha_f32(ctx, rng, causal)
-        op_ms, k_ms, tel = timed(run)
-        tf = flop / (k_ms * 1e-3) / 1e12
-        res[f"cfg2_mha_f32_{'causal' if causal else 'noncausal'}"] = {
-            "kernel": tel.kernel_name, "ms": round(op_ms, 4), "kernel_ms": round(k_ms, 4),
-            "TFLOP/s": round(tf, 2), "frac_of_fp32_matrix_peak": round(tf / PEAK_F32_TFLOPS, 4)}
-    run, flop, append, append_bytes = build_chunked_paged(ctx, rng)
-    op_ms, k_ms, tel = timed(run)
-    tf = flop / (k_ms * 1e-3) / 1e12
-    res["cfg5_chunked_paged_prefill"] = {
-        "kernel": tel.kernel_name, "ms": round(op_ms, 4), "kernel_ms": round(k_ms, 4),
-        "TFLOP/s": round(tf, 2), "frac": round(tf / PEAK_BF16_TFLOPS, 4)}
-    op_ms, k_ms, tel = timed(append)
-    res["cfg5_batched_append_512"] = {
-        "kernel": tel.kernel_name, "ms": round(op_ms, 4), "kernel_ms": round(k_ms, 4),
-        "GB/s": round(append_bytes / (k_ms * 1e-3) / 1e9, 1)}
-    run, flop = build_backward(ctx, rng)
-    op_ms, k_ms, tel = timed(run)
-    tf = flop / (k_ms * 1e-3) / 1e12
-    res["backward_causal_gqa_B2_Hq32_Hkv8_N4096_D128_bf16"] = {
-        "kernel": tel.kernel_name, "ms": round(op_ms, 4), "kernel_ms": round(k_ms, 4),
-        "TFLOP/s": round(tf, 2), "frac": round(tf / PEAK_BF16_TFLOPS, 4),
-        "note": "algorithmic FLOPs = 2.5x forward (five S x S x D products); three launches"}
     for dt, name in ((fa.DTYPE_F32, "f32"), (fa.DTYPE_BF16, "bf16")):
         run, nbytes = build_resident_decode(ctx, rng, dt)
         op_ms, k_ms, tel = timed(run)
@@ -556,6 +613,54 @@ def cpu_baseline(samples: int = 5):
     return res
 
 
+def cpu_baseline_configs(samples: int = 3) -> dict:
+    """Single-core C oracle on bounded samples of configs[0], [1], [4] and the backward: the
+    whole of configs[0]; one (b, h) unit of configs[1] truncated to its first 1024 query rows
+    (and, non-causal, 1024 keys); one (sequence, query head) of configs[4]; one (b, kv head)
+    unit of the backward truncated to 1024 rows. FLOPs counted like the GPU figures."""
+    import oracle  # CPU baseline leg only
+    res = {}
+
+    def rec(flop, fn, sample):
+        t = _timed_samples(fn, samples)
+        return {"value": flop / t["median_s"] / 1e12, "unit": "TFLOP/s", "cores": 1,
+                "kind": "port", "p95_value": flop / t["p95_s"] / 1e12,
+                "sample": f"{sample}; median of {samples} after a warm-up "
+                          f"({t['median_s']:.3f} s)"}
+
+    n, D = 128, 64
+    q, k, v = (oracle.fill_normal(2 * n * D, s) for s in (21, 22, 23))
+    res["cfg1"] = rec(4.0 * 2 * D * n * (n + 1) / 2,
+                      lambda: oracle.forward(q, k, v, 1, 2, n, D, True),
+                      "oracle forward_reference, the whole of configs[0]")
+    n, D = 1024, 128
+    q, k, v = (oracle.fill_normal(n * D, s) for s in (24, 25, 26))
+    res["cfg2_causal"] = rec(4.0 * D * n * (n + 1) / 2,
+                             lambda: oracle.forward(q, k, v, 1, 1, n, D, True),
+                             f"oracle forward_reference f32, one (b,h) unit, {n} rows causal")
+    res["cfg2_noncausal"] = rec(4.0 * D * n * n,
+                                lambda: oracle.forward(q, k, v, 1, 1, n, D, False),
+                                f"oracle forward_reference f32, one (b,h) unit, {n}x{n} keys")
+    ql, kvl, off = 512, 2560, 2048
+    q5 = oracle.fill_normal(ql * D, 27)
+    k5, v5 = oracle.fill_normal(kvl * D, 28), oracle.fill_normal(kvl * D, 29)
+    res["cfg5"] = rec(4.0 * D * (ql * off + ql * (ql + 1) / 2),
+                      lambda: oracle.forward_projection_asymmetric(
+                          q5, k5, v5, 1, 1, 1, ql, kvl, D, off, True, 1e4, off, 0, False),
+                      "oracle asymmetric projection forward (pre-rotated K), one sequence and "
+                      "query head of configs[4]: 512 new rows over 2560 keys")
+    n, G = 1024, 4
+    qb, kb, vb, dob = (oracle.fill_normal(m * n * D, s)
+                       for m, s in ((G, 31), (1, 32), (1, 33), (G, 34)))
+    o, lse = oracle.forward_grouped(qb, kb, vb, 1, G, 1, n, D, True)
+    res["backward"] = rec(10.0 * G * D * n * (n + 1) / 2,
+                          lambda: oracle.backward_grouped(qb, kb, vb, dob, o, lse, 1, G, 1, n, D,
+                                                          True),
+                          f"oracle backward_reference_grouped, one (b, kv head) unit with its {G} "
+                          f"query heads, causal, first {n} rows")
+    return res
+
+
 def cpu_baseline_backward():
     """Scalar C oracle of the recompute backward (oracle/, backward_reference_grouped) on one
     (batch, kv head) unit of the backward workload: its 4 query heads, causal, N = 4096 rows
@@ -591,6 +696,9 @@ def main():
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-other-configs", action="store_true",
+                    help="skip the other BASELINE configs (configs[0], [1], [4], backward, and "
+                         "the alternative cfg3 prefill kernels)")
     ap.add_argument("--prefill-v-layout", type=int, default=0,
                     help="1: transposed-V pre-pass for the 16-bit prefill (fa_ctx_set_prefill_v_layout)")
     ap.add_argument("--prefill-kernel", type=int, default=-1,
@@ -607,7 +715,7 @@ def main():
     ap.add_argument("--decode-split", type=int, default=None,
                     help="tokens per split-K partition of the decode plan (default: automatic)")
     ap.add_argument("--all-configs", action="store_true",
-                    help="also time configs[1] (f32 MHA) and configs[4] (chunked paged prefill)")
+                    help="also time the reference's published decode shapes (M15, M48)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run one device copy of 1 GiB (counter calibration for --pmc runs)")
     ap.add_argument("--data", choices=["normal", "constant"], default="normal",
@@ -663,17 +771,27 @@ def main():
         print(json.dumps(out))
         ctx.close()
         return
+    ev = HipEvents()
+    stream = ctx.stream
     ctx.set_prefill_policy(args.prefill_policy)
     ctx.set_prefill_kernel(args.prefill_kernel)
     ctx.set_prefill_v_layout(args.prefill_v_layout)
-    ev = HipEvents()
-    stream = ctx.stream
     ops = []
     if args.only in (None, "prefill"):
         ops.append(("prefill",) + build_prefill(ctx, rng, args.data))
     if args.only in (None, "decode"):
         ops.append(("decode",) + build_decode(ctx, rng, args.decode_split))
     ctx.synchronize()
+    # The other BASELINE configs are measured next (each after its own warm-up, inputs built
+    # beforehand): the headline's warm-up and timed steps then run right after sustained GPU
+    # work, not after the host-side set-up that leaves the GPU idle (a power-management dip of
+    # ~30 calls follows an idle GPU).
+    baseline_configs = None
+    if args.only is None and not args.no_other_configs and args.data == "normal":
+        baseline_configs = measure_baseline_configs(ctx, ev, rng, max(args.steps // 2, 10),
+                                                    not args.no_cpu_baseline)
+        ctx.set_prefill_policy(args.prefill_policy)
+        ctx.set_prefill_kernel(args.prefill_kernel)
 
     tele = {}
     for _ in range(args.warmup):
@@ -767,12 +885,24 @@ def main():
                      "parallelism": "single GPU"}
     out["prefill"] = details.get("prefill")
     out["decode"] = details.get("decode")
+    # Steady-state check: the op times of the first and second halves of the timed steps. A
+    # clock transient (a GPU that idled before the run) shows as a drift between the halves; a
+    # kernel regression does not.
+    head = "prefill" if "prefill" in details else "decode"
+    v = per_op[head]
+    h = max(len(v) // 2, 1)
+    a, b = float(np.mean(v[:h])), float(np.mean(v[h:] or v))
+    out["steady_state"] = {"op": head, "first_half_ms": round(a, 5), "second_half_ms": round(b, 5),
+                           "drift": round(a / b - 1.0, 4), "steady": abs(a / b - 1.0) < 0.03,
+                           "after_sustained_work": baseline_configs is not None}
     if not args.no_cpu_baseline:
         cb = cpu_baseline()
         primary = cb["prefill"] if "prefill" in details else cb["decode"]
         out["cpu_baseline"] = dict(primary, other=cb["decode"] if "prefill" in details else None)
+    if baseline_configs is not None:
+        out["other_configs"] = baseline_configs
     if args.all_configs:
-        out["other_configs"] = measure_all_configs(ctx, ev, rng, max(args.steps // 2, 5))
+        out["extra_configs"] = measure_all_configs(ctx, ev, rng, max(args.steps // 2, 5))
     ctx.close()
     print(json.dumps(out))
 
