@@ -501,9 +501,12 @@ def mask_program(x: int) -> list[Ins]:
 
 
 def exp_pack_sum(x: int) -> list[Ins]:
-    """P^T = bf16(exp2(S')) into PB[x] and the half-tile row sums of P into V_LT (f32 sums of the
-    exponentials: v_dot* instructions issue to the matrix pipeline and would stall behind the
-    MFMAs, ordinary adds overlap them)."""
+    """P^T = bf16(exp2(S')) into PB[x] and the half-tile row sums of P into V_LT: f32 sums of the
+    rounded probabilities the P.V product uses (so O = sum p v / sum p stays a convex combination
+    of V rows; the stale running max leaves the dominant p off a power of two, where summing the
+    unrounded values would bias O by up to 2^-9 relative). The rounded halves are unpacked into
+    the exponentials' registers (a shift and an and): v_dot* instructions would sum the packed
+    pairs directly but issue to the matrix pipeline and stall behind the MFMAs."""
     out = []
     S = SB[x]
     pend = []
@@ -516,7 +519,9 @@ def exp_pack_sum(x: int) -> list[Ins]:
                 out += pend
                 pend = []
                 dst = PB[x] + 8 * rb + 4 * s + j
-                pend.append(I(f"v_cvt_pk_bf16_f32 {vr(dst)}, {vr(r)}, {vr(r + 1)}"))
+                pend += [I(f"v_cvt_pk_bf16_f32 {vr(dst)}, {vr(r)}, {vr(r + 1)}"),
+                         I(f"v_lshlrev_b32 {vr(r)}, 16, {vr(dst)}"),
+                         I(f"v_and_b32 {vr(r + 1)}, 0xffff0000, {vr(dst)}")]
                 lt = vr(V_LT + rb)
                 if i0 == 0:
                     pend.append(I(f"v_add_f32 {lt}, {vr(r)}, {vr(r + 1)}"))

@@ -187,8 +187,8 @@ struct fa_ctx {
     // 16-bit RoPE prefill scores: 0 = rotated Q/K rounded to the storage type, 1 = split
     // high/residual operands (fa_ctx_set_prefill_precision)
     int prefill_precision = 0;
-    // 16-bit contiguous prefill main loop: -1 automatic (the assembly kernel where it applies),
-    // 0 the HIP kernels only (fa_ctx_set_prefill_kernel)
+    // 16-bit contiguous prefill main loop: 1 the assembly kernel where it applies, -1 (default)
+    // and 0 the HIP kernels (fa_ctx_set_prefill_kernel)
     int prefill_kernel_policy = -1;
     // the stream is being captured into a graph (fa_graph_capture_begin)
     bool capturing = false;
