@@ -397,13 +397,13 @@ def measure_baseline_configs(ctx, ev, rng, steps, with_cpu, warm=100):
              "plus the residual, three Q.K^T MFMAs per k-step (f32-level scores; holds 2e-2 on "
              "the adversarial RoPE corpus)")
     ctx.set_prefill_precision(0)
-    ctx.set_prefill_kernel(1)
+    ctx.set_prefill_kernel(0)
     run, flop, _ = build_prefill(ctx, rng)
     op_ms, k_ms, tel = timed(run)
-    res["cfg3_prefill_assembly_main_loop"] = _rec(
+    res["cfg3_prefill_hip_main_loop"] = _rec(
         tel.kernel_name, op_ms, k_ms, flop, "mfma", PEAK_BF16_TFLOPS, "TFLOP/s",
-        note="fa_ctx_set_prefill_kernel(1): the generated gfx950 assembly kernel (64 query rows "
-             "per wave, persistent grid); opt-in")
+        note="fa_ctx_set_prefill_kernel(0): the HIP main loop (8-wave ping-pong, 32 query rows "
+             "per wave) instead of the default assembly kernel")
     ctx.set_prefill_kernel(-1)
     # chunked prefill into the paged cache (+ the batched append of the chunk)
     run, flop, append, append_bytes = build_chunked_paged(ctx, rng)
@@ -495,7 +495,8 @@ def summarize_pmc(fetch_csv: str, write_csv: str) -> dict:
     copy_w = pick(write, "copyBuffer") * 1024.0
     f_scale, w_scale = COPY_BYTES / copy_f, COPY_BYTES / copy_w
     res = {"copy_bytes": COPY_BYTES, "fetch_scale": f_scale, "write_scale": w_scale}
-    for name, key in (("prefill", "prefill_mfma16"), ("decode", "decode_mfma"),
+    for name, key in (("prefill", "prefill_a64"), ("prefill_hip", "prefill_mfma16"),
+                      ("decode", "decode_mfma"),
                       ("combine", "decode_combine"), ("rotate", "rotate_rows"),
                       ("bwd_delta", "bwd_delta<"), ("bwd_dkdv", "bwd_dkdv<"),
                       ("bwd_dq_ds", "bwd_dq_ds<"), ("bwd_dq", "bwd_dq<")):

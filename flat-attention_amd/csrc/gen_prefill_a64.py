@@ -97,6 +97,8 @@ NSTAGE = 5            # LDS stages of (K 16 KiB, V 16 KiB): tiles j .. j + NSTAG
 PAIR = True           # one barrier per two iterations (needs NSTAGE = 5)
 LDS_BYTES = NSTAGE * 32768
 INVALID_OFF = 0x80000000  # beyond every resource range used for stores
+O_ROWB = 272          # O staging in LDS: 64 rows of 256 bytes per wave, padded to 272
+O_WAVEB = 64 * O_ROWB
 
 # --------------------------------------------------------------------------- registers
 # VGPRs
@@ -130,7 +132,8 @@ V_LOFF = 182          # LSE byte offsets per rb (2)
 V_ROW = 184           # 4 setup temps
 NB = 188              # score bias blocks: NB + 16 rb .. +15 all hold -m of the lane's row
 V_BIG = 220           # 2^64: a half-tile row sum above it sends the phase to the exact path
-NUM_VGPR = 222
+V_EPI = 222           # 4 per-lane epilogue addresses (O staging write/read, row-offset permute, chunk)
+NUM_VGPR = 226
 # AGPRs
 A_O = 0               # O[rb][mb]: a[(rb*4+mb)*16 ..]
 A_Q = 128             # Q[rb][ks]: a[128 + (rb*8+ks)*4 ..]
@@ -833,6 +836,24 @@ def setup(gen: Gen):
        I(f"s_mov_b32 {sr(S_HIMASK)}, 0"),
        I(f"s_mov_b32 {sr(S_HIMASK + 1)}, -1"),
        I(f"s_mov_b32 {sr(S_ROUND)}, 0")])
+    # epilogue addresses (constant per lane): O staging write base wave * O_WAVEB +
+    # (lane & 31) * O_ROWB + 8 g; read base wave * O_WAVEB + (lane >> 4) * O_ROWB +
+    # 16 (lane & 15); row-offset permute source (lane >> 4) * 4; chunk byte 16 (lane & 15)
+    W, R, P, C = V_EPI, V_EPI + 1, V_EPI + 2, V_EPI + 3
+    e([I(f"s_mul_i32 {T0}, {sr(S_WAVE)}, {O_WAVEB}"),
+       I(f"v_and_b32 {vr(V_TMP)}, 31, {vr(V_LANE)}"),
+       I(f"v_mov_b32 {vr(V_TMP + 1)}, {O_ROWB}"),
+       I(f"v_mul_u32_u24 {vr(W)}, {vr(V_TMP)}, {vr(V_TMP + 1)}"),
+       I(f"v_add_u32 {vr(W)}, {T0}, {vr(W)}"),
+       I(f"v_lshrrev_b32 {vr(V_TMP)}, 5, {vr(V_LANE)}"),
+       I(f"v_lshl_add_u32 {vr(W)}, {vr(V_TMP)}, 3, {vr(W)}"),
+       I(f"v_lshrrev_b32 {vr(V_TMP)}, 4, {vr(V_LANE)}"),
+       I(f"v_lshlrev_b32 {vr(P)}, 2, {vr(V_TMP)}"),
+       I(f"v_mul_u32_u24 {vr(R)}, {vr(V_TMP)}, {vr(V_TMP + 1)}"),
+       I(f"v_add_u32 {vr(R)}, {T0}, {vr(R)}"),
+       I(f"v_and_b32 {vr(V_TMP)}, 15, {vr(V_LANE)}"),
+       I(f"v_lshlrev_b32 {vr(C)}, 4, {vr(V_TMP)}"),
+       I(f"v_add_u32 {vr(R)}, {vr(R)}, {vr(C)}")])
 
 
 def setup_block(gen: Gen):
@@ -1196,17 +1217,48 @@ def epilogue_store(gen: Gen):
     e(res(S_RK, "lse", "lse_sb", "lse_sh", S_LNREC))
     for rb in range(2):
         e(I(f"buffer_store_dword {vr(V_U + rb)}, {vr(V_LOFF + rb)}, {sr(S_RK, 4)}, 0 offen"))
+    # O goes out through LDS so that every store instruction writes whole rows: written from the
+    # accumulators a lane holds 4 dims of one row (32 rows per instruction, partial lines), read
+    # back 16 lanes cover one 256-byte row. The staging area (the first 4 * O_WAVEB bytes) overlays
+    # the K/V stages: the barrier retires every wave's reads of this block's tiles, no transfer is
+    # in flight (the last one was waited for before the loop's last barrier), and the next block
+    # refills the stages only after its opening barrier, when these reads have completed.
+    e(I("s_barrier"))
+    W, R, P, C = V_EPI, V_EPI + 1, V_EPI + 2, V_EPI + 3
+    DATA = SB[0]                 # 64 registers: bf16 pairs to stage, then the rows read back
+    n = 0
     for rb in range(2):
         for mb in range(4):
             for q4 in range(4):
                 regs = [A_O + (rb * 4 + mb) * 16 + 4 * q4 + i for i in range(4)]
                 t = V_TMP
+                d = DATA + 2 * n
                 e([I(f"v_accvgpr_read_b32 {vr(t + i)}, {ar(a)}") for i, a in enumerate(regs)])
                 e([I(f"v_mul_f32 {vr(t + i)}, {vr(t + i)}, {vr(V_ALPHA + rb)}") for i in range(4)])
-                e([I(f"v_cvt_pk_bf16_f32 {vr(t + 4)}, {vr(t)}, {vr(t + 1)}"),
-                   I(f"v_cvt_pk_bf16_f32 {vr(t + 5)}, {vr(t + 2)}, {vr(t + 3)}")])
-                e(I(f"buffer_store_dwordx2 {vr(t + 4, 2)}, {vr(V_OOFF + rb)}, {sr(S_RQ, 4)}, 0 "
-                    f"offen offset:{mb * 64 + 16 * q4} nt"))
+                e([I(f"v_cvt_pk_bf16_f32 {vr(d)}, {vr(t)}, {vr(t + 1)}"),
+                   I(f"v_cvt_pk_bf16_f32 {vr(d + 1)}, {vr(t + 2)}, {vr(t + 3)}")])
+                e(I(f"ds_write_b64 {vr(W)}, {vr(d, 2)} "
+                    f"offset:{rb * 32 * O_ROWB + mb * 64 + 16 * q4}"))
+                n += 1
+    e(I("s_waitcnt lgkmcnt(0)"))
+    # rows 4 i .. 4 i + 3 of the wave per store: the byte offset of row 4 i + (lane >> 4) is
+    # V_OOFF of the lane that held it (rows 0..31: lane r of rb 0, rows 32..63: lane r - 32 of
+    # rb 1; lanes 0..31 hold it without the 8 g term, INVALID for rows past the sequence)
+    PERM, SOFF = PB[0], PB[1]
+    for batch in range(4):
+        for k in range(4):
+            i = 4 * batch + k
+            rb = i // 8
+            e(I(f"ds_bpermute_b32 {vr(PERM + i)}, {vr(P)}, {vr(V_OOFF + rb)} offset:{16 * (i % 8)}"))
+            e(I(f"ds_read_b128 {vr(DATA + 4 * i, 4)}, {vr(R)} offset:{i * 4 * O_ROWB}"))
+        e(I("s_waitcnt lgkmcnt(0)"))
+        for k in range(4):
+            i = 4 * batch + k
+            e(I(f"v_add_u32 {vr(SOFF + i)}, {vr(PERM + i)}, {vr(C)}"))
+        for k in range(4):
+            i = 4 * batch + k
+            e(I(f"buffer_store_dwordx4 {vr(DATA + 4 * i, 4)}, {vr(SOFF + i)}, {sr(S_RQ, 4)}, 0 "
+                "offen nt"))
     # next block of the persistent loop
     e([I(f"s_add_u32 {sr(S_ROUND)}, {sr(S_ROUND)}, 1"), I("s_branch .Lblock")])
 

@@ -187,8 +187,8 @@ struct fa_ctx {
     // 16-bit RoPE prefill scores: 0 = rotated Q/K rounded to the storage type, 1 = split
     // high/residual operands (fa_ctx_set_prefill_precision)
     int prefill_precision = 0;
-    // 16-bit contiguous prefill main loop: 1 the assembly kernel where it applies, -1 (default)
-    // and 0 the HIP kernels (fa_ctx_set_prefill_kernel)
+    // 16-bit contiguous prefill main loop: -1 (default) and 1 the assembly kernel where it
+    // applies, 0 the HIP kernels (fa_ctx_set_prefill_kernel)
     int prefill_kernel_policy = -1;
     // the stream is being captured into a graph (fa_graph_capture_begin)
     bool capturing = false;
@@ -959,7 +959,7 @@ int resolve_prefill(fa_ctx* ctx, PrefillJob& j, bool own, PrefillRun* r) {
         if (c.split_qk) r->j.a.split_qk = 1;
         r->j.a.rope_rows = (int)j.max_pos;
     }
-    r->j.a.a64 = ctx->prefill_kernel_policy == 1;
+    r->j.a.a64 = ctx->prefill_kernel_policy != 0;
     r->prerot = prerot;
     if (prerot) {
         if (own) {
@@ -1198,7 +1198,7 @@ int fa_forward_gqa_rope_telemetry(fa_ctx* ctx, const fa_grouped_shape* sh, const
     if (c.prerot) a.rope_k = 0;
     if (c.split_qk) a.split_qk = 1;
     a.vt = c.vt ? (const void*)1 : nullptr;
-    a.a64 = ctx->prefill_kernel_policy == 1;
+    a.a64 = ctx->prefill_kernel_policy != 0;
     a.rope_rows = (int)j.max_pos;
     if (j.rope) a.rope_table = (const float2*)(uintptr_t)16;  // stands for the table the call builds
     describe_prefill(ctx, j, a, c.prerot, c.vt, 1u + c.prerot + c.vt, allocs, bytes, out);

@@ -272,9 +272,9 @@ class HipContext:
         check(lib().fa_ctx_set_prefill_policy(self.handle, prerotate_k))
 
     def set_prefill_kernel(self, assembly: int):
-        """1 the assembly main loop fa_prefill_a64_bf16 where it applies (bf16, head_dim 128,
-        RoPE with pre-rotated K, power-of-two GQA group); -1 (default) and 0 the HIP prefill
-        kernels."""
+        """-1 (default) and 1: the assembly main loop fa_prefill_a64_bf16 where it applies
+        (bf16, head_dim 128, RoPE with pre-rotated K, power-of-two GQA group); 0: the HIP
+        prefill kernels only."""
         check(lib().fa_ctx_set_prefill_kernel(self.handle, assembly))
 
     def set_decode_policy(self, grouped: int):

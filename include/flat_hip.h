@@ -568,12 +568,12 @@ int fa_forward_mha_telemetry(fa_ctx* ctx, const fa_attention_shape* shape,
  * pre-pass, -1 = automatic (default). */
 int fa_ctx_set_prefill_policy(fa_ctx* ctx, int32_t prerotate_k);
 /* Main loop of the 16-bit contiguous prefill (kernel-variant selection, the role of
- * WgpuKernelVariant src/wgpu_backend.rs:31-37): 1 the assembly kernel fa_prefill_a64_bf16 (64
- * query rows per wave, persistent grid) where it applies: bf16, head_dim 128, RoPE with K rotated
- * by the pre-pass, power-of-two GQA group, 16-byte aligned rows; -1 (default) and 0 the HIP
- * kernels. Opt-in: on MI355X it measures a few percent slower than the HIP kernel at BASELINE
- * configs[2]. Both give results within the same tolerance of the oracle; the telemetry's kernel
- * name says which ran. */
+ * WgpuKernelVariant src/wgpu_backend.rs:31-37): -1 (default) and 1 the assembly kernel
+ * fa_prefill_a64_bf16 (64 query rows per wave, persistent grid) where it applies: bf16, head_dim
+ * 128, RoPE with K rotated by the pre-pass, power-of-two GQA group, 16-byte aligned rows; 0 the
+ * HIP kernels only. Other inputs always run the HIP kernels. Both give results within the same
+ * tolerance of the oracle (not bitwise equal: the assembly kernel scales Q by scale * log2 e
+ * before its one rounding to bf16); the telemetry's kernel name says which ran. */
 int fa_ctx_set_prefill_kernel(fa_ctx* ctx, int32_t assembly);
 /* Score precision of the 16-bit RoPE prefill (the NumericalMode choice of src/numerical.rs:18,
  * applied to this backend). 0 (default): the rotated Q and K are rounded to the storage type

@@ -133,7 +133,17 @@ def test_gqa_rope_f32(hip, hq, hkv, theta, offset):
 
 @pytest.mark.parametrize("dtype,rnd", [(fa.DTYPE_BF16, bf16_round), (fa.DTYPE_F16, f16_round)])
 @pytest.mark.parametrize("D", [64, 128])
-def test_gqa_rope_16bit(hip, dtype, rnd, D):
+@pytest.mark.parametrize("kernel", [-1, 0])
+def test_gqa_rope_16bit(hip, dtype, rnd, D, kernel):
+    """kernel -1: the default main loop (assembly for bf16, D 128), 0: the HIP one."""
+    hip.set_prefill_kernel(kernel)
+    try:
+        _gqa_rope_16bit(hip, dtype, rnd, D)
+    finally:
+        hip.set_prefill_kernel(-1)
+
+
+def _gqa_rope_16bit(hip, dtype, rnd, D):
     B, hq, hkv, S = 2, 8, 2, 200
     q = rnd(normal(B * hq * S * D, 21))
     k, v = rnd(normal(B * hkv * S * D, 22)), rnd(normal(B * hkv * S * D, 23))
@@ -153,14 +163,20 @@ def test_prerotated_and_fused_k_rotation_are_bit_identical(hip):
     shape = fa.GroupedAttentionShape(B, hq, hkv, S, D)
     rot = fa.RotaryEmbeddingConfig(1e4, 0)
     cfg = fa.FlatAttentionConfig(True)
-    hip.set_prefill_policy(0)
-    o0, l0 = _run_grouped(hip, q, k, v, shape, cfg, rot, fa.DTYPE_BF16)
-    assert hip.last_telemetry().kernel_id == "PrefillMfmaBf16"
-    hip.set_prefill_policy(1)
-    o1, l1 = _run_grouped(hip, q, k, v, shape, cfg, rot, fa.DTYPE_BF16)
-    t = hip.last_telemetry()
-    assert t.kernel_id == "PrefillMfmaBf16PreRotatedK" and t.dispatch_count == 2
-    hip.set_prefill_policy(-1)
+    # the HIP main loop in both modes (the assembly one needs the pre-rotated K)
+    hip.set_prefill_kernel(0)
+    try:
+        hip.set_prefill_policy(0)
+        o0, l0 = _run_grouped(hip, q, k, v, shape, cfg, rot, fa.DTYPE_BF16)
+        assert hip.last_telemetry().kernel_id == "PrefillMfmaBf16"
+        hip.set_prefill_policy(1)
+        o1, l1 = _run_grouped(hip, q, k, v, shape, cfg, rot, fa.DTYPE_BF16)
+        t = hip.last_telemetry()
+        assert t.kernel_id == "PrefillMfmaBf16PreRotatedK" and t.dispatch_count == 2
+        assert "prefill_mfma16" in t.kernel_name
+    finally:
+        hip.set_prefill_policy(-1)
+        hip.set_prefill_kernel(-1)
     assert np.array_equal(o0.view(np.uint32), o1.view(np.uint32))
     assert np.array_equal(l0.view(np.uint32), l1.view(np.uint32))
 
@@ -178,6 +194,7 @@ def test_transposed_v_layout_is_bit_identical_and_matches_oracle(hip, dtype, rnd
     rot = fa.RotaryEmbeddingConfig(1e4, 3)
     cfg = fa.FlatAttentionConfig(causal)
     hip.set_prefill_v_layout(0)
+    hip.set_prefill_kernel(0)  # both layouts through the HIP main loop
     try:
         o0, l0 = _run_grouped(hip, q, k, v, shape, cfg, rot, dtype)
         assert "transpose_v" not in hip.last_telemetry().kernel_name
@@ -186,6 +203,7 @@ def test_transposed_v_layout_is_bit_identical_and_matches_oracle(hip, dtype, rnd
         assert "transpose_v" in hip.last_telemetry().kernel_name
     finally:
         hip.set_prefill_v_layout(-1)
+        hip.set_prefill_kernel(-1)
     assert np.array_equal(o0.view(np.uint32), o1.view(np.uint32))
     assert np.array_equal(l0.view(np.uint32), l1.view(np.uint32))
     eo, el = _oracle_grouped(q, k, v, shape, causal, rot, units=(0, 1))
@@ -193,7 +211,8 @@ def test_transposed_v_layout_is_bit_identical_and_matches_oracle(hip, dtype, rnd
     assert_close("LSE unit 0", l1[:S], el[:S], H16_ATOL, 0.0)
 
 
-def test_cfg3_full_size_bf16_gqa_rope_causal(hip):
+@pytest.mark.parametrize("kernel", [-1, 0])
+def test_cfg3_full_size_bf16_gqa_rope_causal(hip, kernel):
     """BASELINE configs[2] at full size: B2 Hq32 Hkv8 N4096 D128 bf16, theta 1e4, causal.
     The oracle checks two full (batch, head) units via materialised RoPE (bit-exact to the fused
     oracle, pinned in test_oracle.py); every row is checked for finiteness and LSE bounds."""
@@ -203,6 +222,17 @@ def test_cfg3_full_size_bf16_gqa_rope_causal(hip):
     v = bf16_round(normal(B * hkv * S * D, 33))
     shape = fa.GroupedAttentionShape(B, hq, hkv, S, D)
     rot = fa.RotaryEmbeddingConfig(1e4, 0)
+    hip.set_prefill_kernel(kernel)
+    try:
+        _cfg3_full(hip, q, k, v, shape, rot)
+        name = hip.last_telemetry().kernel_name
+        assert ("prefill_a64" in name) == (kernel == -1), name
+    finally:
+        hip.set_prefill_kernel(-1)
+
+
+def _cfg3_full(hip, q, k, v, shape, rot):
+    B, hq, hkv, S, D = shape.batch, shape.q_heads, shape.kv_heads, shape.seq_len, shape.head_dim
     o, l = _run_grouped(hip, q, k, v, shape, fa.FlatAttentionConfig(True), rot, fa.DTYPE_BF16)
     assert np.all(np.isfinite(o)) and np.all(np.isfinite(l))
     # LSE of causal row t lies in [max score, max score + ln(t+1)] -> at least >= -inf; check
@@ -497,3 +527,63 @@ def test_prepared_forward_matches_one_shot_and_oracle(hip, dtype, rnd, atol, rto
     finally:
         other.close()
     prep.release()
+
+
+@pytest.mark.parametrize("kernel", [-1, 1])
+@pytest.mark.parametrize("where", ["q", "k", "v"])
+def test_nan_in_device_resident_input_stays_in_its_rows(hip, kernel, where):
+    """A NaN inside a device-resident input (the host validation of fa_forward_gqa_rope_host
+    never sees it). prefill.hip is compiled with -fno-honor-nans, so the compiler may assume no
+    NaN reaches its max/compare operations; this pins what the kernels return then.
+    * Q element of row r: row r's O and LSE are NaN, every other row is bitwise unchanged.
+    * K element of key j: O and LSE of every query row of that kv head's group at t >= j are
+      NaN (masked scores are replaced, so rows t < j are bitwise unchanged).
+    * V element (j, d): O[:, d] of that group's rows t >= j is NaN, LSE and every other dim
+      unchanged. Rows t < j of a query block whose key range reaches j's 64-key tile may also
+      come back NaN in dim d: their masked probabilities enter the P.V product as zeros, and
+      0 * NaN is NaN. Rows of blocks that stop before that tile are bitwise unchanged.
+    kernel -1 is the HIP main loop, 1 the assembly one; both use 256-row query blocks, i.e.
+    128 positions of a group of 2."""
+    B, hq, hkv, S, D = 1, 4, 2, 300, 128
+    q, k, v = (fa.host_storage(bf16_round(normal(n, s)), fa.DTYPE_BF16) for n, s in
+               ((B * hq * S * D, 51), (B * hkv * S * D, 52), (B * hkv * S * D, 53)))
+    shape = fa.GroupedAttentionShape(B, hq, hkv, S, D)
+    rot = fa.RotaryEmbeddingConfig(1e4, 0)
+    cfg = fa.FlatAttentionConfig(True)
+    ex = fa.HipRotaryGroupedAttention(hip, fa.DTYPE_BF16)
+
+    def run(qs, ks, vs):
+        bufs = [fa.DeviceBuffer.from_array(hip, x) for x in (qs, ks, vs)]
+        res = ex.download_attention(ex.forward_resident(*bufs, shape, cfg, rot), shape)
+        return (fa.storage_to_f32(res.output, fa.DTYPE_BF16).reshape(hq, S, D),
+                res.lse.reshape(hq, S))
+
+    nan = np.uint16(0x7FC0)
+    hit_o = np.zeros((hq, S, D), bool)   # must be NaN
+    free_o = np.zeros((hq, S, D), bool)  # not asserted
+    hit_l = np.zeros((hq, S), bool)
+    q2, k2, v2 = q.copy(), k.copy(), v.copy()
+    if where == "q":
+        q2[(1 * S + 40) * D + 5] = nan
+        hit_o[1, 40, :] = hit_l[1, 40] = True
+    elif where == "k":
+        k2[(0 * S + 70) * D + 3] = nan
+        hit_o[0:2, 70:, :] = True
+        hit_l[0:2, 70:] = True
+    else:
+        v2[(1 * S + 250) * D + 9] = nan
+        hit_o[2:4, 250:, 9] = True
+        free_o[2:4, 128:250, 9] = True
+    hip.set_prefill_kernel(kernel)
+    try:
+        o0, l0 = run(q, k, v)
+        o1, l1 = run(q2, k2, v2)
+        if kernel == 1:
+            assert "prefill_a64" in hip.last_telemetry().kernel_name
+    finally:
+        hip.set_prefill_kernel(-1)
+    keep = ~(hit_o | free_o)
+    assert np.array_equal(o1[keep].view(np.uint32), o0[keep].view(np.uint32))
+    assert np.array_equal(l1[~hit_l].view(np.uint32), l0[~hit_l].view(np.uint32))
+    assert np.isnan(o1[hit_o]).all(), f"{np.isnan(o1[hit_o]).sum()} of {hit_o.sum()} NaN"
+    assert np.isnan(l1[hit_l]).all(), f"{np.isnan(l1[hit_l]).sum()} of {hit_l.sum()} NaN"

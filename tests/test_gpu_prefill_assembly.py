@@ -1,5 +1,5 @@
-"""GPU parity of the assembly prefill main loop (fa_ctx_set_prefill_kernel(1):
-fa_prefill_a64_bf16, generated gfx950 code, 64 query rows per wave, persistent grid) against
+"""GPU parity of the assembly prefill main loop (the default where it applies; forced with
+fa_ctx_set_prefill_kernel(1): fa_prefill_a64_bf16, generated gfx950 code, 64 query rows per wave, persistent grid) against
 the CPU oracle, through the C ABI.
 
 Tolerance: 16-bit I/O max-abs 2e-2 on O and LSE after quantising the oracle's inputs to bf16
@@ -90,7 +90,7 @@ def test_assembly_prefill_cfg3_full_size(asm):
     assert np.max(np.abs(o1 - 1.0)) <= 2e-2
     assert np.array_equal(l1.view(np.uint32), l.view(np.uint32))
     # the HIP kernel on the same inputs: the two agree within the same bar
-    asm.set_prefill_kernel(-1)
+    asm.set_prefill_kernel(0)
     o0, l0 = _run_grouped(asm, q, k, v, shape, cfg, rot, fa.DTYPE_BF16)
     assert "prefill_a64" not in asm.last_telemetry().kernel_name
     assert_close("O vs HIP kernel", o, o0, H16_ATOL, 0.0)
