@@ -69,10 +69,13 @@ ARGS = [
     ("units", 160, 4), ("fd_units_m", 164, 4), ("fd_units_s", 168, 4), ("batch", 172, 4),
     ("q_nrec", 176, 4), ("o_nrec", 180, 4), ("lse_nrec", 192, 4), ("fd_kvh_m", 196, 4),
     ("fd_kvh_s", 200, 4), ("rope_bytes", 204, 4),
+    # paged kernel only: the block tables (bytes 184..191, unused by the contiguous kernel) and
+    # their row stride in entries (the slot of k_sb: a page pool has no batch stride)
+    ("bt", 184, 8), ("bt_stride", 56, 4),
 ]
 ARG_BYTES = 208
 S_QNREC, S_ONREC, S_LNREC = 52, 53, 56  # (argument registers of q_nrec, o_nrec, lse_nrec)
-S_SPARE = 54          # [54:55]: argument bytes 184..191 are unused (a free aligned pair)
+S_SPARE = 54          # [54:55]: argument bytes 184..191 (the paged kernel's block tables)
 S_ROUND = 3           # persistent loop: blocks this workgroup has finished
 ARG_SGPR0 = 8  # argument dword i lives in s[8 + i]
 
@@ -92,7 +95,13 @@ def arg64(name: str) -> str:
     raise KeyError(name)
 
 
-KERNEL = "fa_prefill_a64_bf16"
+KERNEL_CONTIG = "fa_prefill_a64_bf16"
+KERNEL_PAGED = "fa_prefill_a64_paged_bf16"
+KERNEL = KERNEL_CONTIG
+# Paged K/V (page size 16): transfer instruction i of a tile covers its rows 16 i .. 16 i + 15,
+# i.e. exactly one page, read through a buffer resource based at that page. The page ids of
+# the next transfers sit in one VGPR (lane = page of the tile range), loaded a pair ahead.
+PAGED = False
 NSTAGE = 5            # LDS stages of (K 16 KiB, V 16 KiB): tiles j .. j + NSTAGE - 1 resident
 PAIR = True           # one barrier per two iterations (needs NSTAGE = 5)
 LDS_BYTES = NSTAGE * 32768
@@ -133,7 +142,9 @@ V_ROW = 184           # 4 setup temps
 NB = 188              # score bias blocks: NB + 16 rb .. +15 all hold -m of the lane's row
 V_BIG = 220           # 2^64: a half-tile row sum above it sends the phase to the exact path
 V_EPI = 222           # 4 per-lane epilogue addresses (O staging write/read, row-offset permute, chunk)
-NUM_VGPR = 226
+V_PT = 226            # paged: page ids, lane l = entry l of the loaded block-table range
+V_PTOFF = 227         # paged: 4 * lane (byte offset of the lane's block-table entry)
+NUM_VGPR = 228
 # AGPRs
 A_O = 0               # O[rb][mb]: a[(rb*4+mb)*16 ..]
 A_Q = 128             # Q[rb][ks]: a[128 + (rb*8+ks)*4 ..]
@@ -804,6 +815,69 @@ def transfer_setup(tile_sgpr: str) -> list[Ins]:
     return out
 
 
+S_PLO = 92            # paged: temps of the page offset (S_NREC is unused there) and
+S_PHI = 23            # argument dword 15 (the upper half of the k_sb slot, unused when paged)
+
+
+def transfer_paged(tile_sgpr: str, lane_base: int) -> list[Ins]:
+    """Paged: the 8 transfers of tile `tile_sgpr` into stage S_TSLOT, page i of the tile (its
+    rows 16 i .. 16 i + 15, one page of 16 rows) from V_PT lane lane_base + i. Every transfer
+    uses the in-page lane offsets VTOFF (rows 4 wave + (lane >> 4)) against a resource based
+    at that page of this kv head, bounded to the page's live rows (0 past kv_len)."""
+    T0, T1, T2, T3 = (sr(S_T0), sr(S_T1), sr(S_T2), sr(S_T3))
+    LO, HI = sr(S_PLO), sr(S_PHI)
+    rbytes = arg("k_ss")
+    out = [I(f"s_lshl_b32 {T0}, {tile_sgpr}, 6"),                # key of page 0
+           I(f"s_lshl_b32 {T2}, {sr(S_TSLOT)}, 15"),
+           I(f"s_lshl_b32 {T3}, {sr(S_WAVE)}, 10"),
+           I(f"s_add_u32 {T2}, {T2}, {T3}"),                       # stage base + wave KiB
+           I(f"s_mov_b32 {sr(S_RK + 3)}, 0x20000"),
+           I(f"s_mov_b32 {sr(S_RV + 3)}, 0x20000")]
+    for i in range(4):
+        out += [I(f"v_readlane_b32 {T1}, {vr(V_PT)}, {lane_base + i}"),  # page id
+                I(f"s_sub_u32 {T3}, {arg('kv_len')}, {T0}"),
+                I(f"s_max_i32 {T3}, {T3}, 0"),
+                I(f"s_min_i32 {T3}, {T3}, 16"),
+                I(f"s_mul_i32 {T3}, {T3}, {rbytes}"),               # live bytes of the page
+                I(f"s_lshl_b32 {LO}, {rbytes}, 4"),                 # page bytes
+                I(f"s_mul_hi_u32 {HI}, {T1}, {LO}"),
+                I(f"s_mul_i32 {LO}, {T1}, {LO}"),                   # page * page bytes (64-bit)
+                I(f"s_add_u32 {sr(S_RK)}, {sr(S_KBASE)}, {LO}"),
+                I(f"s_addc_u32 {sr(S_RK + 1)}, {sr(S_KBASE + 1)}, {HI}"),
+                I(f"s_and_b32 {sr(S_RK + 1)}, {sr(S_RK + 1)}, 0xffff"),
+                I(f"s_mov_b32 {sr(S_RK + 2)}, {T3}"),
+                I(f"s_add_u32 {sr(S_RV)}, {sr(S_VBASE)}, {LO}"),
+                I(f"s_addc_u32 {sr(S_RV + 1)}, {sr(S_VBASE + 1)}, {HI}"),
+                I(f"s_and_b32 {sr(S_RV + 1)}, {sr(S_RV + 1)}, 0xffff"),
+                I(f"s_mov_b32 {sr(S_RV + 2)}, {T3}"),
+                I(f"s_add_u32 m0, {T2}, {4096 * i}", writes=["m0"], reads=[f"s{S_T2}"]),
+                I(f"buffer_load_dwordx4 {vr(VTOFF)}, {sr(S_RK, 4)}, 0 offen lds"),
+                I(f"s_add_u32 m0, {T2}, {16384 + 4096 * i}", writes=["m0"], reads=[f"s{S_T2}"]),
+                I(f"buffer_load_dwordx4 {vr(VTOFF)}, {sr(S_RV, 4)}, 0 offen lds"),
+                I(f"s_add_u32 {T0}, {T0}, 16")]
+    return out
+
+
+def pt_load(first_tile_sgpr: str) -> list[Ins]:
+    """Paged: V_PT lane l = block-table entry 4 * first_tile + l of this block's sequence (the
+    resource in S_RQ spans its row; entries past it read 0, only used with zero-length pages)."""
+    T0 = sr(S_T0)
+    return [I(f"s_lshl_b32 {T0}, {first_tile_sgpr}, 4"),
+            I(f"buffer_load_dword {vr(V_PT)}, {vr(V_PTOFF)}, {sr(S_RQ, 4)}, {T0} offen")]
+
+
+def bt_resource() -> list[Ins]:
+    """Paged: S_RQ = the block-table row of sequence S_B (bt_stride entries)."""
+    T0 = sr(S_T0)
+    return [I(f"s_mul_i32 {T0}, {sr(S_B)}, {arg('bt_stride')}"),
+            I(f"s_lshl_b32 {T0}, {T0}, 2"),
+            I(f"s_add_u32 {sr(S_RQ)}, {arg('bt')}, {T0}"),
+            I(f"s_addc_u32 {sr(S_RQ + 1)}, {arg('bt', True)}, 0"),
+            I(f"s_and_b32 {sr(S_RQ + 1)}, {sr(S_RQ + 1)}, 0xffff"),
+            I(f"s_lshl_b32 {sr(S_RQ + 2)}, {arg('bt_stride')}, 2"),
+            I(f"s_mov_b32 {sr(S_RQ + 3)}, 0x20000")]
+
+
 def advance_slot(slot_sgpr: int, addr_base: int, n_addr: int) -> list[Ins]:
     """slot = (slot + 1) % NSTAGE and every read address += the matching stage delta."""
     d = sr(S_KDELTA)
@@ -839,6 +913,7 @@ def setup(gen: Gen):
     # epilogue addresses (constant per lane): O staging write base wave * O_WAVEB +
     # (lane & 31) * O_ROWB + 8 g; read base wave * O_WAVEB + (lane >> 4) * O_ROWB +
     # 16 (lane & 15); row-offset permute source (lane >> 4) * 4; chunk byte 16 (lane & 15)
+    e(I(f"v_lshlrev_b32 {vr(V_PTOFF)}, 2, {vr(V_LANE)}"))
     W, R, P, C = V_EPI, V_EPI + 1, V_EPI + 2, V_EPI + 3
     e([I(f"s_mul_i32 {T0}, {sr(S_WAVE)}, {O_WAVEB}"),
        I(f"v_and_b32 {vr(V_TMP)}, 31, {vr(V_LANE)}"),
@@ -1004,12 +1079,22 @@ def setup_block(gen: Gen):
                 if sh_hi else []) + \
                [I(f"s_add_u32 {sr(dst)}, {sr(dst)}, {T0}"),
                 I(f"s_addc_u32 {sr(dst + 1)}, {sr(dst + 1)}, {T1}")]
-    e(base64(S_KBASE, "k", "k_sb", arg("k_sh"), arg("k_sh", True), sr(S_KVH)))
-    e(base64(S_VBASE, "v", "k_sb", arg("k_sh"), arg("k_sh", True), sr(S_KVH)))
-    # nrec_all = (kv_len - 1) * row_bytes + 256
-    e([I(f"s_sub_u32 {T0}, {arg('kv_len')}, 1"),
-       I(f"s_mul_i32 {sr(S_NREC)}, {T0}, {arg('k_ss')}"),
-       I(f"s_add_u32 {sr(S_NREC)}, {sr(S_NREC)}, 256")])
+    if PAGED:
+        # K/V of this kv head in the page pool (no batch term: pages come from the tables)
+        for dst, ptr in ((S_KBASE, "k"), (S_VBASE, "v")):
+            e([I(f"s_mul_i32 {T0}, {sr(S_KVH)}, {arg('k_sh')}"),
+               I(f"s_mul_hi_u32 {T1}, {sr(S_KVH)}, {arg('k_sh')}"),
+               I(f"s_mul_i32 {T2}, {sr(S_KVH)}, {arg('k_sh', True)}"),
+               I(f"s_add_u32 {T1}, {T1}, {T2}"),
+               I(f"s_add_u32 {sr(dst)}, {arg(ptr)}, {T0}"),
+               I(f"s_addc_u32 {sr(dst + 1)}, {arg(ptr, True)}, {T1}")])
+    else:
+        e(base64(S_KBASE, "k", "k_sb", arg("k_sh"), arg("k_sh", True), sr(S_KVH)))
+        e(base64(S_VBASE, "v", "k_sb", arg("k_sh"), arg("k_sh", True), sr(S_KVH)))
+        # nrec_all = (kv_len - 1) * row_bytes + 256
+        e([I(f"s_sub_u32 {T0}, {arg('kv_len')}, 1"),
+           I(f"s_mul_i32 {sr(S_NREC)}, {T0}, {arg('k_ss')}"),
+           I(f"s_add_u32 {sr(S_NREC)}, {sr(S_NREC)}, 256")])
     # transfer offsets: instruction i covers rows 4 (wave + 4 i) + (lane >> 4); slot chunk
     # lane & 15 holds global chunk (lane & 15) ^ (4 (lane >> 4) + wave)
     e([I(f"v_lshrrev_b32 {vr(V_ROW)}, 4, {vr(V_LANE)}"),           # lane >> 4
@@ -1064,15 +1149,20 @@ def setup_block(gen: Gen):
                I(f"v_lshl_add_u32 {vr(V_TMP)}, {vr(V_TMP)}, 8, {vr(V_TMP + 1)}"),
                I(f"v_add_u32 {vr(V_TMP)}, {vr(V_TMP)}, {vr(V_ROW + 2)}"),
                I(f"v_add_u32 {vr(VVA + mb * 2 + hi)}, 0x4000, {vr(V_TMP)}")])
-    # ---- transfers of tiles 0 and 1 into stages 0 and 1
+    # ---- transfers of tiles 0 .. 2 into stages 0 .. 2 (paged: after the Q loads, once the
+    # page ids of tiles 0 .. 2 have landed)
     e(I(f"s_mov_b32 {sr(S_TSLOT)}, 0"))
     e(I(f"s_mov_b32 {sr(S_TT)}, 0"))
-    for _ in range(3 if PAIR else 2):
-        e(transfer_setup(sr(S_TT)))
-        e(transfer_block("k"))
-        e(transfer_block("v"))
-        e([I(f"s_add_u32 {sr(S_TT)}, {sr(S_TT)}, 1"),
-           I(f"s_add_u32 {sr(S_TSLOT)}, {sr(S_TSLOT)}, 1")])
+    if PAGED:
+        e(bt_resource())
+        e(pt_load(sr(S_TT)))
+    else:
+        for _ in range(3 if PAIR else 2):
+            e(transfer_setup(sr(S_TT)))
+            e(transfer_block("k"))
+            e(transfer_block("v"))
+            e([I(f"s_add_u32 {sr(S_TT)}, {sr(S_TT)}, 1"),
+               I(f"s_add_u32 {sr(S_TSLOT)}, {sr(S_TSLOT)}, 1")])
     # ---- Q rows into AGPRs, rotated when rope_q
     # Q resource base = q + b * q_sb + (kvh << gshift) * q_sh
     e([I(f"s_lshl_b32 {sr(S_T3)}, {sr(S_KVH)}, {gs}")])
@@ -1100,6 +1190,18 @@ def setup_block(gen: Gen):
         for ks in range(8):
             e(I(f"buffer_load_dwordx4 {vr(qt[rb] + 4 * ks, 4)}, {vr(V_QOFF + rb)}, {sr(S_RQ, 4)}, 0 "
                 f"offen offset:{32 * ks}"))
+    if PAGED:
+        # the page ids of tiles 0 .. 2 (issued before the 16 Q loads), then their transfers,
+        # then the page ids of tiles 3 and 4 for the first pair of the loop (S_RQ: the
+        # block-table row again; the Q loads have read their resource)
+        assert PAIR
+        e(I("s_waitcnt vmcnt(16)"))
+        for t in range(3):
+            e(transfer_paged(sr(S_TT), 4 * t))
+            e([I(f"s_add_u32 {sr(S_TT)}, {sr(S_TT)}, 1"),
+               I(f"s_add_u32 {sr(S_TSLOT)}, {sr(S_TSLOT)}, 1")])
+        e(bt_resource())
+        e(pt_load(sr(S_TT)))
     c2 = arg("c2")
 
     def rotate_chunk(w0, cs0):
@@ -1374,8 +1476,16 @@ def iteration(gen: Gen, masked: bool, tag: str, jofs: int, ring_in, xfer_tile_of
     tile S_J + xfer_tile_ofs at its start. Returns the V ring state after it."""
     xfer = []
     if xfer_tile_ofs is not None:
-        xfer = [I(f"s_add_u32 {sr(S_TT)}, {sr(S_J)}, {xfer_tile_ofs}")] + \
-            transfer_setup(sr(S_TT)) + transfer_block("k") + transfer_block("v") + \
+        if PAGED:
+            # tile j+3 from page-id lanes 0..3, tile j+4 from lanes 4..7; after the second,
+            # the page ids of tiles j+5 and j+6 (waited for by the pair's closing vmcnt(0))
+            assert PAIR and xfer_tile_ofs in (3, 4)
+            body = transfer_paged(sr(S_TT), 4 * (xfer_tile_ofs - 3))
+            if xfer_tile_ofs == 4:
+                body += [I(f"s_add_u32 {sr(S_TT)}, {sr(S_J)}, 5")] + pt_load(sr(S_TT))
+        else:
+            body = transfer_setup(sr(S_TT)) + transfer_block("k") + transfer_block("v")
+        xfer = [I(f"s_add_u32 {sr(S_TT)}, {sr(S_J)}, {xfer_tile_ofs}")] + body + \
             [I(f"s_add_u32 {sr(S_TSLOT)}, {sr(S_TSLOT)}, 1"),
              I(f"s_cmp_eq_u32 {sr(S_TSLOT)}, {NSTAGE}"),
              I(f"s_cselect_b32 {sr(S_TSLOT)}, 0, {sr(S_TSLOT)}")]
@@ -1459,81 +1569,84 @@ def finish_phase(gen: Gen, tag: str, x: int, hh: int, s_x) -> None:
 
 
 # --------------------------------------------------------------------------- output
-def render(gen: Gen) -> str:
-    # split the straight-line blocks at conditional branches for the hazard check: the
-    # rescale block is optional; check both with and without it by treating labels as joins.
+def render_kernel(gen: Gen, name: str) -> tuple[list[str], list[str], list[str]]:
+    """The text, kernel descriptor and metadata entry of one generated kernel."""
     fix_hazards(gen.blocks)
-    lines = []
-    lines.append('\t.amdgcn_target "amdgcn-amd-amdhsa--gfx950"')
-    lines.append("\t.amdhsa_code_object_version 5")
-    lines.append("\t.text")
-    lines.append(f"\t.globl {KERNEL}")
-    lines.append("\t.p2align 8")
-    lines.append(f"\t.type {KERNEL},@function")
-    lines.append(f"{KERNEL}:")
+    text = ["\t.text", f"\t.globl {name}", "\t.p2align 8", f"\t.type {name},@function", f"{name}:"]
     for b in gen.blocks:
         for x in b.ins:
             if x.kind == "nop":
-                lines.append("\t" + x.text)
+                text.append("\t" + x.text)
                 continue
             n = x.nops
             while n > 0:
                 k = min(n, 16)
-                lines.append(f"\ts_nop {k - 1}")
+                text.append(f"\ts_nop {k - 1}")
                 n -= k
-            if x.kind == "label":
-                lines.append(x.text)
-            else:
-                lines.append("\t" + x.text)
-    lines.append(f".Lfunc_end:")
-    lines.append(f"\t.size {KERNEL}, .Lfunc_end-{KERNEL}")
-    lines.append("")
-    lines.append("\t.rodata")
-    lines.append("\t.p2align 6")
-    lines.append(f"\t.amdhsa_kernel {KERNEL}")
-    lines.append(f"\t\t.amdhsa_group_segment_fixed_size {LDS_BYTES}")
-    lines.append("\t\t.amdhsa_private_segment_fixed_size 0")
-    lines.append(f"\t\t.amdhsa_kernarg_size {ARG_BYTES}")
-    lines.append("\t\t.amdhsa_user_sgpr_count 2")
-    lines.append("\t\t.amdhsa_user_sgpr_kernarg_segment_ptr 1")
-    lines.append("\t\t.amdhsa_system_sgpr_workgroup_id_x 1")
-    lines.append("\t\t.amdhsa_system_vgpr_workitem_id 0")
+            text.append(x.text if x.kind == "label" else "\t" + x.text)
+    text += [".Lfunc_end:", f"\t.size {name}, .Lfunc_end-{name}", ""]
     acc_off = (NUM_VGPR + 3) // 4 * 4
-    lines.append(f"\t\t.amdhsa_next_free_vgpr {acc_off + NUM_AGPR}")
-    lines.append(f"\t\t.amdhsa_next_free_sgpr {NUM_SGPR}")
-    lines.append(f"\t\t.amdhsa_accum_offset {acc_off}")
-    lines.append("\t\t.amdhsa_reserve_vcc 1")
-    lines.append("\t\t.amdhsa_float_denorm_mode_32 3")
-    lines.append("\t\t.amdhsa_float_denorm_mode_16_64 3")
-    lines.append("\t\t.amdhsa_ieee_mode 1")
-    lines.append("\t\t.amdhsa_dx10_clamp 1")
-    lines.append("\t.end_amdhsa_kernel")
-    lines.append("")
-    lines.append("\t.amdgpu_metadata")
-    lines.append("---")
-    lines.append("amdhsa.kernels:")
-    lines.append(f"  - .agpr_count:     {NUM_AGPR}")
-    lines.append("    .args:")
-    lines.append("      - .offset:         0")
-    lines.append(f"        .size:           {ARG_BYTES}")
-    lines.append("        .value_kind:     by_value")
-    lines.append(f"    .group_segment_fixed_size: {LDS_BYTES}")
-    lines.append("    .kernarg_segment_align: 8")
-    lines.append(f"    .kernarg_segment_size: {ARG_BYTES}")
-    lines.append("    .max_flat_workgroup_size: 256")
-    lines.append(f"    .name:           {KERNEL}")
-    lines.append("    .private_segment_fixed_size: 0")
-    lines.append(f"    .sgpr_count:     {NUM_SGPR + 2}")
-    lines.append(f"    .symbol:         {KERNEL}.kd")
-    lines.append(f"    .vgpr_count:     {acc_off + NUM_AGPR}")
-    lines.append("    .wavefront_size: 64")
-    lines.append("amdhsa.target:   amdgcn-amd-amdhsa--gfx950")
-    lines.append("amdhsa.version:")
-    lines.append("  - 1")
-    lines.append("  - 2")
-    lines.append("...")
-    lines.append("\t.end_amdgpu_metadata")
+    desc = ["\t.rodata", "\t.p2align 6", f"\t.amdhsa_kernel {name}",
+            f"\t\t.amdhsa_group_segment_fixed_size {LDS_BYTES}",
+            "\t\t.amdhsa_private_segment_fixed_size 0",
+            f"\t\t.amdhsa_kernarg_size {ARG_BYTES}",
+            "\t\t.amdhsa_user_sgpr_count 2",
+            "\t\t.amdhsa_user_sgpr_kernarg_segment_ptr 1",
+            "\t\t.amdhsa_system_sgpr_workgroup_id_x 1",
+            "\t\t.amdhsa_system_vgpr_workitem_id 0",
+            f"\t\t.amdhsa_next_free_vgpr {acc_off + NUM_AGPR}",
+            f"\t\t.amdhsa_next_free_sgpr {NUM_SGPR}",
+            f"\t\t.amdhsa_accum_offset {acc_off}",
+            "\t\t.amdhsa_reserve_vcc 1",
+            "\t\t.amdhsa_float_denorm_mode_32 3",
+            "\t\t.amdhsa_float_denorm_mode_16_64 3",
+            "\t\t.amdhsa_ieee_mode 1",
+            "\t\t.amdhsa_dx10_clamp 1",
+            "\t.end_amdhsa_kernel", ""]
+    meta = [f"  - .agpr_count:     {NUM_AGPR}",
+            "    .args:",
+            "      - .offset:         0",
+            f"        .size:           {ARG_BYTES}",
+            "        .value_kind:     by_value",
+            f"    .group_segment_fixed_size: {LDS_BYTES}",
+            "    .kernarg_segment_align: 8",
+            f"    .kernarg_segment_size: {ARG_BYTES}",
+            "    .max_flat_workgroup_size: 256",
+            f"    .name:           {name}",
+            "    .private_segment_fixed_size: 0",
+            f"    .sgpr_count:     {NUM_SGPR + 2}",
+            f"    .symbol:         {name}.kd",
+            f"    .vgpr_count:     {acc_off + NUM_AGPR}",
+            "    .wavefront_size: 64"]
+    return text, desc, meta
+
+
+def render(kernels: list[tuple[Gen, str, str]]) -> str:
+    """One code object holding every kernel: (generator state, symbol, label prefix)."""
+    lines = ['\t.amdgcn_target "amdgcn-amd-amdhsa--gfx950"', "\t.amdhsa_code_object_version 5"]
+    metas = []
+    for gen, name, prefix in kernels:
+        text, desc, meta = render_kernel(gen, name)
+        body = "\n".join(text + desc)
+        if prefix:
+            body = re.sub(r"\.L(\w+)", lambda m: f".L{prefix}{m.group(1)}", body)
+        lines.append(body)
+        metas += meta
+    lines += ["\t.amdgpu_metadata", "---", "amdhsa.kernels:"] + metas + [
+        "amdhsa.target:   amdgcn-amd-amdhsa--gfx950", "amdhsa.version:", "  - 1", "  - 2", "...",
+        "\t.end_amdgpu_metadata"]
     return "\n".join(lines) + "\n"
+
+
+def build_all() -> list[tuple[Gen, str, str]]:
+    """The contiguous and the paged kernel."""
+    global PAGED, KERNEL
+    out = []
+    for paged, name, prefix in ((False, KERNEL_CONTIG, ""), (True, KERNEL_PAGED, "P")):
+        PAGED, KERNEL = paged, name
+        out.append((build(), name, prefix))
+    PAGED, KERNEL = False, KERNEL_CONTIG
+    return out
 
 
 def fix_hazards_with_optional(blocks: list[Block]):
@@ -1569,7 +1682,8 @@ def header(path: str):
     lines = ["// Generated by gen_prefill_a64.py: kernel-argument layout of fa_prefill_a64_bf16.",
              "#pragma once", f"#define FA_A64_ARG_BYTES {ARG_BYTES}",
              f"#define FA_A64_LDS_BYTES {LDS_BYTES}",
-             f'#define FA_A64_KERNEL "{KERNEL}"']
+             f'#define FA_A64_KERNEL "{KERNEL_CONTIG}"',
+             f'#define FA_A64_KERNEL_PAGED "{KERNEL_PAGED}"']
     for n, off, sz in ARGS:
         lines.append(f"#define FA_A64_OFF_{n.upper()} {off}")
     open(path, "w").write("\n".join(lines) + "\n")
@@ -1590,8 +1704,7 @@ def main():
         blob(sys.argv[2], sys.argv[3])
         return
     out_s, out_h = sys.argv[1], sys.argv[2]
-    gen = build()
-    open(out_s, "w").write(render(gen))
+    open(out_s, "w").write(render(build_all()))
     header(out_h)
 
 

@@ -55,14 +55,14 @@ struct PrefillArgs {
 };
 
 // The assembly prefill (64 query rows per wave, code object loaded per device): bf16, Q rotated
-// in the kernel (RoPE), contiguous K/V of 128 dims not rotated in the kernel, power-of-two GQA
-// group, no variable-length metadata,
-// 16-byte aligned rows and slices addressable with 32-bit offsets, module loaded on the current
-// device.
+// in the kernel (RoPE), K/V of 128 dims not rotated in the kernel (contiguous, or paged with
+// 16-row pages), power-of-two GQA group, no variable-length metadata, 16-byte aligned rows and
+// slices addressable with 32-bit offsets, module loaded on the current device.
 bool prefill_a64_eligible(Dtype dt, bool paged, const PrefillArgs& a);
 // Loads the code object on `device` (current); idempotent. Failure leaves the HIP kernels in use.
 hipError_t prefill_a64_load(int device);
-void launch_prefill_a64(const PrefillArgs& a, hipStream_t s, unsigned grid[3], unsigned* block);
+void launch_prefill_a64(const PrefillArgs& a, bool paged, hipStream_t s, unsigned grid[3],
+                        unsigned* block);
 // Workgroups of its persistent grid: min(query blocks, CUs of the current device).
 unsigned prefill_a64_workgroups(const PrefillArgs& a);
 

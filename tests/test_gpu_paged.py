@@ -306,7 +306,8 @@ def test_batched_append_scatter_is_bit_exact(hip):
             assert np.array_equal(vpool[r * width:(r + 1) * width], vs[src:src + width])
 
 
-def test_cfg5_chunked_prefill_over_paged_cache(hip):
+@pytest.mark.parametrize("kernel", [-1, 0])
+def test_cfg5_chunked_prefill_over_paged_cache(hip, kernel):
     """BASELINE configs[4] at its stated size: 8 sequences, each holding 2048 cached tokens + a
     new 512-token chunk in one shuffled page pool (page 16); the chunk attends causally at
     offset 2048 with Q RoPE at 2048 + i and pre-rotated K (rotate-on-append). The oracle checks
@@ -341,7 +342,14 @@ def test_cfg5_chunked_prefill_over_paged_cache(hip):
         res = fa.download_attention(out, plan.layout(), fa.DTYPE_BF16)
         return fa.storage_to_f32(res.output, fa.DTYPE_BF16), res.lse
 
-    o, lse = run(v)
+    hip.set_prefill_kernel(kernel)  # -1: the paged assembly kernel, 0: the HIP one
+    try:
+        o, lse = run(v)
+        name = hip.last_telemetry().kernel_name
+        assert ("prefill_a64" in name) == (kernel == -1), name
+        o1, l1 = run(np.ones_like(v))
+    finally:
+        hip.set_prefill_kernel(-1)
     assert np.isfinite(o).all() and np.isfinite(lse).all()
     # oracle: RoPE materialised on Q (positions cached + i) and K (positions 0..kv_len-1) —
     # bit-exact to rotation inside the dot product (pinned in test_oracle.py) — then the
@@ -360,7 +368,6 @@ def test_cfg5_chunked_prefill_over_paged_cache(hip):
             assert_close(f"O seq {s} head {unit}", got, exp, H16_ATOL, 0.0)
             gl = lse[(s * hq + unit) * ql:(s * hq + unit + 1) * ql]
             assert_close(f"LSE seq {s} head {unit}", gl, el[unit * ql:(unit + 1) * ql], H16_ATOL, 0.0)
-    o1, l1 = run(np.ones_like(v))
     assert np.max(np.abs(o1 - 1.0)) <= 2e-2
     assert np.array_equal(l1.view(np.uint32), lse.view(np.uint32))
 
@@ -463,8 +470,11 @@ def test_paged_prefill_modes_match_oracle_and_gather_bit_exactly(hip, dtype, ps,
     shuf = rng.permutation(total)[:n_seqs * pages_per].astype(np.int32).reshape(n_seqs, pages_per)
     o1, l1 = _paged_prefill(hip, ident, ps, total, n_seqs, hq, hkv, D, cached, ql, theta, raw_k,
                             v, q, dtype, causal)
-    if dtype != fa.DTYPE_F32:  # page % 16 == 0: 8-wave ping-pong kernel; else the 4-wave one
-        assert hip.last_telemetry().workgroup_size == (512 if ps % 16 == 0 else 256)
+    t = hip.last_telemetry()
+    if dtype == fa.DTYPE_BF16 and ps == 16 and D == 128:  # the paged assembly kernel
+        assert "prefill_a64" in t.kernel_name and t.workgroup_size == 256, t.kernel_name
+    elif dtype != fa.DTYPE_F32:  # page % 16 == 0: 8-wave ping-pong kernel; else the 4-wave one
+        assert t.workgroup_size == (512 if ps % 16 == 0 else 256)
     pools = []
     o2, l2 = _paged_prefill(hip, shuf, ps, total, n_seqs, hq, hkv, D, cached, ql, theta, raw_k,
                             v, q, dtype, causal, pools)

@@ -209,3 +209,39 @@ def test_assembly_prefill_falls_back_where_it_does_not_apply(asm, case):
     eo, el = _oracle_grouped(q, k, v, shape, True, rot)
     assert_close("O", o, eo, H16_ATOL, 0.0)
     assert_close("LSE", l, el, H16_ATOL, 0.0)
+
+
+@pytest.mark.parametrize("hq,hkv,cached,ql,causal", [(32, 8, 300, 200, True),
+                                                     (16, 1, 0, 129, True),
+                                                     (8, 8, 1000, 64, False),
+                                                     (4, 2, 17, 300, True)])
+def test_assembly_paged_prefill_matches_paged_oracle(asm, hq, hkv, cached, ql, causal):
+    """The paged assembly kernel (16-row pages): chunked prefill over a shuffled page pool whose
+    unnamed rows hold NaN (a wrong page shows), GQA groups 1..16, ragged last pages, causal
+    offsets from 0 to 1000; checked against the paged oracle over the device's own pool and
+    bitwise against the identity block table."""
+    from test_gpu_paged import _paged_prefill
+    n_seqs, D, ps, theta = 3, 128, 16, 1e4
+    kv_len = cached + ql
+    pages_per = -(-kv_len // ps)
+    total = n_seqs * pages_per + 5
+    rng = np.random.default_rng(kv_len + hq)
+    width = hkv * D
+    raw_k = bf16_round(normal(n_seqs * kv_len * width, 41))
+    v = bf16_round(normal(n_seqs * kv_len * width, 42))
+    q = bf16_round(normal(n_seqs * ql * hq * D, 43))
+    ident = np.arange(n_seqs * pages_per, dtype=np.int32).reshape(n_seqs, pages_per)
+    shuf = rng.permutation(total)[:n_seqs * pages_per].astype(np.int32).reshape(n_seqs, pages_per)
+    o1, l1 = _paged_prefill(asm, ident, ps, total, n_seqs, hq, hkv, D, cached, ql, theta, raw_k,
+                            v, q, fa.DTYPE_BF16, causal)
+    _assert_ran_assembly(asm)
+    pools = []
+    o2, l2 = _paged_prefill(asm, shuf, ps, total, n_seqs, hq, hkv, D, cached, ql, theta, raw_k,
+                            v, q, fa.DTYPE_BF16, causal, pools)
+    _assert_ran_assembly(asm)
+    assert np.array_equal(o1.view(np.uint32), o2.view(np.uint32))
+    assert np.array_equal(l1.view(np.uint32), l2.view(np.uint32))
+    po, pl = oracle.paged_prefill(q, pools[0], pools[1], total, ps, shuf, hq, hkv, ql, kv_len, D,
+                                  cached, causal, theta, cached, threads=4)
+    assert_close("O vs paged oracle", o2, po, H16_ATOL, 0.0)
+    assert_close("LSE vs paged oracle", l2, pl, H16_ATOL, 0.0)
