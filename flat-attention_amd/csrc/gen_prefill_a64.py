@@ -573,14 +573,25 @@ def rescale_block() -> list[Ins]:
     return out
 
 
-def exact_path(gen: "Gen", x: int, hh: int, s_x) -> None:
+def exact_path(gen: "Gen", x: int, hh: int, s_x, recompute: bool = True) -> None:
     """Exact softmax of the half-tile whose scores belong in SB[x] (K half hh of the stage before
     the current K read stage): recompute the raw scores S * c2, mask, take the row maxima, move m
     (alpha = exp2(m_old - m_new)), rescale O and l, re-bias the scores SB[s_x] that this phase's
-    MFMAs accumulated onto the old bias, set the bias blocks, and redo P^T and the row sums."""
+    MFMAs accumulated onto the old bias, set the bias blocks, and redo P^T and the row sums.
+    recompute=False (the prologue): SB[x] already holds the raw scores (the bias blocks are
+    still zero), and the V operands the last phase prefetched stay in flight."""
     e = gen.emit
-    gen.ds_wait_all()
-    e(I("s_waitcnt lgkmcnt(0)"))
+    if recompute:
+        gen.ds_wait_all()
+        e(I("s_waitcnt lgkmcnt(0)"))
+        _recompute_scores(gen, x, hh)
+    e(mask_program(x))
+    _exact_softmax(gen, x, s_x)
+
+
+def _recompute_scores(gen: "Gen", x: int, hh: int) -> None:
+    """SB[x] = the raw scores S * c2 of K half hh of the stage before the current K stage."""
+    e = gen.emit
     # K addresses of the previous stage
     d = sr(S_T0)
     e([I(f"s_cmp_eq_u32 {sr(S_KSLOT)}, 0"),
@@ -600,7 +611,11 @@ def exact_path(gen: "Gen", x: int, hh: int, s_x) -> None:
                         f"{q_op(rb, ks)}, {src_c}")
                 ins.srcc_chain = ks != 0
                 e(ins)
-    e(mask_program(x))
+
+
+def _exact_softmax(gen: "Gen", x: int, s_x) -> None:
+    """Row maxima of the masked raw scores in SB[x], the move of m, rescale, re-bias, redo P."""
+    e = gen.emit
     S = SB[x]
     for rb in range(2):
         r = S + 16 * rb
@@ -1156,13 +1171,6 @@ def setup_block(gen: Gen):
     if PAGED:
         e(bt_resource())
         e(pt_load(sr(S_TT)))
-    else:
-        for _ in range(3 if PAIR else 2):
-            e(transfer_setup(sr(S_TT)))
-            e(transfer_block("k"))
-            e(transfer_block("v"))
-            e([I(f"s_add_u32 {sr(S_TT)}, {sr(S_TT)}, 1"),
-               I(f"s_add_u32 {sr(S_TSLOT)}, {sr(S_TSLOT)}, 1")])
     # ---- Q rows into AGPRs, rotated when rope_q
     # Q resource base = q + b * q_sb + (kvh << gshift) * q_sh
     e([I(f"s_lshl_b32 {sr(S_T3)}, {sr(S_KVH)}, {gs}")])
@@ -1190,18 +1198,29 @@ def setup_block(gen: Gen):
         for ks in range(8):
             e(I(f"buffer_load_dwordx4 {vr(qt[rb] + 4 * ks, 4)}, {vr(V_QOFF + rb)}, {sr(S_RQ, 4)}, 0 "
                 f"offen offset:{32 * ks}"))
-    if PAGED:
-        # the page ids of tiles 0 .. 2 (issued before the 16 Q loads), then their transfers,
-        # then the page ids of tiles 3 and 4 for the first pair of the loop (S_RQ: the
-        # block-table row again; the Q loads have read their resource)
-        assert PAIR
-        e(I("s_waitcnt vmcnt(16)"))
-        for t in range(3):
-            e(transfer_paged(sr(S_TT), 4 * t))
+    def tile_transfers(pending: int) -> int:
+        """The transfers of tiles 0 .. 2 into stages 0 .. 2, issued after the Q loads and the
+        first (cos, sin) loads so that those reach the rotation first. Paged: once the page ids
+        of tiles 0 .. 2 (issued before the Q loads, `pending` loads ago) have landed, then the
+        page ids of tiles 3 and 4 for the first pair of the loop (S_RQ: the block-table row
+        again; the Q loads have read their resource). Returns the loads issued."""
+        if PAGED:
+            assert PAIR
+            e(I(f"s_waitcnt vmcnt({pending})"))
+            for t in range(3):
+                e(transfer_paged(sr(S_TT), 4 * t))
+                e([I(f"s_add_u32 {sr(S_TT)}, {sr(S_TT)}, 1"),
+                   I(f"s_add_u32 {sr(S_TSLOT)}, {sr(S_TSLOT)}, 1")])
+            e(bt_resource())
+            e(pt_load(sr(S_TT)))
+            return 3 * 8 + 1
+        for _ in range(3 if PAIR else 2):
+            e(transfer_setup(sr(S_TT)))
+            e(transfer_block("k"))
+            e(transfer_block("v"))
             e([I(f"s_add_u32 {sr(S_TT)}, {sr(S_TT)}, 1"),
                I(f"s_add_u32 {sr(S_TSLOT)}, {sr(S_TSLOT)}, 1")])
-        e(bt_resource())
-        e(pt_load(sr(S_TT)))
+        return (3 if PAIR else 2) * 8
     c2 = arg("c2")
 
     def rotate_chunk(w0, cs0):
@@ -1223,10 +1242,11 @@ def setup_block(gen: Gen):
 
     e(I(f"s_cmp_eq_u32 {arg('rope_q')}, 0"))
     e(I("s_cbranch_scc1 .Lq_norope"))
-    e([I(f"s_mov_b32 {sr(RT)}, {arg('rope')}"),
-       I(f"s_and_b32 {sr(RT + 1)}, {arg('rope', True)}, 0xffff"),
-       I(f"s_mov_b32 {sr(RT + 2)}, {arg('rope_bytes')}"),
-       I(f"s_mov_b32 {sr(RT + 3)}, 0x20000")])
+    rt_set = [I(f"s_mov_b32 {sr(RT)}, {arg('rope')}"),
+              I(f"s_and_b32 {sr(RT + 1)}, {arg('rope', True)}, 0xffff"),
+              I(f"s_mov_b32 {sr(RT + 2)}, {arg('rope_bytes')}"),
+              I(f"s_mov_b32 {sr(RT + 3)}, 0x20000")]
+    e(rt_set)
 
     def cs_batch(bi):
         rb, k0 = bi // 2, 4 * (bi % 2)
@@ -1237,15 +1257,21 @@ def setup_block(gen: Gen):
 
     e(cs_batch(0))
     e(cs_batch(1))
+    # (paged: the page-id load of tiles 0 .. 2 precedes the 16 Q and 16 (cos, sin) loads)
+    x = tile_transfers(32)
+    e(rt_set)  # (the transfer code used the temps RT overlays)
+    # batches 0 and 1 wait for everything but the loads issued after them (cs1 and the
+    # transfers, then the transfers and cs2); batch 2 also for the transfers
     for bi in range(4):
         rb, k0 = bi // 2, 4 * (bi % 2)
-        e(I(f"s_waitcnt vmcnt({8 if bi < 3 else 0})"))
+        e(I(f"s_waitcnt vmcnt({(8 + x) if bi < 2 else (8 if bi == 2 else 0)})"))
         for k in range(4):
             e(rotate_chunk(qt[rb] + 4 * (k0 + k), cs_area[bi % 2] + 8 * k))
         if bi + 2 < 4:
             e(cs_batch(bi + 2))
     e(I("s_branch .Lq_done"))
     e(I(".Lq_norope:"))
+    tile_transfers(16)
     e(I("s_waitcnt vmcnt(0)"))
     for rb in range(2):
         for w in range(32):
@@ -1261,13 +1287,14 @@ def setup_block(gen: Gen):
     for rb in range(2):
         for w in range(32):
             e(I(f"v_accvgpr_write_b32 {ar(A_Q + rb * 32 + w)}, {vr(qt[rb] + w)}"))
-    # ---- O = 0, running statistics
-    for i in range(128):
-        e(I(f"v_accvgpr_write_b32 {ar(A_O + i)}, 0"))
+    # ---- O = 0 (eight MFMAs of zero operands write the 128 accumulators: 8 instructions
+    # instead of 128 AGPR writes), running statistics
+    e([I(f"v_mov_b32 {vr(NB + i)}, 0") for i in range(32)])
+    for blk in range(8):
+        e(I(f"v_mfma_f32_32x32x16_bf16 {ar(A_O + 16 * blk, 16)}, {vr(NB, 4)}, {vr(NB, 4)}, 0"))
     for rb in range(2):
         e([I(f"v_mov_b32 {vr(V_M + rb)}, 0xff800000"),
            I(f"v_mov_b32 {vr(V_L + rb)}, 0")])
-    e([I(f"v_mov_b32 {vr(NB + i)}, 0") for i in range(32)])
     e(I(f"s_mov_b32 {sr(S_KSLOT)}, 0"))
     e(I(f"s_mov_b32 {sr(S_VSLOT)}, 0"))
     e(I("s_waitcnt vmcnt(0)"))
@@ -1381,7 +1408,7 @@ def build() -> Gen:
     gen.emit(I(f"s_mov_b32 {sr(S_KEY0)}, 0"))
     phase(gen, pv_x=None, pv_hh=0, s_x=1, s_hh=1, sm_x=None, sm_masked=False, prefetch_v_hh=0,
           after_last_k=advance_slot(S_KSLOT, VKA, 8))
-    exact_path(gen, 0, 0, 1)
+    exact_path(gen, 0, 0, 1, recompute=False)
     gen.emit([I(f"v_add_f32 {vr(V_L + rb)}, {vr(V_L + rb)}, {vr(V_LT + rb)}") for rb in range(2)])
     pro_end = gen.cur
     if PAIR:
