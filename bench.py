@@ -700,8 +700,6 @@ def main():
     ap.add_argument("--no-other-configs", action="store_true",
                     help="skip the other BASELINE configs (configs[0], [1], [4], backward, and "
                          "the alternative cfg3 prefill kernels)")
-    ap.add_argument("--prefill-v-layout", type=int, default=0,
-                    help="1: transposed-V pre-pass for the 16-bit prefill (fa_ctx_set_prefill_v_layout)")
     ap.add_argument("--prefill-kernel", type=int, default=-1,
                     help="-1 auto (assembly main loop where it applies), 0 HIP kernels only "
                          "(fa_ctx_set_prefill_kernel)")
@@ -776,7 +774,6 @@ def main():
     stream = ctx.stream
     ctx.set_prefill_policy(args.prefill_policy)
     ctx.set_prefill_kernel(args.prefill_kernel)
-    ctx.set_prefill_v_layout(args.prefill_v_layout)
     ops = []
     if args.only in (None, "prefill"):
         ops.append(("prefill",) + build_prefill(ctx, rng, args.data))

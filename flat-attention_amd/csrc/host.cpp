@@ -173,9 +173,6 @@ struct fa_ctx {
     // growable scratch for the K pre-rotation pass
     void* ws = nullptr;
     size_t ws_bytes = 0;
-    // growable scratch for the transposed V copy of the prefill
-    void* ws_vt = nullptr;
-    size_t ws_vt_bytes = 0;
     // growable scratch for the backward's per-row (LSE log2 e, rowsum(dO * O))
     void* ws_delta = nullptr;
     size_t ws_delta_bytes = 0;
@@ -183,7 +180,6 @@ struct fa_ctx {
     void* ws_ds = nullptr;
     size_t ws_ds_bytes = 0;
     int backward_ds_policy = -1;
-    int transpose_v_policy = -1;
     // 16-bit RoPE prefill scores: 0 = rotated Q/K rounded to the storage type, 1 = split
     // high/residual operands (fa_ctx_set_prefill_precision)
     int prefill_precision = 0;
@@ -576,7 +572,6 @@ int fa_ctx_destroy(fa_ctx* ctx) {
         (void)hipEventDestroy(st.done);
     }
     if (ctx->ws) (void)hipFree(ctx->ws);
-    if (ctx->ws_vt) (void)hipFree(ctx->ws_vt);
     if (ctx->ws_delta) (void)hipFree(ctx->ws_delta);
     if (ctx->ws_ds) (void)hipFree(ctx->ws_ds);
     if (ctx->meta_dev) (void)hipFree(ctx->meta_dev);
@@ -658,12 +653,6 @@ int fa_ctx_kernel_timing_range(fa_ctx* ctx, int32_t kernel_id, double* min_ms, d
         *min_ms = ctx->timed[kernel_id].min_ms;
         *max_ms = ctx->timed[kernel_id].max_ms;
     }
-    return ok();
-}
-
-int fa_ctx_set_prefill_v_layout(fa_ctx* ctx, int32_t transpose_v) {
-    if (!ctx) return fail(FA_ERR_NULL_ARGUMENT, "context is null");
-    ctx->transpose_v_policy = transpose_v < 0 ? -1 : (transpose_v ? 1 : 0);
     return ok();
 }
 
@@ -862,17 +851,15 @@ struct PrefillJob {
     uint64_t max_pos = 0;  // highest RoPE position used + 1
     uint64_t kv_bytes = 0;
     uint64_t k_rows = 0, k_heads = 0, k_period = 0;
-    bool no_vt = false;  // never use the transposed-V copy
 };
 
 // The resolved form of a prefill job: variant decisions and the device memory the launch uses
 // (the context's caches for a one-shot call, memory owned by a prepared forward otherwise).
 struct PrefillRun {
     PrefillJob j;
-    bool prerot = false, vt = false;
+    bool prerot = false;
     float2* table = nullptr;  // RoPE (cos, sin) rows [0, max_pos)
     void* ws = nullptr;       // rotated K (prerot)
-    void* wsv = nullptr;      // V^T (vt)
 };
 
 // Decides the variant and gathers the memory. own == false: the context's growable caches;
@@ -881,7 +868,6 @@ struct PrefillRun {
 struct PrefillChoice {
     bool prerot = false;  // K rotated once by the pre-pass
     bool split_qk = false;  // precise 16-bit scores: K rotated on load, split Q/K
-    bool vt = false;      // transposed-V copy
 };
 
 PrefillChoice choose_prefill(const fa_ctx* ctx, const PrefillJob& j) {
@@ -893,18 +879,11 @@ PrefillChoice choose_prefill(const fa_ctx* ctx, const PrefillJob& j) {
             c.split_qk = true;
         }
     }
-    c.vt = !j.paged && !j.no_vt && j.dtype != FA_DTYPE_F32 && j.a.head_dim % 8 == 0 &&
-           ctx->transpose_v_policy == 1;
     return c;
 }
 
-uint64_t vt_bytes(const PrefillJob& j) {
-    const uint64_t s_pad = ((uint64_t)j.a.kv_len + 63) / 64 * 64;
-    return (uint64_t)j.a.batch * j.a.kv_heads * j.a.head_dim * s_pad * 2u;
-}
-
 // Device allocations a one-shot call of `j` would make through the context's growable caches
-// (RoPE table, rotated-K and V^T workspaces), given what they hold now.
+// (RoPE table, rotated-K workspace), given what they hold now.
 void predict_prefill_allocs(const fa_ctx* ctx, const PrefillJob& j, const PrefillChoice& c,
                             uint32_t* count, uint64_t* bytes) {
     *count = 0;
@@ -921,10 +900,6 @@ void predict_prefill_allocs(const fa_ctx* ctx, const PrefillJob& j, const Prefil
     if (c.prerot && ctx->ws_bytes < j.kv_bytes) {
         ++*count;
         *bytes += j.kv_bytes;
-    }
-    if (c.vt && ctx->ws_vt_bytes < vt_bytes(j)) {
-        ++*count;
-        *bytes += vt_bytes(j);
     }
 }
 
@@ -968,33 +943,13 @@ int resolve_prefill(fa_ctx* ctx, PrefillJob& j, bool own, PrefillRun* r) {
             return rc;
         }
     }
-    // Optional transposed V copy for the 16-bit contiguous kernel (off unless selected): the V^T
-    // operand then comes from plain 16-byte LDS reads instead of transposing ones. It measured
-    // no faster at D = 128, so the extra pass is not run by default.
-    r->vt = choose_prefill(ctx, j).vt;
-    r->j.a.vt = nullptr;
-    r->j.a.vt_row = 0;
-    if (r->vt) {
-        const uint64_t s_pad = ((uint64_t)j.a.kv_len + 63) / 64 * 64;
-        const uint64_t bytes = vt_bytes(j);
-        if ((uint64_t)j.a.head_dim * s_pad * 2u > (uint64_t)INT32_MAX)
-            return fail(FA_ERR_INDEX_SPACE_EXCEEDED,
-                        "one transposed V slice spans %llu bytes; the kernel addresses at most 2 GiB",
-                        (unsigned long long)((uint64_t)j.a.head_dim * s_pad * 2u));
-        if (own) {
-            if (int rc = dev_alloc(ctx, &r->wsv, bytes)) return rc;
-        } else if (int rc = grow(ctx, &ctx->ws_vt, &ctx->ws_vt_bytes, bytes, &r->wsv)) {
-            return rc;
-        }
-        r->j.a.vt_row = (int)s_pad;
-    }
     return FA_OK;
 }
 
 // Telemetry of a prefill whose kernel arguments are `a` (after the pre-passes' substitutions):
 // kernel id and name, geometry, dispatch count, allocations and the fallback reason.
 void describe_prefill(const fa_ctx* ctx, const PrefillJob& j, const fa::PrefillArgs& a,
-                      bool prerot, bool vt, uint32_t dispatches, uint32_t allocs,
+                      bool prerot, uint32_t dispatches, uint32_t allocs,
                       uint64_t alloc_bytes, fa_telemetry* out) {
     // K read already rotated (pre-pass, or a paged cache that stores K rotated on append)
     const int kid = prefill_kernel_id(j.dtype, prerot || (j.paged && j.rope));
@@ -1009,9 +964,8 @@ void describe_prefill(const fa_ctx* ctx, const PrefillJob& j, const fa::PrefillA
     const char* base =
         j.dtype == FA_DTYPE_F32 ? "prefill_mfma_f32" : (a64 ? "prefill_a64" : "prefill_mfma16");
     char name[64];
-    if (prerot || vt)
-        snprintf(name, sizeof name, "%s%s%s<%s>", prerot ? "rotate_rows + " : "",
-                 vt ? "transpose_v + " : "", base, dt);
+    if (prerot)
+        snprintf(name, sizeof name, "rotate_rows + %s<%s>", base, dt);
     else if (j.paged)
         snprintf(name, sizeof name, "%s<%s> (paged%s)", base, dt, j.rope ? ", K stored rotated" : "");
     else if (a.split_qk)
@@ -1024,8 +978,8 @@ void describe_prefill(const fa_ctx* ctx, const PrefillJob& j, const fa::PrefillA
                    alloc_bytes);
 }
 
-// Enqueues the resolved prefill on the context's stream: optional K pre-rotation and V
-// transpose passes, then the prefill kernel. No allocation, copy or wait.
+// Enqueues the resolved prefill on the context's stream: the optional K pre-rotation pass, then
+// the prefill kernel. No allocation, copy or wait.
 int enqueue_prefill(fa_ctx* ctx, const PrefillRun& r) {
     fa::PrefillArgs a = r.j.a;
     const PrefillJob& j = r.j;
@@ -1040,15 +994,6 @@ int enqueue_prefill(fa_ctx* ctx, const PrefillRun& r) {
         a.rope_k = 0;
         dispatches++;
     }
-    if (r.vt) {
-        begin_span(ctx);
-        fa::launch_transpose_v(j.dt, a.v, a.k_sb, a.k_sh, a.k_ss, a.batch, a.kv_heads, a.kv_len,
-                               a.head_dim, a.vt_row, r.wsv, ctx->stream);
-        end_span(ctx, FA_KERNEL_TRANSPOSE_V);
-        HIP_TRY(hipGetLastError());
-        a.vt = r.wsv;
-        dispatches++;
-    }
     unsigned grid[3], block = 0;
     // K read already rotated (pre-pass, or a paged cache that stores K rotated on append)
     const int kid = prefill_kernel_id(j.dtype, r.prerot || (j.paged && j.rope));
@@ -1057,7 +1002,7 @@ int enqueue_prefill(fa_ctx* ctx, const PrefillRun& r) {
     end_span(ctx, kid);
     HIP_TRY(hipGetLastError());
     dispatches++;
-    describe_prefill(ctx, j, a, r.prerot, r.vt, dispatches, ctx->call_allocs,
+    describe_prefill(ctx, j, a, r.prerot, dispatches, ctx->call_allocs,
                      ctx->call_alloc_bytes, &ctx->last);
     return FA_OK;
 }
@@ -1197,11 +1142,10 @@ int fa_forward_gqa_rope_telemetry(fa_ctx* ctx, const fa_grouped_shape* sh, const
     fa::PrefillArgs a = j.a;  // the arguments the prefill kernel would receive
     if (c.prerot) a.rope_k = 0;
     if (c.split_qk) a.split_qk = 1;
-    a.vt = c.vt ? (const void*)1 : nullptr;
     a.a64 = ctx->prefill_kernel_policy != 0;
     a.rope_rows = (int)j.max_pos;
     if (j.rope) a.rope_table = (const float2*)(uintptr_t)16;  // stands for the table the call builds
-    describe_prefill(ctx, j, a, c.prerot, c.vt, 1u + c.prerot + c.vt, allocs, bytes, out);
+    describe_prefill(ctx, j, a, c.prerot, 1u + c.prerot, allocs, bytes, out);
     return ok();
 }
 
@@ -1269,7 +1213,6 @@ int fa_prepared_forward_destroy(fa_prepared_forward* p) {
     (void)hipStreamSynchronize(p->ctx->stream);
     if (p->run.table) (void)hipFree(p->run.table);
     if (p->run.ws) (void)hipFree(p->run.ws);
-    if (p->run.wsv) (void)hipFree(p->run.wsv);
     delete p;
     return ok();
 }
@@ -1467,7 +1410,6 @@ int fa_forward_projection_variable(fa_ctx* ctx, const void* q, size_t q_bytes, c
     PrefillJob j{};
     j.dt = (Dtype)dtype;
     j.dtype = dtype;
-    j.no_vt = true;  // the transposed-V copy would include padded rows
     fa::PrefillArgs& a = j.a;
     const int64_t D = (int64_t)sh->head_dim, QW = (int64_t)sh->q_heads * D,
                   KW = (int64_t)sh->kv_heads * D;

@@ -36,10 +36,6 @@ struct PrefillArgs {
     float scale;               // softmax scale
     const int* block_tables;   // paged only
     int bt_stride, page_size;
-    // Optional transposed V (16-bit contiguous only): vt[(b*kv_heads + h)*head_dim + d][key],
-    // rows of vt_row keys (kv_len rounded up to 64, zero padded). nullptr = read V directly.
-    const void* vt;
-    int vt_row;
     // Variable-length batch (contiguous K/V only): 4 ints per batch element — active query
     // rows, active K/V rows, causal position and RoPE position of query row 0 — overriding
     // q_len, kv_len, causal_offset and q_rope_offset; padded query rows get O = 0, LSE = -inf.
@@ -181,11 +177,6 @@ void launch_append(Dtype dt, const AppendArgs& a, hipStream_t s);
 
 // Rotate every row of a [rows, heads*head_dim] tensor (in place allowed); row r is at RoPE
 // position offset + r % period. head_dim must be a multiple of 8.
-// V [batch, heads, seq, head_dim] (element strides sb, sh, ss) -> V^T
-// out[((b*heads + h)*head_dim + d)*s_pad + key], keys in [seq, s_pad) zero. 16-bit types only.
-void launch_transpose_v(Dtype dt, const void* in, int64_t sb, int64_t sh, int64_t ss, int batch,
-                        int heads, int seq, int head_dim, int s_pad, void* out, hipStream_t s);
-
 void launch_rotate_rows(Dtype dt, const void* in, void* out, int rows, int heads, int head_dim,
                         int64_t period, const float2* table, int offset, hipStream_t s);
 

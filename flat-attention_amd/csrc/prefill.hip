@@ -97,9 +97,7 @@ constexpr float kRescaleLog2 = 8.0f;
 
 // ------------------------------------------------------------------ 16-bit MFMA kernel
 // K/V source addressing modes.
-// kContigVT: contiguous K, V read from its transposed copy (PrefillArgs::vt), so the V^T operand
-// of O^T += V^T.P^T is a plain 16-byte LDS read rather than a transposing one.
-enum : int { kContig = 0, kPaged16 = 1, kPagedAny = 2, kContigVT = 3 };
+enum : int { kContig = 0, kPaged16 = 1, kPagedAny = 2 };
 
 // Physical row of `key` for batch b. kPaged16 requires page_size % 16 == 0 and a key group of
 // 16 consecutive keys per wave, so the block-table entry is wave-uniform (one scalar load).
@@ -130,7 +128,7 @@ __device__ __forceinline__ int64_t paged_row(const PrefillKArgs& ka, int b, int 
 // other group's softmax.
 // (kPaged16: the transferring group stages the paged K/V tiles through registers)
 __host__ __device__ constexpr bool prefill_pingpong(int pmode, bool ropek) {
-    return (pmode == kContig || pmode == kContigVT || pmode == kPaged16) && !ropek;
+    return (pmode == kContig || pmode == kPaged16) && !ropek;
 }
 
 // Scheduling groups (LLVM AMDGPU sched_group_barrier masks: 0x2 VALU, 0x8 MFMA, 0x100 DS read, 0x400 transcendental).
@@ -164,11 +162,8 @@ __global__ __launch_bounds__(64 * NW, SPLIT ? 1 : 2) void prefill_mfma16(Prefill
     constexpr int KPASS = BN / KRPP;
     constexpr int KROWB = DPAD * 2 + 16;    // padded K row (bytes)
     constexpr int VROWB = DPAD * 2 + 64;    // padded V row (bytes)
-    constexpr bool VT = PMODE == kContigVT;
-    constexpr bool CONTIG = PMODE == kContig || VT;
-    constexpr int VTROWB = BN * 2 + 16;     // padded V^T row: 64 keys of one dim (bytes)
-    // (V^T region rounded to whole KiB: each transfer instruction fills 1 KiB)
-    constexpr int VBYTES = VT ? (DPAD * VTROWB + 1023) / 1024 * 1024 : BN * VROWB;
+    constexpr bool CONTIG = PMODE == kContig;
+    constexpr int VBYTES = BN * VROWB;
     // One K/V stage, or two (double buffering: tile j+1 is staged while tile j is computed).
     // (SPLIT: the K residual tile follows V in every stage)
     constexpr int KLO = BN * KROWB + VBYTES;
@@ -179,9 +174,9 @@ __global__ __launch_bounds__(64 * NW, SPLIT ? 1 : 2) void prefill_mfma16(Prefill
     // memory traffic) offset. Instructions beyond a tile's slot count target a dummy KiB.
     constexpr bool DMA = CONTIG && !ROPEK;
     // 16-byte slots per padded row: K, V, V^T (64 keys of one dim)
-    constexpr int KSL = KROWB / 16, VSL = VROWB / 16, VTSL = VTROWB / 16;
+    constexpr int KSL = KROWB / 16, VSL = VROWB / 16;
     // transfer instructions per tile (64 slots each)
-    constexpr int KINS = KSL, VINS = VT ? (DPAD * VTSL + 63) / 64 : VSL;
+    constexpr int KINS = KSL, VINS = VSL;
     // Waves sharing the transfers: all of them, or group 1 alone under the ping-pong schedule.
     constexpr int NWD = PP ? 4 : NW;
     constexpr int KI = (KINS + NWD - 1) / NWD, VI = (VINS + NWD - 1) / NWD;  // per wave
@@ -311,24 +306,6 @@ __global__ __launch_bounds__(64 * NW, SPLIT ? 1 : 2) void prefill_mfma16(Prefill
     const uint32_t lane_off = (uint32_t)k_r * row_bytes + kd2;  // this thread's row/chunk
     constexpr int kRsrcFlags = 0x00020000;
     u32x4_t kreg[KPASS], vreg[KPASS];
-    // V^T staging: thread chunk p covers dim (tid + 256p) / 8, keys 8 * (tid % 8) .. +7 of the
-    // tile; dims >= head_dim lie past the resource range and read as 0. (DPAD * 8 / 256 ==
-    // KPASS chunks per thread.)
-    const uint8_t* const vtb8 =
-        VT ? (const uint8_t*)a.vt + (((int64_t)b * a.kv_heads + kvh) * D) * a.vt_row * 2 : nullptr;
-
-    auto load_vt = [&](int tile) {
-        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-            (void*)vtb8, (short)0, D * a.vt_row * 2, kRsrcFlags);
-#pragma unroll
-        for (int p = 0; p < KPASS; ++p) {
-            const int c = tid + 256 * p;
-            const uint32_t off = ((uint32_t)(c >> 3) * (uint32_t)a.vt_row +
-                                  (uint32_t)(tile * BN + (c & 7) * 8)) * 2u;
-            vreg[p] = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)off, 0, 0);
-        }
-    };
-
     // One tile of K or V (base = kb8 or vb8) into `reg`.
     auto load_one = [&](int tile, const uint8_t* base, u32x4_t (&reg)[KPASS]) {
         const int key_base = tile * BN;
@@ -408,24 +385,11 @@ __global__ __launch_bounds__(64 * NW, SPLIT ? 1 : 2) void prefill_mfma16(Prefill
         }
     };
     auto store_v = [&]() {
-        if constexpr (VT) {
 #pragma unroll
-            for (int p = 0; p < KPASS; ++p) {
-                const int c = tid + 256 * p;
-                *(u32x4_t*)(smem + st_w + BN * KROWB + (c >> 3) * VTROWB + (c & 7) * 16) =
-                    vreg[p];
-            }
-        } else {
-#pragma unroll
-            for (int p = 0; p < KPASS; ++p)
-                *(u32x4_t*)(smem + st_w + BN * KROWB + (p * KRPP + k_r) * VROWB + k_dc * 16) =
-                    vreg[p];
-        }
+        for (int p = 0; p < KPASS; ++p)
+            *(u32x4_t*)(smem + st_w + BN * KROWB + (p * KRPP + k_r) * VROWB + k_dc * 16) = vreg[p];
     };
-    auto load_v = [&](int tile) {
-        if constexpr (VT) load_vt(tile);
-        else load_one(tile, vb8, vreg);
-    };
+    auto load_v = [&](int tile) { load_one(tile, vb8, vreg); };
 
     f32x16_t oacc[MB];
 #pragma unroll
@@ -573,20 +537,7 @@ __global__ __launch_bounds__(64 * NW, SPLIT ? 1 : 2) void prefill_mfma16(Prefill
     };
 
     // ---- O^T += V^T . P^T over the V tile in LDS
-    // V^T layout: lane reads dim mb*32 + (lane & 31), keys 16 s2 + 8 g .. +7 (16 bytes).
-    const int vt_rd = BN * KROWB + (lane & 31) * VTROWB + g * 16;
     auto compute_pv = [&](const u32x4_t (&pop)[4], auto&& hook) {
-        if constexpr (VT) {
-#pragma unroll
-            for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-                for (int s2 = 0; s2 < 4; ++s2) {
-                    const u32x4_t av =
-                        *(const u32x4_t*)(smem + st_v + vt_rd + mb * 32 * VTROWB + s2 * 32);
-                    oacc[mb] = H::mfma32(av, pop[s2], oacc[mb]);
-                }
-            return;
-        }
         // Step i: O^T block mb = i % MB (the MB accumulators rotate), keys 16 s2 .. (s2 = i / MB);
         // the V^T operands of the next RV steps are already being read (two ds_read_b64_tr_b16
         // per step, a register ring).
@@ -646,21 +597,12 @@ __global__ __launch_bounds__(64 * NW, SPLIT ? 1 : 2) void prefill_mfma16(Prefill
         }
 #pragma unroll
         for (int i = 0; i < VI; ++i) {
-            if constexpr (VT) {
-                // V^T row r = dim r, 64 keys (8 slots) of the tile, then one pad slot
-                const int q = 64 * (dw + NWD * i) + lane, r = q / VTSL, c = q % VTSL;
-                voff[i] = (dw + NWD * i < VINS && c < 8 && r < D)
-                              ? ((uint32_t)r * (uint32_t)a.vt_row + (uint32_t)c * 8u) * 2u
-                              : kOob;
-            } else {
-                const int q = 64 * (dw + NWD * i) + lane, r = q / VSL, c = q % VSL;
-                voff[i] = (dw + NWD * i < VINS && c < CPR && (FULLD || c * 8 < D))
-                              ? (uint32_t)r * row_bytes + (uint32_t)c * 16u
-                              : kOob;
-            }
+            const int q = 64 * (dw + NWD * i) + lane, r = q / VSL, c = q % VSL;
+            voff[i] = (dw + NWD * i < VINS && c < CPR && (FULLD || c * 8 < D))
+                          ? (uint32_t)r * row_bytes + (uint32_t)c * 16u
+                          : kOob;
         }
         const int nrec_all = (kv_len_ - 1) * (int)row_bytes + D * 2;
-        const int nrec_vt = VT ? D * a.vt_row * 2 : 0;
         // Tile `tile` of K and V into the stage at byte offset `st`.
         const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_void_t*)smem;
         // One transfer instruction (i-th of this wave) of tile `tile` of K / V into stage `st`.
@@ -672,14 +614,8 @@ __global__ __launch_bounds__(64 * NW, SPLIT ? 1 : 2) void prefill_mfma16(Prefill
             buffer_to_lds16(rk, __builtin_amdgcn_readfirstlane(lds0 + dst), koff[i]);
         };
         auto dma_v1 = [&](int tile, int st, int i) {
-            i32x4_t rv;
-            if constexpr (VT) {
-                const int base = tile * BN * 2;  // key offset within every V^T row
-                rv = make_rsrc_words(vtb8 + base, nrec_vt - base);
-            } else {
-                const int base = tile * BN * (int)row_bytes;
-                rv = make_rsrc_words(vb8 + base, nrec_all - base);
-            }
+            const int base = tile * BN * (int)row_bytes;
+            const i32x4_t rv = make_rsrc_words(vb8 + base, nrec_all - base);
             const int k = dw + NWD * i;
             const int dst = k < VINS ? st + BN * KROWB + k * 1024 : DUMMY;
             buffer_to_lds16(rv, __builtin_amdgcn_readfirstlane(lds0 + dst), voff[i]);
@@ -1282,10 +1218,7 @@ static void launch16r(const PrefillKArgs& ka, int dpad, dim3 grid, hipStream_t s
 template <typename T>
 static void launch16(const PrefillKArgs& ka, bool paged, int dpad, dim3 grid, hipStream_t s) {
     if (!paged) {
-        if (ka.a.vt) {
-            if (ka.a.rope_k) launch16r<T, kContigVT, true>(ka, dpad, grid, s);
-            else launch16r<T, kContigVT, false>(ka, dpad, grid, s);
-        } else if (ka.a.rope_k && ka.a.split_qk) {
+        if (ka.a.rope_k && ka.a.split_qk) {
             launch16r<T, kContig, true, true>(ka, dpad, grid, s);
         } else if (ka.a.rope_k) {
             launch16r<T, kContig, true>(ka, dpad, grid, s);

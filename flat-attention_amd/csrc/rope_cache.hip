@@ -125,45 +125,6 @@ void launch_rotate_rows(Dtype dt, const void* in, void* out, int rows, int heads
     }
 }
 
-// One 64-key tile of one (batch, head): rows of 64 keys staged in LDS, written back as head_dim
-// rows of 64 keys. grid (s_pad / 64, heads, batch), 256 threads.
-template <typename T>
-__global__ __launch_bounds__(256) void transpose_v_kernel(const uint16_t* in, int64_t sb,
-                                                          int64_t sh, int64_t ss, int seq,
-                                                          int head_dim, int s_pad, uint16_t* out) {
-    constexpr int kKeys = 64, kMaxD = 128, kRow = kMaxD + 8;  // padded LDS row (elements)
-    __shared__ uint16_t tile[kKeys * kRow];
-    const int key0 = blockIdx.x * kKeys, h = blockIdx.y, b = blockIdx.z;
-    const uint16_t* src = in + (int64_t)b * sb + (int64_t)h * sh;
-    const int cpr = head_dim / 8;  // 16-byte chunks per key row
-    for (int c = threadIdx.x; c < kKeys * cpr; c += 256) {
-        const int r = c / cpr, d0 = (c % cpr) * 8;
-        const int key = key0 + r;
-        uint4 v = {0u, 0u, 0u, 0u};
-        if (key < seq) v = *(const uint4*)(src + (int64_t)key * ss + d0);
-        *(uint4*)(tile + r * kRow + d0) = v;
-    }
-    __syncthreads();
-    uint16_t* dst = out + ((int64_t)(b * gridDim.y + h) * head_dim) * s_pad + key0;
-    for (int c = threadIdx.x; c < head_dim * (kKeys / 8); c += 256) {
-        const int d = c / (kKeys / 8), k0 = (c % (kKeys / 8)) * 8;
-        uint32_t w[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-            w[j] = (uint32_t)tile[(k0 + 2 * j) * kRow + d] |
-                   ((uint32_t)tile[(k0 + 2 * j + 1) * kRow + d] << 16);
-        *(uint4*)(dst + (int64_t)d * s_pad + k0) = uint4{w[0], w[1], w[2], w[3]};
-    }
-}
-
-void launch_transpose_v(Dtype dt, const void* in, int64_t sb, int64_t sh, int64_t ss, int batch,
-                        int heads, int seq, int head_dim, int s_pad, void* out, hipStream_t s) {
-    (void)dt;  // the transpose moves 16-bit elements; bf16 and f16 share the kernel
-    dim3 grid((unsigned)(s_pad / 64), (unsigned)heads, (unsigned)batch);
-    transpose_v_kernel<bf16_t><<<grid, 256, 0, s>>>((const uint16_t*)in, sb, sh, ss, seq,
-                                                     head_dim, s_pad, (uint16_t*)out);
-}
-
 // grid: (append_len, n_seqs); block: row chunks of 8 elements (kv_heads*head_dim/8 threads,
 // looped when wider than the block).
 template <typename T>

@@ -126,7 +126,6 @@ PROTOTYPES = {
     "fa_ctx_device_name": (INT, [VP, ctypes.c_char_p, SZ]),
     "fa_ctx_set_prefill_policy": (INT, [VP, I32]),
     "fa_ctx_set_prefill_kernel": (INT, [VP, I32]),
-    "fa_ctx_set_prefill_v_layout": (INT, [VP, I32]),
     "fa_kernel_variant_for_shape": (INT, [VP, U64, I32, INT, P(I32)]),
     "fa_buf_alloc": (INT, [VP, SZ, P(VP)]),
     "fa_buf_free": (INT, [VP, VP]),

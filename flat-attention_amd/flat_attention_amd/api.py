@@ -292,10 +292,6 @@ class HipContext:
         1: split high/residual operands, f32-level scores for the 16-bit RoPE prefill."""
         check(lib().fa_ctx_set_prefill_precision(self.handle, mode))
 
-    def set_prefill_v_layout(self, transpose_v: int):
-        """-1 automatic, 0 stream V rows, 1 stream a transposed V copy (16-bit prefill)."""
-        check(lib().fa_ctx_set_prefill_v_layout(self.handle, transpose_v))
-
     def set_kernel_timing(self, enable: bool):
         """Bracket every dispatch with HIP events on the context's stream (clears totals)."""
         check(lib().fa_ctx_set_kernel_timing(self.handle, 1 if enable else 0))

@@ -151,7 +151,7 @@ typedef enum fa_kernel_id {
     FA_KERNEL_ROPE_TABLE = 13,
     FA_KERNEL_ROPE_ROTATE = 14,
     FA_KERNEL_DECODE_PAGED_MFMA = 15,     /* 16-bit KV, page_size % 16 == 0: P.V on MFMA */
-    FA_KERNEL_TRANSPOSE_V = 16,           /* V -> V^T pre-pass of the 16-bit contiguous prefill */
+    /* 16: retired (a transposed-V pre-pass that measured level) */
     FA_KERNEL_BACKWARD_RECOMPUTE = 17     /* delta + dK/dV + dQ recompute backward (MFMA) */
 } fa_kernel_id;
 
@@ -589,11 +589,6 @@ int fa_ctx_set_prefill_precision(fa_ctx* ctx, int32_t mode);
  * page_size % 16 == 0, automatic split and <= 8 KV-head units run head-grouped workgroups),
  * 0 = one-wave workgroups for every plan; 1 = the same as -1. */
 int fa_ctx_set_decode_policy(fa_ctx* ctx, int32_t grouped);
-/* V layout policy of the 16-bit contiguous prefill (same role as the K policy above): 1 = copy
- * V once into a transposed workspace [batch, kv_heads, head_dim, kv_len rounded up to 64] and
- * stream V^T tiles, 0 = stream V rows and transpose in the kernel, -1 = automatic (currently
- * 0). Both layouts give bit-identical results. */
-int fa_ctx_set_prefill_v_layout(fa_ctx* ctx, int32_t transpose_v);
 /* dQ policy of the recompute backward (no counterpart in the reference, whose backward
  * recomputes every product per scalar gradient, src/wgpu_backward_grouped.rs:318). store_ds:
  * -1 = automatic (default) and 1: with 16-bit storage and 16-byte aligned tensors, bwd_dkdv also

@@ -181,36 +181,6 @@ def test_prerotated_and_fused_k_rotation_are_bit_identical(hip):
     assert np.array_equal(l0.view(np.uint32), l1.view(np.uint32))
 
 
-@pytest.mark.parametrize("dtype,rnd", [(fa.DTYPE_BF16, bf16_round), (fa.DTYPE_F16, f16_round)])
-@pytest.mark.parametrize("D,S,causal", [(128, 150, True), (128, 64, False), (64, 200, True),
-                                        (32, 77, False), (120, 131, True)])
-def test_transposed_v_layout_is_bit_identical_and_matches_oracle(hip, dtype, rnd, D, S, causal):
-    """The V^T pre-pass only changes how V reaches the MFMA: results are bitwise identical to
-    streaming V rows, for ragged kv lengths (zero-padded V^T tail) and head_dim < 128."""
-    B, hq, hkv = 2, 8, 2
-    q, k, v = (rnd(normal(n, s)) for n, s in
-               ((B * hq * S * D, 11), (B * hkv * S * D, 12), (B * hkv * S * D, 13)))
-    shape = fa.GroupedAttentionShape(B, hq, hkv, S, D)
-    rot = fa.RotaryEmbeddingConfig(1e4, 3)
-    cfg = fa.FlatAttentionConfig(causal)
-    hip.set_prefill_v_layout(0)
-    hip.set_prefill_kernel(0)  # both layouts through the HIP main loop
-    try:
-        o0, l0 = _run_grouped(hip, q, k, v, shape, cfg, rot, dtype)
-        assert "transpose_v" not in hip.last_telemetry().kernel_name
-        hip.set_prefill_v_layout(1)
-        o1, l1 = _run_grouped(hip, q, k, v, shape, cfg, rot, dtype)
-        assert "transpose_v" in hip.last_telemetry().kernel_name
-    finally:
-        hip.set_prefill_v_layout(-1)
-        hip.set_prefill_kernel(-1)
-    assert np.array_equal(o0.view(np.uint32), o1.view(np.uint32))
-    assert np.array_equal(l0.view(np.uint32), l1.view(np.uint32))
-    eo, el = _oracle_grouped(q, k, v, shape, causal, rot, units=(0, 1))
-    assert_close("O unit 0", o1[:S * D], eo[:S * D], H16_ATOL, 0.0)
-    assert_close("LSE unit 0", l1[:S], el[:S], H16_ATOL, 0.0)
-
-
 @pytest.mark.parametrize("kernel", [-1, 0])
 def test_cfg3_full_size_bf16_gqa_rope_causal(hip, kernel):
     """BASELINE configs[2] at full size: B2 Hq32 Hkv8 N4096 D128 bf16, theta 1e4, causal.

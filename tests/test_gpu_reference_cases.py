@@ -598,7 +598,7 @@ def _same_dispatch(snap, real):
     ("mha", (2, 2, 300, 128), fa.DTYPE_BF16, None, {}),
     ("gqa", (2, 8, 2, 130, 128), fa.DTYPE_BF16, (1e4, 3), {}),
     ("gqa", (1, 6, 1, 77, 64), fa.DTYPE_F16, (5e5, 0), {"precision": 1}),
-    ("gqa", (1, 8, 2, 65, 128), fa.DTYPE_BF16, (1e4, 0), {"v_layout": 1}),
+    ("gqa", (1, 8, 2, 65, 128), fa.DTYPE_BF16, (1e4, 0), {"kernel": 0}),
     ("gqa", (1, 4, 2, 33, 6), fa.DTYPE_F32, (1e4, 0), {}),
     ("gqa", (1, 4, 2, 33, 64), fa.DTYPE_F32, (1e4, 0), {"prerotate": 0}),
 ])
@@ -614,8 +614,8 @@ def test_passive_telemetry_snapshot_matches_the_dispatch(case):
     try:
         if "precision" in pol:
             ctx.set_prefill_precision(pol["precision"])
-        if "v_layout" in pol:
-            ctx.set_prefill_v_layout(pol["v_layout"])
+        if "kernel" in pol:
+            ctx.set_prefill_kernel(pol["kernel"])
         if "prerotate" in pol:
             ctx.set_prefill_policy(pol["prerotate"])
         cfg = fa.FlatAttentionConfig(True)
