@@ -104,6 +104,7 @@ KERNEL = KERNEL_CONTIG
 PAGED = False
 NSTAGE = 5            # LDS stages of (K 16 KiB, V 16 KiB): tiles j .. j + NSTAGE - 1 resident
 PAIR = True           # one barrier per two iterations (needs NSTAGE = 5)
+ISSUE_WEIGHT = {"trans": 2}  # relative issue cost of an instruction kind in the phase scheduler
 LDS_BYTES = NSTAGE * 32768
 INVALID_OFF = 0x80000000  # beyond every resource range used for stores
 O_ROWB = 272          # O staging in LDS: 64 rows of 256 bytes per wave, padded to 272
@@ -744,6 +745,9 @@ def phase(gen: Gen, *, pv_x, pv_hh, s_x, s_hh, sm_x, sm_masked, pre=(),
     # initial reads: fill the rings
     issue_reads(DV + DK)
     total_valu = len(valu_stream)
+    # issue cost of the stream: a transcendental takes about twice an ordinary VALU slot
+    cost = [ISSUE_WEIGHT.get(x.kind, 1) for x in valu_stream]
+    left = sum(cost)
     for mi, (kind, idx, rb) in enumerate(mlist):
         if kind == "pv":
             gen.ds_wait_for(v_issued[idx])
@@ -763,13 +767,15 @@ def phase(gen: Gen, *, pv_x, pv_hh, s_x, s_hh, sm_x, sm_masked, pre=(),
         gen.emit(ins)
         issued_m = mi
         issue_reads(2)
-        # spread the VALU work evenly over the remaining MFMAs
+        # spread the VALU work evenly (by issue cost) over the remaining MFMAs
         remaining_m = nm - mi
-        take = (total_valu - vi + remaining_m - 1) // remaining_m if remaining_m else 0
-        for _ in range(take):
-            if vi < total_valu:
-                gen.emit(valu_stream[vi])
-                vi += 1
+        budget = (left + remaining_m - 1) // remaining_m if remaining_m else 0
+        spent = 0
+        while vi < total_valu and spent < budget:
+            gen.emit(valu_stream[vi])
+            spent += cost[vi]
+            left -= cost[vi]
+            vi += 1
     while vi < total_valu:
         gen.emit(valu_stream[vi])
         vi += 1
