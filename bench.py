@@ -498,7 +498,8 @@ def summarize_pmc(fetch_csv: str, write_csv: str) -> dict:
     for name, key in (("prefill", "prefill_a64"), ("prefill_hip", "prefill_mfma16"),
                       ("decode", "decode_mfma"),
                       ("combine", "decode_combine"), ("rotate", "rotate_rows"),
-                      ("bwd_delta", "bwd_delta<"), ("bwd_dkdv", "bwd_dkdv<"),
+                      ("bwd_delta", "bwd_delta<"), ("bwd_dkdv_a64", "bwd_dkdv_a64"),
+                      ("bwd_dkdv", "bwd_dkdv<"),
                       ("bwd_dq_ds", "bwd_dq_ds<"), ("bwd_dq", "bwd_dq<")):
         try:
             fb = pick(fetch, key) * 1024.0 * f_scale
@@ -708,6 +709,9 @@ def main():
     ap.add_argument("--only", choices=["prefill", "decode", "backward"], default=None,
                     help="time one op alone (backward: the recompute backward at the prefill "
                          "shape, a line of its own)")
+    ap.add_argument("--backward-kernel", type=int, default=-1,
+                    help="--only backward: -1 / 1 the assembly dK/dV kernel where it applies "
+                         "(default), 0 the HIP kernel (fa_ctx_set_backward_kernel)")
     ap.add_argument("--backward-policy", type=int, default=-1,
                     help="--only backward: -1 stored dS (default), 0 dQ recomputes S and dP "
                          "(fa_ctx_set_backward_policy)")
@@ -758,6 +762,7 @@ def main():
     ctx = fa.HipContext(0)
     if args.only == "backward":
         ctx.set_backward_policy(args.backward_policy)
+        ctx.set_backward_kernel(args.backward_kernel)
         out = measure_backward(ctx, rng, args.steps, args.warmup, args.data)
         if args.calibrate_copy:
             a, b = fa.DeviceBuffer(ctx, COPY_BYTES), fa.DeviceBuffer(ctx, COPY_BYTES)

@@ -18,6 +18,7 @@
 #include "common.hpp"
 #include "kernels.hpp"
 
+#include <type_traits>
 #include <utility>
 
 namespace fa {
@@ -273,7 +274,7 @@ __device__ __forceinline__ void stage_rows(uint8_t* dst, const void* src, int nv
 
 // ------------------------------------------------------------------ (LSE log2 e, delta)
 // ld[row] = (LSE * log2 e, sum_d dO * O) for every query row.
-template <typename T>
+template <typename T, bool SPLIT = false>
 __global__ __launch_bounds__(256) void bwd_delta(BackwardArgs a, int64_t rows) {
     using B = Blk<T>;
     const int64_t row = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
@@ -308,7 +309,17 @@ __global__ __launch_bounds__(256) void bwd_delta(BackwardArgs a, int64_t rows) {
     }
 #pragma unroll
     for (int m = 8; m >= 1; m >>= 1) acc += __shfl_xor(acc, m, 16);
-    if (row < rows && sub == 0) a.ld[row] = make_float2(a.lse[row] * kLog2e, acc);
+    if (row < rows && sub == 0) {
+        if (SPLIT) {
+            // the assembly dK/dV kernel's layout: -LSE / scale and -delta, which it adds through
+            // the MFMA accumulator inputs of S and dP (P = exp2(scale log2 e (S - LSE / scale)))
+            float* ld = (float*)a.ld;
+            ld[row] = -(a.lse[row] / a.scale);
+            ld[rows + row] = -acc;
+        } else {
+            a.ld[row] = make_float2(a.lse[row] * kLog2e, acc);
+        }
+    }
 }
 
 // ------------------------------------------------------------------ dK, dV
@@ -988,8 +999,21 @@ void launch_dma(const BackwardArgs& a, hipStream_t s) {
 }
 
 template <typename T>
-void launch_dims(const BackwardArgs& a, hipStream_t s) {
+void launch_dims(const BackwardArgs& a, hipStream_t s, bool* a64_out) {
     const int64_t rows = (int64_t)a.batch * a.q_heads * a.seq;
+    if constexpr (std::is_same_v<T, bf16_t>) {
+        if (bwd_a64_eligible(Dtype::BF16, a)) {
+            hipLaunchKernelGGL((bwd_delta<T, true>), dim3((unsigned)((rows + 15) / 16)),
+                               dim3(256), 0, s, a, rows);
+            launch_bwd_a64(a, s);
+            const int nqd = (a.seq + kDqDsQueries - 1) / kDqDsQueries;
+            hipLaunchKernelGGL((bwd_dq_ds<T, 128>), dim3(nqd * a.batch * a.q_heads), dim3(512),
+                               0, s, a);
+            if (a64_out) *a64_out = true;
+            return;
+        }
+    }
+    if (a64_out) *a64_out = false;
     hipLaunchKernelGGL((bwd_delta<T>), dim3((unsigned)((rows + 15) / 16)), dim3(256), 0, s, a,
                        rows);
     if (a.head_dim <= 32) launch_dma<T, 32>(a, s);
@@ -999,11 +1023,11 @@ void launch_dims(const BackwardArgs& a, hipStream_t s) {
 
 }  // namespace
 
-void launch_backward(Dtype dt, const BackwardArgs& a, hipStream_t s) {
+void launch_backward(Dtype dt, const BackwardArgs& a, hipStream_t s, bool* a64_out) {
     switch (dt) {
-        case Dtype::F32: launch_dims<float>(a, s); break;
-        case Dtype::F16: launch_dims<f16_t>(a, s); break;
-        case Dtype::BF16: launch_dims<bf16_t>(a, s); break;
+        case Dtype::F32: launch_dims<float>(a, s, a64_out); break;
+        case Dtype::F16: launch_dims<f16_t>(a, s, a64_out); break;
+        case Dtype::BF16: launch_dims<bf16_t>(a, s, a64_out); break;
     }
 }
 

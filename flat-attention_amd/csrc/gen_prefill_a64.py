@@ -1602,8 +1602,16 @@ def finish_phase(gen: Gen, tag: str, x: int, hh: int, s_x) -> None:
 
 
 # --------------------------------------------------------------------------- output
-def render_kernel(gen: Gen, name: str) -> tuple[list[str], list[str], list[str]]:
-    """The text, kernel descriptor and metadata entry of one generated kernel."""
+def render_kernel(gen: Gen, name: str, num_vgpr: int = None, num_agpr: int = None,
+                  num_sgpr: int = None, lds_bytes: int = None,
+                  arg_bytes: int = None) -> tuple[list[str], list[str], list[str]]:
+    """The text, kernel descriptor and metadata entry of one generated kernel (resource counts
+    default to this generator's)."""
+    NUM_VGPR = globals()["NUM_VGPR"] if num_vgpr is None else num_vgpr
+    NUM_AGPR = globals()["NUM_AGPR"] if num_agpr is None else num_agpr
+    NUM_SGPR = globals()["NUM_SGPR"] if num_sgpr is None else num_sgpr
+    LDS_BYTES = globals()["LDS_BYTES"] if lds_bytes is None else lds_bytes
+    ARG_BYTES = globals()["ARG_BYTES"] if arg_bytes is None else arg_bytes
     fix_hazards(gen.blocks)
     text = ["\t.text", f"\t.globl {name}", "\t.p2align 8", f"\t.type {name},@function", f"{name}:"]
     for b in gen.blocks:
@@ -1654,12 +1662,14 @@ def render_kernel(gen: Gen, name: str) -> tuple[list[str], list[str], list[str]]
     return text, desc, meta
 
 
-def render(kernels: list[tuple[Gen, str, str]]) -> str:
-    """One code object holding every kernel: (generator state, symbol, label prefix)."""
+def render(kernels: list[tuple]) -> str:
+    """One code object holding every kernel: (generator state, symbol, label prefix[, resource
+    counts for render_kernel])."""
     lines = ['\t.amdgcn_target "amdgcn-amd-amdhsa--gfx950"', "\t.amdhsa_code_object_version 5"]
     metas = []
-    for gen, name, prefix in kernels:
-        text, desc, meta = render_kernel(gen, name)
+    for kern in kernels:
+        gen, name, prefix = kern[:3]
+        text, desc, meta = render_kernel(gen, name, **(kern[3] if len(kern) > 3 else {}))
         body = "\n".join(text + desc)
         if prefix:
             body = re.sub(r"\.L(\w+)", lambda m: f".L{prefix}{m.group(1)}", body)

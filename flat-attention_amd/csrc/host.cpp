@@ -180,6 +180,8 @@ struct fa_ctx {
     void* ws_ds = nullptr;
     size_t ws_ds_bytes = 0;
     int backward_ds_policy = -1;
+    // dK/dV kernel of the backward: -1 / 1 the assembly kernel where it applies, 0 HIP only
+    int backward_kernel_policy = -1;
     // 16-bit RoPE prefill scores: 0 = rotated Q/K rounded to the storage type, 1 = split
     // high/residual operands (fa_ctx_set_prefill_precision)
     int prefill_precision = 0;
@@ -552,6 +554,7 @@ int fa_ctx_create(int device, fa_ctx** out) {
     // the assembly prefill's code object (a load failure leaves the HIP kernels in use, which
     // the telemetry's kernel name shows)
     (void)fa::prefill_a64_load(device);
+    (void)fa::bwd_a64_load(device);
     if (hipEventCreateWithFlags(&ctx->na_copied, hipEventDisableTiming) != hipSuccess)
         ctx->na_copied = nullptr;
     if (hipHostMalloc((void**)&ctx->na_host, kNoAllocMetaBytes, hipHostMallocDefault) !=
@@ -679,6 +682,12 @@ int fa_ctx_set_prefill_precision(fa_ctx* ctx, int32_t mode) {
 int fa_ctx_set_prefill_kernel(fa_ctx* ctx, int32_t assembly) {
     if (!ctx) return fail(FA_ERR_NULL_ARGUMENT, "context is null");
     ctx->prefill_kernel_policy = assembly < 0 ? -1 : (assembly ? 1 : 0);
+    return ok();
+}
+
+int fa_ctx_set_backward_kernel(fa_ctx* ctx, int32_t assembly) {
+    if (!ctx) return fail(FA_ERR_NULL_ARGUMENT, "context is null");
+    ctx->backward_kernel_policy = assembly < 0 ? -1 : (assembly ? 1 : 0);
     return ok();
 }
 
@@ -3026,15 +3035,17 @@ int fa_backward_grouped(fa_ctx* ctx, const void* q, const void* k, const void* v
             a.ds_bytes = (int)bytes;
         }
     }
+    a.a64 = ctx->backward_kernel_policy != 0;
+    bool a64 = false;
     begin_span(ctx);
-    fa::launch_backward((Dtype)dtype, a, ctx->stream);
+    fa::launch_backward((Dtype)dtype, a, ctx->stream, &a64);
     end_span(ctx, FA_KERNEL_BACKWARD_RECOMPUTE);
     HIP_TRY(hipGetLastError());
     const unsigned grid[3] = {(unsigned)(((sh->seq_len + 127) / 128) * sh->batch * sh->kv_heads),
                               1, 1};
     char name[64];
-    snprintf(name, sizeof name, "bwd_delta + bwd_dkdv + %s<%s>", a.ds ? "bwd_dq_ds" : "bwd_dq",
-             dtype_name(dtype));
+    snprintf(name, sizeof name, "bwd_delta + %s + %s<%s>", a64 ? "bwd_dkdv_a64" : "bwd_dkdv",
+             a.ds ? "bwd_dq_ds" : "bwd_dq", dtype_name(dtype));
     record(ctx, FA_KERNEL_BACKWARD_RECOMPUTE, name, 128, 64, grid, 256, 3, 1,
            vec ? nullptr : "unaligned tensors or head_dim off the 16-byte chunk: scalar loads");
     return ok();

@@ -218,6 +218,7 @@ PROTOTYPES = {
     "fa_ctx_set_prefill_precision": (INT, [VP, I32]),
     "fa_ctx_set_decode_policy": (INT, [VP, I32]),
     "fa_ctx_set_backward_policy": (INT, [VP, I32]),
+    "fa_ctx_set_backward_kernel": (INT, [VP, I32]),
     "fa_device_record": (INT, [ctypes.c_char_p, ctypes.c_char_p, I32, I32, I32, ctypes.c_uint64,
                                ctypes.c_char_p, ctypes.c_size_t,
                                ctypes.POINTER(ctypes.c_uint64)]),

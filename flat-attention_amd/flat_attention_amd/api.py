@@ -287,6 +287,11 @@ class HipContext:
         workspace fits in 2 GiB), 0 dQ recomputes S and dP."""
         check(lib().fa_ctx_set_backward_policy(self.handle, store_ds))
 
+    def set_backward_kernel(self, assembly: int):
+        """-1 (default) and 1: the assembly dK/dV kernel fa_bwd_dkdv_a64_bf16 where it applies
+        (bf16, head_dim 128, seq_len a multiple of 128, dS stored); 0: the HIP kernel only."""
+        check(lib().fa_ctx_set_backward_kernel(self.handle, assembly))
+
     def set_prefill_precision(self, mode: int):
         """0: rotated Q/K rounded to the 16-bit storage type before Q.K^T (default, fastest);
         1: split high/residual operands, f32-level scores for the 16-bit RoPE prefill."""

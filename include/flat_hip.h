@@ -596,6 +596,15 @@ int fa_ctx_set_decode_policy(fa_ctx* ctx, int32_t grouped);
  * workspace, used when it fits in 2 GiB) and dQ = dS K reads it back; 0 = dQ recomputes S and dP
  * (no workspace). Both are deterministic and use the same dS values up to MFMA summation order. */
 int fa_ctx_set_backward_policy(fa_ctx* ctx, int32_t store_ds);
+/* dK/dV kernel of the recompute backward (kernel-variant selection, the role of
+ * WgpuKernelVariant src/wgpu_backend.rs:31-37 for the backward of src/wgpu_backward_grouped.rs:
+ * 181-329): -1 (default) and 1 the assembly kernel fa_bwd_dkdv_a64_bf16 where it applies: bf16,
+ * head_dim 128, seq_len a multiple of 128, dS stored (fa_ctx_set_backward_policy), 16-byte
+ * aligned tensors; 0 the HIP kernel only. Both are within the same tolerance of the oracle (not
+ * bitwise equal: the assembly kernel adds -LSE / scale and -delta through the MFMA accumulator
+ * inputs, a different f32 summation order); the telemetry's kernel name says which ran
+ * (bwd_dkdv_a64). */
+int fa_ctx_set_backward_kernel(fa_ctx* ctx, int32_t assembly);
 int fa_kernel_variant_for_shape(fa_ctx* ctx, uint64_t head_dim, int32_t has_rope, int dtype,
                                 int32_t* kernel_id);
 
