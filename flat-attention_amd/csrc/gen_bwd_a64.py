@@ -66,7 +66,8 @@ RB = 256                   # bytes per staged row (128 bf16)
 T_DO = 128 * RB            # dO tile after the Q tile
 T_LD = 2 * 128 * RB        # biases: 128 x -LSE / scale, then 128 x -delta (f32)
 STAGE = T_LD + 1024
-LDS_BYTES = 2 * STAGE
+DUMMY = 2 * STAGE          # bias transfers of waves 1..3 (no bytes read) land here
+LDS_BYTES = 2 * STAGE + 1024
 SUB = 32 * RB              # one 32-row sub-block of a tile
 
 # --------------------------------------------------------------------------- registers
@@ -79,8 +80,8 @@ LB = 130      # 16: bias fragment -LSE / scale of the next S chain
 DB = 146      # 16: -delta
 PF = 162      # 8: P packed (A operand of dV, 2 k-steps x 4)
 DF = 170      # 8: dS packed (A operand of dK; stored)
-RA = 4        # A-operand ring (S/dP row reads)
-ARING = 178   # RA x 4
+RA = 4        # A-operand ring (S/dP row reads): slots 0..3 at ARING, more at ARING_X
+ARING = 178   # 4 x 4
 RBN = 4       # B-operand ring (dV/dK transposing reads)
 BRING = 194   # RBN x 4
 RO = 210      # 8: row-read offsets (m, h)
@@ -93,7 +94,8 @@ V_TMP = 230   # 8 temps
 V_EPW = 238   # epilogue: LDS write base
 V_EPR = 239   # epilogue: LDS read base
 V_EPG = 240   # epilogue: global offset of the lane's row chunk
-NUM_VGPR = 241
+ARING_X = 242  # A-ring slots 4.. (4 registers each, 64-bit aligned)
+NUM_VGPR = ARING_X + 4 * max(0, RA - 4)
 A_DV = 0      # dV[mb]: a[16 mb ..]
 A_DK = 64     # dK[mb]: a[64 + 16 mb ..]
 NUM_AGPR = 128
@@ -121,7 +123,6 @@ S_T0, S_T1, S_T2, S_T3 = 72, 73, 74, 75
 S_MASK = 76        # [76:77] diagonal mask temp
 S_QH0 = 78         # first query row of the group (rows)
 S_S0 = 79          # first active sub-block of the tile
-S_N = 80           # active sub-blocks of the tile
 S_SOFF = 81        # store soffset temp
 S_KROW = 82        # first K row of the (batch, kv head): bkv * seq
 S_NHH = 84         # next tile: head, first query
@@ -129,7 +130,13 @@ S_NQ = 85
 S_NRQ = 86         # next tile's Q/dO resource bytes (0 past the last tile)
 S_NRL = 87         # next tile's bias resource bytes
 S_XST = 88         # stage the next tile goes to
-NUM_SGPR = 90
+S_DQ = 89          # query step between tiles of one head: +128 or -128
+S_XB = 90          # LDS destination of the wave's transfers (stage + 1 KiB * wave)
+S_XBL = 91         # LDS destination of the bias transfer (wave 0: stage + T_LD, else DUMMY)
+S_XNQ = 92         # resource bytes of the next tile's Q / dO (0 past the last tile)
+S_XNL = 93         # and of its biases
+S_XSOFF = 94       # transfer soffset temp
+NUM_SGPR = 96
 
 
 def vr(b, n=1):
@@ -142,6 +149,12 @@ def ar(b, n=1):
 
 def sr(b, n=1):
     return f"s{b}" if n == 1 else f"s[{b}:{b + n - 1}]"
+
+
+def a_slot(j: int) -> int:
+    """First register of A-ring slot j % RA."""
+    x = j % RA
+    return ARING + 4 * x if x < 4 else ARING_X + 4 * (x - 4)
 
 
 def kidx(g, t):
@@ -293,8 +306,18 @@ def setup(gen: Gen):
     for blk in range(8):
         e(I(f"v_mfma_f32_32x32x16_bf16 {ar(16 * blk, 16)}, {vr(V_TMP, 4)}, {vr(V_TMP, 4)}, 0"))
     # ---- tile 0 into stage 0
+    # tile order: query tiles outer, the group's heads inner; the first half of the key blocks
+    # sweeps the queries downwards from the last tile, the second half upwards from its
+    # diagonal. Under a causal mask the heavy first half runs first, one workgroup per CU, and a
+    # second-half workgroup starts on the CU whose first-half workgroup ended, so at any time
+    # the running workgroups of one (batch, kv head) read the same query tile (a shared L2).
     e([I(f"s_mov_b32 {sr(S_J)}, 0"), I(f"s_mov_b32 {sr(S_HH)}, 0"),
-       I(f"s_mov_b32 {sr(S_QT)}, {sr(S_QSTART)}"),
+       I(f"s_lshl_b32 {T0}, {sr(S_KB)}, 8"),
+       I(f"s_sub_u32 {T1}, {arg('seq')}, 128"),
+       I(f"s_mov_b32 {sr(S_DQ)}, 128"),
+       I(f"s_cmp_lt_u32 {T0}, {arg('seq')}"),
+       I(f"s_cselect_b32 {sr(S_QT)}, {T1}, {sr(S_QSTART)}"),
+       I(f"s_cselect_b32 {sr(S_DQ)}, -128, {sr(S_DQ)}"),
        I(f"s_mov_b32 {sr(S_STAGE)}, 0"), I(f"s_mov_b32 {sr(S_CUR)}, 0"),
        I(f"s_mov_b32 {sr(S_CURL)}, 0")])
     # resource bytes of the transfers: a whole tile of Q / dO; the bias resource starts at the
@@ -302,14 +325,16 @@ def setup(gen: Gen):
     e([I(f"s_mov_b32 {sr(S_NRQ)}, {128 * RB}"),
        I(f"s_lshl_b32 {sr(S_NRL)}, {arg('rows')}, 2"),
        I(f"s_add_u32 {sr(S_NRL)}, {sr(S_NRL)}, 512")])
-    e(transfer(sr(S_HH), sr(S_QT), 0, sr(S_NRQ), sr(S_NRL)))
+    e(transfer_setup(sr(S_HH), sr(S_QT), 0, sr(S_NRQ), sr(S_NRL)))
+    for grp in transfer_items():
+        e(grp)
     e([I("s_waitcnt vmcnt(0)"), I("s_barrier")])
 
 
-def transfer(hh_sgpr, qt_sgpr, stage, nrec_q, nrec_l) -> list:
-    """Transfers of tile (hh, qt) into LDS stage `stage` (a constant or an SGPR): 8 Q and 8 dO
-    instructions per wave (16 rows each), the biases by wave 0. nrec_q / nrec_l: resource
-    bytes (SGPRs; 0 for a tile past the last, which then reads nothing)."""
+def transfer_setup(hh_sgpr, qt_sgpr, stage, nrec_q, nrec_l) -> list:
+    """Resources and LDS destinations of the transfers of tile (hh, qt) into LDS stage `stage`
+    (an SGPR or a constant); nrec_q / nrec_l: resource bytes (SGPRs; 0 for a tile past the
+    last, whose transfers then read nothing and write zeros to the free stage)."""
     T0, T1, T2, T3 = (sr(S_T0), sr(S_T1), sr(S_T2), sr(S_T3))
     out = [I(f"s_mul_i32 {T0}, {hh_sgpr}, {arg('seq')}"),
            I(f"s_add_u32 {T0}, {T0}, {sr(S_QH0)}"),
@@ -321,44 +346,35 @@ def transfer(hh_sgpr, qt_sgpr, stage, nrec_q, nrec_l) -> list:
             I(f"s_add_u32 {sr(S_RL)}, {arg('ld')}, {T1}"),
             I(f"s_addc_u32 {sr(S_RL + 1)}, {arg('ld', True)}, 0"),
             I(f"s_and_b32 {sr(S_RL + 1)}, {sr(S_RL + 1)}, 0xffff"),
-            I(f"s_mov_b32 {sr(S_RL + 2)}, {nrec_l}"),
-            I(f"s_mov_b32 {sr(S_RL + 3)}, 0x20000")]
-    st = stage if isinstance(stage, str) else str(stage)
-    out += [I(f"s_lshl_b32 {T3}, {sr(S_WAVE)}, 10")]
-    if isinstance(stage, str):
-        out += [I(f"s_add_u32 {T3}, {T3}, {stage}")]
-    elif stage:
-        out += [I(f"s_add_u32 {T3}, {T3}, {stage}")]
-    for which, rs, region in (("q", S_RQ, 0), ("o", S_RO, T_DO)):
+            I(f"s_mov_b32 {sr(S_RL + 3)}, 0x20000"),
+            I(f"s_lshl_b32 {sr(S_XB)}, {sr(S_WAVE)}, 10"),
+            I(f"s_add_u32 {sr(S_XB)}, {sr(S_XB)}, {stage}"),
+            I(f"s_add_u32 {sr(S_XBL)}, {stage}, {T_LD}"),
+            # the biases: one instruction of wave 0; the other waves read no bytes
+            I(f"s_mov_b32 {T0}, {DUMMY}"),
+            I(f"s_cmp_eq_u32 {sr(S_WAVE)}, 0"),
+            I(f"s_cselect_b32 {sr(S_XBL)}, {sr(S_XBL)}, {T0}"),
+            I(f"s_cselect_b32 {sr(S_RL + 2)}, {nrec_l}, 0")]
+    return out
+
+
+def transfer_items() -> list:
+    """The transfer instructions after transfer_setup, in groups that can be spread over a
+    tile's MFMAs: 8 Q and 8 dO instructions per wave (16 rows each: rows 4 w + 16 i + lane / 16,
+    the same per-lane offsets for both), then the biases."""
+    out = []
+    for rs, region in ((S_RQ, 0), (S_RO, T_DO)):
         for i in range(8):
-            out += [I(f"s_add_u32 m0, {T3}, {region + 4096 * i}", writes=["m0"],
-                      reads=[f"s{S_T3}"]),
-                    I(f"s_mov_b32 {T1}, {4096 * i}"),
-                    I(f"buffer_load_dwordx4 {vr(V_XOFF)}, {sr(rs, 4)}, {T1} offen lds")]
-    # biases: wave 0 only (one instruction, 1 KiB at stage + T_LD)
-    if isinstance(stage, str):
-        out += [I(f"s_add_u32 {T3}, {stage}, {T_LD}")]
-    else:
-        out += [I(f"s_mov_b32 {T3}, {stage + T_LD}")]
-    out += [I(f"s_cmp_eq_u32 {sr(S_WAVE)}, 0"),
-            I(f"s_cselect_b64 {sr(S_T0, 2)}, -1, 0"),
-            I(f"s_and_saveexec_b64 {sr(S_MASK, 2)}, {sr(S_T0, 2)}"),
-            I(f"s_mov_b32 m0, {T3}", writes=["m0"], reads=[f"s{S_T3}"]),
-            I(f"buffer_load_dwordx4 {vr(V_LDOFF)}, {sr(S_RL, 4)}, 0 offen lds"),
-            I(f"s_mov_b64 exec, {sr(S_MASK, 2)}")]
+            out.append([I(f"s_add_u32 m0, {sr(S_XB)}, {region + 4096 * i}", writes=["m0"],
+                          reads=[f"s{S_XB}"]),
+                        I(f"s_mov_b32 {sr(S_XSOFF)}, {4096 * i}"),
+                        I(f"buffer_load_dwordx4 {vr(V_XOFF)}, {sr(rs, 4)}, {sr(S_XSOFF)} offen lds")])
+    out.append([I(f"s_mov_b32 m0, {sr(S_XBL)}", writes=["m0"], reads=[f"s{S_XBL}"]),
+                I(f"buffer_load_dwordx4 {vr(V_LDOFF)}, {sr(S_RL, 4)}, 0 offen lds")])
     return out
 
 
 # --------------------------------------------------------------------------- the tile loop
-def next_tile() -> list:
-    """(hh, qt) of the next tile of the sweep: qt += 128, wrapping to the next head."""
-    return [I(f"s_add_u32 {sr(S_QT)}, {sr(S_QT)}, 128"),
-            I(f"s_cmp_ge_u32 {sr(S_QT)}, {arg('seq')}"),
-            I(f"s_cselect_b32 {sr(S_QT)}, {sr(S_QSTART)}, {sr(S_QT)}"),
-            I(f"s_cselect_b32 {sr(S_T0)}, 1, 0"),
-            I(f"s_add_u32 {sr(S_HH)}, {sr(S_HH)}, {sr(S_T0)}")]
-
-
 def tile_setup() -> list:
     """Per tile: first active sub-block s0 (the wave's diagonal on the first tile of a head
     under a causal mask), the read offsets moved to this tile's stage and s0, the dS store
@@ -462,7 +478,7 @@ def ds_store(i: int) -> list:
               f"offen offset:1024 nt")]
 
 
-def body(gen: Gen, n: int, diag: bool):
+def body(gen: Gen, n: int, diag: bool, xfer: list):
     """The n active sub-blocks of a tile (the first on the causal diagonal when diag): MFMA
     sequence chain(0), [chain(1), dvdk(0)], ..., [dvdk(n-1)]; chain(i) = S'/dP' of sub-block i,
     dvdk(i) = its dV/dK products; softmax(i) spread over chain(i+1)."""
@@ -512,7 +528,7 @@ def body(gen: Gen, n: int, diag: bool):
                     _, i, k = ml[idx]
                     ks = k >> 1
                     off = i * SUB + (T_DO if k & 1 else 0)
-                    slot = ARING + 4 * (j % RA)
+                    slot = a_slot(j)
                     issued[idx] = [gen.ds_issue(f"ds_read_b128 {vr(slot, 4)}, {vr(RO + ks)} "
                                                 f"offset:{off}")]
                     na += 1
@@ -541,9 +557,17 @@ def body(gen: Gen, n: int, diag: bool):
     bias_loads(0)
     issue(RA + RBN)
     streams = {}
+    stores = {}
     for i in range(n):
-        st = softmax(i, diag and i == 0) + ds_store(i)
-        streams[i] = st
+        streams[i] = softmax(i, diag and i == 0)
+        st = ds_store(i)
+        stores[i] = [st[:2], st[2:]]
+    # the next tile's transfers: one group every `stride` MFMAs from the second on, over the
+    # first half of the tile (a burst of them stalls the issue behind the memory pipeline)
+    xfer = list(xfer)
+    stride = max(1, min(4, (len(ml) // 2) // max(1, len(xfer))))
+    xfer_at = {1 + stride * k: grp for k, grp in enumerate(xfer)}
+    vm_order = []     # "x" (transfer) / "s" (dS store), in issue order
     pending_stream = []     # (remaining items, cost, first idx allowed)
     for idx, (kind, i, k) in enumerate(ml):
         # softmax(i) must be out before dvdk(i) starts
@@ -558,7 +582,7 @@ def body(gen: Gen, n: int, diag: bool):
             acc = (DACC if k & 1 else SACC)[i & 1]
             frag = (VF if k & 1 else KF) + 4 * ks
             src = vr((DB if k & 1 else LB), 16) if ks == 0 else vr(acc, 16)
-            slot = ARING + 4 * (reads_a.index(idx) % RA)
+            slot = a_slot(reads_a.index(idx))
             ins = I(f"v_mfma_f32_32x32x16_bf16 {vr(acc, 16)}, {vr(slot, 4)}, {vr(frag, 4)}, "
                     f"{src}")
             ins.srcc_chain = ks != 0
@@ -572,6 +596,13 @@ def body(gen: Gen, n: int, diag: bool):
             ins.srcc_chain = True
         e(ins)
         emitted = idx
+        if idx in xfer_at:
+            e(xfer_at.pop(idx))
+            vm_order.append("x")
+        # the dS stores of sub-block i after its third and ninth dV/dK MFMAs
+        if kind == "d" and k in (2, 8):
+            e(stores[i].pop(0))
+            vm_order.append("s")
         issue(2)
         # next sub-block's biases once this chain's first MFMAs have read the bias registers
         if kind == "c" and k == 6 and i + 1 < n:
@@ -591,9 +622,14 @@ def body(gen: Gen, n: int, diag: bool):
     for i in sorted(streams):
         for x in streams[i]:
             e(x)
+    for k in sorted(xfer_at):
+        e(xfer_at[k])
+        vm_order.append("x")
+    assert not any(stores.values())
     gen.ds_wait_all()
-    # this tile's dS stores may stay in flight; the next tile's transfers (older) must land
-    e(I(f"s_waitcnt vmcnt({2 * n})"))
+    # the dS stores issued after the last transfer may stay in flight; the transfers must land
+    last_x = max(i for i, v in enumerate(vm_order) if v == "x") if "x" in vm_order else -1
+    e(I(f"s_waitcnt vmcnt({len(vm_order) - 1 - last_x})"))
 
 
 # --------------------------------------------------------------------------- epilogue
@@ -662,26 +698,26 @@ def build() -> Gen:
     e = gen.emit
     T0 = sr(S_T0)
     e([I(".Ltile:"),
-       # next tile: qt + 128, wrapping to the next head of the group
-       I(f"s_add_u32 {sr(S_NQ)}, {sr(S_QT)}, 128"),
-       I(f"s_mov_b32 {sr(S_NHH)}, {sr(S_HH)}"),
-       I(f"s_cmp_ge_u32 {sr(S_NQ)}, {arg('seq')}"),
-       I(f"s_cselect_b32 {sr(S_NQ)}, {sr(S_QSTART)}, {sr(S_NQ)}"),
-       I(f"s_cselect_b32 {T0}, 1, 0"),
-       I(f"s_add_u32 {sr(S_NHH)}, {sr(S_NHH)}, {T0}"),
+       # next tile: the next head of the group, wrapping to the next query tile
+       I(f"s_add_u32 {sr(S_NHH)}, {sr(S_HH)}, 1"),
+       I(f"s_mov_b32 {sr(S_NQ)}, {sr(S_QT)}"),
+       I(f"s_cmp_ge_u32 {sr(S_NHH)}, {arg('group')}"),
+       I(f"s_cselect_b32 {sr(S_NHH)}, 0, {sr(S_NHH)}"),
+       I(f"s_cselect_b32 {T0}, {sr(S_DQ)}, 0"),
+       I(f"s_add_u32 {sr(S_NQ)}, {sr(S_NQ)}, {T0}"),
        I(f"s_sub_u32 {sr(S_XST)}, {STAGE}, {sr(S_STAGE)}"),
+       # past the last tile the transfers read nothing
        I(f"s_add_u32 {T0}, {sr(S_J)}, 1"),
-       I(f"s_cmp_ge_u32 {T0}, {sr(S_NT)}"),
-       I("s_cbranch_scc1 .Lnox")])
-    b_x = gen.new_block("xfer", [b_tile])
-    e(transfer(sr(S_NHH), sr(S_NQ), sr(S_XST), sr(S_NRQ), sr(S_NRL)))
-    b_nox = gen.new_block("nox", [b_tile, b_x])
-    e(I(".Lnox:"))
+       I(f"s_cmp_lt_u32 {T0}, {sr(S_NT)}"),
+       I(f"s_cselect_b32 {sr(S_XNQ)}, {sr(S_NRQ)}, 0"),
+       I(f"s_cselect_b32 {sr(S_XNL)}, {sr(S_NRL)}, 0")])
+    e(transfer_setup(sr(S_NHH), sr(S_NQ), sr(S_XST), sr(S_XNQ), sr(S_XNL)))
+    b_nox = b_tile
     e(tile_setup())
     e(I("s_cbranch_scc1 .Ldiag"))
     ends = []
     gen.new_block("full", [b_nox])
-    body(gen, 4, False)
+    body(gen, 4, False, transfer_items())
     e(I("s_branch .Ltend"))
     ends.append(gen.cur)
     b_disp = gen.new_block("diag", [b_nox])
@@ -693,7 +729,7 @@ def build() -> Gen:
         gen.new_block(f"d{n}", [b_disp])
         if n != 1:
             e(I(f".Ld{n}:"))
-        body(gen, n, True)
+        body(gen, n, True, transfer_items())
         e(I("s_branch .Ltend"))
         ends.append(gen.cur)
     b_end = gen.new_block("tend", ends)
