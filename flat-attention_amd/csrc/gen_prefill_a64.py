@@ -662,9 +662,11 @@ def _exact_softmax(gen: "Gen", x: int, s_x) -> None:
 
 # ---- one pipeline phase ------------------------------------------------------------------------
 def phase(gen: Gen, *, pv_x, pv_hh, s_x, s_hh, sm_x, sm_masked, pre=(),
-          prefetch_v_hh=None, after_last_v=(), after_last_k=(), vring_state=None):
+          prefetch_v_hh=None, after_last_v=(), after_last_k=(), vring_state=None, spread=()):
     """Emits one phase: MFMAs of P.V (P in PB[pv_x], V half pv_hh of the current V stage) then
     S (into SB[s_x], K half s_hh), with the softmax of SB[sm_x] spread between them.
+    spread: instruction groups (the tile transfers) issued one every few MFMAs from the third
+    on, so that the memory pipeline takes them one at a time instead of in a burst.
     vring_state: dict carrying the V operands already read into the ring by the previous phase:
     {'ready': {op_index: (slot, [ds ids])}}, and after the phase the prefetched operands of the
     next phase. Returns the new ring state."""
@@ -742,6 +744,10 @@ def phase(gen: Gen, *, pv_x, pv_hh, s_x, s_hh, sm_x, sm_masked, pre=(),
             break
         return n
 
+    spread = list(spread)
+    sp_stride = max(1, min(3, (nm - 4) // max(1, len(spread))))
+    n_pre = len(pre)
+    next_sp = 2
     # initial reads: fill the rings
     issue_reads(DV + DK)
     total_valu = len(valu_stream)
@@ -766,6 +772,10 @@ def phase(gen: Gen, *, pv_x, pv_hh, s_x, s_hh, sm_x, sm_masked, pre=(),
             ins.srcc_chain = idx != 0
         gen.emit(ins)
         issued_m = mi
+        # (a group needs the scalar set-up of `pre`, which the VALU stream emits first)
+        if spread and mi >= next_sp and vi >= n_pre:
+            gen.emit(spread.pop(0))
+            next_sp = mi + sp_stride
         issue_reads(2)
         # spread the VALU work evenly (by issue cost) over the remaining MFMAs
         remaining_m = nm - mi
@@ -779,6 +789,8 @@ def phase(gen: Gen, *, pv_x, pv_hh, s_x, s_hh, sm_x, sm_masked, pre=(),
     while vi < total_valu:
         gen.emit(valu_stream[vi])
         vi += 1
+    for g in spread:
+        gen.emit(g)
     issue_reads(99)
     # prefetch the next phase's first V operands
     new_ready = {}
@@ -1508,7 +1520,17 @@ def iteration(gen: Gen, masked: bool, tag: str, jofs: int, ring_in, xfer_tile_of
     """One loop iteration j = S_J + jofs (phases 2j+1, 2j+2), optionally issuing the transfer of
     tile S_J + xfer_tile_ofs at its start. Returns the V ring state after it."""
     xfer = []
-    if xfer_tile_ofs is not None:
+    groups = []
+    if xfer_tile_ofs is not None and not PAGED:
+        # resources and stage first; the 8 transfer instructions spread over the phase's MFMAs
+        xfer = [I(f"s_add_u32 {sr(S_TT)}, {sr(S_J)}, {xfer_tile_ofs}")] + \
+            transfer_setup(sr(S_TT)) + \
+            [I(f"s_add_u32 {sr(S_TSLOT)}, {sr(S_TSLOT)}, 1"),
+             I(f"s_cmp_eq_u32 {sr(S_TSLOT)}, {NSTAGE}"),
+             I(f"s_cselect_b32 {sr(S_TSLOT)}, 0, {sr(S_TSLOT)}")]
+        tb = transfer_block("k") + transfer_block("v")
+        groups = [tb[2 * i:2 * i + 2] for i in range(len(tb) // 2)]
+    elif xfer_tile_ofs is not None:
         if PAGED:
             # tile j+3 from page-id lanes 0..3, tile j+4 from lanes 4..7; after the second,
             # the page ids of tiles j+5 and j+6 (waited for by the pair's closing vmcnt(0))
@@ -1525,7 +1547,7 @@ def iteration(gen: Gen, masked: bool, tag: str, jofs: int, ring_in, xfer_tile_of
     key_a = [I(f"s_lshl_b32 {sr(S_KEY0)}, {sr(S_J)}, 6"),
              I(f"s_add_u32 {sr(S_KEY0)}, {sr(S_KEY0)}, {64 * jofs + 32}")]
     ring = phase(gen, pv_x=0, pv_hh=0, s_x=0, s_hh=0, sm_x=1, sm_masked=masked,
-                 pre=key_a + xfer, vring_state=ring_in, prefetch_v_hh=1)
+                 pre=key_a + xfer, vring_state=ring_in, prefetch_v_hh=1, spread=groups)
     finish_phase(gen, f"{tag}_a", 1, 1, 0)
     key_b = [I(f"s_lshl_b32 {sr(S_KEY0)}, {sr(S_J)}, 6"),
              I(f"s_add_u32 {sr(S_KEY0)}, {sr(S_KEY0)}, {64 * jofs + 64}")]
