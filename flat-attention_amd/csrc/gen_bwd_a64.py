@@ -12,8 +12,9 @@ query head of the KV head's group, P = exp2(S * scale * log2 e - LSE * log2 e)
 dS = P (dP - delta), dV += P^T dO, dK += dS^T Q (dK takes the softmax scale at the end).
 
 Layout. One workgroup = 4 waves = 128 keys of one (batch, kv head), 32 per wave. Each lane owns
-key c = lane & 31 of its wave; K and V of that key (as stored) are the B operands of S = Q K^T and dP = dO V^T and stay in registers. Tiles of 128
-query rows of Q, dO and the per-row biases (-LSE / scale, -delta) are moved by buffer->LDS
+key c = lane & 31 of its wave; K and V of that key (as stored) are the B operands of S = Q K^T
+and dP = dO V^T and stay in registers. Tiles of 128 query rows of Q, dO and the per-row biases
+(-LSE / scale, -delta) are moved by buffer->LDS
 transfers into two LDS stages (rows of 256 bytes, 16-byte chunks XOR-swizzled, conflict-free
 for both the row reads of the S/dP A operands and the transposing reads of the dV/dK B operands).
 Per 32-query sub-block (32 MFMAs per wave):
@@ -23,7 +24,17 @@ Per 32-query sub-block (32 MFMAs per wave):
                                    packed to bf16 for the MFMAs)
   dV += P^T dO, dK += dS^T Q      (8 + 8 MFMAs, accumulators in 128 AGPRs)
 and dS goes to the workspace the dQ pass reads (the layout of BackwardArgs::ds). The MFMAs of
-S and dP of sub-block i+1 run under the softmax of sub-block i; then its dV/dK MFMAs.
+S and dP of sub-block i+1 run under the softmax of sub-block i; then its dV/dK MFMAs. The next
+tile's transfers are spread over the first half of the tile's MFMAs.
+
+Tile order: query tiles outer, the group's heads inner; the first half of the key blocks sweeps
+the query tiles last-first, the second half first-last from its diagonal (the workgroups of one
+(batch, kv head) that run at the same time then read the same tile).
+
+Memory safety: every global access is a buffer instruction whose resource is bounded to the
+slice it may touch (8 KiB of K/V rows, a 32 KiB Q/dO tile or nothing past the last tile, the
+bias rows, the dS workspace from the group on, 8 KiB of dK/dV rows); every wave runs the same
+number of tiles, so every barrier is met by all four.
 """
 from __future__ import annotations
 
