@@ -1,7 +1,8 @@
 """HIP graphs over the library's launches (fa_graph_*; no counterpart in the reference, whose
 callers record passes into a command encoder and submit it).
 
-A prepared paged decode and a prepared contiguous forward (K pre-rotation pass + prefill) are
+A prepared paged decode, a prepared contiguous forward (K pre-rotation pass + prefill) and a
+prepared recompute backward (delta, the assembly dK/dV kernel, dQ from the stored dS) are
 captured once and replayed several times with new buffer contents between replays and eager
 work and synchronisations in between; every replay must give the same bits as an eager launch
 on the same inputs. Calls that would allocate, upload, fill or wait are refused while
@@ -79,6 +80,39 @@ def test_captured_prepared_forward_replays_match_eager(hip):
         ex.forward_resident(bq, bk, bv, shape, cfg, rot, out_e)
         hip.synchronize()
         assert np.array_equal(_bits(out_g, n), _bits(out_e, n)), rep
+
+
+def test_captured_backward_replays_match_eager(hip):
+    """The default bf16 backward (bwd_delta + fa_bwd_dkdv_a64_bf16 + bwd_dq_ds): its workspaces
+    are grown by an eager call first, so the captured call records only the three launches."""
+    import oracle
+    B, hq, hkv, S, D = 1, 8, 2, 256, 128
+    shape = fa.GroupedAttentionShape(B, hq, hkv, S, D)
+    cfg = fa.FlatAttentionConfig(True)
+    dt = fa.DTYPE_BF16
+    q, k, v, do = (bf16_round(normal(n, 40 + i)) for i, n in enumerate(
+        (B * hq * S * D, B * hkv * S * D, B * hkv * S * D, B * hq * S * D)))
+    o, lse = oracle.forward_grouped(q, k, v, B, hq, hkv, S, D, True)
+    pipe = fa.HipGroupedBackwardRecomputePipeline(hip, dt)
+    lay = pipe.layout(shape)
+    fwd = fa.DeviceBuffer.from_array(hip, fa.pack_grouped_backward_recompute_inputs(
+        q, k, v, do, fa.FlatAttentionOutput(bf16_round(o), lse), shape, dt, lay))
+    g_graph, g_eager = pipe.create_gradient_buffer(shape), pipe.create_gradient_buffer(shape)
+    prep = pipe.prepare(fwd, g_graph, shape, cfg)
+    pipe.encode(fwd, g_eager, shape, cfg)  # grows the delta and dS workspaces
+    with hip.capture() as cap:
+        pipe.encode_prepared(prep)
+    assert "bwd_dkdv_a64" in hip.last_telemetry().kernel_name
+    n = lay.gradient_bytes
+    for rep in range(3):
+        new_do = fa.host_storage(bf16_round(normal(B * hq * S * D, 50 + rep)), dt)
+        fwd.upload(new_do, lay.d_out_offset)
+        cap.graph.launch()
+        pipe.encode(fwd, g_eager, shape, cfg)
+        hip.synchronize()
+        assert np.array_equal(_bits(g_graph, n), _bits(g_eager, n)), rep
+        res = pipe.download_gradients(g_graph, shape)
+        assert all(np.isfinite(x).all() for x in (res.dq, res.dk, res.dv))
 
 
 def test_capture_refuses_allocation_upload_fill_and_wait(hip):
