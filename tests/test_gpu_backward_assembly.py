@@ -110,3 +110,42 @@ def test_recompute_policy_takes_the_hip_kernel(hip, request):
     hip.set_backward_policy(0)
     _, _, name = _run(hip, (1, 4, 2, 256, 128), True, 351)
     assert "bwd_dkdv_a64" not in name and "bwd_dq<" in name, name
+
+
+def test_bench_shape_units_and_closed_forms(hip):
+    """The bench shape (B2 Hq32 Hkv8 N4096 D128 bf16, causal) through the library's own forward
+    and the default backward: the oracle on the first and the last (batch, kv head) unit (its 4
+    query heads, given the same O and LSE), and over every unit the closed forms the softmax
+    fixes: each row of P sums to 1, so sum_k dV[k] = sum over the unit's query rows of dO, and
+    each row of dS sums to 0, so sum_k dK[k] = 0."""
+    B, Hq, Hkv, S, D = 2, 32, 8, 4096, 128
+    G = Hq // Hkv
+    shape = fa.GroupedAttentionShape(B, Hq, Hkv, S, D)
+    cfg = fa.FlatAttentionConfig(True)
+    dt = fa.DTYPE_BF16
+    q, k, v, do = (bf16_round(normal(n, 361 + i)) for i, n in enumerate(
+        (B * Hq * S * D, B * Hkv * S * D, B * Hkv * S * D, B * Hq * S * D)))
+    fwd = fa.HipRotaryGroupedAttention(hip, dt).forward(q, k, v, shape, cfg, None)
+    o = fa.storage_to_f32(fwd.output, dt)
+    got = fa.HipGroupedBackwardRecomputePipeline(hip, dt).backward(
+        q, k, v, do, fa.FlatAttentionOutput(o, fwd.lse), shape, cfg)
+    assert "bwd_dkdv_a64" in hip.last_telemetry().kernel_name
+    dq, dk, dv = (x.reshape(B, -1, S, D) for x in (got.dq, got.dk, got.dv))
+    for x in (dq, dk, dv):
+        assert np.isfinite(x).all()
+    q4, do4, o4 = (x.reshape(B, Hq, S, D) for x in (q, do, o))
+    k4, v4 = (x.reshape(B, Hkv, S, D) for x in (k, v))
+    lse = np.asarray(fwd.lse, np.float32).reshape(B, Hq, S)
+    for b, h in ((0, 0), (B - 1, Hkv - 1)):
+        hs = slice(h * G, (h + 1) * G)
+        want = oracle.backward_grouped(q4[b, hs], k4[b, h], v4[b, h], do4[b, hs], o4[b, hs],
+                                       lse[b, hs], 1, G, 1, S, D, True, threads=8)
+        for name, a, e in zip(("dQ", "dK", "dV"), (dq[b, hs], dk[b, h], dv[b, h]), want):
+            assert_close(f"unit {b},{h} {name}", a.ravel(), e, 2e-2 * float(np.abs(e).max()),
+                         2e-2)
+    # closed forms over every unit (float64 sums of the bf16 gradients)
+    sum_dv = dv.astype(np.float64).sum(axis=2)                       # [B, Hkv, D]
+    want_dv = do4.astype(np.float64).reshape(B, Hkv, G, S, D).sum(axis=(2, 3))
+    assert np.abs(sum_dv - want_dv).max() <= 2e-2 * np.abs(want_dv).max()
+    sum_dk = dk.astype(np.float64).sum(axis=2)
+    assert np.abs(sum_dk).max() <= 2e-2 * np.abs(dk).sum(axis=2).max()
