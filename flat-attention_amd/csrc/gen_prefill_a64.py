@@ -72,6 +72,8 @@ ARGS = [
     # paged kernel only: the block tables (bytes 184..191, unused by the contiguous kernel) and
     # their row stride in entries (the slot of k_sb: a page pool has no batch stride)
     ("bt", 184, 8), ("bt_stride", 56, 4),
+    # precise kernel only: bytes from the rotated K to its residual (the same layout after it)
+    ("klo_off", 184, 8),
 ]
 ARG_BYTES = 208
 S_QNREC, S_ONREC, S_LNREC = 52, 53, 56  # (argument registers of q_nrec, o_nrec, lse_nrec)
@@ -97,11 +99,24 @@ def arg64(name: str) -> str:
 
 KERNEL_CONTIG = "fa_prefill_a64_bf16"
 KERNEL_PAGED = "fa_prefill_a64_paged_bf16"
+KERNEL_PREC = "fa_prefill_a64_precise_bf16"
 KERNEL = KERNEL_CONTIG
 # Paged K/V (page size 16): transfer instruction i of a tile covers its rows 16 i .. 16 i + 15,
 # i.e. exactly one page, read through a buffer resource based at that page. The page ids of
 # the next transfers sit in one VGPR (lane = page of the tile range), loaded a pair ahead.
 PAGED = False
+# Precise scores: K read as its bf16 high part and the residual (a second LDS tile), Q carried
+# the same way (residual in AGPRs), three MFMAs per score k-step (hi.hi + lo.hi + hi.lo)
+PREC = False
+
+
+def STAGE_BYTES() -> int:
+    """One LDS stage: K (16 KiB), (precise: K residual, 16 KiB), V (16 KiB)."""
+    return 49152 if PREC else 32768
+
+
+def V_REGION() -> int:
+    return 32768 if PREC else 16384
 NSTAGE = 5            # LDS stages of (K 16 KiB, V 16 KiB): tiles j .. j + NSTAGE - 1 resident
 PAIR = True           # one barrier per two iterations (needs NSTAGE = 5)
 ISSUE_WEIGHT = {"trans": 2}  # relative issue cost of an instruction kind in the phase scheduler
@@ -145,10 +160,12 @@ V_BIG = 220           # 2^64: a half-tile row sum above it sends the phase to th
 V_EPI = 222           # 4 per-lane epilogue addresses (O staging write/read, row-offset permute, chunk)
 V_PT = 226            # paged: page ids, lane l = entry l of the loaded block-table range
 V_PTOFF = 227         # paged: 4 * lane (byte offset of the lane's block-table entry)
-NUM_VGPR = 228
+KLRING = 228          # precise kernel: K residual operand ring (RK slots x 4)
+NUM_VGPR = 244
 # AGPRs
 A_O = 0               # O[rb][mb]: a[(rb*4+mb)*16 ..]
 A_Q = 128             # Q[rb][ks]: a[128 + (rb*8+ks)*4 ..]
+A_QLO = 192           # precise kernel: the residual of Q, same layout
 NUM_AGPR = 192
 
 # SGPRs (beyond s[0:1] kernarg pointer, s2 workgroup id, s[8:59] arguments)
@@ -468,6 +485,22 @@ def k_read_text(slot: int, ks: int, hh: int) -> str:
     return f"ds_read_b128 {vr(KRING + 4 * slot, 4)}, {vr(VKA + ks)} offset:{hh * 8192}"
 
 
+def klo_read_text(slot: int, ks: int, hh: int) -> str:
+    """Precise kernel: the K residual operand (second tile of the stage)."""
+    return f"ds_read_b128 {vr(KLRING + 4 * slot, 4)}, {vr(VKA + ks)} offset:{16384 + hh * 8192}"
+
+
+def q_lo_op(rb: int, ks: int) -> str:
+    return ar(A_QLO + (rb * 8 + ks) * 4, 4)
+
+
+def s_parts() -> list:
+    """(K ring, Q operand function) of the score MFMAs of one k-step: one, or three (precise)."""
+    if not PREC:
+        return [(KRING, q_op)]
+    return [(KRING, q_op), (KLRING, q_op), (KRING, q_lo_op)]
+
+
 def v_read_texts(slot: int, mb: int, s: int, hh: int) -> list[str]:
     off = hh * 8192 + s * 4096
     base = VRING + 4 * slot
@@ -596,22 +629,26 @@ def _recompute_scores(gen: "Gen", x: int, hh: int) -> None:
     # K addresses of the previous stage
     d = sr(S_T0)
     e([I(f"s_cmp_eq_u32 {sr(S_KSLOT)}, 0"),
-       I(f"s_mov_b32 {d}, 0xffff8000"),
-       I(f"s_cselect_b32 {d}, 0x{(NSTAGE - 1) * 32768:x}, {d}")])
+       I(f"s_mov_b32 {d}, 0x{(-STAGE_BYTES()) & 0xffffffff:x}"),
+       I(f"s_cselect_b32 {d}, 0x{(NSTAGE - 1) * STAGE_BYTES():x}, {d}")])
     e([I(f"v_add_u32 {vr(V_TMP + i)}, {d}, {vr(VKA + i)}") for i in range(8)])
     for half in range(2):
         for k4 in range(4):
             ks = 4 * half + k4
             e(I(f"ds_read_b128 {vr(KRING + 4 * k4, 4)}, {vr(V_TMP + ks)} offset:{hh * 8192}"))
+            if PREC:
+                e(I(f"ds_read_b128 {vr(KLRING + 4 * k4, 4)}, {vr(V_TMP + ks)} "
+                    f"offset:{16384 + hh * 8192}"))
         e(I("s_waitcnt lgkmcnt(0)"))
         for k4 in range(4):
             ks = 4 * half + k4
-            for rb in range(2):
-                src_c = "0" if ks == 0 else s_acc(x, rb)
-                ins = I(f"v_mfma_f32_32x32x16_bf16 {s_acc(x, rb)}, {vr(KRING + 4 * k4, 4)}, "
-                        f"{q_op(rb, ks)}, {src_c}")
-                ins.srcc_chain = ks != 0
-                e(ins)
+            for part, (ring, qf) in enumerate(s_parts()):
+                for rb in range(2):
+                    src_c = "0" if ks == 0 and part == 0 else s_acc(x, rb)
+                    ins = I(f"v_mfma_f32_32x32x16_bf16 {s_acc(x, rb)}, {vr(ring + 4 * k4, 4)}, "
+                            f"{qf(rb, ks)}, {src_c}")
+                    ins.srcc_chain = not (ks == 0 and part == 0)
+                    e(ins)
 
 
 def _exact_softmax(gen: "Gen", x: int, s_x) -> None:
@@ -686,9 +723,9 @@ def phase(gen: Gen, *, pv_x, pv_hh, s_x, s_hh, sm_x, sm_masked, pre=(),
         for rb in range(2):
             mlist.append(("pv", oi, rb))
     for ks in k_ops:
-        order_rb = (0, 1)
-        for rb in order_rb:
-            mlist.append(("s", ks, rb))
+        for part in range(len(s_parts())):
+            for rb in (0, 1):
+                mlist.append(("s", ks, rb, part))
     nm = len(mlist)
     vi = 0  # next VALU item
 
@@ -708,8 +745,13 @@ def phase(gen: Gen, *, pv_x, pv_hh, s_x, s_hh, sm_x, sm_masked, pre=(),
     def last_use_v(oi):  # mlist index of the last MFMA reading operand oi
         return 2 * oi + 1
 
+    last_k = {}
+    for i_, m_ in enumerate(mlist):
+        if m_[0] == "s":
+            last_k[m_[1]] = i_
+
     def last_use_k(ks):
-        return len(pv_ops) * 2 + 2 * ks + 1
+        return last_k[ks]
 
     def can_issue_v(oi):
         prev = oi - DV
@@ -735,6 +777,9 @@ def phase(gen: Gen, *, pv_x, pv_hh, s_x, s_hh, sm_x, sm_masked, pre=(),
                 continue
             if next_k < len(k_ops) and can_issue_k(next_k):
                 k_issued[next_k] = [gen.ds_issue(k_read_text(next_k % DK, next_k, s_hh))]
+                if PREC:
+                    k_issued[next_k].append(
+                        gen.ds_issue(klo_read_text(next_k % DK, next_k, s_hh)))
                 if next_k == len(k_ops) - 1:
                     for x in after_last_k:
                         gen.emit(x)
@@ -754,7 +799,8 @@ def phase(gen: Gen, *, pv_x, pv_hh, s_x, s_hh, sm_x, sm_masked, pre=(),
     # issue cost of the stream: a transcendental takes about twice an ordinary VALU slot
     cost = [ISSUE_WEIGHT.get(x.kind, 1) for x in valu_stream]
     left = sum(cost)
-    for mi, (kind, idx, rb) in enumerate(mlist):
+    for mi, m_ in enumerate(mlist):
+        kind, idx, rb = m_[:3]
         if kind == "pv":
             gen.ds_wait_for(v_issued[idx])
             s, mb = pv_ops[idx]
@@ -763,13 +809,16 @@ def phase(gen: Gen, *, pv_x, pv_hh, s_x, s_hh, sm_x, sm_masked, pre=(),
                     f"{p_op(pv_x, rb, s)}, {o_acc(rb, mb)}")
             ins.srcc_chain = True
         else:
+            part = m_[3]
+            ring, qf = s_parts()[part]
             gen.ds_wait_for(k_issued[idx])
             slot = idx % DK
             # k-step 0 accumulates onto the bias block (-m of the lane's row)
-            src_c = vr(NB + 16 * rb, 16) if idx == 0 else s_acc(s_x, rb)
-            ins = I(f"v_mfma_f32_32x32x16_bf16 {s_acc(s_x, rb)}, {vr(KRING + 4 * slot, 4)}, "
-                    f"{q_op(rb, idx)}, {src_c}")
-            ins.srcc_chain = idx != 0
+            first = idx == 0 and part == 0
+            src_c = vr(NB + 16 * rb, 16) if first else s_acc(s_x, rb)
+            ins = I(f"v_mfma_f32_32x32x16_bf16 {s_acc(s_x, rb)}, {vr(ring + 4 * slot, 4)}, "
+                    f"{qf(rb, idx)}, {src_c}")
+            ins.srcc_chain = not first
         gen.emit(ins)
         issued_m = mi
         # (a group needs the scalar set-up of `pre`, which the VALU stream emits first)
@@ -807,13 +856,25 @@ def transfer_block(which: str) -> list[Ins]:
     """The 4 K or V transfer instructions of this wave for the tile whose resource is set up;
     M0 = stage base (S_T2) + region + (wave + 4 i) KiB."""
     out = []
-    rs = S_RK if which == "k" else S_RV
-    region = 0 if which == "k" else 16384
+    rs = S_RV if which == "v" else S_RK
+    region = {"k": 0, "klo": 16384, "v": V_REGION()}[which]
+    if which == "klo":
+        # the K resource moved to the residual copy (the same rows klo_off bytes further)
+        out += [I(f"s_add_u32 {sr(S_RK)}, {sr(S_RK)}, {arg('klo_off')}"),
+                I(f"s_addc_u32 {sr(S_RK + 1)}, {sr(S_RK + 1)}, {arg('klo_off', True)}"),
+                I(f"s_and_b32 {sr(S_RK + 1)}, {sr(S_RK + 1)}, 0xffff")]
     for i in range(4):
         out.append(I(f"s_add_u32 m0, {sr(S_T2)}, {region + 1024 * 4 * i}", writes=["m0"],
                      reads=[f"s{S_T2}"]))
         out.append(I(f"buffer_load_dwordx4 {vr(VTOFF + i)}, {sr(rs, 4)}, 0 offen lds"))
     return out
+
+
+def kv_transfers() -> list[Ins]:
+    """The wave's K (and, precise, K residual) and V transfer instructions of the tile whose
+    resources transfer_setup built."""
+    return (transfer_block("k") + (transfer_block("klo") if PREC else []) +
+            transfer_block("v"))
 
 
 def transfer_setup(tile_sgpr: str) -> list[Ins]:
@@ -840,8 +901,9 @@ def transfer_setup(tile_sgpr: str) -> list[Ins]:
         I(f"s_and_b32 {sr(S_RV + 1)}, {sr(S_RV + 1)}, 0xffff"),
         I(f"s_mov_b32 {sr(S_RV + 2)}, {t1}"),
         I(f"s_mov_b32 {sr(S_RV + 3)}, 0x20000"),
-        # stage base: tslot * 32 KiB + wave KiB
-        I(f"s_lshl_b32 {sr(S_T2)}, {sr(S_TSLOT)}, 15"),
+        # stage base: tslot * stage bytes + wave KiB
+        (I(f"s_mul_i32 {sr(S_T2)}, {sr(S_TSLOT)}, {STAGE_BYTES()}") if PREC else
+         I(f"s_lshl_b32 {sr(S_T2)}, {sr(S_TSLOT)}, 15")),
         I(f"s_lshl_b32 {sr(S_T3)}, {sr(S_WAVE)}, 10"),
         I(f"s_add_u32 {sr(S_T2)}, {sr(S_T2)}, {sr(S_T3)}"),
     ]
@@ -918,8 +980,8 @@ def advance_slot(slot_sgpr: int, addr_base: int, n_addr: int) -> list[Ins]:
     out = [I(f"s_add_u32 {s}, {s}, 1"),
            I(f"s_cmp_eq_u32 {s}, {NSTAGE}"),
            I(f"s_cselect_b32 {s}, 0, {s}"),
-           I(f"s_mov_b32 {d}, 0x8000"),
-           I(f"s_cselect_b32 {d}, 0x{(-(NSTAGE - 1) * 32768) & 0xffffffff:x}, {d}")]
+           I(f"s_mov_b32 {d}, 0x{STAGE_BYTES():x}"),
+           I(f"s_cselect_b32 {d}, 0x{(-(NSTAGE - 1) * STAGE_BYTES()) & 0xffffffff:x}, {d}")]
     out += [I(f"v_add_u32 {vr(addr_base + i)}, {d}, {vr(addr_base + i)}") for i in range(n_addr)]
     return out
 
@@ -1181,7 +1243,7 @@ def setup_block(gen: Gen):
                I(f"v_lshlrev_b32 {vr(V_TMP + 1)}, 4, {vr(V_TMP + 1)}"),
                I(f"v_lshl_add_u32 {vr(V_TMP)}, {vr(V_TMP)}, 8, {vr(V_TMP + 1)}"),
                I(f"v_add_u32 {vr(V_TMP)}, {vr(V_TMP)}, {vr(V_ROW + 2)}"),
-               I(f"v_add_u32 {vr(VVA + mb * 2 + hi)}, 0x4000, {vr(V_TMP)}")])
+               I(f"v_add_u32 {vr(VVA + mb * 2 + hi)}, 0x{V_REGION():x}, {vr(V_TMP)}")])
     # ---- transfers of tiles 0 .. 2 into stages 0 .. 2 (paged: after the Q loads, once the
     # page ids of tiles 0 .. 2 have landed)
     e(I(f"s_mov_b32 {sr(S_TSLOT)}, 0"))
@@ -1234,14 +1296,25 @@ def setup_block(gen: Gen):
             return 3 * 8 + 1
         for _ in range(3 if PAIR else 2):
             e(transfer_setup(sr(S_TT)))
-            e(transfer_block("k"))
-            e(transfer_block("v"))
+            e(kv_transfers())
             e([I(f"s_add_u32 {sr(S_TT)}, {sr(S_TT)}, 1"),
                I(f"s_add_u32 {sr(S_TSLOT)}, {sr(S_TSLOT)}, 1")])
-        return (3 if PAIR else 2) * 8
+        return (3 if PAIR else 2) * (12 if PREC else 8)
     c2 = arg("c2")
 
-    def rotate_chunk(w0, cs0):
+    def residual(w, t1, od, lo_a):
+        """Precise kernel: a[lo_a] = bf16 residuals of the f32 pair (t1, od) rounded into w."""
+        if not PREC:
+            return []
+        ev = V_TMP + 3
+        return [I(f"v_lshlrev_b32 {vr(ev)}, 16, {vr(w)}"),
+                I(f"v_sub_f32 {vr(t1)}, {vr(t1)}, {vr(ev)}"),
+                I(f"v_and_b32 {vr(ev)}, 0xffff0000, {vr(w)}"),
+                I(f"v_sub_f32 {vr(od)}, {vr(od)}, {vr(ev)}"),
+                I(f"v_cvt_pk_bf16_f32 {vr(ev)}, {vr(t1)}, {vr(od)}"),
+                I(f"v_accvgpr_write_b32 {ar(lo_a)}, {vr(ev)}")]
+
+    def rotate_chunk(w0, cs0, lo_a0):
         out = []
         for j in range(4):
             w = w0 + j
@@ -1256,6 +1329,7 @@ def setup_block(gen: Gen):
                     I(f"v_mul_f32 {vr(t1)}, {c2}, {vr(t1)}"),
                     I(f"v_mul_f32 {vr(od)}, {c2}, {vr(od)}"),
                     I(f"v_cvt_pk_bf16_f32 {vr(w)}, {vr(t1)}, {vr(od)}")]
+            out += residual(w, t1, od, lo_a0 + j)
         return out
 
     e(I(f"s_cmp_eq_u32 {arg('rope_q')}, 0"))
@@ -1284,7 +1358,8 @@ def setup_block(gen: Gen):
         rb, k0 = bi // 2, 4 * (bi % 2)
         e(I(f"s_waitcnt vmcnt({(8 + x) if bi < 2 else (8 if bi == 2 else 0)})"))
         for k in range(4):
-            e(rotate_chunk(qt[rb] + 4 * (k0 + k), cs_area[bi % 2] + 8 * k))
+            e(rotate_chunk(qt[rb] + 4 * (k0 + k), cs_area[bi % 2] + 8 * k,
+                           A_QLO + rb * 32 + 4 * (k0 + k)))
         if bi + 2 < 4:
             e(cs_batch(bi + 2))
     e(I("s_branch .Lq_done"))
@@ -1300,6 +1375,7 @@ def setup_block(gen: Gen):
                I(f"v_mul_f32 {vr(ev)}, {c2}, {vr(ev)}"),
                I(f"v_mul_f32 {vr(od)}, {c2}, {vr(od)}"),
                I(f"v_cvt_pk_bf16_f32 {vr(r)}, {vr(ev)}, {vr(od)}")])
+            e(residual(r, ev, od, A_QLO + rb * 32 + w))
     e(I(".Lq_done:"))
     e(I("s_waitcnt vmcnt(0)"))
     for rb in range(2):
@@ -1319,8 +1395,7 @@ def setup_block(gen: Gen):
     # tiles 2 .. NSTAGE - 2 (their waits come at the ends of the first iterations)
     for _ in range(0 if PAIR else NSTAGE - 3):
         e(transfer_setup(sr(S_TT)))
-        e(transfer_block("k"))
-        e(transfer_block("v"))
+        e(kv_transfers())
         e([I(f"s_add_u32 {sr(S_TT)}, {sr(S_TT)}, 1"),
            I(f"s_add_u32 {sr(S_TSLOT)}, {sr(S_TSLOT)}, 1")])
     e(I("s_barrier"))
@@ -1478,7 +1553,7 @@ def single_loops(gen: Gen, pro_end: Block) -> list:
         ring_in = {"ready": {o: pre_ids[2 * o:2 * o + 2] for o in range(RV)}}
         # iteration j: transfer of tile j + NSTAGE - 1 into the stage of tile j - 1
         xfer = [I(f"s_add_u32 {sr(S_TT)}, {sr(S_J)}, {NSTAGE - 1}")] + \
-            transfer_setup(sr(S_TT)) + transfer_block("k") + transfer_block("v") + \
+            transfer_setup(sr(S_TT)) + kv_transfers() + \
             [I(f"s_add_u32 {sr(S_TSLOT)}, {sr(S_TSLOT)}, 1"),
              I(f"s_cmp_eq_u32 {sr(S_TSLOT)}, {NSTAGE}"),
              I(f"s_cselect_b32 {sr(S_TSLOT)}, 0, {sr(S_TSLOT)}")]
@@ -1528,6 +1603,7 @@ def iteration(gen: Gen, masked: bool, tag: str, jofs: int, ring_in, xfer_tile_of
             [I(f"s_add_u32 {sr(S_TSLOT)}, {sr(S_TSLOT)}, 1"),
              I(f"s_cmp_eq_u32 {sr(S_TSLOT)}, {NSTAGE}"),
              I(f"s_cselect_b32 {sr(S_TSLOT)}, 0, {sr(S_TSLOT)}")]
+        assert not PREC
         tb = transfer_block("k") + transfer_block("v")
         groups = [tb[2 * i:2 * i + 2] for i in range(len(tb) // 2)]
     elif xfer_tile_ofs is not None:
@@ -1539,7 +1615,7 @@ def iteration(gen: Gen, masked: bool, tag: str, jofs: int, ring_in, xfer_tile_of
             if xfer_tile_ofs == 4:
                 body += [I(f"s_add_u32 {sr(S_TT)}, {sr(S_J)}, 5")] + pt_load(sr(S_TT))
         else:
-            body = transfer_setup(sr(S_TT)) + transfer_block("k") + transfer_block("v")
+            body = transfer_setup(sr(S_TT)) + kv_transfers()
         xfer = [I(f"s_add_u32 {sr(S_TT)}, {sr(S_J)}, {xfer_tile_ofs}")] + body + \
             [I(f"s_add_u32 {sr(S_TSLOT)}, {sr(S_TSLOT)}, 1"),
              I(f"s_cmp_eq_u32 {sr(S_TSLOT)}, {NSTAGE}"),
@@ -1703,14 +1779,21 @@ def render(kernels: list[tuple]) -> str:
     return "\n".join(lines) + "\n"
 
 
-def build_all() -> list[tuple[Gen, str, str]]:
-    """The contiguous and the paged kernel."""
-    global PAGED, KERNEL
+def build_all() -> list[tuple]:
+    """The contiguous, the paged and the precise kernel (with its resource counts: the precise
+    kernel holds the Q residual in the last 64 AGPRs and three 48 KiB stages, one barrier per
+    key tile)."""
+    global PAGED, KERNEL, PREC, NSTAGE, PAIR
     out = []
-    for paged, name, prefix in ((False, KERNEL_CONTIG, ""), (True, KERNEL_PAGED, "P")):
-        PAGED, KERNEL = paged, name
-        out.append((build(), name, prefix))
-    PAGED, KERNEL = False, KERNEL_CONTIG
+    for paged, prec, name, prefix in ((False, False, KERNEL_CONTIG, ""),
+                                      (True, False, KERNEL_PAGED, "P"),
+                                      (False, True, KERNEL_PREC, "R")):
+        PAGED, PREC, KERNEL = paged, prec, name
+        NSTAGE, PAIR = (3, False) if prec else (5, True)
+        counts = {"num_agpr": 256 if prec else NUM_AGPR,
+                  "lds_bytes": NSTAGE * STAGE_BYTES()}
+        out.append((build(), name, prefix, counts))
+    PAGED, PREC, KERNEL, NSTAGE, PAIR = False, False, KERNEL_CONTIG, 5, True
     return out
 
 
@@ -1748,7 +1831,8 @@ def header(path: str):
              "#pragma once", f"#define FA_A64_ARG_BYTES {ARG_BYTES}",
              f"#define FA_A64_LDS_BYTES {LDS_BYTES}",
              f'#define FA_A64_KERNEL "{KERNEL_CONTIG}"',
-             f'#define FA_A64_KERNEL_PAGED "{KERNEL_PAGED}"']
+             f'#define FA_A64_KERNEL_PAGED "{KERNEL_PAGED}"',
+             f'#define FA_A64_KERNEL_PREC "{KERNEL_PREC}"']
     for n, off, sz in ARGS:
         lines.append(f"#define FA_A64_OFF_{n.upper()} {off}")
     open(path, "w").write("\n".join(lines) + "\n")

@@ -867,6 +867,7 @@ struct PrefillJob {
 struct PrefillRun {
     PrefillJob j;
     bool prerot = false;
+    bool prec64 = false;      // precise scores in the assembly kernel (K and its residual)
     float2* table = nullptr;  // RoPE (cos, sin) rows [0, max_pos)
     void* ws = nullptr;       // rotated K (prerot)
 };
@@ -877,6 +878,8 @@ struct PrefillRun {
 struct PrefillChoice {
     bool prerot = false;  // K rotated once by the pre-pass
     bool split_qk = false;  // precise 16-bit scores: K rotated on load, split Q/K
+    bool prec64 = false;  // precise 16-bit scores in the assembly kernel: K and its residual
+                          // from the pre-pass (prerot), Q split in the kernel
 };
 
 PrefillChoice choose_prefill(const fa_ctx* ctx, const PrefillJob& j) {
@@ -884,11 +887,31 @@ PrefillChoice choose_prefill(const fa_ctx* ctx, const PrefillJob& j) {
     if (j.rope) {
         c.prerot = j.a.rope_k && !j.paged && want_prerotate(ctx, (uint64_t)j.a.head_dim);
         if (ctx->prefill_precision == 1 && j.a.rope_k && !j.paged && j.dtype != FA_DTYPE_F32) {
-            c.prerot = false;
-            c.split_qk = true;
+            // the assembly kernel where it takes the launch (the arguments it would receive:
+            // K rotated by the pre-pass, the residual beside it), else the HIP split kernel
+            fa::PrefillArgs t = j.a;
+            t.rope_k = 0;
+            t.a64 = ctx->prefill_kernel_policy != 0;
+            t.rope_rows = (int)j.max_pos;
+            t.rope_table = (const float2*)(uintptr_t)16;
+            t.k_lo = (const void*)(uintptr_t)16;
+            if (j.dtype == FA_DTYPE_BF16 && j.a.head_dim % 8 == 0 &&
+                fa::prefill_a64_eligible(j.dt, false, t)) {
+                c.prerot = true;
+                c.prec64 = true;
+            } else {
+                c.prerot = false;
+                c.split_qk = true;
+            }
         }
     }
     return c;
+}
+
+// Bytes of the rotated-K workspace: the rotation, and for the precise assembly kernel its
+// residual right after it.
+uint64_t ws_bytes_for(const PrefillJob& j, const PrefillChoice& c) {
+    return c.prec64 ? 2 * j.kv_bytes : j.kv_bytes;
 }
 
 // Device allocations a one-shot call of `j` would make through the context's growable caches
@@ -906,9 +929,9 @@ void predict_prefill_allocs(const fa_ctx* ctx, const PrefillJob& j, const Prefil
         ++*count;
         *bytes += cap * (hd / 2) * sizeof(float2);
     }
-    if (c.prerot && ctx->ws_bytes < j.kv_bytes) {
+    if (c.prerot && ctx->ws_bytes < ws_bytes_for(j, c)) {
         ++*count;
-        *bytes += j.kv_bytes;
+        *bytes += ws_bytes_for(j, c);
     }
 }
 
@@ -939,6 +962,7 @@ int resolve_prefill(fa_ctx* ctx, PrefillJob& j, bool own, PrefillRun* r) {
         r->j.a.rope_table = r->table;
         const PrefillChoice c = choose_prefill(ctx, j);
         prerot = c.prerot;
+        r->prec64 = c.prec64;
         // precise scores: K rotated in the kernel, which keeps its 16-bit residual
         if (c.split_qk) r->j.a.split_qk = 1;
         r->j.a.rope_rows = (int)j.max_pos;
@@ -946,9 +970,10 @@ int resolve_prefill(fa_ctx* ctx, PrefillJob& j, bool own, PrefillRun* r) {
     r->j.a.a64 = ctx->prefill_kernel_policy != 0;
     r->prerot = prerot;
     if (prerot) {
+        const uint64_t wsb = r->prec64 ? 2 * j.kv_bytes : j.kv_bytes;
         if (own) {
-            if (int rc = dev_alloc(ctx, &r->ws, j.kv_bytes)) return rc;
-        } else if (int rc = ensure_ws(ctx, j.kv_bytes, &r->ws)) {
+            if (int rc = dev_alloc(ctx, &r->ws, wsb)) return rc;
+        } else if (int rc = ensure_ws(ctx, wsb, &r->ws)) {
             return rc;
         }
     }
@@ -973,7 +998,9 @@ void describe_prefill(const fa_ctx* ctx, const PrefillJob& j, const fa::PrefillA
     const char* base =
         j.dtype == FA_DTYPE_F32 ? "prefill_mfma_f32" : (a64 ? "prefill_a64" : "prefill_mfma16");
     char name[64];
-    if (prerot)
+    if (prerot && a.k_lo && a64)
+        snprintf(name, sizeof name, "rotate_rows + %s<%s> (split Q/K scores)", base, dt);
+    else if (prerot)
         snprintf(name, sizeof name, "rotate_rows + %s<%s>", base, dt);
     else if (j.paged)
         snprintf(name, sizeof name, "%s<%s> (paged%s)", base, dt, j.rope ? ", K stored rotated" : "");
@@ -995,12 +1022,18 @@ int enqueue_prefill(fa_ctx* ctx, const PrefillRun& r) {
     uint32_t dispatches = 0;
     if (r.prerot) {
         begin_span(ctx);
-        fa::launch_rotate_rows(j.dt, a.k, r.ws, (int)j.k_rows, (int)j.k_heads, a.head_dim,
-                               (int64_t)j.k_period, r.table, a.kv_rope_offset, ctx->stream);
+        if (r.prec64)
+            fa::launch_rotate_rows_split(a.k, r.ws, (uint8_t*)r.ws + j.kv_bytes, (int)j.k_rows,
+                                         (int)j.k_heads, a.head_dim, (int64_t)j.k_period,
+                                         r.table, a.kv_rope_offset, ctx->stream);
+        else
+            fa::launch_rotate_rows(j.dt, a.k, r.ws, (int)j.k_rows, (int)j.k_heads, a.head_dim,
+                                   (int64_t)j.k_period, r.table, a.kv_rope_offset, ctx->stream);
         end_span(ctx, FA_KERNEL_ROPE_ROTATE);
         HIP_TRY(hipGetLastError());
         a.k = r.ws;
         a.rope_k = 0;
+        if (r.prec64) a.k_lo = (const uint8_t*)r.ws + j.kv_bytes;
         dispatches++;
     }
     unsigned grid[3], block = 0;
@@ -1151,6 +1184,7 @@ int fa_forward_gqa_rope_telemetry(fa_ctx* ctx, const fa_grouped_shape* sh, const
     fa::PrefillArgs a = j.a;  // the arguments the prefill kernel would receive
     if (c.prerot) a.rope_k = 0;
     if (c.split_qk) a.split_qk = 1;
+    if (c.prec64) a.k_lo = (const void*)(uintptr_t)16;  // stands for the residual the call writes
     a.a64 = ctx->prefill_kernel_policy != 0;
     a.rope_rows = (int)j.max_pos;
     if (j.rope) a.rope_table = (const float2*)(uintptr_t)16;  // stands for the table the call builds

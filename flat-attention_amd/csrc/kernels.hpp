@@ -48,6 +48,9 @@ struct PrefillArgs {
     int a64;
     // Rows of rope_table (positions it covers); bounds the assembly kernel's table reads.
     int rope_rows;
+    // Precise scores in the assembly kernel (contiguous K/V, K rotated by the pre-pass): the
+    // bf16 residual of the rotated K, laid out like `k` (launch_rotate_rows_split); null: off.
+    const void* k_lo;
 };
 
 // The assembly prefill (64 query rows per wave, code object loaded per device): bf16, Q rotated
@@ -187,6 +190,11 @@ void launch_append(Dtype dt, const AppendArgs& a, hipStream_t s);
 
 // Rotate every row of a [rows, heads*head_dim] tensor (in place allowed); row r is at RoPE
 // position offset + r % period. head_dim must be a multiple of 8.
+// bf16 rows rotated as launch_rotate_rows, written as the rounding `hi` and the bf16 rounding of
+// the residual `lo` (same layout).
+void launch_rotate_rows_split(const void* in, void* hi, void* lo, int rows, int heads,
+                              int head_dim, int64_t period, const float2* table, int offset,
+                              hipStream_t s);
 void launch_rotate_rows(Dtype dt, const void* in, void* out, int rows, int heads, int head_dim,
                         int64_t period, const float2* table, int offset, hipStream_t s);
 

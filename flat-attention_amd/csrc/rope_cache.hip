@@ -103,6 +103,51 @@ __global__ void rotate_rows_kernel(const uint8_t* in, uint8_t* out, int rows, in
     copy8<T>(in + off, out + off, table + (int64_t)pos * (head_dim / 2) + d0 / 2);
 }
 
+// The same rotation for bf16 rows, written as the rounded rotation `hi` and the rounding of its
+// residual `lo` = bf16(x - hi) (x the f32 rotation): the operands of the precise assembly
+// prefill, whose scores then carry the rotation to about 16 bits.
+__global__ void rotate_rows_split_kernel(const uint8_t* in, uint8_t* hi, uint8_t* lo, int rows,
+                                         int heads, int head_dim, int period,
+                                         const float2* table, int offset) {
+    const int chunks = heads * head_dim / 8;
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (int64_t)rows * chunks) return;
+    const int r = (int)(i / chunks), c = (int)(i % chunks);
+    const int e0 = c * 8;
+    const int d0 = e0 % head_dim;
+    const int pos = offset + r % period;
+    const int64_t off = ((int64_t)r * heads * head_dim + e0) * 2;
+    const float2* cs = table + (int64_t)pos * (head_dim / 2) + d0 / 2;
+    const u32x4_t w = *(const u32x4_t*)(in + off);
+    float x[8], c8[8];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        x[2 * j] = Half<bf16_t>::lo(w[j]);
+        x[2 * j + 1] = Half<bf16_t>::hi(w[j]);
+        c8[2 * j] = cs[j].x;
+        c8[2 * j + 1] = cs[j].y;
+    }
+    rope4(x, c8);
+    u32x4_t h, l;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        h[j] = Half<bf16_t>::pack(x[2 * j], x[2 * j + 1]);
+        l[j] = Half<bf16_t>::pack(x[2 * j] - Half<bf16_t>::lo(h[j]),
+                                  x[2 * j + 1] - Half<bf16_t>::hi(h[j]));
+    }
+    *(u32x4_t*)(hi + off) = h;
+    *(u32x4_t*)(lo + off) = l;
+}
+
+void launch_rotate_rows_split(const void* in, void* hi, void* lo, int rows, int heads,
+                              int head_dim, int64_t period, const float2* table, int offset,
+                              hipStream_t s) {
+    const int64_t n = (int64_t)rows * heads * head_dim / 8;
+    const unsigned g = (unsigned)((n + 255) / 256);
+    rotate_rows_split_kernel<<<g, 256, 0, s>>>((const uint8_t*)in, (uint8_t*)hi, (uint8_t*)lo,
+                                               rows, heads, head_dim, (int)period, table, offset);
+}
+
 void launch_rotate_rows(Dtype dt, const void* in, void* out, int rows, int heads, int head_dim,
                         int64_t period, const float2* table, int offset, hipStream_t s) {
     const int64_t n = (int64_t)rows * heads * head_dim / 8;

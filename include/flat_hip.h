@@ -579,8 +579,10 @@ int fa_ctx_set_prefill_kernel(fa_ctx* ctx, int32_t assembly);
  * applied to this backend). 0 (default): the rotated Q and K are rounded to the storage type
  * before Q.K^T, so a score s carries a relative error up to about 2^-8 (bf16) -- within the
  * 2e-2 bar for unit-scale inputs, not for scores of tens. 1: the rotated Q and K keep their
- * 16-bit residuals and each score block takes three MFMAs (f32-level scores; K is then rotated
- * in the kernel, about half the throughput). Applies to contiguous K that the call rotates;
+ * 16-bit residuals and each score block takes three MFMAs (f32-level scores, about 0.6x the
+ * default's throughput where the assembly kernel runs: bf16, head_dim 128, power-of-two group,
+ * with K and its residual written by a split pre-rotation pass; elsewhere the HIP kernel
+ * rotates K on load, about 0.3x). Applies to contiguous K that the call rotates;
  * K that is stored rotated (paged cache, pre-rotated asymmetric input) is used as stored.
  * Other values: FA_ERR_UNAVAILABLE. */
 int fa_ctx_set_prefill_precision(fa_ctx* ctx, int32_t mode);

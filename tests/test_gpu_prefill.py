@@ -450,7 +450,10 @@ def test_precise_rope_prefill_matches_oracle(hip, dtype, rnd, hq, hkv, S, D, cau
         hip.set_prefill_precision(1)
         o, l = _run_grouped(hip, q, k, v, shape, fa.FlatAttentionConfig(causal), rot, dtype)
         t = hip.last_telemetry()
-        assert "split" in t.kernel_name and t.dispatch_count == 1
+        # bf16 at D 128 with a power-of-two group: the assembly kernel after the split K
+        # rotation (two dispatches); otherwise the HIP kernel rotating K on load (one)
+        assert "split" in t.kernel_name
+        assert t.dispatch_count == (2 if "prefill_a64" in t.kernel_name else 1), t.kernel_name
     finally:
         hip.set_prefill_precision(0)
     eo, el = _oracle_grouped(q, k, v, shape, causal, rot)

@@ -182,7 +182,7 @@ def test_assembly_projection_layout_rect_causal_offset(asm):
             assert_close(f"LSE {ql}x{kl}", res.lse, el, H16_ATOL, 0.0)
 
 
-@pytest.mark.parametrize("case", ["f16", "head_dim_64", "no_rope", "group_3", "precise"])
+@pytest.mark.parametrize("case", ["f16", "head_dim_64", "no_rope", "group_3", "precise_group_3"])
 def test_assembly_prefill_falls_back_where_it_does_not_apply(asm, case):
     """Inputs outside the assembly kernel's scope run the HIP kernels (the telemetry names
     which) and still match the oracle."""
@@ -194,13 +194,13 @@ def test_assembly_prefill_falls_back_where_it_does_not_apply(asm, case):
         D = 64
     elif case == "no_rope":
         rot = None
-    elif case == "group_3":
+    elif case in ("group_3", "precise_group_3"):
         hq, hkv = 6, 2
     q = rnd(normal(B * hq * S * D, 41))
     k, v = rnd(normal(B * hkv * S * D, 42)), rnd(normal(B * hkv * S * D, 43))
     shape = fa.GroupedAttentionShape(B, hq, hkv, S, D)
     try:
-        if case == "precise":
+        if case == "precise_group_3":
             asm.set_prefill_precision(1)
         o, l = _run_grouped(asm, q, k, v, shape, fa.FlatAttentionConfig(True), rot, dtype)
     finally:
@@ -245,3 +245,38 @@ def test_assembly_paged_prefill_matches_paged_oracle(asm, hq, hkv, cached, ql, c
                                   cached, causal, theta, cached, threads=4)
     assert_close("O vs paged oracle", o2, po, H16_ATOL, 0.0)
     assert_close("LSE vs paged oracle", l2, pl, H16_ATOL, 0.0)
+
+
+@pytest.mark.parametrize("hq,hkv,S", [(8, 2, 200), (4, 4, 63), (16, 1, 300), (32, 8, 1000)])
+@pytest.mark.parametrize("causal", [True, False])
+def test_precise_assembly_prefill_matches_oracle_and_hip_split(hip, hq, hkv, S, causal):
+    """Precision mode 1 on the assembly kernel (fa_prefill_a64_precise_bf16: K and its bf16
+    residual from the split rotation pre-pass, Q split in the kernel, three score MFMAs per
+    k-step, three 48 KiB stages): the oracle at the 16-bit bar, and the HIP split-score kernel
+    (fa_ctx_set_prefill_kernel(0)) within it."""
+    B, D = 2, 128
+    q = bf16_round(normal(B * hq * S * D, 950 + S + hq))
+    k = bf16_round(normal(B * hkv * S * D, 951 + S))
+    v = bf16_round(normal(B * hkv * S * D, 952 + S))
+    shape = fa.GroupedAttentionShape(B, hq, hkv, S, D)
+    rot = fa.RotaryEmbeddingConfig(1e4, 5)
+    cfg = fa.FlatAttentionConfig(causal)
+    try:
+        hip.set_prefill_precision(1)
+        o, l = _run_grouped(hip, q, k, v, shape, cfg, rot, fa.DTYPE_BF16)
+        name = hip.last_telemetry().kernel_name
+        assert "prefill_a64" in name and "split" in name, name
+        hip.set_prefill_kernel(0)
+        o0, l0 = _run_grouped(hip, q, k, v, shape, cfg, rot, fa.DTYPE_BF16)
+        assert "prefill_a64" not in hip.last_telemetry().kernel_name
+    finally:
+        hip.set_prefill_precision(0)
+        hip.set_prefill_kernel(-1)
+    assert np.isfinite(o).all() and np.isfinite(l).all()
+    units = (0, B * hq) if S <= 300 else (0, 2)
+    eo, el = _oracle_grouped(q, k, v, shape, causal, rot, units=units)
+    n = (units[1] - units[0]) * S
+    assert_close("O", o[:n * D], eo[:n * D], H16_ATOL, 0.0)
+    assert_close("LSE", l[:n], el[:n], H16_ATOL, 0.0)
+    assert_close("O vs HIP split", o, o0, H16_ATOL, 0.0)
+    assert_close("LSE vs HIP split", l, l0, H16_ATOL, 0.0)
