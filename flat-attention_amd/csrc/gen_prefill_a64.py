@@ -853,8 +853,11 @@ def phase(gen: Gen, *, pv_x, pv_hh, s_x, s_hh, sm_x, sm_masked, pre=(),
 
 
 def transfer_block(which: str) -> list[Ins]:
-    """The 4 K or V transfer instructions of this wave for the tile whose resource is set up;
-    M0 = stage base (S_T2) + region + (wave + 4 i) KiB."""
+    """The 4 K or V transfer instructions of this wave for the tile whose resource is set up:
+    instruction i fills KiB 4 wave + i of the region (rows 16 wave + 4 i .. + 3). One M0 = stage
+    base (S_T2, which includes the wave's 4 KiB) + region serves all four: the instruction offset
+    1024 i moves the LDS and the global address alike, and the lane offsets VTOFF + i carry
+    -1024 i."""
     out = []
     rs = S_RV if which == "v" else S_RK
     region = {"k": 0, "klo": 16384, "v": V_REGION()}[which]
@@ -863,10 +866,10 @@ def transfer_block(which: str) -> list[Ins]:
         out += [I(f"s_add_u32 {sr(S_RK)}, {sr(S_RK)}, {arg('klo_off')}"),
                 I(f"s_addc_u32 {sr(S_RK + 1)}, {sr(S_RK + 1)}, {arg('klo_off', True)}"),
                 I(f"s_and_b32 {sr(S_RK + 1)}, {sr(S_RK + 1)}, 0xffff")]
+    out.append(I(f"s_add_u32 m0, {sr(S_T2)}, {region}", writes=["m0"], reads=[f"s{S_T2}"]))
     for i in range(4):
-        out.append(I(f"s_add_u32 m0, {sr(S_T2)}, {region + 1024 * 4 * i}", writes=["m0"],
-                     reads=[f"s{S_T2}"]))
-        out.append(I(f"buffer_load_dwordx4 {vr(VTOFF + i)}, {sr(rs, 4)}, 0 offen lds"))
+        out.append(I(f"buffer_load_dwordx4 {vr(VTOFF + i)}, {sr(rs, 4)}, 0 offen "
+                     f"offset:{1024 * i} lds"))
     return out
 
 
@@ -879,7 +882,7 @@ def kv_transfers() -> list[Ins]:
 
 def transfer_setup(tile_sgpr: str) -> list[Ins]:
     """Resources of the K and V rows of tile `tile_sgpr` (bounded to its live rows) and the
-    stage base S_T2 = stage * 32 KiB + wave KiB."""
+    stage base S_T2 = stage * stage bytes + 4 wave KiB."""
     t0, t1 = sr(S_T0), sr(S_T1)
     rb = arg("k_ss")
     out = [
@@ -904,7 +907,7 @@ def transfer_setup(tile_sgpr: str) -> list[Ins]:
         # stage base: tslot * stage bytes + wave KiB
         (I(f"s_mul_i32 {sr(S_T2)}, {sr(S_TSLOT)}, {STAGE_BYTES()}") if PREC else
          I(f"s_lshl_b32 {sr(S_T2)}, {sr(S_TSLOT)}, 15")),
-        I(f"s_lshl_b32 {sr(S_T3)}, {sr(S_WAVE)}, 10"),
+        I(f"s_lshl_b32 {sr(S_T3)}, {sr(S_WAVE)}, 12"),
         I(f"s_add_u32 {sr(S_T2)}, {sr(S_T2)}, {sr(S_T3)}"),
     ]
     return out
@@ -1190,19 +1193,38 @@ def setup_block(gen: Gen):
         e([I(f"s_sub_u32 {T0}, {arg('kv_len')}, 1"),
            I(f"s_mul_i32 {sr(S_NREC)}, {T0}, {arg('k_ss')}"),
            I(f"s_add_u32 {sr(S_NREC)}, {sr(S_NREC)}, 256")])
-    # transfer offsets: instruction i covers rows 4 (wave + 4 i) + (lane >> 4); slot chunk
-    # lane & 15 holds global chunk (lane & 15) ^ (4 (lane >> 4) + wave)
-    e([I(f"v_lshrrev_b32 {vr(V_ROW)}, 4, {vr(V_LANE)}"),           # lane >> 4
-       I(f"v_and_b32 {vr(V_ROW + 1)}, 15, {vr(V_LANE)}"),
-       I(f"v_lshl_add_u32 {vr(V_ROW + 2)}, {vr(V_ROW)}, 2, {sr(S_WAVE)}"),
-       I(f"v_xor_b32 {vr(V_ROW + 2)}, {vr(V_ROW + 2)}, {vr(V_ROW + 1)}"),   # global chunk
-       I(f"v_lshlrev_b32 {vr(V_ROW + 2)}, 4, {vr(V_ROW + 2)}"),
-       I(f"s_lshl_b32 {T0}, {sr(S_WAVE)}, 2"),
-       I(f"v_add_u32 {vr(V_ROW + 3)}, {T0}, {vr(V_ROW)}")])          # row of instruction 0
-    for i in range(4):
-        e([I(f"v_add_u32 {vr(V_TMP)}, {16 * i}, {vr(V_ROW + 3)}"),
-           I(f"v_mul_lo_u32 {vr(VTOFF + i)}, {vr(V_TMP)}, {arg('k_ss')}"),
-           I(f"v_add_u32 {vr(VTOFF + i)}, {vr(VTOFF + i)}, {vr(V_ROW + 2)}")])
+    if PAGED:
+        # transfer offsets: instruction i covers rows 4 (wave + 4 i) + (lane >> 4) (in-page:
+        # rows 4 wave + (lane >> 4) of page i); slot chunk lane & 15 holds global chunk
+        # (lane & 15) ^ (4 (lane >> 4) + wave)
+        e([I(f"v_lshrrev_b32 {vr(V_ROW)}, 4, {vr(V_LANE)}"),           # lane >> 4
+           I(f"v_and_b32 {vr(V_ROW + 1)}, 15, {vr(V_LANE)}"),
+           I(f"v_lshl_add_u32 {vr(V_ROW + 2)}, {vr(V_ROW)}, 2, {sr(S_WAVE)}"),
+           I(f"v_xor_b32 {vr(V_ROW + 2)}, {vr(V_ROW + 2)}, {vr(V_ROW + 1)}"),   # global chunk
+           I(f"v_lshlrev_b32 {vr(V_ROW + 2)}, 4, {vr(V_ROW + 2)}"),
+           I(f"s_lshl_b32 {T0}, {sr(S_WAVE)}, 2"),
+           I(f"v_add_u32 {vr(V_ROW + 3)}, {T0}, {vr(V_ROW)}")])          # row of instruction 0
+        for i in range(4):
+            e([I(f"v_add_u32 {vr(V_TMP)}, {16 * i}, {vr(V_ROW + 3)}"),
+               I(f"v_mul_lo_u32 {vr(VTOFF + i)}, {vr(V_TMP)}, {arg('k_ss')}"),
+               I(f"v_add_u32 {vr(VTOFF + i)}, {vr(VTOFF + i)}, {vr(V_ROW + 2)}")])
+    else:
+        # transfer offsets: instruction i covers rows 16 wave + 4 i + (lane >> 4) (LDS KiB
+        # 4 wave + i); slot chunk lane & 15 holds global chunk (lane & 15) ^ (4 (lane >> 4) + i),
+        # less the instruction offset 1024 i
+        e([I(f"v_lshrrev_b32 {vr(V_ROW)}, 4, {vr(V_LANE)}"),           # lane >> 4
+           I(f"v_and_b32 {vr(V_ROW + 1)}, 15, {vr(V_LANE)}"),
+           I(f"v_lshlrev_b32 {vr(V_ROW + 2)}, 2, {vr(V_ROW)}"),         # 4 (lane >> 4)
+           I(f"s_lshl_b32 {T0}, {sr(S_WAVE)}, 4"),
+           I(f"v_add_u32 {vr(V_ROW + 3)}, {T0}, {vr(V_ROW)}")])          # row of instruction 0
+        for i in range(4):
+            e([I(f"v_add_u32 {vr(V_TMP)}, {4 * i}, {vr(V_ROW + 3)}"),
+               I(f"v_mul_lo_u32 {vr(VTOFF + i)}, {vr(V_TMP)}, {arg('k_ss')}"),
+               I(f"v_add_u32 {vr(V_TMP + 1)}, {i}, {vr(V_ROW + 2)}"),
+               I(f"v_xor_b32 {vr(V_TMP + 1)}, {vr(V_TMP + 1)}, {vr(V_ROW + 1)}"),  # global chunk
+               I(f"v_lshlrev_b32 {vr(V_TMP + 1)}, 4, {vr(V_TMP + 1)}"),
+               I(f"v_add_u32 {vr(VTOFF + i)}, {vr(VTOFF + i)}, {vr(V_TMP + 1)}"),
+               I(f"v_add_u32 {vr(VTOFF + i)}, 0x{(-1024 * i) & 0xffffffff:x}, {vr(VTOFF + i)}")])
     # K read addresses (stage 0): row p = perm(lane & 31) (bits 2, 3 swapped),
     # chunk (2 ks + g) ^ swz(p); V^T read addresses (stage 0, V region at +16 KiB)
     e([I(f"v_and_b32 {vr(V_ROW)}, 31, {vr(V_LANE)}"),
@@ -1604,8 +1626,11 @@ def iteration(gen: Gen, masked: bool, tag: str, jofs: int, ring_in, xfer_tile_of
              I(f"s_cmp_eq_u32 {sr(S_TSLOT)}, {NSTAGE}"),
              I(f"s_cselect_b32 {sr(S_TSLOT)}, 0, {sr(S_TSLOT)}")]
         assert not PREC
-        tb = transfer_block("k") + transfer_block("v")
-        groups = [tb[2 * i:2 * i + 2] for i in range(len(tb) // 2)]
+        # one load per group, each block's M0 write with its first load
+        groups = []
+        for which in ("k", "v"):
+            tb = transfer_block(which)
+            groups += [tb[:2]] + [[x] for x in tb[2:]]
     elif xfer_tile_ofs is not None:
         if PAGED:
             # tile j+3 from page-id lanes 0..3, tile j+4 from lanes 4..7; after the second,

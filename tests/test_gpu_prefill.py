@@ -201,6 +201,25 @@ def test_cfg3_full_size_bf16_gqa_rope_causal(hip, kernel):
         hip.set_prefill_kernel(-1)
 
 
+def test_cfg3_full_size_precise_scores(hip):
+    """configs[2] at full size in the precise-score mode (fa_ctx_set_prefill_precision(1)): the
+    assembly kernel over K and its residual from the split rotation pass, Q split in the kernel.
+    The same oracle units and V = 1 property as the default mode."""
+    B, hq, hkv, S, D = 2, 32, 8, 4096, 128
+    q = bf16_round(normal(B * hq * S * D, 34))
+    k = bf16_round(normal(B * hkv * S * D, 35))
+    v = bf16_round(normal(B * hkv * S * D, 36))
+    shape = fa.GroupedAttentionShape(B, hq, hkv, S, D)
+    hip.set_prefill_precision(1)
+    try:
+        _cfg3_full(hip, q, k, v, shape, fa.RotaryEmbeddingConfig(1e4, 0))
+        t = hip.last_telemetry()
+        assert "prefill_a64" in t.kernel_name and "split" in t.kernel_name, t.kernel_name
+        assert t.dispatch_count == 2
+    finally:
+        hip.set_prefill_precision(0)
+
+
 def _cfg3_full(hip, q, k, v, shape, rot):
     B, hq, hkv, S, D = shape.batch, shape.q_heads, shape.kv_heads, shape.seq_len, shape.head_dim
     o, l = _run_grouped(hip, q, k, v, shape, fa.FlatAttentionConfig(True), rot, fa.DTYPE_BF16)
