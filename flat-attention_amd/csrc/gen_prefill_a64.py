@@ -918,41 +918,44 @@ S_PHI = 23            # argument dword 15 (the upper half of the k_sb slot, unus
 
 
 def transfer_paged(tile_sgpr: str, lane_base: int) -> list[Ins]:
-    """Paged: the 8 transfers of tile `tile_sgpr` into stage S_TSLOT, page i of the tile (its
-    rows 16 i .. 16 i + 15, one page of 16 rows) from V_PT lane lane_base + i. Every transfer
-    uses the in-page lane offsets VTOFF (rows 4 wave + (lane >> 4)) against a resource based
-    at that page of this kv head, bounded to the page's live rows (0 past kv_len)."""
+    """Paged: the wave's 8 transfers of tile `tile_sgpr` into stage S_TSLOT. A wave's four K (and
+    four V) instructions cover rows 16 wave .. 16 wave + 15 of the tile, i.e. exactly page `wave`
+    of the tile (one page of 16 rows), whose id is V_PT lane lane_base + wave: one buffer
+    resource based at that page of this kv head, bounded to the page's live rows (0 past
+    kv_len), and one M0 per K or V block (instruction offsets 1024 i, the in-page lane offsets
+    VTOFF + i carrying -1024 i)."""
     T0, T1, T2, T3 = (sr(S_T0), sr(S_T1), sr(S_T2), sr(S_T3))
     LO, HI = sr(S_PLO), sr(S_PHI)
     rbytes = arg("k_ss")
-    out = [I(f"s_lshl_b32 {T0}, {tile_sgpr}, 6"),                # key of page 0
-           I(f"s_lshl_b32 {T2}, {sr(S_TSLOT)}, 15"),
-           I(f"s_lshl_b32 {T3}, {sr(S_WAVE)}, 10"),
-           I(f"s_add_u32 {T2}, {T2}, {T3}"),                       # stage base + wave KiB
+    out = [I(f"s_lshl_b32 {T0}, {tile_sgpr}, 6"),                # key of the tile's page 0
+           I(f"s_lshl_b32 {T3}, {sr(S_WAVE)}, 4"),
+           I(f"s_add_u32 {T0}, {T0}, {T3}"),                       # key of the wave's page
+           I(f"s_add_u32 {T1}, {sr(S_WAVE)}, {lane_base}"),
+           I(f"v_readlane_b32 {T1}, {vr(V_PT)}, {T1}"),            # page id
+           I(f"s_sub_u32 {T3}, {arg('kv_len')}, {T0}"),
+           I(f"s_max_i32 {T3}, {T3}, 0"),
+           I(f"s_min_i32 {T3}, {T3}, 16"),
+           I(f"s_mul_i32 {T3}, {T3}, {rbytes}"),                   # live bytes of the page
+           I(f"s_lshl_b32 {LO}, {rbytes}, 4"),                     # page bytes
+           I(f"s_mul_hi_u32 {HI}, {T1}, {LO}"),
+           I(f"s_mul_i32 {LO}, {T1}, {LO}"),                       # page * page bytes (64-bit)
+           I(f"s_add_u32 {sr(S_RK)}, {sr(S_KBASE)}, {LO}"),
+           I(f"s_addc_u32 {sr(S_RK + 1)}, {sr(S_KBASE + 1)}, {HI}"),
+           I(f"s_and_b32 {sr(S_RK + 1)}, {sr(S_RK + 1)}, 0xffff"),
+           I(f"s_mov_b32 {sr(S_RK + 2)}, {T3}"),
            I(f"s_mov_b32 {sr(S_RK + 3)}, 0x20000"),
-           I(f"s_mov_b32 {sr(S_RV + 3)}, 0x20000")]
-    for i in range(4):
-        out += [I(f"v_readlane_b32 {T1}, {vr(V_PT)}, {lane_base + i}"),  # page id
-                I(f"s_sub_u32 {T3}, {arg('kv_len')}, {T0}"),
-                I(f"s_max_i32 {T3}, {T3}, 0"),
-                I(f"s_min_i32 {T3}, {T3}, 16"),
-                I(f"s_mul_i32 {T3}, {T3}, {rbytes}"),               # live bytes of the page
-                I(f"s_lshl_b32 {LO}, {rbytes}, 4"),                 # page bytes
-                I(f"s_mul_hi_u32 {HI}, {T1}, {LO}"),
-                I(f"s_mul_i32 {LO}, {T1}, {LO}"),                   # page * page bytes (64-bit)
-                I(f"s_add_u32 {sr(S_RK)}, {sr(S_KBASE)}, {LO}"),
-                I(f"s_addc_u32 {sr(S_RK + 1)}, {sr(S_KBASE + 1)}, {HI}"),
-                I(f"s_and_b32 {sr(S_RK + 1)}, {sr(S_RK + 1)}, 0xffff"),
-                I(f"s_mov_b32 {sr(S_RK + 2)}, {T3}"),
-                I(f"s_add_u32 {sr(S_RV)}, {sr(S_VBASE)}, {LO}"),
-                I(f"s_addc_u32 {sr(S_RV + 1)}, {sr(S_VBASE + 1)}, {HI}"),
-                I(f"s_and_b32 {sr(S_RV + 1)}, {sr(S_RV + 1)}, 0xffff"),
-                I(f"s_mov_b32 {sr(S_RV + 2)}, {T3}"),
-                I(f"s_add_u32 m0, {T2}, {4096 * i}", writes=["m0"], reads=[f"s{S_T2}"]),
-                I(f"buffer_load_dwordx4 {vr(VTOFF)}, {sr(S_RK, 4)}, 0 offen lds"),
-                I(f"s_add_u32 m0, {T2}, {16384 + 4096 * i}", writes=["m0"], reads=[f"s{S_T2}"]),
-                I(f"buffer_load_dwordx4 {vr(VTOFF)}, {sr(S_RV, 4)}, 0 offen lds"),
-                I(f"s_add_u32 {T0}, {T0}, 16")]
+           I(f"s_add_u32 {sr(S_RV)}, {sr(S_VBASE)}, {LO}"),
+           I(f"s_addc_u32 {sr(S_RV + 1)}, {sr(S_VBASE + 1)}, {HI}"),
+           I(f"s_and_b32 {sr(S_RV + 1)}, {sr(S_RV + 1)}, 0xffff"),
+           I(f"s_mov_b32 {sr(S_RV + 2)}, {T3}"),
+           I(f"s_mov_b32 {sr(S_RV + 3)}, 0x20000"),
+           I(f"s_lshl_b32 {T2}, {sr(S_TSLOT)}, 15"),
+           I(f"s_lshl_b32 {T3}, {sr(S_WAVE)}, 12"),
+           I(f"s_add_u32 {T2}, {T2}, {T3}")]                       # stage base + 4 wave KiB
+    for region, rs in ((0, S_RK), (16384, S_RV)):
+        out.append(I(f"s_add_u32 m0, {T2}, {region}", writes=["m0"], reads=[f"s{S_T2}"]))
+        out += [I(f"buffer_load_dwordx4 {vr(VTOFF + i)}, {sr(rs, 4)}, 0 offen "
+                  f"offset:{1024 * i} lds") for i in range(4)]
     return out
 
 
@@ -1193,38 +1196,25 @@ def setup_block(gen: Gen):
         e([I(f"s_sub_u32 {T0}, {arg('kv_len')}, 1"),
            I(f"s_mul_i32 {sr(S_NREC)}, {T0}, {arg('k_ss')}"),
            I(f"s_add_u32 {sr(S_NREC)}, {sr(S_NREC)}, 256")])
-    if PAGED:
-        # transfer offsets: instruction i covers rows 4 (wave + 4 i) + (lane >> 4) (in-page:
-        # rows 4 wave + (lane >> 4) of page i); slot chunk lane & 15 holds global chunk
-        # (lane & 15) ^ (4 (lane >> 4) + wave)
-        e([I(f"v_lshrrev_b32 {vr(V_ROW)}, 4, {vr(V_LANE)}"),           # lane >> 4
-           I(f"v_and_b32 {vr(V_ROW + 1)}, 15, {vr(V_LANE)}"),
-           I(f"v_lshl_add_u32 {vr(V_ROW + 2)}, {vr(V_ROW)}, 2, {sr(S_WAVE)}"),
-           I(f"v_xor_b32 {vr(V_ROW + 2)}, {vr(V_ROW + 2)}, {vr(V_ROW + 1)}"),   # global chunk
-           I(f"v_lshlrev_b32 {vr(V_ROW + 2)}, 4, {vr(V_ROW + 2)}"),
-           I(f"s_lshl_b32 {T0}, {sr(S_WAVE)}, 2"),
-           I(f"v_add_u32 {vr(V_ROW + 3)}, {T0}, {vr(V_ROW)}")])          # row of instruction 0
-        for i in range(4):
-            e([I(f"v_add_u32 {vr(V_TMP)}, {16 * i}, {vr(V_ROW + 3)}"),
-               I(f"v_mul_lo_u32 {vr(VTOFF + i)}, {vr(V_TMP)}, {arg('k_ss')}"),
-               I(f"v_add_u32 {vr(VTOFF + i)}, {vr(VTOFF + i)}, {vr(V_ROW + 2)}")])
-    else:
-        # transfer offsets: instruction i covers rows 16 wave + 4 i + (lane >> 4) (LDS KiB
-        # 4 wave + i); slot chunk lane & 15 holds global chunk (lane & 15) ^ (4 (lane >> 4) + i),
-        # less the instruction offset 1024 i
-        e([I(f"v_lshrrev_b32 {vr(V_ROW)}, 4, {vr(V_LANE)}"),           # lane >> 4
-           I(f"v_and_b32 {vr(V_ROW + 1)}, 15, {vr(V_LANE)}"),
-           I(f"v_lshlrev_b32 {vr(V_ROW + 2)}, 2, {vr(V_ROW)}"),         # 4 (lane >> 4)
-           I(f"s_lshl_b32 {T0}, {sr(S_WAVE)}, 4"),
-           I(f"v_add_u32 {vr(V_ROW + 3)}, {T0}, {vr(V_ROW)}")])          # row of instruction 0
-        for i in range(4):
-            e([I(f"v_add_u32 {vr(V_TMP)}, {4 * i}, {vr(V_ROW + 3)}"),
-               I(f"v_mul_lo_u32 {vr(VTOFF + i)}, {vr(V_TMP)}, {arg('k_ss')}"),
-               I(f"v_add_u32 {vr(V_TMP + 1)}, {i}, {vr(V_ROW + 2)}"),
-               I(f"v_xor_b32 {vr(V_TMP + 1)}, {vr(V_TMP + 1)}, {vr(V_ROW + 1)}"),  # global chunk
-               I(f"v_lshlrev_b32 {vr(V_TMP + 1)}, 4, {vr(V_TMP + 1)}"),
-               I(f"v_add_u32 {vr(VTOFF + i)}, {vr(VTOFF + i)}, {vr(V_TMP + 1)}"),
-               I(f"v_add_u32 {vr(VTOFF + i)}, 0x{(-1024 * i) & 0xffffffff:x}, {vr(VTOFF + i)}")])
+    # transfer offsets: instruction i covers rows 16 wave + 4 i + (lane >> 4) of the tile (LDS
+    # KiB 4 wave + i; paged: in-page rows 4 i + (lane >> 4) of page `wave`, whose resource the
+    # transfer code bases at the page); slot chunk lane & 15 holds global chunk
+    # (lane & 15) ^ (4 (lane >> 4) + i), less the instruction offset 1024 i
+    e([I(f"v_lshrrev_b32 {vr(V_ROW)}, 4, {vr(V_LANE)}"),           # lane >> 4
+       I(f"v_and_b32 {vr(V_ROW + 1)}, 15, {vr(V_LANE)}"),
+       I(f"v_lshlrev_b32 {vr(V_ROW + 2)}, 2, {vr(V_ROW)}")])        # 4 (lane >> 4)
+    # row of instruction 0 (paged: in-page, no wave term)
+    e([I(f"v_mov_b32 {vr(V_ROW + 3)}, {vr(V_ROW)}")] if PAGED else
+      [I(f"s_lshl_b32 {T0}, {sr(S_WAVE)}, 4"),
+       I(f"v_add_u32 {vr(V_ROW + 3)}, {T0}, {vr(V_ROW)}")])
+    for i in range(4):
+        e([I(f"v_add_u32 {vr(V_TMP)}, {4 * i}, {vr(V_ROW + 3)}"),
+           I(f"v_mul_lo_u32 {vr(VTOFF + i)}, {vr(V_TMP)}, {arg('k_ss')}"),
+           I(f"v_add_u32 {vr(V_TMP + 1)}, {i}, {vr(V_ROW + 2)}"),
+           I(f"v_xor_b32 {vr(V_TMP + 1)}, {vr(V_TMP + 1)}, {vr(V_ROW + 1)}"),  # global chunk
+           I(f"v_lshlrev_b32 {vr(V_TMP + 1)}, 4, {vr(V_TMP + 1)}"),
+           I(f"v_add_u32 {vr(VTOFF + i)}, {vr(VTOFF + i)}, {vr(V_TMP + 1)}"),
+           I(f"v_add_u32 {vr(VTOFF + i)}, 0x{(-1024 * i) & 0xffffffff:x}, {vr(VTOFF + i)}")])
     # K read addresses (stage 0): row p = perm(lane & 31) (bits 2, 3 swapped),
     # chunk (2 ks + g) ^ swz(p); V^T read addresses (stage 0, V region at +16 KiB)
     e([I(f"v_and_b32 {vr(V_ROW)}, 31, {vr(V_LANE)}"),

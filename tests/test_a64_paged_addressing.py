@@ -8,7 +8,9 @@ shape (8 sequences of 2560 keys in 16-row pages, shuffled tables) and ragged len
 every transfer against the page it must read:
   * resource base = pool + kv_head * head bytes + page * 16 * row bytes (K and V),
   * resource bound = the page's live rows (kv_len - first key, clamped to 0..16) * row bytes,
-  * M0 (the LDS destination) = stage * 32 KiB + wave KiB + (V: 16 KiB) + page * 4 KiB,
+  * a wave reads page `wave` of each 64-key tile (its rows 16 wave .. + 15), through one M0 per
+    K or V block: M0 = stage * 32 KiB + 4 KiB * wave + (V: 16 KiB), instruction offsets
+    1024 i for i = 0 .. 3 (LDS KiB 4 wave + i),
 and every block-table load against the sequence's row (base, bound, first entry).
 The same paths (pool row = page * 16 + in-page row) are what the reference's paged gather
 reads (src/paged_kv.rs:113-174; oracle.paged_prefill)."""
@@ -41,7 +43,7 @@ class Scalar:
         self.scc = 0
         self.m0 = 0
         self.pt = pt          # page-id VGPR: lane -> value (set by the block-table loads)
-        self.loads = []       # (kind, resource, m0 / soffset)
+        self.loads = []       # (kind, resource, m0 + instruction offset / soffset)
 
     def val(self, op):
         op = op.strip()
@@ -103,10 +105,11 @@ class Scalar:
             elif op == "s_max_u32":
                 self.set(ops[0], max(self.val(ops[1]), self.val(ops[2])))
             elif op == "v_readlane_b32":
-                self.set(ops[0], self.pt[int(ops[2], 0)])
+                self.set(ops[0], self.pt[self.val(ops[2])])
             elif op == "buffer_load_dwordx4" and rest.endswith("lds"):
                 res = ops[1].split()[0]
-                self.loads.append(("xfer", self.quad(res), self.m0))
+                off = [int(w[7:]) for w in rest.split() if w.startswith("offset:")]
+                self.loads.append(("xfer", self.quad(res), self.m0 + (off[0] if off else 0)))
             elif op == "buffer_load_dword":
                 self.loads.append(("pt", self.quad(ops[2]), self.val(ops[3].split()[0])))
             elif op.startswith(("s_waitcnt", "s_nop")):
@@ -174,25 +177,26 @@ def _keep_transfer_code(ins_list, g):
     return keep
 
 
-def _expected_pages(bt_row, kv_len, tile):
-    return [(int(bt_row[(64 * tile + 16 * i) // 16]) if 64 * tile + 16 * i < kv_len else None,
-             max(0, min(16, kv_len - (64 * tile + 16 * i)))) for i in range(4)]
+def _expected_page(bt_row, kv_len, tile, wave):
+    """(page id, live rows) of page `wave` of the tile."""
+    key = 64 * tile + 16 * wave
+    return (int(bt_row[key // 16]) if key < kv_len else None, max(0, min(16, kv_len - key)))
 
 
-def _check_tile(loads, tile, stage, wave, pages, *, k_pool, v_pool, kvh_off, row_bytes):
+def _check_tile(loads, tile, stage, wave, page_rows, *, k_pool, v_pool, kvh_off, row_bytes):
     assert len(loads) == 8, loads
-    for i in range(4):
-        page, rows = pages[i]
-        for which, (kind, res, m0) in (("k", loads[2 * i]), ("v", loads[2 * i + 1])):
-            assert kind == "xfer"
-            base = res[0] | ((res[1] & 0xFFFF) << 32)
-            assert res[2] == rows * row_bytes, (tile, i, which, res[2], rows)
-            assert res[3] == 0x20000
-            if rows:
-                pool = k_pool if which == "k" else v_pool
-                assert base == pool + kvh_off + page * 16 * row_bytes, (tile, i, which)
-            region = 0 if which == "k" else 16384
-            assert m0 == stage * 32768 + wave * 1024 + region + 4096 * i, (tile, i, which, m0)
+    page, rows = page_rows
+    for j, (kind, res, lds) in enumerate(loads):
+        which, i = ("k" if j < 4 else "v"), j % 4
+        assert kind == "xfer"
+        base = res[0] | ((res[1] & 0xFFFF) << 32)
+        assert res[2] == rows * row_bytes, (tile, i, which, res[2], rows)
+        assert res[3] == 0x20000
+        if rows:
+            pool = k_pool if which == "k" else v_pool
+            assert base == pool + kvh_off + page * 16 * row_bytes, (tile, i, which)
+        region = 0 if which == "k" else 16384
+        assert lds == stage * 32768 + wave * 4096 + region + 1024 * i, (tile, i, which, lds)
 
 
 @pytest.mark.parametrize("kv_len", [2560, 2553, 77, 16, 1])
@@ -233,7 +237,7 @@ def test_paged_transfers_read_exactly_their_pages(kv_len, b, kvh, wave):
     assert len(xfers) == 24
     kvh_off = kvh * D * 2
     for t in range(3):
-        _check_tile(xfers[8 * t:8 * t + 8], t, t, wave, _expected_pages(bt[b], kv_len, t),
+        _check_tile(xfers[8 * t:8 * t + 8], t, t, wave, _expected_page(bt[b], kv_len, t, wave),
                     k_pool=k_pool, v_pool=v_pool, kvh_off=kvh_off, row_bytes=row_bytes)
 
     # ---- the loop: pair j transfers tiles j+3 (lanes 0..3) and j+4 (lanes 4..7) into the ring
@@ -252,7 +256,7 @@ def test_paged_transfers_read_exactly_their_pages(kv_len, b, kvh, wave):
                 body += [g.I(f"s_add_u32 {g.sr(g.S_TT)}, {g.sr(g.S_J)}, 5")] + g.pt_load(g.sr(g.S_TT))
             cpu.run(body)
             _check_tile(cpu.loads[:8], j + ofs, tslot, wave,
-                        _expected_pages(bt[b], kv_len, j + ofs),
+                        _expected_page(bt[b], kv_len, j + ofs, wave),
                         k_pool=k_pool, v_pool=v_pool, kvh_off=kvh_off, row_bytes=row_bytes)
             if ofs == 4:
                 kind, res, soff = cpu.loads[8]
