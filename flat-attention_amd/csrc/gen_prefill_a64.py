@@ -952,8 +952,14 @@ def transfer_paged(tile_sgpr: str, lane_base: int) -> list[Ins]:
            I(f"s_lshl_b32 {T2}, {sr(S_TSLOT)}, 15"),
            I(f"s_lshl_b32 {T3}, {sr(S_WAVE)}, 12"),
            I(f"s_add_u32 {T2}, {T2}, {T3}")]                       # stage base + 4 wave KiB
+    return out + paged_loads()
+
+
+def paged_loads() -> list[Ins]:
+    """The wave's 8 transfer instructions of the tile whose page resources transfer_paged set."""
+    out = []
     for region, rs in ((0, S_RK), (16384, S_RV)):
-        out.append(I(f"s_add_u32 m0, {T2}, {region}", writes=["m0"], reads=[f"s{S_T2}"]))
+        out.append(I(f"s_add_u32 m0, {sr(S_T2)}, {region}", writes=["m0"], reads=[f"s{S_T2}"]))
         out += [I(f"buffer_load_dwordx4 {vr(VTOFF + i)}, {sr(rs, 4)}, 0 offen "
                   f"offset:{1024 * i} lds") for i in range(4)]
     return out
@@ -1623,10 +1629,14 @@ def iteration(gen: Gen, masked: bool, tag: str, jofs: int, ring_in, xfer_tile_of
             groups += [tb[:2]] + [[x] for x in tb[2:]]
     elif xfer_tile_ofs is not None:
         if PAGED:
-            # tile j+3 from page-id lanes 0..3, tile j+4 from lanes 4..7; after the second,
-            # the page ids of tiles j+5 and j+6 (waited for by the pair's closing vmcnt(0))
+            # tile j+3 from page-id lanes 0..3, tile j+4 from lanes 4..7; after the second's
+            # page ids are read, the page ids of tiles j+5 and j+6 (waited for by the pair's
+            # closing vmcnt(0)); the 8 transfer instructions spread over the phase's MFMAs
             assert PAIR and xfer_tile_ofs in (3, 4)
             body = transfer_paged(sr(S_TT), 4 * (xfer_tile_ofs - 3))
+            nl = len(paged_loads())
+            body, tb = body[:-nl], body[-nl:]
+            groups = [tb[:2]] + [[x] for x in tb[2:5]] + [tb[5:7]] + [[x] for x in tb[7:]]
             if xfer_tile_ofs == 4:
                 body += [I(f"s_add_u32 {sr(S_TT)}, {sr(S_J)}, 5")] + pt_load(sr(S_TT))
         else:
