@@ -98,7 +98,7 @@ BRING = 194   # RBN x 4
 RO = 210      # 8: row-read offsets (m, h)
 TO = 218      # 8: transposing-read offsets (m, h)
 V_LDB = 226   # bias read base
-V_XOFF = 227  # transfer offset (Q/dO rows)
+V_XOFF = 227  # transfer offset of instructions 0 and 4 (Q/dO rows)
 V_LDOFF = 228  # bias transfer offset
 V_DSOFF = 229  # 16 * lane (dS store)
 V_TMP = 230   # 8 temps
@@ -106,7 +106,13 @@ V_EPW = 238   # epilogue: LDS write base
 V_EPR = 239   # epilogue: LDS read base
 V_EPG = 240   # epilogue: global offset of the lane's row chunk
 ARING_X = 242  # A-ring slots 4.. (4 registers each, 64-bit aligned)
-NUM_VGPR = ARING_X + 4 * max(0, RA - 4)
+V_XOFF3 = ARING_X + 4 * max(0, RA - 4)  # 3: transfer offsets of instructions 1..3 (and 5..7)
+NUM_VGPR = V_XOFF3 + 3
+
+
+def xoff(k: int) -> int:
+    """Per-lane offset register of transfer instructions k and k + 4."""
+    return V_XOFF if k == 0 else V_XOFF3 + k - 1
 A_DV = 0      # dV[mb]: a[16 mb ..]
 A_DK = 64     # dK[mb]: a[64 + 16 mb ..]
 NUM_AGPR = 128
@@ -142,11 +148,11 @@ S_NRQ = 86         # next tile's Q/dO resource bytes (0 past the last tile)
 S_NRL = 87         # next tile's bias resource bytes
 S_XST = 88         # stage the next tile goes to
 S_DQ = 89          # query step between tiles of one head: +128 or -128
-S_XB = 90          # LDS destination of the wave's transfers (stage + 1 KiB * wave)
+S_XB = 90          # LDS destination of the wave's transfers (stage + 8 KiB * wave)
 S_XBL = 91         # LDS destination of the bias transfer (wave 0: stage + T_LD, else DUMMY)
 S_XNQ = 92         # resource bytes of the next tile's Q / dO (0 past the last tile)
 S_XNL = 93         # and of its biases
-S_XSOFF = 94       # transfer soffset temp
+S_XSOFF = 94       # transfer soffset of instructions 4..7 (16 rows: 4096)
 NUM_SGPR = 96
 
 
@@ -290,18 +296,21 @@ def setup(gen: Gen):
        I(f"v_lshlrev_b32 {vr(V_LDB)}, 5, {vr(G)}"),
        I(f"v_add_u32 {vr(V_LDB)}, {T_LD}, {vr(V_LDB)}"),
        I(f"v_lshlrev_b32 {vr(V_DSOFF)}, 4, {vr(V_LANE)}")])
-    # transfers: instruction i of wave w covers rows 4 w + 16 i + (lane >> 4); slot lane & 15
-    # holds logical chunk (lane & 15) ^ swz(4 w + (lane >> 4))
-    e([I(f"v_lshrrev_b32 {vr(V_TMP + 3)}, 4, {vr(V_LANE)}"),
-       I(f"s_lshl_b32 {T0}, {sr(S_WAVE)}, 2"),
-       I(f"v_add_u32 {vr(V_TMP + 3)}, {T0}, {vr(V_TMP + 3)}"),                       # r (< 16)
-       I(f"v_and_b32 {vr(V_TMP + 4)}, 3, {vr(V_TMP + 3)}"),
-       I(f"v_bfe_u32 {vr(V_TMP + 5)}, {vr(V_TMP + 3)}, 2, 2"),
-       I(f"v_lshl_or_b32 {vr(V_TMP + 4)}, {vr(V_TMP + 4)}, 2, {vr(V_TMP + 5)}"),
-       I(f"v_and_b32 {vr(V_TMP + 5)}, 15, {vr(V_LANE)}"),
-       I(f"v_xor_b32 {vr(V_TMP + 5)}, {vr(V_TMP + 5)}, {vr(V_TMP + 4)}"),
-       I(f"v_lshlrev_b32 {vr(V_TMP + 5)}, 4, {vr(V_TMP + 5)}"),
-       I(f"v_lshl_add_u32 {vr(V_XOFF)}, {vr(V_TMP + 3)}, 8, {vr(V_TMP + 5)}")])
+    # transfers: instruction i of wave w covers rows 32 w + 4 i + (lane >> 4) (LDS KiB 8 w + i);
+    # slot lane & 15 holds logical chunk (lane & 15) ^ swz(4 (i & 3) + (lane >> 4)), i.e.
+    # (lane & 15) ^ (4 (lane >> 4) + (i & 3)). The instruction offset 1024 (i & 3) moves the LDS
+    # and the global address alike, M0 + 4 KiB and soffset 4096 cover i >= 4, so the lane
+    # offset of instructions k and k + 4 is (32 w + (lane >> 4)) * 256 + 16 chunk.
+    e([I(f"v_lshrrev_b32 {vr(V_TMP + 3)}, 4, {vr(V_LANE)}"),                      # lane >> 4
+       I(f"s_lshl_b32 {T0}, {sr(S_WAVE)}, 5"),
+       I(f"v_add_u32 {vr(V_TMP + 4)}, {T0}, {vr(V_TMP + 3)}"),
+       I(f"v_lshlrev_b32 {vr(V_TMP + 4)}, 8, {vr(V_TMP + 4)}"),                    # row bytes
+       I(f"v_lshlrev_b32 {vr(V_TMP + 5)}, 2, {vr(V_TMP + 3)}"),
+       I(f"v_and_b32 {vr(V_TMP + 6)}, 15, {vr(V_LANE)}")])
+    for k in range(4):
+        e([I(f"v_add_u32 {vr(V_TMP + 7)}, {k}, {vr(V_TMP + 5)}"),
+           I(f"v_xor_b32 {vr(V_TMP + 7)}, {vr(V_TMP + 7)}, {vr(V_TMP + 6)}"),        # chunk
+           I(f"v_lshl_add_u32 {vr(xoff(k))}, {vr(V_TMP + 7)}, 4, {vr(V_TMP + 4)}")])
     # bias transfer (wave 0): lanes 0..31 -LSE rows 4 l .. (16 bytes each), lanes 32..63 the
     # -delta rows, rows * 4 bytes further on
     e([I(f"v_and_b32 {vr(V_TMP + 3)}, 31, {vr(V_LANE)}"),
@@ -358,8 +367,9 @@ def transfer_setup(hh_sgpr, qt_sgpr, stage, nrec_q, nrec_l) -> list:
             I(f"s_addc_u32 {sr(S_RL + 1)}, {arg('ld', True)}, 0"),
             I(f"s_and_b32 {sr(S_RL + 1)}, {sr(S_RL + 1)}, 0xffff"),
             I(f"s_mov_b32 {sr(S_RL + 3)}, 0x20000"),
-            I(f"s_lshl_b32 {sr(S_XB)}, {sr(S_WAVE)}, 10"),
+            I(f"s_lshl_b32 {sr(S_XB)}, {sr(S_WAVE)}, 13"),
             I(f"s_add_u32 {sr(S_XB)}, {sr(S_XB)}, {stage}"),
+            I(f"s_mov_b32 {sr(S_XSOFF)}, 0x1000"),
             I(f"s_add_u32 {sr(S_XBL)}, {stage}, {T_LD}"),
             # the biases: one instruction of wave 0; the other waves read no bytes
             I(f"s_mov_b32 {T0}, {DUMMY}"),
@@ -371,15 +381,19 @@ def transfer_setup(hh_sgpr, qt_sgpr, stage, nrec_q, nrec_l) -> list:
 
 def transfer_items() -> list:
     """The transfer instructions after transfer_setup, in groups that can be spread over a
-    tile's MFMAs: 8 Q and 8 dO instructions per wave (16 rows each: rows 4 w + 16 i + lane / 16,
-    the same per-lane offsets for both), then the biases."""
+    tile's MFMAs: 8 Q and 8 dO instructions per wave (4 rows each: rows 32 w + 4 i + lane / 16,
+    the same per-lane offsets for both; one M0 per four instructions), then the biases."""
     out = []
     for rs, region in ((S_RQ, 0), (S_RO, T_DO)):
         for i in range(8):
-            out.append([I(f"s_add_u32 m0, {sr(S_XB)}, {region + 4096 * i}", writes=["m0"],
-                          reads=[f"s{S_XB}"]),
-                        I(f"s_mov_b32 {sr(S_XSOFF)}, {4096 * i}"),
-                        I(f"buffer_load_dwordx4 {vr(V_XOFF)}, {sr(rs, 4)}, {sr(S_XSOFF)} offen lds")])
+            grp = []
+            if i % 4 == 0:
+                grp.append(I(f"s_add_u32 m0, {sr(S_XB)}, {region + 4096 * (i // 4)}",
+                             writes=["m0"], reads=[f"s{S_XB}"]))
+            soff = "0" if i < 4 else sr(S_XSOFF)
+            grp.append(I(f"buffer_load_dwordx4 {vr(xoff(i % 4))}, {sr(rs, 4)}, {soff} offen "
+                         f"offset:{1024 * (i % 4)} lds"))
+            out.append(grp)
     out.append([I(f"s_mov_b32 m0, {sr(S_XBL)}", writes=["m0"], reads=[f"s{S_XBL}"]),
                 I(f"buffer_load_dwordx4 {vr(V_LDOFF)}, {sr(S_RL, 4)}, 0 offen lds")])
     return out

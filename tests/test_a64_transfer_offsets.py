@@ -8,7 +8,9 @@ offset 1024 i, which moves the LDS and the global address alike; the per-lane of
 carry the rest. This test executes the generated per-lane code that computes VTOFF (the
 contiguous and the paged kernel, several row strides) lane by lane and checks, for every wave,
 instruction and lane, that the global bytes a load reads are the row and chunk its LDS slot must
-hold: tile row r (contiguous) or in-page row r - 16 wave of the wave's page (paged)."""
+hold: tile row r (contiguous) or in-page row r - 16 wave of the wave's page (paged). The same for
+the assembly backward's Q / dO transfers (gen_bwd_a64.py: 128-row tiles, instruction i of wave w
+at LDS KiB 8 w + i, M0 + 4 KiB and soffset 4096 for i >= 4)."""
 import importlib.util
 import os
 
@@ -18,9 +20,9 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 M32 = 0xFFFFFFFF
 
 
-def _gen():
+def _gen(name="gen_prefill_a64"):
     spec = importlib.util.spec_from_file_location(
-        "gen_a64_xfer", os.path.join(ROOT, "flat-attention_amd", "csrc", "gen_prefill_a64.py"))
+        f"{name}_xfer", os.path.join(ROOT, "flat-attention_amd", "csrc", f"{name}.py"))
     g = importlib.util.module_from_spec(spec)
     spec.loader.exec_module(g)
     return g
@@ -73,6 +75,8 @@ def _run(code, lane, sgpr):
             r = a[0] + a[1]
         elif op == "v_mul_lo_u32":
             r = a[0] * a[1]
+        elif op == "v_lshl_add_u32":
+            r = (a[0] << (a[1] & 31)) + a[2]
         elif op == "v_mov_b32":
             r = a[0]
         else:
@@ -107,3 +111,24 @@ def test_every_lane_reads_the_chunk_its_lds_slot_holds(paged, row_bytes):
                 assert (glob % row_bytes) // 16 == slot ^ _swz(r), (wave, lane, i, glob)
                 seen.add(lds)
     assert len(seen) == 1024  # the 16 KiB region exactly once
+
+
+def test_backward_lanes_read_the_chunks_their_lds_slots_hold():
+    g = _gen("gen_bwd_a64")
+    texts = [x.text.strip() for b in g.build().blocks for x in b.ins]
+    first = texts.index(f"v_lshrrev_b32 {g.vr(g.V_TMP + 3)}, 4, {g.vr(g.V_LANE)}")
+    last = max(i for i, t in enumerate(texts)
+               if t.startswith("v_") and t.split(" ", 1)[1].startswith(f"{g.vr(g.xoff(3))},"))
+    code = texts[first:last + 1]
+    seen = set()
+    for wave in range(4):
+        for lane in range(64):
+            v = _run(code, lane, {g.S_WAVE: wave})
+            for i in range(8):
+                glob = v[g.xoff(i % 4)] + 1024 * (i % 4) + 4096 * (i // 4)
+                lds = 8192 * wave + 1024 * i + 16 * lane
+                r, slot = lds // 256, (lds % 256) // 16
+                assert glob // 256 == r, (wave, lane, i, glob)
+                assert (glob % 256) // 16 == slot ^ _swz(r), (wave, lane, i, glob)
+                seen.add(lds)
+    assert len(seen) == 2048  # the 32 KiB Q (or dO) tile exactly once

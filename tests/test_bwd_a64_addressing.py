@@ -11,8 +11,9 @@ DMA, stored dS> uses (csrc/backward.hip; BackwardArgs in csrc/kernels.hpp):
     (causal: the tiles from the key block's diagonal on), each once;
   * K / V: rows (batch, kv head) * seq + k0 .. + 31, 8 KiB; dK / dV stores the same rows;
   * the transfer of every tile after the first is issued during the tile before it, into the
-    other LDS stage: Q and dO rows of (batch, group head) at the tile, 32 KiB, soffset and M0
-    4 KiB apart per instruction, 1 KiB per wave; the bias rows (-LSE / scale then -delta,
+    other LDS stage: Q and dO rows of (batch, group head) at the tile, 32 KiB, instruction i of
+    wave w landing at LDS KiB 8 w + i (M0 per four instructions, instruction offsets 1 KiB apart,
+    soffset 4 KiB for i >= 4); the bias rows (-LSE / scale then -delta,
     rows * 4 bytes further) by wave 0 into stage + 64 KiB, no bytes for waves 1..3;
   * the dS stores of every active 32-query sub-block at the group offset of
     ((b Hq + kvh G + hh) gph + base(t) + k0 / 32) * 8 KiB + 2 KiB * sub-block (base(t) =
@@ -129,7 +130,8 @@ class Scalar:
             elif op == "buffer_load_dwordx4" and rest.endswith(" lds"):
                 res = self.quad(o[1])
                 soff = self.val(o[2].split()[0])
-                self.events.append(("xfer", res, soff, self.m0, t))
+                off = int(rest.split("offset:")[1].split()[0]) if "offset:" in rest else 0
+                self.events.append(("xfer", res, soff, self.m0 + off, t))
             elif op == "buffer_load_dwordx4":
                 off = int(rest.split("offset:")[1]) if "offset:" in rest else 0
                 self.events.append(("load", self.quad(o[2]), off, None, t))
@@ -223,12 +225,13 @@ def test_every_access_matches_the_layout(B, Hq, Hkv, S, causal):
                 assert bq == b and kvh * G <= hq < kvh * G + G, (bid, w, j)
                 tiles.append((hq - kvh * G, qt))
                 for i in range(8):
-                    _, (base, n), soff, m0, t = grp[i]
-                    assert (base, n, soff) == (qbase, 128 * RB, 4096 * i), t
-                    assert m0 == stage + 1024 * w + 4096 * i, t
-                    _, (base, n), soff, m0, t = grp[8 + i]
-                    assert (base, n, soff) == (BASE["dout"] + row0 * RB, 128 * RB, 4096 * i), t
-                    assert m0 == stage + g.T_DO + 1024 * w + 4096 * i, t
+                    _, (base, n), soff, lds, t = grp[i]
+                    assert (base, n, soff) == (qbase, 128 * RB, 4096 * (i // 4)), t
+                    assert lds == stage + 8192 * w + 1024 * i, t
+                    _, (base, n), soff, lds, t = grp[8 + i]
+                    assert (base, n, soff) == (BASE["dout"] + row0 * RB, 128 * RB,
+                                               4096 * (i // 4)), t
+                    assert lds == stage + g.T_DO + 8192 * w + 1024 * i, t
                 _, (base, n), soff, m0, t = grp[16]
                 assert base == BASE["ld"] + 4 * row0 and soff == 0, t
                 if w == 0:
