@@ -419,8 +419,8 @@ def measure_baseline_configs(ctx, ev, rng, steps, with_cpu, warm=100):
     op_ms, k_ms, tel = timed(run)
     res["backward_causal_gqa_B2_Hq32_Hkv8_N4096_D128_bf16"] = _rec(
         tel.kernel_name, op_ms, k_ms, flop, "mfma", PEAK_BF16_TFLOPS, "TFLOP/s",
-        note="algorithmic FLOPs = 2.5x forward (five S x S x D products); kernel_ms is the "
-             "dK/dV kernel, the op has three launches", cpu_baseline=cpu.get("backward"))
+        note="algorithmic FLOPs = 2.5x forward (five S x S x D products); kernel_ms spans the "
+             "op's three launches (bwd_delta, the dK/dV kernel, bwd_dq_ds)", cpu_baseline=cpu.get("backward"))
     return res
 
 
