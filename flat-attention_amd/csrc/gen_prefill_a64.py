@@ -613,14 +613,15 @@ def exact_path(gen: "Gen", x: int, hh: int, s_x, recompute: bool = True) -> None
     (alpha = exp2(m_old - m_new)), rescale O and l, re-bias the scores SB[s_x] that this phase's
     MFMAs accumulated onto the old bias, set the bias blocks, and redo P^T and the row sums.
     recompute=False (the prologue): SB[x] already holds the raw scores (the bias blocks are
-    still zero), and the V operands the last phase prefetched stay in flight."""
+    still zero), the V operands the last phase prefetched stay in flight, and O and l are still
+    zero, so they are not rescaled."""
     e = gen.emit
     if recompute:
         gen.ds_wait_all()
         e(I("s_waitcnt lgkmcnt(0)"))
         _recompute_scores(gen, x, hh)
     e(mask_program(x))
-    _exact_softmax(gen, x, s_x)
+    _exact_softmax(gen, x, s_x, rescale=recompute)
 
 
 def _recompute_scores(gen: "Gen", x: int, hh: int) -> None:
@@ -651,8 +652,9 @@ def _recompute_scores(gen: "Gen", x: int, hh: int) -> None:
                     e(ins)
 
 
-def _exact_softmax(gen: "Gen", x: int, s_x) -> None:
-    """Row maxima of the masked raw scores in SB[x], the move of m, rescale, re-bias, redo P."""
+def _exact_softmax(gen: "Gen", x: int, s_x, rescale: bool = True) -> None:
+    """Row maxima of the masked raw scores in SB[x], the move of m, rescale (when O and l may be
+    non-zero), re-bias, redo P."""
     e = gen.emit
     S = SB[x]
     for rb in range(2):
@@ -681,7 +683,7 @@ def _exact_softmax(gen: "Gen", x: int, s_x) -> None:
            I(f"v_sub_f32 {vr(al)}, {vr(m)}, {vr(mt)}"),
            I(f"v_exp_f32 {vr(al)}, {vr(al)}"),                      # m_old = -inf: 0
            I(f"v_mov_b32 {vr(m)}, {vr(mt)}"),
-           I(f"v_mul_f32 {vr(V_L + rb)}, {vr(V_L + rb)}, {vr(al)}"),
+           *([I(f"v_mul_f32 {vr(V_L + rb)}, {vr(V_L + rb)}, {vr(al)}")] if rescale else []),
            I(f"v_xor_b32 {vr(nbv)}, 0x80000000, {vr(mt)}"),        # new bias -m_new
            I(f"v_sub_f32 {vr(V_U + rb)}, {vr(nbv)}, {vr(NB + 16 * rb)}")])  # bias change
     if s_x is not None:
@@ -690,7 +692,8 @@ def _exact_softmax(gen: "Gen", x: int, s_x) -> None:
             e([I(f"v_add_f32 {vr(r + i)}, {vr(r + i)}, {vr(V_U + rb)}") for i in range(16)])
     for rb in range(2):
         e([I(f"v_mov_b32 {vr(NB + 16 * rb + i)}, {vr(V_NBV + rb)}") for i in range(16)])
-    e(rescale_block())
+    if rescale:
+        e(rescale_block())
     for rb in range(2):
         r = S + 16 * rb
         e([I(f"v_add_f32 {vr(r + i)}, {vr(r + i)}, {vr(V_NBV + rb)}") for i in range(16)])
