@@ -607,21 +607,17 @@ def rescale_block() -> list[Ins]:
     return out
 
 
-def exact_path(gen: "Gen", x: int, hh: int, s_x, recompute: bool = True) -> None:
+def exact_path(gen: "Gen", x: int, hh: int, s_x) -> None:
     """Exact softmax of the half-tile whose scores belong in SB[x] (K half hh of the stage before
     the current K read stage): recompute the raw scores S * c2, mask, take the row maxima, move m
     (alpha = exp2(m_old - m_new)), rescale O and l, re-bias the scores SB[s_x] that this phase's
-    MFMAs accumulated onto the old bias, set the bias blocks, and redo P^T and the row sums.
-    recompute=False (the prologue): SB[x] already holds the raw scores (the bias blocks are
-    still zero), the V operands the last phase prefetched stay in flight, and O and l are still
-    zero, so they are not rescaled."""
+    MFMAs accumulated onto the old bias, set the bias blocks, and redo P^T and the row sums."""
     e = gen.emit
-    if recompute:
-        gen.ds_wait_all()
-        e(I("s_waitcnt lgkmcnt(0)"))
-        _recompute_scores(gen, x, hh)
+    gen.ds_wait_all()
+    e(I("s_waitcnt lgkmcnt(0)"))
+    _recompute_scores(gen, x, hh)
     e(mask_program(x))
-    _exact_softmax(gen, x, s_x, rescale=recompute)
+    _exact_softmax(gen, x, s_x)
 
 
 def _recompute_scores(gen: "Gen", x: int, hh: int) -> None:
@@ -652,9 +648,9 @@ def _recompute_scores(gen: "Gen", x: int, hh: int) -> None:
                     e(ins)
 
 
-def _exact_softmax(gen: "Gen", x: int, s_x, rescale: bool = True) -> None:
-    """Row maxima of the masked raw scores in SB[x], the move of m, rescale (when O and l may be
-    non-zero), re-bias, redo P."""
+def _row_max(gen: "Gen", x: int):
+    """Both 32-row blocks' maxima of the masked raw scores in SB[x], on every lane: returns the
+    registers holding block 0's and block 1's."""
     e = gen.emit
     S = SB[x]
     for rb in range(2):
@@ -677,13 +673,35 @@ def _exact_softmax(gen: "Gen", x: int, s_x, rescale: bool = True) -> None:
        I(f"v_max_f32 {vr(F)}, {vr(mx0)}, {vr(mx1)}"),
        I(f"v_mov_b32 {vr(G)}, {vr(F)}"),
        I(f"v_permlane32_swap_b32 {vr(F)}, {vr(G)}")])
+    return F, G
+
+
+def first_max(gen: "Gen", x: int) -> None:
+    """The block's first half-tile (raw scores in SB[x], masked): m = its row maxima, the bias
+    blocks -m for the next scores, SB[x] biased to S' = S * c2 - m. O and l are still zero."""
+    e = gen.emit
+    F, G = _row_max(gen, x)
+    for rb, mt in ((0, F), (1, G)):
+        e([I(f"v_mov_b32 {vr(V_M + rb)}, {vr(mt)}"),
+           I(f"v_xor_b32 {vr(V_NBV + rb)}, 0x80000000, {vr(mt)}")])
+    for rb in range(2):
+        e([I(f"v_mov_b32 {vr(NB + 16 * rb + i)}, {vr(V_NBV + rb)}") for i in range(16)])
+        r = SB[x] + 16 * rb
+        e([I(f"v_add_f32 {vr(r + i)}, {vr(r + i)}, {vr(V_NBV + rb)}") for i in range(16)])
+
+
+def _exact_softmax(gen: "Gen", x: int, s_x) -> None:
+    """Row maxima of the masked raw scores in SB[x], the move of m, rescale, re-bias, redo P."""
+    e = gen.emit
+    S = SB[x]
+    F, G = _row_max(gen, x)
     for rb, mt in ((0, F), (1, G)):
         m, al, nbv = V_M + rb, V_ALPHA + rb, V_NBV + rb
         e([I(f"v_max_f32 {vr(mt)}, {vr(mt)}, {vr(m)}"),            # m_new (finite)
            I(f"v_sub_f32 {vr(al)}, {vr(m)}, {vr(mt)}"),
            I(f"v_exp_f32 {vr(al)}, {vr(al)}"),                      # m_old = -inf: 0
            I(f"v_mov_b32 {vr(m)}, {vr(mt)}"),
-           *([I(f"v_mul_f32 {vr(V_L + rb)}, {vr(V_L + rb)}, {vr(al)}")] if rescale else []),
+           I(f"v_mul_f32 {vr(V_L + rb)}, {vr(V_L + rb)}, {vr(al)}"),
            I(f"v_xor_b32 {vr(nbv)}, 0x80000000, {vr(mt)}"),        # new bias -m_new
            I(f"v_sub_f32 {vr(V_U + rb)}, {vr(nbv)}, {vr(NB + 16 * rb)}")])  # bias change
     if s_x is not None:
@@ -692,8 +710,7 @@ def _exact_softmax(gen: "Gen", x: int, s_x, rescale: bool = True) -> None:
             e([I(f"v_add_f32 {vr(r + i)}, {vr(r + i)}, {vr(V_U + rb)}") for i in range(16)])
     for rb in range(2):
         e([I(f"v_mov_b32 {vr(NB + 16 * rb + i)}, {vr(V_NBV + rb)}") for i in range(16)])
-    if rescale:
-        e(rescale_block())
+    e(rescale_block())
     for rb in range(2):
         r = S + 16 * rb
         e([I(f"v_add_f32 {vr(r + i)}, {vr(r + i)}, {vr(V_NBV + rb)}") for i in range(16)])
@@ -702,11 +719,13 @@ def _exact_softmax(gen: "Gen", x: int, s_x, rescale: bool = True) -> None:
 
 # ---- one pipeline phase ------------------------------------------------------------------------
 def phase(gen: Gen, *, pv_x, pv_hh, s_x, s_hh, sm_x, sm_masked, pre=(),
-          prefetch_v_hh=None, after_last_v=(), after_last_k=(), vring_state=None, spread=()):
+          prefetch_v_hh=None, after_last_v=(), after_last_k=(), vring_state=None, spread=(),
+          zero_bias=False):
     """Emits one phase: MFMAs of P.V (P in PB[pv_x], V half pv_hh of the current V stage) then
     S (into SB[s_x], K half s_hh), with the softmax of SB[sm_x] spread between them.
     spread: instruction groups (the tile transfers) issued one every few MFMAs from the third
     on, so that the memory pipeline takes them one at a time instead of in a burst.
+    zero_bias: the scores' first k-step accumulates onto 0 instead of the bias blocks.
     vring_state: dict carrying the V operands already read into the ring by the previous phase:
     {'ready': {op_index: (slot, [ds ids])}}, and after the phase the prefetched operands of the
     next phase. Returns the new ring state."""
@@ -818,7 +837,7 @@ def phase(gen: Gen, *, pv_x, pv_hh, s_x, s_hh, sm_x, sm_masked, pre=(),
             slot = idx % DK
             # k-step 0 accumulates onto the bias block (-m of the lane's row)
             first = idx == 0 and part == 0
-            src_c = vr(NB + 16 * rb, 16) if first else s_acc(s_x, rb)
+            src_c = ("0" if zero_bias else vr(NB + 16 * rb, 16)) if first else s_acc(s_x, rb)
             ins = I(f"v_mfma_f32_32x32x16_bf16 {s_acc(s_x, rb)}, {vr(ring + 4 * slot, 4)}, "
                     f"{qf(rb, idx)}, {src_c}")
             ins.srcc_chain = not first
@@ -1404,7 +1423,7 @@ def setup_block(gen: Gen):
             e(I(f"v_accvgpr_write_b32 {ar(A_Q + rb * 32 + w)}, {vr(qt[rb] + w)}"))
     # ---- O = 0 (eight MFMAs of zero operands write the 128 accumulators: 8 instructions
     # instead of 128 AGPR writes), running statistics
-    e([I(f"v_mov_b32 {vr(NB + i)}, 0") for i in range(32)])
+    e([I(f"v_mov_b32 {vr(NB + i)}, 0") for i in range(4)])
     for blk in range(8):
         e(I(f"v_mfma_f32_32x32x16_bf16 {ar(A_O + 16 * blk, 16)}, {vr(NB, 4)}, {vr(NB, 4)}, 0"))
     for rb in range(2):
@@ -1514,16 +1533,26 @@ def build() -> Gen:
     setup(gen)
     b_block = gen.new_block("setup_block", [b_setup])
     setup_block(gen)
-    # ---- prologue: S(0) alone, then S(1) with the exact softmax of half-tile 0 (sets m)
+    # ---- prologue: S(0) alone (onto 0); its mask (only when tile 0 is not visible to every
+    # row of the block) and row maxima set m and the bias blocks; then S(1) onto the bias with
+    # the softmax of half-tile 0 spread over its MFMAs (no overflow: S' <= 0)
     gen.new_block("prologue", [b_block])
     gen.ds_outstanding = []
-    phase(gen, pv_x=None, pv_hh=0, s_x=0, s_hh=0, sm_x=None, sm_masked=False)
+    phase(gen, pv_x=None, pv_hh=0, s_x=0, s_hh=0, sm_x=None, sm_masked=False, zero_bias=True)
     gen.ds_wait_all()
-    gen.emit(I(f"s_mov_b32 {sr(S_KEY0)}, 0"))
-    phase(gen, pv_x=None, pv_hh=0, s_x=1, s_hh=1, sm_x=None, sm_masked=False, prefetch_v_hh=0,
+    gen.emit([I(f"s_mov_b32 {sr(S_KEY0)}, 0"),
+              I(f"s_cmp_lg_u32 {sr(S_NFULL)}, 0"),
+              I("s_cbranch_scc1 .Lpro_max")])
+    br = gen.cur
+    gen.new_block("pro_mask", [br])
+    gen.emit(mask_program(0))
+    mk = gen.cur
+    gen.new_block("pro_max", [br, mk])
+    gen.emit(I(".Lpro_max:"))
+    first_max(gen, 0)
+    phase(gen, pv_x=None, pv_hh=0, s_x=1, s_hh=1, sm_x=0, sm_masked=False, prefetch_v_hh=0,
           after_last_k=advance_slot(S_KSLOT, VKA, 8))
-    exact_path(gen, 0, 0, 1, recompute=False)
-    gen.emit([I(f"v_add_f32 {vr(V_L + rb)}, {vr(V_L + rb)}, {vr(V_LT + rb)}") for rb in range(2)])
+    gen.emit([I(f"v_mov_b32 {vr(V_L + rb)}, {vr(V_LT + rb)}") for rb in range(2)])
     pro_end = gen.cur
     if PAIR:
         epi_preds = pair_loops(gen, pro_end)
