@@ -77,7 +77,6 @@ ARGS = [
 ]
 ARG_BYTES = 208
 S_QNREC, S_ONREC, S_LNREC = 52, 53, 56  # (argument registers of q_nrec, o_nrec, lse_nrec)
-S_SPARE = 54          # [54:55]: argument bytes 184..191 (the paged kernel's block tables)
 S_ROUND = 3           # persistent loop: blocks this workgroup has finished
 ARG_SGPR0 = 8  # argument dword i lives in s[8 + i]
 
@@ -148,7 +147,6 @@ V_LIM = 158
 V_MX = 160            # 4 temps for the cross-lane max
 V_U = 164             # 2 temps
 V_NINF = 166
-V_ONES = 167          # packed bf16 (1, 1)
 V_TMP = 168           # 8 temps (rescale)
 V_QOFF = 176          # Q byte offsets per rb (2)
 V_CSOFF = 178         # (cos, sin) row byte offsets per rb (2)
@@ -200,8 +198,6 @@ S_KSLOT = 100
 S_VSLOT = 101
 S_RQ = 4              # [4:7] Q / O / LSE resource (reused)
 NUM_SGPR = 102
-
-RB_ROWS = 32
 
 
 def vr(base: int, n: int = 1) -> str:
@@ -1034,7 +1030,6 @@ def setup(gen: Gen):
     e(I(f"s_lshr_b32 {sr(S_WAVE)}, {sr(S_WAVE)}, 6"))
     T0, T1, T2, T3 = (sr(S_T0), sr(S_T1), sr(S_T2), sr(S_T3))
     e([I(f"v_mov_b32 {vr(V_NINF)}, 0xff800000"),
-       I(f"v_mov_b32 {vr(V_ONES)}, 0x3f803f80"),
        I(f"v_mov_b32 {vr(V_BIG)}, 0x5f800000"),
        I(f"s_mov_b32 {sr(S_HIMASK)}, 0"),
        I(f"s_mov_b32 {sr(S_HIMASK + 1)}, -1"),
