@@ -310,6 +310,37 @@ def test_chunked_prefill_is_chunk_invariant_and_matches_oracle(hip):
     assert e.value.variant == "ZeroQueryChunkSize"
 
 
+def test_chunked_prefill_precise_scores_bf16(hip):
+    """Chunked prefill (causal offset = the chunk's start) in the precise-score mode at the
+    assembly kernel's shape (bf16, D 128, GQA group 4): chunk sizes 64 and the whole sequence
+    agree within the 16-bit bar, and match the oracle's chunked prefill."""
+    B, hq, hkv, S, D, theta, off = 1, 8, 2, 300, 128, 1e4, 3
+    q = bf16_round(normal(B * S * hq * D, 21))
+    k, v = bf16_round(normal(B * S * hkv * D, 22)), bf16_round(normal(B * S * hkv * D, 23))
+    shape = fa.GroupedAttentionShape(B, hq, hkv, S, D)
+    rot = fa.RotaryEmbeddingConfig(theta, off)
+    pipe = fa.HipChunkedProjectionPrefillPipeline(hip, fa.DTYPE_BF16)
+    qb, kb, vb = (fa.DeviceBuffer.from_array(hip, fa.host_storage(x, fa.DTYPE_BF16))
+                  for x in (q, k, v))
+    outs, names = [], []
+    hip.set_prefill_precision(1)
+    try:
+        for chunk in (64, S):
+            out = pipe.create_output_buffer(shape)
+            pipe.encode(qb, kb, vb, out, shape, fa.FlatAttentionConfig(True), rot, chunk)
+            names.append(hip.last_telemetry().kernel_name)
+            outs.append(fa.download_attention(out, pipe.layout(shape), fa.DTYPE_BF16))
+    finally:
+        hip.set_prefill_precision(0)
+    assert all("split" in n for n in names), names
+    eo, el = oracle.chunked_prefill(q, k, v, B, hq, hkv, S, D, True, theta, off, 3)
+    os_ = [fa.storage_to_f32(r.output, fa.DTYPE_BF16) for r in outs]
+    for o, r in zip(os_, outs):
+        assert_close("O", o, eo, H16_ATOL, 0.0)
+        assert_close("LSE", r.lse, el, H16_ATOL, 0.0)
+    assert_close("O chunk 64 vs whole", os_[0], os_[1], H16_ATOL, 0.0)
+
+
 def test_host_forward_rejects_non_finite_and_bad_lengths(hip):
     ex = fa.HipFlatAttention(hip, fa.DTYPE_F32)
     shape = fa.AttentionShape(1, 1, 4, 8)
