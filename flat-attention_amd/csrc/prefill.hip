@@ -895,17 +895,19 @@ __global__ __launch_bounds__(64 * NW, SPLIT ? 1 : 2) void prefill_mfma16(Prefill
 // per 16-byte LDS read without bank conflicts. Otherwise tiles are staged through registers
 // (paged pools, K rotated on load, other head dims), K rows at an odd stride.
 template <int DPAD, bool PAGED, bool DMA = false>
-__global__ __launch_bounds__(256, 1) void prefill_mfma_f32(PrefillKArgs ka) {
+__global__ __launch_bounds__(256, DMA ? 2 : 1) void prefill_mfma_f32(PrefillKArgs ka) {
     static_assert(!(DMA && PAGED), "transfers need contiguous K/V");
     const PrefillArgs& a = ka.a;
-    constexpr int BM = 128, BN = 64;
+    // transfer path: 32-key tiles, so that two workgroups (two waves per SIMD) share a CU
+    constexpr int BM = 128, BN = DMA ? 32 : 64, KB = BN / 32;
     constexpr int HALFD = DPAD / 2;
     constexpr int MB = DPAD / 32;
     constexpr int KSTR = DMA ? DPAD + 4 : DPAD + 1;  // floats per K row in LDS
     constexpr int VSTR = DPAD;
-    constexpr int STAGE = BN * KSTR * 4 + BN * VSTR * 4;  // bytes; a whole number of KiB
+    constexpr int KREG = (BN * KSTR * 4 + 1023) / 1024 * 1024;  // K rows, whole KiB
+    constexpr int STAGE = KREG + BN * VSTR * 4;  // bytes; a whole number of KiB
     constexpr int KSL = KSTR / 4, VSL = VSTR / 4, CPR = DPAD / 4;  // 16-byte slots per row
-    constexpr int KINS = BN * KSL / 64, VINS = BN * VSL / 64;     // transfers per tile
+    constexpr int KINS = (BN * KSL + 63) / 64, VINS = BN * VSL / 64;  // transfers per tile
     constexpr int KI = (KINS + 3) / 4, VI = (VINS + 3) / 4;        // per wave
     constexpr int DUMMY = 2 * STAGE;
     constexpr bool NEED_DUMMY = DMA && (KINS % 4 != 0 || VINS % 4 != 0);
@@ -913,7 +915,7 @@ __global__ __launch_bounds__(256, 1) void prefill_mfma_f32(PrefillKArgs ka) {
     __shared__ __attribute__((aligned(16)))
     uint8_t smem[DMA ? 2 * STAGE + (NEED_DUMMY ? 1024 : 0) : STAGE];
     float* const k_lds = (float*)smem;
-    float* const v_lds = (float*)(smem + BN * KSTR * 4);
+    float* const v_lds = (float*)(smem + KREG);
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 5;
     const int D = a.head_dim, half = D >> 1;
@@ -987,7 +989,8 @@ __global__ __launch_bounds__(256, 1) void prefill_mfma_f32(PrefillKArgs ka) {
 #pragma unroll
         for (int i = 0; i < KI; ++i) {
             const int k = wave + 4 * i, q = 64 * k + lane, r = q / KSL, c = q % KSL;
-            koff[i] = (k < KINS && c < CPR && c * 4 < D) ? (uint32_t)r * row_bytes + (uint32_t)c * 16u
+            koff[i] = (k < KINS && r < BN && c < CPR && c * 4 < D)
+                          ? (uint32_t)r * row_bytes + (uint32_t)c * 16u
                                                           : kOob;
         }
 #pragma unroll
@@ -1015,7 +1018,7 @@ __global__ __launch_bounds__(256, 1) void prefill_mfma_f32(PrefillKArgs ka) {
             const int k = wave + 4 * i;
             buffer_to_lds16(rv,
                             __builtin_amdgcn_readfirstlane(
-                                lds0 + (k < VINS ? st + BN * KSTR * 4 + k * 1024 : DUMMY)),
+                                lds0 + (k < VINS ? st + KREG + k * 1024 : DUMMY)),
                             voff[i]);
         }
     };
@@ -1041,7 +1044,7 @@ __global__ __launch_bounds__(256, 1) void prefill_mfma_f32(PrefillKArgs ka) {
             const int st = (tile & 1) * STAGE;
             if (tile + 1 < n_tiles) dma_tile(tile + 1, STAGE - st);
             kst = (const float*)(smem + st);
-            vst = (const float*)(smem + st + BN * KSTR * 4);
+            vst = (const float*)(smem + st + KREG);
         } else {
         // ---- stage K (rotated) and V
 #pragma unroll
@@ -1087,16 +1090,16 @@ __global__ __launch_bounds__(256, 1) void prefill_mfma_f32(PrefillKArgs ka) {
         __syncthreads();
         }
 
-        f32x16_t sacc[2];
+        f32x16_t sacc[KB];
         if constexpr (DMA) {
-            // four K operands per 16-byte read; the two key blocks' chains alternate
-            sacc[0] = (f32x16_t)0.0f;
-            sacc[1] = (f32x16_t)0.0f;
+            // four K operands per 16-byte read; the key blocks' chains alternate
+#pragma unroll
+            for (int kb = 0; kb < KB; ++kb) sacc[kb] = (f32x16_t)0.0f;
             const float* kr0 = kst + (lane & 31) * KSTR + g * HALFD;
 #pragma unroll
             for (int j = 0; j < HALFD / 4; ++j)
 #pragma unroll
-                for (int kb = 0; kb < 2; ++kb) {
+                for (int kb = 0; kb < KB; ++kb) {
                     const f32x4_t k4 = *(const f32x4_t*)(kr0 + kb * 32 * KSTR + 4 * j);
 #pragma unroll
                     for (int e = 0; e < 4; ++e)
@@ -1105,7 +1108,7 @@ __global__ __launch_bounds__(256, 1) void prefill_mfma_f32(PrefillKArgs ka) {
                 }
         } else {
 #pragma unroll
-            for (int kb = 0; kb < 2; ++kb) {
+            for (int kb = 0; kb < KB; ++kb) {
                 sacc[kb] = (f32x16_t)0.0f;
                 const float* kr = kst + (kb * 32 + (lane & 31)) * KSTR + g * HALFD;
 #pragma unroll
@@ -1118,7 +1121,7 @@ __global__ __launch_bounds__(256, 1) void prefill_mfma_f32(PrefillKArgs ka) {
         if (tile_end > kv_len_ || (a.causal && tile_end - 1 > cpos_min)) {
             const int lim = a.causal ? min(kv_len_ - 1, cpos) : kv_len_ - 1;
 #pragma unroll
-            for (int kb = 0; kb < 2; ++kb)
+            for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
                 for (int i = 0; i < 16; ++i) {
                     const int key = tile * BN + 32 * kb + 8 * (i >> 2) + 4 * g + (i & 3);
@@ -1128,9 +1131,9 @@ __global__ __launch_bounds__(256, 1) void prefill_mfma_f32(PrefillKArgs ka) {
 
         float mt = sacc[0][0];
 #pragma unroll
-        for (int i = 1; i < 16; ++i) mt = fmaxf(mt, sacc[0][i]);
+        for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) mt = fmaxf(mt, sacc[1][i]);
+            for (int i = 0; i < 16; ++i) mt = fmaxf(mt, sacc[kb][i]);
         mt = fmaxf(mt, shfl_xor(mt, 32));
         {
             const bool need = mt * c2 > m_run * c2 + kRescaleLog2;
@@ -1146,7 +1149,7 @@ __global__ __launch_bounds__(256, 1) void prefill_mfma_f32(PrefillKArgs ka) {
         const float neg = -m_run * c2;
         float lsum = 0.0f;
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
+        for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
                 const float p = fast_exp2(fmaf(sacc[kb][i], c2, neg));
@@ -1159,7 +1162,7 @@ __global__ __launch_bounds__(256, 1) void prefill_mfma_f32(PrefillKArgs ka) {
         for (int mb = 0; mb < MB; ++mb) {
             const float* vc = vst + mb * 32 + (lane & 31);
 #pragma unroll
-            for (int kb = 0; kb < 2; ++kb)
+            for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
                 for (int i = 0; i < 16; ++i) {
                     const int kl = 32 * kb + 8 * (i >> 2) + 4 * g + (i & 3);
