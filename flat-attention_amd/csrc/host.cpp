@@ -311,6 +311,21 @@ void begin_span(fa_ctx* ctx) {
     ctx->open_begin = e;
 }
 
+// The span of a dispatch that records its own start and stop events (hipExtModuleLaunchKernel):
+// false while timing is off or without events, and then the caller brackets it with
+// begin_span / end_span.
+bool dispatch_events(fa_ctx* ctx, hipEvent_t* start, hipEvent_t* stop) {
+    *start = *stop = nullptr;
+    if (!ctx->timing || ctx->timing_paused || ctx->capturing) return false;
+    *start = take_event(ctx);
+    *stop = take_event(ctx);
+    if (*start && *stop) return true;
+    if (*start) ctx->free_events.push_back(*start);
+    if (*stop) ctx->free_events.push_back(*stop);
+    *start = *stop = nullptr;
+    return false;
+}
+
 void end_span(fa_ctx* ctx, int kernel_id) {
     if (!ctx->timing || ctx->timing_paused || ctx->capturing || !ctx->open_begin) return;
     hipEvent_t e = take_event(ctx);
@@ -1039,9 +1054,15 @@ int enqueue_prefill(fa_ctx* ctx, const PrefillRun& r) {
     unsigned grid[3], block = 0;
     // K read already rotated (pre-pass, or a paged cache that stores K rotated on append)
     const int kid = prefill_kernel_id(j.dtype, r.prerot || (j.paged && j.rope));
-    begin_span(ctx);
+    // the assembly kernel records its span's events as part of its dispatch
+    const bool own = fa::prefill_a64_eligible(j.dt, j.paged, a) &&
+                     dispatch_events(ctx, &a.ev_start, &a.ev_stop);
+    if (!own) begin_span(ctx);
     fa::launch_prefill(j.dt, j.paged, a, ctx->stream, grid, &block);
-    end_span(ctx, kid);
+    if (own)
+        ctx->pending.push_back({kid, a.ev_start, a.ev_stop});
+    else
+        end_span(ctx, kid);
     HIP_TRY(hipGetLastError());
     dispatches++;
     describe_prefill(ctx, j, a, r.prerot, dispatches, ctx->call_allocs,
