@@ -19,6 +19,8 @@
 // A unit covered by one segment is finalised directly by the split kernel.
 #include <type_traits>
 
+#include <hip/hip_ext.h>
+
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -752,7 +754,12 @@ static void launch_one(const DecodeKArgs& ka, int chunks, hipStream_t s, unsigne
                 return;
             }
             *grid_x = (unsigned)ka.a.n_waves;
-            decode_mfma_grouped<T, DPAD, GT><<<ka.a.n_waves, threads, 0, s>>>(ka, chunks);
+            if (ka.a.ev_start && ka.a.ev_stop)
+                hipExtLaunchKernelGGL(decode_mfma_grouped<T, DPAD, GT>, dim3(ka.a.n_waves),
+                                      dim3(threads), 0, s, ka.a.ev_start, ka.a.ev_stop, 0, ka,
+                                      chunks);
+            else
+                decode_mfma_grouped<T, DPAD, GT><<<ka.a.n_waves, threads, 0, s>>>(ka, chunks);
             return;
         }
         if (ka.a.page_size % 16 == 0) {

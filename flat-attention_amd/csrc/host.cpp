@@ -851,13 +851,20 @@ const char* kernel_name(int id) {
     }
 }
 
-// Closes the split kernel's timing span and opens the combine's, between the two launches.
+// Closes the split kernel's timing span and opens the combine's, between the two launches
+// (own: the split kernel recorded its span's events in its dispatch, which are filed here).
 struct DecodeMarks {
     fa_ctx* ctx;
     const bool* mfma;
+    bool own = false;
+    hipEvent_t start = nullptr, stop = nullptr;
     static void between(void* user) {
         auto* m = static_cast<DecodeMarks*>(user);
-        end_span(m->ctx, *m->mfma ? FA_KERNEL_DECODE_PAGED_MFMA : FA_KERNEL_DECODE_PAGED_SPLITK);
+        const int kid = *m->mfma ? FA_KERNEL_DECODE_PAGED_MFMA : FA_KERNEL_DECODE_PAGED_SPLITK;
+        if (m->own)
+            m->ctx->pending.push_back({kid, m->start, m->stop});
+        else
+            end_span(m->ctx, kid);
         begin_span(m->ctx);
     }
 };
@@ -2339,7 +2346,15 @@ int enqueue_decode(fa_ctx* ctx, const fa_decode_plan* p, const float2* table, co
     int dispatches = 0;
     bool mfma = false;
     DecodeMarks marks{ctx, &mfma};
-    begin_span(ctx);
+    // the head-grouped split kernel records its span's events as part of its dispatch
+    if (p->dtype != FA_DTYPE_F32 && p->page_size % 16 == 0 && p->grouped > 0 &&
+        dispatch_events(ctx, &a.ev_start, &a.ev_stop)) {
+        marks.own = true;
+        marks.start = a.ev_start;
+        marks.stop = a.ev_stop;
+    } else {
+        begin_span(ctx);
+    }
     fa::launch_decode((Dtype)p->dtype, a, ctx->stream, grid, &block, &dispatches, &mfma,
                       &DecodeMarks::between, &marks);
     end_span(ctx, FA_KERNEL_DECODE_COMBINE);

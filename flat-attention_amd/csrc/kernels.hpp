@@ -99,6 +99,9 @@ struct DecodeArgs {
     // > 0: head-grouped MFMA split kernel, workgroups of `grouped` waves (one per unit) sharing
     // one segment list; seg[1] is then the partial-slot stride between units.
     int grouped;
+    // Timing events the head-grouped split kernel records as part of its own dispatch (null:
+    // none), so that a span brackets that kernel alone.
+    hipEvent_t ev_start, ev_stop;
 };
 
 // Number of workgroups of the split kernel that launch_decode keeps resident at once for this
