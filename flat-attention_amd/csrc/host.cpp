@@ -1061,8 +1061,9 @@ int enqueue_prefill(fa_ctx* ctx, const PrefillRun& r) {
     unsigned grid[3], block = 0;
     // K read already rotated (pre-pass, or a paged cache that stores K rotated on append)
     const int kid = prefill_kernel_id(j.dtype, r.prerot || (j.paged && j.rope));
-    // the assembly kernel records its span's events as part of its dispatch
-    const bool own = fa::prefill_a64_eligible(j.dt, j.paged, a) &&
+    // the assembly and the f32 kernel (one dispatch each) record their span's events as part of
+    // their dispatch
+    const bool own = (j.dtype == FA_DTYPE_F32 || fa::prefill_a64_eligible(j.dt, j.paged, a)) &&
                      dispatch_events(ctx, &a.ev_start, &a.ev_stop);
     if (!own) begin_span(ctx);
     fa::launch_prefill(j.dt, j.paged, a, ctx->stream, grid, &block);

@@ -51,8 +51,9 @@ struct PrefillArgs {
     // Precise scores in the assembly kernel (contiguous K/V, K rotated by the pre-pass): the
     // bf16 residual of the rotated K, laid out like `k` (launch_rotate_rows_split); null: off.
     const void* k_lo;
-    // Timing events the assembly launch records as part of its own dispatch (null: none), so
-    // that a span brackets the kernel alone, as a profiler's dispatch timestamps do.
+    // Timing events the launch records as part of its own dispatch (the assembly kernel and the
+    // f32 kernel; null: none), so that a span brackets the kernel alone, as a profiler's dispatch
+    // timestamps do.
     hipEvent_t ev_start, ev_stop;
 };
 

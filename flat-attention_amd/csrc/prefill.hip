@@ -22,6 +22,8 @@
 // operand of the second MFMA needs.
 #include <type_traits>
 
+#include <hip/hip_ext.h>
+
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -1236,12 +1238,21 @@ static void launch16(const PrefillKArgs& ka, bool paged, int dpad, dim3 grid, hi
     }
 }
 
+// One launch of `kernel`; with the arguments' timing events set, the dispatch records them.
+template <typename K>
+static void launch_timed(K kernel, dim3 grid, dim3 block, hipStream_t s, const PrefillKArgs& ka) {
+    if (ka.a.ev_start && ka.a.ev_stop)
+        hipExtLaunchKernelGGL(kernel, grid, block, 0, s, ka.a.ev_start, ka.a.ev_stop, 0, ka);
+    else
+        hipLaunchKernelGGL(kernel, grid, block, 0, s, ka);
+}
+
 template <bool PAGED, bool DMA = false>
 static void launch32(const PrefillKArgs& ka, int dpad, dim3 grid, hipStream_t s) {
     switch (dpad) {
-        case 32: prefill_mfma_f32<32, PAGED, DMA><<<grid, 256, 0, s>>>(ka); break;
-        case 64: prefill_mfma_f32<64, PAGED, DMA><<<grid, 256, 0, s>>>(ka); break;
-        default: prefill_mfma_f32<128, PAGED, DMA><<<grid, 256, 0, s>>>(ka); break;
+        case 32: launch_timed(prefill_mfma_f32<32, PAGED, DMA>, grid, dim3(256), s, ka); break;
+        case 64: launch_timed(prefill_mfma_f32<64, PAGED, DMA>, grid, dim3(256), s, ka); break;
+        default: launch_timed(prefill_mfma_f32<128, PAGED, DMA>, grid, dim3(256), s, ka); break;
     }
 }
 
