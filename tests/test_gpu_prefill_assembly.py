@@ -280,3 +280,28 @@ def test_precise_assembly_prefill_matches_oracle_and_hip_split(hip, hq, hkv, S, 
     assert_close("LSE", l[:n], el[:n], H16_ATOL, 0.0)
     assert_close("O vs HIP split", o, o0, H16_ATOL, 0.0)
     assert_close("LSE vs HIP split", l, l0, H16_ATOL, 0.0)
+
+
+@pytest.mark.parametrize("dtype,rnd", [(fa.DTYPE_BF16, bf16_round), (fa.DTYPE_F32, lambda x: x)])
+def test_kernel_timing_leaves_results_unchanged(hip, dtype, rnd):
+    """With per-kernel timing on, the assembly kernel (bf16) and the f32 kernel record their
+    span's events as part of their own dispatch: the output is bitwise the one without timing,
+    and the prefill kernel shows one timed dispatch of positive duration."""
+    B, hq, hkv, S, D = 1, 8, 2, 300, 128
+    q = rnd(normal(B * hq * S * D, 971))
+    k, v = rnd(normal(B * hkv * S * D, 972)), rnd(normal(B * hkv * S * D, 973))
+    shape = fa.GroupedAttentionShape(B, hq, hkv, S, D)
+    cfg, rot = fa.FlatAttentionConfig(True), fa.RotaryEmbeddingConfig(1e4, 0)
+    o0, l0 = _run_grouped(hip, q, k, v, shape, cfg, rot, dtype)
+    hip.set_kernel_timing(True)
+    try:
+        o1, l1 = _run_grouped(hip, q, k, v, shape, cfg, rot, dtype)
+        t = hip.last_telemetry()
+        if dtype == fa.DTYPE_BF16:
+            assert "prefill_a64" in t.kernel_name, t.kernel_name
+        ms, n = hip.kernel_timing(t.kernel_id)
+        assert n == 1 and ms > 0.0, (t.kernel_id, ms, n)
+    finally:
+        hip.set_kernel_timing(False)
+    assert np.array_equal(o0.view(np.uint32), o1.view(np.uint32))
+    assert np.array_equal(l0.view(np.uint32), l1.view(np.uint32))
