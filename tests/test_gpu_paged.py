@@ -399,15 +399,20 @@ def test_mixed_lengths_equal_work_partition_matches_oracle(hip, request, grouped
 @pytest.mark.gpu
 def test_kernel_timing_and_mfma_variant_telemetry(hip):
     """bf16 KV with page_size % 16 == 0 selects the MFMA split kernel; per-kernel timing counts
-    one split and one combine dispatch per launch and clears when re-enabled."""
+    one split and one combine dispatch per launch (the split kernel recording its events in its
+    own dispatch, the results bitwise those without timing) and clears when re-enabled."""
     rng = np.random.default_rng(5)
     ctx_lens = [700, 1500, 33]
     ps, hq, hkv, D = 16, 8, 2, 128
     bt, kp, vp, total = _make_pool(rng, ctx_lens, ps, hkv, D, bf16_round)
     q = bf16_round(normal(len(ctx_lens) * hq * D, 3))
+    o0, l0, _ = _decode(hip, bt, ctx_lens, kp, vp, total, ps, hq, hkv, D, q, fa.DTYPE_BF16)
     hip.set_kernel_timing(True)
     try:
-        _, _, plan = _decode(hip, bt, ctx_lens, kp, vp, total, ps, hq, hkv, D, q, fa.DTYPE_BF16)
+        o1, l1, plan = _decode(hip, bt, ctx_lens, kp, vp, total, ps, hq, hkv, D, q,
+                               fa.DTYPE_BF16)
+        assert np.array_equal(np.asarray(o0).view(np.uint32), np.asarray(o1).view(np.uint32))
+        assert np.array_equal(np.asarray(l0).view(np.uint32), np.asarray(l1).view(np.uint32))
         t = hip.last_telemetry()
         assert t.kernel_id == "DecodePagedMfma" and t.dispatch_count == 2
         ms, n = hip.kernel_timing("DecodePagedMfma")
