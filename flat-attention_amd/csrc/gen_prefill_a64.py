@@ -23,7 +23,8 @@ Layout of the work (per workgroup of 4 waves = 256 query rows of one (batch, kv 
 Per 32-key half-tile h (the pipeline unit):
   S^T[32 keys x 32 rows] (rb) = K_perm . Q^T(rb)   v_mfma_f32_32x32x16_bf16, A = K from LDS,
                                                    B = Q^T from AGPRs, 8 k-steps of 16 dims
-  P^T = exp2(S * c2 - m * c2) packed to bf16        (every value a lane holds is its own row)
+  P^T = exp2(S * c2 - m * c2) packed to bf16        (every value a lane holds is its own row;
+                                                   the f16 kernels: f16 MFMAs and packing)
   O^T[128 dims x 32 rows] (rb) += V^T . P^T         A = V^T from LDS (ds_read_b64_tr_b16),
                                                    B = P^T from VGPRs, O in AGPRs
 K rows are fed in a permuted order (bits 2 and 3 of the row swapped) so that accumulator i of a
@@ -99,6 +100,8 @@ def arg64(name: str) -> str:
 KERNEL_CONTIG = "fa_prefill_a64_bf16"
 KERNEL_PAGED = "fa_prefill_a64_paged_bf16"
 KERNEL_PREC = "fa_prefill_a64_precise_bf16"
+KERNEL_CONTIG_F16 = "fa_prefill_a64_f16"
+KERNEL_PAGED_F16 = "fa_prefill_a64_paged_f16"
 KERNEL = KERNEL_CONTIG
 # Paged K/V (page size 16): transfer instruction i of a tile covers its rows 16 i .. 16 i + 15,
 # i.e. exactly one page, read through a buffer resource based at that page. The page ids of
@@ -107,6 +110,27 @@ PAGED = False
 # Precise scores: K read as its bf16 high part and the residual (a second LDS tile), Q carried
 # the same way (residual in AGPRs), three MFMAs per score k-step (hi.hi + lo.hi + hi.lo)
 PREC = False
+
+
+# f16 storage: the same kernels with the f16 MFMA and f16 conversions; the fast path's overflow
+# threshold drops to row sums above 2^15 so that every rounded probability stays finite in f16.
+F16 = False
+
+
+def MF() -> str:
+    return "v_mfma_f32_32x32x16_f16" if F16 else "v_mfma_f32_32x32x16_bf16"
+
+
+def CVT() -> str:
+    return "v_cvt_pk_f16_f32" if F16 else "v_cvt_pk_bf16_f32"
+
+
+def unpack(lo: str, hi: str, src: str) -> list:
+    """The two 16-bit values packed in src as f32 in lo (low half) and hi (high half)."""
+    if F16:
+        return [I(f"v_cvt_f32_f16 {lo}, {src}"),
+                I(f"v_cvt_f32_f16_sdwa {hi}, {src} dst_sel:DWORD src0_sel:WORD_1")]
+    return [I(f"v_lshlrev_b32 {lo}, 16, {src}"), I(f"v_and_b32 {hi}, 0xffff0000, {src}")]
 
 
 def STAGE_BYTES() -> int:
@@ -563,9 +587,8 @@ def exp_pack_sum(x: int) -> list[Ins]:
                 out += pend
                 pend = []
                 dst = PB[x] + 8 * rb + 4 * s + j
-                pend += [I(f"v_cvt_pk_bf16_f32 {vr(dst)}, {vr(r)}, {vr(r + 1)}"),
-                         I(f"v_lshlrev_b32 {vr(r)}, 16, {vr(dst)}"),
-                         I(f"v_and_b32 {vr(r + 1)}, 0xffff0000, {vr(dst)}")]
+                pend += [I(f"{CVT()} {vr(dst)}, {vr(r)}, {vr(r + 1)}")] + \
+                    unpack(vr(r), vr(r + 1), vr(dst))
                 lt = vr(V_LT + rb)
                 if i0 == 0:
                     pend.append(I(f"v_add_f32 {lt}, {vr(r)}, {vr(r + 1)}"))
@@ -638,7 +661,7 @@ def _recompute_scores(gen: "Gen", x: int, hh: int) -> None:
             for part, (ring, qf) in enumerate(s_parts()):
                 for rb in range(2):
                     src_c = "0" if ks == 0 and part == 0 else s_acc(x, rb)
-                    ins = I(f"v_mfma_f32_32x32x16_bf16 {s_acc(x, rb)}, {vr(ring + 4 * k4, 4)}, "
+                    ins = I(f"{MF()} {s_acc(x, rb)}, {vr(ring + 4 * k4, 4)}, "
                             f"{qf(rb, ks)}, {src_c}")
                     ins.srcc_chain = not (ks == 0 and part == 0)
                     e(ins)
@@ -823,7 +846,7 @@ def phase(gen: Gen, *, pv_x, pv_hh, s_x, s_hh, sm_x, sm_masked, pre=(),
             gen.ds_wait_for(v_issued[idx])
             s, mb = pv_ops[idx]
             slot = v_slot(idx)
-            ins = I(f"v_mfma_f32_32x32x16_bf16 {o_acc(rb, mb)}, {vr(VRING + 4 * slot, 4)}, "
+            ins = I(f"{MF()} {o_acc(rb, mb)}, {vr(VRING + 4 * slot, 4)}, "
                     f"{p_op(pv_x, rb, s)}, {o_acc(rb, mb)}")
             ins.srcc_chain = True
         else:
@@ -834,7 +857,7 @@ def phase(gen: Gen, *, pv_x, pv_hh, s_x, s_hh, sm_x, sm_masked, pre=(),
             # k-step 0 accumulates onto the bias block (-m of the lane's row)
             first = idx == 0 and part == 0
             src_c = ("0" if zero_bias else vr(NB + 16 * rb, 16)) if first else s_acc(s_x, rb)
-            ins = I(f"v_mfma_f32_32x32x16_bf16 {s_acc(s_x, rb)}, {vr(ring + 4 * slot, 4)}, "
+            ins = I(f"{MF()} {s_acc(s_x, rb)}, {vr(ring + 4 * slot, 4)}, "
                     f"{qf(rb, idx)}, {src_c}")
             ins.srcc_chain = not first
         gen.emit(ins)
@@ -1030,7 +1053,7 @@ def setup(gen: Gen):
     e(I(f"s_lshr_b32 {sr(S_WAVE)}, {sr(S_WAVE)}, 6"))
     T0, T1, T2, T3 = (sr(S_T0), sr(S_T1), sr(S_T2), sr(S_T3))
     e([I(f"v_mov_b32 {vr(V_NINF)}, 0xff800000"),
-       I(f"v_mov_b32 {vr(V_BIG)}, 0x5f800000"),
+       I(f"v_mov_b32 {vr(V_BIG)}, {'0x47000000' if F16 else '0x5f800000'}"),
        I(f"s_mov_b32 {sr(S_HIMASK)}, 0"),
        I(f"s_mov_b32 {sr(S_HIMASK + 1)}, -1"),
        I(f"s_mov_b32 {sr(S_ROUND)}, 0")])
@@ -1355,15 +1378,14 @@ def setup_block(gen: Gen):
             w = w0 + j
             c, sn = cs0 + 2 * j, cs0 + 2 * j + 1
             ev, od, t1 = V_TMP, V_TMP + 1, V_TMP + 2
-            out += [I(f"v_lshlrev_b32 {vr(ev)}, 16, {vr(w)}"),
-                    I(f"v_and_b32 {vr(od)}, 0xffff0000, {vr(w)}"),
-                    I(f"v_mul_f32 {vr(t1)}, {vr(od)}, {vr(sn)}"),
+            out += unpack(vr(ev), vr(od), vr(w))
+            out += [I(f"v_mul_f32 {vr(t1)}, {vr(od)}, {vr(sn)}"),
                     I(f"v_fma_f32 {vr(t1)}, {vr(ev)}, {vr(c)}, -{vr(t1)}"),
                     I(f"v_mul_f32 {vr(od)}, {vr(od)}, {vr(c)}"),
                     I(f"v_fma_f32 {vr(od)}, {vr(ev)}, {vr(sn)}, {vr(od)}"),
                     I(f"v_mul_f32 {vr(t1)}, {c2}, {vr(t1)}"),
                     I(f"v_mul_f32 {vr(od)}, {c2}, {vr(od)}"),
-                    I(f"v_cvt_pk_bf16_f32 {vr(w)}, {vr(t1)}, {vr(od)}")]
+                    I(f"{CVT()} {vr(w)}, {vr(t1)}, {vr(od)}")]
             out += residual(w, t1, od, lo_a0 + j)
         return out
 
@@ -1405,11 +1427,10 @@ def setup_block(gen: Gen):
         for w in range(32):
             r = qt[rb] + w
             ev, od = V_TMP, V_TMP + 1
-            e([I(f"v_lshlrev_b32 {vr(ev)}, 16, {vr(r)}"),
-               I(f"v_and_b32 {vr(od)}, 0xffff0000, {vr(r)}"),
-               I(f"v_mul_f32 {vr(ev)}, {c2}, {vr(ev)}"),
+            e(unpack(vr(ev), vr(od), vr(r)))
+            e([I(f"v_mul_f32 {vr(ev)}, {c2}, {vr(ev)}"),
                I(f"v_mul_f32 {vr(od)}, {c2}, {vr(od)}"),
-               I(f"v_cvt_pk_bf16_f32 {vr(r)}, {vr(ev)}, {vr(od)}")])
+               I(f"{CVT()} {vr(r)}, {vr(ev)}, {vr(od)}")])
             e(residual(r, ev, od, A_QLO + rb * 32 + w))
     e(I(".Lq_done:"))
     e(I("s_waitcnt vmcnt(0)"))
@@ -1420,7 +1441,7 @@ def setup_block(gen: Gen):
     # instead of 128 AGPR writes), running statistics
     e([I(f"v_mov_b32 {vr(NB + i)}, 0") for i in range(4)])
     for blk in range(8):
-        e(I(f"v_mfma_f32_32x32x16_bf16 {ar(A_O + 16 * blk, 16)}, {vr(NB, 4)}, {vr(NB, 4)}, 0"))
+        e(I(f"{MF()} {ar(A_O + 16 * blk, 16)}, {vr(NB, 4)}, {vr(NB, 4)}, 0"))
     for rb in range(2):
         e([I(f"v_mov_b32 {vr(V_M + rb)}, 0xff800000"),
            I(f"v_mov_b32 {vr(V_L + rb)}, 0")])
@@ -1492,8 +1513,8 @@ def epilogue_store(gen: Gen):
                 d = DATA + 2 * n
                 e([I(f"v_accvgpr_read_b32 {vr(t + i)}, {ar(a)}") for i, a in enumerate(regs)])
                 e([I(f"v_mul_f32 {vr(t + i)}, {vr(t + i)}, {vr(V_ALPHA + rb)}") for i in range(4)])
-                e([I(f"v_cvt_pk_bf16_f32 {vr(d)}, {vr(t)}, {vr(t + 1)}"),
-                   I(f"v_cvt_pk_bf16_f32 {vr(d + 1)}, {vr(t + 2)}, {vr(t + 3)}")])
+                e([I(f"{CVT()} {vr(d)}, {vr(t)}, {vr(t + 1)}"),
+                   I(f"{CVT()} {vr(d + 1)}, {vr(t + 2)}, {vr(t + 3)}")])
                 e(I(f"ds_write_b64 {vr(W)}, {vr(d, 2)} "
                     f"offset:{rb * 32 * O_ROWB + mb * 64 + 16 * q4}"))
                 n += 1
@@ -1835,17 +1856,19 @@ def build_all() -> list[tuple]:
     """The contiguous, the paged and the precise kernel (with its resource counts: the precise
     kernel holds the Q residual in the last 64 AGPRs and three 48 KiB stages, one barrier per
     key tile)."""
-    global PAGED, KERNEL, PREC, NSTAGE, PAIR
+    global PAGED, KERNEL, PREC, NSTAGE, PAIR, F16
     out = []
-    for paged, prec, name, prefix in ((False, False, KERNEL_CONTIG, ""),
-                                      (True, False, KERNEL_PAGED, "P"),
-                                      (False, True, KERNEL_PREC, "R")):
-        PAGED, PREC, KERNEL = paged, prec, name
+    for paged, prec, f16, name, prefix in ((False, False, False, KERNEL_CONTIG, ""),
+                                           (True, False, False, KERNEL_PAGED, "P"),
+                                           (False, True, False, KERNEL_PREC, "R"),
+                                           (False, False, True, KERNEL_CONTIG_F16, "H"),
+                                           (True, False, True, KERNEL_PAGED_F16, "HP")):
+        PAGED, PREC, F16, KERNEL = paged, prec, f16, name
         NSTAGE, PAIR = (3, False) if prec else (5, True)
         counts = {"num_agpr": 256 if prec else NUM_AGPR,
                   "lds_bytes": NSTAGE * STAGE_BYTES()}
         out.append((build(), name, prefix, counts))
-    PAGED, PREC, KERNEL, NSTAGE, PAIR = False, False, KERNEL_CONTIG, 5, True
+    PAGED, PREC, F16, KERNEL, NSTAGE, PAIR = False, False, False, KERNEL_CONTIG, 5, True
     return out
 
 
@@ -1884,7 +1907,9 @@ def header(path: str):
              f"#define FA_A64_LDS_BYTES {LDS_BYTES}",
              f'#define FA_A64_KERNEL "{KERNEL_CONTIG}"',
              f'#define FA_A64_KERNEL_PAGED "{KERNEL_PAGED}"',
-             f'#define FA_A64_KERNEL_PREC "{KERNEL_PREC}"']
+             f'#define FA_A64_KERNEL_PREC "{KERNEL_PREC}"',
+             f'#define FA_A64_KERNEL_F16 "{KERNEL_CONTIG_F16}"',
+             f'#define FA_A64_KERNEL_PAGED_F16 "{KERNEL_PAGED_F16}"']
     for n, off, sz in ARGS:
         lines.append(f"#define FA_A64_OFF_{n.upper()} {off}")
     open(path, "w").write("\n".join(lines) + "\n")

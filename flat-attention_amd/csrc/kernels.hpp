@@ -64,8 +64,8 @@ struct PrefillArgs {
 bool prefill_a64_eligible(Dtype dt, bool paged, const PrefillArgs& a);
 // Loads the code object on `device` (current); idempotent. Failure leaves the HIP kernels in use.
 hipError_t prefill_a64_load(int device);
-void launch_prefill_a64(const PrefillArgs& a, bool paged, hipStream_t s, unsigned grid[3],
-                        unsigned* block);
+void launch_prefill_a64(Dtype dt, const PrefillArgs& a, bool paged, hipStream_t s,
+                        unsigned grid[3], unsigned* block);
 // Workgroups of its persistent grid: min(query blocks, CUs of the current device).
 unsigned prefill_a64_workgroups(const PrefillArgs& a);
 

@@ -1283,7 +1283,7 @@ void launch_prefill(Dtype dt, bool paged, const PrefillArgs& a, hipStream_t s, u
     if (paged) ka.ps = FastDiv((uint32_t)a.page_size);
     const int dpad = a.head_dim <= 32 ? 32 : (a.head_dim <= 64 ? 64 : 128);
     if (prefill_a64_eligible(dt, paged, a)) {
-        launch_prefill_a64(a, paged, s, grid, block);
+        launch_prefill_a64(dt, a, paged, s, grid, block);
         return;
     }
     unsigned rows;

@@ -59,6 +59,38 @@ def test_assembly_prefill_matches_oracle(asm, hq, hkv, S, causal):
     assert np.isfinite(o).all() and np.isfinite(l).all()
 
 
+@pytest.mark.parametrize("hq,hkv,S", [(8, 2, 63), (32, 8, 300), (16, 1, 200), (4, 4, 1000)])
+@pytest.mark.parametrize("causal", [True, False])
+def test_assembly_prefill_f16_matches_oracle_and_hip(asm, hq, hkv, S, causal):
+    """f16 storage (fa_prefill_a64_f16: the same schedule with the f16 MFMA and conversions, the
+    fast path's overflow threshold at row sums of 2^15): the oracle at the 16-bit bar, and the
+    HIP kernel (fa_ctx_set_prefill_kernel(0)) within it."""
+    B, D = 2, 128
+    q = f16_round(normal(B * hq * S * D, 980 + S + hq))
+    k = f16_round(normal(B * hkv * S * D, 981 + S))
+    v = f16_round(normal(B * hkv * S * D, 982 + S))
+    shape = fa.GroupedAttentionShape(B, hq, hkv, S, D)
+    rot = fa.RotaryEmbeddingConfig(1e4, 7)
+    cfg = fa.FlatAttentionConfig(causal)
+    o, l = _run_grouped(asm, q, k, v, shape, cfg, rot, fa.DTYPE_F16)
+    name = asm.last_telemetry().kernel_name
+    assert "prefill_a64<f16>" in name, name
+    try:
+        asm.set_prefill_kernel(0)
+        o0, l0 = _run_grouped(asm, q, k, v, shape, cfg, rot, fa.DTYPE_F16)
+        assert "prefill_a64" not in asm.last_telemetry().kernel_name
+    finally:
+        asm.set_prefill_kernel(-1)
+    assert np.isfinite(o).all() and np.isfinite(l).all()
+    units = (0, B * hq) if S <= 300 else (0, 2)
+    eo, el = _oracle_grouped(q, k, v, shape, causal, rot, units=units)
+    n = (units[1] - units[0]) * S
+    assert_close("O", o[:n * D], eo[:n * D], H16_ATOL, 0.0)
+    assert_close("LSE", l[:n], el[:n], H16_ATOL, 0.0)
+    assert_close("O vs HIP", o, o0, H16_ATOL, 0.0)
+    assert_close("LSE vs HIP", l, l0, H16_ATOL, 0.0)
+
+
 def test_assembly_prefill_cfg3_full_size(asm):
     """BASELINE configs[2] (B2 Hq32 Hkv8 N4096 D128 bf16, theta 1e4, causal): the oracle on the
     first and last (batch, head) units, V = 1 giving O = 1 on every row, and the persistent grid
@@ -97,16 +129,17 @@ def test_assembly_prefill_cfg3_full_size(asm):
     assert_close("LSE vs HIP kernel", l, l0, H16_ATOL, 0.0)
 
 
+@pytest.mark.parametrize("dtype,rnd", [(fa.DTYPE_BF16, bf16_round), (fa.DTYPE_F16, f16_round)])
 @pytest.mark.parametrize("pattern", ["rising", "falling", "alternating"])
-def test_assembly_prefill_adversarial_scores(asm, pattern):
+def test_assembly_prefill_adversarial_scores(asm, pattern, dtype, rnd):
     """Scores rising to 60 (every tile moves the row max: the exact rescale path on each tile),
     falling to -60 (the max never moves), or alternating +-24, over 4096 RoPE positions. The
     rounding of rotated Q and K to bf16 bounds the LSE error by max|s| * 2^-7, the bound the HIP
     kernel's default mode is held to; O is held to 2e-2 where the scores stay small."""
     S, D, theta = 4096, 128, 1e4
     q, k = _rope_adversarial_inputs(pattern, S, D, theta, False)
-    q, k = bf16_round(q), bf16_round(k)
-    v = bf16_round(normal(S * D, 77))
+    q, k = rnd(q), rnd(k)
+    v = rnd(normal(S * D, 77))
     shape = fa.GroupedAttentionShape(1, 1, 1, S, D)
     rot = fa.RotaryEmbeddingConfig(theta, 0)
     qr = oracle.rope_rotate_rows(q, S, 1, D, theta, 0)
@@ -114,7 +147,7 @@ def test_assembly_prefill_adversarial_scores(asm, pattern):
     eo, el = oracle.forward(qr, kr, v, 1, 1, S, D, True)
     smax = float(np.max(np.abs(np.asarray(qr).reshape(S, D) @ np.asarray(kr).reshape(S, D).T
                                / np.sqrt(D))))
-    o, l = _run_grouped(asm, q, k, v, shape, fa.FlatAttentionConfig(True), rot, fa.DTYPE_BF16)
+    o, l = _run_grouped(asm, q, k, v, shape, fa.FlatAttentionConfig(True), rot, dtype)
     _assert_ran_assembly(asm)
     assert np.isfinite(o).all() and np.isfinite(l).all()
     assert_close("LSE", l, el, smax * 2.0 ** -7, 0.0)
@@ -124,7 +157,8 @@ def test_assembly_prefill_adversarial_scores(asm, pattern):
     assert np.all(o.reshape(S, D) >= vr.min(axis=0) - 2e-2)
 
 
-def test_assembly_prefill_tied_and_jumping_scores(asm):
+@pytest.mark.parametrize("dtype,rnd", [(fa.DTYPE_BF16, bf16_round), (fa.DTYPE_F16, f16_round)])
+def test_assembly_prefill_tied_and_jumping_scores(asm, dtype, rnd):
     """Ties (zero keys: every score exactly 0, uniform rows with l = t + 1) held to 2e-2, and
     +-24 jumps between neighbouring keys inside each 64-key tile (the row max moves within a
     tile, P underflows for half the keys) held to the RoPE rounding bound max|s| * 2^-7 on LSE
@@ -132,7 +166,7 @@ def test_assembly_prefill_tied_and_jumping_scores(asm):
     S, D, H, theta = 300, 128, 2, 1e4
     idx = np.arange(S)
     u = np.full(D, 1.0 / np.sqrt(D))
-    v = bf16_round(normal(H * S * D, 5))
+    v = rnd(normal(H * S * D, 5))
     vr = v.reshape(H, S, D)
     shape = fa.GroupedAttentionShape(1, H, H, S, D)
     rot = fa.RotaryEmbeddingConfig(theta, 0)
@@ -140,11 +174,10 @@ def test_assembly_prefill_tied_and_jumping_scores(asm):
                          ("jumps", np.where(idx % 2 == 0, 24.0, -24.0))):
         q1 = _rope64(np.tile(u, (S, 1)), idx, D, theta, -1.0)
         k1 = _rope64(scores[:, None] * np.sqrt(D) * u[None, :], idx, D, theta, -1.0)
-        q = bf16_round(np.tile(q1.astype(np.float32).ravel(), H))
-        k = bf16_round(np.tile(k1.astype(np.float32).ravel(), H))
+        q = rnd(np.tile(q1.astype(np.float32).ravel(), H))
+        k = rnd(np.tile(k1.astype(np.float32).ravel(), H))
         for causal in (True, False):
-            o, l = _run_grouped(asm, q, k, v, shape, fa.FlatAttentionConfig(causal), rot,
-                                fa.DTYPE_BF16)
+            o, l = _run_grouped(asm, q, k, v, shape, fa.FlatAttentionConfig(causal), rot, dtype)
             _assert_ran_assembly(asm)
             eo, el = _oracle_grouped(q, k, v, shape, causal, rot)
             if name == "ties":
@@ -182,14 +215,15 @@ def test_assembly_projection_layout_rect_causal_offset(asm):
             assert_close(f"LSE {ql}x{kl}", res.lse, el, H16_ATOL, 0.0)
 
 
-@pytest.mark.parametrize("case", ["f16", "head_dim_64", "no_rope", "group_3", "precise_group_3"])
+@pytest.mark.parametrize("case", ["f16_head_dim_64", "head_dim_64", "no_rope", "group_3",
+                                  "precise_group_3"])
 def test_assembly_prefill_falls_back_where_it_does_not_apply(asm, case):
     """Inputs outside the assembly kernel's scope run the HIP kernels (the telemetry names
     which) and still match the oracle."""
     B, hq, hkv, S, D = 1, 4, 2, 130, 128
     dtype, rnd, rot = fa.DTYPE_BF16, bf16_round, fa.RotaryEmbeddingConfig(1e4, 0)
-    if case == "f16":
-        dtype, rnd = fa.DTYPE_F16, f16_round
+    if case == "f16_head_dim_64":
+        dtype, rnd, D = fa.DTYPE_F16, f16_round, 64
     elif case == "head_dim_64":
         D = 64
     elif case == "no_rope":
@@ -215,7 +249,9 @@ def test_assembly_prefill_falls_back_where_it_does_not_apply(asm, case):
                                                      (16, 1, 0, 129, True),
                                                      (8, 8, 1000, 64, False),
                                                      (4, 2, 17, 300, True)])
-def test_assembly_paged_prefill_matches_paged_oracle(asm, hq, hkv, cached, ql, causal):
+@pytest.mark.parametrize("dtype,rnd", [(fa.DTYPE_BF16, bf16_round), (fa.DTYPE_F16, f16_round)])
+def test_assembly_paged_prefill_matches_paged_oracle(asm, hq, hkv, cached, ql, causal, dtype,
+                                                     rnd):
     """The paged assembly kernel (16-row pages): chunked prefill over a shuffled page pool whose
     unnamed rows hold NaN (a wrong page shows), GQA groups 1..16, ragged last pages, causal
     offsets from 0 to 1000; checked against the paged oracle over the device's own pool and
@@ -227,17 +263,17 @@ def test_assembly_paged_prefill_matches_paged_oracle(asm, hq, hkv, cached, ql, c
     total = n_seqs * pages_per + 5
     rng = np.random.default_rng(kv_len + hq)
     width = hkv * D
-    raw_k = bf16_round(normal(n_seqs * kv_len * width, 41))
-    v = bf16_round(normal(n_seqs * kv_len * width, 42))
-    q = bf16_round(normal(n_seqs * ql * hq * D, 43))
+    raw_k = rnd(normal(n_seqs * kv_len * width, 41))
+    v = rnd(normal(n_seqs * kv_len * width, 42))
+    q = rnd(normal(n_seqs * ql * hq * D, 43))
     ident = np.arange(n_seqs * pages_per, dtype=np.int32).reshape(n_seqs, pages_per)
     shuf = rng.permutation(total)[:n_seqs * pages_per].astype(np.int32).reshape(n_seqs, pages_per)
     o1, l1 = _paged_prefill(asm, ident, ps, total, n_seqs, hq, hkv, D, cached, ql, theta, raw_k,
-                            v, q, fa.DTYPE_BF16, causal)
+                            v, q, dtype, causal)
     _assert_ran_assembly(asm)
     pools = []
     o2, l2 = _paged_prefill(asm, shuf, ps, total, n_seqs, hq, hkv, D, cached, ql, theta, raw_k,
-                            v, q, fa.DTYPE_BF16, causal, pools)
+                            v, q, dtype, causal, pools)
     _assert_ran_assembly(asm)
     assert np.array_equal(o1.view(np.uint32), o2.view(np.uint32))
     assert np.array_equal(l1.view(np.uint32), l2.view(np.uint32))
