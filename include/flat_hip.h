@@ -569,8 +569,9 @@ int fa_forward_mha_telemetry(fa_ctx* ctx, const fa_attention_shape* shape,
 int fa_ctx_set_prefill_policy(fa_ctx* ctx, int32_t prerotate_k);
 /* Main loop of the 16-bit contiguous prefill (kernel-variant selection, the role of
  * WgpuKernelVariant src/wgpu_backend.rs:31-37): -1 (default) and 1 the assembly kernel
- * fa_prefill_a64_bf16 (64 query rows per wave, persistent grid) where it applies: bf16, head_dim
- * 128, RoPE with K rotated by the pre-pass, power-of-two GQA group, 16-byte aligned rows; 0 the
+ * fa_prefill_a64_bf16 / fa_prefill_a64_f16 (64 query rows per wave, persistent grid) where it
+ * applies: bf16 or f16 storage, head_dim 128, RoPE with K rotated by the pre-pass, power-of-two
+ * GQA group, 16-byte aligned rows (the precise-score mode: bf16 only); 0 the
  * HIP kernels only. Other inputs always run the HIP kernels. Both give results within the same
  * tolerance of the oracle (not bitwise equal: the assembly kernel scales Q by scale * log2 e
  * before its one rounding to bf16); the telemetry's kernel name says which ran. */
