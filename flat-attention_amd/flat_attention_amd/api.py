@@ -274,8 +274,7 @@ class HipContext:
     def set_prefill_kernel(self, assembly: int):
         """-1 (default) and 1: the assembly main loop fa_prefill_a64_bf16 / _f16 where it
         applies (bf16 or f16, head_dim 128, RoPE with pre-rotated K, power-of-two GQA group);
-        0: the HIP
-        prefill kernels only."""
+        0: the HIP prefill kernels only."""
         check(lib().fa_ctx_set_prefill_kernel(self.handle, assembly))
 
     def set_decode_policy(self, grouped: int):
