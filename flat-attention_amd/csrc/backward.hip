@@ -1001,11 +1001,12 @@ void launch_dma(const BackwardArgs& a, hipStream_t s) {
 template <typename T>
 void launch_dims(const BackwardArgs& a, hipStream_t s, bool* a64_out) {
     const int64_t rows = (int64_t)a.batch * a.q_heads * a.seq;
-    if constexpr (std::is_same_v<T, bf16_t>) {
-        if (bwd_a64_eligible(Dtype::BF16, a)) {
+    if constexpr (std::is_same_v<T, bf16_t> || std::is_same_v<T, f16_t>) {
+        constexpr Dtype dt = std::is_same_v<T, bf16_t> ? Dtype::BF16 : Dtype::F16;
+        if (bwd_a64_eligible(dt, a)) {
             hipLaunchKernelGGL((bwd_delta<T, true>), dim3((unsigned)((rows + 15) / 16)),
                                dim3(256), 0, s, a, rows);
-            launch_bwd_a64(a, s);
+            launch_bwd_a64(dt, a, s);
             const int nqd = (a.seq + kDqDsQueries - 1) / kDqDsQueries;
             hipLaunchKernelGGL((bwd_dq_ds<T, 128>), dim3(nqd * a.batch * a.q_heads), dim3(512),
                                0, s, a);

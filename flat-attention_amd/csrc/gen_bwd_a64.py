@@ -49,7 +49,18 @@ P = importlib.util.module_from_spec(_spec)
 _spec.loader.exec_module(P)
 I, Gen, fdiv = P.I, P.Gen, P.fdiv
 
-KERNEL = "fa_bwd_dkdv_a64_bf16"
+KERNEL_BF16 = "fa_bwd_dkdv_a64_bf16"
+KERNEL_F16 = "fa_bwd_dkdv_a64_f16"   # f16 storage: f16 MFMAs and conversions, else identical
+KERNEL = KERNEL_BF16
+F16 = False
+
+
+def MF() -> str:
+    return "v_mfma_f32_32x32x16_f16" if F16 else "v_mfma_f32_32x32x16_bf16"
+
+
+def CVT() -> str:
+    return "v_cvt_pk_f16_f32" if F16 else "v_cvt_pk_bf16_f32"
 
 # --------------------------------------------------------------------------- kernel arguments
 ARGS = [
@@ -324,7 +335,7 @@ def setup(gen: Gen):
     # ---- dK = dV = 0 (eight MFMAs of zero operands)
     e([I(f"v_mov_b32 {vr(V_TMP + i)}, 0") for i in range(4)])
     for blk in range(8):
-        e(I(f"v_mfma_f32_32x32x16_bf16 {ar(16 * blk, 16)}, {vr(V_TMP, 4)}, {vr(V_TMP, 4)}, 0"))
+        e(I(f"{MF()} {ar(16 * blk, 16)}, {vr(V_TMP, 4)}, {vr(V_TMP, 4)}, 0"))
     # ---- tile 0 into stage 0
     # tile order: query tiles outer, the group's heads inner; the first half of the key blocks
     # sweeps the queries downwards from the last tile, the second half upwards from its
@@ -489,8 +500,8 @@ def softmax(i: int, masked: bool) -> list:
         out += [I(f"v_mul_f32 {vr(D + t)}, {vr(S + t)}, {vr(D + t)}"),
                 I(f"v_mul_f32 {vr(D + t + 1)}, {vr(S + t + 1)}, {vr(D + t + 1)}")]
         reg = 4 * (t >> 3) + ((t & 7) >> 1)
-        out += [I(f"v_cvt_pk_bf16_f32 {vr(PF + reg)}, {vr(S + t)}, {vr(S + t + 1)}"),
-                I(f"v_cvt_pk_bf16_f32 {vr(DF + reg)}, {vr(D + t)}, {vr(D + t + 1)}")]
+        out += [I(f"{CVT()} {vr(PF + reg)}, {vr(S + t)}, {vr(S + t + 1)}"),
+                I(f"{CVT()} {vr(DF + reg)}, {vr(D + t)}, {vr(D + t + 1)}")]
     return out
 
 
@@ -608,7 +619,7 @@ def body(gen: Gen, n: int, diag: bool, xfer: list):
             frag = (VF if k & 1 else KF) + 4 * ks
             src = vr((DB if k & 1 else LB), 16) if ks == 0 else vr(acc, 16)
             slot = a_slot(reads_a.index(idx))
-            ins = I(f"v_mfma_f32_32x32x16_bf16 {vr(acc, 16)}, {vr(slot, 4)}, {vr(frag, 4)}, "
+            ins = I(f"{MF()} {vr(acc, 16)}, {vr(slot, 4)}, {vr(frag, 4)}, "
                     f"{src}")
             ins.srcc_chain = ks != 0
         else:
@@ -616,7 +627,7 @@ def body(gen: Gen, n: int, diag: bool, xfer: list):
             acc = (A_DK if is_dk else A_DV) + 16 * mb
             a_op = (DF if is_dk else PF) + 4 * s_
             slot = BRING + 4 * (reads_b.index(idx) % RBN)
-            ins = I(f"v_mfma_f32_32x32x16_bf16 {ar(acc, 16)}, {vr(a_op, 4)}, {vr(slot, 4)}, "
+            ins = I(f"{MF()} {ar(acc, 16)}, {vr(a_op, 4)}, {vr(slot, 4)}, "
                     f"{ar(acc, 16)}")
             ins.srcc_chain = True
         e(ins)
@@ -690,7 +701,7 @@ def epilogue(gen: Gen):
             e([I(f"v_accvgpr_read_b32 {vr(X + r)}, {ar(abase + 16 * mb + r)}") for r in range(16)])
             if scaled:
                 e([I(f"v_mul_f32 {vr(X + r)}, {arg('scale')}, {vr(X + r)}") for r in range(16)])
-            e([I(f"v_cvt_pk_bf16_f32 {vr(X + r)}, {vr(X + r)}, 0") for r in range(16)])
+            e([I(f"{CVT()} {vr(X + r)}, {vr(X + r)}, 0") for r in range(16)])
             for r in range(16):
                 off = tensor * EP_TENSOR + (8 * (r >> 2) + (r & 3)) * EP_ROWB + 64 * mb
                 e(I(f"ds_write_b16 {vr(V_EPW)}, {vr(X + r)} offset:{off}"))
@@ -801,10 +812,16 @@ def required(prev, cur) -> int:
 def render() -> str:
     P.required = required
     try:
-        return P.render([(build(), KERNEL, "", {"num_vgpr": NUM_VGPR, "num_agpr": NUM_AGPR,
-                                                 "num_sgpr": NUM_SGPR, "lds_bytes": LDS_BYTES,
-                                                 "arg_bytes": ARG_BYTES})])
+        global F16, KERNEL
+        out = []
+        for f16, name, prefix in ((False, KERNEL_BF16, ""), (True, KERNEL_F16, "H")):
+            F16, KERNEL = f16, name
+            out.append((build(), name, prefix, {"num_vgpr": NUM_VGPR, "num_agpr": NUM_AGPR,
+                                                "num_sgpr": NUM_SGPR, "lds_bytes": LDS_BYTES,
+                                                "arg_bytes": ARG_BYTES}))
+        return P.render(out)
     finally:
+        F16, KERNEL = False, KERNEL_BF16
         P.required = _base_required
 
 
@@ -812,7 +829,8 @@ def header(path: str):
     lines = ["// Generated by gen_bwd_a64.py: kernel-argument layout of fa_bwd_dkdv_a64_bf16.",
              "#pragma once", f"#define FA_BWD_A64_ARG_BYTES {ARG_BYTES}",
              f"#define FA_BWD_A64_LDS_BYTES {LDS_BYTES}",
-             f'#define FA_BWD_A64_KERNEL "{KERNEL}"']
+             f'#define FA_BWD_A64_KERNEL "{KERNEL_BF16}"',
+             f'#define FA_BWD_A64_KERNEL_F16 "{KERNEL_F16}"']
     for n, off, sz in ARGS:
         lines.append(f"#define FA_BWD_A64_OFF_{n.upper()} {off}")
     open(path, "w").write("\n".join(lines) + "\n")
@@ -822,7 +840,7 @@ def blob(co_path: str, out_cpp: str):
     data = open(co_path, "rb").read()
     rows = [", ".join(f"0x{b:02x}" for b in data[i:i + 16]) for i in range(0, len(data), 16)]
     text = ("// Generated by gen_bwd_a64.py --blob: the assembled gfx950 code object of "
-            "fa_bwd_dkdv_a64_bf16.\n#include <stddef.h>\nnamespace fa {\n"
+            "fa_bwd_dkdv_a64_bf16 and fa_bwd_dkdv_a64_f16.\n#include <stddef.h>\nnamespace fa {\n"
             "extern const unsigned char kBwdA64Co[] = {\n" + ",\n".join(rows) +
             f"\n}};\nextern const size_t kBwdA64CoSize = {len(data)};\n}}  // namespace fa\n")
     open(out_cpp, "w").write(text)

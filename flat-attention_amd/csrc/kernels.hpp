@@ -144,7 +144,7 @@ struct BackwardArgs {
     int ds_nb, ds_bytes;
     int batch, q_heads, kv_heads, group, seq, head_dim, causal, vec, dma;
     float scale;
-    // Allow the assembly dK/dV kernel (fa_bwd_dkdv_a64_bf16) where bwd_a64_eligible() holds.
+    // Allow the assembly dK/dV kernel (fa_bwd_dkdv_a64_bf16 / _f16) where bwd_a64_eligible() holds.
     // It reads `ld` as two f32 arrays of batch*q_heads*seq rows, -LSE / scale then -delta.
     int a64;
 };
@@ -152,11 +152,11 @@ struct BackwardArgs {
 // tells whether the assembly dK/dV kernel ran.
 void launch_backward(Dtype dt, const BackwardArgs& a, hipStream_t s, bool* a64_out = nullptr);
 
-// The assembly dK/dV kernel (gen_bwd_a64.py): bf16, head_dim 128, seq a multiple of 128, dS
+// The assembly dK/dV kernel (gen_bwd_a64.py): bf16 or f16, head_dim 128, seq a multiple of 128, dS
 // stored, 16-byte aligned tensors, 32-bit offsets; its module loaded on the current device.
 bool bwd_a64_eligible(Dtype dt, const BackwardArgs& a);
 hipError_t bwd_a64_load(int device);
-void launch_bwd_a64(const BackwardArgs& a, hipStream_t s);
+void launch_bwd_a64(Dtype dt, const BackwardArgs& a, hipStream_t s);
 
 // (cos, sin) table: table[pos*half + p] for pos < rows, p < half = head_dim/2, with
 // angle = float(pos) * inv_freq[p]. The frequencies travel in the kernel arguments (no copy).

@@ -1,4 +1,5 @@
-"""GPU parity of the assembly dK/dV backward kernel (fa_bwd_dkdv_a64_bf16, generated gfx950 code,
+"""GPU parity of the assembly dK/dV backward kernels (fa_bwd_dkdv_a64_bf16 and its f16 twin
+fa_bwd_dkdv_a64_f16, generated gfx950 code,
 selected by fa_ctx_set_backward_kernel) against the CPU oracle (backward_reference_grouped,
 src/backward_grouped.rs:17) and against the HIP dK/dV kernel on the same inputs.
 
@@ -64,11 +65,22 @@ def test_matches_oracle(hip, dims, causal):
         assert_close(f"{dims}-{causal}-{tag}", a, e, 2e-2 * float(np.abs(e).max()), 2e-2)
 
 
+@pytest.mark.parametrize("dims,causal", [CASES[0], CASES[3], CASES[4], CASES[6]])
+def test_f16_matches_oracle(hip, dims, causal):
+    """f16 storage: the f16 twin (f16 MFMAs, dS and dK/dV stored as f16)."""
+    got, want, name = _run(hip, dims, causal, 305, dtype=fa.DTYPE_F16)
+    assert "bwd_dkdv_a64" in name and "<f16>" in name, name
+    for tag, a, e in zip(("dQ", "dK", "dV"), (got.dq, got.dk, got.dv), want):
+        assert np.isfinite(a).all(), tag
+        assert_close(f"{dims}-{causal}-{tag}", a, e, 2e-2 * float(np.abs(e).max()), 2e-2)
+
+
+@pytest.mark.parametrize("dtype", [fa.DTYPE_BF16, fa.DTYPE_F16])
 @pytest.mark.parametrize("dims,causal", [((2, 8, 2, 384, 128), True),
                                          ((1, 16, 2, 256, 128), False)])
-def test_agrees_with_hip_kernel(hip, dims, causal):
-    got, _, name = _run(hip, dims, causal, 311)
-    ref, _, name0 = _run(hip, dims, causal, 311, kernel=0)
+def test_agrees_with_hip_kernel(hip, dims, causal, dtype):
+    got, _, name = _run(hip, dims, causal, 311, dtype=dtype)
+    ref, _, name0 = _run(hip, dims, causal, 311, kernel=0, dtype=dtype)
     assert "bwd_dkdv_a64" in name and "bwd_dkdv_a64" not in name0, (name, name0)
     for tag, a, b in zip(("dQ", "dK", "dV"), (got.dq, got.dk, got.dv),
                          (ref.dq, ref.dk, ref.dv)):
@@ -96,7 +108,7 @@ def test_deterministic(hip):
 
 @pytest.mark.parametrize("dims,dtype", [((1, 4, 2, 130, 128), fa.DTYPE_BF16),   # ragged
                                         ((1, 4, 2, 256, 64), fa.DTYPE_BF16),    # head_dim 64
-                                        ((1, 4, 2, 256, 128), fa.DTYPE_F16)])
+                                        ((1, 4, 2, 256, 64), fa.DTYPE_F16)])
 def test_other_shapes_take_the_hip_kernel(hip, dims, dtype):
     got, want, name = _run(hip, dims, True, 341, dtype=dtype)
     assert "bwd_dkdv_a64" not in name and "bwd_dkdv" in name, name
